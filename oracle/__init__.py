@@ -1,0 +1,345 @@
+"""ctypes view of the CPU oracle (``oracle/_build/libptwm_oracle.so``).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
+and ``bench.py``'s ``cpu_baseline`` leg, always as the checker or the timed
+CPU baseline, never as the product path.  The C sources restate the
+reference algorithms (``crates/ptwm-core/src/...``); each C function cites
+the reference file:line it follows.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "libptwm_oracle.so")
+
+CODEC_IDENTITY = 0x0000
+CODEC_HUFFMAN = 0x0001
+CODEC_RANS = 0x0003
+
+CHAIN_IEEE16_SPLIT2 = 1
+CHAIN_IEEE32_SPLIT4 = 2
+CHAIN_E4M3_NIBBLE = 3
+CHAIN_E5M2_NIBBLE = 4
+CHAIN_NIBBLE_SPLIT = 5
+CHAIN_PASSTHROUGH = 6
+
+OUT_ENCODED, OUT_NOT_BENEFICIAL, OUT_INCOMPRESSIBLE, OUT_DST_TOO_SMALL, OUT_LEN_OVERFLOW = range(5)
+
+
+class OracleError(RuntimeError):
+    """A negative return code from the oracle (the reference returned Err)."""
+
+    def __init__(self, rc: int, what: str):
+        super().__init__(f"{what}: rc={rc}")
+        self.rc = rc
+
+
+def build() -> str:
+    """Compile the oracle with gcc (oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+_lib = None
+u8p = C.POINTER(C.c_uint8)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        sz, i64, vp = C.c_size_t, C.c_int64, C.c_void_p
+        L.por_huf_compress.restype = i64
+        L.por_huf_compress.argtypes = [vp, sz, vp, sz, C.POINTER(C.c_int)]
+        L.por_huf_decompress.restype = i64
+        L.por_huf_decompress.argtypes = [vp, sz, vp, sz]
+        L.por_rans_compress.restype = i64
+        L.por_rans_compress.argtypes = [vp, sz, vp, sz, C.POINTER(C.c_int)]
+        L.por_rans_decompress.restype = i64
+        L.por_rans_decompress.argtypes = [vp, sz, vp, sz]
+        L.por_codec_encode.restype = i64
+        L.por_codec_encode.argtypes = [C.c_int, vp, sz, vp, sz]
+        L.por_codec_decode.restype = i64
+        L.por_codec_decode.argtypes = [C.c_int, vp, sz, vp, sz]
+        L.por_codec_decoded_len.restype = i64
+        L.por_codec_decoded_len.argtypes = [C.c_int, vp, sz]
+        L.por_codec_encode_bound.restype = sz
+        L.por_codec_encode_bound.argtypes = [sz]
+        L.por_encode_plane_chunked.restype = i64
+        L.por_encode_plane_chunked.argtypes = [C.c_int, vp, sz, C.c_uint32, vp, sz, vp, sz, C.POINTER(sz)]
+        L.por_decode_plane_chunked.restype = i64
+        L.por_decode_plane_chunked.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz]
+        L.por_decode_plane_chunked_mt.restype = i64
+        L.por_decode_plane_chunked_mt.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz, C.c_int]
+        L.por_huf_lengths_from_freqs.restype = C.c_int
+        L.por_huf_lengths_from_freqs.argtypes = [vp, vp]
+        L.por_huf_from_lengths.restype = C.c_int
+        L.por_huf_from_lengths.argtypes = [vp, vp, vp]
+        L.por_huf_encode_weights.restype = i64
+        L.por_huf_encode_weights.argtypes = [vp, sz, vp, sz]
+        L.por_huf_decode_weights.restype = i64
+        L.por_huf_decode_weights.argtypes = [vp, sz, vp, C.POINTER(C.c_int)]
+        L.por_bitwriter_pack.restype = i64
+        L.por_bitwriter_pack.argtypes = [vp, vp, sz, vp, sz]
+        L.por_rans_normalize.restype = C.c_int
+        L.por_rans_normalize.argtypes = [vp, vp, vp]
+        L.por_rans_enc_update.restype = C.c_uint32
+        L.por_rans_enc_update.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32]
+        L.por_chain_forward.restype = C.c_int
+        L.por_chain_forward.argtypes = [C.c_int, vp, sz, vp]
+        L.por_chain_inverse.restype = C.c_int
+        L.por_chain_inverse.argtypes = [C.c_int, vp, sz, vp]
+        L.por_chain_plane_len.restype = i64
+        L.por_chain_plane_len.argtypes = [C.c_int, sz]
+        L.por_chain_nplanes.restype = C.c_int
+        L.por_chain_nplanes.argtypes = [C.c_int]
+        for nm in ("por_reorder16_buf", "por_revert16_buf", "por_reorder32_buf", "por_revert32_buf"):
+            getattr(L, nm).restype = None
+            getattr(L, nm).argtypes = [vp, sz]
+        L.por_byte_split.restype = None
+        L.por_byte_split.argtypes = [vp, sz, C.c_int, vp]
+        L.por_byte_merge.restype = None
+        L.por_byte_merge.argtypes = [vp, sz, C.c_int, vp]
+        L.por_nibble_split.restype = None
+        L.por_nibble_split.argtypes = [vp, sz, vp, vp]
+        L.por_nibble_merge.restype = None
+        L.por_nibble_merge.argtypes = [vp, vp, sz, vp]
+        for nm in ("por_reorder_e4m3", "por_revert_e4m3", "por_reorder_e5m2", "por_revert_e5m2"):
+            getattr(L, nm).restype = C.c_uint8
+            getattr(L, nm).argtypes = [C.c_uint8]
+        for nm in ("por_reorder16x2", "por_revert16x2", "por_reorder32", "por_revert32"):
+            getattr(L, nm).restype = C.c_uint32
+            getattr(L, nm).argtypes = [C.c_uint32]
+        L.por_crc32.restype = C.c_uint32
+        L.por_crc32.argtypes = [C.c_uint32, vp, sz]
+        L.por_xxh64.restype = C.c_uint64
+        L.por_xxh64.argtypes = [vp, sz, C.c_uint64]
+        L.por_blake3.restype = None
+        L.por_blake3.argtypes = [vp, sz, vp]
+        L.por_histogram.restype = None
+        L.por_histogram.argtypes = [vp, sz, vp]
+        _lib = L
+    return _lib
+
+
+def _buf(data) -> np.ndarray:
+    if isinstance(data, np.ndarray):
+        return np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+    return np.frombuffer(bytes(data), dtype=np.uint8)
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p) if a.size else None
+
+
+# ---- entropy coders (raw blobs, entropy/{huffman,rans}) ----
+
+def huf_compress(src, cap=None):
+    """entropy/huffman/compress.rs:9 -> (outcome, blob)."""
+    s = _buf(src)
+    cap = cap if cap is not None else 2 * s.size + 4096
+    dst = np.zeros(max(cap, 1), np.uint8)
+    oc = C.c_int(0)
+    n = lib().por_huf_compress(_ptr(dst), cap, _ptr(s), s.size, C.byref(oc))
+    if n < 0:
+        raise OracleError(n, "huf_compress")
+    return oc.value, dst[:n].tobytes()
+
+
+def huf_decompress(blob, n_out: int) -> bytes:
+    b = _buf(blob)
+    dst = np.zeros(max(n_out, 1), np.uint8)
+    r = lib().por_huf_decompress(_ptr(dst), n_out, _ptr(b), b.size)
+    if r < 0:
+        raise OracleError(r, "huf_decompress")
+    return dst[:n_out].tobytes()
+
+
+def rans_compress(src, cap=None):
+    s = _buf(src)
+    cap = cap if cap is not None else 2 * s.size + 4096
+    dst = np.zeros(max(cap, 1), np.uint8)
+    oc = C.c_int(0)
+    n = lib().por_rans_compress(_ptr(dst), cap, _ptr(s), s.size, C.byref(oc))
+    if n < 0:
+        raise OracleError(n, "rans_compress")
+    return oc.value, dst[:n].tobytes()
+
+
+def rans_decompress(blob, n_out: int) -> bytes:
+    b = _buf(blob)
+    dst = np.zeros(max(n_out, 1), np.uint8)
+    r = lib().por_rans_decompress(_ptr(dst), n_out, _ptr(b), b.size)
+    if r < 0:
+        raise OracleError(r, "rans_decompress")
+    return dst[:n_out].tobytes()
+
+
+# ---- plane codec payloads (codecs/{identity,huffman,rans}.rs) ----
+
+def codec_encode(codec: int, plane) -> bytes:
+    s = _buf(plane)
+    cap = int(lib().por_codec_encode_bound(s.size))
+    out = np.zeros(max(cap, 1), np.uint8)
+    n = lib().por_codec_encode(codec, _ptr(s), s.size, _ptr(out), cap)
+    if n < 0:
+        raise OracleError(n, "codec_encode")
+    return out[:n].tobytes()
+
+
+def codec_decode(codec: int, payload, cap: int) -> bytes:
+    p = _buf(payload)
+    out = np.zeros(max(cap, 1), np.uint8)
+    n = lib().por_codec_decode(codec, _ptr(p), p.size, _ptr(out), cap)
+    if n < 0:
+        raise OracleError(n, "codec_decode")
+    return out[:n].tobytes()
+
+
+def encode_plane_chunked(codec: int, plane, chunk_size: int):
+    """compressor.rs:324-381 -> (payload bytes, entries uint32[n,2])."""
+    s = _buf(plane)
+    cs = max(int(chunk_size), 1)
+    nch = max(1, -(-s.size // cs))
+    cap = nch * 5 + s.size + 5 * nch + 16
+    out = np.zeros(cap, np.uint8)
+    ent = np.zeros((nch, 2), np.uint32)
+    nc = C.c_size_t(0)
+    n = lib().por_encode_plane_chunked(codec, _ptr(s), s.size, cs, _ptr(out), cap, _ptr(ent), nch, C.byref(nc))
+    if n < 0:
+        raise OracleError(n, "encode_plane_chunked")
+    return out[:n].tobytes(), ent[: nc.value].copy()
+
+
+def decode_plane_chunked(codec: int, payload, entries, threads: int = 1) -> bytes:
+    p = _buf(payload)
+    ent = np.ascontiguousarray(entries, dtype=np.uint32)
+    total = int(ent[:, 1].astype(np.uint64).sum()) if ent.size else 0
+    out = np.zeros(max(total, 1), np.uint8)
+    r = lib().por_decode_plane_chunked_mt(codec, _ptr(p), p.size, _ptr(ent), ent.shape[0], _ptr(out), total, threads)
+    if r < 0:
+        raise OracleError(r, "decode_plane_chunked")
+    return out[:total].tobytes()
+
+
+# ---- chains (transforms/fusion.rs) ----
+
+def chain_forward(chain: int, data) -> list[bytes]:
+    s = _buf(data)
+    pl = int(lib().por_chain_plane_len(chain, s.size))
+    if pl < 0:
+        raise OracleError(-1, "chain_forward length")
+    n = lib().por_chain_nplanes(chain)
+    planes = [np.zeros(max(pl, 1), np.uint8) for _ in range(n)]
+    ptrs = (C.c_void_p * n)(*[p.ctypes.data for p in planes])
+    r = lib().por_chain_forward(chain, _ptr(s), s.size, ptrs)
+    if r < 0:
+        raise OracleError(r, "chain_forward")
+    return [p[:pl].tobytes() for p in planes]
+
+
+def chain_inverse(chain: int, planes) -> bytes:
+    arrs = [_buf(p) for p in planes]
+    n = lib().por_chain_nplanes(chain)
+    assert len(arrs) == n and len({a.size for a in arrs}) == 1
+    pl = arrs[0].size
+    total = {CHAIN_IEEE16_SPLIT2: 2, CHAIN_IEEE32_SPLIT4: 4}.get(chain, 1) * pl
+    out = np.zeros(max(total, 1), np.uint8)
+    keep = [a if a.size else np.zeros(1, np.uint8) for a in arrs]
+    ptrs = (C.c_void_p * n)(*[a.ctypes.data for a in keep])
+    r = lib().por_chain_inverse(chain, ptrs, pl, _ptr(out))
+    if r < 0:
+        raise OracleError(r, "chain_inverse")
+    return out[:total].tobytes()
+
+
+# ---- Huffman internals ----
+
+def huf_lengths(freqs):
+    f = np.ascontiguousarray(freqs, dtype=np.uint32)
+    assert f.size == 256
+    lengths = np.zeros(256, np.uint8)
+    ok = lib().por_huf_lengths_from_freqs(_ptr(f), _ptr(lengths))
+    return lengths if ok else None
+
+
+def huf_table(lengths):
+    """tree.rs:102-177 -> (max_bits, decode_table, rev_codes) or None."""
+    l8 = np.ascontiguousarray(lengths, dtype=np.uint8)
+    assert l8.size == 256
+    table = np.zeros(2048, np.uint16)
+    rev = np.zeros(256, np.uint16)
+    mb = lib().por_huf_from_lengths(_ptr(l8), _ptr(table), _ptr(rev))
+    if mb == 0:
+        return None
+    return mb, table[: 1 << mb].copy(), rev
+
+
+def huf_encode_weights(weights) -> bytes:
+    w = _buf(weights)
+    out = np.zeros(260, np.uint8)
+    n = lib().por_huf_encode_weights(_ptr(w), w.size, _ptr(out), out.size)
+    if n < 0:
+        raise OracleError(n, "encode_weights")
+    return out[:n].tobytes()
+
+
+def huf_decode_weights(src):
+    s = _buf(src)
+    w = np.zeros(256, np.uint8)
+    nn = C.c_int(0)
+    used = lib().por_huf_decode_weights(_ptr(s), s.size, _ptr(w), C.byref(nn))
+    if used < 0:
+        raise OracleError(used, "decode_weights")
+    return w[: nn.value].tobytes(), int(used)
+
+
+def bitwriter_pack(codes) -> bytes:
+    bits = np.array([c[0] for c in codes], np.uint16)
+    nb = np.array([c[1] for c in codes], np.uint8)
+    out = np.zeros(len(codes) * 2 + 16, np.uint8)
+    n = lib().por_bitwriter_pack(_ptr(bits), _ptr(nb), len(codes), _ptr(out), out.size)
+    if n < 0:
+        raise OracleError(n, "bitwriter_pack")
+    return out[:n].tobytes()
+
+
+def rans_normalize(raw):
+    r = np.ascontiguousarray(raw, dtype=np.uint32)
+    f = np.zeros(256, np.uint16)
+    cum = np.zeros(256, np.uint16)
+    ok = lib().por_rans_normalize(_ptr(r), _ptr(f), _ptr(cum))
+    return (f, cum) if ok else None
+
+
+# ---- integrity ----
+
+def crc32(data, crc: int = 0) -> int:
+    b = _buf(data)
+    return int(lib().por_crc32(crc, _ptr(b), b.size))
+
+
+def xxh64(data, seed: int = 0) -> int:
+    b = _buf(data)
+    return int(lib().por_xxh64(_ptr(b), b.size, seed))
+
+
+def blake3(data) -> bytes:
+    b = _buf(data)
+    out = np.zeros(32, np.uint8)
+    lib().por_blake3(_ptr(b), b.size, _ptr(out))
+    return out.tobytes()
+
+
+def histogram(data):
+    b = _buf(data)
+    h = np.zeros(256, np.uint32)
+    lib().por_histogram(_ptr(b), b.size, _ptr(h))
+    return h

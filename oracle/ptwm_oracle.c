@@ -1,0 +1,1018 @@
+/*
+ * ptwm_oracle.c -- CPU restatement of the PTWM plane-codec hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker and the timed CPU baseline); see
+ * ptwm_oracle.h.  Citations are file:line under crates/ptwm-core/src/ of the
+ * reference tree.  Arithmetic follows the reference's integer widths,
+ * including its wrapping u8 bit counter in the Huffman reader (release
+ * builds of the reference do not check overflow: Cargo.toml [profile.release]
+ * leaves overflow-checks off).
+ *
+ * Parity pinning (what checks each part) is listed in tests/test_oracle_*.py.
+ */
+#include "ptwm_oracle.h"
+
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------- */
+/* bit reorder: split/dtype8.rs:30-62, dtype16.rs:11-59, dtype32.rs:13-55     */
+/* ------------------------------------------------------------------------- */
+
+uint8_t por_reorder_e4m3(uint8_t v) { return (uint8_t)(((v & 0x78) << 1) | ((v & 0x80) >> 4) | (v & 0x07)); }
+uint8_t por_revert_e4m3(uint8_t v) { return (uint8_t)(((v & 0xF0) >> 1) | ((v & 0x08) << 4) | (v & 0x07)); }
+uint8_t por_reorder_e5m2(uint8_t v) { return (uint8_t)(((v & 0x7C) << 1) | ((v & 0x80) >> 5) | (v & 0x03)); }
+uint8_t por_revert_e5m2(uint8_t v) { return (uint8_t)(((v & 0xF8) >> 1) | ((v & 0x04) << 5) | (v & 0x03)); }
+
+uint32_t por_reorder16x2(uint32_t v) {
+    return ((v << 1) & 0xFF00FF00u) | ((v >> 8) & 0x00800080u) | (v & 0x007F007Fu);
+}
+uint32_t por_revert16x2(uint32_t v) {
+    return ((v << 8) & 0x80008000u) | ((v >> 1) & 0x7F807F80u) | (v & 0x007F007Fu);
+}
+uint32_t por_reorder32(uint32_t v) {
+    return ((v << 1) & 0xFF000000u) | ((v >> 8) & 0x00800000u) | (v & 0x007FFFFFu);
+}
+uint32_t por_revert32(uint32_t v) {
+    return ((v << 8) & 0x80000000u) | ((v >> 1) & 0x7F800000u) | (v & 0x007FFFFFu);
+}
+
+static uint32_t ld32(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24); }
+static void st32(uint8_t *p, uint32_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); p[2] = (uint8_t)(v >> 16); p[3] = (uint8_t)(v >> 24); }
+
+/* dtype16.rs:31-59 -- only floor(len/4) words; a trailing element is left as is */
+void por_reorder16_buf(uint8_t *d, size_t len) { for (size_t i = 0; i + 4 <= len; i += 4) st32(d + i, por_reorder16x2(ld32(d + i))); }
+void por_revert16_buf(uint8_t *d, size_t len) { for (size_t i = 0; i + 4 <= len; i += 4) st32(d + i, por_revert16x2(ld32(d + i))); }
+/* dtype32.rs:28-55 */
+void por_reorder32_buf(uint8_t *d, size_t len) { for (size_t i = 0; i + 4 <= len; i += 4) st32(d + i, por_reorder32(ld32(d + i))); }
+void por_revert32_buf(uint8_t *d, size_t len) { for (size_t i = 0; i + 4 <= len; i += 4) st32(d + i, por_revert32(ld32(d + i))); }
+
+/* ------------------------------------------------------------------------- */
+/* byte / nibble split: transforms/byte_split.rs:86-176, nibble_split.rs:72-120 */
+/* ------------------------------------------------------------------------- */
+
+void por_byte_split(const uint8_t *in, size_t len, int n, uint8_t *const *planes) {
+    for (size_t j = 0; j < len; j++) planes[j % (size_t)n][j / (size_t)n] = in[j];
+}
+void por_byte_merge(const uint8_t *const *planes, size_t plane_len, int n, uint8_t *out) {
+    for (int p = 0; p < n; p++)
+        for (size_t j = 0; j < plane_len; j++) out[j * (size_t)n + (size_t)p] = planes[p][j];
+}
+void por_nibble_split(const uint8_t *in, size_t len, uint8_t *hi, uint8_t *lo) {
+    for (size_t i = 0; i < len; i++) { hi[i] = (in[i] >> 4) & 0x0F; lo[i] = in[i] & 0x0F; }
+}
+void por_nibble_merge(const uint8_t *hi, const uint8_t *lo, size_t len, uint8_t *out) {
+    for (size_t i = 0; i < len; i++) out[i] = (uint8_t)(((hi[i] & 0x0F) << 4) | (lo[i] & 0x0F));
+}
+
+/* ------------------------------------------------------------------------- */
+/* fused chains: transforms/fusion.rs:32-519                                  */
+/* ------------------------------------------------------------------------- */
+
+int por_chain_nplanes(int chain) {
+    switch (chain) {
+    case POR_CHAIN_IEEE16_SPLIT2: return 2;
+    case POR_CHAIN_IEEE32_SPLIT4: return 4;
+    case POR_CHAIN_E4M3_NIBBLE: case POR_CHAIN_E5M2_NIBBLE: case POR_CHAIN_NIBBLE_SPLIT: return 2;
+    case POR_CHAIN_PASSTHROUGH: return 1;
+    default: return -1;
+    }
+}
+
+int64_t por_chain_plane_len(int chain, size_t len) {
+    switch (chain) {
+    case POR_CHAIN_IEEE16_SPLIT2: return (len % 2) ? -1 : (int64_t)(len / 2);   /* fusion.rs:37-42 */
+    case POR_CHAIN_IEEE32_SPLIT4: return (len % 4) ? -1 : (int64_t)(len / 4);   /* fusion.rs:209-215 */
+    case POR_CHAIN_E4M3_NIBBLE: case POR_CHAIN_E5M2_NIBBLE: case POR_CHAIN_NIBBLE_SPLIT:
+    case POR_CHAIN_PASSTHROUGH: return (int64_t)len;
+    default: return -1;
+    }
+}
+
+int por_chain_forward(int chain, const uint8_t *src, size_t len, uint8_t *const *pl) {
+    size_t i;
+    switch (chain) {
+    case POR_CHAIN_IEEE16_SPLIT2: { /* fusion.rs:35-94 */
+        if (len % 2) return POR_EINVAL;
+        size_t words = len / 4;
+        for (i = 0; i < words; i++) {
+            uint32_t r = por_reorder16x2(ld32(src + 4 * i));
+            pl[0][2 * i] = (uint8_t)r; pl[1][2 * i] = (uint8_t)(r >> 8);
+            pl[0][2 * i + 1] = (uint8_t)(r >> 16); pl[1][2 * i + 1] = (uint8_t)(r >> 24);
+        }
+        if (len % 4 == 2) { /* trailing element IS reordered here (fusion.rs:73-89) */
+            size_t k = len - 2;
+            uint16_t v = (uint16_t)(src[k] | (src[k + 1] << 8));
+            uint16_t r = (uint16_t)(((v << 1) & 0xFF00) | ((v >> 8) & 0x0080) | (v & 0x007F));
+            pl[0][len / 2 - 1] = (uint8_t)r; pl[1][len / 2 - 1] = (uint8_t)(r >> 8);
+        }
+        return 0;
+    }
+    case POR_CHAIN_IEEE32_SPLIT4: /* fusion.rs:208-255 */
+        if (len % 4) return POR_EINVAL;
+        for (i = 0; i < len / 4; i++) {
+            uint32_t r = por_reorder32(ld32(src + 4 * i));
+            pl[0][i] = (uint8_t)r; pl[1][i] = (uint8_t)(r >> 8); pl[2][i] = (uint8_t)(r >> 16); pl[3][i] = (uint8_t)(r >> 24);
+        }
+        return 0;
+    case POR_CHAIN_E4M3_NIBBLE: /* fusion.rs:329-338 */
+        for (i = 0; i < len; i++) { uint8_t r = por_reorder_e4m3(src[i]); pl[0][i] = r >> 4; pl[1][i] = r & 0x0F; }
+        return 0;
+    case POR_CHAIN_E5M2_NIBBLE: /* fusion.rs:431-440 */
+        for (i = 0; i < len; i++) { uint8_t r = por_reorder_e5m2(src[i]); pl[0][i] = r >> 4; pl[1][i] = r & 0x0F; }
+        return 0;
+    case POR_CHAIN_NIBBLE_SPLIT: por_nibble_split(src, len, pl[0], pl[1]); return 0;
+    case POR_CHAIN_PASSTHROUGH: if (len) memcpy(pl[0], src, len); return 0;
+    default: return POR_EUNSUP;
+    }
+}
+
+int por_chain_inverse(int chain, const uint8_t *const *pl, size_t n, uint8_t *out) {
+    size_t i;
+    switch (chain) {
+    case POR_CHAIN_IEEE16_SPLIT2: { /* fusion.rs:127-194 */
+        for (i = 0; i < n / 2; i++) {
+            uint32_t r = (uint32_t)pl[0][2 * i] | ((uint32_t)pl[1][2 * i] << 8) |
+                         ((uint32_t)pl[0][2 * i + 1] << 16) | ((uint32_t)pl[1][2 * i + 1] << 24);
+            st32(out + 4 * i, por_revert16x2(r));
+        }
+        if (n % 2) {
+            size_t k = n - 1;
+            uint16_t r = (uint16_t)(pl[0][k] | (pl[1][k] << 8));
+            uint16_t v = (uint16_t)(((r << 8) & 0x8000) | ((r >> 1) & 0x7F80) | (r & 0x007F));
+            out[2 * k] = (uint8_t)v; out[2 * k + 1] = (uint8_t)(v >> 8);
+        }
+        return 0;
+    }
+    case POR_CHAIN_IEEE32_SPLIT4: /* fusion.rs:261-315 */
+        for (i = 0; i < n; i++) {
+            uint32_t r = (uint32_t)pl[0][i] | ((uint32_t)pl[1][i] << 8) | ((uint32_t)pl[2][i] << 16) | ((uint32_t)pl[3][i] << 24);
+            st32(out + 4 * i, por_revert32(r));
+        }
+        return 0;
+    case POR_CHAIN_E4M3_NIBBLE: /* fusion.rs:376-399 */
+        for (i = 0; i < n; i++) out[i] = por_revert_e4m3((uint8_t)(((pl[0][i] & 0x0F) << 4) | (pl[1][i] & 0x0F)));
+        return 0;
+    case POR_CHAIN_E5M2_NIBBLE: /* fusion.rs:478-501 */
+        for (i = 0; i < n; i++) out[i] = por_revert_e5m2((uint8_t)(((pl[0][i] & 0x0F) << 4) | (pl[1][i] & 0x0F)));
+        return 0;
+    case POR_CHAIN_NIBBLE_SPLIT: por_nibble_merge(pl[0], pl[1], n, out); return 0;
+    case POR_CHAIN_PASSTHROUGH: if (n) memcpy(out, pl[0], n); return 0;
+    default: return POR_EUNSUP;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* entropy helpers: entropy/mod.rs:34-40, stream_frame.rs:27-62               */
+/* ------------------------------------------------------------------------- */
+
+void por_histogram(const uint8_t *d, size_t len, uint32_t h[256]) {
+    memset(h, 0, 256 * sizeof(uint32_t));
+    for (size_t i = 0; i < len; i++) h[d[i]]++;
+}
+
+void por_split_four(size_t len, size_t s[4], size_t e[4]) {
+    size_t base = len / 4, rem = len % 4, start = 0;
+    for (int i = 0; i < 4; i++) { size_t l = base + ((size_t)i < rem); s[i] = start; e[i] = start + l; start += l; }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Huffman tree: entropy/huffman/tree.rs                                      */
+/* ------------------------------------------------------------------------- */
+
+#define HUF_MAX_TABLE_LOG 11
+
+/* min-heap over (freq, id); keys are distinct, so the pop order matches any
+ * correct priority queue, including Rust's BinaryHeap<Reverse<(u64,usize)>> */
+typedef struct { uint64_t f; uint32_t id; } hkey;
+static int hless(hkey a, hkey b) { return a.f < b.f || (a.f == b.f && a.id < b.id); }
+static void hpush(hkey *h, int *n, hkey k) {
+    int i = (*n)++;
+    h[i] = k;
+    while (i > 0) { int p = (i - 1) / 2; if (!hless(h[i], h[p])) break; hkey t = h[i]; h[i] = h[p]; h[p] = t; i = p; }
+}
+static hkey hpop(hkey *h, int *n) {
+    hkey top = h[0];
+    h[0] = h[--(*n)];
+    int i = 0;
+    for (;;) {
+        int l = 2 * i + 1, r = l + 1, m = i;
+        if (l < *n && hless(h[l], h[m])) m = l;
+        if (r < *n && hless(h[r], h[m])) m = r;
+        if (m == i) break;
+        hkey t = h[i]; h[i] = h[m]; h[m] = t; i = m;
+    }
+    return top;
+}
+
+/* tree.rs:212-242 */
+static void enforce_max_code_length(uint8_t *lengths, uint8_t max_len) {
+    int clamped = 0;
+    for (int s = 0; s < 256; s++) if (lengths[s] > max_len) { lengths[s] = max_len; clamped = 1; }
+    if (!clamped) return;
+    uint32_t cap = 1u << max_len;
+    for (;;) {
+        uint32_t kraft = 0;
+        for (int s = 0; s < 256; s++) if (lengths[s]) kraft += 1u << (max_len - lengths[s]);
+        if (kraft <= cap) break;
+        int victim = -1;
+        for (int s = 0; s < 256; s++)  /* min_by_key keeps the first minimum */
+            if (lengths[s] > 0 && lengths[s] < max_len && (victim < 0 || lengths[s] < lengths[victim])) victim = s;
+        if (victim < 0) break;
+        lengths[victim]++;
+    }
+}
+
+/* tree.rs:19-85 */
+int por_huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]) {
+    int sym[256], n = 0;
+    memset(lengths, 0, 256);
+    for (int i = 0; i < 256; i++) if (freqs[i] > 0) sym[n++] = i;
+    if (n == 0) return 0;
+    if (n == 1) { lengths[sym[0]] = 1; return 1; }
+    uint64_t nf[512];
+    int left[512], right[512];
+    hkey heap[512];
+    int hn = 0;
+    for (int id = 0; id < n; id++) { nf[id] = freqs[sym[id]]; hpush(heap, &hn, (hkey){nf[id], (uint32_t)id}); }
+    int next = n;
+    while (hn > 1) {
+        hkey a = hpop(heap, &hn), b = hpop(heap, &hn);
+        nf[next] = a.f + b.f; left[next] = (int)a.id; right[next] = (int)b.id;
+        hpush(heap, &hn, (hkey){a.f + b.f, (uint32_t)next});
+        next++;
+    }
+    int root = (int)hpop(heap, &hn).id;
+    int stack_id[512]; uint8_t stack_d[512]; int sp = 0;
+    stack_id[sp] = root; stack_d[sp] = 0; sp++;
+    while (sp > 0) {
+        sp--; int id = stack_id[sp]; uint8_t d = stack_d[sp];
+        if (id < n) lengths[sym[id]] = d;
+        else {
+            uint8_t nd = d == 255 ? 255 : (uint8_t)(d + 1);
+            stack_id[sp] = left[id]; stack_d[sp] = nd; sp++;
+            stack_id[sp] = right[id]; stack_d[sp] = nd; sp++;
+        }
+    }
+    enforce_max_code_length(lengths, HUF_MAX_TABLE_LOG);
+    return 1;
+}
+
+static uint16_t reverse_bits(uint16_t code, int nbits) {
+    uint16_t out = 0;
+    for (int i = 0; i < nbits; i++) { out = (uint16_t)((out << 1) | (code & 1)); code >>= 1; }
+    return out;
+}
+
+/* tree.rs:102-177: returns max_bits, or 0 for None */
+int por_huf_from_lengths(const uint8_t lengths[256], uint16_t *table, uint16_t rev_codes[256]) {
+    int max_bits = 0;
+    for (int s = 0; s < 256; s++) if (lengths[s] > max_bits) max_bits = lengths[s];
+    if (max_bits < 1) max_bits = 1;
+    if (max_bits > HUF_MAX_TABLE_LOG) return 0;
+    uint16_t counts[HUF_MAX_TABLE_LOG + 1] = {0};
+    uint32_t total = 0;
+    for (int s = 0; s < 256; s++) if (lengths[s]) { counts[lengths[s]]++; total++; }
+    if (total == 0) return 0;
+    uint16_t next_code[HUF_MAX_TABLE_LOG + 1] = {0};
+    uint16_t code = 0;
+    for (int b = 1; b <= max_bits; b++) {
+        code = (uint16_t)((code + counts[b - 1]) << 1);
+        if (code > (1u << b)) return 0;
+        next_code[b] = code;
+    }
+    uint16_t codes[256] = {0};
+    for (int s = 0; s < 256; s++) {
+        int l = lengths[s];
+        if (!l) continue;
+        uint16_t c = next_code[l];
+        if (c >= (1u << l)) return 0;
+        codes[s] = c; next_code[l] = (uint16_t)(c + 1);
+    }
+    size_t tsize = (size_t)1 << max_bits;
+    uint16_t fallback = (uint16_t)(max_bits << 8);
+    for (size_t i = 0; i < tsize; i++) table[i] = fallback;
+    for (int s = 0; s < 256; s++) {
+        int l = lengths[s];
+        if (!l) continue;
+        uint16_t rev = reverse_bits(codes[s], l);
+        if (rev_codes) rev_codes[s] = rev;
+        uint16_t entry = (uint16_t)((l << 8) | s);
+        for (size_t i = 0; i < ((size_t)1 << (max_bits - l)); i++) {
+            size_t idx = rev | (i << l);
+            if (table[idx] != fallback && table[idx] != entry) return 0;
+            table[idx] = entry;
+        }
+    }
+    return max_bits;
+}
+
+/* weights.rs:8-32 */
+int64_t por_huf_encode_weights(const uint8_t *w, size_t n, uint8_t *out, size_t cap) {
+    if (n == 0 || n > 256) return POR_EINVAL;
+    size_t need = (n <= 127 ? 1 : 2) + (n + 1) / 2, o = 0;
+    if (need > cap) return POR_ESMALL;
+    if (n <= 127) out[o++] = (uint8_t)(0x80 | n);
+    else { out[o++] = 0x80; out[o++] = (uint8_t)n; }
+    for (size_t i = 0; i < n; i += 2) {
+        uint8_t lo = w[i] & 0x0F, hi = (i + 1 < n) ? (w[i + 1] & 0x0F) : 0;
+        out[o++] = (uint8_t)(lo | (hi << 4));
+    }
+    return (int64_t)o;
+}
+
+/* weights.rs:34-85 */
+int64_t por_huf_decode_weights(const uint8_t *src, size_t len, uint8_t w[256], int *n_out) {
+    if (len == 0) return POR_EINVAL;
+    uint8_t h = src[0];
+    if (!(h & 0x80)) return POR_EINVAL;
+    size_t n, hb;
+    if (h == 0x80) {
+        if (len < 2) return POR_EINVAL;
+        n = src[1] ? src[1] : 256;
+        if (n < 128) return POR_EINVAL;
+        hb = 2;
+    } else {
+        n = h & 0x7F;
+        if (n == 0) return POR_EINVAL;
+        hb = 1;
+    }
+    size_t need = hb + (n + 1) / 2;
+    if (len < need) return POR_EINVAL;
+    for (size_t i = 0; i < n; i++) { uint8_t b = src[hb + i / 2]; w[i] = (i % 2 == 0) ? (b & 0x0F) : ((b >> 4) & 0x0F); }
+    *n_out = (int)n;
+    return (int64_t)need;
+}
+
+/* ------------------------------------------------------------------------- */
+/* backward bitstream: entropy/huffman/bitstream.rs                           */
+/* ------------------------------------------------------------------------- */
+
+typedef struct { uint8_t *buf; size_t ptr; uint64_t cont; uint32_t cnt; } bw_t;
+
+/* bitstream.rs:22-35 */
+static void bw_write(bw_t *w, uint16_t bits, uint8_t nbits) {
+    w->cont |= (uint64_t)bits << w->cnt;
+    w->cnt += nbits;
+    if (w->cnt >= 32) {
+        w->ptr -= 4;
+        uint32_t v = (uint32_t)w->cont; /* BE: lowest bits land at the highest index */
+        w->buf[w->ptr] = (uint8_t)(v >> 24); w->buf[w->ptr + 1] = (uint8_t)(v >> 16);
+        w->buf[w->ptr + 2] = (uint8_t)(v >> 8); w->buf[w->ptr + 3] = (uint8_t)v;
+        w->cont >>= 32; w->cnt -= 32;
+    }
+}
+/* bitstream.rs:40-50 */
+static size_t bw_finish(bw_t *w) {
+    while (w->cnt > 0) {
+        w->ptr -= 1;
+        w->buf[w->ptr] = (uint8_t)(w->cont & 0xFF);
+        w->cont >>= 8;
+        w->cnt = w->cnt >= 8 ? w->cnt - 8 : 0;
+    }
+    return w->ptr;
+}
+
+int64_t por_bitwriter_pack(const uint16_t *bits, const uint8_t *nbits, size_t n, uint8_t *out, size_t cap) {
+    size_t total = 0;
+    for (size_t i = 0; i < n; i++) total += nbits[i];
+    size_t scratch_len = (total + 7) / 8 + 8;
+    uint8_t *scratch = (uint8_t *)calloc(scratch_len, 1);
+    if (!scratch) return POR_ESMALL;
+    bw_t w = {scratch, scratch_len, 0, 0};
+    for (size_t i = 0; i < n; i++) bw_write(&w, bits[i], nbits[i]);
+    size_t start = bw_finish(&w), m = scratch_len - start;
+    if (m > cap) { free(scratch); return POR_ESMALL; }
+    memcpy(out, scratch + start, m);
+    free(scratch);
+    return (int64_t)m;
+}
+
+typedef struct { const uint8_t *data; int64_t bi; uint64_t cont; uint8_t cnt; } br_t;
+
+/* bitstream.rs:63-82 */
+static void br_init(br_t *r, const uint8_t *d, size_t n) {
+    r->data = d; r->bi = (int64_t)n - 1; r->cont = 0; r->cnt = 0;
+    int64_t avail = r->bi + 1; if (avail > 8) avail = 8;
+    for (int64_t i = 0; i < avail; i++) { r->cont |= (uint64_t)d[r->bi] << r->cnt; r->cnt = (uint8_t)(r->cnt + 8); r->bi--; }
+}
+/* bitstream.rs:88-106 */
+static void br_reload(br_t *r) {
+    if (r->cnt == 0 && r->bi >= 7) {
+        const uint8_t *p = r->data + r->bi - 7;
+        uint64_t w = 0;
+        for (int i = 0; i < 8; i++) w = (w << 8) | p[i];
+        r->cont = w; r->cnt = 64; r->bi -= 8;
+    } else if (r->cnt <= 32 && r->bi >= 3) {
+        const uint8_t *p = r->data + r->bi - 3;
+        uint32_t w = ((uint32_t)p[0] << 24) | ((uint32_t)p[1] << 16) | ((uint32_t)p[2] << 8) | p[3];
+        r->cont |= (uint64_t)w << r->cnt; r->cnt = (uint8_t)(r->cnt + 32); r->bi -= 4;
+    }
+}
+/* bitstream.rs:108-121 */
+static void br_refill(br_t *r) {
+    if (r->cnt <= 32 && r->bi >= 3) br_reload(r);
+    else while (r->cnt < 56 && r->bi >= 0) { r->cont |= (uint64_t)r->data[r->bi] << r->cnt; r->cnt = (uint8_t)(r->cnt + 8); r->bi--; }
+}
+/* bitstream.rs:129-137 -- the u8 counter wraps on malformed input */
+static uint8_t br_decode(br_t *r, const uint16_t *table, uint64_t mask) {
+    uint16_t e = table[r->cont & mask];
+    uint8_t nb = (uint8_t)(e >> 8);
+    r->cont >>= nb; r->cnt = (uint8_t)(r->cnt - nb);
+    return (uint8_t)(e & 0xFF);
+}
+static void br_refill_to(br_t *r, uint8_t nbits) {
+    while (r->cnt < nbits && r->bi >= 0) { r->cont |= (uint64_t)r->data[r->bi] << r->cnt; r->cnt = (uint8_t)(r->cnt + 8); r->bi--; }
+}
+static size_t br_avail(const br_t *r) { return (size_t)r->cnt + (size_t)(r->bi + 1 > 0 ? r->bi + 1 : 0) * 8; }
+static int br_exhausted(const br_t *r) { return r->bi < 0 && r->cont == 0; }
+
+/* ------------------------------------------------------------------------- */
+/* Huffman compress: entropy/huffman/compress.rs:9-103                        */
+/* ------------------------------------------------------------------------- */
+
+int64_t por_huf_compress(uint8_t *dst, size_t cap, const uint8_t *src, size_t len, int *outcome) {
+    *outcome = POR_OUT_INCOMPRESSIBLE;
+    if (len == 0) return 0;
+    uint32_t freqs[256];
+    por_histogram(src, len, freqs);
+    uint8_t lengths[256];
+    uint16_t table[1 << HUF_MAX_TABLE_LOG], rev[256];
+    if (!por_huf_lengths_from_freqs(freqs, lengths)) return 0;
+    int max_bits = por_huf_from_lengths(lengths, table, rev);
+    if (!max_bits) return 0;
+    int n = 0;
+    for (int s = 0; s < 256; s++) if (lengths[s]) n = s + 1;
+    uint8_t hdr[2 + 128 + 16];
+    int64_t wl = por_huf_encode_weights(lengths, (size_t)n, hdr, sizeof(hdr));
+    if (wl < 0) return 0;
+    size_t jt = (size_t)wl, header_len = jt + 16;
+    memset(hdr + jt, 0, 16);
+    if (header_len >= cap) { *outcome = POR_OUT_DST_TOO_SMALL; return 0; }
+    memcpy(dst, hdr, header_len);
+    size_t s[4], e[4];
+    por_split_four(len, s, e);
+    size_t max_seg = 0;
+    for (int i = 0; i < 4; i++) if (e[i] - s[i] > max_seg) max_seg = e[i] - s[i];
+    size_t max_out = (max_seg * (size_t)max_bits + 7) / 8 + 8;
+    uint8_t *scratch = (uint8_t *)malloc(max_out);
+    if (!scratch) return POR_ESMALL;
+    uint32_t lens[4];
+    size_t off = header_len;
+    for (int i = 0; i < 4; i++) {
+        bw_t w = {scratch, max_out, 0, 0};
+        for (size_t k = s[i]; k < e[i]; k++) bw_write(&w, rev[src[k]], lengths[src[k]]);
+        size_t start = bw_finish(&w), written = max_out - start;
+        if (off + written > cap) { free(scratch); *outcome = POR_OUT_DST_TOO_SMALL; return 0; }
+        if (written > 0xFFFFFFFFu) { free(scratch); *outcome = POR_OUT_LEN_OVERFLOW; return 0; }
+        memcpy(dst + off, scratch + start, written);
+        off += written;
+        lens[i] = (uint32_t)written;
+    }
+    free(scratch);
+    if (off >= len) { *outcome = POR_OUT_NOT_BENEFICIAL; return 0; }
+    for (int i = 0; i < 4; i++) st32(dst + jt + 4 * i, lens[i]);
+    *outcome = POR_OUT_ENCODED;
+    return (int64_t)off;
+}
+
+/* ------------------------------------------------------------------------- */
+/* Huffman decompress: entropy/huffman/decompress.rs:8-211, mod.rs:34-43      */
+/* ------------------------------------------------------------------------- */
+
+/* decompress.rs:152-211 */
+static int huf_tail(br_t *r, const uint16_t *table, uint64_t mask, uint8_t max_bits, uint8_t *out, size_t len) {
+    size_t i = 0;
+    while (i < len && r->bi >= 3) {
+        if (r->cnt < max_bits) br_refill(r);
+        out[i++] = br_decode(r, table, mask);
+    }
+    size_t tsize = (size_t)1 << max_bits;
+    while (i < len) {
+        size_t avail = br_avail(r);
+        if (avail == 0) return POR_EINVAL;
+        br_refill_to(r, max_bits);              /* peek_bits */
+        if (r->cnt == 0) return POR_EINVAL;
+        size_t idx = (size_t)(r->cont & (((uint64_t)1 << max_bits) - 1));
+        if (idx >= tsize) return POR_EINVAL;
+        uint16_t e = table[idx];
+        uint8_t nb = (uint8_t)(e >> 8), sym = (uint8_t)(e & 0xFF);
+        if ((size_t)nb > avail) return POR_EINVAL;
+        if (nb) {                               /* consume */
+            if (r->cnt < nb) br_refill_to(r, nb);
+            if (r->cnt < nb) return POR_EINVAL;
+            r->cont >>= nb; r->cnt = (uint8_t)(r->cnt - nb);
+        }
+        out[i++] = sym;
+    }
+    return 0;
+}
+
+int64_t por_huf_decompress(uint8_t *dst, size_t dst_len, const uint8_t *src, size_t src_len) {
+    uint8_t w[256];
+    int n = 0;
+    int64_t pos = por_huf_decode_weights(src, src_len, w, &n);
+    if (pos < 0) return POR_EINVAL;
+    uint8_t lengths[256] = {0};
+    for (int i = 0; i < n; i++) { if (w[i] > HUF_MAX_TABLE_LOG) return POR_EINVAL; lengths[i] = w[i]; }
+    uint16_t table[1 << HUF_MAX_TABLE_LOG];
+    int max_bits = por_huf_from_lengths(lengths, table, NULL);
+    if (!max_bits) return POR_EINVAL;
+    size_t p = (size_t)pos;
+    if (src_len - p < 16) return POR_EINVAL;
+    uint64_t lens[4], total = 0;
+    for (int i = 0; i < 4; i++) { lens[i] = ld32(src + p + 4 * i); total += lens[i]; }
+    p += 16;
+    if (total != (uint64_t)(src_len - p)) return POR_EINVAL;
+    br_t r[4];
+    size_t so = p;
+    for (int i = 0; i < 4; i++) { br_init(&r[i], src + so, (size_t)lens[i]); so += (size_t)lens[i]; }
+    size_t s[4], e[4];
+    por_split_four(dst_len, s, e);
+    uint64_t mask = ((uint64_t)1 << max_bits) - 1;
+    size_t op[4] = {s[0], s[1], s[2], s[3]}, fe[4];
+    for (int i = 0; i < 4; i++) fe[i] = e[i] >= 3 ? e[i] - 3 : 0;
+    while (op[0] < fe[0] && op[1] < fe[1] && op[2] < fe[2] && op[3] < fe[3] &&
+           r[0].bi >= 3 && r[1].bi >= 3 && r[2].bi >= 3 && r[3].bi >= 3) {
+        for (int round = 0; round < 2; round++) {
+            for (int i = 0; i < 4; i++) br_refill(&r[i]);
+            for (int k = 0; k < 2; k++)
+                for (int i = 0; i < 4; i++) dst[op[i]++] = br_decode(&r[i], table, mask);
+        }
+    }
+    for (int i = 0; i < 4; i++)
+        if (huf_tail(&r[i], table, mask, (uint8_t)max_bits, dst + op[i], e[i] - op[i]) < 0) return POR_EINVAL;
+    for (int i = 0; i < 4; i++) if (!br_exhausted(&r[i])) return POR_EINVAL;
+    return (int64_t)dst_len;
+}
+
+/* ------------------------------------------------------------------------- */
+/* rANS: entropy/rans/compress.rs, decompress.rs                              */
+/* ------------------------------------------------------------------------- */
+
+#define RANS_PROB_BITS 11
+#define RANS_PROB_SCALE (1u << RANS_PROB_BITS)
+#define RANS_L (1u << 23)
+
+/* compress.rs:72-122 */
+int por_rans_normalize(const uint32_t raw[256], uint16_t f[256], uint16_t cum[256]) {
+    uint64_t total = 0;
+    for (int i = 0; i < 256; i++) total += raw[i];
+    memset(f, 0, 512); memset(cum, 0, 512);
+    if (total == 0) return 0;
+    uint32_t assigned = 0;
+    int max_sym = 0, max_freq_sym = 0;
+    for (int i = 0; i < 256; i++) {
+        if (raw[i] > 0) {
+            uint64_t v = ((uint64_t)raw[i] * RANS_PROB_SCALE) / total;
+            if (v < 1) v = 1;
+            f[i] = (uint16_t)v;
+            assigned += f[i];
+            max_sym = i;
+            if (raw[i] > raw[max_freq_sym]) max_freq_sym = i;
+        }
+    }
+    if (assigned > RANS_PROB_SCALE) {
+        uint32_t excess = assigned - RANS_PROB_SCALE;
+        if ((uint32_t)f[max_freq_sym] > excess) f[max_freq_sym] = (uint16_t)(f[max_freq_sym] - excess);
+        else return 0;
+    } else if (assigned < RANS_PROB_SCALE) {
+        f[max_freq_sym] = (uint16_t)(f[max_freq_sym] + (RANS_PROB_SCALE - assigned));
+    }
+    uint16_t run = 0;
+    for (int i = 0; i <= max_sym; i++) { cum[i] = run; run = (uint16_t)(run + f[i]); }
+    return 1;
+}
+
+/* EncSymbol (compress.rs:35-68) and the reciprocal update (:164-165) */
+typedef struct { uint32_t freq, cmpl, bias, rcp, shift; } encsym_t;
+static encsym_t encsym(uint32_t start, uint32_t freq) {
+    encsym_t s;
+    s.freq = freq; s.cmpl = RANS_PROB_SCALE - freq;
+    if (freq < 2) { s.bias = start + RANS_PROB_SCALE - 1; s.rcp = 0xFFFFFFFFu; s.shift = 0; }
+    else {
+        uint32_t sh = 0;
+        while (freq > (1u << sh)) sh++;
+        s.rcp = (uint32_t)((((uint64_t)1 << (sh + 31)) + freq - 1) / freq);
+        s.bias = start; s.shift = sh - 1;
+    }
+    return s;
+}
+static uint32_t encsym_update(const encsym_t *s, uint32_t x) {
+    uint32_t q = (uint32_t)(((uint64_t)x * s->rcp) >> 32) >> s->shift;
+    return x + s->bias + q * s->cmpl;
+}
+uint32_t por_rans_enc_update(uint32_t x, uint32_t start, uint32_t freq) {
+    encsym_t s = encsym(start, freq);
+    return encsym_update(&s, x);
+}
+
+/* compress.rs:187-260 */
+int64_t por_rans_compress(uint8_t *dst, size_t cap, const uint8_t *src, size_t len, int *outcome) {
+    *outcome = POR_OUT_INCOMPRESSIBLE;
+    if (len == 0) return 0;
+    uint32_t raw[256];
+    por_histogram(src, len, raw);
+    uint16_t f[256], cum[256];
+    if (!por_rans_normalize(raw, f, cum)) return 0;
+    encsym_t syms[256];
+    for (int i = 0; i < 256; i++) syms[i] = encsym(cum[i], f[i]);
+    /* encode_freq_table (compress.rs:128-135) */
+    int max_sym = 0;
+    for (int i = 0; i < 256; i++) if (f[i]) max_sym = i;
+    size_t jt = 1 + 2 * (size_t)(max_sym + 1), header_len = jt + 16;
+    if (header_len >= cap) { *outcome = POR_OUT_DST_TOO_SMALL; return 0; }
+    dst[0] = (uint8_t)max_sym;
+    for (int i = 0; i <= max_sym; i++) { dst[1 + 2 * i] = (uint8_t)f[i]; dst[2 + 2 * i] = (uint8_t)(f[i] >> 8); }
+    memset(dst + jt, 0, 16);
+    size_t s[4], e[4];
+    por_split_four(len, s, e);
+    size_t max_seg = 0;
+    for (int i = 0; i < 4; i++) if (e[i] - s[i] > max_seg) max_seg = e[i] - s[i];
+    size_t scap = 4 + 2 * max_seg + 16;
+    uint8_t *scratch = (uint8_t *)malloc(scap);
+    if (!scratch) return POR_ESMALL;
+    uint32_t lens[4];
+    size_t off = header_len;
+    for (int i = 0; i < 4; i++) {
+        /* encode_stream_into (compress.rs:140-185) */
+        uint32_t x = RANS_L;
+        size_t nb = 4;
+        for (size_t k = e[i]; k > s[i]; k--) {
+            const encsym_t *sy = &syms[src[k - 1]];
+            uint32_t max_state = ((RANS_L >> RANS_PROB_BITS) << 8) * sy->freq;
+            while (x >= max_state) {
+                if (nb >= scap) { scap *= 2; scratch = (uint8_t *)realloc(scratch, scap); }
+                scratch[nb++] = (uint8_t)(x & 0xFF);
+                x >>= 8;
+            }
+            x = encsym_update(sy, x);
+        }
+        st32(scratch, x);
+        for (size_t a = 4, b = nb - 1; a < b; a++, b--) { uint8_t t = scratch[a]; scratch[a] = scratch[b]; scratch[b] = t; }
+        size_t written = nb;
+        if (off + written > cap) { free(scratch); *outcome = POR_OUT_DST_TOO_SMALL; return 0; }
+        if (written > 0xFFFFFFFFu) { free(scratch); *outcome = POR_OUT_LEN_OVERFLOW; return 0; }
+        memcpy(dst + off, scratch, written);
+        off += written;
+        lens[i] = (uint32_t)written;
+    }
+    free(scratch);
+    if (off >= len) { *outcome = POR_OUT_NOT_BENEFICIAL; return 0; }
+    for (int i = 0; i < 4; i++) st32(dst + jt + 4 * i, lens[i]);
+    *outcome = POR_OUT_ENCODED;
+    return (int64_t)off;
+}
+
+/* decompress.rs:113-166 */
+int64_t por_rans_decompress(uint8_t *dst, size_t dst_len, const uint8_t *src, size_t src_len) {
+    /* decode_freq_table :24-52 */
+    if (src_len == 0) return POR_EINVAL;
+    size_t max_sym = src[0], need = 1 + 2 * (max_sym + 1);
+    if (src_len < need) return POR_EINVAL;
+    uint16_t f[256] = {0};
+    uint32_t tot = 0;
+    for (size_t i = 0; i <= max_sym; i++) { f[i] = (uint16_t)(src[1 + 2 * i] | (src[2 + 2 * i] << 8)); tot += f[i]; }
+    if (tot != RANS_PROB_SCALE) return POR_EINVAL;
+    size_t p = need;
+    if (src_len - p < 16) return POR_EINVAL;
+    uint64_t lens[4], total = 0;
+    for (int i = 0; i < 4; i++) { lens[i] = ld32(src + p + 4 * i); total += lens[i]; }
+    p += 16;
+    if (total != (uint64_t)(src_len - p)) return POR_EINVAL;
+    /* build_decode_table :55-77 */
+    uint8_t tsym[RANS_PROB_SCALE];
+    uint16_t tfreq[RANS_PROB_SCALE], tstart[RANS_PROB_SCALE];
+    uint32_t pos = 0;
+    for (int s = 0; s < 256; s++) {
+        for (uint32_t j = 0; j < f[s]; j++) { tsym[pos + j] = (uint8_t)s; tfreq[pos + j] = f[s]; tstart[pos + j] = (uint16_t)pos; }
+        pos += f[s];
+    }
+    size_t s[4], e[4];
+    por_split_four(dst_len, s, e);
+    size_t so = p;
+    for (int i = 0; i < 4; i++) {
+        const uint8_t *st = src + so;
+        size_t sl = (size_t)lens[i];
+        so += sl;
+        if (s[i] == e[i]) continue;
+        /* decode_stream :80-111 */
+        if (sl < 4) return POR_EINVAL;
+        uint32_t x = ld32(st);
+        size_t q = 4;
+        for (size_t k = s[i]; k < e[i]; k++) {
+            uint32_t idx = x & (RANS_PROB_SCALE - 1);
+            dst[k] = tsym[idx];
+            x = (uint32_t)tfreq[idx] * (x >> RANS_PROB_BITS) + idx - tstart[idx];
+            while (x < RANS_L) {
+                if (q >= sl) return POR_EINVAL;
+                x = (x << 8) | st[q++];
+            }
+        }
+    }
+    return (int64_t)dst_len;
+}
+
+/* ------------------------------------------------------------------------- */
+/* plane codec payloads: codecs/huffman.rs:37-141, codecs/rans.rs:38-144,    */
+/* codec_tagged.rs:98-194, codecs/length_prefix.rs:30-33, codecs/identity.rs  */
+/* ------------------------------------------------------------------------- */
+
+size_t por_codec_encode_bound(size_t len) { return len + 5; }
+
+static int length_prefix_accepted(size_t decoded_len, size_t body_len) {
+    if (decoded_len > 0xFFFFFFFFu) return 0;
+    return decoded_len <= ((size_t)1 << 30) || decoded_len <= body_len * 64;
+}
+
+static int64_t emit_raw(const uint8_t *plane, size_t len, uint8_t *out, size_t cap) {
+    if (1 + len > cap) return POR_ESMALL;
+    out[0] = 0;
+    if (len) memcpy(out + 1, plane, len);
+    return (int64_t)(1 + len);
+}
+
+int64_t por_codec_encode(int codec, const uint8_t *plane, size_t len, uint8_t *out, size_t cap) {
+    if (codec == POR_CODEC_IDENTITY) {
+        if (len > cap) return POR_ESMALL;
+        if (len) memcpy(out, plane, len);
+        return (int64_t)len;
+    }
+    if (codec != POR_CODEC_HUFFMAN && codec != POR_CODEC_RANS) return POR_EUNSUP;
+    if (len == 0) { if (cap < 1) return POR_ESMALL; out[0] = 0; return 1; }
+    size_t bound = len * 2 + 4096;          /* huffman_output_bound / rans_output_bound */
+    uint8_t *buf = (uint8_t *)malloc(bound);
+    if (!buf) return POR_ESMALL;
+    int outcome;
+    int64_t n = codec == POR_CODEC_HUFFMAN ? por_huf_compress(buf, bound, plane, len, &outcome)
+                                           : por_rans_compress(buf, bound, plane, len, &outcome);
+    int64_t r;
+    if (n < 0) r = n;
+    else if (outcome == POR_OUT_ENCODED && len <= 0xFFFFFFFFu &&
+             (codec == POR_CODEC_HUFFMAN || length_prefix_accepted(len, (size_t)n))) {
+        if ((size_t)n + 5 > cap) r = POR_ESMALL;
+        else {
+            out[0] = 1; st32(out + 1, (uint32_t)len);
+            memcpy(out + 5, buf, (size_t)n);
+            r = n + 5;
+        }
+    } else r = emit_raw(plane, len, out, cap);
+    free(buf);
+    return r;
+}
+
+int64_t por_codec_decoded_len(int codec, const uint8_t *payload, size_t len) {
+    if (codec == POR_CODEC_IDENTITY) return (int64_t)len;
+    if (len == 0) return POR_EINVAL;
+    if (payload[0] == 0) return (int64_t)(len - 1);
+    if (payload[0] != 1 || len < 5) return POR_EINVAL;
+    return (int64_t)ld32(payload + 1);
+}
+
+int64_t por_codec_decode(int codec, const uint8_t *pl, size_t len, uint8_t *out, size_t cap) {
+    if (codec == POR_CODEC_IDENTITY) {            /* identity.rs decode + check_decoded_len */
+        if (len > cap) return POR_EINVAL;
+        if (len) memcpy(out, pl, len);
+        return (int64_t)len;
+    }
+    if (codec != POR_CODEC_HUFFMAN && codec != POR_CODEC_RANS) return POR_EUNSUP;
+    if (len == 0) return POR_EINVAL;
+    uint8_t tag = pl[0];
+    if (tag == 0) {
+        if (len - 1 > cap) return POR_EINVAL;
+        if (len > 1) memcpy(out, pl + 1, len - 1);
+        return (int64_t)(len - 1);
+    }
+    if (tag != 1) return POR_EINVAL;
+    if (len - 1 < 4) return POR_EINVAL;
+    size_t orig = ld32(pl + 1);
+    const uint8_t *enc = pl + 5;
+    size_t enc_len = len - 5;
+    if (codec == POR_CODEC_HUFFMAN) {
+        if (orig > enc_len * 32 + 4096) return POR_EINVAL;   /* huffman.rs:122-131 */
+        if (orig > cap) return POR_EINVAL;                    /* check_decoded_len */
+        return por_huf_decompress(out, orig, enc, enc_len);
+    }
+    /* rANS: decode_bounded's check_within runs first (rans.rs:158-160) */
+    if (orig > cap) return POR_EINVAL;
+    if (!length_prefix_accepted(orig, enc_len)) return POR_EINVAL;
+    if (orig == 0) return 0;                                  /* decode_tagged expected_len == 0 */
+    return por_rans_decompress(out, orig, enc, enc_len);
+}
+
+/* ------------------------------------------------------------------------- */
+/* chunk framing: compressor.rs:316-381, container.rs:1975-2050               */
+/* ------------------------------------------------------------------------- */
+
+int64_t por_encode_plane_chunked(int codec, const uint8_t *plane, size_t len, uint32_t chunk_size,
+                                 uint8_t *out, size_t cap, uint32_t *ent, size_t max_ent, size_t *n_chunks) {
+    size_t cs = chunk_size ? chunk_size : 1;
+    size_t nch = len == 0 ? 1 : (len + cs - 1) / cs;
+    if (nch > max_ent) return POR_ESMALL;
+    size_t off = 0;
+    for (size_t k = 0; k < nch; k++) {
+        size_t a = k * cs, b = a + cs > len ? len : a + cs;
+        if (off > 0xFFFFFFFFu) return POR_EINVAL;
+        if (off + 5 > cap) return POR_ESMALL;
+        out[off] = 0; st32(out + off + 1, 0);      /* frame_chunk: [ver=0][state_len=0] */
+        int64_t n = por_codec_encode(codec, plane + a, b - a, out + off + 5, cap - off - 5);
+        if (n < 0) return n;
+        ent[2 * k] = (uint32_t)off; ent[2 * k + 1] = (uint32_t)(b - a);
+        off += 5 + (size_t)n;
+    }
+    *n_chunks = nch;
+    return (int64_t)off;
+}
+
+static int64_t decode_one_chunk(int codec, const uint8_t *payload, size_t payload_len, const uint32_t *ent,
+                                size_t n_chunks, size_t i, uint8_t *dst) {
+    size_t start = ent[2 * i], end = i + 1 < n_chunks ? ent[2 * (i + 1)] : payload_len;
+    if (start > end || end > payload_len) return POR_EINVAL;
+    const uint8_t *fr = payload + start;
+    size_t fl = end - start;
+    if (fl < 5) return POR_EINVAL;
+    size_t sl = ld32(fr + 1);
+    if (fl - 5 < sl) return POR_EINVAL;
+    size_t want = ent[2 * i + 1];
+    int64_t n = por_codec_decode(codec, fr + 5 + sl, fl - 5 - sl, dst, want);
+    if (n < 0) return n;
+    if ((size_t)n != want) return POR_EINVAL;
+    return n;
+}
+
+int64_t por_decode_plane_chunked(int codec, const uint8_t *payload, size_t payload_len, const uint32_t *ent,
+                                 size_t n_chunks, uint8_t *out, size_t cap) {
+    size_t total = 0;
+    for (size_t i = 0; i < n_chunks; i++) total += ent[2 * i + 1];
+    if (total > cap) return POR_EINVAL;
+    size_t o = 0;
+    for (size_t i = 0; i < n_chunks; i++) {
+        int64_t n = decode_one_chunk(codec, payload, payload_len, ent, n_chunks, i, out + o);
+        if (n < 0) return n;
+        o += (size_t)n;
+    }
+    return (int64_t)o;
+}
+
+typedef struct {
+    int codec; const uint8_t *payload; size_t payload_len; const uint32_t *ent; size_t n;
+    const size_t *dst_off; uint8_t *out; size_t next; pthread_mutex_t *mu; int64_t err;
+} mt_job_t;
+
+static void *mt_worker(void *arg) {
+    mt_job_t *j = (mt_job_t *)arg;
+    for (;;) {
+        pthread_mutex_lock(j->mu);
+        size_t i = j->next++;
+        pthread_mutex_unlock(j->mu);
+        if (i >= j->n) break;
+        int64_t r = decode_one_chunk(j->codec, j->payload, j->payload_len, j->ent, j->n, i, j->out + j->dst_off[i]);
+        if (r < 0) { pthread_mutex_lock(j->mu); j->err = r; pthread_mutex_unlock(j->mu); }
+    }
+    return NULL;
+}
+
+int64_t por_decode_plane_chunked_mt(int codec, const uint8_t *payload, size_t payload_len, const uint32_t *ent,
+                                    size_t n_chunks, uint8_t *out, size_t cap, int threads) {
+    if (threads <= 1) return por_decode_plane_chunked(codec, payload, payload_len, ent, n_chunks, out, cap);
+    size_t *dst_off = (size_t *)malloc((n_chunks + 1) * sizeof(size_t));
+    if (!dst_off) return POR_ESMALL;
+    size_t total = 0;
+    for (size_t i = 0; i < n_chunks; i++) { dst_off[i] = total; total += ent[2 * i + 1]; }
+    if (total > cap) { free(dst_off); return POR_EINVAL; }
+    pthread_mutex_t mu = PTHREAD_MUTEX_INITIALIZER;
+    mt_job_t job = {codec, payload, payload_len, ent, n_chunks, dst_off, out, 0, &mu, 0};
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
+    for (int t = 0; t < threads; t++) pthread_create(&th[t], NULL, mt_worker, &job);
+    for (int t = 0; t < threads; t++) pthread_join(th[t], NULL);
+    free(th); free(dst_off);
+    return job.err ? job.err : (int64_t)total;
+}
+
+/* ------------------------------------------------------------------------- */
+/* CRC-32/ISO-HDLC (crc32fast 1.5.0), reflected poly 0xEDB88320              */
+/* ------------------------------------------------------------------------- */
+
+uint32_t por_crc32(uint32_t crc, const uint8_t *d, size_t len) {
+    static uint32_t tab[256];
+    static int init = 0;
+    if (!init) {
+        for (uint32_t i = 0; i < 256; i++) {
+            uint32_t c = i;
+            for (int k = 0; k < 8; k++) c = (c & 1) ? (c >> 1) ^ 0xEDB88320u : c >> 1;
+            tab[i] = c;
+        }
+        init = 1;
+    }
+    crc = ~crc;
+    for (size_t i = 0; i < len; i++) crc = tab[(crc ^ d[i]) & 0xFF] ^ (crc >> 8);
+    return ~crc;
+}
+
+/* ------------------------------------------------------------------------- */
+/* XXH64 (xxhash-rust 0.8.18 / XXH 0.8), from the published specification     */
+/* ------------------------------------------------------------------------- */
+
+#define XP1 11400714785074694791ULL
+#define XP2 14029467366897019727ULL
+#define XP3 1609587929392839161ULL
+#define XP4 9650029242287828579ULL
+#define XP5 2870177450012600261ULL
+static uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
+static uint64_t ld64(const uint8_t *p) { return (uint64_t)ld32(p) | ((uint64_t)ld32(p + 4) << 32); }
+static uint64_t xround(uint64_t acc, uint64_t in) { acc += in * XP2; acc = rotl64(acc, 31); return acc * XP1; }
+static uint64_t xmerge(uint64_t acc, uint64_t v) { acc ^= xround(0, v); return acc * XP1 + XP4; }
+
+uint64_t por_xxh64(const uint8_t *p, size_t len, uint64_t seed) {
+    const uint8_t *end = p + len;
+    uint64_t h;
+    if (len >= 32) {
+        uint64_t v1 = seed + XP1 + XP2, v2 = seed + XP2, v3 = seed, v4 = seed - XP1;
+        const uint8_t *lim = end - 32;
+        do {
+            v1 = xround(v1, ld64(p)); v2 = xround(v2, ld64(p + 8));
+            v3 = xround(v3, ld64(p + 16)); v4 = xround(v4, ld64(p + 24));
+            p += 32;
+        } while (p <= lim);
+        h = rotl64(v1, 1) + rotl64(v2, 7) + rotl64(v3, 12) + rotl64(v4, 18);
+        h = xmerge(h, v1); h = xmerge(h, v2); h = xmerge(h, v3); h = xmerge(h, v4);
+    } else h = seed + XP5;
+    h += (uint64_t)len;
+    while (p + 8 <= end) { h ^= xround(0, ld64(p)); h = rotl64(h, 27) * XP1 + XP4; p += 8; }
+    if (p + 4 <= end) { h ^= (uint64_t)ld32(p) * XP1; h = rotl64(h, 23) * XP2 + XP3; p += 4; }
+    while (p < end) { h ^= (*p) * XP5; h = rotl64(h, 11) * XP1; p++; }
+    h ^= h >> 33; h *= XP2; h ^= h >> 29; h *= XP3; h ^= h >> 32;
+    return h;
+}
+
+/* ------------------------------------------------------------------------- */
+/* BLAKE3 (hash mode), from the published specification (used for canonical  */
+/* extension ids, extension/id.rs:21-30)                                      */
+/* ------------------------------------------------------------------------- */
+
+static const uint32_t B3_IV[8] = {0x6A09E667u, 0xBB67AE85u, 0x3C6EF372u, 0xA54FF53Au,
+                                  0x510E527Fu, 0x9B05688Cu, 0x1F83D9ABu, 0x5BE0CD19u};
+static const int B3_PERM[16] = {2, 6, 3, 10, 7, 0, 4, 13, 1, 11, 12, 5, 9, 14, 15, 8};
+#define B3_CHUNK_START 1u
+#define B3_CHUNK_END 2u
+#define B3_PARENT 4u
+#define B3_ROOT 8u
+static uint32_t rotr32(uint32_t x, int r) { return (x >> r) | (x << (32 - r)); }
+static void b3_g(uint32_t *s, int a, int b, int c, int d, uint32_t mx, uint32_t my) {
+    s[a] = s[a] + s[b] + mx; s[d] = rotr32(s[d] ^ s[a], 16);
+    s[c] = s[c] + s[d]; s[b] = rotr32(s[b] ^ s[c], 12);
+    s[a] = s[a] + s[b] + my; s[d] = rotr32(s[d] ^ s[a], 8);
+    s[c] = s[c] + s[d]; s[b] = rotr32(s[b] ^ s[c], 7);
+}
+static void b3_compress(const uint32_t cv[8], const uint32_t block[16], uint64_t counter, uint32_t blen,
+                        uint32_t flags, uint32_t out[16]) {
+    uint32_t s[16], m[16], t[16];
+    for (int i = 0; i < 8; i++) s[i] = cv[i];
+    for (int i = 0; i < 4; i++) s[8 + i] = B3_IV[i];
+    s[12] = (uint32_t)counter; s[13] = (uint32_t)(counter >> 32); s[14] = blen; s[15] = flags;
+    memcpy(m, block, 64);
+    for (int r = 0; r < 7; r++) {
+        b3_g(s, 0, 4, 8, 12, m[0], m[1]); b3_g(s, 1, 5, 9, 13, m[2], m[3]);
+        b3_g(s, 2, 6, 10, 14, m[4], m[5]); b3_g(s, 3, 7, 11, 15, m[6], m[7]);
+        b3_g(s, 0, 5, 10, 15, m[8], m[9]); b3_g(s, 1, 6, 11, 12, m[10], m[11]);
+        b3_g(s, 2, 7, 8, 13, m[12], m[13]); b3_g(s, 3, 4, 9, 14, m[14], m[15]);
+        if (r < 6) { for (int i = 0; i < 16; i++) t[i] = m[B3_PERM[i]]; memcpy(m, t, 64); }
+    }
+    for (int i = 0; i < 8; i++) { out[i] = s[i] ^ s[i + 8]; out[i + 8] = s[i + 8] ^ cv[i]; }
+}
+/* chaining value of one chunk (<= 1024 bytes); when root, returns the root output block */
+static void b3_chunk(const uint32_t key[8], const uint8_t *d, size_t len, uint64_t ctr, int root, uint32_t out[16]) {
+    uint32_t cv[8], blk[16], o[16];
+    memcpy(cv, key, 32);
+    size_t nblocks = len == 0 ? 1 : (len + 63) / 64;
+    for (size_t b = 0; b < nblocks; b++) {
+        uint8_t buf[64] = {0};
+        size_t bl = len - b * 64 > 64 ? 64 : len - b * 64;
+        if (len == 0) bl = 0;
+        memcpy(buf, d + b * 64, bl);
+        for (int i = 0; i < 16; i++) blk[i] = ld32(buf + 4 * i);
+        uint32_t fl = (b == 0 ? B3_CHUNK_START : 0) | (b == nblocks - 1 ? B3_CHUNK_END : 0);
+        if (b == nblocks - 1 && root) fl |= B3_ROOT;
+        b3_compress(cv, blk, ctr, (uint32_t)bl, fl, o);
+        memcpy(cv, o, 32);
+        if (b == nblocks - 1) memcpy(out, o, 64);
+    }
+}
+/* hash of a subtree of whole chunks, returning its chaining value */
+static void b3_subtree(const uint8_t *d, size_t len, uint64_t ctr, int root, uint32_t out[16]) {
+    if (len <= 1024) { b3_chunk(B3_IV, d, len, ctr, root, out); return; }
+    /* left subtree holds the largest power-of-two number of chunks < total */
+    size_t chunks = (len + 1023) / 1024, lc = 1;
+    while (lc * 2 < chunks) lc *= 2;
+    uint32_t l[16], r[16], blk[16];
+    b3_subtree(d, lc * 1024, ctr, 0, l);
+    b3_subtree(d + lc * 1024, len - lc * 1024, ctr + lc, 0, r);
+    memcpy(blk, l, 32); memcpy(blk + 8, r, 32);
+    b3_compress(B3_IV, blk, 0, 64, B3_PARENT | (root ? B3_ROOT : 0), out);
+}
+void por_blake3(const uint8_t *d, size_t len, uint8_t out[32]) {
+    uint32_t o[16];
+    b3_subtree(d, len, 0, 1, o);
+    for (int i = 0; i < 8; i++) st32(out + 4 * i, o[i]);
+}
