@@ -1,0 +1,127 @@
+/*
+ * ptwm_mi355x.h -- C ABI of libptwm_mi355x.so, the MI355X (gfx950) plane
+ * codec library for PTWM.
+ *
+ * Section 1 is the reference's native extension ABI, symbol for symbol: the
+ * loader in crates/ptwm-core/src/flavor/native.rs resolves these names with
+ * dlopen (native.rs:143-146, 239-311) and calls them with the signatures
+ * given there.  Section 2 holds this library's own additions; the reference
+ * has no counterpart for them.
+ *
+ * Return convention (native.rs:634-657): >= 0 is the number of bytes written
+ * (never more than the stated capacity); -1 invalid input, -2 buffer too
+ * small, -3 missing capability, -4 missing native dependency, -5 unsupported,
+ * any other negative value an internal error.
+ *
+ * Device ("_cuda") entry points take device addresses as u64 and a device
+ * ordinal.  They run on the library's own per-device stream (the handle the
+ * *_stream_handle symbols return) and synchronise it before returning, so
+ * the output is complete and visible to any stream when they return
+ * (native.rs:152-162).  Input and output must be distinct allocations.
+ * Calls on one device are serialised internally.
+ */
+#ifndef PTWM_MI355X_H
+#define PTWM_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===================================================================== */
+/* 1. Reference native extension ABI                                      */
+/* ===================================================================== */
+
+/* Host-buffer plane codec, PlaneCodecFn (native.rs:62-67).  The codec is this
+ * extension's own wire format ("huff_ilv", see DESIGN/INTEGRATION docs):
+ * encode/decode run on device 0 through staging copies.  Encode returns -2
+ * when out_len is too small. */
+int64_t ptwm_plane_codec_v1_encode(const uint8_t *in, size_t in_len, uint8_t *out, size_t out_len);
+int64_t ptwm_plane_codec_v1_decode(const uint8_t *in, size_t in_len, uint8_t *out, size_t out_len);
+
+/* PlaneCodecStatefulFn (native.rs:75-83).  The codec carries no state: any
+ * state_len other than 0 is rejected with -1. */
+int64_t ptwm_plane_codec_v1_decode_stateful(uint8_t state_format_version, const uint8_t *state_ptr,
+                                            size_t state_len, const uint8_t *in, size_t in_len,
+                                            uint8_t *out, size_t out_cap);
+
+/* PlaneCodecCudaStreamHandleFn (native.rs:150): the library's hipStream_t for
+ * the device as an integer, 0 if the device is unavailable. */
+uint64_t ptwm_plane_codec_v1_cuda_stream_handle(uint32_t device_ordinal);
+
+/* PlaneCodecCudaDecodeFn (native.rs:163-174).  codec_id is a 32-byte
+ * canonical id naming the payload's wire format:
+ *   built-in identity / huffman / rans (ids derived for versions 1.0.0 and
+ *   1.1.0, extension/builtins.rs:18-27) -> the reference plane payloads of
+ *   codecs/identity.rs, codecs/huffman.rs:50-87, codecs/rans.rs:50-94;
+ *   this extension's plane codec id -> its own "huff_ilv" payload.
+ * Returns the decoded length; -2 if out_cap is smaller than the payload
+ * declares; -1 for malformed payloads (exactly where the reference decoder
+ * returns an error). */
+int64_t ptwm_plane_codec_v1_decode_cuda(uint8_t state_format_version, const uint8_t *state_ptr,
+                                        size_t state_len, const uint8_t *codec_id_ptr, size_t codec_id_len,
+                                        uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                                        size_t out_cap, uint32_t device_ordinal);
+
+/* PlaneCodecCudaEncodeFn (native.rs:185-197).  Same codec ids as decode; the
+ * built-in formats are produced byte-identical to the reference encoder.
+ * When out_cap is too small, writes the needed size to *needed_out and
+ * returns -2. */
+int64_t ptwm_plane_codec_v1_encode_cuda(uint8_t state_format_version, const uint8_t *state_ptr,
+                                        size_t state_len, const uint8_t *codec_id_ptr, size_t codec_id_len,
+                                        uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                                        size_t out_cap, uint64_t *needed_out, uint32_t device_ordinal);
+
+/* HardwareBackendCudaStreamHandleFn (native.rs:105-111). */
+uint64_t ptwm_hardware_backend_v1_cuda_stream_handle(uint32_t device_ordinal);
+
+/* HardwareBackendCudaDispatchDecodeFn (native.rs:112-141): tensor-level
+ * decode.  codec_id must be this library's decode-plan id; state_ptr holds a
+ * decode plan (PTMD v1, layout in INTEGRATION.md) describing one or more
+ * tensors as the container stores them: chain, and per plane codec id,
+ * payload offset/length inside the input buffer, decoded length, optional
+ * CRC32 and chunk table.  Every tensor is restored (entropy decode + inverse
+ * chain) into the output buffer at its stated offset.  Returns the number of
+ * restored bytes. */
+int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_version, const uint8_t *state_ptr,
+                                                      size_t state_len, const uint8_t *codec_id_ptr,
+                                                      size_t codec_id_len, uint64_t in_dev_ptr, size_t in_len,
+                                                      uint64_t out_dev_ptr, size_t out_len,
+                                                      uint32_t device_ordinal);
+
+/* ===================================================================== */
+/* 2. Library additions (no counterpart in the reference)                 */
+/* ===================================================================== */
+
+/* ABI revision of this library (bumped on any incompatible change). */
+uint32_t ptwm_mi355x_abi_version(void);
+
+/* The canonical ids this library recognises: which = 0 own plane codec,
+ * 1 hardware backend, 2 decode-plan format.  Writes 32 bytes; returns 0 or -1. */
+int64_t ptwm_mi355x_canonical_id(uint32_t which, uint8_t *out32);
+
+/* Forward chain (bit reorder + byte/nibble split) on device: the tensor at
+ * in_dev (in_len bytes) is split into planes[0..n) of plane_len bytes each.
+ * chain: 1 ieee16/2-way, 2 ieee32/4-way, 3 e4m3/nibble, 4 e5m2/nibble,
+ * 5 nibble split, 6 passthrough.  All addresses 16-byte aligned.  Returns the
+ * plane length. */
+int64_t ptwm_mi355x_split_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, const uint64_t *plane_dev_ptrs,
+                               uint32_t n_planes, uint32_t device_ordinal);
+
+/* Inverse chain (merge + bit revert) on device.  Returns the tensor length. */
+int64_t ptwm_mi355x_merge_cuda(uint32_t chain, const uint64_t *plane_dev_ptrs, uint32_t n_planes, size_t plane_len,
+                               uint64_t out_dev_ptr, size_t out_cap, uint32_t device_ordinal);
+
+/* Kernel timing with HIP events recorded on the library stream around each
+ * phase of the next calls on the device (off by default). */
+int64_t ptwm_mi355x_set_profiling(uint32_t device_ordinal, uint32_t on);
+/* Durations of the last profiled call in milliseconds: out3[0] entropy-decode
+ * kernel(s), out3[1] merge kernel(s), out3[2] both. */
+int64_t ptwm_mi355x_last_kernel_ms(uint32_t device_ordinal, float *out3);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

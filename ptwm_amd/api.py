@@ -1,0 +1,119 @@
+"""Python entry points mirroring the reference's PyO3 device API.
+
+Same names, argument meaning and error behaviour as
+``crates/ptwm-py/src/plane_codec_cuda.rs:74-190`` and
+``crates/ptwm-py/src/hardware.rs:55-154``, backed by libptwm_mi355x.so:
+
+- ``plane_codec_encode_cuda(selector, codec_id, state_bytes, src, dst, device_ordinal)``
+- ``plane_codec_decode_cuda(selector, codec_id, state_bytes, src, dst, device_ordinal)``
+- ``hardware_backend_cuda_stream_handle(canonical_id, device_ordinal)``
+- ``hardware_backend_dispatch_decode_cuda(canonical_id, codec_id, state_bytes, compressed, out, device_ordinal)``
+
+``src``/``dst`` are contiguous ``torch.Tensor`` objects resident on the
+device.  As in the reference, each tensor is exported with
+``__dlpack__(stream=<library stream>)`` so that torch orders its pending
+work before the library's stream touches the memory; the device ordinal of
+every tensor must equal ``device_ordinal`` (plane_codec_cuda.rs:120-124).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+from . import ids
+from ._native import NativeError, check, lib
+
+
+def _dev_ptr_len(t, name: str, device_ordinal: int, stream: int, writable: bool):
+    if not hasattr(t, "__dlpack__") or not hasattr(t, "data_ptr"):
+        raise TypeError(f"{name}: expected a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: tensor is not on a GPU device")
+    if t.device.index != device_ordinal:
+        raise ValueError(f"{name}: tensor is on device {t.device.index}, call names device {device_ordinal}")
+    # stream-ordered hand-off, like the reference's __dlpack__(stream=...)
+    t.__dlpack__(stream=stream)
+    return int(t.data_ptr()), int(t.numel() * t.element_size())
+
+
+def _resolve_own(selector: str, label: str) -> None:
+    got = ids.resolve_codec_selector(selector)
+    if got.hex() != ids.OWN_IDS[label]:
+        raise LookupError(f"selector {selector!r} does not name this library's {label}")
+
+
+def plane_codec_decode_cuda(selector: str, codec_id: str, state_bytes: bytes, src, dst,
+                            device_ordinal: int, policy=None) -> int:
+    _resolve_own(selector, ids.PLANE_CODEC_LABEL)
+    codec = ids.resolve_codec_selector(codec_id)
+    L = lib()
+    stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
+    if stream == 0:
+        raise NativeError(-5, "plane_codec_decode_cuda: no stream for device")
+    ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)
+    op, ol = _dev_ptr_len(dst, "dst", device_ordinal, stream, True)
+    st = bytes(state_bytes)
+    rc = L.ptwm_plane_codec_v1_decode_cuda(1, st if st else None, len(st), codec, 32, ip, il, op, ol,
+                                           device_ordinal)
+    return check(rc, "plane_codec_decode_cuda")
+
+
+def plane_codec_encode_cuda(selector: str, codec_id: str, state_bytes: bytes, src, dst,
+                            device_ordinal: int, policy=None) -> int:
+    _resolve_own(selector, ids.PLANE_CODEC_LABEL)
+    codec = ids.resolve_codec_selector(codec_id)
+    L = lib()
+    stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
+    if stream == 0:
+        raise NativeError(-5, "plane_codec_encode_cuda: no stream for device")
+    ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)
+    op, ol = _dev_ptr_len(dst, "dst", device_ordinal, stream, True)
+    st = bytes(state_bytes)
+    needed = C.c_uint64(0)
+    rc = L.ptwm_plane_codec_v1_encode_cuda(1, st if st else None, len(st), codec, 32, ip, il, op, ol,
+                                           C.byref(needed), device_ordinal)
+    if rc == -2:
+        err = NativeError(rc, f"plane_codec_encode_cuda: needs {needed.value} bytes")
+        err.needed = needed.value
+        raise err
+    return check(rc, "plane_codec_encode_cuda")
+
+
+def hardware_backend_cuda_stream_handle(canonical_id: str, device_ordinal: int, policy=None) -> int:
+    _resolve_own(canonical_id, ids.HARDWARE_BACKEND_LABEL)
+    h = int(lib().ptwm_hardware_backend_v1_cuda_stream_handle(device_ordinal))
+    if h == 0:
+        raise NativeError(-5, "hardware backend failed to produce a stream handle")
+    return h
+
+
+def hardware_backend_dispatch_decode_cuda(canonical_id: str, codec_id: str, state_bytes: bytes, compressed, out,
+                                          device_ordinal: int, policy=None) -> int:
+    stream = hardware_backend_cuda_stream_handle(canonical_id, device_ordinal)
+    codec = ids.resolve_codec_selector(codec_id)
+    ip, il = _dev_ptr_len(compressed, "compressed", device_ordinal, stream, False)
+    op, ol = _dev_ptr_len(out, "out", device_ordinal, stream, True)
+    st = bytes(state_bytes)
+    rc = lib().ptwm_hardware_backend_v1_dispatch_decode_cuda(1, st if st else None, len(st), codec, 32, ip, il, op,
+                                                             ol, device_ordinal)
+    return check(rc, "hardware_backend_dispatch_decode_cuda")
+
+
+def split_cuda(chain: int, src, planes, device_ordinal: int = 0) -> int:
+    """Forward chain on device (library addition)."""
+    L = lib()
+    stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
+    ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)
+    arr = (C.c_uint64 * len(planes))(*[_dev_ptr_len(p, "plane", device_ordinal, stream, True)[0] for p in planes])
+    return check(L.ptwm_mi355x_split_cuda(chain, ip, il, arr, len(planes), device_ordinal), "split_cuda")
+
+
+def merge_cuda(chain: int, planes, out, device_ordinal: int = 0) -> int:
+    """Inverse chain on device (library addition)."""
+    L = lib()
+    stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
+    ptrs = [_dev_ptr_len(p, "plane", device_ordinal, stream, False) for p in planes]
+    op, ol = _dev_ptr_len(out, "out", device_ordinal, stream, True)
+    arr = (C.c_uint64 * len(planes))(*[p[0] for p in ptrs])
+    return check(L.ptwm_mi355x_merge_cuda(chain, arr, len(planes), ptrs[0][1], op, ol, device_ordinal), "merge_cuda")

@@ -1,0 +1,304 @@
+// abi.hip -- extern "C" entry points of libptwm_mi355x.so.
+//
+// The reference's native extension ABI (crates/ptwm-core/src/flavor/
+// native.rs:62-197) plus this library's additions; declarations and the
+// contract of every symbol are in include/ptwm_mi355x.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+
+#include "../../include/ptwm_mi355x.h"
+#include "runtime.h"
+
+namespace ptwm {
+namespace {
+
+// Built-in canonical ids: blake3([0xBB;32] || 0 || name || 0 || version)
+// (extension/id.rs:21-30, extension/mod.rs:36, builtins.rs:18-27).  Both the
+// current (1.1.0) and the 1.0.0 derivations are accepted, as readers map
+// older ids to the current ones (builtins.rs:20-26).
+struct KnownId {
+  const char* hex;
+  uint32_t codec;
+};
+constexpr KnownId kBuiltinIds[] = {
+    {"fc2dea1265e3394c57c2df3b868b732ccaa1ee876bd4b1ce27d38f842c6112b5", kCodecIdentity},  // identity@1.1.0
+    {"614155b5a8c9efb689219bcca3cbf7855e29d3023208ce61cca7a36849248e33", kCodecHuffman},   // huffman@1.1.0
+    {"39c875ef9793a9c5ebe199116debac4c9d5388b8b7cf2fe6b575845f0ca1624e", kCodecRans},      // rans@1.1.0
+    {"eb31edfe6fd156b309010ca750571766fc8ae6e4056bc2b4a228679922edea30", kCodecIdentity},  // identity@1.0.0
+    {"571e8fae548f0db5faa961fb65ba5ea2443bdb1e95dac04fbf1d5d97228ec945", kCodecHuffman},   // huffman@1.0.0
+    {"87c8ca053fbd0646c07d18da4d0396a92550eb6d44bcd4e461538902874d4bc7", kCodecRans},      // rans@1.0.0
+    // this extension: blake3([0;32] || 0 || "io.ptwm.mi355x.plane_codec" || 0 || "0.1.0")
+    {"cfd8cc03483eb4a43cdddb4b3cbf95b32e0a3f0e17e5ec85a0b52de04e8caf04", kCodecHuffIlv},
+};
+// blake3([0;32] || 0 || "io.ptwm.mi355x.hardware_backend" || 0 || "0.1.0")
+constexpr const char* kBackendIdHex = "a432dc02f57030b41a3660762bbcec5668cde8abbc807999d56ca0a3304d39cf";
+// blake3([0;32] || 0 || "io.ptwm.mi355x.decode_plan" || 0 || "0.1.0")
+constexpr const char* kPlanIdHex = "1b0e48b156b01d0d733a5aa62a90bcbde34945ff024d8d8e56cb714a48c6e770";
+constexpr const char* kOwnCodecIdHex = "cfd8cc03483eb4a43cdddb4b3cbf95b32e0a3f0e17e5ec85a0b52de04e8caf04";
+
+bool hex_eq(const char* hex, const uint8_t* id) {
+  for (int i = 0; i < 32; ++i) {
+    auto nib = [](char c) -> int { return c <= '9' ? c - '0' : c - 'a' + 10; };
+    int v = (nib(hex[2 * i]) << 4) | nib(hex[2 * i + 1]);
+    if (v != id[i]) return false;
+  }
+  return true;
+}
+
+void hex_to(const char* hex, uint8_t* out) {
+  for (int i = 0; i < 32; ++i) {
+    auto nib = [](char c) -> int { return c <= '9' ? c - '0' : c - 'a' + 10; };
+    out[i] = (uint8_t)((nib(hex[2 * i]) << 4) | nib(hex[2 * i + 1]));
+  }
+}
+
+// Resolve a codec id to a wire id; returns false if unknown.
+bool lookup_codec(const uint8_t* id, size_t len, uint32_t& codec) {
+  if (!id || len != 32) return false;
+  for (const KnownId& k : kBuiltinIds)
+    if (hex_eq(k.hex, id)) {
+      codec = k.codec;
+      return true;
+    }
+  return false;
+}
+
+// RAII: lock the device context, make its device current, restore after.
+struct DeviceScope {
+  DevCtx* ctx;
+  std::unique_lock<std::mutex> lk;
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceScope(uint32_t ord) : ctx(get_ctx(ord)) {
+    if (!ctx) return;
+    lk = std::unique_lock<std::mutex>(ctx->mu);
+    (void)hipGetDevice(&prev);
+    ok = hipSetDevice(ctx->dev) == hipSuccess;
+  }
+  ~DeviceScope() {
+    if (ctx && prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+int64_t decode_one_payload(DevCtx& ctx, uint32_t codec, uint64_t in_dev, size_t in_len, uint64_t out_dev,
+                           size_t out_cap) {
+  uint64_t expected = 0;
+  if (codec == kCodecIdentity) {
+    expected = in_len;
+  } else if (codec == kCodecHuffman || codec == kCodecRans) {
+    if (in_len == 0) return kInvalidInput;
+    PTWM_HIP_TRY(ctx.h_small.ensure(64));
+    uint8_t* hdr = static_cast<uint8_t*>(ctx.h_small.ptr);
+    size_t n = in_len < 5 ? in_len : 5;
+    PTWM_HIP_TRY(hipMemcpyAsync(hdr, reinterpret_cast<const void*>(in_dev), n, hipMemcpyDeviceToHost, ctx.stream));
+    PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+    if (hdr[0] == 0) {
+      expected = in_len - 1;
+    } else if (hdr[0] == 1 && in_len >= 5) {
+      expected = (uint64_t)hdr[1] | ((uint64_t)hdr[2] << 8) | ((uint64_t)hdr[3] << 16) | ((uint64_t)hdr[4] << 24);
+    } else {
+      return kInvalidInput;
+    }
+  } else {
+    return kUnsupported;
+  }
+  if (expected > out_cap) return kBufferTooSmall;
+  if (expected == 0 && codec == kCodecIdentity) return 0;
+  PTWM_HIP_TRY(ctx.jobs.ensure(sizeof(DecodeJob)));
+  PTWM_HIP_TRY(ctx.status.ensure(64));
+  PTWM_HIP_TRY(ctx.h_jobs.ensure(sizeof(DecodeJob)));
+  PTWM_HIP_TRY(ctx.h_status.ensure(64));
+  DecodeJob* J = static_cast<DecodeJob*>(ctx.h_jobs.ptr);
+  std::memset(J, 0, sizeof(*J));
+  J->src = in_dev;
+  J->src_len = in_len;
+  J->dst = out_dev;
+  J->dst_len = expected;
+  J->codec = codec;
+  J->framed = 0;
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, J, sizeof(DecodeJob), hipMemcpyHostToDevice, ctx.stream));
+  PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr),
+                                   static_cast<uint32_t*>(ctx.status.ptr), 1, ctx.stream));
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.h_status.ptr, ctx.status.ptr, 4, hipMemcpyDeviceToHost, ctx.stream));
+  PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+  if (*static_cast<uint32_t*>(ctx.h_status.ptr) != kStOk) return kInvalidInput;
+  return (int64_t)expected;
+}
+
+}  // namespace
+}  // namespace ptwm
+
+using namespace ptwm;
+
+extern "C" {
+
+uint32_t ptwm_mi355x_abi_version(void) { return 1; }
+
+int64_t ptwm_mi355x_canonical_id(uint32_t which, uint8_t* out32) {
+  if (!out32) return kInvalidInput;
+  const char* hex = which == 0 ? kOwnCodecIdHex : which == 1 ? kBackendIdHex : which == 2 ? kPlanIdHex : nullptr;
+  if (!hex) return kInvalidInput;
+  hex_to(hex, out32);
+  return 0;
+}
+
+uint64_t ptwm_plane_codec_v1_cuda_stream_handle(uint32_t device_ordinal) {
+  DevCtx* c = get_ctx(device_ordinal);
+  return c ? reinterpret_cast<uint64_t>(c->stream) : 0;
+}
+
+uint64_t ptwm_hardware_backend_v1_cuda_stream_handle(uint32_t device_ordinal) {
+  return ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal);
+}
+
+int64_t ptwm_plane_codec_v1_decode_cuda(uint8_t state_format_version, const uint8_t* state_ptr, size_t state_len,
+                                        const uint8_t* codec_id_ptr, size_t codec_id_len, uint64_t in_dev_ptr,
+                                        size_t in_len, uint64_t out_dev_ptr, size_t out_cap,
+                                        uint32_t device_ordinal) {
+  (void)state_format_version;
+  (void)state_ptr;
+  uint32_t codec = 0;
+  if (!lookup_codec(codec_id_ptr, codec_id_len, codec)) return kUnsupported;
+  if (state_len != 0) return kInvalidInput;  // none of these codecs carries state
+  if ((in_len && !in_dev_ptr) || (out_cap && !out_dev_ptr)) return kInvalidInput;
+  if (codec == kCodecHuffIlv) return kUnsupported;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  return decode_one_payload(*ds.ctx, codec, in_dev_ptr, in_len, out_dev_ptr, out_cap);
+}
+
+int64_t ptwm_plane_codec_v1_encode_cuda(uint8_t state_format_version, const uint8_t* state_ptr, size_t state_len,
+                                        const uint8_t* codec_id_ptr, size_t codec_id_len, uint64_t in_dev_ptr,
+                                        size_t in_len, uint64_t out_dev_ptr, size_t out_cap, uint64_t* needed_out,
+                                        uint32_t device_ordinal) {
+  (void)state_format_version;
+  (void)state_ptr;
+  (void)in_dev_ptr;
+  (void)in_len;
+  (void)out_dev_ptr;
+  (void)out_cap;
+  (void)needed_out;
+  (void)device_ordinal;
+  uint32_t codec = 0;
+  if (!lookup_codec(codec_id_ptr, codec_id_len, codec)) return kUnsupported;
+  if (state_len != 0) return kInvalidInput;
+  return kUnsupported;
+}
+
+int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_version, const uint8_t* state_ptr,
+                                                      size_t state_len, const uint8_t* codec_id_ptr,
+                                                      size_t codec_id_len, uint64_t in_dev_ptr, size_t in_len,
+                                                      uint64_t out_dev_ptr, size_t out_len,
+                                                      uint32_t device_ordinal) {
+  (void)state_format_version;
+  if (!codec_id_ptr || codec_id_len != 32 || !hex_eq(kPlanIdHex, codec_id_ptr)) return kUnsupported;
+  Plan plan;
+  int64_t rc = parse_plan(state_ptr, state_len, in_len, out_len, plan);
+  if (rc != kOk) return rc;
+  // tensors must not overlap in the output
+  std::vector<std::pair<uint64_t, uint64_t>> spans;
+  uint64_t total = 0;
+  for (const PlanTensor& t : plan.tensors) {
+    spans.emplace_back(t.out_offset, t.out_len);
+    total += t.out_len;
+  }
+  std::sort(spans.begin(), spans.end());
+  for (size_t i = 1; i < spans.size(); ++i)
+    if (spans[i - 1].first + spans[i - 1].second > spans[i].first) return kInvalidInput;
+  if (total && (!in_dev_ptr || !out_dev_ptr)) return kInvalidInput;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  rc = execute_plan(*ds.ctx, plan, in_dev_ptr, out_dev_ptr);
+  return rc == kOk ? (int64_t)total : rc;
+}
+
+int64_t ptwm_plane_codec_v1_encode(const uint8_t* in, size_t in_len, uint8_t* out, size_t out_len) {
+  (void)in;
+  (void)in_len;
+  (void)out;
+  (void)out_len;
+  return kUnsupported;
+}
+
+int64_t ptwm_plane_codec_v1_decode(const uint8_t* in, size_t in_len, uint8_t* out, size_t out_len) {
+  (void)in;
+  (void)in_len;
+  (void)out;
+  (void)out_len;
+  return kUnsupported;
+}
+
+int64_t ptwm_plane_codec_v1_decode_stateful(uint8_t state_format_version, const uint8_t* state_ptr,
+                                            size_t state_len, const uint8_t* in, size_t in_len, uint8_t* out,
+                                            size_t out_cap) {
+  (void)state_format_version;
+  (void)state_ptr;
+  if (state_len != 0) return kInvalidInput;
+  return ptwm_plane_codec_v1_decode(in, in_len, out, out_cap);
+}
+
+int64_t ptwm_mi355x_split_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, const uint64_t* plane_dev_ptrs,
+                               uint32_t n_planes, uint32_t device_ordinal) {
+  int np = chain_planes(chain);
+  if (np < 0 || (uint32_t)np != n_planes || !plane_dev_ptrs) return kInvalidInput;
+  uint64_t ratio = (uint64_t)chain_ratio(chain);
+  if (in_len % ratio) return kInvalidInput;
+  uint64_t plane_len = in_len / ratio;
+  if (plane_len == 0) return 0;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  uint8_t* pl[4] = {};
+  for (int i = 0; i < np; ++i) pl[i] = reinterpret_cast<uint8_t*>(plane_dev_ptrs[i]);
+  if (launch_split(chain, reinterpret_cast<const uint8_t*>(in_dev_ptr), plane_len, pl, ds.ctx->stream) !=
+      hipSuccess)
+    return kInvalidInput;
+  PTWM_HIP_TRY(hipStreamSynchronize(ds.ctx->stream));
+  return (int64_t)plane_len;
+}
+
+int64_t ptwm_mi355x_merge_cuda(uint32_t chain, const uint64_t* plane_dev_ptrs, uint32_t n_planes, size_t plane_len,
+                               uint64_t out_dev_ptr, size_t out_cap, uint32_t device_ordinal) {
+  int np = chain_planes(chain);
+  if (np < 0 || (uint32_t)np != n_planes || !plane_dev_ptrs) return kInvalidInput;
+  uint64_t out_len = (uint64_t)plane_len * (uint64_t)chain_ratio(chain);
+  if (out_len > out_cap) return kBufferTooSmall;
+  if (plane_len == 0) return 0;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  const uint8_t* pl[4] = {};
+  for (int i = 0; i < np; ++i) pl[i] = reinterpret_cast<const uint8_t*>(plane_dev_ptrs[i]);
+  DevCtx& ctx = *ds.ctx;
+  if (ctx.profile) {
+    PTWM_HIP_TRY(ctx.ensure_events());
+    PTWM_HIP_TRY(hipEventRecord(ctx.ev[1], ctx.stream));
+  }
+  if (launch_merge(chain, pl, plane_len, reinterpret_cast<uint8_t*>(out_dev_ptr), ctx.stream) != hipSuccess)
+    return kInvalidInput;
+  if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], ctx.stream));
+  PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+  if (ctx.profile) {
+    ctx.last_ms[0] = 0;
+    PTWM_HIP_TRY(hipEventElapsedTime(&ctx.last_ms[1], ctx.ev[1], ctx.ev[2]));
+    ctx.last_ms[2] = ctx.last_ms[1];
+  }
+  return (int64_t)out_len;
+}
+
+int64_t ptwm_mi355x_set_profiling(uint32_t device_ordinal, uint32_t on) {
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  ds.ctx->profile = on != 0;
+  return 0;
+}
+
+int64_t ptwm_mi355x_last_kernel_ms(uint32_t device_ordinal, float* out3) {
+  if (!out3) return kInvalidInput;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  for (int i = 0; i < 3; ++i) out3[i] = ds.ctx->last_ms[i];
+  return 0;
+}
+
+}  // extern "C"

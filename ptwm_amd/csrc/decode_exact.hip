@@ -1,0 +1,453 @@
+// decode_exact.hip -- reference-format plane payload decode on gfx950.
+//
+// One 64-lane wavefront per independently coded unit (a plane payload or
+// one chunk of a chunked plane).  The whole wave parses the payload header
+// and builds the decode table in LDS; then four lanes, one per segment of
+// the reference's 4-segment frame (entropy/stream_frame.rs:27-39), run the
+// reference reader state machine bit for bit:
+//   Huffman: entropy/huffman/decompress.rs:8-211 with the backward
+//            BitReader of entropy/huffman/bitstream.rs:58-187, including the
+//            lockstep 4-stream fast loop whose exit depends on all four
+//            streams and the wrapping u8 bit counter, so acceptance and
+//            output match the reference for every input, malformed or not.
+//   rANS:    entropy/rans/decompress.rs:24-166.
+// Payload framing follows codecs/huffman.rs:90-141, codecs/rans.rs:97-170,
+// codec_tagged.rs:98-194 and codecs/length_prefix.rs:30-33; chunk frames
+// follow container.rs:2010-2049.
+//
+// This kernel is the exact path: it is used for the reference formats.
+// Throughput-oriented paths live in decode_fast.hip / huff_ilv.hip.
+#include "ptwm_common.h"
+
+namespace ptwm {
+
+namespace {
+
+constexpr int kHufMaxBits = 11;
+constexpr uint32_t kRansProbBits = 11;
+constexpr uint32_t kRansScale = 1u << kRansProbBits;
+constexpr uint32_t kRansL = 1u << 23;
+
+__device__ inline uint32_t ld_u32le(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+// Backward bit reader, state identical to bitstream.rs:58-67.
+struct Reader {
+  const uint8_t* data;
+  int64_t bi;       // next byte to read, moving toward 0
+  uint64_t cont;    // LSB-aligned bit container
+  uint32_t cnt;     // u8 in the reference; kept masked to 8 bits here
+};
+
+__device__ inline void rd_init(Reader& r, const uint8_t* d, uint64_t n) {
+  r.data = d;
+  r.bi = (int64_t)n - 1;
+  r.cont = 0;
+  r.cnt = 0;
+  int64_t avail = r.bi + 1 < 8 ? r.bi + 1 : 8;   // initial_fill (bitstream.rs:76-82)
+  for (int64_t i = 0; i < avail; ++i) {
+    r.cont |= (uint64_t)d[r.bi] << r.cnt;
+    r.cnt = (r.cnt + 8) & 0xFF;
+    r.bi--;
+  }
+}
+
+// reload (bitstream.rs:88-106)
+__device__ inline void rd_reload(Reader& r) {
+  if (r.cnt == 0 && r.bi >= 7) {
+    const uint8_t* p = r.data + (r.bi - 7);
+    uint64_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w = (w << 8) | p[i];
+    r.cont = w;
+    r.cnt = 64;
+    r.bi -= 8;
+  } else if (r.cnt <= 32 && r.bi >= 3) {
+    const uint8_t* p = r.data + (r.bi - 3);
+    uint32_t w = ((uint32_t)p[0] << 24) | ((uint32_t)p[1] << 16) | ((uint32_t)p[2] << 8) | p[3];
+    r.cont |= (uint64_t)w << r.cnt;
+    r.cnt = (r.cnt + 32) & 0xFF;
+    r.bi -= 4;
+  }
+}
+
+// refill (bitstream.rs:108-121)
+__device__ inline void rd_refill(Reader& r) {
+  if (r.cnt <= 32 && r.bi >= 3) {
+    rd_reload(r);
+  } else {
+    while (r.cnt < 56 && r.bi >= 0) {
+      r.cont |= (uint64_t)r.data[r.bi] << r.cnt;
+      r.cnt = (r.cnt + 8) & 0xFF;
+      r.bi--;
+    }
+  }
+}
+
+// decode_symbol (bitstream.rs:129-137); the counter wraps like the u8.
+__device__ inline uint8_t rd_decode(Reader& r, const uint16_t* table, uint64_t mask) {
+  uint16_t e = table[r.cont & mask];
+  uint32_t nb = e >> 8;
+  r.cont >>= nb;
+  r.cnt = (r.cnt - nb) & 0xFF;
+  return (uint8_t)(e & 0xFF);
+}
+
+__device__ inline void rd_refill_to(Reader& r, uint32_t nbits) {
+  while (r.cnt < nbits && r.bi >= 0) {
+    r.cont |= (uint64_t)r.data[r.bi] << r.cnt;
+    r.cnt = (r.cnt + 8) & 0xFF;
+    r.bi--;
+  }
+}
+
+// decode_stream_tail (decompress.rs:152-211); returns false on error.
+__device__ bool huf_tail(Reader& r, const uint16_t* table, uint64_t mask, uint32_t max_bits, uint8_t* out,
+                         uint64_t len) {
+  uint64_t i = 0;
+  while (i < len && r.bi >= 3) {
+    if (r.cnt < max_bits) rd_refill(r);
+    out[i++] = rd_decode(r, table, mask);
+  }
+  while (i < len) {
+    uint64_t avail = (uint64_t)r.cnt + (uint64_t)(r.bi + 1 > 0 ? r.bi + 1 : 0) * 8;
+    if (avail == 0) return false;
+    rd_refill_to(r, max_bits);
+    if (r.cnt == 0) return false;
+    uint16_t e = table[r.cont & mask];
+    uint32_t nb = e >> 8;
+    if ((uint64_t)nb > avail) return false;
+    if (nb) {
+      if (r.cnt < nb) rd_refill_to(r, nb);
+      if (r.cnt < nb) return false;
+      r.cont >>= nb;
+      r.cnt = (r.cnt - nb) & 0xFF;
+    }
+    out[i++] = (uint8_t)(e & 0xFF);
+  }
+  return true;
+}
+
+__device__ inline void split_four(uint64_t len, uint64_t* s, uint64_t* e) {
+  uint64_t base = len / 4, rem = len % 4, start = 0;
+  for (int i = 0; i < 4; ++i) {
+    uint64_t l = base + ((uint64_t)i < rem ? 1 : 0);
+    s[i] = start;
+    e[i] = start + l;
+    start += l;
+  }
+}
+
+struct SharedHeader {
+  uint64_t enc_off;   // offset of the entropy blob inside src
+  uint64_t enc_len;
+  uint32_t kind;      // 0 copy, 1 huffman, 2 rans, 3 empty-ok, 4 error
+  uint32_t status;
+  uint64_t copy_off;  // for kind 0
+  uint32_t max_bits;
+  uint32_t nw;        // number of weights
+  uint64_t seg_src[4];
+  uint64_t seg_len[4];
+  uint32_t err;
+};
+
+}  // namespace
+
+// Parse the chunk frame and tag, decide what to run.  Executed by lane 0.
+__device__ void parse_job(const DecodeJob& job, SharedHeader& h) {
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(job.src);
+  uint64_t off = 0, len = job.src_len;
+  h.status = kStOk;
+  h.kind = 4;
+  if (job.framed) {
+    if (len < 5) { h.status = kStBadFrame; return; }
+    uint64_t sl = ld_u32le(src + 1);
+    if (len - 5 < sl) { h.status = kStBadFrame; return; }
+    off = 5 + sl;
+    len -= off;
+  }
+  if (job.codec == kCodecIdentity) {  // codecs/identity.rs: payload is the plane
+    if (len != job.dst_len) { h.status = kStBadLength; return; }
+    h.kind = 0;
+    h.copy_off = off;
+    return;
+  }
+  if (len == 0) { h.status = kStBadTag; return; }
+  uint8_t tag = src[off];
+  if (tag == 0) {                     // TAG_RAW
+    if (len - 1 != job.dst_len) { h.status = kStBadLength; return; }
+    h.kind = 0;
+    h.copy_off = off + 1;
+    return;
+  }
+  if (tag != 1) { h.status = kStBadTag; return; }
+  if (len - 1 < 4) { h.status = kStBadTag; return; }
+  uint64_t orig = ld_u32le(src + off + 1);
+  uint64_t enc_len = len - 5;
+  if (job.codec == kCodecHuffman) {
+    if (orig > enc_len * 32 + 4096) { h.status = kStBadLength; return; }  // huffman.rs:122-131
+    if (orig != job.dst_len) { h.status = kStBadLength; return; }
+    h.kind = 1;
+  } else if (job.codec == kCodecRans) {
+    if (orig > job.dst_len) { h.status = kStBadLength; return; }          // rans.rs:158-160
+    bool accepted = orig <= (1ull << 30) || orig <= enc_len * 64;           // length_prefix.rs:30-33
+    if (!accepted) { h.status = kStBadLength; return; }
+    if (orig == 0) {                                                        // codec_tagged.rs:108-110
+      h.kind = 3;
+      if (job.dst_len != 0) h.status = kStBadLength;
+      return;
+    }
+    if (orig != job.dst_len) { h.status = kStBadLength; return; }
+    h.kind = 2;
+  } else {
+    h.status = kStBadTag;
+    return;
+  }
+  h.enc_off = off + 5;
+  h.enc_len = enc_len;
+}
+
+__global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __restrict__ jobs,
+                                                          uint32_t* __restrict__ status) {
+  __shared__ SharedHeader h;
+  __shared__ uint8_t lengths[256];
+  __shared__ uint16_t counts[kHufMaxBits + 1];
+  __shared__ uint16_t next_code[kHufMaxBits + 1];
+  __shared__ uint16_t rev[256];
+  __shared__ uint32_t table32[kRansScale];  // rANS: sym | freq << 8 | start << 20
+  uint16_t* table16 = reinterpret_cast<uint16_t*>(table32);  // Huffman: (len << 8) | sym
+
+  const uint32_t lane = threadIdx.x;
+  const DecodeJob job = jobs[blockIdx.x];
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(job.src);
+  uint8_t* dst = reinterpret_cast<uint8_t*>(job.dst);
+
+  if (lane == 0) {
+    parse_job(job, h);
+    h.err = 0;
+  }
+  __syncthreads();
+  if (h.status != kStOk || h.kind == 3) {
+    if (lane == 0) status[blockIdx.x] = h.status;
+    return;
+  }
+  if (h.kind == 0) {  // stored bytes
+    const uint8_t* s = src + h.copy_off;
+    for (uint64_t i = lane; i < job.dst_len; i += 64) dst[i] = s[i];
+    if (lane == 0) status[blockIdx.x] = kStOk;
+    return;
+  }
+  const uint8_t* enc = src + h.enc_off;
+  const uint64_t enc_len = h.enc_len;
+
+  if (h.kind == 1) {
+    // ---- weights header (weights.rs:34-85) and tree (tree.rs:87-177) ----
+    if (lane == 0) {
+      uint32_t st = kStOk;
+      uint64_t n = 0, hb = 0;
+      if (enc_len == 0 || !(enc[0] & 0x80)) st = kStBadHeader;
+      else if (enc[0] == 0x80) {
+        if (enc_len < 2) st = kStBadHeader;
+        else {
+          n = enc[1] ? enc[1] : 256;
+          hb = 2;
+          if (n < 128) st = kStBadHeader;
+        }
+      } else {
+        n = enc[0] & 0x7F;
+        hb = 1;
+        if (n == 0) st = kStBadHeader;
+      }
+      if (st == kStOk && enc_len < hb + (n + 1) / 2) st = kStBadHeader;
+      uint32_t maxb = 0, total = 0;
+      for (int i = 0; i <= kHufMaxBits; ++i) counts[i] = 0;
+      if (st == kStOk) {
+        for (uint64_t i = 0; i < 256; ++i) {
+          uint8_t w = 0;
+          if (i < n) {
+            uint8_t b = enc[hb + i / 2];
+            w = (i % 2 == 0) ? (b & 0x0F) : ((b >> 4) & 0x0F);
+          }
+          if (w > kHufMaxBits) { st = kStBadHeader; break; }
+          lengths[i] = w;
+          if (w) { counts[w]++; total++; if (w > maxb) maxb = w; }
+        }
+      }
+      if (st == kStOk && total == 0) st = kStBadHeader;
+      if (maxb < 1) maxb = 1;
+      // canonical codes (tree.rs:119-141)
+      if (st == kStOk) {
+        uint32_t code = 0;
+        for (uint32_t b = 1; b <= maxb; ++b) {
+          code = ((code + counts[b - 1]) << 1) & 0xFFFF;
+          if (code > (1u << b)) { st = kStBadHeader; break; }
+          next_code[b] = (uint16_t)code;
+        }
+      }
+      if (st == kStOk) {
+        for (int s = 0; s < 256; ++s) {
+          uint32_t l = lengths[s];
+          if (!l) continue;
+          uint32_t c = next_code[l];
+          if (c >= (1u << l)) { st = kStBadHeader; break; }
+          next_code[l] = (uint16_t)(c + 1);
+          uint32_t rv = 0;
+          for (uint32_t k = 0; k < l; ++k) rv |= ((c >> k) & 1u) << (l - 1 - k);
+          rev[s] = (uint16_t)rv;
+        }
+      }
+      // jump table and segment streams (decompress.rs:14-48)
+      uint64_t pos = hb + (n + 1) / 2;
+      if (st == kStOk && enc_len - pos < 16) st = kStBadHeader;
+      if (st == kStOk) {
+        uint64_t tot = 0, so = pos + 16;
+        for (int i = 0; i < 4; ++i) {
+          h.seg_len[i] = ld_u32le(enc + pos + 4 * i);
+          h.seg_src[i] = so;
+          so += h.seg_len[i];
+          tot += h.seg_len[i];
+        }
+        if (tot != enc_len - pos - 16) st = kStBadHeader;
+      }
+      h.status = st;
+      h.max_bits = maxb;
+    }
+    __syncthreads();
+    if (h.status != kStOk) {
+      if (lane == 0) status[blockIdx.x] = h.status;
+      return;
+    }
+    const uint32_t max_bits = h.max_bits;
+    const uint32_t tsize = 1u << max_bits;
+    const uint16_t fallback = (uint16_t)(max_bits << 8);
+    for (uint32_t i = lane; i < tsize; i += 64) table16[i] = fallback;
+    __syncthreads();
+    // The Kraft check above guarantees a prefix code, so spreads never collide.
+    for (uint32_t s = lane; s < 256; s += 64) {
+      uint32_t l = lengths[s];
+      if (!l) continue;
+      uint16_t entry = (uint16_t)((l << 8) | s);
+      uint32_t spread = 1u << (max_bits - l);
+      for (uint32_t i = 0; i < spread; ++i) table16[rev[s] | (i << l)] = entry;
+    }
+    __syncthreads();
+
+    if (lane < 4) {
+      Reader r;
+      rd_init(r, enc + h.seg_src[lane], h.seg_len[lane]);
+      uint64_t s4[4], e4[4];
+      split_four(job.dst_len, s4, e4);
+      uint64_t op = s4[lane], end = e4[lane];
+      uint64_t fe = end >= 3 ? end - 3 : 0;
+      const uint64_t mask = (1ull << max_bits) - 1;
+      // lockstep fast loop: continues only while all four streams qualify
+      for (;;) {
+        bool ok = op < fe && r.bi >= 3;
+        uint64_t b = __ballot(ok);
+        if ((b & 0xFull) != 0xFull) break;
+#pragma unroll
+        for (int round = 0; round < 2; ++round) {
+          rd_refill(r);
+          dst[op] = rd_decode(r, table16, mask);
+          dst[op + 1] = rd_decode(r, table16, mask);
+          op += 2;
+        }
+      }
+      bool good = huf_tail(r, table16, mask, max_bits, dst + op, end - op);
+      good = good && (r.bi < 0 && r.cont == 0);   // is_exhausted
+      if (!good) atomicOr(&h.err, 1u);
+    }
+    __syncthreads();
+    if (lane == 0) status[blockIdx.x] = h.err ? kStBadStream : kStOk;
+    return;
+  }
+
+  // ---- rANS (rans/decompress.rs) ----
+  if (lane == 0) {
+    uint32_t st = kStOk;
+    uint64_t max_sym = 0, need = 0;
+    if (enc_len == 0) st = kStBadHeader;
+    else {
+      max_sym = enc[0];
+      need = 1 + 2 * (max_sym + 1);
+      if (enc_len < need) st = kStBadHeader;
+    }
+    uint32_t tot = 0;
+    if (st == kStOk) {
+      for (uint64_t i = 0; i < 256; ++i) {
+        uint32_t f = i <= max_sym ? ((uint32_t)enc[1 + 2 * i] | ((uint32_t)enc[2 + 2 * i] << 8)) : 0;
+        rev[i] = (uint16_t)f;   // reuse: per-symbol frequency
+        tot += f;
+      }
+      if (tot != kRansScale) st = kStBadHeader;
+    }
+    if (st == kStOk && enc_len - need < 16) st = kStBadHeader;
+    if (st == kStOk) {
+      uint64_t t = 0, so = need + 16;
+      for (int i = 0; i < 4; ++i) {
+        h.seg_len[i] = ld_u32le(enc + need + 4 * i);
+        h.seg_src[i] = so;
+        so += h.seg_len[i];
+        t += h.seg_len[i];
+      }
+      if (t != enc_len - need - 16) st = kStBadHeader;
+    }
+    h.status = st;
+  }
+  __syncthreads();
+  if (h.status != kStOk) {
+    if (lane == 0) status[blockIdx.x] = h.status;
+    return;
+  }
+  // cumulative starts: lane 0 (256 adds), then parallel fill
+  __shared__ uint16_t cum[257];
+  if (lane == 0) {
+    uint32_t run = 0;
+    for (int s = 0; s < 256; ++s) { cum[s] = (uint16_t)run; run += rev[s]; }
+    cum[256] = (uint16_t)run;
+  }
+  __syncthreads();
+  for (uint32_t s = lane; s < 256; s += 64) {
+    uint32_t f = rev[s], st = cum[s];
+    uint32_t entry = s | (f << 8) | (st << 20);
+    for (uint32_t j = 0; j < f; ++j) table32[st + j] = entry;
+  }
+  __syncthreads();
+  if (lane < 4) {
+    uint64_t s4[4], e4[4];
+    split_four(job.dst_len, s4, e4);
+    bool good = true;
+    if (s4[lane] != e4[lane]) {
+      const uint8_t* st = enc + h.seg_src[lane];
+      uint64_t sl = h.seg_len[lane];
+      if (sl < 4) good = false;
+      else {
+        uint32_t x = ld_u32le(st);
+        uint64_t q = 4;
+        for (uint64_t k = s4[lane]; k < e4[lane] && good; ++k) {
+          uint32_t idx = x & (kRansScale - 1);
+          uint32_t e = table32[idx];
+          dst[k] = (uint8_t)(e & 0xFF);
+          x = ((e >> 8) & 0xFFF) * (x >> kRansProbBits) + idx - (e >> 20);
+          while (x < kRansL) {
+            if (q >= sl) { good = false; break; }
+            x = (x << 8) | st[q++];
+          }
+        }
+      }
+    }
+    if (!good) atomicOr(&h.err, 1u);
+  }
+  __syncthreads();
+  if (lane == 0) status[blockIdx.x] = h.err ? kStBadStream : kStOk;
+}
+
+hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
+                               hipStream_t stream) {
+  if (n_jobs == 0) return hipSuccess;
+  hipLaunchKernelGGL(decode_exact_kernel, dim3(n_jobs), dim3(64), 0, stream, jobs_dev, status_dev);
+  return hipGetLastError();
+}
+
+}  // namespace ptwm

@@ -1,0 +1,81 @@
+// ptwm_common.h -- shared definitions for the MI355X plane-codec library.
+//
+// Error codes follow the reference native ABI return convention
+// (crates/ptwm-core/src/flavor/native.rs:634-657): >= 0 bytes written,
+// -1 InvalidInput, -2 BufferTooSmall, -3 MissingCapability,
+// -4 MissingNativeDep, -5 Unsupported, anything else InternalError.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace ptwm {
+
+// Native 128-bit vector (dwordx4 loads/stores; usable with the nontemporal
+// builtins, unlike HIP's uint4 struct).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__host__ __device__ inline u32x4 u32x4_make(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u32x4 r = {a, b, c, d};
+  return r;
+}
+
+constexpr int64_t kOk = 0;
+constexpr int64_t kInvalidInput = -1;
+constexpr int64_t kBufferTooSmall = -2;
+constexpr int64_t kMissingCapability = -3;
+constexpr int64_t kMissingNativeDep = -4;
+constexpr int64_t kUnsupported = -5;
+constexpr int64_t kInternal = -6;
+
+// Codec wire ids (crates/ptwm-core/src/codec.rs:3-23) plus this library's
+// GPU-native codec, registered as a third-party plane codec.
+constexpr uint32_t kCodecIdentity = 0x0000;
+constexpr uint32_t kCodecHuffman = 0x0001;
+constexpr uint32_t kCodecRans = 0x0003;
+constexpr uint32_t kCodecHuffIlv = 0x7F01;  // GPU-native interleaved Huffman
+
+// Chain kinds: the fused reorder+split pairs of transforms/fusion.rs plus
+// the unfused NibbleSplit and BytePassthrough used by the u8 chains.
+enum ChainKind : uint32_t {
+  kChainIeee16Split2 = 1,
+  kChainIeee32Split4 = 2,
+  kChainE4m3Nibble = 3,
+  kChainE5m2Nibble = 4,
+  kChainNibbleSplit = 5,
+  kChainPassthrough = 6,
+};
+
+// Per-job decode status written by the device (0 = ok).
+enum DecodeStatus : uint32_t {
+  kStOk = 0,
+  kStBadFrame = 1,       // chunk frame truncated / state_len past the end
+  kStBadTag = 2,         // tag byte not 0/1 or payload empty
+  kStBadLength = 3,      // declared length disagrees with the chunk table / cap
+  kStBadHeader = 4,      // weights / frequency table / jump table invalid
+  kStBadStream = 5,      // bitstream inconsistent (reference decoder errors)
+  kStNotRun = 0xFFFFFFFFu,
+};
+
+// One independently coded unit: a whole plane payload, or one chunk frame
+// of a chunked plane (compressor.rs:316-321 frame: [ver u8][state_len u32]
+// [state][payload]).  64 bytes so the array is naturally aligned.
+struct DecodeJob {
+  uint64_t src;       // device address of the payload (or of the chunk frame)
+  uint64_t src_len;   // bytes available at src
+  uint64_t dst;       // device address of the decoded bytes
+  uint64_t dst_len;   // exact decoded size expected (chunk table decoded_size)
+  uint32_t codec;     // kCodec*
+  uint32_t framed;    // 1: src starts with a chunk frame header
+  uint32_t pad[6];
+};
+static_assert(sizeof(DecodeJob) == 64, "DecodeJob layout");
+
+#define PTWM_HIP_TRY(expr)                      \
+  do {                                          \
+    hipError_t _e = (expr);                     \
+    if (_e != hipSuccess) return ::ptwm::kInternal; \
+  } while (0)
+
+}  // namespace ptwm

@@ -1,0 +1,98 @@
+// runtime.h -- per-device context, scratch memory and decode-plan execution.
+#pragma once
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "ptwm_common.h"
+
+namespace ptwm {
+
+// Grow-only device allocation reused across calls on one device.
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t cap = 0;
+  hipError_t ensure(size_t bytes);
+  ~DeviceBuffer();
+};
+
+struct PinnedBuffer {
+  void* ptr = nullptr;
+  size_t cap = 0;
+  hipError_t ensure(size_t bytes);
+  ~PinnedBuffer();
+};
+
+// One per device ordinal.  All entry points serialise on `mu`: the stream
+// and the scratch buffers are shared by every call on that device.
+struct DevCtx {
+  int dev = -1;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  DeviceBuffer jobs;     // DecodeJob array
+  DeviceBuffer status;   // per-job status words
+  DeviceBuffer planes;   // decoded plane scratch (unfused path)
+  DeviceBuffer aux;      // small per-call tables
+  PinnedBuffer h_jobs;
+  PinnedBuffer h_status;
+  PinnedBuffer h_small;
+  // optional per-phase kernel timing with HIP events on `stream`
+  bool profile = false;
+  hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  float last_ms[3] = {0, 0, 0};  // entropy decode, merge, whole call
+  hipError_t ensure_events();
+};
+
+// Returns nullptr if the ordinal is invalid or HIP initialisation fails.
+DevCtx* get_ctx(uint32_t device_ordinal);
+
+// Parsed decode plan (the state bytes of the hardware-backend entry point).
+struct PlanChunk {
+  uint32_t offset_in_payload;
+  uint32_t decoded_size;
+};
+struct PlanPlane {
+  uint32_t codec = 0;
+  bool chunked = false;
+  uint64_t payload_offset = 0;
+  uint64_t payload_len = 0;
+  uint64_t plane_len = 0;
+  uint32_t crc32 = 0;
+  std::vector<PlanChunk> chunks;
+};
+struct PlanTensor {
+  uint64_t out_offset = 0;
+  uint64_t out_len = 0;
+  uint32_t chain = 0;
+  bool has_crc = false;
+  std::vector<PlanPlane> planes;
+};
+struct Plan {
+  std::vector<PlanTensor> tensors;
+};
+
+// Parse + validate against the input/output buffer sizes.  Returns kOk or
+// kInvalidInput.
+int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint64_t out_len, Plan& plan);
+
+// Decode every tensor of the plan from in_dev into out_dev (device
+// addresses).  Blocks until the work has completed.  Returns kOk or an
+// error code.
+int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev);
+
+// kernel launchers (decode_exact.hip, transform.hip)
+hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
+                               hipStream_t stream);
+hipError_t launch_merge(uint32_t chain, const uint8_t* const* planes, uint64_t plane_len, uint8_t* out,
+                        hipStream_t stream);
+hipError_t launch_split(uint32_t chain, const uint8_t* in, uint64_t plane_len, uint8_t* const* planes,
+                        hipStream_t stream);
+hipError_t launch_copy(const uint8_t* in, uint8_t* out, uint64_t n, hipStream_t stream);
+
+int chain_planes(uint32_t chain);
+// tensor bytes per plane byte for the chain (2 for bf16 split, 4 for fp32, 1 otherwise)
+int chain_ratio(uint32_t chain);
+
+}  // namespace ptwm

@@ -1,0 +1,297 @@
+// runtime.hip -- device contexts, scratch memory, decode-plan parsing and
+// execution for the reference plane formats.
+//
+// A decode plan describes one or more tensors as the container stores them
+// (container.rs:1795-2196): per tensor its chain (which fixes the inverse
+// merge) and per plane its codec id, payload location, decoded length and,
+// for chunked planes, the chunk table (plane_record.rs:16-20).  Every
+// independently coded unit becomes one DecodeJob; all jobs of all tensors go
+// to the device in one launch, then each tensor is merged.
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <cstring>
+#include <memory>
+
+#include "runtime.h"
+
+namespace ptwm {
+
+hipError_t DeviceBuffer::ensure(size_t bytes) {
+  if (bytes <= cap && ptr) return hipSuccess;
+  if (ptr) {
+    (void)hipFree(ptr);
+    ptr = nullptr;
+    cap = 0;
+  }
+  size_t want = bytes < 4096 ? 4096 : bytes;
+  hipError_t e = hipMalloc(&ptr, want);
+  if (e == hipSuccess) cap = want;
+  return e;
+}
+DeviceBuffer::~DeviceBuffer() {}
+
+hipError_t PinnedBuffer::ensure(size_t bytes) {
+  if (bytes <= cap && ptr) return hipSuccess;
+  if (ptr) {
+    (void)hipHostFree(ptr);
+    ptr = nullptr;
+    cap = 0;
+  }
+  size_t want = bytes < 4096 ? 4096 : bytes;
+  hipError_t e = hipHostMalloc(&ptr, want, hipHostMallocDefault);
+  if (e == hipSuccess) cap = want;
+  return e;
+}
+PinnedBuffer::~PinnedBuffer() {}
+
+hipError_t DevCtx::ensure_events() {
+  for (auto& e : ev)
+    if (!e) {
+      hipError_t r = hipEventCreate(&e);
+      if (r != hipSuccess) return r;
+    }
+  return hipSuccess;
+}
+
+namespace {
+std::mutex g_ctx_mu;
+std::array<std::unique_ptr<DevCtx>, 64> g_ctx;
+}  // namespace
+
+DevCtx* get_ctx(uint32_t ord) {
+  if (ord >= g_ctx.size()) return nullptr;
+  std::lock_guard<std::mutex> lk(g_ctx_mu);
+  if (g_ctx[ord]) return g_ctx[ord].get();
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || (int)ord >= n) return nullptr;
+  int prev = 0;
+  (void)hipGetDevice(&prev);
+  if (hipSetDevice((int)ord) != hipSuccess) return nullptr;
+  auto ctx = std::make_unique<DevCtx>();
+  ctx->dev = (int)ord;
+  // default priority: mixing stream priorities is avoided on purpose
+  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+    (void)hipSetDevice(prev);
+    return nullptr;
+  }
+  (void)hipSetDevice(prev);
+  g_ctx[ord] = std::move(ctx);
+  return g_ctx[ord].get();
+}
+
+int chain_planes(uint32_t chain) {
+  switch (chain) {
+    case kChainIeee16Split2: return 2;
+    case kChainIeee32Split4: return 4;
+    case kChainE4m3Nibble:
+    case kChainE5m2Nibble:
+    case kChainNibbleSplit: return 2;
+    case kChainPassthrough: return 1;
+    default: return -1;
+  }
+}
+
+int chain_ratio(uint32_t chain) {
+  switch (chain) {
+    case kChainIeee16Split2: return 2;
+    case kChainIeee32Split4: return 4;
+    default: return 1;
+  }
+}
+
+namespace {
+
+struct Cursor {
+  const uint8_t* p;
+  size_t n;
+  size_t off = 0;
+  bool ok = true;
+  template <typename T>
+  T get() {
+    T v{};
+    if (!ok || n - off < sizeof(T)) {
+      ok = false;
+      return v;
+    }
+    std::memcpy(&v, p + off, sizeof(T));
+    off += sizeof(T);
+    return v;
+  }
+};
+
+constexpr uint32_t kPlanMagic = 0x444D5450u;  // "PTMD"
+
+}  // namespace
+
+int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint64_t out_len, Plan& plan) {
+  if (!state) return kInvalidInput;
+  Cursor c{state, state_len};
+  if (c.get<uint32_t>() != kPlanMagic || !c.ok) return kInvalidInput;
+  uint16_t ver = c.get<uint16_t>();
+  uint16_t flags = c.get<uint16_t>();
+  uint32_t n_tensors = c.get<uint32_t>();
+  if (!c.ok || ver != 1 || flags != 0) return kInvalidInput;
+  if (n_tensors > (1u << 24)) return kInvalidInput;
+  plan.tensors.resize(n_tensors);
+  for (uint32_t t = 0; t < n_tensors; ++t) {
+    PlanTensor& T = plan.tensors[t];
+    T.out_offset = c.get<uint64_t>();
+    T.out_len = c.get<uint64_t>();
+    T.chain = c.get<uint8_t>();
+    uint32_t np = c.get<uint8_t>();
+    uint16_t tflags = c.get<uint16_t>();
+    if (!c.ok) return kInvalidInput;
+    T.has_crc = (tflags & 1u) != 0;
+    int want_np = chain_planes(T.chain);
+    if (want_np < 0 || (int)np != want_np || (tflags & ~1u)) return kInvalidInput;
+    if (T.out_offset > out_len || out_len - T.out_offset < T.out_len) return kInvalidInput;
+    T.planes.resize(np);
+    for (uint32_t p = 0; p < np; ++p) {
+      PlanPlane& P = T.planes[p];
+      P.codec = c.get<uint16_t>();
+      uint16_t pflags = c.get<uint16_t>();
+      uint32_t nch = c.get<uint32_t>();
+      P.payload_offset = c.get<uint64_t>();
+      P.payload_len = c.get<uint64_t>();
+      P.plane_len = c.get<uint64_t>();
+      P.crc32 = T.has_crc ? c.get<uint32_t>() : 0;
+      if (!c.ok || (pflags & ~1u)) return kInvalidInput;
+      P.chunked = (pflags & 1u) != 0;
+      if (P.codec != kCodecIdentity && P.codec != kCodecHuffman && P.codec != kCodecRans) return kUnsupported;
+      if (P.payload_offset > in_len || in_len - P.payload_offset < P.payload_len) return kInvalidInput;
+      if (P.chunked) {
+        if (nch == 0 || nch > (1u << 26) || state_len - c.off < (size_t)nch * 8) return kInvalidInput;
+        P.chunks.resize(nch);
+        uint64_t tot = 0;
+        for (uint32_t k = 0; k < nch; ++k) {
+          P.chunks[k].offset_in_payload = c.get<uint32_t>();
+          P.chunks[k].decoded_size = c.get<uint32_t>();
+          tot += P.chunks[k].decoded_size;
+          // container.rs:2000-2015: offsets must not decrease and stay in the payload
+          uint64_t start = P.chunks[k].offset_in_payload;
+          if (start > P.payload_len) return kInvalidInput;
+          if (k > 0 && start < P.chunks[k - 1].offset_in_payload) return kInvalidInput;
+        }
+        if (!c.ok || tot != P.plane_len) return kInvalidInput;
+      } else if (nch != 0) {
+        return kInvalidInput;
+      }
+      // every plane of a chain has the same length (fusion.rs inverse checks)
+      if (P.plane_len != T.planes[0].plane_len) return kInvalidInput;
+    }
+    uint64_t pl = T.planes[0].plane_len;
+    if (pl * (uint64_t)chain_ratio(T.chain) != T.out_len) return kInvalidInput;
+  }
+  if (c.off != state_len) return kInvalidInput;
+  return kOk;
+}
+
+static inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev) {
+  // Pass 1: lay out plane scratch and count jobs.  A plane needs decoding
+  // into scratch unless it is a single unchunked Identity payload whose
+  // (16-byte aligned) bytes can feed the merge directly from the input.
+  constexpr uint64_t kDirect = UINT64_MAX;
+  std::vector<std::vector<uint64_t>> scratch_off(plan.tensors.size());
+  uint64_t scratch_bytes = 0;
+  size_t n_jobs = 0;
+  for (size_t t = 0; t < plan.tensors.size(); ++t) {
+    const PlanTensor& T = plan.tensors[t];
+    scratch_off[t].assign(T.planes.size(), kDirect);
+    for (size_t p = 0; p < T.planes.size(); ++p) {
+      const PlanPlane& P = T.planes[p];
+      uint64_t direct = in_dev + P.payload_offset;
+      if (P.codec == kCodecIdentity && !P.chunked && P.payload_len == P.plane_len && (direct & 15u) == 0)
+        continue;
+      scratch_off[t][p] = scratch_bytes;
+      scratch_bytes = align_up(scratch_bytes + P.plane_len, 256);
+      n_jobs += P.chunked ? P.chunks.size() : 1;
+    }
+  }
+  if (n_jobs > 0xFFFFFFFFull) return kInvalidInput;
+  PTWM_HIP_TRY(ctx.planes.ensure(scratch_bytes ? scratch_bytes : 256));
+  PTWM_HIP_TRY(ctx.jobs.ensure(n_jobs * sizeof(DecodeJob) + 64));
+  PTWM_HIP_TRY(ctx.status.ensure(n_jobs * sizeof(uint32_t) + 64));
+  PTWM_HIP_TRY(ctx.h_jobs.ensure(n_jobs * sizeof(DecodeJob) + 64));
+  PTWM_HIP_TRY(ctx.h_status.ensure(n_jobs * sizeof(uint32_t) + 64));
+  const uint64_t scratch_base = reinterpret_cast<uint64_t>(ctx.planes.ptr);
+  DecodeJob* hj = static_cast<DecodeJob*>(ctx.h_jobs.ptr);
+  std::vector<std::vector<uint64_t>> plane_addr(plan.tensors.size());
+  size_t j = 0;
+  for (size_t t = 0; t < plan.tensors.size(); ++t) {
+    const PlanTensor& T = plan.tensors[t];
+    plane_addr[t].resize(T.planes.size());
+    for (size_t p = 0; p < T.planes.size(); ++p) {
+      const PlanPlane& P = T.planes[p];
+      if (scratch_off[t][p] == kDirect) {
+        plane_addr[t][p] = in_dev + P.payload_offset;
+        continue;
+      }
+      const uint64_t a = scratch_base + scratch_off[t][p];
+      plane_addr[t][p] = a;
+      if (!P.chunked) {
+        DecodeJob& J = hj[j++];
+        std::memset(&J, 0, sizeof(J));
+        J.src = in_dev + P.payload_offset;
+        J.src_len = P.payload_len;
+        J.dst = a;
+        J.dst_len = P.plane_len;
+        J.codec = P.codec;
+        J.framed = 0;
+        continue;
+      }
+      uint64_t dst_off = 0;
+      for (size_t k = 0; k < P.chunks.size(); ++k) {
+        uint64_t start = P.chunks[k].offset_in_payload;
+        uint64_t end = k + 1 < P.chunks.size() ? P.chunks[k + 1].offset_in_payload : P.payload_len;
+        DecodeJob& J = hj[j++];
+        std::memset(&J, 0, sizeof(J));
+        J.src = in_dev + P.payload_offset + start;
+        J.src_len = end - start;
+        J.dst = a + dst_off;
+        J.dst_len = P.chunks[k].decoded_size;
+        J.codec = P.codec;
+        J.framed = 1;
+        dst_off += P.chunks[k].decoded_size;
+      }
+    }
+  }
+  if (j != n_jobs) return kInternal;
+  hipStream_t s = ctx.stream;
+  if (ctx.profile) PTWM_HIP_TRY(ctx.ensure_events());
+  if (n_jobs) PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, hj, n_jobs * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
+  if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[0], s));
+  if (n_jobs) {
+    PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr),
+                                     static_cast<uint32_t*>(ctx.status.ptr), (uint32_t)n_jobs, s));
+  }
+  if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[1], s));
+  for (size_t t = 0; t < plan.tensors.size(); ++t) {
+    const PlanTensor& T = plan.tensors[t];
+    const uint8_t* pp[4] = {nullptr, nullptr, nullptr, nullptr};
+    for (size_t p = 0; p < T.planes.size(); ++p) pp[p] = reinterpret_cast<const uint8_t*>(plane_addr[t][p]);
+    uint8_t* out = reinterpret_cast<uint8_t*>(out_dev + T.out_offset);
+    if (T.planes[0].plane_len == 0) continue;
+    if ((reinterpret_cast<uintptr_t>(out) & 15u) != 0) return kInvalidInput;
+    PTWM_HIP_TRY(launch_merge(T.chain, pp, T.planes[0].plane_len, out, s));
+  }
+  if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], s));
+  if (n_jobs) {
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.h_status.ptr, ctx.status.ptr, n_jobs * sizeof(uint32_t),
+                                hipMemcpyDeviceToHost, s));
+  }
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  if (ctx.profile) {
+    PTWM_HIP_TRY(hipEventElapsedTime(&ctx.last_ms[0], ctx.ev[0], ctx.ev[1]));
+    PTWM_HIP_TRY(hipEventElapsedTime(&ctx.last_ms[1], ctx.ev[1], ctx.ev[2]));
+    PTWM_HIP_TRY(hipEventElapsedTime(&ctx.last_ms[2], ctx.ev[0], ctx.ev[2]));
+  }
+  const uint32_t* st = static_cast<const uint32_t*>(ctx.h_status.ptr);
+  for (size_t k = 0; k < n_jobs; ++k)
+    if (st[k] != kStOk) return kInvalidInput;
+  return kOk;
+}
+
+}  // namespace ptwm

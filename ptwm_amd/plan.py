@@ -1,0 +1,91 @@
+"""Decode plans: the state bytes of the tensor-level entry point.
+
+A plan lists tensors the way the container stores them
+(crates/ptwm-core/src/container.rs:1795-2196): per tensor its chain and, per
+plane, the codec wire id, the payload's offset and length in the input
+buffer, the decoded plane length, an optional CRC32 and the chunk table
+(plane_record.rs:16-20: ``(offset_in_payload u32, decoded_size u32)``).
+Binary layout (little endian), "PTMD" version 1:
+
+    u32 magic 0x444D5450 | u16 version=1 | u16 flags=0 | u32 n_tensors
+    tensor: u64 out_offset | u64 out_len | u8 chain | u8 n_planes | u16 flags (bit0 crc)
+      plane: u16 codec | u16 flags (bit0 chunked) | u32 n_chunks
+             | u64 payload_offset | u64 payload_len | u64 plane_len
+             | [u32 crc32 if tensor crc flag] | n_chunks x (u32 offset, u32 size)
+"""
+from __future__ import annotations
+
+import struct
+from dataclasses import dataclass, field
+
+CHAIN_IEEE16_SPLIT2 = 1
+CHAIN_IEEE32_SPLIT4 = 2
+CHAIN_E4M3_NIBBLE = 3
+CHAIN_E5M2_NIBBLE = 4
+CHAIN_NIBBLE_SPLIT = 5
+CHAIN_PASSTHROUGH = 6
+CHAIN_PLANES = {1: 2, 2: 4, 3: 2, 4: 2, 5: 2, 6: 1}
+CHAIN_RATIO = {1: 2, 2: 4, 3: 1, 4: 1, 5: 1, 6: 1}
+MAGIC = 0x444D5450
+
+
+@dataclass
+class PlanePlan:
+    codec: int
+    payload_offset: int
+    payload_len: int
+    plane_len: int
+    chunks: list[tuple[int, int]] | None = None   # (offset_in_payload, decoded_size)
+    crc32: int | None = None
+
+
+@dataclass
+class TensorPlan:
+    chain: int
+    out_offset: int
+    out_len: int
+    planes: list[PlanePlan] = field(default_factory=list)
+
+
+def encode_plan(tensors: list[TensorPlan]) -> bytes:
+    out = bytearray(struct.pack("<IHHI", MAGIC, 1, 0, len(tensors)))
+    for t in tensors:
+        has_crc = any(p.crc32 is not None for p in t.planes)
+        out += struct.pack("<QQBBH", t.out_offset, t.out_len, t.chain, len(t.planes), 1 if has_crc else 0)
+        for p in t.planes:
+            ch = p.chunks or []
+            out += struct.pack("<HHIQQQ", p.codec, 1 if p.chunks is not None else 0, len(ch),
+                               p.payload_offset, p.payload_len, p.plane_len)
+            if has_crc:
+                out += struct.pack("<I", p.crc32 or 0)
+            for off, size in ch:
+                out += struct.pack("<II", off, size)
+    return bytes(out)
+
+
+def decode_plan(buf: bytes) -> list[TensorPlan]:
+    magic, ver, flags, n = struct.unpack_from("<IHHI", buf, 0)
+    if magic != MAGIC or ver != 1 or flags != 0:
+        raise ValueError("not a PTMD v1 plan")
+    o = 12
+    res = []
+    for _ in range(n):
+        off, ln, chain, np_, tfl = struct.unpack_from("<QQBBH", buf, o)
+        o += 20
+        t = TensorPlan(chain, off, ln)
+        for _ in range(np_):
+            codec, pfl, nch, po, pl, plen = struct.unpack_from("<HHIQQQ", buf, o)
+            o += 32
+            crc = None
+            if tfl & 1:
+                (crc,) = struct.unpack_from("<I", buf, o)
+                o += 4
+            chunks = None
+            if pfl & 1:
+                chunks = [struct.unpack_from("<II", buf, o + 8 * k) for k in range(nch)]
+                o += 8 * nch
+            t.planes.append(PlanePlan(codec, po, pl, plen, chunks, crc))
+        res.append(t)
+    if o != len(buf):
+        raise ValueError("trailing bytes in plan")
+    return res
