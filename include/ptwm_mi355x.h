@@ -114,6 +114,24 @@ int64_t ptwm_mi355x_split_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_le
 int64_t ptwm_mi355x_merge_cuda(uint32_t chain, const uint64_t *plane_dev_ptrs, uint32_t n_planes, size_t plane_len,
                                uint64_t out_dev_ptr, size_t out_cap, uint32_t device_ordinal);
 
+/* Tensor-level encode (the forward counterpart of the hardware-backend decode):
+ * the tensor at in_dev is split by `chain` into planes, every plane is coded
+ * with this library's huff_ilv codec (stored as Identity when coding does not
+ * shrink it), and the payloads are written to out_dev (256-byte aligned; each
+ * payload starts at a 256-byte boundary).  A PTMD v1 decode plan describing
+ * the result (payload offsets relative to out_dev) is written to plan_out and
+ * its length to *plan_len_out.  Returns the bytes used in out_dev; -2 with
+ * *needed_out set when out_cap is too small. */
+int64_t ptwm_mi355x_encode_tensor_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                                       size_t out_cap, uint8_t *plan_out, size_t plan_cap, size_t *plan_len_out,
+                                       uint64_t *needed_out, uint32_t device_ordinal);
+
+/* Canonical Huffman code lengths the reference encoder assigns to a 256-bin
+ * histogram (entropy/huffman/tree.rs:19-85 with the 11-bit limit of
+ * :212-242), computed on the host.  Returns 0, or -1 for an all-zero
+ * histogram. */
+int64_t ptwm_mi355x_huffman_code_lengths(const uint32_t *freqs, uint8_t *lengths_out);
+
 /* Kernel timing with HIP events recorded on the library stream around each
  * phase of the next calls on the device (off by default). */
 int64_t ptwm_mi355x_set_profiling(uint32_t device_ordinal, uint32_t on);

@@ -343,3 +343,32 @@ def histogram(data):
     h = np.zeros(256, np.uint32)
     lib().por_histogram(_ptr(b), b.size, _ptr(h))
     return h
+
+
+# ---- huff_ilv (this build's own codec; the functions are its spec) ----
+
+def ilv_encode(plane) -> bytes:
+    L = lib()
+    L.por_ilv_encode.restype = C.c_int64
+    L.por_ilv_encode.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]
+    L.por_ilv_encode_bound.restype = C.c_size_t
+    L.por_ilv_encode_bound.argtypes = [C.c_size_t]
+    s = _buf(plane)
+    cap = int(L.por_ilv_encode_bound(s.size))
+    out = np.zeros(cap, np.uint8)
+    n = L.por_ilv_encode(_ptr(s), s.size, _ptr(out), cap)
+    if n < 0:
+        raise OracleError(n, "ilv_encode")
+    return out[:n].tobytes()
+
+
+def ilv_decode(payload, cap: int) -> bytes:
+    L = lib()
+    L.por_ilv_decode.restype = C.c_int64
+    L.por_ilv_decode.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]
+    p = _buf(payload)
+    out = np.zeros(max(cap, 1), np.uint8)
+    n = L.por_ilv_decode(_ptr(p), p.size, _ptr(out), cap)
+    if n < 0:
+        raise OracleError(n, "ilv_decode")
+    return out[:n].tobytes()

@@ -891,6 +891,151 @@ int64_t por_decode_plane_chunked_mt(int codec, const uint8_t *payload, size_t pa
 }
 
 /* ------------------------------------------------------------------------- */
+/* huff_ilv (this build's own codec; executable specification)               */
+/*                                                                           */
+/* payload: [tag u8] tag 0: stored plane bytes follow.  tag 1:               */
+/*   [orig_len u32][weights header (weights.rs)][0-pad to 4][off u32 x nb+1] */
+/*   [data]; nb = ceil(n / 16384).  Block b = data[off[b]..off[b+1]):        */
+/*   [64 x u8 lane word counts][lane 0 words][lane 1 words]...(u32 LE).      */
+/*   Lane j codes groups g = j + 64 r (r = 0..15), group g = plane positions  */
+/*   [b*16384 + 16 g, +16) clipped to n, as rev(canonical code) bits packed  */
+/*   LSB-first into its words (the reference's code/bit order, tree.rs).     */
+/* ------------------------------------------------------------------------- */
+
+#define ILV_BLOCK 16384
+#define ILV_LANES 64
+#define ILV_GROUP 16
+
+size_t por_ilv_encode_bound(size_t len) {
+    size_t nb = (len + ILV_BLOCK - 1) / ILV_BLOCK;
+    return 1 + len + 5 + 130 + 3 + 4 * (nb + 1) + nb * 64 + len * 11 / 8 + nb * 64 * 4 + 16;
+}
+
+int64_t por_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap) {
+    if (n == 0) { if (cap < 1) return POR_ESMALL; out[0] = 0; return 1; }
+    uint32_t freqs[256];
+    por_histogram(plane, n, freqs);
+    uint8_t lengths[256];
+    uint16_t table[1 << HUF_MAX_TABLE_LOG], rev[256];
+    int ok = por_huf_lengths_from_freqs(freqs, lengths) && por_huf_from_lengths(lengths, table, rev);
+    size_t nb = (n + ILV_BLOCK - 1) / ILV_BLOCK;
+    if (ok && n <= 0xFFFFFFFFu) {
+        int nw = 0;
+        for (int s = 0; s < 256; s++) if (lengths[s]) nw = s + 1;
+        uint8_t hdr[140];
+        int64_t wl = por_huf_encode_weights(lengths, (size_t)nw, hdr, sizeof(hdr));
+        size_t head = 5 + (size_t)wl;
+        head += (4 - head % 4) % 4;
+        size_t tab = head, data0 = tab + 4 * (nb + 1);
+        /* size pass */
+        size_t total = 0;
+        uint32_t *words = (uint32_t *)malloc(nb * ILV_LANES * sizeof(uint32_t));
+        for (size_t b = 0; b < nb; b++) {
+            size_t bsz = 64;
+            for (int j = 0; j < ILV_LANES; j++) {
+                uint64_t bits = 0;
+                for (int r = 0; r < ILV_BLOCK / (ILV_LANES * ILV_GROUP); r++) {
+                    size_t g = (size_t)j + (size_t)ILV_LANES * r, a = b * ILV_BLOCK + ILV_GROUP * g;
+                    for (size_t k = a; k < a + ILV_GROUP && k < n; k++) bits += lengths[plane[k]];
+                }
+                words[b * ILV_LANES + j] = (uint32_t)((bits + 31) / 32);
+                bsz += 4 * (size_t)words[b * ILV_LANES + j];
+            }
+            total += bsz;
+        }
+        if (data0 + total < 1 + n && data0 + total <= cap) {
+            memset(out, 0, data0 + total);
+            out[0] = 1; st32(out + 1, (uint32_t)n);
+            memcpy(out + 5, hdr, (size_t)wl);
+            size_t off = 0;
+            for (size_t b = 0; b < nb; b++) {
+                st32(out + tab + 4 * b, (uint32_t)off);
+                uint8_t *blk = out + data0 + off;
+                size_t wpos = 0;
+                for (int j = 0; j < ILV_LANES; j++) {
+                    blk[j] = (uint8_t)words[b * ILV_LANES + j];
+                    uint8_t *lw = blk + 64 + 4 * wpos;
+                    uint64_t acc = 0; uint32_t cnt = 0; size_t wi = 0;
+                    for (int r = 0; r < ILV_BLOCK / (ILV_LANES * ILV_GROUP); r++) {
+                        size_t g = (size_t)j + (size_t)ILV_LANES * r, a = b * ILV_BLOCK + ILV_GROUP * g;
+                        for (size_t k = a; k < a + ILV_GROUP && k < n; k++) {
+                            acc |= (uint64_t)rev[plane[k]] << cnt;
+                            cnt += lengths[plane[k]];
+                            if (cnt >= 32) { st32(lw + 4 * wi++, (uint32_t)acc); acc >>= 32; cnt -= 32; }
+                        }
+                    }
+                    if (cnt) st32(lw + 4 * wi++, (uint32_t)acc);
+                    wpos += words[b * ILV_LANES + j];
+                }
+                off += 64 + 4 * wpos;
+            }
+            st32(out + tab + 4 * nb, (uint32_t)off);
+            free(words);
+            return (int64_t)(data0 + total);
+        }
+        free(words);
+    }
+    if (1 + n > cap) return POR_ESMALL;
+    out[0] = 0;
+    memcpy(out + 1, plane, n);
+    return (int64_t)(1 + n);
+}
+
+int64_t por_ilv_decode(const uint8_t *p, size_t len, uint8_t *out, size_t cap) {
+    if (len == 0) return POR_EINVAL;
+    if (p[0] == 0) {
+        if (len - 1 > cap) return POR_ESMALL;
+        memcpy(out, p + 1, len - 1);
+        return (int64_t)(len - 1);
+    }
+    if (p[0] != 1 || len < 5) return POR_EINVAL;
+    size_t n = ld32(p + 1);
+    if (n > cap) return POR_ESMALL;
+    uint8_t w[256];
+    int nw = 0;
+    int64_t wl = por_huf_decode_weights(p + 5, len - 5, w, &nw);
+    if (wl < 0) return POR_EINVAL;
+    uint8_t lengths[256] = {0};
+    for (int i = 0; i < nw; i++) { if (w[i] > HUF_MAX_TABLE_LOG) return POR_EINVAL; lengths[i] = w[i]; }
+    uint16_t table[1 << HUF_MAX_TABLE_LOG];
+    int mb = por_huf_from_lengths(lengths, table, NULL);
+    if (!mb) return POR_EINVAL;
+    size_t head = 5 + (size_t)wl;
+    head += (4 - head % 4) % 4;
+    size_t nb = (n + ILV_BLOCK - 1) / ILV_BLOCK, data0 = head + 4 * (nb + 1);
+    if (data0 > len) return POR_EINVAL;
+    size_t dlen = len - data0;
+    if (ld32(p + head) != 0 || ld32(p + head + 4 * nb) != dlen) return POR_EINVAL;
+    for (size_t b = 0; b < nb; b++) {
+        size_t o0 = ld32(p + head + 4 * b), o1 = ld32(p + head + 4 * (b + 1));
+        if (o1 < o0 || o1 > dlen || o1 - o0 < 64) return POR_EINVAL;
+        const uint8_t *blk = p + data0 + o0;
+        size_t wpos = 0;
+        for (int j = 0; j < ILV_LANES; j++) wpos += blk[j];
+        if (64 + 4 * wpos != o1 - o0) return POR_EINVAL;
+        wpos = 0;
+        for (int j = 0; j < ILV_LANES; j++) {
+            const uint8_t *lw = blk + 64 + 4 * wpos;
+            size_t nwords = blk[j], wi = 0;
+            uint64_t acc = 0, used = 0; uint32_t cnt = 0;
+            for (int r = 0; r < ILV_BLOCK / (ILV_LANES * ILV_GROUP); r++) {
+                size_t g = (size_t)j + (size_t)ILV_LANES * r, a = b * ILV_BLOCK + ILV_GROUP * g;
+                for (size_t k = a; k < a + ILV_GROUP && k < n; k++) {
+                    if (cnt < 32) { if (wi < nwords) acc |= (uint64_t)ld32(lw + 4 * wi) << cnt; wi++; cnt += 32; }
+                    uint16_t e = table[acc & (((uint64_t)1 << mb) - 1)];
+                    out[k] = (uint8_t)e;
+                    acc >>= (e >> 8); cnt -= (e >> 8); used += (e >> 8);
+                }
+            }
+            /* a lane's words hold exactly its codes (acceptance rule) */
+            if ((used + 31) / 32 != nwords) return POR_EINVAL;
+            wpos += nwords;
+        }
+    }
+    return (int64_t)n;
+}
+
+/* ------------------------------------------------------------------------- */
 /* CRC-32/ISO-HDLC (crc32fast 1.5.0), reflected poly 0xEDB88320              */
 /* ------------------------------------------------------------------------- */
 

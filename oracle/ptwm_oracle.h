@@ -129,6 +129,15 @@ int64_t por_decode_plane_chunked_mt(int codec, const uint8_t *payload, size_t pa
                                     const uint32_t *entries, size_t n_chunks, uint8_t *out,
                                     size_t cap, int threads);
 
+/* ---- huff_ilv: this build's GPU-native plane codec (no reference
+ * counterpart; its wire format is specified by these two functions).  Code
+ * lengths, canonical codes and the weights header are the reference
+ * Huffman's (tree.rs, weights.rs); the bits are split over 64 lane
+ * sub-streams per 16384-symbol block. ---- */
+int64_t por_ilv_encode(const uint8_t *plane, size_t len, uint8_t *out, size_t cap);
+int64_t por_ilv_decode(const uint8_t *payload, size_t len, uint8_t *out, size_t cap);
+size_t por_ilv_encode_bound(size_t len);
+
 /* ---- integrity (crc32fast 1.5.0 / xxhash-rust 0.8.18 / blake3 1.x) ---- */
 uint32_t por_crc32(uint32_t crc, const uint8_t *data, size_t len);
 uint64_t por_xxh64(const uint8_t *data, size_t len, uint64_t seed);

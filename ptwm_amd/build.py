@@ -16,7 +16,8 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libptwm_mi355x.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["transform.hip", "decode_exact.hip", "runtime.hip", "abi.hip"]
+SOURCES = ["transform.hip", "decode_exact.hip", "huff_ilv.hip", "ilv_host.hip", "huffman_host.cpp", "runtime.hip",
+           "abi.hip"]
 
 CFLAGS = [
     "--offload-arch=gfx950",
@@ -31,7 +32,7 @@ CFLAGS = [
 
 
 def _compile(src: str) -> str:
-    obj = os.path.join(OBJ, src.replace(".hip", ".o"))
+    obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
     cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"

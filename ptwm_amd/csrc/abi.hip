@@ -9,6 +9,7 @@
 #include <cstring>
 
 #include "../../include/ptwm_mi355x.h"
+#include "ilv_host.h"
 #include "runtime.h"
 
 namespace ptwm {
@@ -127,6 +128,46 @@ int64_t decode_one_payload(DevCtx& ctx, uint32_t codec, uint64_t in_dev, size_t 
   return (int64_t)expected;
 }
 
+// One huff_ilv payload -> plane bytes (fused kernel, passthrough chain).
+int64_t ilv_decode_payload(DevCtx& ctx, uint64_t in_dev, size_t in_len, uint64_t out_dev, size_t out_cap) {
+  if (in_len == 0) return kInvalidInput;
+  PTWM_HIP_TRY(ctx.h_small.ensure(64));
+  uint8_t* hdr = static_cast<uint8_t*>(ctx.h_small.ptr);
+  const size_t nh = in_len < 5 ? in_len : 5;
+  PTWM_HIP_TRY(hipMemcpyAsync(hdr, reinterpret_cast<const void*>(in_dev), nh, hipMemcpyDeviceToHost, ctx.stream));
+  PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+  uint64_t expected;
+  if (hdr[0] == 0) {
+    expected = in_len - 1;
+  } else if (hdr[0] == 1 && in_len >= 5) {
+    expected = (uint64_t)hdr[1] | ((uint64_t)hdr[2] << 8) | ((uint64_t)hdr[3] << 16) | ((uint64_t)hdr[4] << 24);
+  } else {
+    return kInvalidInput;
+  }
+  if (expected > out_cap) return kBufferTooSmall;
+  if (expected == 0) return 0;
+  if (hdr[0] == 0) {
+    PTWM_HIP_TRY(launch_copy(reinterpret_cast<const uint8_t*>(in_dev + 1), reinterpret_cast<uint8_t*>(out_dev),
+                             expected, ctx.stream));
+    PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+    return (int64_t)expected;
+  }
+  if (out_dev & 15u) return kInvalidInput;
+  IlvTensor X{};
+  X.out = out_dev;
+  X.n = expected;
+  X.chain = kChainPassthrough;
+  X.n_planes = 1;
+  X.planes[0].base = in_dev;
+  X.planes[0].len = in_len;
+  X.planes[0].coded = 1;
+  int64_t rc = ilv_decode_tensors(ctx, std::vector<IlvTensor>{X});
+  return rc == kOk ? (int64_t)expected : rc;
+}
+
+// Host-buffer entry points stage through device memory on device 0.
+constexpr uint32_t kHostDevice = 0;
+
 }  // namespace
 }  // namespace ptwm
 
@@ -163,9 +204,9 @@ int64_t ptwm_plane_codec_v1_decode_cuda(uint8_t state_format_version, const uint
   if (!lookup_codec(codec_id_ptr, codec_id_len, codec)) return kUnsupported;
   if (state_len != 0) return kInvalidInput;  // none of these codecs carries state
   if ((in_len && !in_dev_ptr) || (out_cap && !out_dev_ptr)) return kInvalidInput;
-  if (codec == kCodecHuffIlv) return kUnsupported;
   DeviceScope ds(device_ordinal);
   if (!ds.ok) return kInvalidInput;
+  if (codec == kCodecHuffIlv) return ilv_decode_payload(*ds.ctx, in_dev_ptr, in_len, out_dev_ptr, out_cap);
   return decode_one_payload(*ds.ctx, codec, in_dev_ptr, in_len, out_dev_ptr, out_cap);
 }
 
@@ -175,16 +216,19 @@ int64_t ptwm_plane_codec_v1_encode_cuda(uint8_t state_format_version, const uint
                                         uint32_t device_ordinal) {
   (void)state_format_version;
   (void)state_ptr;
-  (void)in_dev_ptr;
-  (void)in_len;
-  (void)out_dev_ptr;
-  (void)out_cap;
-  (void)needed_out;
-  (void)device_ordinal;
   uint32_t codec = 0;
   if (!lookup_codec(codec_id_ptr, codec_id_len, codec)) return kUnsupported;
   if (state_len != 0) return kInvalidInput;
-  return kUnsupported;
+  if ((in_len && !in_dev_ptr) || (out_cap && !out_dev_ptr)) return kInvalidInput;
+  if (codec != kCodecHuffIlv) return kUnsupported;
+  if ((in_dev_ptr & 15u) || (out_dev_ptr & 3u)) return kInvalidInput;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  IlvEncResult r{};
+  uint64_t needed = 0, n = in_len;
+  int64_t rc = ilv_encode_planes(*ds.ctx, &in_dev_ptr, &n, 1, out_dev_ptr, out_cap, false, &r, &needed);
+  if (rc == kBufferTooSmall && needed_out) *needed_out = needed;
+  return rc < 0 ? rc : (int64_t)r.len;
 }
 
 int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_version, const uint8_t* state_ptr,
@@ -215,19 +259,39 @@ int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_versi
 }
 
 int64_t ptwm_plane_codec_v1_encode(const uint8_t* in, size_t in_len, uint8_t* out, size_t out_len) {
-  (void)in;
-  (void)in_len;
-  (void)out;
-  (void)out_len;
-  return kUnsupported;
+  if ((in_len && !in) || (out_len && !out)) return kInvalidInput;
+  DeviceScope ds(kHostDevice);
+  if (!ds.ok) return kMissingCapability;
+  DevCtx& ctx = *ds.ctx;
+  PTWM_HIP_TRY(ctx.stage_in.ensure(in_len + 16));
+  const uint64_t bound = in_len + 1;  // stored size; the coded size is smaller or unused
+  PTWM_HIP_TRY(ctx.stage_out.ensure(bound + 64));
+  if (in_len) PTWM_HIP_TRY(hipMemcpyAsync(ctx.stage_in.ptr, in, in_len, hipMemcpyHostToDevice, ctx.stream));
+  IlvEncResult r{};
+  uint64_t needed = 0, n = in_len, src = reinterpret_cast<uint64_t>(ctx.stage_in.ptr);
+  int64_t rc = ilv_encode_planes(ctx, &src, &n, 1, reinterpret_cast<uint64_t>(ctx.stage_out.ptr), bound, false, &r,
+                                 &needed);
+  if (rc < 0) return rc;
+  if (r.len > out_len) return kBufferTooSmall;
+  PTWM_HIP_TRY(hipMemcpyAsync(out, ctx.stage_out.ptr, r.len, hipMemcpyDeviceToHost, ctx.stream));
+  PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+  return (int64_t)r.len;
 }
 
 int64_t ptwm_plane_codec_v1_decode(const uint8_t* in, size_t in_len, uint8_t* out, size_t out_len) {
-  (void)in;
-  (void)in_len;
-  (void)out;
-  (void)out_len;
-  return kUnsupported;
+  if ((in_len && !in) || (out_len && !out)) return kInvalidInput;
+  DeviceScope ds(kHostDevice);
+  if (!ds.ok) return kMissingCapability;
+  DevCtx& ctx = *ds.ctx;
+  PTWM_HIP_TRY(ctx.stage_in.ensure(in_len + 16));
+  PTWM_HIP_TRY(ctx.stage_out.ensure(out_len + 64));
+  if (in_len) PTWM_HIP_TRY(hipMemcpyAsync(ctx.stage_in.ptr, in, in_len, hipMemcpyHostToDevice, ctx.stream));
+  int64_t rc = ilv_decode_payload(ctx, reinterpret_cast<uint64_t>(ctx.stage_in.ptr), in_len,
+                                  reinterpret_cast<uint64_t>(ctx.stage_out.ptr), out_len);
+  if (rc <= 0) return rc;
+  PTWM_HIP_TRY(hipMemcpyAsync(out, ctx.stage_out.ptr, (size_t)rc, hipMemcpyDeviceToHost, ctx.stream));
+  PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+  return rc;
 }
 
 int64_t ptwm_plane_codec_v1_decode_stateful(uint8_t state_format_version, const uint8_t* state_ptr,
@@ -284,6 +348,59 @@ int64_t ptwm_mi355x_merge_cuda(uint32_t chain, const uint64_t* plane_dev_ptrs, u
     ctx.last_ms[2] = ctx.last_ms[1];
   }
   return (int64_t)out_len;
+}
+
+int64_t ptwm_mi355x_encode_tensor_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                                       size_t out_cap, uint8_t* plan_out, size_t plan_cap, size_t* plan_len_out,
+                                       uint64_t* needed_out, uint32_t device_ordinal) {
+  const int np = chain_planes(chain);
+  if (np < 0 || !plan_out || !plan_len_out) return kInvalidInput;
+  const uint64_t ratio = (uint64_t)chain_ratio(chain);
+  if (in_len % ratio || (in_dev_ptr & 15u) || (out_dev_ptr & 255u)) return kInvalidInput;
+  const uint64_t plane_len = in_len / ratio;
+  const size_t plan_len = 12 + 20 + (size_t)np * 32;
+  if (plan_cap < plan_len) return kBufferTooSmall;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  DevCtx& ctx = *ds.ctx;
+  // forward chain into plane scratch, then every plane through the encoder
+  const uint64_t stride = (plane_len + 255) / 256 * 256;
+  PTWM_HIP_TRY(ctx.enc_split.ensure(stride * np + 256));
+  uint8_t* pl[4] = {};
+  uint64_t srcs[4], lens[4];
+  for (int i = 0; i < np; ++i) {
+    pl[i] = static_cast<uint8_t*>(ctx.enc_split.ptr) + stride * i;
+    srcs[i] = reinterpret_cast<uint64_t>(pl[i]);
+    lens[i] = plane_len;
+  }
+  if (plane_len && launch_split(chain, reinterpret_cast<const uint8_t*>(in_dev_ptr), plane_len, pl, ctx.stream) !=
+                       hipSuccess)
+    return kInvalidInput;
+  IlvEncResult r[4] = {};
+  uint64_t needed = 0;
+  int64_t rc = ilv_encode_planes(ctx, srcs, lens, (uint32_t)np, out_dev_ptr, out_cap, true, r, &needed);
+  if (rc == kBufferTooSmall && needed_out) *needed_out = needed;
+  if (rc < 0) return rc;
+  // decode plan (PTMD v1) for the one tensor
+  uint8_t* o = plan_out;
+  auto put = [&](const void* v, size_t k) {
+    std::memcpy(o, v, k);
+    o += k;
+  };
+  const uint32_t magic = 0x444D5450u, ntens = 1;
+  const uint16_t ver = 1, flags = 0, tflags = 0;
+  const uint64_t zero64 = 0, out_len = in_len;
+  const uint8_t ch = (uint8_t)chain, npl = (uint8_t)np;
+  put(&magic, 4); put(&ver, 2); put(&flags, 2); put(&ntens, 4);
+  put(&zero64, 8); put(&out_len, 8); put(&ch, 1); put(&npl, 1); put(&tflags, 2);
+  for (int i = 0; i < np; ++i) {
+    const uint16_t codec = (uint16_t)r[i].codec, pf = 0;
+    const uint32_t nch = 0;
+    put(&codec, 2); put(&pf, 2); put(&nch, 4);
+    put(&r[i].offset, 8); put(&r[i].len, 8); put(&plane_len, 8);
+  }
+  *plan_len_out = (size_t)(o - plan_out);
+  return rc;
 }
 
 int64_t ptwm_mi355x_set_profiling(uint32_t device_ordinal, uint32_t on) {

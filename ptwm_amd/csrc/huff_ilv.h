@@ -1,0 +1,66 @@
+// huff_ilv.h -- descriptors and launchers of the GPU-native interleaved
+// Huffman codec (format and design notes in huff_ilv.hip).
+#pragma once
+
+#include "ptwm_common.h"
+
+namespace ptwm {
+
+constexpr uint32_t kIlvBlock = 16384;   // symbols per block (one wavefront)
+constexpr uint32_t kIlvLanes = 64;
+constexpr uint32_t kIlvGroup = 16;      // symbols per lane per round
+constexpr uint32_t kIlvRounds = kIlvBlock / (kIlvLanes * kIlvGroup);  // 16
+constexpr uint32_t kIlvBlocksPerTile = 16;  // blocks per workgroup (4 per wave)
+
+// status bits (per tensor)
+constexpr uint32_t kIlvErrHeader = 1;   // tag / length / weights / table bounds
+constexpr uint32_t kIlvErrBlock = 2;    // block offsets or lane word counts inconsistent
+constexpr uint32_t kIlvErrLane = 4;     // a lane's word count disagrees with its codes
+
+struct IlvPlane {
+  uint64_t base;   // coded: payload address; raw: plane bytes (16-byte aligned)
+  uint64_t len;    // coded: payload length
+  uint32_t coded;  // 1: huff_ilv coded payload; 0: raw plane bytes
+  uint32_t lut;    // LDS table slot of a coded plane
+};
+
+struct IlvTensor {
+  uint64_t out;    // output tensor address (16-byte aligned)
+  uint64_t n;      // plane length (elements)
+  uint32_t chain;
+  uint32_t n_planes;
+  IlvPlane planes[4];
+};
+
+struct IlvTile {
+  uint32_t tensor;
+  uint32_t block0;
+  uint32_t nblocks;
+  uint32_t pad;
+};
+
+struct IlvEncPlane {
+  uint64_t src;        // plane bytes (16-byte aligned)
+  uint64_t n;
+  uint32_t code_slot;  // index of its 256-entry code table
+  uint32_t pad;
+};
+
+struct IlvEncBlock {
+  uint64_t dst;        // device address of the block's data (lane counts first)
+  uint32_t plane;
+  uint32_t block;      // block index within the plane
+  uint32_t lw;         // row of this block in the size pass's lane word counts
+  uint32_t pad;
+};
+
+hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const IlvTile* tiles, uint32_t n_tiles,
+                             uint32_t* status, hipStream_t stream);
+hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_t max_n, uint32_t* hist,
+                           hipStream_t stream);
+hipError_t launch_ilv_size(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,
+                           const uint32_t* codes, uint8_t* lane_words, uint32_t* block_bytes, hipStream_t stream);
+hipError_t launch_ilv_encode(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,
+                             const uint32_t* codes, const uint8_t* lane_words, hipStream_t stream);
+
+}  // namespace ptwm

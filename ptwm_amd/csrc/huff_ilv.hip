@@ -1,0 +1,590 @@
+// huff_ilv.hip -- the GPU-native interleaved Huffman plane codec on gfx950.
+//
+// Wire format (codec wire id 0x7F01, this library's plane-codec id):
+//   [tag u8] 0: stored plane bytes follow.  1: coded:
+//   [orig_len u32 LE][weights header (entropy/huffman/weights.rs)][0-pad to 4]
+//   [block offset table u32 x (nb + 1)][data],  nb = ceil(n / 16384)
+//   block b = data[off[b] .. off[b+1]):
+//     [64 x u8 lane word counts][lane 0 words][lane 1 words]...  (u32 LE)
+//   lane j codes the 16-symbol groups g = j + 64 r (r = 0..15) of its block,
+//   group g = plane positions [16384 b + 16 g, +16) (clipped to n), as the
+//   reference's bit-reversed canonical codes (tree.rs:102-177) packed
+//   LSB-first.  Acceptance: each lane's word count == ceil(bits used / 32).
+//
+// Decode: one wavefront per block.  In round r every lane decodes one group,
+// so a round's 64 groups are 1024 consecutive symbols and the merged output
+// of a round is one contiguous span: all stores are coalesced dwordx4.  An
+// 11-bit multi-symbol lookup table in LDS (up to 3 symbols per lookup) is
+// built per workgroup from the payload's weights header.  Tensors whose
+// planes are all stored-aligned or huff_ilv-coded are decoded and merged in
+// one pass (decode -> inverse chain -> store), so planes never round-trip
+// through HBM.
+//
+// Encode: LDS-privatised histograms merged with atomics, host code-table
+// build (256 symbols), a size pass (one wave per block: per-lane bit counts
+// from the code lengths), a host prefix sum for block offsets, and an encode
+// pass that writes each lane's words at its prefix-summed offset.
+#include "huff_ilv.h"
+
+#include <cstring>
+
+namespace ptwm {
+
+namespace {
+
+__device__ __forceinline__ uint32_t revert16x2(uint32_t v) {
+  return ((v << 8) & 0x80008000u) | ((v >> 1) & 0x7F807F80u) | (v & 0x007F007Fu);
+}
+__device__ __forceinline__ uint32_t revert32(uint32_t v) {
+  return ((v << 8) & 0x80000000u) | ((v >> 1) & 0x7F800000u) | (v & 0x007FFFFFu);
+}
+__device__ __forceinline__ uint32_t revert_e4m3x4(uint32_t r) {
+  return ((r & 0xF0F0F0F0u) >> 1) | ((r & 0x08080808u) << 4) | (r & 0x07070707u);
+}
+__device__ __forceinline__ uint32_t revert_e5m2x4(uint32_t r) {
+  return ((r & 0xF8F8F8F8u) >> 1) | ((r & 0x04040404u) << 5) | (r & 0x03030303u);
+}
+__device__ __forceinline__ void zip2(uint32_t a, uint32_t b, uint32_t& lo, uint32_t& hi) {
+  lo = __builtin_amdgcn_perm(b, a, 0x05010400u);
+  hi = __builtin_amdgcn_perm(b, a, 0x07030602u);
+}
+__device__ __forceinline__ uint32_t ld_u32le(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+// inclusive prefix sum across the 64 lanes of a wavefront
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+  for (uint32_t d = 1; d < 64; d <<= 1) {
+    uint32_t t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+// Per-plane decode tables in LDS.
+struct LutSet {
+  uint32_t lut[2048];   // s0 | s1 << 8 | s2 << 16 | n << 24 | bits << 26
+  uint16_t t16[2048];   // single-symbol table (len << 8 | sym), tree.rs:143-169
+  uint8_t len[256];     // code length per symbol
+  uint16_t rev[256];
+  uint32_t counts[16];
+  uint32_t next_code[16];
+  uint32_t wave_len_count[4][16];
+  uint32_t max_bits;
+  uint32_t status;
+};
+
+// Build the tables of one plane from the weights header at hdr (hdr_avail
+// bytes readable).  All 256 threads of the workgroup take part.  Returns the
+// header length in ls.status's upper bits; ls.status low bit set on error.
+__device__ void build_tables(LutSet& ls, const uint8_t* hdr, uint64_t hdr_avail, uint32_t* hdr_len_out) {
+  const uint32_t t = threadIdx.x;
+  __shared__ uint32_t s_nw, s_hb, s_err;
+  if (t == 0) {
+    uint32_t err = 0, n = 0, hb = 0;
+    if (hdr_avail < 1 || !(hdr[0] & 0x80)) err = 1;
+    else if (hdr[0] == 0x80) {
+      if (hdr_avail < 2) err = 1;
+      else {
+        n = hdr[1] ? hdr[1] : 256;
+        hb = 2;
+        if (n < 128) err = 1;
+      }
+    } else {
+      n = hdr[0] & 0x7F;
+      hb = 1;
+      if (n == 0) err = 1;
+    }
+    if (!err && hdr_avail < hb + (n + 1) / 2) err = 1;
+    s_nw = n;
+    s_hb = hb;
+    s_err = err;
+    *hdr_len_out = hb + (n + 1) / 2;
+    for (int i = 0; i < 16; ++i) ls.counts[i] = 0;
+  }
+  __syncthreads();
+  const uint32_t n = s_nw, hb = s_hb;
+  uint32_t w = 0;
+  if (!s_err && t < n) {
+    uint8_t b = hdr[hb + t / 2];
+    w = (t % 2 == 0) ? (b & 0x0F) : ((b >> 4) & 0x0F);
+  }
+  if (w > 11) atomicOr(&s_err, 1u);
+  if (w > 11) w = 0;
+  ls.len[t] = (uint8_t)w;
+  // rank among same-length symbols with a smaller index: ballots per length
+  const uint32_t wave = t >> 6, lane = t & 63u;
+  uint32_t rank_in_wave = 0;
+  for (uint32_t l = 1; l <= 11; ++l) {
+    uint64_t m = __ballot(w == l);
+    if (w == l) rank_in_wave = __popcll(m & ((1ull << lane) - 1ull));
+    if (lane == 0) ls.wave_len_count[wave][l] = __popcll(m);
+  }
+  __syncthreads();
+  if (t == 0) {
+    uint32_t maxb = 0, total = 0;
+    for (uint32_t l = 1; l <= 11; ++l) {
+      uint32_t c = 0;
+      for (int wv = 0; wv < 4; ++wv) c += ls.wave_len_count[wv][l];
+      ls.counts[l] = c;
+      total += c;
+      if (c) maxb = l;
+    }
+    if (total == 0) s_err = 1;
+    if (maxb < 1) maxb = 1;
+    uint32_t code = 0;
+    ls.counts[0] = 0;
+    for (uint32_t b = 1; b <= maxb; ++b) {
+      code = (code + ls.counts[b - 1]) << 1;
+      if (code > (1u << b)) s_err = 1;
+      ls.next_code[b] = code;
+    }
+    // Kraft <= 1 (equivalent to the per-symbol c < 2^len checks of tree.rs)
+    uint32_t kraft = 0;
+    for (uint32_t l = 1; l <= maxb; ++l) kraft += ls.counts[l] << (11 - l);
+    if (kraft > 2048) s_err = 1;
+    ls.max_bits = maxb;
+  }
+  __syncthreads();
+  const uint32_t max_bits = ls.max_bits;
+  if (w) {
+    uint32_t before = 0;
+    for (uint32_t wv = 0; wv < wave; ++wv) before += ls.wave_len_count[wv][w];
+    uint32_t c = ls.next_code[w] + before + rank_in_wave;
+    uint32_t r = 0;
+    for (uint32_t k = 0; k < w; ++k) r |= ((c >> k) & 1u) << (w - 1 - k);
+    ls.rev[t] = (uint16_t)r;
+  } else {
+    ls.rev[t] = 0;
+  }
+  const uint16_t fallback = (uint16_t)(max_bits << 8);
+  for (uint32_t i = t; i < 2048; i += 256) ls.t16[i] = fallback;
+  __syncthreads();
+  if (!s_err && w) {
+    uint16_t e = (uint16_t)((w << 8) | t);
+    uint32_t spread = 1u << (max_bits - w);
+    for (uint32_t i = 0; i < spread; ++i) ls.t16[ls.rev[t] | (i << w)] = e;
+  }
+  __syncthreads();
+  const uint32_t mask = (1u << max_bits) - 1u;
+  for (uint32_t i = t; i < 2048; i += 256) {
+    uint32_t e0 = ls.t16[i & mask];
+    uint32_t l0 = e0 >> 8, used = l0, n_sym = 1, syms = e0 & 0xFF;
+    uint32_t e1 = ls.t16[(i >> used) & mask];
+    if ((e1 >> 8) <= 11 - used) {
+      syms |= (e1 & 0xFF) << 8;
+      used += e1 >> 8;
+      n_sym = 2;
+      uint32_t e2 = ls.t16[(i >> used) & mask];
+      if ((e2 >> 8) <= 11 - used) {
+        syms |= (e2 & 0xFF) << 16;
+        used += e2 >> 8;
+        n_sym = 3;
+      }
+    }
+    ls.lut[i] = syms | (n_sym << 24) | (used << 26);
+  }
+  if (t == 0) ls.status = s_err;
+  __syncthreads();
+}
+
+// Decoder state of one coded plane within a block, per lane.
+struct LaneBits {
+  const uint32_t* ptr;
+  const uint32_t* end;
+  uint64_t buf;
+  uint32_t cnt;
+  uint32_t used;
+};
+
+// Decode `count` (<= 16) symbols into 4 words (bytes in order).
+__device__ __forceinline__ void decode_group(const LutSet& ls, LaneBits& lb, uint32_t count, uint32_t& w0,
+                                             uint32_t& w1, uint32_t& w2, uint32_t& w3) {
+  uint64_t acc = 0;
+  uint32_t fill = 0, produced = 0, emitted = 0;
+  w0 = w1 = w2 = w3 = 0;
+  while (produced < count) {
+    if (lb.cnt < 32) {
+      uint32_t x = lb.ptr < lb.end ? *lb.ptr : 0u;
+      lb.ptr++;
+      lb.buf |= (uint64_t)x << lb.cnt;
+      lb.cnt += 32;
+    }
+    uint32_t e = ls.lut[(uint32_t)lb.buf & 2047u];
+    uint32_t n = (e >> 24) & 3u, bits = e >> 26;
+    const uint32_t rem = count - produced;
+    if (n > rem) {
+      const uint32_t mask = (1u << ls.max_bits) - 1u;
+      n = rem;
+      bits = ls.t16[(uint32_t)lb.buf & mask] >> 8;
+      if (n == 2) bits += ls.t16[(uint32_t)(lb.buf >> bits) & mask] >> 8;
+    }
+    lb.buf >>= bits;
+    lb.cnt -= bits;
+    lb.used += bits;
+    const uint32_t keep = n == 3 ? 0xFFFFFFu : (n == 2 ? 0xFFFFu : 0xFFu);
+    acc |= (uint64_t)(e & keep) << (8 * fill);
+    fill += n;
+    produced += n;
+    if (fill >= 4) {
+      w0 = w1; w1 = w2; w2 = w3; w3 = (uint32_t)acc;
+      acc >>= 32;
+      fill -= 4;
+      emitted++;
+    }
+  }
+  if (fill) {
+    w0 = w1; w1 = w2; w2 = w3; w3 = (uint32_t)acc;
+    emitted++;
+  }
+  // partial group: move the emitted words to the front
+  while (emitted < 4) {
+    w0 = w1; w1 = w2; w2 = w3; w3 = 0;
+    emitted++;
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// decode (fused with the inverse chain)
+// ---------------------------------------------------------------------------
+
+template <uint32_t kChain>
+struct ChainInfo;
+template <> struct ChainInfo<kChainIeee16Split2> { static constexpr uint32_t np = 2, ratio = 2; };
+template <> struct ChainInfo<kChainIeee32Split4> { static constexpr uint32_t np = 4, ratio = 4; };
+template <> struct ChainInfo<kChainE4m3Nibble> { static constexpr uint32_t np = 2, ratio = 1; };
+template <> struct ChainInfo<kChainE5m2Nibble> { static constexpr uint32_t np = 2, ratio = 1; };
+template <> struct ChainInfo<kChainNibbleSplit> { static constexpr uint32_t np = 2, ratio = 1; };
+template <> struct ChainInfo<kChainPassthrough> { static constexpr uint32_t np = 1, ratio = 1; };
+
+// Merge one group (16 elements; v[p][k] = plane p bytes 4k..4k+3) into the
+// output words o[] (ratio * 4 words).
+template <uint32_t kChain>
+__device__ __forceinline__ void merge_group(const uint32_t (&v)[ChainInfo<kChain>::np][4],
+                                            uint32_t (&o)[4 * ChainInfo<kChain>::ratio]) {
+  if constexpr (kChain == kChainIeee16Split2) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t lo, hi;
+      zip2(v[0][k], v[1][k], lo, hi);
+      o[2 * k] = revert16x2(lo);
+      o[2 * k + 1] = revert16x2(hi);
+    }
+  } else if constexpr (kChain == kChainIeee32Split4) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t ab_lo, ab_hi, cd_lo, cd_hi;
+      zip2(v[0][k], v[1][k], ab_lo, ab_hi);
+      zip2(v[2][k], v[3][k], cd_lo, cd_hi);
+      o[4 * k + 0] = revert32(__builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u));
+      o[4 * k + 1] = revert32(__builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u));
+      o[4 * k + 2] = revert32(__builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u));
+      o[4 * k + 3] = revert32(__builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u));
+    }
+  } else if constexpr (kChain == kChainPassthrough) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = v[0][k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t r8 = ((v[0][k] & 0x0F0F0F0Fu) << 4) | (v[1][k] & 0x0F0F0F0Fu);
+      if constexpr (kChain == kChainE4m3Nibble) o[k] = revert_e4m3x4(r8);
+      else if constexpr (kChain == kChainE5m2Nibble) o[k] = revert_e5m2x4(r8);
+      else o[k] = r8;
+    }
+  }
+}
+
+template <uint32_t kChain>
+__global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __restrict__ tensors,
+                                                         const IlvTile* __restrict__ tiles,
+                                                         uint32_t* __restrict__ status) {
+  constexpr uint32_t NP = ChainInfo<kChain>::np;
+  constexpr uint32_t RATIO = ChainInfo<kChain>::ratio;
+  __shared__ LutSet lsets[NP];
+  __shared__ uint64_t s_table[NP], s_data[NP], s_datalen[NP], s_raw[NP];
+  __shared__ uint32_t s_bad, s_hlen, s_coded[NP];
+  const IlvTile tile = tiles[blockIdx.x];
+  const IlvTensor& T = tensors[tile.tensor];
+  const uint32_t t = threadIdx.x;
+  const uint64_t n = T.n;
+  const uint32_t nb = (uint32_t)((n + kIlvBlock - 1) / kIlvBlock);
+  if (t == 0) {
+    s_bad = 0;
+    for (uint32_t p = 0; p < NP; ++p) {
+      const IlvPlane& P = T.planes[p];
+      s_raw[p] = P.base;
+      s_coded[p] = 0;
+      if (!P.coded) continue;
+      // huff_ilv payload: tag 0 stores the plane after the tag byte
+      const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
+      if (P.len == 0) s_bad |= kIlvErrHeader;
+      else if (pay[0] == 0) {
+        if (P.len != n + 1) s_bad |= kIlvErrHeader;
+        s_raw[p] = P.base + 1;
+      } else if (pay[0] == 1 && P.len >= 5 && ld_u32le(pay + 1) == n) {
+        s_coded[p] = 1;
+      } else {
+        s_bad |= kIlvErrHeader;
+      }
+    }
+  }
+  __syncthreads();
+  // ---- prologue: per coded plane, parse the header and build LDS tables ----
+#pragma unroll
+  for (uint32_t p = 0; p < NP; ++p) {
+    const IlvPlane P = T.planes[p];
+    if (!s_coded[p]) continue;
+    const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
+    build_tables(lsets[p], pay + 5, P.len >= 5 ? P.len - 5 : 0, &s_hlen);
+    if (t == 0) {
+      if (lsets[p].status) s_bad |= kIlvErrHeader;
+      uint64_t head = 5 + s_hlen;
+      head += (4 - head % 4) % 4;
+      const uint64_t data0 = head + 4ull * (nb + 1);
+      if (data0 > P.len) {
+        s_bad |= kIlvErrHeader;
+      } else {
+        s_table[p] = P.base + head;
+        s_data[p] = P.base + data0;
+        s_datalen[p] = P.len - data0;
+        const uint32_t* tab = reinterpret_cast<const uint32_t*>(P.base + head);
+        if (tab[0] != 0 || tab[nb] != s_datalen[p]) s_bad |= kIlvErrBlock;
+      }
+    }
+    __syncthreads();
+  }
+  if (s_bad) {
+    if (t == 0) atomicOr(&status[tile.tensor], s_bad);
+    return;
+  }
+  // ---- main loop: one wavefront per block ----
+  const uint32_t wave = t >> 6, lane = t & 63u;
+  uint32_t bad = 0;
+  uint8_t* out = reinterpret_cast<uint8_t*>(T.out);
+  for (uint32_t bi = tile.block0 + wave; bi < tile.block0 + tile.nblocks; bi += 4) {
+    const uint64_t bstart = (uint64_t)bi * kIlvBlock;
+    LaneBits lb[NP];
+    uint32_t lane_c[NP];
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p) {
+      lane_c[p] = 0;
+      lb[p].ptr = lb[p].end = nullptr;
+      lb[p].buf = 0;
+      lb[p].cnt = 0;
+      lb[p].used = 0;
+      if (!s_coded[p]) continue;
+      const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
+      const uint32_t o0 = tab[bi], o1 = tab[bi + 1];
+      const bool bok = o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64;
+      const uint8_t* blk = reinterpret_cast<const uint8_t*>(s_data[p]) + (bok ? o0 : 0);
+      const uint32_t c = bok ? blk[lane] : 0u;
+      const uint32_t incl = wave_incl_scan(c);
+      const uint32_t total = __shfl(incl, 63, 64);
+      const bool sized = bok && 64u + 4u * total == o1 - o0;
+      if (!sized) bad |= kIlvErrBlock;
+      const uint32_t* words = reinterpret_cast<const uint32_t*>(blk + 64);
+      lb[p].ptr = words + (incl - c);
+      lb[p].end = sized ? words + incl : lb[p].ptr;
+      lane_c[p] = c;
+    }
+    for (uint32_t r = 0; r < kIlvRounds; ++r) {
+      const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
+      const uint32_t count = pos < n ? (uint32_t)(n - pos < kIlvGroup ? n - pos : kIlvGroup) : 0u;
+      uint32_t v[NP][4];
+#pragma unroll
+      for (uint32_t p = 0; p < NP; ++p) {
+        const uint64_t raw = s_raw[p] + pos;
+        if (s_coded[p]) {
+          decode_group(lsets[p], lb[p], count, v[p][0], v[p][1], v[p][2], v[p][3]);
+        } else if (count == kIlvGroup && (raw & 15u) == 0) {
+          u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(raw));
+          v[p][0] = x.x; v[p][1] = x.y; v[p][2] = x.z; v[p][3] = x.w;
+        } else {
+          uint32_t tmp[4] = {0, 0, 0, 0};
+          const uint8_t* src = reinterpret_cast<const uint8_t*>(raw);
+          for (uint32_t k = 0; k < count; ++k) tmp[k >> 2] |= (uint32_t)src[k] << (8 * (k & 3));
+          v[p][0] = tmp[0]; v[p][1] = tmp[1]; v[p][2] = tmp[2]; v[p][3] = tmp[3];
+        }
+      }
+      if (count == 0) continue;
+      uint32_t o[4 * RATIO];
+      merge_group<kChain>(v, o);
+      if (count == kIlvGroup) {
+        u32x4* dst = reinterpret_cast<u32x4*>(out + RATIO * pos);
+#pragma unroll
+        for (uint32_t k = 0; k < RATIO; ++k)
+          __builtin_nontemporal_store(u32x4_make(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]), dst + k);
+      } else {
+        for (uint32_t k = 0; k < RATIO * count; ++k) out[RATIO * pos + k] = (uint8_t)(o[k >> 2] >> (8 * (k & 3)));
+      }
+    }
+    // acceptance: every lane's words hold exactly its codes
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p)
+      if (s_coded[p] && (lb[p].used + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
+  }
+  if (bad) atomicOr(&status[tile.tensor], bad);
+}
+
+// ---------------------------------------------------------------------------
+// encode kernels
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256) ilv_hist_kernel(const IlvEncPlane* __restrict__ planes,
+                                                       uint32_t* __restrict__ hist) {
+  __shared__ uint32_t h[4][256];
+  const IlvEncPlane P = planes[blockIdx.y];
+  const uint32_t t = threadIdx.x, wave = t >> 6;
+  for (uint32_t i = t; i < 1024; i += 256) (&h[0][0])[i] = 0;
+  __syncthreads();
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(P.src);
+  const uint64_t nvec = P.n / 16;
+  const uint64_t stride = (uint64_t)gridDim.x * 256u;
+  for (uint64_t v = (uint64_t)blockIdx.x * 256u + t; v < nvec; v += stride) {
+    u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + v);
+    const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) atomicAdd(&h[wave][(xs[k] >> (8 * b)) & 0xFF], 1u);
+  }
+  if (blockIdx.x == 0)
+    for (uint64_t i = nvec * 16 + t; i < P.n; i += 256) atomicAdd(&h[wave][src[i]], 1u);
+  __syncthreads();
+  uint32_t s = h[0][t] + h[1][t] + h[2][t] + h[3][t];
+  if (s) atomicAdd(&hist[256u * blockIdx.y + t], s);
+}
+
+// One wavefront per block: lane word counts and block byte size.
+__global__ void __launch_bounds__(64) ilv_size_kernel(const IlvEncPlane* __restrict__ planes,
+                                                      const IlvEncBlock* __restrict__ blocks,
+                                                      const uint32_t* __restrict__ codes,
+                                                      uint8_t* __restrict__ lane_words,
+                                                      uint32_t* __restrict__ block_bytes) {
+  __shared__ uint8_t len[256];
+  const IlvEncBlock B = blocks[blockIdx.x];
+  const IlvEncPlane P = planes[B.plane];
+  const uint32_t lane = threadIdx.x;
+  for (uint32_t i = lane; i < 256; i += 64) len[i] = (uint8_t)(codes[256u * P.code_slot + i] >> 16);
+  __syncthreads();
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(P.src);
+  const uint64_t bstart = (uint64_t)B.block * kIlvBlock;
+  uint32_t bits = 0;
+  for (uint32_t r = 0; r < kIlvRounds; ++r) {
+    const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
+    if (pos >= P.n) continue;
+    if (P.n - pos >= kIlvGroup) {
+      u32x4 x = *reinterpret_cast<const u32x4*>(src + pos);
+      const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) bits += len[(xs[k] >> (8 * b)) & 0xFF];
+    } else {
+      for (uint64_t k = pos; k < P.n; ++k) bits += len[src[k]];
+    }
+  }
+  const uint32_t words = (bits + 31) / 32;
+  lane_words[64ull * blockIdx.x + lane] = (uint8_t)words;
+  uint32_t incl = wave_incl_scan(words);
+  if (lane == 63) block_bytes[blockIdx.x] = 64u + 4u * incl;
+}
+
+// One wavefront per block: write lane word counts and packed lane streams.
+__global__ void __launch_bounds__(64) ilv_encode_kernel(const IlvEncPlane* __restrict__ planes,
+                                                        const IlvEncBlock* __restrict__ blocks,
+                                                        const uint32_t* __restrict__ codes,
+                                                        const uint8_t* __restrict__ lane_words) {
+  __shared__ uint32_t code[256];
+  const IlvEncBlock B = blocks[blockIdx.x];
+  const IlvEncPlane P = planes[B.plane];
+  const uint32_t lane = threadIdx.x;
+  for (uint32_t i = lane; i < 256; i += 64) code[i] = codes[256u * P.code_slot + i];
+  __syncthreads();
+  uint8_t* blk = reinterpret_cast<uint8_t*>(B.dst);
+  const uint32_t c = lane_words[64ull * B.lw + lane];
+  blk[lane] = (uint8_t)c;
+  const uint32_t incl = wave_incl_scan(c);
+  uint32_t* w = reinterpret_cast<uint32_t*>(blk + 64) + (incl - c);
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(P.src);
+  const uint64_t bstart = (uint64_t)B.block * kIlvBlock;
+  uint64_t acc = 0;
+  uint32_t cnt = 0, wi = 0;
+  for (uint32_t r = 0; r < kIlvRounds; ++r) {
+    const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
+    if (pos >= P.n) continue;
+    const uint64_t end = P.n - pos >= kIlvGroup ? pos + kIlvGroup : P.n;
+    for (uint64_t k = pos; k < end; ++k) {
+      const uint32_t e = code[src[k]];
+      acc |= (uint64_t)(e & 0xFFFFu) << cnt;
+      cnt += e >> 16;
+      if (cnt >= 32) {
+        w[wi++] = (uint32_t)acc;
+        acc >>= 32;
+        cnt -= 32;
+      }
+    }
+  }
+  if (cnt) w[wi++] = (uint32_t)acc;
+}
+
+hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const IlvTile* tiles, uint32_t n_tiles,
+                             uint32_t* status, hipStream_t stream) {
+  if (!n_tiles) return hipSuccess;
+  const dim3 g(n_tiles), b(256);
+  switch (chain) {
+    case kChainIeee16Split2:
+      hipLaunchKernelGGL(ilv_decode_kernel<kChainIeee16Split2>, g, b, 0, stream, tensors, tiles, status);
+      break;
+    case kChainIeee32Split4:
+      hipLaunchKernelGGL(ilv_decode_kernel<kChainIeee32Split4>, g, b, 0, stream, tensors, tiles, status);
+      break;
+    case kChainE4m3Nibble:
+      hipLaunchKernelGGL(ilv_decode_kernel<kChainE4m3Nibble>, g, b, 0, stream, tensors, tiles, status);
+      break;
+    case kChainE5m2Nibble:
+      hipLaunchKernelGGL(ilv_decode_kernel<kChainE5m2Nibble>, g, b, 0, stream, tensors, tiles, status);
+      break;
+    case kChainNibbleSplit:
+      hipLaunchKernelGGL(ilv_decode_kernel<kChainNibbleSplit>, g, b, 0, stream, tensors, tiles, status);
+      break;
+    case kChainPassthrough:
+      hipLaunchKernelGGL(ilv_decode_kernel<kChainPassthrough>, g, b, 0, stream, tensors, tiles, status);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_t max_n, uint32_t* hist,
+                           hipStream_t stream) {
+  if (!n_planes) return hipSuccess;
+  uint64_t blocks = (max_n / 16 + 255) / 256;
+  if (blocks > 512) blocks = 512;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(ilv_hist_kernel, dim3((uint32_t)blocks, n_planes), dim3(256), 0, stream, planes, hist);
+  return hipGetLastError();
+}
+
+hipError_t launch_ilv_size(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,
+                           const uint32_t* codes, uint8_t* lane_words, uint32_t* block_bytes, hipStream_t stream) {
+  if (!n_blocks) return hipSuccess;
+  hipLaunchKernelGGL(ilv_size_kernel, dim3(n_blocks), dim3(64), 0, stream, planes, blocks, codes, lane_words,
+                     block_bytes);
+  return hipGetLastError();
+}
+
+hipError_t launch_ilv_encode(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,
+                             const uint32_t* codes, const uint8_t* lane_words, hipStream_t stream) {
+  if (!n_blocks) return hipSuccess;
+  hipLaunchKernelGGL(ilv_encode_kernel, dim3(n_blocks), dim3(64), 0, stream, planes, blocks, codes, lane_words);
+  return hipGetLastError();
+}
+
+}  // namespace ptwm

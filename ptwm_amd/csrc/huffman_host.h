@@ -1,0 +1,21 @@
+// huffman_host.h -- host-side canonical Huffman table construction.
+#pragma once
+
+#include <cstdint>
+
+namespace ptwm {
+
+constexpr int kHufMaxBits = 11;  // MAX_TABLE_LOG (entropy/huffman/tree.rs:5)
+
+// Code lengths from a histogram (tree.rs:19-85 + enforce_max_code_length
+// :212-242).  Returns false when every count is zero.
+bool huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]);
+
+// Canonical codes (tree.rs:102-177): fills bit-reversed codes, returns
+// max_bits or 0 if the lengths do not form a valid prefix code.
+int huf_canonical(const uint8_t lengths[256], uint16_t rev_codes[256]);
+
+// Weights header (weights.rs:8-32) into out (<= 130 bytes); returns its length.
+int huf_encode_weights(const uint8_t lengths[256], uint8_t* out);
+
+}  // namespace ptwm

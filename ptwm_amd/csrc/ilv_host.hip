@@ -1,0 +1,244 @@
+// ilv_host.hip -- host orchestration of the huff_ilv encoder and decoder.
+//
+// Encode (per call, any number of planes): histogram kernel -> host code
+// tables (huffman_host.cpp) -> size kernel -> host prefix sums and payload
+// layout -> encode kernel plus header / offset-table uploads.  A plane whose
+// coded payload is not smaller than the plane is stored instead.
+//
+// Decode: tensors are grouped by chain and decoded with one fused launch per
+// chain (ilv_decode_kernel<chain>), tiles of 16 blocks per workgroup.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "huff_ilv.h"
+#include "huffman_host.h"
+#include "ilv_host.h"
+#include "runtime.h"
+
+namespace ptwm {
+
+static inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, uint32_t np, uint64_t out_dev,
+                          uint64_t out_cap, bool identity_fallback, IlvEncResult* res, uint64_t* needed) {
+  hipStream_t s = ctx.stream;
+  if (np == 0) return 0;
+  for (uint32_t p = 0; p < np; ++p)
+    if ((src[p] & 15u) != 0 || n[p] > 0xFFFFFFFFull) return kInvalidInput;
+  // ---- histograms ----
+  std::vector<IlvEncPlane> hp(np);
+  uint64_t max_n = 0;
+  for (uint32_t p = 0; p < np; ++p) {
+    hp[p] = IlvEncPlane{src[p], n[p], p, 0};
+    max_n = std::max(max_n, n[p]);
+  }
+  PTWM_HIP_TRY(ctx.enc_planes.ensure(np * sizeof(IlvEncPlane)));
+  PTWM_HIP_TRY(ctx.enc_hist.ensure(np * 256 * sizeof(uint32_t)));
+  PTWM_HIP_TRY(ctx.h_enc.ensure(np * 256 * sizeof(uint32_t) + np * sizeof(IlvEncPlane)));
+  std::memcpy(ctx.h_enc.ptr, hp.data(), np * sizeof(IlvEncPlane));
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.enc_planes.ptr, ctx.h_enc.ptr, np * sizeof(IlvEncPlane), hipMemcpyHostToDevice, s));
+  PTWM_HIP_TRY(hipMemsetAsync(ctx.enc_hist.ptr, 0, np * 256 * sizeof(uint32_t), s));
+  PTWM_HIP_TRY(launch_ilv_hist(static_cast<const IlvEncPlane*>(ctx.enc_planes.ptr), np, max_n,
+                               static_cast<uint32_t*>(ctx.enc_hist.ptr), s));
+  std::vector<uint32_t> hist(np * 256);
+  PTWM_HIP_TRY(hipMemcpyAsync(hist.data(), ctx.enc_hist.ptr, np * 256 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  // ---- code tables ----
+  std::vector<uint32_t> codes(np * 256, 0);
+  std::vector<std::vector<uint8_t>> weights(np);
+  std::vector<bool> codable(np, false);
+  for (uint32_t p = 0; p < np; ++p) {
+    if (n[p] == 0) continue;
+    uint8_t lengths[256];
+    uint16_t rev[256];
+    if (!huf_lengths_from_freqs(&hist[256 * p], lengths)) continue;
+    if (!huf_canonical(lengths, rev)) continue;
+    for (int sy = 0; sy < 256; ++sy) codes[256 * p + sy] = ((uint32_t)lengths[sy] << 16) | rev[sy];
+    uint8_t w[140];
+    int wl = huf_encode_weights(lengths, w);
+    if (wl < 0) continue;
+    weights[p].assign(w, w + wl);
+    codable[p] = true;
+  }
+  // ---- size pass over every block of every codable plane ----
+  std::vector<IlvEncBlock> blocks;
+  std::vector<uint32_t> first_block(np, 0), nbs(np, 0);
+  for (uint32_t p = 0; p < np; ++p) {
+    first_block[p] = (uint32_t)blocks.size();
+    if (!codable[p]) continue;
+    nbs[p] = (uint32_t)((n[p] + kIlvBlock - 1) / kIlvBlock);
+    for (uint32_t b = 0; b < nbs[p]; ++b) blocks.push_back(IlvEncBlock{0, p, b, 0, 0});
+  }
+  const uint32_t nblk = (uint32_t)blocks.size();
+  std::vector<uint32_t> bbytes(nblk);
+  if (nblk) {
+    PTWM_HIP_TRY(ctx.enc_codes.ensure(codes.size() * sizeof(uint32_t)));
+    PTWM_HIP_TRY(ctx.enc_blocks.ensure(nblk * sizeof(IlvEncBlock)));
+    PTWM_HIP_TRY(ctx.enc_lane_words.ensure((size_t)nblk * 64));
+    PTWM_HIP_TRY(ctx.enc_block_bytes.ensure(nblk * sizeof(uint32_t)));
+    PTWM_HIP_TRY(ctx.h_enc.ensure(codes.size() * 4 + nblk * sizeof(IlvEncBlock) + nblk * 4 + 64));
+    uint8_t* hb = static_cast<uint8_t*>(ctx.h_enc.ptr);
+    std::memcpy(hb, codes.data(), codes.size() * 4);
+    std::memcpy(hb + codes.size() * 4, blocks.data(), nblk * sizeof(IlvEncBlock));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.enc_codes.ptr, hb, codes.size() * 4, hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.enc_blocks.ptr, hb + codes.size() * 4, nblk * sizeof(IlvEncBlock),
+                                hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(launch_ilv_size(static_cast<const IlvEncPlane*>(ctx.enc_planes.ptr),
+                                 static_cast<const IlvEncBlock*>(ctx.enc_blocks.ptr), nblk,
+                                 static_cast<const uint32_t*>(ctx.enc_codes.ptr),
+                                 static_cast<uint8_t*>(ctx.enc_lane_words.ptr),
+                                 static_cast<uint32_t*>(ctx.enc_block_bytes.ptr), s));
+    PTWM_HIP_TRY(hipMemcpyAsync(bbytes.data(), ctx.enc_block_bytes.ptr, nblk * 4, hipMemcpyDeviceToHost, s));
+    PTWM_HIP_TRY(hipStreamSynchronize(s));
+  }
+  // ---- layout: payloads at 256-byte aligned offsets ----
+  uint64_t off = 0;
+  std::vector<uint64_t> head(np, 0), data_bytes(np, 0);
+  for (uint32_t p = 0; p < np; ++p) {
+    off = align_up(off, 256);
+    res[p].offset = off;
+    bool coded = false;
+    if (codable[p]) {
+      uint64_t d = 0;
+      for (uint32_t b = 0; b < nbs[p]; ++b) d += bbytes[first_block[p] + b];
+      head[p] = align_up(5 + weights[p].size(), 4);
+      data_bytes[p] = d;
+      uint64_t pay = head[p] + 4ull * (nbs[p] + 1) + d;
+      // coded only when smaller than the stored form (Identity: n, tag 0: n + 1)
+      if (pay < (identity_fallback ? n[p] : n[p] + 1) && d <= 0xFFFFFFFFull) {
+        coded = true;
+        res[p].len = pay;
+      }
+    }
+    res[p].coded = coded ? 1 : 0;
+    if (!coded) res[p].len = identity_fallback ? n[p] : n[p] + 1;
+    res[p].codec = coded ? kCodecHuffIlv : (identity_fallback ? kCodecIdentity : kCodecHuffIlv);
+    off += res[p].len;
+  }
+  const uint64_t total = off;
+  if (total > out_cap) {
+    if (needed) *needed = total;
+    return kBufferTooSmall;
+  }
+  // ---- headers, offset tables and block destinations ----
+  uint64_t host_bytes = 0;
+  for (uint32_t p = 0; p < np; ++p)
+    if (res[p].coded) host_bytes += head[p] + 4ull * (nbs[p] + 1);
+  PTWM_HIP_TRY(ctx.h_enc.ensure(host_bytes + nblk * sizeof(IlvEncBlock) + np * 8 + 64));
+  uint8_t* hb = static_cast<uint8_t*>(ctx.h_enc.ptr);
+  IlvEncBlock* hblk = reinterpret_cast<IlvEncBlock*>(hb + host_bytes);
+  std::memcpy(hblk, blocks.data(), nblk * sizeof(IlvEncBlock));
+  uint64_t hoff = 0;
+  for (uint32_t p = 0; p < np; ++p) {
+    const uint64_t dst = out_dev + res[p].offset;
+    if (!res[p].coded) {
+      if (n[p] == 0 && identity_fallback) continue;
+      uint64_t raw_dst = dst;
+      if (!identity_fallback) {
+        uint8_t* tag = hb + host_bytes + nblk * sizeof(IlvEncBlock) + 8 * p;
+        *tag = 0;
+        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), tag, 1, hipMemcpyHostToDevice, s));
+        raw_dst = dst + 1;
+      }
+      if (n[p])
+        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(raw_dst), reinterpret_cast<const void*>(src[p]), n[p],
+                                    hipMemcpyDeviceToDevice, s));
+      continue;
+    }
+    uint8_t* h = hb + hoff;
+    std::memset(h, 0, head[p]);
+    h[0] = 1;
+    uint32_t nn = (uint32_t)n[p];
+    std::memcpy(h + 1, &nn, 4);
+    std::memcpy(h + 5, weights[p].data(), weights[p].size());
+    uint32_t* tab = reinterpret_cast<uint32_t*>(h + head[p]);
+    uint64_t acc = 0;
+    const uint64_t data_dev = dst + head[p] + 4ull * (nbs[p] + 1);
+    for (uint32_t b = 0; b < nbs[p]; ++b) {
+      tab[b] = (uint32_t)acc;
+      hblk[first_block[p] + b].dst = data_dev + acc;
+      acc += bbytes[first_block[p] + b];
+    }
+    tab[nbs[p]] = (uint32_t)acc;
+    const uint64_t hl = head[p] + 4ull * (nbs[p] + 1);
+    PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), h, hl, hipMemcpyHostToDevice, s));
+    hoff += hl;
+  }
+  if (nblk) {
+    // only blocks of coded planes are written; lw keeps the size-pass index
+    uint32_t live = 0;
+    for (uint32_t i = 0; i < nblk; ++i)
+      if (res[hblk[i].plane].coded) {
+        IlvEncBlock bk = hblk[i];
+        bk.lw = i;
+        hblk[live++] = bk;
+      }
+    if (live) {
+      PTWM_HIP_TRY(hipMemcpyAsync(ctx.enc_blocks.ptr, hblk, live * sizeof(IlvEncBlock), hipMemcpyHostToDevice, s));
+      PTWM_HIP_TRY(launch_ilv_encode(static_cast<const IlvEncPlane*>(ctx.enc_planes.ptr),
+                                     static_cast<const IlvEncBlock*>(ctx.enc_blocks.ptr), live,
+                                     static_cast<const uint32_t*>(ctx.enc_codes.ptr),
+                                     static_cast<const uint8_t*>(ctx.enc_lane_words.ptr), s));
+    }
+  }
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  return (int64_t)total;
+}
+
+int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors) {
+  hipStream_t s = ctx.stream;
+  if (tensors.empty()) return kOk;
+  const size_t nt = tensors.size();
+  // tiles grouped by chain: one launch per chain present
+  std::vector<IlvTile> tiles;
+  std::vector<std::pair<uint32_t, std::pair<uint32_t, uint32_t>>> launches;  // chain, [first, count)
+  for (uint32_t chain = 1; chain <= 6; ++chain) {
+    uint32_t first = (uint32_t)tiles.size();
+    for (uint32_t ti = 0; ti < nt; ++ti) {
+      const IlvTensor& T = tensors[ti];
+      if (T.chain != chain || T.n == 0) continue;
+      const uint32_t nb = (uint32_t)((T.n + kIlvBlock - 1) / kIlvBlock);
+      for (uint32_t b = 0; b < nb; b += kIlvBlocksPerTile)
+        tiles.push_back(IlvTile{ti, b, std::min<uint32_t>(kIlvBlocksPerTile, nb - b), 0});
+    }
+    if (tiles.size() > first) launches.push_back({chain, {first, (uint32_t)tiles.size() - first}});
+  }
+  PTWM_HIP_TRY(ctx.ilv_tensors.ensure(nt * sizeof(IlvTensor)));
+  PTWM_HIP_TRY(ctx.ilv_tiles.ensure(tiles.size() * sizeof(IlvTile) + 16));
+  PTWM_HIP_TRY(ctx.ilv_status.ensure(nt * sizeof(uint32_t)));
+  PTWM_HIP_TRY(ctx.h_ilv.ensure(nt * sizeof(IlvTensor) + tiles.size() * sizeof(IlvTile) + nt * 4 + 64));
+  uint8_t* h = static_cast<uint8_t*>(ctx.h_ilv.ptr);
+  std::memcpy(h, tensors.data(), nt * sizeof(IlvTensor));
+  std::memcpy(h + nt * sizeof(IlvTensor), tiles.data(), tiles.size() * sizeof(IlvTile));
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.ilv_tensors.ptr, h, nt * sizeof(IlvTensor), hipMemcpyHostToDevice, s));
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.ilv_tiles.ptr, h + nt * sizeof(IlvTensor), tiles.size() * sizeof(IlvTile),
+                              hipMemcpyHostToDevice, s));
+  PTWM_HIP_TRY(hipMemsetAsync(ctx.ilv_status.ptr, 0, nt * sizeof(uint32_t), s));
+  if (ctx.profile) {
+    PTWM_HIP_TRY(ctx.ensure_events());
+    PTWM_HIP_TRY(hipEventRecord(ctx.ev[3], s));
+  }
+  for (auto& L : launches) {
+    PTWM_HIP_TRY(launch_ilv_decode(L.first, static_cast<const IlvTensor*>(ctx.ilv_tensors.ptr),
+                                   static_cast<const IlvTile*>(ctx.ilv_tiles.ptr) + L.second.first,
+                                   L.second.second, static_cast<uint32_t*>(ctx.ilv_status.ptr), s));
+  }
+  if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], s));
+  uint32_t* hs = reinterpret_cast<uint32_t*>(h + nt * sizeof(IlvTensor) + tiles.size() * sizeof(IlvTile));
+  PTWM_HIP_TRY(hipMemcpyAsync(hs, ctx.ilv_status.ptr, nt * 4, hipMemcpyDeviceToHost, s));
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  if (ctx.profile) {
+    float ms = 0;
+    PTWM_HIP_TRY(hipEventElapsedTime(&ms, ctx.ev[3], ctx.ev[2]));
+    ctx.last_ms[0] += ms;
+    ctx.last_ms[2] += ms;
+  }
+  for (size_t i = 0; i < nt; ++i)
+    if (hs[i]) return kInvalidInput;
+  return kOk;
+}
+
+}  // namespace ptwm

@@ -38,6 +38,11 @@ struct DevCtx {
   PinnedBuffer h_jobs;
   PinnedBuffer h_status;
   PinnedBuffer h_small;
+  // huff_ilv encoder / decoder scratch
+  DeviceBuffer enc_planes, enc_hist, enc_codes, enc_blocks, enc_lane_words, enc_block_bytes;
+  DeviceBuffer ilv_tensors, ilv_tiles, ilv_status;
+  PinnedBuffer h_enc, h_ilv;
+  DeviceBuffer stage_in, stage_out, enc_split;
   // optional per-phase kernel timing with HIP events on `stream`
   bool profile = false;
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};

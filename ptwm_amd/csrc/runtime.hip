@@ -13,6 +13,7 @@
 #include <cstring>
 #include <memory>
 
+#include "ilv_host.h"
 #include "runtime.h"
 
 namespace ptwm {
@@ -158,7 +159,8 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
       P.crc32 = T.has_crc ? c.get<uint32_t>() : 0;
       if (!c.ok || (pflags & ~1u)) return kInvalidInput;
       P.chunked = (pflags & 1u) != 0;
-      if (P.codec != kCodecIdentity && P.codec != kCodecHuffman && P.codec != kCodecRans) return kUnsupported;
+      if (P.codec != kCodecIdentity && P.codec != kCodecHuffman && P.codec != kCodecRans && P.codec != kCodecHuffIlv)
+        return kUnsupported;
       if (P.payload_offset > in_len || in_len - P.payload_offset < P.payload_len) return kInvalidInput;
       if (P.chunked) {
         if (nch == 0 || nch > (1u << 26) || state_len - c.off < (size_t)nch * 8) return kInvalidInput;
@@ -190,14 +192,47 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
 static inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
 int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev) {
-  // Pass 1: lay out plane scratch and count jobs.  A plane needs decoding
-  // into scratch unless it is a single unchunked Identity payload whose
+  // Route 1 (fused): a tensor whose planes are all unchunked Identity or
+  // huff_ilv payloads, with at least one huff_ilv plane, is decoded and
+  // merged in one pass by the huff_ilv kernel.
+  // Route 2 (exact): every other tensor; reference-format planes become
+  // DecodeJobs into plane scratch (huff_ilv planes decode into scratch through
+  // the fused kernel's passthrough chain), then the merge kernel runs.
+  const size_t nt = plan.tensors.size();
+  std::vector<IlvTensor> ilv;
+  std::vector<char> fused(nt, 0);
+  for (size_t t = 0; t < nt; ++t) {
+    const PlanTensor& T = plan.tensors[t];
+    bool any_ilv = false, ok = ((out_dev + T.out_offset) & 15u) == 0;
+    for (const PlanPlane& P : T.planes) {
+      if (P.chunked) ok = false;
+      if (P.codec == kCodecHuffIlv) any_ilv = true;
+      else if (P.codec != kCodecIdentity || P.payload_len != P.plane_len) ok = false;
+    }
+    if (!ok || !any_ilv) continue;
+    fused[t] = 1;
+    IlvTensor X{};
+    X.out = out_dev + T.out_offset;
+    X.n = T.planes[0].plane_len;
+    X.chain = T.chain;
+    X.n_planes = (uint32_t)T.planes.size();
+    for (size_t p = 0; p < T.planes.size(); ++p) {
+      X.planes[p].base = in_dev + T.planes[p].payload_offset;
+      X.planes[p].len = T.planes[p].payload_len;
+      X.planes[p].coded = T.planes[p].codec == kCodecHuffIlv ? 1 : 0;
+      X.planes[p].lut = (uint32_t)p;
+    }
+    ilv.push_back(X);
+  }
+  // Pass 1 (exact route): lay out plane scratch and count jobs.  A plane
+  // needs scratch unless it is a single unchunked Identity payload whose
   // (16-byte aligned) bytes can feed the merge directly from the input.
   constexpr uint64_t kDirect = UINT64_MAX;
-  std::vector<std::vector<uint64_t>> scratch_off(plan.tensors.size());
+  std::vector<std::vector<uint64_t>> scratch_off(nt);
   uint64_t scratch_bytes = 0;
   size_t n_jobs = 0;
-  for (size_t t = 0; t < plan.tensors.size(); ++t) {
+  for (size_t t = 0; t < nt; ++t) {
+    if (fused[t]) continue;
     const PlanTensor& T = plan.tensors[t];
     scratch_off[t].assign(T.planes.size(), kDirect);
     for (size_t p = 0; p < T.planes.size(); ++p) {
@@ -205,9 +240,10 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
       uint64_t direct = in_dev + P.payload_offset;
       if (P.codec == kCodecIdentity && !P.chunked && P.payload_len == P.plane_len && (direct & 15u) == 0)
         continue;
+      if (P.codec == kCodecHuffIlv && P.chunked) return kUnsupported;
       scratch_off[t][p] = scratch_bytes;
       scratch_bytes = align_up(scratch_bytes + P.plane_len, 256);
-      n_jobs += P.chunked ? P.chunks.size() : 1;
+      if (P.codec != kCodecHuffIlv) n_jobs += P.chunked ? P.chunks.size() : 1;
     }
   }
   if (n_jobs > 0xFFFFFFFFull) return kInvalidInput;
@@ -218,9 +254,10 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   PTWM_HIP_TRY(ctx.h_status.ensure(n_jobs * sizeof(uint32_t) + 64));
   const uint64_t scratch_base = reinterpret_cast<uint64_t>(ctx.planes.ptr);
   DecodeJob* hj = static_cast<DecodeJob*>(ctx.h_jobs.ptr);
-  std::vector<std::vector<uint64_t>> plane_addr(plan.tensors.size());
+  std::vector<std::vector<uint64_t>> plane_addr(nt);
   size_t j = 0;
-  for (size_t t = 0; t < plan.tensors.size(); ++t) {
+  for (size_t t = 0; t < nt; ++t) {
+    if (fused[t]) continue;
     const PlanTensor& T = plan.tensors[t];
     plane_addr[t].resize(T.planes.size());
     for (size_t p = 0; p < T.planes.size(); ++p) {
@@ -231,6 +268,19 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
       }
       const uint64_t a = scratch_base + scratch_off[t][p];
       plane_addr[t][p] = a;
+      if (P.codec == kCodecHuffIlv) {
+        if (P.plane_len == 0) continue;
+        IlvTensor X{};
+        X.out = a;
+        X.n = P.plane_len;
+        X.chain = kChainPassthrough;
+        X.n_planes = 1;
+        X.planes[0].base = in_dev + P.payload_offset;
+        X.planes[0].len = P.payload_len;
+        X.planes[0].coded = 1;
+        ilv.push_back(X);
+        continue;
+      }
       if (!P.chunked) {
         DecodeJob& J = hj[j++];
         std::memset(&J, 0, sizeof(J));
@@ -260,7 +310,15 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   }
   if (j != n_jobs) return kInternal;
   hipStream_t s = ctx.stream;
-  if (ctx.profile) PTWM_HIP_TRY(ctx.ensure_events());
+  if (ctx.profile) {
+    PTWM_HIP_TRY(ctx.ensure_events());
+    ctx.last_ms[0] = ctx.last_ms[1] = ctx.last_ms[2] = 0;
+  }
+  // huff_ilv first: fused tensors straight to the output, passthrough planes to scratch
+  if (!ilv.empty()) {
+    int64_t rc = ilv_decode_tensors(ctx, ilv);
+    if (rc != kOk) return rc;
+  }
   if (n_jobs) PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, hj, n_jobs * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[0], s));
   if (n_jobs) {
@@ -268,7 +326,8 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
                                      static_cast<uint32_t*>(ctx.status.ptr), (uint32_t)n_jobs, s));
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[1], s));
-  for (size_t t = 0; t < plan.tensors.size(); ++t) {
+  for (size_t t = 0; t < nt; ++t) {
+    if (fused[t]) continue;
     const PlanTensor& T = plan.tensors[t];
     const uint8_t* pp[4] = {nullptr, nullptr, nullptr, nullptr};
     for (size_t p = 0; p < T.planes.size(); ++p) pp[p] = reinterpret_cast<const uint8_t*>(plane_addr[t][p]);
@@ -284,9 +343,12 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   }
   PTWM_HIP_TRY(hipStreamSynchronize(s));
   if (ctx.profile) {
-    PTWM_HIP_TRY(hipEventElapsedTime(&ctx.last_ms[0], ctx.ev[0], ctx.ev[1]));
-    PTWM_HIP_TRY(hipEventElapsedTime(&ctx.last_ms[1], ctx.ev[1], ctx.ev[2]));
-    PTWM_HIP_TRY(hipEventElapsedTime(&ctx.last_ms[2], ctx.ev[0], ctx.ev[2]));
+    float a = 0, b = 0;
+    PTWM_HIP_TRY(hipEventElapsedTime(&a, ctx.ev[0], ctx.ev[1]));
+    PTWM_HIP_TRY(hipEventElapsedTime(&b, ctx.ev[1], ctx.ev[2]));
+    ctx.last_ms[0] += a;
+    ctx.last_ms[1] += b;
+    ctx.last_ms[2] += a + b;
   }
   const uint32_t* st = static_cast<const uint32_t*>(ctx.h_status.ptr);
   for (size_t k = 0; k < n_jobs; ++k)
