@@ -11,6 +11,7 @@ constexpr uint32_t kIlvLanes = 64;
 constexpr uint32_t kIlvGroup = 16;      // symbols per lane per round
 constexpr uint32_t kIlvRounds = kIlvBlock / (kIlvLanes * kIlvGroup);  // 16
 constexpr uint32_t kIlvBlocksPerTile = 16;  // blocks per workgroup (4 per wave)
+constexpr uint32_t kIlvScratchBytes = 5120;  // LDS table-build scratch per workgroup
 
 // status bits (per tensor)
 constexpr uint32_t kIlvErrHeader = 1;   // tag / length / weights / table bounds
@@ -54,8 +55,9 @@ struct IlvEncBlock {
   uint32_t pad;
 };
 
+// n_slots: LDS table slots per workgroup (>= the coded planes of any tensor)
 hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const IlvTile* tiles, uint32_t n_tiles,
-                             uint32_t* status, hipStream_t stream);
+                             uint32_t* status, uint32_t n_slots, hipStream_t stream);
 hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_t max_n, uint32_t* hist,
                            hipStream_t stream);
 hipError_t launch_ilv_size(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,

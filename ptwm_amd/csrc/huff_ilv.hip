@@ -63,25 +63,29 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   return v;
 }
 
-// Per-plane decode tables in LDS.
+// Per-coded-plane decode tables, resident in LDS for the whole workgroup.
 struct LutSet {
-  uint32_t lut[2048];   // s0 | s1 << 8 | s2 << 16 | n << 24 | bits << 26
-  uint16_t t16[2048];   // single-symbol table (len << 8 | sym), tree.rs:143-169
+  uint32_t lut[2048];   // s0 | s1 << 8 | s2 << 16 | n << 24 | bits << 26 | fb0 << 30 | fb1 << 31
   uint8_t len[256];     // code length per symbol
+  uint32_t max_bits;
+  uint32_t status;
+  uint32_t pad[2];
+};
+// Build-time scratch, shared by every plane of the workgroup.
+struct BuildScratch {
+  uint16_t t16[2048];   // single-symbol table (len << 8 | sym), tree.rs:143-169
   uint16_t rev[256];
   uint32_t counts[16];
   uint32_t next_code[16];
   uint32_t wave_len_count[4][16];
-  uint32_t max_bits;
-  uint32_t status;
+  uint32_t nw, hb, err, hdr_len;
 };
 
 // Build the tables of one plane from the weights header at hdr (hdr_avail
-// bytes readable).  All 256 threads of the workgroup take part.  Returns the
-// header length in ls.status's upper bits; ls.status low bit set on error.
-__device__ void build_tables(LutSet& ls, const uint8_t* hdr, uint64_t hdr_avail, uint32_t* hdr_len_out) {
+// bytes readable).  All 256 threads of the workgroup take part.  Sets
+// ls.status (nonzero: invalid header) and bs.hdr_len.
+__device__ void build_tables(LutSet& ls, BuildScratch& bs, const uint8_t* hdr, uint64_t hdr_avail) {
   const uint32_t t = threadIdx.x;
-  __shared__ uint32_t s_nw, s_hb, s_err;
   if (t == 0) {
     uint32_t err = 0, n = 0, hb = 0;
     if (hdr_avail < 1 || !(hdr[0] & 0x80)) err = 1;
@@ -98,20 +102,19 @@ __device__ void build_tables(LutSet& ls, const uint8_t* hdr, uint64_t hdr_avail,
       if (n == 0) err = 1;
     }
     if (!err && hdr_avail < hb + (n + 1) / 2) err = 1;
-    s_nw = n;
-    s_hb = hb;
-    s_err = err;
-    *hdr_len_out = hb + (n + 1) / 2;
-    for (int i = 0; i < 16; ++i) ls.counts[i] = 0;
+    bs.nw = n;
+    bs.hb = hb;
+    bs.err = err;
+    bs.hdr_len = hb + (n + 1) / 2;
   }
   __syncthreads();
-  const uint32_t n = s_nw, hb = s_hb;
+  const uint32_t n = bs.nw, hb = bs.hb;
   uint32_t w = 0;
-  if (!s_err && t < n) {
+  if (!bs.err && t < n) {
     uint8_t b = hdr[hb + t / 2];
     w = (t % 2 == 0) ? (b & 0x0F) : ((b >> 4) & 0x0F);
   }
-  if (w > 11) atomicOr(&s_err, 1u);
+  if (w > 11) atomicOr(&bs.err, 1u);
   if (w > 11) w = 0;
   ls.len[t] = (uint8_t)w;
   // rank among same-length symbols with a smaller index: ballots per length
@@ -120,84 +123,100 @@ __device__ void build_tables(LutSet& ls, const uint8_t* hdr, uint64_t hdr_avail,
   for (uint32_t l = 1; l <= 11; ++l) {
     uint64_t m = __ballot(w == l);
     if (w == l) rank_in_wave = __popcll(m & ((1ull << lane) - 1ull));
-    if (lane == 0) ls.wave_len_count[wave][l] = __popcll(m);
+    if (lane == 0) bs.wave_len_count[wave][l] = __popcll(m);
   }
   __syncthreads();
   if (t == 0) {
     uint32_t maxb = 0, total = 0;
+    bs.counts[0] = 0;
     for (uint32_t l = 1; l <= 11; ++l) {
       uint32_t c = 0;
-      for (int wv = 0; wv < 4; ++wv) c += ls.wave_len_count[wv][l];
-      ls.counts[l] = c;
+      for (int wv = 0; wv < 4; ++wv) c += bs.wave_len_count[wv][l];
+      bs.counts[l] = c;
       total += c;
       if (c) maxb = l;
     }
-    if (total == 0) s_err = 1;
+    if (total == 0) bs.err = 1;
     if (maxb < 1) maxb = 1;
     uint32_t code = 0;
-    ls.counts[0] = 0;
     for (uint32_t b = 1; b <= maxb; ++b) {
-      code = (code + ls.counts[b - 1]) << 1;
-      if (code > (1u << b)) s_err = 1;
-      ls.next_code[b] = code;
+      code = (code + bs.counts[b - 1]) << 1;
+      if (code > (1u << b)) bs.err = 1;
+      bs.next_code[b] = code;
     }
     // Kraft <= 1 (equivalent to the per-symbol c < 2^len checks of tree.rs)
     uint32_t kraft = 0;
-    for (uint32_t l = 1; l <= maxb; ++l) kraft += ls.counts[l] << (11 - l);
-    if (kraft > 2048) s_err = 1;
+    for (uint32_t l = 1; l <= maxb; ++l) kraft += bs.counts[l] << (11 - l);
+    if (kraft > 2048) bs.err = 1;
     ls.max_bits = maxb;
   }
   __syncthreads();
   const uint32_t max_bits = ls.max_bits;
   if (w) {
     uint32_t before = 0;
-    for (uint32_t wv = 0; wv < wave; ++wv) before += ls.wave_len_count[wv][w];
-    uint32_t c = ls.next_code[w] + before + rank_in_wave;
+    for (uint32_t wv = 0; wv < wave; ++wv) before += bs.wave_len_count[wv][w];
+    uint32_t c = bs.next_code[w] + before + rank_in_wave;
     uint32_t r = 0;
     for (uint32_t k = 0; k < w; ++k) r |= ((c >> k) & 1u) << (w - 1 - k);
-    ls.rev[t] = (uint16_t)r;
+    bs.rev[t] = (uint16_t)r;
   } else {
-    ls.rev[t] = 0;
+    bs.rev[t] = 0;
   }
   const uint16_t fallback = (uint16_t)(max_bits << 8);
-  for (uint32_t i = t; i < 2048; i += 256) ls.t16[i] = fallback;
+  for (uint32_t i = t; i < 2048; i += 256) bs.t16[i] = fallback;
   __syncthreads();
-  if (!s_err && w) {
+  if (!bs.err && w) {
     uint16_t e = (uint16_t)((w << 8) | t);
     uint32_t spread = 1u << (max_bits - w);
-    for (uint32_t i = 0; i < spread; ++i) ls.t16[ls.rev[t] | (i << w)] = e;
+    for (uint32_t i = 0; i < spread; ++i) bs.t16[bs.rev[t] | (i << w)] = e;
   }
   __syncthreads();
+  // multi-symbol entries: greedy decode of up to 3 whole codes in 11 bits
   const uint32_t mask = (1u << max_bits) - 1u;
   for (uint32_t i = t; i < 2048; i += 256) {
-    uint32_t e0 = ls.t16[i & mask];
-    uint32_t l0 = e0 >> 8, used = l0, n_sym = 1, syms = e0 & 0xFF;
-    uint32_t e1 = ls.t16[(i >> used) & mask];
+    uint32_t e0 = bs.t16[i & mask];
+    uint32_t used = e0 >> 8, n_sym = 1, syms = e0 & 0xFF;
+    uint32_t fb = (e0 == fallback && ls.len[0] != max_bits) ? (1u << 30) : 0u;
+    uint32_t e1 = bs.t16[(i >> used) & mask];
     if ((e1 >> 8) <= 11 - used) {
       syms |= (e1 & 0xFF) << 8;
+      fb |= (e1 == fallback && ls.len[0] != max_bits) ? (1u << 31) : 0u;
       used += e1 >> 8;
       n_sym = 2;
-      uint32_t e2 = ls.t16[(i >> used) & mask];
+      uint32_t e2 = bs.t16[(i >> used) & mask];
       if ((e2 >> 8) <= 11 - used) {
         syms |= (e2 & 0xFF) << 16;
         used += e2 >> 8;
         n_sym = 3;
       }
     }
-    ls.lut[i] = syms | (n_sym << 24) | (used << 26);
+    ls.lut[i] = syms | (n_sym << 24) | (used << 26) | fb;
   }
-  if (t == 0) ls.status = s_err;
+  if (t == 0) ls.status = bs.err;
   __syncthreads();
 }
 
-// Decoder state of one coded plane within a block, per lane.
+// Decoder state of one coded plane within a block, per lane.  `nxt` holds
+// the next stream word, loaded one refill ahead so that the load's latency
+// overlaps the lookups in between.
 struct LaneBits {
   const uint32_t* ptr;
   const uint32_t* end;
   uint64_t buf;
   uint32_t cnt;
   uint32_t used;
+  uint32_t nxt;
 };
+
+__device__ __forceinline__ void lane_start(LaneBits& lb, const uint32_t* ptr, const uint32_t* end) {
+  lb.ptr = ptr;
+  lb.end = end;
+  lb.buf = 0;
+  lb.cnt = 0;
+  lb.used = 0;
+  lb.nxt = lb.ptr < lb.end ? *lb.ptr : 0u;
+  lb.ptr++;
+}
 
 // Decode `count` (<= 16) symbols into 4 words (bytes in order).
 __device__ __forceinline__ void decode_group(const LutSet& ls, LaneBits& lb, uint32_t count, uint32_t& w0,
@@ -207,19 +226,19 @@ __device__ __forceinline__ void decode_group(const LutSet& ls, LaneBits& lb, uin
   w0 = w1 = w2 = w3 = 0;
   while (produced < count) {
     if (lb.cnt < 32) {
-      uint32_t x = lb.ptr < lb.end ? *lb.ptr : 0u;
-      lb.ptr++;
-      lb.buf |= (uint64_t)x << lb.cnt;
+      lb.buf |= (uint64_t)lb.nxt << lb.cnt;
       lb.cnt += 32;
+      lb.nxt = lb.ptr < lb.end ? *lb.ptr : 0u;
+      lb.ptr++;
     }
-    uint32_t e = ls.lut[(uint32_t)lb.buf & 2047u];
-    uint32_t n = (e >> 24) & 3u, bits = e >> 26;
+    const uint32_t e = ls.lut[(uint32_t)lb.buf & 2047u];
+    uint32_t n = (e >> 24) & 3u, bits = (e >> 26) & 15u;
     const uint32_t rem = count - produced;
     if (n > rem) {
-      const uint32_t mask = (1u << ls.max_bits) - 1u;
+      // group end inside this entry: lengths of the first one or two codes
       n = rem;
-      bits = ls.t16[(uint32_t)lb.buf & mask] >> 8;
-      if (n == 2) bits += ls.t16[(uint32_t)(lb.buf >> bits) & mask] >> 8;
+      bits = (e & (1u << 30)) ? ls.max_bits : ls.len[e & 0xFF];
+      if (n == 2) bits += (e & (1u << 31)) ? ls.max_bits : ls.len[(e >> 8) & 0xFF];
     }
     lb.buf >>= bits;
     lb.cnt -= bits;
@@ -245,6 +264,8 @@ __device__ __forceinline__ void decode_group(const LutSet& ls, LaneBits& lb, uin
     emitted++;
   }
 }
+
+static_assert(sizeof(BuildScratch) <= kIlvScratchBytes, "scratch layout");
 
 }  // namespace
 
@@ -302,12 +323,15 @@ __device__ __forceinline__ void merge_group(const uint32_t (&v)[ChainInfo<kChain
 template <uint32_t kChain>
 __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __restrict__ tensors,
                                                          const IlvTile* __restrict__ tiles,
-                                                         uint32_t* __restrict__ status) {
+                                                         uint32_t* __restrict__ status, uint32_t n_slots) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
   constexpr uint32_t RATIO = ChainInfo<kChain>::ratio;
-  __shared__ LutSet lsets[NP];
+  // dynamic LDS: [BuildScratch][LutSet x n_slots], one slot per coded plane
+  extern __shared__ __align__(16) uint8_t smem[];
+  BuildScratch& bs = *reinterpret_cast<BuildScratch*>(smem);
+  LutSet* slots = reinterpret_cast<LutSet*>(smem + kIlvScratchBytes);
   __shared__ uint64_t s_table[NP], s_data[NP], s_datalen[NP], s_raw[NP];
-  __shared__ uint32_t s_bad, s_hlen, s_coded[NP];
+  __shared__ uint32_t s_bad, s_slot[NP];   // s_slot: 0 = not coded, k = slot k - 1
   const IlvTile tile = tiles[blockIdx.x];
   const IlvTensor& T = tensors[tile.tensor];
   const uint32_t t = threadIdx.x;
@@ -315,10 +339,11 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
   const uint32_t nb = (uint32_t)((n + kIlvBlock - 1) / kIlvBlock);
   if (t == 0) {
     s_bad = 0;
+    uint32_t next_slot = 0;
     for (uint32_t p = 0; p < NP; ++p) {
       const IlvPlane& P = T.planes[p];
       s_raw[p] = P.base;
-      s_coded[p] = 0;
+      s_slot[p] = 0;
       if (!P.coded) continue;
       // huff_ilv payload: tag 0 stores the plane after the tag byte
       const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
@@ -327,7 +352,8 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
         if (P.len != n + 1) s_bad |= kIlvErrHeader;
         s_raw[p] = P.base + 1;
       } else if (pay[0] == 1 && P.len >= 5 && ld_u32le(pay + 1) == n) {
-        s_coded[p] = 1;
+        if (next_slot < n_slots) s_slot[p] = ++next_slot;
+        else s_bad |= kIlvErrHeader;
       } else {
         s_bad |= kIlvErrHeader;
       }
@@ -338,12 +364,13 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
 #pragma unroll
   for (uint32_t p = 0; p < NP; ++p) {
     const IlvPlane P = T.planes[p];
-    if (!s_coded[p]) continue;
+    if (!s_slot[p]) continue;
+    LutSet& ls = slots[s_slot[p] - 1];
     const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
-    build_tables(lsets[p], pay + 5, P.len >= 5 ? P.len - 5 : 0, &s_hlen);
+    build_tables(ls, bs, pay + 5, P.len >= 5 ? P.len - 5 : 0);
     if (t == 0) {
-      if (lsets[p].status) s_bad |= kIlvErrHeader;
-      uint64_t head = 5 + s_hlen;
+      if (ls.status) s_bad |= kIlvErrHeader;
+      uint64_t head = 5 + bs.hdr_len;
       head += (4 - head % 4) % 4;
       const uint64_t data0 = head + 4ull * (nb + 1);
       if (data0 > P.len) {
@@ -377,7 +404,8 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       lb[p].buf = 0;
       lb[p].cnt = 0;
       lb[p].used = 0;
-      if (!s_coded[p]) continue;
+      lb[p].nxt = 0;
+      if (!s_slot[p]) continue;
       const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
       const uint32_t o0 = tab[bi], o1 = tab[bi + 1];
       const bool bok = o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64;
@@ -388,8 +416,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       const bool sized = bok && 64u + 4u * total == o1 - o0;
       if (!sized) bad |= kIlvErrBlock;
       const uint32_t* words = reinterpret_cast<const uint32_t*>(blk + 64);
-      lb[p].ptr = words + (incl - c);
-      lb[p].end = sized ? words + incl : lb[p].ptr;
+      lane_start(lb[p], words + (incl - c), sized ? words + incl : words + (incl - c));
       lane_c[p] = c;
     }
     for (uint32_t r = 0; r < kIlvRounds; ++r) {
@@ -399,8 +426,8 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
 #pragma unroll
       for (uint32_t p = 0; p < NP; ++p) {
         const uint64_t raw = s_raw[p] + pos;
-        if (s_coded[p]) {
-          decode_group(lsets[p], lb[p], count, v[p][0], v[p][1], v[p][2], v[p][3]);
+        if (s_slot[p]) {
+          decode_group(slots[s_slot[p] - 1], lb[p], count, v[p][0], v[p][1], v[p][2], v[p][3]);
         } else if (count == kIlvGroup && (raw & 15u) == 0) {
           u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(raw));
           v[p][0] = x.x; v[p][1] = x.y; v[p][2] = x.z; v[p][3] = x.w;
@@ -426,7 +453,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
     // acceptance: every lane's words hold exactly its codes
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p)
-      if (s_coded[p] && (lb[p].used + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
+      if (s_slot[p] && (lb[p].used + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
   }
   if (bad) atomicOr(&status[tile.tensor], bad);
 }
@@ -534,28 +561,22 @@ __global__ void __launch_bounds__(64) ilv_encode_kernel(const IlvEncPlane* __res
 }
 
 hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const IlvTile* tiles, uint32_t n_tiles,
-                             uint32_t* status, hipStream_t stream) {
+                             uint32_t* status, uint32_t n_slots, hipStream_t stream) {
   if (!n_tiles) return hipSuccess;
   const dim3 g(n_tiles), b(256);
+  const size_t lds = kIlvScratchBytes + (size_t)n_slots * sizeof(LutSet);
   switch (chain) {
-    case kChainIeee16Split2:
-      hipLaunchKernelGGL(ilv_decode_kernel<kChainIeee16Split2>, g, b, 0, stream, tensors, tiles, status);
-      break;
-    case kChainIeee32Split4:
-      hipLaunchKernelGGL(ilv_decode_kernel<kChainIeee32Split4>, g, b, 0, stream, tensors, tiles, status);
-      break;
-    case kChainE4m3Nibble:
-      hipLaunchKernelGGL(ilv_decode_kernel<kChainE4m3Nibble>, g, b, 0, stream, tensors, tiles, status);
-      break;
-    case kChainE5m2Nibble:
-      hipLaunchKernelGGL(ilv_decode_kernel<kChainE5m2Nibble>, g, b, 0, stream, tensors, tiles, status);
-      break;
-    case kChainNibbleSplit:
-      hipLaunchKernelGGL(ilv_decode_kernel<kChainNibbleSplit>, g, b, 0, stream, tensors, tiles, status);
-      break;
-    case kChainPassthrough:
-      hipLaunchKernelGGL(ilv_decode_kernel<kChainPassthrough>, g, b, 0, stream, tensors, tiles, status);
-      break;
+#define PTWM_ILV_CASE(C)                                                                              \
+  case C:                                                                                             \
+    hipLaunchKernelGGL(ilv_decode_kernel<C>, g, b, lds, stream, tensors, tiles, status, n_slots); \
+    break;
+    PTWM_ILV_CASE(kChainIeee16Split2)
+    PTWM_ILV_CASE(kChainIeee32Split4)
+    PTWM_ILV_CASE(kChainE4m3Nibble)
+    PTWM_ILV_CASE(kChainE5m2Nibble)
+    PTWM_ILV_CASE(kChainNibbleSplit)
+    PTWM_ILV_CASE(kChainPassthrough)
+#undef PTWM_ILV_CASE
     default:
       return hipErrorInvalidValue;
   }

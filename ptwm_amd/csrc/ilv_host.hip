@@ -194,17 +194,27 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors) {
   const size_t nt = tensors.size();
   // tiles grouped by chain: one launch per chain present
   std::vector<IlvTile> tiles;
-  std::vector<std::pair<uint32_t, std::pair<uint32_t, uint32_t>>> launches;  // chain, [first, count)
+  struct Launch {
+    uint32_t chain, first, count, slots;
+  };
+  std::vector<Launch> launches;
+  // 16 blocks per workgroup amortise the table build when there is work for
+  // >= 16 workgroups per CU; smaller jobs use 4 (one block per wavefront).
+  uint64_t total_blocks = 0;
+  for (const IlvTensor& T : tensors) total_blocks += (T.n + kIlvBlock - 1) / kIlvBlock;
+  const uint32_t per_tile = total_blocks >= 256ull * 16 * kIlvBlocksPerTile ? kIlvBlocksPerTile : 4;
   for (uint32_t chain = 1; chain <= 6; ++chain) {
-    uint32_t first = (uint32_t)tiles.size();
+    uint32_t first = (uint32_t)tiles.size(), slots = 0;
     for (uint32_t ti = 0; ti < nt; ++ti) {
       const IlvTensor& T = tensors[ti];
       if (T.chain != chain || T.n == 0) continue;
+      uint32_t coded = 0;
+      for (uint32_t p = 0; p < T.n_planes; ++p) coded += T.planes[p].coded ? 1 : 0;
+      slots = std::max(slots, coded);
       const uint32_t nb = (uint32_t)((T.n + kIlvBlock - 1) / kIlvBlock);
-      for (uint32_t b = 0; b < nb; b += kIlvBlocksPerTile)
-        tiles.push_back(IlvTile{ti, b, std::min<uint32_t>(kIlvBlocksPerTile, nb - b), 0});
+      for (uint32_t b = 0; b < nb; b += per_tile) tiles.push_back(IlvTile{ti, b, std::min<uint32_t>(per_tile, nb - b), 0});
     }
-    if (tiles.size() > first) launches.push_back({chain, {first, (uint32_t)tiles.size() - first}});
+    if (tiles.size() > first) launches.push_back(Launch{chain, first, (uint32_t)tiles.size() - first, slots});
   }
   PTWM_HIP_TRY(ctx.ilv_tensors.ensure(nt * sizeof(IlvTensor)));
   PTWM_HIP_TRY(ctx.ilv_tiles.ensure(tiles.size() * sizeof(IlvTile) + 16));
@@ -221,10 +231,10 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors) {
     PTWM_HIP_TRY(ctx.ensure_events());
     PTWM_HIP_TRY(hipEventRecord(ctx.ev[3], s));
   }
-  for (auto& L : launches) {
-    PTWM_HIP_TRY(launch_ilv_decode(L.first, static_cast<const IlvTensor*>(ctx.ilv_tensors.ptr),
-                                   static_cast<const IlvTile*>(ctx.ilv_tiles.ptr) + L.second.first,
-                                   L.second.second, static_cast<uint32_t*>(ctx.ilv_status.ptr), s));
+  for (const Launch& L : launches) {
+    PTWM_HIP_TRY(launch_ilv_decode(L.chain, static_cast<const IlvTensor*>(ctx.ilv_tensors.ptr),
+                                   static_cast<const IlvTile*>(ctx.ilv_tiles.ptr) + L.first, L.count,
+                                   static_cast<uint32_t*>(ctx.ilv_status.ptr), L.slots, s));
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], s));
   uint32_t* hs = reinterpret_cast<uint32_t*>(h + nt * sizeof(IlvTensor) + tiles.size() * sizeof(IlvTile));
