@@ -196,39 +196,58 @@ __device__ void build_tables(LutSet& ls, BuildScratch& bs, const uint8_t* hdr, u
   __syncthreads();
 }
 
+// Plain global-memory load (the address arrives through LDS, so the
+// compiler cannot infer the address space and would emit a flat load).
+__device__ __forceinline__ uint32_t gload_u32(const uint32_t* p) {
+  return *(const __attribute__((address_space(1))) uint32_t*)(uintptr_t)p;
+}
+
 // Decoder state of one coded plane within a block, per lane.  `nxt` holds
-// the next stream word, loaded one refill ahead so that the load's latency
-// overlaps the lookups in between.
+// the next stream word, loaded one refill ahead: the load is issued straight
+// into `nxt` (no select on the value, which would force a wait), from the
+// lane's stream or, past its end, from `safe` (the block's first word, always
+// readable).  Words past the end are never part of an accepted stream: a lane
+// whose symbols reach past its words consumes more than 32 * count bits and
+// fails the word-count check, exactly as the specification decoder (which
+// reads zeros there) does.
 struct LaneBits {
   const uint32_t* ptr;
   const uint32_t* end;
+  const uint32_t* safe;
+  const uint32_t* start;
   uint64_t buf;
   uint32_t cnt;
-  uint32_t used;
   uint32_t nxt;
 };
 
-__device__ __forceinline__ void lane_start(LaneBits& lb, const uint32_t* ptr, const uint32_t* end) {
+__device__ __forceinline__ void lane_start(LaneBits& lb, const uint32_t* ptr, const uint32_t* end,
+                                           const uint32_t* safe) {
   lb.ptr = ptr;
+  lb.start = ptr;
   lb.end = end;
+  lb.safe = safe;
   lb.buf = 0;
   lb.cnt = 0;
-  lb.used = 0;
-  lb.nxt = lb.ptr < lb.end ? *lb.ptr : 0u;
+  lb.nxt = gload_u32(lb.ptr < lb.end ? lb.ptr : lb.safe);
   lb.ptr++;
 }
 
-// Decode `count` (<= 16) symbols into 4 words (bytes in order).
-__device__ __forceinline__ void decode_group(const LutSet& ls, LaneBits& lb, uint32_t count, uint32_t& w0,
-                                             uint32_t& w1, uint32_t& w2, uint32_t& w3) {
-  uint64_t acc = 0;
-  uint32_t fill = 0, produced = 0, emitted = 0;
-  w0 = w1 = w2 = w3 = 0;
+// bits consumed so far: words pulled into the buffer minus what it still holds
+__device__ __forceinline__ uint32_t lane_used(const LaneBits& lb) {
+  return 32u * (uint32_t)(lb.ptr - lb.start - 1) - lb.cnt;
+}
+
+// Decode `count` (<= 16) symbols of one group.  Symbols go to the lane's
+// 20-byte LDS staging slot (three byte stores per lookup; bytes past the
+// group land in the slot's padding) and come back as 4 words.
+__device__ __forceinline__ void decode_group(const LutSet& ls, LaneBits& lb, uint32_t count, uint8_t* stage,
+                                             uint32_t& w0, uint32_t& w1, uint32_t& w2, uint32_t& w3) {
+  uint32_t produced = 0;
   while (produced < count) {
     if (lb.cnt < 32) {
       lb.buf |= (uint64_t)lb.nxt << lb.cnt;
       lb.cnt += 32;
-      lb.nxt = lb.ptr < lb.end ? *lb.ptr : 0u;
+      lb.nxt = gload_u32(lb.ptr < lb.end ? lb.ptr : lb.safe);
       lb.ptr++;
     }
     const uint32_t e = ls.lut[(uint32_t)lb.buf & 2047u];
@@ -242,27 +261,16 @@ __device__ __forceinline__ void decode_group(const LutSet& ls, LaneBits& lb, uin
     }
     lb.buf >>= bits;
     lb.cnt -= bits;
-    lb.used += bits;
-    const uint32_t keep = n == 3 ? 0xFFFFFFu : (n == 2 ? 0xFFFFu : 0xFFu);
-    acc |= (uint64_t)(e & keep) << (8 * fill);
-    fill += n;
+    stage[produced] = (uint8_t)e;
+    stage[produced + 1] = (uint8_t)(e >> 8);
+    stage[produced + 2] = (uint8_t)(e >> 16);
     produced += n;
-    if (fill >= 4) {
-      w0 = w1; w1 = w2; w2 = w3; w3 = (uint32_t)acc;
-      acc >>= 32;
-      fill -= 4;
-      emitted++;
-    }
   }
-  if (fill) {
-    w0 = w1; w1 = w2; w2 = w3; w3 = (uint32_t)acc;
-    emitted++;
-  }
-  // partial group: move the emitted words to the front
-  while (emitted < 4) {
-    w0 = w1; w1 = w2; w2 = w3; w3 = 0;
-    emitted++;
-  }
+  const uint32_t* sw = reinterpret_cast<const uint32_t*>(stage);
+  w0 = sw[0];
+  w1 = sw[1];
+  w2 = sw[2];
+  w3 = sw[3];
 }
 
 static_assert(sizeof(BuildScratch) <= kIlvScratchBytes, "scratch layout");
@@ -330,6 +338,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
   extern __shared__ __align__(16) uint8_t smem[];
   BuildScratch& bs = *reinterpret_cast<BuildScratch*>(smem);
   LutSet* slots = reinterpret_cast<LutSet*>(smem + kIlvScratchBytes);
+  uint8_t* stage_base = smem + kIlvScratchBytes + n_slots * sizeof(LutSet);  // 256 lanes x 20 bytes
   __shared__ uint64_t s_table[NP], s_data[NP], s_datalen[NP], s_raw[NP];
   __shared__ uint32_t s_bad, s_slot[NP];   // s_slot: 0 = not coded, k = slot k - 1
   const IlvTile tile = tiles[blockIdx.x];
@@ -400,10 +409,9 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
       lane_c[p] = 0;
-      lb[p].ptr = lb[p].end = nullptr;
+      lb[p].ptr = lb[p].end = lb[p].safe = lb[p].start = nullptr;
       lb[p].buf = 0;
       lb[p].cnt = 0;
-      lb[p].used = 0;
       lb[p].nxt = 0;
       if (!s_slot[p]) continue;
       const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
@@ -416,7 +424,8 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       const bool sized = bok && 64u + 4u * total == o1 - o0;
       if (!sized) bad |= kIlvErrBlock;
       const uint32_t* words = reinterpret_cast<const uint32_t*>(blk + 64);
-      lane_start(lb[p], words + (incl - c), sized ? words + incl : words + (incl - c));
+      lane_start(lb[p], words + (incl - c), sized ? words + incl : words + (incl - c),
+                 reinterpret_cast<const uint32_t*>(blk));
       lane_c[p] = c;
     }
     for (uint32_t r = 0; r < kIlvRounds; ++r) {
@@ -427,7 +436,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       for (uint32_t p = 0; p < NP; ++p) {
         const uint64_t raw = s_raw[p] + pos;
         if (s_slot[p]) {
-          decode_group(slots[s_slot[p] - 1], lb[p], count, v[p][0], v[p][1], v[p][2], v[p][3]);
+          decode_group(slots[s_slot[p] - 1], lb[p], count, stage_base + 20u * t, v[p][0], v[p][1], v[p][2], v[p][3]);
         } else if (count == kIlvGroup && (raw & 15u) == 0) {
           u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(raw));
           v[p][0] = x.x; v[p][1] = x.y; v[p][2] = x.z; v[p][3] = x.w;
@@ -453,7 +462,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
     // acceptance: every lane's words hold exactly its codes
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p)
-      if (s_slot[p] && (lb[p].used + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
+      if (s_slot[p] && (lane_used(lb[p]) + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
   }
   if (bad) atomicOr(&status[tile.tensor], bad);
 }
@@ -564,7 +573,7 @@ hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const Ilv
                              uint32_t* status, uint32_t n_slots, hipStream_t stream) {
   if (!n_tiles) return hipSuccess;
   const dim3 g(n_tiles), b(256);
-  const size_t lds = kIlvScratchBytes + (size_t)n_slots * sizeof(LutSet);
+  const size_t lds = kIlvScratchBytes + (size_t)n_slots * sizeof(LutSet) + 256 * 20;
   switch (chain) {
 #define PTWM_ILV_CASE(C)                                                                              \
   case C:                                                                                             \
