@@ -113,6 +113,10 @@ def build_workload(name: str) -> Workload:
         specs = [((4096, 4096), "fp32o")]
         desc = "config 2: fp32 4096x4096 N(0,0.02) + 1% x50 outliers, 4-plane split"
         kernel = "ilv_decode_kernel<2>"
+    elif name == "bf16_1g":
+        specs = [((32768, 16384), "w")]
+        desc = "one bf16 32768x16384 N(0,0.02) tensor (1 GiB, config 4 distribution) for counter runs"
+        kernel = "ilv_decode_kernel<1>"
     else:
         raise SystemExit(f"unknown workload {name}")
     wl = Workload(desc)
@@ -171,6 +175,8 @@ def main():
     ap.add_argument("--workload", default="llama8b")
     ap.add_argument("--extra", default="fp8", help="comma list of secondary workloads reported in config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 1 GiB device copy (known bytes) to scale FETCH_SIZE/WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus above 1 is not part of it",
@@ -214,6 +220,14 @@ def main():
         kms = sum(kern) / len(kern)
         return ms_step, kms
 
+    if args.copy_calibration:
+        a = torch.ones(1 << 30, dtype=torch.uint8, device="cuda:0")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+        log("[bench] calibration copy: 3 x 1 GiB device-to-device")
     log(f"[bench] workload {args.workload}")
     wl = build_workload(args.workload)
     ms_step, kms = measure(wl, args.steps, args.warmup)
