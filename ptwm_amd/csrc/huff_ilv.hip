@@ -273,6 +273,66 @@ __device__ __forceinline__ void decode_group(const LutSet& ls, LaneBits& lb, uin
   w3 = sw[3];
 }
 
+// Lane state when the block's words are staged in LDS: word indexes into the
+// wavefront's staging array instead of global pointers.
+struct LaneLds {
+  uint32_t off;
+  uint32_t end;
+  uint32_t start;
+  uint32_t cnt;
+  uint64_t buf;
+  uint32_t nxt;
+};
+
+__device__ __forceinline__ void lane_start_lds(LaneLds& lb, const uint32_t* sw, uint32_t off, uint32_t end) {
+  lb.off = off;
+  lb.start = off;
+  lb.end = end;
+  lb.buf = 0;
+  lb.cnt = 0;
+  lb.nxt = sw[off < end ? off : 0u];
+  lb.off++;
+}
+
+__device__ __forceinline__ uint32_t lane_used_lds(const LaneLds& lb) {
+  return 32u * (lb.off - lb.start - 1u) - lb.cnt;
+}
+
+// decode_group with the lane's words read from LDS (sw: the wavefront's
+// staged words; reads past the lane's end use word 0, see LaneBits).
+__device__ __forceinline__ void decode_group_lds(const LutSet& ls, const uint32_t* sw, LaneLds& lb, uint32_t count,
+                                                 uint8_t* stage, uint32_t& w0, uint32_t& w1, uint32_t& w2,
+                                                 uint32_t& w3) {
+  uint32_t produced = 0;
+  while (produced < count) {
+    if (lb.cnt < 32) {
+      lb.buf |= (uint64_t)lb.nxt << lb.cnt;
+      lb.cnt += 32;
+      lb.nxt = sw[lb.off < lb.end ? lb.off : 0u];
+      lb.off++;
+    }
+    const uint32_t e = ls.lut[(uint32_t)lb.buf & 2047u];
+    uint32_t n = (e >> 24) & 3u, bits = (e >> 26) & 15u;
+    const uint32_t rem = count - produced;
+    if (n > rem) {
+      n = rem;
+      bits = (e & (1u << 30)) ? ls.max_bits : ls.len[e & 0xFF];
+      if (n == 2) bits += (e & (1u << 31)) ? ls.max_bits : ls.len[(e >> 8) & 0xFF];
+    }
+    lb.buf >>= bits;
+    lb.cnt -= bits;
+    stage[produced] = (uint8_t)e;
+    stage[produced + 1] = (uint8_t)(e >> 8);
+    stage[produced + 2] = (uint8_t)(e >> 16);
+    produced += n;
+  }
+  const uint32_t* st = reinterpret_cast<const uint32_t*>(stage);
+  w0 = st[0];
+  w1 = st[1];
+  w2 = st[2];
+  w3 = st[3];
+}
+
 static_assert(sizeof(BuildScratch) <= kIlvScratchBytes, "scratch layout");
 
 }  // namespace
@@ -331,14 +391,18 @@ __device__ __forceinline__ void merge_group(const uint32_t (&v)[ChainInfo<kChain
 template <uint32_t kChain>
 __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __restrict__ tensors,
                                                          const IlvTile* __restrict__ tiles,
-                                                         uint32_t* __restrict__ status, uint32_t n_slots) {
+                                                         uint32_t* __restrict__ status, uint32_t n_slots,
+                                                         uint32_t stage_words) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
   constexpr uint32_t RATIO = ChainInfo<kChain>::ratio;
-  // dynamic LDS: [BuildScratch][LutSet x n_slots], one slot per coded plane
+  // dynamic LDS: [LutSet x n_slots][byte staging: 256 lanes x 20 B]
+  //              [word staging: 4 wavefronts x stage_words], the table-build
+  //              scratch aliasing the word staging (built before any staging)
   extern __shared__ __align__(16) uint8_t smem[];
-  BuildScratch& bs = *reinterpret_cast<BuildScratch*>(smem);
-  LutSet* slots = reinterpret_cast<LutSet*>(smem + kIlvScratchBytes);
-  uint8_t* stage_base = smem + kIlvScratchBytes + n_slots * sizeof(LutSet);  // 256 lanes x 20 bytes
+  LutSet* slots = reinterpret_cast<LutSet*>(smem);
+  uint8_t* stage_base = smem + n_slots * sizeof(LutSet);
+  uint32_t* word_stage = reinterpret_cast<uint32_t*>(stage_base + 256 * 20);
+  BuildScratch& bs = *reinterpret_cast<BuildScratch*>(word_stage);
   __shared__ uint64_t s_table[NP], s_data[NP], s_datalen[NP], s_raw[NP];
   __shared__ uint32_t s_bad, s_slot[NP];   // s_slot: 0 = not coded, k = slot k - 1
   const IlvTile tile = tiles[blockIdx.x];
@@ -402,17 +466,26 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
   const uint32_t wave = t >> 6, lane = t & 63u;
   uint32_t bad = 0;
   uint8_t* out = reinterpret_cast<uint8_t*>(T.out);
+  uint32_t* const sw = word_stage + wave * stage_words;
   for (uint32_t bi = tile.block0 + wave; bi < tile.block0 + tile.nblocks; bi += 4) {
     const uint64_t bstart = (uint64_t)bi * kIlvBlock;
     LaneBits lb[NP];
+    LaneLds ll[NP];
     uint32_t lane_c[NP];
+    bool staged[NP];
+    uint32_t budget = stage_words;
+    // the previous block's last reads of `sw` must finish before restaging
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
       lane_c[p] = 0;
+      staged[p] = false;
       lb[p].ptr = lb[p].end = lb[p].safe = lb[p].start = nullptr;
       lb[p].buf = 0;
       lb[p].cnt = 0;
       lb[p].nxt = 0;
+      ll[p].off = ll[p].end = ll[p].start = ll[p].cnt = ll[p].nxt = 0;
+      ll[p].buf = 0;
       if (!s_slot[p]) continue;
       const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
       const uint32_t o0 = tab[bi], o1 = tab[bi + 1];
@@ -424,10 +497,20 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       const bool sized = bok && 64u + 4u * total == o1 - o0;
       if (!sized) bad |= kIlvErrBlock;
       const uint32_t* words = reinterpret_cast<const uint32_t*>(blk + 64);
-      lane_start(lb[p], words + (incl - c), sized ? words + incl : words + (incl - c),
-                 reinterpret_cast<const uint32_t*>(blk));
       lane_c[p] = c;
+      if (sized && total <= budget) {
+        // coalesced copy of the block's words into this wavefront's LDS
+        const uint32_t base = stage_words - budget;
+        for (uint32_t i = lane; i < total; i += 64) sw[base + i] = gload_u32(words + i);
+        budget -= total;
+        staged[p] = true;
+        lane_start_lds(ll[p], sw, base + incl - c, base + incl);
+      } else {
+        lane_start(lb[p], words + (incl - c), sized ? words + incl : words + (incl - c),
+                   reinterpret_cast<const uint32_t*>(blk));
+      }
     }
+    __builtin_amdgcn_wave_barrier();
     for (uint32_t r = 0; r < kIlvRounds; ++r) {
       const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
       const uint32_t count = pos < n ? (uint32_t)(n - pos < kIlvGroup ? n - pos : kIlvGroup) : 0u;
@@ -435,7 +518,10 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
 #pragma unroll
       for (uint32_t p = 0; p < NP; ++p) {
         const uint64_t raw = s_raw[p] + pos;
-        if (s_slot[p]) {
+        if (staged[p]) {
+          decode_group_lds(slots[s_slot[p] - 1], sw, ll[p], count, stage_base + 20u * t, v[p][0], v[p][1], v[p][2],
+                           v[p][3]);
+        } else if (s_slot[p]) {
           decode_group(slots[s_slot[p] - 1], lb[p], count, stage_base + 20u * t, v[p][0], v[p][1], v[p][2], v[p][3]);
         } else if (count == kIlvGroup && (raw & 15u) == 0) {
           u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(raw));
@@ -461,8 +547,11 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
     }
     // acceptance: every lane's words hold exactly its codes
 #pragma unroll
-    for (uint32_t p = 0; p < NP; ++p)
-      if (s_slot[p] && (lane_used(lb[p]) + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
+    for (uint32_t p = 0; p < NP; ++p) {
+      if (!s_slot[p]) continue;
+      const uint32_t used = staged[p] ? lane_used_lds(ll[p]) : lane_used(lb[p]);
+      if ((used + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
+    }
   }
   if (bad) atomicOr(&status[tile.tensor], bad);
 }
@@ -573,11 +662,19 @@ hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const Ilv
                              uint32_t* status, uint32_t n_slots, hipStream_t stream) {
   if (!n_tiles) return hipSuccess;
   const dim3 g(n_tiles), b(256);
-  const size_t lds = kIlvScratchBytes + (size_t)n_slots * sizeof(LutSet) + 256 * 20;
+  // word staging per wavefront: up to 6.5 KB, within a 64 KB workgroup
+  // budget, and never smaller than the table-build scratch it aliases
+  const size_t fixed = (size_t)n_slots * sizeof(LutSet) + 256 * 20;
+  size_t per_wave = (65536 - fixed) / 4;
+  if (per_wave > 6656) per_wave = 6656;
+  per_wave &= ~(size_t)15;
+  if (per_wave * 4 < kIlvScratchBytes) return hipErrorInvalidValue;
+  const uint32_t stage_words = (uint32_t)(per_wave / 4);
+  const size_t lds = fixed + 4 * per_wave;
   switch (chain) {
 #define PTWM_ILV_CASE(C)                                                                              \
   case C:                                                                                             \
-    hipLaunchKernelGGL(ilv_decode_kernel<C>, g, b, lds, stream, tensors, tiles, status, n_slots); \
+    hipLaunchKernelGGL(ilv_decode_kernel<C>, g, b, lds, stream, tensors, tiles, status, n_slots, stage_words); \
     break;
     PTWM_ILV_CASE(kChainIeee16Split2)
     PTWM_ILV_CASE(kChainIeee32Split4)
