@@ -10,8 +10,9 @@ constexpr uint32_t kIlvBlock = 16384;   // symbols per block (one wavefront)
 constexpr uint32_t kIlvLanes = 64;
 constexpr uint32_t kIlvGroup = 16;      // symbols per lane per round
 constexpr uint32_t kIlvRounds = kIlvBlock / (kIlvLanes * kIlvGroup);  // 16
-constexpr uint32_t kIlvBlocksPerTile = 16;  // blocks per workgroup (4 per wave)
-constexpr uint32_t kIlvScratchBytes = 5120;  // LDS table-build scratch per workgroup
+constexpr uint32_t kIlvBlocksPerTile = 4;   // blocks per tile (one per wavefront)
+constexpr uint32_t kIlvStageSpare = 96;     // spare LDS words after the staging area
+constexpr uint32_t kIlvMaxLds = 65536;      // LDS budget of one decode workgroup
 
 // status bits (per tensor)
 constexpr uint32_t kIlvErrHeader = 1;   // tag / length / weights / table bounds
@@ -33,13 +34,6 @@ struct IlvTensor {
   IlvPlane planes[4];
 };
 
-struct IlvTile {
-  uint32_t tensor;
-  uint32_t block0;
-  uint32_t nblocks;
-  uint32_t pad;
-};
-
 struct IlvEncPlane {
   uint64_t src;        // plane bytes (16-byte aligned)
   uint64_t n;
@@ -55,9 +49,17 @@ struct IlvEncBlock {
   uint32_t pad;
 };
 
-// n_slots: LDS table slots per workgroup (>= the coded planes of any tensor)
-hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const IlvTile* tiles, uint32_t n_tiles,
-                             uint32_t* status, uint32_t n_slots, hipStream_t stream);
+// Fused decode of the tensors tix[0..m) (indexes into `tensors`, all of
+// chain `chain`); tensor tix[j] owns the 4-block tiles tpre[j] ..
+// tpre[j+1] - 1.  grid: persistent workgroups, each taking an equal range of
+// tiles.  n_slots: LDS table slots per workgroup (>= the coded planes of any
+// tensor); stage_words: LDS staging words per wavefront (multiple of 4);
+// blocks needing more are decoded from global memory.
+hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uint32_t* tix, const uint32_t* tpre,
+                             uint32_t m, uint32_t grid, uint32_t* status, uint32_t n_slots, uint32_t stage_words,
+                             hipStream_t stream);
+size_t ilv_decode_lds_bytes(uint32_t n_slots, uint32_t stage_words);
+hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, int* wg_per_cu);
 hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_t max_n, uint32_t* hist,
                            hipStream_t stream);
 hipError_t launch_ilv_size(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,

@@ -13,12 +13,18 @@
 //
 // Decode: one wavefront per block.  In round r every lane decodes one group,
 // so a round's 64 groups are 1024 consecutive symbols and the merged output
-// of a round is one contiguous span: all stores are coalesced dwordx4.  An
-// 11-bit multi-symbol lookup table in LDS (up to 3 symbols per lookup) is
-// built per workgroup from the payload's weights header.  Tensors whose
-// planes are all stored-aligned or huff_ilv-coded are decoded and merged in
-// one pass (decode -> inverse chain -> store), so planes never round-trip
-// through HBM.
+// of a round is one contiguous span: all stores are coalesced dwordx4.  The
+// block's lane streams are first copied into the wavefront's LDS region with
+// coalesced loads; every lane then decodes its 16 symbols per round on a
+// fixed schedule (no data-dependent branches): every second symbol a 32-bit
+// window is read from LDS at the lane's bit position (ds_read2 + alignbit)
+// and two 11-bit table lookups consume it.  The 2048-entry table (one entry
+// per 11-bit window) is built per workgroup in LDS from the payload's
+// weights header.  Tensors whose planes are all stored-aligned or
+// huff_ilv-coded are decoded and merged in one pass (decode -> inverse chain
+// -> store), so planes never round-trip through HBM.  Workgroups are
+// persistent: each takes a contiguous range of 4-block tiles and rebuilds
+// its tables only when the range crosses into the next tensor.
 //
 // Encode: LDS-privatised histograms merged with atomics, host code-table
 // build (256 symbols), a size pass (one wave per block: per-lane bit counts
@@ -63,17 +69,31 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   return v;
 }
 
-// Per-coded-plane decode tables, resident in LDS for the whole workgroup.
+// Plain global-memory loads (addresses that arrive through LDS would
+// otherwise become flat loads).  Payload words are 4-byte aligned (the host
+// realigns payloads that are not).
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ uint32_t gload_u32(const uint32_t* p) {
+  return *(const __attribute__((address_space(1))) uint32_t*)(uintptr_t)p;
+}
+__device__ __forceinline__ u32x4a4 gload_u32x4(const uint32_t* p) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4a4*)(uintptr_t)p);
+}
+
+// Per-coded-plane decode table, resident in LDS: one entry per 11-bit
+// window, entry = code length | symbol << 8.  Windows that match no code
+// decode as symbol 0 with length max_bits (the gap fill of tree.rs:143-169);
+// a table for max_bits < 11 is replicated over the unused high index bits.
 struct LutSet {
-  uint32_t lut[2048];   // s0 | s1 << 8 | s2 << 16 | n << 24 | bits << 26 | fb0 << 30 | fb1 << 31
-  uint8_t len[256];     // code length per symbol
+  uint16_t t[2048];
   uint32_t max_bits;
   uint32_t status;
   uint32_t pad[2];
 };
+static_assert(sizeof(LutSet) % 16 == 0, "LutSet keeps the staging area 16-byte aligned");
+
 // Build-time scratch, shared by every plane of the workgroup.
 struct BuildScratch {
-  uint16_t t16[2048];   // single-symbol table (len << 8 | sym), tree.rs:143-169
   uint16_t rev[256];
   uint32_t counts[16];
   uint32_t next_code[16];
@@ -81,7 +101,7 @@ struct BuildScratch {
   uint32_t nw, hb, err, hdr_len;
 };
 
-// Build the tables of one plane from the weights header at hdr (hdr_avail
+// Build the table of one plane from the weights header at hdr (hdr_avail
 // bytes readable).  All 256 threads of the workgroup take part.  Sets
 // ls.status (nonzero: invalid header) and bs.hdr_len.
 __device__ void build_tables(LutSet& ls, BuildScratch& bs, const uint8_t* hdr, uint64_t hdr_avail) {
@@ -116,7 +136,6 @@ __device__ void build_tables(LutSet& ls, BuildScratch& bs, const uint8_t* hdr, u
   }
   if (w > 11) atomicOr(&bs.err, 1u);
   if (w > 11) w = 0;
-  ls.len[t] = (uint8_t)w;
   // rank among same-length symbols with a smaller index: ballots per length
   const uint32_t wave = t >> 6, lane = t & 63u;
   uint32_t rank_in_wave = 0;
@@ -162,178 +181,81 @@ __device__ void build_tables(LutSet& ls, BuildScratch& bs, const uint8_t* hdr, u
   } else {
     bs.rev[t] = 0;
   }
-  const uint16_t fallback = (uint16_t)(max_bits << 8);
-  for (uint32_t i = t; i < 2048; i += 256) bs.t16[i] = fallback;
+  for (uint32_t i = t; i < 2048; i += 256) ls.t[i] = (uint16_t)max_bits;
   __syncthreads();
   if (!bs.err && w) {
-    uint16_t e = (uint16_t)((w << 8) | t);
-    uint32_t spread = 1u << (max_bits - w);
-    for (uint32_t i = 0; i < spread; ++i) bs.t16[bs.rev[t] | (i << w)] = e;
-  }
-  __syncthreads();
-  // multi-symbol entries: greedy decode of up to 3 whole codes in 11 bits
-  const uint32_t mask = (1u << max_bits) - 1u;
-  for (uint32_t i = t; i < 2048; i += 256) {
-    uint32_t e0 = bs.t16[i & mask];
-    uint32_t used = e0 >> 8, n_sym = 1, syms = e0 & 0xFF;
-    uint32_t fb = (e0 == fallback && ls.len[0] != max_bits) ? (1u << 30) : 0u;
-    uint32_t e1 = bs.t16[(i >> used) & mask];
-    if ((e1 >> 8) <= 11 - used) {
-      syms |= (e1 & 0xFF) << 8;
-      fb |= (e1 == fallback && ls.len[0] != max_bits) ? (1u << 31) : 0u;
-      used += e1 >> 8;
-      n_sym = 2;
-      uint32_t e2 = bs.t16[(i >> used) & mask];
-      if ((e2 >> 8) <= 11 - used) {
-        syms |= (e2 & 0xFF) << 16;
-        used += e2 >> 8;
-        n_sym = 3;
-      }
-    }
-    ls.lut[i] = syms | (n_sym << 24) | (used << 26) | fb;
+    const uint16_t e = (uint16_t)(w | (t << 8));
+    const uint32_t spread = 1u << (11 - w);
+    for (uint32_t i = 0; i < spread; ++i) ls.t[bs.rev[t] | (i << w)] = e;
   }
   if (t == 0) ls.status = bs.err;
   __syncthreads();
 }
 
-// Plain global-memory load (the address arrives through LDS, so the
-// compiler cannot infer the address space and would emit a flat load).
-__device__ __forceinline__ uint32_t gload_u32(const uint32_t* p) {
-  return *(const __attribute__((address_space(1))) uint32_t*)(uintptr_t)p;
-}
-
-// Decoder state of one coded plane within a block, per lane.  `nxt` holds
-// the next stream word, loaded one refill ahead: the load is issued straight
-// into `nxt` (no select on the value, which would force a wait), from the
-// lane's stream or, past its end, from `safe` (the block's first word, always
-// readable).  Words past the end are never part of an accepted stream: a lane
-// whose symbols reach past its words consumes more than 32 * count bits and
-// fails the word-count check, exactly as the specification decoder (which
-// reads zeros there) does.
-struct LaneBits {
-  const uint32_t* ptr;
-  const uint32_t* end;
-  const uint32_t* safe;
-  const uint32_t* start;
-  uint64_t buf;
-  uint32_t cnt;
-  uint32_t nxt;
-};
-
-__device__ __forceinline__ void lane_start(LaneBits& lb, const uint32_t* ptr, const uint32_t* end,
-                                           const uint32_t* safe) {
-  lb.ptr = ptr;
-  lb.start = ptr;
-  lb.end = end;
-  lb.safe = safe;
-  lb.buf = 0;
-  lb.cnt = 0;
-  lb.nxt = gload_u32(lb.ptr < lb.end ? lb.ptr : lb.safe);
-  lb.ptr++;
-}
-
-// bits consumed so far: words pulled into the buffer minus what it still holds
-__device__ __forceinline__ uint32_t lane_used(const LaneBits& lb) {
-  return 32u * (uint32_t)(lb.ptr - lb.start - 1) - lb.cnt;
-}
-
-// Decode `count` (<= 16) symbols of one group.  Symbols go to the lane's
-// 20-byte LDS staging slot (three byte stores per lookup; bytes past the
-// group land in the slot's padding) and come back as 4 words.
-__device__ __forceinline__ void decode_group(const LutSet& ls, LaneBits& lb, uint32_t count, uint8_t* stage,
-                                             uint32_t& w0, uint32_t& w1, uint32_t& w2, uint32_t& w3) {
-  uint32_t produced = 0;
-  while (produced < count) {
-    if (lb.cnt < 32) {
-      lb.buf |= (uint64_t)lb.nxt << lb.cnt;
-      lb.cnt += 32;
-      lb.nxt = gload_u32(lb.ptr < lb.end ? lb.ptr : lb.safe);
-      lb.ptr++;
-    }
-    const uint32_t e = ls.lut[(uint32_t)lb.buf & 2047u];
-    uint32_t n = (e >> 24) & 3u, bits = (e >> 26) & 15u;
-    const uint32_t rem = count - produced;
-    if (n > rem) {
-      // group end inside this entry: lengths of the first one or two codes
-      n = rem;
-      bits = (e & (1u << 30)) ? ls.max_bits : ls.len[e & 0xFF];
-      if (n == 2) bits += (e & (1u << 31)) ? ls.max_bits : ls.len[(e >> 8) & 0xFF];
-    }
-    lb.buf >>= bits;
-    lb.cnt -= bits;
-    stage[produced] = (uint8_t)e;
-    stage[produced + 1] = (uint8_t)(e >> 8);
-    stage[produced + 2] = (uint8_t)(e >> 16);
-    produced += n;
+// Pack the symbol bytes (byte 1 of each entry) of 16 entries into 4 words.
+__device__ __forceinline__ void pack_symbols(const uint32_t (&e)[16], uint32_t (&v)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t a = __builtin_amdgcn_perm(e[4 * j + 1], e[4 * j], 0x0c0c0501u);
+    const uint32_t b = __builtin_amdgcn_perm(e[4 * j + 3], e[4 * j + 2], 0x05010c0cu);
+    v[j] = a | b;
   }
-  const uint32_t* sw = reinterpret_cast<const uint32_t*>(stage);
-  w0 = sw[0];
-  w1 = sw[1];
-  w2 = sw[2];
-  w3 = sw[3];
 }
 
-// Lane state when the block's words are staged in LDS: word indexes into the
-// wavefront's staging array instead of global pointers.
-struct LaneLds {
-  uint32_t off;
-  uint32_t end;
-  uint32_t start;
-  uint32_t cnt;
-  uint64_t buf;
-  uint32_t nxt;
-};
-
-__device__ __forceinline__ void lane_start_lds(LaneLds& lb, const uint32_t* sw, uint32_t off, uint32_t end) {
-  lb.off = off;
-  lb.start = off;
-  lb.end = end;
-  lb.buf = 0;
-  lb.cnt = 0;
-  lb.nxt = sw[off < end ? off : 0u];
-  lb.off++;
-}
-
-__device__ __forceinline__ uint32_t lane_used_lds(const LaneLds& lb) {
-  return 32u * (lb.off - lb.start - 1u) - lb.cnt;
-}
-
-// decode_group with the lane's words read from LDS (sw: the wavefront's
-// staged words; reads past the lane's end use word 0, see LaneBits).
-__device__ __forceinline__ void decode_group_lds(const LutSet& ls, const uint32_t* sw, LaneLds& lb, uint32_t count,
-                                                 uint8_t* stage, uint32_t& w0, uint32_t& w1, uint32_t& w2,
-                                                 uint32_t& w3) {
-  uint32_t produced = 0;
-  while (produced < count) {
-    if (lb.cnt < 32) {
-      lb.buf |= (uint64_t)lb.nxt << lb.cnt;
-      lb.cnt += 32;
-      lb.nxt = sw[lb.off < lb.end ? lb.off : 0u];
-      lb.off++;
-    }
-    const uint32_t e = ls.lut[(uint32_t)lb.buf & 2047u];
-    uint32_t n = (e >> 24) & 3u, bits = (e >> 26) & 15u;
-    const uint32_t rem = count - produced;
-    if (n > rem) {
-      n = rem;
-      bits = (e & (1u << 30)) ? ls.max_bits : ls.len[e & 0xFF];
-      if (n == 2) bits += (e & (1u << 31)) ? ls.max_bits : ls.len[(e >> 8) & 0xFF];
-    }
-    lb.buf >>= bits;
-    lb.cnt -= bits;
-    stage[produced] = (uint8_t)e;
-    stage[produced + 1] = (uint8_t)(e >> 8);
-    stage[produced + 2] = (uint8_t)(e >> 16);
-    produced += n;
+// Decode one group (16 symbols; with kTail only the first `count` advance
+// the stream) from the wavefront's staged words `sw`.  qm = the lane's bit
+// position in sw minus one: bit 0 of each window is the bit before the next
+// code, so `window & 0xFFE` is directly the byte offset of its table entry.
+// Reads stay inside the workgroup's staging area: a lane reads at most 90
+// words past its first word, and the area ends with 96 spare words.
+template <bool kTail>
+__device__ __forceinline__ void group_lds(const uint16_t* __restrict__ lut, const uint32_t* __restrict__ sw,
+                                          uint32_t& qm, uint32_t count, uint32_t (&v)[4]) {
+  const uint8_t* lb = reinterpret_cast<const uint8_t*>(lut);
+  uint32_t e[16];
+#pragma unroll
+  for (uint32_t k = 0; k < 16; k += 2) {
+    const uint32_t wi = qm >> 5;
+    const uint32_t win = __builtin_amdgcn_alignbit(sw[wi + 1], sw[wi], qm);
+    const uint32_t e0 = *reinterpret_cast<const uint16_t*>(lb + (win & 0xFFEu));
+    uint32_t l0 = e0 & 0xFFu;
+    if (kTail && k >= count) l0 = 0;
+    const uint32_t win1 = __builtin_amdgcn_alignbit(0u, win, l0);
+    const uint32_t e1 = *reinterpret_cast<const uint16_t*>(lb + (win1 & 0xFFEu));
+    uint32_t l1 = e1 & 0xFFu;
+    if (kTail && k + 1 >= count) l1 = 0;
+    qm += l0 + l1;
+    e[k] = e0;
+    e[k + 1] = e1;
   }
-  const uint32_t* st = reinterpret_cast<const uint32_t*>(stage);
-  w0 = st[0];
-  w1 = st[1];
-  w2 = st[2];
-  w3 = st[3];
+  pack_symbols(e, v);
 }
 
-static_assert(sizeof(BuildScratch) <= kIlvScratchBytes, "scratch layout");
+// Fallback for a block that does not fit the staging budget: the same
+// decode reading the lane's words (nw of them) from global memory; words
+// past the lane's count read as zero, as in the specification decoder.
+// q = bits consumed by the lane so far.
+__device__ __forceinline__ void group_global(const uint16_t* __restrict__ lut, const uint32_t* words, uint32_t nw,
+                                             uint32_t& q, uint32_t count, uint32_t (&v)[4]) {
+  uint32_t e[16];
+#pragma unroll
+  for (uint32_t k = 0; k < 16; k += 2) {
+    const uint32_t wi = q >> 5;
+    const uint32_t lo = wi < nw ? gload_u32(words + wi) : 0u;
+    const uint32_t hi = wi + 1 < nw ? gload_u32(words + wi + 1) : 0u;
+    const uint32_t win = __builtin_amdgcn_alignbit(hi, lo, q);
+    const uint32_t e0 = lut[win & 2047u];
+    const uint32_t l0 = k < count ? (e0 & 0xFFu) : 0u;
+    const uint32_t e1 = lut[__builtin_amdgcn_alignbit(0u, win, l0) & 2047u];
+    const uint32_t l1 = k + 1 < count ? (e1 & 0xFFu) : 0u;
+    q += l0 + l1;
+    e[k] = e0;
+    e[k + 1] = e1;
+  }
+  pack_symbols(e, v);
+}
+
+static_assert(sizeof(BuildScratch) <= 1024, "scratch layout");
 
 }  // namespace
 
@@ -388,172 +310,251 @@ __device__ __forceinline__ void merge_group(const uint32_t (&v)[ChainInfo<kChain
   }
 }
 
+// Per-block state of one wavefront: for each plane, a raw-byte base or a
+// coded stream (staged: bit position in the LDS region; global: lane word
+// pointer, word count and bits consumed).
+template <uint32_t NP>
+struct BlockState {
+  uint64_t raw[NP];
+  const uint16_t* lut[NP];
+  const uint32_t* words[NP];
+  uint32_t nw[NP];
+  uint32_t q[NP];
+  uint32_t coded_mask;
+};
+
+// The 16 rounds of one block: decode one group per coded plane, load the
+// raw planes' groups, merge and store.
+template <uint32_t kChain, bool kTail, bool kStaged>
+__device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& st, const uint32_t* sw, uint8_t* out,
+                                             uint64_t n, uint64_t bstart, uint32_t lane) {
+  constexpr uint32_t NP = ChainInfo<kChain>::np;
+  constexpr uint32_t RATIO = ChainInfo<kChain>::ratio;
+  for (uint32_t r = 0; r < kIlvRounds; ++r) {
+    const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
+    uint32_t count = kIlvGroup;
+    if (kTail) count = pos < n ? (uint32_t)(n - pos < kIlvGroup ? n - pos : kIlvGroup) : 0u;
+    uint32_t v[NP][4];
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p) {
+      const uint64_t raw = st.raw[p] + pos;
+      if (st.coded_mask & (1u << p)) {
+        if constexpr (kStaged) group_lds<kTail>(st.lut[p], sw, st.q[p], count, v[p]);
+        else group_global(st.lut[p], st.words[p], st.nw[p], st.q[p], count, v[p]);
+      } else if (count == kIlvGroup && (st.raw[p] & 15u) == 0) {
+        u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(raw));
+        v[p][0] = x.x;
+        v[p][1] = x.y;
+        v[p][2] = x.z;
+        v[p][3] = x.w;
+      } else {
+        uint32_t tmp[4] = {0, 0, 0, 0};
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(raw);
+        for (uint32_t k = 0; k < count; ++k) tmp[k >> 2] |= (uint32_t)src[k] << (8 * (k & 3));
+        v[p][0] = tmp[0];
+        v[p][1] = tmp[1];
+        v[p][2] = tmp[2];
+        v[p][3] = tmp[3];
+      }
+    }
+    if (kTail && count == 0) continue;
+    uint32_t o[4 * RATIO];
+    merge_group<kChain>(v, o);
+    if (count == kIlvGroup) {
+      u32x4* dst = reinterpret_cast<u32x4*>(out + RATIO * pos);
+#pragma unroll
+      for (uint32_t k = 0; k < RATIO; ++k)
+        __builtin_nontemporal_store(u32x4_make(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]), dst + k);
+    } else {
+      for (uint32_t k = 0; k < RATIO * count; ++k) out[RATIO * pos + k] = (uint8_t)(o[k >> 2] >> (8 * (k & 3)));
+    }
+  }
+}
+
+// tensors: all tensors of the call; tix[j]: the tensor of this launch's j-th
+// entry, whose 4-block tiles are tpre[j] .. tpre[j+1] - 1 (m entries,
+// n_tiles = tpre[m]).  Workgroup g takes tiles [g n_tiles / G, (g+1) n_tiles / G).
 template <uint32_t kChain>
 __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __restrict__ tensors,
-                                                         const IlvTile* __restrict__ tiles,
+                                                         const uint32_t* __restrict__ tix,
+                                                         const uint32_t* __restrict__ tpre, uint32_t m,
                                                          uint32_t* __restrict__ status, uint32_t n_slots,
                                                          uint32_t stage_words) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
-  constexpr uint32_t RATIO = ChainInfo<kChain>::ratio;
-  // dynamic LDS: [LutSet x n_slots][byte staging: 256 lanes x 20 B]
-  //              [word staging: 4 wavefronts x stage_words], the table-build
-  //              scratch aliasing the word staging (built before any staging)
+  // dynamic LDS: [LutSet x n_slots][4 wavefronts x stage_words][96 spare words]
   extern __shared__ __align__(16) uint8_t smem[];
   LutSet* slots = reinterpret_cast<LutSet*>(smem);
-  uint8_t* stage_base = smem + n_slots * sizeof(LutSet);
-  uint32_t* word_stage = reinterpret_cast<uint32_t*>(stage_base + 256 * 20);
-  BuildScratch& bs = *reinterpret_cast<BuildScratch*>(word_stage);
+  uint32_t* const stage = reinterpret_cast<uint32_t*>(smem + n_slots * sizeof(LutSet));
+  __shared__ BuildScratch bs;
   __shared__ uint64_t s_table[NP], s_data[NP], s_datalen[NP], s_raw[NP];
-  __shared__ uint32_t s_bad, s_slot[NP];   // s_slot: 0 = not coded, k = slot k - 1
-  const IlvTile tile = tiles[blockIdx.x];
-  const IlvTensor& T = tensors[tile.tensor];
-  const uint32_t t = threadIdx.x;
-  const uint64_t n = T.n;
-  const uint32_t nb = (uint32_t)((n + kIlvBlock - 1) / kIlvBlock);
-  if (t == 0) {
-    s_bad = 0;
-    uint32_t next_slot = 0;
-    for (uint32_t p = 0; p < NP; ++p) {
-      const IlvPlane& P = T.planes[p];
-      s_raw[p] = P.base;
-      s_slot[p] = 0;
-      if (!P.coded) continue;
-      // huff_ilv payload: tag 0 stores the plane after the tag byte
-      const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
-      if (P.len == 0) s_bad |= kIlvErrHeader;
-      else if (pay[0] == 0) {
-        if (P.len != n + 1) s_bad |= kIlvErrHeader;
-        s_raw[p] = P.base + 1;
-      } else if (pay[0] == 1 && P.len >= 5 && ld_u32le(pay + 1) == n) {
-        if (next_slot < n_slots) s_slot[p] = ++next_slot;
-        else s_bad |= kIlvErrHeader;
-      } else {
-        s_bad |= kIlvErrHeader;
-      }
-    }
+  __shared__ uint32_t s_bad, s_slot[NP];  // s_slot: 0 = not coded, k = slot k - 1
+  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
+  const uint32_t n_tiles = tpre[m];
+  const uint32_t tile0 = (uint32_t)((uint64_t)blockIdx.x * n_tiles / gridDim.x);
+  const uint32_t tile1 = (uint32_t)((uint64_t)(blockIdx.x + 1) * n_tiles / gridDim.x);
+  if (tile0 >= tile1) return;
+  // entry holding tile0: the last j with tpre[j] <= tile0
+  uint32_t lo = 0, hi = m;
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) / 2;
+    if (tpre[mid] <= tile0) lo = mid;
+    else hi = mid;
   }
-  __syncthreads();
-  // ---- prologue: per coded plane, parse the header and build LDS tables ----
+  uint32_t j = lo, cur = 0xFFFFFFFFu, bad = 0;
+  uint32_t* const sw = stage + wave * stage_words;
+  for (uint32_t tile = tile0; tile < tile1; ++tile) {
+    while (tile >= tpre[j + 1]) ++j;
+    const uint32_t ti = tix[j];
+    const IlvTensor& T = tensors[ti];
+    const uint64_t n = T.n;
+    const uint32_t nb = (uint32_t)((n + kIlvBlock - 1) / kIlvBlock);
+    if (ti != cur) {
+      // ---- new tensor: parse its plane headers and build the LDS tables ----
+      if (bad) atomicOr(&status[cur], bad);
+      bad = 0;
+      cur = ti;
+      __syncthreads();  // every wavefront is done with the previous tables
+      if (t == 0) {
+        s_bad = 0;
+        uint32_t next_slot = 0;
+        for (uint32_t p = 0; p < NP; ++p) {
+          const IlvPlane& P = T.planes[p];
+          s_raw[p] = P.base;
+          s_slot[p] = 0;
+          if (!P.coded) continue;
+          // huff_ilv payload: tag 0 stores the plane after the tag byte
+          const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
+          if (P.len == 0) s_bad |= kIlvErrHeader;
+          else if (pay[0] == 0) {
+            if (P.len != n + 1) s_bad |= kIlvErrHeader;
+            s_raw[p] = P.base + 1;
+          } else if (pay[0] == 1 && P.len >= 5 && ld_u32le(pay + 1) == n) {
+            if (next_slot < n_slots) s_slot[p] = ++next_slot;
+            else s_bad |= kIlvErrHeader;
+          } else {
+            s_bad |= kIlvErrHeader;
+          }
+        }
+      }
+      __syncthreads();
 #pragma unroll
-  for (uint32_t p = 0; p < NP; ++p) {
-    const IlvPlane P = T.planes[p];
-    if (!s_slot[p]) continue;
-    LutSet& ls = slots[s_slot[p] - 1];
-    const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
-    build_tables(ls, bs, pay + 5, P.len >= 5 ? P.len - 5 : 0);
-    if (t == 0) {
-      if (ls.status) s_bad |= kIlvErrHeader;
-      uint64_t head = 5 + bs.hdr_len;
-      head += (4 - head % 4) % 4;
-      const uint64_t data0 = head + 4ull * (nb + 1);
-      if (data0 > P.len) {
-        s_bad |= kIlvErrHeader;
-      } else {
-        s_table[p] = P.base + head;
-        s_data[p] = P.base + data0;
-        s_datalen[p] = P.len - data0;
-        const uint32_t* tab = reinterpret_cast<const uint32_t*>(P.base + head);
-        if (tab[0] != 0 || tab[nb] != s_datalen[p]) s_bad |= kIlvErrBlock;
+      for (uint32_t p = 0; p < NP; ++p) {
+        if (!s_slot[p]) continue;
+        const IlvPlane P = T.planes[p];
+        LutSet& ls = slots[s_slot[p] - 1];
+        const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
+        build_tables(ls, bs, pay + 5, P.len >= 5 ? P.len - 5 : 0);
+        if (t == 0) {
+          if (ls.status) s_bad |= kIlvErrHeader;
+          uint64_t head = 5 + bs.hdr_len;
+          head += (4 - head % 4) % 4;
+          const uint64_t data0 = head + 4ull * (nb + 1);
+          if (data0 > P.len) {
+            s_bad |= kIlvErrHeader;
+          } else {
+            s_table[p] = P.base + head;
+            s_data[p] = P.base + data0;
+            s_datalen[p] = P.len - data0;
+            const uint32_t* tab = reinterpret_cast<const uint32_t*>(P.base + head);
+            if (tab[0] != 0 || tab[nb] != s_datalen[p]) s_bad |= kIlvErrBlock;
+          }
+        }
+        __syncthreads();
       }
+      if (t == 0 && s_bad) atomicOr(&status[ti], s_bad);
     }
-    __syncthreads();
-  }
-  if (s_bad) {
-    if (t == 0) atomicOr(&status[tile.tensor], s_bad);
-    return;
-  }
-  // ---- main loop: one wavefront per block ----
-  const uint32_t wave = t >> 6, lane = t & 63u;
-  uint32_t bad = 0;
-  uint8_t* out = reinterpret_cast<uint8_t*>(T.out);
-  uint32_t* const sw = word_stage + wave * stage_words;
-  for (uint32_t bi = tile.block0 + wave; bi < tile.block0 + tile.nblocks; bi += 4) {
+    if (s_bad) continue;  // uniform: the tensor is rejected
+    const uint32_t bi = kIlvBlocksPerTile * (tile - tpre[j]) + wave;
+    if (bi >= nb) continue;
+    // ---- one wavefront per block ----
     const uint64_t bstart = (uint64_t)bi * kIlvBlock;
-    LaneBits lb[NP];
-    LaneLds ll[NP];
-    uint32_t lane_c[NP];
-    bool staged[NP];
-    uint32_t budget = stage_words;
-    // the previous block's last reads of `sw` must finish before restaging
-    __builtin_amdgcn_wave_barrier();
+    BlockState<NP> st;
+    uint32_t lane_c[NP], tot[NP], first[NP];
+    uint32_t need = 4;
+    bool ok = true;
+    st.coded_mask = 0;
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
-      lane_c[p] = 0;
-      staged[p] = false;
-      lb[p].ptr = lb[p].end = lb[p].safe = lb[p].start = nullptr;
-      lb[p].buf = 0;
-      lb[p].cnt = 0;
-      lb[p].nxt = 0;
-      ll[p].off = ll[p].end = ll[p].start = ll[p].cnt = ll[p].nxt = 0;
-      ll[p].buf = 0;
-      if (!s_slot[p]) continue;
+      st.raw[p] = s_raw[p];
+      st.lut[p] = nullptr;
+      st.words[p] = nullptr;
+      st.nw[p] = 0;
+      st.q[p] = 0;
+      lane_c[p] = tot[p] = first[p] = 0;
+      const uint32_t slot = __builtin_amdgcn_readfirstlane(s_slot[p]);
+      if (!slot) continue;
+      st.coded_mask |= 1u << p;
+      st.lut[p] = slots[slot - 1].t;
       const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
       const uint32_t o0 = tab[bi], o1 = tab[bi + 1];
-      const bool bok = o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64;
+      // offsets of an accepted stream are multiples of 4 (tab[0] == 0 and
+      // every block is 64 + 4 x words bytes long)
+      const bool bok = o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64 && (o0 & 3u) == 0;
       const uint8_t* blk = reinterpret_cast<const uint8_t*>(s_data[p]) + (bok ? o0 : 0);
       const uint32_t c = bok ? blk[lane] : 0u;
       const uint32_t incl = wave_incl_scan(c);
       const uint32_t total = __shfl(incl, 63, 64);
-      const bool sized = bok && 64u + 4u * total == o1 - o0;
-      if (!sized) bad |= kIlvErrBlock;
-      const uint32_t* words = reinterpret_cast<const uint32_t*>(blk + 64);
+      if (!bok || 64u + 4u * total != o1 - o0) ok = false;
+      st.words[p] = reinterpret_cast<const uint32_t*>(blk + 64);
       lane_c[p] = c;
-      if (sized && total <= budget) {
-        // coalesced copy of the block's words into this wavefront's LDS
-        const uint32_t base = stage_words - budget;
-        for (uint32_t i = lane; i < total; i += 64) sw[base + i] = gload_u32(words + i);
-        budget -= total;
-        staged[p] = true;
-        lane_start_lds(ll[p], sw, base + incl - c, base + incl);
-      } else {
-        lane_start(lb[p], words + (incl - c), sized ? words + incl : words + (incl - c),
-                   reinterpret_cast<const uint32_t*>(blk));
-      }
+      tot[p] = total;
+      first[p] = incl - c;
+      need += (total + 3u) & ~3u;
     }
-    __builtin_amdgcn_wave_barrier();
-    for (uint32_t r = 0; r < kIlvRounds; ++r) {
-      const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
-      const uint32_t count = pos < n ? (uint32_t)(n - pos < kIlvGroup ? n - pos : kIlvGroup) : 0u;
-      uint32_t v[NP][4];
+    if (!ok) {
+      bad |= kIlvErrBlock;
+      continue;
+    }
+    const bool full = bstart + kIlvBlock <= n;
+    uint8_t* out = reinterpret_cast<uint8_t*>(T.out);
+    uint32_t q0[NP];
+    if (need <= stage_words) {
+      // coalesced copy of the block's lane streams into this wavefront's
+      // LDS region (16-byte aligned slices from word 4 on)
+      __builtin_amdgcn_wave_barrier();
+      uint32_t base = 4;
 #pragma unroll
       for (uint32_t p = 0; p < NP; ++p) {
-        const uint64_t raw = s_raw[p] + pos;
-        if (staged[p]) {
-          decode_group_lds(slots[s_slot[p] - 1], sw, ll[p], count, stage_base + 20u * t, v[p][0], v[p][1], v[p][2],
-                           v[p][3]);
-        } else if (s_slot[p]) {
-          decode_group(slots[s_slot[p] - 1], lb[p], count, stage_base + 20u * t, v[p][0], v[p][1], v[p][2], v[p][3]);
-        } else if (count == kIlvGroup && (raw & 15u) == 0) {
-          u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(raw));
-          v[p][0] = x.x; v[p][1] = x.y; v[p][2] = x.z; v[p][3] = x.w;
-        } else {
-          uint32_t tmp[4] = {0, 0, 0, 0};
-          const uint8_t* src = reinterpret_cast<const uint8_t*>(raw);
-          for (uint32_t k = 0; k < count; ++k) tmp[k >> 2] |= (uint32_t)src[k] << (8 * (k & 3));
-          v[p][0] = tmp[0]; v[p][1] = tmp[1]; v[p][2] = tmp[2]; v[p][3] = tmp[3];
+        q0[p] = 0;
+        if (!(st.coded_mask & (1u << p))) continue;
+        const uint32_t* src = st.words[p];
+        uint32_t* dst = sw + base;
+        for (uint32_t i = 4 * lane; i < tot[p]; i += 256) {
+          if (i + 4 <= tot[p]) {
+            const u32x4a4 x = gload_u32x4(src + i);
+            *reinterpret_cast<u32x4*>(dst + i) = u32x4_make(x.x, x.y, x.z, x.w);
+          } else {
+            for (uint32_t k = i; k < tot[p]; ++k) dst[k] = gload_u32(src + k);
+          }
         }
+        st.q[p] = (base + first[p]) * 32u - 1u;
+        q0[p] = st.q[p];
+        base += (tot[p] + 3u) & ~3u;
       }
-      if (count == 0) continue;
-      uint32_t o[4 * RATIO];
-      merge_group<kChain>(v, o);
-      if (count == kIlvGroup) {
-        u32x4* dst = reinterpret_cast<u32x4*>(out + RATIO * pos);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (full) decode_block<kChain, false, true>(st, sw, out, n, bstart, lane);
+      else decode_block<kChain, true, true>(st, sw, out, n, bstart, lane);
+      __builtin_amdgcn_wave_barrier();
+    } else {
 #pragma unroll
-        for (uint32_t k = 0; k < RATIO; ++k)
-          __builtin_nontemporal_store(u32x4_make(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]), dst + k);
-      } else {
-        for (uint32_t k = 0; k < RATIO * count; ++k) out[RATIO * pos + k] = (uint8_t)(o[k >> 2] >> (8 * (k & 3)));
+      for (uint32_t p = 0; p < NP; ++p) {
+        if (st.words[p]) st.words[p] += first[p];
+        st.nw[p] = lane_c[p];
+        q0[p] = 0;
       }
+      decode_block<kChain, true, false>(st, sw, out, n, bstart, lane);
     }
     // acceptance: every lane's words hold exactly its codes
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
-      if (!s_slot[p]) continue;
-      const uint32_t used = staged[p] ? lane_used_lds(ll[p]) : lane_used(lb[p]);
+      if (!(st.coded_mask & (1u << p))) continue;
+      const uint32_t used = st.q[p] - q0[p];
       if ((used + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
     }
   }
-  if (bad) atomicOr(&status[tile.tensor], bad);
+  if (bad) atomicOr(&status[cur], bad);
 }
 
 // ---------------------------------------------------------------------------
@@ -658,23 +659,39 @@ __global__ void __launch_bounds__(64) ilv_encode_kernel(const IlvEncPlane* __res
   if (cnt) w[wi++] = (uint32_t)acc;
 }
 
-hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const IlvTile* tiles, uint32_t n_tiles,
-                             uint32_t* status, uint32_t n_slots, hipStream_t stream) {
-  if (!n_tiles) return hipSuccess;
-  const dim3 g(n_tiles), b(256);
-  // word staging per wavefront: up to 6.5 KB, within a 64 KB workgroup
-  // budget, and never smaller than the table-build scratch it aliases
-  const size_t fixed = (size_t)n_slots * sizeof(LutSet) + 256 * 20;
-  size_t per_wave = (65536 - fixed) / 4;
-  if (per_wave > 6656) per_wave = 6656;
-  per_wave &= ~(size_t)15;
-  if (per_wave * 4 < kIlvScratchBytes) return hipErrorInvalidValue;
-  const uint32_t stage_words = (uint32_t)(per_wave / 4);
-  const size_t lds = fixed + 4 * per_wave;
+size_t ilv_decode_lds_bytes(uint32_t n_slots, uint32_t stage_words) {
+  return (size_t)n_slots * sizeof(LutSet) + (4ull * stage_words + kIlvStageSpare) * 4ull;
+}
+
+static const void* ilv_decode_fn(uint32_t chain) {
   switch (chain) {
-#define PTWM_ILV_CASE(C)                                                                              \
-  case C:                                                                                             \
-    hipLaunchKernelGGL(ilv_decode_kernel<C>, g, b, lds, stream, tensors, tiles, status, n_slots, stage_words); \
+    case kChainIeee16Split2: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainIeee16Split2>);
+    case kChainIeee32Split4: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainIeee32Split4>);
+    case kChainE4m3Nibble: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainE4m3Nibble>);
+    case kChainE5m2Nibble: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainE5m2Nibble>);
+    case kChainNibbleSplit: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainNibbleSplit>);
+    case kChainPassthrough: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainPassthrough>);
+    default: return nullptr;
+  }
+}
+
+hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, int* wg_per_cu) {
+  const void* fn = ilv_decode_fn(chain);
+  if (!fn) return hipErrorInvalidValue;
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(wg_per_cu, fn, 256, ilv_decode_lds_bytes(n_slots, stage_words));
+}
+
+hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uint32_t* tix, const uint32_t* tpre,
+                             uint32_t m, uint32_t grid, uint32_t* status, uint32_t n_slots, uint32_t stage_words,
+                             hipStream_t stream) {
+  if (!grid || !m) return hipSuccess;
+  if (stage_words % 4 != 0 || stage_words < 8) return hipErrorInvalidValue;
+  const size_t lds = ilv_decode_lds_bytes(n_slots, stage_words);
+  switch (chain) {
+#define PTWM_ILV_CASE(C)                                                                                        \
+  case C:                                                                                                       \
+    hipLaunchKernelGGL(ilv_decode_kernel<C>, dim3(grid), dim3(256), lds, stream, tensors, tix, tpre, m, status, \
+                       n_slots, stage_words);                                                                   \
     break;
     PTWM_ILV_CASE(kChainIeee16Split2)
     PTWM_ILV_CASE(kChainIeee32Split4)

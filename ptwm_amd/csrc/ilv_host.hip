@@ -6,7 +6,8 @@
 // coded payload is not smaller than the plane is stored instead.
 //
 // Decode: tensors are grouped by chain and decoded with one fused launch per
-// chain (ilv_decode_kernel<chain>), tiles of 16 blocks per workgroup.
+// chain (ilv_decode_kernel<chain>): persistent workgroups (as many as fit on
+// the device at the launch's LDS size) over 4-block tiles.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -188,43 +189,91 @@ int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, u
   return (int64_t)total;
 }
 
-int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors) {
+int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in) {
   hipStream_t s = ctx.stream;
-  if (tensors.empty()) return kOk;
+  if (tensors_in.empty()) return kOk;
+  std::vector<IlvTensor> tensors = tensors_in;
   const size_t nt = tensors.size();
-  // tiles grouped by chain: one launch per chain present
-  std::vector<IlvTile> tiles;
+  if (ctx.cu_count <= 0) {
+    PTWM_HIP_TRY(hipDeviceGetAttribute(&ctx.cu_count, hipDeviceAttributeMultiprocessorCount, ctx.dev));
+    if (ctx.cu_count <= 0) ctx.cu_count = 1;
+  }
+  // Coded payloads are read as 32-bit words: copy the ones that do not
+  // start on a 4-byte boundary to aligned scratch first.
+  uint64_t realign_bytes = 0;
+  for (const IlvTensor& T : tensors)
+    for (uint32_t p = 0; p < T.n_planes; ++p)
+      if (T.planes[p].coded && (T.planes[p].base & 3u)) realign_bytes = align_up(realign_bytes + T.planes[p].len, 256);
+  if (realign_bytes) {
+    PTWM_HIP_TRY(ctx.ilv_realign.ensure(realign_bytes));
+    uint64_t off = 0;
+    for (IlvTensor& T : tensors)
+      for (uint32_t p = 0; p < T.n_planes; ++p) {
+        IlvPlane& P = T.planes[p];
+        if (!P.coded || !(P.base & 3u)) continue;
+        const uint64_t dst = reinterpret_cast<uint64_t>(ctx.ilv_realign.ptr) + off;
+        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(P.base), P.len,
+                                    hipMemcpyDeviceToDevice, s));
+        P.base = dst;
+        off = align_up(off + P.len, 256);
+      }
+  }
+  // One persistent launch per chain present.  Per launch: the tensor list,
+  // its 4-block tile prefix sums, the LDS table slots (most coded planes of
+  // any tensor) and the staging words per wavefront: the largest estimated
+  // block of any tensor (coded payload words per block, +2%, rounded up),
+  // capped by the workgroup LDS budget.  Blocks above it take the kernel's
+  // global-memory path.
   struct Launch {
-    uint32_t chain, first, count, slots;
+    uint32_t chain, first, m, slots, stage_words, grid;
   };
   std::vector<Launch> launches;
-  // 16 blocks per workgroup amortise the table build when there is work for
-  // >= 16 workgroups per CU; smaller jobs use 4 (one block per wavefront).
-  uint64_t total_blocks = 0;
-  for (const IlvTensor& T : tensors) total_blocks += (T.n + kIlvBlock - 1) / kIlvBlock;
-  const uint32_t per_tile = total_blocks >= 256ull * 16 * kIlvBlocksPerTile ? kIlvBlocksPerTile : 4;
+  std::vector<uint32_t> idx;  // per launch: [m + 1 prefix][m tensor indexes]
   for (uint32_t chain = 1; chain <= 6; ++chain) {
-    uint32_t first = (uint32_t)tiles.size(), slots = 0;
+    std::vector<uint32_t> tix, tpre{0};
+    uint32_t slots = 0;
+    uint64_t est = 0;
     for (uint32_t ti = 0; ti < nt; ++ti) {
       const IlvTensor& T = tensors[ti];
       if (T.chain != chain || T.n == 0) continue;
+      const uint64_t nb = (T.n + kIlvBlock - 1) / kIlvBlock;
       uint32_t coded = 0;
-      for (uint32_t p = 0; p < T.n_planes; ++p) coded += T.planes[p].coded ? 1 : 0;
+      uint64_t words = 4;
+      for (uint32_t p = 0; p < T.n_planes; ++p) {
+        if (!T.planes[p].coded) continue;
+        ++coded;
+        const uint64_t per_block = (T.planes[p].len + 4 * nb - 1) / (4 * nb);
+        words += align_up(per_block + per_block / 50 + 4, 4);
+      }
       slots = std::max(slots, coded);
-      const uint32_t nb = (uint32_t)((T.n + kIlvBlock - 1) / kIlvBlock);
-      for (uint32_t b = 0; b < nb; b += per_tile) tiles.push_back(IlvTile{ti, b, std::min<uint32_t>(per_tile, nb - b), 0});
+      est = std::max(est, words);
+      tix.push_back(ti);
+      tpre.push_back(tpre.back() + (uint32_t)((nb + kIlvBlocksPerTile - 1) / kIlvBlocksPerTile));
     }
-    if (tiles.size() > first) launches.push_back(Launch{chain, first, (uint32_t)tiles.size() - first, slots});
+    if (tix.empty()) continue;
+    const uint64_t fixed = ilv_decode_lds_bytes(slots, 0);
+    uint64_t cap_words = ((kIlvMaxLds - std::min<uint64_t>(fixed, kIlvMaxLds)) / 16) & ~3ull;
+    uint64_t stage = align_up(std::max<uint64_t>(est, 8), 4);
+    if (stage > cap_words) stage = cap_words;
+    if (stage < 8) return kInternal;
+    int per_cu = 0;
+    PTWM_HIP_TRY(ilv_decode_occupancy(chain, slots, (uint32_t)stage, &per_cu));
+    if (per_cu < 1) per_cu = 1;
+    const uint64_t n_tiles = tpre.back();
+    const uint32_t grid = (uint32_t)std::min<uint64_t>(n_tiles, (uint64_t)per_cu * ctx.cu_count);
+    launches.push_back(Launch{chain, (uint32_t)idx.size(), (uint32_t)tix.size(), slots, (uint32_t)stage, grid});
+    idx.insert(idx.end(), tpre.begin(), tpre.end());
+    idx.insert(idx.end(), tix.begin(), tix.end());
   }
   PTWM_HIP_TRY(ctx.ilv_tensors.ensure(nt * sizeof(IlvTensor)));
-  PTWM_HIP_TRY(ctx.ilv_tiles.ensure(tiles.size() * sizeof(IlvTile) + 16));
+  PTWM_HIP_TRY(ctx.ilv_tiles.ensure(idx.size() * sizeof(uint32_t) + 16));
   PTWM_HIP_TRY(ctx.ilv_status.ensure(nt * sizeof(uint32_t)));
-  PTWM_HIP_TRY(ctx.h_ilv.ensure(nt * sizeof(IlvTensor) + tiles.size() * sizeof(IlvTile) + nt * 4 + 64));
+  PTWM_HIP_TRY(ctx.h_ilv.ensure(nt * sizeof(IlvTensor) + idx.size() * sizeof(uint32_t) + nt * 4 + 64));
   uint8_t* h = static_cast<uint8_t*>(ctx.h_ilv.ptr);
   std::memcpy(h, tensors.data(), nt * sizeof(IlvTensor));
-  std::memcpy(h + nt * sizeof(IlvTensor), tiles.data(), tiles.size() * sizeof(IlvTile));
+  std::memcpy(h + nt * sizeof(IlvTensor), idx.data(), idx.size() * sizeof(uint32_t));
   PTWM_HIP_TRY(hipMemcpyAsync(ctx.ilv_tensors.ptr, h, nt * sizeof(IlvTensor), hipMemcpyHostToDevice, s));
-  PTWM_HIP_TRY(hipMemcpyAsync(ctx.ilv_tiles.ptr, h + nt * sizeof(IlvTensor), tiles.size() * sizeof(IlvTile),
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.ilv_tiles.ptr, h + nt * sizeof(IlvTensor), idx.size() * sizeof(uint32_t),
                               hipMemcpyHostToDevice, s));
   PTWM_HIP_TRY(hipMemsetAsync(ctx.ilv_status.ptr, 0, nt * sizeof(uint32_t), s));
   if (ctx.profile) {
@@ -232,12 +281,13 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors) {
     PTWM_HIP_TRY(hipEventRecord(ctx.ev[3], s));
   }
   for (const Launch& L : launches) {
-    PTWM_HIP_TRY(launch_ilv_decode(L.chain, static_cast<const IlvTensor*>(ctx.ilv_tensors.ptr),
-                                   static_cast<const IlvTile*>(ctx.ilv_tiles.ptr) + L.first, L.count,
-                                   static_cast<uint32_t*>(ctx.ilv_status.ptr), L.slots, s));
+    const uint32_t* base = static_cast<const uint32_t*>(ctx.ilv_tiles.ptr) + L.first;
+    PTWM_HIP_TRY(launch_ilv_decode(L.chain, static_cast<const IlvTensor*>(ctx.ilv_tensors.ptr), base + L.m + 1, base,
+                                   L.m, L.grid, static_cast<uint32_t*>(ctx.ilv_status.ptr), L.slots, L.stage_words,
+                                   s));
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], s));
-  uint32_t* hs = reinterpret_cast<uint32_t*>(h + nt * sizeof(IlvTensor) + tiles.size() * sizeof(IlvTile));
+  uint32_t* hs = reinterpret_cast<uint32_t*>(h + nt * sizeof(IlvTensor) + idx.size() * sizeof(uint32_t));
   PTWM_HIP_TRY(hipMemcpyAsync(hs, ctx.ilv_status.ptr, nt * 4, hipMemcpyDeviceToHost, s));
   PTWM_HIP_TRY(hipStreamSynchronize(s));
   if (ctx.profile) {

@@ -40,8 +40,9 @@ struct DevCtx {
   PinnedBuffer h_small;
   // huff_ilv encoder / decoder scratch
   DeviceBuffer enc_planes, enc_hist, enc_codes, enc_blocks, enc_lane_words, enc_block_bytes;
-  DeviceBuffer ilv_tensors, ilv_tiles, ilv_status;
+  DeviceBuffer ilv_tensors, ilv_tiles, ilv_status, ilv_realign;
   PinnedBuffer h_enc, h_ilv;
+  int cu_count = 0;  // compute units of the device (0: not queried yet)
   DeviceBuffer stage_in, stage_out, enc_split;
   // optional per-phase kernel timing with HIP events on `stream`
   bool profile = false;
