@@ -32,6 +32,22 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 
+# Measured HBM bytes per launch of the workload's dominant kernel: the
+# copy-calibrated FETCH_SIZE + WRITE_SIZE of two rocprofv3 --pmc runs of this
+# script, recorded (with the commands and raw counters) in these summaries.
+TRAFFIC_PROFILES = {"llama8b": "profiles/ilv_decode_kernel_bf16_llama8b.md"}
+
+
+def measured_traffic(workload: str):
+    rel = TRAFFIC_PROFILES.get(workload)
+    if not rel or not os.path.exists(os.path.join(ROOT, rel)):
+        return None, None
+    with open(os.path.join(ROOT, rel)) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1]), rel
+    return None, None
+
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
@@ -252,6 +268,7 @@ def main():
                         "ratio": round(wl.comp_bytes / wl.restored, 4), "encode_gbs": round(wl.encode_gbs, 1),
                         "description": wl.name}
     primary["secondary"] = extras
+    traffic_meas, traffic_src = measured_traffic(args.workload)
     res = {
         "metric": "decode GB/s (restored bytes) per MI355X",
         "value": round(value, 2),
@@ -268,7 +285,7 @@ def main():
         "config": primary,
         "roofline": {"bound": "hbm", "kernel": kernel_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel_ms": round(kms, 4),
-                     "traffic": None},
+                     "traffic": traffic_meas, "traffic_source": traffic_src},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

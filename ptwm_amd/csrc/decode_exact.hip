@@ -16,7 +16,7 @@
 // follow container.rs:2010-2049.
 //
 // This kernel is the exact path: it is used for the reference formats.
-// Throughput-oriented paths live in decode_fast.hip / huff_ilv.hip.
+// The throughput-oriented path is the huff_ilv codec (huff_ilv.hip).
 #include "ptwm_common.h"
 
 namespace ptwm {

@@ -38,18 +38,6 @@ namespace ptwm {
 
 namespace {
 
-__device__ __forceinline__ uint32_t revert16x2(uint32_t v) {
-  return ((v << 8) & 0x80008000u) | ((v >> 1) & 0x7F807F80u) | (v & 0x007F007Fu);
-}
-__device__ __forceinline__ uint32_t revert32(uint32_t v) {
-  return ((v << 8) & 0x80000000u) | ((v >> 1) & 0x7F800000u) | (v & 0x007FFFFFu);
-}
-__device__ __forceinline__ uint32_t revert_e4m3x4(uint32_t r) {
-  return ((r & 0xF0F0F0F0u) >> 1) | ((r & 0x08080808u) << 4) | (r & 0x07070707u);
-}
-__device__ __forceinline__ uint32_t revert_e5m2x4(uint32_t r) {
-  return ((r & 0xF8F8F8F8u) >> 1) | ((r & 0x04040404u) << 5) | (r & 0x03030303u);
-}
 __device__ __forceinline__ void zip2(uint32_t a, uint32_t b, uint32_t& lo, uint32_t& hi) {
   lo = __builtin_amdgcn_perm(b, a, 0x05010400u);
   hi = __builtin_amdgcn_perm(b, a, 0x07030602u);
@@ -79,18 +67,80 @@ __device__ __forceinline__ uint32_t gload_u32(const uint32_t* p) {
 __device__ __forceinline__ u32x4a4 gload_u32x4(const uint32_t* p) {
   return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4a4*)(uintptr_t)p);
 }
+// Streaming (nontemporal) 16-byte load / store and byte access at a device
+// address.  Explicitly global: flat accesses would also count against the
+// LDS wait counter and stall every table lookup behind them.
+__device__ __forceinline__ u32x4 gload_nt16(uint64_t a) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4*)(uintptr_t)a);
+}
+__device__ __forceinline__ void gstore_nt16(uint64_t a, u32x4 v) {
+  __builtin_nontemporal_store(v, (__attribute__((address_space(1))) u32x4*)(uintptr_t)a);
+}
+__device__ __forceinline__ uint32_t gload_u8(uint64_t a) {
+  return *(const __attribute__((address_space(1))) uint8_t*)(uintptr_t)a;
+}
+__device__ __forceinline__ void gstore_u8(uint64_t a, uint32_t v) {
+  *(__attribute__((address_space(1))) uint8_t*)(uintptr_t)a = (uint8_t)v;
+}
 
-// Per-coded-plane decode table, resident in LDS: one entry per 11-bit
-// window, entry = code length | symbol << 8.  Windows that match no code
-// decode as symbol 0 with length max_bits (the gap fill of tree.rs:143-169);
-// a table for max_bits < 11 is replicated over the unused high index bits.
-struct LutSet {
-  uint16_t t[2048];
-  uint32_t max_bits;
-  uint32_t status;
-  uint32_t pad[2];
+// LDS addresses as plain 32-bit integers: lane bit positions are absolute
+// LDS bit addresses, so a window's word address is (q >> 3) & ~3 with no
+// base to add, and table bases are constants folded into the ds offsets.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ uint32_t lds_ld32(uint32_t a) {
+  return *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)a;
+}
+__device__ __forceinline__ uint32_t lds_ld16(uint32_t a) {
+  return *(const __attribute__((address_space(3))) uint16_t*)(uintptr_t)a;
+}
+
+// Per-coded-plane decode table, resident in LDS (kIlvLutBytes): one u16
+// entry per 11-bit window, entry = code length | symbol' << 8.  Windows that
+// match no code decode as symbol 0 with length max_bits (the gap fill of
+// tree.rs:143-169); a table for max_bits < 11 is replicated over the unused
+// high index bits.  symbol' is the symbol after the plane's part of the
+// inverse chain (Xform below), so the merge only combines planes.
+constexpr uint32_t kIlvLutBytes = 4096;
+
+// Symbol transforms: the per-plane half of each chain's inverse
+// (transforms/fusion.rs:150-176, 279-296, 392-399; dtype8.rs:39-62).
+enum Xform : uint32_t {
+  kXNone = 0,
+  kXRot1 = 1,     // IEEE exponent byte e -> (e >> 1) | (e & 1) << 7
+  kXHi3 = 2,      // fp8 exponent nibble h -> (h & 0xF) << 3
+  kXE4m3Lo = 3,   // E4M3 sign/mantissa nibble l -> (l & 8) << 4 | (l & 7)
+  kXE5m2Lo = 4,   // E5M2 sign/mantissa nibble l -> (l & 8) >> 1 | (l & 4) << 5 | (l & 3)
+  kXHi4 = 5,      // nibble split high plane h -> (h & 0xF) << 4
+  kXLo4 = 6,      // nibble split low plane l -> l & 0xF
 };
-static_assert(sizeof(LutSet) % 16 == 0, "LutSet keeps the staging area 16-byte aligned");
+
+__device__ __forceinline__ uint32_t xform_byte(uint32_t x, uint32_t s) {
+  switch (x) {
+    case kXRot1: return ((s >> 1) | (s << 7)) & 0xFFu;
+    case kXHi3: return (s & 0xFu) << 3;
+    case kXE4m3Lo: return ((s & 8u) << 4) | (s & 7u);
+    case kXE5m2Lo: return ((s & 8u) >> 1) | ((s & 4u) << 5) | (s & 3u);
+    case kXHi4: return (s & 0xFu) << 4;
+    case kXLo4: return s & 0xFu;
+    default: return s;
+  }
+}
+
+// The same transform on 4 packed bytes (raw planes; x is a constant after
+// unrolling, so the switch folds away).
+__device__ __forceinline__ uint32_t xform_word(uint32_t x, uint32_t v) {
+  switch (x) {
+    case kXRot1: return ((v >> 1) & 0x7F7F7F7Fu) | ((v << 7) & 0x80808080u);
+    case kXHi3: return (v & 0x0F0F0F0Fu) << 3;
+    case kXE4m3Lo: return ((v & 0x08080808u) << 4) | (v & 0x07070707u);
+    case kXE5m2Lo: return ((v & 0x08080808u) >> 1) | ((v & 0x04040404u) << 5) | (v & 0x03030303u);
+    case kXHi4: return (v & 0x0F0F0F0Fu) << 4;
+    case kXLo4: return v & 0x0F0F0F0Fu;
+    default: return v;
+  }
+}
 
 // Build-time scratch, shared by every plane of the workgroup.
 struct BuildScratch {
@@ -98,13 +148,23 @@ struct BuildScratch {
   uint32_t counts[16];
   uint32_t next_code[16];
   uint32_t wave_len_count[4][16];
-  uint32_t nw, hb, err, hdr_len;
+  uint32_t nw, hb, err, hdr_len, max_bits;
 };
 
-// Build the table of one plane from the weights header at hdr (hdr_avail
-// bytes readable).  All 256 threads of the workgroup take part.  Sets
-// ls.status (nonzero: invalid header) and bs.hdr_len.
-__device__ void build_tables(LutSet& ls, BuildScratch& bs, const uint8_t* hdr, uint64_t hdr_avail) {
+// Per-workgroup decode state kept in LDS after the tables.
+struct DecodeCtl {
+  BuildScratch bs;
+  uint64_t table[4], data[4], datalen[4], raw[4];  // per plane
+  uint32_t coded[4];
+  uint32_t bad;
+};
+static_assert(sizeof(DecodeCtl) % 16 == 0, "DecodeCtl keeps the staging area 16-byte aligned");
+
+// Build the table `tab` of one plane from the weights header at hdr
+// (hdr_avail bytes readable), symbols transformed by `xf`.  All 256 threads
+// of the workgroup take part.  Sets bs.err (nonzero: invalid header) and
+// bs.hdr_len.
+__device__ void build_tables(uint16_t* tab, uint32_t xf, BuildScratch& bs, const uint8_t* hdr, uint64_t hdr_avail) {
   const uint32_t t = threadIdx.x;
   if (t == 0) {
     uint32_t err = 0, n = 0, hb = 0;
@@ -167,10 +227,10 @@ __device__ void build_tables(LutSet& ls, BuildScratch& bs, const uint8_t* hdr, u
     uint32_t kraft = 0;
     for (uint32_t l = 1; l <= maxb; ++l) kraft += bs.counts[l] << (11 - l);
     if (kraft > 2048) bs.err = 1;
-    ls.max_bits = maxb;
+    bs.max_bits = maxb;
   }
   __syncthreads();
-  const uint32_t max_bits = ls.max_bits;
+  const uint32_t max_bits = bs.max_bits;
   if (w) {
     uint32_t before = 0;
     for (uint32_t wv = 0; wv < wave; ++wv) before += bs.wave_len_count[wv][w];
@@ -181,15 +241,34 @@ __device__ void build_tables(LutSet& ls, BuildScratch& bs, const uint8_t* hdr, u
   } else {
     bs.rev[t] = 0;
   }
-  for (uint32_t i = t; i < 2048; i += 256) ls.t[i] = (uint16_t)max_bits;
+  // gap fill: symbol 0 (every transform maps 0 to 0) with length max_bits
+  for (uint32_t i = t; i < 2048; i += 256) tab[i] = (uint16_t)max_bits;
   __syncthreads();
   if (!bs.err && w) {
-    const uint16_t e = (uint16_t)(w | (t << 8));
+    const uint16_t e = (uint16_t)(w | (xform_byte(xf, t) << 8));
     const uint32_t spread = 1u << (11 - w);
-    for (uint32_t i = 0; i < spread; ++i) ls.t[bs.rev[t] | (i << w)] = e;
+    for (uint32_t i = 0; i < spread; ++i) tab[bs.rev[t] | (i << w)] = e;
   }
-  if (t == 0) ls.status = bs.err;
   __syncthreads();
+}
+
+// q + (e & 0xFF) in one instruction (SDWA byte select of the VOP2 add).
+__device__ __forceinline__ uint32_t add_byte0(uint32_t q, uint32_t e) {
+  uint32_t r;
+  asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
+      : "=v"(r)
+      : "v"(e), "v"(q));
+  return r;
+}
+
+// LDS address of the table entry for window bits 1..11: (win & 0xFFE) | lut
+// (lut is a multiple of kIlvLutBytes).  One v_and_or_b32 with the mask in a
+// VGPR: gfx9 VOP3 has no literal operand and reads at most one SGPR.
+__device__ __forceinline__ uint32_t lut_entry_addr(uint32_t win, uint32_t lut) {
+  if (__builtin_constant_p(lut) && lut == 0) return win & 0xFFEu;
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(win), "v"(0xFFEu), "s"(lut));
+  return r;
 }
 
 // Pack the symbol bytes (byte 1 of each entry) of 16 entries into 4 words.
@@ -203,28 +282,30 @@ __device__ __forceinline__ void pack_symbols(const uint32_t (&e)[16], uint32_t (
 }
 
 // Decode one group (16 symbols; with kTail only the first `count` advance
-// the stream) from the wavefront's staged words `sw`.  qm = the lane's bit
-// position in sw minus one: bit 0 of each window is the bit before the next
-// code, so `window & 0xFFE` is directly the byte offset of its table entry.
-// Reads stay inside the workgroup's staging area: a lane reads at most 90
-// words past its first word, and the area ends with 96 spare words.
+// the stream) from the wavefront's staged words.  qm = the lane's absolute
+// LDS bit address minus one: bit 0 of each window is the bit before the next
+// code, so `window & 0xFFE` is directly the byte offset of its entry in the
+// table at LDS address `lut`.  Reads stay inside the workgroup's staging
+// area: a lane reads at most 90 words past its first word, and the area ends
+// with 96 spare words.
 template <bool kTail>
-__device__ __forceinline__ void group_lds(const uint16_t* __restrict__ lut, const uint32_t* __restrict__ sw,
-                                          uint32_t& qm, uint32_t count, uint32_t (&v)[4]) {
-  const uint8_t* lb = reinterpret_cast<const uint8_t*>(lut);
+__device__ __forceinline__ void group_lds(uint32_t lut, uint32_t& qm, uint32_t count, uint32_t (&v)[4]) {
   uint32_t e[16];
 #pragma unroll
   for (uint32_t k = 0; k < 16; k += 2) {
-    const uint32_t wi = qm >> 5;
-    const uint32_t win = __builtin_amdgcn_alignbit(sw[wi + 1], sw[wi], qm);
-    const uint32_t e0 = *reinterpret_cast<const uint16_t*>(lb + (win & 0xFFEu));
-    uint32_t l0 = e0 & 0xFFu;
-    if (kTail && k >= count) l0 = 0;
-    const uint32_t win1 = __builtin_amdgcn_alignbit(0u, win, l0);
-    const uint32_t e1 = *reinterpret_cast<const uint16_t*>(lb + (win1 & 0xFFEu));
-    uint32_t l1 = e1 & 0xFFu;
-    if (kTail && k + 1 >= count) l1 = 0;
-    qm += l0 + l1;
+    const uint32_t wa = (qm >> 3) & ~3u;
+    const uint32_t win = __builtin_amdgcn_alignbit(lds_ld32(wa + 4), lds_ld32(wa), qm);
+    const uint32_t e0 = lds_ld16(lut_entry_addr(win, lut));
+    // the shift uses the low 5 bits of the entry: its code length
+    const uint32_t win1 = __builtin_amdgcn_alignbit(0u, win, kTail && k >= count ? 0u : e0);
+    const uint32_t e1 = lds_ld16(lut_entry_addr(win1, lut));
+    if constexpr (kTail) {
+      const uint32_t l0 = k >= count ? 0u : (e0 & 0xFFu);
+      const uint32_t l1 = k + 1 >= count ? 0u : (e1 & 0xFFu);
+      qm += l0 + l1;
+    } else {
+      qm = add_byte0(add_byte0(qm, e0), e1);
+    }
     e[k] = e0;
     e[k + 1] = e1;
   }
@@ -235,8 +316,8 @@ __device__ __forceinline__ void group_lds(const uint16_t* __restrict__ lut, cons
 // decode reading the lane's words (nw of them) from global memory; words
 // past the lane's count read as zero, as in the specification decoder.
 // q = bits consumed by the lane so far.
-__device__ __forceinline__ void group_global(const uint16_t* __restrict__ lut, const uint32_t* words, uint32_t nw,
-                                             uint32_t& q, uint32_t count, uint32_t (&v)[4]) {
+__device__ __forceinline__ void group_global(uint32_t lut, const uint32_t* words, uint32_t nw, uint32_t& q,
+                                             uint32_t count, uint32_t (&v)[4]) {
   uint32_t e[16];
 #pragma unroll
   for (uint32_t k = 0; k < 16; k += 2) {
@@ -244,9 +325,9 @@ __device__ __forceinline__ void group_global(const uint16_t* __restrict__ lut, c
     const uint32_t lo = wi < nw ? gload_u32(words + wi) : 0u;
     const uint32_t hi = wi + 1 < nw ? gload_u32(words + wi + 1) : 0u;
     const uint32_t win = __builtin_amdgcn_alignbit(hi, lo, q);
-    const uint32_t e0 = lut[win & 2047u];
+    const uint32_t e0 = lds_ld16(lut + ((win << 1) & 0xFFEu));
     const uint32_t l0 = k < count ? (e0 & 0xFFu) : 0u;
-    const uint32_t e1 = lut[__builtin_amdgcn_alignbit(0u, win, l0) & 2047u];
+    const uint32_t e1 = lds_ld16(lut + ((__builtin_amdgcn_alignbit(0u, win, l0) << 1) & 0xFFEu));
     const uint32_t l1 = k + 1 < count ? (e1 & 0xFFu) : 0u;
     q += l0 + l1;
     e[k] = e0;
@@ -263,27 +344,55 @@ static_assert(sizeof(BuildScratch) <= 1024, "scratch layout");
 // decode (fused with the inverse chain)
 // ---------------------------------------------------------------------------
 
+// Planes, output bytes per plane byte, and the symbol transform of each
+// plane (applied by the decode table for coded planes, by xform_word for
+// raw ones) for every chain.
 template <uint32_t kChain>
 struct ChainInfo;
-template <> struct ChainInfo<kChainIeee16Split2> { static constexpr uint32_t np = 2, ratio = 2; };
-template <> struct ChainInfo<kChainIeee32Split4> { static constexpr uint32_t np = 4, ratio = 4; };
-template <> struct ChainInfo<kChainE4m3Nibble> { static constexpr uint32_t np = 2, ratio = 1; };
-template <> struct ChainInfo<kChainE5m2Nibble> { static constexpr uint32_t np = 2, ratio = 1; };
-template <> struct ChainInfo<kChainNibbleSplit> { static constexpr uint32_t np = 2, ratio = 1; };
-template <> struct ChainInfo<kChainPassthrough> { static constexpr uint32_t np = 1, ratio = 1; };
+template <> struct ChainInfo<kChainIeee16Split2> {
+  static constexpr uint32_t np = 2, ratio = 2;
+  static constexpr uint32_t xf[2] = {kXNone, kXRot1};
+};
+template <> struct ChainInfo<kChainIeee32Split4> {
+  static constexpr uint32_t np = 4, ratio = 4;
+  static constexpr uint32_t xf[4] = {kXNone, kXNone, kXNone, kXRot1};
+};
+template <> struct ChainInfo<kChainE4m3Nibble> {
+  static constexpr uint32_t np = 2, ratio = 1;
+  static constexpr uint32_t xf[2] = {kXHi3, kXE4m3Lo};
+};
+template <> struct ChainInfo<kChainE5m2Nibble> {
+  static constexpr uint32_t np = 2, ratio = 1;
+  static constexpr uint32_t xf[2] = {kXHi3, kXE5m2Lo};
+};
+template <> struct ChainInfo<kChainNibbleSplit> {
+  static constexpr uint32_t np = 2, ratio = 1;
+  static constexpr uint32_t xf[2] = {kXHi4, kXLo4};
+};
+template <> struct ChainInfo<kChainPassthrough> {
+  static constexpr uint32_t np = 1, ratio = 1;
+  static constexpr uint32_t xf[1] = {kXNone};
+};
 
-// Merge one group (16 elements; v[p][k] = plane p bytes 4k..4k+3) into the
-// output words o[] (ratio * 4 words).
+// Merge one group (16 elements; v[p][k] = transformed plane p bytes
+// 4k..4k+3) into the output words o[] (ratio * 4 words).  With the exponent
+// byte rotated (e' = e >> 1 | (e & 1) << 7), the IEEE inverses of
+// fusion.rs:150-176 / 279-296 become a byte interleave plus one bit-select:
+// out.lo = mant_lo.7bits | e'.bit7, out.hi = sign | e'.7bits.  The fp8 and
+// nibble inverses become a plain OR of the two transformed nibble planes.
 template <uint32_t kChain>
 __device__ __forceinline__ void merge_group(const uint32_t (&v)[ChainInfo<kChain>::np][4],
                                             uint32_t (&o)[4 * ChainInfo<kChain>::ratio]) {
   if constexpr (kChain == kChainIeee16Split2) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      uint32_t lo, hi;
-      zip2(v[0][k], v[1][k], lo, hi);
-      o[2 * k] = revert16x2(lo);
-      o[2 * k + 1] = revert16x2(hi);
+      // a = [m0 e0' m1 e1'], b = [e0' m0 e1' m1] (and the same for bytes 2, 3)
+      const uint32_t a0 = __builtin_amdgcn_perm(v[1][k], v[0][k], 0x05010400u);
+      const uint32_t b0 = __builtin_amdgcn_perm(v[1][k], v[0][k], 0x01050004u);
+      const uint32_t a1 = __builtin_amdgcn_perm(v[1][k], v[0][k], 0x07030602u);
+      const uint32_t b1 = __builtin_amdgcn_perm(v[1][k], v[0][k], 0x03070206u);
+      o[2 * k] = (a0 & 0x7F7F7F7Fu) | (b0 & 0x80808080u);
+      o[2 * k + 1] = (a1 & 0x7F7F7F7Fu) | (b1 & 0x80808080u);
     }
   } else if constexpr (kChain == kChainIeee32Split4) {
 #pragma unroll
@@ -291,82 +400,111 @@ __device__ __forceinline__ void merge_group(const uint32_t (&v)[ChainInfo<kChain
       uint32_t ab_lo, ab_hi, cd_lo, cd_hi;
       zip2(v[0][k], v[1][k], ab_lo, ab_hi);
       zip2(v[2][k], v[3][k], cd_lo, cd_hi);
-      o[4 * k + 0] = revert32(__builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u));
-      o[4 * k + 1] = revert32(__builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u));
-      o[4 * k + 2] = revert32(__builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u));
-      o[4 * k + 3] = revert32(__builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u));
+      // a = [b0 b1 b2 e'], b = [b0 b1 e' b2]: keep a's 0x7F7FFFFF bits
+      const uint32_t a[4] = {__builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u),
+                             __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u),
+                             __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u),
+                             __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t b = __builtin_amdgcn_perm(a[i], a[i], 0x02030100u);
+        o[4 * k + i] = (a[i] & 0x7F7FFFFFu) | (b & 0x80800000u);
+      }
     }
   } else if constexpr (kChain == kChainPassthrough) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) o[k] = v[0][k];
   } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      uint32_t r8 = ((v[0][k] & 0x0F0F0F0Fu) << 4) | (v[1][k] & 0x0F0F0F0Fu);
-      if constexpr (kChain == kChainE4m3Nibble) o[k] = revert_e4m3x4(r8);
-      else if constexpr (kChain == kChainE5m2Nibble) o[k] = revert_e5m2x4(r8);
-      else o[k] = r8;
-    }
+    for (int k = 0; k < 4; ++k) o[k] = v[0][k] | v[1][k];
   }
 }
 
 // Per-block state of one wavefront: for each plane, a raw-byte base or a
-// coded stream (staged: bit position in the LDS region; global: lane word
-// pointer, word count and bits consumed).
+// coded stream (staged: absolute LDS bit address; global: lane word pointer,
+// word count and bits consumed).
 template <uint32_t NP>
 struct BlockState {
   uint64_t raw[NP];
-  const uint16_t* lut[NP];
   const uint32_t* words[NP];
   uint32_t nw[NP];
   uint32_t q[NP];
   uint32_t coded_mask;
 };
 
-// The 16 rounds of one block: decode one group per coded plane, load the
-// raw planes' groups, merge and store.
+// Symbols of plane positions [pos, pos + 16) clipped to n.
+template <bool kTail>
+__device__ __forceinline__ uint32_t group_count(uint64_t pos, uint64_t n) {
+  if (!kTail) return kIlvGroup;
+  return pos < n ? (uint32_t)(n - pos < kIlvGroup ? n - pos : kIlvGroup) : 0u;
+}
+
+// Load the raw (uncoded) planes' bytes of the group at plane position pos.
+template <uint32_t kChain, bool kTail>
+__device__ __forceinline__ void load_raw(const BlockState<ChainInfo<kChain>::np>& st, uint64_t pos, uint64_t n,
+                                         uint32_t (&x)[ChainInfo<kChain>::np][4]) {
+  constexpr uint32_t NP = ChainInfo<kChain>::np;
+  const uint32_t count = group_count<kTail>(pos, n);
+#pragma unroll
+  for (uint32_t p = 0; p < NP; ++p) {
+    if (st.coded_mask & (1u << p)) continue;
+    const uint64_t raw = st.raw[p] + pos;
+    if (count == kIlvGroup && (st.raw[p] & 15u) == 0) {
+      const u32x4 w = gload_nt16(raw);
+      x[p][0] = w.x;
+      x[p][1] = w.y;
+      x[p][2] = w.z;
+      x[p][3] = w.w;
+    } else {
+      uint32_t tmp[4] = {0, 0, 0, 0};
+      for (uint32_t k = 0; k < count; ++k) tmp[k >> 2] |= gload_u8(raw + k) << (8 * (k & 3));
+      x[p][0] = tmp[0];
+      x[p][1] = tmp[1];
+      x[p][2] = tmp[2];
+      x[p][3] = tmp[3];
+    }
+  }
+}
+
+// The 16 rounds of one block: decode one group per coded plane, take the
+// raw planes' groups (loaded one round ahead, so their latency overlaps the
+// table lookups), merge and store.  luts: LDS address of the first table
+// slot; plane p uses slot NP - 1 - p.  out: output tensor address.
 template <uint32_t kChain, bool kTail, bool kStaged>
-__device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& st, const uint32_t* sw, uint8_t* out,
+__device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& st, uint32_t luts, uint64_t out,
                                              uint64_t n, uint64_t bstart, uint32_t lane) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
   constexpr uint32_t RATIO = ChainInfo<kChain>::ratio;
+  uint32_t nxt[NP][4];
+  load_raw<kChain, kTail>(st, bstart + (uint64_t)kIlvGroup * lane, n, nxt);
   for (uint32_t r = 0; r < kIlvRounds; ++r) {
     const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
-    uint32_t count = kIlvGroup;
-    if (kTail) count = pos < n ? (uint32_t)(n - pos < kIlvGroup ? n - pos : kIlvGroup) : 0u;
+    const uint32_t count = group_count<kTail>(pos, n);
     uint32_t v[NP][4];
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
-      const uint64_t raw = st.raw[p] + pos;
-      if (st.coded_mask & (1u << p)) {
-        if constexpr (kStaged) group_lds<kTail>(st.lut[p], sw, st.q[p], count, v[p]);
-        else group_global(st.lut[p], st.words[p], st.nw[p], st.q[p], count, v[p]);
-      } else if (count == kIlvGroup && (st.raw[p] & 15u) == 0) {
-        u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(raw));
-        v[p][0] = x.x;
-        v[p][1] = x.y;
-        v[p][2] = x.z;
-        v[p][3] = x.w;
-      } else {
-        uint32_t tmp[4] = {0, 0, 0, 0};
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(raw);
-        for (uint32_t k = 0; k < count; ++k) tmp[k >> 2] |= (uint32_t)src[k] << (8 * (k & 3));
-        v[p][0] = tmp[0];
-        v[p][1] = tmp[1];
-        v[p][2] = tmp[2];
-        v[p][3] = tmp[3];
-      }
+      if (!(st.coded_mask & (1u << p))) continue;
+      const uint32_t lut = luts + (NP - 1 - p) * kIlvLutBytes;
+      if constexpr (kStaged) group_lds<kTail>(lut, st.q[p], count, v[p]);
+      else group_global(lut, st.words[p], st.nw[p], st.q[p], count, v[p]);
     }
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p) {
+      if (st.coded_mask & (1u << p)) continue;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[p][k] = xform_word(ChainInfo<kChain>::xf[p], nxt[p][k]);
+    }
+    if (r + 1 < kIlvRounds) load_raw<kChain, kTail>(st, pos + (uint64_t)kIlvGroup * 64u, n, nxt);
     if (kTail && count == 0) continue;
     uint32_t o[4 * RATIO];
     merge_group<kChain>(v, o);
+    const uint64_t dst = out + RATIO * pos;
     if (count == kIlvGroup) {
-      u32x4* dst = reinterpret_cast<u32x4*>(out + RATIO * pos);
 #pragma unroll
       for (uint32_t k = 0; k < RATIO; ++k)
-        __builtin_nontemporal_store(u32x4_make(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]), dst + k);
+        gstore_nt16(dst + 16 * k, u32x4_make(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]));
     } else {
-      for (uint32_t k = 0; k < RATIO * count; ++k) out[RATIO * pos + k] = (uint8_t)(o[k >> 2] >> (8 * (k & 3)));
+      for (uint32_t k = 0; k < RATIO * count; ++k) gstore_u8(dst + k, o[k >> 2] >> (8 * (k & 3)));
     }
   }
 }
@@ -381,14 +519,28 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
                                                          uint32_t* __restrict__ status, uint32_t n_slots,
                                                          uint32_t stage_words) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
-  // dynamic LDS: [LutSet x n_slots][4 wavefronts x stage_words][96 spare words]
+  // The kernel has no static LDS, so the dynamic area starts at LDS address
+  // 0 and every table sits on a kIlvLutBytes boundary (entry address =
+  // (window & 0xFFE) | table base).  Layout:
+  //   [n_slots tables (plane p in slot NP-1-p)][DecodeCtl]
+  //   [4 wavefronts x stage_words][96 spare words]
   extern __shared__ __align__(16) uint8_t smem[];
-  LutSet* slots = reinterpret_cast<LutSet*>(smem);
-  uint32_t* const stage = reinterpret_cast<uint32_t*>(smem + n_slots * sizeof(LutSet));
-  __shared__ BuildScratch bs;
-  __shared__ uint64_t s_table[NP], s_data[NP], s_datalen[NP], s_raw[NP];
-  __shared__ uint32_t s_bad, s_slot[NP];  // s_slot: 0 = not coded, k = slot k - 1
+  DecodeCtl& ctl = *reinterpret_cast<DecodeCtl*>(smem + n_slots * kIlvLutBytes);
+  uint32_t* const stage = reinterpret_cast<uint32_t*>(smem + n_slots * kIlvLutBytes + sizeof(DecodeCtl));
+  const uint32_t luts = lds_addr(smem);
+  BuildScratch& bs = ctl.bs;
+  uint64_t* const s_table = ctl.table;
+  uint64_t* const s_data = ctl.data;
+  uint64_t* const s_datalen = ctl.datalen;
+  uint64_t* const s_raw = ctl.raw;
+  uint32_t* const s_coded = ctl.coded;
+  uint32_t& s_bad = ctl.bad;
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
+  if (luts & (kIlvLutBytes - 1)) {
+    // not reachable with the layout above; refuse rather than mis-decode
+    if (t == 0 && blockIdx.x == 0) atomicOr(&status[tix[0]], kIlvErrHeader);
+    return;
+  }
   const uint32_t n_tiles = tpre[m];
   const uint32_t tile0 = (uint32_t)((uint64_t)blockIdx.x * n_tiles / gridDim.x);
   const uint32_t tile1 = (uint32_t)((uint64_t)(blockIdx.x + 1) * n_tiles / gridDim.x);
@@ -416,11 +568,10 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       __syncthreads();  // every wavefront is done with the previous tables
       if (t == 0) {
         s_bad = 0;
-        uint32_t next_slot = 0;
         for (uint32_t p = 0; p < NP; ++p) {
           const IlvPlane& P = T.planes[p];
           s_raw[p] = P.base;
-          s_slot[p] = 0;
+          s_coded[p] = 0;
           if (!P.coded) continue;
           // huff_ilv payload: tag 0 stores the plane after the tag byte
           const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
@@ -429,8 +580,8 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
             if (P.len != n + 1) s_bad |= kIlvErrHeader;
             s_raw[p] = P.base + 1;
           } else if (pay[0] == 1 && P.len >= 5 && ld_u32le(pay + 1) == n) {
-            if (next_slot < n_slots) s_slot[p] = ++next_slot;
-            else s_bad |= kIlvErrHeader;
+            if (NP - 1 - p < n_slots) s_coded[p] = 1;
+            else s_bad |= kIlvErrHeader;  // the launch reserved no table slot for it
           } else {
             s_bad |= kIlvErrHeader;
           }
@@ -439,13 +590,13 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       __syncthreads();
 #pragma unroll
       for (uint32_t p = 0; p < NP; ++p) {
-        if (!s_slot[p]) continue;
+        if (!s_coded[p]) continue;
         const IlvPlane P = T.planes[p];
-        LutSet& ls = slots[s_slot[p] - 1];
+        uint16_t* tab16 = reinterpret_cast<uint16_t*>(smem + (NP - 1 - p) * kIlvLutBytes);
         const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
-        build_tables(ls, bs, pay + 5, P.len >= 5 ? P.len - 5 : 0);
+        build_tables(tab16, ChainInfo<kChain>::xf[p], bs, pay + 5, P.len >= 5 ? P.len - 5 : 0);
         if (t == 0) {
-          if (ls.status) s_bad |= kIlvErrHeader;
+          if (bs.err) s_bad |= kIlvErrHeader;
           uint64_t head = 5 + bs.hdr_len;
           head += (4 - head % 4) % 4;
           const uint64_t data0 = head + 4ull * (nb + 1);
@@ -476,22 +627,19 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
       st.raw[p] = s_raw[p];
-      st.lut[p] = nullptr;
       st.words[p] = nullptr;
       st.nw[p] = 0;
       st.q[p] = 0;
       lane_c[p] = tot[p] = first[p] = 0;
-      const uint32_t slot = __builtin_amdgcn_readfirstlane(s_slot[p]);
-      if (!slot) continue;
+      if (!__builtin_amdgcn_readfirstlane(s_coded[p])) continue;
       st.coded_mask |= 1u << p;
-      st.lut[p] = slots[slot - 1].t;
       const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
-      const uint32_t o0 = tab[bi], o1 = tab[bi + 1];
+      const uint32_t o0 = gload_u32(tab + bi), o1 = gload_u32(tab + bi + 1);
       // offsets of an accepted stream are multiples of 4 (tab[0] == 0 and
       // every block is 64 + 4 x words bytes long)
       const bool bok = o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64 && (o0 & 3u) == 0;
       const uint8_t* blk = reinterpret_cast<const uint8_t*>(s_data[p]) + (bok ? o0 : 0);
-      const uint32_t c = bok ? blk[lane] : 0u;
+      const uint32_t c = bok ? gload_u8(reinterpret_cast<uint64_t>(blk) + lane) : 0u;
       const uint32_t incl = wave_incl_scan(c);
       const uint32_t total = __shfl(incl, 63, 64);
       if (!bok || 64u + 4u * total != o1 - o0) ok = false;
@@ -506,7 +654,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       continue;
     }
     const bool full = bstart + kIlvBlock <= n;
-    uint8_t* out = reinterpret_cast<uint8_t*>(T.out);
+    const uint64_t out = T.out;
     uint32_t q0[NP];
     if (need <= stage_words) {
       // coalesced copy of the block's lane streams into this wavefront's
@@ -527,15 +675,15 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
             for (uint32_t k = i; k < tot[p]; ++k) dst[k] = gload_u32(src + k);
           }
         }
-        st.q[p] = (base + first[p]) * 32u - 1u;
+        st.q[p] = lds_addr(sw + base + first[p]) * 8u - 1u;
         q0[p] = st.q[p];
         base += (tot[p] + 3u) & ~3u;
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (full) decode_block<kChain, false, true>(st, sw, out, n, bstart, lane);
-      else decode_block<kChain, true, true>(st, sw, out, n, bstart, lane);
+      if (full) decode_block<kChain, false, true>(st, luts, out, n, bstart, lane);
+      else decode_block<kChain, true, true>(st, luts, out, n, bstart, lane);
       __builtin_amdgcn_wave_barrier();
     } else {
 #pragma unroll
@@ -544,7 +692,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
         st.nw[p] = lane_c[p];
         q0[p] = 0;
       }
-      decode_block<kChain, true, false>(st, sw, out, n, bstart, lane);
+      decode_block<kChain, true, false>(st, luts, out, n, bstart, lane);
     }
     // acceptance: every lane's words hold exactly its codes
 #pragma unroll
@@ -660,7 +808,7 @@ __global__ void __launch_bounds__(64) ilv_encode_kernel(const IlvEncPlane* __res
 }
 
 size_t ilv_decode_lds_bytes(uint32_t n_slots, uint32_t stage_words) {
-  return (size_t)n_slots * sizeof(LutSet) + (4ull * stage_words + kIlvStageSpare) * 4ull;
+  return (size_t)n_slots * kIlvLutBytes + sizeof(DecodeCtl) + (4ull * stage_words + kIlvStageSpare) * 4ull;
 }
 
 static const void* ilv_decode_fn(uint32_t chain) {

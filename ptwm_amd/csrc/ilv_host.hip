@@ -237,15 +237,17 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
       const IlvTensor& T = tensors[ti];
       if (T.chain != chain || T.n == 0) continue;
       const uint64_t nb = (T.n + kIlvBlock - 1) / kIlvBlock;
-      uint32_t coded = 0;
+      // the kernel keeps plane p's table in slot n_planes - 1 - p (the
+      // exponent plane, last in every IEEE chain, in slot 0)
+      uint32_t need_slots = 0;
       uint64_t words = 4;
       for (uint32_t p = 0; p < T.n_planes; ++p) {
         if (!T.planes[p].coded) continue;
-        ++coded;
+        need_slots = std::max(need_slots, T.n_planes - p);
         const uint64_t per_block = (T.planes[p].len + 4 * nb - 1) / (4 * nb);
         words += align_up(per_block + per_block / 50 + 4, 4);
       }
-      slots = std::max(slots, coded);
+      slots = std::max(slots, need_slots);
       est = std::max(est, words);
       tix.push_back(ti);
       tpre.push_back(tpre.back() + (uint32_t)((nb + kIlvBlocksPerTile - 1) / kIlvBlocksPerTile));
