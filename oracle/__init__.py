@@ -80,6 +80,10 @@ def lib():
         L.por_decode_plane_chunked_mt.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz, C.c_int]
         L.por_huf_lengths_from_freqs.restype = C.c_int
         L.por_huf_lengths_from_freqs.argtypes = [vp, vp]
+        L.por_huf_lengths_limited.restype = C.c_int
+        L.por_huf_lengths_limited.argtypes = [vp, vp, C.c_int]
+        L.por_ilv_lengths.restype = C.c_int
+        L.por_ilv_lengths.argtypes = [vp, vp]
         L.por_huf_from_lengths.restype = C.c_int
         L.por_huf_from_lengths.argtypes = [vp, vp, vp]
         L.por_huf_encode_weights.restype = i64
@@ -267,6 +271,24 @@ def huf_lengths(freqs):
     assert f.size == 256
     lengths = np.zeros(256, np.uint8)
     ok = lib().por_huf_lengths_from_freqs(_ptr(f), _ptr(lengths))
+    return lengths if ok else None
+
+
+def huf_lengths_limited(freqs, max_len):
+    """The reference tree with enforce_max_code_length at max_len."""
+    f = np.ascontiguousarray(freqs, dtype=np.uint32)
+    assert f.size == 256
+    lengths = np.zeros(256, np.uint8)
+    ok = lib().por_huf_lengths_limited(_ptr(f), _ptr(lengths), int(max_len))
+    return lengths if ok else None
+
+
+def ilv_lengths(freqs):
+    """huff_ilv encoder code lengths (limit 6 for nibble alphabets, else 11)."""
+    f = np.ascontiguousarray(freqs, dtype=np.uint32)
+    assert f.size == 256
+    lengths = np.zeros(256, np.uint8)
+    ok = lib().por_ilv_lengths(_ptr(f), _ptr(lengths))
     return lengths if ok else None
 
 

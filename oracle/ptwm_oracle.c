@@ -224,8 +224,8 @@ static void enforce_max_code_length(uint8_t *lengths, uint8_t max_len) {
     }
 }
 
-/* tree.rs:19-85 */
-int por_huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]) {
+/* tree.rs:19-85 with enforce_max_code_length (tree.rs:212-242) at max_len */
+int por_huf_lengths_limited(const uint32_t freqs[256], uint8_t lengths[256], int max_len) {
     int sym[256], n = 0;
     memset(lengths, 0, 256);
     for (int i = 0; i < 256; i++) if (freqs[i] > 0) sym[n++] = i;
@@ -255,8 +255,13 @@ int por_huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]) 
             stack_id[sp] = right[id]; stack_d[sp] = nd; sp++;
         }
     }
-    enforce_max_code_length(lengths, HUF_MAX_TABLE_LOG);
+    enforce_max_code_length(lengths, (uint8_t)max_len);
     return 1;
+}
+
+/* tree.rs:19-85 + :212-242, the reference encoder's 11-bit limit */
+int por_huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]) {
+    return por_huf_lengths_limited(freqs, lengths, HUF_MAX_TABLE_LOG);
 }
 
 static uint16_t reverse_bits(uint16_t code, int nbits) {
@@ -900,11 +905,23 @@ int64_t por_decode_plane_chunked_mt(int codec, const uint8_t *payload, size_t pa
 /*   Lane j codes groups g = j + 64 r (r = 0..15), group g = plane positions  */
 /*   [b*16384 + 16 g, +16) clipped to n, as rev(canonical code) bits packed  */
 /*   LSB-first into its words (the reference's code/bit order, tree.rs).     */
+/* Code lengths: the reference tree (tree.rs:19-85) with its length limit    */
+/*   (tree.rs:212-242) set to 6 when every symbol is < 16 (nibble planes),   */
+/*   else 11.  Any lengths <= 11 decode; <= 6 lets decoders take two         */
+/*   symbols per 12-bit table lookup.                                        */
 /* ------------------------------------------------------------------------- */
 
 #define ILV_BLOCK 16384
 #define ILV_LANES 64
 #define ILV_GROUP 16
+#define ILV_NIBBLE_MAX_LEN 6
+
+/* the huff_ilv encoder's code lengths (see above) */
+int por_ilv_lengths(const uint32_t freqs[256], uint8_t lengths[256]) {
+    int nibble = 1;
+    for (int s = 16; s < 256; s++) if (freqs[s]) nibble = 0;
+    return por_huf_lengths_limited(freqs, lengths, nibble ? ILV_NIBBLE_MAX_LEN : HUF_MAX_TABLE_LOG);
+}
 
 size_t por_ilv_encode_bound(size_t len) {
     size_t nb = (len + ILV_BLOCK - 1) / ILV_BLOCK;
@@ -917,7 +934,7 @@ int64_t por_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap)
     por_histogram(plane, n, freqs);
     uint8_t lengths[256];
     uint16_t table[1 << HUF_MAX_TABLE_LOG], rev[256];
-    int ok = por_huf_lengths_from_freqs(freqs, lengths) && por_huf_from_lengths(lengths, table, rev);
+    int ok = por_ilv_lengths(freqs, lengths) && por_huf_from_lengths(lengths, table, rev);
     size_t nb = (n + ILV_BLOCK - 1) / ILV_BLOCK;
     if (ok && n <= 0xFFFFFFFFu) {
         int nw = 0;

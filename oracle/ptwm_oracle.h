@@ -84,6 +84,8 @@ void por_split_four(size_t len, size_t starts[4], size_t ends[4]);
 /* ---- Huffman (entropy/huffman/) ---- */
 /* tree.rs:19-85 + enforce_max_code_length :212-242.  Returns 1 ok, 0 None. */
 int por_huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]);
+/* the same tree with the length limit max_len (1..11) instead of 11 */
+int por_huf_lengths_limited(const uint32_t freqs[256], uint8_t lengths[256], int max_len);
 /* tree.rs:102-177.  decode_table must hold 2048 entries.  Returns max_bits
  * or 0 if the lengths are invalid (None). rev_codes may be NULL. */
 int por_huf_from_lengths(const uint8_t lengths[256], uint16_t *decode_table, uint16_t rev_codes[256]);
@@ -132,8 +134,10 @@ int64_t por_decode_plane_chunked_mt(int codec, const uint8_t *payload, size_t pa
 /* ---- huff_ilv: this build's GPU-native plane codec (no reference
  * counterpart; its wire format is specified by these two functions).  Code
  * lengths, canonical codes and the weights header are the reference
- * Huffman's (tree.rs, weights.rs); the bits are split over 64 lane
- * sub-streams per 16384-symbol block. ---- */
+ * Huffman's (tree.rs, weights.rs) with the length limit 6 for alphabets
+ * of symbols < 16, else 11 (por_ilv_lengths); the bits are split over 64
+ * lane sub-streams per 16384-symbol block. ---- */
+int por_ilv_lengths(const uint32_t freqs[256], uint8_t lengths[256]);
 int64_t por_ilv_encode(const uint8_t *plane, size_t len, uint8_t *out, size_t cap);
 int64_t por_ilv_decode(const uint8_t *payload, size_t len, uint8_t *out, size_t cap);
 size_t por_ilv_encode_bound(size_t len);

@@ -58,7 +58,7 @@ struct IlvEncBlock {
 hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uint32_t* tix, const uint32_t* tpre,
                              uint32_t m, uint32_t grid, uint32_t* status, uint32_t n_slots, uint32_t stage_words,
                              hipStream_t stream);
-size_t ilv_decode_lds_bytes(uint32_t n_slots, uint32_t stage_words);
+size_t ilv_decode_lds_bytes(uint32_t chain, uint32_t n_slots, uint32_t stage_words);
 hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, int* wg_per_cu);
 hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_t max_n, uint32_t* hist,
                            hipStream_t stream);

@@ -96,13 +96,26 @@ __device__ __forceinline__ uint32_t lds_ld16(uint32_t a) {
   return *(const __attribute__((address_space(3))) uint16_t*)(uintptr_t)a;
 }
 
-// Per-coded-plane decode table, resident in LDS (kIlvLutBytes): one u16
-// entry per 11-bit window, entry = code length | symbol' << 8.  Windows that
-// match no code decode as symbol 0 with length max_bits (the gap fill of
-// tree.rs:143-169); a table for max_bits < 11 is replicated over the unused
-// high index bits.  symbol' is the symbol after the plane's part of the
-// inverse chain (Xform below), so the merge only combines planes.
+// Per-coded-plane decode tables, resident in LDS.
+//
+// Single mode (any alphabet): 2048 u16 entries, one per 11-bit window,
+// entry = code length | symbol' << 8.  Windows that match no code decode as
+// symbol 0 with length max_bits (the gap fill of tree.rs:143-169); a table
+// for max_bits < 11 is replicated over the unused high index bits.  symbol'
+// is the symbol after the plane's part of the inverse chain (Xform below),
+// so the merge only combines planes.
+//
+// Pair mode (symbols < 16 and every code <= 6 bits, the huff_ilv encoder's
+// choice for nibble planes): 4096 u16 entries, one per 12-bit window,
+// each decoding the next two codes: entry = (len0 + len1) | s0 << 8 |
+// s1 << 12 (raw nibbles; both codes always fit 12 bits).  Partial groups
+// use a 64-entry single-mode table (6-bit windows, symbol' bytes) kept in
+// DecodeCtl.
+//
+// A table slot is 4 KiB for the IEEE and passthrough chains and 8 KiB for
+// the nibble chains (the only ones that use pair mode).
 constexpr uint32_t kIlvLutBytes = 4096;
+constexpr uint32_t kIlvPairLutBytes = 8192;
 
 // Symbol transforms: the per-plane half of each chain's inverse
 // (transforms/fusion.rs:150-176, 279-296, 392-399; dtype8.rs:39-62).
@@ -145,26 +158,32 @@ __device__ __forceinline__ uint32_t xform_word(uint32_t x, uint32_t v) {
 // Build-time scratch, shared by every plane of the workgroup.
 struct BuildScratch {
   uint16_t rev[256];
+  uint16_t t64raw[64];  // pair mode: 6-bit single table with raw symbols
   uint32_t counts[16];
   uint32_t next_code[16];
   uint32_t wave_len_count[4][16];
-  uint32_t nw, hb, err, hdr_len, max_bits;
+  uint32_t nw, hb, err, hdr_len, max_bits, pair;
 };
 
-// Per-workgroup decode state kept in LDS after the tables.
-struct DecodeCtl {
+// Per-workgroup decode state kept in LDS after the tables (t64 first: its
+// 128-byte tables stay aligned for the and_or entry addressing).
+struct alignas(16) DecodeCtl {
+  uint16_t t64[4][64];  // pair-mode planes: 6-bit single tables (symbol')
   BuildScratch bs;
   uint64_t table[4], data[4], datalen[4], raw[4];  // per plane
   uint32_t coded[4];
+  uint32_t pair[4];
   uint32_t bad;
 };
 static_assert(sizeof(DecodeCtl) % 16 == 0, "DecodeCtl keeps the staging area 16-byte aligned");
 
-// Build the table `tab` of one plane from the weights header at hdr
-// (hdr_avail bytes readable), symbols transformed by `xf`.  All 256 threads
-// of the workgroup take part.  Sets bs.err (nonzero: invalid header) and
-// bs.hdr_len.
-__device__ void build_tables(uint16_t* tab, uint32_t xf, BuildScratch& bs, const uint8_t* hdr, uint64_t hdr_avail) {
+// Build the tables of one plane from the weights header at hdr (hdr_avail
+// bytes readable), symbols transformed by `xf`: the pair table at `tab` plus
+// the 6-bit table at `t64` when pair_ok and the code allows it, else the
+// single table at `tab`.  All 256 threads of the workgroup take part.  Sets
+// bs.err (nonzero: invalid header), bs.pair and bs.hdr_len.
+__device__ void build_tables(uint16_t* tab, uint16_t* t64, bool pair_ok, uint32_t xf, BuildScratch& bs,
+                             const uint8_t* hdr, uint64_t hdr_avail) {
   const uint32_t t = threadIdx.x;
   if (t == 0) {
     uint32_t err = 0, n = 0, hb = 0;
@@ -228,6 +247,7 @@ __device__ void build_tables(uint16_t* tab, uint32_t xf, BuildScratch& bs, const
     for (uint32_t l = 1; l <= maxb; ++l) kraft += bs.counts[l] << (11 - l);
     if (kraft > 2048) bs.err = 1;
     bs.max_bits = maxb;
+    bs.pair = pair_ok && bs.nw <= 16 && maxb <= 6 ? 1u : 0u;
   }
   __syncthreads();
   const uint32_t max_bits = bs.max_bits;
@@ -240,6 +260,31 @@ __device__ void build_tables(uint16_t* tab, uint32_t xf, BuildScratch& bs, const
     bs.rev[t] = (uint16_t)r;
   } else {
     bs.rev[t] = 0;
+  }
+  if (bs.pair) {
+    // 6-bit single tables (gap fill: symbol 0, every transform maps 0 to 0)
+    if (t < 64) {
+      t64[t] = (uint16_t)max_bits;
+      bs.t64raw[t] = (uint16_t)max_bits;
+    }
+    __syncthreads();
+    if (!bs.err && w) {
+      const uint32_t spread = 1u << (6 - w);
+      for (uint32_t i = 0; i < spread; ++i) {
+        t64[bs.rev[t] | (i << w)] = (uint16_t)(w | (xform_byte(xf, t) << 8));
+        bs.t64raw[bs.rev[t] | (i << w)] = (uint16_t)(w | (t << 8));
+      }
+    }
+    __syncthreads();
+    // pair entries: the two codes at the start of each 12-bit window
+    for (uint32_t i = t; i < 4096; i += 256) {
+      const uint32_t e0 = bs.t64raw[i & 63u];
+      const uint32_t l0 = e0 & 0xFFu;
+      const uint32_t e1 = bs.t64raw[(i >> l0) & 63u];
+      tab[i] = (uint16_t)((l0 + (e1 & 0xFFu)) | ((e0 >> 8) << 8) | ((e1 >> 8) << 12));
+    }
+    __syncthreads();
+    return;
   }
   // gap fill: symbol 0 (every transform maps 0 to 0) with length max_bits
   for (uint32_t i = t; i < 2048; i += 256) tab[i] = (uint16_t)max_bits;
@@ -261,13 +306,18 @@ __device__ __forceinline__ uint32_t add_byte0(uint32_t q, uint32_t e) {
   return r;
 }
 
-// LDS address of the table entry for window bits 1..11: (win & 0xFFE) | lut
-// (lut is a multiple of kIlvLutBytes).  One v_and_or_b32 with the mask in a
-// VGPR: gfx9 VOP3 has no literal operand and reads at most one SGPR.
+// Entry-address masks: window bits 1..11 (single table), 1..12 (pair
+// table), 1..6 (the 64-entry tables), each times the 2-byte entry size.
+constexpr uint32_t kMask11 = 0xFFEu, kMask12 = 0x1FFEu, kMask6 = 0x7Eu;
+
+// LDS address of the table entry for a window: (win & kMask) | lut (lut is a
+// multiple of the table size).  One v_and_or_b32 with the mask in a VGPR:
+// gfx9 VOP3 has no literal operand and reads at most one SGPR.
+template <uint32_t kMask>
 __device__ __forceinline__ uint32_t lut_entry_addr(uint32_t win, uint32_t lut) {
-  if (__builtin_constant_p(lut) && lut == 0) return win & 0xFFEu;
+  if (__builtin_constant_p(lut) && lut == 0) return win & kMask;
   uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(win), "v"(0xFFEu), "s"(lut));
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(win), "v"(kMask), "s"(lut));
   return r;
 }
 
@@ -284,21 +334,21 @@ __device__ __forceinline__ void pack_symbols(const uint32_t (&e)[16], uint32_t (
 // Decode one group (16 symbols; with kTail only the first `count` advance
 // the stream) from the wavefront's staged words.  qm = the lane's absolute
 // LDS bit address minus one: bit 0 of each window is the bit before the next
-// code, so `window & 0xFFE` is directly the byte offset of its entry in the
-// table at LDS address `lut`.  Reads stay inside the workgroup's staging
-// area: a lane reads at most 90 words past its first word, and the area ends
-// with 96 spare words.
-template <bool kTail>
+// code, so `window & kMask` is directly the byte offset of its entry in the
+// single-mode table at LDS address `lut`.  Reads stay inside the
+// workgroup's staging area: a lane reads at most 90 words past its first
+// word, and the area ends with 96 spare words.
+template <bool kTail, uint32_t kMask>
 __device__ __forceinline__ void group_lds(uint32_t lut, uint32_t& qm, uint32_t count, uint32_t (&v)[4]) {
   uint32_t e[16];
 #pragma unroll
   for (uint32_t k = 0; k < 16; k += 2) {
     const uint32_t wa = (qm >> 3) & ~3u;
     const uint32_t win = __builtin_amdgcn_alignbit(lds_ld32(wa + 4), lds_ld32(wa), qm);
-    const uint32_t e0 = lds_ld16(lut_entry_addr(win, lut));
+    const uint32_t e0 = lds_ld16(lut_entry_addr<kMask>(win, lut));
     // the shift uses the low 5 bits of the entry: its code length
     const uint32_t win1 = __builtin_amdgcn_alignbit(0u, win, kTail && k >= count ? 0u : e0);
-    const uint32_t e1 = lds_ld16(lut_entry_addr(win1, lut));
+    const uint32_t e1 = lds_ld16(lut_entry_addr<kMask>(win1, lut));
     if constexpr (kTail) {
       const uint32_t l0 = k >= count ? 0u : (e0 & 0xFFu);
       const uint32_t l1 = k + 1 >= count ? 0u : (e1 & 0xFFu);
@@ -312,10 +362,52 @@ __device__ __forceinline__ void group_lds(uint32_t lut, uint32_t& qm, uint32_t c
   pack_symbols(e, v);
 }
 
+// Pair mode, full group: 8 lookups in the 12-bit pair table at `lut`, one
+// 32-bit window per two lookups (<= 24 code bits plus the leading bit).
+// Yields the 16 raw nibble symbols, one per byte.
+__device__ __forceinline__ void group_lds_pair(uint32_t lut, uint32_t& qm, uint32_t (&v)[4]) {
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t wa = (qm >> 3) & ~3u;
+    const uint32_t win = __builtin_amdgcn_alignbit(lds_ld32(wa + 4), lds_ld32(wa), qm);
+    const uint32_t e0 = lds_ld16(lut_entry_addr<kMask12>(win, lut));
+    const uint32_t e1 = lds_ld16(lut_entry_addr<kMask12>(__builtin_amdgcn_alignbit(0u, win, e0), lut));
+    qm = add_byte0(add_byte0(qm, e0), e1);
+    // [s0|s1<<4, 0, s2|s3<<4, 0] -> one nibble per byte
+    const uint32_t w = __builtin_amdgcn_perm(e1, e0, 0x0c050c01u);
+    v[j] = (w | (w << 4)) & 0x0F0F0F0Fu;
+  }
+}
+
+// Two pair-mode planes of one block (plane a at table la, plane b at lb):
+// the same steps as group_lds_pair, with the two independent lookup chains
+// interleaved so that each one's LDS latency overlaps the other's work.
+__device__ __forceinline__ void group_lds_pair2(uint32_t la, uint32_t& qa, uint32_t (&va)[4], uint32_t lb,
+                                                uint32_t& qb, uint32_t (&vb)[4]) {
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t wa = (qa >> 3) & ~3u, wb = (qb >> 3) & ~3u;
+    const uint32_t xa = __builtin_amdgcn_alignbit(lds_ld32(wa + 4), lds_ld32(wa), qa);
+    const uint32_t xb = __builtin_amdgcn_alignbit(lds_ld32(wb + 4), lds_ld32(wb), qb);
+    const uint32_t a0 = lds_ld16(lut_entry_addr<kMask12>(xa, la));
+    const uint32_t b0 = lds_ld16(lut_entry_addr<kMask12>(xb, lb));
+    const uint32_t a1 = lds_ld16(lut_entry_addr<kMask12>(__builtin_amdgcn_alignbit(0u, xa, a0), la));
+    const uint32_t b1 = lds_ld16(lut_entry_addr<kMask12>(__builtin_amdgcn_alignbit(0u, xb, b0), lb));
+    qa = add_byte0(add_byte0(qa, a0), a1);
+    qb = add_byte0(add_byte0(qb, b0), b1);
+    const uint32_t ua = __builtin_amdgcn_perm(a1, a0, 0x0c050c01u);
+    const uint32_t ub = __builtin_amdgcn_perm(b1, b0, 0x0c050c01u);
+    va[j] = (ua | (ua << 4)) & 0x0F0F0F0Fu;
+    vb[j] = (ub | (ub << 4)) & 0x0F0F0F0Fu;
+  }
+}
+
 // Fallback for a block that does not fit the staging budget: the same
 // decode reading the lane's words (nw of them) from global memory; words
 // past the lane's count read as zero, as in the specification decoder.
-// q = bits consumed by the lane so far.
+// q = bits consumed by the lane so far.  kMask selects the single-mode
+// table (11-bit) or a pair-mode plane's 64-entry table.
+template <uint32_t kMask>
 __device__ __forceinline__ void group_global(uint32_t lut, const uint32_t* words, uint32_t nw, uint32_t& q,
                                              uint32_t count, uint32_t (&v)[4]) {
   uint32_t e[16];
@@ -325,9 +417,9 @@ __device__ __forceinline__ void group_global(uint32_t lut, const uint32_t* words
     const uint32_t lo = wi < nw ? gload_u32(words + wi) : 0u;
     const uint32_t hi = wi + 1 < nw ? gload_u32(words + wi + 1) : 0u;
     const uint32_t win = __builtin_amdgcn_alignbit(hi, lo, q);
-    const uint32_t e0 = lds_ld16(lut + ((win << 1) & 0xFFEu));
+    const uint32_t e0 = lds_ld16(lut + ((win << 1) & kMask));
     const uint32_t l0 = k < count ? (e0 & 0xFFu) : 0u;
-    const uint32_t e1 = lds_ld16(lut + ((__builtin_amdgcn_alignbit(0u, win, l0) << 1) & 0xFFEu));
+    const uint32_t e1 = lds_ld16(lut + ((__builtin_amdgcn_alignbit(0u, win, l0) << 1) & kMask));
     const uint32_t l1 = k + 1 < count ? (e1 & 0xFFu) : 0u;
     q += l0 + l1;
     e[k] = e0;
@@ -336,7 +428,7 @@ __device__ __forceinline__ void group_global(uint32_t lut, const uint32_t* words
   pack_symbols(e, v);
 }
 
-static_assert(sizeof(BuildScratch) <= 1024, "scratch layout");
+static_assert(sizeof(DecodeCtl) <= 2048, "LDS control block stays small");
 
 }  // namespace
 
@@ -344,35 +436,39 @@ static_assert(sizeof(BuildScratch) <= 1024, "scratch layout");
 // decode (fused with the inverse chain)
 // ---------------------------------------------------------------------------
 
-// Planes, output bytes per plane byte, and the symbol transform of each
-// plane (applied by the decode table for coded planes, by xform_word for
-// raw ones) for every chain.
+// Planes, output bytes per plane byte, the symbol transform of each plane
+// (applied by the decode table for coded planes, by xform_word for raw
+// ones), and the LDS table slot size (pair-mode capable or not) per chain.
 template <uint32_t kChain>
 struct ChainInfo;
 template <> struct ChainInfo<kChainIeee16Split2> {
-  static constexpr uint32_t np = 2, ratio = 2;
+  static constexpr uint32_t np = 2, ratio = 2, slot = kIlvLutBytes;
   static constexpr uint32_t xf[2] = {kXNone, kXRot1};
 };
 template <> struct ChainInfo<kChainIeee32Split4> {
-  static constexpr uint32_t np = 4, ratio = 4;
+  static constexpr uint32_t np = 4, ratio = 4, slot = kIlvLutBytes;
   static constexpr uint32_t xf[4] = {kXNone, kXNone, kXNone, kXRot1};
 };
 template <> struct ChainInfo<kChainE4m3Nibble> {
-  static constexpr uint32_t np = 2, ratio = 1;
+  static constexpr uint32_t np = 2, ratio = 1, slot = kIlvPairLutBytes;
   static constexpr uint32_t xf[2] = {kXHi3, kXE4m3Lo};
 };
 template <> struct ChainInfo<kChainE5m2Nibble> {
-  static constexpr uint32_t np = 2, ratio = 1;
+  static constexpr uint32_t np = 2, ratio = 1, slot = kIlvPairLutBytes;
   static constexpr uint32_t xf[2] = {kXHi3, kXE5m2Lo};
 };
 template <> struct ChainInfo<kChainNibbleSplit> {
-  static constexpr uint32_t np = 2, ratio = 1;
+  static constexpr uint32_t np = 2, ratio = 1, slot = kIlvPairLutBytes;
   static constexpr uint32_t xf[2] = {kXHi4, kXLo4};
 };
 template <> struct ChainInfo<kChainPassthrough> {
-  static constexpr uint32_t np = 1, ratio = 1;
+  static constexpr uint32_t np = 1, ratio = 1, slot = kIlvPairLutBytes;
   static constexpr uint32_t xf[1] = {kXNone};
 };
+
+__host__ __device__ constexpr uint32_t chain_slot_bytes(uint32_t chain) {
+  return chain == kChainIeee16Split2 || chain == kChainIeee32Split4 ? kIlvLutBytes : kIlvPairLutBytes;
+}
 
 // Merge one group (16 elements; v[p][k] = transformed plane p bytes
 // 4k..4k+3) into the output words o[] (ratio * 4 words).  With the exponent
@@ -429,7 +525,9 @@ struct BlockState {
   const uint32_t* words[NP];
   uint32_t nw[NP];
   uint32_t q[NP];
-  uint32_t coded_mask;
+  uint32_t t64[NP];     // LDS address of a pair-mode plane's 64-entry table
+  uint32_t coded_mask;  // bit p: plane p is huff_ilv coded
+  uint32_t pair_mask;   // bit p: plane p decodes in pair mode
 };
 
 // Symbols of plane positions [pos, pos + 16) clipped to n.
@@ -480,13 +578,38 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
   for (uint32_t r = 0; r < kIlvRounds; ++r) {
     const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
     const uint32_t count = group_count<kTail>(pos, n);
+    constexpr uint32_t SLOT = ChainInfo<kChain>::slot;
     uint32_t v[NP][4];
+    bool done = false;
+    if constexpr (NP == 2 && kStaged && !kTail) {
+      if (st.coded_mask == 3u && st.pair_mask == 3u) {
+        // both nibble planes in pair mode: their two lookup chains interleaved
+        group_lds_pair2(luts + SLOT, st.q[0], v[0], luts, st.q[1], v[1]);
+#pragma unroll
+        for (uint32_t p = 0; p < 2; ++p)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[p][k] = xform_word(ChainInfo<kChain>::xf[p], v[p][k]);
+        done = true;
+      }
+    }
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
-      if (!(st.coded_mask & (1u << p))) continue;
-      const uint32_t lut = luts + (NP - 1 - p) * kIlvLutBytes;
-      if constexpr (kStaged) group_lds<kTail>(lut, st.q[p], count, v[p]);
-      else group_global(lut, st.words[p], st.nw[p], st.q[p], count, v[p]);
+      if (done || !(st.coded_mask & (1u << p))) continue;
+      const uint32_t lut = luts + (NP - 1 - p) * SLOT;
+      if (st.pair_mask & (1u << p)) {
+        if constexpr (kStaged && !kTail) {
+          group_lds_pair(lut, st.q[p], v[p]);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[p][k] = xform_word(ChainInfo<kChain>::xf[p], v[p][k]);
+        } else if constexpr (kStaged) {
+          group_lds<kTail, kMask6>(st.t64[p], st.q[p], count, v[p]);
+        } else {
+          group_global<kMask6>(st.t64[p], st.words[p], st.nw[p], st.q[p], count, v[p]);
+        }
+      } else {
+        if constexpr (kStaged) group_lds<kTail, kMask11>(lut, st.q[p], count, v[p]);
+        else group_global<kMask11>(lut, st.words[p], st.nw[p], st.q[p], count, v[p]);
+      }
     }
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
@@ -519,14 +642,15 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
                                                          uint32_t* __restrict__ status, uint32_t n_slots,
                                                          uint32_t stage_words) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
+  constexpr uint32_t SLOT = ChainInfo<kChain>::slot;
   // The kernel has no static LDS, so the dynamic area starts at LDS address
-  // 0 and every table sits on a kIlvLutBytes boundary (entry address =
-  // (window & 0xFFE) | table base).  Layout:
+  // 0 and every table sits on a SLOT boundary (entry address =
+  // (window & mask) | table base).  Layout:
   //   [n_slots tables (plane p in slot NP-1-p)][DecodeCtl]
   //   [4 wavefronts x stage_words][96 spare words]
   extern __shared__ __align__(16) uint8_t smem[];
-  DecodeCtl& ctl = *reinterpret_cast<DecodeCtl*>(smem + n_slots * kIlvLutBytes);
-  uint32_t* const stage = reinterpret_cast<uint32_t*>(smem + n_slots * kIlvLutBytes + sizeof(DecodeCtl));
+  DecodeCtl& ctl = *reinterpret_cast<DecodeCtl*>(smem + n_slots * SLOT);
+  uint32_t* const stage = reinterpret_cast<uint32_t*>(smem + n_slots * SLOT + sizeof(DecodeCtl));
   const uint32_t luts = lds_addr(smem);
   BuildScratch& bs = ctl.bs;
   uint64_t* const s_table = ctl.table;
@@ -534,9 +658,10 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
   uint64_t* const s_datalen = ctl.datalen;
   uint64_t* const s_raw = ctl.raw;
   uint32_t* const s_coded = ctl.coded;
+  uint32_t* const s_pair = ctl.pair;
   uint32_t& s_bad = ctl.bad;
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
-  if (luts & (kIlvLutBytes - 1)) {
+  if (luts & (SLOT - 1)) {
     // not reachable with the layout above; refuse rather than mis-decode
     if (t == 0 && blockIdx.x == 0) atomicOr(&status[tix[0]], kIlvErrHeader);
     return;
@@ -592,10 +717,12 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       for (uint32_t p = 0; p < NP; ++p) {
         if (!s_coded[p]) continue;
         const IlvPlane P = T.planes[p];
-        uint16_t* tab16 = reinterpret_cast<uint16_t*>(smem + (NP - 1 - p) * kIlvLutBytes);
+        uint16_t* tab16 = reinterpret_cast<uint16_t*>(smem + (NP - 1 - p) * SLOT);
         const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
-        build_tables(tab16, ChainInfo<kChain>::xf[p], bs, pay + 5, P.len >= 5 ? P.len - 5 : 0);
+        build_tables(tab16, ctl.t64[p], SLOT == kIlvPairLutBytes, ChainInfo<kChain>::xf[p], bs, pay + 5,
+                     P.len >= 5 ? P.len - 5 : 0);
         if (t == 0) {
+          s_pair[p] = bs.pair;
           if (bs.err) s_bad |= kIlvErrHeader;
           uint64_t head = 5 + bs.hdr_len;
           head += (4 - head % 4) % 4;
@@ -621,17 +748,20 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
     const uint64_t bstart = (uint64_t)bi * kIlvBlock;
     BlockState<NP> st;
     uint32_t lane_c[NP], tot[NP], first[NP];
-    uint32_t need = 4;
+    uint32_t need = 4, need_skew = 0, uni_mask = 0;
     bool ok = true;
     st.coded_mask = 0;
+    st.pair_mask = 0;
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
       st.raw[p] = s_raw[p];
       st.words[p] = nullptr;
       st.nw[p] = 0;
       st.q[p] = 0;
+      st.t64[p] = lds_addr(ctl.t64[p]);
       lane_c[p] = tot[p] = first[p] = 0;
       if (!__builtin_amdgcn_readfirstlane(s_coded[p])) continue;
+      if (__builtin_amdgcn_readfirstlane(s_pair[p])) st.pair_mask |= 1u << p;
       st.coded_mask |= 1u << p;
       const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
       const uint32_t o0 = gload_u32(tab + bi), o1 = gload_u32(tab + bi + 1);
@@ -648,6 +778,11 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       tot[p] = total;
       first[p] = incl - c;
       need += (total + 3u) & ~3u;
+      const uint32_t c0 = __builtin_amdgcn_readfirstlane(c);
+      if (__ballot(c != c0) == 0 && c0 >= 4) {
+        uni_mask |= 1u << p;
+        need_skew += 128u;  // room for up to two skew words per lane
+      }
     }
     if (!ok) {
       bad |= kIlvErrBlock;
@@ -656,9 +791,14 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
     const bool full = bstart + kIlvBlock <= n;
     const uint64_t out = T.out;
     uint32_t q0[NP];
+    // skew uniform planes only when the staging budget has room for it
+    if (need + need_skew > stage_words) uni_mask = 0;
     if (need <= stage_words) {
-      // coalesced copy of the block's lane streams into this wavefront's
-      // LDS region (16-byte aligned slices from word 4 on)
+      // Coalesced copy of the block's lane streams into this wavefront's LDS
+      // region.  When every lane holds the same number of words c (a
+      // fixed-length code, e.g. a uniform nibble plane: 32 words per lane),
+      // lane j's stream goes to word (c + skew) j with c + skew odd; left
+      // contiguous, all 64 lanes' windows would fall into gcd(c, 64) banks.
       __builtin_amdgcn_wave_barrier();
       uint32_t base = 4;
 #pragma unroll
@@ -667,17 +807,44 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
         if (!(st.coded_mask & (1u << p))) continue;
         const uint32_t* src = st.words[p];
         uint32_t* dst = sw + base;
+        const uint32_t c0 = __builtin_amdgcn_readfirstlane(lane_c[p]);
+        const bool uniform = (uni_mask >> p) & 1u;
+        const uint32_t skew = uniform ? ((c0 & 1u) ? 2u : 1u) : 0u;
         for (uint32_t i = 4 * lane; i < tot[p]; i += 256) {
-          if (i + 4 <= tot[p]) {
-            const u32x4a4 x = gload_u32x4(src + i);
-            *reinterpret_cast<u32x4*>(dst + i) = u32x4_make(x.x, x.y, x.z, x.w);
+          if (!uniform) {
+            if (i + 4 <= tot[p]) {
+              const u32x4a4 x = gload_u32x4(src + i);
+              *reinterpret_cast<u32x4*>(dst + i) = u32x4_make(x.x, x.y, x.z, x.w);
+            } else {
+              for (uint32_t k = i; k < tot[p]; ++k) dst[k] = gload_u32(src + k);
+            }
           } else {
-            for (uint32_t k = i; k < tot[p]; ++k) dst[k] = gload_u32(src + k);
+            // lane of word i: i / c0 (float estimate, then exact correction);
+            // c0 >= 4, so the four words span at most two lanes
+            uint32_t j0 = (uint32_t)((float)i * __builtin_amdgcn_rcpf((float)c0));
+            if (j0 * c0 > i) --j0;
+            if ((j0 + 1) * c0 <= i) ++j0;
+            const uint32_t bnd = (j0 + 1) * c0;
+            uint32_t x[4] = {0, 0, 0, 0};
+            if (i + 4 <= tot[p]) {
+              const u32x4a4 v4 = gload_u32x4(src + i);
+              x[0] = v4.x;
+              x[1] = v4.y;
+              x[2] = v4.z;
+              x[3] = v4.w;
+            } else {
+              for (uint32_t k = i; k < tot[p]; ++k) x[k - i] = gload_u32(src + k);
+            }
+#pragma unroll
+            for (uint32_t d = 0; d < 4; ++d) {
+              const uint32_t w = i + d;
+              if (w < tot[p]) dst[w + skew * (j0 + (w >= bnd ? 1u : 0u))] = x[d];
+            }
           }
         }
-        st.q[p] = lds_addr(sw + base + first[p]) * 8u - 1u;
+        st.q[p] = lds_addr(dst + first[p] + skew * lane) * 8u - 1u;
         q0[p] = st.q[p];
-        base += (tot[p] + 3u) & ~3u;
+        base += (tot[p] + (uniform ? 128u : 0u) + 3u) & ~3u;
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -807,8 +974,8 @@ __global__ void __launch_bounds__(64) ilv_encode_kernel(const IlvEncPlane* __res
   if (cnt) w[wi++] = (uint32_t)acc;
 }
 
-size_t ilv_decode_lds_bytes(uint32_t n_slots, uint32_t stage_words) {
-  return (size_t)n_slots * kIlvLutBytes + sizeof(DecodeCtl) + (4ull * stage_words + kIlvStageSpare) * 4ull;
+size_t ilv_decode_lds_bytes(uint32_t chain, uint32_t n_slots, uint32_t stage_words) {
+  return (size_t)n_slots * chain_slot_bytes(chain) + sizeof(DecodeCtl) + (4ull * stage_words + kIlvStageSpare) * 4ull;
 }
 
 static const void* ilv_decode_fn(uint32_t chain) {
@@ -826,7 +993,8 @@ static const void* ilv_decode_fn(uint32_t chain) {
 hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, int* wg_per_cu) {
   const void* fn = ilv_decode_fn(chain);
   if (!fn) return hipErrorInvalidValue;
-  return hipOccupancyMaxActiveBlocksPerMultiprocessor(wg_per_cu, fn, 256, ilv_decode_lds_bytes(n_slots, stage_words));
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(wg_per_cu, fn, 256,
+                                                      ilv_decode_lds_bytes(chain, n_slots, stage_words));
 }
 
 hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uint32_t* tix, const uint32_t* tpre,
@@ -834,7 +1002,7 @@ hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uin
                              hipStream_t stream) {
   if (!grid || !m) return hipSuccess;
   if (stage_words % 4 != 0 || stage_words < 8) return hipErrorInvalidValue;
-  const size_t lds = ilv_decode_lds_bytes(n_slots, stage_words);
+  const size_t lds = ilv_decode_lds_bytes(chain, n_slots, stage_words);
   switch (chain) {
 #define PTWM_ILV_CASE(C)                                                                                        \
   case C:                                                                                                       \

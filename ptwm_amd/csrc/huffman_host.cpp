@@ -17,7 +17,8 @@
 
 namespace ptwm {
 
-bool huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]) {
+bool huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256], int max_len) {
+  if (max_len < 1 || max_len > kHufMaxBits) return false;
   std::memset(lengths, 0, 256);
   int sym[256];
   int n = 0;
@@ -64,25 +65,32 @@ bool huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]) {
   // enforce_max_code_length (tree.rs:212-242)
   bool clamped = false;
   for (int s = 0; s < 256; ++s)
-    if (lengths[s] > kHufMaxBits) {
-      lengths[s] = kHufMaxBits;
+    if (lengths[s] > max_len) {
+      lengths[s] = (uint8_t)max_len;
       clamped = true;
     }
   if (clamped) {
-    const uint32_t cap = 1u << kHufMaxBits;
+    const uint32_t cap = 1u << max_len;
     for (;;) {
       uint32_t kraft = 0;
       for (int s = 0; s < 256; ++s)
-        if (lengths[s]) kraft += 1u << (kHufMaxBits - lengths[s]);
+        if (lengths[s]) kraft += 1u << (max_len - lengths[s]);
       if (kraft <= cap) break;
       int victim = -1;
       for (int s = 0; s < 256; ++s)
-        if (lengths[s] > 0 && lengths[s] < kHufMaxBits && (victim < 0 || lengths[s] < lengths[victim])) victim = s;
+        if (lengths[s] > 0 && lengths[s] < max_len && (victim < 0 || lengths[s] < lengths[victim])) victim = s;
       if (victim < 0) break;
       lengths[victim]++;
     }
   }
   return true;
+}
+
+bool ilv_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]) {
+  bool nibble = true;
+  for (int s = 16; s < 256; ++s)
+    if (freqs[s]) nibble = false;
+  return huf_lengths_from_freqs(freqs, lengths, nibble ? kIlvNibbleMaxLen : kHufMaxBits);
 }
 
 int huf_canonical(const uint8_t lengths[256], uint16_t rev_codes[256]) {

@@ -8,8 +8,14 @@ namespace ptwm {
 constexpr int kHufMaxBits = 11;  // MAX_TABLE_LOG (entropy/huffman/tree.rs:5)
 
 // Code lengths from a histogram (tree.rs:19-85 + enforce_max_code_length
-// :212-242).  Returns false when every count is zero.
-bool huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]);
+// :212-242 at max_len, the reference encoder's 11 by default).  Returns false
+// when every count is zero.
+bool huf_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256], int max_len = kHufMaxBits);
+
+// huff_ilv's code lengths: the limit is 6 when every symbol is < 16 (nibble
+// planes, so that every pair of codes fits one 12-bit decode lookup), else 11.
+constexpr int kIlvNibbleMaxLen = 6;
+bool ilv_lengths_from_freqs(const uint32_t freqs[256], uint8_t lengths[256]);
 
 // Canonical codes (tree.rs:102-177): fills bit-reversed codes, returns
 // max_bits or 0 if the lengths do not form a valid prefix code.

@@ -55,7 +55,7 @@ int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, u
     if (n[p] == 0) continue;
     uint8_t lengths[256];
     uint16_t rev[256];
-    if (!huf_lengths_from_freqs(&hist[256 * p], lengths)) continue;
+    if (!ilv_lengths_from_freqs(&hist[256 * p], lengths)) continue;
     if (!huf_canonical(lengths, rev)) continue;
     for (int sy = 0; sy < 256; ++sy) codes[256 * p + sy] = ((uint32_t)lengths[sy] << 16) | rev[sy];
     uint8_t w[140];
@@ -245,7 +245,10 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
         if (!T.planes[p].coded) continue;
         need_slots = std::max(need_slots, T.n_planes - p);
         const uint64_t per_block = (T.planes[p].len + 4 * nb - 1) / (4 * nb);
-        words += align_up(per_block + per_block / 50 + 4, 4);
+        // nibble chains may carry fixed-length codes: room for the kernel's
+        // per-lane skew of equal-length lane streams (two words per lane)
+        const uint64_t skew = chain == kChainIeee16Split2 || chain == kChainIeee32Split4 ? 0 : 128;
+        words += align_up(per_block + per_block / 50 + skew + 4, 4);
       }
       slots = std::max(slots, need_slots);
       est = std::max(est, words);
@@ -253,7 +256,7 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
       tpre.push_back(tpre.back() + (uint32_t)((nb + kIlvBlocksPerTile - 1) / kIlvBlocksPerTile));
     }
     if (tix.empty()) continue;
-    const uint64_t fixed = ilv_decode_lds_bytes(slots, 0);
+    const uint64_t fixed = ilv_decode_lds_bytes(chain, slots, 0);
     uint64_t cap_words = ((kIlvMaxLds - std::min<uint64_t>(fixed, kIlvMaxLds)) / 16) & ~3ull;
     uint64_t stage = align_up(std::max<uint64_t>(est, 8), 4);
     if (stage > cap_words) stage = cap_words;

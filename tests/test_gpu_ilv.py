@@ -47,6 +47,10 @@ def cases():
         yield f"geo{n}", rng.geometric(0.3, n).clip(0, 255).astype(np.uint8).tobytes()
     yield "const", bytes([200]) * 33333
     yield "nib", rng.integers(0, 16, 50000).astype(np.uint8).tobytes()
+    # pair-mode planes (symbols < 16, codes <= 6 bits): skewed, one symbol, ragged tail
+    yield "nibskew", (16 - rng.geometric(0.45, 70001).clip(1, 16)).astype(np.uint8).tobytes()
+    yield "nibconst", bytes([7]) * 20000
+    yield "nibtail", rng.integers(0, 16, 16384 * 3 + 77).astype(np.uint8).tobytes()
     yield "rand", rng.integers(0, 256, 20000).astype(np.uint8).tobytes()
     w = (torch.randn(300_000, generator=torch.Generator().manual_seed(4)) * 0.02).to(torch.bfloat16)
     yield "bf16exp", O.chain_forward(O.CHAIN_IEEE16_SPLIT2, w.view(torch.uint8).numpy().tobytes())[1]
@@ -83,9 +87,17 @@ def test_gpu_decode_spec_payloads():
         assert n == len(src) and out == src, name
 
 
-def test_gpu_decode_malformed_matches_spec():
+MALFORMED_SOURCES = [
+    ("single-mode", lambda rng: rng.geometric(0.3, 40000).clip(0, 255).astype(np.uint8).tobytes()),
+    # nibble plane: pair-mode tables; header corruptions leave incomplete codes (table gaps)
+    ("pair-mode", lambda rng: (16 - rng.geometric(0.45, 40000).clip(1, 16)).astype(np.uint8).tobytes()),
+]
+
+
+@pytest.mark.parametrize("name,make", MALFORMED_SOURCES, ids=[m[0] for m in MALFORMED_SOURCES])
+def test_gpu_decode_malformed_matches_spec(name, make):
     rng = np.random.default_rng(5)
-    src = rng.geometric(0.3, 40000).clip(0, 255).astype(np.uint8).tobytes()
+    src = make(rng)
     good = O.ilv_encode(src)
     for k in range(80):
         b = bytearray(good)
@@ -111,6 +123,36 @@ def test_gpu_decode_malformed_matches_spec():
             assert n < 0, k
         else:
             assert n == len(want) and got == want, k
+
+
+def test_gpu_decode_incomplete_codes_match_spec():
+    """Weights headers edited so that the code is incomplete (Kraft < 1):
+    windows that match no code decode as symbol 0 with length max_bits
+    (tree.rs:143-169 gap fill), in single and in pair mode, exactly as the
+    specification decoder does; acceptance then decides."""
+    rng = np.random.default_rng(8)
+    for name, src in (("pair", (16 - rng.geometric(0.45, 30000).clip(1, 16)).astype(np.uint8).tobytes()),
+                      ("single", rng.geometric(0.3, 30000).clip(0, 40).astype(np.uint8).tobytes())):
+        good = O.ilv_encode(src)
+        assert good[0] == 1
+        nw = good[5] & 0x7F
+        for s in range(nw):
+            b = bytearray(good)
+            byte = 6 + s // 2
+            w = (b[byte] >> (4 * (s % 2))) & 0xF
+            if w == 0 or w >= (6 if name == "pair" else 11):
+                continue
+            b[byte] = (b[byte] & ~(0xF << (4 * (s % 2)))) | ((w + 1) << (4 * (s % 2)))
+            note(f"ilv incomplete code {name} symbol={s}")
+            try:
+                want = O.ilv_decode(bytes(b), len(src))
+            except O.OracleError:
+                want = None
+            n, got = gpu_decode(bytes(b), len(src))
+            if want is None:
+                assert n < 0, (name, s)
+            else:
+                assert n == len(want) and got == want, (name, s)
 
 
 def bf16(n, seed):

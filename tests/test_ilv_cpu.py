@@ -62,6 +62,8 @@ def ilv_cases():
     yield 5000, bytes([9]) * 5000
     yield 70000, rng.integers(0, 16, 70000).astype(np.uint8).tobytes()
     yield 4096, rng.integers(0, 256, 4096).astype(np.uint8).tobytes()
+    yield 50001, (15 - rng.geometric(0.45, 50001).clip(1, 16) + 1).astype(np.uint8).tobytes()  # skewed nibbles
+    yield 3000, bytes([7]) * 3000                                                              # one nibble symbol
 
 
 @pytest.mark.parametrize("n,src", list(ilv_cases()))
@@ -125,3 +127,44 @@ def test_ilv_decoder_rejects_corruption(orc):
     cut = bytes(p[:-4])
     with pytest.raises(O.OracleError):
         O.ilv_decode(cut, 20000)
+
+
+def _kraft(lengths):
+    return sum(2.0 ** -int(l) for l in lengths if l)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_ilv_length_policy(orc, seed):
+    """huff_ilv code lengths: the reference tree with the length limit 6 for
+    alphabets of symbols < 16 (every pair of codes then fits one 12-bit
+    decode lookup), else the reference's 11.  Checked by properties that do
+    not restate the clamp: the limit holds, the code stays a prefix code,
+    and a histogram whose tree already fits keeps the plain Huffman lengths
+    (pinned by the optimality tests of the reference restatement)."""
+    rng = np.random.default_rng(1000 + seed)
+    f = np.zeros(256, np.uint32)
+    nibble = seed % 2 == 0
+    k = int(rng.integers(1, 17 if nibble else 257))
+    syms = rng.choice(16 if nibble else 256, k, replace=False)
+    f[syms] = (2.0 ** rng.uniform(0, 24, k)).astype(np.uint64).clip(1, 2**31)
+    got = O.ilv_lengths(f)
+    plain = O.huf_lengths(f)
+    limit = 6 if nibble else 11
+    assert got.max() <= limit and _kraft(got) <= 1.0 + 1e-12
+    assert np.array_equal(got > 0, f > 0)
+    if plain.max() <= limit:
+        assert np.array_equal(got, plain)
+    assert np.array_equal(got, O.huf_lengths_limited(f, limit))
+
+
+def test_ilv_nibble_limit_on_fp8_exponent_histogram(orc):
+    """The E4M3 exponent-nibble histogram of config 3 (per-row absmax N(0,1)):
+    the 6-bit limit codes it no larger than the reference's 11-bit limit."""
+    p = [0.00011, 0.00011, 0.00022, 0.00042, 0.00085, 0.00172, 0.00343, 0.00683, 0.01374, 0.0274, 0.05453,
+         0.10744, 0.20101, 0.30964, 0.24284, 0.02971]
+    f = np.zeros(256, np.uint32)
+    f[:16] = np.round(np.array(p) * 1e7).astype(np.uint32)
+    lim = O.ilv_lengths(f)
+    ref = O.huf_lengths(f)
+    assert ref.max() == 11 and lim.max() <= 6
+    assert (f * lim.astype(np.uint64)).sum() <= (f * ref.astype(np.uint64)).sum()
