@@ -10,10 +10,11 @@ Same names, argument meaning and error behaviour as
 - ``hardware_backend_dispatch_decode_cuda(canonical_id, codec_id, state_bytes, compressed, out, device_ordinal)``
 
 ``src``/``dst`` are contiguous ``torch.Tensor`` objects resident on the
-device.  As in the reference, each tensor is exported with
-``__dlpack__(stream=<library stream>)`` so that torch orders its pending
-work before the library's stream touches the memory; the device ordinal of
-every tensor must equal ``device_ordinal`` (plane_codec_cuda.rs:120-124).
+device.  As in the reference, which exports each tensor with
+``__dlpack__(stream=<library stream>)``, work pending on the producer's
+stream is ordered before the library's stream touches the memory (for torch
+tensors with one event, see ``_order_after_producer``); the device ordinal
+of every tensor must equal ``device_ordinal`` (plane_codec_cuda.rs:120-124).
 """
 from __future__ import annotations
 
@@ -23,7 +24,40 @@ from . import ids
 from ._native import NativeError, check, lib
 
 
-def _dev_ptr_len(t, name: str, device_ordinal: int, stream: int, writable: bool):
+_order_cache: dict = {}   # (device, library stream) -> (ExternalStream, reusable Event)
+
+
+def _order_after_producer(t, device_ordinal: int, stream: int) -> None:
+    """Stream-ordered hand-off, as the reference's ``__dlpack__(stream=...)``:
+    work already queued on the producer's current stream completes before
+    the library stream touches the memory.  For torch tensors this is one
+    event recorded on torch's current stream and waited on by the library
+    stream (what ``__dlpack__`` does, without building a capsule); any other
+    DLPack object goes through ``__dlpack__`` itself."""
+    import torch
+    if not isinstance(t, torch.Tensor):
+        t.__dlpack__(stream=stream)
+        return
+    cur = torch.cuda.current_stream(device_ordinal)
+    if cur.cuda_stream == stream:
+        return
+    key = (device_ordinal, stream)
+    ent = _order_cache.get(key)
+    if ent is None:
+        ent = (torch.cuda.ExternalStream(stream, device=device_ordinal), torch.cuda.Event())
+        _order_cache[key] = ent
+    ext, ev = ent
+    ev.record(cur)
+    ext.wait_event(ev)
+
+
+def _both_torch(a, b) -> bool:
+    """One ordering event covers both tensors when both are torch tensors
+    (they share torch's current stream)."""
+    return type(a).__module__.startswith("torch") and type(b).__module__.startswith("torch")
+
+
+def _dev_ptr_len(t, name: str, device_ordinal: int, stream: int, writable: bool, ordered: bool = False):
     if not hasattr(t, "__dlpack__") or not hasattr(t, "data_ptr"):
         raise TypeError(f"{name}: expected a device tensor")
     if not t.is_contiguous():
@@ -32,8 +66,8 @@ def _dev_ptr_len(t, name: str, device_ordinal: int, stream: int, writable: bool)
         raise ValueError(f"{name}: tensor is not on a GPU device")
     if t.device.index != device_ordinal:
         raise ValueError(f"{name}: tensor is on device {t.device.index}, call names device {device_ordinal}")
-    # stream-ordered hand-off, like the reference's __dlpack__(stream=...)
-    t.__dlpack__(stream=stream)
+    if not ordered:
+        _order_after_producer(t, device_ordinal, stream)
     return int(t.data_ptr()), int(t.numel() * t.element_size())
 
 
@@ -52,7 +86,7 @@ def plane_codec_decode_cuda(selector: str, codec_id: str, state_bytes: bytes, sr
     if stream == 0:
         raise NativeError(-5, "plane_codec_decode_cuda: no stream for device")
     ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)
-    op, ol = _dev_ptr_len(dst, "dst", device_ordinal, stream, True)
+    op, ol = _dev_ptr_len(dst, "dst", device_ordinal, stream, True, _both_torch(src, dst))
     st = bytes(state_bytes)
     rc = L.ptwm_plane_codec_v1_decode_cuda(1, st if st else None, len(st), codec, 32, ip, il, op, ol,
                                            device_ordinal)
@@ -68,7 +102,7 @@ def plane_codec_encode_cuda(selector: str, codec_id: str, state_bytes: bytes, sr
     if stream == 0:
         raise NativeError(-5, "plane_codec_encode_cuda: no stream for device")
     ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)
-    op, ol = _dev_ptr_len(dst, "dst", device_ordinal, stream, True)
+    op, ol = _dev_ptr_len(dst, "dst", device_ordinal, stream, True, _both_torch(src, dst))
     st = bytes(state_bytes)
     needed = C.c_uint64(0)
     rc = L.ptwm_plane_codec_v1_encode_cuda(1, st if st else None, len(st), codec, 32, ip, il, op, ol,
@@ -93,7 +127,7 @@ def hardware_backend_dispatch_decode_cuda(canonical_id: str, codec_id: str, stat
     stream = hardware_backend_cuda_stream_handle(canonical_id, device_ordinal)
     codec = ids.resolve_codec_selector(codec_id)
     ip, il = _dev_ptr_len(compressed, "compressed", device_ordinal, stream, False)
-    op, ol = _dev_ptr_len(out, "out", device_ordinal, stream, True)
+    op, ol = _dev_ptr_len(out, "out", device_ordinal, stream, True, _both_torch(compressed, out))
     st = bytes(state_bytes)
     rc = lib().ptwm_hardware_backend_v1_dispatch_decode_cuda(1, st if st else None, len(st), codec, 32, ip, il, op,
                                                              ol, device_ordinal)

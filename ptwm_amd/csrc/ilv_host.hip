@@ -262,7 +262,14 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     if (stage > cap_words) stage = cap_words;
     if (stage < 8) return kInternal;
     int per_cu = 0;
-    PTWM_HIP_TRY(ilv_decode_occupancy(chain, slots, (uint32_t)stage, &per_cu));
+    const uint64_t occ_key = (uint64_t)chain | ((uint64_t)slots << 8) | (stage << 16);
+    auto it = ctx.ilv_occupancy.find(occ_key);
+    if (it != ctx.ilv_occupancy.end()) {
+      per_cu = it->second;
+    } else {
+      PTWM_HIP_TRY(ilv_decode_occupancy(chain, slots, (uint32_t)stage, &per_cu));
+      ctx.ilv_occupancy[occ_key] = per_cu;
+    }
     if (per_cu < 1) per_cu = 1;
     const uint64_t n_tiles = tpre.back();
     const uint32_t grid = (uint32_t)std::min<uint64_t>(n_tiles, (uint64_t)per_cu * ctx.cu_count);
@@ -270,30 +277,33 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     idx.insert(idx.end(), tpre.begin(), tpre.end());
     idx.insert(idx.end(), tix.begin(), tix.end());
   }
-  PTWM_HIP_TRY(ctx.ilv_tensors.ensure(nt * sizeof(IlvTensor)));
-  PTWM_HIP_TRY(ctx.ilv_tiles.ensure(idx.size() * sizeof(uint32_t) + 16));
-  PTWM_HIP_TRY(ctx.ilv_status.ensure(nt * sizeof(uint32_t)));
-  PTWM_HIP_TRY(ctx.h_ilv.ensure(nt * sizeof(IlvTensor) + idx.size() * sizeof(uint32_t) + nt * 4 + 64));
+  // one upload: [tensor descriptors][launch index arrays][zeroed status words]
+  const size_t off_idx = align_up(nt * sizeof(IlvTensor), 16);
+  const size_t off_status = align_up(off_idx + idx.size() * sizeof(uint32_t), 16);
+  const size_t args_bytes = off_status + nt * sizeof(uint32_t);
+  PTWM_HIP_TRY(ctx.ilv_args.ensure(args_bytes));
+  PTWM_HIP_TRY(ctx.h_ilv.ensure(args_bytes + nt * sizeof(uint32_t)));
   uint8_t* h = static_cast<uint8_t*>(ctx.h_ilv.ptr);
   std::memcpy(h, tensors.data(), nt * sizeof(IlvTensor));
-  std::memcpy(h + nt * sizeof(IlvTensor), idx.data(), idx.size() * sizeof(uint32_t));
-  PTWM_HIP_TRY(hipMemcpyAsync(ctx.ilv_tensors.ptr, h, nt * sizeof(IlvTensor), hipMemcpyHostToDevice, s));
-  PTWM_HIP_TRY(hipMemcpyAsync(ctx.ilv_tiles.ptr, h + nt * sizeof(IlvTensor), idx.size() * sizeof(uint32_t),
-                              hipMemcpyHostToDevice, s));
-  PTWM_HIP_TRY(hipMemsetAsync(ctx.ilv_status.ptr, 0, nt * sizeof(uint32_t), s));
+  std::memcpy(h + off_idx, idx.data(), idx.size() * sizeof(uint32_t));
+  std::memset(h + off_status, 0, nt * sizeof(uint32_t));
+  uint8_t* d = static_cast<uint8_t*>(ctx.ilv_args.ptr);
+  PTWM_HIP_TRY(hipMemcpyAsync(d, h, args_bytes, hipMemcpyHostToDevice, s));
   if (ctx.profile) {
     PTWM_HIP_TRY(ctx.ensure_events());
     PTWM_HIP_TRY(hipEventRecord(ctx.ev[3], s));
   }
+  uint32_t* status_dev = reinterpret_cast<uint32_t*>(d + off_status);
   for (const Launch& L : launches) {
-    const uint32_t* base = static_cast<const uint32_t*>(ctx.ilv_tiles.ptr) + L.first;
-    PTWM_HIP_TRY(launch_ilv_decode(L.chain, static_cast<const IlvTensor*>(ctx.ilv_tensors.ptr), base + L.m + 1, base,
-                                   L.m, L.grid, static_cast<uint32_t*>(ctx.ilv_status.ptr), L.slots, L.stage_words,
-                                   s));
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(d + off_idx) + L.first;
+    PTWM_HIP_TRY(launch_ilv_decode(L.chain, reinterpret_cast<const IlvTensor*>(d), base + L.m + 1, base, L.m, L.grid,
+                                   status_dev, L.slots, L.stage_words, s));
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], s));
-  uint32_t* hs = reinterpret_cast<uint32_t*>(h + nt * sizeof(IlvTensor) + idx.size() * sizeof(uint32_t));
-  PTWM_HIP_TRY(hipMemcpyAsync(hs, ctx.ilv_status.ptr, nt * 4, hipMemcpyDeviceToHost, s));
+  // status read back into the host buffer's tail (the upload above is
+  // ordered before it on the same stream)
+  uint32_t* hs = reinterpret_cast<uint32_t*>(h + args_bytes);
+  PTWM_HIP_TRY(hipMemcpyAsync(hs, status_dev, nt * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   PTWM_HIP_TRY(hipStreamSynchronize(s));
   if (ctx.profile) {
     float ms = 0;

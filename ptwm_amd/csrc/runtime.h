@@ -2,6 +2,7 @@
 #pragma once
 
 #include <cstdint>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -40,9 +41,10 @@ struct DevCtx {
   PinnedBuffer h_small;
   // huff_ilv encoder / decoder scratch
   DeviceBuffer enc_planes, enc_hist, enc_codes, enc_blocks, enc_lane_words, enc_block_bytes;
-  DeviceBuffer ilv_tensors, ilv_tiles, ilv_status, ilv_realign;
+  DeviceBuffer ilv_args, ilv_realign;
   PinnedBuffer h_enc, h_ilv;
   int cu_count = 0;  // compute units of the device (0: not queried yet)
+  std::map<uint64_t, int> ilv_occupancy;  // (chain, slots, stage words) -> workgroups per CU
   DeviceBuffer stage_in, stage_out, enc_split;
   // optional per-phase kernel timing with HIP events on `stream`
   bool profile = false;

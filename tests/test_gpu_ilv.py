@@ -224,3 +224,22 @@ def test_multi_tensor_plan_mixed_codecs():
     r = host(restored)
     assert n == len(a) + len(b)
     assert r[: len(a)] == a and r[out_off:] == b
+
+
+def test_stream_ordering_after_torch_producer():
+    """The library stream waits for work queued on torch's current stream
+    (the reference's __dlpack__(stream=...) contract): the payload is copied
+    in after a bounded spin on torch's stream and decoded at once; reading
+    it before the copy lands would give a different result."""
+    rng = np.random.default_rng(21)
+    src = rng.geometric(0.3, 200_000).clip(0, 255).astype(np.uint8).tobytes()
+    payload = O.ilv_encode(src)
+    host_t = torch.from_numpy(np.frombuffer(payload, np.uint8).copy()).pin_memory()
+    for trial in range(3):
+        note(f"ordering trial {trial}")
+        blob = torch.zeros(len(payload), dtype=torch.uint8, device="cuda:0")
+        dst = torch.zeros(len(src), dtype=torch.uint8, device="cuda:0")
+        torch.cuda._sleep(20_000_000)
+        blob.copy_(host_t, non_blocking=True)
+        n = api.plane_codec_decode_cuda(SEL, OWN, b"", blob, dst, 0)
+        assert n == len(src) and host(dst) == src
