@@ -76,7 +76,7 @@ def llama8b_shapes():
 class Workload:
     def __init__(self, name):
         self.name = name
-        self.tensors = []        # (raw uint8 device tensor, chain)
+        self.tensors = []        # (raw uint8 device tensor, chain, reference codecs or None)
         self.blob = None
         self.plan_bytes = b""
         self.out_len = 0
@@ -103,16 +103,36 @@ def gen_tensor(kind, shape, seed):
         m = torch.rand(shape, generator=g, device="cuda:0") < 0.01
         w[m] *= 50
         return w.view(torch.uint8).reshape(-1)
+    if kind == "fp4":          # two near-uniform FP4 (e2m1) codes per byte (config 5 weights)
+        return torch.randint(0, 256, shape, generator=g, device="cuda:0", dtype=torch.uint8).reshape(-1)
+    if kind == "e8m0":         # E8M0 block scales: round(N(-6, 1.5)) + 127 (config 5 scales)
+        s = torch.round(torch.randn(shape, generator=g, device="cuda:0") * 1.5 - 6) + 127
+        return s.clamp(0, 255).to(torch.uint8).reshape(-1)
     raise ValueError(kind)
 
 
+HUF, RANS = 1, 3   # reference codec wire ids (crates/ptwm-core/src/codec.rs:7-9)
+EXACT_ROUTE = "decode_exact (reference streams) + merge"
+
+
 def build_workload(name: str) -> Workload:
+    """`name` is a workload below, optionally suffixed "+crc" (every plane's
+    CRC-32 in the plan, verified by the decode) and/or "+hash" (every
+    tensor's XXH64 in the plan, verified by the decode)."""
     import torch
 
     from ptwm_amd import api, plan
 
+    base, *opts = name.split("+")
+    if set(opts) - {"crc", "hash"}:
+        raise SystemExit(f"unknown workload option in {name}")
+    name = base
+
     CH = {"w": plan.CHAIN_IEEE16_SPLIT2, "n": plan.CHAIN_IEEE16_SPLIT2, "fp8": plan.CHAIN_E4M3_NIBBLE,
-          "fp32o": plan.CHAIN_IEEE32_SPLIT4}
+          "fp32o": plan.CHAIN_IEEE32_SPLIT4, "fp4": plan.CHAIN_NIBBLE_SPLIT, "e8m0": plan.CHAIN_PASSTHROUGH}
+    # reference formats: (per-plane codecs, chunk size) by spec kind; None = the GPU-native codec
+    ref = None
+    exact = EXACT_ROUTE
     if name == "llama8b":
         specs = [(s, k) for _, s, k in llama8b_shapes()]
         desc = "config 4: Llama-3-8B-shaped bf16 model, 290 tensors, N(0,0.02) weights, norms 1+-0.01"
@@ -133,6 +153,37 @@ def build_workload(name: str) -> Workload:
         specs = [((32768, 16384), "w")]
         desc = "one bf16 32768x16384 N(0,0.02) tensor (1 GiB, config 4 distribution) for counter runs"
         kernel = "ilv_decode_kernel<1>"
+    elif name == "mxfp4":
+        specs = [((14336, 2048), "fp4"), ((14336, 128), "e8m0")]
+        desc = "config 5: MXFP4 weights 14336x2048 (nibble split) + E8M0 scales 14336x128 (byte plane)"
+        kernel = "ilv_decode_kernel<5>, <6>"
+    # the configs in the reference's own plane formats (GPU-encoded, byte-identical
+    # to the reference encoder), decoded by the exact route
+    elif name == "c1_ref":
+        specs = [((1024, 1024), "w")]
+        ref = {"w": ([HUF, HUF], 0)}
+        desc = "config 1 in reference format: bf16 1024x1024, Huffman on each plane"
+        kernel = exact
+    elif name == "c2_ref":
+        specs = [((4096, 4096), "fp32o")]
+        ref = {"fp32o": ([HUF, HUF, HUF, RANS], 262144)}
+        desc = "config 2 in reference format: fp32 4096x4096 + outliers, rANS exponent, Huffman mantissas, 256 KiB chunks"
+        kernel = exact
+    elif name == "c3_huf":
+        specs = [((8192, 8192), "fp8")]
+        ref = {"fp8": ([HUF, HUF], 0)}
+        desc = "config 3 in reference format: e4m3 8192x8192, Huffman on both nibble planes"
+        kernel = exact
+    elif name == "c3_rans":
+        specs = [((8192, 8192), "fp8")]
+        ref = {"fp8": ([RANS, RANS], 0)}
+        desc = "config 3 in reference format: e4m3 8192x8192, rANS on both nibble planes"
+        kernel = exact
+    elif name == "c5_ref":
+        specs = [((14336, 2048), "fp4"), ((14336, 128), "e8m0")]
+        ref = {"fp4": ([HUF, HUF], 0), "e8m0": ([HUF], 0)}
+        desc = "config 5 in reference format: MXFP4 weights (Huffman nibble planes) + E8M0 scales (Huffman)"
+        kernel = exact
     else:
         raise SystemExit(f"unknown workload {name}")
     wl = Workload(desc)
@@ -141,7 +192,7 @@ def build_workload(name: str) -> Workload:
     total_raw = 0
     for i, (shape, kind) in enumerate(specs):
         raw = gen_tensor(kind, shape, 1000 + i)
-        tensors.append((raw, CH[kind]))
+        tensors.append((raw, CH[kind], ref[kind] if ref else None))
         total_raw += raw.numel()
     log(f"[bench] generated {len(tensors)} tensors, {total_raw / 2**30:.2f} GiB")
     # encode every tensor with the library's GPU encoder into one blob
@@ -151,8 +202,11 @@ def build_workload(name: str) -> Workload:
     out_off = 0
     plans = []
     t0 = time.perf_counter()
-    for raw, chain in tensors:
-        used, st = api.encode_tensor_cuda(chain, raw, blob[off:], 0)
+    for raw, chain, rf in tensors:
+        if rf is None:
+            used, st = api.encode_tensor_cuda(chain, raw, blob[off:], 0)
+        else:
+            used, st = api.encode_tensor_ref_cuda(chain, rf[0], rf[1], raw, blob[off:], 0)
         t = plan.decode_plan(st)[0]
         t.out_offset = out_off
         for p in t.planes:
@@ -162,6 +216,15 @@ def build_workload(name: str) -> Workload:
         out_off = (out_off + raw.numel() + 255) // 256 * 256
     torch.cuda.synchronize()
     enc_s = time.perf_counter() - t0
+    for (raw, chain, _), t in zip(tensors, plans):
+        if "crc" in opts:
+            for p, c in zip(t.planes, api.plane_crc32_cuda(chain, raw, 0)):
+                p.crc32 = c
+        if "hash" in opts:
+            t.xxh64 = api.xxh64_cuda(raw, 0)
+    if opts:
+        wl.name += " (plan carries " + " and ".join(
+            {"crc": "plane CRC-32", "hash": "tensor XXH64"}[o] for o in opts) + ", verified by the decode)"
     wl.tensors = tensors
     wl.blob = blob[:off]
     wl.plan_bytes = plan.encode_plan(plans)
@@ -177,7 +240,7 @@ def build_workload(name: str) -> Workload:
 def verify(wl, out) -> bool:
     import torch
 
-    for raw, t in zip((r for r, _ in wl.tensors), wl.plans):
+    for raw, t in zip((r for r, _, _ in wl.tensors), wl.plans):
         if not torch.equal(out[t.out_offset: t.out_offset + raw.numel()], raw):
             return False
     return True
@@ -236,7 +299,9 @@ def main():
         for _ in range(steps):
             step()
             L.ptwm_mi355x_last_kernel_ms(0, ms)
-            kern.append(ms[0])
+            # [0]: entropy decode (fused with the merge on the huff_ilv route),
+            # [2]: every kernel of the call (exact route: decode + merge)
+            kern.append(ms[2] if wl.kernel == EXACT_ROUTE else ms[0])
         L.ptwm_mi355x_set_profiling(0, 0)
         kms = sum(kern) / len(kern)
         return ms_step, kms

@@ -126,6 +126,21 @@ int64_t ptwm_mi355x_encode_tensor_cuda(uint32_t chain, uint64_t in_dev_ptr, size
                                        size_t out_cap, uint8_t *plan_out, size_t plan_cap, size_t *plan_len_out,
                                        uint64_t *needed_out, uint32_t device_ordinal);
 
+/* Tensor-level encode into the reference's own plane formats: the tensor is
+ * split by `chain`, and plane p is coded with plane_codecs[p] (wire id 0x0000
+ * Identity, 0x0001 Huffman, 0x0003 rANS), in chunks of chunk_size bytes with
+ * the reference's chunk frames and chunk table (compressor.rs:316-381) when
+ * chunk_size > 0, else as one payload.  Every payload is byte-identical to
+ * the reference encoder's (codecs/huffman.rs:37-87, codecs/rans.rs:38-94).
+ * Planes start at 256-byte boundaries of out_dev (256-byte aligned; in_dev
+ * 16-byte aligned).  Writes the PTMD v1 plan to plan_out (-2 with
+ * *plan_len_out = needed size when plan_cap is too small); returns the bytes
+ * used in out_dev, or -2 with *needed_out when out_cap is too small. */
+int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t *plane_codecs, uint32_t n_codecs,
+                                           uint32_t chunk_size, uint64_t in_dev_ptr, size_t in_len,
+                                           uint64_t out_dev_ptr, size_t out_cap, uint8_t *plan_out, size_t plan_cap,
+                                           size_t *plan_len_out, uint64_t *needed_out, uint32_t device_ordinal);
+
 /* Canonical Huffman code lengths the reference encoder assigns to a 256-bin
  * histogram (entropy/huffman/tree.rs:19-85 with the 11-bit limit of
  * :212-242), computed on the host.  Returns 0, or -1 for an all-zero

@@ -155,6 +155,60 @@ def encode_tensor_cuda(chain: int, src, out, device_ordinal: int = 0) -> tuple[i
     return rc, bytes(plan_buf[: plan_len.value])
 
 
+def encode_tensor_ref_cuda(chain: int, plane_codecs, chunk_size: int, src, out,
+                           device_ordinal: int = 0) -> tuple[int, bytes]:
+    """Tensor-level GPU encode into the reference's plane formats (library
+    addition): split by ``chain``; plane p coded with ``plane_codecs[p]``
+    (wire ids 0 Identity, 1 Huffman, 3 rANS), chunked at ``chunk_size``
+    bytes (0: one payload per plane).  Returns (bytes used in ``out``, PTMD
+    decode plan)."""
+    L = lib()
+    stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
+    ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)
+    op, ol = _dev_ptr_len(out, "out", device_ordinal, stream, True, _both_torch(src, out))
+    codecs = (C.c_uint16 * len(plane_codecs))(*plane_codecs)
+    plan_len = C.c_size_t(0)
+    needed = C.c_uint64(0)
+    cap = 4096
+    while True:
+        plan_buf = (C.c_uint8 * cap)()
+        rc = L.ptwm_mi355x_encode_tensor_ref_cuda(chain, codecs, len(plane_codecs), chunk_size, ip, il, op, ol,
+                                                  plan_buf, cap, C.byref(plan_len), C.byref(needed), device_ordinal)
+        if rc == -2 and plan_len.value > cap:
+            cap = plan_len.value
+            continue
+        break
+    if rc == -2:
+        err = NativeError(rc, f"encode_tensor_ref_cuda: needs {needed.value} bytes")
+        err.needed = needed.value
+        raise err
+    check(rc, "encode_tensor_ref_cuda")
+    return rc, bytes(plan_buf[: plan_len.value])
+
+
+def plane_crc32_cuda(chain: int, src, device_ordinal: int = 0) -> list[int]:
+    """CRC-32 (crc32fast::hash) of every plane of the device tensor ``src``
+    split by ``chain`` (library addition; the per-plane checksum of
+    container.rs:2154-2159)."""
+    L = lib()
+    stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
+    ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)
+    out = (C.c_uint32 * 4)()
+    n = check(L.ptwm_mi355x_plane_crc32_cuda(chain, ip, il, out, 4, device_ordinal), "plane_crc32_cuda")
+    return [int(out[i]) for i in range(n)]
+
+
+def xxh64_cuda(src, device_ordinal: int = 0) -> int:
+    """XXH64 (seed 0) of the device bytes ``src`` (library addition; the
+    tensor payload hash of container.rs:2185-2194)."""
+    L = lib()
+    stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
+    ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)
+    h = C.c_uint64(0)
+    check(L.ptwm_mi355x_xxh64_cuda(ip, il, C.byref(h), device_ordinal), "xxh64_cuda")
+    return int(h.value)
+
+
 def split_cuda(chain: int, src, planes, device_ordinal: int = 0) -> int:
     """Forward chain on device (library addition)."""
     L = lib()

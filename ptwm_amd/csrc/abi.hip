@@ -10,6 +10,7 @@
 
 #include "../../include/ptwm_mi355x.h"
 #include "ilv_host.h"
+#include "ref_encode.h"
 #include "runtime.h"
 
 namespace ptwm {
@@ -220,6 +221,33 @@ int64_t ptwm_plane_codec_v1_encode_cuda(uint8_t state_format_version, const uint
   if (!lookup_codec(codec_id_ptr, codec_id_len, codec)) return kUnsupported;
   if (state_len != 0) return kInvalidInput;
   if ((in_len && !in_dev_ptr) || (out_cap && !out_dev_ptr)) return kInvalidInput;
+  if (codec == kCodecHuffman || codec == kCodecRans || codec == kCodecIdentity) {
+    // the reference's payloads, byte-identical to its encoder
+    DeviceScope ds(device_ordinal);
+    if (!ds.ok) return kInvalidInput;
+    if (codec == kCodecIdentity) {  // codecs/identity.rs: payload = plane
+      if (in_len > out_cap) {
+        if (needed_out) *needed_out = in_len;
+        return kBufferTooSmall;
+      }
+      if (in_len) {
+        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(out_dev_ptr), reinterpret_cast<const void*>(in_dev_ptr),
+                                    in_len, hipMemcpyDeviceToDevice, ds.ctx->stream));
+        PTWM_HIP_TRY(hipStreamSynchronize(ds.ctx->stream));
+      }
+      return (int64_t)in_len;
+    }
+    RefEncoder enc;
+    std::vector<uint64_t> len;
+    int64_t rc = enc.plan(*ds.ctx, {RefJob{in_dev_ptr, in_len, codec}}, len);
+    if (rc < 0) return rc;
+    if (len[0] > out_cap) {
+      if (needed_out) *needed_out = len[0];
+      return kBufferTooSmall;
+    }
+    rc = enc.write(*ds.ctx, {out_dev_ptr});
+    return rc < 0 ? rc : (int64_t)len[0];
+  }
   if (codec != kCodecHuffIlv) return kUnsupported;
   if ((in_dev_ptr & 15u) || (out_dev_ptr & 3u)) return kInvalidInput;
   DeviceScope ds(device_ordinal);
@@ -401,6 +429,113 @@ int64_t ptwm_mi355x_encode_tensor_cuda(uint32_t chain, uint64_t in_dev_ptr, size
   }
   *plan_len_out = (size_t)(o - plan_out);
   return rc;
+}
+
+int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane_codecs, uint32_t n_codecs,
+                                           uint32_t chunk_size, uint64_t in_dev_ptr, size_t in_len,
+                                           uint64_t out_dev_ptr, size_t out_cap, uint8_t* plan_out, size_t plan_cap,
+                                           size_t* plan_len_out, uint64_t* needed_out, uint32_t device_ordinal) {
+  const int np = chain_planes(chain);
+  if (np < 0 || !plan_out || !plan_len_out || !plane_codecs || n_codecs != (uint32_t)np) return kInvalidInput;
+  for (int p = 0; p < np; ++p)
+    if (plane_codecs[p] != kCodecIdentity && plane_codecs[p] != kCodecHuffman && plane_codecs[p] != kCodecRans)
+      return kUnsupported;
+  const uint64_t ratio = (uint64_t)chain_ratio(chain);
+  if (in_len % ratio || (in_dev_ptr & 15u) || (out_dev_ptr & 255u)) return kInvalidInput;
+  const uint64_t plane_len = in_len / ratio;
+  // chunks: plane.chunks(chunk_size) (compressor.rs:316-381); 0 = unchunked
+  const uint64_t cs = chunk_size ? chunk_size : (plane_len ? plane_len : 1);
+  const uint64_t nch = chunk_size ? (plane_len == 0 ? 1 : (plane_len + cs - 1) / cs) : 1;
+  if (nch > 0xFFFFFFFFull) return kInvalidInput;
+  const size_t plan_len = 12 + 20 + (size_t)np * (32 + (chunk_size ? 8 * nch : 0));
+  if (plan_cap < plan_len) {
+    *plan_len_out = plan_len;
+    return kBufferTooSmall;
+  }
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  DevCtx& ctx = *ds.ctx;
+  const uint64_t stride = (plane_len + 255) / 256 * 256;
+  PTWM_HIP_TRY(ctx.enc_split.ensure(stride * np + 256));
+  uint8_t* pl[4] = {};
+  for (int i = 0; i < np; ++i) pl[i] = static_cast<uint8_t*>(ctx.enc_split.ptr) + stride * i;
+  if (plane_len && launch_split(chain, reinterpret_cast<const uint8_t*>(in_dev_ptr), plane_len, pl, ctx.stream) !=
+                       hipSuccess)
+    return kInvalidInput;
+  // one job per coded chunk; Identity payloads are the bytes themselves
+  std::vector<RefJob> jobs;
+  std::vector<int> job_of(np * nch, -1);
+  for (int p = 0; p < np; ++p)
+    for (uint64_t k = 0; k < nch; ++k) {
+      const uint64_t a = k * cs, b = std::min(plane_len, a + cs);
+      if (plane_codecs[p] == kCodecIdentity) continue;
+      job_of[p * nch + k] = (int)jobs.size();
+      jobs.push_back(RefJob{reinterpret_cast<uint64_t>(pl[p]) + a, b - a, plane_codecs[p]});
+    }
+  RefEncoder enc;
+  std::vector<uint64_t> plen;
+  int64_t rc = enc.plan(ctx, jobs, plen);
+  if (rc < 0) return rc;
+  // layout: planes at 256-byte boundaries; a chunked plane is its frames
+  // [ver u8 = 0][state_len u32 = 0][payload] back to back
+  std::vector<uint64_t> dst(jobs.size(), 0), poff(np), plen_total(np);
+  std::vector<std::vector<std::pair<uint32_t, uint32_t>>> table(np);
+  std::vector<std::pair<uint64_t, std::vector<uint8_t>>> literal;
+  std::vector<RefCopyOp> copies;
+  uint64_t off = 0;
+  for (int p = 0; p < np; ++p) {
+    off = (off + 255) / 256 * 256;
+    poff[p] = off;
+    uint64_t q = 0;
+    for (uint64_t k = 0; k < nch; ++k) {
+      const uint64_t a = k * cs, b = std::min(plane_len, a + cs);
+      if (chunk_size) {
+        if (q > 0xFFFFFFFFull) return kInvalidInput;
+        table[p].emplace_back((uint32_t)q, (uint32_t)(b - a));
+        literal.emplace_back(out_dev_ptr + off + q, std::vector<uint8_t>(5, 0));
+        q += 5;
+      }
+      const int j = job_of[p * nch + k];
+      if (j >= 0) {
+        dst[j] = out_dev_ptr + off + q;
+        q += plen[j];
+      } else {
+        copies.push_back(RefCopyOp{reinterpret_cast<uint64_t>(pl[p]) + a, out_dev_ptr + off + q, b - a, ~0ull});
+        q += b - a;
+      }
+    }
+    plen_total[p] = q;
+    off += q;
+  }
+  if (off > out_cap) {
+    if (needed_out) *needed_out = off;
+    return kBufferTooSmall;
+  }
+  rc = enc.write(ctx, dst, literal, copies);
+  if (rc < 0) return rc;
+  uint8_t* o = plan_out;
+  auto put = [&](const void* v, size_t k) {
+    std::memcpy(o, v, k);
+    o += k;
+  };
+  const uint32_t magic = 0x444D5450u, ntens = 1;
+  const uint16_t ver = 1, flags = 0, tflags = 0;
+  const uint64_t zero64 = 0, out_len = in_len;
+  const uint8_t ch = (uint8_t)chain, npl = (uint8_t)np;
+  put(&magic, 4); put(&ver, 2); put(&flags, 2); put(&ntens, 4);
+  put(&zero64, 8); put(&out_len, 8); put(&ch, 1); put(&npl, 1); put(&tflags, 2);
+  for (int p = 0; p < np; ++p) {
+    const uint16_t codec = plane_codecs[p], pf = chunk_size ? 1 : 0;
+    const uint32_t n_ch = chunk_size ? (uint32_t)nch : 0;
+    put(&codec, 2); put(&pf, 2); put(&n_ch, 4);
+    put(&poff[p], 8); put(&plen_total[p], 8); put(&plane_len, 8);
+    for (const auto& e : table[p]) {
+      put(&e.first, 4);
+      put(&e.second, 4);
+    }
+  }
+  *plan_len_out = (size_t)(o - plan_out);
+  return (int64_t)off;
 }
 
 int64_t ptwm_mi355x_set_profiling(uint32_t device_ordinal, uint32_t on) {

@@ -1,0 +1,545 @@
+// ref_encode.hip -- GPU encoder for the reference's Huffman and rANS plane
+// payloads, byte-identical to the reference encoder.
+//
+// Payload framing: codecs/huffman.rs:37-87 and codecs/rans.rs:38-94
+// ([00] empty, [00]+raw when not beneficial, [01][orig_len u32][blob]);
+// blobs: entropy/huffman/compress.rs:9-103 (weights header, jump table,
+// four backward bitstreams over split_four segments) and
+// entropy/rans/compress.rs:128-260 (frequency header, jump table, four
+// streams [x_final u32][renorm bytes in decoder order]).
+//
+// One call encodes a batch of jobs (each one payload: a whole plane or one
+// chunk of a chunked plane):
+//   1. histogram per job (ref_hist_kernel);
+//   2. host: code tables per job (huffman_host.cpp: the reference tree,
+//      canonical codes and weights header; rANS: normalize_freqs and the
+//      EncSymbol reciprocal parameters of rans/compress.rs:35-122);
+//   3. Huffman: bits per segment (ref_huf_bits_kernel); rANS: each segment
+//      encoded by one lane into scratch (ref_rans_kernel; a segment's state
+//      chain is serial by construction, 64 segments run per wavefront);
+//   4. host: payload sizes, coded-or-raw decisions, output layout;
+//   5. Huffman segments packed in parallel (ref_huf_pack_kernel: every
+//      symbol's bit offset is a prefix sum of code lengths, so its final
+//      position in the backward stream is known), then headers, streams and
+//      raw fallbacks placed by one gather launch (ref_copy_kernel).
+#include "ref_encode.h"
+
+#include <algorithm>
+#include <cstring>
+
+#include "huffman_host.h"
+
+namespace ptwm {
+
+namespace {
+
+constexpr uint32_t kRansProbBits = 11;
+constexpr uint32_t kRansScale = 1u << kRansProbBits;
+constexpr uint32_t kRansL = 1u << 23;
+
+__device__ __forceinline__ uint8_t gbyte(uint64_t a) {
+  return *(const __attribute__((address_space(1))) uint8_t*)(uintptr_t)a;
+}
+
+// 256-bin histogram per job (blockIdx.y); any source alignment.
+__global__ void __launch_bounds__(256) ref_hist_kernel(const RefJobDev* __restrict__ jobs, uint32_t* __restrict__ hist) {
+  __shared__ uint32_t h[4][256];
+  const RefJobDev J = jobs[blockIdx.y];
+  const uint32_t t = threadIdx.x, wave = t >> 6;
+  for (uint32_t i = t; i < 1024; i += 256) (&h[0][0])[i] = 0;
+  __syncthreads();
+  const uint64_t head = J.n == 0 ? 0 : std::min<uint64_t>(J.n, (16 - (J.src & 15)) & 15);
+  const uint64_t nvec = (J.n - head) / 16;
+  const uint64_t stride = (uint64_t)gridDim.x * 256u;
+  const u32x4* v = reinterpret_cast<const u32x4*>(J.src + head);
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + t; i < nvec; i += stride) {
+    const u32x4 x = __builtin_nontemporal_load(v + i);
+    const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) atomicAdd(&h[wave][(xs[k] >> (8 * b)) & 0xFF], 1u);
+  }
+  if (blockIdx.x == 0) {
+    for (uint64_t i = t; i < head; i += 256) atomicAdd(&h[wave][gbyte(J.src + i)], 1u);
+    for (uint64_t i = head + nvec * 16 + t; i < J.n; i += 256) atomicAdd(&h[wave][gbyte(J.src + i)], 1u);
+  }
+  __syncthreads();
+  const uint32_t s = h[0][t] + h[1][t] + h[2][t] + h[3][t];
+  if (s) atomicAdd(&hist[256u * blockIdx.y + t], s);
+}
+
+// Huffman: total code bits of each segment.
+__global__ void __launch_bounds__(256) ref_huf_bits_kernel(const RefSegDev* __restrict__ segs,
+                                                           const uint32_t* __restrict__ codes,
+                                                           unsigned long long* __restrict__ seg_bits) {
+  __shared__ uint8_t len[256];
+  __shared__ unsigned long long part[4];
+  const RefSegDev S = segs[blockIdx.x];
+  const uint32_t t = threadIdx.x;
+  len[t] = (uint8_t)(codes[256u * S.table + t] >> 16);
+  __syncthreads();
+  unsigned long long bits = 0;
+  for (uint64_t i = t; i < S.n; i += 256) bits += len[gbyte(S.src + i)];
+  for (int d = 32; d >= 1; d >>= 1) bits += __shfl_down(bits, d, 64);
+  if ((t & 63u) == 0) part[t >> 6] = bits;
+  __syncthreads();
+  if (t == 0) seg_bits[blockIdx.x] = part[0] + part[1] + part[2] + part[3];
+}
+
+// Huffman: pack one segment's codes (bit-reversed canonical codes,
+// LSB-first, bitstream.rs:22-50) straight into their final byte order.  The
+// logical stream P (bit k = bit k % 8 of byte k / 8) is stored reversed
+// (S[m-1-i] = P[i]); in the segment's word-aligned scratch area of W words
+// whose last m bytes are S, logical word w is the byte-swapped word W-1-w.
+// The area must be zero; words shared by two threads are combined with OR.
+constexpr uint32_t kPackPerThread = 8;
+__global__ void __launch_bounds__(256) ref_huf_pack_kernel(const RefSegDev* __restrict__ segs,
+                                                           const uint32_t* __restrict__ codes,
+                                                           uint32_t* __restrict__ scratch) {
+  __shared__ uint32_t code[256];
+  __shared__ uint32_t wave_sum[4];
+  __shared__ unsigned long long s_base;
+  const RefSegDev S = segs[blockIdx.x];
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  code[t] = codes[256u * S.table + t];
+  if (t == 0) s_base = 0;
+  __syncthreads();
+  uint32_t* area = scratch + S.scratch_word;
+  const uint64_t W = S.words;
+  for (uint64_t pass = 0; pass < S.n; pass += 256ull * kPackPerThread) {
+    const uint64_t i0 = pass + (uint64_t)t * kPackPerThread;
+    uint32_t sym_code[kPackPerThread];
+    uint32_t bits = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kPackPerThread; ++k) {
+      const uint64_t i = i0 + k;
+      sym_code[k] = i < S.n ? code[gbyte(S.src + i)] : 0u;
+      bits += sym_code[k] >> 16;
+    }
+    // exclusive prefix of bits over the workgroup
+    uint32_t incl = bits;
+#pragma unroll
+    for (uint32_t d = 1; d < 64; d <<= 1) {
+      const uint32_t o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) wave_sum[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, pass_bits = 0;
+    for (uint32_t w = 0; w < 4; ++w) {
+      if (w < wave) before += wave_sum[w];
+      pass_bits += wave_sum[w];
+    }
+    const unsigned long long off = s_base + before + (incl - bits);
+    // pack: acc holds the bits from word (off >> 5) on
+    uint64_t w = off >> 5;
+    uint32_t fill = (uint32_t)(off & 31u);
+    uint64_t acc = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kPackPerThread; ++k) {
+      const uint32_t l = sym_code[k] >> 16;
+      acc |= (uint64_t)(sym_code[k] & 0xFFFFu) << fill;
+      fill += l;
+      if (fill >= 32) {
+        atomicOr(area + (W - 1 - w), __builtin_bswap32((uint32_t)acc));
+        acc >>= 32;
+        fill -= 32;
+        ++w;
+      }
+    }
+    if (fill) atomicOr(area + (W - 1 - w), __builtin_bswap32((uint32_t)acc));
+    __syncthreads();
+    if (t == 0) s_base += pass_bits;
+    __syncthreads();
+  }
+}
+
+// rANS: one lane encodes one segment backward (encode_stream_into,
+// rans/compress.rs:140-185) into its scratch area: [x_final u32 LE][renorm
+// bytes in emission order]; seg_len = 4 + renorm bytes.  Table entries per
+// symbol: {rcp, bias, cmpl | freq << 12 | shift << 24, 0}.
+__global__ void __launch_bounds__(64) ref_rans_kernel(const RefSegDev* __restrict__ segs, uint32_t n_segs,
+                                                      const uint4* __restrict__ tables, uint8_t* __restrict__ scratch,
+                                                      unsigned long long* __restrict__ seg_len) {
+  const uint32_t s = blockIdx.x * 64u + threadIdx.x;
+  if (s >= n_segs) return;
+  const RefSegDev S = segs[s];
+  const uint4* tab = tables + 256u * S.table;
+  uint8_t* out = scratch + S.scratch_byte;
+  uint32_t x = kRansL;
+  uint64_t nb = 4;
+  for (uint64_t k = S.n; k > 0; --k) {
+    const uint4 e = tab[gbyte(S.src + k - 1)];
+    const uint32_t freq = (e.z >> 12) & 0xFFFu;
+    if (freq == 0) {  // a symbol the table does not code: refuse (seg_len 0)
+      seg_len[s] = 0;
+      return;
+    }
+    const uint32_t max_state = freq << 20;  // ((RANS_L >> PROB_BITS) << 8) * freq
+    while (x >= max_state) {
+      out[nb++] = (uint8_t)(x & 0xFFu);
+      x >>= 8;
+    }
+    const uint32_t q = __umulhi(x, e.x) >> (e.z >> 24);
+    x = x + e.y + q * (e.z & 0xFFFu);
+  }
+  out[0] = (uint8_t)x;
+  out[1] = (uint8_t)(x >> 8);
+  out[2] = (uint8_t)(x >> 16);
+  out[3] = (uint8_t)(x >> 24);
+  seg_len[s] = nb;
+}
+
+// Byte copies of a batch of ranges: bytes [0, rev_from) forward, bytes
+// [rev_from, n) taken from the end of the source backward (the rANS renorm
+// bytes, emitted in the reverse of decoder order).
+__global__ void __launch_bounds__(256) ref_copy_kernel(const RefCopyOp* __restrict__ ops) {
+  const RefCopyOp op = ops[blockIdx.x];
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(op.src);
+  uint8_t* dst = reinterpret_cast<uint8_t*>(op.dst);
+  const uint64_t fwd = op.rev_from < op.n ? op.rev_from : op.n;
+  for (uint64_t i = threadIdx.x; i < fwd; i += 256) dst[i] = src[i];
+  for (uint64_t i = fwd + threadIdx.x; i < op.n; i += 256) dst[i] = src[op.n - 1 - (i - fwd)];
+}
+
+// ---- host restatements of the reference's table construction ----
+
+// normalize_freqs (rans/compress.rs:72-122): returns false when it fails.
+bool rans_normalize(const uint32_t raw[256], uint16_t f[256], uint16_t cum[256], int* max_sym_out) {
+  uint64_t total = 0;
+  for (int i = 0; i < 256; ++i) total += raw[i];
+  std::memset(f, 0, 512);
+  std::memset(cum, 0, 512);
+  if (total == 0) return false;
+  uint32_t assigned = 0;
+  int max_sym = 0, max_freq_sym = 0;
+  for (int i = 0; i < 256; ++i) {
+    if (raw[i] > 0) {
+      uint64_t v = ((uint64_t)raw[i] * kRansScale) / total;
+      if (v < 1) v = 1;
+      f[i] = (uint16_t)v;
+      assigned += f[i];
+      max_sym = i;
+      if (raw[i] > raw[max_freq_sym]) max_freq_sym = i;
+    }
+  }
+  if (assigned > kRansScale) {
+    const uint32_t excess = assigned - kRansScale;
+    if ((uint32_t)f[max_freq_sym] > excess) f[max_freq_sym] = (uint16_t)(f[max_freq_sym] - excess);
+    else return false;
+  } else if (assigned < kRansScale) {
+    f[max_freq_sym] = (uint16_t)(f[max_freq_sym] + (kRansScale - assigned));
+  }
+  uint16_t run = 0;
+  for (int i = 0; i <= max_sym; ++i) {
+    cum[i] = run;
+    run = (uint16_t)(run + f[i]);
+  }
+  *max_sym_out = max_sym;
+  return true;
+}
+
+// EncSymbol (rans/compress.rs:35-68) packed for ref_rans_kernel.
+void rans_encsym(uint32_t start, uint32_t freq, uint32_t out[4]) {
+  uint32_t rcp, bias, shift;
+  if (freq < 2) {
+    bias = start + kRansScale - 1;
+    rcp = 0xFFFFFFFFu;
+    shift = 0;
+  } else {
+    uint32_t sh = 0;
+    while (freq > (1u << sh)) ++sh;
+    rcp = (uint32_t)((((uint64_t)1 << (sh + 31)) + freq - 1) / freq);
+    bias = start;
+    shift = sh - 1;
+  }
+  out[0] = rcp;
+  out[1] = bias;
+  out[2] = (kRansScale - freq) | (freq << 12) | (shift << 24);
+  out[3] = 0;
+}
+
+void split_four(uint64_t len, uint64_t start[4], uint64_t n[4]) {
+  const uint64_t q = len / 4, r = len % 4;
+  uint64_t off = 0;
+  for (int i = 0; i < 4; ++i) {
+    start[i] = off;
+    n[i] = q + (i < (int)r ? 1 : 0);
+    off += n[i];
+  }
+}
+
+inline void put32(std::vector<uint8_t>& v, uint32_t x) {
+  for (int i = 0; i < 4; ++i) v.push_back((uint8_t)(x >> (8 * i)));
+}
+
+inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+int64_t RefEncoder::plan(DevCtx& ctx, const std::vector<RefJob>& jobs, std::vector<uint64_t>& payload_len) {
+  hipStream_t s = ctx.stream;
+  jobs_ = jobs;
+  const uint32_t nj = (uint32_t)jobs.size();
+  payload_len.assign(nj, 0);
+  info_.assign(nj, JobInfo{});
+  segs_.clear();
+  if (nj == 0) return kOk;
+  // ---- 1. histograms ----
+  std::vector<RefJobDev> jd(nj);
+  uint64_t max_n = 0;
+  for (uint32_t j = 0; j < nj; ++j) {
+    if (jobs[j].codec != kCodecHuffman && jobs[j].codec != kCodecRans) return kUnsupported;
+    jd[j] = RefJobDev{jobs[j].src, jobs[j].n};
+    max_n = std::max(max_n, jobs[j].n);
+  }
+  PTWM_HIP_TRY(ctx.ref_jobs.ensure(nj * sizeof(RefJobDev)));
+  PTWM_HIP_TRY(ctx.ref_hist.ensure((size_t)nj * 256 * sizeof(uint32_t)));
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.ref_jobs.ptr, jd.data(), nj * sizeof(RefJobDev), hipMemcpyHostToDevice, s));
+  PTWM_HIP_TRY(hipMemsetAsync(ctx.ref_hist.ptr, 0, (size_t)nj * 256 * sizeof(uint32_t), s));
+  uint64_t hb = (max_n / 16 + 255) / 256;
+  hb = std::max<uint64_t>(1, std::min<uint64_t>(hb, 256));
+  for (uint32_t j0 = 0; j0 < nj; j0 += 65535) {
+    const uint32_t cnt = std::min<uint32_t>(65535, nj - j0);
+    hipLaunchKernelGGL(ref_hist_kernel, dim3((uint32_t)hb, cnt), dim3(256), 0, s,
+                       static_cast<const RefJobDev*>(ctx.ref_jobs.ptr) + j0,
+                       static_cast<uint32_t*>(ctx.ref_hist.ptr) + 256ull * j0);
+    PTWM_HIP_TRY(hipGetLastError());
+  }
+  std::vector<uint32_t> hist((size_t)nj * 256);
+  PTWM_HIP_TRY(hipMemcpyAsync(hist.data(), ctx.ref_hist.ptr, hist.size() * 4, hipMemcpyDeviceToHost, s));
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  // ---- 2. tables; segments ----
+  huf_codes_.assign((size_t)nj * 256, 0);
+  rans_tab_.assign((size_t)nj * 256 * 4, 0);
+  uint64_t scratch_words = 0, rans_scratch = 0;
+  for (uint32_t j = 0; j < nj; ++j) {
+    JobInfo& I = info_[j];
+    const uint64_t n = jobs[j].n;
+    I.raw = true;
+    if (n == 0) continue;
+    const uint32_t* h = &hist[256ull * j];
+    if (jobs[j].codec == kCodecHuffman) {
+      uint8_t lengths[256];
+      uint16_t rev[256];
+      if (!huf_lengths_from_freqs(h, lengths) || !huf_canonical(lengths, rev)) continue;
+      uint8_t w[140];
+      const int wl = huf_encode_weights(lengths, w);
+      if (wl < 0) continue;
+      I.header.assign(w, w + wl);
+      for (int sy = 0; sy < 256; ++sy) huf_codes_[256ull * j + sy] = ((uint32_t)lengths[sy] << 16) | rev[sy];
+    } else {
+      uint16_t f[256], cum[256];
+      int max_sym = 0;
+      if (!rans_normalize(h, f, cum, &max_sym)) continue;
+      I.header.push_back((uint8_t)max_sym);
+      for (int i = 0; i <= max_sym; ++i) {
+        I.header.push_back((uint8_t)f[i]);
+        I.header.push_back((uint8_t)(f[i] >> 8));
+      }
+      for (int sy = 0; sy < 256; ++sy) rans_encsym(cum[sy], f[sy], &rans_tab_[(256ull * j + sy) * 4]);
+    }
+    I.raw = false;
+    uint64_t st[4], sn[4];
+    split_four(n, st, sn);
+    I.seg0 = (uint32_t)segs_.size();
+    for (int i = 0; i < 4; ++i) {
+      RefSegDev g{};
+      g.src = jobs[j].src + st[i];
+      g.n = sn[i];
+      g.table = j;
+      if (jobs[j].codec == kCodecRans) {
+        g.scratch_byte = rans_scratch;
+        rans_scratch = align_up(rans_scratch + 4 + 2 * sn[i] + 16, 16);
+      }
+      segs_.push_back(g);
+    }
+  }
+  const uint32_t ns = (uint32_t)segs_.size();
+  seg_len_.assign(ns, 0);
+  if (ns) {
+    PTWM_HIP_TRY(ctx.ref_segs.ensure(ns * sizeof(RefSegDev)));
+    PTWM_HIP_TRY(ctx.ref_seglen.ensure(ns * sizeof(unsigned long long)));
+    PTWM_HIP_TRY(ctx.ref_codes.ensure(huf_codes_.size() * 4));
+    PTWM_HIP_TRY(ctx.ref_rans_tab.ensure(rans_tab_.size() * 4));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.ref_segs.ptr, segs_.data(), ns * sizeof(RefSegDev), hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.ref_codes.ptr, huf_codes_.data(), huf_codes_.size() * 4, hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(
+        hipMemcpyAsync(ctx.ref_rans_tab.ptr, rans_tab_.data(), rans_tab_.size() * 4, hipMemcpyHostToDevice, s));
+    // ---- 3. Huffman bits per segment; rANS segments encoded ----
+    hipLaunchKernelGGL(ref_huf_bits_kernel, dim3(ns), dim3(256), 0, s, static_cast<const RefSegDev*>(ctx.ref_segs.ptr),
+                       static_cast<const uint32_t*>(ctx.ref_codes.ptr),
+                       static_cast<unsigned long long*>(ctx.ref_seglen.ptr));
+    PTWM_HIP_TRY(hipGetLastError());
+    std::vector<unsigned long long> bits(ns);
+    PTWM_HIP_TRY(hipMemcpyAsync(bits.data(), ctx.ref_seglen.ptr, ns * 8, hipMemcpyDeviceToHost, s));
+    // the rANS kernel gets the rANS segments only (a Huffman job's rANS
+    // table row is empty)
+    std::vector<RefSegDev> rsegs;
+    std::vector<uint32_t> ridx;
+    for (uint32_t g = 0; g < ns; ++g)
+      if (jobs[segs_[g].table].codec == kCodecRans) {
+        rsegs.push_back(segs_[g]);
+        ridx.push_back(g);
+      }
+    const uint32_t nr = (uint32_t)rsegs.size();
+    std::vector<unsigned long long> rlen(nr, 0);
+    if (nr) {
+      PTWM_HIP_TRY(ctx.ref_rans_scratch.ensure(rans_scratch));
+      PTWM_HIP_TRY(ctx.ref_rans_segs.ensure(nr * sizeof(RefSegDev)));
+      PTWM_HIP_TRY(ctx.ref_rans_len.ensure(nr * sizeof(unsigned long long)));
+      PTWM_HIP_TRY(
+          hipMemcpyAsync(ctx.ref_rans_segs.ptr, rsegs.data(), nr * sizeof(RefSegDev), hipMemcpyHostToDevice, s));
+      hipLaunchKernelGGL(ref_rans_kernel, dim3((nr + 63) / 64), dim3(64), 0, s,
+                         static_cast<const RefSegDev*>(ctx.ref_rans_segs.ptr), nr,
+                         static_cast<const uint4*>(ctx.ref_rans_tab.ptr),
+                         static_cast<uint8_t*>(ctx.ref_rans_scratch.ptr),
+                         static_cast<unsigned long long*>(ctx.ref_rans_len.ptr));
+      PTWM_HIP_TRY(hipGetLastError());
+      PTWM_HIP_TRY(hipMemcpyAsync(rlen.data(), ctx.ref_rans_len.ptr, nr * 8, hipMemcpyDeviceToHost, s));
+    }
+    PTWM_HIP_TRY(hipStreamSynchronize(s));
+    std::vector<unsigned long long> rlen_of(ns, 0);
+    for (uint32_t k = 0; k < nr; ++k) {
+      if (rlen[k] < 4) return kInternal;  // every rANS stream holds at least x_final
+      rlen_of[ridx[k]] = rlen[k];
+    }
+    for (uint32_t g = 0; g < ns; ++g) {
+      const RefJob& J = jobs[segs_[g].table];
+      if (J.codec == kCodecHuffman) {
+        seg_len_[g] = (bits[g] + 7) / 8;
+        segs_[g].words = (bits[g] + 31) / 32;
+        segs_[g].scratch_word = scratch_words;
+        scratch_words += segs_[g].words + 1;
+      } else {
+        seg_len_[g] = rlen_of[g];
+      }
+    }
+  }
+  pack_words_ = scratch_words;
+  // ---- 4. sizes and coded-or-raw (codecs/huffman.rs:50-87, codecs/rans.rs:50-94) ----
+  for (uint32_t j = 0; j < nj; ++j) {
+    JobInfo& I = info_[j];
+    const uint64_t n = jobs[j].n;
+    if (n == 0) {
+      payload_len[j] = 1;  // [00]
+      continue;
+    }
+    if (!I.raw) {
+      uint64_t blob = I.header.size() + 16;
+      for (int i = 0; i < 4; ++i) blob += seg_len_[I.seg0 + i];
+      bool coded = blob < n && n <= 0xFFFFFFFFull;  // NotBeneficial when blob >= len (compress.rs:72-75)
+      for (int i = 0; i < 4; ++i) coded = coded && seg_len_[I.seg0 + i] <= 0xFFFFFFFFull;
+      // length_prefix::accepted (codecs/length_prefix.rs:15-56), rANS only
+      if (coded && jobs[j].codec == kCodecRans) coded = n <= (1ull << 30) || n <= blob * 64;
+      if (coded) {
+        I.blob = blob;
+        payload_len[j] = 5 + blob;
+        continue;
+      }
+      I.raw = true;
+    }
+    payload_len[j] = 1 + n;  // [00] + plane
+  }
+  return kOk;
+}
+
+int64_t RefEncoder::write(DevCtx& ctx, const std::vector<uint64_t>& dst,
+                          const std::vector<std::pair<uint64_t, std::vector<uint8_t>>>& literal,
+                          const std::vector<RefCopyOp>& copies) {
+  hipStream_t s = ctx.stream;
+  const uint32_t nj = (uint32_t)jobs_.size();
+  if (dst.size() != nj) return kInternal;
+  // headers: [tag][orig_len][table header][jump table] per coded job, [00] per raw job
+  std::vector<uint8_t> hdr;
+  std::vector<uint64_t> hdr_off(nj + 1, 0);
+  for (uint32_t j = 0; j < nj; ++j) {
+    const JobInfo& I = info_[j];
+    hdr_off[j] = hdr.size();
+    if (I.raw) {
+      hdr.push_back(0);
+      continue;
+    }
+    hdr.push_back(1);
+    put32(hdr, (uint32_t)jobs_[j].n);
+    hdr.insert(hdr.end(), I.header.begin(), I.header.end());
+    for (int i = 0; i < 4; ++i) put32(hdr, (uint32_t)seg_len_[I.seg0 + i]);
+  }
+  hdr_off[nj] = hdr.size();
+  std::vector<uint64_t> lit_off;
+  for (const auto& l : literal) {
+    lit_off.push_back(hdr.size());
+    hdr.insert(hdr.end(), l.second.begin(), l.second.end());
+  }
+  PTWM_HIP_TRY(ctx.ref_hdr.ensure(hdr.size() + 16));
+  if (!hdr.empty()) PTWM_HIP_TRY(hipMemcpyAsync(ctx.ref_hdr.ptr, hdr.data(), hdr.size(), hipMemcpyHostToDevice, s));
+  // Huffman segments packed into zeroed word scratch
+  if (pack_words_) {
+    PTWM_HIP_TRY(ctx.ref_pack.ensure(pack_words_ * 4));
+    PTWM_HIP_TRY(hipMemsetAsync(ctx.ref_pack.ptr, 0, pack_words_ * 4, s));
+    std::vector<RefSegDev> hs;
+    for (const RefSegDev& g : segs_)
+      if (jobs_[g.table].codec == kCodecHuffman && !info_[g.table].raw && g.n) hs.push_back(g);
+    if (!hs.empty()) {
+      PTWM_HIP_TRY(ctx.ref_segs.ensure(hs.size() * sizeof(RefSegDev)));
+      PTWM_HIP_TRY(hipMemcpyAsync(ctx.ref_segs.ptr, hs.data(), hs.size() * sizeof(RefSegDev), hipMemcpyHostToDevice,
+                                  s));
+      hipLaunchKernelGGL(ref_huf_pack_kernel, dim3((uint32_t)hs.size()), dim3(256), 0, s,
+                         static_cast<const RefSegDev*>(ctx.ref_segs.ptr),
+                         static_cast<const uint32_t*>(ctx.ref_codes.ptr), static_cast<uint32_t*>(ctx.ref_pack.ptr));
+      PTWM_HIP_TRY(hipGetLastError());
+    }
+  }
+  // gather: headers, streams, raw planes
+  std::vector<RefCopyOp> ops;
+  const uint64_t hdr_dev = reinterpret_cast<uint64_t>(ctx.ref_hdr.ptr);
+  for (size_t k = 0; k < literal.size(); ++k)
+    if (!literal[k].second.empty())
+      ops.push_back(RefCopyOp{hdr_dev + lit_off[k], literal[k].first, literal[k].second.size(), ~0ull});
+  for (const RefCopyOp& c : copies) {
+    // forward copies in pieces of at most 1 MiB, one workgroup each
+    for (uint64_t o = 0; o < c.n; o += (1ull << 20))
+      ops.push_back(RefCopyOp{c.src + o, c.dst + o, std::min<uint64_t>(1ull << 20, c.n - o), ~0ull});
+  }
+  for (uint32_t j = 0; j < nj; ++j) {
+    const JobInfo& I = info_[j];
+    const uint64_t hl = hdr_off[j + 1] - hdr_off[j];
+    ops.push_back(RefCopyOp{hdr_dev + hdr_off[j], dst[j], hl, ~0ull});
+    if (I.raw) {
+      for (uint64_t o = 0; o < jobs_[j].n; o += (1ull << 20))
+        ops.push_back(RefCopyOp{jobs_[j].src + o, dst[j] + 1 + o, std::min<uint64_t>(1ull << 20, jobs_[j].n - o), ~0ull});
+      continue;
+    }
+    uint64_t o = dst[j] + hl;
+    for (int i = 0; i < 4; ++i) {
+      const RefSegDev& g = segs_[I.seg0 + i];
+      const uint64_t m = seg_len_[I.seg0 + i];
+      if (m) {
+        if (jobs_[j].codec == kCodecHuffman) {
+          // the stream is the last m bytes of the segment's word area
+          const uint64_t area = reinterpret_cast<uint64_t>(ctx.ref_pack.ptr) + 4 * g.scratch_word;
+          ops.push_back(RefCopyOp{area + 4 * g.words - m, o, m, ~0ull});
+        } else {
+          const uint64_t area = reinterpret_cast<uint64_t>(ctx.ref_rans_scratch.ptr) + g.scratch_byte;
+          ops.push_back(RefCopyOp{area, o, m, 4});
+        }
+      }
+      o += m;
+    }
+  }
+  if (!ops.empty()) {
+    PTWM_HIP_TRY(ctx.ref_ops.ensure(ops.size() * sizeof(RefCopyOp)));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.ref_ops.ptr, ops.data(), ops.size() * sizeof(RefCopyOp), hipMemcpyHostToDevice, s));
+    for (size_t k0 = 0; k0 < ops.size(); k0 += 65535) {
+      const uint32_t cnt = (uint32_t)std::min<size_t>(65535, ops.size() - k0);
+      hipLaunchKernelGGL(ref_copy_kernel, dim3(cnt), dim3(256), 0, s,
+                         static_cast<const RefCopyOp*>(ctx.ref_ops.ptr) + k0);
+      PTWM_HIP_TRY(hipGetLastError());
+    }
+  }
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  return kOk;
+}
+
+}  // namespace ptwm

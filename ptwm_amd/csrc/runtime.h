@@ -42,6 +42,9 @@ struct DevCtx {
   // huff_ilv encoder / decoder scratch
   DeviceBuffer enc_planes, enc_hist, enc_codes, enc_blocks, enc_lane_words, enc_block_bytes;
   DeviceBuffer ilv_args, ilv_realign;
+  // reference-format (Huffman / rANS) encoder scratch
+  DeviceBuffer ref_jobs, ref_hist, ref_segs, ref_seglen, ref_codes, ref_rans_tab, ref_rans_segs, ref_rans_scratch,
+      ref_rans_len, ref_hdr, ref_pack, ref_ops;
   PinnedBuffer h_enc, h_ilv;
   int cu_count = 0;  // compute units of the device (0: not queried yet)
   std::map<uint64_t, int> ilv_occupancy;  // (chain, slots, stage words) -> workgroups per CU

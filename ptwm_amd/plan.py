@@ -4,11 +4,14 @@ A plan lists tensors the way the container stores them
 (crates/ptwm-core/src/container.rs:1795-2196): per tensor its chain and, per
 plane, the codec wire id, the payload's offset and length in the input
 buffer, the decoded plane length, an optional CRC32 and the chunk table
-(plane_record.rs:16-20: ``(offset_in_payload u32, decoded_size u32)``).
+(plane_record.rs:16-20: ``(offset_in_payload u32, decoded_size u32)``), and
+per tensor an optional payload hash (container.rs:2185-2194: xxh64, seed 0,
+of the restored bytes).
 Binary layout (little endian), "PTMD" version 1:
 
     u32 magic 0x444D5450 | u16 version=1 | u16 flags=0 | u32 n_tensors
-    tensor: u64 out_offset | u64 out_len | u8 chain | u8 n_planes | u16 flags (bit0 crc)
+    tensor: u64 out_offset | u64 out_len | u8 chain | u8 n_planes | u16 flags (bit0 crc, bit1 hash)
+            | [u64 xxh64 (seed 0) of the restored tensor if hash flag]
       plane: u16 codec | u16 flags (bit0 chunked) | u32 n_chunks
              | u64 payload_offset | u64 payload_len | u64 plane_len
              | [u32 crc32 if tensor crc flag] | n_chunks x (u32 offset, u32 size)
@@ -45,13 +48,17 @@ class TensorPlan:
     out_offset: int
     out_len: int
     planes: list[PlanePlan] = field(default_factory=list)
+    xxh64: int | None = None
 
 
 def encode_plan(tensors: list[TensorPlan]) -> bytes:
     out = bytearray(struct.pack("<IHHI", MAGIC, 1, 0, len(tensors)))
     for t in tensors:
         has_crc = any(p.crc32 is not None for p in t.planes)
-        out += struct.pack("<QQBBH", t.out_offset, t.out_len, t.chain, len(t.planes), 1 if has_crc else 0)
+        tflags = (1 if has_crc else 0) | (2 if t.xxh64 is not None else 0)
+        out += struct.pack("<QQBBH", t.out_offset, t.out_len, t.chain, len(t.planes), tflags)
+        if t.xxh64 is not None:
+            out += struct.pack("<Q", t.xxh64)
         for p in t.planes:
             ch = p.chunks or []
             out += struct.pack("<HHIQQQ", p.codec, 1 if p.chunks is not None else 0, len(ch),
@@ -73,6 +80,9 @@ def decode_plan(buf: bytes) -> list[TensorPlan]:
         off, ln, chain, np_, tfl = struct.unpack_from("<QQBBH", buf, o)
         o += 20
         t = TensorPlan(chain, off, ln)
+        if tfl & 2:
+            (t.xxh64,) = struct.unpack_from("<Q", buf, o)
+            o += 8
         for _ in range(np_):
             codec, pfl, nch, po, pl, plen = struct.unpack_from("<HHIQQQ", buf, o)
             o += 32

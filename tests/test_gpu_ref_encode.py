@@ -1,0 +1,145 @@
+"""GPU encode of the reference's plane formats against the CPU oracle.
+
+The oracle's encoder restates the reference encoder (tree.rs, weights.rs,
+bitstream.rs, huffman/compress.rs, rans/compress.rs, codecs/*.rs,
+compressor.rs chunk frames); GPU output must equal it byte for byte, so
+GPU-encoded streams decode through the reference CPU decoder.  Tensor-level
+encodes of the BASELINE configs' shapes are also decoded again on the GPU
+(exact route) and checked against the input.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from ptwm_amd import api, ids, plan
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+SEL = ids.PLANE_CODEC_LABEL
+CODEC_NAME = {O.CODEC_IDENTITY: "identity", O.CODEC_HUFFMAN: "huffman", O.CODEC_RANS: "rans"}
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def dev(b: bytes, offset: int = 0):
+    """Device copy of b starting `offset` bytes into a fresh allocation."""
+    a = np.frombuffer(bytes(b), np.uint8)
+    t = torch.zeros(len(a) + offset + 16, dtype=torch.uint8, device="cuda:0")
+    if len(a):
+        t[offset: offset + len(a)].copy_(torch.from_numpy(a.copy()))
+    return t[offset: offset + len(a)]
+
+
+def host(t) -> bytes:
+    torch.cuda.synchronize()
+    return t.cpu().numpy().tobytes()
+
+
+def cases():
+    rng = np.random.default_rng(17)
+    yield "empty", b""
+    yield "one", b"\x07"
+    for n in (2, 3, 4, 5, 7, 8, 17, 65):
+        yield f"skew{n}", bytes(rng.geometric(0.5, n).clip(0, 255).astype(np.uint8))
+    yield "single", bytes([42]) * 1024
+    yield "two", bytes([0] * 3000 + [1] * 1000)
+    yield "uniform", bytes(range(256)) * 16                      # not beneficial -> raw
+    yield "geo", bytes(rng.geometric(0.25, 100_003).clip(0, 255).astype(np.uint8))
+    f = np.zeros(256, np.int64)
+    a, b = 1, 1
+    for i in range(24):                                           # deep tree: 11-bit limit
+        f[i] = a
+        a, b = b, a + b
+    yield "fib", bytes(np.repeat(np.arange(24), f[:24]).astype(np.uint8)[rng.permutation(int(f.sum()))])
+    w = (torch.randn(512 * 1024, generator=torch.Generator().manual_seed(1)) * 0.02).to(torch.bfloat16)
+    yield "bf16exp", O.chain_forward(O.CHAIN_IEEE16_SPLIT2, w.view(torch.uint8).numpy().tobytes())[1]
+    yield "low2mb", bytes(np.where(rng.random(2 << 20) < 0.97, 3, rng.integers(0, 8, 2 << 20)).astype(np.uint8))
+
+
+@pytest.mark.parametrize("codec", [O.CODEC_HUFFMAN, O.CODEC_RANS, O.CODEC_IDENTITY],
+                         ids=["huffman", "rans", "identity"])
+def test_plane_encode_matches_reference_bytes(codec):
+    for k, (name, src) in enumerate(cases()):
+        note(f"ref encode {CODEC_NAME[codec]} {name} n={len(src)}")
+        s = dev(src, offset=k % 13)                                # any source alignment
+        out = torch.zeros(2 * len(src) + 4096, dtype=torch.uint8, device="cuda:0")
+        n = api.plane_codec_encode_cuda(SEL, CODEC_NAME[codec], b"", s, out, 0)
+        want = O.codec_encode(codec, src)
+        got = host(out)[:n]
+        assert got == want, name
+        # and the reference decoder (oracle restatement) restores it
+        assert O.codec_decode(codec, got, len(src)) == src
+
+
+def test_plane_encode_buffer_too_small_reports_needed():
+    src = bytes(np.random.default_rng(3).geometric(0.3, 50_000).clip(0, 255).astype(np.uint8))
+    want = O.codec_encode(O.CODEC_HUFFMAN, src)
+    s = dev(src)
+    out = torch.zeros(len(want) - 1, dtype=torch.uint8, device="cuda:0")
+    with pytest.raises(Exception) as ei:
+        api.plane_codec_encode_cuda(SEL, "huffman", b"", s, out, 0)
+    assert getattr(ei.value, "rc", None) == -2 and ei.value.needed == len(want)
+
+
+def bf16(shape, seed):
+    return (torch.randn(*shape, generator=torch.Generator().manual_seed(seed)) * 0.02).to(torch.bfloat16)
+
+
+def c2_fp32(rows, cols, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(rows, cols, generator=g) * 0.02
+    m = torch.rand(rows, cols, generator=g) < 0.01
+    w[m] *= 50
+    return w
+
+
+def c3_fp8(rows, cols, seed):
+    x = torch.randn(rows, cols, generator=torch.Generator().manual_seed(seed))
+    return (x / x.abs().amax(1, keepdim=True) * 448).to(torch.float8_e4m3fn)
+
+
+H, R, I = O.CODEC_HUFFMAN, O.CODEC_RANS, O.CODEC_IDENTITY
+TENSORS = [
+    # config 1: bf16 1024x1024, Huffman on each plane, unchunked
+    ("c1-bf16", plan.CHAIN_IEEE16_SPLIT2, lambda: bf16((1024, 1024), 1).view(torch.uint8), [H, H], 0),
+    # config 2 (a quarter of its rows): fp32 with 1% outliers, rANS exponent, Huffman mantissas, 256 KiB chunks
+    ("c2-fp32", plan.CHAIN_IEEE32_SPLIT4, lambda: c2_fp32(1024, 4096, 2).view(torch.uint8), [H, H, H, R], 262144),
+    # config 3 (an eighth of its rows), Huffman and rANS
+    ("c3-fp8-huf", plan.CHAIN_E4M3_NIBBLE, lambda: c3_fp8(1024, 8192, 3).view(torch.uint8), [H, H], 0),
+    ("c3-fp8-rans", plan.CHAIN_E4M3_NIBBLE, lambda: c3_fp8(1024, 8192, 3).view(torch.uint8), [R, R], 0),
+    # config 5 weights: nibble split of near-uniform FP4 codes, chunked
+    ("c5-mxfp4", plan.CHAIN_NIBBLE_SPLIT,
+     lambda: torch.from_numpy(np.random.default_rng(5).integers(0, 256, 14336 * 64).astype(np.uint8)), [H, R], 1 << 20),
+    ("identity-chunked", plan.CHAIN_IEEE16_SPLIT2, lambda: bf16((300, 777), 6).view(torch.uint8), [I, H], 100_000),
+]
+
+
+@pytest.mark.parametrize("name,chain,make,codecs,chunk", TENSORS, ids=[t[0] for t in TENSORS])
+def test_tensor_ref_encode_matches_reference_and_decodes(name, chain, make, codecs, chunk):
+    note(f"tensor ref encode {name}")
+    data = make().contiguous().numpy().tobytes()
+    src = dev(data)
+    out = torch.zeros(2 * len(data) + (1 << 20), dtype=torch.uint8, device="cuda:0")
+    used, st = api.encode_tensor_ref_cuda(chain, codecs, chunk, src, out, 0)
+    blob = host(out[:used])
+    t = plan.decode_plan(st)[0]
+    planes = O.chain_forward(chain, data)
+    for p, pp in enumerate(t.planes):
+        payload = blob[pp.payload_offset: pp.payload_offset + pp.payload_len]
+        if chunk:
+            want, ent = O.encode_plane_chunked(codecs[p], planes[p], chunk)
+            assert [tuple(map(int, e)) for e in ent] == [tuple(c) for c in pp.chunks], (name, p)
+        else:
+            want = O.codec_encode(codecs[p], planes[p])
+        assert payload == want, (name, p)
+    # GPU decode of the GPU-encoded reference streams (exact route)
+    restored = torch.zeros(len(data), dtype=torch.uint8, device="cuda:0")
+    n = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, st,
+                                                  out[:used], restored, 0)
+    assert n == len(data) and host(restored) == data
