@@ -141,6 +141,19 @@ int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t *plane
                                            uint64_t out_dev_ptr, size_t out_cap, uint8_t *plan_out, size_t plan_cap,
                                            size_t *plan_len_out, uint64_t *needed_out, uint32_t device_ordinal);
 
+/* CRC-32/ISO-HDLC of every plane of a device tensor: the tensor at in_dev is
+ * split by `chain` (any alignment) and crc_out[p] receives crc32fast::hash of
+ * plane p, the checksum the reference stores per plane record and verifies
+ * at container.rs:2154-2159.  Returns the number of planes (n_out must be at
+ * least that). */
+int64_t ptwm_mi355x_plane_crc32_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, uint32_t *crc_out,
+                                     uint32_t n_out, uint32_t device_ordinal);
+
+/* XXH64 with seed 0 of in_len device bytes (any alignment): the tensor
+ * payload hash of container.rs:2185-2194 and compact.rs:441-445.  Serial per
+ * buffer by the hash's definition.  Returns 0. */
+int64_t ptwm_mi355x_xxh64_cuda(uint64_t in_dev_ptr, size_t in_len, uint64_t *hash_out, uint32_t device_ordinal);
+
 /* Canonical Huffman code lengths the reference encoder assigns to a 256-bin
  * histogram (entropy/huffman/tree.rs:19-85 with the 11-bit limit of
  * :212-242), computed on the host.  Returns 0, or -1 for an all-zero

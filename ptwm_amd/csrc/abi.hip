@@ -10,6 +10,7 @@
 
 #include "../../include/ptwm_mi355x.h"
 #include "ilv_host.h"
+#include "integrity.h"
 #include "ref_encode.h"
 #include "runtime.h"
 
@@ -536,6 +537,64 @@ int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane
   }
   *plan_len_out = (size_t)(o - plan_out);
   return (int64_t)off;
+}
+
+int64_t ptwm_mi355x_plane_crc32_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, uint32_t* crc_out,
+                                     uint32_t n_out, uint32_t device_ordinal) {
+  const int np = chain_planes(chain);
+  if (np < 0 || !crc_out || n_out < (uint32_t)np) return kInvalidInput;
+  const uint64_t ratio = (uint64_t)chain_ratio(chain);
+  if (in_len % ratio || (in_len && !in_dev_ptr)) return kInvalidInput;
+  const uint64_t n = in_len / ratio;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  DevCtx& ctx = *ds.ctx;
+  uint64_t src = in_dev_ptr;
+  if (n && (src & 15u)) {  // the kernels read dwordx4: realign into staging
+    PTWM_HIP_TRY(ctx.stage_in.ensure(in_len + 16));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.stage_in.ptr, reinterpret_cast<const void*>(src), in_len,
+                                hipMemcpyDeviceToDevice, ctx.stream));
+    src = reinterpret_cast<uint64_t>(ctx.stage_in.ptr);
+  }
+  std::vector<CrcTask> tasks;
+  if (crc_chain_supported(chain)) {
+    tasks.push_back(CrcTask{src, n, chain});
+  } else {  // nibble chains: forward chain into plane scratch, then each plane
+    const uint64_t stride = (n + 255) / 256 * 256;
+    PTWM_HIP_TRY(ctx.enc_split.ensure(stride * np + 256));
+    uint8_t* pl[4] = {};
+    for (int i = 0; i < np; ++i) {
+      pl[i] = static_cast<uint8_t*>(ctx.enc_split.ptr) + stride * i;
+      tasks.push_back(CrcTask{reinterpret_cast<uint64_t>(pl[i]), n, kChainPassthrough});
+    }
+    if (n && launch_split(chain, reinterpret_cast<const uint8_t*>(src), n, pl, ctx.stream) != hipSuccess)
+      return kInvalidInput;
+  }
+  std::vector<uint32_t> crcs;
+  const int64_t rc = crc32_planes(ctx, tasks, crcs);
+  if (rc != kOk) return rc;
+  if (crcs.size() != (size_t)np) return kInternal;
+  for (int i = 0; i < np; ++i) crc_out[i] = crcs[i];
+  return np;
+}
+
+int64_t ptwm_mi355x_xxh64_cuda(uint64_t in_dev_ptr, size_t in_len, uint64_t* hash_out, uint32_t device_ordinal) {
+  if (!hash_out || (in_len && !in_dev_ptr)) return kInvalidInput;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  DevCtx& ctx = *ds.ctx;
+  uint64_t src = in_dev_ptr;
+  if (in_len && (src & 15u)) {
+    PTWM_HIP_TRY(ctx.stage_in.ensure(in_len + 16));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.stage_in.ptr, reinterpret_cast<const void*>(src), in_len,
+                                hipMemcpyDeviceToDevice, ctx.stream));
+    src = reinterpret_cast<uint64_t>(ctx.stage_in.ptr);
+  }
+  std::vector<uint64_t> h;
+  const int64_t rc = xxh64_buffers(ctx, {HashTask{src, in_len}}, h);
+  if (rc != kOk) return rc;
+  *hash_out = h[0];
+  return 0;
 }
 
 int64_t ptwm_mi355x_set_profiling(uint32_t device_ordinal, uint32_t on) {

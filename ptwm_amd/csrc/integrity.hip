@@ -1,0 +1,404 @@
+// integrity.hip -- CRC-32/ISO-HDLC of device buffers (decoded planes).
+//
+// The reference checks each decoded plane against the CRC its record carries
+// (container.rs:2154-2159: crc32fast::hash of the plane bytes, crc32fast
+// 1.5.0 = reflected polynomial 0xEDB88320, init and final xor 0xFFFFFFFF).
+//
+// GPU formulation.  A zero-initialised CRC register is linear in the data,
+// and advancing it over m zero bytes multiplies it by x^(8m) mod P.  So:
+//   - each workgroup takes a range of a buffer; thread t owns the 16-byte
+//     pieces t, t+256, ... (coalesced dwordx4 loads) and keeps one register:
+//     advance by the 4080 bytes between its pieces (four byte-sliced lookups),
+//     then fold the piece in (slicing-by-4, Kounavis & Berry 2005);
+//   - every thread's register is moved to the range end by one GF(2)
+//     multiply with x^(8d) (d = its distance to the end) and the 256 values
+//     are xor-reduced: the range's zero-init CRC;
+//   - a second kernel chains the ranges of each buffer the same way (Horner
+//     with x^(8 range_len)) and applies init / final xor:
+//     crc = ~(~0 * x^(8n) xor raw).
+#include "integrity.h"
+
+#include "chain_ops.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace ptwm {
+
+namespace {
+
+constexpr uint32_t kPoly = 0xEDB88320u;  // reflected x^32 + x^26 + ... + 1; bit 31 = x^0
+constexpr uint32_t kOne = 0x80000000u;   // the polynomial 1
+constexpr uint32_t kPiece = 16, kThreads = 256, kTile = kPiece * kThreads;
+
+// Table layout in device memory (words):
+//   [0, 1024)     T0..T3: one-byte table and its slicing-by-4 successors
+//   [1024, 2048)  S0..S3: byte-sliced advance over kTile - kPiece zero bytes
+//   [2048, 2304)  K[t] = x^(8 * 16 * (255 - t))
+//   [2304, 2368)  X[k] = x^(8 * 2^k)
+constexpr uint32_t kTabS = 1024, kTabK = 2048, kTabX = 2304, kTabWords = 2368;
+
+// a * b mod P, reflected representation (bit 31 - i holds the x^i coefficient)
+__host__ __device__ inline uint32_t gf2_mulmod(uint32_t a, uint32_t b) {
+  uint32_t p = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    p ^= b & (0u - ((a >> (31 - i)) & 1u));
+    b = (b >> 1) ^ (kPoly & (0u - (b & 1u)));
+  }
+  return p;
+}
+
+// x^(8 n) mod P from the squares table X (X[k] = x^(8 * 2^k))
+__host__ __device__ inline uint32_t xpow8(uint64_t n, const uint32_t* X) {
+  uint32_t r = kOne;
+  for (int k = 0; n; ++k, n >>= 1)
+    if (n & 1u) r = gf2_mulmod(r, X[k]);
+  return r;
+}
+
+std::vector<uint32_t> build_tables() {
+  std::vector<uint32_t> tab(kTabWords, 0);
+  for (uint32_t i = 0; i < 256; ++i) {
+    uint32_t c = i;
+    for (int k = 0; k < 8; ++k) c = (c >> 1) ^ (kPoly & (0u - (c & 1u)));
+    tab[i] = c;
+  }
+  for (int k = 1; k < 4; ++k)
+    for (uint32_t i = 0; i < 256; ++i) {
+      const uint32_t prev = tab[256 * (k - 1) + i];
+      tab[256 * k + i] = (prev >> 8) ^ tab[prev & 255u];
+    }
+  uint32_t* X = &tab[kTabX];
+  X[0] = kOne >> 8;  // x^8
+  for (int k = 1; k < 64; ++k) X[k] = gf2_mulmod(X[k - 1], X[k - 1]);
+  const uint32_t adv = xpow8(kTile - kPiece, X);
+  for (int k = 0; k < 4; ++k)
+    for (uint32_t b = 0; b < 256; ++b) tab[kTabS + 256 * k + b] = gf2_mulmod(b << (8 * k), adv);
+  for (uint32_t t = 0; t < kThreads; ++t) tab[kTabK + t] = xpow8((uint64_t)kPiece * (kThreads - 1 - t), X);
+  return tab;
+}
+
+__device__ __forceinline__ uint32_t sliced(const uint32_t* L, uint32_t c) {
+  return L[c & 255u] ^ L[256 + ((c >> 8) & 255u)] ^ L[512 + ((c >> 16) & 255u)] ^ L[768 + (c >> 24)];
+}
+
+// one word through the one-byte tables T0..T3 (T3 takes the first byte)
+__device__ __forceinline__ uint32_t crc_word(const uint32_t* T, uint32_t c, uint32_t w) {
+  c ^= w;
+  return T[768 + (c & 255u)] ^ T[512 + ((c >> 8) & 255u)] ^ T[256 + ((c >> 16) & 255u)] ^ T[c >> 24];
+}
+
+__device__ __forceinline__ uint32_t crc_piece(const uint32_t* T, uint32_t c, u32x4 v) {
+  c = crc_word(T, c, v.x);
+  c = crc_word(T, c, v.y);
+  c = crc_word(T, c, v.z);
+  return crc_word(T, c, v.w);
+}
+
+__device__ __forceinline__ uint32_t block_xor(uint32_t v, uint32_t* red) {
+  for (int d = 32; d >= 1; d >>= 1) v ^= __shfl_xor(v, d, 64);
+  if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
+// Zero-init CRC of each range, relative to the range's end, for every plane
+// of the range.  A range is a run of whole elements of one buffer; with
+// kChain = passthrough the buffer is a plane itself, otherwise a restored
+// tensor whose plane bytes are re-derived by the (bijective) forward chain.
+template <uint32_t kChain>
+__global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restrict__ ranges,
+                                                        const uint32_t* __restrict__ gtab,
+                                                        uint32_t* __restrict__ part) {
+  constexpr int kNp = kChain == kChainIeee16Split2 ? 2 : kChain == kChainIeee32Split4 ? 4 : 1;
+  constexpr int kRatio = kNp;  // tensor bytes per plane byte for these chains
+  __shared__ uint32_t tab[kTabK];  // T0..T3, S0..S3
+  __shared__ uint32_t red[4];
+  const uint32_t t = threadIdx.x;
+  for (uint32_t i = t; i < kTabK; i += kThreads) tab[i] = gtab[i];
+  const CrcRange R = ranges[blockIdx.x];
+  __syncthreads();
+  const uint32_t* T = tab;
+  const uint32_t* S = tab + kTabS;
+  const uint64_t full = R.n / kTile, tail = R.n % kTile;
+  const u32x4* p = reinterpret_cast<const u32x4*>(R.src) + (uint64_t)t * kRatio;
+  uint32_t acc[kNp];
+#pragma unroll
+  for (int j = 0; j < kNp; ++j) acc[j] = 0;
+  auto step = [&](uint64_t k) {
+    u32x4 v[kRatio], pl[kNp];
+#pragma unroll
+    for (int h = 0; h < kRatio; ++h) v[h] = __builtin_nontemporal_load(p + k * kThreads * kRatio + h);
+    forward16<kChain>(v, pl);
+#pragma unroll
+    for (int j = 0; j < kNp; ++j) acc[j] = crc_piece(T, sliced(S, acc[j]), pl[j]);
+  };
+  uint64_t k = 0;
+  for (; k + 2 <= full; k += 2) {
+    step(k);
+    step(k + 1);
+  }
+  for (; k < full; ++k) step(k);
+  if (tail == 0) {
+    if (full) {
+      const uint32_t K = gtab[kTabK + t];
+#pragma unroll
+      for (int j = 0; j < kNp; ++j) acc[j] = gf2_mulmod(acc[j], K);
+    }
+  } else {
+    // the last, partial tile: thread t's piece may be whole, cut, or absent
+    const uint64_t base = full * kTile + (uint64_t)kPiece * t;
+    uint64_t end = full ? base - kTile + kPiece : 0;
+    bool any = full != 0;
+    if (base + kPiece <= R.n) {
+      step(full);
+      end = base + kPiece;
+      any = true;
+    } else if (base < R.n) {
+      const uint8_t* b = reinterpret_cast<const uint8_t*>(R.src);
+#pragma unroll
+      for (int j = 0; j < kNp; ++j) {
+        uint32_t c = sliced(S, acc[j]);
+        for (uint64_t i = base; i < R.n; ++i) c = T[(c ^ forward_byte<kChain>(b, i, j)) & 255u] ^ (c >> 8);
+        acc[j] = c;
+      }
+      end = R.n;
+      any = true;
+    }
+    if (any) {
+      const uint32_t K = xpow8(R.n - end, gtab + kTabX);
+#pragma unroll
+      for (int j = 0; j < kNp; ++j) acc[j] = gf2_mulmod(acc[j], K);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kNp; ++j) {
+    const uint32_t v = block_xor(acc[j], red);
+    if (t == 0) part[4ull * blockIdx.x + j] = v;
+    __syncthreads();
+  }
+}
+
+// Chains the ranges of one plane (blockIdx.x), applies init / final xor,
+// writes the plane's CRC.
+__global__ void __launch_bounds__(256) crc_combine_kernel(const CrcPlane* __restrict__ planes,
+                                                          const uint32_t* __restrict__ part,
+                                                          const uint32_t* __restrict__ gtab,
+                                                          uint32_t* __restrict__ crc_out) {
+  __shared__ uint32_t red[4];
+  const CrcPlane B = planes[blockIdx.x];
+  const uint32_t* X = gtab + kTabX;
+  const uint32_t t = threadIdx.x;
+  const uint32_t q = (B.n_ranges + kThreads - 1) / kThreads;
+  const uint32_t r0 = std::min(B.n_ranges, t * q), r1 = std::min(B.n_ranges, r0 + q);
+  uint32_t acc = 0;
+  if (r0 < r1) {
+    const uint64_t last_len = B.n - (uint64_t)(B.n_ranges - 1) * B.range_len;
+    const uint32_t s_full = xpow8(B.range_len, X);
+    for (uint32_t r = r0; r < r1; ++r) {
+      const uint32_t s = r + 1 == B.n_ranges ? xpow8(last_len, X) : s_full;
+      acc = gf2_mulmod(acc, s) ^ part[4ull * (B.first_range + r) + B.plane];
+    }
+    const uint64_t end = r1 == B.n_ranges ? B.n : (uint64_t)r1 * B.range_len;
+    acc = gf2_mulmod(acc, xpow8(B.n - end, X));
+  }
+  acc = block_xor(acc, red);
+  if (t == 0) crc_out[blockIdx.x] = ~(gf2_mulmod(0xFFFFFFFFu, xpow8(B.n, X)) ^ acc);
+}
+
+// ---- XXH64 (seed 0) of restored tensors ----
+// xxhash-rust 0.8.18 xxh64 (container.rs:2185-2194, compact.rs:441-445),
+// from the published XXH64 specification.  The four accumulators of one
+// buffer are serial chains over its 32-byte stripes; lanes 0-3 of one
+// wavefront carry them, the whole wavefront loads 64 stripes at a time and
+// precomputes the input * PRIME64_2 products off the serial path.
+constexpr uint64_t kXP1 = 0x9E3779B185EBCA87ull, kXP2 = 0xC2B2AE3D27D4EB4Full, kXP3 = 0x165667B19E3779F9ull,
+                   kXP4 = 0x85EBCA77C2B2AE63ull, kXP5 = 0x27D4EB2F165667C5ull;
+
+__device__ __forceinline__ uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
+__device__ __forceinline__ uint64_t xx_round(uint64_t acc, uint64_t in) { return rotl64(acc + in * kXP2, 31) * kXP1; }
+__device__ __forceinline__ uint64_t xx_merge(uint64_t h, uint64_t v) { return (h ^ xx_round(0, v)) * kXP1 + kXP4; }
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int src) {
+  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, 64);
+  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, 64);
+  return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+__global__ void __launch_bounds__(64) xxh64_kernel(const HashTask* __restrict__ tasks, uint64_t* __restrict__ out) {
+  __shared__ uint64_t prod[64][4];
+  const HashTask H = tasks[blockIdx.x];
+  const uint32_t l = threadIdx.x;
+  const uint64_t stripes = H.n / 32;
+  const u32x4* src = reinterpret_cast<const u32x4*>(H.src);
+  uint64_t v = l == 0 ? kXP1 + kXP2 : l == 1 ? kXP2 : l == 2 ? 0 : 0 - kXP1;
+  u32x4 a = u32x4_make(0, 0, 0, 0), b = a;
+  if (l < stripes) {
+    a = __builtin_nontemporal_load(src + 2 * l);
+    b = __builtin_nontemporal_load(src + 2 * l + 1);
+  }
+  for (uint64_t s0 = 0; s0 < stripes; s0 += 64) {
+    if (s0 + l < stripes) {
+      prod[l][0] = ((uint64_t)a.x | ((uint64_t)a.y << 32)) * kXP2;
+      prod[l][1] = ((uint64_t)a.z | ((uint64_t)a.w << 32)) * kXP2;
+      prod[l][2] = ((uint64_t)b.x | ((uint64_t)b.y << 32)) * kXP2;
+      prod[l][3] = ((uint64_t)b.z | ((uint64_t)b.w << 32)) * kXP2;
+    }
+    __syncthreads();
+    const uint64_t sn = s0 + 64 + l;  // next block, loaded while lanes 0-3 run the chains
+    if (sn < stripes) {
+      a = __builtin_nontemporal_load(src + 2 * sn);
+      b = __builtin_nontemporal_load(src + 2 * sn + 1);
+    }
+    const uint32_t cnt = (uint32_t)(stripes - s0 < 64 ? stripes - s0 : 64);
+    if (l < 4)
+      for (uint32_t k = 0; k < cnt; ++k) v = rotl64(v + prod[k][l], 31) * kXP1;
+    __syncthreads();
+  }
+  const uint64_t v1 = lane_u64(v, 0), v2 = lane_u64(v, 1), v3 = lane_u64(v, 2), v4 = lane_u64(v, 3);
+  if (l != 0) return;
+  uint64_t h;
+  if (H.n >= 32) {
+    h = rotl64(v1, 1) + rotl64(v2, 7) + rotl64(v3, 12) + rotl64(v4, 18);
+    h = xx_merge(h, v1);
+    h = xx_merge(h, v2);
+    h = xx_merge(h, v3);
+    h = xx_merge(h, v4);
+  } else {
+    h = kXP5;
+  }
+  h += H.n;
+  // the last < 32 bytes start 16-byte aligned: 8- and 4-byte loads are aligned
+  const uint8_t* p = reinterpret_cast<const uint8_t*>(H.src) + stripes * 32;
+  uint64_t rest = H.n - stripes * 32;
+  for (; rest >= 8; rest -= 8, p += 8) h = rotl64(h ^ xx_round(0, *reinterpret_cast<const uint64_t*>(p)), 27) * kXP1 + kXP4;
+  if (rest >= 4) {
+    h = rotl64(h ^ ((uint64_t)*reinterpret_cast<const uint32_t*>(p) * kXP1), 23) * kXP2 + kXP3;
+    rest -= 4;
+    p += 4;
+  }
+  for (; rest; --rest, ++p) h = rotl64(h ^ ((uint64_t)*p * kXP5), 11) * kXP1;
+  h ^= h >> 33;
+  h *= kXP2;
+  h ^= h >> 29;
+  h *= kXP3;
+  h ^= h >> 32;
+  out[blockIdx.x] = h;
+}
+
+int chain_np(uint32_t chain) { return chain == kChainIeee16Split2 ? 2 : chain == kChainIeee32Split4 ? 4 : 1; }
+
+}  // namespace
+
+bool crc_chain_supported(uint32_t chain) {
+  return chain == kChainIeee16Split2 || chain == kChainIeee32Split4 || chain == kChainPassthrough;
+}
+
+int64_t crc32_planes(DevCtx& ctx, const std::vector<CrcTask>& tasks, std::vector<uint32_t>& crcs) {
+  crcs.clear();
+  if (tasks.empty()) return kOk;
+  hipStream_t s = ctx.stream;
+  if (!ctx.crc_tab_ready) {
+    const std::vector<uint32_t> tab = build_tables();
+    PTWM_HIP_TRY(ctx.crc_tab.ensure(tab.size() * 4));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.crc_tab.ptr, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(hipStreamSynchronize(s));
+    ctx.crc_tab_ready = true;
+  }
+  // Range length (plane bytes): a multiple of the 4 KiB tile, sized so the
+  // whole batch makes about 16 workgroups per CU.
+  uint64_t total = 0;
+  for (const CrcTask& k : tasks) {
+    if (!crc_chain_supported(k.chain)) return kInternal;
+    if (k.n && (k.src & 15u)) return kInternal;  // callers pass 16-byte aligned buffers
+    total += k.n * (uint64_t)chain_np(k.chain);
+  }
+  const uint64_t cus = ctx.cu_count > 0 ? (uint64_t)ctx.cu_count : 256;
+  uint64_t rl = (total / (cus * 16) + kTile - 1) / kTile * kTile;
+  rl = std::max<uint64_t>(rl, 16 * kTile);
+  rl = std::min<uint64_t>(rl, 1ull << 30);
+  // ranges grouped by chain (one launch per chain), planes in task order
+  const uint32_t chains[3] = {kChainIeee16Split2, kChainIeee32Split4, kChainPassthrough};
+  std::vector<CrcRange> ranges;
+  std::vector<CrcPlane> planes;
+  uint32_t first[4] = {0, 0, 0, 0};
+  std::vector<uint32_t> task_plane0(tasks.size(), 0);
+  for (int c = 0; c < 3; ++c) {
+    first[c] = (uint32_t)ranges.size();
+    for (size_t i = 0; i < tasks.size(); ++i) {
+      const CrcTask& k = tasks[i];
+      if (k.chain != chains[c]) continue;
+      const uint32_t fr = (uint32_t)ranges.size();
+      const uint64_t ratio = (uint64_t)chain_np(k.chain);
+      for (uint64_t o = 0; o < k.n; o += rl) ranges.push_back(CrcRange{k.src + o * ratio, std::min(rl, k.n - o)});
+      (void)fr;
+    }
+  }
+  first[3] = (uint32_t)ranges.size();
+  // planes: walk tasks again in order, matching the range numbering above
+  {
+    std::vector<uint32_t> next(3);
+    for (int c = 0; c < 3; ++c) next[c] = first[c];
+    for (size_t i = 0; i < tasks.size(); ++i) {
+      const CrcTask& k = tasks[i];
+      const int c = k.chain == kChainIeee16Split2 ? 0 : k.chain == kChainIeee32Split4 ? 1 : 2;
+      const uint32_t nr = (uint32_t)((k.n + rl - 1) / rl);
+      task_plane0[i] = (uint32_t)planes.size();
+      for (int j = 0; j < chain_np(k.chain); ++j)
+        planes.push_back(CrcPlane{k.n, (uint32_t)rl, next[c], nr, (uint32_t)j});
+      next[c] += nr;
+    }
+  }
+  const size_t nr = ranges.size(), np = planes.size();
+  PTWM_HIP_TRY(ctx.crc_args.ensure(nr * sizeof(CrcRange) + np * sizeof(CrcPlane) + (4 * nr + np) * 4 + 64));
+  uint8_t* base = static_cast<uint8_t*>(ctx.crc_args.ptr);
+  CrcRange* d_ranges = reinterpret_cast<CrcRange*>(base);
+  CrcPlane* d_planes = reinterpret_cast<CrcPlane*>(base + nr * sizeof(CrcRange));
+  uint32_t* d_part = reinterpret_cast<uint32_t*>(base + nr * sizeof(CrcRange) + np * sizeof(CrcPlane));
+  uint32_t* d_out = d_part + 4 * nr;
+  if (nr) PTWM_HIP_TRY(hipMemcpyAsync(d_ranges, ranges.data(), nr * sizeof(CrcRange), hipMemcpyHostToDevice, s));
+  PTWM_HIP_TRY(hipMemcpyAsync(d_planes, planes.data(), np * sizeof(CrcPlane), hipMemcpyHostToDevice, s));
+  const uint32_t* gtab = static_cast<const uint32_t*>(ctx.crc_tab.ptr);
+  for (int c = 0; c < 3; ++c) {
+    const uint32_t cnt = first[c + 1] - first[c];
+    if (!cnt) continue;
+    const CrcRange* r = d_ranges + first[c];
+    uint32_t* pp = d_part + 4ull * first[c];
+    if (c == 0) hipLaunchKernelGGL(crc_range_kernel<kChainIeee16Split2>, dim3(cnt), dim3(kThreads), 0, s, r, gtab, pp);
+    if (c == 1) hipLaunchKernelGGL(crc_range_kernel<kChainIeee32Split4>, dim3(cnt), dim3(kThreads), 0, s, r, gtab, pp);
+    if (c == 2) hipLaunchKernelGGL(crc_range_kernel<kChainPassthrough>, dim3(cnt), dim3(kThreads), 0, s, r, gtab, pp);
+    PTWM_HIP_TRY(hipGetLastError());
+  }
+  for (size_t p0 = 0; p0 < np; p0 += 65535) {
+    const uint32_t cnt = (uint32_t)std::min<size_t>(65535, np - p0);
+    hipLaunchKernelGGL(crc_combine_kernel, dim3(cnt), dim3(kThreads), 0, s, d_planes + p0, d_part, gtab, d_out + p0);
+    PTWM_HIP_TRY(hipGetLastError());
+  }
+  crcs.assign(np, 0);
+  PTWM_HIP_TRY(hipMemcpyAsync(crcs.data(), d_out, np * 4, hipMemcpyDeviceToHost, s));
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  return kOk;
+}
+
+int64_t xxh64_buffers(DevCtx& ctx, const std::vector<HashTask>& tasks, std::vector<uint64_t>& hashes) {
+  hashes.assign(tasks.size(), 0);
+  if (tasks.empty()) return kOk;
+  for (const HashTask& h : tasks)
+    if (h.n && (h.src & 15u)) return kInternal;  // callers pass 16-byte aligned buffers
+  hipStream_t s = ctx.stream;
+  const size_t n = tasks.size();
+  PTWM_HIP_TRY(ctx.hash_args.ensure(n * (sizeof(HashTask) + 8) + 64));
+  HashTask* d_tasks = static_cast<HashTask*>(ctx.hash_args.ptr);
+  uint64_t* d_out = reinterpret_cast<uint64_t*>(d_tasks + n);
+  PTWM_HIP_TRY(hipMemcpyAsync(d_tasks, tasks.data(), n * sizeof(HashTask), hipMemcpyHostToDevice, s));
+  for (size_t k0 = 0; k0 < n; k0 += 65535) {
+    const uint32_t cnt = (uint32_t)std::min<size_t>(65535, n - k0);
+    hipLaunchKernelGGL(xxh64_kernel, dim3(cnt), dim3(64), 0, s, d_tasks + k0, d_out + k0);
+    PTWM_HIP_TRY(hipGetLastError());
+  }
+  PTWM_HIP_TRY(hipMemcpyAsync(hashes.data(), d_out, n * 8, hipMemcpyDeviceToHost, s));
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  return kOk;
+}
+
+}  // namespace ptwm

@@ -46,6 +46,9 @@ struct DevCtx {
   DeviceBuffer ref_jobs, ref_hist, ref_segs, ref_seglen, ref_codes, ref_rans_tab, ref_rans_segs, ref_rans_scratch,
       ref_rans_len, ref_hdr, ref_pack, ref_ops;
   PinnedBuffer h_enc, h_ilv;
+  // integrity (CRC-32 / XXH64) tables and arguments
+  DeviceBuffer crc_tab, crc_args, hash_args;
+  bool crc_tab_ready = false;
   int cu_count = 0;  // compute units of the device (0: not queried yet)
   std::map<uint64_t, int> ilv_occupancy;  // (chain, slots, stage words) -> workgroups per CU
   DeviceBuffer stage_in, stage_out, enc_split;
@@ -78,6 +81,8 @@ struct PlanTensor {
   uint64_t out_len = 0;
   uint32_t chain = 0;
   bool has_crc = false;
+  bool has_hash = false;  // xxh64 (seed 0) of the restored tensor
+  uint64_t xxh64 = 0;
   std::vector<PlanPlane> planes;
 };
 struct Plan {

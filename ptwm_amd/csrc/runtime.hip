@@ -14,6 +14,7 @@
 #include <memory>
 
 #include "ilv_host.h"
+#include "integrity.h"
 #include "runtime.h"
 
 namespace ptwm {
@@ -144,8 +145,10 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
     uint16_t tflags = c.get<uint16_t>();
     if (!c.ok) return kInvalidInput;
     T.has_crc = (tflags & 1u) != 0;
+    T.has_hash = (tflags & 2u) != 0;
+    if (T.has_hash) T.xxh64 = c.get<uint64_t>();
     int want_np = chain_planes(T.chain);
-    if (want_np < 0 || (int)np != want_np || (tflags & ~1u)) return kInvalidInput;
+    if (!c.ok || want_np < 0 || (int)np != want_np || (tflags & ~3u)) return kInvalidInput;
     if (T.out_offset > out_len || out_len - T.out_offset < T.out_len) return kInvalidInput;
     T.planes.resize(np);
     for (uint32_t p = 0; p < np; ++p) {
@@ -210,6 +213,9 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
       else if (P.codec != kCodecIdentity || P.payload_len != P.plane_len) ok = false;
     }
     if (!ok || !any_ilv) continue;
+    // a plane CRC is checked on the restored tensor where the chain is a
+    // bijection on plane bytes; other chains keep their planes in scratch
+    if (T.has_crc && !crc_chain_supported(T.chain)) continue;
     fused[t] = 1;
     IlvTensor X{};
     X.out = out_dev + T.out_offset;
@@ -353,6 +359,44 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   const uint32_t* st = static_cast<const uint32_t*>(ctx.h_status.ptr);
   for (size_t k = 0; k < n_jobs; ++k)
     if (st[k] != kStOk) return kInvalidInput;
+  // Integrity, after every tensor is restored: CRC-32 of each decoded plane
+  // (container.rs:2154-2159) and XXH64 of each restored tensor
+  // (container.rs:2185-2194); a mismatch is InvalidContainer there.
+  std::vector<CrcTask> crc_tasks;
+  std::vector<uint32_t> crc_want;
+  std::vector<HashTask> hash_tasks;
+  std::vector<uint64_t> hash_want;
+  for (size_t t = 0; t < nt; ++t) {
+    const PlanTensor& T = plan.tensors[t];
+    if (T.has_crc) {
+      if (fused[t]) {
+        crc_tasks.push_back(CrcTask{out_dev + T.out_offset, T.planes[0].plane_len, T.chain});
+      } else {
+        for (size_t p = 0; p < T.planes.size(); ++p)
+          crc_tasks.push_back(CrcTask{plane_addr[t][p], T.planes[p].plane_len, kChainPassthrough});
+      }
+      for (const PlanPlane& P : T.planes) crc_want.push_back(P.crc32);
+    }
+    if (T.has_hash) {
+      hash_tasks.push_back(HashTask{out_dev + T.out_offset, T.out_len});
+      hash_want.push_back(T.xxh64);
+    }
+  }
+  if (!crc_tasks.empty()) {
+    std::vector<uint32_t> got;
+    const int64_t rc = crc32_planes(ctx, crc_tasks, got);
+    if (rc != kOk) return rc;
+    if (got.size() != crc_want.size()) return kInternal;
+    for (size_t k = 0; k < got.size(); ++k)
+      if (got[k] != crc_want[k]) return kInvalidInput;
+  }
+  if (!hash_tasks.empty()) {
+    std::vector<uint64_t> got;
+    const int64_t rc = xxh64_buffers(ctx, hash_tasks, got);
+    if (rc != kOk) return rc;
+    for (size_t k = 0; k < got.size(); ++k)
+      if (got[k] != hash_want[k]) return kInvalidInput;
+  }
   return kOk;
 }
 

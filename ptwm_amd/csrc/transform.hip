@@ -8,48 +8,12 @@
 // Semantics follow transforms/fusion.rs (forward :35-94,208-255,329-338,
 // 431-440; inverse :127-194,261-315,376-399,478-501), NibbleSplit
 // (transforms/nibble_split.rs:72-120) and BytePassthrough.
+#include "chain_ops.h"
 #include "ptwm_common.h"
 
 namespace ptwm {
 
 namespace {
-
-__device__ __forceinline__ uint32_t reorder16x2(uint32_t v) {
-  return ((v << 1) & 0xFF00FF00u) | ((v >> 8) & 0x00800080u) | (v & 0x007F007Fu);
-}
-__device__ __forceinline__ uint32_t revert16x2(uint32_t v) {
-  return ((v << 8) & 0x80008000u) | ((v >> 1) & 0x7F807F80u) | (v & 0x007F007Fu);
-}
-__device__ __forceinline__ uint32_t reorder32(uint32_t v) {
-  return ((v << 1) & 0xFF000000u) | ((v >> 8) & 0x00800000u) | (v & 0x007FFFFFu);
-}
-__device__ __forceinline__ uint32_t revert32(uint32_t v) {
-  return ((v << 8) & 0x80000000u) | ((v >> 1) & 0x7F800000u) | (v & 0x007FFFFFu);
-}
-// four fp8 bytes at once (split/dtype8.rs:30-62)
-__device__ __forceinline__ uint32_t reorder_e4m3x4(uint32_t v) {
-  return ((v & 0x78787878u) << 1) | ((v & 0x80808080u) >> 4) | (v & 0x07070707u);
-}
-__device__ __forceinline__ uint32_t revert_e4m3x4(uint32_t r) {
-  return ((r & 0xF0F0F0F0u) >> 1) | ((r & 0x08080808u) << 4) | (r & 0x07070707u);
-}
-__device__ __forceinline__ uint32_t reorder_e5m2x4(uint32_t v) {
-  return ((v & 0x7C7C7C7Cu) << 1) | ((v & 0x80808080u) >> 5) | (v & 0x03030303u);
-}
-__device__ __forceinline__ uint32_t revert_e5m2x4(uint32_t r) {
-  return ((r & 0xF8F8F8F8u) >> 1) | ((r & 0x04040404u) << 5) | (r & 0x03030303u);
-}
-
-// byte interleave helpers: (a0 a1 a2 a3), (b0 b1 b2 b3) -> (a0 b0 a1 b1), (a2 b2 a3 b3)
-__device__ __forceinline__ void zip2(uint32_t a, uint32_t b, uint32_t& lo, uint32_t& hi) {
-  lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // bytes: a0 b0 a1 b1
-  hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // bytes: a2 b2 a3 b3
-}
-// inverse of zip2
-__device__ __forceinline__ void unzip2(uint32_t lo, uint32_t hi, uint32_t& a, uint32_t& b) {
-  a = __builtin_amdgcn_perm(hi, lo, 0x06040200u);  // lo.b0 lo.b2 hi.b0 hi.b2
-  b = __builtin_amdgcn_perm(hi, lo, 0x07050301u);
-}
 
 struct Planes {
   uint8_t* p[4];
