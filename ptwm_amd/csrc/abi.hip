@@ -9,6 +9,7 @@
 #include <cstring>
 
 #include "../../include/ptwm_mi355x.h"
+#include "decode_sync.h"
 #include "ilv_host.h"
 #include "integrity.h"
 #include "ref_encode.h"
@@ -109,10 +110,7 @@ int64_t decode_one_payload(DevCtx& ctx, uint32_t codec, uint64_t in_dev, size_t 
   }
   if (expected > out_cap) return kBufferTooSmall;
   if (expected == 0 && codec == kCodecIdentity) return 0;
-  PTWM_HIP_TRY(ctx.jobs.ensure(sizeof(DecodeJob)));
-  PTWM_HIP_TRY(ctx.status.ensure(64));
   PTWM_HIP_TRY(ctx.h_jobs.ensure(sizeof(DecodeJob)));
-  PTWM_HIP_TRY(ctx.h_status.ensure(64));
   DecodeJob* J = static_cast<DecodeJob*>(ctx.h_jobs.ptr);
   std::memset(J, 0, sizeof(*J));
   J->src = in_dev;
@@ -121,11 +119,8 @@ int64_t decode_one_payload(DevCtx& ctx, uint32_t codec, uint64_t in_dev, size_t 
   J->dst_len = expected;
   J->codec = codec;
   J->framed = 0;
-  PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, J, sizeof(DecodeJob), hipMemcpyHostToDevice, ctx.stream));
-  PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr),
-                                   static_cast<uint32_t*>(ctx.status.ptr), 1, ctx.stream));
-  PTWM_HIP_TRY(hipMemcpyAsync(ctx.h_status.ptr, ctx.status.ptr, 4, hipMemcpyDeviceToHost, ctx.stream));
-  PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+  const int64_t rc = decode_jobs(ctx, J, 1);
+  if (rc != kOk) return rc;
   if (*static_cast<uint32_t*>(ctx.h_status.ptr) != kStOk) return kInvalidInput;
   return (int64_t)expected;
 }

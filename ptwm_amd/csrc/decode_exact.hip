@@ -15,8 +15,13 @@
 // codec_tagged.rs:98-194 and codecs/length_prefix.rs:30-33; chunk frames
 // follow container.rs:2010-2049.
 //
-// This kernel is the exact path: it is used for the reference formats.
+// This kernel is the exact path: it is used for the reference formats.  A
+// large Huffman payload (DecodeJob::sync_id != 0) stops after the header and
+// decode table: its four streams continue on the parallel path
+// (decode_sync.hip), which hands back any payload it cannot prove it decodes
+// exactly as this kernel would.
 // The throughput-oriented path is the huff_ilv codec (huff_ilv.hip).
+#include "decode_sync.h"
 #include "ptwm_common.h"
 
 namespace ptwm {
@@ -209,7 +214,9 @@ __device__ void parse_job(const DecodeJob& job, SharedHeader& h) {
 }
 
 __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __restrict__ jobs,
-                                                          uint32_t* __restrict__ status) {
+                                                          uint32_t* __restrict__ status,
+                                                          SyncStream* __restrict__ sync_streams,
+                                                          uint16_t* __restrict__ sync_tables) {
   __shared__ SharedHeader h;
   __shared__ uint8_t lengths[256];
   __shared__ uint16_t counts[kHufMaxBits + 1];
@@ -333,6 +340,33 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
     }
     __syncthreads();
 
+    if (job.sync_id) {
+      // parallel path: publish the table and the four streams, stop here
+      const uint32_t d = job.sync_id - 1;
+      for (uint32_t i = lane; i < tsize; i += 64) sync_tables[2048ull * d + i] = table16[i];
+      if (lane < 4) {
+        uint64_t s4[4], e4[4];
+        split_four(job.dst_len, s4, e4);
+        uint32_t sub = job.sync_sub0;
+        for (int i = 0; i < (int)lane; ++i) sub += (uint32_t)((h.seg_len[i] * 8 + kSyncSubBits - 1) / kSyncSubBits);
+        SyncStream S;
+        S.src = job.src + h.enc_off + h.seg_src[lane];
+        S.m = h.seg_len[lane];
+        S.dst = job.dst + s4[lane];
+        S.n = e4[lane] - s4[lane];
+        S.T = ~0ull;
+        S.job = blockIdx.x;
+        S.first_sub = sub;
+        S.n_sub = (uint32_t)((h.seg_len[lane] * 8 + kSyncSubBits - 1) / kSyncSubBits);
+        S.max_bits = max_bits;
+        S.table = d;
+        S.pad = 0;
+        sync_streams[4ull * d + lane] = S;
+      }
+      if (lane == 0) status[blockIdx.x] = kStDeferred;
+      return;
+    }
+
     if (lane < 4) {
       Reader r;
       rd_init(r, enc + h.seg_src[lane], h.seg_len[lane]);
@@ -444,9 +478,10 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
 }
 
 hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
-                               hipStream_t stream) {
+                               SyncStream* sync_streams, uint16_t* sync_tables, hipStream_t stream) {
   if (n_jobs == 0) return hipSuccess;
-  hipLaunchKernelGGL(decode_exact_kernel, dim3(n_jobs), dim3(64), 0, stream, jobs_dev, status_dev);
+  hipLaunchKernelGGL(decode_exact_kernel, dim3(n_jobs), dim3(64), 0, stream, jobs_dev, status_dev, sync_streams,
+                     sync_tables);
   return hipGetLastError();
 }
 

@@ -1,0 +1,43 @@
+// decode_sync.h -- parallel decode of the reference's Huffman streams.
+#pragma once
+
+#include "runtime.h"
+
+namespace ptwm {
+
+// Bits per subsequence: one lane decodes one subsequence of a stream.  A
+// multiple of 32 with an odd word count, so lanes of a wavefront start in
+// different LDS banks.
+constexpr uint32_t kSyncSubBits = 480;
+// Payloads (Huffman, tag 1) at least this long take the parallel path.
+constexpr uint64_t kSyncMinBytes = 16384;
+
+// One of the four streams of a deferred payload, written by the exact
+// kernel once the header and the decode table are known.
+struct SyncStream {
+  uint64_t src;        // device address of stream byte 0
+  uint64_t m;          // stream bytes
+  uint64_t dst;        // device address of the segment's first output byte
+  uint64_t n;          // symbols of the segment (split_four of orig_len)
+  uint64_t T;          // bit position after symbol n-1 (write kernel); ~0 if not reached
+  uint32_t job;        // index into the job / status arrays
+  uint32_t first_sub;  // global slot of the stream's subsequence 0
+  uint32_t n_sub;      // ceil(8 m / kSyncSubBits)
+  uint32_t max_bits;   // decode table width
+  uint32_t table;      // deferred payload slot (decode table index)
+  uint32_t pad;
+};
+static_assert(sizeof(SyncStream) == 64, "SyncStream layout");
+
+// Decode the jobs hj[0..n) (host copies; uploaded here).  Reference-format
+// Huffman payloads of at least kSyncMinBytes decode on the parallel path;
+// a payload it declines, and every other job, decode on the exact path.
+// On return (stream synchronised) the host status array ctx.h_status holds
+// each job's final status.
+int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs);
+
+// exact-path kernel launch (decode_exact.hip)
+hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
+                               SyncStream* sync_streams, uint16_t* sync_tables, hipStream_t stream);
+
+}  // namespace ptwm

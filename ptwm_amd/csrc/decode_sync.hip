@@ -1,0 +1,419 @@
+// decode_sync.hip -- parallel decode of the reference's Huffman streams.
+//
+// A reference Huffman payload has four backward bitstreams
+// (entropy/huffman/compress.rs:9-103, bitstream.rs:22-50), each decoded
+// serially by the reference (decompress.rs:8-211).  Prefix codes
+// resynchronise: a decoder started at an arbitrary bit soon lands on a true
+// codeword boundary.  So every stream is cut into subsequences of
+// kSyncSubBits bits, one lane each:
+//   pass 1   each lane decodes from its subsequence's first bit up to the
+//            first codeword boundary at or past its end (its "exit"); lanes
+//            of a wavefront then restart from their left neighbour's exit
+//            until no start changes (sync_pass_kernel);
+//   fix      the same across wavefronts, repeated until no wavefront's first
+//            start differs from the previous wavefront's last exit
+//            (sync_fix_kernel; the host loops on a flag);
+//   scan     per stream, symbol counts -> output offsets (sync_scan_kernel);
+//   write    each lane decodes its subsequence again and writes the symbols
+//            (staged in LDS, stored coalesced), recording where symbol n-1
+//            ends (sync_write_kernel);
+//   check    the payload is accepted here only when, for all four streams,
+//            that end T satisfies ceil(T / 8) == stream bytes and the bits
+//            after T are zero (sync_check_kernel).
+// Under that condition the reference reader (BitReader, decode_symbol,
+// decode_stream_tail) never lets its bit counter wrap and always indexes the
+// table with real stream bits, so it produces exactly the zero-padded
+// sequential decode and ends exhausted (byte_index < 0, container 0): the
+// output here is the reference's, bit for bit.  A payload that fails the
+// condition (malformed, or encoded with trailing bytes) is decoded again on
+// the exact path, whose state machine replicates the reference for every
+// input.
+//
+// Logical bit k of a stream of m bytes is bit k % 8 of byte m - 1 - k / 8
+// (bitstream.rs:58-121); the kernels stage each wavefront's span of the
+// stream in LDS in logical order, so a 32-bit window at any bit is two LDS
+// words and one funnel shift.
+#include "decode_sync.h"
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+namespace ptwm {
+
+namespace {
+
+constexpr uint32_t kLanes = 64;
+constexpr uint32_t kSubBytes = kSyncSubBits / 8;
+constexpr uint32_t kWaveBits = kLanes * kSyncSubBits;
+constexpr uint32_t kStageWords = kWaveBits / 32 + 2;  // + the window overrun
+constexpr uint32_t kOutStage = 16384;                 // LDS output staging per wavefront
+constexpr uint32_t kMaxFixPasses = 256;
+static_assert(kSyncSubBits % 32 == 0 && (kSyncSubBits / 32) % 2 == 1, "subsequence size");
+
+struct SyncArrays {
+  uint64_t* start;   // per subsequence: first bit (stream-absolute)
+  uint64_t* exit;    // first codeword boundary at or past the subsequence end
+  uint32_t* count;   // symbols decoded from start to exit
+  uint64_t* prefix;  // symbols before the subsequence (scan)
+};
+
+// Which stream of deferred payload d, and which wavefront of it, wavefront
+// `w` of the payload's launch range covers; -1 when past the last.
+__device__ inline int locate(const SyncStream* S4, uint32_t& w) {
+  for (int s = 0; s < 4; ++s) {
+    const uint32_t ws = (S4[s].n_sub + kLanes - 1) / kLanes;
+    if (w < ws) return s;
+    w -= ws;
+  }
+  return -1;
+}
+
+__device__ inline uint8_t gbyte(uint64_t a) {
+  return *(const __attribute__((address_space(1))) uint8_t*)(uintptr_t)a;
+}
+
+// Stage logical bytes [L0, L0 + 4 * kStageWords) of the stream in LDS
+// (logical order, zero past the stream's end) and its decode table.
+__device__ inline void stage_wave(const SyncStream& S, uint64_t L0, const uint16_t* __restrict__ tables,
+                                  uint32_t* stage, uint16_t* tab) {
+  const uint32_t lane = threadIdx.x;
+  const uint32_t tsize = 1u << S.max_bits;
+  const uint16_t* gt = tables + 2048ull * S.table;
+  for (uint32_t i = lane; i < tsize; i += kLanes) tab[i] = gt[i];
+  for (uint32_t q = lane; q < kStageWords; q += kLanes) {
+    uint32_t v = 0;
+#pragma unroll
+    for (uint32_t t = 0; t < 4; ++t) {
+      const uint64_t i = L0 + 4ull * q + t;
+      if (i < S.m) v |= (uint32_t)gbyte(S.src + S.m - 1 - i) << (8 * t);
+    }
+    stage[q] = v;
+  }
+  __syncthreads();
+}
+
+// Decode from bit p (relative to the staged span) until p >= stop; returns
+// the exit bit, symbol count in `cnt`.  Every table entry consumes >= 1 bit.
+__device__ inline uint32_t run(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t p, uint32_t stop,
+                               uint32_t& cnt) {
+  uint32_t c = 0;
+  while (p < stop) {
+    const uint32_t wi = p >> 5;
+    const uint32_t win = __builtin_amdgcn_alignbit(stage[wi + 1], stage[wi], p & 31u);
+    const uint32_t e = tab[win & mask];
+    const uint32_t l = e >> 8;
+    p += l;
+    ++c;
+    if (p >= stop) break;
+    p += tab[(win >> l) & mask] >> 8;
+    ++c;
+  }
+  cnt = c;
+  return p;
+}
+
+// Lanes restart from their left neighbour's exit until no start changes (at
+// most 63 rounds: each round fixes at least one more lane).
+__device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32_t mask, bool valid, uint32_t& st,
+                              uint32_t& ex, uint32_t& cnt, bool& changed) {
+  const uint32_t lane = threadIdx.x;
+  for (uint32_t round = 0; round < kLanes; ++round) {
+    const uint32_t prev = (uint32_t)__shfl_up((int)ex, 1, 64);
+    const bool ch = valid && lane > 0 && prev != st;
+    if (__ballot(ch) == 0) break;
+    if (ch) {
+      st = prev;
+      ex = run(stage, tab, mask, st, (lane + 1) * kSyncSubBits, cnt);
+      changed = true;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(64) sync_pass_kernel(const SyncStream* __restrict__ streams,
+                                                       const uint32_t* __restrict__ wave_job,
+                                                       const uint32_t* __restrict__ job_wave0,
+                                                       const uint16_t* __restrict__ tables, SyncArrays A) {
+  __shared__ uint16_t tab[2048];
+  __shared__ uint32_t stage[kStageWords];
+  const uint32_t d = wave_job[blockIdx.x];
+  uint32_t w = blockIdx.x - job_wave0[d];
+  const int s = locate(streams + 4ull * d, w);
+  if (s < 0) return;
+  const SyncStream S = streams[4ull * d + s];
+  const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
+  stage_wave(S, L0, tables, stage, tab);
+  const uint32_t lane = threadIdx.x, mask = (1u << S.max_bits) - 1;
+  const uint32_t k = w * kLanes + lane;
+  const bool valid = k < S.n_sub;
+  uint32_t st = lane * kSyncSubBits, cnt = 0, ex = st;
+  if (valid) ex = run(stage, tab, mask, st, st + kSyncSubBits, cnt);
+  bool changed = false;
+  settle(stage, tab, mask, valid, st, ex, cnt, changed);
+  if (valid) {
+    const uint64_t g = (uint64_t)S.first_sub + k;
+    A.start[g] = L0 * 8 + st;
+    A.exit[g] = L0 * 8 + ex;
+    A.count[g] = cnt;
+  }
+}
+
+// One fix pass: a wavefront whose first start differs from the previous
+// wavefront's last exit restarts from it and settles again.
+__global__ void __launch_bounds__(64) sync_fix_kernel(const SyncStream* __restrict__ streams,
+                                                      const uint32_t* __restrict__ wave_job,
+                                                      const uint32_t* __restrict__ job_wave0,
+                                                      const uint16_t* __restrict__ tables, SyncArrays A,
+                                                      uint32_t* __restrict__ flag) {
+  __shared__ uint16_t tab[2048];
+  __shared__ uint32_t stage[kStageWords];
+  const uint32_t d = wave_job[blockIdx.x];
+  uint32_t w = blockIdx.x - job_wave0[d];
+  const int s = locate(streams + 4ull * d, w);
+  if (s < 0 || w == 0) return;
+  const SyncStream S = streams[4ull * d + s];
+  const uint64_t g0 = (uint64_t)S.first_sub + (uint64_t)w * kLanes;
+  const uint64_t prev_exit = A.exit[g0 - 1];
+  if (prev_exit == A.start[g0]) return;
+  const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
+  stage_wave(S, L0, tables, stage, tab);
+  const uint32_t lane = threadIdx.x, mask = (1u << S.max_bits) - 1;
+  const uint32_t k = w * kLanes + lane;
+  const bool valid = k < S.n_sub;
+  uint32_t st = 0, ex = 0, cnt = 0;
+  if (valid) {
+    st = (uint32_t)(A.start[g0 + lane] - L0 * 8);
+    ex = (uint32_t)(A.exit[g0 + lane] - L0 * 8);
+    cnt = A.count[g0 + lane];
+  }
+  bool changed = false;
+  if (lane == 0) {  // prev_exit lies in [L0 * 8, L0 * 8 + 11): a codeword overruns by < 11 bits
+    st = (uint32_t)std::min<uint64_t>(prev_exit - L0 * 8, kSyncSubBits);
+    ex = run(stage, tab, mask, st, kSyncSubBits, cnt);
+    changed = true;
+  }
+  settle(stage, tab, mask, valid, st, ex, cnt, changed);
+  if (valid && changed) {
+    A.start[g0 + lane] = L0 * 8 + st;
+    A.exit[g0 + lane] = L0 * 8 + ex;
+    A.count[g0 + lane] = cnt;
+  }
+  if (lane == 0) *flag = 1u;
+}
+
+// Exclusive scan of the subsequence counts of one stream (blockIdx.x).
+__global__ void __launch_bounds__(256) sync_scan_kernel(const SyncStream* __restrict__ streams, SyncArrays A) {
+  __shared__ uint64_t part[256];
+  const SyncStream S = streams[blockIdx.x];
+  const uint32_t t = threadIdx.x;
+  const uint32_t per = (S.n_sub + 255) / 256;
+  const uint32_t a = std::min(S.n_sub, t * per), b = std::min(S.n_sub, a + per);
+  uint64_t sum = 0;
+  for (uint32_t k = a; k < b; ++k) sum += A.count[(uint64_t)S.first_sub + k];
+  part[t] = sum;
+  __syncthreads();
+  if (t == 0) {
+    uint64_t run_sum = 0;
+    for (int i = 0; i < 256; ++i) {
+      const uint64_t v = part[i];
+      part[i] = run_sum;
+      run_sum += v;
+    }
+  }
+  __syncthreads();
+  uint64_t acc = part[t];
+  for (uint32_t k = a; k < b; ++k) {
+    A.prefix[(uint64_t)S.first_sub + k] = acc;
+    acc += A.count[(uint64_t)S.first_sub + k];
+  }
+}
+
+// Decode again from the settled starts and write symbols [0, n) of the
+// segment; the lane holding symbol n-1 records where it ends.
+__global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__ streams,
+                                                        const uint32_t* __restrict__ wave_job,
+                                                        const uint32_t* __restrict__ job_wave0,
+                                                        const uint16_t* __restrict__ tables, SyncArrays A) {
+  __shared__ uint16_t tab[2048];
+  __shared__ uint32_t stage[kStageWords];
+  __shared__ uint8_t out[kOutStage];
+  const uint32_t d = wave_job[blockIdx.x];
+  uint32_t w = blockIdx.x - job_wave0[d];
+  const int s = locate(streams + 4ull * d, w);
+  if (s < 0) return;
+  SyncStream* Sp = streams + 4ull * d + s;
+  const SyncStream S = *Sp;
+  const uint64_t g0 = (uint64_t)S.first_sub + (uint64_t)w * kLanes;
+  const uint64_t base = A.prefix[g0];
+  if (base >= S.n) return;  // the whole wavefront decodes padding
+  const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
+  stage_wave(S, L0, tables, stage, tab);
+  const uint32_t lane = threadIdx.x, mask = (1u << S.max_bits) - 1;
+  const uint32_t k = w * kLanes + lane;
+  const bool valid = k < S.n_sub;
+  uint64_t first = ~0ull, cnt = 0;
+  uint32_t p = 0;
+  if (valid) {
+    first = A.prefix[g0 + lane];
+    cnt = A.count[g0 + lane];
+    p = (uint32_t)(A.start[g0 + lane] - L0 * 8);
+  }
+  // symbols [first, first + cnt) of the segment, of which those below n are real
+  const uint32_t last_lane = (uint32_t)std::min<uint64_t>(kLanes, S.n_sub - (uint64_t)w * kLanes) - 1;
+  const uint64_t wave_end = std::min<uint64_t>(S.n, A.prefix[g0 + last_lane] + A.count[g0 + last_lane]);
+  const uint64_t wave_len = wave_end - base;
+  const bool staged = wave_len <= kOutStage;
+  uint8_t* dst = reinterpret_cast<uint8_t*>(S.dst);
+  if (valid && first < S.n) {
+    const uint64_t m = std::min<uint64_t>(cnt, S.n - first);
+    for (uint64_t i = 0; i < m; ++i) {
+      const uint32_t wi = p >> 5;
+      const uint32_t win = __builtin_amdgcn_alignbit(stage[wi + 1], stage[wi], p & 31u);
+      const uint32_t e = tab[win & mask];
+      p += e >> 8;
+      if (staged) out[first - base + i] = (uint8_t)e;
+      else dst[first + i] = (uint8_t)e;
+    }
+    if (first + m == S.n) Sp->T = L0 * 8 + p;
+  }
+  if (staged) {
+    __syncthreads();
+    for (uint64_t i = lane; i < wave_len; i += kLanes) dst[base + i] = out[i];
+  }
+}
+
+// Accept a deferred payload only under the exactness condition above.
+__global__ void __launch_bounds__(64) sync_check_kernel(const SyncStream* __restrict__ streams, uint32_t n_def,
+                                                        uint32_t* __restrict__ status) {
+  const uint32_t d = blockIdx.x * kLanes + threadIdx.x;
+  if (d >= n_def) return;
+  const uint32_t job = streams[4ull * d].job;
+  if (status[job] != kStDeferred) return;  // final already (the header was rejected)
+  bool ok = true;
+  for (int s = 0; s < 4; ++s) {
+    const SyncStream S = streams[4ull * d + s];
+    if (S.n == 0) {
+      ok = ok && S.m == 0;
+      continue;
+    }
+    if (S.T == ~0ull || S.T > 8 * S.m || S.T <= 8 * (S.m - 1)) {
+      ok = false;
+      continue;
+    }
+    const uint32_t used = (uint32_t)(S.T - 8 * (S.m - 1));  // bits of the last logical byte, 1..8
+    if (used < 8 && (gbyte(S.src) >> used) != 0) ok = false;
+  }
+  status[job] = ok ? kStOk : kStFallback;
+}
+
+}  // namespace
+
+int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
+  hipStream_t s = ctx.stream;
+  PTWM_HIP_TRY(ctx.status.ensure(n_jobs * sizeof(uint32_t) + 64));
+  PTWM_HIP_TRY(ctx.h_status.ensure(n_jobs * sizeof(uint32_t) + 64));
+  if (n_jobs == 0) return kOk;
+  // choose the payloads for the parallel path and lay out their slots
+  std::vector<uint32_t> wave_job, job_wave0;
+  uint64_t subs = 0;
+  uint32_t n_def = 0;
+  for (size_t j = 0; j < n_jobs; ++j) {
+    hj[j].sync_id = 0;
+    hj[j].sync_sub0 = 0;
+    if (hj[j].codec != kCodecHuffman || hj[j].src_len < kSyncMinBytes) continue;
+    const uint64_t u = (hj[j].src_len * 8 + kSyncSubBits - 1) / kSyncSubBits + 4;
+    const uint64_t waves = (u + kLanes - 1) / kLanes + 4;
+    if (subs + u > 0xFFFFFFFFull || wave_job.size() + waves > 0x7FFFFFFFull) continue;
+    hj[j].sync_id = ++n_def;
+    hj[j].sync_sub0 = (uint32_t)subs;
+    job_wave0.push_back((uint32_t)wave_job.size());
+    wave_job.insert(wave_job.end(), waves, n_def - 1);
+    subs += u;
+  }
+  PTWM_HIP_TRY(ctx.jobs.ensure(n_jobs * sizeof(DecodeJob) + 64));
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, hj, n_jobs * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
+  SyncStream* streams = nullptr;
+  uint16_t* tables = nullptr;
+  SyncArrays A{};
+  uint32_t *d_wave_job = nullptr, *d_job_wave0 = nullptr, *d_flag = nullptr;
+  if (n_def) {
+    PTWM_HIP_TRY(ctx.sync_streams.ensure(4ull * n_def * sizeof(SyncStream)));
+    PTWM_HIP_TRY(ctx.sync_tables.ensure(2048ull * 2 * n_def));
+    PTWM_HIP_TRY(ctx.sync_sub.ensure(subs * (8 + 8 + 8 + 4) + 64));
+    PTWM_HIP_TRY(ctx.sync_waves.ensure((wave_job.size() + job_wave0.size() + 1) * 4 + 64));
+    streams = static_cast<SyncStream*>(ctx.sync_streams.ptr);
+    tables = static_cast<uint16_t*>(ctx.sync_tables.ptr);
+    uint8_t* sb = static_cast<uint8_t*>(ctx.sync_sub.ptr);
+    A.start = reinterpret_cast<uint64_t*>(sb);
+    A.exit = A.start + subs;
+    A.prefix = A.exit + subs;
+    A.count = reinterpret_cast<uint32_t*>(A.prefix + subs);
+    d_wave_job = static_cast<uint32_t*>(ctx.sync_waves.ptr);
+    d_job_wave0 = d_wave_job + wave_job.size();
+    d_flag = d_job_wave0 + job_wave0.size();
+    PTWM_HIP_TRY(hipMemsetAsync(streams, 0, 4ull * n_def * sizeof(SyncStream), s));
+    PTWM_HIP_TRY(hipMemcpyAsync(d_wave_job, wave_job.data(), wave_job.size() * 4, hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(hipMemcpyAsync(d_job_wave0, job_wave0.data(), job_wave0.size() * 4, hipMemcpyHostToDevice, s));
+  }
+  uint32_t* status = static_cast<uint32_t*>(ctx.status.ptr);
+  PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr), status, (uint32_t)n_jobs, streams,
+                                   tables, s));
+  if (n_def) {
+    const uint32_t nw = (uint32_t)wave_job.size();
+    hipLaunchKernelGGL(sync_pass_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables, A);
+    PTWM_HIP_TRY(hipGetLastError());
+    PTWM_HIP_TRY(ctx.h_small.ensure(64));
+    volatile uint32_t* h_flag = static_cast<uint32_t*>(ctx.h_small.ptr);
+    bool settled = false;
+    for (uint32_t pass = 0; pass < kMaxFixPasses; ++pass) {
+      PTWM_HIP_TRY(hipMemsetAsync(d_flag, 0, 4, s));
+      hipLaunchKernelGGL(sync_fix_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables, A,
+                         d_flag);
+      PTWM_HIP_TRY(hipGetLastError());
+      PTWM_HIP_TRY(hipMemcpyAsync(const_cast<uint32_t*>(h_flag), d_flag, 4, hipMemcpyDeviceToHost, s));
+      PTWM_HIP_TRY(hipStreamSynchronize(s));
+      if (*h_flag == 0) {
+        settled = true;
+        break;
+      }
+    }
+    if (settled) {
+      hipLaunchKernelGGL(sync_scan_kernel, dim3(4 * n_def), dim3(256), 0, s, streams, A);
+      PTWM_HIP_TRY(hipGetLastError());
+      hipLaunchKernelGGL(sync_write_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables,
+                         A);
+      PTWM_HIP_TRY(hipGetLastError());
+      hipLaunchKernelGGL(sync_check_kernel, dim3((n_def + kLanes - 1) / kLanes), dim3(kLanes), 0, s, streams, n_def,
+                         status);
+      PTWM_HIP_TRY(hipGetLastError());
+    }
+  }
+  uint32_t* hs = static_cast<uint32_t*>(ctx.h_status.ptr);
+  PTWM_HIP_TRY(hipMemcpyAsync(hs, status, n_jobs * 4, hipMemcpyDeviceToHost, s));
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  // payloads the parallel path declined (or did not settle) go to the exact path
+  std::vector<DecodeJob> again;
+  std::vector<size_t> again_idx;
+  for (size_t j = 0; j < n_jobs; ++j) {
+    if (hs[j] == kStFallback || hs[j] == kStDeferred) {
+      DecodeJob J = hj[j];
+      J.sync_id = 0;
+      J.sync_sub0 = 0;
+      again.push_back(J);
+      again_idx.push_back(j);
+    }
+  }
+  if (!again.empty()) {
+    const size_t na = again.size();
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, again.data(), na * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr), status, (uint32_t)na, nullptr,
+                                     nullptr, s));
+    std::vector<uint32_t> st2(na);
+    PTWM_HIP_TRY(hipMemcpyAsync(st2.data(), status, na * 4, hipMemcpyDeviceToHost, s));
+    PTWM_HIP_TRY(hipStreamSynchronize(s));
+    for (size_t i = 0; i < na; ++i) hs[again_idx[i]] = st2[i];
+  }
+  return kOk;
+}
+
+}  // namespace ptwm

@@ -55,6 +55,8 @@ enum DecodeStatus : uint32_t {
   kStBadLength = 3,      // declared length disagrees with the chunk table / cap
   kStBadHeader = 4,      // weights / frequency table / jump table invalid
   kStBadStream = 5,      // bitstream inconsistent (reference decoder errors)
+  kStDeferred = 6,       // header parsed, streams handed to the parallel Huffman path
+  kStFallback = 7,       // parallel path declined the payload: decode it on the exact path
   kStNotRun = 0xFFFFFFFFu,
 };
 
@@ -68,7 +70,9 @@ struct DecodeJob {
   uint64_t dst_len;   // exact decoded size expected (chunk table decoded_size)
   uint32_t codec;     // kCodec*
   uint32_t framed;    // 1: src starts with a chunk frame header
-  uint32_t pad[6];
+  uint32_t sync_id;   // 0, or 1 + slot of a Huffman payload whose streams go to the parallel path
+  uint32_t sync_sub0; // first subsequence slot of that payload
+  uint32_t pad[4];
 };
 static_assert(sizeof(DecodeJob) == 64, "DecodeJob layout");
 

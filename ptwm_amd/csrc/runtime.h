@@ -46,6 +46,8 @@ struct DevCtx {
   DeviceBuffer ref_jobs, ref_hist, ref_segs, ref_seglen, ref_codes, ref_rans_tab, ref_rans_segs, ref_rans_scratch,
       ref_rans_len, ref_hdr, ref_pack, ref_ops;
   PinnedBuffer h_enc, h_ilv;
+  // parallel Huffman decode of reference streams
+  DeviceBuffer sync_streams, sync_tables, sync_sub, sync_waves;
   // integrity (CRC-32 / XXH64) tables and arguments
   DeviceBuffer crc_tab, crc_args, hash_args;
   bool crc_tab_ready = false;
@@ -98,9 +100,7 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
 // error code.
 int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev);
 
-// kernel launchers (decode_exact.hip, transform.hip)
-hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
-                               hipStream_t stream);
+// kernel launchers (transform.hip; the decode launchers are in decode_sync.h)
 hipError_t launch_merge(uint32_t chain, const uint8_t* const* planes, uint64_t plane_len, uint8_t* out,
                         hipStream_t stream);
 hipError_t launch_split(uint32_t chain, const uint8_t* in, uint64_t plane_len, uint8_t* const* planes,

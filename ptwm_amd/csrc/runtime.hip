@@ -13,6 +13,7 @@
 #include <cstring>
 #include <memory>
 
+#include "decode_sync.h"
 #include "ilv_host.h"
 #include "integrity.h"
 #include "runtime.h"
@@ -325,11 +326,15 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     int64_t rc = ilv_decode_tensors(ctx, ilv);
     if (rc != kOk) return rc;
   }
-  if (n_jobs) PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, hj, n_jobs * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[0], s));
   if (n_jobs) {
-    PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr),
-                                     static_cast<uint32_t*>(ctx.status.ptr), (uint32_t)n_jobs, s));
+    // reference-format payloads: parallel Huffman path where it applies,
+    // exact path otherwise; final statuses in h_status
+    const int64_t rc = decode_jobs(ctx, hj, n_jobs);
+    if (rc != kOk) return rc;
+    const uint32_t* st = static_cast<const uint32_t*>(ctx.h_status.ptr);
+    for (size_t k = 0; k < n_jobs; ++k)
+      if (st[k] != kStOk) return kInvalidInput;
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[1], s));
   for (size_t t = 0; t < nt; ++t) {
@@ -343,10 +348,6 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     PTWM_HIP_TRY(launch_merge(T.chain, pp, T.planes[0].plane_len, out, s));
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], s));
-  if (n_jobs) {
-    PTWM_HIP_TRY(hipMemcpyAsync(ctx.h_status.ptr, ctx.status.ptr, n_jobs * sizeof(uint32_t),
-                                hipMemcpyDeviceToHost, s));
-  }
   PTWM_HIP_TRY(hipStreamSynchronize(s));
   if (ctx.profile) {
     float a = 0, b = 0;
@@ -356,9 +357,6 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     ctx.last_ms[1] += b;
     ctx.last_ms[2] += a + b;
   }
-  const uint32_t* st = static_cast<const uint32_t*>(ctx.h_status.ptr);
-  for (size_t k = 0; k < n_jobs; ++k)
-    if (st[k] != kStOk) return kInvalidInput;
   // Integrity, after every tensor is restored: CRC-32 of each decoded plane
   // (container.rs:2154-2159) and XXH64 of each restored tensor
   // (container.rs:2185-2194); a mismatch is InvalidContainer there.

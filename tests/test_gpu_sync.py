@@ -1,0 +1,120 @@
+"""Parallel decode of reference Huffman payloads (decode_sync.hip) against
+the CPU oracle (the reference decoder, decompress.rs:8-211).
+
+Payloads of at least 16 KiB take the parallel path; it must restore exactly
+the oracle's bytes, and a payload it declines (malformed, trailing bytes)
+must still get the oracle's outcome through the exact path.  Each case is
+decoded through the plane-level device entry point.
+"""
+import struct
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from ptwm_amd import api, ids
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+SEL = ids.PLANE_CODEC_LABEL
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def dev(b: bytes):
+    t = torch.zeros(len(b) + 16, dtype=torch.uint8, device="cuda:0")
+    if b:
+        t[: len(b)].copy_(torch.from_numpy(np.frombuffer(b, np.uint8).copy()))
+    return t[: len(b)]
+
+
+def gpu_decode(payload: bytes, cap: int):
+    out = torch.zeros(cap + 16, dtype=torch.uint8, device="cuda:0")
+    try:
+        n = api.plane_codec_decode_cuda(SEL, "huffman", b"", dev(payload), out[:cap], 0)
+    except Exception as e:  # noqa: BLE001
+        return None, getattr(e, "rc", None)
+    torch.cuda.synchronize()
+    return out[:n].cpu().numpy().tobytes(), n
+
+
+def oracle_decode(payload: bytes, cap: int):
+    try:
+        return O.codec_decode(O.CODEC_HUFFMAN, payload, cap)
+    except Exception:  # noqa: BLE001
+        return None
+
+
+def planes():
+    rng = np.random.default_rng(23)
+    yield "geo100k", rng.geometric(0.3, 100_000).clip(0, 255).astype(np.uint8).tobytes()
+    w = (torch.randn(1 << 20, generator=torch.Generator().manual_seed(2)) * 0.02).to(torch.bfloat16)
+    yield "bf16exp1m", O.chain_forward(O.CHAIN_IEEE16_SPLIT2, w.view(torch.uint8).numpy().tobytes())[1]
+    yield "bf16mant1m", O.chain_forward(O.CHAIN_IEEE16_SPLIT2, w.view(torch.uint8).numpy().tobytes())[0]
+    # 1-bit codes: more symbols per wavefront than the LDS output stage holds
+    yield "two2m", rng.choice([3, 9], 2 << 20, p=[0.97, 0.03]).astype(np.uint8).tobytes()
+    yield "uni16", rng.integers(0, 16, 300_000).astype(np.uint8).tobytes()
+    f = [1, 1]
+    while len(f) < 20:
+        f.append(f[-1] + f[-2])
+    p = np.array(f, float)
+    yield "fib11bit", rng.choice(20, 500_000, p=p / p.sum()).astype(np.uint8).tobytes()
+    x = torch.randn(2048, 4096, generator=torch.Generator().manual_seed(3))
+    x = (x / x.abs().amax(1, keepdim=True) * 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy().tobytes()
+    hi, lo = O.chain_forward(O.CHAIN_E4M3_NIBBLE, x)
+    yield "e4m3hi8m", hi
+    yield "e4m3lo8m", lo
+
+
+@pytest.mark.parametrize("name,plane", list(planes()), ids=[n for n, _ in planes()])
+def test_parallel_huffman_decode_matches_reference(name, plane):
+    payload = O.codec_encode(O.CODEC_HUFFMAN, plane)
+    note(f"sync decode {name}: plane {len(plane)} payload {len(payload)} tag {payload[0]}")
+    got, n = gpu_decode(payload, len(plane))
+    assert n == len(plane) and got == plane
+
+
+def _streams_start(payload: bytes) -> int:
+    blob = payload[5:]
+    _, used = O.huf_decode_weights(blob)
+    return 5 + used + 16
+
+
+def test_parallel_huffman_malformed_matches_reference_outcome():
+    rng = np.random.default_rng(99)
+    base = rng.geometric(0.25, 200_000).clip(0, 255).astype(np.uint8).tobytes()
+    payload = O.codec_encode(O.CODEC_HUFFMAN, base)
+    s0 = _streams_start(payload)
+    jump = struct.unpack_from("<4I", payload, s0 - 16)
+    cases = []
+    for k in range(30):                                   # bit flips inside the streams
+        b = bytearray(payload)
+        for _ in range(1 + k % 3):
+            i = int(rng.integers(s0, len(b)))
+            b[i] ^= 1 << int(rng.integers(0, 8))
+        cases.append((f"flip{k}", bytes(b)))
+    for s in range(4):                                    # first byte of each stream (the end bits)
+        b = bytearray(payload)
+        b[s0 + sum(jump[:s])] ^= 0x80
+        cases.append((f"lastbits{s}", bytes(b)))
+    b = bytearray(payload)                                # a zero byte appended to stream 3
+    b += b"\x00"
+    struct.pack_into("<I", b, s0 - 4, jump[3] + 1)
+    cases.append(("trailing0", bytes(b)))
+    b = bytearray(payload)                                # streams 0/1 boundary moved by one byte
+    struct.pack_into("<I", b, s0 - 16, jump[0] + 1)
+    struct.pack_into("<I", b, s0 - 12, jump[1] - 1)
+    cases.append(("moved", bytes(b)))
+    cases.append(("truncated", payload[:-7]))
+    for name, p in cases:
+        note(f"sync malformed {name}")
+        want = oracle_decode(p, len(base))
+        got, _ = gpu_decode(p, len(base))
+        assert (got is None) == (want is None), name
+        if want is not None:
+            assert got == want, name
