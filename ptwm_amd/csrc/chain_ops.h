@@ -83,18 +83,20 @@ __device__ __forceinline__ void forward16(const u32x4* s, u32x4* out) {
   }
 }
 
-// Forward chain of one element: byte of plane j for element i of tensor t.
+// Forward chain of one element: byte of plane j for element i of the tensor
+// at device address t.
 template <uint32_t kChain>
-__device__ __forceinline__ uint8_t forward_byte(const uint8_t* t, uint64_t i, int j) {
+__device__ __forceinline__ uint8_t forward_byte(uint64_t t, uint64_t i, int j) {
   if constexpr (kChain == kChainIeee16Split2) {
-    const uint32_t v = (uint32_t)t[2 * i] | ((uint32_t)t[2 * i + 1] << 8);
+    const uint32_t v = (uint32_t)g_ld<uint8_t>(t + 2 * i) | ((uint32_t)g_ld<uint8_t>(t + 2 * i + 1) << 8);
     return (uint8_t)(reorder16x2(v) >> (8 * j));
   } else if constexpr (kChain == kChainIeee32Split4) {
-    const uint32_t v = (uint32_t)t[4 * i] | ((uint32_t)t[4 * i + 1] << 8) | ((uint32_t)t[4 * i + 2] << 16) |
-                       ((uint32_t)t[4 * i + 3] << 24);
+    uint32_t v = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) v |= (uint32_t)g_ld<uint8_t>(t + 4 * i + b) << (8 * b);
     return (uint8_t)(reorder32(v) >> (8 * j));
   } else {
-    return t[i];
+    return g_ld<uint8_t>(t + i);
   }
 }
 

@@ -32,6 +32,8 @@ constexpr int kHufMaxBits = 11;
 constexpr uint32_t kRansProbBits = 11;
 constexpr uint32_t kRansScale = 1u << kRansProbBits;
 constexpr uint32_t kRansL = 1u << 23;
+constexpr uint32_t kRansStage = 1024;  // staged bytes per stream per round
+constexpr uint32_t kRansRound = 384;   // symbols per stream per round (<= 2 bytes each)
 
 __device__ inline uint32_t ld_u32le(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
@@ -52,7 +54,7 @@ __device__ inline void rd_init(Reader& r, const uint8_t* d, uint64_t n) {
   r.cnt = 0;
   int64_t avail = r.bi + 1 < 8 ? r.bi + 1 : 8;   // initial_fill (bitstream.rs:76-82)
   for (int64_t i = 0; i < avail; ++i) {
-    r.cont |= (uint64_t)d[r.bi] << r.cnt;
+    r.cont |= (uint64_t)g_ld<uint8_t>((uint64_t)(d + r.bi)) << r.cnt;
     r.cnt = (r.cnt + 8) & 0xFF;
     r.bi--;
   }
@@ -64,13 +66,15 @@ __device__ inline void rd_reload(Reader& r) {
     const uint8_t* p = r.data + (r.bi - 7);
     uint64_t w = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w = (w << 8) | p[i];
+    for (int i = 0; i < 8; ++i) w = (w << 8) | g_ld<uint8_t>((uint64_t)(p + i));
     r.cont = w;
     r.cnt = 64;
     r.bi -= 8;
   } else if (r.cnt <= 32 && r.bi >= 3) {
     const uint8_t* p = r.data + (r.bi - 3);
-    uint32_t w = ((uint32_t)p[0] << 24) | ((uint32_t)p[1] << 16) | ((uint32_t)p[2] << 8) | p[3];
+    const uint64_t a = (uint64_t)p;
+    uint32_t w = ((uint32_t)g_ld<uint8_t>(a) << 24) | ((uint32_t)g_ld<uint8_t>(a + 1) << 16) |
+                 ((uint32_t)g_ld<uint8_t>(a + 2) << 8) | g_ld<uint8_t>(a + 3);
     r.cont |= (uint64_t)w << r.cnt;
     r.cnt = (r.cnt + 32) & 0xFF;
     r.bi -= 4;
@@ -83,7 +87,7 @@ __device__ inline void rd_refill(Reader& r) {
     rd_reload(r);
   } else {
     while (r.cnt < 56 && r.bi >= 0) {
-      r.cont |= (uint64_t)r.data[r.bi] << r.cnt;
+      r.cont |= (uint64_t)g_ld<uint8_t>((uint64_t)(r.data + r.bi)) << r.cnt;
       r.cnt = (r.cnt + 8) & 0xFF;
       r.bi--;
     }
@@ -101,7 +105,7 @@ __device__ inline uint8_t rd_decode(Reader& r, const uint16_t* table, uint64_t m
 
 __device__ inline void rd_refill_to(Reader& r, uint32_t nbits) {
   while (r.cnt < nbits && r.bi >= 0) {
-    r.cont |= (uint64_t)r.data[r.bi] << r.cnt;
+    r.cont |= (uint64_t)g_ld<uint8_t>((uint64_t)(r.data + r.bi)) << r.cnt;
     r.cnt = (r.cnt + 8) & 0xFF;
     r.bi--;
   }
@@ -113,7 +117,7 @@ __device__ bool huf_tail(Reader& r, const uint16_t* table, uint64_t mask, uint32
   uint64_t i = 0;
   while (i < len && r.bi >= 3) {
     if (r.cnt < max_bits) rd_refill(r);
-    out[i++] = rd_decode(r, table, mask);
+    g_st<uint8_t>((uint64_t)(out + i++), rd_decode(r, table, mask));
   }
   while (i < len) {
     uint64_t avail = (uint64_t)r.cnt + (uint64_t)(r.bi + 1 > 0 ? r.bi + 1 : 0) * 8;
@@ -129,7 +133,7 @@ __device__ bool huf_tail(Reader& r, const uint16_t* table, uint64_t mask, uint32
       r.cont >>= nb;
       r.cnt = (r.cnt - nb) & 0xFF;
     }
-    out[i++] = (uint8_t)(e & 0xFF);
+    g_st<uint8_t>((uint64_t)(out + i++), (uint8_t)(e & 0xFF));
   }
   return true;
 }
@@ -216,7 +220,8 @@ __device__ void parse_job(const DecodeJob& job, SharedHeader& h) {
 __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __restrict__ jobs,
                                                           uint32_t* __restrict__ status,
                                                           SyncStream* __restrict__ sync_streams,
-                                                          uint16_t* __restrict__ sync_tables) {
+                                                          uint16_t* __restrict__ sync_tables,
+                                                          uint64_t* __restrict__ copy_src) {
   __shared__ SharedHeader h;
   __shared__ uint8_t lengths[256];
   __shared__ uint16_t counts[kHufMaxBits + 1];
@@ -241,7 +246,15 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
   }
   if (h.kind == 0) {  // stored bytes
     const uint8_t* s = src + h.copy_off;
-    for (uint64_t i = lane; i < job.dst_len; i += 64) dst[i] = s[i];
+    if (copy_src && job.dst_len >= kCopyDeferMin) {
+      // large: copied by raw_copy_kernel, one workgroup per 64 KiB
+      if (lane == 0) {
+        copy_src[blockIdx.x] = reinterpret_cast<uint64_t>(s);
+        status[blockIdx.x] = kStOk;
+      }
+      return;
+    }
+    for (uint64_t i = lane; i < job.dst_len; i += 64) g_st<uint8_t>((uint64_t)(dst + i), g_ld<uint8_t>((uint64_t)(s + i)));
     if (lane == 0) status[blockIdx.x] = kStOk;
     return;
   }
@@ -383,8 +396,8 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
 #pragma unroll
         for (int round = 0; round < 2; ++round) {
           rd_refill(r);
-          dst[op] = rd_decode(r, table16, mask);
-          dst[op + 1] = rd_decode(r, table16, mask);
+          g_st<uint8_t>((uint64_t)(dst + op), rd_decode(r, table16, mask));
+          g_st<uint8_t>((uint64_t)(dst + op + 1), rd_decode(r, table16, mask));
           op += 2;
         }
       }
@@ -448,40 +461,99 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
     for (uint32_t j = 0; j < f; ++j) table32[st + j] = entry;
   }
   __syncthreads();
-  if (lane < 4) {
-    uint64_t s4[4], e4[4];
-    split_four(job.dst_len, s4, e4);
-    bool good = true;
-    if (s4[lane] != e4[lane]) {
-      const uint8_t* st = enc + h.seg_src[lane];
-      uint64_t sl = h.seg_len[lane];
-      if (sl < 4) good = false;
-      else {
-        uint32_t x = ld_u32le(st);
-        uint64_t q = 4;
-        for (uint64_t k = s4[lane]; k < e4[lane] && good; ++k) {
-          uint32_t idx = x & (kRansScale - 1);
-          uint32_t e = table32[idx];
-          dst[k] = (uint8_t)(e & 0xFF);
-          x = ((e >> 8) & 0xFFF) * (x >> kRansProbBits) + idx - (e >> 20);
+  // Four lanes run the four serial state chains.  The bytes each chain
+  // renormalises from are staged in LDS by the whole wavefront, a window per
+  // round; a lane that exhausts its window mid-renormalisation suspends and
+  // resumes after the next staging (every round makes progress).
+  __shared__ uint8_t rbuf[4][kRansStage];
+  __shared__ uint64_t rq[4];
+  __shared__ uint32_t rbusy;
+  uint64_t s4[4], e4[4];
+  split_four(job.dst_len, s4, e4);
+  const uint8_t* st = enc + h.seg_src[lane & 3];
+  const uint32_t sl = (uint32_t)h.seg_len[lane & 3];  // jump-table lengths are u32
+  uint32_t k = (uint32_t)s4[lane & 3], q = 4;
+  const uint32_t end = (uint32_t)e4[lane & 3];
+  const uint64_t out = reinterpret_cast<uint64_t>(dst);
+  uint32_t x = 0;
+  bool good = true, done = true, pending = false;
+  if (lane < 4 && k != end) {
+    if (sl < 4) good = false;
+    else {
+      x = ld_u32le(st);
+      done = false;
+    }
+  }
+  for (;;) {
+    if (lane < 4) rq[lane] = done ? ~0ull : q;
+    if (lane == 0) rbusy = 0;
+    __syncthreads();
+    if (lane < 4 && !done) atomicOr(&rbusy, 1u);
+    for (uint32_t i = lane; i < 4 * kRansStage; i += 64) {
+      const uint32_t sj = i / kRansStage, o = i % kRansStage;
+      const uint64_t qb = rq[sj];
+      if (qb != ~0ull && qb + o < h.seg_len[sj]) rbuf[sj][o] = g_ld<uint8_t>((uint64_t)(enc + h.seg_src[sj] + qb + o));
+    }
+    __syncthreads();
+    if (rbusy == 0) break;
+    if (lane < 4 && !done) {
+      const uint32_t qb = q;
+      const uint32_t qlim = sl - qb < kRansStage ? sl : qb + kRansStage;  // staged bytes: [qb, qlim)
+      const uint8_t* buf = rbuf[lane];
+      for (uint32_t n = 0;;) {
+        if (pending) {  // careful renormalisation after a careful symbol (decompress.rs:104-107)
+          bool suspend = false;
           while (x < kRansL) {
-            if (q >= sl) { good = false; break; }
-            x = (x << 8) | st[q++];
+            if (q >= sl) { good = false; done = true; break; }
+            if (q >= qlim) { suspend = true; break; }
+            x = (x << 8) | buf[q - qb];
+            ++q;
           }
+          if (done || suspend) break;
+          pending = false;
         }
+        // fast stretch: normalised state (x >= L, so at most two renormalising
+        // bytes per symbol) and two staged stream bytes in hand
+        while (x >= kRansL && k < end && n < kRansRound && q + 2 <= qlim) {
+          const uint32_t idx = x & (kRansScale - 1);
+          const uint32_t e = table32[idx];
+          const uint32_t b0 = buf[q - qb], b1 = buf[q - qb + 1];
+          g_st<uint8_t>(out + k, (uint8_t)(e & 0xFF));
+          x = ((e >> 8) & 0xFFF) * (x >> kRansProbBits) + idx - (e >> 20);
+          const bool n1 = x < kRansL;
+          x = n1 ? (x << 8) | b0 : x;
+          const bool n2 = x < kRansL;
+          x = n2 ? (x << 8) | b1 : x;
+          q += (uint32_t)n1 + (uint32_t)n2;
+          ++k;
+          ++n;
+        }
+        // here pending is false: the last symbol's renormalisation is complete
+        if (k == end) { done = true; break; }
+        if (n >= kRansRound) break;
+        // one careful symbol (unnormalised start, or the stage's last bytes)
+        const uint32_t idx = x & (kRansScale - 1);
+        const uint32_t e = table32[idx];
+        g_st<uint8_t>(out + k, (uint8_t)(e & 0xFF));
+        x = ((e >> 8) & 0xFFF) * (x >> kRansProbBits) + idx - (e >> 20);
+        ++k;
+        ++n;
+        pending = true;
       }
     }
-    if (!good) atomicOr(&h.err, 1u);
+    __syncthreads();
   }
+  if (lane < 4 && !good) atomicOr(&h.err, 1u);
   __syncthreads();
   if (lane == 0) status[blockIdx.x] = h.err ? kStBadStream : kStOk;
 }
 
 hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
-                               SyncStream* sync_streams, uint16_t* sync_tables, hipStream_t stream) {
+                               SyncStream* sync_streams, uint16_t* sync_tables, uint64_t* copy_src,
+                               hipStream_t stream) {
   if (n_jobs == 0) return hipSuccess;
   hipLaunchKernelGGL(decode_exact_kernel, dim3(n_jobs), dim3(64), 0, stream, jobs_dev, status_dev, sync_streams,
-                     sync_tables);
+                     sync_tables, copy_src);
   return hipGetLastError();
 }
 

@@ -36,8 +36,15 @@ static_assert(sizeof(SyncStream) == 64, "SyncStream layout");
 // each job's final status.
 int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs);
 
-// exact-path kernel launch (decode_exact.hip)
+// Stored (tag 0 / Identity) payloads at least this long are copied by a
+// multi-workgroup kernel after the exact kernel has parsed them.
+constexpr uint64_t kCopyDeferMin = 4096;
+constexpr uint64_t kCopyChunk = 65536;
+
+// exact-path kernel launch (decode_exact.hip); copy_src (may be null): per
+// job, the source of a deferred stored-bytes copy (0: none)
 hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
-                               SyncStream* sync_streams, uint16_t* sync_tables, hipStream_t stream);
+                               SyncStream* sync_streams, uint16_t* sync_tables, uint64_t* copy_src,
+                               hipStream_t stream);
 
 }  // namespace ptwm

@@ -52,10 +52,11 @@ constexpr uint32_t kMaxFixPasses = 256;
 static_assert(kSyncSubBits % 32 == 0 && (kSyncSubBits / 32) % 2 == 1, "subsequence size");
 
 struct SyncArrays {
-  uint64_t* start;   // per subsequence: first bit (stream-absolute)
-  uint64_t* exit;    // first codeword boundary at or past the subsequence end
-  uint32_t* count;   // symbols decoded from start to exit
-  uint64_t* prefix;  // symbols before the subsequence (scan)
+  uint64_t* start;        // per subsequence: first bit (stream-absolute)
+  uint64_t* exit;         // first codeword boundary at or past the subsequence end
+  uint32_t* count;        // symbols decoded from start to exit
+  uint32_t* wave_sum;     // per launched wavefront: symbols of its 64 subsequences
+  uint64_t* wave_prefix;  // per launched wavefront: symbols of the stream before it
 };
 
 // Which stream of deferred payload d, and which wavefront of it, wavefront
@@ -201,84 +202,141 @@ __global__ void __launch_bounds__(64) sync_fix_kernel(const SyncStream* __restri
   if (lane == 0) *flag = 1u;
 }
 
-// Exclusive scan of the subsequence counts of one stream (blockIdx.x).
-__global__ void __launch_bounds__(256) sync_scan_kernel(const SyncStream* __restrict__ streams, SyncArrays A) {
+// Symbols per wavefront (sum of its 64 subsequence counts).
+__global__ void __launch_bounds__(64) sync_wave_sum_kernel(const SyncStream* __restrict__ streams,
+                                                           const uint32_t* __restrict__ wave_job,
+                                                           const uint32_t* __restrict__ job_wave0, SyncArrays A) {
+  const uint32_t d = wave_job[blockIdx.x];
+  uint32_t w = blockIdx.x - job_wave0[d];
+  const int s = locate(streams + 4ull * d, w);
+  if (s < 0) return;
+  const SyncStream S = streams[4ull * d + s];
+  const uint32_t lane = threadIdx.x, k = w * kLanes + lane;
+  uint32_t c = k < S.n_sub ? A.count[(uint64_t)S.first_sub + k] : 0u;
+  for (int o = 32; o >= 1; o >>= 1) c += (uint32_t)__shfl_xor((int)c, o, 64);
+  if (lane == 0) A.wave_sum[blockIdx.x] = c;
+}
+
+// Exclusive scan of the wavefront sums of one stream (blockIdx.x = 4 d + s);
+// its wavefronts are consecutive in the launch, after those of streams < s.
+__global__ void __launch_bounds__(256) sync_scan_kernel(const SyncStream* __restrict__ streams,
+                                                        const uint32_t* __restrict__ job_wave0, SyncArrays A) {
   __shared__ uint64_t part[256];
-  const SyncStream S = streams[blockIdx.x];
+  const uint32_t d = blockIdx.x / 4, s = blockIdx.x % 4;
+  uint32_t w0 = job_wave0[d];
+  for (uint32_t i = 0; i < s; ++i) w0 += (streams[4ull * d + i].n_sub + kLanes - 1) / kLanes;
+  const uint32_t nw = (streams[blockIdx.x].n_sub + kLanes - 1) / kLanes;
   const uint32_t t = threadIdx.x;
-  const uint32_t per = (S.n_sub + 255) / 256;
-  const uint32_t a = std::min(S.n_sub, t * per), b = std::min(S.n_sub, a + per);
+  const uint32_t per = (nw + 255) / 256;
+  const uint32_t a = std::min(nw, t * per), b = std::min(nw, a + per);
   uint64_t sum = 0;
-  for (uint32_t k = a; k < b; ++k) sum += A.count[(uint64_t)S.first_sub + k];
+  for (uint32_t k = a; k < b; ++k) sum += A.wave_sum[w0 + k];
   part[t] = sum;
   __syncthreads();
-  if (t == 0) {
-    uint64_t run_sum = 0;
-    for (int i = 0; i < 256; ++i) {
-      const uint64_t v = part[i];
-      part[i] = run_sum;
-      run_sum += v;
-    }
+  for (uint32_t o = 1; o < 256; o <<= 1) {  // inclusive Hillis-Steele scan
+    const uint64_t v = t >= o ? part[t - o] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
   }
-  __syncthreads();
-  uint64_t acc = part[t];
+  uint64_t acc = t ? part[t - 1] : 0;
   for (uint32_t k = a; k < b; ++k) {
-    A.prefix[(uint64_t)S.first_sub + k] = acc;
-    acc += A.count[(uint64_t)S.first_sub + k];
+    A.wave_prefix[w0 + k] = acc;
+    acc += A.wave_sum[w0 + k];
   }
 }
 
 // Decode again from the settled starts and write symbols [0, n) of the
-// segment; the lane holding symbol n-1 records where it ends.
+// segment; the lane holding symbol n-1 records where it ends.  Symbols are
+// staged in LDS at their output address mod 16, so the store is dwordx4.
 __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__ streams,
                                                         const uint32_t* __restrict__ wave_job,
                                                         const uint32_t* __restrict__ job_wave0,
                                                         const uint16_t* __restrict__ tables, SyncArrays A) {
   __shared__ uint16_t tab[2048];
   __shared__ uint32_t stage[kStageWords];
-  __shared__ uint8_t out[kOutStage];
+  __shared__ __attribute__((aligned(16))) uint8_t out[kOutStage + 16];
   const uint32_t d = wave_job[blockIdx.x];
   uint32_t w = blockIdx.x - job_wave0[d];
   const int s = locate(streams + 4ull * d, w);
   if (s < 0) return;
   SyncStream* Sp = streams + 4ull * d + s;
   const SyncStream S = *Sp;
-  const uint64_t g0 = (uint64_t)S.first_sub + (uint64_t)w * kLanes;
-  const uint64_t base = A.prefix[g0];
+  const uint64_t base = A.wave_prefix[blockIdx.x];
   if (base >= S.n) return;  // the whole wavefront decodes padding
   const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
   stage_wave(S, L0, tables, stage, tab);
   const uint32_t lane = threadIdx.x, mask = (1u << S.max_bits) - 1;
-  const uint32_t k = w * kLanes + lane;
-  const bool valid = k < S.n_sub;
-  uint64_t first = ~0ull, cnt = 0;
-  uint32_t p = 0;
-  if (valid) {
-    first = A.prefix[g0 + lane];
-    cnt = A.count[g0 + lane];
-    p = (uint32_t)(A.start[g0 + lane] - L0 * 8);
+  const uint64_t g = (uint64_t)S.first_sub + (uint64_t)w * kLanes + lane;
+  const bool valid = w * kLanes + lane < S.n_sub;
+  const uint32_t cnt = valid ? A.count[g] : 0u;
+  uint32_t incl = cnt;  // in-wave inclusive scan of the counts
+  for (uint32_t o = 1; o < kLanes; o <<= 1) {
+    const uint32_t v = (uint32_t)__shfl_up((int)incl, o, 64);
+    if (lane >= o) incl += v;
   }
-  // symbols [first, first + cnt) of the segment, of which those below n are real
-  const uint32_t last_lane = (uint32_t)std::min<uint64_t>(kLanes, S.n_sub - (uint64_t)w * kLanes) - 1;
-  const uint64_t wave_end = std::min<uint64_t>(S.n, A.prefix[g0 + last_lane] + A.count[g0 + last_lane]);
+  const uint64_t first = base + (incl - cnt);
+  const uint64_t wave_end = std::min<uint64_t>(S.n, base + A.wave_sum[blockIdx.x]);
   const uint64_t wave_len = wave_end - base;
   const bool staged = wave_len <= kOutStage;
-  uint8_t* dst = reinterpret_cast<uint8_t*>(S.dst);
+  const uint64_t gA = S.dst + base, gB = S.dst + wave_end;
+  const uint32_t skew = (uint32_t)(gA & 15u);
   if (valid && first < S.n) {
+    uint32_t p = (uint32_t)(A.start[g] - L0 * 8);
     const uint64_t m = std::min<uint64_t>(cnt, S.n - first);
     for (uint64_t i = 0; i < m; ++i) {
       const uint32_t wi = p >> 5;
       const uint32_t win = __builtin_amdgcn_alignbit(stage[wi + 1], stage[wi], p & 31u);
       const uint32_t e = tab[win & mask];
       p += e >> 8;
-      if (staged) out[first - base + i] = (uint8_t)e;
-      else dst[first + i] = (uint8_t)e;
+      if (staged) out[skew + (first - base) + i] = (uint8_t)e;
+      else g_st<uint8_t>(S.dst + first + i, (uint8_t)e);
     }
     if (first + m == S.n) Sp->T = L0 * 8 + p;
   }
   if (staged) {
     __syncthreads();
-    for (uint64_t i = lane; i < wave_len; i += kLanes) dst[base + i] = out[i];
+    const uint64_t al0 = std::min<uint64_t>((gA + 15) & ~15ull, gB);
+    const uint64_t al1 = std::max<uint64_t>(gB & ~15ull, al0);
+    const uint64_t lbase = gA & ~15ull;  // LDS offset of address X is X - lbase
+    for (uint64_t x = gA + lane; x < al0; x += kLanes) g_st<uint8_t>(x, out[x - lbase]);
+    for (uint64_t x = al1 + lane; x < gB; x += kLanes) g_st<uint8_t>(x, out[x - lbase]);
+    for (uint64_t x = al0 + 16ull * lane; x < al1; x += 16ull * kLanes)
+      g_st<u32x4>(x, *reinterpret_cast<const u32x4*>(out + (x - lbase)));
+  }
+}
+
+// Stored bytes the exact kernel deferred (copy_src[j] != 0): one workgroup
+// per kCopyChunk of output.  Aligned dword stores; the source is realigned
+// with a funnel shift of two aligned words, used only where both words hold
+// source bytes.
+__global__ void __launch_bounds__(256) raw_copy_kernel(const DecodeJob* __restrict__ jobs,
+                                                       const uint64_t* __restrict__ copy_src,
+                                                       const uint32_t* __restrict__ chunk_job,
+                                                       const uint32_t* __restrict__ job_chunk0) {
+  const uint32_t j = chunk_job[blockIdx.x];
+  const uint64_t s = copy_src[j];
+  if (s == 0) return;
+  const DecodeJob J = jobs[j];
+  const uint64_t a = (uint64_t)(blockIdx.x - job_chunk0[j]) * kCopyChunk;
+  const uint64_t b = std::min<uint64_t>(J.dst_len, a + kCopyChunk);
+  if (a >= b) return;
+  const uint32_t t = threadIdx.x;
+  const uint64_t ba = J.dst + a, bb = J.dst + b;
+  const uint64_t lo = std::min<uint64_t>((ba + 3) & ~3ull, bb);
+  const uint64_t hi = std::max<uint64_t>(bb & ~3ull, lo);
+  for (uint64_t x = ba + t; x < lo; x += 256) g_st<uint8_t>(x, g_ld<uint8_t>(s + (x - J.dst)));
+  for (uint64_t x = hi + t; x < bb; x += 256) g_st<uint8_t>(x, g_ld<uint8_t>(s + (x - J.dst)));
+  for (uint64_t x = lo + 4ull * t; x < hi; x += 1024) {
+    const uint64_t o = x - J.dst;
+    if (o + 5 <= J.dst_len) {
+      const uint64_t S = s + o;
+      const uint64_t sa = S & ~3ull;
+      g_st<uint32_t>(x, __builtin_amdgcn_alignbyte(g_ld<uint32_t>(sa + 4), g_ld<uint32_t>(sa), (uint32_t)(S & 3u)));
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) g_st<uint8_t>(x + k, g_ld<uint8_t>(s + o + k));
+    }
   }
 }
 
@@ -313,13 +371,20 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   PTWM_HIP_TRY(ctx.status.ensure(n_jobs * sizeof(uint32_t) + 64));
   PTWM_HIP_TRY(ctx.h_status.ensure(n_jobs * sizeof(uint32_t) + 64));
   if (n_jobs == 0) return kOk;
-  // choose the payloads for the parallel path and lay out their slots
-  std::vector<uint32_t> wave_job, job_wave0;
+  // Payloads for the parallel path and their slots; output chunks for
+  // deferred stored-bytes copies (any job may turn out to be stored).
+  std::vector<uint32_t> wave_job, job_wave0, chunk_job, job_chunk0(n_jobs, 0);
   uint64_t subs = 0;
   uint32_t n_def = 0;
   for (size_t j = 0; j < n_jobs; ++j) {
     hj[j].sync_id = 0;
     hj[j].sync_sub0 = 0;
+    job_chunk0[j] = (uint32_t)chunk_job.size();
+    if (hj[j].dst_len >= kCopyDeferMin) {
+      const uint64_t nc = (hj[j].dst_len + kCopyChunk - 1) / kCopyChunk;
+      if (chunk_job.size() + nc > 0x7FFFFFFFull) return kInvalidInput;
+      chunk_job.insert(chunk_job.end(), nc, (uint32_t)j);
+    }
     if (hj[j].codec != kCodecHuffman || hj[j].src_len < kSyncMinBytes) continue;
     const uint64_t u = (hj[j].src_len * 8 + kSyncSubBits - 1) / kSyncSubBits + 4;
     const uint64_t waves = (u + kLanes - 1) / kLanes + 4;
@@ -332,22 +397,36 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   }
   PTWM_HIP_TRY(ctx.jobs.ensure(n_jobs * sizeof(DecodeJob) + 64));
   PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, hj, n_jobs * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
+  const DecodeJob* d_jobs = static_cast<const DecodeJob*>(ctx.jobs.ptr);
+  // deferred copies: source per job, chunk -> job map, job -> first chunk
+  const size_t nck = chunk_job.size();
+  PTWM_HIP_TRY(ctx.copy_args.ensure(n_jobs * 8 + (nck + n_jobs) * 4 + 64));
+  uint64_t* d_copy_src = static_cast<uint64_t*>(ctx.copy_args.ptr);
+  uint32_t* d_chunk_job = reinterpret_cast<uint32_t*>(d_copy_src + n_jobs);
+  uint32_t* d_job_chunk0 = d_chunk_job + nck;
+  PTWM_HIP_TRY(hipMemsetAsync(d_copy_src, 0, n_jobs * 8, s));
+  if (nck) {
+    PTWM_HIP_TRY(hipMemcpyAsync(d_chunk_job, chunk_job.data(), nck * 4, hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(hipMemcpyAsync(d_job_chunk0, job_chunk0.data(), n_jobs * 4, hipMemcpyHostToDevice, s));
+  }
   SyncStream* streams = nullptr;
   uint16_t* tables = nullptr;
   SyncArrays A{};
   uint32_t *d_wave_job = nullptr, *d_job_wave0 = nullptr, *d_flag = nullptr;
+  const uint32_t nw = (uint32_t)wave_job.size();
   if (n_def) {
     PTWM_HIP_TRY(ctx.sync_streams.ensure(4ull * n_def * sizeof(SyncStream)));
     PTWM_HIP_TRY(ctx.sync_tables.ensure(2048ull * 2 * n_def));
-    PTWM_HIP_TRY(ctx.sync_sub.ensure(subs * (8 + 8 + 8 + 4) + 64));
+    PTWM_HIP_TRY(ctx.sync_sub.ensure(subs * (8 + 8 + 4) + (uint64_t)nw * (8 + 4) + 64));
     PTWM_HIP_TRY(ctx.sync_waves.ensure((wave_job.size() + job_wave0.size() + 1) * 4 + 64));
     streams = static_cast<SyncStream*>(ctx.sync_streams.ptr);
     tables = static_cast<uint16_t*>(ctx.sync_tables.ptr);
     uint8_t* sb = static_cast<uint8_t*>(ctx.sync_sub.ptr);
     A.start = reinterpret_cast<uint64_t*>(sb);
     A.exit = A.start + subs;
-    A.prefix = A.exit + subs;
-    A.count = reinterpret_cast<uint32_t*>(A.prefix + subs);
+    A.wave_prefix = A.exit + subs;
+    A.count = reinterpret_cast<uint32_t*>(A.wave_prefix + nw);
+    A.wave_sum = A.count + subs;
     d_wave_job = static_cast<uint32_t*>(ctx.sync_waves.ptr);
     d_job_wave0 = d_wave_job + wave_job.size();
     d_flag = d_job_wave0 + job_wave0.size();
@@ -356,10 +435,13 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
     PTWM_HIP_TRY(hipMemcpyAsync(d_job_wave0, job_wave0.data(), job_wave0.size() * 4, hipMemcpyHostToDevice, s));
   }
   uint32_t* status = static_cast<uint32_t*>(ctx.status.ptr);
-  PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr), status, (uint32_t)n_jobs, streams,
-                                   tables, s));
+  PTWM_HIP_TRY(launch_decode_exact(d_jobs, status, (uint32_t)n_jobs, streams, tables, d_copy_src, s));
+  if (nck) {
+    hipLaunchKernelGGL(raw_copy_kernel, dim3((uint32_t)nck), dim3(256), 0, s, d_jobs, d_copy_src, d_chunk_job,
+                       d_job_chunk0);
+    PTWM_HIP_TRY(hipGetLastError());
+  }
   if (n_def) {
-    const uint32_t nw = (uint32_t)wave_job.size();
     hipLaunchKernelGGL(sync_pass_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables, A);
     PTWM_HIP_TRY(hipGetLastError());
     PTWM_HIP_TRY(ctx.h_small.ensure(64));
@@ -378,7 +460,9 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
       }
     }
     if (settled) {
-      hipLaunchKernelGGL(sync_scan_kernel, dim3(4 * n_def), dim3(256), 0, s, streams, A);
+      hipLaunchKernelGGL(sync_wave_sum_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, A);
+      PTWM_HIP_TRY(hipGetLastError());
+      hipLaunchKernelGGL(sync_scan_kernel, dim3(4 * n_def), dim3(256), 0, s, streams, d_job_wave0, A);
       PTWM_HIP_TRY(hipGetLastError());
       hipLaunchKernelGGL(sync_write_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables,
                          A);
@@ -406,8 +490,7 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   if (!again.empty()) {
     const size_t na = again.size();
     PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, again.data(), na * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
-    PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr), status, (uint32_t)na, nullptr,
-                                     nullptr, s));
+    PTWM_HIP_TRY(launch_decode_exact(d_jobs, status, (uint32_t)na, nullptr, nullptr, nullptr, s));
     std::vector<uint32_t> st2(na);
     PTWM_HIP_TRY(hipMemcpyAsync(st2.data(), status, na * 4, hipMemcpyDeviceToHost, s));
     PTWM_HIP_TRY(hipStreamSynchronize(s));

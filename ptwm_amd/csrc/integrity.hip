@@ -129,7 +129,7 @@ __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restri
   auto step = [&](uint64_t k) {
     u32x4 v[kRatio], pl[kNp];
 #pragma unroll
-    for (int h = 0; h < kRatio; ++h) v[h] = __builtin_nontemporal_load(p + k * kThreads * kRatio + h);
+    for (int h = 0; h < kRatio; ++h) v[h] = g_ld_nt16(reinterpret_cast<uint64_t>(p + k * kThreads * kRatio + h));
     forward16<kChain>(v, pl);
 #pragma unroll
     for (int j = 0; j < kNp; ++j) acc[j] = crc_piece(T, sliced(S, acc[j]), pl[j]);
@@ -156,11 +156,10 @@ __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restri
       end = base + kPiece;
       any = true;
     } else if (base < R.n) {
-      const uint8_t* b = reinterpret_cast<const uint8_t*>(R.src);
 #pragma unroll
       for (int j = 0; j < kNp; ++j) {
         uint32_t c = sliced(S, acc[j]);
-        for (uint64_t i = base; i < R.n; ++i) c = T[(c ^ forward_byte<kChain>(b, i, j)) & 255u] ^ (c >> 8);
+        for (uint64_t i = base; i < R.n; ++i) c = T[(c ^ forward_byte<kChain>(R.src, i, j)) & 255u] ^ (c >> 8);
         acc[j] = c;
       }
       end = R.n;
@@ -234,8 +233,8 @@ __global__ void __launch_bounds__(64) xxh64_kernel(const HashTask* __restrict__ 
   uint64_t v = l == 0 ? kXP1 + kXP2 : l == 1 ? kXP2 : l == 2 ? 0 : 0 - kXP1;
   u32x4 a = u32x4_make(0, 0, 0, 0), b = a;
   if (l < stripes) {
-    a = __builtin_nontemporal_load(src + 2 * l);
-    b = __builtin_nontemporal_load(src + 2 * l + 1);
+    a = g_ld_nt16(reinterpret_cast<uint64_t>(src + 2 * l));
+    b = g_ld_nt16(reinterpret_cast<uint64_t>(src + 2 * l + 1));
   }
   for (uint64_t s0 = 0; s0 < stripes; s0 += 64) {
     if (s0 + l < stripes) {
@@ -247,8 +246,8 @@ __global__ void __launch_bounds__(64) xxh64_kernel(const HashTask* __restrict__ 
     __syncthreads();
     const uint64_t sn = s0 + 64 + l;  // next block, loaded while lanes 0-3 run the chains
     if (sn < stripes) {
-      a = __builtin_nontemporal_load(src + 2 * sn);
-      b = __builtin_nontemporal_load(src + 2 * sn + 1);
+      a = g_ld_nt16(reinterpret_cast<uint64_t>(src + 2 * sn));
+      b = g_ld_nt16(reinterpret_cast<uint64_t>(src + 2 * sn + 1));
     }
     const uint32_t cnt = (uint32_t)(stripes - s0 < 64 ? stripes - s0 : 64);
     if (l < 4)

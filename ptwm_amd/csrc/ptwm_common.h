@@ -21,6 +21,21 @@ __host__ __device__ inline u32x4 u32x4_make(uint32_t a, uint32_t b, uint32_t c, 
   return r;
 }
 
+// Global-memory accesses in address space 1.  Generic (flat) accesses also
+// count against the LDS wait counter, so a kernel that mixes LDS lookups
+// with flat loads or stores waits for memory on every LDS use.
+template <typename T>
+__device__ __forceinline__ T g_ld(uint64_t a) {
+  return *(const __attribute__((address_space(1))) T*)(uintptr_t)a;
+}
+template <typename T>
+__device__ __forceinline__ void g_st(uint64_t a, T v) {
+  *(__attribute__((address_space(1))) T*)(uintptr_t)a = v;
+}
+__device__ __forceinline__ u32x4 g_ld_nt16(uint64_t a) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4*)(uintptr_t)a);
+}
+
 constexpr int64_t kOk = 0;
 constexpr int64_t kInvalidInput = -1;
 constexpr int64_t kBufferTooSmall = -2;

@@ -41,6 +41,12 @@ __device__ __forceinline__ uint8_t gbyte(uint64_t a) {
   return *(const __attribute__((address_space(1))) uint8_t*)(uintptr_t)a;
 }
 
+// atomic OR into global memory (not a flat atomic: see g_ld)
+__device__ __forceinline__ void or_global(uint32_t* p, uint32_t v) {
+  __hip_atomic_fetch_or((__attribute__((address_space(1))) uint32_t*)(uintptr_t)p, v, __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // 256-bin histogram per job (blockIdx.y); any source alignment.
 __global__ void __launch_bounds__(256) ref_hist_kernel(const RefJobDev* __restrict__ jobs, uint32_t* __restrict__ hist) {
   __shared__ uint32_t h[4][256];
@@ -53,7 +59,7 @@ __global__ void __launch_bounds__(256) ref_hist_kernel(const RefJobDev* __restri
   const uint64_t stride = (uint64_t)gridDim.x * 256u;
   const u32x4* v = reinterpret_cast<const u32x4*>(J.src + head);
   for (uint64_t i = (uint64_t)blockIdx.x * 256u + t; i < nvec; i += stride) {
-    const u32x4 x = __builtin_nontemporal_load(v + i);
+    const u32x4 x = g_ld_nt16(reinterpret_cast<uint64_t>(v + i));
     const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k)
@@ -142,13 +148,13 @@ __global__ void __launch_bounds__(256) ref_huf_pack_kernel(const RefSegDev* __re
       acc |= (uint64_t)(sym_code[k] & 0xFFFFu) << fill;
       fill += l;
       if (fill >= 32) {
-        atomicOr(area + (W - 1 - w), __builtin_bswap32((uint32_t)acc));
+        or_global(area + (W - 1 - w), __builtin_bswap32((uint32_t)acc));
         acc >>= 32;
         fill -= 32;
         ++w;
       }
     }
-    if (fill) atomicOr(area + (W - 1 - w), __builtin_bswap32((uint32_t)acc));
+    if (fill) or_global(area + (W - 1 - w), __builtin_bswap32((uint32_t)acc));
     __syncthreads();
     if (t == 0) s_base += pass_bits;
     __syncthreads();
@@ -165,12 +171,12 @@ __global__ void __launch_bounds__(64) ref_rans_kernel(const RefSegDev* __restric
   const uint32_t s = blockIdx.x * 64u + threadIdx.x;
   if (s >= n_segs) return;
   const RefSegDev S = segs[s];
-  const uint4* tab = tables + 256u * S.table;
-  uint8_t* out = scratch + S.scratch_byte;
+  const uint64_t tab = reinterpret_cast<uint64_t>(tables + 256u * S.table);
+  const uint64_t out = reinterpret_cast<uint64_t>(scratch + S.scratch_byte);
   uint32_t x = kRansL;
   uint64_t nb = 4;
   for (uint64_t k = S.n; k > 0; --k) {
-    const uint4 e = tab[gbyte(S.src + k - 1)];
+    const u32x4 e = g_ld<u32x4>(tab + 16ull * gbyte(S.src + k - 1));
     const uint32_t freq = (e.z >> 12) & 0xFFFu;
     if (freq == 0) {  // a symbol the table does not code: refuse (seg_len 0)
       seg_len[s] = 0;
@@ -178,16 +184,16 @@ __global__ void __launch_bounds__(64) ref_rans_kernel(const RefSegDev* __restric
     }
     const uint32_t max_state = freq << 20;  // ((RANS_L >> PROB_BITS) << 8) * freq
     while (x >= max_state) {
-      out[nb++] = (uint8_t)(x & 0xFFu);
+      g_st<uint8_t>(out + nb++, (uint8_t)(x & 0xFFu));
       x >>= 8;
     }
     const uint32_t q = __umulhi(x, e.x) >> (e.z >> 24);
     x = x + e.y + q * (e.z & 0xFFFu);
   }
-  out[0] = (uint8_t)x;
-  out[1] = (uint8_t)(x >> 8);
-  out[2] = (uint8_t)(x >> 16);
-  out[3] = (uint8_t)(x >> 24);
+  g_st<uint8_t>(out, (uint8_t)x);
+  g_st<uint8_t>(out + 1, (uint8_t)(x >> 8));
+  g_st<uint8_t>(out + 2, (uint8_t)(x >> 16));
+  g_st<uint8_t>(out + 3, (uint8_t)(x >> 24));
   seg_len[s] = nb;
 }
 
@@ -196,11 +202,9 @@ __global__ void __launch_bounds__(64) ref_rans_kernel(const RefSegDev* __restric
 // bytes, emitted in the reverse of decoder order).
 __global__ void __launch_bounds__(256) ref_copy_kernel(const RefCopyOp* __restrict__ ops) {
   const RefCopyOp op = ops[blockIdx.x];
-  const uint8_t* src = reinterpret_cast<const uint8_t*>(op.src);
-  uint8_t* dst = reinterpret_cast<uint8_t*>(op.dst);
   const uint64_t fwd = op.rev_from < op.n ? op.rev_from : op.n;
-  for (uint64_t i = threadIdx.x; i < fwd; i += 256) dst[i] = src[i];
-  for (uint64_t i = fwd + threadIdx.x; i < op.n; i += 256) dst[i] = src[op.n - 1 - (i - fwd)];
+  for (uint64_t i = threadIdx.x; i < fwd; i += 256) g_st<uint8_t>(op.dst + i, gbyte(op.src + i));
+  for (uint64_t i = fwd + threadIdx.x; i < op.n; i += 256) g_st<uint8_t>(op.dst + i, gbyte(op.src + op.n - 1 - (i - fwd)));
 }
 
 // ---- host restatements of the reference's table construction ----

@@ -47,7 +47,7 @@ struct DevCtx {
       ref_rans_len, ref_hdr, ref_pack, ref_ops;
   PinnedBuffer h_enc, h_ilv;
   // parallel Huffman decode of reference streams
-  DeviceBuffer sync_streams, sync_tables, sync_sub, sync_waves;
+  DeviceBuffer sync_streams, sync_tables, sync_sub, sync_waves, copy_args;
   // integrity (CRC-32 / XXH64) tables and arguments
   DeviceBuffer crc_tab, crc_args, hash_args;
   bool crc_tab_ready = false;

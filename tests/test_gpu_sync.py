@@ -118,3 +118,18 @@ def test_parallel_huffman_malformed_matches_reference_outcome():
         assert (got is None) == (want is None), name
         if want is not None:
             assert got == want, name
+
+
+@pytest.mark.parametrize("n", [4095, 4096, 4097, 65536, 65539, (1 << 20) + 1, 3 * (1 << 20) + 7])
+def test_stored_payload_copy(n):
+    """Stored (tag 0) payloads of 4 KiB and more are copied by the
+    multi-workgroup copy kernel; the source sits one byte past the tag."""
+    plane = np.random.default_rng(n).integers(0, 256, n, dtype=np.uint8).tobytes()
+    for codec, name in [(O.CODEC_HUFFMAN, "huffman"), (O.CODEC_RANS, "rans")]:
+        payload = O.codec_encode(codec, plane)
+        assert payload[0] == 0
+        note(f"stored copy {name} n={n}")
+        out = torch.zeros(n + 16, dtype=torch.uint8, device="cuda:0")
+        got = api.plane_codec_decode_cuda(SEL, name, b"", dev(payload), out[:n], 0)
+        torch.cuda.synchronize()
+        assert got == n and out[:n].cpu().numpy().tobytes() == plane
