@@ -394,3 +394,30 @@ def ilv_decode(payload, cap: int) -> bytes:
     if n < 0:
         raise OracleError(n, "ilv_decode")
     return out[:n].tobytes()
+
+
+def rans_ilv_encode(plane) -> bytes:
+    """rans_ilv (this build's GPU-native interleaved rANS codec) payload of
+    a plane: the format's specification (por_rans_ilv_encode)."""
+    L = lib()
+    L.por_rans_ilv_encode.restype = C.c_int64
+    L.por_rans_ilv_encode.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]
+    s = _buf(plane)
+    cap = s.size + 1
+    out = np.zeros(cap, np.uint8)
+    n = L.por_rans_ilv_encode(_ptr(s), s.size, _ptr(out), cap)
+    if n < 0:
+        raise OracleError(n, "rans_ilv_encode")
+    return out[:n].tobytes()
+
+
+def rans_ilv_decode(payload, cap: int) -> bytes:
+    L = lib()
+    L.por_rans_ilv_decode.restype = C.c_int64
+    L.por_rans_ilv_decode.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]
+    p = _buf(payload)
+    out = np.zeros(max(cap, 1), np.uint8)
+    n = L.por_rans_ilv_decode(_ptr(p), p.size, _ptr(out), cap)
+    if n < 0:
+        raise OracleError(n, "rans_ilv_decode")
+    return out[:n].tobytes()

@@ -1053,6 +1053,159 @@ int64_t por_ilv_decode(const uint8_t *p, size_t len, uint8_t *out, size_t cap) {
 }
 
 /* ------------------------------------------------------------------------- */
+/* rans_ilv: this build's GPU-native interleaved rANS plane codec (no          */
+/* reference counterpart; this function pair is its specification).          */
+/*   [0x00][plane]  stored (empty plane: [0x00])                              */
+/*   [0x01][n u32][max_sym u8][f u16 x (max_sym + 1)][0-pad to 4]             */
+/*        [off u32 x (nb + 1)][blocks], nb = ceil(n / 16384)                  */
+/*   frequencies: the reference's normalisation (rans/compress.rs:72-135,     */
+/*   11-bit, sum 2048).  Block b: [nw u32][x_j u32 x 64][w u16 x nw][0-pad    */
+/*   to 4].  Step s = 0..255 (r = s / 16, t = s % 16): lanes j = 0..63 in     */
+/*   order whose position P = 16384 b + 16 (64 r + j) + t is < n decode       */
+/*   slot = x & 2047, x = f (x >> 11) + slot - cum, and when x < 2^16 take     */
+/*   the next word: x = x << 16 | w.  The encoder starts every lane at 2^16,   */
+/*   so a block is accepted iff all nw words are taken and every final        */
+/*   state is 2^16.                                                            */
+/* ------------------------------------------------------------------------- */
+
+#define RILV_L (1u << 16)
+
+static size_t rilv_pos(size_t b, int j, int s) {
+    return b * ILV_BLOCK + (size_t)ILV_GROUP * ((size_t)ILV_LANES * (size_t)(s / ILV_GROUP) + (size_t)j) +
+           (size_t)(s % ILV_GROUP);
+}
+
+int64_t por_rans_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap) {
+    if (n == 0) { if (cap < 1) return POR_ESMALL; out[0] = 0; return 1; }
+    uint32_t raw[256];
+    por_histogram(plane, n, raw);
+    uint16_t f[256], cum[256];
+    if (n <= 0xFFFFFFFFu && por_rans_normalize(raw, f, cum)) {
+        int max_sym = 0;
+        for (int i = 0; i < 256; i++) if (raw[i]) max_sym = i;
+        size_t nb = (n + ILV_BLOCK - 1) / ILV_BLOCK;
+        size_t head = 5 + 1 + 2 * (size_t)(max_sym + 1);
+        head += (4 - head % 4) % 4;
+        size_t data0 = head + 4 * (nb + 1);
+        /* encode every block into scratch: words in decode order, states */
+        uint16_t *words = (uint16_t *)malloc(ILV_BLOCK * sizeof(uint16_t));
+        uint32_t *bw = (uint32_t *)malloc(nb * sizeof(uint32_t));
+        size_t total = 0;
+        for (size_t b = 0; b < nb; b++) {
+            size_t nwb = 0;
+            uint32_t x[ILV_LANES];
+            for (int j = 0; j < ILV_LANES; j++) x[j] = RILV_L;
+            for (int s = ILV_BLOCK / ILV_LANES - 1; s >= 0; s--)
+                for (int j = 0; j < ILV_LANES; j++) {
+                    size_t P = rilv_pos(b, j, s);
+                    if (P >= n) continue;
+                    uint32_t fs = f[plane[P]];
+                    if ((uint64_t)x[j] >= ((uint64_t)fs << 21)) { nwb++; x[j] >>= 16; }
+                    x[j] = (x[j] / fs) * 2048u + (x[j] % fs) + cum[plane[P]];
+                }
+            bw[b] = (uint32_t)nwb;
+            total += (4 + 256 + 2 * nwb + 3) & ~(size_t)3;
+        }
+        if (data0 + total < 1 + n && data0 + total <= cap && total <= 0xFFFFFFFFu) {
+            memset(out, 0, data0 + total);
+            out[0] = 1; st32(out + 1, (uint32_t)n);
+            out[5] = (uint8_t)max_sym;
+            for (int i = 0; i <= max_sym; i++) { out[6 + 2 * i] = (uint8_t)f[i]; out[7 + 2 * i] = (uint8_t)(f[i] >> 8); }
+            size_t off = 0;
+            for (size_t b = 0; b < nb; b++) {
+                st32(out + head + 4 * b, (uint32_t)off);
+                uint8_t *blk = out + data0 + off;
+                uint32_t x[ILV_LANES];
+                for (int j = 0; j < ILV_LANES; j++) x[j] = RILV_L;
+                size_t tail = bw[b];                     /* words fill from the end, a step at a time */
+                for (int s = ILV_BLOCK / ILV_LANES - 1; s >= 0; s--) {
+                    int ne = 0;
+                    uint16_t ew[ILV_LANES];
+                    for (int j = 0; j < ILV_LANES; j++) {
+                        size_t P = rilv_pos(b, j, s);
+                        if (P >= n) continue;
+                        uint32_t fs = f[plane[P]];
+                        if ((uint64_t)x[j] >= ((uint64_t)fs << 21)) { ew[ne++] = (uint16_t)x[j]; x[j] >>= 16; }
+                        x[j] = (x[j] / fs) * 2048u + (x[j] % fs) + cum[plane[P]];
+                    }
+                    tail -= (size_t)ne;
+                    for (int i = 0; i < ne; i++) words[tail + (size_t)i] = ew[i];
+                }
+                st32(blk, bw[b]);
+                for (int j = 0; j < ILV_LANES; j++) st32(blk + 4 + 4 * j, x[j]);
+                for (size_t i = 0; i < bw[b]; i++) { blk[260 + 2 * i] = (uint8_t)words[i]; blk[261 + 2 * i] = (uint8_t)(words[i] >> 8); }
+                off += (4 + 256 + 2 * (size_t)bw[b] + 3) & ~(size_t)3;
+            }
+            st32(out + head + 4 * nb, (uint32_t)off);
+            free(words); free(bw);
+            return (int64_t)(data0 + total);
+        }
+        free(words); free(bw);
+    }
+    if (1 + n > cap) return POR_ESMALL;
+    out[0] = 0;
+    memcpy(out + 1, plane, n);
+    return (int64_t)(1 + n);
+}
+
+int64_t por_rans_ilv_decode(const uint8_t *p, size_t len, uint8_t *out, size_t cap) {
+    if (len == 0) return POR_EINVAL;
+    if (p[0] == 0) {
+        if (len - 1 > cap) return POR_ESMALL;
+        memcpy(out, p + 1, len - 1);
+        return (int64_t)(len - 1);
+    }
+    if (p[0] != 1 || len < 6) return POR_EINVAL;
+    size_t n = ld32(p + 1);
+    if (n > cap) return POR_ESMALL;
+    int max_sym = p[5];
+    size_t head = 5 + 1 + 2 * (size_t)(max_sym + 1);
+    if (head > len) return POR_EINVAL;
+    uint32_t tab[2048];
+    uint32_t run = 0;
+    for (int i = 0; i <= max_sym; i++) {
+        uint32_t fi = (uint32_t)p[6 + 2 * i] | ((uint32_t)p[7 + 2 * i] << 8);
+        if (run + fi > 2048) return POR_EINVAL;
+        for (uint32_t k = 0; k < fi; k++) tab[run + k] = (uint32_t)i | (fi << 8) | (k << 20);  /* k = slot - cum */
+        run += fi;
+    }
+    if (run != 2048) return POR_EINVAL;
+    head += (4 - head % 4) % 4;
+    size_t nb = (n + ILV_BLOCK - 1) / ILV_BLOCK, data0 = head + 4 * (nb + 1);
+    if (data0 > len) return POR_EINVAL;
+    size_t dlen = len - data0;
+    for (size_t i = 5 + 1 + 2 * (size_t)(max_sym + 1); i < head; i++) if (p[i]) return POR_EINVAL;
+    if (ld32(p + head) != 0 || ld32(p + head + 4 * nb) != dlen) return POR_EINVAL;
+    for (size_t b = 0; b < nb; b++) {
+        size_t o0 = ld32(p + head + 4 * b), o1 = ld32(p + head + 4 * (b + 1));
+        if (o1 < o0 || o1 > dlen || o1 - o0 < 260) return POR_EINVAL;
+        const uint8_t *blk = p + data0 + o0;
+        size_t nwb = ld32(blk);
+        if (((4 + 256 + 2 * nwb + 3) & ~(size_t)3) != o1 - o0) return POR_EINVAL;
+        if (nwb & 1) { if (blk[260 + 2 * nwb] || blk[261 + 2 * nwb]) return POR_EINVAL; }
+        uint32_t x[ILV_LANES];
+        for (int j = 0; j < ILV_LANES; j++) x[j] = ld32(blk + 4 + 4 * j);
+        size_t pos = 0;
+        for (int s = 0; s < ILV_BLOCK / ILV_LANES; s++)
+            for (int j = 0; j < ILV_LANES; j++) {
+                size_t P = rilv_pos(b, j, s);
+                if (P >= n) continue;
+                uint32_t e = tab[x[j] & 2047u];
+                out[P] = (uint8_t)e;
+                x[j] = ((e >> 8) & 0xFFFu) * (x[j] >> 11) + (e >> 20);
+                if (x[j] < RILV_L) {
+                    if (pos >= nwb) return POR_EINVAL;
+                    x[j] = (x[j] << 16) | ((uint32_t)blk[260 + 2 * pos] | ((uint32_t)blk[261 + 2 * pos] << 8));
+                    pos++;
+                }
+            }
+        if (pos != nwb) return POR_EINVAL;
+        for (int j = 0; j < ILV_LANES; j++) if (x[j] != RILV_L) return POR_EINVAL;
+    }
+    return (int64_t)n;
+}
+
+/* ------------------------------------------------------------------------- */
 /* CRC-32/ISO-HDLC (crc32fast 1.5.0), reflected poly 0xEDB88320              */
 /* ------------------------------------------------------------------------- */
 
