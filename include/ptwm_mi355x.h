@@ -98,8 +98,9 @@ int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_versi
 /* ABI revision of this library (bumped on any incompatible change). */
 uint32_t ptwm_mi355x_abi_version(void);
 
-/* The canonical ids this library recognises: which = 0 own plane codec,
- * 1 hardware backend, 2 decode-plan format.  Writes 32 bytes; returns 0 or -1. */
+/* The canonical ids this library recognises: which = 0 own plane codec
+ * (huff_ilv), 1 hardware backend, 2 decode-plan format, 3 own rANS plane
+ * codec (rans_ilv).  Writes 32 bytes; returns 0 or -1. */
 int64_t ptwm_mi355x_canonical_id(uint32_t which, uint8_t *out32);
 
 /* Forward chain (bit reorder + byte/nibble split) on device: the tensor at
@@ -125,6 +126,13 @@ int64_t ptwm_mi355x_merge_cuda(uint32_t chain, const uint64_t *plane_dev_ptrs, u
 int64_t ptwm_mi355x_encode_tensor_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
                                        size_t out_cap, uint8_t *plan_out, size_t plan_cap, size_t *plan_len_out,
                                        uint64_t *needed_out, uint32_t device_ordinal);
+
+/* The same with this library's GPU-native rANS codec (rans_ilv, wire id
+ * 0x7F02): every plane coded with rans_ilv, stored as Identity when coding
+ * does not shrink it.  No counterpart in the reference (a new codec id). */
+int64_t ptwm_mi355x_encode_tensor_rans_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                                            size_t out_cap, uint8_t *plan_out, size_t plan_cap, size_t *plan_len_out,
+                                            uint64_t *needed_out, uint32_t device_ordinal);
 
 /* Tensor-level encode into the reference's own plane formats: the tensor is
  * split by `chain`, and plane p is coded with plane_codecs[p] (wire id 0x0000

@@ -134,19 +134,20 @@ def hardware_backend_dispatch_decode_cuda(canonical_id: str, codec_id: str, stat
     return check(rc, "hardware_backend_dispatch_decode_cuda")
 
 
-def encode_tensor_cuda(chain: int, src, out, device_ordinal: int = 0) -> tuple[int, bytes]:
+def encode_tensor_cuda(chain: int, src, out, device_ordinal: int = 0, codec: str = "huff_ilv") -> tuple[int, bytes]:
     """Tensor-level GPU encode (library addition): split by ``chain``, code
-    every plane with huff_ilv (Identity when coding does not shrink it).
-    Returns (bytes used in ``out``, PTMD decode plan)."""
+    every plane with this library's GPU-native codec ``codec`` ("huff_ilv"
+    or "rans_ilv"; Identity when coding does not shrink a plane).  Returns
+    (bytes used in ``out``, PTMD decode plan)."""
     L = lib()
+    fn = {"huff_ilv": L.ptwm_mi355x_encode_tensor_cuda, "rans_ilv": L.ptwm_mi355x_encode_tensor_rans_cuda}[codec]
     stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
     ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)
     op, ol = _dev_ptr_len(out, "out", device_ordinal, stream, True)
     plan_buf = (C.c_uint8 * 4096)()
     plan_len = C.c_size_t(0)
     needed = C.c_uint64(0)
-    rc = L.ptwm_mi355x_encode_tensor_cuda(chain, ip, il, op, ol, plan_buf, 4096, C.byref(plan_len), C.byref(needed),
-                                          device_ordinal)
+    rc = fn(chain, ip, il, op, ol, plan_buf, 4096, C.byref(plan_len), C.byref(needed), device_ordinal)
     if rc == -2:
         err = NativeError(rc, f"encode_tensor_cuda: needs {needed.value} bytes")
         err.needed = needed.value

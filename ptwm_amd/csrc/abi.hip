@@ -35,12 +35,15 @@ constexpr KnownId kBuiltinIds[] = {
     {"87c8ca053fbd0646c07d18da4d0396a92550eb6d44bcd4e461538902874d4bc7", kCodecRans},      // rans@1.0.0
     // this extension: blake3([0;32] || 0 || "io.ptwm.mi355x.plane_codec" || 0 || "0.1.0")
     {"cfd8cc03483eb4a43cdddb4b3cbf95b32e0a3f0e17e5ec85a0b52de04e8caf04", kCodecHuffIlv},
+    // blake3([0;32] || 0 || "io.ptwm.mi355x.plane_codec.rans" || 0 || "0.1.0")
+    {"968f8be9f06b14b33fcd066622493f1101954d074c25d63e78380d33708fe1f5", kCodecRansIlv},
 };
 // blake3([0;32] || 0 || "io.ptwm.mi355x.hardware_backend" || 0 || "0.1.0")
 constexpr const char* kBackendIdHex = "a432dc02f57030b41a3660762bbcec5668cde8abbc807999d56ca0a3304d39cf";
 // blake3([0;32] || 0 || "io.ptwm.mi355x.decode_plan" || 0 || "0.1.0")
 constexpr const char* kPlanIdHex = "1b0e48b156b01d0d733a5aa62a90bcbde34945ff024d8d8e56cb714a48c6e770";
 constexpr const char* kOwnCodecIdHex = "cfd8cc03483eb4a43cdddb4b3cbf95b32e0a3f0e17e5ec85a0b52de04e8caf04";
+constexpr const char* kRansCodecIdHex = "968f8be9f06b14b33fcd066622493f1101954d074c25d63e78380d33708fe1f5";
 
 bool hex_eq(const char* hex, const uint8_t* id) {
   for (int i = 0; i < 32; ++i) {
@@ -125,8 +128,10 @@ int64_t decode_one_payload(DevCtx& ctx, uint32_t codec, uint64_t in_dev, size_t 
   return (int64_t)expected;
 }
 
-// One huff_ilv payload -> plane bytes (fused kernel, passthrough chain).
-int64_t ilv_decode_payload(DevCtx& ctx, uint64_t in_dev, size_t in_len, uint64_t out_dev, size_t out_cap) {
+// One huff_ilv or rans_ilv payload -> plane bytes (fused kernel,
+// passthrough chain).
+int64_t ilv_decode_payload(DevCtx& ctx, uint64_t in_dev, size_t in_len, uint64_t out_dev, size_t out_cap,
+                           uint32_t family = kFamilyHuff) {
   if (in_len == 0) return kInvalidInput;
   PTWM_HIP_TRY(ctx.h_small.ensure(64));
   uint8_t* hdr = static_cast<uint8_t*>(ctx.h_small.ptr);
@@ -158,6 +163,7 @@ int64_t ilv_decode_payload(DevCtx& ctx, uint64_t in_dev, size_t in_len, uint64_t
   X.planes[0].base = in_dev;
   X.planes[0].len = in_len;
   X.planes[0].coded = 1;
+  X.family = family;
   int64_t rc = ilv_decode_tensors(ctx, std::vector<IlvTensor>{X});
   return rc == kOk ? (int64_t)expected : rc;
 }
@@ -176,7 +182,11 @@ uint32_t ptwm_mi355x_abi_version(void) { return 1; }
 
 int64_t ptwm_mi355x_canonical_id(uint32_t which, uint8_t* out32) {
   if (!out32) return kInvalidInput;
-  const char* hex = which == 0 ? kOwnCodecIdHex : which == 1 ? kBackendIdHex : which == 2 ? kPlanIdHex : nullptr;
+  const char* hex = which == 0   ? kOwnCodecIdHex
+                    : which == 1 ? kBackendIdHex
+                    : which == 2 ? kPlanIdHex
+                    : which == 3 ? kRansCodecIdHex
+                                 : nullptr;
   if (!hex) return kInvalidInput;
   hex_to(hex, out32);
   return 0;
@@ -204,6 +214,8 @@ int64_t ptwm_plane_codec_v1_decode_cuda(uint8_t state_format_version, const uint
   DeviceScope ds(device_ordinal);
   if (!ds.ok) return kInvalidInput;
   if (codec == kCodecHuffIlv) return ilv_decode_payload(*ds.ctx, in_dev_ptr, in_len, out_dev_ptr, out_cap);
+  if (codec == kCodecRansIlv)
+    return ilv_decode_payload(*ds.ctx, in_dev_ptr, in_len, out_dev_ptr, out_cap, kFamilyRans);
   return decode_one_payload(*ds.ctx, codec, in_dev_ptr, in_len, out_dev_ptr, out_cap);
 }
 
@@ -244,13 +256,15 @@ int64_t ptwm_plane_codec_v1_encode_cuda(uint8_t state_format_version, const uint
     rc = enc.write(*ds.ctx, {out_dev_ptr});
     return rc < 0 ? rc : (int64_t)len[0];
   }
-  if (codec != kCodecHuffIlv) return kUnsupported;
+  if (codec != kCodecHuffIlv && codec != kCodecRansIlv) return kUnsupported;
   if ((in_dev_ptr & 15u) || (out_dev_ptr & 3u)) return kInvalidInput;
   DeviceScope ds(device_ordinal);
   if (!ds.ok) return kInvalidInput;
   IlvEncResult r{};
   uint64_t needed = 0, n = in_len;
-  int64_t rc = ilv_encode_planes(*ds.ctx, &in_dev_ptr, &n, 1, out_dev_ptr, out_cap, false, &r, &needed);
+  int64_t rc = codec == kCodecHuffIlv
+                   ? ilv_encode_planes(*ds.ctx, &in_dev_ptr, &n, 1, out_dev_ptr, out_cap, false, &r, &needed)
+                   : rilv_encode_planes(*ds.ctx, &in_dev_ptr, &n, 1, out_dev_ptr, out_cap, false, &r, &needed);
   if (rc == kBufferTooSmall && needed_out) *needed_out = needed;
   return rc < 0 ? rc : (int64_t)r.len;
 }
@@ -374,9 +388,9 @@ int64_t ptwm_mi355x_merge_cuda(uint32_t chain, const uint64_t* plane_dev_ptrs, u
   return (int64_t)out_len;
 }
 
-int64_t ptwm_mi355x_encode_tensor_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
-                                       size_t out_cap, uint8_t* plan_out, size_t plan_cap, size_t* plan_len_out,
-                                       uint64_t* needed_out, uint32_t device_ordinal) {
+static int64_t encode_tensor_native(uint32_t family, uint32_t chain, uint64_t in_dev_ptr, size_t in_len,
+                                    uint64_t out_dev_ptr, size_t out_cap, uint8_t* plan_out, size_t plan_cap,
+                                    size_t* plan_len_out, uint64_t* needed_out, uint32_t device_ordinal) {
   const int np = chain_planes(chain);
   if (np < 0 || !plan_out || !plan_len_out) return kInvalidInput;
   const uint64_t ratio = (uint64_t)chain_ratio(chain);
@@ -402,7 +416,9 @@ int64_t ptwm_mi355x_encode_tensor_cuda(uint32_t chain, uint64_t in_dev_ptr, size
     return kInvalidInput;
   IlvEncResult r[4] = {};
   uint64_t needed = 0;
-  int64_t rc = ilv_encode_planes(ctx, srcs, lens, (uint32_t)np, out_dev_ptr, out_cap, true, r, &needed);
+  int64_t rc = family == kFamilyHuff
+                   ? ilv_encode_planes(ctx, srcs, lens, (uint32_t)np, out_dev_ptr, out_cap, true, r, &needed)
+                   : rilv_encode_planes(ctx, srcs, lens, (uint32_t)np, out_dev_ptr, out_cap, true, r, &needed);
   if (rc == kBufferTooSmall && needed_out) *needed_out = needed;
   if (rc < 0) return rc;
   // decode plan (PTMD v1) for the one tensor
@@ -425,6 +441,20 @@ int64_t ptwm_mi355x_encode_tensor_cuda(uint32_t chain, uint64_t in_dev_ptr, size
   }
   *plan_len_out = (size_t)(o - plan_out);
   return rc;
+}
+
+int64_t ptwm_mi355x_encode_tensor_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                                       size_t out_cap, uint8_t* plan_out, size_t plan_cap, size_t* plan_len_out,
+                                       uint64_t* needed_out, uint32_t device_ordinal) {
+  return encode_tensor_native(kFamilyHuff, chain, in_dev_ptr, in_len, out_dev_ptr, out_cap, plan_out, plan_cap,
+                              plan_len_out, needed_out, device_ordinal);
+}
+
+int64_t ptwm_mi355x_encode_tensor_rans_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                                            size_t out_cap, uint8_t* plan_out, size_t plan_cap, size_t* plan_len_out,
+                                            uint64_t* needed_out, uint32_t device_ordinal) {
+  return encode_tensor_native(kFamilyRans, chain, in_dev_ptr, in_len, out_dev_ptr, out_cap, plan_out, plan_cap,
+                              plan_len_out, needed_out, device_ordinal);
 }
 
 int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane_codecs, uint32_t n_codecs,

@@ -22,8 +22,14 @@ constexpr uint32_t kIlvErrLane = 4;     // a lane's word count disagrees with it
 struct IlvPlane {
   uint64_t base;   // coded: payload address; raw: plane bytes (16-byte aligned)
   uint64_t len;    // coded: payload length
-  uint32_t coded;  // 1: huff_ilv coded payload; 0: raw plane bytes
+  uint32_t coded;  // 1: coded payload of the tensor's codec family; 0: raw plane bytes
   uint32_t lut;    // LDS table slot of a coded plane
+};
+
+// Codec family of a fused tensor: which GPU-native codec its coded planes use.
+enum IlvFamily : uint32_t {
+  kFamilyHuff = 0,  // huff_ilv (this file)
+  kFamilyRans = 1,  // rans_ilv (rans_ilv.h)
 };
 
 struct IlvTensor {
@@ -32,6 +38,8 @@ struct IlvTensor {
   uint32_t chain;
   uint32_t n_planes;
   IlvPlane planes[4];
+  uint32_t family;  // IlvFamily
+  uint32_t pad;
 };
 
 struct IlvEncPlane {

@@ -148,6 +148,43 @@ int huf_encode_weights(const uint8_t lengths[256], uint8_t* out) {
   return o;
 }
 
+constexpr uint32_t kRansNormScale = 2048;  // 1 << PROB_BITS (rans/compress.rs)
+
+// normalize_freqs (rans/compress.rs:72-122): returns false when it fails.
+bool rans_normalize_freqs(const uint32_t raw[256], uint16_t f[256], uint16_t cum[256], int* max_sym_out) {
+  uint64_t total = 0;
+  for (int i = 0; i < 256; ++i) total += raw[i];
+  std::memset(f, 0, 512);
+  std::memset(cum, 0, 512);
+  if (total == 0) return false;
+  uint32_t assigned = 0;
+  int max_sym = 0, max_freq_sym = 0;
+  for (int i = 0; i < 256; ++i) {
+    if (raw[i] > 0) {
+      uint64_t v = ((uint64_t)raw[i] * kRansNormScale) / total;
+      if (v < 1) v = 1;
+      f[i] = (uint16_t)v;
+      assigned += f[i];
+      max_sym = i;
+      if (raw[i] > raw[max_freq_sym]) max_freq_sym = i;
+    }
+  }
+  if (assigned > kRansNormScale) {
+    const uint32_t excess = assigned - kRansNormScale;
+    if ((uint32_t)f[max_freq_sym] > excess) f[max_freq_sym] = (uint16_t)(f[max_freq_sym] - excess);
+    else return false;
+  } else if (assigned < kRansNormScale) {
+    f[max_freq_sym] = (uint16_t)(f[max_freq_sym] + (kRansNormScale - assigned));
+  }
+  uint16_t run = 0;
+  for (int i = 0; i <= max_sym; ++i) {
+    cum[i] = run;
+    run = (uint16_t)(run + f[i]);
+  }
+  *max_sym_out = max_sym;
+  return true;
+}
+
 }  // namespace ptwm
 
 extern "C" int64_t ptwm_mi355x_huffman_code_lengths(const uint32_t* freqs, uint8_t* lengths_out) {

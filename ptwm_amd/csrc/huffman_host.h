@@ -24,4 +24,10 @@ int huf_canonical(const uint8_t lengths[256], uint16_t rev_codes[256]);
 // Weights header (weights.rs:8-32) into out (<= 130 bytes); returns its length.
 int huf_encode_weights(const uint8_t lengths[256], uint8_t* out);
 
+// rANS frequency normalisation of the reference (rans/compress.rs:72-122):
+// 11-bit frequencies summing to 2048, at least 1 for every present symbol,
+// the excess or deficit absorbed by the first most frequent symbol.
+// Returns false when that fails (the reference then stores the plane).
+bool rans_normalize_freqs(const uint32_t raw[256], uint16_t f[256], uint16_t cum[256], int* max_sym_out);
+
 }  // namespace ptwm

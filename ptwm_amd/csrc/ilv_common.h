@@ -1,0 +1,183 @@
+// ilv_common.h -- device code shared by the GPU-native interleaved plane
+// codecs (huff_ilv.hip, rans_ilv.hip): the fused inverse chain (symbol
+// transforms and per-group merge), group geometry and memory helpers.
+#pragma once
+
+#include "chain_ops.h"
+#include "huff_ilv.h"
+#include "ptwm_common.h"
+
+namespace ptwm {
+
+// inclusive prefix sum across the 64 lanes of a wavefront
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+  for (uint32_t d = 1; d < 64; d <<= 1) {
+    uint32_t t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+// Plain global-memory loads (addresses that arrive through LDS would
+// otherwise become flat loads).  Payload words are 4-byte aligned (the host
+// realigns payloads that are not).
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ uint32_t gload_u32(const uint32_t* p) {
+  return *(const __attribute__((address_space(1))) uint32_t*)(uintptr_t)p;
+}
+__device__ __forceinline__ u32x4a4 gload_u32x4(const uint32_t* p) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4a4*)(uintptr_t)p);
+}
+// Streaming (nontemporal) 16-byte load / store and byte access at a device
+// address.  Explicitly global: flat accesses would also count against the
+// LDS wait counter and stall every table lookup behind them.
+__device__ __forceinline__ u32x4 gload_nt16(uint64_t a) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4*)(uintptr_t)a);
+}
+__device__ __forceinline__ void gstore_nt16(uint64_t a, u32x4 v) {
+  __builtin_nontemporal_store(v, (__attribute__((address_space(1))) u32x4*)(uintptr_t)a);
+}
+__device__ __forceinline__ uint32_t gload_u8(uint64_t a) {
+  return *(const __attribute__((address_space(1))) uint8_t*)(uintptr_t)a;
+}
+__device__ __forceinline__ void gstore_u8(uint64_t a, uint32_t v) {
+  *(__attribute__((address_space(1))) uint8_t*)(uintptr_t)a = (uint8_t)v;
+}
+
+// LDS addresses as plain 32-bit integers: lane bit positions are absolute
+// LDS bit addresses, so a window's word address is (q >> 3) & ~3 with no
+// base to add, and table bases are constants folded into the ds offsets.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ uint32_t lds_ld32(uint32_t a) {
+  return *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)a;
+}
+__device__ __forceinline__ uint32_t lds_ld16(uint32_t a) {
+  return *(const __attribute__((address_space(3))) uint16_t*)(uintptr_t)a;
+}
+
+// Symbol transforms: the per-plane half of each chain's inverse
+// (transforms/fusion.rs:150-176, 279-296, 392-399; dtype8.rs:39-62).
+enum Xform : uint32_t {
+  kXNone = 0,
+  kXRot1 = 1,     // IEEE exponent byte e -> (e >> 1) | (e & 1) << 7
+  kXHi3 = 2,      // fp8 exponent nibble h -> (h & 0xF) << 3
+  kXE4m3Lo = 3,   // E4M3 sign/mantissa nibble l -> (l & 8) << 4 | (l & 7)
+  kXE5m2Lo = 4,   // E5M2 sign/mantissa nibble l -> (l & 8) >> 1 | (l & 4) << 5 | (l & 3)
+  kXHi4 = 5,      // nibble split high plane h -> (h & 0xF) << 4
+  kXLo4 = 6,      // nibble split low plane l -> l & 0xF
+};
+
+__device__ __forceinline__ uint32_t xform_byte(uint32_t x, uint32_t s) {
+  switch (x) {
+    case kXRot1: return ((s >> 1) | (s << 7)) & 0xFFu;
+    case kXHi3: return (s & 0xFu) << 3;
+    case kXE4m3Lo: return ((s & 8u) << 4) | (s & 7u);
+    case kXE5m2Lo: return ((s & 8u) >> 1) | ((s & 4u) << 5) | (s & 3u);
+    case kXHi4: return (s & 0xFu) << 4;
+    case kXLo4: return s & 0xFu;
+    default: return s;
+  }
+}
+
+// The same transform on 4 packed bytes (raw planes; x is a constant after
+// unrolling, so the switch folds away).
+__device__ __forceinline__ uint32_t xform_word(uint32_t x, uint32_t v) {
+  switch (x) {
+    case kXRot1: return ((v >> 1) & 0x7F7F7F7Fu) | ((v << 7) & 0x80808080u);
+    case kXHi3: return (v & 0x0F0F0F0Fu) << 3;
+    case kXE4m3Lo: return ((v & 0x08080808u) << 4) | (v & 0x07070707u);
+    case kXE5m2Lo: return ((v & 0x08080808u) >> 1) | ((v & 0x04040404u) << 5) | (v & 0x03030303u);
+    case kXHi4: return (v & 0x0F0F0F0Fu) << 4;
+    case kXLo4: return v & 0x0F0F0F0Fu;
+    default: return v;
+  }
+}
+
+// Planes, output bytes per plane byte and the symbol transform of each plane
+// (applied by the decode table for coded planes, by xform_word for raw
+// ones) per chain.
+template <uint32_t kChain>
+struct ChainInfo;
+template <> struct ChainInfo<kChainIeee16Split2> {
+  static constexpr uint32_t np = 2, ratio = 2;
+  static constexpr uint32_t xf[2] = {kXNone, kXRot1};
+};
+template <> struct ChainInfo<kChainIeee32Split4> {
+  static constexpr uint32_t np = 4, ratio = 4;
+  static constexpr uint32_t xf[4] = {kXNone, kXNone, kXNone, kXRot1};
+};
+template <> struct ChainInfo<kChainE4m3Nibble> {
+  static constexpr uint32_t np = 2, ratio = 1;
+  static constexpr uint32_t xf[2] = {kXHi3, kXE4m3Lo};
+};
+template <> struct ChainInfo<kChainE5m2Nibble> {
+  static constexpr uint32_t np = 2, ratio = 1;
+  static constexpr uint32_t xf[2] = {kXHi3, kXE5m2Lo};
+};
+template <> struct ChainInfo<kChainNibbleSplit> {
+  static constexpr uint32_t np = 2, ratio = 1;
+  static constexpr uint32_t xf[2] = {kXHi4, kXLo4};
+};
+template <> struct ChainInfo<kChainPassthrough> {
+  static constexpr uint32_t np = 1, ratio = 1;
+  static constexpr uint32_t xf[1] = {kXNone};
+};
+
+// Merge one group (16 elements; v[p][k] = transformed plane p bytes
+// 4k..4k+3) into the output words o[] (ratio * 4 words).  With the exponent
+// byte rotated (e' = e >> 1 | (e & 1) << 7), the IEEE inverses of
+// fusion.rs:150-176 / 279-296 become a byte interleave plus one bit-select:
+// out.lo = mant_lo.7bits | e'.bit7, out.hi = sign | e'.7bits.  The fp8 and
+// nibble inverses become a plain OR of the two transformed nibble planes.
+template <uint32_t kChain>
+__device__ __forceinline__ void merge_group(const uint32_t (&v)[ChainInfo<kChain>::np][4],
+                                            uint32_t (&o)[4 * ChainInfo<kChain>::ratio]) {
+  if constexpr (kChain == kChainIeee16Split2) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      // a = [m0 e0' m1 e1'], b = [e0' m0 e1' m1] (and the same for bytes 2, 3)
+      const uint32_t a0 = __builtin_amdgcn_perm(v[1][k], v[0][k], 0x05010400u);
+      const uint32_t b0 = __builtin_amdgcn_perm(v[1][k], v[0][k], 0x01050004u);
+      const uint32_t a1 = __builtin_amdgcn_perm(v[1][k], v[0][k], 0x07030602u);
+      const uint32_t b1 = __builtin_amdgcn_perm(v[1][k], v[0][k], 0x03070206u);
+      o[2 * k] = (a0 & 0x7F7F7F7Fu) | (b0 & 0x80808080u);
+      o[2 * k + 1] = (a1 & 0x7F7F7F7Fu) | (b1 & 0x80808080u);
+    }
+  } else if constexpr (kChain == kChainIeee32Split4) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t ab_lo, ab_hi, cd_lo, cd_hi;
+      zip2(v[0][k], v[1][k], ab_lo, ab_hi);
+      zip2(v[2][k], v[3][k], cd_lo, cd_hi);
+      // a = [b0 b1 b2 e'], b = [b0 b1 e' b2]: keep a's 0x7F7FFFFF bits
+      const uint32_t a[4] = {__builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u),
+                             __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u),
+                             __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u),
+                             __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t b = __builtin_amdgcn_perm(a[i], a[i], 0x02030100u);
+        o[4 * k + i] = (a[i] & 0x7F7FFFFFu) | (b & 0x80800000u);
+      }
+    }
+  } else if constexpr (kChain == kChainPassthrough) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = v[0][k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = v[0][k] | v[1][k];
+  }
+}
+
+// Symbols of plane positions [pos, pos + 16) clipped to n.
+template <bool kTail>
+__device__ __forceinline__ uint32_t group_count(uint64_t pos, uint64_t n) {
+  if (!kTail) return kIlvGroup;
+  return pos < n ? (uint32_t)(n - pos < kIlvGroup ? n - pos : kIlvGroup) : 0u;
+}
+
+}  // namespace ptwm

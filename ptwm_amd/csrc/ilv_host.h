@@ -22,7 +22,12 @@ struct IlvEncResult {
 int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, uint32_t np, uint64_t out_dev,
                           uint64_t out_cap, bool identity_fallback, IlvEncResult* res, uint64_t* needed);
 
-// Decode and merge the given tensors (fused path).  Returns kOk or kInvalidInput.
+// The same for the rans_ilv codec (rans_host.hip).
+int64_t rilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, uint32_t np, uint64_t out_dev,
+                           uint64_t out_cap, bool identity_fallback, IlvEncResult* res, uint64_t* needed);
+
+// Decode and merge the given tensors (fused path; each tensor's coded planes
+// are of its codec family).  Returns kOk or kInvalidInput.
 int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors);
 
 }  // namespace ptwm

@@ -17,6 +17,7 @@
 #include "huff_ilv.h"
 #include "huffman_host.h"
 #include "ilv_host.h"
+#include "rans_ilv.h"
 #include "runtime.h"
 
 namespace ptwm {
@@ -225,29 +226,31 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
   // capped by the workgroup LDS budget.  Blocks above it take the kernel's
   // global-memory path.
   struct Launch {
-    uint32_t chain, first, m, slots, stage_words, grid;
+    uint32_t family, chain, first, m, slots, stage_words, grid;
   };
   std::vector<Launch> launches;
   std::vector<uint32_t> idx;  // per launch: [m + 1 prefix][m tensor indexes]
+  for (uint32_t fam = kFamilyHuff; fam <= kFamilyRans; ++fam)
   for (uint32_t chain = 1; chain <= 6; ++chain) {
     std::vector<uint32_t> tix, tpre{0};
     uint32_t slots = 0;
     uint64_t est = 0;
     for (uint32_t ti = 0; ti < nt; ++ti) {
       const IlvTensor& T = tensors[ti];
-      if (T.chain != chain || T.n == 0) continue;
+      if (T.family != fam || T.chain != chain || T.n == 0) continue;
       const uint64_t nb = (T.n + kIlvBlock - 1) / kIlvBlock;
-      // the kernel keeps plane p's table in slot n_planes - 1 - p (the
+      // the kernels keep plane p's table in slot n_planes - 1 - p (the
       // exponent plane, last in every IEEE chain, in slot 0)
       uint32_t need_slots = 0;
-      uint64_t words = 4;
+      uint64_t words = fam == kFamilyHuff ? 4 : 0;
       for (uint32_t p = 0; p < T.n_planes; ++p) {
         if (!T.planes[p].coded) continue;
         need_slots = std::max(need_slots, T.n_planes - p);
         const uint64_t per_block = (T.planes[p].len + 4 * nb - 1) / (4 * nb);
-        // nibble chains may carry fixed-length codes: room for the kernel's
-        // per-lane skew of equal-length lane streams (two words per lane)
-        const uint64_t skew = chain == kChainIeee16Split2 || chain == kChainIeee32Split4 ? 0 : 128;
+        // huff_ilv nibble chains may carry fixed-length codes: room for the
+        // kernel's per-lane skew of equal-length lane streams (two words per lane)
+        const uint64_t skew =
+            fam == kFamilyRans || chain == kChainIeee16Split2 || chain == kChainIeee32Split4 ? 0 : 128;
         words += align_up(per_block + per_block / 50 + skew + 4, 4);
       }
       slots = std::max(slots, need_slots);
@@ -256,24 +259,26 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
       tpre.push_back(tpre.back() + (uint32_t)((nb + kIlvBlocksPerTile - 1) / kIlvBlocksPerTile));
     }
     if (tix.empty()) continue;
-    const uint64_t fixed = ilv_decode_lds_bytes(chain, slots, 0);
-    uint64_t cap_words = ((kIlvMaxLds - std::min<uint64_t>(fixed, kIlvMaxLds)) / 16) & ~3ull;
+    const uint64_t max_lds = fam == kFamilyHuff ? kIlvMaxLds : kRilvMaxLds;
+    const uint64_t fixed = fam == kFamilyHuff ? ilv_decode_lds_bytes(chain, slots, 0) : rilv_decode_lds_bytes(chain, slots, 0);
+    uint64_t cap_words = ((max_lds - std::min<uint64_t>(fixed, max_lds)) / 16) & ~3ull;
     uint64_t stage = align_up(std::max<uint64_t>(est, 8), 4);
     if (stage > cap_words) stage = cap_words;
     if (stage < 8) return kInternal;
     int per_cu = 0;
-    const uint64_t occ_key = (uint64_t)chain | ((uint64_t)slots << 8) | (stage << 16);
+    const uint64_t occ_key = (uint64_t)chain | ((uint64_t)slots << 8) | (stage << 16) | ((uint64_t)fam << 62);
     auto it = ctx.ilv_occupancy.find(occ_key);
     if (it != ctx.ilv_occupancy.end()) {
       per_cu = it->second;
     } else {
-      PTWM_HIP_TRY(ilv_decode_occupancy(chain, slots, (uint32_t)stage, &per_cu));
+      if (fam == kFamilyHuff) PTWM_HIP_TRY(ilv_decode_occupancy(chain, slots, (uint32_t)stage, &per_cu));
+      else PTWM_HIP_TRY(rilv_decode_occupancy(chain, slots, (uint32_t)stage, &per_cu));
       ctx.ilv_occupancy[occ_key] = per_cu;
     }
     if (per_cu < 1) per_cu = 1;
     const uint64_t n_tiles = tpre.back();
     const uint32_t grid = (uint32_t)std::min<uint64_t>(n_tiles, (uint64_t)per_cu * ctx.cu_count);
-    launches.push_back(Launch{chain, (uint32_t)idx.size(), (uint32_t)tix.size(), slots, (uint32_t)stage, grid});
+    launches.push_back(Launch{fam, chain, (uint32_t)idx.size(), (uint32_t)tix.size(), slots, (uint32_t)stage, grid});
     idx.insert(idx.end(), tpre.begin(), tpre.end());
     idx.insert(idx.end(), tix.begin(), tix.end());
   }
@@ -296,8 +301,13 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
   uint32_t* status_dev = reinterpret_cast<uint32_t*>(d + off_status);
   for (const Launch& L : launches) {
     const uint32_t* base = reinterpret_cast<const uint32_t*>(d + off_idx) + L.first;
-    PTWM_HIP_TRY(launch_ilv_decode(L.chain, reinterpret_cast<const IlvTensor*>(d), base + L.m + 1, base, L.m, L.grid,
-                                   status_dev, L.slots, L.stage_words, s));
+    const IlvTensor* td = reinterpret_cast<const IlvTensor*>(d);
+    if (L.family == kFamilyHuff)
+      PTWM_HIP_TRY(launch_ilv_decode(L.chain, td, base + L.m + 1, base, L.m, L.grid, status_dev, L.slots,
+                                     L.stage_words, s));
+    else
+      PTWM_HIP_TRY(launch_rilv_decode(L.chain, td, base + L.m + 1, base, L.m, L.grid, status_dev, L.slots,
+                                      L.stage_words, s));
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], s));
   // status read back into the host buffer's tail (the upload above is

@@ -50,6 +50,7 @@ constexpr uint32_t kCodecIdentity = 0x0000;
 constexpr uint32_t kCodecHuffman = 0x0001;
 constexpr uint32_t kCodecRans = 0x0003;
 constexpr uint32_t kCodecHuffIlv = 0x7F01;  // GPU-native interleaved Huffman
+constexpr uint32_t kCodecRansIlv = 0x7F02;  // GPU-native interleaved rANS
 
 // Chain kinds: the fused reorder+split pairs of transforms/fusion.rs plus
 // the unfused NibbleSplit and BytePassthrough used by the u8 chains.

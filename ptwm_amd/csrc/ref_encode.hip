@@ -209,41 +209,6 @@ __global__ void __launch_bounds__(256) ref_copy_kernel(const RefCopyOp* __restri
 
 // ---- host restatements of the reference's table construction ----
 
-// normalize_freqs (rans/compress.rs:72-122): returns false when it fails.
-bool rans_normalize(const uint32_t raw[256], uint16_t f[256], uint16_t cum[256], int* max_sym_out) {
-  uint64_t total = 0;
-  for (int i = 0; i < 256; ++i) total += raw[i];
-  std::memset(f, 0, 512);
-  std::memset(cum, 0, 512);
-  if (total == 0) return false;
-  uint32_t assigned = 0;
-  int max_sym = 0, max_freq_sym = 0;
-  for (int i = 0; i < 256; ++i) {
-    if (raw[i] > 0) {
-      uint64_t v = ((uint64_t)raw[i] * kRansScale) / total;
-      if (v < 1) v = 1;
-      f[i] = (uint16_t)v;
-      assigned += f[i];
-      max_sym = i;
-      if (raw[i] > raw[max_freq_sym]) max_freq_sym = i;
-    }
-  }
-  if (assigned > kRansScale) {
-    const uint32_t excess = assigned - kRansScale;
-    if ((uint32_t)f[max_freq_sym] > excess) f[max_freq_sym] = (uint16_t)(f[max_freq_sym] - excess);
-    else return false;
-  } else if (assigned < kRansScale) {
-    f[max_freq_sym] = (uint16_t)(f[max_freq_sym] + (kRansScale - assigned));
-  }
-  uint16_t run = 0;
-  for (int i = 0; i <= max_sym; ++i) {
-    cum[i] = run;
-    run = (uint16_t)(run + f[i]);
-  }
-  *max_sym_out = max_sym;
-  return true;
-}
-
 // EncSymbol (rans/compress.rs:35-68) packed for ref_rans_kernel.
 void rans_encsym(uint32_t start, uint32_t freq, uint32_t out[4]) {
   uint32_t rcp, bias, shift;
@@ -336,7 +301,7 @@ int64_t RefEncoder::plan(DevCtx& ctx, const std::vector<RefJob>& jobs, std::vect
     } else {
       uint16_t f[256], cum[256];
       int max_sym = 0;
-      if (!rans_normalize(h, f, cum, &max_sym)) continue;
+      if (!rans_normalize_freqs(h, f, cum, &max_sym)) continue;
       I.header.push_back((uint8_t)max_sym);
       for (int i = 0; i <= max_sym; ++i) {
         I.header.push_back((uint8_t)f[i]);

@@ -163,7 +163,8 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
       P.crc32 = T.has_crc ? c.get<uint32_t>() : 0;
       if (!c.ok || (pflags & ~1u)) return kInvalidInput;
       P.chunked = (pflags & 1u) != 0;
-      if (P.codec != kCodecIdentity && P.codec != kCodecHuffman && P.codec != kCodecRans && P.codec != kCodecHuffIlv)
+      if (P.codec != kCodecIdentity && P.codec != kCodecHuffman && P.codec != kCodecRans && P.codec != kCodecHuffIlv &&
+          P.codec != kCodecRansIlv)
         return kUnsupported;
       if (P.payload_offset > in_len || in_len - P.payload_offset < P.payload_len) return kInvalidInput;
       if (P.chunked) {
@@ -197,23 +198,27 @@ static inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a
 
 int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev) {
   // Route 1 (fused): a tensor whose planes are all unchunked Identity or
-  // huff_ilv payloads, with at least one huff_ilv plane, is decoded and
-  // merged in one pass by the huff_ilv kernel.
+  // GPU-native payloads of one codec family (huff_ilv or rans_ilv), with at
+  // least one coded plane, is decoded and merged in one pass by that
+  // family's kernel.
   // Route 2 (exact): every other tensor; reference-format planes become
-  // DecodeJobs into plane scratch (huff_ilv planes decode into scratch through
-  // the fused kernel's passthrough chain), then the merge kernel runs.
+  // DecodeJobs into plane scratch (GPU-native planes decode into scratch
+  // through their fused kernel's passthrough chain), then the merge kernel
+  // runs.
   const size_t nt = plan.tensors.size();
   std::vector<IlvTensor> ilv;
   std::vector<char> fused(nt, 0);
   for (size_t t = 0; t < nt; ++t) {
     const PlanTensor& T = plan.tensors[t];
-    bool any_ilv = false, ok = ((out_dev + T.out_offset) & 15u) == 0;
+    bool any_huff = false, any_rans = false, ok = ((out_dev + T.out_offset) & 15u) == 0;
     for (const PlanPlane& P : T.planes) {
       if (P.chunked) ok = false;
-      if (P.codec == kCodecHuffIlv) any_ilv = true;
+      if (P.codec == kCodecHuffIlv) any_huff = true;
+      else if (P.codec == kCodecRansIlv) any_rans = true;
       else if (P.codec != kCodecIdentity || P.payload_len != P.plane_len) ok = false;
     }
-    if (!ok || !any_ilv) continue;
+    // one codec family per fused tensor
+    if (!ok || any_huff == any_rans) continue;
     // a plane CRC is checked on the restored tensor where the chain is a
     // bijection on plane bytes; other chains keep their planes in scratch
     if (T.has_crc && !crc_chain_supported(T.chain)) continue;
@@ -223,10 +228,12 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     X.n = T.planes[0].plane_len;
     X.chain = T.chain;
     X.n_planes = (uint32_t)T.planes.size();
+    X.family = any_rans ? kFamilyRans : kFamilyHuff;
+    const uint32_t coded_codec = any_rans ? kCodecRansIlv : kCodecHuffIlv;
     for (size_t p = 0; p < T.planes.size(); ++p) {
       X.planes[p].base = in_dev + T.planes[p].payload_offset;
       X.planes[p].len = T.planes[p].payload_len;
-      X.planes[p].coded = T.planes[p].codec == kCodecHuffIlv ? 1 : 0;
+      X.planes[p].coded = T.planes[p].codec == coded_codec ? 1 : 0;
       X.planes[p].lut = (uint32_t)p;
     }
     ilv.push_back(X);
@@ -247,10 +254,11 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
       uint64_t direct = in_dev + P.payload_offset;
       if (P.codec == kCodecIdentity && !P.chunked && P.payload_len == P.plane_len && (direct & 15u) == 0)
         continue;
-      if (P.codec == kCodecHuffIlv && P.chunked) return kUnsupported;
+      const bool native = P.codec == kCodecHuffIlv || P.codec == kCodecRansIlv;
+      if (native && P.chunked) return kUnsupported;
       scratch_off[t][p] = scratch_bytes;
       scratch_bytes = align_up(scratch_bytes + P.plane_len, 256);
-      if (P.codec != kCodecHuffIlv) n_jobs += P.chunked ? P.chunks.size() : 1;
+      if (!native) n_jobs += P.chunked ? P.chunks.size() : 1;
     }
   }
   if (n_jobs > 0xFFFFFFFFull) return kInvalidInput;
@@ -275,7 +283,7 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
       }
       const uint64_t a = scratch_base + scratch_off[t][p];
       plane_addr[t][p] = a;
-      if (P.codec == kCodecHuffIlv) {
+      if (P.codec == kCodecHuffIlv || P.codec == kCodecRansIlv) {
         if (P.plane_len == 0) continue;
         IlvTensor X{};
         X.out = a;
@@ -285,6 +293,7 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
         X.planes[0].base = in_dev + P.payload_offset;
         X.planes[0].len = P.payload_len;
         X.planes[0].coded = 1;
+        X.family = P.codec == kCodecRansIlv ? kFamilyRans : kFamilyHuff;
         ilv.push_back(X);
         continue;
       }

@@ -18,7 +18,8 @@ BUILTIN_IDS = {
 }
 CURRENT_BUILTIN_VERSION = "1.1.0"   # extension/builtins.rs:19 (crate version)
 
-PLANE_CODEC_LABEL = "io.ptwm.mi355x.plane_codec"
+PLANE_CODEC_LABEL = "io.ptwm.mi355x.plane_codec"            # huff_ilv
+RANS_CODEC_LABEL = "io.ptwm.mi355x.plane_codec.rans"        # rans_ilv
 HARDWARE_BACKEND_LABEL = "io.ptwm.mi355x.hardware_backend"
 DECODE_PLAN_LABEL = "io.ptwm.mi355x.decode_plan"
 OWN_VERSION = "0.1.0"
@@ -26,13 +27,15 @@ OWN_IDS = {
     PLANE_CODEC_LABEL: "cfd8cc03483eb4a43cdddb4b3cbf95b32e0a3f0e17e5ec85a0b52de04e8caf04",
     HARDWARE_BACKEND_LABEL: "a432dc02f57030b41a3660762bbcec5668cde8abbc807999d56ca0a3304d39cf",
     DECODE_PLAN_LABEL: "1b0e48b156b01d0d733a5aa62a90bcbde34945ff024d8d8e56cb714a48c6e770",
+    RANS_CODEC_LABEL: "968f8be9f06b14b33fcd066622493f1101954d074c25d63e78380d33708fe1f5",
 }
 
 # codec wire ids (crates/ptwm-core/src/codec.rs:3-23)
 CODEC_IDENTITY = 0x0000
 CODEC_HUFFMAN = 0x0001
 CODEC_RANS = 0x0003
-CODEC_HUFF_ILV = 0x7F01            # this library's GPU-native codec
+CODEC_HUFF_ILV = 0x7F01            # this library's GPU-native codecs
+CODEC_RANS_ILV = 0x7F02
 CODEC_NAMES = {"identity": CODEC_IDENTITY, "huffman": CODEC_HUFFMAN, "rans": CODEC_RANS}
 
 
@@ -61,4 +64,6 @@ def codec_wire_id(canonical: bytes) -> int:
             return CODEC_NAMES[name]
     if h == OWN_IDS[PLANE_CODEC_LABEL]:
         return CODEC_HUFF_ILV
+    if h == OWN_IDS[RANS_CODEC_LABEL]:
+        return CODEC_RANS_ILV
     raise LookupError(f"unknown codec id {h}")

@@ -43,7 +43,8 @@ def test_abi_version_and_ids(orc):
     L = _native.lib()
     assert L.ptwm_mi355x_abi_version() == 1
     out = (C.c_uint8 * 32)()
-    for which, label in enumerate([ids.PLANE_CODEC_LABEL, ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL]):
+    for which, label in enumerate([ids.PLANE_CODEC_LABEL, ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL,
+                                   ids.RANS_CODEC_LABEL]):
         assert L.ptwm_mi355x_canonical_id(which, out) == 0
         want = orc.blake3(bytes(32) + b"\x00" + label.encode() + b"\x00" + ids.OWN_VERSION.encode())
         assert bytes(out) == want == bytes.fromhex(ids.OWN_IDS[label])
