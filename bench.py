@@ -126,7 +126,11 @@ def build_workload(name: str) -> Workload:
     base, *opts = name.split("+")
     if set(opts) - {"crc", "hash"}:
         raise SystemExit(f"unknown workload option in {name}")
-    name = base
+    # "<workload>@rans": the GPU-native planes coded with rans_ilv instead of huff_ilv
+    name, _, codec_tag = base.partition("@")
+    if codec_tag not in ("", "rans"):
+        raise SystemExit(f"unknown codec tag in {base}")
+    native = "rans_ilv" if codec_tag == "rans" else "huff_ilv"
 
     CH = {"w": plan.CHAIN_IEEE16_SPLIT2, "n": plan.CHAIN_IEEE16_SPLIT2, "fp8": plan.CHAIN_E4M3_NIBBLE,
           "fp32o": plan.CHAIN_IEEE32_SPLIT4, "fp4": plan.CHAIN_NIBBLE_SPLIT, "e8m0": plan.CHAIN_PASSTHROUGH}
@@ -186,6 +190,9 @@ def build_workload(name: str) -> Workload:
         kernel = exact
     else:
         raise SystemExit(f"unknown workload {name}")
+    if native == "rans_ilv":
+        desc += ", planes coded with rans_ilv (GPU-native interleaved rANS)"
+        kernel = kernel.replace("ilv_decode_kernel", "rilv_decode_kernel")
     wl = Workload(desc)
     wl.kernel = kernel
     tensors = []
@@ -204,7 +211,7 @@ def build_workload(name: str) -> Workload:
     t0 = time.perf_counter()
     for raw, chain, rf in tensors:
         if rf is None:
-            used, st = api.encode_tensor_cuda(chain, raw, blob[off:], 0)
+            used, st = api.encode_tensor_cuda(chain, raw, blob[off:], 0, codec=native)
         else:
             used, st = api.encode_tensor_ref_cuda(chain, rf[0], rf[1], raw, blob[off:], 0)
         t = plan.decode_plan(st)[0]
