@@ -195,6 +195,12 @@ def build_workload(name: str) -> Workload:
         kernel = kernel.replace("ilv_decode_kernel", "rilv_decode_kernel")
     wl = Workload(desc)
     wl.kernel = kernel
+    if ref is not None:
+        wl.codec = "reference Huffman / rANS plane payloads (exact route)"
+    elif native == "rans_ilv":
+        wl.codec = "rans_ilv (GPU-native interleaved rANS, packed-nibble and stored forms) + Identity"
+    else:
+        wl.codec = "huff_ilv (GPU-native interleaved Huffman, packed-nibble and stored forms) + Identity"
     tensors = []
     total_raw = 0
     for i, (shape, kind) in enumerate(specs):
@@ -330,7 +336,7 @@ def main():
     primary = {"workload": args.workload, "description": wl.name, "restored_bytes": wl.restored,
                "compressed_bytes": wl.comp_bytes, "ratio": round(wl.comp_bytes / wl.restored, 4),
                "encode_gbs": round(wl.encode_gbs, 1), "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
-               "codec": "huff_ilv (GPU-native interleaved Huffman) + Identity"}
+               "codec": wl.codec}
     kernel_name = wl.kernel
     log(f"[bench] {ms_step:.3f} ms/step, kernel {kms:.3f} ms, {value:.1f} GB/s restored")
     extras = {}

@@ -898,7 +898,8 @@ int64_t por_decode_plane_chunked_mt(int codec, const uint8_t *payload, size_t pa
 /* ------------------------------------------------------------------------- */
 /* huff_ilv (this build's own codec; executable specification)               */
 /*                                                                           */
-/* payload: [tag u8] tag 0: stored plane bytes follow.  tag 1:               */
+/* payload: [tag u8] tag 0: stored plane bytes follow.  tag 2: packed       */
+/*   nibbles (ilv_emit_packed).  tag 1:                                      */
 /*   [orig_len u32][weights header (weights.rs)][0-pad to 4][off u32 x nb+1] */
 /*   [data]; nb = ceil(n / 16384).  Block b = data[off[b]..off[b+1]):        */
 /*   [64 x u8 lane word counts][lane 0 words][lane 1 words]...(u32 LE).      */
@@ -912,6 +913,38 @@ int64_t por_decode_plane_chunked_mt(int codec, const uint8_t *payload, size_t pa
 /* ------------------------------------------------------------------------- */
 
 #define ILV_BLOCK 16384
+
+/* Packed nibbles, the third payload form of both GPU-native codecs: a plane
+ * whose symbols are all < 16 may be stored two symbols per byte:
+ *   [0x02][n u32][0 0 0][ceil(n / 2) bytes], byte i = s[2i] | s[2i+1] << 4
+ * (the high nibble of the last byte is 0 when n is odd).  Encoders choose
+ * the smallest of coded, packed and stored (packed needs n >= 16 to beat
+ * stored; coded wins only when strictly smaller than both). */
+static size_t ilv_packed_size(size_t n) { return 8 + (n + 1) / 2; }
+
+static int ilv_all_nibbles(const uint32_t freqs[256]) {
+    for (int s = 16; s < 256; s++) if (freqs[s]) return 0;
+    return 1;
+}
+
+static int64_t ilv_emit_packed(const uint8_t *plane, size_t n, uint8_t *out, size_t cap) {
+    size_t len = ilv_packed_size(n);
+    if (len > cap) return POR_ESMALL;
+    memset(out, 0, len);
+    out[0] = 2; st32(out + 1, (uint32_t)n);
+    for (size_t i = 0; i < n; i++) out[8 + i / 2] |= (uint8_t)((plane[i] & 0xF) << (4 * (i & 1)));
+    return (int64_t)len;
+}
+
+static int64_t ilv_decode_packed(const uint8_t *p, size_t len, uint8_t *out, size_t cap) {
+    if (len < 8 || p[5] || p[6] || p[7]) return POR_EINVAL;
+    size_t n = ld32(p + 1);
+    if (len != ilv_packed_size(n)) return POR_EINVAL;
+    if ((n & 1) && (p[len - 1] >> 4)) return POR_EINVAL;
+    if (n > cap) return POR_ESMALL;
+    for (size_t i = 0; i < n; i++) out[i] = (uint8_t)((p[8 + i / 2] >> (4 * (i & 1))) & 0xF);
+    return (int64_t)n;
+}
 #define ILV_LANES 64
 #define ILV_GROUP 16
 #define ILV_NIBBLE_MAX_LEN 6
@@ -960,7 +993,8 @@ int64_t por_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap)
             }
             total += bsz;
         }
-        if (data0 + total < 1 + n && data0 + total <= cap) {
+        size_t best_other = ilv_all_nibbles(freqs) && ilv_packed_size(n) < 1 + n ? ilv_packed_size(n) : 1 + n;
+        if (data0 + total < best_other && data0 + total <= cap) {
             memset(out, 0, data0 + total);
             out[0] = 1; st32(out + 1, (uint32_t)n);
             memcpy(out + 5, hdr, (size_t)wl);
@@ -992,6 +1026,7 @@ int64_t por_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap)
         }
         free(words);
     }
+    if (n <= 0xFFFFFFFFu && ilv_all_nibbles(freqs) && ilv_packed_size(n) < 1 + n) return ilv_emit_packed(plane, n, out, cap);
     if (1 + n > cap) return POR_ESMALL;
     out[0] = 0;
     memcpy(out + 1, plane, n);
@@ -1005,6 +1040,7 @@ int64_t por_ilv_decode(const uint8_t *p, size_t len, uint8_t *out, size_t cap) {
         memcpy(out, p + 1, len - 1);
         return (int64_t)(len - 1);
     }
+    if (p[0] == 2) return ilv_decode_packed(p, len, out, cap);
     if (p[0] != 1 || len < 5) return POR_EINVAL;
     size_t n = ld32(p + 1);
     if (n > cap) return POR_ESMALL;
@@ -1055,7 +1091,8 @@ int64_t por_ilv_decode(const uint8_t *p, size_t len, uint8_t *out, size_t cap) {
 /* ------------------------------------------------------------------------- */
 /* rans_ilv: this build's GPU-native interleaved rANS plane codec (no          */
 /* reference counterpart; this function pair is its specification).          */
-/*   [0x00][plane]  stored (empty plane: [0x00])                              */
+/*   [0x00][plane]  stored (empty plane: [0x00]); [0x02]... packed nibbles   */
+/*   (ilv_emit_packed, as huff_ilv)                                           */
 /*   [0x01][n u32][max_sym u8][f u16 x (max_sym + 1)][0-pad to 4]             */
 /*        [off u32 x (nb + 1)][blocks], nb = ceil(n / 16384)                  */
 /*   frequencies: the reference's normalisation (rans/compress.rs:72-135,     */
@@ -1106,7 +1143,8 @@ int64_t por_rans_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t
             bw[b] = (uint32_t)nwb;
             total += (4 + 256 + 2 * nwb + 3) & ~(size_t)3;
         }
-        if (data0 + total < 1 + n && data0 + total <= cap && total <= 0xFFFFFFFFu) {
+        size_t best_other = ilv_all_nibbles(raw) && ilv_packed_size(n) < 1 + n ? ilv_packed_size(n) : 1 + n;
+        if (data0 + total < best_other && data0 + total <= cap && total <= 0xFFFFFFFFu) {
             memset(out, 0, data0 + total);
             out[0] = 1; st32(out + 1, (uint32_t)n);
             out[5] = (uint8_t)max_sym;
@@ -1142,6 +1180,7 @@ int64_t por_rans_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t
         }
         free(words); free(bw);
     }
+    if (n <= 0xFFFFFFFFu && ilv_all_nibbles(raw) && ilv_packed_size(n) < 1 + n) return ilv_emit_packed(plane, n, out, cap);
     if (1 + n > cap) return POR_ESMALL;
     out[0] = 0;
     memcpy(out + 1, plane, n);
@@ -1155,6 +1194,7 @@ int64_t por_rans_ilv_decode(const uint8_t *p, size_t len, uint8_t *out, size_t c
         memcpy(out, p + 1, len - 1);
         return (int64_t)(len - 1);
     }
+    if (p[0] == 2) return ilv_decode_packed(p, len, out, cap);
     if (p[0] != 1 || len < 6) return POR_EINVAL;
     size_t n = ld32(p + 1);
     if (n > cap) return POR_ESMALL;

@@ -141,7 +141,8 @@ int64_t ilv_decode_payload(DevCtx& ctx, uint64_t in_dev, size_t in_len, uint64_t
   uint64_t expected;
   if (hdr[0] == 0) {
     expected = in_len - 1;
-  } else if (hdr[0] == 1 && in_len >= 5) {
+  } else if ((hdr[0] == 1 && in_len >= 5) || (hdr[0] == 2 && in_len >= kPackedHeadBytes)) {
+    // coded (tag 1) and packed-nibble (tag 2) payloads carry n after the tag
     expected = (uint64_t)hdr[1] | ((uint64_t)hdr[2] << 8) | ((uint64_t)hdr[3] << 16) | ((uint64_t)hdr[4] << 24);
   } else {
     return kInvalidInput;

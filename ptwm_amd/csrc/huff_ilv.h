@@ -57,6 +57,17 @@ struct IlvEncBlock {
   uint32_t pad;
 };
 
+// Packed-nibble payload (tag 2): [2][n u32][0 0 0][ceil(n / 2) bytes].
+constexpr uint32_t kPackedHeadBytes = 8;
+
+// A packed-nibble payload body (tag 2): n symbols < 16 at src (16-byte
+// aligned) packed two per byte to dst (8-byte aligned).
+struct IlvPackJob {
+  uint64_t src;
+  uint64_t dst;
+  uint64_t n;
+};
+
 // Fused decode of the tensors tix[0..m) (indexes into `tensors`, all of
 // chain `chain`); tensor tix[j] owns the 4-block tiles tpre[j] ..
 // tpre[j+1] - 1.  grid: persistent workgroups, each taking an equal range of
@@ -68,6 +79,7 @@ hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uin
                              hipStream_t stream);
 size_t ilv_decode_lds_bytes(uint32_t chain, uint32_t n_slots, uint32_t stage_words);
 hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, int* wg_per_cu);
+hipError_t launch_ilv_pack(const IlvPackJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream);
 hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_t max_n, uint32_t* hist,
                            hipStream_t stream);
 hipError_t launch_ilv_size(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,

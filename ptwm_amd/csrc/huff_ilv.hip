@@ -1,7 +1,9 @@
 // huff_ilv.hip -- the GPU-native interleaved Huffman plane codec on gfx950.
 //
 // Wire format (codec wire id 0x7F01, this library's plane-codec id):
-//   [tag u8] 0: stored plane bytes follow.  1: coded:
+//   [tag u8] 0: stored plane bytes follow.  2: packed nibbles,
+//   [n u32][0 0 0][ceil(n / 2) bytes], byte i = s[2i] | s[2i+1] << 4 (a plane
+//   of symbols < 16 that codes no smaller, e.g. MXFP4 codes).  1: coded:
 //   [orig_len u32 LE][weights header (entropy/huffman/weights.rs)][0-pad to 4]
 //   [block offset table u32 x (nb + 1)][data],  nb = ceil(n / 16384)
 //   block b = data[off[b] .. off[b+1]):
@@ -82,6 +84,7 @@ struct alignas(16) DecodeCtl {
   uint64_t table[4], data[4], datalen[4], raw[4];  // per plane
   uint32_t coded[4];
   uint32_t pair[4];
+  uint32_t packed[4];   // plane stored as packed nibbles (tag 2)
   uint32_t bad;
 };
 static_assert(sizeof(DecodeCtl) % 16 == 0, "DecodeCtl keeps the staging area 16-byte aligned");
@@ -360,8 +363,9 @@ struct BlockState {
   uint32_t nw[NP];
   uint32_t q[NP];
   uint32_t t64[NP];     // LDS address of a pair-mode plane's 64-entry table
-  uint32_t coded_mask;  // bit p: plane p is huff_ilv coded
-  uint32_t pair_mask;   // bit p: plane p decodes in pair mode
+  uint32_t coded_mask;   // bit p: plane p is huff_ilv coded
+  uint32_t pair_mask;    // bit p: plane p decodes in pair mode
+  uint32_t packed_mask;  // bit p: plane p is stored as packed nibbles
 };
 
 // Load the raw (uncoded) planes' bytes of the group at plane position pos.
@@ -373,21 +377,7 @@ __device__ __forceinline__ void load_raw(const BlockState<ChainInfo<kChain>::np>
 #pragma unroll
   for (uint32_t p = 0; p < NP; ++p) {
     if (st.coded_mask & (1u << p)) continue;
-    const uint64_t raw = st.raw[p] + pos;
-    if (count == kIlvGroup && (st.raw[p] & 15u) == 0) {
-      const u32x4 w = gload_nt16(raw);
-      x[p][0] = w.x;
-      x[p][1] = w.y;
-      x[p][2] = w.z;
-      x[p][3] = w.w;
-    } else {
-      uint32_t tmp[4] = {0, 0, 0, 0};
-      for (uint32_t k = 0; k < count; ++k) tmp[k >> 2] |= gload_u8(raw + k) << (8 * (k & 3));
-      x[p][0] = tmp[0];
-      x[p][1] = tmp[1];
-      x[p][2] = tmp[2];
-      x[p][3] = tmp[3];
-    }
+    load_group(st.raw[p], (st.packed_mask >> p) & 1u, pos, count, x[p]);
   }
 }
 
@@ -524,13 +514,18 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
           const IlvPlane& P = T.planes[p];
           s_raw[p] = P.base;
           s_coded[p] = 0;
+          ctl.packed[p] = 0;
           if (!P.coded) continue;
-          // huff_ilv payload: tag 0 stores the plane after the tag byte
+          // huff_ilv payload: tag 0 stores the plane after the tag byte, tag 2 packs it
           const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
           if (P.len == 0) s_bad |= kIlvErrHeader;
           else if (pay[0] == 0) {
             if (P.len != n + 1) s_bad |= kIlvErrHeader;
             s_raw[p] = P.base + 1;
+          } else if (pay[0] == 2) {
+            if (!packed_header_ok(pay, P.len, n)) s_bad |= kIlvErrHeader;
+            s_raw[p] = P.base + kPackedHeadBytes;
+            ctl.packed[p] = 1;
           } else if (pay[0] == 1 && P.len >= 5 && ld_u32le(pay + 1) == n) {
             if (NP - 1 - p < n_slots) s_coded[p] = 1;
             else s_bad |= kIlvErrHeader;  // the launch reserved no table slot for it
@@ -579,9 +574,11 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
     bool ok = true;
     st.coded_mask = 0;
     st.pair_mask = 0;
+    st.packed_mask = 0;
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
       st.raw[p] = s_raw[p];
+      if (__builtin_amdgcn_readfirstlane(ctl.packed[p])) st.packed_mask |= 1u << p;
       st.words[p] = nullptr;
       st.nw[p] = 0;
       st.q[p] = 0;
@@ -846,6 +843,48 @@ hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uin
     default:
       return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+// Packed-nibble payload bodies: job blockIdx.y, each thread turns 16 plane
+// bytes (symbols < 16) into 8 output bytes, byte i = s[2i] | s[2i+1] << 4.
+// The thread whose vector index is n / 16 packs the tail.
+__device__ __forceinline__ uint32_t pack_nibbles4(uint32_t w) {
+  // bytes s0 s1 s2 s3 -> (s0 | s1 << 4) | (s2 | s3 << 4) << 8
+  const uint32_t t = (w & 0x000F000Fu) | ((w >> 4) & 0x00F000F0u);
+  return (t & 0xFFu) | ((t >> 8) & 0xFF00u);
+}
+
+__global__ void __launch_bounds__(256) ilv_pack_kernel(const IlvPackJob* __restrict__ jobs) {
+  const IlvPackJob J = jobs[blockIdx.y];
+  const uint64_t nvec = J.n / 16;
+  const uint64_t stride = (uint64_t)gridDim.x * 256u;
+  for (uint64_t v = (uint64_t)blockIdx.x * 256u + threadIdx.x; v <= nvec; v += stride) {
+    if (v < nvec) {
+      const u32x4 x = gload_nt16(J.src + 16 * v);
+      const uint32_t lo = pack_nibbles4(x.x) | (pack_nibbles4(x.y) << 16);
+      const uint32_t hi = pack_nibbles4(x.z) | (pack_nibbles4(x.w) << 16);
+      const uint64_t w = (uint64_t)lo | ((uint64_t)hi << 32);
+      if ((J.dst & 7u) == 0) {
+        g_st<uint64_t>(J.dst + 8 * v, w);
+      } else {  // output buffer not 8-byte aligned
+        for (int k = 0; k < 8; ++k) gstore_u8(J.dst + 8 * v + k, (uint32_t)(w >> (8 * k)) & 0xFFu);
+      }
+    } else {
+      for (uint64_t i = 16 * nvec; i < J.n; i += 2) {
+        uint32_t b = gload_u8(J.src + i) & 0xFu;
+        if (i + 1 < J.n) b |= (gload_u8(J.src + i + 1) & 0xFu) << 4;
+        gstore_u8(J.dst + i / 2, b);
+      }
+    }
+  }
+}
+
+hipError_t launch_ilv_pack(const IlvPackJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream) {
+  if (!n_jobs) return hipSuccess;
+  uint64_t blocks = (max_n / 16 + 256) / 256;
+  if (blocks > 1024) blocks = 1024;
+  hipLaunchKernelGGL(ilv_pack_kernel, dim3((uint32_t)blocks, n_jobs), dim3(256), 0, stream, jobs);
   return hipGetLastError();
 }
 

@@ -180,4 +180,48 @@ __device__ __forceinline__ uint32_t group_count(uint64_t pos, uint64_t n) {
   return pos < n ? (uint32_t)(n - pos < kIlvGroup ? n - pos : kIlvGroup) : 0u;
 }
 
+// Packed-nibble payloads (tag 2 of both GPU-native codecs):
+// [2][n u32][0 0 0][ceil(n / 2) bytes], byte i = s[2i] | s[2i+1] << 4, the
+// high nibble of the last byte 0 when n is odd.
+__device__ __forceinline__ bool packed_header_ok(const uint8_t* pay, uint64_t len, uint64_t n) {
+  if (len < kPackedHeadBytes || pay[5] || pay[6] || pay[7]) return false;
+  const uint64_t pn = (uint64_t)pay[1] | ((uint64_t)pay[2] << 8) | ((uint64_t)pay[3] << 16) | ((uint64_t)pay[4] << 24);
+  if (pn != n || len != kPackedHeadBytes + (n + 1) / 2) return false;
+  return !(n & 1u) || (pay[len - 1] >> 4) == 0;
+}
+
+// The 16 symbols of the group at plane position pos (count of them inside
+// the plane) of a stored plane at `base`: bytes, or packed nibbles (base =
+// payload + 8, 4-byte aligned) expanded to one symbol per byte.
+__device__ __forceinline__ void load_group(uint64_t base, bool packed, uint64_t pos, uint32_t count,
+                                           uint32_t (&x)[4]) {
+  if (!packed) {
+    const uint64_t a = base + pos;
+    if (count == kIlvGroup && (base & 15u) == 0) {
+      const u32x4 w = gload_nt16(a);
+      x[0] = w.x;
+      x[1] = w.y;
+      x[2] = w.z;
+      x[3] = w.w;
+    } else {
+      x[0] = x[1] = x[2] = x[3] = 0;
+      for (uint32_t k = 0; k < count; ++k) x[k >> 2] |= gload_u8(a + k) << (8 * (k & 3));
+    }
+    return;
+  }
+  const uint64_t a = base + pos / 2;  // pos is a multiple of 16
+  uint32_t w[2] = {0, 0};
+  if (count == kIlvGroup && (base & 3u) == 0) {
+    w[0] = g_ld<uint32_t>(a);
+    w[1] = g_ld<uint32_t>(a + 4);
+  } else {
+    for (uint32_t k = 0; k < (count + 1) / 2; ++k) w[k >> 2] |= gload_u8(a + k) << (8 * (k & 3));
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // even nibbles and odd nibbles, then interleaved back into symbol order
+    zip2(w[h] & 0x0F0F0F0Fu, (w[h] >> 4) & 0x0F0F0F0Fu, x[2 * h], x[2 * h + 1]);
+  }
+}
+
 }  // namespace ptwm

@@ -2,8 +2,9 @@
 //
 // Encode (per call, any number of planes): histogram kernel -> host code
 // tables (huffman_host.cpp) -> size kernel -> host prefix sums and payload
-// layout -> encode kernel plus header / offset-table uploads.  A plane whose
-// coded payload is not smaller than the plane is stored instead.
+// layout -> encode kernel plus header / offset-table uploads.  Each plane
+// takes the smallest payload form (ilv_choose_form): coded, packed nibbles
+// or stored.
 //
 // Decode: tensors are grouped by chain and decoded with one fused launch per
 // chain (ilv_decode_kernel<chain>): persistent workgroups (as many as fit on
@@ -23,6 +24,65 @@
 namespace ptwm {
 
 static inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+uint32_t ilv_choose_form(uint64_t n, bool nibbles, bool codable, uint64_t coded_len, bool identity_fallback,
+                         uint64_t* len) {
+  const uint64_t stored = n + 1, packed = kPackedHeadBytes + (n + 1) / 2;
+  const bool pack_ok = nibbles && packed < stored;
+  const uint64_t other = pack_ok ? packed : stored;
+  uint32_t form = kFormStored;
+  uint64_t l = stored;
+  if (codable && coded_len < other) {
+    form = kFormCoded;
+    l = coded_len;
+  } else if (pack_ok) {
+    form = kFormPacked;
+    l = packed;
+  }
+  if (identity_fallback && (form == kFormStored || l >= n)) {
+    form = kFormIdentity;
+    l = n;
+  }
+  *len = l;
+  return form;
+}
+
+int64_t ilv_store_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, uint32_t np, uint64_t out_dev,
+                         const IlvEncResult* res, const uint32_t* form, std::vector<uint8_t>& keep) {
+  hipStream_t s = ctx.stream;
+  keep.assign((size_t)np * (8 + sizeof(IlvPackJob)), 0);
+  IlvPackJob* jobs = reinterpret_cast<IlvPackJob*>(keep.data() + 8 * np);
+  uint32_t nj = 0;
+  uint64_t max_n = 0;
+  for (uint32_t p = 0; p < np; ++p) {
+    const uint64_t dst = out_dev + res[p].offset;
+    uint8_t* head = keep.data() + 8 * p;
+    if (form[p] == kFormIdentity) {
+      if (n[p])
+        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src[p]), n[p],
+                                    hipMemcpyDeviceToDevice, s));
+    } else if (form[p] == kFormStored) {
+      head[0] = 0;
+      PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), head, 1, hipMemcpyHostToDevice, s));
+      if (n[p])
+        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst + 1), reinterpret_cast<const void*>(src[p]), n[p],
+                                    hipMemcpyDeviceToDevice, s));
+    } else if (form[p] == kFormPacked) {
+      head[0] = 2;
+      const uint32_t nn = (uint32_t)n[p];
+      std::memcpy(head + 1, &nn, 4);
+      PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), head, kPackedHeadBytes, hipMemcpyHostToDevice, s));
+      jobs[nj++] = IlvPackJob{src[p], dst + kPackedHeadBytes, n[p]};
+      max_n = std::max(max_n, n[p]);
+    }
+  }
+  if (nj) {
+    PTWM_HIP_TRY(ctx.enc_pack.ensure(nj * sizeof(IlvPackJob)));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.enc_pack.ptr, jobs, nj * sizeof(IlvPackJob), hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(launch_ilv_pack(static_cast<const IlvPackJob*>(ctx.enc_pack.ptr), nj, max_n, s));
+  }
+  return kOk;
+}
 
 int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, uint32_t np, uint64_t out_dev,
                           uint64_t out_cap, bool identity_fallback, IlvEncResult* res, uint64_t* needed) {
@@ -98,26 +158,23 @@ int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, u
   }
   // ---- layout: payloads at 256-byte aligned offsets ----
   uint64_t off = 0;
-  std::vector<uint64_t> head(np, 0), data_bytes(np, 0);
+  std::vector<uint64_t> head(np, 0);
+  std::vector<uint32_t> form(np, kFormStored);
   for (uint32_t p = 0; p < np; ++p) {
     off = align_up(off, 256);
     res[p].offset = off;
-    bool coded = false;
-    if (codable[p]) {
+    uint64_t pay = 0;
+    bool codable_p = codable[p];
+    if (codable_p) {
       uint64_t d = 0;
       for (uint32_t b = 0; b < nbs[p]; ++b) d += bbytes[first_block[p] + b];
       head[p] = align_up(5 + weights[p].size(), 4);
-      data_bytes[p] = d;
-      uint64_t pay = head[p] + 4ull * (nbs[p] + 1) + d;
-      // coded only when smaller than the stored form (Identity: n, tag 0: n + 1)
-      if (pay < (identity_fallback ? n[p] : n[p] + 1) && d <= 0xFFFFFFFFull) {
-        coded = true;
-        res[p].len = pay;
-      }
+      pay = head[p] + 4ull * (nbs[p] + 1) + d;
+      codable_p = d <= 0xFFFFFFFFull;
     }
-    res[p].coded = coded ? 1 : 0;
-    if (!coded) res[p].len = identity_fallback ? n[p] : n[p] + 1;
-    res[p].codec = coded ? kCodecHuffIlv : (identity_fallback ? kCodecIdentity : kCodecHuffIlv);
+    form[p] = ilv_choose_form(n[p], all_nibbles(&hist[256 * p]), codable_p, pay, identity_fallback, &res[p].len);
+    res[p].coded = form[p] == kFormCoded ? 1 : 0;
+    res[p].codec = form[p] == kFormIdentity ? kCodecIdentity : kCodecHuffIlv;
     off += res[p].len;
   }
   const uint64_t total = off;
@@ -129,27 +186,16 @@ int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, u
   uint64_t host_bytes = 0;
   for (uint32_t p = 0; p < np; ++p)
     if (res[p].coded) host_bytes += head[p] + 4ull * (nbs[p] + 1);
-  PTWM_HIP_TRY(ctx.h_enc.ensure(host_bytes + nblk * sizeof(IlvEncBlock) + np * 8 + 64));
+  PTWM_HIP_TRY(ctx.h_enc.ensure(host_bytes + nblk * sizeof(IlvEncBlock) + 64));
   uint8_t* hb = static_cast<uint8_t*>(ctx.h_enc.ptr);
   IlvEncBlock* hblk = reinterpret_cast<IlvEncBlock*>(hb + host_bytes);
   std::memcpy(hblk, blocks.data(), nblk * sizeof(IlvEncBlock));
+  std::vector<uint8_t> keep;
+  if (int64_t rc = ilv_store_planes(ctx, src, n, np, out_dev, res, form.data(), keep); rc != kOk) return rc;
   uint64_t hoff = 0;
   for (uint32_t p = 0; p < np; ++p) {
     const uint64_t dst = out_dev + res[p].offset;
-    if (!res[p].coded) {
-      if (n[p] == 0 && identity_fallback) continue;
-      uint64_t raw_dst = dst;
-      if (!identity_fallback) {
-        uint8_t* tag = hb + host_bytes + nblk * sizeof(IlvEncBlock) + 8 * p;
-        *tag = 0;
-        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), tag, 1, hipMemcpyHostToDevice, s));
-        raw_dst = dst + 1;
-      }
-      if (n[p])
-        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(raw_dst), reinterpret_cast<const void*>(src[p]), n[p],
-                                    hipMemcpyDeviceToDevice, s));
-      continue;
-    }
+    if (!res[p].coded) continue;
     uint8_t* h = hb + hoff;
     std::memset(h, 0, head[p]);
     h[0] = 1;

@@ -3,8 +3,8 @@
 // Per call, any number of planes: histogram kernel (shared with huff_ilv) ->
 // host normalisation (the reference's normalize_freqs) -> size kernel (word
 // counts per block) -> host layout and header / offset-table uploads ->
-// write kernel.  A plane whose coded payload is not smaller than the plane
-// is stored instead.  Decode runs through ilv_decode_tensors (family
+// write kernel.  Each plane takes the smallest payload form
+// (ilv_choose_form): coded, packed nibbles or stored.  Decode runs through ilv_decode_tensors (family
 // kFamilyRans).
 #include <hip/hip_runtime.h>
 
@@ -89,23 +89,22 @@ int64_t rilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, 
   // ---- layout: payloads at 256-byte aligned offsets ----
   uint64_t off = 0;
   std::vector<uint64_t> head(np, 0);
+  std::vector<uint32_t> form(np, kFormStored);
   for (uint32_t p = 0; p < np; ++p) {
     off = align_up(off, 256);
     res[p].offset = off;
-    bool coded = false;
-    if (codable[p]) {
+    uint64_t pay = 0;
+    bool codable_p = codable[p];
+    if (codable_p) {
       uint64_t d = 0;
       for (uint32_t b = 0; b < nbs[p]; ++b) d += align_up(kRilvBlockHead + 2ull * bwords[first_block[p] + b], 4);
       head[p] = align_up(5 + header[p].size(), 4);
-      const uint64_t pay = head[p] + 4ull * (nbs[p] + 1) + d;
-      if (pay < (identity_fallback ? n[p] : n[p] + 1) && d <= 0xFFFFFFFFull) {
-        coded = true;
-        res[p].len = pay;
-      }
+      pay = head[p] + 4ull * (nbs[p] + 1) + d;
+      codable_p = d <= 0xFFFFFFFFull;
     }
-    res[p].coded = coded ? 1 : 0;
-    if (!coded) res[p].len = identity_fallback ? n[p] : n[p] + 1;
-    res[p].codec = coded ? kCodecRansIlv : (identity_fallback ? kCodecIdentity : kCodecRansIlv);
+    form[p] = ilv_choose_form(n[p], all_nibbles(&hist[256 * p]), codable_p, pay, identity_fallback, &res[p].len);
+    res[p].coded = form[p] == kFormCoded ? 1 : 0;
+    res[p].codec = form[p] == kFormIdentity ? kCodecIdentity : kCodecRansIlv;
     off += res[p].len;
   }
   const uint64_t total = off;
@@ -113,27 +112,17 @@ int64_t rilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, 
     if (needed) *needed = total;
     return kBufferTooSmall;
   }
-  // ---- headers, offset tables, stored planes; block destinations ----
+  // ---- headers, offset tables, stored / packed planes; block destinations ----
   // (host buffers of the asynchronous uploads stay alive until the final
   // stream synchronisation)
+  std::vector<uint8_t> keep;
+  if (int64_t rc = ilv_store_planes(ctx, src, n, np, out_dev, res, form.data(), keep); rc != kOk) return rc;
   std::vector<std::vector<uint8_t>> hbufs(np);
   std::vector<RilvEncBlock> live;
   std::vector<uint32_t> lw;
   for (uint32_t p = 0; p < np; ++p) {
     const uint64_t dst = out_dev + res[p].offset;
-    if (!res[p].coded) {
-      if (n[p] == 0 && identity_fallback) continue;
-      uint64_t raw_dst = dst;
-      if (!identity_fallback) {
-        static const uint8_t zero = 0;
-        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), &zero, 1, hipMemcpyHostToDevice, s));
-        raw_dst = dst + 1;
-      }
-      if (n[p])
-        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(raw_dst), reinterpret_cast<const void*>(src[p]), n[p],
-                                    hipMemcpyDeviceToDevice, s));
-      continue;
-    }
+    if (!res[p].coded) continue;
     std::vector<uint8_t>& hbuf = hbufs[p];
     hbuf.assign(head[p] + 4ull * (nbs[p] + 1), 0);
     hbuf[0] = 1;

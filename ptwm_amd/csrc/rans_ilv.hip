@@ -2,7 +2,8 @@
 //
 // Wire format (codec wire id 0x7F02, this library's second plane codec; the
 // executable specification is oracle por_rans_ilv_encode/decode):
-//   [tag u8] 0: stored plane bytes follow.  1: coded:
+//   [tag u8] 0: stored plane bytes follow.  2: packed nibbles, as huff_ilv.
+//   1: coded:
 //   [n u32][max_sym u8][f u16 x (max_sym + 1)][0-pad to 4]
 //   [block offset table u32 x (nb + 1)][data],  nb = ceil(n / 16384)
 //   frequencies: the reference's normalisation (rans/compress.rs:72-135),
@@ -43,6 +44,7 @@ struct alignas(16) RilvCtl {
   uint64_t datalen[4];  // block data bytes
   uint64_t raw[4];      // stored plane bytes (tag 0 or raw planes)
   uint32_t coded[4];
+  uint32_t packed[4];   // plane stored as packed nibbles (tag 2)
   uint32_t bad;
   uint32_t pad[3];
   uint16_t cum[264];    // table build scratch: cumulative frequencies
@@ -89,6 +91,7 @@ struct RilvBlock {
   uint32_t nw[4];
   uint64_t raw[4];
   uint32_t coded_mask;
+  uint32_t packed_mask;
 };
 
 template <uint32_t kChain, bool kTail, bool kStaged>
@@ -104,17 +107,8 @@ __device__ __forceinline__ void rilv_decode_block(RilvBlock& st, uint32_t luts, 
     for (uint32_t p = 0; p < NP; ++p) {
       v[p][0] = v[p][1] = v[p][2] = v[p][3] = 0;
       if (st.coded_mask & (1u << p)) continue;
-      // raw plane: 16 bytes of the group
-      const uint64_t a = st.raw[p] + pos;
-      if (count == kIlvGroup && (st.raw[p] & 15u) == 0) {
-        const u32x4 w = gload_nt16(a);
-        v[p][0] = w.x;
-        v[p][1] = w.y;
-        v[p][2] = w.z;
-        v[p][3] = w.w;
-      } else {
-        for (uint32_t k = 0; k < count; ++k) v[p][k >> 2] |= gload_u8(a + k) << (8 * (k & 3));
-      }
+      // stored plane: the group's 16 bytes (or 8 bytes of packed nibbles)
+      load_group(st.raw[p], (st.packed_mask >> p) & 1u, pos, count, v[p]);
 #pragma unroll
       for (int k = 0; k < 4; ++k) v[p][k] = xform_word(ChainInfo<kChain>::xf[p], v[p][k]);
     }
@@ -202,12 +196,17 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
           const IlvPlane& P = T.planes[p];
           ctl.raw[p] = P.base;
           ctl.coded[p] = 0;
+          ctl.packed[p] = 0;
           if (!P.coded) continue;
           const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
           if (P.len == 0) ctl.bad |= kIlvErrHeader;
           else if (pay[0] == 0) {
             if (P.len != n + 1) ctl.bad |= kIlvErrHeader;
             ctl.raw[p] = P.base + 1;
+          } else if (pay[0] == 2) {
+            if (!packed_header_ok(pay, P.len, n)) ctl.bad |= kIlvErrHeader;
+            ctl.raw[p] = P.base + kPackedHeadBytes;
+            ctl.packed[p] = 1;
           } else if (pay[0] == 1 && P.len >= 6 && ld_le32(pay + 1) == n) {
             if (NP - 1 - p < n_slots) ctl.coded[p] = 1;
             else ctl.bad |= kIlvErrHeader;
@@ -265,12 +264,14 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
     const uint64_t bstart = (uint64_t)bi * kIlvBlock;
     RilvBlock st;
     st.coded_mask = 0;
+    st.packed_mask = 0;
     bool ok = true;
     uint32_t need = 0;
     uint64_t wsrc[4];
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
       st.raw[p] = ctl.raw[p];
+      if (__builtin_amdgcn_readfirstlane(ctl.packed[p])) st.packed_mask |= 1u << p;
       st.x[p] = kRilvL;
       st.sw[p] = 0;
       st.gw[p] = 0;

@@ -40,7 +40,7 @@ struct DevCtx {
   PinnedBuffer h_status;
   PinnedBuffer h_small;
   // huff_ilv encoder / decoder scratch
-  DeviceBuffer enc_planes, enc_hist, enc_codes, enc_blocks, enc_lane_words, enc_block_bytes;
+  DeviceBuffer enc_planes, enc_hist, enc_codes, enc_blocks, enc_lane_words, enc_block_bytes, enc_pack;
   DeviceBuffer ilv_args, ilv_realign;
   // reference-format (Huffman / rANS) encoder scratch
   DeviceBuffer ref_jobs, ref_hist, ref_segs, ref_seglen, ref_codes, ref_rans_tab, ref_rans_segs, ref_rans_scratch,

@@ -65,8 +65,8 @@ def test_header_and_entropy_bound(kind):
     n = 3 * BLOCK + 1234
     if kind == "geo":
         x = rng.geometric(0.3, n).clip(0, 255).astype(np.uint8)
-    elif kind == "nib":
-        x = rng.integers(0, 16, n).astype(np.uint8)
+    elif kind == "nib":  # skewed nibbles (uniform ones are stored packed, see below)
+        x = (16 - rng.geometric(0.3, n).clip(1, 16)).astype(np.uint8)
     elif kind == "skew":
         x = rng.choice([0, 1, 2, 200], n, p=[0.9, 0.05, 0.04, 0.01]).astype(np.uint8)
     else:
@@ -135,3 +135,27 @@ def test_corruptions_rejected():
         O.rans_ilv_decode(bytes(b), n)
     with pytest.raises(O.OracleError):
         O.rans_ilv_decode(p[:-4], n)
+
+
+@pytest.mark.parametrize("enc,dec", [(O.rans_ilv_encode, O.rans_ilv_decode), (O.ilv_encode, O.ilv_decode)],
+                         ids=["rans_ilv", "huff_ilv"])
+def test_packed_nibble_form(enc, dec):
+    """Near-uniform nibble planes (MXFP4 codes) are stored two symbols per
+    byte: [2][n u32][0 0 0][byte i = s[2i] | s[2i+1] << 4], the smallest of
+    the three forms for them; malformed packed payloads are rejected."""
+    rng = np.random.default_rng(4)
+    for n in (16, 17, 18, 1001, 3 * BLOCK + 5):
+        x = rng.integers(0, 16, n).astype(np.uint8)
+        p = enc(x.tobytes())
+        assert p[0] == 2 and struct.unpack_from("<I", p, 1)[0] == n and p[5:8] == b"\0\0\0"
+        assert len(p) == 8 + (n + 1) // 2
+        assert all(p[8 + i // 2] >> (4 * (i & 1)) & 15 == x[i] for i in range(n))
+        assert dec(p, n) == x.tobytes()
+    p = bytearray(enc(rng.integers(0, 16, 101).astype(np.uint8).tobytes()))
+    for bad in (bytes(p[:-1]), bytes(p) + b"\0", bytes(p[:5]) + b"\1" + bytes(p[6:]),
+                bytes(p[:-1]) + bytes([p[-1] | 0x10])):
+        with pytest.raises(O.OracleError):
+            dec(bad, 101)
+    # a skewed nibble plane still codes (smaller than packed)
+    y = (16 - rng.geometric(0.45, 20000).clip(1, 16)).astype(np.uint8)
+    assert enc(y.tobytes())[0] == 1
