@@ -363,21 +363,27 @@ struct BlockState {
   uint32_t nw[NP];
   uint32_t q[NP];
   uint32_t t64[NP];     // LDS address of a pair-mode plane's 64-entry table
+  uint32_t rbytes[NP];   // bytes of a raw plane's data (0 for a coded plane)
   uint32_t coded_mask;   // bit p: plane p is huff_ilv coded
   uint32_t pair_mask;    // bit p: plane p decodes in pair mode
   uint32_t packed_mask;  // bit p: plane p is stored as packed nibbles
 };
 
-// Load the raw (uncoded) planes' bytes of the group at plane position pos.
+// Load the raw (uncoded) planes' bytes of the group at plane position pos:
+// full blocks with aligned planes issue one load per plane (expanded by the
+// consumer), other blocks load and expand the group's symbols.
 template <uint32_t kChain, bool kTail>
 __device__ __forceinline__ void load_raw(const BlockState<ChainInfo<kChain>::np>& st, uint64_t pos, uint64_t n,
-                                         uint32_t (&x)[ChainInfo<kChain>::np][4]) {
+                                         uint32_t (&x)[ChainInfo<kChain>::np][4], bool live = true) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
-  const uint32_t count = group_count<kTail>(pos, n);
 #pragma unroll
   for (uint32_t p = 0; p < NP; ++p) {
-    if (st.coded_mask & (1u << p)) continue;
-    load_group(st.raw[p], (st.packed_mask >> p) & 1u, pos, count, x[p]);
+    if constexpr (kTail) {
+      if (st.coded_mask & (1u << p)) continue;
+      load_group(st.raw[p], (st.packed_mask >> p) & 1u, pos, group_count<kTail>(pos, n), x[p]);
+    } else {
+      load_group_fast(st.raw[p], st.rbytes[p], (st.packed_mask >> p) & 1u, (uint32_t)pos, live, x[p]);
+    }
   }
 }
 
@@ -392,6 +398,10 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
   constexpr uint32_t RATIO = ChainInfo<kChain>::ratio;
   uint32_t nxt[NP][4];
   load_raw<kChain, kTail>(st, bstart + (uint64_t)kIlvGroup * lane, n, nxt);
+  if constexpr (!kTail) {
+#pragma unroll
+    for (uint32_t k = 0; k < RATIO; ++k) vmem_nop(out, k);
+  }
   for (uint32_t r = 0; r < kIlvRounds; ++r) {
     const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
     const uint32_t count = group_count<kTail>(pos, n);
@@ -430,19 +440,34 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
     }
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
-      if (st.coded_mask & (1u << p)) continue;
+      if constexpr (kTail) {
+        if (st.coded_mask & (1u << p)) continue;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) v[p][k] = xform_word(ChainInfo<kChain>::xf[p], nxt[p][k]);
+        for (int k = 0; k < 4; ++k) v[p][k] = xform_word(ChainInfo<kChain>::xf[p], nxt[p][k]);
+      } else {
+        // every plane's load is consumed here (coded planes loaded zeros)
+        uint32_t x[4];
+        expand_group((st.packed_mask >> p) & 1u, nxt[p], x);
+        const bool raw = !(st.coded_mask & (1u << p));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[p][k] = raw ? xform_word(ChainInfo<kChain>::xf[p], x[k]) : v[p][k];
+      }
     }
-    if (r + 1 < kIlvRounds) load_raw<kChain, kTail>(st, pos + (uint64_t)kIlvGroup * 64u, n, nxt);
+    if constexpr (kTail) {
+      if (r + 1 < kIlvRounds) load_raw<kChain, kTail>(st, pos + (uint64_t)kIlvGroup * 64u, n, nxt);
+    } else {
+      load_raw<kChain, kTail>(st, pos + (uint64_t)kIlvGroup * 64u, n, nxt, r + 1 < kIlvRounds);
+    }
     if (kTail && count == 0) continue;
     uint32_t o[4 * RATIO];
     merge_group<kChain>(v, o);
     const uint64_t dst = out + RATIO * pos;
-    if (count == kIlvGroup) {
+    if constexpr (!kTail) {
+      store_group_full<RATIO>(dst, lane, o);
+    } else if (count == kIlvGroup) {
 #pragma unroll
       for (uint32_t k = 0; k < RATIO; ++k)
-        gstore_nt16(dst + 16 * k, u32x4_make(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]));
+        g_st<u32x4>(dst + 16 * k, u32x4_make(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]));
     } else {
       for (uint32_t k = 0; k < RATIO * count; ++k) gstore_u8(dst + k, o[k >> 2] >> (8 * (k & 3)));
     }
@@ -504,7 +529,8 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
     const uint32_t nb = (uint32_t)((n + kIlvBlock - 1) / kIlvBlock);
     if (ti != cur) {
       // ---- new tensor: parse its plane headers and build the LDS tables ----
-      if (bad) atomicOr(&status[cur], bad);
+      bad = wave_or_status(bad);
+      if (bad && lane == 0) atomicOr(&status[cur], bad);
       bad = 0;
       cur = ti;
       __syncthreads();  // every wavefront is done with the previous tables
@@ -612,7 +638,15 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       bad |= kIlvErrBlock;
       continue;
     }
-    const bool full = bstart + kIlvBlock <= n;
+    // the fast path takes whole blocks of planes under 4 GiB whose raw
+    // planes are aligned
+    bool full = bstart + kIlvBlock <= n && n <= 0xFFFFFFFFull;
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p) {
+      const bool packed = (st.packed_mask >> p) & 1u;
+      st.rbytes[p] = (st.coded_mask & (1u << p)) ? 0u : (uint32_t)(packed ? (n + 1) / 2 : n);
+      if (!(st.coded_mask & (1u << p)) && !raw_aligned(st.raw[p], packed)) full = false;
+    }
     const uint64_t out = T.out;
     uint32_t q0[NP];
     // skew uniform planes only when the staging budget has room for it
@@ -693,7 +727,8 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       if ((used + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
     }
   }
-  if (bad) atomicOr(&status[cur], bad);
+  bad = wave_or_status(bad);
+  if (bad && lane == 0) atomicOr(&status[cur], bad);
 }
 
 // ---------------------------------------------------------------------------

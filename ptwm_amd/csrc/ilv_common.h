@@ -224,4 +224,97 @@ __device__ __forceinline__ void load_group(uint64_t base, bool packed, uint64_t 
   }
 }
 
+// Fast path of the raw-plane loads (full groups of planes under 4 GiB, bases
+// aligned as raw_aligned requires): one buffer load per plane per round,
+// issued for every plane unconditionally (a coded plane has an empty
+// resource: loads past num_records return zeros without a memory access),
+// so each round issues a fixed sequence of memory operations and the wait
+// before the consumer (expand_group) leaves the stores issued after the
+// load in flight.  A packed plane's 16-byte load at pos / 2 uses its first
+// 8 bytes; the rest may lie past the plane and then reads as zeros.
+__device__ __forceinline__ bool raw_aligned(uint64_t base, bool packed) {
+  return (base & (packed ? 7u : 15u)) == 0;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(uint64_t base, uint32_t bytes) {
+  // raw buffer: stride 0, 32-bit data format word of the gfx9 family
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// live == false: a load at offset `bytes`, past the resource (zeros, no
+// memory access), keeping the sequence of memory operations fixed.
+__device__ __forceinline__ void load_group_fast(uint64_t base, uint32_t bytes, bool packed, uint32_t pos, bool live,
+                                                uint32_t (&x)[4]) {
+  const uint32_t off = live ? (packed ? pos / 2 : pos) : bytes;
+  const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(plane_rsrc(base, bytes), off, 0, 0));
+  x[0] = w.x;
+  x[1] = w.y;
+  x[2] = w.z;
+  x[3] = w.w;
+}
+
+// A vector memory operation that does nothing: a buffer store to an empty
+// resource (num_records 0), discarded without a memory access.  The fast
+// decode loop issues one per output store after its first raw loads, so
+// that the loop is entered with the same count of memory operations behind
+// its loads as every later round has (the raw loads, then the stores); the
+// compiler's wait before the consumer then leaves the stores in flight.
+// (k: distinct offsets, so that repeated calls are not merged)
+__device__ __forceinline__ void vmem_nop(uint64_t base, uint32_t k) {
+  __builtin_amdgcn_raw_buffer_store_b32(0u, plane_rsrc(base, 0), 4 * k, 0, (int)0x80000000u);  // volatile: kept apart
+}
+
+// Store of the RATIO * 16 output bytes of each lane's group in a full round
+// (all 64 lanes storing whole, adjacent groups).  Plain (temporal) stores,
+// so that the L2 combines the pieces of a line; with RATIO 2 the lanes of
+// each quad first exchange halves (DPP quad permutes), so that every store
+// instruction writes whole 64-byte segments: lane q of the quad at qb
+// stores bytes [16 q, 16 q + 16) of [qb, qb + 64) and then of
+// [qb + 64, qb + 128), taken from lane q / 2, resp. 2 + q / 2, half q & 1.
+template <uint32_t RATIO>
+__device__ __forceinline__ void store_group_full(uint64_t dst, uint32_t lane, const uint32_t (&o)[4 * RATIO]) {
+  if constexpr (RATIO == 2) {
+    const uint32_t q = lane & 3u;
+    const uint64_t qb = dst - 32u * q;
+    uint32_t a0[4], a1[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      // quad_perm [0,0,1,1] = 0x50, [2,2,3,3] = 0xFA
+      const uint32_t x0 = __builtin_amdgcn_mov_dpp(o[d], 0x50, 0xF, 0xF, false);
+      const uint32_t y0 = __builtin_amdgcn_mov_dpp(o[4 + d], 0x50, 0xF, 0xF, false);
+      const uint32_t x1 = __builtin_amdgcn_mov_dpp(o[d], 0xFA, 0xF, 0xF, false);
+      const uint32_t y1 = __builtin_amdgcn_mov_dpp(o[4 + d], 0xFA, 0xF, 0xF, false);
+      a0[d] = (q & 1u) ? y0 : x0;
+      a1[d] = (q & 1u) ? y1 : x1;
+    }
+    g_st<u32x4>(qb + 16u * q, u32x4_make(a0[0], a0[1], a0[2], a0[3]));
+    g_st<u32x4>(qb + 64u + 16u * q, u32x4_make(a1[0], a1[1], a1[2], a1[3]));
+  } else {
+#pragma unroll
+    for (uint32_t k = 0; k < RATIO; ++k)
+      g_st<u32x4>(dst + 16 * k, u32x4_make(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]));
+  }
+}
+
+// OR of a status word (bits 0..7) over the wavefront's active lanes, so
+// that one lane reports it: per-lane atomics on one status word serialise.
+__device__ __forceinline__ uint32_t wave_or_status(uint32_t v) {
+  uint32_t r = 0;
+#pragma unroll
+  for (uint32_t b = 0; b < 8; ++b)
+    if (__ballot((v >> b) & 1u)) r |= 1u << b;
+  return r;
+}
+
+// The 16 symbols of a group loaded by load_group_fast, one per byte.  Reads
+// all four words whatever `packed` is (selects, no branch), so that every
+// path waits for the load at this point and nowhere later.
+__device__ __forceinline__ void expand_group(bool packed, const uint32_t (&x)[4], uint32_t (&v)[4]) {
+  uint32_t u[4];
+  zip2(x[0] & 0x0F0F0F0Fu, (x[0] >> 4) & 0x0F0F0F0Fu, u[0], u[1]);
+  zip2(x[1] & 0x0F0F0F0Fu, (x[1] >> 4) & 0x0F0F0F0Fu, u[2], u[3]);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = packed ? u[k] : x[k];
+}
+
 }  // namespace ptwm

@@ -90,6 +90,7 @@ struct RilvBlock {
   uint32_t wpos[4];   // words taken
   uint32_t nw[4];
   uint64_t raw[4];
+  uint32_t rbytes[4];  // bytes of a raw plane's data (0 for a coded plane)
   uint32_t coded_mask;
   uint32_t packed_mask;
 };
@@ -99,6 +100,18 @@ __device__ __forceinline__ void rilv_decode_block(RilvBlock& st, uint32_t luts, 
                                                   uint64_t bstart, uint32_t lane) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
   constexpr uint32_t RATIO = ChainInfo<kChain>::ratio;
+  // full blocks: the raw planes' next group is loaded a round ahead, one
+  // buffer load per plane (see load_group_fast), so its latency overlaps
+  // the round's rANS steps
+  uint32_t nxt[NP][4];
+  if constexpr (!kTail) {
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p)
+      load_group_fast(st.raw[p], st.rbytes[p], (st.packed_mask >> p) & 1u, (uint32_t)(bstart + kIlvGroup * lane), true,
+                      nxt[p]);
+#pragma unroll
+    for (uint32_t k = 0; k < RATIO; ++k) vmem_nop(out, k);
+  }
   for (uint32_t r = 0; r < kIlvRounds; ++r) {
     const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
     const uint32_t count = group_count<kTail>(pos, n);
@@ -106,11 +119,26 @@ __device__ __forceinline__ void rilv_decode_block(RilvBlock& st, uint32_t luts, 
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
       v[p][0] = v[p][1] = v[p][2] = v[p][3] = 0;
-      if (st.coded_mask & (1u << p)) continue;
-      // stored plane: the group's 16 bytes (or 8 bytes of packed nibbles)
-      load_group(st.raw[p], (st.packed_mask >> p) & 1u, pos, count, v[p]);
+      if constexpr (kTail) {
+        if (st.coded_mask & (1u << p)) continue;
+        // stored plane: the group's 16 bytes (or 8 bytes of packed nibbles)
+        load_group(st.raw[p], (st.packed_mask >> p) & 1u, pos, count, v[p]);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) v[p][k] = xform_word(ChainInfo<kChain>::xf[p], v[p][k]);
+        for (int k = 0; k < 4; ++k) v[p][k] = xform_word(ChainInfo<kChain>::xf[p], v[p][k]);
+      } else {
+        // every plane's load is consumed here (coded planes loaded zeros)
+        uint32_t x[4];
+        expand_group((st.packed_mask >> p) & 1u, nxt[p], x);
+        const bool raw = !(st.coded_mask & (1u << p));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[p][k] = raw ? xform_word(ChainInfo<kChain>::xf[p], x[k]) : 0u;
+      }
+    }
+    if constexpr (!kTail) {
+#pragma unroll
+      for (uint32_t p = 0; p < NP; ++p)
+        load_group_fast(st.raw[p], st.rbytes[p], (st.packed_mask >> p) & 1u, (uint32_t)(pos + kIlvGroup * 64u),
+                        r + 1 < kIlvRounds, nxt[p]);
     }
 #pragma unroll
     for (uint32_t t = 0; t < kIlvGroup; ++t) {
@@ -127,10 +155,12 @@ __device__ __forceinline__ void rilv_decode_block(RilvBlock& st, uint32_t luts, 
     uint32_t o[4 * RATIO];
     merge_group<kChain>(v, o);
     const uint64_t dst = out + RATIO * pos;
-    if (count == kIlvGroup) {
+    if constexpr (!kTail) {
+      store_group_full<RATIO>(dst, lane, o);
+    } else if (count == kIlvGroup) {
 #pragma unroll
       for (uint32_t k = 0; k < RATIO; ++k)
-        gstore_nt16(dst + 16 * k, u32x4_make(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]));
+        g_st<u32x4>(dst + 16 * k, u32x4_make(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]));
     } else {
       for (uint32_t k = 0; k < RATIO * count; ++k) gstore_u8(dst + k, o[k >> 2] >> (8 * (k & 3)));
     }
@@ -186,7 +216,8 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
     const uint32_t nb = (uint32_t)((n + kIlvBlock - 1) / kIlvBlock);
     if (ti != cur) {
       // ---- new tensor: parse the plane headers, build the slot tables ----
-      if (bad) atomicOr(&status[cur], bad);
+      bad = wave_or_status(bad);
+      if (bad && lane == 0) atomicOr(&status[cur], bad);
       bad = 0;
       cur = ti;
       __syncthreads();
@@ -298,7 +329,15 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
       bad |= kIlvErrBlock;
       continue;
     }
-    const bool full = bstart + kIlvBlock <= n;
+    // the fast path takes whole blocks of planes under 4 GiB whose raw
+    // planes are aligned
+    bool full = bstart + kIlvBlock <= n && n <= 0xFFFFFFFFull;
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p) {
+      const bool packed = (st.packed_mask >> p) & 1u;
+      st.rbytes[p] = (st.coded_mask & (1u << p)) ? 0u : (uint32_t)(packed ? (n + 1) / 2 : n);
+      if (!(st.coded_mask & (1u << p)) && !raw_aligned(st.raw[p], packed)) full = false;
+    }
     const uint64_t out = T.out;
     if (need <= stage_words) {
       // coalesced copy of each coded plane's words into this wavefront's LDS
@@ -328,7 +367,8 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
       if (st.wpos[p] != st.nw[p] || __ballot(st.x[p] != kRilvL) != 0) bad |= kRilvErrState;
     }
   }
-  if (bad) atomicOr(&status[cur], bad);
+  bad = wave_or_status(bad);
+  if (bad && lane == 0) atomicOr(&status[cur], bad);
 }
 
 // ---------------------------------------------------------------------------
