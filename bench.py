@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+import gc
 import json
 import os
 import sys
@@ -115,10 +116,17 @@ HUF, RANS = 1, 3   # reference codec wire ids (crates/ptwm-core/src/codec.rs:7-9
 EXACT_ROUTE = "decode_exact (reference streams) + merge"
 
 
-def build_workload(name: str) -> Workload:
+MIN_DISTINCT_BYTES = 1 << 30   # rotate inputs of smaller workloads (the MALL holds 256 MB)
+
+
+def build_workload(name: str, resident: bool = False) -> Workload:
     """`name` is a workload below, optionally suffixed "+crc" (every plane's
     CRC-32 in the plan, verified by the decode) and/or "+hash" (every
-    tensor's XXH64 in the plan, verified by the decode)."""
+    tensor's XXH64 in the plan, verified by the decode).  A workload under
+    1 GiB is built in as many distinct replicas (other seeds) as make 1 GiB,
+    and consecutive steps decode consecutive replicas, so that no step finds
+    its inputs in the 256 MB Infinity Cache; `resident` builds one replica
+    (cache-resident numbers)."""
     import torch
 
     from ptwm_amd import api, plan
@@ -193,8 +201,35 @@ def build_workload(name: str) -> Workload:
     if native == "rans_ilv":
         desc += ", planes coded with rans_ilv (GPU-native interleaved rANS)"
         kernel = kernel.replace("ilv_decode_kernel", "rilv_decode_kernel")
-    wl = Workload(desc)
+    if resident:
+        n_rep = 1
+    else:
+        one = sum(int(np_prod(shape)) for shape, _ in specs)
+        n_rep = max(1, -(-MIN_DISTINCT_BYTES // max(one, 1)))
+    reps = [build_replica(desc, specs, CH, ref, native, opts, r) for r in range(n_rep)]
+    wl = reps[0]
+    wl.replicas = reps
     wl.kernel = kernel
+    wl.encode_gbs = sum(r.restored for r in reps) / sum(r.enc_s for r in reps) / 1e9
+    wl.comp_bytes = round(sum(r.comp_bytes for r in reps) / n_rep)
+    log(f"[bench] {n_rep} replica(s) of {wl.restored / 2**30:.3f} GiB; encoded at {wl.encode_gbs:.1f} GB/s input, "
+        f"ratio {wl.comp_bytes / wl.restored:.4f}")
+    return wl
+
+
+def np_prod(shape):
+    n = 1
+    for d in shape:
+        n *= d
+    return n
+
+
+def build_replica(desc, specs, CH, ref, native, opts, rep) -> Workload:
+    import torch
+
+    from ptwm_amd import api, plan
+
+    wl = Workload(desc)
     if ref is not None:
         wl.codec = "reference Huffman / rANS plane payloads (exact route)"
     elif native == "rans_ilv":
@@ -204,10 +239,11 @@ def build_workload(name: str) -> Workload:
     tensors = []
     total_raw = 0
     for i, (shape, kind) in enumerate(specs):
-        raw = gen_tensor(kind, shape, 1000 + i)
+        raw = gen_tensor(kind, shape, 1000 + i + 7919 * rep)
         tensors.append((raw, CH[kind], ref[kind] if ref else None))
         total_raw += raw.numel()
-    log(f"[bench] generated {len(tensors)} tensors, {total_raw / 2**30:.2f} GiB")
+    if rep == 0:
+        log(f"[bench] generated {len(tensors)} tensors, {total_raw / 2**30:.2f} GiB")
     # encode every tensor with the library's GPU encoder into one blob
     cap = total_raw + 65536 * len(tensors) + (1 << 20)
     blob = torch.empty(cap, dtype=torch.uint8, device="cuda:0")
@@ -245,8 +281,7 @@ def build_workload(name: str) -> Workload:
     wl.restored = total_raw
     wl.comp_bytes = sum(p.payload_len for t in plans for p in t.planes)
     wl.plans = plans
-    wl.encode_gbs = total_raw / enc_s / 1e9
-    log(f"[bench] encoded in {enc_s:.2f}s ({wl.encode_gbs:.1f} GB/s input), ratio {wl.comp_bytes / total_raw:.4f}")
+    wl.enc_s = enc_s
     return wl
 
 
@@ -265,8 +300,11 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="llama8b")
-    ap.add_argument("--extra", default="fp8", help="comma list of secondary workloads reported in config")
+    ap.add_argument("--extra", default="fp8,mxfp4,llama8b+crc",
+                    help="comma list of secondary workloads reported in config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--resident", action="store_true",
+                    help="one replica of a workload under 1 GiB (inputs may stay in the Infinity Cache)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (known bytes) to scale FETCH_SIZE/WRITE_SIZE counters")
     args = ap.parse_args()
@@ -283,25 +321,37 @@ def main():
     L = lib()
 
     def measure(wl, steps, warmup):
-        out = torch.empty(wl.out_len, dtype=torch.uint8, device="cuda:0")
+        reps = wl.replicas
+        outs = [torch.empty(r.out_len, dtype=torch.uint8, device="cuda:0") for r in reps]
+        cur = [0]
 
         def step():
+            k = cur[0] % len(reps)
+            cur[0] += 1
             return api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL,
-                                                             wl.plan_bytes, wl.blob, out, 0)
-        for _ in range(warmup):
+                                                             reps[k].plan_bytes, reps[k].blob, outs[k], 0)
+
+        def check(n, when):
+            for r, o in list(zip(reps, outs))[:n]:
+                if not verify(r, o):
+                    raise SystemExit(f"decode mismatch on {wl.name}{when}")
+
+        # warmup decodes every replica once (at least `warmup` steps)
+        for _ in range(max(warmup, len(reps))):
             step()
         torch.cuda.synchronize()
-        if not verify(wl, out):
-            raise SystemExit(f"decode mismatch on {wl.name}")
-        out.zero_()
+        check(len(reps), "")
+        for o in outs:
+            o.zero_()
         torch.cuda.synchronize()
+        cur[0] = 0
         t0 = time.perf_counter()
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        if not verify(wl, out):
-            raise SystemExit(f"decode mismatch on {wl.name} (timed steps)")
+        # the replicas the timed steps decoded were zeroed before them
+        check(min(steps, len(reps)), " (timed steps)")
         ms_step = (t1 - t0) * 1e3 / steps
         # kernel durations: HIP events around the decode kernels on the
         # library stream, in separate (untimed) steps so the events do not
@@ -328,7 +378,7 @@ def main():
         del a, b
         log("[bench] calibration copy: 3 x 1 GiB device-to-device")
     log(f"[bench] workload {args.workload}")
-    wl = build_workload(args.workload)
+    wl = build_workload(args.workload, args.resident)
     ms_step, kms = measure(wl, args.steps, args.warmup)
     value = wl.restored / (ms_step * 1e-3) / 1e9
     traffic = wl.comp_bytes + wl.restored
@@ -336,22 +386,31 @@ def main():
     primary = {"workload": args.workload, "description": wl.name, "restored_bytes": wl.restored,
                "compressed_bytes": wl.comp_bytes, "ratio": round(wl.comp_bytes / wl.restored, 4),
                "encode_gbs": round(wl.encode_gbs, 1), "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
-               "codec": wl.codec}
+               "codec": wl.codec, "replicas": len(wl.replicas),
+               "distinct_input_bytes": sum(r.comp_bytes for r in wl.replicas)}
     kernel_name = wl.kernel
     log(f"[bench] {ms_step:.3f} ms/step, kernel {kms:.3f} ms, {value:.1f} GB/s restored")
     extras = {}
     for name in [x for x in args.extra.split(",") if x and x != args.workload]:
         del wl
+        gc.collect()
         torch.cuda.empty_cache()
-        wl = build_workload(name)
+        wl = build_workload(name, args.resident)
         m2, k2 = measure(wl, max(3, args.steps), 1)
         extras[name] = {"restored_gbs": round(wl.restored / (m2 * 1e-3) / 1e9, 1),
                         "kernel_gbs_restored": round(wl.restored / (k2 * 1e-3) / 1e9, 1),
                         "kernel_gbs_traffic": round((wl.restored + wl.comp_bytes) / (k2 * 1e-3) / 1e9, 1),
                         "ratio": round(wl.comp_bytes / wl.restored, 4), "encode_gbs": round(wl.encode_gbs, 1),
-                        "description": wl.name}
+                        "replicas": len(wl.replicas), "description": wl.name}
     primary["secondary"] = extras
     traffic_meas, traffic_src = measured_traffic(args.workload)
+    ceil = hbm_ceilings()
+    # the workload's bound from those ceilings: its R restored bytes must be
+    # written (write ceiling) and its C + R bytes moved (copy ceiling)
+    t_min = max(primary["restored_bytes"] / (ceil["write_gbs"] * 1e9),
+                (primary["restored_bytes"] + primary["compressed_bytes"]) / (ceil["copy_gbs"] * 1e9))
+    ceil["restored_gbs_bound"] = round(primary["restored_bytes"] / t_min / 1e9, 1)
+    ceil["kernel_frac_of_bound"] = round(t_min / (kms * 1e-3), 4)
     res = {
         "metric": "decode GB/s (restored bytes) per MI355X",
         "value": round(value, 2),
@@ -368,12 +427,41 @@ def main():
         "config": primary,
         "roofline": {"bound": "hbm", "kernel": kernel_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel_ms": round(kms, 4),
-                     "traffic": traffic_meas, "traffic_source": traffic_src},
+                     "traffic": traffic_meas, "traffic_source": traffic_src, "ceilings": ceil},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
+
+
+def hbm_ceilings():
+    """Practical HBM rates of this device, measured in the same run: a 2 GiB
+    device copy (reads + writes) and a 2 GiB fill (writes only), torch's own
+    kernels, best of 5."""
+    import torch
+
+    n = 2 << 30
+    a = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    b = torch.empty_like(a)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def best(fn):
+        ms = []
+        for _ in range(5):
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            ms.append(e0.elapsed_time(e1))
+        return min(ms)
+
+    copy_ms = best(lambda: b.copy_(a))
+    fill_ms = best(lambda: b.fill_(7))
+    del a, b
+    torch.cuda.empty_cache()
+    return {"copy_gbs": round(2 * n / (copy_ms * 1e-3) / 1e9, 1), "write_gbs": round(n / (fill_ms * 1e-3) / 1e9, 1),
+            "source": "torch copy_ / fill_ of 2 GiB on this device, same run"}
 
 
 def cpu_baseline():
@@ -391,20 +479,35 @@ def cpu_baseline():
     w = (torch.randn(4096 * 4096, generator=g) * 0.02).to(torch.bfloat16).view(torch.uint8).numpy().tobytes()
     p0, p1 = O.chain_forward(O.CHAIN_IEEE16_SPLIT2, w)
     enc = [O.encode_plane_chunked(O.CODEC_HUFFMAN, p, 1 << 20) for p in (p0, p1)]
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        planes = [O.decode_plane_chunked(O.CODEC_HUFFMAN, pay, ent, threads=threads) for pay, ent in enc]
-        out = O.chain_inverse(O.CHAIN_IEEE16_SPLIT2, planes)
-        reps += 1
-        if time.perf_counter() - t0 > 10.0:
-            break
-    dt = time.perf_counter() - t0
-    assert out == w
+    def rate(nthreads, seconds):
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            planes = [O.decode_plane_chunked(O.CODEC_HUFFMAN, pay, ent, threads=nthreads) for pay, ent in enc]
+            out = O.chain_inverse(O.CHAIN_IEEE16_SPLIT2, planes)
+            reps += 1
+            if time.perf_counter() - t0 > seconds:
+                break
+        dt = time.perf_counter() - t0
+        assert out == w
+        return len(w) * reps / dt / 1e9, reps
+
+    value, reps = rate(threads, 10.0)
+    one, reps1 = rate(1, 4.0)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     del np
-    return {"value": round(len(w) * reps / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} x 32 MiB bf16 4096x4096 N(0,0.02): Huffman planes in 1 MiB chunks, "
-                      "decode over threads + fused inverse (oracle C restatement)"}
+    return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "value_1_thread": round(one, 3), "cpu_model": model, "nproc": os.cpu_count(),
+            "sample": f"{reps} x 32 MiB bf16 4096x4096 N(0,0.02) at {threads} threads ({reps1} at 1 thread): "
+                      "Huffman planes in 1 MiB chunks, decode over threads + fused inverse (oracle C restatement)"}
 
 
 if __name__ == "__main__":
