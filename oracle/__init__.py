@@ -396,6 +396,23 @@ def ilv_decode(payload, cap: int) -> bytes:
     return out[:n].tobytes()
 
 
+def ilv_encode_coded(plane) -> bytes:
+    """The huff_ilv coded form (tag 1) of a plane whatever its size: test
+    payloads that no encoder would choose but every decoder must accept."""
+    L = lib()
+    L.por_ilv_encode_coded.restype = C.c_int64
+    L.por_ilv_encode_coded.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]
+    L.por_ilv_encode_bound.restype = C.c_size_t
+    L.por_ilv_encode_bound.argtypes = [C.c_size_t]
+    s = _buf(plane)
+    cap = int(L.por_ilv_encode_bound(s.size)) + 4096
+    out = np.zeros(cap, np.uint8)
+    n = L.por_ilv_encode_coded(_ptr(s), s.size, _ptr(out), cap)
+    if n < 0:
+        raise OracleError(n, "ilv_encode_coded")
+    return out[:n].tobytes()
+
+
 def rans_ilv_encode(plane) -> bytes:
     """rans_ilv (this build's GPU-native interleaved rANS codec) payload of
     a plane: the format's specification (por_rans_ilv_encode)."""
@@ -408,6 +425,21 @@ def rans_ilv_encode(plane) -> bytes:
     n = L.por_rans_ilv_encode(_ptr(s), s.size, _ptr(out), cap)
     if n < 0:
         raise OracleError(n, "rans_ilv_encode")
+    return out[:n].tobytes()
+
+
+def rans_ilv_encode_coded(plane) -> bytes:
+    """The rans_ilv coded form (tag 1) of a plane whatever its size (test
+    payloads, as ilv_encode_coded)."""
+    L = lib()
+    L.por_rans_ilv_encode_coded.restype = C.c_int64
+    L.por_rans_ilv_encode_coded.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]
+    s = _buf(plane)
+    cap = 2 * s.size + 65536
+    out = np.zeros(cap, np.uint8)
+    n = L.por_rans_ilv_encode_coded(_ptr(s), s.size, _ptr(out), cap)
+    if n < 0:
+        raise OracleError(n, "rans_ilv_encode_coded")
     return out[:n].tobytes()
 
 

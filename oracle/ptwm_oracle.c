@@ -961,8 +961,11 @@ size_t por_ilv_encode_bound(size_t len) {
     return 1 + len + 5 + 130 + 3 + 4 * (nb + 1) + nb * 64 + len * 11 / 8 + nb * 64 * 4 + 16;
 }
 
-int64_t por_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap) {
-    if (n == 0) { if (cap < 1) return POR_ESMALL; out[0] = 0; return 1; }
+/* force_coded: the coded form (tag 1) whatever its size, POR_EINVAL when the
+ * plane has no code (empty); test fixtures only (decoders must accept any
+ * valid coded payload, also one no encoder would choose). */
+static int64_t ilv_encode_impl(const uint8_t *plane, size_t n, uint8_t *out, size_t cap, int force_coded) {
+    if (n == 0) { if (force_coded) return POR_EINVAL; if (cap < 1) return POR_ESMALL; out[0] = 0; return 1; }
     uint32_t freqs[256];
     por_histogram(plane, n, freqs);
     uint8_t lengths[256];
@@ -994,7 +997,7 @@ int64_t por_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap)
             total += bsz;
         }
         size_t best_other = ilv_all_nibbles(freqs) && ilv_packed_size(n) < 1 + n ? ilv_packed_size(n) : 1 + n;
-        if (data0 + total < best_other && data0 + total <= cap) {
+        if ((force_coded || data0 + total < best_other) && data0 + total <= cap) {
             memset(out, 0, data0 + total);
             out[0] = 1; st32(out + 1, (uint32_t)n);
             memcpy(out + 5, hdr, (size_t)wl);
@@ -1026,11 +1029,20 @@ int64_t por_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap)
         }
         free(words);
     }
+    if (force_coded) return POR_EINVAL;
     if (n <= 0xFFFFFFFFu && ilv_all_nibbles(freqs) && ilv_packed_size(n) < 1 + n) return ilv_emit_packed(plane, n, out, cap);
     if (1 + n > cap) return POR_ESMALL;
     out[0] = 0;
     memcpy(out + 1, plane, n);
     return (int64_t)(1 + n);
+}
+
+int64_t por_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap) {
+    return ilv_encode_impl(plane, n, out, cap, 0);
+}
+
+int64_t por_ilv_encode_coded(const uint8_t *plane, size_t n, uint8_t *out, size_t cap) {
+    return ilv_encode_impl(plane, n, out, cap, 1);
 }
 
 int64_t por_ilv_decode(const uint8_t *p, size_t len, uint8_t *out, size_t cap) {
@@ -1112,8 +1124,9 @@ static size_t rilv_pos(size_t b, int j, int s) {
            (size_t)(s % ILV_GROUP);
 }
 
-int64_t por_rans_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap) {
-    if (n == 0) { if (cap < 1) return POR_ESMALL; out[0] = 0; return 1; }
+/* force_coded: as ilv_encode_impl */
+static int64_t rans_ilv_encode_impl(const uint8_t *plane, size_t n, uint8_t *out, size_t cap, int force_coded) {
+    if (n == 0) { if (force_coded) return POR_EINVAL; if (cap < 1) return POR_ESMALL; out[0] = 0; return 1; }
     uint32_t raw[256];
     por_histogram(plane, n, raw);
     uint16_t f[256], cum[256];
@@ -1144,7 +1157,7 @@ int64_t por_rans_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t
             total += (4 + 256 + 2 * nwb + 3) & ~(size_t)3;
         }
         size_t best_other = ilv_all_nibbles(raw) && ilv_packed_size(n) < 1 + n ? ilv_packed_size(n) : 1 + n;
-        if (data0 + total < best_other && data0 + total <= cap && total <= 0xFFFFFFFFu) {
+        if ((force_coded || data0 + total < best_other) && data0 + total <= cap && total <= 0xFFFFFFFFu) {
             memset(out, 0, data0 + total);
             out[0] = 1; st32(out + 1, (uint32_t)n);
             out[5] = (uint8_t)max_sym;
@@ -1180,11 +1193,20 @@ int64_t por_rans_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t
         }
         free(words); free(bw);
     }
+    if (force_coded) return POR_EINVAL;
     if (n <= 0xFFFFFFFFu && ilv_all_nibbles(raw) && ilv_packed_size(n) < 1 + n) return ilv_emit_packed(plane, n, out, cap);
     if (1 + n > cap) return POR_ESMALL;
     out[0] = 0;
     memcpy(out + 1, plane, n);
     return (int64_t)(1 + n);
+}
+
+int64_t por_rans_ilv_encode(const uint8_t *plane, size_t n, uint8_t *out, size_t cap) {
+    return rans_ilv_encode_impl(plane, n, out, cap, 0);
+}
+
+int64_t por_rans_ilv_encode_coded(const uint8_t *plane, size_t n, uint8_t *out, size_t cap) {
+    return rans_ilv_encode_impl(plane, n, out, cap, 1);
 }
 
 int64_t por_rans_ilv_decode(const uint8_t *p, size_t len, uint8_t *out, size_t cap) {

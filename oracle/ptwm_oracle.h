@@ -139,12 +139,14 @@ int64_t por_decode_plane_chunked_mt(int codec, const uint8_t *payload, size_t pa
  * lane sub-streams per 16384-symbol block. ---- */
 int por_ilv_lengths(const uint32_t freqs[256], uint8_t lengths[256]);
 int64_t por_ilv_encode(const uint8_t *plane, size_t len, uint8_t *out, size_t cap);
+int64_t por_ilv_encode_coded(const uint8_t *plane, size_t n, uint8_t *out, size_t cap);
 int64_t por_ilv_decode(const uint8_t *payload, size_t len, uint8_t *out, size_t cap);
 size_t por_ilv_encode_bound(size_t len);
 /* ---- rans_ilv: this build's GPU-native interleaved rANS plane codec (no
  * reference counterpart; the format is specified above por_rans_ilv_encode).
  * Encode returns the payload length (stored when coding does not shrink). */
 int64_t por_rans_ilv_encode(const uint8_t *plane, size_t len, uint8_t *out, size_t cap);
+int64_t por_rans_ilv_encode_coded(const uint8_t *plane, size_t n, uint8_t *out, size_t cap);
 int64_t por_rans_ilv_decode(const uint8_t *payload, size_t len, uint8_t *out, size_t cap);
 
 /* ---- integrity (crc32fast 1.5.0 / xxhash-rust 0.8.18 / blake3 1.x) ---- */

@@ -18,6 +18,11 @@ constexpr uint32_t kIlvMaxLds = 81920;      // LDS budget of one decode workgrou
 constexpr uint32_t kIlvErrHeader = 1;   // tag / length / weights / table bounds
 constexpr uint32_t kIlvErrBlock = 2;    // block offsets or lane word counts inconsistent
 constexpr uint32_t kIlvErrLane = 4;     // a lane's word count disagrees with its codes
+// Not an input error: a coded plane found no LDS table slot in this launch
+// (the host reserves slots for the planes whose payload length is neither
+// the stored nor the packed length) and the tensor is decoded again with a
+// slot for every plane.
+constexpr uint32_t kIlvRetrySlots = 16;
 
 struct IlvPlane {
   uint64_t base;   // coded: payload address; raw: plane bytes (16-byte aligned)

@@ -68,143 +68,167 @@ constexpr uint32_t kIlvPairLutBytes = 8192;
 
 // Build-time scratch, shared by every plane of the workgroup.
 struct BuildScratch {
-  uint16_t rev[256];
   uint16_t t64raw[64];  // pair mode: 6-bit single table with raw symbols
-  uint32_t counts[16];
-  uint32_t next_code[16];
-  uint32_t wave_len_count[4][16];
-  uint32_t nw, hb, err, hdr_len, max_bits, pair;
+  uint8_t sorted[256];  // symbols by (code length, symbol): canonical code order
+  uint32_t wave_len_count[4][12];  // per wavefront: symbols of each length ([0]: any length > 11)
+  uint32_t cnt[12];                // symbols of each length
+  uint32_t off[12];                // per length: canonical index of its first symbol
+  uint32_t base[12];               // per length: first canonical index minus first code
+  uint32_t lim[12];                // per length: end of the codes of length <= l, left-aligned to 11 bits
+  uint32_t err, hdr_len, pair, max_bits;
 };
 
-// Per-workgroup decode state kept in LDS after the tables (t64 first: its
-// 128-byte tables stay aligned for the and_or entry addressing).
+constexpr uint32_t kIlvHeadWords = 36;  // payload bytes kept per plane: tag, n, weights (<= 135)
+
 struct alignas(16) DecodeCtl {
   uint16_t t64[4][64];  // pair-mode planes: 6-bit single tables (symbol')
+  uint32_t head[4][kIlvHeadWords];  // first 144 bytes of each native payload
+  uint32_t last[4];                 // its last byte
   BuildScratch bs;
   uint64_t table[4], data[4], datalen[4], raw[4];  // per plane
   uint32_t coded[4];
   uint32_t pair[4];
   uint32_t packed[4];   // plane stored as packed nibbles (tag 2)
+  uint32_t slot[4];     // LDS table slot of a coded plane
   uint32_t bad;
+  uint32_t pad[3];
 };
 static_assert(sizeof(DecodeCtl) % 16 == 0, "DecodeCtl keeps the staging area 16-byte aligned");
 
-// Build the tables of one plane from the weights header at hdr (hdr_avail
-// bytes readable), symbols transformed by `xf`: the pair table at `tab` plus
-// the 6-bit table at `t64` when pair_ok and the code allows it, else the
-// single table at `tab`.  All 256 threads of the workgroup take part.  Sets
+// Build the tables of one plane from the weights header at hdr (LDS,
+// hdr_avail bytes valid), symbols transformed by `xf`: the pair table at
+// `tab` plus the 6-bit table at `t64` when pair_ok and the code allows it,
+// else the single table at `tab`.  All 256 threads of the workgroup take
+// part: every thread evaluates the header and the per-length counts
+// (uniform values), and every table entry is filled by decoding its window
+// against the canonical limits: with codes assigned in (length, symbol)
+// order, the codes of length <= l, left-aligned to 11 bits, are exactly the
+// values below lim[l], so a window's code length is 1 + the number of
+// limits it reaches and its symbol is sorted[base[len] + code].  Sets
 // bs.err (nonzero: invalid header), bs.pair and bs.hdr_len.
 __device__ void build_tables(uint16_t* tab, uint16_t* t64, bool pair_ok, uint32_t xf, BuildScratch& bs,
                              const uint8_t* hdr, uint64_t hdr_avail) {
-  const uint32_t t = threadIdx.x;
-  if (t == 0) {
-    uint32_t err = 0, n = 0, hb = 0;
-    if (hdr_avail < 1 || !(hdr[0] & 0x80)) err = 1;
-    else if (hdr[0] == 0x80) {
-      if (hdr_avail < 2) err = 1;
-      else {
-        n = hdr[1] ? hdr[1] : 256;
-        hb = 2;
-        if (n < 128) err = 1;
-      }
+  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
+  // weights header (weights.rs): 0x80 | n, or 0x80, n (n = 128..256)
+  uint32_t err = 0, n = 0, hb = 0;
+  const uint32_t h0 = hdr_avail >= 1 ? hdr[0] : 0u;
+  if (!(h0 & 0x80u)) {
+    err = 1;
+  } else if (h0 == 0x80u) {
+    if (hdr_avail < 2) {
+      err = 1;
     } else {
-      n = hdr[0] & 0x7F;
-      hb = 1;
-      if (n == 0) err = 1;
+      const uint32_t h1 = hdr[1];
+      n = h1 ? h1 : 256u;
+      hb = 2;
+      if (n < 128) err = 1;
     }
-    if (!err && hdr_avail < hb + (n + 1) / 2) err = 1;
-    bs.nw = n;
-    bs.hb = hb;
-    bs.err = err;
-    bs.hdr_len = hb + (n + 1) / 2;
+  } else {
+    n = h0 & 0x7Fu;
+    hb = 1;
+    if (n == 0) err = 1;
   }
-  __syncthreads();
-  const uint32_t n = bs.nw, hb = bs.hb;
+  if (!err && hdr_avail < hb + (n + 1) / 2) err = 1;
   uint32_t w = 0;
-  if (!bs.err && t < n) {
-    uint8_t b = hdr[hb + t / 2];
-    w = (t % 2 == 0) ? (b & 0x0F) : ((b >> 4) & 0x0F);
+  if (!err && t < n) {
+    const uint32_t b = hdr[hb + t / 2];
+    w = (t % 2 == 0) ? (b & 0x0Fu) : ((b >> 4) & 0x0Fu);
   }
-  if (w > 11) atomicOr(&bs.err, 1u);
-  if (w > 11) w = 0;
-  // rank among same-length symbols with a smaller index: ballots per length
-  const uint32_t wave = t >> 6, lane = t & 63u;
-  uint32_t rank_in_wave = 0;
+  // per wavefront: symbols of each length and rank among them; [0]: any
+  // length above 11
+  const bool too_long = w > 11;
+  if (too_long) w = 0;
+  uint32_t rank = 0;
+#pragma unroll
   for (uint32_t l = 1; l <= 11; ++l) {
-    uint64_t m = __ballot(w == l);
-    if (w == l) rank_in_wave = __popcll(m & ((1ull << lane) - 1ull));
+    const uint64_t m = __ballot(w == l);
+    if (w == l) rank = __popcll(m & ((1ull << lane) - 1ull));
     if (lane == 0) bs.wave_len_count[wave][l] = __popcll(m);
   }
+  const uint64_t tl = __ballot(too_long);
+  if (lane == 0) bs.wave_len_count[wave][0] = tl ? 1u : 0u;
+  __syncthreads();
+  // symbols per length (threads 1..11), then the canonical codes, offsets
+  // and limits (thread 0, eleven steps)
+  if (t >= 1 && t <= 11)
+    bs.cnt[t] = bs.wave_len_count[0][t] + bs.wave_len_count[1][t] + bs.wave_len_count[2][t] + bs.wave_len_count[3][t];
+  uint32_t before = 0;
+  for (uint32_t wv = 0; wv < wave; ++wv) before += w ? bs.wave_len_count[wv][w] : 0u;
   __syncthreads();
   if (t == 0) {
-    uint32_t maxb = 0, total = 0;
-    bs.counts[0] = 0;
+    if (bs.wave_len_count[0][0] | bs.wave_len_count[1][0] | bs.wave_len_count[2][0] | bs.wave_len_count[3][0]) err = 1;
+    uint32_t code = 0, off = 0, kraft = 0, total = 0, max_bits = 0, cprev = 0;
     for (uint32_t l = 1; l <= 11; ++l) {
-      uint32_t c = 0;
-      for (int wv = 0; wv < 4; ++wv) c += bs.wave_len_count[wv][l];
-      bs.counts[l] = c;
+      const uint32_t c = bs.cnt[l];
+      code = (code + cprev) << 1;  // first code of length l
+      if (c && code + c > (1u << l)) err = 1;
+      bs.off[l] = off;
+      bs.base[l] = off - code;
+      bs.lim[l] = (code + c) << (11 - l);
+      off += c;
       total += c;
-      if (c) maxb = l;
+      kraft += c << (11 - l);
+      if (c) max_bits = l;
+      cprev = c;
     }
-    if (total == 0) bs.err = 1;
-    if (maxb < 1) maxb = 1;
-    uint32_t code = 0;
-    for (uint32_t b = 1; b <= maxb; ++b) {
-      code = (code + bs.counts[b - 1]) << 1;
-      if (code > (1u << b)) bs.err = 1;
-      bs.next_code[b] = code;
-    }
-    // Kraft <= 1 (equivalent to the per-symbol c < 2^len checks of tree.rs)
-    uint32_t kraft = 0;
-    for (uint32_t l = 1; l <= maxb; ++l) kraft += bs.counts[l] << (11 - l);
-    if (kraft > 2048) bs.err = 1;
-    bs.max_bits = maxb;
-    bs.pair = pair_ok && bs.nw <= 16 && maxb <= 6 ? 1u : 0u;
+    if (total == 0 || kraft > 2048) err = 1;
+    if (max_bits < 1) max_bits = 1;
+    bs.err = err;
+    bs.max_bits = max_bits;
+    bs.hdr_len = hb + (n + 1) / 2;
+    bs.pair = pair_ok && n <= 16 && max_bits <= 6 ? 1u : 0u;
   }
   __syncthreads();
+  err = bs.err;
   const uint32_t max_bits = bs.max_bits;
-  if (w) {
-    uint32_t before = 0;
-    for (uint32_t wv = 0; wv < wave; ++wv) before += bs.wave_len_count[wv][w];
-    uint32_t c = bs.next_code[w] + before + rank_in_wave;
-    uint32_t r = 0;
-    for (uint32_t k = 0; k < w; ++k) r |= ((c >> k) & 1u) << (w - 1 - k);
-    bs.rev[t] = (uint16_t)r;
-  } else {
-    bs.rev[t] = 0;
-  }
-  if (bs.pair) {
-    // 6-bit single tables (gap fill: symbol 0, every transform maps 0 to 0)
+  const bool pair = bs.pair;
+  if (w && !err) bs.sorted[bs.off[w] + before + rank] = (uint8_t)t;  // symbols in canonical order
+  // the limits, uniform: scalar registers
+  uint32_t lim[12];
+#pragma unroll
+  for (uint32_t l = 1; l <= 11; ++l) lim[l] = __builtin_amdgcn_readfirstlane(bs.lim[l]);
+  __syncthreads();
+  if (pair) {
+    // 6-bit single tables (raw symbols and symbol'), then the pair table:
+    // the two codes at the start of each 12-bit window (both <= 6 bits)
     if (t < 64) {
-      t64[t] = (uint16_t)max_bits;
-      bs.t64raw[t] = (uint16_t)max_bits;
-    }
-    __syncthreads();
-    if (!bs.err && w) {
-      const uint32_t spread = 1u << (6 - w);
-      for (uint32_t i = 0; i < spread; ++i) {
-        t64[bs.rev[t] | (i << w)] = (uint16_t)(w | (xform_byte(xf, t) << 8));
-        bs.t64raw[bs.rev[t] | (i << w)] = (uint16_t)(w | (t << 8));
+      const uint32_t v = (__builtin_bitreverse32(t) >> 26) << 5;
+      uint32_t len = 1;
+#pragma unroll
+      for (uint32_t l = 1; l <= 10; ++l) len += v >= lim[l] ? 1u : 0u;
+      uint32_t e = max_bits, er = max_bits;
+      if (v < lim[11] && !err) {
+        const uint32_t sym = bs.sorted[bs.base[len] + (v >> (11 - len))];
+        e = len | (xform_byte(xf, sym) << 8);
+        er = len | (sym << 8);
       }
+      t64[t] = (uint16_t)e;
+      bs.t64raw[t] = (uint16_t)er;
     }
     __syncthreads();
-    // pair entries: the two codes at the start of each 12-bit window
-    for (uint32_t i = t; i < 4096; i += 256) {
-      const uint32_t e0 = bs.t64raw[i & 63u];
-      const uint32_t l0 = e0 & 0xFFu;
+    const uint32_t e0 = bs.t64raw[t & 63u];  // window bits 0..5 of every i = t + 256 k
+    const uint32_t l0 = e0 & 0xFFu;
+#pragma unroll 4
+    for (uint32_t k = 0; k < 16; ++k) {
+      const uint32_t i = t + 256 * k;
       const uint32_t e1 = bs.t64raw[(i >> l0) & 63u];
       tab[i] = (uint16_t)((l0 + (e1 & 0xFFu)) | ((e0 >> 8) << 8) | ((e1 >> 8) << 12));
     }
     __syncthreads();
     return;
   }
-  // gap fill: symbol 0 (every transform maps 0 to 0) with length max_bits
-  for (uint32_t i = t; i < 2048; i += 256) tab[i] = (uint16_t)max_bits;
-  __syncthreads();
-  if (!bs.err && w) {
-    const uint16_t e = (uint16_t)(w | (xform_byte(xf, t) << 8));
-    const uint32_t spread = 1u << (11 - w);
-    for (uint32_t i = 0; i < spread; ++i) tab[bs.rev[t] | (i << w)] = e;
+  // single table: a window matching no code (incomplete code) decodes as
+  // symbol 0 (every transform maps 0 to 0) with length max_bits
+#pragma unroll 1
+  for (uint32_t k = 0; k < 8; ++k) {
+    const uint32_t i = t + 256 * k;
+    const uint32_t v = __builtin_bitreverse32(i) >> 21;
+    uint32_t len = 1;
+#pragma unroll
+    for (uint32_t l = 1; l <= 10; ++l) len += v >= lim[l] ? 1u : 0u;
+    uint32_t e = max_bits;
+    if (v < lim[11] && !err) e = len | (xform_byte(xf, bs.sorted[bs.base[len] + (v >> (11 - len))]) << 8);
+    tab[i] = (uint16_t)e;
   }
   __syncthreads();
 }
@@ -340,7 +364,7 @@ __device__ __forceinline__ void group_global(uint32_t lut, const uint32_t* words
   pack_symbols(e, v);
 }
 
-static_assert(sizeof(DecodeCtl) <= 2048, "LDS control block stays small");
+static_assert(sizeof(DecodeCtl) <= 3072, "LDS control block stays small");
 
 }  // namespace
 
@@ -363,6 +387,7 @@ struct BlockState {
   uint32_t nw[NP];
   uint32_t q[NP];
   uint32_t t64[NP];     // LDS address of a pair-mode plane's 64-entry table
+  uint32_t lut[NP];     // LDS address of a coded plane's table
   uint32_t rbytes[NP];   // bytes of a raw plane's data (0 for a coded plane)
   uint32_t coded_mask;   // bit p: plane p is huff_ilv coded
   uint32_t pair_mask;    // bit p: plane p decodes in pair mode
@@ -390,7 +415,7 @@ __device__ __forceinline__ void load_raw(const BlockState<ChainInfo<kChain>::np>
 // The 16 rounds of one block: decode one group per coded plane, take the
 // raw planes' groups (loaded one round ahead, so their latency overlaps the
 // table lookups), merge and store.  luts: LDS address of the first table
-// slot; plane p uses slot NP - 1 - p.  out: output tensor address.
+// slot; plane p uses the table at st.lut[p].  out: output tensor address.
 template <uint32_t kChain, bool kTail, bool kStaged>
 __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& st, uint32_t luts, uint64_t out,
                                              uint64_t n, uint64_t bstart, uint32_t lane) {
@@ -411,7 +436,7 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
     if constexpr (NP == 2 && kStaged && !kTail) {
       if (st.coded_mask == 3u && st.pair_mask == 3u) {
         // both nibble planes in pair mode: their two lookup chains interleaved
-        group_lds_pair2(luts + SLOT, st.q[0], v[0], luts, st.q[1], v[1]);
+        group_lds_pair2(st.lut[0], st.q[0], v[0], st.lut[1], st.q[1], v[1]);
 #pragma unroll
         for (uint32_t p = 0; p < 2; ++p)
 #pragma unroll
@@ -422,7 +447,7 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
       if (done || !(st.coded_mask & (1u << p))) continue;
-      const uint32_t lut = luts + (NP - 1 - p) * SLOT;
+      const uint32_t lut = st.lut[p];
       if (st.pair_mask & (1u << p)) {
         if constexpr (kStaged && !kTail) {
           group_lds_pair(lut, st.q[p], v[p]);
@@ -488,7 +513,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
   // The kernel has no static LDS, so the dynamic area starts at LDS address
   // 0 and every table sits on a SLOT boundary (entry address =
   // (window & mask) | table base).  Layout:
-  //   [n_slots tables (plane p in slot NP-1-p)][DecodeCtl]
+  //   [n_slots tables (coded planes from the last one down)][DecodeCtl]
   //   [4 wavefronts x stage_words][96 spare words]
   extern __shared__ __align__(16) uint8_t smem[];
   DecodeCtl& ctl = *reinterpret_cast<DecodeCtl*>(smem + n_slots * SLOT);
@@ -534,6 +559,25 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       bad = 0;
       cur = ti;
       __syncthreads();  // every wavefront is done with the previous tables
+      // the payload heads (tag, n, weights header) and last bytes, loaded
+      // by all threads at once (coded payloads start 4-byte aligned)
+      for (uint32_t k = t; k < NP * (kIlvHeadWords + 1); k += 256) {
+        const uint32_t p = k / (kIlvHeadWords + 1), w = k % (kIlvHeadWords + 1);
+        const uint64_t base = T.planes[p].base, len = T.planes[p].len;
+        uint32_t v = 0;
+        if (T.planes[p].coded) {
+          if (w == kIlvHeadWords) {
+            if (len) v = gload_u8(base + len - 1);
+          } else if (4ull * w + 4 <= len) {
+            v = g_ld<uint32_t>(base + 4ull * w);
+          } else {
+            for (uint64_t b = 4ull * w; b < len && b < 4ull * w + 4; ++b) v |= gload_u8(base + b) << (8 * (b & 3));
+          }
+        }
+        if (w == kIlvHeadWords) ctl.last[p] = v;
+        else ctl.head[p][w] = v;
+      }
+      __syncthreads();
       if (t == 0) {
         s_bad = 0;
         for (uint32_t p = 0; p < NP; ++p) {
@@ -543,20 +587,32 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
           ctl.packed[p] = 0;
           if (!P.coded) continue;
           // huff_ilv payload: tag 0 stores the plane after the tag byte, tag 2 packs it
-          const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
+          const uint8_t* pay = reinterpret_cast<const uint8_t*>(ctl.head[p]);
           if (P.len == 0) s_bad |= kIlvErrHeader;
           else if (pay[0] == 0) {
             if (P.len != n + 1) s_bad |= kIlvErrHeader;
             s_raw[p] = P.base + 1;
           } else if (pay[0] == 2) {
-            if (!packed_header_ok(pay, P.len, n)) s_bad |= kIlvErrHeader;
+            if (!packed_header_ok(pay, P.len, n, ctl.last[p])) s_bad |= kIlvErrHeader;
             s_raw[p] = P.base + kPackedHeadBytes;
             ctl.packed[p] = 1;
           } else if (pay[0] == 1 && P.len >= 5 && ld_u32le(pay + 1) == n) {
-            if (NP - 1 - p < n_slots) s_coded[p] = 1;
-            else s_bad |= kIlvErrHeader;  // the launch reserved no table slot for it
+            s_coded[p] = 1;
           } else {
             s_bad |= kIlvErrHeader;
+          }
+        }
+        // table slots of the coded planes, from the last plane down (the
+        // exponent plane of the IEEE chains takes slot 0)
+        uint32_t k = 0;
+        for (uint32_t p = NP; p-- > 0;) {
+          ctl.slot[p] = k;
+          if (!s_coded[p]) continue;
+          if (k < n_slots) {
+            ++k;
+          } else {  // no table for it in this launch: the tensor is decoded again
+            s_coded[p] = 0;
+            s_bad |= kIlvRetrySlots;
           }
         }
       }
@@ -565,10 +621,11 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       for (uint32_t p = 0; p < NP; ++p) {
         if (!s_coded[p]) continue;
         const IlvPlane P = T.planes[p];
-        uint16_t* tab16 = reinterpret_cast<uint16_t*>(smem + (NP - 1 - p) * SLOT);
-        const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
+        uint16_t* tab16 = reinterpret_cast<uint16_t*>(smem + ctl.slot[p] * SLOT);
+        const uint8_t* pay = reinterpret_cast<const uint8_t*>(ctl.head[p]);
+        const uint64_t avail = P.len < 4 * kIlvHeadWords ? P.len : 4 * kIlvHeadWords;
         build_tables(tab16, ctl.t64[p], SLOT == kIlvPairLutBytes, ChainInfo<kChain>::xf[p], bs, pay + 5,
-                     P.len >= 5 ? P.len - 5 : 0);
+                     avail >= 5 ? avail - 5 : 0);
         if (t == 0) {
           s_pair[p] = bs.pair;
           if (bs.err) s_bad |= kIlvErrHeader;
@@ -578,11 +635,11 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
           if (data0 > P.len) {
             s_bad |= kIlvErrHeader;
           } else {
+            // tab[0] == 0 and tab[nb] == datalen are checked by the
+            // wavefronts of the first and last block
             s_table[p] = P.base + head;
             s_data[p] = P.base + data0;
             s_datalen[p] = P.len - data0;
-            const uint32_t* tab = reinterpret_cast<const uint32_t*>(P.base + head);
-            if (tab[0] != 0 || tab[nb] != s_datalen[p]) s_bad |= kIlvErrBlock;
           }
         }
         __syncthreads();
@@ -609,6 +666,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       st.nw[p] = 0;
       st.q[p] = 0;
       st.t64[p] = lds_addr(ctl.t64[p]);
+      st.lut[p] = luts + __builtin_amdgcn_readfirstlane(ctl.slot[p]) * SLOT;
       lane_c[p] = tot[p] = first[p] = 0;
       if (!__builtin_amdgcn_readfirstlane(s_coded[p])) continue;
       if (__builtin_amdgcn_readfirstlane(s_pair[p])) st.pair_mask |= 1u << p;
@@ -617,7 +675,8 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       const uint32_t o0 = gload_u32(tab + bi), o1 = gload_u32(tab + bi + 1);
       // offsets of an accepted stream are multiples of 4 (tab[0] == 0 and
       // every block is 64 + 4 x words bytes long)
-      const bool bok = o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64 && (o0 & 3u) == 0;
+      const bool bok = o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64 && (o0 & 3u) == 0 &&
+                       (bi != 0 || o0 == 0) && (bi + 1 != nb || o1 == s_datalen[p]);
       const uint8_t* blk = reinterpret_cast<const uint8_t*>(s_data[p]) + (bok ? o0 : 0);
       const uint32_t c = bok ? gload_u8(reinterpret_cast<uint64_t>(blk) + lane) : 0u;
       const uint32_t incl = wave_incl_scan(c);

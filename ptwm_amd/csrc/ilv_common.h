@@ -183,11 +183,12 @@ __device__ __forceinline__ uint32_t group_count(uint64_t pos, uint64_t n) {
 // Packed-nibble payloads (tag 2 of both GPU-native codecs):
 // [2][n u32][0 0 0][ceil(n / 2) bytes], byte i = s[2i] | s[2i+1] << 4, the
 // high nibble of the last byte 0 when n is odd.
-__device__ __forceinline__ bool packed_header_ok(const uint8_t* pay, uint64_t len, uint64_t n) {
+// pay: the payload's first 8 bytes; last: its last byte.
+__device__ __forceinline__ bool packed_header_ok(const uint8_t* pay, uint64_t len, uint64_t n, uint32_t last) {
   if (len < kPackedHeadBytes || pay[5] || pay[6] || pay[7]) return false;
   const uint64_t pn = (uint64_t)pay[1] | ((uint64_t)pay[2] << 8) | ((uint64_t)pay[3] << 16) | ((uint64_t)pay[4] << 24);
   if (pn != n || len != kPackedHeadBytes + (n + 1) / 2) return false;
-  return !(n & 1u) || (pay[len - 1] >> 4) == 0;
+  return !(n & 1u) || (last >> 4) == 0;
 }
 
 // The 16 symbols of the group at plane position pos (count of them inside

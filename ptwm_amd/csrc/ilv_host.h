@@ -54,6 +54,6 @@ int64_t rilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, 
 
 // Decode and merge the given tensors (fused path; each tensor's coded planes
 // are of its codec family).  Returns kOk or kInvalidInput.
-int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors);
+int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors, bool all_slots = false);
 
 }  // namespace ptwm

@@ -236,7 +236,7 @@ int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, u
   return (int64_t)total;
 }
 
-int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in) {
+int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in, bool all_slots) {
   hipStream_t s = ctx.stream;
   if (tensors_in.empty()) return kOk;
   std::vector<IlvTensor> tensors = tensors_in;
@@ -285,13 +285,18 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
       const IlvTensor& T = tensors[ti];
       if (T.family != fam || T.chain != chain || T.n == 0) continue;
       const uint64_t nb = (T.n + kIlvBlock - 1) / kIlvBlock;
-      // the kernels keep plane p's table in slot n_planes - 1 - p (the
-      // exponent plane, last in every IEEE chain, in slot 0)
+      // LDS table slots and staging for the planes that may be coded: a
+      // native payload of the stored (n + 1) or packed (8 + ceil(n / 2))
+      // length is taken as such.  A coded plane of either length finds no
+      // slot, and its tensor is decoded again with a slot for every plane
+      // (kIlvRetrySlots); its blocks may take the kernel's global-memory path.
       uint32_t need_slots = 0;
       uint64_t words = fam == kFamilyHuff ? 4 : 0;
       for (uint32_t p = 0; p < T.n_planes; ++p) {
-        if (!T.planes[p].coded) continue;
-        need_slots = std::max(need_slots, T.n_planes - p);
+        const IlvPlane& P = T.planes[p];
+        if (!P.coded) continue;
+        if (!all_slots && (P.len == T.n + 1 || P.len == kPackedHeadBytes + (T.n + 1) / 2)) continue;
+        ++need_slots;
         const uint64_t per_block = (T.planes[p].len + 4 * nb - 1) / (4 * nb);
         // huff_ilv nibble chains may carry fixed-length codes: room for the
         // kernel's per-lane skew of equal-length lane streams (two words per lane)
@@ -367,8 +372,15 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     ctx.last_ms[0] += ms;
     ctx.last_ms[2] += ms;
   }
-  for (size_t i = 0; i < nt; ++i)
-    if (hs[i]) return kInvalidInput;
+  std::vector<IlvTensor> again;
+  for (size_t i = 0; i < nt; ++i) {
+    if (hs[i] & ~kIlvRetrySlots) return kInvalidInput;
+    if (hs[i]) again.push_back(tensors[i]);
+  }
+  if (!again.empty()) {
+    if (all_slots) return kInternal;
+    return ilv_decode_tensors(ctx, again, true);
+  }
   return kOk;
 }
 

@@ -45,6 +45,7 @@ struct alignas(16) RilvCtl {
   uint64_t raw[4];      // stored plane bytes (tag 0 or raw planes)
   uint32_t coded[4];
   uint32_t packed[4];   // plane stored as packed nibbles (tag 2)
+  uint32_t slot[4];     // LDS table slot of a coded plane
   uint32_t bad;
   uint32_t pad[3];
   uint16_t cum[264];    // table build scratch: cumulative frequencies
@@ -91,6 +92,7 @@ struct RilvBlock {
   uint32_t nw[4];
   uint64_t raw[4];
   uint32_t rbytes[4];  // bytes of a raw plane's data (0 for a coded plane)
+  uint32_t lut[4];     // LDS address of a coded plane's table
   uint32_t coded_mask;
   uint32_t packed_mask;
 };
@@ -146,7 +148,7 @@ __device__ __forceinline__ void rilv_decode_block(RilvBlock& st, uint32_t luts, 
 #pragma unroll
       for (uint32_t p = 0; p < NP; ++p) {
         if (!(st.coded_mask & (1u << p))) continue;
-        const uint32_t lut = luts + (NP - 1 - p) * kRilvTableBytes;
+        const uint32_t lut = st.lut[p];
         const uint32_t sym = rilv_step<kTail, kStaged>(st.x[p], lut, st.sw[p], st.gw[p], st.nw[p], st.wpos[p], active);
         v[p][t >> 2] |= sym << (8 * (t & 3));
       }
@@ -190,7 +192,7 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
                                                           uint32_t* __restrict__ status, uint32_t n_slots,
                                                           uint32_t stage_words) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
-  // LDS: [n_slots tables (plane p in slot NP-1-p)][RilvCtl][4 x stage_words]
+  // LDS: [n_slots tables (coded planes from the last one down)][RilvCtl][4 x stage_words]
   extern __shared__ __align__(16) uint8_t smem[];
   RilvCtl& ctl = *reinterpret_cast<RilvCtl*>(smem + n_slots * kRilvTableBytes);
   uint32_t* const stage = reinterpret_cast<uint32_t*>(smem + n_slots * kRilvTableBytes + sizeof(RilvCtl));
@@ -235,14 +237,25 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
             if (P.len != n + 1) ctl.bad |= kIlvErrHeader;
             ctl.raw[p] = P.base + 1;
           } else if (pay[0] == 2) {
-            if (!packed_header_ok(pay, P.len, n)) ctl.bad |= kIlvErrHeader;
+            if (!packed_header_ok(pay, P.len, n, pay[P.len - 1])) ctl.bad |= kIlvErrHeader;
             ctl.raw[p] = P.base + kPackedHeadBytes;
             ctl.packed[p] = 1;
           } else if (pay[0] == 1 && P.len >= 6 && ld_le32(pay + 1) == n) {
-            if (NP - 1 - p < n_slots) ctl.coded[p] = 1;
-            else ctl.bad |= kIlvErrHeader;
+            ctl.coded[p] = 1;
           } else {
             ctl.bad |= kIlvErrHeader;
+          }
+        }
+        // table slots of the coded planes, from the last plane down
+        uint32_t k = 0;
+        for (uint32_t p = NP; p-- > 0;) {
+          ctl.slot[p] = k;
+          if (!ctl.coded[p]) continue;
+          if (k < n_slots) {
+            ++k;
+          } else {  // no table for it in this launch: the tensor is decoded again
+            ctl.coded[p] = 0;
+            ctl.bad |= kIlvRetrySlots;
           }
         }
       }
@@ -282,7 +295,7 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
         }
         __syncthreads();
         if (!ctl.bad)
-          rilv_build_table<kChain>(reinterpret_cast<uint32_t*>(smem + (NP - 1 - p) * kRilvTableBytes), ctl,
+          rilv_build_table<kChain>(reinterpret_cast<uint32_t*>(smem + ctl.slot[p] * kRilvTableBytes), ctl,
                                    ChainInfo<kChain>::xf[p]);
         __syncthreads();
       }
@@ -302,6 +315,7 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
       st.raw[p] = ctl.raw[p];
+      st.lut[p] = luts + __builtin_amdgcn_readfirstlane(ctl.slot[p]) * kRilvTableBytes;
       if (__builtin_amdgcn_readfirstlane(ctl.packed[p])) st.packed_mask |= 1u << p;
       st.x[p] = kRilvL;
       st.sw[p] = 0;

@@ -7,7 +7,10 @@ plane codecs (huff_ilv and rans_ilv):
   block and group) and reject malformed ones where the specification's
   decoder does;
 - tensor level: an MXFP4 tensor (nibble split) whose planes are packed goes
-  through GPU encode -> fused decode -> merge bit-exact.
+  through GPU encode -> fused decode -> merge bit-exact;
+- a coded payload that happens to have the stored or packed length (the
+  host reserves LDS tables only for planes of other lengths) decodes through
+  the kernel's retry with a table for every plane.
 """
 import sys
 
@@ -120,3 +123,62 @@ def test_mxfp4_tensor_with_packed_planes(name, label, enc, dec, wire):
         got = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, st,
                                                         out[:used], restored, 0)
         assert got == n and host(restored) == data
+
+
+def _collision(enc, target, ns, gen):
+    """First n (deterministic per-n data) whose coded payload has length
+    target(n)."""
+    for n in ns:
+        x = gen(np.random.default_rng(n), n)
+        c = enc(x)
+        if len(c) == target(n):
+            return x, c
+    raise AssertionError("no length collision found")
+
+
+def _skewed_bytes(rng, n):
+    return np.minimum(rng.geometric(0.004, n), 255).astype(np.uint8).tobytes()
+
+
+def _skewed_nibbles(rng, n):
+    x = (rng.integers(0, 16, n) & rng.integers(0, 16, n)) | rng.integers(0, 2, n)
+    return (x & 15).astype(np.uint8).tobytes()
+
+
+COLLISIONS = [
+    ("huff_ilv-stored-length", ids.PLANE_CODEC_LABEL, O.ilv_encode_coded, ids.CODEC_HUFF_ILV,
+     lambda n: n + 1, range(1000, 40000), _skewed_bytes),
+    ("huff_ilv-packed-length", ids.PLANE_CODEC_LABEL, O.ilv_encode_coded, ids.CODEC_HUFF_ILV,
+     lambda n: 8 + (n + 1) // 2, range(2000, 60000), _skewed_nibbles),
+    ("rans_ilv-stored-length", ids.RANS_CODEC_LABEL, O.rans_ilv_encode_coded, ids.CODEC_RANS_ILV,
+     lambda n: n + 1, range(1000, 40000), _skewed_bytes),
+]
+
+
+@pytest.mark.parametrize("name,label,enc,wire,target,ns,gen", COLLISIONS, ids=[c[0] for c in COLLISIONS])
+def test_coded_payload_with_stored_or_packed_length(name, label, enc, wire, target, ns, gen):
+    """A coded (tag 1) payload whose length equals the stored (n + 1) or the
+    packed (8 + ceil(n / 2)) length: the host reserves no LDS table for a
+    plane of those lengths, the kernel reports it, and the tensor is decoded
+    again with a table for every plane.  Plane level, then a two-plane bf16
+    tensor whose other plane is coded too (slot numbering)."""
+    x, payload = _collision(enc, target, ns, gen)
+    n = len(x)
+    assert payload[0] == 1
+    note(f"{name} n={n}")
+    got_n, got = gpu_decode(label, payload, n)
+    assert got_n == n and got == x
+    # tensor level: plane 0 the colliding payload, plane 1 an ordinary coded one
+    other = np.minimum(np.random.default_rng(99).geometric(0.3, n), 255).astype(np.uint8).tobytes()
+    p1 = enc(other)
+    assert p1[0] == 1 and len(p1) not in (n + 1, 8 + (n + 1) // 2)
+    blob = bytearray(payload)
+    off1 = (len(blob) + 255) // 256 * 256
+    blob += b"\0" * (off1 - len(blob)) + p1
+    pl = [plan.PlanePlan(wire, 0, len(payload), n), plan.PlanePlan(wire, off1, len(p1), n)]
+    data = O.chain_inverse(O.CHAIN_IEEE16_SPLIT2, [x, other])
+    st = plan.encode_plan([plan.TensorPlan(plan.CHAIN_IEEE16_SPLIT2, 0, len(data), pl)])
+    restored = torch.zeros(len(data), dtype=torch.uint8, device="cuda:0")
+    got = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, st,
+                                                    dev(bytes(blob)), restored, 0)
+    assert got == len(data) and host(restored) == data
