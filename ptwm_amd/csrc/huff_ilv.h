@@ -24,6 +24,10 @@ constexpr uint32_t kIlvErrLane = 4;     // a lane's word count disagrees with it
 // slot for every plane.
 constexpr uint32_t kIlvRetrySlots = 16;
 
+// Payload bytes read per native plane at a tensor's start (tag, n, weights
+// header: at most 135), kept in the staging area.
+constexpr uint32_t kIlvHeadWords = 36;
+
 struct IlvPlane {
   uint64_t base;   // coded: payload address; raw: plane bytes (16-byte aligned)
   uint64_t len;    // coded: payload length

@@ -78,12 +78,9 @@ struct BuildScratch {
   uint32_t err, hdr_len, pair, max_bits;
 };
 
-constexpr uint32_t kIlvHeadWords = 36;  // payload bytes kept per plane: tag, n, weights (<= 135)
-
 struct alignas(16) DecodeCtl {
   uint16_t t64[4][64];  // pair-mode planes: 6-bit single tables (symbol')
-  uint32_t head[4][kIlvHeadWords];  // first 144 bytes of each native payload
-  uint32_t last[4];                 // its last byte
+  uint32_t last[4];     // last byte of each native payload
   BuildScratch bs;
   uint64_t table[4], data[4], datalen[4], raw[4];  // per plane
   uint32_t coded[4];
@@ -518,6 +515,9 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
   extern __shared__ __align__(16) uint8_t smem[];
   DecodeCtl& ctl = *reinterpret_cast<DecodeCtl*>(smem + n_slots * SLOT);
   uint32_t* const stage = reinterpret_cast<uint32_t*>(smem + n_slots * SLOT + sizeof(DecodeCtl));
+  // while a tensor's tables are built, the staging area holds the payload
+  // heads (the host sizes it for NP x kIlvHeadWords words at least)
+  uint32_t (*const head)[kIlvHeadWords] = reinterpret_cast<uint32_t (*)[kIlvHeadWords]>(stage);
   const uint32_t luts = lds_addr(smem);
   BuildScratch& bs = ctl.bs;
   uint64_t* const s_table = ctl.table;
@@ -575,7 +575,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
           }
         }
         if (w == kIlvHeadWords) ctl.last[p] = v;
-        else ctl.head[p][w] = v;
+        else head[p][w] = v;
       }
       __syncthreads();
       if (t == 0) {
@@ -587,7 +587,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
           ctl.packed[p] = 0;
           if (!P.coded) continue;
           // huff_ilv payload: tag 0 stores the plane after the tag byte, tag 2 packs it
-          const uint8_t* pay = reinterpret_cast<const uint8_t*>(ctl.head[p]);
+          const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
           if (P.len == 0) s_bad |= kIlvErrHeader;
           else if (pay[0] == 0) {
             if (P.len != n + 1) s_bad |= kIlvErrHeader;
@@ -622,7 +622,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
         if (!s_coded[p]) continue;
         const IlvPlane P = T.planes[p];
         uint16_t* tab16 = reinterpret_cast<uint16_t*>(smem + ctl.slot[p] * SLOT);
-        const uint8_t* pay = reinterpret_cast<const uint8_t*>(ctl.head[p]);
+        const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
         const uint64_t avail = P.len < 4 * kIlvHeadWords ? P.len : 4 * kIlvHeadWords;
         build_tables(tab16, ctl.t64[p], SLOT == kIlvPairLutBytes, ChainInfo<kChain>::xf[p], bs, pay + 5,
                      avail >= 5 ? avail - 5 : 0);

@@ -313,9 +313,11 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     const uint64_t max_lds = fam == kFamilyHuff ? kIlvMaxLds : kRilvMaxLds;
     const uint64_t fixed = fam == kFamilyHuff ? ilv_decode_lds_bytes(chain, slots, 0) : rilv_decode_lds_bytes(chain, slots, 0);
     uint64_t cap_words = ((max_lds - std::min<uint64_t>(fixed, max_lds)) / 16) & ~3ull;
-    uint64_t stage = align_up(std::max<uint64_t>(est, 8), 4);
+    // the staging area also holds the payload heads at a tensor's start
+    const uint64_t head_min = fam == kFamilyHuff ? kIlvHeadWords : kRilvHeadWords;  // 4 planes over 4 wavefronts
+    uint64_t stage = align_up(std::max<uint64_t>(std::max<uint64_t>(est, 8), head_min), 4);
     if (stage > cap_words) stage = cap_words;
-    if (stage < 8) return kInternal;
+    if (stage < head_min) return kInternal;
     int per_cu = 0;
     const uint64_t occ_key = (uint64_t)chain | ((uint64_t)slots << 8) | (stage << 16) | ((uint64_t)fam << 62);
     auto it = ctx.ilv_occupancy.find(occ_key);

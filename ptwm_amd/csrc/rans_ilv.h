@@ -12,6 +12,9 @@ constexpr uint32_t kRilvProbBits = 11;
 constexpr uint32_t kRilvL = 1u << 16;         // state lower bound; words are 16 bits
 constexpr uint32_t kRilvBlockHead = 260;      // [nw u32][64 x u32 states]
 constexpr uint32_t kRilvMaxLds = 81920;
+// Payload bytes read per native plane at a tensor's start (tag, n, max_sym,
+// 256 frequencies, padding), kept in the staging area.
+constexpr uint32_t kRilvHeadWords = 132;
 
 // status bits (per tensor), in addition to kIlvErrHeader / kIlvErrBlock
 constexpr uint32_t kRilvErrState = 8;  // words left over / missing or a final state != 2^16

@@ -38,6 +38,7 @@ namespace ptwm {
 
 namespace {
 
+
 struct alignas(16) RilvCtl {
   uint64_t table[4];    // per plane: block offset table address
   uint64_t data[4];     // block data base
@@ -47,6 +48,8 @@ struct alignas(16) RilvCtl {
   uint32_t packed[4];   // plane stored as packed nibbles (tag 2)
   uint32_t slot[4];     // LDS table slot of a coded plane
   uint32_t bad;
+  uint32_t wsum[4];     // table build scratch: per-wavefront frequency sums
+  uint32_t last[4];     // last byte of each native payload
   uint32_t pad[3];
   uint16_t cum[264];    // table build scratch: cumulative frequencies
   uint16_t f[256];
@@ -196,6 +199,9 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
   extern __shared__ __align__(16) uint8_t smem[];
   RilvCtl& ctl = *reinterpret_cast<RilvCtl*>(smem + n_slots * kRilvTableBytes);
   uint32_t* const stage = reinterpret_cast<uint32_t*>(smem + n_slots * kRilvTableBytes + sizeof(RilvCtl));
+  // while a tensor's tables are built, the staging area holds the payload
+  // heads (the host sizes it for NP x kRilvHeadWords words at least)
+  uint32_t (*const head)[kRilvHeadWords] = reinterpret_cast<uint32_t (*)[kRilvHeadWords]>(stage);
   const uint32_t luts = lds_addr(smem);
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
   const uint32_t n_tiles = tpre[m];
@@ -223,6 +229,25 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
       bad = 0;
       cur = ti;
       __syncthreads();
+      // the payload heads and last bytes, loaded by all threads at once
+      // (native payloads start 4-byte aligned)
+      for (uint32_t k = t; k < NP * (kRilvHeadWords + 1); k += 256) {
+        const uint32_t p = k / (kRilvHeadWords + 1), w = k % (kRilvHeadWords + 1);
+        const uint64_t base = T.planes[p].base, len = T.planes[p].len;
+        uint32_t v = 0;
+        if (T.planes[p].coded) {
+          if (w == kRilvHeadWords) {
+            if (len) v = gload_u8(base + len - 1);
+          } else if (4ull * w + 4 <= len) {
+            v = g_ld<uint32_t>(base + 4ull * w);
+          } else {
+            for (uint64_t b = 4ull * w; b < len && b < 4ull * w + 4; ++b) v |= gload_u8(base + b) << (8 * (b & 3));
+          }
+        }
+        if (w == kRilvHeadWords) ctl.last[p] = v;
+        else head[p][w] = v;
+      }
+      __syncthreads();
       if (t == 0) {
         ctl.bad = 0;
         for (uint32_t p = 0; p < NP; ++p) {
@@ -231,13 +256,13 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
           ctl.coded[p] = 0;
           ctl.packed[p] = 0;
           if (!P.coded) continue;
-          const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
+          const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
           if (P.len == 0) ctl.bad |= kIlvErrHeader;
           else if (pay[0] == 0) {
             if (P.len != n + 1) ctl.bad |= kIlvErrHeader;
             ctl.raw[p] = P.base + 1;
           } else if (pay[0] == 2) {
-            if (!packed_header_ok(pay, P.len, n, pay[P.len - 1])) ctl.bad |= kIlvErrHeader;
+            if (!packed_header_ok(pay, P.len, n, ctl.last[p])) ctl.bad |= kIlvErrHeader;
             ctl.raw[p] = P.base + kPackedHeadBytes;
             ctl.packed[p] = 1;
           } else if (pay[0] == 1 && P.len >= 6 && ld_le32(pay + 1) == n) {
@@ -264,20 +289,23 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
       for (uint32_t p = 0; p < NP; ++p) {
         if (!ctl.coded[p]) continue;
         const IlvPlane P = T.planes[p];
-        const uint8_t* pay = reinterpret_cast<const uint8_t*>(P.base);
+        const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
+        // frequencies: f[s] for s <= max_sym, cumulative by a workgroup scan
+        const uint32_t ms = pay[5];
+        const uint64_t hl = 6 + 2ull * (ms + 1);
+        const bool hok = hl <= P.len;  // the head holds 6 + 512 bytes at most
+        const uint32_t fs = hok && t <= ms ? (uint32_t)pay[6 + 2 * t] | ((uint32_t)pay[7 + 2 * t] << 8) : 0u;
+        const uint32_t incl = wave_incl_scan(fs);
+        if (lane == 63) ctl.wsum[wave] = incl;
+        __syncthreads();
+        uint32_t run = incl - fs;
+        for (uint32_t wv = 0; wv < wave; ++wv) run += ctl.wsum[wv];
+        ctl.cum[t] = (uint16_t)(run < 2048u ? run : 2048u);
+        ctl.f[t] = (uint16_t)fs;
         if (t == 0) {
-          const uint32_t ms = pay[5];
-          const uint64_t hl = 6 + 2ull * (ms + 1);
-          uint32_t run = 0;
-          bool ok = hl <= P.len;
-          for (uint32_t s = 0; s < 256; ++s) {
-            const uint32_t fs = ok && s <= ms ? (uint32_t)pay[6 + 2 * s] | ((uint32_t)pay[7 + 2 * s] << 8) : 0u;
-            ctl.cum[s] = (uint16_t)(run < 2048u ? run : 2048u);
-            ctl.f[s] = (uint16_t)fs;
-            run += fs;
-          }
           ctl.cum[256] = 2048;
-          ok = ok && run == 2048u;
+          const uint32_t total = ctl.wsum[0] + ctl.wsum[1] + ctl.wsum[2] + ctl.wsum[3];
+          bool ok = hok && total == 2048u;
           const uint64_t head = (hl + 3) & ~3ull;
           const uint64_t data0 = head + 4ull * (nb + 1);
           ok = ok && data0 <= P.len;
@@ -286,11 +314,11 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
           if (!ok) {
             ctl.bad |= kIlvErrHeader;
           } else {
+            // tab[0] == 0 and tab[nb] == datalen are checked by the
+            // wavefronts of the first and last block
             ctl.table[p] = P.base + head;
             ctl.data[p] = P.base + data0;
             ctl.datalen[p] = P.len - data0;
-            const uint32_t* tb = reinterpret_cast<const uint32_t*>(P.base + head);
-            if (tb[0] != 0 || tb[nb] != ctl.datalen[p]) ctl.bad |= kIlvErrBlock;
           }
         }
         __syncthreads();
@@ -327,7 +355,8 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
       st.coded_mask |= 1u << p;
       const uint64_t tb = ctl.table[p];
       const uint32_t o0 = g_ld<uint32_t>(tb + 4ull * bi), o1 = g_ld<uint32_t>(tb + 4ull * bi + 4);
-      const bool bok = o1 >= o0 && o1 - o0 >= kRilvBlockHead && o1 <= ctl.datalen[p] && (o0 & 3u) == 0;
+      const bool bok = o1 >= o0 && o1 - o0 >= kRilvBlockHead && o1 <= ctl.datalen[p] && (o0 & 3u) == 0 &&
+                       (bi != 0 || o0 == 0) && (bi + 1 != nb || o1 == ctl.datalen[p]);
       const uint64_t blk = ctl.data[p] + (bok ? o0 : 0);
       const uint32_t nwb = bok ? g_ld<uint32_t>(blk) : 0u;
       if (!bok || nwb > 16384u || ((kRilvBlockHead + 2u * nwb + 3u) & ~3u) != o1 - o0) ok = false;
