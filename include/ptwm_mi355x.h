@@ -168,6 +168,24 @@ int64_t ptwm_mi355x_xxh64_cuda(uint64_t in_dev_ptr, size_t in_len, uint64_t *has
  * histogram. */
 int64_t ptwm_mi355x_huffman_code_lengths(const uint32_t *freqs, uint8_t *lengths_out);
 
+/* Stream-ordered hand-off from a producer: work already queued on
+ * `producer_stream` (a hipStream_t of the device; 0 = the null stream)
+ * completes before the library stream runs anything queued after this call.
+ * What the reference's PyO3 layer obtains with __dlpack__(stream=<library
+ * stream>) (crates/ptwm-py/src/plane_codec_cuda.rs:104-109), as one event
+ * record and wait.  No counterpart in the reference C ABI.  Returns 0. */
+int64_t ptwm_mi355x_stream_wait(uint64_t producer_stream, uint32_t device_ordinal);
+
+/* use != 0: run this thread's subsequent calls for `device_ordinal` on
+ * `stream` (a hipStream_t of that device, 0 = the null stream), e.g. the
+ * caller's current stream, so that work queued there before a call is
+ * ordered before it without an event; use == 0: the library's own stream
+ * again (the default; the stream-handle entry points always return that
+ * one).  Calls still complete before they return.  No counterpart in the
+ * reference C ABI: the ordering the reference's PyO3 layer gets from
+ * __dlpack__(stream=...) (plane_codec_cuda.rs:104-109).  Returns 0. */
+int64_t ptwm_mi355x_use_stream(uint64_t stream, uint32_t use, uint32_t device_ordinal);
+
 /* Kernel timing with HIP events recorded on the library stream around each
  * phase of the next calls on the device (off by default). */
 int64_t ptwm_mi355x_set_profiling(uint32_t device_ordinal, uint32_t on);

@@ -19,36 +19,48 @@ of every tensor must equal ``device_ordinal`` (plane_codec_cuda.rs:120-124).
 from __future__ import annotations
 
 import ctypes as C
+import threading
 
 from . import ids
 from ._native import NativeError, check, lib
 
 
-_order_cache: dict = {}   # (device, library stream) -> (ExternalStream, reusable Event)
+def _current_raw_stream(device_ordinal: int) -> int:
+    import torch
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return int(raw(device_ordinal))
+    return int(torch.cuda.current_stream(device_ordinal).cuda_stream)
+
+
+_tls = threading.local()   # per thread: device -> stream the library was asked to run on
+
+
+def _use_stream(device_ordinal: int, s) -> None:
+    """Ask the library to run this thread's calls on stream s (None: its own)."""
+    used = getattr(_tls, "used", None)
+    if used is None:
+        used = _tls.used = {}
+    if used.get(device_ordinal, "own") == s:
+        return
+    check(lib().ptwm_mi355x_use_stream(0 if s is None else s, 0 if s is None else 1, device_ordinal),
+          "stream selection")
+    used[device_ordinal] = s
 
 
 def _order_after_producer(t, device_ordinal: int, stream: int) -> None:
     """Stream-ordered hand-off, as the reference's ``__dlpack__(stream=...)``:
     work already queued on the producer's current stream completes before
-    the library stream touches the memory.  For torch tensors this is one
-    event recorded on torch's current stream and waited on by the library
-    stream (what ``__dlpack__`` does, without building a capsule); any other
-    DLPack object goes through ``__dlpack__`` itself."""
+    the library touches the memory.  For torch tensors the library runs this
+    thread's calls on torch's current stream (``ptwm_mi355x_use_stream``), so
+    no event is needed; any other DLPack object goes through ``__dlpack__``
+    with the library's own stream."""
     import torch
     if not isinstance(t, torch.Tensor):
+        _use_stream(device_ordinal, None)
         t.__dlpack__(stream=stream)
         return
-    cur = torch.cuda.current_stream(device_ordinal)
-    if cur.cuda_stream == stream:
-        return
-    key = (device_ordinal, stream)
-    ent = _order_cache.get(key)
-    if ent is None:
-        ent = (torch.cuda.ExternalStream(stream, device=device_ordinal), torch.cuda.Event())
-        _order_cache[key] = ent
-    ext, ev = ent
-    ev.record(cur)
-    ext.wait_event(ev)
+    _use_stream(device_ordinal, _current_raw_stream(device_ordinal))
 
 
 def _both_torch(a, b) -> bool:

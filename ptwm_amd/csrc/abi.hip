@@ -73,6 +73,15 @@ bool lookup_codec(const uint8_t* id, size_t len, uint32_t& codec) {
 }
 
 // RAII: lock the device context, make its device current, restore after.
+// Stream the calling thread asked the library to run on, per device
+// (ptwm_mi355x_use_stream); calls without one use the library's own stream.
+struct ThreadStream {
+  uint32_t dev = 0;
+  uint64_t stream = 0;
+  bool set = false;
+};
+thread_local ThreadStream t_stream;
+
 struct DeviceScope {
   DevCtx* ctx;
   std::unique_lock<std::mutex> lk;
@@ -81,6 +90,7 @@ struct DeviceScope {
   explicit DeviceScope(uint32_t ord) : ctx(get_ctx(ord)) {
     if (!ctx) return;
     lk = std::unique_lock<std::mutex>(ctx->mu);
+    ctx->stream = t_stream.set && t_stream.dev == ord ? reinterpret_cast<hipStream_t>(t_stream.stream) : ctx->own_stream;
     (void)hipGetDevice(&prev);
     ok = hipSetDevice(ctx->dev) == hipSuccess;
   }
@@ -195,7 +205,7 @@ int64_t ptwm_mi355x_canonical_id(uint32_t which, uint8_t* out32) {
 
 uint64_t ptwm_plane_codec_v1_cuda_stream_handle(uint32_t device_ordinal) {
   DevCtx* c = get_ctx(device_ordinal);
-  return c ? reinterpret_cast<uint64_t>(c->stream) : 0;
+  return c ? reinterpret_cast<uint64_t>(c->own_stream) : 0;
 }
 
 uint64_t ptwm_hardware_backend_v1_cuda_stream_handle(uint32_t device_ordinal) {
@@ -620,6 +630,26 @@ int64_t ptwm_mi355x_xxh64_cuda(uint64_t in_dev_ptr, size_t in_len, uint64_t* has
   const int64_t rc = xxh64_buffers(ctx, {HashTask{src, in_len}}, h);
   if (rc != kOk) return rc;
   *hash_out = h[0];
+  return 0;
+}
+
+int64_t ptwm_mi355x_use_stream(uint64_t stream, uint32_t use, uint32_t device_ordinal) {
+  if (!get_ctx(device_ordinal)) return kInvalidInput;
+  t_stream.dev = device_ordinal;
+  t_stream.stream = stream;
+  t_stream.set = use != 0;
+  return 0;
+}
+
+int64_t ptwm_mi355x_stream_wait(uint64_t producer_stream, uint32_t device_ordinal) {
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  DevCtx& ctx = *ds.ctx;
+  hipStream_t prod = reinterpret_cast<hipStream_t>(producer_stream);
+  if (prod == ctx.stream) return 0;
+  if (!ctx.order_ev) PTWM_HIP_TRY(hipEventCreateWithFlags(&ctx.order_ev, hipEventDisableTiming));
+  PTWM_HIP_TRY(hipEventRecord(ctx.order_ev, prod));
+  PTWM_HIP_TRY(hipStreamWaitEvent(ctx.stream, ctx.order_ev, 0));
   return 0;
 }
 

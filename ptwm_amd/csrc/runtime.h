@@ -30,7 +30,8 @@ struct PinnedBuffer {
 // and the scratch buffers are shared by every call on that device.
 struct DevCtx {
   int dev = -1;
-  hipStream_t stream = nullptr;
+  hipStream_t stream = nullptr;      // the stream of the current call (own_stream or the caller's)
+  hipStream_t own_stream = nullptr;  // the library's stream of this device
   std::mutex mu;
   DeviceBuffer jobs;     // DecodeJob array
   DeviceBuffer status;   // per-job status words
@@ -57,6 +58,7 @@ struct DevCtx {
   // optional per-phase kernel timing with HIP events on `stream`
   bool profile = false;
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t order_ev = nullptr;  // producer-stream ordering (ptwm_mi355x_stream_wait)
   float last_ms[3] = {0, 0, 0};  // entropy decode, merge, whole call
   hipError_t ensure_events();
 };

@@ -74,10 +74,11 @@ DevCtx* get_ctx(uint32_t ord) {
   auto ctx = std::make_unique<DevCtx>();
   ctx->dev = (int)ord;
   // default priority: mixing stream priorities is avoided on purpose
-  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+  if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
     (void)hipSetDevice(prev);
     return nullptr;
   }
+  ctx->stream = ctx->own_stream;
   (void)hipSetDevice(prev);
   g_ctx[ord] = std::move(ctx);
   return g_ctx[ord].get();
