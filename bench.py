@@ -251,18 +251,23 @@ def build_replica(desc, specs, CH, ref, native, opts, rep) -> Workload:
     out_off = 0
     plans = []
     t0 = time.perf_counter()
-    for raw, chain, rf in tensors:
-        if rf is None:
-            used, st = api.encode_tensor_cuda(chain, raw, blob[off:], 0, codec=native)
-        else:
+    if ref is None:
+        # GPU-native codecs: every tensor in one batched encoder call
+        used, st = api.encode_tensors_cuda([(chain, raw) for raw, chain, _ in tensors], blob, 0, codec=native)
+        plans = plan.decode_plan(st)
+        off = (used + 255) // 256 * 256
+        out_off = plans[-1].out_offset + plans[-1].out_len if plans else 0
+        out_off = (out_off + 255) // 256 * 256
+    else:
+        for raw, chain, rf in tensors:
             used, st = api.encode_tensor_ref_cuda(chain, rf[0], rf[1], raw, blob[off:], 0)
-        t = plan.decode_plan(st)[0]
-        t.out_offset = out_off
-        for p in t.planes:
-            p.payload_offset += off
-        plans.append(t)
-        off = (off + used + 255) // 256 * 256
-        out_off = (out_off + raw.numel() + 255) // 256 * 256
+            t = plan.decode_plan(st)[0]
+            t.out_offset = out_off
+            for p in t.planes:
+                p.payload_offset += off
+            plans.append(t)
+            off = (off + used + 255) // 256 * 256
+            out_off = (out_off + raw.numel() + 255) // 256 * 256
     torch.cuda.synchronize()
     enc_s = time.perf_counter() - t0
     for (raw, chain, _), t in zip(tensors, plans):

@@ -134,6 +134,22 @@ int64_t ptwm_mi355x_encode_tensor_rans_cuda(uint32_t chain, uint64_t in_dev_ptr,
                                             size_t out_cap, uint8_t *plan_out, size_t plan_cap, size_t *plan_len_out,
                                             uint64_t *needed_out, uint32_t device_ordinal);
 
+/* Tensor-level GPU encode of n_tensors tensors in one call (library
+ * addition, no reference counterpart): tensor i is in_lens[i] bytes at
+ * in_dev_ptrs[i] (16-byte aligned) with chain chains[i]; family 0 codes the
+ * planes with huff_ilv, 1 with rans_ilv (each plane the smallest of coded,
+ * packed, Identity).  Tensors are processed in batches of about 1 GiB of
+ * input, each batch's planes through one histogram, size and encode pass.
+ * Payloads go to out_dev_ptr (256-byte aligned) at 256-byte aligned
+ * offsets; *plan_out receives one PTMD plan for all tensors, restored back
+ * to back at 256-byte aligned offsets in the given order.  Returns the
+ * bytes used in out; -2 with *needed_out an upper bound when out_cap is too
+ * small. */
+int64_t ptwm_mi355x_encode_tensors_cuda(uint32_t family, uint32_t n_tensors, const uint32_t *chains,
+                                        const uint64_t *in_dev_ptrs, const uint64_t *in_lens, uint64_t out_dev_ptr,
+                                        size_t out_cap, uint8_t *plan_out, size_t plan_cap, size_t *plan_len_out,
+                                        uint64_t *needed_out, uint32_t device_ordinal);
+
 /* Tensor-level encode into the reference's own plane formats: the tensor is
  * split by `chain`, and plane p is coded with plane_codecs[p] (wire id 0x0000
  * Identity, 0x0001 Huffman, 0x0003 rANS), in chunks of chunk_size bytes with

@@ -49,6 +49,9 @@ _SIGS = {
     "ptwm_mi355x_encode_tensor_cuda": (
         C.c_int64, [C.c_uint32, C.c_uint64, C.c_size_t, C.c_uint64, C.c_size_t, _u8p, C.c_size_t,
                     C.POINTER(C.c_size_t), C.POINTER(C.c_uint64), C.c_uint32]),
+    "ptwm_mi355x_encode_tensors_cuda": (
+        C.c_int64, [C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_size_t, C.c_void_p,
+                    C.c_size_t, C.POINTER(C.c_size_t), C.POINTER(C.c_uint64), C.c_uint32]),
     "ptwm_mi355x_encode_tensor_rans_cuda": (
         C.c_int64, [C.c_uint32, C.c_uint64, C.c_size_t, C.c_uint64, C.c_size_t, _u8p, C.c_size_t,
                     C.POINTER(C.c_size_t), C.POINTER(C.c_uint64), C.c_uint32]),

@@ -168,6 +168,39 @@ def encode_tensor_cuda(chain: int, src, out, device_ordinal: int = 0, codec: str
     return rc, bytes(plan_buf[: plan_len.value])
 
 
+def encode_tensors_cuda(items, out, device_ordinal: int = 0, codec: str = "huff_ilv") -> tuple[int, bytes]:
+    """Tensor-level GPU encode of many tensors in one call (library
+    addition): ``items`` is a sequence of (chain, device tensor); every plane
+    coded with ``codec`` ("huff_ilv" or "rans_ilv"), batches of about 1 GiB
+    of input through one encoder pass each.  Returns (bytes used in ``out``,
+    one PTMD plan whose tensors are restored back to back at 256-byte
+    aligned offsets in the given order)."""
+    L = lib()
+    fam = {"huff_ilv": 0, "rans_ilv": 1}[codec]
+    stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
+    items = list(items)
+    n = len(items)
+    chains = (C.c_uint32 * max(n, 1))()
+    ptrs = (C.c_uint64 * max(n, 1))()
+    lens = (C.c_uint64 * max(n, 1))()
+    for i, (chain, src) in enumerate(items):
+        ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False, i > 0)
+        chains[i], ptrs[i], lens[i] = chain, ip, il
+    op, ol = _dev_ptr_len(out, "out", device_ordinal, stream, True, True)
+    cap = 12 + sum(20 + 32 * 4 for _ in range(n))
+    plan_buf = (C.c_uint8 * cap)()
+    plan_len = C.c_size_t(0)
+    needed = C.c_uint64(0)
+    rc = L.ptwm_mi355x_encode_tensors_cuda(fam, n, chains, ptrs, lens, op, ol, plan_buf, cap, C.byref(plan_len),
+                                           C.byref(needed), device_ordinal)
+    if rc == -2:
+        err = NativeError(rc, f"encode_tensors_cuda: needs {needed.value} bytes")
+        err.needed = needed.value
+        raise err
+    check(rc, "encode_tensors_cuda")
+    return rc, bytes(plan_buf[: plan_len.value])
+
+
 def encode_tensor_ref_cuda(chain: int, plane_codecs, chunk_size: int, src, out,
                            device_ordinal: int = 0) -> tuple[int, bytes]:
     """Tensor-level GPU encode into the reference's plane formats (library

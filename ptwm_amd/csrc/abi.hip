@@ -468,6 +468,123 @@ int64_t ptwm_mi355x_encode_tensor_rans_cuda(uint32_t chain, uint64_t in_dev_ptr,
                               plan_len_out, needed_out, device_ordinal);
 }
 
+int64_t ptwm_mi355x_encode_tensors_cuda(uint32_t family, uint32_t n_tensors, const uint32_t* chains,
+                                        const uint64_t* in_dev_ptrs, const uint64_t* in_lens, uint64_t out_dev_ptr,
+                                        size_t out_cap, uint8_t* plan_out, size_t plan_cap, size_t* plan_len_out,
+                                        uint64_t* needed_out, uint32_t device_ordinal) {
+  if (family > kFamilyRans || !plan_out || !plan_len_out || (n_tensors && (!chains || !in_dev_ptrs || !in_lens)))
+    return kInvalidInput;
+  if (out_dev_ptr & 255u) return kInvalidInput;
+  size_t plan_len = 12;
+  for (uint32_t i = 0; i < n_tensors; ++i) {
+    const int np = chain_planes(chains[i]);
+    if (np < 0) return kInvalidInput;
+    const uint64_t ratio = (uint64_t)chain_ratio(chains[i]);
+    if (in_lens[i] % ratio || (in_dev_ptrs[i] & 15u)) return kInvalidInput;
+    plan_len += 20 + (size_t)np * 32;
+  }
+  if (plan_cap < plan_len) return kBufferTooSmall;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  DevCtx& ctx = *ds.ctx;
+  // Batches of tensors (at most kBatchBytes of input each, or one larger
+  // tensor): forward chains of the batch into plane scratch, then every
+  // plane of the batch through one encoder pass (one histogram, size and
+  // encode launch each), payloads appended at 256-byte aligned offsets.
+  constexpr uint64_t kBatchBytes = 1ull << 30;
+  std::vector<IlvEncResult> res;     // per plane, offsets relative to out_dev_ptr
+  uint64_t out_used = 0, needed_total = 0;
+  bool too_small = false;
+  for (uint32_t b0 = 0; b0 < n_tensors;) {
+    uint32_t b1 = b0;
+    uint64_t scratch = 0;
+    while (b1 < n_tensors && (b1 == b0 || scratch + in_lens[b1] + 1024 <= kBatchBytes)) {
+      const uint64_t pl = in_lens[b1] / (uint64_t)chain_ratio(chains[b1]);
+      scratch += (uint64_t)chain_planes(chains[b1]) * ((pl + 255) / 256 * 256);
+      ++b1;
+    }
+    PTWM_HIP_TRY(ctx.enc_split.ensure(scratch + 256));
+    std::vector<uint64_t> srcs, lens;
+    uint64_t so = 0;
+    for (uint32_t i = b0; i < b1; ++i) {
+      const int np = chain_planes(chains[i]);
+      const uint64_t pl = in_lens[i] / (uint64_t)chain_ratio(chains[i]);
+      uint8_t* p[4] = {};
+      for (int k = 0; k < np; ++k) {
+        p[k] = static_cast<uint8_t*>(ctx.enc_split.ptr) + so;
+        srcs.push_back(reinterpret_cast<uint64_t>(p[k]));
+        lens.push_back(pl);
+        so += (pl + 255) / 256 * 256;
+      }
+      if (pl && launch_split(chains[i], reinterpret_cast<const uint8_t*>(in_dev_ptrs[i]), pl, p, ctx.stream) !=
+                    hipSuccess)
+        return kInvalidInput;
+    }
+    std::vector<IlvEncResult> r(srcs.size());
+    uint64_t needed = 0;
+    const uint64_t base = (out_used + 255) / 256 * 256;
+    const uint64_t cap = out_cap > base ? out_cap - base : 0;
+    int64_t rc = too_small ? kBufferTooSmall
+                 : family == kFamilyHuff
+                     ? ilv_encode_planes(ctx, srcs.data(), lens.data(), (uint32_t)srcs.size(), out_dev_ptr + base, cap,
+                                         true, r.data(), &needed)
+                     : rilv_encode_planes(ctx, srcs.data(), lens.data(), (uint32_t)srcs.size(), out_dev_ptr + base,
+                                          cap, true, r.data(), &needed);
+    if (rc == kBufferTooSmall) {
+      // keep sizing the remaining batches for *needed_out
+      if (!too_small) {
+        too_small = true;
+        needed_total = base;
+      }
+      if (needed == 0) {
+        // sizes of this batch are unknown once the buffer ran out: the
+        // stored size bounds every payload
+        for (uint64_t l : lens) needed = (needed + 255) / 256 * 256 + l + 1;
+      }
+      needed_total = (needed_total + 255) / 256 * 256 + needed;
+    } else if (rc < 0) {
+      return rc;
+    } else {
+      out_used = base + (uint64_t)rc;
+      for (IlvEncResult& x : r) x.offset += base;
+      res.insert(res.end(), r.begin(), r.end());
+    }
+    b0 = b1;
+  }
+  if (too_small) {
+    if (needed_out) *needed_out = needed_total;
+    return kBufferTooSmall;
+  }
+  // decode plan (PTMD v1): tensors restored back to back at 256-byte
+  // aligned offsets, in the order given
+  uint8_t* o = plan_out;
+  auto put = [&](const void* v, size_t k) {
+    std::memcpy(o, v, k);
+    o += k;
+  };
+  const uint32_t magic = 0x444D5450u, ntens = n_tensors;
+  const uint16_t ver = 1, flags = 0, tflags = 0;
+  put(&magic, 4); put(&ver, 2); put(&flags, 2); put(&ntens, 4);
+  uint64_t out_off = 0;
+  size_t ri = 0;
+  for (uint32_t i = 0; i < n_tensors; ++i) {
+    const int np = chain_planes(chains[i]);
+    const uint64_t pl = in_lens[i] / (uint64_t)chain_ratio(chains[i]);
+    const uint64_t out_len = in_lens[i];
+    const uint8_t ch = (uint8_t)chains[i], npl = (uint8_t)np;
+    put(&out_off, 8); put(&out_len, 8); put(&ch, 1); put(&npl, 1); put(&tflags, 2);
+    for (int k = 0; k < np; ++k, ++ri) {
+      const uint16_t codec = (uint16_t)res[ri].codec, pf = 0;
+      const uint32_t nch = 0;
+      put(&codec, 2); put(&pf, 2); put(&nch, 4);
+      put(&res[ri].offset, 8); put(&res[ri].len, 8); put(&pl, 8);
+    }
+    out_off = (out_off + out_len + 255) / 256 * 256;
+  }
+  *plan_len_out = (size_t)(o - plan_out);
+  return (int64_t)out_used;
+}
+
 int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane_codecs, uint32_t n_codecs,
                                            uint32_t chunk_size, uint64_t in_dev_ptr, size_t in_len,
                                            uint64_t out_dev_ptr, size_t out_cap, uint8_t* plan_out, size_t plan_cap,
