@@ -794,28 +794,36 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
 // encode kernels
 // ---------------------------------------------------------------------------
 
+// Histogram of plane blockIdx.y.  16 LDS copies per workgroup, lane l
+// counting into copy l % 16, laid out [symbol][17] so that lanes adding the
+// same symbol hit different banks: a skewed plane (an exponent plane has a
+// handful of common values) then costs at most four-way conflicts per
+// atomic instead of 64.
+constexpr uint32_t kHistCopies = 16, kHistStride = 17;
+
 __global__ void __launch_bounds__(256) ilv_hist_kernel(const IlvEncPlane* __restrict__ planes,
                                                        uint32_t* __restrict__ hist) {
-  __shared__ uint32_t h[4][256];
+  __shared__ uint32_t h[256 * kHistStride];
   const IlvEncPlane P = planes[blockIdx.y];
-  const uint32_t t = threadIdx.x, wave = t >> 6;
-  for (uint32_t i = t; i < 1024; i += 256) (&h[0][0])[i] = 0;
+  const uint32_t t = threadIdx.x, copy = t % kHistCopies;
+  for (uint32_t i = t; i < 256 * kHistStride; i += 256) h[i] = 0;
   __syncthreads();
-  const uint8_t* src = reinterpret_cast<const uint8_t*>(P.src);
   const uint64_t nvec = P.n / 16;
   const uint64_t stride = (uint64_t)gridDim.x * 256u;
   for (uint64_t v = (uint64_t)blockIdx.x * 256u + t; v < nvec; v += stride) {
-    u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + v);
+    const u32x4 x = gload_nt16(P.src + 16 * v);
     const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) atomicAdd(&h[wave][(xs[k] >> (8 * b)) & 0xFF], 1u);
+      for (int b = 0; b < 4; ++b) atomicAdd(&h[((xs[k] >> (8 * b)) & 0xFFu) * kHistStride + copy], 1u);
   }
   if (blockIdx.x == 0)
-    for (uint64_t i = nvec * 16 + t; i < P.n; i += 256) atomicAdd(&h[wave][src[i]], 1u);
+    for (uint64_t i = nvec * 16 + t; i < P.n; i += 256) atomicAdd(&h[gload_u8(P.src + i) * kHistStride + copy], 1u);
   __syncthreads();
-  uint32_t s = h[0][t] + h[1][t] + h[2][t] + h[3][t];
+  uint32_t s = 0;
+#pragma unroll
+  for (uint32_t c = 0; c < kHistCopies; ++c) s += h[t * kHistStride + c];
   if (s) atomicAdd(&hist[256u * blockIdx.y + t], s);
 }
 
@@ -876,9 +884,21 @@ __global__ void __launch_bounds__(64) ilv_encode_kernel(const IlvEncPlane* __res
   for (uint32_t r = 0; r < kIlvRounds; ++r) {
     const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
     if (pos >= P.n) continue;
-    const uint64_t end = P.n - pos >= kIlvGroup ? pos + kIlvGroup : P.n;
-    for (uint64_t k = pos; k < end; ++k) {
-      const uint32_t e = code[gload_u8(P.src + k)];
+    // the group's symbols: one 16-byte load (planes are 16-byte aligned), or
+    // byte loads for the plane's partial last group
+    uint32_t xs[4] = {0, 0, 0, 0};
+    const uint32_t count = P.n - pos >= kIlvGroup ? kIlvGroup : (uint32_t)(P.n - pos);
+    if (count == kIlvGroup) {
+      const u32x4 x = gload_nt16(P.src + pos);
+      xs[0] = x.x;
+      xs[1] = x.y;
+      xs[2] = x.z;
+      xs[3] = x.w;
+    } else {
+      for (uint32_t k = 0; k < count; ++k) xs[k >> 2] |= gload_u8(P.src + pos + k) << (8 * (k & 3));
+    }
+    for (uint32_t k = 0; k < count; ++k) {
+      const uint32_t e = code[(xs[k >> 2] >> (8 * (k & 3))) & 0xFFu];
       acc |= (uint64_t)(e & 0xFFFFu) << cnt;
       cnt += e >> 16;
       if (cnt >= 32) {
