@@ -7,9 +7,12 @@
 // GPU formulation.  A zero-initialised CRC register is linear in the data,
 // and advancing it over m zero bytes multiplies it by x^(8m) mod P.  So:
 //   - each workgroup takes a range of a buffer; thread t owns the 16-byte
-//     pieces t, t+256, ... (coalesced dwordx4 loads) and keeps one register:
-//     advance by the 4080 bytes between its pieces (four byte-sliced lookups),
-//     then fold the piece in (slicing-by-4, Kounavis & Berry 2005);
+//     pieces t, t+256, ... (coalesced dwordx4 loads) and keeps one register
+//     r, relative to the end of its latest piece: r' = r x^(8 * 4096) xor
+//     crc0(piece), the advance by one 4 KiB tile as four byte-sliced
+//     lookups and crc0 (the zero-init CRC of the 16 bytes, slicing-by-4,
+//     Kounavis & Berry 2005) independent of r, so that the serial chain per
+//     piece is one round of lookups;
 //   - every thread's register is moved to the range end by one GF(2)
 //     multiply with x^(8d) (d = its distance to the end) and the 256 values
 //     are xor-reduced: the range's zero-init CRC;
@@ -33,7 +36,7 @@ constexpr uint32_t kPiece = 16, kThreads = 256, kTile = kPiece * kThreads;
 
 // Table layout in device memory (words):
 //   [0, 1024)     T0..T3: one-byte table and its slicing-by-4 successors
-//   [1024, 2048)  S0..S3: byte-sliced advance over kTile - kPiece zero bytes
+//   [1024, 2048)  S0..S3: byte-sliced advance over kTile zero bytes
 //   [2048, 2304)  K[t] = x^(8 * 16 * (255 - t))
 //   [2304, 2368)  X[k] = x^(8 * 2^k)
 constexpr uint32_t kTabS = 1024, kTabK = 2048, kTabX = 2304, kTabWords = 2368;
@@ -72,7 +75,7 @@ std::vector<uint32_t> build_tables() {
   uint32_t* X = &tab[kTabX];
   X[0] = kOne >> 8;  // x^8
   for (int k = 1; k < 64; ++k) X[k] = gf2_mulmod(X[k - 1], X[k - 1]);
-  const uint32_t adv = xpow8(kTile - kPiece, X);
+  const uint32_t adv = xpow8(kTile, X);
   for (int k = 0; k < 4; ++k)
     for (uint32_t b = 0; b < 256; ++b) tab[kTabS + 256 * k + b] = gf2_mulmod(b << (8 * k), adv);
   for (uint32_t t = 0; t < kThreads; ++t) tab[kTabK + t] = xpow8((uint64_t)kPiece * (kThreads - 1 - t), X);
@@ -132,12 +135,25 @@ __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restri
     for (int h = 0; h < kRatio; ++h) v[h] = g_ld_nt16(reinterpret_cast<uint64_t>(p + k * kThreads * kRatio + h));
     forward16<kChain>(v, pl);
 #pragma unroll
-    for (int j = 0; j < kNp; ++j) acc[j] = crc_piece(T, sliced(S, acc[j]), pl[j]);
+    for (int j = 0; j < kNp; ++j) acc[j] = sliced(S, acc[j]) ^ crc_piece(T, 0u, pl[j]);
   };
+  // four tiles per iteration, their loads issued before any lookup
+  constexpr int kU = 4;
   uint64_t k = 0;
-  for (; k + 2 <= full; k += 2) {
-    step(k);
-    step(k + 1);
+  for (; k + kU <= full; k += kU) {
+    u32x4 v[kU][kRatio];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int h = 0; h < kRatio; ++h)
+        v[u][h] = g_ld_nt16(reinterpret_cast<uint64_t>(p + (k + u) * kThreads * kRatio + h));
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      u32x4 pl[kNp];
+      forward16<kChain>(v[u], pl);
+#pragma unroll
+      for (int j = 0; j < kNp; ++j) acc[j] = sliced(S, acc[j]) ^ crc_piece(T, 0u, pl[j]);
+    }
   }
   for (; k < full; ++k) step(k);
   if (tail == 0) {
@@ -156,9 +172,11 @@ __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restri
       end = base + kPiece;
       any = true;
     } else if (base < R.n) {
+      // the register advanced over the gap before this piece
+      const uint32_t gap = full ? xpow8(kTile - kPiece, gtab + kTabX) : 0u;
 #pragma unroll
       for (int j = 0; j < kNp; ++j) {
-        uint32_t c = sliced(S, acc[j]);
+        uint32_t c = gf2_mulmod(acc[j], gap);
         for (uint64_t i = base; i < R.n; ++i) c = T[(c ^ forward_byte<kChain>(R.src, i, j)) & 255u] ^ (c >> 8);
         acc[j] = c;
       }
