@@ -175,6 +175,7 @@ int64_t ilv_decode_payload(DevCtx& ctx, uint64_t in_dev, size_t in_len, uint64_t
   X.planes[0].len = in_len;
   X.planes[0].coded = 1;
   X.family = family;
+  X.crc_first = kIlvNoCrc;
   int64_t rc = ilv_decode_tensors(ctx, std::vector<IlvTensor>{X});
   return rc == kOk ? (int64_t)expected : rc;
 }

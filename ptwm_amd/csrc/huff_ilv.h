@@ -48,8 +48,14 @@ struct IlvTensor {
   uint32_t n_planes;
   IlvPlane planes[4];
   uint32_t family;  // IlvFamily
-  uint32_t pad;
+  // huff_ilv family, chains with CRC-able planes (crc_chain_supported): the
+  // zero-init CRC-32 of every whole 16 KiB block of each plane, relative to
+  // the block's end, goes to crc_part[4 * (crc_first + block) + plane];
+  // kIlvNoCrc: none
+  uint32_t crc_first;
 };
+constexpr uint32_t kIlvNoCrc = 0xFFFFFFFFu;
+constexpr uint32_t kIlvCrcWords = 2048;  // LDS words of the fused CRC's tables (T0..T3, 1 KiB advance)
 
 struct IlvEncPlane {
   uint64_t src;        // plane bytes (16-byte aligned)
@@ -82,12 +88,14 @@ struct IlvPackJob {
 // tpre[j+1] - 1.  grid: persistent workgroups, each taking an equal range of
 // tiles.  n_slots: LDS table slots per workgroup (>= the coded planes of any
 // tensor); stage_words: LDS staging words per wavefront (multiple of 4);
-// blocks needing more are decoded from global memory.
+// blocks needing more are decoded from global memory.  crc_tab: the CRC
+// tables (crc_device.h layout) when some tensor has crc_first set, else
+// null; the kernel then also writes the CRC block partials to crc_part.
 hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uint32_t* tix, const uint32_t* tpre,
                              uint32_t m, uint32_t grid, uint32_t* status, uint32_t n_slots, uint32_t stage_words,
-                             hipStream_t stream);
-size_t ilv_decode_lds_bytes(uint32_t chain, uint32_t n_slots, uint32_t stage_words);
-hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, int* wg_per_cu);
+                             const uint32_t* crc_tab, uint32_t* crc_part, hipStream_t stream);
+size_t ilv_decode_lds_bytes(uint32_t chain, uint32_t n_slots, uint32_t stage_words, bool crc);
+hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, bool crc, int* wg_per_cu);
 hipError_t launch_ilv_pack(const IlvPackJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream);
 hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_t max_n, uint32_t* hist,
                            hipStream_t stream);

@@ -33,6 +33,7 @@
 // from the code lengths), a host prefix sum for block offsets, and an encode
 // pass that writes each lane's words at its prefix-summed offset.
 #include "huff_ilv.h"
+#include "crc_device.h"
 #include "ilv_common.h"
 
 #include <cstring>
@@ -413,9 +414,17 @@ __device__ __forceinline__ void load_raw(const BlockState<ChainInfo<kChain>::np>
 // raw planes' groups (loaded one round ahead, so their latency overlaps the
 // table lookups), merge and store.  luts: LDS address of the first table
 // slot; plane p uses the table at st.lut[p].  out: output tensor address.
-template <uint32_t kChain, bool kTail, bool kStaged>
+//
+// kCrc (crc_on uniform, whole blocks only): acc[p] becomes the zero-init
+// CRC-32 of the lane's 16 pieces of plane p (pieces 1 KiB apart), relative
+// to the end of its last piece: acc' = acc x^(8 * 1024) xor crc0(piece),
+// the advance by byte-sliced lookups (crcL + 1024) and crc0 by slicing-by-4
+// (crcL), off the register's serial chain.
+template <uint32_t kChain, bool kTail, bool kStaged, bool kCrc = false>
 __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& st, uint32_t luts, uint64_t out,
-                                             uint64_t n, uint64_t bstart, uint32_t lane) {
+                                             uint64_t n, uint64_t bstart, uint32_t lane,
+                                             const uint32_t* crcL = nullptr, bool crc_on = false,
+                                             uint32_t* acc = nullptr) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
   constexpr uint32_t RATIO = ChainInfo<kChain>::ratio;
   uint32_t nxt[NP][4];
@@ -427,7 +436,6 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
   for (uint32_t r = 0; r < kIlvRounds; ++r) {
     const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
     const uint32_t count = group_count<kTail>(pos, n);
-    constexpr uint32_t SLOT = chain_slot_bytes(kChain);
     uint32_t v[NP][4];
     bool done = false;
     if constexpr (NP == 2 && kStaged && !kTail) {
@@ -480,6 +488,17 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
     } else {
       load_raw<kChain, kTail>(st, pos + (uint64_t)kIlvGroup * 64u, n, nxt, r + 1 < kIlvRounds);
     }
+    if constexpr (kCrc) {
+      if (crc_on) {
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+          const uint32_t xf = ChainInfo<kChain>::xf[p];
+          const u32x4 pl = u32x4_make(unxform_word(xf, v[p][0]), unxform_word(xf, v[p][1]),
+                                      unxform_word(xf, v[p][2]), unxform_word(xf, v[p][3]));
+          acc[p] = sliced(crcL + 1024, acc[p]) ^ crc_piece(crcL, 0u, pl);
+        }
+      }
+    }
     if (kTail && count == 0) continue;
     uint32_t o[4 * RATIO];
     merge_group<kChain>(v, o);
@@ -499,19 +518,20 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
 // tensors: all tensors of the call; tix[j]: the tensor of this launch's j-th
 // entry, whose 4-block tiles are tpre[j] .. tpre[j+1] - 1 (m entries,
 // n_tiles = tpre[m]).  Workgroup g takes tiles [g n_tiles / G, (g+1) n_tiles / G).
-template <uint32_t kChain>
+template <uint32_t kChain, bool kCrc>
 __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __restrict__ tensors,
                                                          const uint32_t* __restrict__ tix,
                                                          const uint32_t* __restrict__ tpre, uint32_t m,
                                                          uint32_t* __restrict__ status, uint32_t n_slots,
-                                                         uint32_t stage_words) {
+                                                         uint32_t stage_words, const uint32_t* __restrict__ crc_tab,
+                                                         uint32_t* __restrict__ crc_part) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
   constexpr uint32_t SLOT = chain_slot_bytes(kChain);
   // The kernel has no static LDS, so the dynamic area starts at LDS address
   // 0 and every table sits on a SLOT boundary (entry address =
   // (window & mask) | table base).  Layout:
   //   [n_slots tables (coded planes from the last one down)][DecodeCtl]
-  //   [4 wavefronts x stage_words][96 spare words]
+  //   [4 wavefronts x stage_words][96 spare words][kCrc: CRC tables]
   extern __shared__ __align__(16) uint8_t smem[];
   DecodeCtl& ctl = *reinterpret_cast<DecodeCtl*>(smem + n_slots * SLOT);
   uint32_t* const stage = reinterpret_cast<uint32_t*>(smem + n_slots * SLOT + sizeof(DecodeCtl));
@@ -546,6 +566,12 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
   }
   uint32_t j = lo, cur = 0xFFFFFFFFu, bad = 0;
   uint32_t* const sw = stage + wave * stage_words;
+  // CRC tables: T0..T3 and the byte-sliced advance over 1 KiB (visible
+  // after the first tile's barriers)
+  uint32_t* const crcL = stage + 4 * stage_words + kIlvStageSpare;
+  if constexpr (kCrc) {
+    for (uint32_t i = t; i < kIlvCrcWords; i += 256) crcL[i] = crc_tab[i < 1024 ? i : i - 1024 + kCrcTabS1024];
+  }
   for (uint32_t tile = tile0; tile < tile1; ++tile) {
     while (tile >= tpre[j + 1]) ++j;
     const uint32_t ti = tix[j];
@@ -708,6 +734,10 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
     }
     const uint64_t out = T.out;
     uint32_t q0[NP];
+    const bool crc_on = kCrc && T.crc_first != kIlvNoCrc && bstart + kIlvBlock <= n;
+    uint32_t acc[NP];
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p) acc[p] = 0;
     // skew uniform planes only when the staging budget has room for it
     if (need + need_skew > stage_words) uni_mask = 0;
     if (need <= stage_words) {
@@ -766,8 +796,8 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (full) decode_block<kChain, false, true>(st, luts, out, n, bstart, lane);
-      else decode_block<kChain, true, true>(st, luts, out, n, bstart, lane);
+      if (full) decode_block<kChain, false, true, kCrc>(st, luts, out, n, bstart, lane, crcL, crc_on, acc);
+      else decode_block<kChain, true, true, kCrc>(st, luts, out, n, bstart, lane, crcL, crc_on, acc);
       __builtin_amdgcn_wave_barrier();
     } else {
 #pragma unroll
@@ -776,7 +806,20 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
         st.nw[p] = lane_c[p];
         q0[p] = 0;
       }
-      decode_block<kChain, true, false>(st, luts, out, n, bstart, lane);
+      decode_block<kChain, true, false, kCrc>(st, luts, out, n, bstart, lane, crcL, crc_on, acc);
+    }
+    if constexpr (kCrc) {
+      if (crc_on) {
+        // lane l's last piece ends 16 (63 - l) bytes before the block's end
+        const uint32_t K = crc_tab[kCrcTabK64 + lane];
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+          uint32_t a = gf2_mulmod(acc[p], K);
+#pragma unroll
+          for (int d = 32; d >= 1; d >>= 1) a ^= __shfl_xor(a, d, 64);
+          if (lane == 0) g_st<uint32_t>(reinterpret_cast<uint64_t>(crc_part + 4ull * (T.crc_first + bi) + p), a);
+        }
+      }
     }
     // acceptance: every lane's words hold exactly its codes
 #pragma unroll
@@ -912,52 +955,57 @@ __global__ void __launch_bounds__(64) ilv_encode_kernel(const IlvEncPlane* __res
   if (cnt && wi < c) g_st<uint32_t>(w + 4ull * wi, (uint32_t)acc);
 }
 
-size_t ilv_decode_lds_bytes(uint32_t chain, uint32_t n_slots, uint32_t stage_words) {
-  return (size_t)n_slots * chain_slot_bytes(chain) + sizeof(DecodeCtl) + (4ull * stage_words + kIlvStageSpare) * 4ull;
+size_t ilv_decode_lds_bytes(uint32_t chain, uint32_t n_slots, uint32_t stage_words, bool crc) {
+  return (size_t)n_slots * chain_slot_bytes(chain) + sizeof(DecodeCtl) +
+         (4ull * stage_words + kIlvStageSpare + (crc ? kIlvCrcWords : 0u)) * 4ull;
 }
 
-static const void* ilv_decode_fn(uint32_t chain) {
+// the fused plane CRC exists for the chains whose plane bytes are the
+// decoded symbols up to a byte rotation (crc_chain_supported)
+static bool ilv_crc_chain(uint32_t chain) {
+  return chain == kChainIeee16Split2 || chain == kChainIeee32Split4 || chain == kChainPassthrough;
+}
+
+static const void* ilv_decode_fn(uint32_t chain, bool crc) {
+  if (crc) {
+    switch (chain) {
+      case kChainIeee16Split2: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainIeee16Split2, true>);
+      case kChainIeee32Split4: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainIeee32Split4, true>);
+      case kChainPassthrough: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainPassthrough, true>);
+      default: return nullptr;
+    }
+  }
   switch (chain) {
-    case kChainIeee16Split2: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainIeee16Split2>);
-    case kChainIeee32Split4: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainIeee32Split4>);
-    case kChainE4m3Nibble: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainE4m3Nibble>);
-    case kChainE5m2Nibble: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainE5m2Nibble>);
-    case kChainNibbleSplit: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainNibbleSplit>);
-    case kChainPassthrough: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainPassthrough>);
+    case kChainIeee16Split2: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainIeee16Split2, false>);
+    case kChainIeee32Split4: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainIeee32Split4, false>);
+    case kChainE4m3Nibble: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainE4m3Nibble, false>);
+    case kChainE5m2Nibble: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainE5m2Nibble, false>);
+    case kChainNibbleSplit: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainNibbleSplit, false>);
+    case kChainPassthrough: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainPassthrough, false>);
     default: return nullptr;
   }
 }
 
-hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, int* wg_per_cu) {
-  const void* fn = ilv_decode_fn(chain);
+hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, bool crc, int* wg_per_cu) {
+  const void* fn = ilv_decode_fn(chain, crc);
   if (!fn) return hipErrorInvalidValue;
   return hipOccupancyMaxActiveBlocksPerMultiprocessor(wg_per_cu, fn, 256,
-                                                      ilv_decode_lds_bytes(chain, n_slots, stage_words));
+                                                      ilv_decode_lds_bytes(chain, n_slots, stage_words, crc));
 }
 
 hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uint32_t* tix, const uint32_t* tpre,
                              uint32_t m, uint32_t grid, uint32_t* status, uint32_t n_slots, uint32_t stage_words,
-                             hipStream_t stream) {
+                             const uint32_t* crc_tab, uint32_t* crc_part, hipStream_t stream) {
   if (!grid || !m) return hipSuccess;
   if (stage_words % 4 != 0 || stage_words < 8) return hipErrorInvalidValue;
-  const size_t lds = ilv_decode_lds_bytes(chain, n_slots, stage_words);
-  switch (chain) {
-#define PTWM_ILV_CASE(C)                                                                                        \
-  case C:                                                                                                       \
-    hipLaunchKernelGGL(ilv_decode_kernel<C>, dim3(grid), dim3(256), lds, stream, tensors, tix, tpre, m, status, \
-                       n_slots, stage_words);                                                                   \
-    break;
-    PTWM_ILV_CASE(kChainIeee16Split2)
-    PTWM_ILV_CASE(kChainIeee32Split4)
-    PTWM_ILV_CASE(kChainE4m3Nibble)
-    PTWM_ILV_CASE(kChainE5m2Nibble)
-    PTWM_ILV_CASE(kChainNibbleSplit)
-    PTWM_ILV_CASE(kChainPassthrough)
-#undef PTWM_ILV_CASE
-    default:
-      return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  const bool crc = crc_tab != nullptr;
+  if (crc && (!crc_part || !ilv_crc_chain(chain))) return hipErrorInvalidValue;
+  const size_t lds = ilv_decode_lds_bytes(chain, n_slots, stage_words, crc);
+  const void* fn = ilv_decode_fn(chain, crc);
+  if (!fn) return hipErrorInvalidValue;
+  void* args[] = {&tensors, &tix, &tpre, &m, &status, &n_slots, &stage_words, &crc_tab, &crc_part};
+  const hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, lds, stream);
+  return e != hipSuccess ? e : hipGetLastError();
 }
 
 // Packed-nibble payload bodies: job blockIdx.y, each thread turns 16 plane

@@ -100,6 +100,13 @@ __device__ __forceinline__ uint32_t xform_word(uint32_t x, uint32_t v) {
 // Planes, output bytes per plane byte and the symbol transform of each plane
 // (applied by the decode table for coded planes, by xform_word for raw
 // ones) per chain.
+// Plane bytes back from xform_word's output, for the transforms of the
+// chains whose fused decode also computes plane CRCs (kXNone, kXRot1: the
+// inverse rotates each byte left by one).
+__device__ __forceinline__ uint32_t unxform_word(uint32_t x, uint32_t v) {
+  return x == kXRot1 ? ((v << 1) & 0xFEFEFEFEu) | ((v >> 7) & 0x01010101u) : v;
+}
+
 template <uint32_t kChain>
 struct ChainInfo;
 template <> struct ChainInfo<kChainIeee16Split2> {

@@ -18,6 +18,7 @@
 #include "huff_ilv.h"
 #include "huffman_host.h"
 #include "ilv_host.h"
+#include "integrity.h"
 #include "rans_ilv.h"
 #include "runtime.h"
 
@@ -273,6 +274,7 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
   // global-memory path.
   struct Launch {
     uint32_t family, chain, first, m, slots, stage_words, grid;
+    bool crc;  // some tensor of the launch has fused CRC partials (huff_ilv family)
   };
   std::vector<Launch> launches;
   std::vector<uint32_t> idx;  // per launch: [m + 1 prefix][m tensor indexes]
@@ -281,9 +283,14 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     std::vector<uint32_t> tix, tpre{0};
     uint32_t slots = 0;
     uint64_t est = 0;
+    bool crc = false;
     for (uint32_t ti = 0; ti < nt; ++ti) {
       const IlvTensor& T = tensors[ti];
       if (T.family != fam || T.chain != chain || T.n == 0) continue;
+      if (T.crc_first != kIlvNoCrc) {
+        if (fam != kFamilyHuff) return kInternal;
+        crc = true;
+      }
       const uint64_t nb = (T.n + kIlvBlock - 1) / kIlvBlock;
       // LDS table slots and staging for the planes that may be coded: a
       // native payload of the stored (n + 1) or packed (8 + ceil(n / 2))
@@ -311,7 +318,8 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     }
     if (tix.empty()) continue;
     const uint64_t max_lds = fam == kFamilyHuff ? kIlvMaxLds : kRilvMaxLds;
-    const uint64_t fixed = fam == kFamilyHuff ? ilv_decode_lds_bytes(chain, slots, 0) : rilv_decode_lds_bytes(chain, slots, 0);
+    const uint64_t fixed =
+        fam == kFamilyHuff ? ilv_decode_lds_bytes(chain, slots, 0, crc) : rilv_decode_lds_bytes(chain, slots, 0);
     uint64_t cap_words = ((max_lds - std::min<uint64_t>(fixed, max_lds)) / 16) & ~3ull;
     // the staging area also holds the payload heads at a tensor's start
     const uint64_t head_min = fam == kFamilyHuff ? kIlvHeadWords : kRilvHeadWords;  // 4 planes over 4 wavefronts
@@ -319,19 +327,20 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     if (stage > cap_words) stage = cap_words;
     if (stage < head_min) return kInternal;
     int per_cu = 0;
-    const uint64_t occ_key = (uint64_t)chain | ((uint64_t)slots << 8) | (stage << 16) | ((uint64_t)fam << 62);
+    const uint64_t occ_key =
+        (uint64_t)chain | ((uint64_t)slots << 8) | (stage << 16) | ((uint64_t)crc << 61) | ((uint64_t)fam << 62);
     auto it = ctx.ilv_occupancy.find(occ_key);
     if (it != ctx.ilv_occupancy.end()) {
       per_cu = it->second;
     } else {
-      if (fam == kFamilyHuff) PTWM_HIP_TRY(ilv_decode_occupancy(chain, slots, (uint32_t)stage, &per_cu));
+      if (fam == kFamilyHuff) PTWM_HIP_TRY(ilv_decode_occupancy(chain, slots, (uint32_t)stage, crc, &per_cu));
       else PTWM_HIP_TRY(rilv_decode_occupancy(chain, slots, (uint32_t)stage, &per_cu));
       ctx.ilv_occupancy[occ_key] = per_cu;
     }
     if (per_cu < 1) per_cu = 1;
     const uint64_t n_tiles = tpre.back();
     const uint32_t grid = (uint32_t)std::min<uint64_t>(n_tiles, (uint64_t)per_cu * ctx.cu_count);
-    launches.push_back(Launch{fam, chain, (uint32_t)idx.size(), (uint32_t)tix.size(), slots, (uint32_t)stage, grid});
+    launches.push_back(Launch{fam, chain, (uint32_t)idx.size(), (uint32_t)tix.size(), slots, (uint32_t)stage, grid, crc});
     idx.insert(idx.end(), tpre.begin(), tpre.end());
     idx.insert(idx.end(), tix.begin(), tix.end());
   }
@@ -352,12 +361,17 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     PTWM_HIP_TRY(hipEventRecord(ctx.ev[3], s));
   }
   uint32_t* status_dev = reinterpret_cast<uint32_t*>(d + off_status);
+  const uint32_t* crc_tab = nullptr;
+  for (const Launch& L : launches)
+    if (L.crc && !crc_tab)
+      if (int64_t rc = crc_tables(ctx, &crc_tab); rc != kOk) return rc;
   for (const Launch& L : launches) {
     const uint32_t* base = reinterpret_cast<const uint32_t*>(d + off_idx) + L.first;
     const IlvTensor* td = reinterpret_cast<const IlvTensor*>(d);
     if (L.family == kFamilyHuff)
       PTWM_HIP_TRY(launch_ilv_decode(L.chain, td, base + L.m + 1, base, L.m, L.grid, status_dev, L.slots,
-                                     L.stage_words, s));
+                                     L.stage_words, L.crc ? crc_tab : nullptr,
+                                     static_cast<uint32_t*>(ctx.crc_part.ptr), s));
     else
       PTWM_HIP_TRY(launch_rilv_decode(L.chain, td, base + L.m + 1, base, L.m, L.grid, status_dev, L.slots,
                                       L.stage_words, s));

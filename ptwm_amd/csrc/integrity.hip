@@ -22,6 +22,7 @@
 #include "integrity.h"
 
 #include "chain_ops.h"
+#include "crc_device.h"
 
 #include <algorithm>
 #include <vector>
@@ -30,41 +31,11 @@ namespace ptwm {
 
 namespace {
 
-constexpr uint32_t kPoly = 0xEDB88320u;  // reflected x^32 + x^26 + ... + 1; bit 31 = x^0
-constexpr uint32_t kOne = 0x80000000u;   // the polynomial 1
-constexpr uint32_t kPiece = 16, kThreads = 256, kTile = kPiece * kThreads;
-
-// Table layout in device memory (words):
-//   [0, 1024)     T0..T3: one-byte table and its slicing-by-4 successors
-//   [1024, 2048)  S0..S3: byte-sliced advance over kTile zero bytes
-//   [2048, 2304)  K[t] = x^(8 * 16 * (255 - t))
-//   [2304, 2368)  X[k] = x^(8 * 2^k)
-constexpr uint32_t kTabS = 1024, kTabK = 2048, kTabX = 2304, kTabWords = 2368;
-
-// a * b mod P, reflected representation (bit 31 - i holds the x^i coefficient)
-__host__ __device__ inline uint32_t gf2_mulmod(uint32_t a, uint32_t b) {
-  uint32_t p = 0;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    p ^= b & (0u - ((a >> (31 - i)) & 1u));
-    b = (b >> 1) ^ (kPoly & (0u - (b & 1u)));
-  }
-  return p;
-}
-
-// x^(8 n) mod P from the squares table X (X[k] = x^(8 * 2^k))
-__host__ __device__ inline uint32_t xpow8(uint64_t n, const uint32_t* X) {
-  uint32_t r = kOne;
-  for (int k = 0; n; ++k, n >>= 1)
-    if (n & 1u) r = gf2_mulmod(r, X[k]);
-  return r;
-}
-
 std::vector<uint32_t> build_tables() {
-  std::vector<uint32_t> tab(kTabWords, 0);
+  std::vector<uint32_t> tab(kCrcTabWords, 0);
   for (uint32_t i = 0; i < 256; ++i) {
     uint32_t c = i;
-    for (int k = 0; k < 8; ++k) c = (c >> 1) ^ (kPoly & (0u - (c & 1u)));
+    for (int k = 0; k < 8; ++k) c = (c >> 1) ^ (kCrcPoly & (0u - (c & 1u)));
     tab[i] = c;
   }
   for (int k = 1; k < 4; ++k)
@@ -72,31 +43,18 @@ std::vector<uint32_t> build_tables() {
       const uint32_t prev = tab[256 * (k - 1) + i];
       tab[256 * k + i] = (prev >> 8) ^ tab[prev & 255u];
     }
-  uint32_t* X = &tab[kTabX];
-  X[0] = kOne >> 8;  // x^8
+  uint32_t* X = &tab[kCrcTabX];
+  X[0] = kCrcOne >> 8;  // x^8
   for (int k = 1; k < 64; ++k) X[k] = gf2_mulmod(X[k - 1], X[k - 1]);
-  const uint32_t adv = xpow8(kTile, X);
+  const uint32_t adv = xpow8(kCrcTile, X);
   for (int k = 0; k < 4; ++k)
-    for (uint32_t b = 0; b < 256; ++b) tab[kTabS + 256 * k + b] = gf2_mulmod(b << (8 * k), adv);
-  for (uint32_t t = 0; t < kThreads; ++t) tab[kTabK + t] = xpow8((uint64_t)kPiece * (kThreads - 1 - t), X);
+    for (uint32_t b = 0; b < 256; ++b) tab[kCrcTabS + 256 * k + b] = gf2_mulmod(b << (8 * k), adv);
+  for (uint32_t t = 0; t < kCrcThreads; ++t) tab[kCrcTabK + t] = xpow8((uint64_t)kCrcPiece * (kCrcThreads - 1 - t), X);
+  const uint32_t adv1k = xpow8(1024, X);
+  for (int k = 0; k < 4; ++k)
+    for (uint32_t b = 0; b < 256; ++b) tab[kCrcTabS1024 + 256 * k + b] = gf2_mulmod(b << (8 * k), adv1k);
+  for (uint32_t l = 0; l < 64; ++l) tab[kCrcTabK64 + l] = xpow8(16ull * (63 - l), X);
   return tab;
-}
-
-__device__ __forceinline__ uint32_t sliced(const uint32_t* L, uint32_t c) {
-  return L[c & 255u] ^ L[256 + ((c >> 8) & 255u)] ^ L[512 + ((c >> 16) & 255u)] ^ L[768 + (c >> 24)];
-}
-
-// one word through the one-byte tables T0..T3 (T3 takes the first byte)
-__device__ __forceinline__ uint32_t crc_word(const uint32_t* T, uint32_t c, uint32_t w) {
-  c ^= w;
-  return T[768 + (c & 255u)] ^ T[512 + ((c >> 8) & 255u)] ^ T[256 + ((c >> 16) & 255u)] ^ T[c >> 24];
-}
-
-__device__ __forceinline__ uint32_t crc_piece(const uint32_t* T, uint32_t c, u32x4 v) {
-  c = crc_word(T, c, v.x);
-  c = crc_word(T, c, v.y);
-  c = crc_word(T, c, v.z);
-  return crc_word(T, c, v.w);
 }
 
 __device__ __forceinline__ uint32_t block_xor(uint32_t v, uint32_t* red) {
@@ -107,24 +65,26 @@ __device__ __forceinline__ uint32_t block_xor(uint32_t v, uint32_t* red) {
 }
 
 // Zero-init CRC of each range, relative to the range's end, for every plane
-// of the range.  A range is a run of whole elements of one buffer; with
-// kChain = passthrough the buffer is a plane itself, otherwise a restored
-// tensor whose plane bytes are re-derived by the (bijective) forward chain.
+// of the range, to part[4 * r + plane] with r = slot[range] (slot null: r =
+// range).  A range is a run of whole elements of one buffer; with kChain =
+// passthrough the buffer is a plane itself, otherwise a restored tensor
+// whose plane bytes are re-derived by the (bijective) forward chain.
 template <uint32_t kChain>
 __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restrict__ ranges,
                                                         const uint32_t* __restrict__ gtab,
-                                                        uint32_t* __restrict__ part) {
+                                                        uint32_t* __restrict__ part,
+                                                        const uint32_t* __restrict__ slot) {
   constexpr int kNp = kChain == kChainIeee16Split2 ? 2 : kChain == kChainIeee32Split4 ? 4 : 1;
   constexpr int kRatio = kNp;  // tensor bytes per plane byte for these chains
-  __shared__ uint32_t tab[kTabK];  // T0..T3, S0..S3
+  __shared__ uint32_t tab[kCrcTabK];  // T0..T3, S0..S3
   __shared__ uint32_t red[4];
   const uint32_t t = threadIdx.x;
-  for (uint32_t i = t; i < kTabK; i += kThreads) tab[i] = gtab[i];
+  for (uint32_t i = t; i < kCrcTabK; i += kCrcThreads) tab[i] = gtab[i];
   const CrcRange R = ranges[blockIdx.x];
   __syncthreads();
   const uint32_t* T = tab;
-  const uint32_t* S = tab + kTabS;
-  const uint64_t full = R.n / kTile, tail = R.n % kTile;
+  const uint32_t* S = tab + kCrcTabS;
+  const uint64_t full = R.n / kCrcTile, tail = R.n % kCrcTile;
   const u32x4* p = reinterpret_cast<const u32x4*>(R.src) + (uint64_t)t * kRatio;
   uint32_t acc[kNp];
 #pragma unroll
@@ -132,7 +92,7 @@ __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restri
   auto step = [&](uint64_t k) {
     u32x4 v[kRatio], pl[kNp];
 #pragma unroll
-    for (int h = 0; h < kRatio; ++h) v[h] = g_ld_nt16(reinterpret_cast<uint64_t>(p + k * kThreads * kRatio + h));
+    for (int h = 0; h < kRatio; ++h) v[h] = g_ld_nt16(reinterpret_cast<uint64_t>(p + k * kCrcThreads * kRatio + h));
     forward16<kChain>(v, pl);
 #pragma unroll
     for (int j = 0; j < kNp; ++j) acc[j] = sliced(S, acc[j]) ^ crc_piece(T, 0u, pl[j]);
@@ -146,7 +106,7 @@ __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restri
     for (int u = 0; u < kU; ++u)
 #pragma unroll
       for (int h = 0; h < kRatio; ++h)
-        v[u][h] = g_ld_nt16(reinterpret_cast<uint64_t>(p + (k + u) * kThreads * kRatio + h));
+        v[u][h] = g_ld_nt16(reinterpret_cast<uint64_t>(p + (k + u) * kCrcThreads * kRatio + h));
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       u32x4 pl[kNp];
@@ -158,22 +118,22 @@ __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restri
   for (; k < full; ++k) step(k);
   if (tail == 0) {
     if (full) {
-      const uint32_t K = gtab[kTabK + t];
+      const uint32_t K = gtab[kCrcTabK + t];
 #pragma unroll
       for (int j = 0; j < kNp; ++j) acc[j] = gf2_mulmod(acc[j], K);
     }
   } else {
     // the last, partial tile: thread t's piece may be whole, cut, or absent
-    const uint64_t base = full * kTile + (uint64_t)kPiece * t;
-    uint64_t end = full ? base - kTile + kPiece : 0;
+    const uint64_t base = full * kCrcTile + (uint64_t)kCrcPiece * t;
+    uint64_t end = full ? base - kCrcTile + kCrcPiece : 0;
     bool any = full != 0;
-    if (base + kPiece <= R.n) {
+    if (base + kCrcPiece <= R.n) {
       step(full);
-      end = base + kPiece;
+      end = base + kCrcPiece;
       any = true;
     } else if (base < R.n) {
       // the register advanced over the gap before this piece
-      const uint32_t gap = full ? xpow8(kTile - kPiece, gtab + kTabX) : 0u;
+      const uint32_t gap = full ? xpow8(kCrcTile - kCrcPiece, gtab + kCrcTabX) : 0u;
 #pragma unroll
       for (int j = 0; j < kNp; ++j) {
         uint32_t c = gf2_mulmod(acc[j], gap);
@@ -184,7 +144,7 @@ __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restri
       any = true;
     }
     if (any) {
-      const uint32_t K = xpow8(R.n - end, gtab + kTabX);
+      const uint32_t K = xpow8(R.n - end, gtab + kCrcTabX);
 #pragma unroll
       for (int j = 0; j < kNp; ++j) acc[j] = gf2_mulmod(acc[j], K);
     }
@@ -192,7 +152,7 @@ __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restri
 #pragma unroll
   for (int j = 0; j < kNp; ++j) {
     const uint32_t v = block_xor(acc[j], red);
-    if (t == 0) part[4ull * blockIdx.x + j] = v;
+    if (t == 0) part[4ull * (slot ? slot[blockIdx.x] : blockIdx.x) + j] = v;
     __syncthreads();
   }
 }
@@ -205,9 +165,9 @@ __global__ void __launch_bounds__(256) crc_combine_kernel(const CrcPlane* __rest
                                                           uint32_t* __restrict__ crc_out) {
   __shared__ uint32_t red[4];
   const CrcPlane B = planes[blockIdx.x];
-  const uint32_t* X = gtab + kTabX;
+  const uint32_t* X = gtab + kCrcTabX;
   const uint32_t t = threadIdx.x;
-  const uint32_t q = (B.n_ranges + kThreads - 1) / kThreads;
+  const uint32_t q = (B.n_ranges + kCrcThreads - 1) / kCrcThreads;
   const uint32_t r0 = std::min(B.n_ranges, t * q), r1 = std::min(B.n_ranges, r0 + q);
   uint32_t acc = 0;
   if (r0 < r1) {
@@ -305,23 +265,107 @@ __global__ void __launch_bounds__(64) xxh64_kernel(const HashTask* __restrict__ 
 
 int chain_np(uint32_t chain) { return chain == kChainIeee16Split2 ? 2 : chain == kChainIeee32Split4 ? 4 : 1; }
 
+// c: 0 = IEEE16 split2, 1 = IEEE32 split4, 2 = passthrough
+hipError_t launch_crc_ranges(int c, uint32_t cnt, const CrcRange* r, const uint32_t* gtab, uint32_t* part,
+                             const uint32_t* slot, hipStream_t s) {
+  const dim3 g(cnt), b(kCrcThreads);
+  if (c == 0) hipLaunchKernelGGL(crc_range_kernel<kChainIeee16Split2>, g, b, 0, s, r, gtab, part, slot);
+  if (c == 1) hipLaunchKernelGGL(crc_range_kernel<kChainIeee32Split4>, g, b, 0, s, r, gtab, part, slot);
+  if (c == 2) hipLaunchKernelGGL(crc_range_kernel<kChainPassthrough>, g, b, 0, s, r, gtab, part, slot);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool crc_chain_supported(uint32_t chain) {
   return chain == kChainIeee16Split2 || chain == kChainIeee32Split4 || chain == kChainPassthrough;
 }
 
+int64_t crc_tables(DevCtx& ctx, const uint32_t** tab) {
+  if (!ctx.crc_tab_ready) {
+    const std::vector<uint32_t> t = build_tables();
+    PTWM_HIP_TRY(ctx.crc_tab.ensure(t.size() * 4));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.crc_tab.ptr, t.data(), t.size() * 4, hipMemcpyHostToDevice, ctx.stream));
+    PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+    ctx.crc_tab_ready = true;
+  }
+  *tab = static_cast<const uint32_t*>(ctx.crc_tab.ptr);
+  return kOk;
+}
+
+int64_t crc32_combine(DevCtx& ctx, const std::vector<CrcPlane>& planes, const uint32_t* d_part,
+                      std::vector<uint32_t>& crcs) {
+  crcs.assign(planes.size(), 0);
+  if (planes.empty()) return kOk;
+  hipStream_t s = ctx.stream;
+  const uint32_t* gtab = nullptr;
+  if (int64_t rc = crc_tables(ctx, &gtab); rc != kOk) return rc;
+  const size_t np = planes.size();
+  PTWM_HIP_TRY(ctx.crc_comb.ensure(np * (sizeof(CrcPlane) + 4) + 64));
+  CrcPlane* d_planes = static_cast<CrcPlane*>(ctx.crc_comb.ptr);
+  uint32_t* d_out = reinterpret_cast<uint32_t*>(d_planes + np);
+  PTWM_HIP_TRY(hipMemcpyAsync(d_planes, planes.data(), np * sizeof(CrcPlane), hipMemcpyHostToDevice, s));
+  for (size_t p0 = 0; p0 < np; p0 += 65535) {
+    const uint32_t cnt = (uint32_t)std::min<size_t>(65535, np - p0);
+    hipLaunchKernelGGL(crc_combine_kernel, dim3(cnt), dim3(kCrcThreads), 0, s, d_planes + p0, d_part, gtab, d_out + p0);
+    PTWM_HIP_TRY(hipGetLastError());
+  }
+  PTWM_HIP_TRY(hipMemcpyAsync(crcs.data(), d_out, np * 4, hipMemcpyDeviceToHost, s));
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  return kOk;
+}
+
+int64_t crc32_fused(DevCtx& ctx, const std::vector<FusedCrc>& tensors, uint32_t* d_part, std::vector<uint32_t>& crcs) {
+  crcs.clear();
+  if (tensors.empty()) return kOk;
+  hipStream_t s = ctx.stream;
+  const uint32_t* gtab = nullptr;
+  if (int64_t rc = crc_tables(ctx, &gtab); rc != kOk) return rc;
+  // the partial last blocks, by chain (the decode wrote the whole ones)
+  const uint32_t chains[3] = {kChainIeee16Split2, kChainIeee32Split4, kChainPassthrough};
+  std::vector<CrcRange> ranges;
+  std::vector<uint32_t> slots;
+  uint32_t first[4] = {0, 0, 0, 0};
+  std::vector<CrcPlane> planes;
+  for (int c = 0; c < 3; ++c) {
+    first[c] = (uint32_t)ranges.size();
+    for (const FusedCrc& f : tensors) {
+      if (f.chain != chains[c] || f.n % kFusedCrcBlock == 0) continue;
+      const uint64_t nb = (f.n + kFusedCrcBlock - 1) / kFusedCrcBlock;
+      const uint64_t b0 = (nb - 1) * kFusedCrcBlock;
+      if (f.out & 15u) return kInternal;
+      ranges.push_back(CrcRange{f.out + b0 * (uint64_t)chain_np(f.chain), f.n - b0});
+      slots.push_back((uint32_t)(f.first_block + nb - 1));
+    }
+  }
+  first[3] = (uint32_t)ranges.size();
+  for (const FusedCrc& f : tensors) {
+    if (!crc_chain_supported(f.chain) || f.n == 0) return kInternal;
+    const uint32_t nb = (uint32_t)((f.n + kFusedCrcBlock - 1) / kFusedCrcBlock);
+    for (int j = 0; j < chain_np(f.chain); ++j)
+      planes.push_back(CrcPlane{f.n, kFusedCrcBlock, f.first_block, nb, (uint32_t)j});
+  }
+  const size_t nr = ranges.size();
+  if (nr) {
+    PTWM_HIP_TRY(ctx.crc_args.ensure(nr * (sizeof(CrcRange) + 4) + 64));
+    CrcRange* d_ranges = static_cast<CrcRange*>(ctx.crc_args.ptr);
+    uint32_t* d_slots = reinterpret_cast<uint32_t*>(d_ranges + nr);
+    PTWM_HIP_TRY(hipMemcpyAsync(d_ranges, ranges.data(), nr * sizeof(CrcRange), hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(hipMemcpyAsync(d_slots, slots.data(), nr * 4, hipMemcpyHostToDevice, s));
+    for (int c = 0; c < 3; ++c) {
+      const uint32_t cnt = first[c + 1] - first[c];
+      if (cnt) PTWM_HIP_TRY(launch_crc_ranges(c, cnt, d_ranges + first[c], gtab, d_part, d_slots + first[c], s));
+    }
+  }
+  return crc32_combine(ctx, planes, d_part, crcs);
+}
+
 int64_t crc32_planes(DevCtx& ctx, const std::vector<CrcTask>& tasks, std::vector<uint32_t>& crcs) {
   crcs.clear();
   if (tasks.empty()) return kOk;
   hipStream_t s = ctx.stream;
-  if (!ctx.crc_tab_ready) {
-    const std::vector<uint32_t> tab = build_tables();
-    PTWM_HIP_TRY(ctx.crc_tab.ensure(tab.size() * 4));
-    PTWM_HIP_TRY(hipMemcpyAsync(ctx.crc_tab.ptr, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, s));
-    PTWM_HIP_TRY(hipStreamSynchronize(s));
-    ctx.crc_tab_ready = true;
-  }
+  const uint32_t* tabs = nullptr;
+  if (int64_t rc = crc_tables(ctx, &tabs); rc != kOk) return rc;
   // Range length (plane bytes): a multiple of the 4 KiB tile, sized so the
   // whole batch makes about 16 workgroups per CU.
   uint64_t total = 0;
@@ -331,8 +375,8 @@ int64_t crc32_planes(DevCtx& ctx, const std::vector<CrcTask>& tasks, std::vector
     total += k.n * (uint64_t)chain_np(k.chain);
   }
   const uint64_t cus = ctx.cu_count > 0 ? (uint64_t)ctx.cu_count : 256;
-  uint64_t rl = (total / (cus * 16) + kTile - 1) / kTile * kTile;
-  rl = std::max<uint64_t>(rl, 16 * kTile);
+  uint64_t rl = (total / (cus * 16) + kCrcTile - 1) / kCrcTile * kCrcTile;
+  rl = std::max<uint64_t>(rl, 16 * kCrcTile);
   rl = std::min<uint64_t>(rl, 1ull << 30);
   // ranges grouped by chain (one launch per chain), planes in task order
   const uint32_t chains[3] = {kChainIeee16Split2, kChainIeee32Split4, kChainPassthrough};
@@ -375,20 +419,17 @@ int64_t crc32_planes(DevCtx& ctx, const std::vector<CrcTask>& tasks, std::vector
   uint32_t* d_out = d_part + 4 * nr;
   if (nr) PTWM_HIP_TRY(hipMemcpyAsync(d_ranges, ranges.data(), nr * sizeof(CrcRange), hipMemcpyHostToDevice, s));
   PTWM_HIP_TRY(hipMemcpyAsync(d_planes, planes.data(), np * sizeof(CrcPlane), hipMemcpyHostToDevice, s));
-  const uint32_t* gtab = static_cast<const uint32_t*>(ctx.crc_tab.ptr);
+  const uint32_t* gtab = tabs;
   for (int c = 0; c < 3; ++c) {
     const uint32_t cnt = first[c + 1] - first[c];
     if (!cnt) continue;
     const CrcRange* r = d_ranges + first[c];
     uint32_t* pp = d_part + 4ull * first[c];
-    if (c == 0) hipLaunchKernelGGL(crc_range_kernel<kChainIeee16Split2>, dim3(cnt), dim3(kThreads), 0, s, r, gtab, pp);
-    if (c == 1) hipLaunchKernelGGL(crc_range_kernel<kChainIeee32Split4>, dim3(cnt), dim3(kThreads), 0, s, r, gtab, pp);
-    if (c == 2) hipLaunchKernelGGL(crc_range_kernel<kChainPassthrough>, dim3(cnt), dim3(kThreads), 0, s, r, gtab, pp);
-    PTWM_HIP_TRY(hipGetLastError());
+    PTWM_HIP_TRY(launch_crc_ranges(c, cnt, r, gtab, pp, nullptr, s));
   }
   for (size_t p0 = 0; p0 < np; p0 += 65535) {
     const uint32_t cnt = (uint32_t)std::min<size_t>(65535, np - p0);
-    hipLaunchKernelGGL(crc_combine_kernel, dim3(cnt), dim3(kThreads), 0, s, d_planes + p0, d_part, gtab, d_out + p0);
+    hipLaunchKernelGGL(crc_combine_kernel, dim3(cnt), dim3(kCrcThreads), 0, s, d_planes + p0, d_part, gtab, d_out + p0);
     PTWM_HIP_TRY(hipGetLastError());
   }
   crcs.assign(np, 0);

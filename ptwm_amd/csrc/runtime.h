@@ -42,6 +42,7 @@ struct DevCtx {
   PinnedBuffer h_small;
   // huff_ilv encoder / decoder scratch
   DeviceBuffer enc_planes, enc_hist, enc_codes, enc_blocks, enc_lane_words, enc_block_bytes, enc_pack;
+  DeviceBuffer crc_comb, crc_part;  // CRC combine arguments; fused-decode CRC block partials
   DeviceBuffer ilv_args, ilv_realign;
   // reference-format (Huffman / rANS) encoder scratch
   DeviceBuffer ref_jobs, ref_hist, ref_segs, ref_seglen, ref_codes, ref_rans_tab, ref_rans_segs, ref_rans_scratch,

@@ -209,6 +209,10 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   const size_t nt = plan.tensors.size();
   std::vector<IlvTensor> ilv;
   std::vector<char> fused(nt, 0);
+  // huff_ilv tensors with plane CRCs: the decode kernel also writes the CRC
+  // partials of their whole blocks (tensor t's from block crc_first[t])
+  std::vector<uint32_t> crc_first(nt, kIlvNoCrc);
+  uint64_t crc_blocks = 0;
   for (size_t t = 0; t < nt; ++t) {
     const PlanTensor& T = plan.tensors[t];
     bool any_huff = false, any_rans = false, ok = ((out_dev + T.out_offset) & 15u) == 0;
@@ -230,6 +234,12 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     X.chain = T.chain;
     X.n_planes = (uint32_t)T.planes.size();
     X.family = any_rans ? kFamilyRans : kFamilyHuff;
+    X.crc_first = kIlvNoCrc;
+    if (T.has_crc && !any_rans && X.n > 0) {
+      X.crc_first = crc_first[t] = (uint32_t)crc_blocks;
+      crc_blocks += (X.n + kIlvBlock - 1) / kIlvBlock;
+      if (crc_blocks > 0xFFFFFFFEull) return kInvalidInput;
+    }
     const uint32_t coded_codec = any_rans ? kCodecRansIlv : kCodecHuffIlv;
     for (size_t p = 0; p < T.planes.size(); ++p) {
       X.planes[p].base = in_dev + T.planes[p].payload_offset;
@@ -295,6 +305,7 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
         X.planes[0].len = P.payload_len;
         X.planes[0].coded = 1;
         X.family = P.codec == kCodecRansIlv ? kFamilyRans : kFamilyHuff;
+        X.crc_first = kIlvNoCrc;
         ilv.push_back(X);
         continue;
       }
@@ -333,6 +344,7 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   }
   // huff_ilv first: fused tensors straight to the output, passthrough planes to scratch
   if (!ilv.empty()) {
+    if (crc_blocks) PTWM_HIP_TRY(ctx.crc_part.ensure(16ull * crc_blocks));
     int64_t rc = ilv_decode_tensors(ctx, ilv);
     if (rc != kOk) return rc;
   }
@@ -372,11 +384,16 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   // (container.rs:2185-2194); a mismatch is InvalidContainer there.
   std::vector<CrcTask> crc_tasks;
   std::vector<uint32_t> crc_want;
+  std::vector<FusedCrc> crc_fused;
+  std::vector<uint32_t> crc_fused_want;
   std::vector<HashTask> hash_tasks;
   std::vector<uint64_t> hash_want;
   for (size_t t = 0; t < nt; ++t) {
     const PlanTensor& T = plan.tensors[t];
-    if (T.has_crc) {
+    if (T.has_crc && crc_first[t] != kIlvNoCrc) {
+      crc_fused.push_back(FusedCrc{out_dev + T.out_offset, T.planes[0].plane_len, T.chain, crc_first[t]});
+      for (const PlanPlane& P : T.planes) crc_fused_want.push_back(P.crc32);
+    } else if (T.has_crc) {
       if (fused[t]) {
         crc_tasks.push_back(CrcTask{out_dev + T.out_offset, T.planes[0].plane_len, T.chain});
       } else {
@@ -397,6 +414,14 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     if (got.size() != crc_want.size()) return kInternal;
     for (size_t k = 0; k < got.size(); ++k)
       if (got[k] != crc_want[k]) return kInvalidInput;
+  }
+  if (!crc_fused.empty()) {
+    std::vector<uint32_t> got;
+    const int64_t rc = crc32_fused(ctx, crc_fused, static_cast<uint32_t*>(ctx.crc_part.ptr), got);
+    if (rc != kOk) return rc;
+    if (got.size() != crc_fused_want.size()) return kInternal;
+    for (size_t k = 0; k < got.size(); ++k)
+      if (got[k] != crc_fused_want[k]) return kInvalidInput;
   }
   if (!hash_tasks.empty()) {
     std::vector<uint64_t> got;
