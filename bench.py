@@ -24,6 +24,7 @@ import argparse
 import ctypes as C
 import gc
 import json
+import re
 import os
 import sys
 import time
@@ -201,6 +202,13 @@ def build_workload(name: str, resident: bool = False) -> Workload:
     if native == "rans_ilv":
         desc += ", planes coded with rans_ilv (GPU-native interleaved rANS)"
         kernel = kernel.replace("ilv_decode_kernel", "rilv_decode_kernel")
+    elif kernel != exact:
+        # huff_ilv kernels carry a second template argument: plane CRC-32
+        # computed in the decode (bf16, fp32 and passthrough chains with CRCs)
+        fused_crc = "crc" in opts and name in ("llama8b", "bf16_1k", "bf16_1g", "fp32_4k")
+        kernel = re.sub(r"<(\d)>", lambda m: f"<{m.group(1)}, {'true' if fused_crc else 'false'}>", kernel)
+        if fused_crc:
+            kernel += " + plane CRC-32 fused"
     if resident:
         n_rep = 1
     else:
