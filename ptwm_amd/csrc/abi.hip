@@ -492,7 +492,7 @@ int64_t ptwm_mi355x_encode_tensors_cuda(uint32_t family, uint32_t n_tensors, con
   // tensor): forward chains of the batch into plane scratch, then every
   // plane of the batch through one encoder pass (one histogram, size and
   // encode launch each), payloads appended at 256-byte aligned offsets.
-  constexpr uint64_t kBatchBytes = 1ull << 30;
+  constexpr uint64_t kBatchBytes = 4ull << 30;
   std::vector<IlvEncResult> res;     // per plane, offsets relative to out_dev_ptr
   uint64_t out_used = 0, needed_total = 0;
   bool too_small = false;

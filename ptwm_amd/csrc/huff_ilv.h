@@ -101,7 +101,11 @@ hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_
                            hipStream_t stream);
 hipError_t launch_ilv_size(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,
                            const uint32_t* codes, uint8_t* lane_words, uint32_t* block_bytes, hipStream_t stream);
+// stage_words (<= kIlvEncStageMax): LDS words per workgroup for assembling
+// a block's coded words (blocks with more are written lane by lane)
+constexpr uint32_t kIlvEncStageMax = 4096;
 hipError_t launch_ilv_encode(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,
-                             const uint32_t* codes, const uint8_t* lane_words, hipStream_t stream);
+                             const uint32_t* codes, const uint8_t* lane_words, uint32_t stage_words,
+                             hipStream_t stream);
 
 }  // namespace ptwm

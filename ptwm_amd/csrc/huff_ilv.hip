@@ -905,11 +905,22 @@ __global__ void __launch_bounds__(64) ilv_size_kernel(const IlvEncPlane* __restr
 }
 
 // One wavefront per block: write lane word counts and packed lane streams.
+__device__ __forceinline__ void put_word(bool staged, uint32_t* sw, uint64_t w, uint32_t wi, uint32_t v) {
+  if (staged) sw[wi] = v;
+  else g_st<uint32_t>(w + 4ull * wi, v);
+}
+
+// A block whose coded words (sum of the lane counts) fit stage_words is
+// assembled in LDS and written out by the whole wavefront in consecutive
+// words; lanes writing their own streams directly scatter 4-byte stores over
+// the block (each lane's stream is a different part of it).
 __global__ void __launch_bounds__(64) ilv_encode_kernel(const IlvEncPlane* __restrict__ planes,
                                                         const IlvEncBlock* __restrict__ blocks,
                                                         const uint32_t* __restrict__ codes,
-                                                        const uint8_t* __restrict__ lane_words) {
+                                                        const uint8_t* __restrict__ lane_words,
+                                                        uint32_t stage_words) {
   __shared__ uint32_t code[256];
+  extern __shared__ uint32_t sbuf[];
   const IlvEncBlock B = blocks[blockIdx.x];
   const IlvEncPlane P = planes[B.plane];
   const uint32_t lane = threadIdx.x;
@@ -919,40 +930,62 @@ __global__ void __launch_bounds__(64) ilv_encode_kernel(const IlvEncPlane* __res
   gstore_u8(B.dst + lane, c);
   const uint32_t incl = wave_incl_scan(c);
   const uint64_t w = B.dst + 64 + 4ull * (incl - c);  // this lane's words
+  const uint32_t total = __shfl(incl, 63, 64);
+  const bool staged = total <= stage_words;           // uniform
+  uint32_t* const sw = sbuf + (incl - c);
   const uint64_t bstart = (uint64_t)B.block * kIlvBlock;
   uint64_t acc = 0;
   uint32_t cnt = 0, wi = 0;
   // (wi < c: the size pass counted these words; the bound only guards a
   // source that changed between the passes)
+  // whole groups: one 16-byte load (planes are 16-byte aligned), issued one
+  // round ahead; the 16 code lookups issued together
+  u32x4 nxt = u32x4_make(0, 0, 0, 0);
+  if (bstart + (uint64_t)kIlvGroup * lane + kIlvGroup <= P.n) nxt = gload_nt16(P.src + bstart + (uint64_t)kIlvGroup * lane);
   for (uint32_t r = 0; r < kIlvRounds; ++r) {
     const uint64_t pos = bstart + (uint64_t)kIlvGroup * (r * 64u + lane);
     if (pos >= P.n) continue;
-    // the group's symbols: one 16-byte load (planes are 16-byte aligned), or
-    // byte loads for the plane's partial last group
-    uint32_t xs[4] = {0, 0, 0, 0};
-    const uint32_t count = P.n - pos >= kIlvGroup ? kIlvGroup : (uint32_t)(P.n - pos);
-    if (count == kIlvGroup) {
-      const u32x4 x = gload_nt16(P.src + pos);
-      xs[0] = x.x;
-      xs[1] = x.y;
-      xs[2] = x.z;
-      xs[3] = x.w;
-    } else {
-      for (uint32_t k = 0; k < count; ++k) xs[k >> 2] |= gload_u8(P.src + pos + k) << (8 * (k & 3));
+    if (pos + kIlvGroup <= P.n) {
+      const u32x4 x = nxt;
+      const uint64_t pn = pos + (uint64_t)kIlvGroup * 64u;
+      if (r + 1 < kIlvRounds && pn + kIlvGroup <= P.n) nxt = gload_nt16(P.src + pn);
+      uint32_t e[kIlvGroup];
+#pragma unroll
+      for (uint32_t k = 0; k < kIlvGroup; ++k) e[k] = code[(x[k >> 2] >> (8 * (k & 3))) & 0xFFu];
+#pragma unroll
+      for (uint32_t k = 0; k < kIlvGroup; ++k) {
+        acc |= (uint64_t)(e[k] & 0xFFFFu) << cnt;
+        cnt += e[k] >> 16;
+        if (cnt >= 32) {
+          if (wi < c) put_word(staged, sw, w, wi, (uint32_t)acc);
+          ++wi;
+          acc >>= 32;
+          cnt -= 32;
+        }
+      }
+      continue;
     }
+    // the plane's partial last group: byte loads
+    uint32_t xs[4] = {0, 0, 0, 0};
+    const uint32_t count = (uint32_t)(P.n - pos);
+    for (uint32_t k = 0; k < count; ++k) xs[k >> 2] |= gload_u8(P.src + pos + k) << (8 * (k & 3));
     for (uint32_t k = 0; k < count; ++k) {
       const uint32_t e = code[(xs[k >> 2] >> (8 * (k & 3))) & 0xFFu];
       acc |= (uint64_t)(e & 0xFFFFu) << cnt;
       cnt += e >> 16;
       if (cnt >= 32) {
-        if (wi < c) g_st<uint32_t>(w + 4ull * wi, (uint32_t)acc);
+        if (wi < c) put_word(staged, sw, w, wi, (uint32_t)acc);
         ++wi;
         acc >>= 32;
         cnt -= 32;
       }
     }
   }
-  if (cnt && wi < c) g_st<uint32_t>(w + 4ull * wi, (uint32_t)acc);
+  if (cnt && wi < c) put_word(staged, sw, w, wi, (uint32_t)acc);
+  if (staged) {
+    __syncthreads();  // one wavefront: its LDS writes are visible to every lane
+    for (uint32_t i = lane; i < total; i += 64) g_st<uint32_t>(B.dst + 64 + 4ull * i, sbuf[i]);
+  }
 }
 
 size_t ilv_decode_lds_bytes(uint32_t chain, uint32_t n_slots, uint32_t stage_words, bool crc) {
@@ -1069,9 +1102,12 @@ hipError_t launch_ilv_size(const IlvEncPlane* planes, const IlvEncBlock* blocks,
 }
 
 hipError_t launch_ilv_encode(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,
-                             const uint32_t* codes, const uint8_t* lane_words, hipStream_t stream) {
+                             const uint32_t* codes, const uint8_t* lane_words, uint32_t stage_words,
+                             hipStream_t stream) {
   if (!n_blocks) return hipSuccess;
-  hipLaunchKernelGGL(ilv_encode_kernel, dim3(n_blocks), dim3(64), 0, stream, planes, blocks, codes, lane_words);
+  if (stage_words > kIlvEncStageMax) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(ilv_encode_kernel, dim3(n_blocks), dim3(64), 4ull * stage_words, stream, planes, blocks, codes,
+                     lane_words, stage_words);
   return hipGetLastError();
 }
 

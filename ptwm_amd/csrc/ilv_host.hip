@@ -218,19 +218,23 @@ int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, u
   }
   if (nblk) {
     // only blocks of coded planes are written; lw keeps the size-pass index
-    uint32_t live = 0;
+    uint32_t live = 0, max_words = 0;
     for (uint32_t i = 0; i < nblk; ++i)
       if (res[hblk[i].plane].coded) {
         IlvEncBlock bk = hblk[i];
         bk.lw = i;
         hblk[live++] = bk;
+        max_words = std::max(max_words, bbytes[i] >= 64 ? (bbytes[i] - 64) / 4 : 0u);
       }
+    // LDS for the largest block's words, within the cap (larger blocks are
+    // written lane by lane)
+    const uint32_t stage_words = std::min<uint32_t>(kIlvEncStageMax, (max_words + 3) & ~3u);
     if (live) {
       PTWM_HIP_TRY(hipMemcpyAsync(ctx.enc_blocks.ptr, hblk, live * sizeof(IlvEncBlock), hipMemcpyHostToDevice, s));
       PTWM_HIP_TRY(launch_ilv_encode(static_cast<const IlvEncPlane*>(ctx.enc_planes.ptr),
                                      static_cast<const IlvEncBlock*>(ctx.enc_blocks.ptr), live,
                                      static_cast<const uint32_t*>(ctx.enc_codes.ptr),
-                                     static_cast<const uint8_t*>(ctx.enc_lane_words.ptr), s));
+                                     static_cast<const uint8_t*>(ctx.enc_lane_words.ptr), stage_words, s));
     }
   }
   PTWM_HIP_TRY(hipStreamSynchronize(s));
