@@ -97,6 +97,17 @@ hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uin
 size_t ilv_decode_lds_bytes(uint32_t chain, uint32_t n_slots, uint32_t stage_words, bool crc);
 hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, bool crc, int* wg_per_cu);
 hipError_t launch_ilv_pack(const IlvPackJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream);
+
+// Stored and Identity payload bodies: n plane bytes from src to dst + shift;
+// shift 1 (stored form) also writes the tag byte 0 at dst.
+struct IlvStoreJob {
+  uint64_t src;  // 16-byte aligned
+  uint64_t dst;
+  uint64_t n;
+  uint32_t shift;  // 0 or 1
+  uint32_t pad;
+};
+hipError_t launch_ilv_store(const IlvStoreJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream);
 hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_t max_n, uint32_t* hist,
                            hipStream_t stream);
 hipError_t launch_ilv_size(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,

@@ -1075,6 +1075,46 @@ __global__ void __launch_bounds__(256) ilv_pack_kernel(const IlvPackJob* __restr
   }
 }
 
+// Job blockIdx.y; output vector v = bytes [16 v, 16 v + 16) of the payload
+// body at dst (shift 1: body byte 0 is the tag, byte k + 1 plane byte k).
+// The thread past the last whole output vector writes the tail bytewise.
+__global__ void __launch_bounds__(256) ilv_store_kernel(const IlvStoreJob* __restrict__ jobs) {
+  const IlvStoreJob J = jobs[blockIdx.y];
+  const uint64_t out_n = J.n + J.shift;
+  const uint64_t nvec = out_n / 16;
+  const uint64_t stride = (uint64_t)gridDim.x * 256u;
+  const bool aligned = (J.dst & 15u) == 0;
+  for (uint64_t v = (uint64_t)blockIdx.x * 256u + threadIdx.x; v <= nvec; v += stride) {
+    if (v < nvec) {
+      // plane bytes [16 v - shift, 16 v + 16 - shift); the 16-byte aligned
+      // load at 16 v starts inside the plane (16 v < n)
+      const u32x4 x = gload_nt16(J.src + 16 * v);
+      u32x4 o = x;
+      if (J.shift) {
+        const uint32_t prev = v == 0 ? 0u : gload_u8(J.src + 16 * v - 1);  // tag 0 before plane byte 0
+        o = u32x4_make((x.x << 8) | prev, __builtin_amdgcn_alignbit(x.y, x.x, 24),
+                       __builtin_amdgcn_alignbit(x.z, x.y, 24), __builtin_amdgcn_alignbit(x.w, x.z, 24));
+      }
+      if (aligned) {
+        g_st<u32x4>(J.dst + 16 * v, o);
+      } else {
+        for (int k = 0; k < 16; ++k) gstore_u8(J.dst + 16 * v + k, o[k >> 2] >> (8 * (k & 3)));
+      }
+    } else {
+      for (uint64_t i = 16 * nvec; i < out_n; ++i)
+        gstore_u8(J.dst + i, i < J.shift ? 0u : gload_u8(J.src + i - J.shift));
+    }
+  }
+}
+
+hipError_t launch_ilv_store(const IlvStoreJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream) {
+  if (!n_jobs) return hipSuccess;
+  uint64_t blocks = (max_n / 16 + 256) / 256;
+  if (blocks > 1024) blocks = 1024;
+  hipLaunchKernelGGL(ilv_store_kernel, dim3((uint32_t)blocks, n_jobs), dim3(256), 0, stream, jobs);
+  return hipGetLastError();
+}
+
 hipError_t launch_ilv_pack(const IlvPackJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream) {
   if (!n_jobs) return hipSuccess;
   uint64_t blocks = (max_n / 16 + 256) / 256;

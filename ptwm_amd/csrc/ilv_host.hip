@@ -51,23 +51,21 @@ uint32_t ilv_choose_form(uint64_t n, bool nibbles, bool codable, uint64_t coded_
 int64_t ilv_store_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, uint32_t np, uint64_t out_dev,
                          const IlvEncResult* res, const uint32_t* form, std::vector<uint8_t>& keep) {
   hipStream_t s = ctx.stream;
-  keep.assign((size_t)np * (8 + sizeof(IlvPackJob)), 0);
+  // [8 header bytes per plane][pack jobs][store jobs]; the job arrays go
+  // to the device in one upload
+  keep.assign((size_t)np * (8 + sizeof(IlvPackJob) + sizeof(IlvStoreJob)), 0);
   IlvPackJob* jobs = reinterpret_cast<IlvPackJob*>(keep.data() + 8 * np);
-  uint32_t nj = 0;
-  uint64_t max_n = 0;
+  IlvStoreJob* sjobs = reinterpret_cast<IlvStoreJob*>(keep.data() + (8 + sizeof(IlvPackJob)) * (size_t)np);
+  uint32_t nj = 0, ns = 0;
+  uint64_t max_n = 0, max_s = 0;
   for (uint32_t p = 0; p < np; ++p) {
     const uint64_t dst = out_dev + res[p].offset;
     uint8_t* head = keep.data() + 8 * p;
-    if (form[p] == kFormIdentity) {
-      if (n[p])
-        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src[p]), n[p],
-                                    hipMemcpyDeviceToDevice, s));
-    } else if (form[p] == kFormStored) {
-      head[0] = 0;
-      PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), head, 1, hipMemcpyHostToDevice, s));
-      if (n[p])
-        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst + 1), reinterpret_cast<const void*>(src[p]), n[p],
-                                    hipMemcpyDeviceToDevice, s));
+    if (form[p] == kFormIdentity || form[p] == kFormStored) {
+      const uint32_t shift = form[p] == kFormStored ? 1u : 0u;
+      if (n[p] + shift == 0) continue;
+      sjobs[ns++] = IlvStoreJob{src[p], dst, n[p], shift, 0};
+      max_s = std::max(max_s, n[p] + shift);
     } else if (form[p] == kFormPacked) {
       head[0] = 2;
       const uint32_t nn = (uint32_t)n[p];
@@ -77,10 +75,15 @@ int64_t ilv_store_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, ui
       max_n = std::max(max_n, n[p]);
     }
   }
-  if (nj) {
-    PTWM_HIP_TRY(ctx.enc_pack.ensure(nj * sizeof(IlvPackJob)));
-    PTWM_HIP_TRY(hipMemcpyAsync(ctx.enc_pack.ptr, jobs, nj * sizeof(IlvPackJob), hipMemcpyHostToDevice, s));
-    PTWM_HIP_TRY(launch_ilv_pack(static_cast<const IlvPackJob*>(ctx.enc_pack.ptr), nj, max_n, s));
+  if (nj || ns) {
+    const size_t pack_bytes = nj * sizeof(IlvPackJob);
+    PTWM_HIP_TRY(ctx.enc_pack.ensure(pack_bytes + ns * sizeof(IlvStoreJob)));
+    if (ns) std::memmove(reinterpret_cast<uint8_t*>(jobs) + pack_bytes, sjobs, ns * sizeof(IlvStoreJob));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.enc_pack.ptr, jobs, pack_bytes + ns * sizeof(IlvStoreJob), hipMemcpyHostToDevice,
+                                s));
+    uint8_t* d = static_cast<uint8_t*>(ctx.enc_pack.ptr);
+    PTWM_HIP_TRY(launch_ilv_pack(reinterpret_cast<const IlvPackJob*>(d), nj, max_n, s));
+    PTWM_HIP_TRY(launch_ilv_store(reinterpret_cast<const IlvStoreJob*>(d + pack_bytes), ns, max_s, s));
   }
   return kOk;
 }
