@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <thread>
 #include <vector>
 
 #include "huff_ilv.h"
@@ -115,19 +116,33 @@ int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, u
   // ---- code tables ----
   std::vector<uint32_t> codes(np * 256, 0);
   std::vector<std::vector<uint8_t>> weights(np);
-  std::vector<bool> codable(np, false);
-  for (uint32_t p = 0; p < np; ++p) {
-    if (n[p] == 0) continue;
-    uint8_t lengths[256];
-    uint16_t rev[256];
-    if (!ilv_lengths_from_freqs(&hist[256 * p], lengths)) continue;
-    if (!huf_canonical(lengths, rev)) continue;
-    for (int sy = 0; sy < 256; ++sy) codes[256 * p + sy] = ((uint32_t)lengths[sy] << 16) | rev[sy];
-    uint8_t w[140];
-    int wl = huf_encode_weights(lengths, w);
-    if (wl < 0) continue;
-    weights[p].assign(w, w + wl);
-    codable[p] = true;
+  std::vector<uint8_t> codable(np, 0);
+  // planes are independent (each writes its own entries): spread large
+  // batches over host threads
+  auto build_codes = [&](uint32_t p0, uint32_t p1) {
+    for (uint32_t p = p0; p < p1; ++p) {
+      if (n[p] == 0) continue;
+      uint8_t lengths[256];
+      uint16_t rev[256];
+      if (!ilv_lengths_from_freqs(&hist[256 * p], lengths)) continue;
+      if (!huf_canonical(lengths, rev)) continue;
+      for (int sy = 0; sy < 256; ++sy) codes[256 * p + sy] = ((uint32_t)lengths[sy] << 16) | rev[sy];
+      uint8_t w[140];
+      int wl = huf_encode_weights(lengths, w);
+      if (wl < 0) continue;
+      weights[p].assign(w, w + wl);
+      codable[p] = 1;
+    }
+  };
+  const uint32_t hw = std::max(1u, std::thread::hardware_concurrency());
+  const uint32_t nthr = np >= 64 ? std::min<uint32_t>(std::min<uint32_t>(hw, 8), np / 16) : 1;
+  if (nthr <= 1) {
+    build_codes(0, np);
+  } else {
+    std::vector<std::thread> pool;
+    for (uint32_t t = 0; t < nthr; ++t)
+      pool.emplace_back(build_codes, (uint32_t)((uint64_t)np * t / nthr), (uint32_t)((uint64_t)np * (t + 1) / nthr));
+    for (std::thread& th : pool) th.join();
   }
   // ---- size pass over every block of every codable plane ----
   std::vector<IlvEncBlock> blocks;
