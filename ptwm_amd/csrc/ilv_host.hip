@@ -130,6 +130,17 @@ int64_t ilv_encode_planes(DevCtx& ctx, const uint64_t* src, const uint64_t* n, u
       uint8_t w[140];
       int wl = huf_encode_weights(lengths, w);
       if (wl < 0) continue;
+      // a coded payload is at least its header, offset table, lane counts
+      // and ceil(code bits / 8): a plane for which that is not shorter than
+      // the stored or packed form is not sized (the form choice below would
+      // not take the coded form)
+      uint64_t bits = 0;
+      for (int sy = 0; sy < 256; ++sy) bits += (uint64_t)hist[256 * p + sy] * lengths[sy];
+      const uint64_t nb = (n[p] + kIlvBlock - 1) / kIlvBlock;
+      const uint64_t lower = align_up(5 + (uint64_t)wl, 4) + 4 * (nb + 1) + 64 * nb + (bits + 7) / 8;
+      const uint64_t stored = n[p] + 1, packed = kPackedHeadBytes + (n[p] + 1) / 2;
+      const uint64_t other = all_nibbles(&hist[256 * p]) && packed < stored ? packed : stored;
+      if (lower >= other) continue;
       weights[p].assign(w, w + wl);
       codable[p] = 1;
     }
