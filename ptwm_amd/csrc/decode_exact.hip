@@ -514,19 +514,32 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
         }
         // fast stretch: normalised state (x >= L, so at most two renormalising
         // bytes per symbol) and two staged stream bytes in hand
-        while (x >= kRansL && k < end && n < kRansRound && q + 2 <= qlim) {
-          const uint32_t idx = x & (kRansScale - 1);
-          const uint32_t e = table32[idx];
-          const uint32_t b0 = buf[q - qb], b1 = buf[q - qb + 1];
-          g_st<uint8_t>(out + k, (uint8_t)(e & 0xFF));
-          x = ((e >> 8) & 0xFFF) * (x >> kRansProbBits) + idx - (e >> 20);
-          const bool n1 = x < kRansL;
-          x = n1 ? (x << 8) | b0 : x;
-          const bool n2 = x < kRansL;
-          x = n2 ? (x << 8) | b1 : x;
-          q += (uint32_t)n1 + (uint32_t)n2;
-          ++k;
-          ++n;
+        // A normalised state decodes to at least x >> 11 >= 2^12, so two
+        // bytes always renormalise it: the state stays normalised through
+        // the stretch and m steps need no checks.
+        if (x >= kRansL) {
+          uint32_t m = end - k < kRansRound - n ? end - k : kRansRound - n;
+          if (q + 2 <= qlim && (qlim - q) / 2 < m) m = (qlim - q) / 2;
+          if (q + 2 > qlim) m = 0;
+          auto step = [&]() {
+            const uint32_t idx = x & (kRansScale - 1);
+            const uint32_t e = table32[idx];
+            const uint32_t b0 = buf[q - qb], b1 = buf[q - qb + 1];
+            g_st<uint8_t>(out + k, (uint8_t)(e & 0xFF));
+            x = ((e >> 8) & 0xFFF) * (x >> kRansProbBits) + idx - (e >> 20);
+            const bool n1 = x < kRansL;
+            x = n1 ? (x << 8) | b0 : x;
+            const bool n2 = x < kRansL;
+            x = n2 ? (x << 8) | b1 : x;
+            q += (uint32_t)n1 + (uint32_t)n2;
+            ++k;
+          };
+          n += m;
+          for (; m >= 2; m -= 2) {
+            step();
+            step();
+          }
+          if (m) step();
         }
         // here pending is false: the last symbol's renormalisation is complete
         if (k == end) { done = true; break; }
