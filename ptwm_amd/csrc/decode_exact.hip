@@ -527,10 +527,11 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
             const uint32_t b0 = buf[q - qb], b1 = buf[q - qb + 1];
             g_st<uint8_t>(out + k, (uint8_t)(e & 0xFF));
             x = ((e >> 8) & 0xFFF) * (x >> kRansProbBits) + idx - (e >> 20);
-            const bool n1 = x < kRansL;
-            x = n1 ? (x << 8) | b0 : x;
-            const bool n2 = x < kRansL;
-            x = n2 ? (x << 8) | b1 : x;
+            // one byte when x < L = 2^23, a second when (x << 8 | b0) < L,
+            // i.e. x < 2^15: both tests on the decoded state
+            const bool n1 = x < kRansL, n2 = x < (kRansL >> 8);
+            const uint32_t x1 = (x << 8) | b0;
+            x = n2 ? (x1 << 8) | b1 : n1 ? x1 : x;
             q += (uint32_t)n1 + (uint32_t)n2;
             ++k;
           };
