@@ -424,14 +424,34 @@ __device__ __forceinline__ uint64_t rilv_pos(uint32_t b, uint32_t lane, uint32_t
   return (uint64_t)b * kIlvBlock + (uint64_t)kIlvGroup * (64u * (s / kIlvGroup) + lane) + (s % kIlvGroup);
 }
 
-// The encoder's step for one lane: renormalise (emit) then encode.
-__device__ __forceinline__ bool rilv_enc_step(uint32_t& x, uint32_t fc, uint32_t& word) {
+// 1 / f of each symbol's frequency (f = 0, a symbol the histogram did not
+// see, as 1), for the encoder's quotient estimate
+__device__ __forceinline__ float rilv_rcp(uint32_t fc) {
+  const uint32_t f0 = fc & 0xFFFFu;
+  return 1.0f / (float)(f0 ? f0 : 1u);
+}
+
+// The encoder's step for one lane: renormalise (emit) then encode.  After
+// renormalisation x < f 2^21, so q = x / f < 2^21 and the float estimate
+// x * (1 / f) is within one of it (x rounds by at most f / 8, the product
+// and the reciprocal add under 2^-22 relative); one correction step makes
+// q and r exact.
+__device__ __forceinline__ bool rilv_enc_step(uint32_t& x, uint32_t fc, float rf, uint32_t& word) {
   const uint32_t f0 = fc & 0xFFFFu, c = fc >> 16;
   const uint32_t f = f0 ? f0 : 1u;  // a symbol the histogram did not see (source changed): a bad stream, no trap
   const bool emit = (uint64_t)x >= ((uint64_t)f << 21);
   word = x & 0xFFFFu;
   if (emit) x >>= 16;
-  x = (x / f) * 2048u + (x % f) + c;
+  uint32_t q = (uint32_t)((float)x * rf);
+  int32_t r = (int32_t)(x - q * f);  // true value in [-f, 2f): exact as int32
+  if (r < 0) {
+    --q;
+    r += (int32_t)f;
+  } else if (r >= (int32_t)f) {
+    ++q;
+    r -= (int32_t)f;
+  }
+  x = q * 2048u + (uint32_t)r + c;
   return emit;
 }
 
@@ -455,10 +475,14 @@ __global__ void __launch_bounds__(64) rilv_size_kernel(const IlvEncPlane* __rest
                                                        const uint32_t* __restrict__ syms,
                                                        uint32_t* __restrict__ block_words) {
   __shared__ uint32_t fc[256];
+  __shared__ float rf[256];
   const RilvEncBlock B = blocks[blockIdx.x];
   const IlvEncPlane P = planes[B.plane];
   const uint32_t lane = threadIdx.x;
-  for (uint32_t i = lane; i < 256; i += 64) fc[i] = syms[256u * P.code_slot + i];
+  for (uint32_t i = lane; i < 256; i += 64) {
+    fc[i] = syms[256u * P.code_slot + i];
+    rf[i] = rilv_rcp(fc[i]);
+  }
   __syncthreads();
   uint32_t x = kRilvL, nw = 0;
   for (int r = (int)kIlvRounds - 1; r >= 0; --r) {
@@ -469,7 +493,8 @@ __global__ void __launch_bounds__(64) rilv_size_kernel(const IlvEncPlane* __rest
       bool emit = false;
       if (g0 + tt < P.n) {
         uint32_t w;
-        emit = rilv_enc_step(x, fc[(sym[tt >> 2] >> (8 * (tt & 3))) & 0xFFu], w);
+        const uint32_t sy = (sym[tt >> 2] >> (8 * (tt & 3))) & 0xFFu;
+        emit = rilv_enc_step(x, fc[sy], rf[sy], w);
       }
       nw += (uint32_t)__builtin_popcountll(__ballot(emit));
     }
@@ -483,10 +508,14 @@ __global__ void __launch_bounds__(64) rilv_encode_kernel(const IlvEncPlane* __re
                                                          const uint32_t* __restrict__ syms,
                                                          const uint32_t* __restrict__ block_words) {
   __shared__ uint32_t fc[256];
+  __shared__ float rf[256];
   const RilvEncBlock B = blocks[blockIdx.x];
   const IlvEncPlane P = planes[B.plane];
   const uint32_t lane = threadIdx.x;
-  for (uint32_t i = lane; i < 256; i += 64) fc[i] = syms[256u * P.code_slot + i];
+  for (uint32_t i = lane; i < 256; i += 64) {
+    fc[i] = syms[256u * P.code_slot + i];
+    rf[i] = rilv_rcp(fc[i]);
+  }
   __syncthreads();
   const uint32_t nw = block_words[blockIdx.x];
   const uint64_t words = B.dst + kRilvBlockHead;
@@ -498,7 +527,10 @@ __global__ void __launch_bounds__(64) rilv_encode_kernel(const IlvEncPlane* __re
     for (int tt = (int)kIlvGroup - 1; tt >= 0; --tt) {
       bool emit = false;
       uint32_t w = 0;
-      if (g0 + tt < P.n) emit = rilv_enc_step(x, fc[(sym[tt >> 2] >> (8 * (tt & 3))) & 0xFFu], w);
+      if (g0 + tt < P.n) {
+        const uint32_t sy = (sym[tt >> 2] >> (8 * (tt & 3))) & 0xFFu;
+        emit = rilv_enc_step(x, fc[sy], rf[sy], w);
+      }
       const uint64_t bal = __ballot(emit);
       tail -= (uint32_t)__builtin_popcountll(bal);
       const uint32_t rank =
