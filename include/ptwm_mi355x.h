@@ -138,7 +138,7 @@ int64_t ptwm_mi355x_encode_tensor_rans_cuda(uint32_t chain, uint64_t in_dev_ptr,
  * addition, no reference counterpart): tensor i is in_lens[i] bytes at
  * in_dev_ptrs[i] (16-byte aligned) with chain chains[i]; family 0 codes the
  * planes with huff_ilv, 1 with rans_ilv (each plane the smallest of coded,
- * packed, Identity).  Tensors are processed in batches of about 1 GiB of
+ * packed, Identity).  Tensors are processed in batches of about 4 GiB of
  * input, each batch's planes through one histogram, size and encode pass.
  * Payloads go to out_dev_ptr (256-byte aligned) at 256-byte aligned
  * offsets; *plan_out receives one PTMD plan for all tensors, restored back

@@ -171,7 +171,7 @@ def encode_tensor_cuda(chain: int, src, out, device_ordinal: int = 0, codec: str
 def encode_tensors_cuda(items, out, device_ordinal: int = 0, codec: str = "huff_ilv") -> tuple[int, bytes]:
     """Tensor-level GPU encode of many tensors in one call (library
     addition): ``items`` is a sequence of (chain, device tensor); every plane
-    coded with ``codec`` ("huff_ilv" or "rans_ilv"), batches of about 1 GiB
+    coded with ``codec`` ("huff_ilv" or "rans_ilv"), batches of about 4 GiB
     of input through one encoder pass each.  Returns (bytes used in ``out``,
     one PTMD plan whose tensors are restored back to back at 256-byte
     aligned offsets in the given order)."""
