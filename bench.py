@@ -1,22 +1,28 @@
 """Decode-throughput benchmark of the MI355X plane-codec path.
 
-``python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload llama8b|fp8|bf16_1k|fp32_4k]``
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload llama8b+crc|llama8b|fp8|...]``
 
 A "step" restores every tensor of the workload from its compressed planes,
 resident in HBM, through the library's tensor-level entry point
 (``ptwm_hardware_backend_v1_dispatch_decode_cuda``): entropy decode plus the
-inverse chain (merge + bit revert) in one fused kernel per chain.  Inputs are
-synthetic tensors of the BASELINE.json shapes, generated on the GPU from
-fixed seeds and encoded by the library's own GPU encoder
-(``ptwm_mi355x_encode_tensor_cuda``: huff_ilv planes, Identity when coding
-does not shrink a plane).  Every step's output is checked bit-exact against
-the original tensors after the timed region.
+inverse chain (merge + bit revert) in one fused kernel per chain and, for the
+default headline (config 4, ``llama8b+crc``), the CRC-32 of every decoded
+plane checked against the plan inside the timed region, as the reference's
+container decode does by default (container.rs:2154-2159,
+_config.py:179).  Inputs are synthetic tensors of the BASELINE.json shapes,
+generated on the GPU from fixed seeds and encoded by the library's own GPU
+encoder (huff_ilv planes, Identity when coding does not shrink a plane).
+Every step's output is checked bit-exact against the original tensors after
+the timed region.
 
 Prints one JSON line: ``value`` = restored GB/s (whole job, one GPU),
-``roofline`` for the dominant kernel (HIP events on the library stream), and
-``cpu_baseline`` = the C restatement of the reference CPU decoder (4-segment
-Huffman decode + fused inverse, parallel over chunks) on a bounded sample of
-the same workload, timed on this host.
+``roofline`` for the dominant kernel (HIP events on the library stream),
+``config.hash_verified`` = the same decode with every tensor's XXH64 also
+verified, ``config.secondary`` = the same bytes without verification, the
+other configs and the reference-format routes, and ``cpu_baseline`` = the C
+restatement of the reference CPU decoder (4-segment Huffman decode + fused
+inverse, tensors over threads) on a bounded sample of the same workload,
+timed on this host.
 """
 from __future__ import annotations
 
@@ -37,7 +43,8 @@ HBM_PEAK_GBS = 8000.0
 # Measured HBM bytes per launch of the workload's dominant kernel: the
 # copy-calibrated FETCH_SIZE + WRITE_SIZE of two rocprofv3 --pmc runs of this
 # script, recorded (with the commands and raw counters) in these summaries.
-TRAFFIC_PROFILES = {"llama8b": "profiles/ilv_decode_kernel_bf16_llama8b.md"}
+TRAFFIC_PROFILES = {"llama8b": "profiles/ilv_decode_kernel_bf16_llama8b.md",
+                    "llama8b+crc": "profiles/ilv_decode_kernel_crc_llama8b_crc.md"}
 
 
 def measured_traffic(workload: str):
@@ -120,25 +127,30 @@ EXACT_ROUTE = "decode_exact (reference streams) + merge"
 MIN_DISTINCT_BYTES = 1 << 30   # rotate inputs of smaller workloads (the MALL holds 256 MB)
 
 
-def build_workload(name: str, resident: bool = False) -> Workload:
-    """`name` is a workload below, optionally suffixed "+crc" (every plane's
-    CRC-32 in the plan, verified by the decode) and/or "+hash" (every
-    tensor's XXH64 in the plan, verified by the decode).  A workload under
-    1 GiB is built in as many distinct replicas (other seeds) as make 1 GiB,
-    and consecutive steps decode consecutive replicas, so that no step finds
-    its inputs in the 256 MB Infinity Cache; `resident` builds one replica
-    (cache-resident numbers)."""
-    import torch
-
-    from ptwm_amd import api, plan
-
+def parse_workload(name: str):
+    """"<workload>[@rans][+crc][+hash]" -> (workload, codec tag, options)."""
     base, *opts = name.split("+")
     if set(opts) - {"crc", "hash"}:
         raise SystemExit(f"unknown workload option in {name}")
-    # "<workload>@rans": the GPU-native planes coded with rans_ilv instead of huff_ilv
-    name, _, codec_tag = base.partition("@")
+    wl_name, _, codec_tag = base.partition("@")
     if codec_tag not in ("", "rans"):
         raise SystemExit(f"unknown codec tag in {base}")
+    return wl_name, codec_tag, set(opts)
+
+
+def build_workload(name: str, resident: bool = False, integrity: bool = False) -> Workload:
+    """`name` is a workload below, optionally suffixed "@rans" (GPU-native
+    planes coded with rans_ilv).  With `integrity`, every plane's CRC-32 and
+    every tensor's XXH64 are computed (by the library's own entry points) and
+    kept, so that plan variants with and without them can be measured on the
+    same compressed bytes (`plan_bytes`).  A workload under 1 GiB is built in
+    as many distinct replicas (other seeds) as make 1 GiB, and consecutive
+    steps decode consecutive replicas, so that no step finds its inputs in
+    the 256 MB Infinity Cache; `resident` builds one replica (cache-resident
+    numbers)."""
+    from ptwm_amd import plan
+
+    name, codec_tag, _ = parse_workload(name)
     native = "rans_ilv" if codec_tag == "rans" else "huff_ilv"
 
     CH = {"w": plan.CHAIN_IEEE16_SPLIT2, "n": plan.CHAIN_IEEE16_SPLIT2, "fp8": plan.CHAIN_E4M3_NIBBLE,
@@ -190,7 +202,7 @@ def build_workload(name: str, resident: bool = False) -> Workload:
     elif name == "c3_rans":
         specs = [((8192, 8192), "fp8")]
         ref = {"fp8": ([RANS, RANS], 0)}
-        desc = "config 3 in reference format: e4m3 8192x8192, rANS on both nibble planes"
+        desc = "config 3 in reference format: e4m3 8192x8192, rANS on both nibble planes (unchunked)"
         kernel = exact
     elif name == "c5_ref":
         specs = [((14336, 2048), "fp4"), ((14336, 128), "e8m0")]
@@ -199,22 +211,15 @@ def build_workload(name: str, resident: bool = False) -> Workload:
         kernel = exact
     else:
         raise SystemExit(f"unknown workload {name}")
-    if native == "rans_ilv":
+    if native == "rans_ilv" and ref is None:
         desc += ", planes coded with rans_ilv (GPU-native interleaved rANS)"
         kernel = kernel.replace("ilv_decode_kernel", "rilv_decode_kernel")
-    elif kernel != exact:
-        # huff_ilv kernels carry a second template argument: plane CRC-32
-        # computed in the decode (bf16, fp32 and passthrough chains with CRCs)
-        fused_crc = "crc" in opts and name in ("llama8b", "bf16_1k", "bf16_1g", "fp32_4k")
-        kernel = re.sub(r"<(\d)>", lambda m: f"<{m.group(1)}, {'true' if fused_crc else 'false'}>", kernel)
-        if fused_crc:
-            kernel += " + plane CRC-32 fused"
     if resident:
         n_rep = 1
     else:
         one = sum(int(np_prod(shape)) for shape, _ in specs)
         n_rep = max(1, -(-MIN_DISTINCT_BYTES // max(one, 1)))
-    reps = [build_replica(desc, specs, CH, ref, native, opts, r) for r in range(n_rep)]
+    reps = [build_replica(desc, specs, CH, ref, native, integrity, r) for r in range(n_rep)]
     wl = reps[0]
     wl.replicas = reps
     wl.kernel = kernel
@@ -225,6 +230,18 @@ def build_workload(name: str, resident: bool = False) -> Workload:
     return wl
 
 
+def kernel_label(wl, crc: bool) -> str:
+    """The dominant kernel's name for a plan variant: huff_ilv kernels carry a
+    second template argument, plane CRC-32 computed in the decode (bf16, fp32
+    and passthrough chains)."""
+    k = wl.kernel
+    if k == EXACT_ROUTE or k.startswith("rilv"):
+        return k
+    fused = crc and any(t.chain in (1, 2, 6) for t in wl.plans)
+    k = re.sub(r"<(\d)>", lambda m: f"<{m.group(1)}, {'true' if fused else 'false'}>", k)
+    return k + (" + plane CRC-32 fused" if fused else "")
+
+
 def np_prod(shape):
     n = 1
     for d in shape:
@@ -232,7 +249,23 @@ def np_prod(shape):
     return n
 
 
-def build_replica(desc, specs, CH, ref, native, opts, rep) -> Workload:
+def plan_bytes(rep, crc: bool, hsh: bool) -> bytes:
+    """The replica's PTMD plan with or without plane CRC-32 and tensor XXH64."""
+    import copy
+
+    from ptwm_amd.plan import encode_plan
+
+    plans = copy.deepcopy(rep.plans)
+    for t in plans:
+        if not hsh:
+            t.xxh64 = None
+        for p in t.planes:
+            if not crc:
+                p.crc32 = None
+    return encode_plan(plans)
+
+
+def build_replica(desc, specs, CH, ref, native, integrity, rep) -> Workload:
     import torch
 
     from ptwm_amd import api, plan
@@ -274,7 +307,7 @@ def build_replica(desc, specs, CH, ref, native, opts, rep) -> Workload:
             used, st = api.encode_tensors_cuda([(chain, raw) for raw, chain, _ in tensors], blob, 0, codec=native)
             torch.cuda.synchronize()
             times.append(time.perf_counter() - t0)
-        native_s = sorted(times)[len(times) // 2]
+        enc_s = sorted(times)[len(times) // 2]
         plans = plan.decode_plan(st)
         off = (used + 255) // 256 * 256
         out_off = plans[-1].out_offset + plans[-1].out_len if plans else 0
@@ -289,24 +322,20 @@ def build_replica(desc, specs, CH, ref, native, opts, rep) -> Workload:
             plans.append(t)
             off = (off + used + 255) // 256 * 256
             out_off = (out_off + raw.numel() + 255) // 256 * 256
-    torch.cuda.synchronize()
-    enc_s = native_s if ref is None else time.perf_counter() - t0
-    for (raw, chain, _), t in zip(tensors, plans):
-        if "crc" in opts:
+        torch.cuda.synchronize()
+        enc_s = time.perf_counter() - t0
+    if integrity:
+        for (raw, chain, _), t in zip(tensors, plans):
             for p, c in zip(t.planes, api.plane_crc32_cuda(chain, raw, 0)):
                 p.crc32 = c
-        if "hash" in opts:
             t.xxh64 = api.xxh64_cuda(raw, 0)
-    if opts:
-        wl.name += " (plan carries " + " and ".join(
-            {"crc": "plane CRC-32", "hash": "tensor XXH64"}[o] for o in opts) + ", verified by the decode)"
     wl.tensors = tensors
     wl.blob = blob[:off]
-    wl.plan_bytes = plan.encode_plan(plans)
+    wl.plans = plans
+    wl.plan_bytes = plan_bytes(wl, False, False)
     wl.out_len = out_off
     wl.restored = total_raw
     wl.comp_bytes = sum(p.payload_len for t in plans for p in t.planes)
-    wl.plans = plans
     wl.enc_s = enc_s
     return wl
 
@@ -320,13 +349,86 @@ def verify(wl, out) -> bool:
     return True
 
 
+def measure(wl, steps, warmup, crc=False, hsh=False):
+    """Time `steps` decodes of the workload's plan variant (CRC-32 / XXH64
+    verified or not) after `warmup` (at least one per replica), every
+    restored byte checked after the warmup and after the timed steps.
+    Returns (ms per step, dominant-kernel ms per step from HIP events)."""
+    import torch
+
+    from ptwm_amd import api, ids
+    from ptwm_amd._native import lib
+
+    L = lib()
+    reps = wl.replicas
+    plans = [plan_bytes(r, crc, hsh) for r in reps]
+    outs = [torch.empty(r.out_len, dtype=torch.uint8, device="cuda:0") for r in reps]
+    cur = [0]
+
+    def step():
+        k = cur[0] % len(reps)
+        cur[0] += 1
+        return api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL,
+                                                         plans[k], reps[k].blob, outs[k], 0)
+
+    def check(n, when):
+        for r, o in list(zip(reps, outs))[:n]:
+            if not verify(r, o):
+                raise SystemExit(f"decode mismatch on {wl.name}{when}")
+
+    for _ in range(max(warmup, len(reps))):
+        step()
+    torch.cuda.synchronize()
+    check(len(reps), "")
+    for o in outs:
+        o.zero_()
+    torch.cuda.synchronize()
+    cur[0] = 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    # the replicas the timed steps decoded were zeroed before them
+    check(min(steps, len(reps)), " (timed steps)")
+    ms_step = (t1 - t0) * 1e3 / steps
+    # kernel durations: HIP events around the decode kernels on the
+    # library stream, in separate (untimed) steps so the events do not
+    # add to the whole-call time above
+    L.ptwm_mi355x_set_profiling(0, 1)
+    ms = (C.c_float * 3)()
+    kern = []
+    for _ in range(min(steps, 5) if hsh else steps):
+        step()
+        L.ptwm_mi355x_last_kernel_ms(0, ms)
+        # [0]: entropy decode (fused with the merge on the huff_ilv route),
+        # [2]: every kernel of the call (exact route: decode + merge)
+        kern.append(ms[2] if wl.kernel == EXACT_ROUTE else ms[0])
+    L.ptwm_mi355x_set_profiling(0, 0)
+    return ms_step, sum(kern) / len(kern)
+
+
+def secondary_line(wl, ms, kms, crc=False, hsh=False):
+    return {"restored_gbs": round(wl.restored / (ms * 1e-3) / 1e9, 1),
+            "ms_per_step": round(ms, 4),
+            "kernel_gbs_restored": round(wl.restored / (kms * 1e-3) / 1e9, 1),
+            "kernel_gbs_traffic": round((wl.restored + wl.comp_bytes) / (kms * 1e-3) / 1e9, 1),
+            "kernel": kernel_label(wl, crc),
+            "ratio": round(wl.comp_bytes / wl.restored, 4), "encode_gbs": round(wl.encode_gbs, 1),
+            "replicas": len(wl.replicas),
+            "verified": "plane CRC-32 and tensor XXH64" if hsh else "plane CRC-32" if crc else "none",
+            "description": wl.name}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="llama8b")
-    ap.add_argument("--extra", default="fp8,mxfp4,llama8b+crc",
+    ap.add_argument("--workload", default="llama8b+crc",
+                    help="<workload>[@rans][+crc][+hash]: the headline decode (default: config 4, plane "
+                         "CRC-32 verified inside the timed region)")
+    ap.add_argument("--extra", default="fp8,mxfp4,c1_ref,c2_ref,c3_huf,c3_rans,c5_ref",
                     help="comma list of secondary workloads reported in config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--resident", action="store_true",
@@ -341,60 +443,6 @@ def main():
 
     import torch
 
-    from ptwm_amd import api, ids
-    from ptwm_amd._native import lib
-
-    L = lib()
-
-    def measure(wl, steps, warmup):
-        reps = wl.replicas
-        outs = [torch.empty(r.out_len, dtype=torch.uint8, device="cuda:0") for r in reps]
-        cur = [0]
-
-        def step():
-            k = cur[0] % len(reps)
-            cur[0] += 1
-            return api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL,
-                                                             reps[k].plan_bytes, reps[k].blob, outs[k], 0)
-
-        def check(n, when):
-            for r, o in list(zip(reps, outs))[:n]:
-                if not verify(r, o):
-                    raise SystemExit(f"decode mismatch on {wl.name}{when}")
-
-        # warmup decodes every replica once (at least `warmup` steps)
-        for _ in range(max(warmup, len(reps))):
-            step()
-        torch.cuda.synchronize()
-        check(len(reps), "")
-        for o in outs:
-            o.zero_()
-        torch.cuda.synchronize()
-        cur[0] = 0
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            step()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        # the replicas the timed steps decoded were zeroed before them
-        check(min(steps, len(reps)), " (timed steps)")
-        ms_step = (t1 - t0) * 1e3 / steps
-        # kernel durations: HIP events around the decode kernels on the
-        # library stream, in separate (untimed) steps so the events do not
-        # add to the whole-call time above
-        L.ptwm_mi355x_set_profiling(0, 1)
-        ms = (C.c_float * 3)()
-        kern = []
-        for _ in range(steps):
-            step()
-            L.ptwm_mi355x_last_kernel_ms(0, ms)
-            # [0]: entropy decode (fused with the merge on the huff_ilv route),
-            # [2]: every kernel of the call (exact route: decode + merge)
-            kern.append(ms[2] if wl.kernel == EXACT_ROUTE else ms[0])
-        L.ptwm_mi355x_set_profiling(0, 0)
-        kms = sum(kern) / len(kern)
-        return ms_step, kms
-
     if args.copy_calibration:
         a = torch.ones(1 << 30, dtype=torch.uint8, device="cuda:0")
         b = torch.empty_like(a)
@@ -404,30 +452,42 @@ def main():
         del a, b
         log("[bench] calibration copy: 3 x 1 GiB device-to-device")
     log(f"[bench] workload {args.workload}")
-    wl = build_workload(args.workload, args.resident)
-    ms_step, kms = measure(wl, args.steps, args.warmup)
+    _, _, opts = parse_workload(args.workload)
+    crc, hsh = "crc" in opts, "hash" in opts
+    wl = build_workload(args.workload, args.resident, integrity=bool(opts) or args.workload == "llama8b")
+    ms_step, kms = measure(wl, args.steps, args.warmup, crc, hsh)
     value = wl.restored / (ms_step * 1e-3) / 1e9
     traffic = wl.comp_bytes + wl.restored
     achieved = traffic / (kms * 1e-3) / 1e9
-    primary = {"workload": args.workload, "description": wl.name, "restored_bytes": wl.restored,
-               "compressed_bytes": wl.comp_bytes, "ratio": round(wl.comp_bytes / wl.restored, 4),
-               "encode_gbs": round(wl.encode_gbs, 1), "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
-               "codec": wl.codec, "replicas": len(wl.replicas),
-               "distinct_input_bytes": sum(r.comp_bytes for r in wl.replicas)}
-    kernel_name = wl.kernel
-    log(f"[bench] {ms_step:.3f} ms/step, kernel {kms:.3f} ms, {value:.1f} GB/s restored")
+    verified = "plane CRC-32 and tensor XXH64" if hsh else "plane CRC-32" if crc else "none"
+    primary = {"workload": args.workload, "description": wl.name, "verified_in_timed_region": verified,
+               "restored_bytes": wl.restored, "compressed_bytes": wl.comp_bytes,
+               "ratio": round(wl.comp_bytes / wl.restored, 4), "encode_gbs": round(wl.encode_gbs, 1),
+               "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4), "codec": wl.codec,
+               "replicas": len(wl.replicas), "distinct_input_bytes": sum(r.comp_bytes for r in wl.replicas)}
+    kernel_name = kernel_label(wl, crc)
+    log(f"[bench] {ms_step:.3f} ms/step, kernel {kms:.3f} ms, {value:.1f} GB/s restored ({verified} verified)")
     extras = {}
+    base = args.workload.split("+")[0]
+    if wl.plans and wl.plans[0].xxh64 is not None:
+        # the same compressed bytes: without any verification, and with the
+        # tensor XXH64 as well (reported in its own field)
+        if crc or hsh:
+            m2, k2 = measure(wl, args.steps, 1)
+            extras[base] = secondary_line(wl, m2, k2)
+            log(f"[bench] {base} without verification: {m2:.3f} ms/step")
+        if not hsh:
+            m3, k3 = measure(wl, 3, 1, True, True)
+            primary["hash_verified"] = secondary_line(wl, m3, k3, True, True)
+            log(f"[bench] {base} with CRC-32 + XXH64: {m3:.3f} ms/step")
     for name in [x for x in args.extra.split(",") if x and x != args.workload]:
         del wl
         gc.collect()
         torch.cuda.empty_cache()
-        wl = build_workload(name, args.resident)
-        m2, k2 = measure(wl, max(3, args.steps), 1)
-        extras[name] = {"restored_gbs": round(wl.restored / (m2 * 1e-3) / 1e9, 1),
-                        "kernel_gbs_restored": round(wl.restored / (k2 * 1e-3) / 1e9, 1),
-                        "kernel_gbs_traffic": round((wl.restored + wl.comp_bytes) / (k2 * 1e-3) / 1e9, 1),
-                        "ratio": round(wl.comp_bytes / wl.restored, 4), "encode_gbs": round(wl.encode_gbs, 1),
-                        "replicas": len(wl.replicas), "description": wl.name}
+        slow = name == "c3_rans"   # four serial rANS chains per 64 MiB plane: seconds per step
+        wl = build_workload(name, args.resident or slow)
+        m2, k2 = measure(wl, 1 if slow else max(3, args.steps), 0 if slow else 1)
+        extras[name] = secondary_line(wl, m2, k2)
     primary["secondary"] = extras
     traffic_meas, traffic_src = measured_traffic(args.workload)
     ceil = hbm_ceilings()
@@ -491,32 +551,46 @@ def hbm_ceilings():
 
 
 def cpu_baseline():
-    """The oracle (C restatement of the reference CPU path) decoding a bounded
+    """The oracle's C restatement of the reference CPU decode on a bounded
     sample of config 4: bf16 N(0,0.02) tensors split into two planes, each
-    plane Huffman-coded in 1 MiB chunks (reference framing), then decoded
-    across threads and merged (fused inverse), timed on this host."""
-    import numpy as np
+    plane Huffman-coded in 256 KiB chunks (the reference's default
+    compression_chunk, _config.py:151) with its chunk frames; the whole set
+    decoded as the container does it (container.rs:1766-2050: tensors over
+    worker threads, each tensor's planes chunk by chunk, then the fused
+    inverse chain), timed on this host at `nproc` (at most 16) threads and at
+    one thread."""
+    import concurrent.futures as cf
+
     import torch
 
     import oracle as O
 
     threads = min(16, os.cpu_count() or 1)
+    n_tensors = 2 * threads
     g = torch.Generator().manual_seed(7)
-    w = (torch.randn(4096 * 4096, generator=g) * 0.02).to(torch.bfloat16).view(torch.uint8).numpy().tobytes()
-    p0, p1 = O.chain_forward(O.CHAIN_IEEE16_SPLIT2, w)
-    enc = [O.encode_plane_chunked(O.CODEC_HUFFMAN, p, 1 << 20) for p in (p0, p1)]
+    raws = [(torch.randn(4096 * 4096, generator=g) * 0.02).to(torch.bfloat16).view(torch.uint8).numpy().tobytes()
+            for _ in range(n_tensors)]
+
+    def enc(w):
+        return (len(w), [O.encode_plane_chunked(O.CODEC_HUFFMAN, p, 256 << 10)
+                         for p in O.chain_forward(O.CHAIN_IEEE16_SPLIT2, w)])
+
+    with cf.ThreadPoolExecutor(threads) as ex:   # the oracle's C calls release the GIL
+        batch = O.TensorBatch(O.CODEC_HUFFMAN, O.CHAIN_IEEE16_SPLIT2, list(ex.map(enc, raws)))
+    comp = sum(len(pay) for _, planes in [enc(raws[0])] for pay, _ in planes)
+    batch.decode(threads)
+    assert all(batch.output(i) == raws[i] for i in range(n_tensors)), "CPU baseline round trip"
+
     def rate(nthreads, seconds):
         t0 = time.perf_counter()
         reps = 0
         while True:
-            planes = [O.decode_plane_chunked(O.CODEC_HUFFMAN, pay, ent, threads=nthreads) for pay, ent in enc]
-            out = O.chain_inverse(O.CHAIN_IEEE16_SPLIT2, planes)
+            batch.decode(nthreads)
             reps += 1
             if time.perf_counter() - t0 > seconds:
                 break
         dt = time.perf_counter() - t0
-        assert out == w
-        return len(w) * reps / dt / 1e9, reps
+        return sum(len(w) for w in raws) * reps / dt / 1e9, reps
 
     value, reps = rate(threads, 10.0)
     one, reps1 = rate(1, 4.0)
@@ -529,11 +603,12 @@ def cpu_baseline():
                     break
     except OSError:
         pass
-    del np
     return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "value_1_thread": round(one, 3), "cpu_model": model, "nproc": os.cpu_count(),
-            "sample": f"{reps} x 32 MiB bf16 4096x4096 N(0,0.02) at {threads} threads ({reps1} at 1 thread): "
-                      "Huffman planes in 1 MiB chunks, decode over threads + fused inverse (oracle C restatement)"}
+            "sample": f"{reps} passes over {n_tensors} x 32 MiB bf16 4096x4096 N(0,0.02) tensors at {threads} "
+                      f"threads ({reps1} passes at 1 thread), Huffman planes in 256 KiB chunks (ratio "
+                      f"{comp / len(raws[0]):.3f}); tensors over threads, chunks, fused inverse; oracle C "
+                      "restatement, no CRC / XXH64"}
 
 
 if __name__ == "__main__":

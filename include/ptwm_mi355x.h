@@ -95,6 +95,7 @@ int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_versi
 /* 2. Library additions (no counterpart in the reference)                 */
 /* ===================================================================== */
 
+
 /* ABI revision of this library (bumped on any incompatible change). */
 uint32_t ptwm_mi355x_abi_version(void);
 
@@ -150,6 +151,12 @@ int64_t ptwm_mi355x_encode_tensors_cuda(uint32_t family, uint32_t n_tensors, con
                                         size_t out_cap, uint8_t *plan_out, size_t plan_cap, size_t *plan_len_out,
                                         uint64_t *needed_out, uint32_t device_ordinal);
 
+/* Input bytes per batch of ptwm_mi355x_encode_tensors_cuda on the device
+ * (0 = the default, 4 GiB): the size of its plane scratch.  A smaller value
+ * bounds the scratch memory (more, smaller batches).  Library addition, no
+ * reference counterpart.  Returns 0. */
+int64_t ptwm_mi355x_set_encode_batch_bytes(uint64_t bytes, uint32_t device_ordinal);
+
 /* Tensor-level encode into the reference's own plane formats: the tensor is
  * split by `chain`, and plane p is coded with plane_codecs[p] (wire id 0x0000
  * Identity, 0x0001 Huffman, 0x0003 rANS), in chunks of chunk_size bytes with
@@ -175,7 +182,9 @@ int64_t ptwm_mi355x_plane_crc32_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t
 
 /* XXH64 with seed 0 of in_len device bytes (any alignment): the tensor
  * payload hash of container.rs:2185-2194 and compact.rs:441-445.  Serial per
- * buffer by the hash's definition.  Returns 0. */
+ * buffer by the hash's definition, so it runs on host cores: the bytes are
+ * copied to pinned host memory in chunks, after the work queued on the
+ * call's stream.  Returns 0. */
 int64_t ptwm_mi355x_xxh64_cuda(uint64_t in_dev_ptr, size_t in_len, uint64_t *hash_out, uint32_t device_ordinal);
 
 /* Canonical Huffman code lengths the reference encoder assigns to a 256-bin

@@ -78,6 +78,8 @@ def lib():
         L.por_decode_plane_chunked.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz]
         L.por_decode_plane_chunked_mt.restype = i64
         L.por_decode_plane_chunked_mt.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz, C.c_int]
+        L.por_decode_tensors_mt.restype = i64
+        L.por_decode_tensors_mt.argtypes = [C.c_int, C.c_int, sz, vp, vp, vp, vp, vp, vp, C.c_int]
         L.por_huf_lengths_from_freqs.restype = C.c_int
         L.por_huf_lengths_from_freqs.argtypes = [vp, vp]
         L.por_huf_lengths_limited.restype = C.c_int
@@ -231,6 +233,51 @@ def decode_plane_chunked(codec: int, payload, entries, threads: int = 1) -> byte
     if r < 0:
         raise OracleError(r, "decode_plane_chunked")
     return out[:total].tobytes()
+
+
+class TensorBatch:
+    """Chunked plane payloads of several tensors of one chain and codec,
+    decoded together by por_decode_tensors_mt (tensors over threads, chunks,
+    fused inverse): the whole-container decode of container.rs:1766-2050."""
+
+    def __init__(self, codec: int, chain: int, tensors):
+        """tensors: iterable of (out_len, [(payload, entries) per plane])."""
+        self.codec, self.chain = codec, chain
+        np_ = lib().por_chain_nplanes(chain)
+        self._keep = []
+        pays, plens, ents, nents, outs, olens = [], [], [], [], [], []
+        for out_len, planes in tensors:
+            assert len(planes) == np_
+            for pay, ent in planes:
+                p = _buf(pay)
+                e = np.ascontiguousarray(ent, dtype=np.uint32)
+                self._keep += [p, e]
+                pays.append(p.ctypes.data)
+                plens.append(p.size)
+                ents.append(e.ctypes.data)
+                nents.append(e.shape[0])
+            o = np.zeros(max(out_len, 1), np.uint8)
+            self._keep.append(o)
+            outs.append(o)
+            olens.append(out_len)
+        self.outs = outs
+        self.out_lens = olens
+        self.n = len(olens)
+        self._pays = (C.c_void_p * len(pays))(*pays)
+        self._plens = (C.c_size_t * len(plens))(*plens)
+        self._ents = (C.c_void_p * len(ents))(*ents)
+        self._nents = (C.c_size_t * len(nents))(*nents)
+        self._outs = (C.c_void_p * self.n)(*[o.ctypes.data for o in outs])
+        self._olens = (C.c_size_t * self.n)(*olens)
+
+    def decode(self, threads: int) -> None:
+        r = lib().por_decode_tensors_mt(self.codec, self.chain, self.n, self._pays, self._plens, self._ents,
+                                        self._nents, self._outs, self._olens, threads)
+        if r < 0:
+            raise OracleError(r, "decode_tensors_mt")
+
+    def output(self, i: int) -> bytes:
+        return self.outs[i][: self.out_lens[i]].tobytes()
 
 
 # ---- chains (transforms/fusion.rs) ----

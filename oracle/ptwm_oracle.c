@@ -895,6 +895,68 @@ int64_t por_decode_plane_chunked_mt(int codec, const uint8_t *payload, size_t pa
     return job.err ? job.err : (int64_t)total;
 }
 
+/* Whole-container decode, the timed CPU baseline: tensors in parallel over
+ * `threads` pthreads (container.rs:1766-1780 runs the per-tensor decode over
+ * rayon workers), each tensor's planes chunk by chunk (container.rs:
+ * 1975-2050) into per-worker plane buffers, then the fused inverse chain
+ * into the tensor's output (fusion.rs inverse, via por_chain_inverse).
+ * Tensor t has planes np = por_chain_nplanes(chain); plane p of tensor t is
+ * payloads[t * np + p] (payload_lens, entries, n_entries likewise), plane
+ * length out_lens[t] / ratio.  Returns 0 or the first error. */
+typedef struct {
+    int codec, chain, np; size_t n;
+    const uint8_t *const *payloads; const size_t *payload_lens;
+    const uint32_t *const *entries; const size_t *n_entries;
+    uint8_t *const *outs; const size_t *out_lens;
+    size_t next, max_plane; pthread_mutex_t *mu; int64_t err;
+} mtt_job_t;
+
+static void *mtt_worker(void *arg) {
+    mtt_job_t *j = (mtt_job_t *)arg;
+    uint8_t *buf[4] = {0, 0, 0, 0};
+    for (int p = 0; p < j->np; p++) buf[p] = (uint8_t *)malloc(j->max_plane ? j->max_plane : 1);
+    for (;;) {
+        pthread_mutex_lock(j->mu);
+        size_t t = j->next++;
+        pthread_mutex_unlock(j->mu);
+        if (t >= j->n) break;
+        int64_t plane_len = por_chain_plane_len(j->chain, j->out_lens[t]);
+        int64_t r = plane_len < 0 ? POR_EINVAL : 0;
+        for (int p = 0; p < j->np && r >= 0; p++) {
+            size_t k = t * (size_t)j->np + (size_t)p;
+            r = por_decode_plane_chunked(j->codec, j->payloads[k], j->payload_lens[k], j->entries[k],
+                                         j->n_entries[k], buf[p], (size_t)plane_len);
+            if (r >= 0 && r != plane_len) r = POR_EINVAL;
+        }
+        if (r >= 0) r = por_chain_inverse(j->chain, (const uint8_t *const *)buf, (size_t)plane_len, j->outs[t]);
+        if (r < 0) { pthread_mutex_lock(j->mu); j->err = r; pthread_mutex_unlock(j->mu); }
+    }
+    for (int p = 0; p < j->np; p++) free(buf[p]);
+    return NULL;
+}
+
+int64_t por_decode_tensors_mt(int codec, int chain, size_t n_tensors, const uint8_t *const *payloads,
+                              const size_t *payload_lens, const uint32_t *const *entries, const size_t *n_entries,
+                              uint8_t *const *outs, const size_t *out_lens, int threads) {
+    int np = por_chain_nplanes(chain);
+    if (np <= 0 || np > 4) return POR_EINVAL;
+    size_t max_plane = 0;
+    for (size_t t = 0; t < n_tensors; t++) {
+        int64_t pl = por_chain_plane_len(chain, out_lens[t]);
+        if (pl < 0) return POR_EINVAL;
+        if ((size_t)pl > max_plane) max_plane = (size_t)pl;
+    }
+    if (threads < 1) threads = 1;
+    pthread_mutex_t mu = PTHREAD_MUTEX_INITIALIZER;
+    mtt_job_t job = {codec, chain, np, n_tensors, payloads, payload_lens, entries, n_entries,
+                     outs, out_lens, 0, max_plane, &mu, 0};
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
+    for (int t = 0; t < threads; t++) pthread_create(&th[t], NULL, mtt_worker, &job);
+    for (int t = 0; t < threads; t++) pthread_join(th[t], NULL);
+    free(th);
+    return job.err;
+}
+
 /* ------------------------------------------------------------------------- */
 /* huff_ilv (this build's own codec; executable specification)               */
 /*                                                                           */

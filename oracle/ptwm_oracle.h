@@ -131,6 +131,12 @@ int64_t por_decode_plane_chunked_mt(int codec, const uint8_t *payload, size_t pa
                                     const uint32_t *entries, size_t n_chunks, uint8_t *out,
                                     size_t cap, int threads);
 
+/* whole-container CPU decode (tensors over threads, chunks, fused inverse):
+ * the timed CPU baseline; layout of the arrays above its definition */
+int64_t por_decode_tensors_mt(int codec, int chain, size_t n_tensors, const uint8_t *const *payloads,
+                              const size_t *payload_lens, const uint32_t *const *entries, const size_t *n_entries,
+                              uint8_t *const *outs, const size_t *out_lens, int threads);
+
 /* ---- huff_ilv: this build's GPU-native plane codec (no reference
  * counterpart; its wire format is specified by these two functions).  Code
  * lengths, canonical codes and the weights header are the reference

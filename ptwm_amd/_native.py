@@ -64,6 +64,7 @@ _SIGS = {
     "ptwm_mi355x_huffman_code_lengths": (C.c_int64, [_u8p, _u8p]),
     "ptwm_mi355x_stream_wait": (C.c_int64, [C.c_uint64, C.c_uint32]),
     "ptwm_mi355x_use_stream": (C.c_int64, [C.c_uint64, C.c_uint32, C.c_uint32]),
+    "ptwm_mi355x_set_encode_batch_bytes": (C.c_int64, [C.c_uint64, C.c_uint32]),
     "ptwm_mi355x_set_profiling": (C.c_int64, [C.c_uint32, C.c_uint32]),
     "ptwm_mi355x_last_kernel_ms": (C.c_int64, [C.c_uint32, C.POINTER(C.c_float)]),
     "ptwm_mi355x_split_cuda": (

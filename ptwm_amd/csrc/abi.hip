@@ -165,9 +165,12 @@ int64_t ilv_decode_payload(DevCtx& ctx, uint64_t in_dev, size_t in_len, uint64_t
     PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
     return (int64_t)expected;
   }
-  if (out_dev & 15u) return kInvalidInput;
+  // the fused kernel stores 16-byte pieces: an output that is not 16-byte
+  // aligned is decoded into aligned staging and copied
+  const bool realign = (out_dev & 15u) != 0;
+  if (realign) PTWM_HIP_TRY(ctx.stage_out.ensure(expected + 64));
   IlvTensor X{};
-  X.out = out_dev;
+  X.out = realign ? reinterpret_cast<uint64_t>(ctx.stage_out.ptr) : out_dev;
   X.n = expected;
   X.chain = kChainPassthrough;
   X.n_planes = 1;
@@ -177,11 +180,40 @@ int64_t ilv_decode_payload(DevCtx& ctx, uint64_t in_dev, size_t in_len, uint64_t
   X.family = family;
   X.crc_first = kIlvNoCrc;
   int64_t rc = ilv_decode_tensors(ctx, std::vector<IlvTensor>{X});
-  return rc == kOk ? (int64_t)expected : rc;
+  if (rc != kOk) return rc;
+  if (realign) {
+    PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(out_dev), ctx.stage_out.ptr, expected,
+                                hipMemcpyDeviceToDevice, ctx.stream));
+    PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+  }
+  return (int64_t)expected;
 }
 
 // Host-buffer entry points stage through device memory on device 0.
 constexpr uint32_t kHostDevice = 0;
+
+
+// The tensor-level decode's argument checks: the decode-plan id, the plan
+// itself (parse_plan) and tensors that do not overlap in the output.
+// *total: the restored bytes.
+int64_t accept_plan(const uint8_t* state_ptr, size_t state_len, const uint8_t* codec_id_ptr, size_t codec_id_len,
+                    uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr, size_t out_len, Plan& plan,
+                    uint64_t* total) {
+  if (!codec_id_ptr || codec_id_len != 32 || !hex_eq(kPlanIdHex, codec_id_ptr)) return kUnsupported;
+  int64_t rc = parse_plan(state_ptr, state_len, in_len, out_len, plan);
+  if (rc != kOk) return rc;
+  std::vector<std::pair<uint64_t, uint64_t>> spans;
+  *total = 0;
+  for (const PlanTensor& t : plan.tensors) {
+    spans.emplace_back(t.out_offset, t.out_len);
+    *total += t.out_len;
+  }
+  std::sort(spans.begin(), spans.end());
+  for (size_t i = 1; i < spans.size(); ++i)
+    if (spans[i - 1].first + spans[i - 1].second > spans[i].first) return kInvalidInput;
+  if (*total && (!in_dev_ptr || !out_dev_ptr)) return kInvalidInput;
+  return kOk;
+}
 
 }  // namespace
 }  // namespace ptwm
@@ -287,21 +319,11 @@ int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_versi
                                                       uint64_t out_dev_ptr, size_t out_len,
                                                       uint32_t device_ordinal) {
   (void)state_format_version;
-  if (!codec_id_ptr || codec_id_len != 32 || !hex_eq(kPlanIdHex, codec_id_ptr)) return kUnsupported;
   Plan plan;
-  int64_t rc = parse_plan(state_ptr, state_len, in_len, out_len, plan);
-  if (rc != kOk) return rc;
-  // tensors must not overlap in the output
-  std::vector<std::pair<uint64_t, uint64_t>> spans;
   uint64_t total = 0;
-  for (const PlanTensor& t : plan.tensors) {
-    spans.emplace_back(t.out_offset, t.out_len);
-    total += t.out_len;
-  }
-  std::sort(spans.begin(), spans.end());
-  for (size_t i = 1; i < spans.size(); ++i)
-    if (spans[i - 1].first + spans[i - 1].second > spans[i].first) return kInvalidInput;
-  if (total && (!in_dev_ptr || !out_dev_ptr)) return kInvalidInput;
+  int64_t rc = accept_plan(state_ptr, state_len, codec_id_ptr, codec_id_len, in_dev_ptr, in_len, out_dev_ptr,
+                           out_len, plan, &total);
+  if (rc != kOk) return rc;
   DeviceScope ds(device_ordinal);
   if (!ds.ok) return kInvalidInput;
   rc = execute_plan(*ds.ctx, plan, in_dev_ptr, out_dev_ptr);
@@ -492,7 +514,7 @@ int64_t ptwm_mi355x_encode_tensors_cuda(uint32_t family, uint32_t n_tensors, con
   // tensor): forward chains of the batch into plane scratch, then every
   // plane of the batch through one encoder pass (one histogram, size and
   // encode launch each), payloads appended at 256-byte aligned offsets.
-  constexpr uint64_t kBatchBytes = 4ull << 30;
+  const uint64_t kBatchBytes = ctx.enc_batch_bytes;
   std::vector<IlvEncResult> res;     // per plane, offsets relative to out_dev_ptr
   uint64_t out_used = 0, needed_total = 0;
   bool too_small = false;
@@ -503,6 +525,16 @@ int64_t ptwm_mi355x_encode_tensors_cuda(uint32_t family, uint32_t n_tensors, con
       const uint64_t pl = in_lens[b1] / (uint64_t)chain_ratio(chains[b1]);
       scratch += (uint64_t)chain_planes(chains[b1]) * ((pl + 255) / 256 * 256);
       ++b1;
+    }
+    if (too_small) {
+      // the output ran out in an earlier batch: only a size bound is
+      // needed, and the stored size (n + 1) bounds every payload form
+      for (uint32_t i = b0; i < b1; ++i) {
+        const uint64_t pl = in_lens[i] / (uint64_t)chain_ratio(chains[i]);
+        for (int k = 0; k < chain_planes(chains[i]); ++k) needed_total = (needed_total + 255) / 256 * 256 + pl + 1;
+      }
+      b0 = b1;
+      continue;
     }
     PTWM_HIP_TRY(ctx.enc_split.ensure(scratch + 256));
     std::vector<uint64_t> srcs, lens;
@@ -525,24 +557,16 @@ int64_t ptwm_mi355x_encode_tensors_cuda(uint32_t family, uint32_t n_tensors, con
     uint64_t needed = 0;
     const uint64_t base = (out_used + 255) / 256 * 256;
     const uint64_t cap = out_cap > base ? out_cap - base : 0;
-    int64_t rc = too_small ? kBufferTooSmall
-                 : family == kFamilyHuff
+    int64_t rc = family == kFamilyHuff
                      ? ilv_encode_planes(ctx, srcs.data(), lens.data(), (uint32_t)srcs.size(), out_dev_ptr + base, cap,
                                          true, r.data(), &needed)
                      : rilv_encode_planes(ctx, srcs.data(), lens.data(), (uint32_t)srcs.size(), out_dev_ptr + base,
                                           cap, true, r.data(), &needed);
     if (rc == kBufferTooSmall) {
-      // keep sizing the remaining batches for *needed_out
-      if (!too_small) {
-        too_small = true;
-        needed_total = base;
-      }
-      if (needed == 0) {
-        // sizes of this batch are unknown once the buffer ran out: the
-        // stored size bounds every payload
-        for (uint64_t l : lens) needed = (needed + 255) / 256 * 256 + l + 1;
-      }
-      needed_total = (needed_total + 255) / 256 * 256 + needed;
+      // this batch's exact size (the encoder sized it); later batches are
+      // only bounded (above)
+      too_small = true;
+      needed_total = base + needed;
     } else if (rc < 0) {
       return rc;
     } else {
@@ -736,18 +760,17 @@ int64_t ptwm_mi355x_xxh64_cuda(uint64_t in_dev_ptr, size_t in_len, uint64_t* has
   if (!hash_out || (in_len && !in_dev_ptr)) return kInvalidInput;
   DeviceScope ds(device_ordinal);
   if (!ds.ok) return kInvalidInput;
-  DevCtx& ctx = *ds.ctx;
-  uint64_t src = in_dev_ptr;
-  if (in_len && (src & 15u)) {
-    PTWM_HIP_TRY(ctx.stage_in.ensure(in_len + 16));
-    PTWM_HIP_TRY(hipMemcpyAsync(ctx.stage_in.ptr, reinterpret_cast<const void*>(src), in_len,
-                                hipMemcpyDeviceToDevice, ctx.stream));
-    src = reinterpret_cast<uint64_t>(ctx.stage_in.ptr);
-  }
   std::vector<uint64_t> h;
-  const int64_t rc = xxh64_buffers(ctx, {HashTask{src, in_len}}, h);
+  const int64_t rc = xxh64_buffers(*ds.ctx, {HashTask{in_dev_ptr, in_len}}, h);
   if (rc != kOk) return rc;
   *hash_out = h[0];
+  return 0;
+}
+
+int64_t ptwm_mi355x_set_encode_batch_bytes(uint64_t bytes, uint32_t device_ordinal) {
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  ds.ctx->enc_batch_bytes = bytes ? bytes : kDefaultEncBatchBytes;
   return 0;
 }
 

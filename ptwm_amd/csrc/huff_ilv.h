@@ -13,6 +13,7 @@ constexpr uint32_t kIlvRounds = kIlvBlock / (kIlvLanes * kIlvGroup);  // 16
 constexpr uint32_t kIlvBlocksPerTile = 4;   // blocks per tile (one per wavefront)
 constexpr uint32_t kIlvStageSpare = 96;     // spare LDS words after the staging area
 constexpr uint32_t kIlvMaxLds = 81920;      // LDS budget of one decode workgroup (2 per CU)
+constexpr uint32_t kMaxGridY = 65535;       // launches with one plane or job per gridDim.y slot are sliced
 
 // status bits (per tensor)
 constexpr uint32_t kIlvErrHeader = 1;   // tag / length / weights / table bounds

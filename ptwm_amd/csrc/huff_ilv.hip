@@ -1111,7 +1111,11 @@ hipError_t launch_ilv_store(const IlvStoreJob* jobs, uint32_t n_jobs, uint64_t m
   if (!n_jobs) return hipSuccess;
   uint64_t blocks = (max_n / 16 + 256) / 256;
   if (blocks > 1024) blocks = 1024;
-  hipLaunchKernelGGL(ilv_store_kernel, dim3((uint32_t)blocks, n_jobs), dim3(256), 0, stream, jobs);
+  // gridDim.y is at most 65535: slices of jobs
+  for (uint32_t j0 = 0; j0 < n_jobs; j0 += kMaxGridY) {
+    const uint32_t cnt = n_jobs - j0 < kMaxGridY ? n_jobs - j0 : kMaxGridY;
+    hipLaunchKernelGGL(ilv_store_kernel, dim3((uint32_t)blocks, cnt), dim3(256), 0, stream, jobs + j0);
+  }
   return hipGetLastError();
 }
 
@@ -1119,7 +1123,10 @@ hipError_t launch_ilv_pack(const IlvPackJob* jobs, uint32_t n_jobs, uint64_t max
   if (!n_jobs) return hipSuccess;
   uint64_t blocks = (max_n / 16 + 256) / 256;
   if (blocks > 1024) blocks = 1024;
-  hipLaunchKernelGGL(ilv_pack_kernel, dim3((uint32_t)blocks, n_jobs), dim3(256), 0, stream, jobs);
+  for (uint32_t j0 = 0; j0 < n_jobs; j0 += kMaxGridY) {
+    const uint32_t cnt = n_jobs - j0 < kMaxGridY ? n_jobs - j0 : kMaxGridY;
+    hipLaunchKernelGGL(ilv_pack_kernel, dim3((uint32_t)blocks, cnt), dim3(256), 0, stream, jobs + j0);
+  }
   return hipGetLastError();
 }
 
@@ -1129,7 +1136,11 @@ hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_
   uint64_t blocks = (max_n / 16 + 255) / 256;
   if (blocks > 512) blocks = 512;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(ilv_hist_kernel, dim3((uint32_t)blocks, n_planes), dim3(256), 0, stream, planes, hist);
+  for (uint32_t p0 = 0; p0 < n_planes; p0 += kMaxGridY) {
+    const uint32_t cnt = n_planes - p0 < kMaxGridY ? n_planes - p0 : kMaxGridY;
+    hipLaunchKernelGGL(ilv_hist_kernel, dim3((uint32_t)blocks, cnt), dim3(256), 0, stream, planes + p0,
+                       hist + 256ull * p0);
+  }
   return hipGetLastError();
 }
 

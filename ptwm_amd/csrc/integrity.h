@@ -1,4 +1,5 @@
-// integrity.h -- CRC-32 of decoded planes and XXH64 of restored tensors on the GPU.
+// integrity.h -- CRC-32 of decoded planes (GPU) and XXH64 of restored
+// tensors (host cores, fed by device-to-host copies).
 #pragma once
 
 #include <vector>
@@ -26,9 +27,20 @@ struct CrcTask {
   uint32_t chain;
 };
 
-struct HashTask {  // XXH64 (seed 0) of n bytes at src (16-byte aligned)
+struct HashTask {  // XXH64 (seed 0) of n device bytes at src (any alignment)
   uint64_t src;
   uint64_t n;
+};
+
+// Streaming XXH64 with seed 0 (hash_host.hip).
+struct Xxh64 {
+  uint64_t v[4];
+  uint64_t total;
+  uint8_t buf[32];
+  uint32_t buf_len;
+  void reset();
+  void update(const uint8_t* p, size_t n);
+  uint64_t digest() const;
 };
 
 bool crc_chain_supported(uint32_t chain);
@@ -63,7 +75,9 @@ struct FusedCrc {
 // block partials combined.  Blocks until done.
 int64_t crc32_fused(DevCtx& ctx, const std::vector<FusedCrc>& tensors, uint32_t* d_part, std::vector<uint32_t>& crcs);
 
-// XXH64 with seed 0 of every task's bytes.  Blocks until done.
+// XXH64 with seed 0 of every task's bytes, after the work queued on
+// ctx.stream: the buffers are copied to pinned host memory in chunks by up to
+// kHashWorkers threads and hashed there.  Blocks until done.
 int64_t xxh64_buffers(DevCtx& ctx, const std::vector<HashTask>& tasks, std::vector<uint64_t>& hashes);
 
 }  // namespace ptwm

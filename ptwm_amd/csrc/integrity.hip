@@ -184,85 +184,6 @@ __global__ void __launch_bounds__(256) crc_combine_kernel(const CrcPlane* __rest
   if (t == 0) crc_out[blockIdx.x] = ~(gf2_mulmod(0xFFFFFFFFu, xpow8(B.n, X)) ^ acc);
 }
 
-// ---- XXH64 (seed 0) of restored tensors ----
-// xxhash-rust 0.8.18 xxh64 (container.rs:2185-2194, compact.rs:441-445),
-// from the published XXH64 specification.  The four accumulators of one
-// buffer are serial chains over its 32-byte stripes; lanes 0-3 of one
-// wavefront carry them, the whole wavefront loads 64 stripes at a time and
-// precomputes the input * PRIME64_2 products off the serial path.
-constexpr uint64_t kXP1 = 0x9E3779B185EBCA87ull, kXP2 = 0xC2B2AE3D27D4EB4Full, kXP3 = 0x165667B19E3779F9ull,
-                   kXP4 = 0x85EBCA77C2B2AE63ull, kXP5 = 0x27D4EB2F165667C5ull;
-
-__device__ __forceinline__ uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
-__device__ __forceinline__ uint64_t xx_round(uint64_t acc, uint64_t in) { return rotl64(acc + in * kXP2, 31) * kXP1; }
-__device__ __forceinline__ uint64_t xx_merge(uint64_t h, uint64_t v) { return (h ^ xx_round(0, v)) * kXP1 + kXP4; }
-__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int src) {
-  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, 64);
-  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, 64);
-  return (uint64_t)lo | ((uint64_t)hi << 32);
-}
-
-__global__ void __launch_bounds__(64) xxh64_kernel(const HashTask* __restrict__ tasks, uint64_t* __restrict__ out) {
-  __shared__ uint64_t prod[64][4];
-  const HashTask H = tasks[blockIdx.x];
-  const uint32_t l = threadIdx.x;
-  const uint64_t stripes = H.n / 32;
-  const u32x4* src = reinterpret_cast<const u32x4*>(H.src);
-  uint64_t v = l == 0 ? kXP1 + kXP2 : l == 1 ? kXP2 : l == 2 ? 0 : 0 - kXP1;
-  u32x4 a = u32x4_make(0, 0, 0, 0), b = a;
-  if (l < stripes) {
-    a = g_ld_nt16(reinterpret_cast<uint64_t>(src + 2 * l));
-    b = g_ld_nt16(reinterpret_cast<uint64_t>(src + 2 * l + 1));
-  }
-  for (uint64_t s0 = 0; s0 < stripes; s0 += 64) {
-    if (s0 + l < stripes) {
-      prod[l][0] = ((uint64_t)a.x | ((uint64_t)a.y << 32)) * kXP2;
-      prod[l][1] = ((uint64_t)a.z | ((uint64_t)a.w << 32)) * kXP2;
-      prod[l][2] = ((uint64_t)b.x | ((uint64_t)b.y << 32)) * kXP2;
-      prod[l][3] = ((uint64_t)b.z | ((uint64_t)b.w << 32)) * kXP2;
-    }
-    __syncthreads();
-    const uint64_t sn = s0 + 64 + l;  // next block, loaded while lanes 0-3 run the chains
-    if (sn < stripes) {
-      a = g_ld_nt16(reinterpret_cast<uint64_t>(src + 2 * sn));
-      b = g_ld_nt16(reinterpret_cast<uint64_t>(src + 2 * sn + 1));
-    }
-    const uint32_t cnt = (uint32_t)(stripes - s0 < 64 ? stripes - s0 : 64);
-    if (l < 4)
-      for (uint32_t k = 0; k < cnt; ++k) v = rotl64(v + prod[k][l], 31) * kXP1;
-    __syncthreads();
-  }
-  const uint64_t v1 = lane_u64(v, 0), v2 = lane_u64(v, 1), v3 = lane_u64(v, 2), v4 = lane_u64(v, 3);
-  if (l != 0) return;
-  uint64_t h;
-  if (H.n >= 32) {
-    h = rotl64(v1, 1) + rotl64(v2, 7) + rotl64(v3, 12) + rotl64(v4, 18);
-    h = xx_merge(h, v1);
-    h = xx_merge(h, v2);
-    h = xx_merge(h, v3);
-    h = xx_merge(h, v4);
-  } else {
-    h = kXP5;
-  }
-  h += H.n;
-  // the last < 32 bytes start 16-byte aligned: 8- and 4-byte loads are aligned
-  const uint8_t* p = reinterpret_cast<const uint8_t*>(H.src) + stripes * 32;
-  uint64_t rest = H.n - stripes * 32;
-  for (; rest >= 8; rest -= 8, p += 8) h = rotl64(h ^ xx_round(0, *reinterpret_cast<const uint64_t*>(p)), 27) * kXP1 + kXP4;
-  if (rest >= 4) {
-    h = rotl64(h ^ ((uint64_t)*reinterpret_cast<const uint32_t*>(p) * kXP1), 23) * kXP2 + kXP3;
-    rest -= 4;
-    p += 4;
-  }
-  for (; rest; --rest, ++p) h = rotl64(h ^ ((uint64_t)*p * kXP5), 11) * kXP1;
-  h ^= h >> 33;
-  h *= kXP2;
-  h ^= h >> 29;
-  h *= kXP3;
-  h ^= h >> 32;
-  out[blockIdx.x] = h;
-}
-
 int chain_np(uint32_t chain) { return chain == kChainIeee16Split2 ? 2 : chain == kChainIeee32Split4 ? 4 : 1; }
 
 // c: 0 = IEEE16 split2, 1 = IEEE32 split4, 2 = passthrough
@@ -434,27 +355,6 @@ int64_t crc32_planes(DevCtx& ctx, const std::vector<CrcTask>& tasks, std::vector
   }
   crcs.assign(np, 0);
   PTWM_HIP_TRY(hipMemcpyAsync(crcs.data(), d_out, np * 4, hipMemcpyDeviceToHost, s));
-  PTWM_HIP_TRY(hipStreamSynchronize(s));
-  return kOk;
-}
-
-int64_t xxh64_buffers(DevCtx& ctx, const std::vector<HashTask>& tasks, std::vector<uint64_t>& hashes) {
-  hashes.assign(tasks.size(), 0);
-  if (tasks.empty()) return kOk;
-  for (const HashTask& h : tasks)
-    if (h.n && (h.src & 15u)) return kInternal;  // callers pass 16-byte aligned buffers
-  hipStream_t s = ctx.stream;
-  const size_t n = tasks.size();
-  PTWM_HIP_TRY(ctx.hash_args.ensure(n * (sizeof(HashTask) + 8) + 64));
-  HashTask* d_tasks = static_cast<HashTask*>(ctx.hash_args.ptr);
-  uint64_t* d_out = reinterpret_cast<uint64_t*>(d_tasks + n);
-  PTWM_HIP_TRY(hipMemcpyAsync(d_tasks, tasks.data(), n * sizeof(HashTask), hipMemcpyHostToDevice, s));
-  for (size_t k0 = 0; k0 < n; k0 += 65535) {
-    const uint32_t cnt = (uint32_t)std::min<size_t>(65535, n - k0);
-    hipLaunchKernelGGL(xxh64_kernel, dim3(cnt), dim3(64), 0, s, d_tasks + k0, d_out + k0);
-    PTWM_HIP_TRY(hipGetLastError());
-  }
-  PTWM_HIP_TRY(hipMemcpyAsync(hashes.data(), d_out, n * 8, hipMemcpyDeviceToHost, s));
   PTWM_HIP_TRY(hipStreamSynchronize(s));
   return kOk;
 }

@@ -26,6 +26,20 @@ struct PinnedBuffer {
   ~PinnedBuffer();
 };
 
+// One host hashing worker (hash_host.hip): its stream, two pinned chunk
+// buffers and their copy-done events.
+constexpr uint64_t kHashChunk = 16ull << 20;
+constexpr uint32_t kHashWorkers = 8;
+struct HashWorker {
+  hipStream_t stream = nullptr;
+  void* pinned[2] = {nullptr, nullptr};
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  hipError_t init();
+};
+
+// Input bytes per batch of the batched tensor encoder (its plane scratch).
+constexpr uint64_t kDefaultEncBatchBytes = 4ull << 30;
+
 // One per device ordinal.  All entry points serialise on `mu`: the stream
 // and the scratch buffers are shared by every call on that device.
 struct DevCtx {
@@ -51,11 +65,14 @@ struct DevCtx {
   // parallel Huffman decode of reference streams
   DeviceBuffer sync_streams, sync_tables, sync_sub, sync_waves, copy_args;
   // integrity (CRC-32 / XXH64) tables and arguments
-  DeviceBuffer crc_tab, crc_args, hash_args;
+  DeviceBuffer crc_tab, crc_args;
+  std::vector<HashWorker> hash_workers;  // XXH64 on host cores (hash_host.hip)
+  hipEvent_t hash_ready = nullptr;       // the restore is complete before the copies
   bool crc_tab_ready = false;
   int cu_count = 0;  // compute units of the device (0: not queried yet)
   std::map<uint64_t, int> ilv_occupancy;  // (chain, slots, stage words) -> workgroups per CU
   DeviceBuffer stage_in, stage_out, enc_split;
+  uint64_t enc_batch_bytes = kDefaultEncBatchBytes;  // ptwm_mi355x_set_encode_batch_bytes
   // optional per-phase kernel timing with HIP events on `stream`
   bool profile = false;
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -102,6 +119,12 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
 // addresses).  Blocks until the work has completed.  Returns kOk or an
 // error code.
 int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev);
+
+// Whether the tensor is restored by the fused decode kernel (every plane an
+// unchunked GPU-native payload of one codec family or a stored Identity
+// plane, at least one coded, 16-byte aligned output, and a plane CRC only
+// for the chains the fused CRC covers).
+bool fused_eligible(const PlanTensor& T, uint64_t out_dev);
 
 // kernel launchers (transform.hip; the decode launchers are in decode_sync.h)
 hipError_t launch_merge(uint32_t chain, const uint8_t* const* planes, uint64_t plane_len, uint8_t* out,

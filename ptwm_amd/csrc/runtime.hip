@@ -197,6 +197,20 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
 
 static inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
+bool fused_eligible(const PlanTensor& T, uint64_t out_dev) {
+  bool any_huff = false, any_rans = false, ok = ((out_dev + T.out_offset) & 15u) == 0;
+  for (const PlanPlane& P : T.planes) {
+    if (P.chunked) ok = false;
+    if (P.codec == kCodecHuffIlv) any_huff = true;
+    else if (P.codec == kCodecRansIlv) any_rans = true;
+    else if (P.codec != kCodecIdentity || P.payload_len != P.plane_len) ok = false;
+  }
+  // one codec family per fused tensor; a plane CRC is checked on the
+  // restored tensor where the chain is a bijection on plane bytes (other
+  // chains keep their planes in scratch)
+  return ok && any_huff != any_rans && (!T.has_crc || crc_chain_supported(T.chain));
+}
+
 int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev) {
   // Route 1 (fused): a tensor whose planes are all unchunked Identity or
   // GPU-native payloads of one codec family (huff_ilv or rans_ilv), with at
@@ -215,18 +229,9 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   uint64_t crc_blocks = 0;
   for (size_t t = 0; t < nt; ++t) {
     const PlanTensor& T = plan.tensors[t];
-    bool any_huff = false, any_rans = false, ok = ((out_dev + T.out_offset) & 15u) == 0;
-    for (const PlanPlane& P : T.planes) {
-      if (P.chunked) ok = false;
-      if (P.codec == kCodecHuffIlv) any_huff = true;
-      else if (P.codec == kCodecRansIlv) any_rans = true;
-      else if (P.codec != kCodecIdentity || P.payload_len != P.plane_len) ok = false;
-    }
-    // one codec family per fused tensor
-    if (!ok || any_huff == any_rans) continue;
-    // a plane CRC is checked on the restored tensor where the chain is a
-    // bijection on plane bytes; other chains keep their planes in scratch
-    if (T.has_crc && !crc_chain_supported(T.chain)) continue;
+    if (!fused_eligible(T, out_dev)) continue;
+    bool any_rans = false;
+    for (const PlanPlane& P : T.planes) any_rans |= P.codec == kCodecRansIlv;
     fused[t] = 1;
     IlvTensor X{};
     X.out = out_dev + T.out_offset;
@@ -271,6 +276,15 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
       scratch_bytes = align_up(scratch_bytes + P.plane_len, 256);
       if (!native) n_jobs += P.chunked ? P.chunks.size() : 1;
     }
+  }
+  // the merge kernels store 16-byte pieces: a tensor whose output is not
+  // 16-byte aligned is merged into scratch and copied
+  std::vector<uint64_t> merge_tmp(nt, kDirect);
+  for (size_t t = 0; t < nt; ++t) {
+    const PlanTensor& T = plan.tensors[t];
+    if (fused[t] || T.out_len == 0 || ((out_dev + T.out_offset) & 15u) == 0) continue;
+    merge_tmp[t] = scratch_bytes;
+    scratch_bytes = align_up(scratch_bytes + T.out_len, 256);
   }
   if (n_jobs > 0xFFFFFFFFull) return kInvalidInput;
   PTWM_HIP_TRY(ctx.planes.ensure(scratch_bytes ? scratch_bytes : 256));
@@ -366,8 +380,13 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     for (size_t p = 0; p < T.planes.size(); ++p) pp[p] = reinterpret_cast<const uint8_t*>(plane_addr[t][p]);
     uint8_t* out = reinterpret_cast<uint8_t*>(out_dev + T.out_offset);
     if (T.planes[0].plane_len == 0) continue;
-    if ((reinterpret_cast<uintptr_t>(out) & 15u) != 0) return kInvalidInput;
-    PTWM_HIP_TRY(launch_merge(T.chain, pp, T.planes[0].plane_len, out, s));
+    if (merge_tmp[t] == kDirect) {
+      PTWM_HIP_TRY(launch_merge(T.chain, pp, T.planes[0].plane_len, out, s));
+    } else {
+      uint8_t* tmp = reinterpret_cast<uint8_t*>(scratch_base + merge_tmp[t]);
+      PTWM_HIP_TRY(launch_merge(T.chain, pp, T.planes[0].plane_len, tmp, s));
+      PTWM_HIP_TRY(hipMemcpyAsync(out, tmp, T.out_len, hipMemcpyDeviceToDevice, s));
+    }
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], s));
   PTWM_HIP_TRY(hipStreamSynchronize(s));

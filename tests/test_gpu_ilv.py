@@ -243,3 +243,35 @@ def test_stream_ordering_after_torch_producer():
         blob.copy_(host_t, non_blocking=True)
         n = api.plane_codec_decode_cuda(SEL, OWN, b"", blob, dst, 0)
         assert n == len(src) and host(dst) == src
+
+
+@pytest.mark.parametrize("codec", ["huff_ilv", "rans_ilv"])
+def test_decode_into_unaligned_output(codec):
+    """A valid payload decoded into a device slice that does not start on a
+    16-byte boundary restores the plane (the fused kernel's 16-byte stores
+    go through aligned staging), through the plane codec entry point and a
+    plan whose tensor sits at an odd output offset."""
+    rng = np.random.default_rng(23)
+    src = rng.geometric(0.3, 40_001).clip(0, 255).astype(np.uint8).tobytes()
+    payload = O.ilv_encode(src) if codec == "huff_ilv" else O.rans_ilv_encode(src)
+    cid = OWN if codec == "huff_ilv" else ids.RANS_CODEC_LABEL
+    d_in = dev(payload)
+    for shift in (1, 3, 8, 13):
+        note(f"unaligned {codec} decode, output offset {shift}")
+        buf = torch.zeros(len(src) + 64, dtype=torch.uint8, device="cuda:0")
+        n = api.plane_codec_decode_cuda(SEL, cid, b"", d_in, buf[shift: shift + len(src)], 0)
+        assert n == len(src) and host(buf)[shift: shift + n] == src
+    # tensor level: bf16 split chain, exponent plane native-coded, output at offset 5
+    w = (torch.randn(20_000, generator=torch.Generator().manual_seed(9)) * 0.02).to(torch.bfloat16)
+    data = w.view(torch.uint8).numpy().tobytes()
+    p0, p1 = O.chain_forward(O.CHAIN_IEEE16_SPLIT2, data)
+    e1 = O.ilv_encode(p1) if codec == "huff_ilv" else O.rans_ilv_encode(p1)
+    off1 = (len(p0) + 255) // 256 * 256
+    blob = p0 + b"\0" * (off1 - len(p0)) + e1
+    wire = 0x7F01 if codec == "huff_ilv" else 0x7F02
+    st = plan.encode_plan([plan.TensorPlan(plan.CHAIN_IEEE16_SPLIT2, 5, len(data), [
+        plan.PlanePlan(0, 0, len(p0), len(p0)), plan.PlanePlan(wire, off1, len(e1), len(p1))])])
+    out = torch.zeros(len(data) + 64, dtype=torch.uint8, device="cuda:0")
+    n = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, st, dev(blob),
+                                                  out, 0)
+    assert n == len(data) and host(out)[5: 5 + n] == data

@@ -117,6 +117,11 @@ TENSORS = [
     ("c5-mxfp4", plan.CHAIN_NIBBLE_SPLIT,
      lambda: torch.from_numpy(np.random.default_rng(5).integers(0, 256, 14336 * 64).astype(np.uint8)), [H, R], 1 << 20),
     ("identity-chunked", plan.CHAIN_IEEE16_SPLIT2, lambda: bf16((300, 777), 6).view(torch.uint8), [I, H], 100_000),
+    # full-size config 2 (4096 x 4096 fp32, 64 chunks of 256 KiB per plane) and config 3
+    # (8192 x 8192 e4m3, one 64 MiB payload per plane), Huffman and rANS
+    ("c2-full", plan.CHAIN_IEEE32_SPLIT4, lambda: c2_fp32(4096, 4096, 12).view(torch.uint8), [H, H, H, R], 262144),
+    ("c3-full-huf", plan.CHAIN_E4M3_NIBBLE, lambda: c3_fp8(8192, 8192, 13).view(torch.uint8), [H, H], 0),
+    ("c3-full-rans", plan.CHAIN_E4M3_NIBBLE, lambda: c3_fp8(8192, 8192, 13).view(torch.uint8), [R, R], 0),
 ]
 
 
