@@ -95,6 +95,31 @@ int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_versi
 /* 2. Library additions (no counterpart in the reference)                 */
 /* ===================================================================== */
 
+/* Allocation-free tensor-level decode.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, plan format and results as
+ * ptwm_hardware_backend_v1_dispatch_decode_cuda, for plans whose every
+ * tensor takes the fused decode: planes this library's huff_ilv or rans_ilv
+ * payloads (one codec per tensor, at least one coded plane, 4-byte aligned
+ * in the input) or unchunked Identity planes, output 16-byte aligned, plane
+ * CRC-32 only for the ieee16 / ieee32 / passthrough chains, no tensor XXH64.
+ * All device scratch (descriptors, status words, CRC tables and block
+ * partials) is one fixed array of PTWM_MI355X_NOALLOC_SCRATCH_BYTES per
+ * device, held until the process ends; it calls no hipMalloc, hipFree or
+ * hipHostMalloc.  Plans outside these limits (more than
+ * PTWM_MI355X_NOALLOC_MAX_TENSORS tensors, or more than
+ * PTWM_MI355X_NOALLOC_MAX_CRC_BLOCKS CRC-checked 16384-byte plane blocks in
+ * all) return -5 (Unsupported); -3 if the device's scratch could not be
+ * resolved.  Calls on one device are serialised by the library; the array
+ * keeps the last call's contents (every call rewrites what it reads). */
+#define PTWM_MI355X_NOALLOC_SCRATCH_BYTES (16u << 20)
+#define PTWM_MI355X_NOALLOC_MAX_TENSORS 4096u
+#define PTWM_MI355X_NOALLOC_MAX_CRC_BLOCKS 883456u
+int64_t ptwm_mi355x_dispatch_decode_noalloc_cuda(uint8_t state_format_version, const uint8_t *state_ptr,
+                                                 size_t state_len, const uint8_t *codec_id_ptr, size_t codec_id_len,
+                                                 uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                                                 size_t out_len, uint32_t device_ordinal);
 
 /* ABI revision of this library (bumped on any incompatible change). */
 uint32_t ptwm_mi355x_abi_version(void);

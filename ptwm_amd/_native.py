@@ -65,6 +65,9 @@ _SIGS = {
     "ptwm_mi355x_stream_wait": (C.c_int64, [C.c_uint64, C.c_uint32]),
     "ptwm_mi355x_use_stream": (C.c_int64, [C.c_uint64, C.c_uint32, C.c_uint32]),
     "ptwm_mi355x_set_encode_batch_bytes": (C.c_int64, [C.c_uint64, C.c_uint32]),
+    "ptwm_mi355x_dispatch_decode_noalloc_cuda": (
+        C.c_int64, [C.c_uint8, _u8p, C.c_size_t, _u8p, C.c_size_t, C.c_uint64, C.c_size_t, C.c_uint64, C.c_size_t,
+                    C.c_uint32]),
     "ptwm_mi355x_set_profiling": (C.c_int64, [C.c_uint32, C.c_uint32]),
     "ptwm_mi355x_last_kernel_ms": (C.c_int64, [C.c_uint32, C.POINTER(C.c_float)]),
     "ptwm_mi355x_split_cuda": (

@@ -192,6 +192,9 @@ int64_t ilv_decode_payload(DevCtx& ctx, uint64_t in_dev, size_t in_len, uint64_t
 // Host-buffer entry points stage through device memory on device 0.
 constexpr uint32_t kHostDevice = 0;
 
+static_assert(PTWM_MI355X_NOALLOC_SCRATCH_BYTES == kNoAllocScratchBytes, "allocation-free scratch size");
+static_assert(PTWM_MI355X_NOALLOC_MAX_TENSORS == kNoAllocMaxTensors, "allocation-free tensor limit");
+static_assert(PTWM_MI355X_NOALLOC_MAX_CRC_BLOCKS == kNoAllocMaxCrcBlocks, "allocation-free CRC block limit");
 
 // The tensor-level decode's argument checks: the decode-plan id, the plan
 // itself (parse_plan) and tensors that do not overlap in the output.
@@ -327,6 +330,22 @@ int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_versi
   DeviceScope ds(device_ordinal);
   if (!ds.ok) return kInvalidInput;
   rc = execute_plan(*ds.ctx, plan, in_dev_ptr, out_dev_ptr);
+  return rc == kOk ? (int64_t)total : rc;
+}
+
+int64_t ptwm_mi355x_dispatch_decode_noalloc_cuda(uint8_t state_format_version, const uint8_t* state_ptr,
+                                                 size_t state_len, const uint8_t* codec_id_ptr, size_t codec_id_len,
+                                                 uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                                                 size_t out_len, uint32_t device_ordinal) {
+  (void)state_format_version;
+  Plan plan;
+  uint64_t total = 0;
+  int64_t rc = accept_plan(state_ptr, state_len, codec_id_ptr, codec_id_len, in_dev_ptr, in_len, out_dev_ptr,
+                           out_len, plan, &total);
+  if (rc != kOk) return rc;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  rc = execute_plan_noalloc(*ds.ctx, plan, in_dev_ptr, out_dev_ptr);
   return rc == kOk ? (int64_t)total : rc;
 }
 

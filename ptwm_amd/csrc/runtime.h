@@ -3,6 +3,7 @@
 
 #include <cstdint>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -11,10 +12,14 @@
 
 namespace ptwm {
 
-// Grow-only device allocation reused across calls on one device.
+// Grow-only device allocation reused across calls on one device.  A
+// borrowed buffer is a view of memory owned elsewhere (the allocation-free
+// decode's fixed scratch): ensure() never allocates for it and fails when
+// the view is too small.
 struct DeviceBuffer {
   void* ptr = nullptr;
   size_t cap = 0;
+  bool borrowed = false;
   hipError_t ensure(size_t bytes);
   ~DeviceBuffer();
 };
@@ -22,9 +27,28 @@ struct DeviceBuffer {
 struct PinnedBuffer {
   void* ptr = nullptr;
   size_t cap = 0;
+  bool borrowed = false;
   hipError_t ensure(size_t bytes);
   ~PinnedBuffer();
 };
+
+// The allocation-free decode (ptwm_mi355x_dispatch_decode_noalloc_cuda):
+// all its device scratch lives in one fixed array per device (runtime.hip),
+// laid out as [CRC tables][tensor descriptors, launch indexes, status]
+// [CRC range arguments][CRC combine arguments][exact-route stubs][CRC block
+// partials], and its host staging in a fixed per-device host area.
+constexpr uint64_t kNoAllocScratchBytes = 16ull << 20;
+constexpr uint64_t kNoAllocTabOff = 0, kNoAllocTabBytes = 16ull << 10;
+constexpr uint64_t kNoAllocArgsOff = kNoAllocTabOff + kNoAllocTabBytes, kNoAllocArgsBytes = 1ull << 20;
+constexpr uint64_t kNoAllocCrcArgsOff = kNoAllocArgsOff + kNoAllocArgsBytes, kNoAllocCrcArgsBytes = 1ull << 20;
+constexpr uint64_t kNoAllocCombOff = kNoAllocCrcArgsOff + kNoAllocCrcArgsBytes, kNoAllocCombBytes = 512ull << 10;
+constexpr uint64_t kNoAllocStubOff = kNoAllocCombOff + kNoAllocCombBytes, kNoAllocStubBytes = 4096;
+constexpr uint64_t kNoAllocPartOff = kNoAllocStubOff + kNoAllocStubBytes;
+constexpr uint64_t kNoAllocPartBytes = kNoAllocScratchBytes - kNoAllocPartOff;
+constexpr uint64_t kNoAllocHostBytes = 1ull << 20;
+// limits of a plan the allocation-free decode accepts
+constexpr uint32_t kNoAllocMaxTensors = 4096;
+constexpr uint64_t kNoAllocMaxCrcBlocks = kNoAllocPartBytes / 16;
 
 // One host hashing worker (hash_host.hip): its stream, two pinned chunk
 // buffers and their copy-done events.
@@ -79,6 +103,13 @@ struct DevCtx {
   hipEvent_t order_ev = nullptr;  // producer-stream ordering (ptwm_mi355x_stream_wait)
   float last_ms[3] = {0, 0, 0};  // entropy decode, merge, whole call
   hipError_t ensure_events();
+  // allocation-free decode: this device's copy of the fixed scratch array
+  // (its device address, resolved once at set-up; null if that failed), the
+  // host staging area (allocated at set-up) and whether the CRC tables are
+  // in the scratch yet
+  uint8_t* noalloc_dev = nullptr;
+  std::unique_ptr<uint8_t[]> noalloc_host;
+  bool noalloc_tab_ready = false;
 };
 
 // Returns nullptr if the ordinal is invalid or HIP initialisation fails.
@@ -119,6 +150,13 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
 // addresses).  Blocks until the work has completed.  Returns kOk or an
 // error code.
 int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev);
+
+// The same without allocating device or pinned memory: every tensor must
+// take the fused route (fused_eligible), carry no XXH64, have 4-byte aligned
+// coded payloads and fit the fixed scratch (kNoAllocMaxTensors,
+// kNoAllocMaxCrcBlocks); kUnsupported otherwise, kMissingCapability when the
+// device's scratch address could not be resolved.
+int64_t execute_plan_noalloc(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev);
 
 // Whether the tensor is restored by the fused decode kernel (every plane an
 // unchunked GPU-native payload of one codec family or a stored Identity

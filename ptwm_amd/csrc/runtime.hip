@@ -22,6 +22,7 @@ namespace ptwm {
 
 hipError_t DeviceBuffer::ensure(size_t bytes) {
   if (bytes <= cap && ptr) return hipSuccess;
+  if (borrowed) return hipErrorOutOfMemory;
   if (ptr) {
     (void)hipFree(ptr);
     ptr = nullptr;
@@ -36,6 +37,7 @@ DeviceBuffer::~DeviceBuffer() {}
 
 hipError_t PinnedBuffer::ensure(size_t bytes) {
   if (bytes <= cap && ptr) return hipSuccess;
+  if (borrowed) return hipErrorOutOfMemory;
   if (ptr) {
     (void)hipHostFree(ptr);
     ptr = nullptr;
@@ -60,6 +62,13 @@ hipError_t DevCtx::ensure_events() {
 namespace {
 std::mutex g_ctx_mu;
 std::array<std::unique_ptr<DevCtx>, 64> g_ctx;
+
+// Device scratch of the allocation-free decode: one copy per device (the
+// code object's data segment), held until the process ends.  Host code
+// never passes this name to a kernel or copy: get_ctx resolves each
+// device's copy to its device address once (DevCtx::noalloc_dev), and only
+// that address is used.
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 }  // namespace
 
 DevCtx* get_ctx(uint32_t ord) {
@@ -79,6 +88,16 @@ DevCtx* get_ctx(uint32_t ord) {
     return nullptr;
   }
   ctx->stream = ctx->own_stream;
+  // the allocation-free decode's scratch on this device (the device is
+  // current): its address, or null, and the entry point then reports
+  // MissingCapability
+  void* sp = nullptr;
+  if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess && sp) {
+    ctx->noalloc_dev = static_cast<uint8_t*>(sp);
+    ctx->noalloc_host.reset(new uint8_t[kNoAllocHostBytes]);
+  } else {
+    (void)hipGetLastError();
+  }
   (void)hipSetDevice(prev);
   g_ctx[ord] = std::move(ctx);
   return g_ctx[ord].get();
@@ -209,6 +228,81 @@ bool fused_eligible(const PlanTensor& T, uint64_t out_dev) {
   // restored tensor where the chain is a bijection on plane bytes (other
   // chains keep their planes in scratch)
   return ok && any_huff != any_rans && (!T.has_crc || crc_chain_supported(T.chain));
+}
+
+namespace {
+
+// Views of the fixed scratch in place of the device context's grow-only
+// buffers for the length of one allocation-free call; the context's own
+// buffers come back when it ends.
+struct Borrow {
+  DeviceBuffer* dst[9];
+  DeviceBuffer saved[9];
+  PinnedBuffer* hdst[3];
+  PinnedBuffer hsaved[3];
+  bool tab_ready;
+  DevCtx& ctx;
+  explicit Borrow(DevCtx& c) : ctx(c) {
+    uint8_t* d = c.noalloc_dev;
+    struct View {
+      DeviceBuffer* b;
+      uint64_t off, len;
+    } v[9] = {{&c.crc_tab, kNoAllocTabOff, kNoAllocTabBytes},
+              {&c.ilv_args, kNoAllocArgsOff, kNoAllocArgsBytes},
+              {&c.crc_args, kNoAllocCrcArgsOff, kNoAllocCrcArgsBytes},
+              {&c.crc_comb, kNoAllocCombOff, kNoAllocCombBytes},
+              {&c.planes, kNoAllocStubOff, 1024},
+              {&c.jobs, kNoAllocStubOff + 1024, 1024},
+              {&c.status, kNoAllocStubOff + 2048, 1024},
+              {&c.crc_part, kNoAllocPartOff, kNoAllocPartBytes},
+              {&c.ilv_realign, 0, 0}};
+    for (int i = 0; i < 9; ++i) {
+      dst[i] = v[i].b;
+      saved[i] = *v[i].b;
+      v[i].b->ptr = v[i].len ? d + v[i].off : nullptr;
+      v[i].b->cap = v[i].len;
+      v[i].b->borrowed = true;
+    }
+    uint8_t* h = c.noalloc_host.get();
+    PinnedBuffer* hb[3] = {&c.h_ilv, &c.h_jobs, &c.h_status};
+    const uint64_t hoff[3] = {0, kNoAllocHostBytes - 2048, kNoAllocHostBytes - 1024};
+    const uint64_t hlen[3] = {kNoAllocHostBytes - 2048, 1024, 1024};
+    for (int i = 0; i < 3; ++i) {
+      hdst[i] = hb[i];
+      hsaved[i] = *hb[i];
+      hb[i]->ptr = h + hoff[i];
+      hb[i]->cap = hlen[i];
+      hb[i]->borrowed = true;
+    }
+    tab_ready = c.crc_tab_ready;
+    c.crc_tab_ready = c.noalloc_tab_ready;
+  }
+  ~Borrow() {
+    ctx.noalloc_tab_ready = ctx.crc_tab_ready;
+    ctx.crc_tab_ready = tab_ready;
+    for (int i = 0; i < 9; ++i) *dst[i] = saved[i];
+    for (int i = 0; i < 3; ++i) *hdst[i] = hsaved[i];
+  }
+};
+
+}  // namespace
+
+int64_t execute_plan_noalloc(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev) {
+  if (!ctx.noalloc_dev || !ctx.noalloc_host) return kMissingCapability;
+  if (plan.tensors.size() > kNoAllocMaxTensors) return kUnsupported;
+  uint64_t crc_blocks = 0;
+  for (const PlanTensor& T : plan.tensors) {
+    if (T.has_hash || !fused_eligible(T, out_dev)) return kUnsupported;
+    bool rans = false;
+    for (const PlanPlane& P : T.planes) {
+      rans |= P.codec == kCodecRansIlv;
+      if (P.codec != kCodecIdentity && ((in_dev + P.payload_offset) & 3u)) return kUnsupported;
+    }
+    if (T.has_crc && !rans) crc_blocks += (T.planes[0].plane_len + kIlvBlock - 1) / kIlvBlock;
+  }
+  if (crc_blocks > kNoAllocMaxCrcBlocks) return kUnsupported;
+  Borrow b(ctx);
+  return execute_plan(ctx, plan, in_dev, out_dev);
 }
 
 int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev) {
