@@ -395,17 +395,20 @@ struct BlockState {
 // Load the raw (uncoded) planes' bytes of the group at plane position pos:
 // full blocks with aligned planes issue one load per plane (expanded by the
 // consumer), other blocks load and expand the group's symbols.
-template <uint32_t kChain, bool kTail>
-__device__ __forceinline__ void load_raw(const BlockState<ChainInfo<kChain>::np>& st, uint64_t pos, uint64_t n,
+// kSkipCoded (plane forms fixed at compile time): coded planes issue no load.
+template <uint32_t kChain, bool kTail, bool kSkipCoded = false>
+__device__ __forceinline__ void load_raw(const BlockState<ChainInfo<kChain>::np>& st, uint32_t coded_mask,
+                                         uint32_t packed_mask, uint64_t pos, uint64_t n,
                                          uint32_t (&x)[ChainInfo<kChain>::np][4], bool live = true) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
 #pragma unroll
   for (uint32_t p = 0; p < NP; ++p) {
     if constexpr (kTail) {
-      if (st.coded_mask & (1u << p)) continue;
-      load_group(st.raw[p], (st.packed_mask >> p) & 1u, pos, group_count<kTail>(pos, n), x[p]);
+      if (coded_mask & (1u << p)) continue;
+      load_group(st.raw[p], (packed_mask >> p) & 1u, pos, group_count<kTail>(pos, n), x[p]);
     } else {
-      load_group_fast(st.raw[p], st.rbytes[p], (st.packed_mask >> p) & 1u, (uint32_t)pos, live, x[p]);
+      if (kSkipCoded && (coded_mask & (1u << p))) continue;
+      load_group_fast(st.raw[p], st.rbytes[p], (packed_mask >> p) & 1u, (uint32_t)pos, live, x[p]);
     }
   }
 }
@@ -417,18 +420,23 @@ __device__ __forceinline__ void load_raw(const BlockState<ChainInfo<kChain>::np>
 //
 // kCrc (crc_on uniform, whole blocks only): acc[p] becomes the zero-init
 // CRC-32 of the lane's 16 pieces of plane p (pieces 1 KiB apart), relative
-// to the end of its last piece: acc' = acc x^(8 * 1024) xor crc0(piece),
-// the advance by byte-sliced lookups (crcL + 1024) and crc0 by slicing-by-4
-// (crcL), off the register's serial chain.
-template <uint32_t kChain, bool kTail, bool kStaged, bool kCrc = false>
+// to the end of its last piece: acc' = acc x^(8 * 1024) xor crc0(piece).
+// crc0 by slicing-by-4 (Kounavis & Berry) and the advance by four
+// byte-sliced lookups, from tables at LDS address 0 (crc_round_lds0); a
+// plane whose symbols are held rotated is rotated back first.
+template <uint32_t kChain, bool kTail, bool kStaged, bool kCrc = false, uint32_t kFix = 0>
 __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& st, uint32_t luts, uint64_t out,
                                              uint64_t n, uint64_t bstart, uint32_t lane,
-                                             const uint32_t* crcL = nullptr, bool crc_on = false,
                                              uint32_t* acc = nullptr) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
   constexpr uint32_t RATIO = ChainInfo<kChain>::ratio;
+  static_assert(kFix == 0 || (!kTail && kStaged), "fixed plane forms: fast staged path only");
+  const uint32_t coded_mask = kFix ? kFix - 1 : st.coded_mask;
+  const uint32_t pair_mask = kFix ? 0u : st.pair_mask;
+  const uint32_t packed_mask = kFix ? 0u : st.packed_mask;
+  static_assert(kIlvCrcWords == kCrcLdsWords, "LDS copy of the CRC tables");
   uint32_t nxt[NP][4];
-  load_raw<kChain, kTail>(st, bstart + (uint64_t)kIlvGroup * lane, n, nxt);
+  load_raw<kChain, kTail, kFix != 0>(st, coded_mask, packed_mask, bstart + (uint64_t)kIlvGroup * lane, n, nxt);
   if constexpr (!kTail) {
 #pragma unroll
     for (uint32_t k = 0; k < RATIO; ++k) vmem_nop(out, k);
@@ -439,7 +447,7 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
     uint32_t v[NP][4];
     bool done = false;
     if constexpr (NP == 2 && kStaged && !kTail) {
-      if (st.coded_mask == 3u && st.pair_mask == 3u) {
+      if (coded_mask == 3u && pair_mask == 3u) {
         // both nibble planes in pair mode: their two lookup chains interleaved
         group_lds_pair2(st.lut[0], st.q[0], v[0], st.lut[1], st.q[1], v[1]);
 #pragma unroll
@@ -451,9 +459,9 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
     }
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
-      if (done || !(st.coded_mask & (1u << p))) continue;
+      if (done || !(coded_mask & (1u << p))) continue;
       const uint32_t lut = st.lut[p];
-      if (st.pair_mask & (1u << p)) {
+      if (pair_mask & (1u << p)) {
         if constexpr (kStaged && !kTail) {
           group_lds_pair(lut, st.q[p], v[p]);
 #pragma unroll
@@ -471,32 +479,31 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
 #pragma unroll
     for (uint32_t p = 0; p < NP; ++p) {
       if constexpr (kTail) {
-        if (st.coded_mask & (1u << p)) continue;
+        if (coded_mask & (1u << p)) continue;
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[p][k] = xform_word(ChainInfo<kChain>::xf[p], nxt[p][k]);
       } else {
-        // every plane's load is consumed here (coded planes loaded zeros)
+        // every plane's load is consumed here (coded planes loaded zeros,
+        // or nothing with fixed plane forms)
+        const bool raw = !(coded_mask & (1u << p));
+        if (kFix && !raw) continue;
         uint32_t x[4];
-        expand_group((st.packed_mask >> p) & 1u, nxt[p], x);
-        const bool raw = !(st.coded_mask & (1u << p));
+        expand_group((packed_mask >> p) & 1u, nxt[p], x);
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[p][k] = raw ? xform_word(ChainInfo<kChain>::xf[p], x[k]) : v[p][k];
       }
     }
     if constexpr (kTail) {
-      if (r + 1 < kIlvRounds) load_raw<kChain, kTail>(st, pos + (uint64_t)kIlvGroup * 64u, n, nxt);
+      if (r + 1 < kIlvRounds) load_raw<kChain, kTail, kFix != 0>(st, coded_mask, packed_mask, pos + (uint64_t)kIlvGroup * 64u, n, nxt);
     } else {
-      load_raw<kChain, kTail>(st, pos + (uint64_t)kIlvGroup * 64u, n, nxt, r + 1 < kIlvRounds);
+      load_raw<kChain, kTail, kFix != 0>(st, coded_mask, packed_mask, pos + (uint64_t)kIlvGroup * 64u, n, nxt, r + 1 < kIlvRounds);
     }
     if constexpr (kCrc) {
-      if (crc_on) {
 #pragma unroll
-        for (uint32_t p = 0; p < NP; ++p) {
-          const uint32_t xf = ChainInfo<kChain>::xf[p];
-          const u32x4 pl = u32x4_make(unxform_word(xf, v[p][0]), unxform_word(xf, v[p][1]),
-                                      unxform_word(xf, v[p][2]), unxform_word(xf, v[p][3]));
-          acc[p] = sliced(crcL + 1024, acc[p]) ^ crc_piece(crcL, 0u, pl);
-        }
+      for (uint32_t p = 0; p < NP; ++p) {
+        const uint32_t xf = ChainInfo<kChain>::xf[p];
+        acc[p] = crc_round_lds0(acc[p], u32x4_make(unxform_word(xf, v[p][0]), unxform_word(xf, v[p][1]),
+                                                   unxform_word(xf, v[p][2]), unxform_word(xf, v[p][3])));
       }
     }
     if (kTail && count == 0) continue;
@@ -530,9 +537,11 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
   // The kernel has no static LDS, so the dynamic area starts at LDS address
   // 0 and every table sits on a SLOT boundary (entry address =
   // (window & mask) | table base).  Layout:
+  //   [kCrc: CRC tables, 8 KiB at address 0 (crc_round_lds0)]
   //   [n_slots tables (coded planes from the last one down)][DecodeCtl]
-  //   [4 wavefronts x stage_words][96 spare words][kCrc: CRC tables]
-  extern __shared__ __align__(16) uint8_t smem[];
+  //   [4 wavefronts x stage_words][96 spare words]
+  extern __shared__ __align__(16) uint8_t lds[];
+  uint8_t* const smem = lds + (kCrc ? 4u * kIlvCrcWords : 0u);
   DecodeCtl& ctl = *reinterpret_cast<DecodeCtl*>(smem + n_slots * SLOT);
   uint32_t* const stage = reinterpret_cast<uint32_t*>(smem + n_slots * SLOT + sizeof(DecodeCtl));
   // while a tensor's tables are built, the staging area holds the payload
@@ -566,11 +575,15 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
   }
   uint32_t j = lo, cur = 0xFFFFFFFFu, bad = 0;
   uint32_t* const sw = stage + wave * stage_words;
-  // CRC tables: T0..T3 and the byte-sliced advance over 1 KiB (visible
-  // after the first tile's barriers)
-  uint32_t* const crcL = stage + 4 * stage_words + kIlvStageSpare;
+  // CRC nibble tables N, NR, NA (visible after the first tile's barriers)
   if constexpr (kCrc) {
-    for (uint32_t i = t; i < kIlvCrcWords; i += 256) crcL[i] = crc_tab[i < 1024 ? i : i - 1024 + kCrcTabS1024];
+    // T0..T3 and the byte-sliced advance over 1 KiB
+    uint32_t* const crcT = reinterpret_cast<uint32_t*>(lds);
+    if (lds_addr(crcT) != 0) {  // not reachable: the kernel has no static LDS
+      if (t == 0 && blockIdx.x == 0) atomicOr(&status[tix[0]], kIlvErrHeader);
+      return;
+    }
+    for (uint32_t i = t; i < kIlvCrcWords; i += 256) crcT[i] = crc_tab[i < 1024 ? i : i - 1024 + kCrcTabS1024];
   }
   for (uint32_t tile = tile0; tile < tile1; ++tile) {
     while (tile >= tpre[j + 1]) ++j;
@@ -796,8 +809,20 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (full) decode_block<kChain, false, true, kCrc>(st, luts, out, n, bstart, lane, crcL, crc_on, acc);
-      else decode_block<kChain, true, true, kCrc>(st, luts, out, n, bstart, lane, crcL, crc_on, acc);
+      // the bf16 exponent-coded plane forms get a branch-free round body
+      const bool fix = kChain == kChainIeee16Split2 && st.coded_mask == 2u && st.pair_mask == 0u &&
+                       st.packed_mask == 0u;
+      if (full && crc_on) {
+        if (fix) decode_block<kChain, false, true, kCrc, 3>(st, luts, out, n, bstart, lane, acc);
+        else decode_block<kChain, false, true, kCrc>(st, luts, out, n, bstart, lane, acc);
+      } else if (full) {
+        if (fix) decode_block<kChain, false, true, false, 3>(st, luts, out, n, bstart, lane);
+        else decode_block<kChain, false, true, false>(st, luts, out, n, bstart, lane);
+      } else if (crc_on) {
+        decode_block<kChain, true, true, kCrc>(st, luts, out, n, bstart, lane, acc);
+      } else {
+        decode_block<kChain, true, true, false>(st, luts, out, n, bstart, lane);
+      }
       __builtin_amdgcn_wave_barrier();
     } else {
 #pragma unroll
@@ -806,7 +831,8 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
         st.nw[p] = lane_c[p];
         q0[p] = 0;
       }
-      decode_block<kChain, true, false, kCrc>(st, luts, out, n, bstart, lane, crcL, crc_on, acc);
+      if (crc_on) decode_block<kChain, true, false, kCrc>(st, luts, out, n, bstart, lane, acc);
+      else decode_block<kChain, true, false, false>(st, luts, out, n, bstart, lane);
     }
     if constexpr (kCrc) {
       if (crc_on) {
@@ -814,7 +840,7 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
         const uint32_t K = crc_tab[kCrcTabK64 + lane];
 #pragma unroll
         for (uint32_t p = 0; p < NP; ++p) {
-          uint32_t a = gf2_mulmod(acc[p], K);
+          uint32_t a = gf2_mulmod_seq(acc[p], K);
 #pragma unroll
           for (int d = 32; d >= 1; d >>= 1) a ^= __shfl_xor(a, d, 64);
           if (lane == 0) g_st<uint32_t>(reinterpret_cast<uint64_t>(crc_part + 4ull * (T.crc_first + bi) + p), a);
