@@ -296,6 +296,63 @@ __device__ __forceinline__ void group_lds(uint32_t lut, uint32_t& qm, uint32_t c
   pack_symbols(e, v);
 }
 
+// A lane's staged stream with its next words held in registers (the fast
+// path's reader).  The window of two lookups comes from w0:w1 with one
+// alignbit, so the dependent chain of a step is the two table lookups; the
+// word after w1 is read from LDS at the end of every step (a re-read of the
+// same word when no word was finished), one step before it can be needed.
+// A step consumes at most 22 bits, so bo stays below 32 + 22 and at most
+// one word is finished per step.
+struct BitReg {
+  uint32_t w0, w1, w2;  // stream words j, j + 1, j + 2 (word -1 reads as 0)
+  uint32_t bo;          // bit of w0 just before the next code
+  uint32_t wp;          // LDS byte address of word j + 2
+};
+
+// From the reader position qm (LDS bit address of the lane's first word,
+// minus one: the state before the lane's first code).
+__device__ __forceinline__ BitReg bitreg_open(uint32_t qm) {
+  const uint32_t wa = (qm + 1u) >> 3;
+  return BitReg{0u, lds_ld32(wa), lds_ld32(wa + 4), 31u, wa + 4};
+}
+
+// The reader position qm0 + bits consumed (32 j + bo + 1), for the
+// acceptance check.
+__device__ __forceinline__ uint32_t bitreg_close(const BitReg& b, uint32_t qm0) {
+  const uint32_t wa = (qm0 + 1u) >> 3;
+  return qm0 + 8u * (b.wp - wa) - 63u + b.bo;
+}
+
+__device__ __forceinline__ uint32_t bitreg_window(const BitReg& b) {
+  return __builtin_amdgcn_alignbit(b.w1, b.w0, b.bo);
+}
+
+// bo_next = bo + the step's code bits (< 64)
+__device__ __forceinline__ void bitreg_step(BitReg& b, uint32_t bo_next) {
+  const bool s = bo_next >= 32u;
+  b.w0 = s ? b.w1 : b.w0;
+  b.w1 = s ? b.w2 : b.w1;
+  b.wp += s ? 4u : 0u;
+  b.bo = bo_next & 31u;
+  b.w2 = lds_ld32(b.wp);
+}
+
+// group_lds<false, kMask> from the register reader
+template <uint32_t kMask>
+__device__ __forceinline__ void group_reg(uint32_t lut, BitReg& b, uint32_t (&v)[4]) {
+  uint32_t e[16];
+#pragma unroll
+  for (uint32_t k = 0; k < 16; k += 2) {
+    const uint32_t win = bitreg_window(b);
+    const uint32_t e0 = lds_ld16(lut_entry_addr<kMask>(win, lut));
+    const uint32_t e1 = lds_ld16(lut_entry_addr<kMask>(__builtin_amdgcn_alignbit(0u, win, e0), lut));
+    bitreg_step(b, add_byte0(add_byte0(b.bo, e0), e1));
+    e[k] = e0;
+    e[k + 1] = e1;
+  }
+  pack_symbols(e, v);
+}
+
 // Pair mode, full group: 8 lookups in the 12-bit pair table at `lut`, one
 // 32-bit window per two lookups (<= 24 code bits plus the leading bit).
 // Yields the 16 raw nibble symbols, one per byte.
@@ -435,6 +492,16 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
   const uint32_t pair_mask = kFix ? 0u : st.pair_mask;
   const uint32_t packed_mask = kFix ? 0u : st.packed_mask;
   static_assert(kIlvCrcWords == kCrcLdsWords, "LDS copy of the CRC tables");
+  // the fixed-form fast path reads the coded planes' staged streams through
+  // registers (elsewhere the readers' extra registers cost more occupancy
+  // than the shorter lookup chain gains)
+  constexpr bool kReg = kStaged && !kTail && kFix != 0;
+  BitReg br[NP];
+  if constexpr (kReg) {
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p)
+      if (coded_mask & (1u << p)) br[p] = bitreg_open(st.q[p]);
+  }
   uint32_t nxt[NP][4];
   load_raw<kChain, kTail, kFix != 0>(st, coded_mask, packed_mask, bstart + (uint64_t)kIlvGroup * lane, n, nxt);
   if constexpr (!kTail) {
@@ -472,7 +539,8 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
           group_global<kMask6>(st.t64[p], st.words[p], st.nw[p], st.q[p], count, v[p]);
         }
       } else {
-        if constexpr (kStaged) group_lds<kTail, kMask11>(lut, st.q[p], count, v[p]);
+        if constexpr (kReg) group_reg<kMask11>(lut, br[p], v[p]);
+        else if constexpr (kStaged) group_lds<kTail, kMask11>(lut, st.q[p], count, v[p]);
         else group_global<kMask11>(lut, st.words[p], st.nw[p], st.q[p], count, v[p]);
       }
     }
@@ -519,6 +587,11 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
     } else {
       for (uint32_t k = 0; k < RATIO * count; ++k) gstore_u8(dst + k, o[k >> 2] >> (8 * (k & 3)));
     }
+  }
+  if constexpr (kReg) {
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p)
+      if (coded_mask & (1u << p)) st.q[p] = bitreg_close(br[p], st.q[p]);
   }
 }
 
