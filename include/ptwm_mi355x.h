@@ -121,6 +121,45 @@ int64_t ptwm_mi355x_dispatch_decode_noalloc_cuda(uint8_t state_format_version, c
                                                  uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
                                                  size_t out_len, uint32_t device_ordinal);
 
+/* One tensor of a container, as ptwm_mi355x_container_plan lists it (in
+ * record order, the order the reference's tools list and decode them). */
+typedef struct ptwm_mi355x_container_tensor {
+  uint64_t name_offset;   /* the UTF-8 tensor name: byte range in the file */
+  uint64_t orig_size;     /* restored bytes (the record's orig_size) */
+  uint64_t out_offset;    /* where the plan restores it in the output buffer */
+  uint64_t record_offset; /* the tensor record: byte range in the file */
+  uint64_t record_len;
+  uint32_t name_len;      /* 0 for a \x89PTWS frame (no name) */
+  uint16_t dtype_code;    /* public dtype code (dtype.rs:79-103) */
+  uint8_t input_format;
+  uint8_t chain;          /* decode-plan chain 1..6, 0 when not planned */
+  int32_t status;         /* 0 planned; -1 the record is invalid (the reference
+                             fails to decode it); -5 a chain, codec or codec
+                             state this library does not decode */
+  int32_t plan_index;     /* its entry in the plan, -1 when not planned */
+  uint32_t flags;         /* bit 0: payload XXH64 checked, bit 1: plane CRC-32s checked */
+  uint32_t reserved;
+} ptwm_mi355x_container_tensor;
+
+/* Reference-side plan construction: reads a whole .ptwm file (legacy
+ * \x89PTWM / \x89PTWX, compact \x89PTWC) or a \x89PTWS frame held in host
+ * memory and writes the PTMD decode plan (the state bytes of
+ * ptwm_hardware_backend_v1_dispatch_decode_cuda) for its tensors: payload
+ * offsets index the file's own bytes, so the file copied to the device is
+ * the input buffer, and the tensors are laid out at 256-byte aligned
+ * offsets of an output buffer of *out_len bytes.  Replaces the open and
+ * per-tensor decode set-up of container.rs:1590-1790, 1795-1892 and
+ * compact.rs:407-480; the chain, codec, chunk table, plane CRC-32 and
+ * payload hash of each tensor come from its record.  Writes *plan_len,
+ * *n_tensors and *out_len, then the plan and the tensor list.  Returns the
+ * number of planned tensors; -1 if the file's header, tables, registry or
+ * index are invalid or the magic is none of these (opening it fails in the
+ * reference); -2 when plan_cap or max_tensors is too small (the sizes needed
+ * are written). */
+int64_t ptwm_mi355x_container_plan(const uint8_t *file, size_t file_len, uint8_t *plan, size_t plan_cap,
+                                   size_t *plan_len, ptwm_mi355x_container_tensor *tensors, size_t max_tensors,
+                                   size_t *n_tensors, uint64_t *out_len);
+
 /* ABI revision of this library (bumped on any incompatible change). */
 uint32_t ptwm_mi355x_abi_version(void);
 

@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(HERE, "_build", "libptwm_oracle.so")
 CODEC_IDENTITY = 0x0000
 CODEC_HUFFMAN = 0x0001
 CODEC_RANS = 0x0003
+CODEC_TANS = 0x0007
 
 CHAIN_IEEE16_SPLIT2 = 1
 CHAIN_IEEE32_SPLIT4 = 2
@@ -65,6 +66,12 @@ def lib():
         L.por_rans_decompress.restype = i64
         L.por_rans_decompress.argtypes = [vp, sz, vp, sz]
         L.por_codec_encode.restype = i64
+        L.por_tans_compress.argtypes = [vp, sz, vp, sz]
+        L.por_tans_compress.restype = C.c_int64
+        L.por_tans_decompress.argtypes = [vp, sz, vp, sz]
+        L.por_tans_decompress.restype = C.c_int64
+        L.por_tans_decode_table.argtypes = [vp, vp, vp, vp]
+        L.por_tans_spread.argtypes = [vp, vp]
         L.por_codec_encode.argtypes = [C.c_int, vp, sz, vp, sz]
         L.por_codec_decode.restype = i64
         L.por_codec_decode.argtypes = [C.c_int, vp, sz, vp, sz]
@@ -186,6 +193,44 @@ def rans_decompress(blob, n_out: int) -> bytes:
     if r < 0:
         raise OracleError(r, "rans_decompress")
     return dst[:n_out].tobytes()
+
+
+def tans_compress(src) -> bytes:
+    """entropy/tans/mod.rs:273 -> blob (b'' = store raw)."""
+    s = _buf(src)
+    dst = np.zeros(max(s.size, 1), np.uint8)
+    n = lib().por_tans_compress(_ptr(dst), s.size, _ptr(s), s.size)
+    if n < 0:
+        raise OracleError(n, "tans_compress")
+    return dst[:n].tobytes()
+
+
+def tans_decompress(blob, n_out: int) -> bytes:
+    """entropy/tans/mod.rs:372."""
+    b = _buf(blob)
+    dst = np.zeros(max(n_out, 1), np.uint8)
+    r = lib().por_tans_decompress(_ptr(dst), n_out, _ptr(b), b.size)
+    if r < 0:
+        raise OracleError(r, "tans_decompress")
+    return dst[:n_out].tobytes()
+
+
+def tans_spread(norm):
+    """entropy/tans/mod.rs:199 -> uint8[2048] slot symbols."""
+    nm = np.ascontiguousarray(norm, np.uint32)
+    t = np.zeros(2048, np.uint8)
+    lib().por_tans_spread(_ptr(nm), _ptr(t))
+    return t
+
+
+def tans_decode_table(norm):
+    """entropy/tans/mod.rs:346 -> (sym, nb_bits, baseline) arrays of 2048."""
+    nm = np.ascontiguousarray(norm, np.uint32)
+    sym = np.zeros(2048, np.uint8)
+    nb = np.zeros(2048, np.uint8)
+    base = np.zeros(2048, np.uint16)
+    lib().por_tans_decode_table(_ptr(nm), _ptr(sym), _ptr(nb), _ptr(base))
+    return sym, nb, base
 
 
 # ---- plane codec payloads (codecs/{identity,huffman,rans}.rs) ----

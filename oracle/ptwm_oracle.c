@@ -40,6 +40,7 @@ uint32_t por_revert32(uint32_t v) {
 
 static uint32_t ld32(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24); }
 static void st32(uint8_t *p, uint32_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); p[2] = (uint8_t)(v >> 16); p[3] = (uint8_t)(v >> 24); }
+static uint64_t ld64(const uint8_t *p) { return (uint64_t)ld32(p) | ((uint64_t)ld32(p + 4) << 32); }
 
 /* dtype16.rs:31-59 -- only floor(len/4) words; a trailing element is left as is */
 void por_reorder16_buf(uint8_t *d, size_t len) { for (size_t i = 0; i + 4 <= len; i += 4) st32(d + i, por_reorder16x2(ld32(d + i))); }
@@ -720,6 +721,188 @@ int64_t por_rans_decompress(uint8_t *dst, size_t dst_len, const uint8_t *src, si
 }
 
 /* ------------------------------------------------------------------------- */
+/* tANS: entropy/tans/mod.rs (TABLE_LOG 11, single stream, LIFO bit stream)  */
+/* ------------------------------------------------------------------------- */
+
+#define TANS_LOG 11
+#define TANS_L (1u << TANS_LOG)
+
+static uint32_t highbit32(uint32_t x) { return 31u - (uint32_t)__builtin_clz(x); }
+
+/* normalize :153-195 -- scale to sum L, every present symbol >= 1; surplus
+ * comes off the first largest entry, deficit goes to the first most frequent
+ * symbol */
+static void tans_normalize(const uint32_t counts[256], uint64_t total, uint32_t norm[256]) {
+    uint32_t sum = 0, max_count = 0;
+    int max_sym = 0;
+    for (int s = 0; s < 256; s++) {
+        norm[s] = 0;
+        if (!counts[s]) continue;
+        uint32_t v = (uint32_t)(((uint64_t)counts[s] * TANS_L) / total);
+        if (!v) v = 1;
+        norm[s] = v;
+        sum += v;
+        if (counts[s] > max_count) { max_count = counts[s]; max_sym = s; }
+    }
+    while (sum > TANS_L) {
+        int bi = -1;
+        uint32_t bv = 1;
+        for (int s = 0; s < 256; s++)
+            if (norm[s] > bv) { bv = norm[s]; bi = s; }
+        norm[bi]--;
+        sum--;
+    }
+    while (sum < TANS_L) { norm[max_sym]++; sum++; }
+}
+
+/* spread :199-211 -- symbols in order, step (L/2 + L/8 + 3) mod L */
+void por_tans_spread(const uint32_t norm[256], uint8_t table[2048]) {
+    const uint32_t step = (TANS_L >> 1) + (TANS_L >> 3) + 3, mask = TANS_L - 1;
+    uint32_t pos = 0;
+    for (int s = 0; s < 256; s++)
+        for (uint32_t k = 0; k < norm[s]; k++) { table[pos] = (uint8_t)s; pos = (pos + step) & mask; }
+}
+
+/* build_decode :346-368 -- slot u of symbol s with occurrence x (norm[s] ..
+ * 2 norm[s] - 1): nb = 11 - floor(log2 x), baseline = (x << nb) - L */
+void por_tans_decode_table(const uint32_t norm[256], uint8_t sym[2048], uint8_t nb[2048], uint16_t base[2048]) {
+    uint32_t next[256];
+    por_tans_spread(norm, sym);
+    for (int s = 0; s < 256; s++) next[s] = norm[s];
+    for (uint32_t u = 0; u < TANS_L; u++) {
+        uint32_t x = next[sym[u]]++;
+        uint32_t b = TANS_LOG - highbit32(x);
+        nb[u] = (uint8_t)b;
+        base[u] = (uint16_t)((x << b) - TANS_L);
+    }
+}
+
+/* compress :273-341 -- returns the blob length, or 0 for "store raw" */
+int64_t por_tans_compress(uint8_t *dst, size_t cap, const uint8_t *src, size_t n) {
+    if (n == 0) return 0;
+    uint32_t counts[256] = {0}, norm[256];
+    for (size_t i = 0; i < n; i++) counts[src[i]]++;
+    int nsym = 0;
+    for (int s = 0; s < 256; s++) nsym += counts[s] != 0;
+    if (nsym < 2) return 0;
+    tans_normalize(counts, n, norm);
+    uint8_t sym[TANS_L];
+    por_tans_spread(norm, sym);
+    /* build_encode :225-268: next-state table packed per symbol and the
+     * per-symbol (delta_nb_bits, delta_find_state) transform */
+    uint32_t cumul[256], fill[256], run = 0;
+    for (int s = 0; s < 256; s++) { cumul[s] = run; run += norm[s]; fill[s] = cumul[s]; }
+    uint16_t state_table[TANS_L];
+    for (uint32_t u = 0; u < TANS_L; u++) state_table[fill[sym[u]]++] = (uint16_t)(TANS_L + u);
+    uint32_t dnb[256] = {0};
+    int32_t dfs[256] = {0};
+    int32_t total = 0;
+    for (int s = 0; s < 256; s++) {
+        uint32_t c = norm[s];
+        if (!c) continue;
+        if (c == 1) {
+            dnb[s] = (TANS_LOG << 16) - TANS_L;
+            dfs[s] = total - 1;
+            total += 1;
+        } else {
+            uint32_t max_bits = TANS_LOG - highbit32(c - 1);
+            dnb[s] = (max_bits << 16) - (c << max_bits);
+            dfs[s] = total - (int32_t)c;
+            total += (int32_t)c;
+        }
+    }
+    /* LSB-first bit writer :60-100; symbols encoded last to first from state L */
+    size_t bs_cap = n * 2 + 16;
+    uint8_t *bs = (uint8_t *)malloc(bs_cap);
+    if (!bs) return POR_ESMALL;
+    size_t bl = 0;
+    uint64_t acc = 0, tot = 0;
+    uint32_t nbits = 0, value = TANS_L;
+    for (size_t i = n; i-- > 0;) {
+        uint8_t b = src[i];
+        uint32_t k = (value + dnb[b]) >> 16;
+        if (k) {
+            acc |= ((uint64_t)value & ((1ull << k) - 1)) << nbits;
+            nbits += k; tot += k;
+            while (nbits >= 8) { bs[bl++] = (uint8_t)acc; acc >>= 8; nbits -= 8; }
+        }
+        value = state_table[(int32_t)(value >> k) + dfs[b]];
+    }
+    acc |= ((uint64_t)value & (TANS_L - 1)) << nbits;
+    nbits += TANS_LOG; tot += TANS_LOG;
+    while (nbits >= 8) { bs[bl++] = (uint8_t)acc; acc >>= 8; nbits -= 8; }
+    if (nbits) bs[bl++] = (uint8_t)acc;
+    size_t blob = 1 + 2 + (size_t)nsym * 3 + 8 + bl;
+    if (blob >= n || blob > cap) { free(bs); return 0; }
+    size_t w = 0;
+    dst[w++] = TANS_LOG;
+    dst[w++] = (uint8_t)nsym; dst[w++] = (uint8_t)(nsym >> 8);
+    for (int s = 0; s < 256; s++) {
+        if (!norm[s]) continue;
+        dst[w++] = (uint8_t)s; dst[w++] = (uint8_t)norm[s]; dst[w++] = (uint8_t)(norm[s] >> 8);
+    }
+    st32(dst + w, (uint32_t)tot); st32(dst + w + 4, (uint32_t)(tot >> 32)); w += 8;
+    memcpy(dst + w, bs, bl);
+    free(bs);
+    return (int64_t)(w + bl);
+}
+
+/* LIFO reader :102-150: pops the nb most recently written bits */
+static int tans_read(const uint8_t *bs, size_t bl, uint64_t *pos, uint32_t nb, uint32_t *v) {
+    if (nb == 0) { *v = 0; return 0; }
+    if (*pos < nb) return -1;
+    uint64_t start = *pos - nb;
+    size_t bi = (size_t)(start >> 3);
+    uint32_t w = bs[bi];
+    if (bi + 1 < bl) w |= (uint32_t)bs[bi + 1] << 8;
+    if (bi + 2 < bl) w |= (uint32_t)bs[bi + 2] << 16;
+    *v = (w >> (start & 7)) & ((1u << nb) - 1);
+    *pos = start;
+    return 0;
+}
+
+/* decompress :372-455 -- n symbols from a compress blob */
+int64_t por_tans_decompress(uint8_t *dst, size_t n, const uint8_t *src, size_t len) {
+    if (n == 0) return 0;
+    if (len < 3) return POR_EINVAL;
+    if (src[0] != TANS_LOG) return POR_EINVAL;
+    size_t nsym = (size_t)src[1] | ((size_t)src[2] << 8);
+    if (nsym < 2 || nsym > 256) return POR_EINVAL;
+    size_t p = 3, pairs_end = p + nsym * 3;
+    if (pairs_end + 8 > len) return POR_EINVAL;
+    uint32_t norm[256] = {0}, sum = 0;
+    for (size_t i = 0; i < nsym; i++, p += 3) {
+        uint32_t s = src[p], f = (uint32_t)src[p + 1] | ((uint32_t)src[p + 2] << 8);
+        if (norm[s]) return POR_EINVAL;        /* duplicate symbol */
+        if (!f) return POR_EINVAL;             /* zero frequency */
+        norm[s] = f;
+        sum += f;
+    }
+    if (sum != TANS_L) return POR_EINVAL;
+    uint64_t total_bits = ld64(src + p);
+    p += 8;
+    const uint8_t *bs = src + p;
+    size_t bl = len - p;
+    if (total_bits > (uint64_t)bl * 8) return POR_EINVAL;
+    uint8_t sym[TANS_L], nb[TANS_L];
+    uint16_t base[TANS_L];
+    por_tans_decode_table(norm, sym, nb, base);
+    uint64_t pos = total_bits;
+    uint32_t state, low;
+    if (tans_read(bs, bl, &pos, TANS_LOG, &state)) return POR_EINVAL;
+    if (state >= TANS_L) return POR_EINVAL;
+    for (size_t i = 0; i < n; i++) {
+        dst[i] = sym[state];
+        if (tans_read(bs, bl, &pos, nb[state], &low)) return POR_EINVAL;
+        state = base[state] + low;
+        if (state >= TANS_L) return POR_EINVAL;
+    }
+    if (pos != 0) return POR_EINVAL;           /* trailing bits */
+    if (state != 0) return POR_EINVAL;         /* not back at the start state */
+    return (int64_t)n;
+}
+
+/* ------------------------------------------------------------------------- */
 /* plane codec payloads: codecs/huffman.rs:37-141, codecs/rans.rs:38-144,    */
 /* codec_tagged.rs:98-194, codecs/length_prefix.rs:30-33, codecs/identity.rs  */
 /* ------------------------------------------------------------------------- */
@@ -744,14 +927,19 @@ int64_t por_codec_encode(int codec, const uint8_t *plane, size_t len, uint8_t *o
         if (len) memcpy(out, plane, len);
         return (int64_t)len;
     }
-    if (codec != POR_CODEC_HUFFMAN && codec != POR_CODEC_RANS) return POR_EUNSUP;
+    if (codec != POR_CODEC_HUFFMAN && codec != POR_CODEC_RANS && codec != POR_CODEC_TANS) return POR_EUNSUP;
     if (len == 0) { if (cap < 1) return POR_ESMALL; out[0] = 0; return 1; }
     size_t bound = len * 2 + 4096;          /* huffman_output_bound / rans_output_bound */
     uint8_t *buf = (uint8_t *)malloc(bound);
     if (!buf) return POR_ESMALL;
     int outcome;
-    int64_t n = codec == POR_CODEC_HUFFMAN ? por_huf_compress(buf, bound, plane, len, &outcome)
-                                           : por_rans_compress(buf, bound, plane, len, &outcome);
+    int64_t n;
+    if (codec == POR_CODEC_TANS) {          /* codecs/tans.rs:39-92: scratch of plane.len() bytes */
+        n = por_tans_compress(buf, len, plane, len);
+        outcome = n > 0 ? POR_OUT_ENCODED : POR_OUT_NOT_BENEFICIAL;
+    } else
+        n = codec == POR_CODEC_HUFFMAN ? por_huf_compress(buf, bound, plane, len, &outcome)
+                                       : por_rans_compress(buf, bound, plane, len, &outcome);
     int64_t r;
     if (n < 0) r = n;
     else if (outcome == POR_OUT_ENCODED && len <= 0xFFFFFFFFu &&
@@ -781,7 +969,7 @@ int64_t por_codec_decode(int codec, const uint8_t *pl, size_t len, uint8_t *out,
         if (len) memcpy(out, pl, len);
         return (int64_t)len;
     }
-    if (codec != POR_CODEC_HUFFMAN && codec != POR_CODEC_RANS) return POR_EUNSUP;
+    if (codec != POR_CODEC_HUFFMAN && codec != POR_CODEC_RANS && codec != POR_CODEC_TANS) return POR_EUNSUP;
     if (len == 0) return POR_EINVAL;
     uint8_t tag = pl[0];
     if (tag == 0) {
@@ -799,10 +987,12 @@ int64_t por_codec_decode(int codec, const uint8_t *pl, size_t len, uint8_t *out,
         if (orig > cap) return POR_EINVAL;                    /* check_decoded_len */
         return por_huf_decompress(out, orig, enc, enc_len);
     }
-    /* rANS: decode_bounded's check_within runs first (rans.rs:158-160) */
+    /* rANS / tANS: decode_bounded's check_within runs first (rans.rs:158-160,
+     * tans.rs:150-152), then the length-prefix rule (tans.rs:118-126) */
     if (orig > cap) return POR_EINVAL;
     if (!length_prefix_accepted(orig, enc_len)) return POR_EINVAL;
     if (orig == 0) return 0;                                  /* decode_tagged expected_len == 0 */
+    if (codec == POR_CODEC_TANS) return por_tans_decompress(out, orig, enc, enc_len);
     return por_rans_decompress(out, orig, enc, enc_len);
 }
 
@@ -1359,7 +1549,6 @@ uint32_t por_crc32(uint32_t crc, const uint8_t *d, size_t len) {
 #define XP4 9650029242287828579ULL
 #define XP5 2870177450012600261ULL
 static uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
-static uint64_t ld64(const uint8_t *p) { return (uint64_t)ld32(p) | ((uint64_t)ld32(p + 4) << 32); }
 static uint64_t xround(uint64_t acc, uint64_t in) { acc += in * XP2; acc = rotl64(acc, 31); return acc * XP1; }
 static uint64_t xmerge(uint64_t acc, uint64_t v) { acc ^= xround(0, v); return acc * XP1 + XP4; }
 

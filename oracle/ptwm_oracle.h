@@ -38,6 +38,7 @@ extern "C" {
 #define POR_CODEC_IDENTITY 0x0000
 #define POR_CODEC_HUFFMAN  0x0001
 #define POR_CODEC_RANS     0x0003
+#define POR_CODEC_TANS     0x0007
 
 /* fused chain kinds (transforms/fusion.rs) */
 #define POR_CHAIN_IEEE16_SPLIT2   1 /* FusedIeee16ByteSplit2  */
@@ -107,6 +108,13 @@ int64_t por_rans_compress(uint8_t *dst, size_t dst_cap, const uint8_t *src, size
 int64_t por_rans_decompress(uint8_t *dst, size_t dst_len, const uint8_t *src, size_t src_len);
 /* EncSymbol reciprocal state update (compress.rs:35-68,164-165) */
 uint32_t por_rans_enc_update(uint32_t state, uint32_t start, uint32_t freq);
+
+/* ---- tANS (entropy/tans/mod.rs): TABLE_LOG 11, single LIFO stream ---- */
+void por_tans_spread(const uint32_t norm[256], uint8_t table[2048]);
+void por_tans_decode_table(const uint32_t norm[256], uint8_t sym[2048], uint8_t nb[2048], uint16_t base[2048]);
+/* blob length, or 0 = store raw (incompressible / one symbol / no gain) */
+int64_t por_tans_compress(uint8_t *dst, size_t cap, const uint8_t *src, size_t n);
+int64_t por_tans_decompress(uint8_t *dst, size_t n, const uint8_t *src, size_t len);
 
 /* ---- plane codec payloads (codecs/huffman.rs, codecs/rans.rs, identity.rs) ---- */
 /* bound on encoded payload size for a plane of len bytes */

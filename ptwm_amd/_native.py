@@ -68,6 +68,9 @@ _SIGS = {
     "ptwm_mi355x_dispatch_decode_noalloc_cuda": (
         C.c_int64, [C.c_uint8, _u8p, C.c_size_t, _u8p, C.c_size_t, C.c_uint64, C.c_size_t, C.c_uint64, C.c_size_t,
                     C.c_uint32]),
+    "ptwm_mi355x_container_plan": (
+        C.c_int64, [_u8p, C.c_size_t, _u8p, C.c_size_t, C.POINTER(C.c_size_t), C.c_void_p, C.c_size_t,
+                    C.POINTER(C.c_size_t), C.POINTER(C.c_uint64)]),
     "ptwm_mi355x_set_profiling": (C.c_int64, [C.c_uint32, C.c_uint32]),
     "ptwm_mi355x_last_kernel_ms": (C.c_int64, [C.c_uint32, C.POINTER(C.c_float)]),
     "ptwm_mi355x_split_cuda": (
@@ -87,6 +90,16 @@ class NativeError(RuntimeError):
 
 
 _lib = None
+
+
+class ContainerTensor(C.Structure):
+    """ptwm_mi355x_container_tensor (include/ptwm_mi355x.h)."""
+    _fields_ = [
+        ("name_offset", C.c_uint64), ("orig_size", C.c_uint64), ("out_offset", C.c_uint64),
+        ("record_offset", C.c_uint64), ("record_len", C.c_uint64), ("name_len", C.c_uint32),
+        ("dtype_code", C.c_uint16), ("input_format", C.c_uint8), ("chain", C.c_uint8),
+        ("status", C.c_int32), ("plan_index", C.c_int32), ("flags", C.c_uint32), ("reserved", C.c_uint32),
+    ]
 
 
 def lib() -> C.CDLL:

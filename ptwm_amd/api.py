@@ -22,7 +22,8 @@ import ctypes as C
 import threading
 
 from . import ids
-from ._native import NativeError, check, lib
+from . import _native
+from ._native import RC_BUFFER_TOO_SMALL, NativeError, check, lib
 
 
 def _current_raw_stream(device_ordinal: int) -> int:
@@ -272,3 +273,51 @@ def merge_cuda(chain: int, planes, out, device_ordinal: int = 0) -> int:
     op, ol = _dev_ptr_len(out, "out", device_ordinal, stream, True)
     arr = (C.c_uint64 * len(planes))(*[p[0] for p in ptrs])
     return check(L.ptwm_mi355x_merge_cuda(chain, arr, len(planes), ptrs[0][1], op, ol, device_ordinal), "merge_cuda")
+
+
+class ContainerEntry:
+    """One tensor of a container as ``container_plan`` lists it."""
+
+    __slots__ = ("name", "orig_size", "out_offset", "record_offset", "record_len", "dtype_code", "input_format",
+                 "chain", "status", "plan_index", "hash_checked", "crc_checked")
+
+    def __init__(self, t, data: bytes):
+        # a record the reader rejected (status -1) may hold a malformed name
+        self.name = bytes(data[t.name_offset:t.name_offset + t.name_len]).decode("utf-8", errors="replace")
+        self.orig_size = int(t.orig_size)
+        self.out_offset = int(t.out_offset)
+        self.record_offset = int(t.record_offset)
+        self.record_len = int(t.record_len)
+        self.dtype_code = int(t.dtype_code)
+        self.input_format = int(t.input_format)
+        self.chain = int(t.chain)
+        self.status = int(t.status)
+        self.plan_index = int(t.plan_index)
+        self.hash_checked = bool(t.flags & 1)
+        self.crc_checked = bool(t.flags & 2)
+
+    def __repr__(self):
+        return (f"ContainerEntry({self.name!r}, orig_size={self.orig_size}, chain={self.chain}, "
+                f"status={self.status}, out_offset={self.out_offset})")
+
+
+def container_plan(data) -> tuple[bytes, list[ContainerEntry], int]:
+    """Read a .ptwm container (legacy or PTWC) or a PTWS frame held in host
+    memory (library addition: the reference-side plan construction of
+    container.rs:1590-1892 / compact.rs:407-480).  Returns the PTMD plan
+    whose payload offsets index ``data``, the tensors in record order, and
+    the output buffer length the plan restores into."""
+    buf = bytes(data)
+    L = lib()
+    plan_len, n_t, out_len = C.c_size_t(0), C.c_size_t(0), C.c_uint64(0)
+    rc = L.ptwm_mi355x_container_plan(buf, len(buf), None, 0, C.byref(plan_len), None, 0, C.byref(n_t),
+                                      C.byref(out_len))
+    if rc != RC_BUFFER_TOO_SMALL and rc < 0:
+        check(rc, "container_plan")
+    plan = (C.c_uint8 * max(plan_len.value, 1))()
+    arr = (_native.ContainerTensor * max(n_t.value, 1))()
+    rc = L.ptwm_mi355x_container_plan(buf, len(buf), plan, plan_len.value, C.byref(plan_len), arr, n_t.value,
+                                      C.byref(n_t), C.byref(out_len))
+    check(rc, "container_plan")
+    entries = [ContainerEntry(arr[i], buf) for i in range(n_t.value)]
+    return bytes(plan[:plan_len.value]), entries, int(out_len.value)

@@ -33,6 +33,8 @@ constexpr KnownId kBuiltinIds[] = {
     {"eb31edfe6fd156b309010ca750571766fc8ae6e4056bc2b4a228679922edea30", kCodecIdentity},  // identity@1.0.0
     {"571e8fae548f0db5faa961fb65ba5ea2443bdb1e95dac04fbf1d5d97228ec945", kCodecHuffman},   // huffman@1.0.0
     {"87c8ca053fbd0646c07d18da4d0396a92550eb6d44bcd4e461538902874d4bc7", kCodecRans},      // rans@1.0.0
+    {"e4868545e7b22282695972441494e70569ab27595d19349114e852125d96daa4", kCodecTans},      // tans@1.1.0
+    {"ee06c9c76d008d4cfd5dca6289485aecc5328a88b035b6bc7583eb88d218fd8f", kCodecTans},      // tans@1.0.0
     // this extension: blake3([0;32] || 0 || "io.ptwm.mi355x.plane_codec" || 0 || "0.1.0")
     {"cfd8cc03483eb4a43cdddb4b3cbf95b32e0a3f0e17e5ec85a0b52de04e8caf04", kCodecHuffIlv},
     // blake3([0;32] || 0 || "io.ptwm.mi355x.plane_codec.rans" || 0 || "0.1.0")
@@ -104,7 +106,7 @@ int64_t decode_one_payload(DevCtx& ctx, uint32_t codec, uint64_t in_dev, size_t 
   uint64_t expected = 0;
   if (codec == kCodecIdentity) {
     expected = in_len;
-  } else if (codec == kCodecHuffman || codec == kCodecRans) {
+  } else if (codec == kCodecHuffman || codec == kCodecRans || codec == kCodecTans) {
     if (in_len == 0) return kInvalidInput;
     PTWM_HIP_TRY(ctx.h_small.ensure(64));
     uint8_t* hdr = static_cast<uint8_t*>(ctx.h_small.ptr);

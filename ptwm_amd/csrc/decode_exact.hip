@@ -198,17 +198,19 @@ __device__ void parse_job(const DecodeJob& job, SharedHeader& h) {
     if (orig > enc_len * 32 + 4096) { h.status = kStBadLength; return; }  // huffman.rs:122-131
     if (orig != job.dst_len) { h.status = kStBadLength; return; }
     h.kind = 1;
-  } else if (job.codec == kCodecRans) {
-    if (orig > job.dst_len) { h.status = kStBadLength; return; }          // rans.rs:158-160
-    bool accepted = orig <= (1ull << 30) || orig <= enc_len * 64;           // length_prefix.rs:30-33
+  } else if (job.codec == kCodecRans || job.codec == kCodecTans) {
+    // rans.rs:158-160 / tans.rs:150-152 (check_within), then
+    // length_prefix.rs:30-33 (tans.rs:118-126)
+    if (orig > job.dst_len) { h.status = kStBadLength; return; }
+    bool accepted = orig <= (1ull << 30) || orig <= enc_len * 64;
     if (!accepted) { h.status = kStBadLength; return; }
-    if (orig == 0) {                                                        // codec_tagged.rs:108-110
+    if (orig == 0) {  // codec_tagged.rs:108-110; tans::decompress of 0 symbols
       h.kind = 3;
       if (job.dst_len != 0) h.status = kStBadLength;
       return;
     }
     if (orig != job.dst_len) { h.status = kStBadLength; return; }
-    h.kind = 2;
+    h.kind = job.codec == kCodecTans ? 5 : 2;
   } else {
     h.status = kStBadTag;
     return;
@@ -407,6 +409,99 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
     }
     __syncthreads();
     if (lane == 0) status[blockIdx.x] = h.err ? kStBadStream : kStOk;
+    return;
+  }
+
+  if (h.kind == 5) {
+    // ---- tANS (entropy/tans/mod.rs:372-455): one serial state chain ----
+    // Header: table_log 11, nsym in 2..=256, (sym u8, freq u16) pairs with no
+    // repeat and no zero summing to L = 2048, total_bits u64 <= 8 x stream.
+    __shared__ uint16_t tcum[256];
+    if (lane == 0) {
+      uint32_t st = kStOk, nsym = 0, sum = 0;
+      if (enc_len < 3 || enc[0] != 11) {
+        st = kStBadHeader;
+      } else {
+        nsym = (uint32_t)enc[1] | ((uint32_t)enc[2] << 8);
+        if (nsym < 2 || nsym > 256 || 3 + 3 * (uint64_t)nsym + 8 > enc_len) st = kStBadHeader;
+      }
+      for (int s = 0; s < 256; ++s) rev[s] = 0;  // reuse: normalized frequency per symbol
+      for (uint32_t i = 0; st == kStOk && i < nsym; ++i) {
+        const uint8_t* e = enc + 3 + 3 * i;
+        const uint32_t s = e[0], f = (uint32_t)e[1] | ((uint32_t)e[2] << 8);
+        if (rev[s] != 0 || f == 0) st = kStBadHeader;
+        rev[s] = (uint16_t)f;
+        sum += f;
+      }
+      if (st == kStOk && sum != 2048) st = kStBadHeader;
+      const uint64_t bs_off = 3 + 3 * (uint64_t)nsym + 8;
+      if (st == kStOk) {
+        uint64_t tb = 0;
+        for (int k = 7; k >= 0; --k) tb = (tb << 8) | enc[bs_off - 8 + (uint64_t)k];
+        if (tb > (enc_len - bs_off) * 8) st = kStBadHeader;
+        h.seg_src[0] = bs_off;
+        h.seg_len[0] = tb;  // total bits of the stream
+      }
+      uint32_t run = 0;
+      for (int s = 0; s < 256; ++s) {
+        tcum[s] = (uint16_t)run;
+        run += rev[s];
+      }
+      h.status = st;
+    }
+    __syncthreads();
+    if (h.status != kStOk) {
+      if (lane == 0) status[blockIdx.x] = h.status;
+      return;
+    }
+    // spread (mod.rs:199-211): the k-th placement, in symbol order, lands on
+    // slot k (L/2 + L/8 + 3) mod L; the step is odd, so every slot once
+    for (uint32_t s = lane; s < 256; s += 64)
+      for (uint32_t k = tcum[s], e = tcum[s] + rev[s]; k < e; ++k) table32[(k * 1283u) & 2047u] = s;
+    __syncthreads();
+    if (lane == 0) {
+      // build_decode (mod.rs:346-368): slots in order; the occurrence x of
+      // the slot's symbol runs from norm[s] to 2 norm[s] - 1
+      for (uint32_t u = 0; u < 2048; ++u) {
+        const uint32_t s = table32[u] & 255u;
+        const uint32_t x = rev[s]++;
+        const uint32_t nb = 11u - (31u - (uint32_t)__builtin_clz(x));
+        table32[u] = s | (nb << 8) | (((x << nb) - 2048u) << 16);
+      }
+      // LIFO reader (mod.rs:102-150): pops the nb bits below `pos`; a 64-bit
+      // window of the stream at bit wb serves several pops per reload
+      const uint8_t* bs = enc + h.seg_src[0];
+      const uint64_t bl = enc_len - h.seg_src[0];
+      uint64_t pos = h.seg_len[0], wb = ~0ull, w = 0;
+      bool good = true;
+      auto pop = [&](uint32_t nb) -> uint32_t {
+        if (nb == 0) return 0;
+        if (pos < nb) {
+          good = false;
+          return 0;
+        }
+        const uint64_t start = pos - nb;
+        if (wb == ~0ull || start < wb) {
+          wb = start > 40 ? (start - 40) & ~7ull : 0;
+          w = 0;
+          for (uint64_t k = 0; k < 8; ++k)
+            if ((wb >> 3) + k < bl) w |= (uint64_t)g_ld<uint8_t>((uint64_t)(bs + (wb >> 3) + k)) << (8 * k);
+        }
+        pos = start;
+        return (uint32_t)(w >> (start - wb)) & ((1u << nb) - 1u);
+      };
+      uint32_t state = pop(11);
+      if (state >= 2048u) good = false;
+      for (uint64_t i = 0; good && i < job.dst_len; ++i) {
+        const uint32_t e = table32[state];
+        g_st<uint8_t>((uint64_t)(dst + i), (uint8_t)e);
+        state = (e >> 16) + pop((e >> 8) & 15u);
+        if (state >= 2048u) good = false;
+      }
+      // fully consumed and back at the start state (mod.rs:444-453)
+      if (good && (pos != 0 || state != 0)) good = false;
+      status[blockIdx.x] = good ? kStOk : kStBadStream;
+    }
     return;
   }
 

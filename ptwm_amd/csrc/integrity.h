@@ -5,6 +5,7 @@
 #include <vector>
 
 #include "runtime.h"
+#include "xxh64_host.h"
 
 namespace ptwm {
 
@@ -32,16 +33,6 @@ struct HashTask {  // XXH64 (seed 0) of n device bytes at src (any alignment)
   uint64_t n;
 };
 
-// Streaming XXH64 with seed 0 (hash_host.hip).
-struct Xxh64 {
-  uint64_t v[4];
-  uint64_t total;
-  uint8_t buf[32];
-  uint32_t buf_len;
-  void reset();
-  void update(const uint8_t* p, size_t n);
-  uint64_t digest() const;
-};
 
 bool crc_chain_supported(uint32_t chain);
 
