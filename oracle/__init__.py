@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(HERE, "_build", "libptwm_oracle.so")
 CODEC_IDENTITY = 0x0000
 CODEC_HUFFMAN = 0x0001
 CODEC_RANS = 0x0003
+CODEC_ZSTD = 0x0004
 CODEC_TANS = 0x0007
 
 CHAIN_IEEE16_SPLIT2 = 1
@@ -66,6 +67,8 @@ def lib():
         L.por_rans_decompress.restype = i64
         L.por_rans_decompress.argtypes = [vp, sz, vp, sz]
         L.por_codec_encode.restype = i64
+        L.por_zstd_decompress.argtypes = [vp, sz, vp, sz]
+        L.por_zstd_decompress.restype = C.c_int64
         L.por_tans_compress.argtypes = [vp, sz, vp, sz]
         L.por_tans_compress.restype = C.c_int64
         L.por_tans_decompress.argtypes = [vp, sz, vp, sz]
@@ -193,6 +196,16 @@ def rans_decompress(blob, n_out: int) -> bytes:
     if r < 0:
         raise OracleError(r, "rans_decompress")
     return dst[:n_out].tobytes()
+
+
+def zstd_decompress(blob, cap: int) -> bytes:
+    """RFC 8878 frames (the zstd crate's decode_all, bounded by cap)."""
+    b = _buf(blob)
+    dst = np.zeros(max(cap, 1), np.uint8)
+    r = lib().por_zstd_decompress(_ptr(dst), cap, _ptr(b), b.size)
+    if r < 0:
+        raise OracleError(r, "zstd_decompress")
+    return dst[:r].tobytes()
 
 
 def tans_compress(src) -> bytes:

@@ -969,6 +969,10 @@ int64_t por_codec_decode(int codec, const uint8_t *pl, size_t len, uint8_t *out,
         if (len) memcpy(out, pl, len);
         return (int64_t)len;
     }
+    if (codec == POR_CODEC_ZSTD) {                /* zstd.rs decode_bounded: the payload is the frames */
+        int64_t n = por_zstd_decompress(out, cap, pl, len);
+        return n < 0 ? POR_EINVAL : n;
+    }
     if (codec != POR_CODEC_HUFFMAN && codec != POR_CODEC_RANS && codec != POR_CODEC_TANS) return POR_EUNSUP;
     if (len == 0) return POR_EINVAL;
     uint8_t tag = pl[0];

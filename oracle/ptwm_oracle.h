@@ -38,6 +38,7 @@ extern "C" {
 #define POR_CODEC_IDENTITY 0x0000
 #define POR_CODEC_HUFFMAN  0x0001
 #define POR_CODEC_RANS     0x0003
+#define POR_CODEC_ZSTD     0x0004
 #define POR_CODEC_TANS     0x0007
 
 /* fused chain kinds (transforms/fusion.rs) */
@@ -115,6 +116,11 @@ void por_tans_decode_table(const uint32_t norm[256], uint8_t sym[2048], uint8_t 
 /* blob length, or 0 = store raw (incompressible / one symbol / no gain) */
 int64_t por_tans_compress(uint8_t *dst, size_t cap, const uint8_t *src, size_t n);
 int64_t por_tans_decompress(uint8_t *dst, size_t n, const uint8_t *src, size_t len);
+
+/* ---- Zstd frames (codecs/zstd.rs -> zstd crate decode_all; RFC 8878), zstd_oracle.c ----
+ * one or more frames into out[0..cap); decoded length, or POR_EINVAL for a
+ * malformed payload or more than cap bytes */
+int64_t por_zstd_decompress(uint8_t *out, size_t cap, const uint8_t *src, size_t n);
 
 /* ---- plane codec payloads (codecs/huffman.rs, codecs/rans.rs, identity.rs) ---- */
 /* bound on encoded payload size for a plane of len bytes */

@@ -97,7 +97,8 @@ bool known_codec(uint64_t id) {
 // Plane codecs the device decode takes (runtime.hip parse_plan).
 constexpr uint16_t kHuffIlv = 0x7F01, kRansIlv = 0x7F02;
 bool device_codec(uint16_t c) {
-  return c == 0x0000 || c == 0x0001 || c == 0x0003 || c == 0x0007 || c == kHuffIlv || c == kRansIlv;
+  return c == 0x0000 || c == 0x0001 || c == 0x0003 || c == 0x0004 || c == 0x0007 || c == kHuffIlv ||
+         c == kRansIlv;
 }
 
 // This library's own plane codec contributions (blake3 ids of

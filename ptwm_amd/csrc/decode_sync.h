@@ -46,5 +46,8 @@ constexpr uint64_t kCopyChunk = 65536;
 hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
                                SyncStream* sync_streams, uint16_t* sync_tables, uint64_t* copy_src,
                                hipStream_t stream);
+// Zstd payloads of the job list (zstd_device.hip): one workgroup per job,
+// jobs of other codecs are left to the exact kernel
+hipError_t launch_zstd_decode(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs, hipStream_t stream);
 
 }  // namespace ptwm

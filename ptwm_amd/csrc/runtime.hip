@@ -183,8 +183,8 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
       P.crc32 = T.has_crc ? c.get<uint32_t>() : 0;
       if (!c.ok || (pflags & ~1u)) return kInvalidInput;
       P.chunked = (pflags & 1u) != 0;
-      if (P.codec != kCodecIdentity && P.codec != kCodecHuffman && P.codec != kCodecRans && P.codec != kCodecTans &&
-          P.codec != kCodecHuffIlv && P.codec != kCodecRansIlv)
+      if (P.codec != kCodecIdentity && P.codec != kCodecHuffman && P.codec != kCodecRans && P.codec != kCodecZstd &&
+          P.codec != kCodecTans && P.codec != kCodecHuffIlv && P.codec != kCodecRansIlv)
         return kUnsupported;
       if (P.payload_offset > in_len || in_len - P.payload_offset < P.payload_len) return kInvalidInput;
       if (P.chunked) {

@@ -96,10 +96,10 @@ def test_ptws_frames(orc, path):
     e = ents[0]
     assert e.name == "" and e.hash_checked == path.endswith("_hash.body")
     if e.plan_index >= 0:
-        out = plan_oracle.decode_plan(frame, plan, out_len)
+        out = plan_oracle.decode_plan(frame, plan, out_len)  # checks the frame's hash / CRCs
         raw = out[:e.orig_size]
-        if "stored" in path or e.chain == 6:
-            assert raw == frame[-e.orig_size:] if e.orig_size else True
+        if body[0] & 0x20:  # FLAG_STORED: the body is the raw bytes
+            assert raw == frame[len(frame) - e.orig_size:]
     else:
         assert e.status == -5
 
