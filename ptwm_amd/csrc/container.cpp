@@ -795,8 +795,8 @@ void read_legacy_record(const uint8_t* f, uint64_t off, uint64_t len, const std:
   t.orig = r.u64();
   const uint16_t nl = r.u16();
   t.name_off = off + r.o;
-  t.name_len = nl;
   const uint8_t* name = r.take(nl);
+  t.name_len = name ? nl : 0;  // a name past the record's end is not reported
   if (name && !valid_utf8(name, nl)) r.ok = false;
   r.take((4 - nl % 4) % 4);
   if (flags & 4u) {

@@ -8,6 +8,7 @@
 #include <string>
 #include <vector>
 
+#include "plan_types.h"
 #include "ptwm_common.h"
 
 namespace ptwm {
@@ -115,36 +116,6 @@ struct DevCtx {
 // Returns nullptr if the ordinal is invalid or HIP initialisation fails.
 DevCtx* get_ctx(uint32_t device_ordinal);
 
-// Parsed decode plan (the state bytes of the hardware-backend entry point).
-struct PlanChunk {
-  uint32_t offset_in_payload;
-  uint32_t decoded_size;
-};
-struct PlanPlane {
-  uint32_t codec = 0;
-  bool chunked = false;
-  uint64_t payload_offset = 0;
-  uint64_t payload_len = 0;
-  uint64_t plane_len = 0;
-  uint32_t crc32 = 0;
-  std::vector<PlanChunk> chunks;
-};
-struct PlanTensor {
-  uint64_t out_offset = 0;
-  uint64_t out_len = 0;
-  uint32_t chain = 0;
-  bool has_crc = false;
-  bool has_hash = false;  // xxh64 (seed 0) of the restored tensor
-  uint64_t xxh64 = 0;
-  std::vector<PlanPlane> planes;
-};
-struct Plan {
-  std::vector<PlanTensor> tensors;
-};
-
-// Parse + validate against the input/output buffer sizes.  Returns kOk or
-// kInvalidInput.
-int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint64_t out_len, Plan& plan);
 
 // Decode every tensor of the plan from in_dev into out_dev (device
 // addresses).  Blocks until the work has completed.  Returns kOk or an
@@ -171,8 +142,5 @@ hipError_t launch_split(uint32_t chain, const uint8_t* in, uint64_t plane_len, u
                         hipStream_t stream);
 hipError_t launch_copy(const uint8_t* in, uint8_t* out, uint64_t n, hipStream_t stream);
 
-int chain_planes(uint32_t chain);
-// tensor bytes per plane byte for the chain (2 for bf16 split, 4 for fp32, 1 otherwise)
-int chain_ratio(uint32_t chain);
 
 }  // namespace ptwm

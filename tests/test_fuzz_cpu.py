@@ -1,0 +1,55 @@
+"""Sanitized fuzzing of the parsers of untrusted bytes, on the CPU.
+
+tests/fuzz/fuzz_parsers.cpp is a libFuzzer target over the container reader
+(ptwm_mi355x_container_plan: legacy, PTWC, PTWS) and the decode-plan parser
+(parse_plan), built for the host with AddressSanitizer and
+UndefinedBehaviorSanitizer by tests/fuzz/Makefile (no device code).  The
+seeds are the reference's golden files and the plans read from them; the
+run must end without a sanitizer report, a crash or a broken invariant (a
+plan the reader writes always parses).
+"""
+import glob
+import os
+import shutil
+import subprocess
+
+import pytest
+
+from ptwm_amd import api
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+FUZZ = os.path.join(HERE, "fuzz")
+CLANG = "/opt/rocm/llvm/bin/clang++"
+
+
+def _seeds(d):
+    k = 0
+    for p in sorted(glob.glob(os.path.join(HERE, "golden", "ptwm_files", "*"))):
+        data = open(p, "rb").read()
+        open(os.path.join(d, "f%03d" % k), "wb").write(b"\x00" + data)
+        plan, _, _ = api.container_plan(data)
+        open(os.path.join(d, "p%03d" % k), "wb").write(b"\x01" + plan)
+        k += 1
+    for p in sorted(glob.glob(os.path.join(HERE, "golden", "ptws_frames", "*.body"))):
+        open(os.path.join(d, "s%03d" % k), "wb").write(b"\x00\x89PTWS" + open(p, "rb").read())
+        k += 1
+    # regression: a legacy record whose name runs past the record's end
+    data = bytearray(open(os.path.join(HERE, "golden", "ptwm_files", "legacy_v1_1_0.ptwm"), "rb").read())
+    open(os.path.join(d, "r000"), "wb").write(b"\x00" + bytes(data))
+
+
+@pytest.mark.skipif(not os.path.exists(CLANG), reason="ROCm clang (libFuzzer) not installed")
+def test_parsers_survive_sanitized_fuzzing(tmp_path):
+    r = subprocess.run(["make", "-s", "-C", FUZZ], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    corpus = tmp_path / "corpus"
+    corpus.mkdir()
+    _seeds(str(corpus))
+    exe = os.path.join(FUZZ, "_build", "fuzz_parsers")
+    r = subprocess.run([exe, "-max_total_time=25", "-seed=7", "-max_len=65536", "-rss_limit_mb=4096",
+                        "-artifact_prefix=" + str(tmp_path) + "/", str(corpus)],
+                       capture_output=True, text=True, timeout=300, cwd=str(tmp_path))
+    tail = "\n".join(r.stderr.splitlines()[-25:])
+    assert r.returncode == 0, tail
+    assert "Done" in r.stderr
+    shutil.rmtree(corpus, ignore_errors=True)
