@@ -109,6 +109,8 @@ struct IlvStoreJob {
   uint32_t pad;
 };
 hipError_t launch_ilv_store(const IlvStoreJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream);
+// copies of n bytes from any source alignment to 16-byte aligned dst (shift unused)
+hipError_t launch_ilv_realign(const IlvStoreJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream);
 hipError_t launch_ilv_hist(const IlvEncPlane* planes, uint32_t n_planes, uint64_t max_n, uint32_t* hist,
                            hipStream_t stream);
 hipError_t launch_ilv_size(const IlvEncPlane* planes, const IlvEncBlock* blocks, uint32_t n_blocks,

@@ -1206,6 +1206,42 @@ __global__ void __launch_bounds__(256) ilv_store_kernel(const IlvStoreJob* __res
   }
 }
 
+// Realigned copies of coded payloads (any source alignment) to 16-byte
+// aligned scratch: per 16 output bytes, the five source dwords that hold
+// them, shifted into place with alignbyte.  A source dword is read only if
+// it starts before the payload's end, so no read leaves the dword that holds
+// the payload's last byte.
+__global__ void __launch_bounds__(256) ilv_realign_kernel(const IlvStoreJob* __restrict__ jobs) {
+  const IlvStoreJob J = jobs[blockIdx.y];
+  const uint64_t nvec = (J.n + 15) / 16, end = J.src + J.n;
+  const uint64_t stride = (uint64_t)gridDim.x * 256u;
+  for (uint64_t v = (uint64_t)blockIdx.x * 256u + threadIdx.x; v < nvec; v += stride) {
+    const uint64_t s = J.src + 16 * v, a = s & ~3ull;
+    const uint32_t sh = (uint32_t)(s & 3u);
+    uint32_t w[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) w[k] = a + 4u * k < end ? g_ld<uint32_t>(a + 4u * k) : 0u;
+    const u32x4 o = u32x4_make(__builtin_amdgcn_alignbyte(w[1], w[0], sh), __builtin_amdgcn_alignbyte(w[2], w[1], sh),
+                               __builtin_amdgcn_alignbyte(w[3], w[2], sh), __builtin_amdgcn_alignbyte(w[4], w[3], sh));
+    if (16 * v + 16 <= J.n) {
+      g_st<u32x4>(J.dst + 16 * v, o);
+    } else {
+      for (uint64_t k = 16 * v; k < J.n; ++k) gstore_u8(J.dst + k, o[(k - 16 * v) >> 2] >> (8 * ((k - 16 * v) & 3)));
+    }
+  }
+}
+
+hipError_t launch_ilv_realign(const IlvStoreJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream) {
+  if (!n_jobs) return hipSuccess;
+  uint64_t blocks = (max_n / 16 + 256) / 256;
+  if (blocks > 1024) blocks = 1024;
+  for (uint32_t j0 = 0; j0 < n_jobs; j0 += kMaxGridY) {
+    const uint32_t cnt = n_jobs - j0 < kMaxGridY ? n_jobs - j0 : kMaxGridY;
+    hipLaunchKernelGGL(ilv_realign_kernel, dim3((uint32_t)blocks, cnt), dim3(256), 0, stream, jobs + j0);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_ilv_store(const IlvStoreJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream) {
   if (!n_jobs) return hipSuccess;
   uint64_t blocks = (max_n / 16 + 256) / 256;

@@ -286,18 +286,28 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     for (uint32_t p = 0; p < T.n_planes; ++p)
       if (T.planes[p].coded && (T.planes[p].base & 3u)) realign_bytes = align_up(realign_bytes + T.planes[p].len, 256);
   if (realign_bytes) {
+    // one batched copy for all of them (chunk frames put most payloads of a
+    // chunked plane off 4-byte boundaries)
     PTWM_HIP_TRY(ctx.ilv_realign.ensure(realign_bytes));
-    uint64_t off = 0;
+    std::vector<IlvStoreJob> jobs;
+    uint64_t off = 0, max_n = 0;
     for (IlvTensor& T : tensors)
       for (uint32_t p = 0; p < T.n_planes; ++p) {
         IlvPlane& P = T.planes[p];
         if (!P.coded || !(P.base & 3u)) continue;
         const uint64_t dst = reinterpret_cast<uint64_t>(ctx.ilv_realign.ptr) + off;
-        PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(P.base), P.len,
-                                    hipMemcpyDeviceToDevice, s));
+        jobs.push_back(IlvStoreJob{P.base, dst, P.len, 0, 0});
+        max_n = P.len > max_n ? P.len : max_n;
         P.base = dst;
         off = align_up(off + P.len, 256);
       }
+    const size_t jb = jobs.size() * sizeof(IlvStoreJob);
+    PTWM_HIP_TRY(ctx.realign_jobs.ensure(jb));
+    PTWM_HIP_TRY(ctx.h_realign.ensure(jb));
+    std::memcpy(ctx.h_realign.ptr, jobs.data(), jb);
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.realign_jobs.ptr, ctx.h_realign.ptr, jb, hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(launch_ilv_realign(static_cast<const IlvStoreJob*>(ctx.realign_jobs.ptr), (uint32_t)jobs.size(),
+                                    max_n, s));
   }
   // One persistent launch per chain present.  Per launch: the tensor list,
   // its 4-block tile prefix sums, the LDS table slots (most coded planes of

@@ -82,13 +82,17 @@ struct DevCtx {
   // huff_ilv encoder / decoder scratch
   DeviceBuffer enc_planes, enc_hist, enc_codes, enc_blocks, enc_lane_words, enc_block_bytes, enc_pack;
   DeviceBuffer crc_comb, crc_part;  // CRC combine arguments; fused-decode CRC block partials
-  DeviceBuffer ilv_args, ilv_realign;
+  DeviceBuffer ilv_args, ilv_realign, realign_jobs;
+  PinnedBuffer h_realign;
   // reference-format (Huffman / rANS) encoder scratch
   DeviceBuffer ref_jobs, ref_hist, ref_segs, ref_seglen, ref_codes, ref_rans_tab, ref_rans_segs, ref_rans_scratch,
       ref_rans_len, ref_hdr, ref_pack, ref_ops;
   PinnedBuffer h_enc, h_ilv;
   // parallel Huffman decode of reference streams
   DeviceBuffer sync_streams, sync_tables, sync_sub, sync_waves, copy_args;
+  // chunk frame headers of GPU-native planes (gathered before the decode)
+  DeviceBuffer chunk_addr, chunk_head;
+  PinnedBuffer h_chunk;
   // integrity (CRC-32 / XXH64) tables and arguments
   DeviceBuffer crc_tab, crc_args;
   std::vector<HashWorker> hash_workers;  // XXH64 on host cores (hash_host.hip)

@@ -195,6 +195,121 @@ int64_t execute_plan_noalloc(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uin
   return execute_plan(ctx, plan, in_dev, out_dev);
 }
 
+namespace {
+
+// The five header bytes [ver u8][state_len u32] of each chunk frame.
+__global__ void gather_chunk_heads(const uint64_t* __restrict__ addr, uint32_t n, uint8_t* __restrict__ out) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t a = addr[i];
+#pragma unroll
+  for (uint32_t k = 0; k < 5; ++k) out[8ull * i + k] = g_ld<uint8_t>(a + k);
+}
+
+// Payload ranges of the chunk frames of GPU-native planes (compressor.rs:
+// 316-381 frames [ver][state_len u32][state][payload]; container.rs:
+// 1975-2050 reads them), for the tensors that hold such planes.  The
+// headers live in device memory: one gather kernel and one copy bring them
+// over.  A native chunk carries no codec state (the codecs are stateless,
+// as the plane codec entry points require); an Identity chunk with state
+// keeps its frame for the exact path.  Per tensor, per plane, per chunk:
+// the payload's device address and length (len = UINT64_MAX: keep framed).
+struct ChunkRanges {
+  std::vector<std::vector<std::vector<std::pair<uint64_t, uint64_t>>>> r;  // [t][p][k]
+};
+
+bool native_codec(uint32_t c) { return c == kCodecHuffIlv || c == kCodecRansIlv; }
+
+int64_t chunk_ranges(DevCtx& ctx, const Plan& plan, uint64_t in_dev, ChunkRanges& cr) {
+  const size_t nt = plan.tensors.size();
+  cr.r.assign(nt, {});
+  std::vector<uint64_t> addr;
+  for (size_t t = 0; t < nt; ++t) {
+    const PlanTensor& T = plan.tensors[t];
+    bool any = false;
+    for (const PlanPlane& P : T.planes) any |= P.chunked && native_codec(P.codec);
+    if (!any) continue;
+    cr.r[t].resize(T.planes.size());
+    for (size_t p = 0; p < T.planes.size(); ++p) {
+      const PlanPlane& P = T.planes[p];
+      if (!P.chunked || !(native_codec(P.codec) || P.codec == kCodecIdentity)) continue;
+      for (size_t k = 0; k < P.chunks.size(); ++k) {
+        const uint64_t a = P.chunks[k].offset_in_payload;
+        const uint64_t b = k + 1 < P.chunks.size() ? P.chunks[k + 1].offset_in_payload : P.payload_len;
+        if (b - a < 5) return kInvalidInput;  // container.rs:2011-2015
+        addr.push_back(in_dev + P.payload_offset + a);
+      }
+    }
+  }
+  if (addr.empty()) return kOk;
+  const uint32_t n = (uint32_t)addr.size();
+  PTWM_HIP_TRY(ctx.chunk_addr.ensure(8ull * n));
+  PTWM_HIP_TRY(ctx.chunk_head.ensure(8ull * n));
+  PTWM_HIP_TRY(ctx.h_chunk.ensure(8ull * n));
+  hipStream_t s = ctx.stream;
+  std::memcpy(ctx.h_chunk.ptr, addr.data(), 8ull * n);
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.chunk_addr.ptr, ctx.h_chunk.ptr, 8ull * n, hipMemcpyHostToDevice, s));
+  hipLaunchKernelGGL(gather_chunk_heads, dim3((n + 255) / 256), dim3(256), 0, s,
+                     static_cast<const uint64_t*>(ctx.chunk_addr.ptr), n, static_cast<uint8_t*>(ctx.chunk_head.ptr));
+  PTWM_HIP_TRY(hipGetLastError());
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.h_chunk.ptr, ctx.chunk_head.ptr, 8ull * n, hipMemcpyDeviceToHost, s));
+  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  const uint8_t* h = static_cast<const uint8_t*>(ctx.h_chunk.ptr);
+  size_t j = 0;
+  for (size_t t = 0; t < nt; ++t) {
+    if (cr.r[t].empty()) continue;
+    const PlanTensor& T = plan.tensors[t];
+    for (size_t p = 0; p < T.planes.size(); ++p) {
+      const PlanPlane& P = T.planes[p];
+      if (!P.chunked || !(native_codec(P.codec) || P.codec == kCodecIdentity)) continue;
+      auto& v = cr.r[t][p];
+      for (size_t k = 0; k < P.chunks.size(); ++k, ++j) {
+        const uint64_t a = P.chunks[k].offset_in_payload;
+        const uint64_t b = k + 1 < P.chunks.size() ? P.chunks[k + 1].offset_in_payload : P.payload_len;
+        const uint8_t* hd = h + 8 * j;
+        const uint64_t sl = (uint64_t)hd[1] | ((uint64_t)hd[2] << 8) | ((uint64_t)hd[3] << 16) | ((uint64_t)hd[4] << 24);
+        if (b - a - 5 < sl) return kInvalidInput;  // state_len past the frame (container.rs:2019-2023)
+        if (sl != 0) {
+          if (native_codec(P.codec)) return kInvalidInput;  // a stateless codec given state
+          v.emplace_back(0, UINT64_MAX);
+          continue;
+        }
+        v.emplace_back(in_dev + P.payload_offset + a + 5, b - a - 5);
+      }
+    }
+  }
+  return kOk;
+}
+
+// A tensor whose planes are all chunked GPU-native / Identity planes of one
+// family with the same chunk boundaries, every chunk but the last a whole
+// number of 16384-symbol blocks, decodes in the fused route as one
+// sub-tensor per chunk: chunk k of every plane restores elements
+// [a_k, a_k + size_k) straight into the output, and the CRC block partials
+// of the sub-tensors follow each other as those of the whole tensor would.
+bool chunked_fused_eligible(const PlanTensor& T, uint64_t out_dev, const ChunkRanges& cr, size_t t) {
+  if (cr.r[t].empty() || ((out_dev + T.out_offset) & 15u)) return false;
+  bool any_huff = false, any_rans = false;
+  const PlanPlane& P0 = T.planes[0];
+  for (size_t p = 0; p < T.planes.size(); ++p) {
+    const PlanPlane& P = T.planes[p];
+    if (!P.chunked || P.chunks.size() != P0.chunks.size()) return false;
+    if (P.codec == kCodecHuffIlv) any_huff = true;
+    else if (P.codec == kCodecRansIlv) any_rans = true;
+    else if (P.codec != kCodecIdentity) return false;
+    for (size_t k = 0; k < P.chunks.size(); ++k) {
+      if (P.chunks[k].decoded_size != P0.chunks[k].decoded_size) return false;
+      if (k + 1 < P.chunks.size() && P.chunks[k].decoded_size % kIlvBlock) return false;
+      const auto& rg = cr.r[t][p][k];
+      if (rg.second == UINT64_MAX) return false;
+      if (P.codec == kCodecIdentity && rg.second != P.chunks[k].decoded_size) return false;
+    }
+  }
+  return any_huff != any_rans && (!T.has_crc || crc_chain_supported(T.chain));
+}
+
+}  // namespace
+
 int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t out_dev) {
   // Route 1 (fused): a tensor whose planes are all unchunked Identity or
   // GPU-native payloads of one codec family (huff_ilv or rans_ilv), with at
@@ -211,9 +326,47 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   // partials of their whole blocks (tensor t's from block crc_first[t])
   std::vector<uint32_t> crc_first(nt, kIlvNoCrc);
   uint64_t crc_blocks = 0;
+  ChunkRanges cr;
+  {
+    const int64_t rc = chunk_ranges(ctx, plan, in_dev, cr);
+    if (rc != kOk) return rc;
+  }
   for (size_t t = 0; t < nt; ++t) {
     const PlanTensor& T = plan.tensors[t];
-    if (!fused_eligible(T, out_dev)) continue;
+    if (!fused_eligible(T, out_dev)) {
+      if (!chunked_fused_eligible(T, out_dev, cr, t)) continue;
+      // one sub-tensor per chunk (chunked_fused_eligible)
+      bool any_rans = false;
+      for (const PlanPlane& P : T.planes) any_rans |= P.codec == kCodecRansIlv;
+      fused[t] = 1;
+      const uint64_t n = T.planes[0].plane_len;
+      if (T.has_crc && !any_rans && n > 0) {
+        crc_first[t] = (uint32_t)crc_blocks;
+        crc_blocks += (n + kIlvBlock - 1) / kIlvBlock;
+        if (crc_blocks > 0xFFFFFFFEull) return kInvalidInput;
+      }
+      const uint32_t coded_codec = any_rans ? kCodecRansIlv : kCodecHuffIlv;
+      const uint64_t ratio = (uint64_t)chain_ratio(T.chain);
+      uint64_t a = 0;
+      for (size_t k = 0; k < T.planes[0].chunks.size(); ++k) {
+        IlvTensor X{};
+        X.out = out_dev + T.out_offset + a * ratio;
+        X.n = T.planes[0].chunks[k].decoded_size;
+        X.chain = T.chain;
+        X.n_planes = (uint32_t)T.planes.size();
+        X.family = any_rans ? kFamilyRans : kFamilyHuff;
+        X.crc_first = crc_first[t] == kIlvNoCrc ? kIlvNoCrc : crc_first[t] + (uint32_t)(a / kIlvBlock);
+        for (size_t p = 0; p < T.planes.size(); ++p) {
+          X.planes[p].base = cr.r[t][p][k].first;
+          X.planes[p].len = cr.r[t][p][k].second;
+          X.planes[p].coded = T.planes[p].codec == coded_codec ? 1 : 0;
+          X.planes[p].lut = (uint32_t)p;
+        }
+        if (X.n > 0) ilv.push_back(X);
+        a += X.n;
+      }
+      continue;
+    }
     bool any_rans = false;
     for (const PlanPlane& P : T.planes) any_rans |= P.codec == kCodecRansIlv;
     fused[t] = 1;
@@ -255,7 +408,9 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
       if (P.codec == kCodecIdentity && !P.chunked && P.payload_len == P.plane_len && (direct & 15u) == 0)
         continue;
       const bool native = P.codec == kCodecHuffIlv || P.codec == kCodecRansIlv;
-      if (native && P.chunked) return kUnsupported;
+      if (native && P.chunked)  // chunk k restores at the plane offset a_k: 16-byte aligned stores
+        for (size_t k = 0, a = 0; k < P.chunks.size(); a += P.chunks[k].decoded_size, ++k)
+          if (a & 15u) return kUnsupported;
       scratch_off[t][p] = scratch_bytes;
       scratch_bytes = align_up(scratch_bytes + P.plane_len, 256);
       if (!native) n_jobs += P.chunked ? P.chunks.size() : 1;
@@ -292,6 +447,24 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
       }
       const uint64_t a = scratch_base + scratch_off[t][p];
       plane_addr[t][p] = a;
+      if ((P.codec == kCodecHuffIlv || P.codec == kCodecRansIlv) && P.chunked) {
+        uint64_t off = 0;
+        for (size_t k = 0; k < P.chunks.size(); ++k) {
+          IlvTensor X{};
+          X.out = a + off;
+          X.n = P.chunks[k].decoded_size;
+          X.chain = kChainPassthrough;
+          X.n_planes = 1;
+          X.planes[0].base = cr.r[t][p][k].first;
+          X.planes[0].len = cr.r[t][p][k].second;
+          X.planes[0].coded = 1;
+          X.family = P.codec == kCodecRansIlv ? kFamilyRans : kFamilyHuff;
+          X.crc_first = kIlvNoCrc;
+          if (X.n > 0) ilv.push_back(X);
+          off += P.chunks[k].decoded_size;
+        }
+        continue;
+      }
       if (P.codec == kCodecHuffIlv || P.codec == kCodecRansIlv) {
         if (P.plane_len == 0) continue;
         IlvTensor X{};
