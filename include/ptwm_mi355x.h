@@ -35,7 +35,7 @@ extern "C" {
 /* ===================================================================== */
 
 /* Host-buffer plane codec, PlaneCodecFn (native.rs:62-67).  The codec is this
- * extension's own wire format ("huff_ilv", see DESIGN/INTEGRATION docs):
+ * extension's own wire format ("huff_ilv", its format in ptwm_amd/csrc/huff_ilv.hip):
  * encode/decode run on device 0 through staging copies.  Encode returns -2
  * when out_len is too small. */
 int64_t ptwm_plane_codec_v1_encode(const uint8_t *in, size_t in_len, uint8_t *out, size_t out_len);
@@ -79,7 +79,7 @@ uint64_t ptwm_hardware_backend_v1_cuda_stream_handle(uint32_t device_ordinal);
 
 /* HardwareBackendCudaDispatchDecodeFn (native.rs:112-141): tensor-level
  * decode.  codec_id must be this library's decode-plan id; state_ptr holds a
- * decode plan (PTMD v1, layout in INTEGRATION.md) describing one or more
+ * decode plan (PTMD v1, layout in ptwm_amd/plan.py) describing one or more
  * tensors as the container stores them: chain, and per plane codec id,
  * payload offset/length inside the input buffer, decoded length, optional
  * CRC32 and chunk table.  Every tensor is restored (entropy decode + inverse
@@ -230,7 +230,12 @@ int64_t ptwm_mi355x_set_encode_batch_bytes(uint64_t bytes, uint32_t device_ordin
  * Planes start at 256-byte boundaries of out_dev (256-byte aligned; in_dev
  * 16-byte aligned).  Writes the PTMD v1 plan to plan_out (-2 with
  * *plan_len_out = needed size when plan_cap is too small); returns the bytes
- * used in out_dev, or -2 with *needed_out when out_cap is too small. */
+ * used in out_dev, or -2 with *needed_out when out_cap is too small.
+ * plane_codecs[p] = PTWM_MI355X_CODEC_SELECT picks the plane's codec by the
+ * reference's trial encode (select.rs:27-64): the whole plane's Huffman,
+ * rANS and Identity payload sizes, in that menu order (dispatch.rs:13-49),
+ * the smallest wins and the first on ties; the plan names the winner. */
+#define PTWM_MI355X_CODEC_SELECT 0xFFFFu
 int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t *plane_codecs, uint32_t n_codecs,
                                            uint32_t chunk_size, uint64_t in_dev_ptr, size_t in_len,
                                            uint64_t out_dev_ptr, size_t out_cap, uint8_t *plan_out, size_t plan_cap,

@@ -69,6 +69,8 @@ def lib():
         L.por_codec_encode.restype = i64
         L.por_zstd_decompress.argtypes = [vp, sz, vp, sz]
         L.por_zstd_decompress.restype = C.c_int64
+        L.por_select_encode.argtypes = [vp, sz, vp, sz, vp, vp, sz]
+        L.por_select_encode.restype = C.c_int64
         L.por_tans_compress.argtypes = [vp, sz, vp, sz]
         L.por_tans_compress.restype = C.c_int64
         L.por_tans_decompress.argtypes = [vp, sz, vp, sz]
@@ -256,6 +258,24 @@ def codec_encode(codec: int, plane) -> bytes:
     if n < 0:
         raise OracleError(n, "codec_encode")
     return out[:n].tobytes()
+
+
+# dispatch.rs:13-49 order of the codecs this oracle encodes (Identity last:
+# priority 0 below the entropy coders' 1)
+DEFAULT_MENU = (CODEC_HUFFMAN, CODEC_RANS, CODEC_TANS, CODEC_IDENTITY)
+
+
+def select_encode(plane, menu=DEFAULT_MENU):
+    """select.rs:27-64 trial encode -> (chosen codec, payload)."""
+    s = _buf(plane)
+    m = np.array(menu, np.uint16)
+    cap = int(lib().por_codec_encode_bound(s.size))
+    out = np.zeros(max(cap, 1), np.uint8)
+    ch = np.zeros(1, np.uint16)
+    n = lib().por_select_encode(_ptr(s), s.size, _ptr(m), m.size, _ptr(ch), _ptr(out), cap)
+    if n < 0:
+        raise OracleError(n, "select_encode")
+    return int(ch[0]), out[:n].tobytes()
 
 
 def codec_decode(codec: int, payload, cap: int) -> bytes:

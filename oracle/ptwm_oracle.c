@@ -1001,6 +1001,32 @@ int64_t por_codec_decode(int codec, const uint8_t *pl, size_t len, uint8_t *out,
 }
 
 /* ------------------------------------------------------------------------- */
+/* trial-encode selection: select.rs:27-64 over a menu in dispatch.rs:13-49   */
+/* order; the smallest state + payload wins, the first in the menu on ties    */
+/* ------------------------------------------------------------------------- */
+
+int64_t por_select_encode(const uint8_t *plane, size_t len, const uint16_t *menu, size_t menu_len,
+                          uint16_t *chosen, uint8_t *out, size_t cap) {
+    if (menu_len == 0) return POR_EINVAL;                 /* "empty codec menu" */
+    size_t bound = por_codec_encode_bound(len);
+    uint8_t *tmp = (uint8_t *)malloc(bound ? bound : 1);
+    if (!tmp) return POR_ESMALL;
+    int64_t best = -1;
+    for (size_t i = 0; i < menu_len; i++) {
+        int64_t n = por_codec_encode(menu[i], plane, len, tmp, bound);
+        if (n < 0) { free(tmp); return n; }
+        if (best < 0 || n < best) {                       /* min_by_key keeps the first minimum */
+            if ((size_t)n > cap) { free(tmp); return POR_ESMALL; }
+            best = n;
+            *chosen = menu[i];
+            memcpy(out, tmp, (size_t)n);
+        }
+    }
+    free(tmp);
+    return best;
+}
+
+/* ------------------------------------------------------------------------- */
 /* chunk framing: compressor.rs:316-381, container.rs:1975-2050               */
 /* ------------------------------------------------------------------------- */
 

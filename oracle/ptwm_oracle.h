@@ -123,6 +123,13 @@ int64_t por_tans_decompress(uint8_t *dst, size_t n, const uint8_t *src, size_t l
 int64_t por_zstd_decompress(uint8_t *out, size_t cap, const uint8_t *src, size_t n);
 
 /* ---- plane codec payloads (codecs/huffman.rs, codecs/rans.rs, identity.rs) ---- */
+/* trial-encode selection (select.rs:27-64): every menu codec encodes the
+ * plane, the smallest payload wins, the first in menu order on ties; the
+ * default menu for byte planes restricted to these codecs is dispatch.rs:13-49
+ * order: Huffman, Rans, (Tans, Zstd), Identity.  Returns the payload length,
+ * the winner in *chosen. */
+int64_t por_select_encode(const uint8_t *plane, size_t len, const uint16_t *menu, size_t menu_len,
+                          uint16_t *chosen, uint8_t *out, size_t cap);
 /* bound on encoded payload size for a plane of len bytes */
 size_t por_codec_encode_bound(size_t len);
 int64_t por_codec_encode(int codec, const uint8_t *plane, size_t len, uint8_t *out, size_t cap);

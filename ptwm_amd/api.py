@@ -202,13 +202,17 @@ def encode_tensors_cuda(items, out, device_ordinal: int = 0, codec: str = "huff_
     return rc, bytes(plan_buf[: plan_len.value])
 
 
+CODEC_SELECT = 0xFFFF  # PTWM_MI355X_CODEC_SELECT: trial-encode selection
+
+
 def encode_tensor_ref_cuda(chain: int, plane_codecs, chunk_size: int, src, out,
                            device_ordinal: int = 0) -> tuple[int, bytes]:
     """Tensor-level GPU encode into the reference's plane formats (library
     addition): split by ``chain``; plane p coded with ``plane_codecs[p]``
-    (wire ids 0 Identity, 1 Huffman, 3 rANS), chunked at ``chunk_size``
-    bytes (0: one payload per plane).  Returns (bytes used in ``out``, PTMD
-    decode plan)."""
+    (wire ids 0 Identity, 1 Huffman, 3 rANS, or CODEC_SELECT: the
+    reference's trial encode picks one), chunked at ``chunk_size`` bytes (0:
+    one payload per plane).  Returns (bytes used in ``out``, PTMD decode
+    plan)."""
     L = lib()
     stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
     ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)

@@ -637,9 +637,15 @@ int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane
                                            size_t* plan_len_out, uint64_t* needed_out, uint32_t device_ordinal) {
   const int np = chain_planes(chain);
   if (np < 0 || !plan_out || !plan_len_out || !plane_codecs || n_codecs != (uint32_t)np) return kInvalidInput;
-  for (int p = 0; p < np; ++p)
-    if (plane_codecs[p] != kCodecIdentity && plane_codecs[p] != kCodecHuffman && plane_codecs[p] != kCodecRans)
+  uint32_t codecs[4] = {0, 0, 0, 0};
+  bool select = false;
+  for (int p = 0; p < np; ++p) {
+    codecs[p] = plane_codecs[p];
+    select |= codecs[p] == PTWM_MI355X_CODEC_SELECT;
+    if (codecs[p] != kCodecIdentity && codecs[p] != kCodecHuffman && codecs[p] != kCodecRans &&
+        codecs[p] != PTWM_MI355X_CODEC_SELECT)
       return kUnsupported;
+  }
   const uint64_t ratio = (uint64_t)chain_ratio(chain);
   if (in_len % ratio || (in_dev_ptr & 15u) || (out_dev_ptr & 255u)) return kInvalidInput;
   const uint64_t plane_len = in_len / ratio;
@@ -662,15 +668,48 @@ int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane
   if (plane_len && launch_split(chain, reinterpret_cast<const uint8_t*>(in_dev_ptr), plane_len, pl, ctx.stream) !=
                        hipSuccess)
     return kInvalidInput;
+  if (select) {
+    // trial encode of the whole plane (select.rs:27-64): Huffman, rANS and
+    // Identity sizes in menu order (dispatch.rs:13-49), smallest first wins;
+    // a chunked plane is then chunked with the winner (compressor.rs:316-381)
+    std::vector<RefJob> trial;
+    for (int p = 0; p < np; ++p) {
+      if (codecs[p] != PTWM_MI355X_CODEC_SELECT) continue;
+      if (plane_len == 0) {
+        codecs[p] = kCodecIdentity;  // 0 bytes against a 1-byte raw tag
+        continue;
+      }
+      trial.push_back(RefJob{reinterpret_cast<uint64_t>(pl[p]), plane_len, kCodecHuffman});
+      trial.push_back(RefJob{reinterpret_cast<uint64_t>(pl[p]), plane_len, kCodecRans});
+    }
+    if (!trial.empty()) {
+      RefEncoder t;
+      std::vector<uint64_t> tl;
+      const int64_t rc = t.plan(ctx, trial, tl);
+      if (rc < 0) return rc;
+      size_t j = 0;
+      for (int p = 0; p < np; ++p) {
+        if (codecs[p] != PTWM_MI355X_CODEC_SELECT) continue;
+        uint64_t best = tl[j];
+        codecs[p] = kCodecHuffman;
+        if (tl[j + 1] < best) {
+          best = tl[j + 1];
+          codecs[p] = kCodecRans;
+        }
+        if (plane_len < best) codecs[p] = kCodecIdentity;
+        j += 2;
+      }
+    }
+  }
   // one job per coded chunk; Identity payloads are the bytes themselves
   std::vector<RefJob> jobs;
   std::vector<int> job_of(np * nch, -1);
   for (int p = 0; p < np; ++p)
     for (uint64_t k = 0; k < nch; ++k) {
       const uint64_t a = k * cs, b = std::min(plane_len, a + cs);
-      if (plane_codecs[p] == kCodecIdentity) continue;
+      if (codecs[p] == kCodecIdentity) continue;
       job_of[p * nch + k] = (int)jobs.size();
-      jobs.push_back(RefJob{reinterpret_cast<uint64_t>(pl[p]) + a, b - a, plane_codecs[p]});
+      jobs.push_back(RefJob{reinterpret_cast<uint64_t>(pl[p]) + a, b - a, codecs[p]});
     }
   RefEncoder enc;
   std::vector<uint64_t> plen;
@@ -725,7 +764,7 @@ int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane
   put(&magic, 4); put(&ver, 2); put(&flags, 2); put(&ntens, 4);
   put(&zero64, 8); put(&out_len, 8); put(&ch, 1); put(&npl, 1); put(&tflags, 2);
   for (int p = 0; p < np; ++p) {
-    const uint16_t codec = plane_codecs[p], pf = chunk_size ? 1 : 0;
+    const uint16_t codec = (uint16_t)codecs[p], pf = chunk_size ? 1 : 0;
     const uint32_t n_ch = chunk_size ? (uint32_t)nch : 0;
     put(&codec, 2); put(&pf, 2); put(&n_ch, 4);
     put(&poff[p], 8); put(&plen_total[p], 8); put(&plane_len, 8);

@@ -148,3 +148,36 @@ def test_tensor_ref_encode_matches_reference_and_decodes(name, chain, make, code
     n = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, st,
                                                   out[:used], restored, 0)
     assert n == len(data) and host(restored) == data
+
+
+GPU_MENU = (O.CODEC_HUFFMAN, O.CODEC_RANS, O.CODEC_IDENTITY)  # dispatch.rs:13-49 order of the GPU encoders
+SELECT_TENSORS = [t for t in TENSORS if t[0] in ("c1-bf16", "c2-fp32", "c3-fp8-huf", "c5-mxfp4", "identity-chunked")]
+
+
+@pytest.mark.parametrize("name,chain,make,codecs,chunk", SELECT_TENSORS, ids=[t[0] for t in SELECT_TENSORS])
+def test_trial_encode_selection_matches_the_oracle(name, chain, make, codecs, chunk):
+    """select.rs:27-64 on the device: every plane's codec and payload bytes
+    equal the oracle's trial encode over the same menu."""
+    note(f"trial-encode selection {name}")
+    data = make().contiguous().numpy().tobytes()
+    src = dev(data)
+    out = torch.zeros(2 * len(data) + (1 << 20), dtype=torch.uint8, device="cuda:0")
+    np_ = plan.CHAIN_PLANES[chain]
+    used, st = api.encode_tensor_ref_cuda(chain, [api.CODEC_SELECT] * np_, chunk, src, out, 0)
+    blob = host(out[:used])
+    t = plan.decode_plan(st)[0]
+    planes = O.chain_forward(chain, data)
+    for p, pp in enumerate(t.planes):
+        chosen, whole = O.select_encode(planes[p], GPU_MENU)
+        assert pp.codec == chosen, (name, p, pp.codec, chosen)
+        payload = blob[pp.payload_offset: pp.payload_offset + pp.payload_len]
+        if chunk:
+            want, ent = O.encode_plane_chunked(chosen, planes[p], chunk)
+            assert [tuple(map(int, e)) for e in ent] == [tuple(c) for c in pp.chunks], (name, p)
+        else:
+            want = whole
+        assert payload == want, (name, p)
+    restored = torch.zeros(len(data), dtype=torch.uint8, device="cuda:0")
+    n = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, st,
+                                                  out[:used], restored, 0)
+    assert n == len(data) and host(restored) == data
