@@ -118,6 +118,9 @@ def lib():
         L.por_chain_plane_len.argtypes = [C.c_int, sz]
         L.por_chain_nplanes.restype = C.c_int
         L.por_chain_nplanes.argtypes = [C.c_int]
+        for nm in ("por_int_delta", "por_predictor_xor", "por_mantissa_zero_strip"):
+            getattr(L, nm).restype = C.c_int
+            getattr(L, nm).argtypes = [vp, sz, C.c_uint, C.c_int, vp]
         for nm in ("por_reorder16_buf", "por_revert16_buf", "por_reorder32_buf", "por_revert32_buf"):
             getattr(L, nm).restype = None
             getattr(L, nm).argtypes = [vp, sz]
@@ -387,6 +390,47 @@ def chain_inverse(chain: int, planes) -> bytes:
     if r < 0:
         raise OracleError(r, "chain_inverse")
     return out[:total].tobytes()
+
+
+# ---- plane ops on one terminal plane (chain/dispatch.rs:96-122) ----
+
+PLANE_OP_NONE = 0
+PLANE_OP_INT_DELTA = 1
+PLANE_OP_PREDICTOR_XOR = 2
+PLANE_OP_MANTISSA_ZERO_STRIP = 3
+
+
+def _plane_op(fn: str, data, param: int, inverse: bool) -> bytes:
+    s = _buf(data)
+    out = np.zeros(max(s.size, 1), np.uint8)
+    r = getattr(lib(), fn)(_ptr(s), s.size, param, 1 if inverse else 0, _ptr(out))
+    if r < 0:
+        raise OracleError(r, fn)
+    return out[: s.size].tobytes()
+
+
+def int_delta(data, width: int = 1, inverse: bool = False) -> bytes:
+    """transforms/int_delta.rs: wrapping delta at the element width (forward) or its running sum (inverse)."""
+    return _plane_op("por_int_delta", data, width, inverse)
+
+
+def predictor_xor(data, width: int = 1, inverse: bool = False) -> bytes:
+    """transforms/predictor_xor.rs: fcm prediction residuals (forward) or the recovered values (inverse)."""
+    return _plane_op("por_predictor_xor", data, width, inverse)
+
+
+def mantissa_zero_strip(data, k: int, inverse: bool = False) -> bytes:
+    """transforms/mantissa_zero.rs: b >> k (forward, refused on nonzero low bits) or b << k (inverse)."""
+    return _plane_op("por_mantissa_zero_strip", data, k, inverse)
+
+
+def plane_op(op: int, param: int, data, inverse: bool) -> bytes:
+    """One plane op by its PTMD code (PLANE_OP_*): param = width (deltas) or k (strip)."""
+    if op == PLANE_OP_NONE:
+        return bytes(data)
+    fn = {PLANE_OP_INT_DELTA: int_delta, PLANE_OP_PREDICTOR_XOR: predictor_xor,
+          PLANE_OP_MANTISSA_ZERO_STRIP: mantissa_zero_strip}[op]
+    return fn(data, param, inverse)
 
 
 # ---- Huffman internals ----

@@ -165,6 +165,79 @@ int por_chain_inverse(int chain, const uint8_t *const *pl, size_t n, uint8_t *ou
 }
 
 /* ------------------------------------------------------------------------- */
+/* plane ops on one terminal plane (chain/dispatch.rs:96-122)                 */
+/* ------------------------------------------------------------------------- */
+
+/* little-endian element i of width w (1, 2, 4, 8) */
+static uint64_t ld_elem(const uint8_t *p, unsigned w) {
+    uint64_t v = 0;
+    for (unsigned k = 0; k < w; ++k) v |= (uint64_t)p[k] << (8 * k);
+    return v;
+}
+static void st_elem(uint8_t *p, unsigned w, uint64_t v) {
+    for (unsigned k = 0; k < w; ++k) p[k] = (uint8_t)(v >> (8 * k));
+}
+static uint64_t width_mask(unsigned w) { return w == 8 ? ~0ull : (1ull << (8 * w)) - 1; }
+static int width_ok(unsigned w, size_t len) { return (w == 1 || w == 2 || w == 4 || w == 8) && len % w == 0; }
+
+/* IntDelta (transforms/int_delta.rs:38-46, 134-226): out[0] = in[0],
+ * out[i] = in[i] - in[i-1] (wrapping at the element width); the inverse is
+ * the running wrapping sum.  A length that is not a multiple of the width
+ * is InvalidContainer (:77-83, :104-110). */
+int por_int_delta(const uint8_t *in, size_t len, unsigned width, int inverse, uint8_t *out) {
+    if (!width_ok(width, len)) return POR_EINVAL;
+    const uint64_t m = width_mask(width);
+    uint64_t prev = 0;
+    for (size_t i = 0; i < len; i += width) {
+        const uint64_t v = ld_elem(in + i, width);
+        if (inverse) {
+            prev = i == 0 ? v : (prev + v) & m;
+            st_elem(out + i, width, prev);
+        } else {
+            st_elem(out + i, width, i == 0 ? v : (v - prev) & m);
+            prev = v;
+        }
+    }
+    return 0;
+}
+
+/* PredictorXor (transforms/predictor_xor.rs:10-25, 192-246): a 2^16-entry
+ * table of past values, zeroed per plane; per element the prediction is
+ * table[hash], the residual value ^ prediction, then table[hash] = value
+ * and hash = ((hash << 6) ^ value) & 0xFFFF, starting from hash 0.  The
+ * inverse runs the same recurrence on the recovered values. */
+int por_predictor_xor(const uint8_t *in, size_t len, unsigned width, int inverse, uint8_t *out) {
+    if (!width_ok(width, len)) return POR_EINVAL;
+    if (len == 0) return 0;
+    uint64_t *table = (uint64_t *)calloc(1u << 16, sizeof(uint64_t));
+    if (!table) return POR_ESMALL;
+    uint64_t hash = 0;
+    for (size_t i = 0; i < len; i += width) {
+        const uint64_t x = ld_elem(in + i, width);
+        const uint64_t pred = table[hash];
+        const uint64_t value = inverse ? x ^ pred : x;
+        st_elem(out + i, width, x ^ pred);
+        table[hash] = value;
+        hash = ((hash << 6) ^ value) & 0xFFFFu;
+    }
+    free(table);
+    return 0;
+}
+
+/* MantissaZeroStrip (transforms/mantissa_zero.rs): k in 1..=7 (new(),
+ * chain/dispatch.rs:96-104); forward b >> k, refused when any byte has a
+ * nonzero low k bits; inverse b << k (u8, high bits dropped). */
+int por_mantissa_zero_strip(const uint8_t *in, size_t len, unsigned k, int inverse, uint8_t *out) {
+    if (k < 1 || k > 7) return POR_EINVAL;
+    const uint8_t low = (uint8_t)((1u << k) - 1);
+    if (!inverse)
+        for (size_t i = 0; i < len; ++i)
+            if (in[i] & low) return POR_EINVAL;
+    for (size_t i = 0; i < len; ++i) out[i] = inverse ? (uint8_t)(in[i] << k) : (uint8_t)(in[i] >> k);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
 /* entropy helpers: entropy/mod.rs:34-40, stream_frame.rs:27-62               */
 /* ------------------------------------------------------------------------- */
 

@@ -79,6 +79,15 @@ int64_t por_chain_plane_len(int chain, size_t len);
 int por_chain_forward(int chain, const uint8_t *in, size_t len, uint8_t *const *planes);
 int por_chain_inverse(int chain, const uint8_t *const *planes, size_t plane_len, uint8_t *out);
 
+/* ---- plane ops on one terminal plane (chain/dispatch.rs:96-122); inverse
+ * selects the decode direction; out may not alias in.  0 or POR_EINVAL ---- */
+/* transforms/int_delta.rs: width 1, 2, 4 or 8 bytes per element */
+int por_int_delta(const uint8_t *in, size_t len, unsigned width, int inverse, uint8_t *out);
+/* transforms/predictor_xor.rs: fcm predictor, width 1, 2, 4 or 8 */
+int por_predictor_xor(const uint8_t *in, size_t len, unsigned width, int inverse, uint8_t *out);
+/* transforms/mantissa_zero.rs: k in 1..7; forward refuses nonzero low bits */
+int por_mantissa_zero_strip(const uint8_t *in, size_t len, unsigned k, int inverse, uint8_t *out);
+
 /* ---- entropy helpers ---- */
 void por_histogram(const uint8_t *data, size_t len, uint32_t hist[256]);
 void por_split_four(size_t len, size_t starts[4], size_t ends[4]);

@@ -28,6 +28,14 @@ constexpr uint32_t kCodecTans = 0x0007;   // entropy/tans (single stream, decode
 constexpr uint32_t kCodecHuffIlv = 0x7F01;  // GPU-native interleaved Huffman
 constexpr uint32_t kCodecRansIlv = 0x7F02;  // GPU-native interleaved rANS
 
+// Inverse plane ops on one terminal plane (chain/dispatch.rs:96-122; OpId
+// wire ids 0x0052, 0x0053, 0x0064 of transforms/op.rs).  Parameter: the
+// element width in bytes (IntDelta, PredictorXor) or k (MantissaZeroStrip).
+constexpr uint32_t kPlaneOpNone = 0;
+constexpr uint32_t kPlaneOpIntDelta = 1;
+constexpr uint32_t kPlaneOpPredictorXor = 2;
+constexpr uint32_t kPlaneOpMantissaZeroStrip = 3;
+
 // Chain kinds: the fused reorder+split pairs of transforms/fusion.rs plus
 // the unfused NibbleSplit and BytePassthrough used by the u8 chains.
 enum ChainKind : uint32_t {

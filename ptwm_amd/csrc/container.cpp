@@ -56,6 +56,9 @@ enum : uint16_t {
   kOpByteSplit = 0x0020,
   kOpNibbleSplit = 0x0021,
   kOpBytePassthrough = 0x0030,
+  kOpIntDelta = 0x0052,
+  kOpPredictorXor = 0x0053,
+  kOpMantissaZeroStrip = 0x0064,
 };
 
 struct NamedId {
@@ -558,11 +561,65 @@ enum : uint8_t { kPtmdIeee16 = 1, kPtmdIeee32 = 2, kPtmdE4M3 = 3, kPtmdE5M2 = 4,
 int ptmd_planes(int ch) { return ch == kPtmdIeee32 ? 4 : ch == kPtmdPass ? 1 : 2; }
 int ptmd_ratio(int ch) { return ch == kPtmdIeee16 ? 2 : ch == kPtmdIeee32 ? 4 : 1; }
 
-// Recognise a chain the device restores.  Returns the PTMD chain (0: none)
-// and, per terminal, the plane of that chain it carries.
-int recognise(const Chain& c, std::vector<int>& perm) {
+// The production split chains with one plane op (python/ptwm/preprocessing/
+// _chains.py:360-600): Source -> BitReorderIeee16|32 -> ByteSplit(2|4), and
+// ByteSplit output j -> IntDelta | PredictorXor | MantissaZeroStrip(k) ->
+// terminal, the other outputs terminals themselves.  Returns the PTMD chain
+// (0: another shape, -1: the op's parameters are refused by
+// chain/dispatch.rs:96-122), the terminal-to-plane map and op_flags[j], the
+// PTMD plane flag bits of the op (byte elements: a ByteSplit output).
+int recognise_plane_op(const Chain& c, std::vector<int>& perm, std::vector<uint32_t>& op_flags) {
+  if (c.nodes.size() != 4 || c.nodes[0].op != kOpSource || c.edges.size() != 3) return 0;
+  for (size_t i = 0; i < 2; ++i) {
+    const Edge& e = c.edges[i];
+    if (e.src != i || e.src_out != 0 || e.dst != i + 1 || e.dst_in != 0) return 0;
+  }
+  const Node& split = c.nodes[2];
+  if (split.op != kOpByteSplit || split.params.size() != 1 || !c.nodes[1].params.empty()) return 0;
+  int ch = 0;
+  if (c.nodes[1].op == kOpBitReorderIeee16 && split.params[0] == 2) ch = kPtmdIeee16;
+  else if (c.nodes[1].op == kOpBitReorderIeee32 && split.params[0] == 4) ch = kPtmdIeee32;
+  if (!ch) return 0;
+  const int np = split.params[0];
+  const Edge& e = c.edges[2];
+  if (e.src != 2 || e.src_out >= (uint32_t)np || e.dst != 3 || e.dst_in != 0) return 0;
+  const Node& op = c.nodes[3];
+  uint32_t flags = 0;
+  if (op.op == kOpIntDelta || op.op == kOpPredictorXor) {
+    if (!op.params.empty()) return -1;  // expect_empty_params
+    flags = (op.op == kOpIntDelta ? 1u : 2u) << 1;  // element width 1: code 0
+  } else if (op.op == kOpMantissaZeroStrip) {
+    if (op.params.empty() || op.params[0] < 1 || op.params[0] > 7) return -1;  // MantissaZeroStrip::new
+    flags = (3u << 1) | ((uint32_t)op.params[0] << 3);
+  } else {
+    return 0;
+  }
+  if ((int)c.terms.size() != np) return 0;
+  perm.assign((size_t)np, -1);
+  std::vector<char> seen((size_t)np, 0);
+  for (int k = 0; k < np; ++k) {
+    const Term& t = c.terms[(size_t)k];
+    uint32_t q;
+    if (t.node == 3 && t.out == 0) q = e.src_out;
+    else if (t.node == 2 && t.out < (uint32_t)np && t.out != e.src_out) q = t.out;
+    else return 0;
+    if (seen[q]) return 0;
+    seen[q] = 1;
+    perm[(size_t)k] = (int)q;
+  }
+  op_flags.assign((size_t)np, 0);
+  op_flags[e.src_out] = flags;
+  return ch;
+}
+
+// Recognise a chain the device restores.  Returns the PTMD chain (0: none,
+// -1: refused by the reference), per terminal the plane of that chain it
+// carries, and per plane the PTMD plane-op flag bits.
+int recognise(const Chain& c, std::vector<int>& perm, std::vector<uint32_t>& op_flags) {
   const size_t nn = c.nodes.size();
+  op_flags.clear();
   if (nn == 0 || c.nodes[0].op != kOpSource) return 0;
+  if (nn == 4) return recognise_plane_op(c, perm, op_flags);
   for (size_t i = 1; i < nn; ++i)
     if (!c.nodes[i].params.empty() && c.nodes[i].op != kOpByteSplit) return 0;
   // the node chain must be the spine 0 -> 1 -> ... (one input each)
@@ -589,6 +646,7 @@ int recognise(const Chain& c, std::vector<int>& perm) {
   }
   if (!ch) return 0;
   const int np = ptmd_planes(ch);
+  op_flags.assign((size_t)np, 0);
   if ((int)c.terms.size() != np) return 0;
   perm.assign((size_t)np, -1);
   std::vector<char> seen((size_t)np, 0);
@@ -720,7 +778,9 @@ struct Builder {
     if (!source_len(c.nodes[0].params, slen, sdt)) return kInvalid;
     if (strict ? slen != t.orig : (t.orig > UINT64_MAX / 8 || slen > 8 * t.orig)) return kInvalid;
     std::vector<int> perm;
-    const int ch = recognise(c, perm);
+    std::vector<uint32_t> op_flags;
+    const int ch = recognise(c, perm, op_flags);
+    if (ch < 0) return kInvalid;
     if (!ch) return kUnsup;
     if (!width_ok(ch, sdt)) return kInvalid;
     const int np = ptmd_planes(ch);
@@ -758,7 +818,7 @@ struct Builder {
       while (perm[j] != q) ++j;
       const PlaneRec& p = t.planes[j];
       put(plan, p.codec, 2);
-      put(plan, p.chunked ? 1u : 0u, 2);
+      put(plan, (p.chunked ? 1u : 0u) | op_flags[(size_t)q], 2);
       put(plan, p.chunked ? p.chunks.size() / 2 : 0, 4);
       put(plan, p.payload_off, 8);
       put(plan, p.payload_len, 8);

@@ -88,8 +88,26 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
       P.payload_len = c.get<uint64_t>();
       P.plane_len = c.get<uint64_t>();
       P.crc32 = T.has_crc ? c.get<uint32_t>() : 0;
-      if (!c.ok || (pflags & ~1u)) return kInvalidInput;
+      if (!c.ok || (pflags & ~0x3Fu)) return kInvalidInput;
       P.chunked = (pflags & 1u) != 0;
+      // bits 1-2: inverse plane op; bits 3-5: log2 of its element width
+      // (IntDelta, PredictorXor) or k (MantissaZeroStrip)
+      P.op = (pflags >> 1) & 3u;
+      const uint32_t pc = (pflags >> 3) & 7u;
+      if (P.op == kPlaneOpNone) {
+        if (pc) return kInvalidInput;
+      } else if (P.op == kPlaneOpMantissaZeroStrip) {
+        if (pc == 0) return kInvalidInput;  // mantissa_zero.rs new(): k in 1..=7
+        P.op_param = pc;
+      } else {
+        if (pc > 3) return kInvalidInput;
+        P.op_param = 1u << pc;
+      }
+      // the ops refuse nibble-width planes (int_delta.rs, predictor_xor.rs
+      // reject_nibble; mantissa_zero.rs needs byte elements)
+      if (P.op != kPlaneOpNone && (T.chain == kChainE4m3Nibble || T.chain == kChainE5m2Nibble ||
+                                   T.chain == kChainNibbleSplit))
+        return kInvalidInput;
       if (P.codec != kCodecIdentity && P.codec != kCodecHuffman && P.codec != kCodecRans && P.codec != kCodecZstd &&
           P.codec != kCodecTans && P.codec != kCodecHuffIlv && P.codec != kCodecRansIlv)
         return kUnsupported;
@@ -113,6 +131,8 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
       }
       // every plane of a chain has the same length (fusion.rs inverse checks)
       if (P.plane_len != T.planes[0].plane_len) return kInvalidInput;
+      // a delta op's plane holds whole elements (int_delta.rs:104-110)
+      if ((P.op == kPlaneOpIntDelta || P.op == kPlaneOpPredictorXor) && P.plane_len % P.op_param) return kInvalidInput;
     }
     uint64_t pl = T.planes[0].plane_len;
     if (pl > T.out_len || pl * (uint64_t)chain_ratio(T.chain) != T.out_len) return kInvalidInput;

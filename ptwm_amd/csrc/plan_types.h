@@ -21,6 +21,8 @@ struct PlanPlane {
   uint64_t payload_len = 0;
   uint64_t plane_len = 0;
   uint32_t crc32 = 0;
+  uint32_t op = kPlaneOpNone;  // inverse plane op after the decode (codes.h)
+  uint32_t op_param = 0;       // its element width in bytes, or k
   std::vector<PlanChunk> chunks;
 };
 struct PlanTensor {

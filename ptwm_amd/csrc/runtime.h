@@ -90,6 +90,9 @@ struct DevCtx {
   PinnedBuffer h_enc, h_ilv;
   // parallel Huffman decode of reference streams
   DeviceBuffer sync_streams, sync_tables, sync_sub, sync_waves, copy_args;
+  // inverse plane ops (plane_ops.hip): job list and IntDelta tile sums
+  DeviceBuffer op_jobs, op_sums;
+  PinnedBuffer h_op;
   // chunk frame headers of GPU-native planes (gathered before the decode)
   DeviceBuffer chunk_addr, chunk_head;
   PinnedBuffer h_chunk;

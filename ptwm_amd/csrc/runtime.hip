@@ -16,6 +16,7 @@
 #include "decode_sync.h"
 #include "ilv_host.h"
 #include "integrity.h"
+#include "plane_ops.h"
 #include "runtime.h"
 
 namespace ptwm {
@@ -109,7 +110,7 @@ static inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a
 bool fused_eligible(const PlanTensor& T, uint64_t out_dev) {
   bool any_huff = false, any_rans = false, ok = ((out_dev + T.out_offset) & 15u) == 0;
   for (const PlanPlane& P : T.planes) {
-    if (P.chunked) ok = false;
+    if (P.chunked || P.op != kPlaneOpNone) ok = false;
     if (P.codec == kCodecHuffIlv) any_huff = true;
     else if (P.codec == kCodecRansIlv) any_rans = true;
     else if (P.codec != kCodecIdentity || P.payload_len != P.plane_len) ok = false;
@@ -293,7 +294,7 @@ bool chunked_fused_eligible(const PlanTensor& T, uint64_t out_dev, const ChunkRa
   const PlanPlane& P0 = T.planes[0];
   for (size_t p = 0; p < T.planes.size(); ++p) {
     const PlanPlane& P = T.planes[p];
-    if (!P.chunked || P.chunks.size() != P0.chunks.size()) return false;
+    if (!P.chunked || P.chunks.size() != P0.chunks.size() || P.op != kPlaneOpNone) return false;
     if (P.codec == kCodecHuffIlv) any_huff = true;
     else if (P.codec == kCodecRansIlv) any_rans = true;
     else if (P.codec != kCodecIdentity) return false;
@@ -320,6 +321,9 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   // through their fused kernel's passthrough chain), then the merge kernel
   // runs.
   const size_t nt = plan.tensors.size();
+  for (const PlanTensor& T : plan.tensors)
+    for (const PlanPlane& P : T.planes)
+      if (!plane_op_supported(P.op, P.op_param)) return kUnsupported;
   std::vector<IlvTensor> ilv;
   std::vector<char> fused(nt, 0);
   // huff_ilv tensors with plane CRCs: the decode kernel also writes the CRC
@@ -425,6 +429,19 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     merge_tmp[t] = scratch_bytes;
     scratch_bytes = align_up(scratch_bytes + T.out_len, 256);
   }
+  // planes with an inverse plane op: the op's output in scratch (the
+  // decoded plane stays as it is for its CRC)
+  std::vector<std::vector<uint64_t>> op_off(nt);
+  for (size_t t = 0; t < nt; ++t) {
+    if (fused[t]) continue;
+    const PlanTensor& T = plan.tensors[t];
+    op_off[t].assign(T.planes.size(), kDirect);
+    for (size_t p = 0; p < T.planes.size(); ++p) {
+      if (T.planes[p].op == kPlaneOpNone) continue;
+      op_off[t][p] = scratch_bytes;
+      scratch_bytes = align_up(scratch_bytes + T.planes[p].plane_len, 256);
+    }
+  }
   if (n_jobs > 0xFFFFFFFFull) return kInvalidInput;
   PTWM_HIP_TRY(ctx.planes.ensure(scratch_bytes ? scratch_bytes : 256));
   PTWM_HIP_TRY(ctx.jobs.ensure(n_jobs * sizeof(DecodeJob) + 64));
@@ -529,12 +546,29 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     for (size_t k = 0; k < n_jobs; ++k)
       if (st[k] != kStOk) return kInvalidInput;
   }
+  // inverse plane ops: decoded plane -> the plane the merge reads
+  std::vector<std::vector<uint64_t>> merge_addr = plane_addr;
+  {
+    std::vector<PlaneOpJob> ops;
+    for (size_t t = 0; t < nt; ++t) {
+      if (fused[t]) continue;
+      const PlanTensor& T = plan.tensors[t];
+      for (size_t p = 0; p < T.planes.size(); ++p) {
+        const PlanPlane& P = T.planes[p];
+        if (P.op == kPlaneOpNone) continue;
+        merge_addr[t][p] = scratch_base + op_off[t][p];
+        if (P.plane_len) ops.push_back(PlaneOpJob{plane_addr[t][p], merge_addr[t][p], P.plane_len, P.op, P.op_param, 0, 0});
+      }
+    }
+    const int64_t rc = run_plane_ops(ctx, ops);
+    if (rc != kOk) return rc;
+  }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[1], s));
   for (size_t t = 0; t < nt; ++t) {
     if (fused[t]) continue;
     const PlanTensor& T = plan.tensors[t];
     const uint8_t* pp[4] = {nullptr, nullptr, nullptr, nullptr};
-    for (size_t p = 0; p < T.planes.size(); ++p) pp[p] = reinterpret_cast<const uint8_t*>(plane_addr[t][p]);
+    for (size_t p = 0; p < T.planes.size(); ++p) pp[p] = reinterpret_cast<const uint8_t*>(merge_addr[t][p]);
     uint8_t* out = reinterpret_cast<uint8_t*>(out_dev + T.out_offset);
     if (T.planes[0].plane_len == 0) continue;
     if (merge_tmp[t] == kDirect) {

@@ -12,9 +12,14 @@ Binary layout (little endian), "PTMD" version 1:
     u32 magic 0x444D5450 | u16 version=1 | u16 flags=0 | u32 n_tensors
     tensor: u64 out_offset | u64 out_len | u8 chain | u8 n_planes | u16 flags (bit0 crc, bit1 hash)
             | [u64 xxh64 (seed 0) of the restored tensor if hash flag]
-      plane: u16 codec | u16 flags (bit0 chunked) | u32 n_chunks
+      plane: u16 codec | u16 flags | u32 n_chunks
              | u64 payload_offset | u64 payload_len | u64 plane_len
              | [u32 crc32 if tensor crc flag] | n_chunks x (u32 offset, u32 size)
+      plane flags: bit0 chunked; bits 1-2 the inverse plane op applied to the
+      decoded plane before the merge (0 none, 1 IntDelta, 2 PredictorXor,
+      3 MantissaZeroStrip: chain/dispatch.rs:96-122); bits 3-5 its parameter
+      (log2 of the element width for IntDelta / PredictorXor, k for the strip).
+      The plane CRC covers the decoded plane, before the op (container.rs:2152-2170).
 """
 from __future__ import annotations
 
@@ -30,6 +35,10 @@ CHAIN_PASSTHROUGH = 6
 CHAIN_PLANES = {1: 2, 2: 4, 3: 2, 4: 2, 5: 2, 6: 1}
 CHAIN_RATIO = {1: 2, 2: 4, 3: 1, 4: 1, 5: 1, 6: 1}
 MAGIC = 0x444D5450
+PLANE_OP_NONE = 0
+PLANE_OP_INT_DELTA = 1
+PLANE_OP_PREDICTOR_XOR = 2
+PLANE_OP_MANTISSA_ZERO_STRIP = 3
 
 
 @dataclass
@@ -40,6 +49,8 @@ class PlanePlan:
     plane_len: int
     chunks: list[tuple[int, int]] | None = None   # (offset_in_payload, decoded_size)
     crc32: int | None = None
+    op: int = PLANE_OP_NONE   # inverse plane op after the decode
+    op_param: int = 0         # element width in bytes (deltas) or k (strip)
 
 
 @dataclass
@@ -49,6 +60,14 @@ class TensorPlan:
     out_len: int
     planes: list[PlanePlan] = field(default_factory=list)
     xxh64: int | None = None
+
+
+def _plane_flags(p: PlanePlane) -> int:
+    f = 1 if p.chunks is not None else 0
+    if p.op == PLANE_OP_NONE:
+        return f
+    code = p.op_param if p.op == PLANE_OP_MANTISSA_ZERO_STRIP else p.op_param.bit_length() - 1
+    return f | (p.op << 1) | (code << 3)
 
 
 def encode_plan(tensors: list[TensorPlan]) -> bytes:
@@ -61,7 +80,7 @@ def encode_plan(tensors: list[TensorPlan]) -> bytes:
             out += struct.pack("<Q", t.xxh64)
         for p in t.planes:
             ch = p.chunks or []
-            out += struct.pack("<HHIQQQ", p.codec, 1 if p.chunks is not None else 0, len(ch),
+            out += struct.pack("<HHIQQQ", p.codec, _plane_flags(p), len(ch),
                                p.payload_offset, p.payload_len, p.plane_len)
             if has_crc:
                 out += struct.pack("<I", p.crc32 or 0)
@@ -94,7 +113,9 @@ def decode_plan(buf: bytes) -> list[TensorPlan]:
             if pfl & 1:
                 chunks = [struct.unpack_from("<II", buf, o + 8 * k) for k in range(nch)]
                 o += 8 * nch
-            t.planes.append(PlanePlan(codec, po, pl, plen, chunks, crc))
+            op, code = (pfl >> 1) & 3, (pfl >> 3) & 7
+            param = 0 if op == PLANE_OP_NONE else code if op == PLANE_OP_MANTISSA_ZERO_STRIP else 1 << code
+            t.planes.append(PlanePlan(codec, po, pl, plen, chunks, crc, op, param))
         res.append(t)
     if o != len(buf):
         raise ValueError("trailing bytes in plan")

@@ -104,6 +104,19 @@ def test_ptws_frames(orc, path):
         assert e.status == -5
 
 
+@pytest.mark.parametrize("name,plane", [("bf16_smooth", 1), ("fp32_smooth", 3), ("byte_bf16", 1)])
+def test_smooth_frames_carry_int_delta_on_the_exponent_plane(name, plane):
+    """The reference's smooth-data frames use the split chain with IntDelta on
+    the exponent terminal (_chains.py:360-390, 581-600); the plan carries it
+    as plane op 1 at byte width, on that plane only."""
+    for path in sorted(glob.glob(os.path.join(FRAMES, name + "_*.body"))):
+        plan, ents, _ = api.container_plan(PTWS + _read(path))
+        assert ents[0].status == 0 and ents[0].plan_index == 0
+        t = P.decode_plan(plan)[0]
+        assert [(p.op, p.op_param) for p in t.planes] == [
+            (P.PLANE_OP_INT_DELTA, 1) if i == plane else (P.PLANE_OP_NONE, 0) for i in range(len(t.planes))]
+
+
 def test_reader_rejects_broken_files():
     good = _read(os.path.join(FILES, "legacy_v1_1_0.ptwm"))
     for bad in (b"", b"\x89PTWM", good[:-1], good[:90] + good[91:], b"\x89PTWQ" + good[5:]):

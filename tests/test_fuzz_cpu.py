@@ -31,7 +31,10 @@ def _seeds(d):
         open(os.path.join(d, "p%03d" % k), "wb").write(b"\x01" + plan)
         k += 1
     for p in sorted(glob.glob(os.path.join(HERE, "golden", "ptws_frames", "*.body"))):
-        open(os.path.join(d, "s%03d" % k), "wb").write(b"\x00\x89PTWS" + open(p, "rb").read())
+        frame = b"\x89PTWS" + open(p, "rb").read()
+        open(os.path.join(d, "s%03d" % k), "wb").write(b"\x00" + frame)
+        plan, _, _ = api.container_plan(frame)  # plans with plane ops (the smooth frames)
+        open(os.path.join(d, "q%03d" % k), "wb").write(b"\x01" + plan)
         k += 1
     # regression: a legacy record whose name runs past the record's end
     data = bytearray(open(os.path.join(HERE, "golden", "ptwm_files", "legacy_v1_1_0.ptwm"), "rb").read())
