@@ -118,6 +118,10 @@ def lib():
         L.por_chain_plane_len.argtypes = [C.c_int, sz]
         L.por_chain_nplanes.restype = C.c_int
         L.por_chain_nplanes.argtypes = [C.c_int]
+        L.por_o1sac_decode.restype = i64
+        L.por_o1sac_decode.argtypes = [vp, sz, C.c_uint, vp, sz, sz, vp, sz]
+        L.por_o1sac_encode.restype = i64
+        L.por_o1sac_encode.argtypes = [vp, sz, vp, sz, sz, vp, sz]
         for nm in ("por_int_delta", "por_predictor_xor", "por_mantissa_zero_strip"):
             getattr(L, nm).restype = C.c_int
             getattr(L, nm).argtypes = [vp, sz, C.c_uint, C.c_int, vp]
@@ -390,6 +394,31 @@ def chain_inverse(chain: int, planes) -> bytes:
     if r < 0:
         raise OracleError(r, "chain_inverse")
     return out[:total].tobytes()
+
+
+# ---- Order1ScaleAC (codecs/order1_scale_ac.rs, range_coder.rs) ----
+
+CODEC_O1SAC = 0x0011
+
+
+def o1sac_decode(state, payload, n: int, row_len: int = 0, state_version: int = 1) -> bytes:
+    """n symbols of an Order1ScaleAC payload under `state` (row_len 0: Flat)."""
+    st, p = _buf(state), _buf(payload)
+    out = np.zeros(max(n, 1), np.uint8)
+    r = lib().por_o1sac_decode(_ptr(st), st.size, state_version, _ptr(p), p.size, row_len, _ptr(out), n)
+    if r < 0:
+        raise OracleError(r, "o1sac_decode")
+    return out[:n].tobytes()
+
+
+def o1sac_encode(state, plane, row_len: int = 0) -> bytes:
+    st, s = _buf(state), _buf(plane)
+    cap = 64 + 2 * s.size
+    out = np.zeros(cap, np.uint8)
+    r = lib().por_o1sac_encode(_ptr(st), st.size, _ptr(s), s.size, row_len, _ptr(out), cap)
+    if r < 0:
+        raise OracleError(r, "o1sac_encode")
+    return out[:r].tobytes()
 
 
 # ---- plane ops on one terminal plane (chain/dispatch.rs:96-122) ----

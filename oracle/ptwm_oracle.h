@@ -131,6 +131,16 @@ int64_t por_tans_decompress(uint8_t *dst, size_t n, const uint8_t *src, size_t l
  * malformed payload or more than cap bytes */
 int64_t por_zstd_decompress(uint8_t *out, size_t cap, const uint8_t *src, size_t n);
 
+/* ---- Order1ScaleAC (codecs/order1_scale_ac.rs, range_coder.rs), o1sac_oracle.c ----
+ * state: the codec state bytes ([bitmap 32 B][marginal u16 x 256][rows]);
+ * row_len 0 = Flat layout (one row).  decode: n symbols or POR_EINVAL;
+ * encode: payload length, POR_ESMALL if cap is too small. */
+#define POR_CODEC_O1SAC 0x0011
+int64_t por_o1sac_decode(const uint8_t *state, size_t state_len, unsigned state_version, const uint8_t *payload,
+                         size_t payload_len, size_t row_len, uint8_t *out, size_t n);
+int64_t por_o1sac_encode(const uint8_t *state, size_t state_len, const uint8_t *plane, size_t n, size_t row_len,
+                         uint8_t *out, size_t cap);
+
 /* ---- plane codec payloads (codecs/huffman.rs, codecs/rans.rs, identity.rs) ---- */
 /* trial-encode selection (select.rs:27-64): every menu codec encodes the
  * plane, the smallest payload wins, the first in menu order on ties; the

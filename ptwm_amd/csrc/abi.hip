@@ -306,16 +306,35 @@ int64_t ptwm_plane_codec_v1_encode_cuda(uint8_t state_format_version, const uint
     return rc < 0 ? rc : (int64_t)len[0];
   }
   if (codec != kCodecHuffIlv && codec != kCodecRansIlv) return kUnsupported;
-  if ((in_dev_ptr & 15u) || (out_dev_ptr & 3u)) return kInvalidInput;
   DeviceScope ds(device_ordinal);
   if (!ds.ok) return kInvalidInput;
+  DevCtx& ctx = *ds.ctx;
+  // the encoder reads dwordx4 and writes 4-byte words: a plane or an output
+  // buffer at other alignments (a torch slice) goes through aligned staging
+  uint64_t src = in_dev_ptr, dst = out_dev_ptr;
+  if (in_len && (src & 15u)) {
+    PTWM_HIP_TRY(ctx.stage_in.ensure(in_len + 16));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.stage_in.ptr, reinterpret_cast<const void*>(src), in_len,
+                                hipMemcpyDeviceToDevice, ctx.stream));
+    src = reinterpret_cast<uint64_t>(ctx.stage_in.ptr);
+  }
+  const bool restage = out_cap && (dst & 3u);
+  if (restage) {
+    PTWM_HIP_TRY(ctx.stage_out.ensure(out_cap + 16));
+    dst = reinterpret_cast<uint64_t>(ctx.stage_out.ptr);
+  }
   IlvEncResult r{};
   uint64_t needed = 0, n = in_len;
-  int64_t rc = codec == kCodecHuffIlv
-                   ? ilv_encode_planes(*ds.ctx, &in_dev_ptr, &n, 1, out_dev_ptr, out_cap, false, &r, &needed)
-                   : rilv_encode_planes(*ds.ctx, &in_dev_ptr, &n, 1, out_dev_ptr, out_cap, false, &r, &needed);
+  int64_t rc = codec == kCodecHuffIlv ? ilv_encode_planes(ctx, &src, &n, 1, dst, out_cap, false, &r, &needed)
+                                      : rilv_encode_planes(ctx, &src, &n, 1, dst, out_cap, false, &r, &needed);
   if (rc == kBufferTooSmall && needed_out) *needed_out = needed;
-  return rc < 0 ? rc : (int64_t)r.len;
+  if (rc < 0) return rc;
+  if (restage && r.len) {
+    PTWM_HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(out_dev_ptr), ctx.stage_out.ptr, r.len,
+                                hipMemcpyDeviceToDevice, ctx.stream));
+    PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+  }
+  return (int64_t)r.len;
 }
 
 int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_version, const uint8_t* state_ptr,

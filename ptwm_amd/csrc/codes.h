@@ -25,6 +25,7 @@ constexpr uint32_t kCodecHuffman = 0x0001;
 constexpr uint32_t kCodecRans = 0x0003;
 constexpr uint32_t kCodecZstd = 0x0004;   // RFC 8878 frames (zstd_device.hip)
 constexpr uint32_t kCodecTans = 0x0007;   // entropy/tans (single stream, decode only)
+constexpr uint32_t kCodecO1sac = 0x0011;  // Order1ScaleAC (range coder, stateful, decode only)
 constexpr uint32_t kCodecHuffIlv = 0x7F01;  // GPU-native interleaved Huffman
 constexpr uint32_t kCodecRansIlv = 0x7F02;  // GPU-native interleaved rANS
 

@@ -33,6 +33,7 @@
 // the canonical-form rejections of the compact layouts (minimal
 // encodings are still required of varints).
 #include <algorithm>
+#include <array>
 #include <cstdint>
 #include <cstring>
 #include <string>
@@ -99,8 +100,9 @@ bool known_codec(uint64_t id) {
 
 // Plane codecs the device decode takes (runtime.hip parse_plan).
 constexpr uint16_t kHuffIlv = 0x7F01, kRansIlv = 0x7F02;
+constexpr uint16_t kO1sac = 0x0011;  // Order1ScaleAC (codecs/order1_scale_ac.rs)
 bool device_codec(uint16_t c) {
-  return c == 0x0000 || c == 0x0001 || c == 0x0003 || c == 0x0004 || c == 0x0007 || c == kHuffIlv ||
+  return c == 0x0000 || c == 0x0001 || c == 0x0003 || c == 0x0004 || c == 0x0007 || c == kO1sac || c == kHuffIlv ||
          c == kRansIlv;
 }
 
@@ -676,7 +678,12 @@ bool width_ok(int ch, uint16_t src_dtype) {
 struct PlaneRec {
   uint16_t codec = 0;   // resolved through the Extension Table
   int et_kind = 0;
+  uint8_t role = 0;
   uint8_t state_source = 0;
+  uint8_t state_version = 0;
+  uint16_t state_info = 0;                // shared state id (state_source 2)
+  uint64_t inl_off = 0, inl_len = 0;      // inline state bytes (absolute file offsets)
+  uint32_t row_len = 0;                   // plane layout: 0 Flat, else Rows { row_len }
   uint64_t payload_off = 0, payload_len = 0;  // absolute file offsets
   bool has_crc = false;
   uint32_t crc = 0;
@@ -708,9 +715,10 @@ bool read_legacy_plane(Rd& r, uint64_t base, const std::vector<EtEntry>& et, Pla
   const uint8_t flags = r.u8();
   const uint16_t codec_raw = r.u16();
   const uint16_t cti = r.u16();
+  p.role = role;
   p.state_source = r.u8();
-  r.u8();   // state_version
-  r.u16();  // state_info
+  p.state_version = r.u8();
+  p.state_info = r.u16();
   const uint32_t isl = r.u32();
   p.payload_len = r.u64();
   if (!r.ok || !known_role(role) || !known_codec(codec_raw) || p.state_source > 3) return r.ok = false;
@@ -734,10 +742,13 @@ bool read_legacy_plane(Rd& r, uint64_t base, const std::vector<EtEntry>& et, Pla
   }
   const uint8_t layout = r.u8();
   if (layout == 1) {
-    if (r.u32() == 0) r.ok = false;
+    p.row_len = r.u32();
+    if (p.row_len == 0) r.ok = false;
   } else if (layout != 0) {
     r.ok = false;
   }
+  p.inl_off = base + r.o;
+  p.inl_len = isl;
   r.take(isl);
   if (!r.ok || p.payload_len > r.left()) return r.ok = false;
   p.payload_off = base + r.o;
@@ -746,6 +757,41 @@ bool read_legacy_plane(Rd& r, uint64_t base, const std::vector<EtEntry>& et, Pla
   p.et_kind = et[cti].kind;
   p.codec = et[cti].id;
   return r.ok;
+}
+
+// One shared-state prelude entry (prelude.rs:5-20): the state bytes stay in
+// the file, at [off, off + len).
+struct PreludeEnt {
+  uint16_t id = 0, codec = 0;
+  uint8_t version = 0, mask = 0;
+  uint64_t hash = 0;
+  uint64_t off = 0, len = 0;
+};
+
+// parse_prelude (prelude.rs:65-150); base = file offset of r's start
+bool read_prelude(Rd& r, uint64_t base, std::vector<PreludeEnt>& out) {
+  const uint32_t pc = r.u32();
+  if (!r.ok || pc > r.left() / 22) return false;  // MIN_ENTRY_BYTES
+  out.clear();
+  for (uint32_t i = 0; i < pc; ++i) {
+    PreludeEnt e;
+    e.id = r.u16();
+    e.codec = r.u16();
+    e.version = r.u8();
+    e.mask = r.u8();
+    r.u16();  // reserved
+    e.hash = r.u64();
+    const uint16_t nl = r.u16();
+    const uint8_t* name = r.take(nl);
+    if (!r.ok || !known_codec(e.codec) || !valid_utf8(name, nl)) return false;
+    r.take((4 - nl % 4) % 4);
+    e.len = r.u32();
+    e.off = base + r.o;
+    r.take((size_t)e.len);
+    if (!r.ok) return false;
+    out.push_back(e);
+  }
+  return true;
 }
 
 // ---- plan assembly ---------------------------------------------------------
@@ -761,6 +807,8 @@ struct Builder {
   uint32_t n_plan = 0;
   uint64_t out_len = 0;
   bool strict = false;  // compact layouts: Source length == orig_size
+  const uint8_t* file = nullptr;
+  std::vector<PreludeEnt> prelude;
   Builder() { put(plan, 0x444D5450u, 4), put(plan, 1, 2), put(plan, 0, 2), put(plan, 0, 4); }
 
   // status of one tensor; appends its plan entry when planned
@@ -789,11 +837,35 @@ struct Builder {
     if (t.orig % ratio) return kInvalid;
     const uint64_t plane_len = t.orig / ratio;
     bool all_crc = true, any_crc = false;
-    for (const PlaneRec& p : t.planes) {
+    // per plane: Order1ScaleAC state (offset, length, version)
+    std::vector<std::array<uint64_t, 3>> st(t.planes.size(), {0, 0, 0});
+    for (size_t pi = 0; pi < t.planes.size(); ++pi) {
+      const PlaneRec& p = t.planes[pi];
       if (p.et_kind != 2) return p.et_kind == 1 ? kInvalid : kUnsup;
       if (p.state_source == 3) return kInvalid;  // container.rs:2104-2108
-      if (p.state_source == 2) return kUnsup;    // shared prelude state
       if (!device_codec(p.codec)) return kUnsup;
+      if (p.codec == kO1sac && !p.chunked) {
+        // container.rs:2051-2100: the plane's state, inline or from the
+        // prelude (same version, role covered by applies_to_mask, bytes
+        // matching the stored xxh64); chunked planes carry theirs per frame
+        if (p.state_source == 1) {
+          st[pi] = {p.inl_off, p.inl_len, p.state_version};
+        } else if (p.state_source == 2) {
+          const PreludeEnt* e = nullptr;
+          for (const PreludeEnt& x : prelude)
+            if (x.id == p.state_info) {
+              e = &x;
+              break;
+            }
+          if (!e || p.state_version != e->version) return kInvalid;
+          if (p.role >= 1 && p.role <= 8 && !(e->mask & (1u << (p.role - 1)))) return kInvalid;
+          if (xxh64_once(file + e->off, (size_t)e->len) != e->hash) return kInvalid;
+          st[pi] = {e->off, e->len, e->version};
+        }  // state_source 0: no state; the decode refuses it
+        if (st[pi][1] > 0xFFFFFFFFull) return kInvalid;
+      } else if (p.state_source == 2) {
+        return kUnsup;  // shared state of another codec
+      }
       all_crc &= p.has_crc;
       any_crc |= p.has_crc;
       if (p.chunked) {
@@ -817,13 +889,20 @@ struct Builder {
       size_t j = 0;
       while (perm[j] != q) ++j;
       const PlaneRec& p = t.planes[j];
+      const bool o1 = p.codec == kO1sac;
       put(plan, p.codec, 2);
-      put(plan, (p.chunked ? 1u : 0u) | op_flags[(size_t)q], 2);
+      put(plan, (p.chunked ? 1u : 0u) | op_flags[(size_t)q] | (o1 ? 0x40u : 0u), 2);
       put(plan, p.chunked ? p.chunks.size() / 2 : 0, 4);
       put(plan, p.payload_off, 8);
       put(plan, p.payload_len, 8);
       put(plan, plane_len, 8);
       if (all_crc) put(plan, p.crc, 4);
+      if (o1) {
+        put(plan, st[j][0], 8);
+        put(plan, st[j][1], 4);
+        put(plan, p.row_len, 4);
+        put(plan, st[j][2], 4);
+      }
       for (uint32_t v : p.chunks) put(plan, v, 4);
     }
     chain_out = (uint8_t)ch;
@@ -898,7 +977,8 @@ void read_legacy_record(const uint8_t* f, uint64_t off, uint64_t len, const std:
   if (!r.ok) t.status = kInvalid;
 }
 
-int64_t read_legacy(const uint8_t* f, size_t n, std::vector<TensorRec>& out, std::vector<Chain>& reg) {
+int64_t read_legacy(const uint8_t* f, size_t n, std::vector<TensorRec>& out, std::vector<Chain>& reg,
+                    std::vector<PreludeEnt>& prelude) {
   if (n < 91 + 8 || std::memcmp(f + n - 8, kEofSentinel, 8) != 0) return kInvalid;
   Rd h(f, 91);
   const bool ptwx = std::memcmp(f, kMagicPtwx, 9) == 0;
@@ -917,14 +997,7 @@ int64_t read_legacy(const uint8_t* f, size_t n, std::vector<TensorRec>& out, std
   }
   // prelude, then the chain registry, inside the shared-prelude section
   Rd sp(f + sp_off, (size_t)sp_len);
-  const uint32_t pc = sp.u32();
-  for (uint32_t i = 0; i < pc && sp.ok; ++i) {
-    sp.u16(); sp.u16(); sp.u8(); sp.u8(); sp.u16(); sp.u64();
-    const uint16_t nl = sp.u16();
-    sp.take(nl);
-    sp.take((4 - nl % 4) % 4);
-    sp.take(sp.u32());
-  }
+  if (!read_prelude(sp, sp_off, prelude)) return kInvalid;
   const uint16_t nc = sp.u16();
   if (!sp.ok || nc > 0x8000u) return kInvalid;
   std::vector<uint16_t> reg_ids(nc);
@@ -1037,6 +1110,7 @@ void read_compact_record(const uint8_t* f, uint64_t off, uint64_t len, const std
     if (!r.ok || (pf & 0xC0u)) return fail();
     p.state_source = (pf >> 2) & 3u;
     const uint8_t role = r.u8();
+    p.role = role;
     const uint64_t cref = r.var_max(0xFFFF);
     if (!r.ok || !known_role(role) || cref >= et.size() || et[cref].kind != 2) return fail();
     p.et_kind = 2;
@@ -1045,12 +1119,15 @@ void read_compact_record(const uint8_t* f, uint64_t off, uint64_t len, const std
       const uint8_t v = r.u8();
       const uint64_t info = r.var_max(0xFFFF);
       if (v == 0 && info == 0) return fail();
+      p.state_version = v;
+      p.state_info = (uint16_t)info;
     }
     const size_t inl_len = p.state_source == 1 ? r.var_len() : 0;
     p.payload_len = r.var_len();
     if (pf & 0x10u) {
       const uint64_t row = r.var_max(0xFFFFFFFFull);
       if (row == 0) return fail();
+      p.row_len = (uint32_t)row;
     }
     if (pf & 0x01u) {
       p.has_crc = true;
@@ -1071,6 +1148,8 @@ void read_compact_record(const uint8_t* f, uint64_t off, uint64_t len, const std
       r.u8();
       if (rf & 1u) r.take(32);
     }
+    p.inl_off = off + r.o;
+    p.inl_len = inl_len;
     r.take(inl_len);
     if (!r.ok || p.payload_len > r.left()) return fail();
     p.payload_off = off + r.o;
@@ -1080,7 +1159,8 @@ void read_compact_record(const uint8_t* f, uint64_t off, uint64_t len, const std
   if (!r.done()) return fail();
 }
 
-int64_t read_ptwc(const uint8_t* f, size_t n, std::vector<TensorRec>& out, std::vector<Chain>& reg) {
+int64_t read_ptwc(const uint8_t* f, size_t n, std::vector<TensorRec>& out, std::vector<Chain>& reg,
+                  std::vector<PreludeEnt>& prelude) {
   constexpr size_t kFooter = 16;
   if (n < 9 + 2 + kFooter || std::memcmp(f + n - 8, kEofSentinel, 8) != 0) return kInvalid;
   const size_t footer = n - kFooter;
@@ -1109,19 +1189,9 @@ int64_t read_ptwc(const uint8_t* f, size_t n, std::vector<TensorRec>& out, std::
   if (x.digest() != meta) return kInvalid;
   std::vector<EtEntry> et;
   if (!read_compact_table(f + hdr_end, (size_t)et_len, et)) return kInvalid;
-  // the prelude is parsed within its section (shared state is not planned)
+  // the prelude fills its section exactly
   Rd pr(f + et_end, (size_t)pre_len);
-  if (pre_len) {
-    const uint32_t pc = pr.u32();
-    for (uint32_t i = 0; i < pc && pr.ok; ++i) {
-      pr.u16(); pr.u16(); pr.u8(); pr.u8(); pr.u16(); pr.u64();
-      const uint16_t nl = pr.u16();
-      pr.take(nl);
-      pr.take((4 - nl % 4) % 4);
-      pr.take(pr.u32());
-    }
-    if (!pr.done()) return kInvalid;
-  }
+  if (pre_len && (!read_prelude(pr, et_end, prelude) || !pr.done())) return kInvalid;
   // registry (ptwc.rs:193-227)
   Rd rg(f + pre_end, (size_t)reg_len);
   const uint64_t nc = rg.var_max(0x8000);
@@ -1280,12 +1350,13 @@ int64_t container_plan(const uint8_t* f, size_t n, std::vector<uint8_t>& plan,
   std::vector<TensorRec> recs;
   std::vector<Chain> reg;
   Builder b;
+  b.file = f;
   int64_t rc;
   if (n >= 9 && (std::memcmp(f, kMagicPtwm, 9) == 0 || std::memcmp(f, kMagicPtwx, 9) == 0)) {
-    rc = read_legacy(f, n, recs, reg);
+    rc = read_legacy(f, n, recs, reg, b.prelude);
   } else if (n >= 9 && std::memcmp(f, kMagicPtwc, 9) == 0) {
     b.strict = true;
-    rc = read_ptwc(f, n, recs, reg);
+    rc = read_ptwc(f, n, recs, reg, b.prelude);
   } else if (n >= 5 && std::memcmp(f, kMagicPtws, 5) == 0) {
     b.strict = true;
     rc = read_ptws(f, n, recs);

@@ -234,7 +234,7 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
 
   const uint32_t lane = threadIdx.x;
   const DecodeJob job = jobs[blockIdx.x];
-  if (job.codec == kCodecZstd) return;  // zstd_decode_kernel's job
+  if (job.codec == kCodecZstd || job.codec == kCodecO1sac) return;  // zstd_decode_kernel's / o1sac_decode_kernel's job
   const uint8_t* src = reinterpret_cast<const uint8_t*>(job.src);
   uint8_t* dst = reinterpret_cast<uint8_t*>(job.dst);
 

@@ -49,5 +49,10 @@ hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, 
 // Zstd payloads of the job list (zstd_device.hip): one workgroup per job,
 // jobs of other codecs are left to the exact kernel
 hipError_t launch_zstd_decode(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs, hipStream_t stream);
+// Order1ScaleAC payloads of the job list (o1sac_device.hip): one wavefront
+// per job, jobs of other codecs are left to the other kernels.  A job's
+// state: its chunk frame's, else pad[0..1] = state address, pad[2] = state
+// length | format version << 24; pad[3] = the plane's row length (0 Flat).
+hipError_t launch_o1sac_decode(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs, hipStream_t stream);
 
 }  // namespace ptwm

@@ -439,6 +439,9 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   bool any_zstd = false;
   for (size_t j = 0; j < n_jobs; ++j) any_zstd |= hj[j].codec == kCodecZstd;
   if (any_zstd) PTWM_HIP_TRY(launch_zstd_decode(d_jobs, status, (uint32_t)n_jobs, s));
+  bool any_o1sac = false;
+  for (size_t j = 0; j < n_jobs; ++j) any_o1sac |= hj[j].codec == kCodecO1sac;
+  if (any_o1sac) PTWM_HIP_TRY(launch_o1sac_decode(d_jobs, status, (uint32_t)n_jobs, s));
   if (nck) {
     hipLaunchKernelGGL(raw_copy_kernel, dim3((uint32_t)nck), dim3(256), 0, s, d_jobs, d_copy_src, d_chunk_job,
                        d_job_chunk0);

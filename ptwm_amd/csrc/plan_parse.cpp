@@ -88,7 +88,17 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
       P.payload_len = c.get<uint64_t>();
       P.plane_len = c.get<uint64_t>();
       P.crc32 = T.has_crc ? c.get<uint32_t>() : 0;
-      if (!c.ok || (pflags & ~0x3Fu)) return kInvalidInput;
+      // bit 6: codec state and layout follow (Order1ScaleAC)
+      P.has_state = (pflags & 0x40u) != 0;
+      if (P.has_state) {
+        P.state_offset = c.get<uint64_t>();
+        P.state_len = c.get<uint32_t>();
+        P.row_len = c.get<uint32_t>();
+        P.state_version = c.get<uint32_t>();
+        if (!c.ok || P.state_offset > in_len || in_len - P.state_offset < P.state_len || P.state_version > 255)
+          return kInvalidInput;
+      }
+      if (!c.ok || (pflags & ~0x7Fu)) return kInvalidInput;
       P.chunked = (pflags & 1u) != 0;
       // bits 1-2: inverse plane op; bits 3-5: log2 of its element width
       // (IntDelta, PredictorXor) or k (MantissaZeroStrip)
@@ -109,8 +119,10 @@ int64_t parse_plan(const uint8_t* state, size_t state_len, uint64_t in_len, uint
                                    T.chain == kChainNibbleSplit))
         return kInvalidInput;
       if (P.codec != kCodecIdentity && P.codec != kCodecHuffman && P.codec != kCodecRans && P.codec != kCodecZstd &&
-          P.codec != kCodecTans && P.codec != kCodecHuffIlv && P.codec != kCodecRansIlv)
+          P.codec != kCodecTans && P.codec != kCodecHuffIlv && P.codec != kCodecRansIlv && P.codec != kCodecO1sac)
         return kUnsupported;
+      // Order1ScaleAC needs its state and layout; the other codecs take none
+      if (P.has_state != (P.codec == kCodecO1sac)) return kInvalidInput;
       if (P.payload_offset > in_len || in_len - P.payload_offset < P.payload_len) return kInvalidInput;
       if (P.chunked) {
         if (nch == 0 || nch > (1u << 26) || state_len - c.off < (size_t)nch * 8) return kInvalidInput;

@@ -23,6 +23,12 @@ struct PlanPlane {
   uint32_t crc32 = 0;
   uint32_t op = kPlaneOpNone;  // inverse plane op after the decode (codes.h)
   uint32_t op_param = 0;       // its element width in bytes, or k
+  // codec state and plane layout (Order1ScaleAC): the state bytes at
+  // [state_offset, +state_len) of the input (chunked planes: each chunk
+  // frame's own), its format version, and the row length (0 = Flat)
+  bool has_state = false;
+  uint64_t state_offset = 0;
+  uint32_t state_len = 0, row_len = 0, state_version = 0;
   std::vector<PlanChunk> chunks;
 };
 struct PlanTensor {

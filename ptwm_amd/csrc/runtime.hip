@@ -322,8 +322,12 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
   // runs.
   const size_t nt = plan.tensors.size();
   for (const PlanTensor& T : plan.tensors)
-    for (const PlanPlane& P : T.planes)
+    for (const PlanPlane& P : T.planes) {
       if (!plane_op_supported(P.op, P.op_param)) return kUnsupported;
+      // an Order1ScaleAC state is at most 32 + 512 * 257 bytes
+      // (order1_scale_ac.rs:159-182): a longer one is malformed
+      if (P.has_state && P.state_len > 32u + 512u * 257u) return kInvalidInput;
+    }
   std::vector<IlvTensor> ilv;
   std::vector<char> fused(nt, 0);
   // huff_ilv tensors with plane CRCs: the decode kernel also writes the CRC
@@ -506,6 +510,13 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
         J.dst_len = P.plane_len;
         J.codec = P.codec;
         J.framed = 0;
+        if (P.has_state) {  // Order1ScaleAC: its state and row length
+          const uint64_t sa = in_dev + P.state_offset;
+          J.pad[0] = (uint32_t)sa;
+          J.pad[1] = (uint32_t)(sa >> 32);
+          J.pad[2] = P.state_len | (P.state_version << 24);
+          J.pad[3] = P.row_len;
+        }
         continue;
       }
       uint64_t dst_off = 0;
@@ -520,6 +531,7 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
         J.dst_len = P.chunks[k].decoded_size;
         J.codec = P.codec;
         J.framed = 1;
+        J.pad[3] = P.row_len;  // Order1ScaleAC: chunk frames carry the state
         dst_off += P.chunks[k].decoded_size;
       }
     }

@@ -14,12 +14,18 @@ Binary layout (little endian), "PTMD" version 1:
             | [u64 xxh64 (seed 0) of the restored tensor if hash flag]
       plane: u16 codec | u16 flags | u32 n_chunks
              | u64 payload_offset | u64 payload_len | u64 plane_len
-             | [u32 crc32 if tensor crc flag] | n_chunks x (u32 offset, u32 size)
+             | [u32 crc32 if tensor crc flag]
+             | [u64 state_offset | u32 state_len | u32 row_len | u32 state_version if plane flag bit 6]
+             | n_chunks x (u32 offset, u32 size)
       plane flags: bit0 chunked; bits 1-2 the inverse plane op applied to the
       decoded plane before the merge (0 none, 1 IntDelta, 2 PredictorXor,
       3 MantissaZeroStrip: chain/dispatch.rs:96-122); bits 3-5 its parameter
       (log2 of the element width for IntDelta / PredictorXor, k for the strip).
       The plane CRC covers the decoded plane, before the op (container.rs:2152-2170).
+      Bit 6: the codec state and plane layout of an Order1ScaleAC plane
+      (codecs/order1_scale_ac.rs): the state bytes in the input buffer (a
+      chunked plane's chunk frames carry their own), their format version and
+      the row length (0 = Flat); required for that codec, refused for others.
 """
 from __future__ import annotations
 
@@ -51,6 +57,7 @@ class PlanePlan:
     crc32: int | None = None
     op: int = PLANE_OP_NONE   # inverse plane op after the decode
     op_param: int = 0         # element width in bytes (deltas) or k (strip)
+    state: tuple[int, int, int, int] | None = None  # (offset, length, row_len, version): Order1ScaleAC
 
 
 @dataclass
@@ -63,7 +70,7 @@ class TensorPlan:
 
 
 def _plane_flags(p: PlanePlane) -> int:
-    f = 1 if p.chunks is not None else 0
+    f = (1 if p.chunks is not None else 0) | (0x40 if p.state is not None else 0)
     if p.op == PLANE_OP_NONE:
         return f
     code = p.op_param if p.op == PLANE_OP_MANTISSA_ZERO_STRIP else p.op_param.bit_length() - 1
@@ -84,6 +91,8 @@ def encode_plan(tensors: list[TensorPlan]) -> bytes:
                                p.payload_offset, p.payload_len, p.plane_len)
             if has_crc:
                 out += struct.pack("<I", p.crc32 or 0)
+            if p.state is not None:
+                out += struct.pack("<QIII", *p.state)
             for off, size in ch:
                 out += struct.pack("<II", off, size)
     return bytes(out)
@@ -109,13 +118,17 @@ def decode_plan(buf: bytes) -> list[TensorPlan]:
             if tfl & 1:
                 (crc,) = struct.unpack_from("<I", buf, o)
                 o += 4
+            state = None
+            if pfl & 0x40:
+                state = struct.unpack_from("<QIII", buf, o)
+                o += 20
             chunks = None
             if pfl & 1:
                 chunks = [struct.unpack_from("<II", buf, o + 8 * k) for k in range(nch)]
                 o += 8 * nch
             op, code = (pfl >> 1) & 3, (pfl >> 3) & 7
             param = 0 if op == PLANE_OP_NONE else code if op == PLANE_OP_MANTISSA_ZERO_STRIP else 1 << code
-            t.planes.append(PlanePlan(codec, po, pl, plen, chunks, crc, op, param))
+            t.planes.append(PlanePlan(codec, po, pl, plen, chunks, crc, op, param, state))
         res.append(t)
     if o != len(buf):
         raise ValueError("trailing bytes in plan")

@@ -14,11 +14,27 @@ from ptwm_amd import plan as P
 HUFF_ILV, RANS_ILV = 0x7F01, 0x7F02  # this library's GPU-native codecs (their specification is the oracle's)
 
 
+def _o1sac_plane(data: bytes, p: P.PlanePlan, payload: bytes) -> bytes:
+    """Order1ScaleAC: the plane's state (or each chunk frame's own, container.rs:2010-2049)."""
+    off, ln, row_len, ver = p.state
+    if p.chunks is None:
+        return O.o1sac_decode(data[off:off + ln], payload, p.plane_len, row_len, ver)
+    out = b""
+    for k, (start, size) in enumerate(p.chunks):
+        end = p.chunks[k + 1][0] if k + 1 < len(p.chunks) else len(payload)
+        frame = payload[start:end]
+        sl = int.from_bytes(frame[1:5], "little")
+        out += O.o1sac_decode(frame[5:5 + sl], frame[5 + sl:], size, row_len, frame[0])
+    return out
+
+
 def decode_tensor(data: bytes, t: P.TensorPlan) -> bytes:
     planes = []
     for p in t.planes:
         payload = data[p.payload_offset:p.payload_offset + p.payload_len]
-        if p.chunks is not None:
+        if p.codec == O.CODEC_O1SAC:
+            plane = _o1sac_plane(data, p, payload)
+        elif p.chunks is not None:
             plane = O.decode_plane_chunked(p.codec, payload, p.chunks)
         elif p.codec == HUFF_ILV:
             plane = O.ilv_decode(payload, p.plane_len)

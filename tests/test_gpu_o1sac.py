@@ -1,0 +1,151 @@
+"""Order1ScaleAC (codec 0x0011) payloads decoded on the device against the oracle.
+
+The oracle's decoder is pinned by the reference's golden scale tensors
+(tests/test_oracle_o1sac.py); those files also decode on the device in
+tests/test_gpu_container.py.  Here plans with Order1ScaleAC planes (whole
+payloads with the state in the input, and chunk frames that carry their own
+states) restore bit-exactly, and malformed states or lengths are refused
+with InvalidInput (-1) as the reference refuses them (order1_scale_ac.rs:
+159-203, 411-472).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from ptwm_amd import api, ids, plan as P
+
+import plan_oracle
+from test_oracle_o1sac import make_state, markov_plane
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def dev_bytes(b: bytes):
+    t = torch.empty(max(1, len(b)), dtype=torch.uint8, device="cuda:0")
+    if b:
+        t[: len(b)].copy_(torch.from_numpy(np.frombuffer(b, np.uint8).copy()))
+    return t[: len(b)]
+
+
+def dispatch(state: bytes, blob: bytes, out_len: int) -> bytes:
+    out = torch.full((max(out_len, 1),), 0xA5, dtype=torch.uint8, device="cuda:0")
+    n = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, state,
+                                                  dev_bytes(blob), out[:out_len], 0)
+    torch.cuda.synchronize()
+    assert n >= 0
+    return out[:out_len].cpu().numpy().tobytes()
+
+
+def align(b: bytearray, a=16):
+    b += b"\0" * (-len(b) % a)
+
+
+def plan_for(items):
+    """items: (plane bytes, state bytes, row_len, chunk_size or None).  One
+    passthrough tensor per item; states and payloads at unaligned offsets."""
+    blob = bytearray(b"\x07")
+    tps, out_off = [], 0
+    for plane, st, rl, chunk in items:
+        soff = len(blob)
+        blob += st + b"\x01"
+        if chunk is None:
+            pay = O.o1sac_encode(st, plane, rl)
+            poff = len(blob)
+            blob += pay
+            pp = P.PlanePlan(O.CODEC_O1SAC, poff, len(pay), len(plane), None, O.crc32(plane), state=(soff, len(st), rl, 1))
+        else:
+            poff, body, ents = len(blob), bytearray(), []
+            for a in range(0, len(plane), chunk):
+                part = plane[a:a + chunk]
+                ents.append((len(body), len(part)))
+                body += bytes([1]) + len(st).to_bytes(4, "little") + st + O.o1sac_encode(st, part, rl)
+            blob += body
+            pp = P.PlanePlan(O.CODEC_O1SAC, poff, len(body), len(plane), ents, O.crc32(plane), state=(0, 0, rl, 1))
+        tps.append(P.TensorPlan(P.CHAIN_PASSTHROUGH, out_off, len(plane), [pp], O.xxh64(plane)))
+        out_off = (out_off + len(plane) + 255) // 256 * 256
+    return P.encode_plan(tps), bytes(blob), out_off
+
+
+def check(items):
+    state, blob, out_len = plan_for(items)
+    want = plan_oracle.decode_plan(blob, state, out_len)
+    got = dispatch(state, blob, out_len)
+    for t, (plane, *_r) in zip(P.decode_plan(state), items):
+        assert got[t.out_offset:t.out_offset + t.out_len] == plane
+        assert want[t.out_offset:t.out_offset + t.out_len] == plane
+
+
+@pytest.mark.parametrize("row_len", [0, 1, 5, 128, 4096])
+def test_whole_payloads(row_len):
+    note(f"o1sac whole payload row_len={row_len}")
+    rng = np.random.default_rng(row_len + 10)
+    st = make_state(rng, range(0, 16))
+    n = 5 * 4096 if row_len != 5 else 5 * 3001
+    check([(markov_plane(rng, n, row_len), st, row_len, None)])
+
+
+def test_chunk_frames_and_many_tensors():
+    note("o1sac chunk frames, 12 tensors")
+    rng = np.random.default_rng(21)
+    items = []
+    for i in range(12):
+        st = make_state(rng, rng.choice(256, size=int(rng.integers(0, 40)), replace=False).tolist())
+        rl = [0, 64, 100][i % 3]
+        n = [0, 1, 4096, 10000, 33333 // 100 * 100][i % 5]
+        if rl and n % rl:
+            n = n // rl * rl
+        items.append((markov_plane(rng, n, rl, k=30), st, rl, [None, 1024, 4000][i % 3] if n else None))
+    check(items)
+
+
+def test_scale_plane_of_config_5_size():
+    """An E8M0-like scale plane of 14336 x 128 (config 5), rows of 128."""
+    note("o1sac 14336x128 scale plane")
+    rng = np.random.default_rng(5)
+    e = np.clip(np.round(rng.normal(-6, 1.5, (14336, 128))) + 127, 0, 255).astype(np.uint8)
+    plane = e.tobytes()
+    st = make_state(rng, sorted(set(plane)), skew=2.0)
+    check([(plane, st, 128, None)])
+
+
+def test_malformed_states_and_lengths_are_refused():
+    note("o1sac refusals")
+    rng = np.random.default_rng(8)
+    st = make_state(rng, [1, 2, 3])
+    plane = markov_plane(rng, 3000, 100)
+    state, blob, out_len = plan_for([(plane, st, 100, None)])
+    t = P.decode_plan(state)
+    soff = t[0].planes[0].state[0]
+    cases = []
+    b = bytearray(blob)
+    b[soff + 32] = b[soff + 33] = 0  # a zero count
+    cases.append((state, bytes(b)))
+    b = bytearray(blob)
+    b[soff + 32 + 512 + 3] ^= 4  # a row sum off
+    cases.append((state, bytes(b)))
+    b = bytearray(blob)
+    b[soff] |= 1  # bitmap popcount no longer matches the length
+    cases.append((state, bytes(b)))
+    t2 = P.decode_plan(state)
+    o, ln, rl, v = t2[0].planes[0].state
+    t2[0].planes[0].state = (o, ln, 7, v)  # 7 does not divide 3000
+    cases.append((P.encode_plan(t2), blob))
+    t3 = P.decode_plan(state)
+    t3[0].planes[0].state = (o, ln, rl, 2)  # unknown state version
+    cases.append((P.encode_plan(t3), blob))
+    t4 = P.decode_plan(state)
+    t4[0].planes[0].payload_len = 6  # 3000 symbols cannot fit a 6-byte payload
+    cases.append((P.encode_plan(t4), blob))
+    for k, (s, bl) in enumerate(cases):
+        note(f"refusal case {k}")
+        with pytest.raises(Exception) as ei:
+            dispatch(s, bl, out_len)
+        assert getattr(ei.value, "rc", None) == -1, k
