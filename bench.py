@@ -292,9 +292,13 @@ def build_replica(desc, specs, CH, ref, native, integrity, rep) -> Workload:
     out_off = 0
     plans = []
     torch.cuda.synchronize()   # the generators' kernels are not part of the encode
-    if ref is None and rep == 0:
+    if rep == 0:
         # one untimed call: the encoder's scratch buffers are allocated once per process
-        api.encode_tensors_cuda([(chain, raw) for raw, chain, _ in tensors], blob, 0, codec=native)
+        if ref is None:
+            api.encode_tensors_cuda([(chain, raw) for raw, chain, _ in tensors], blob, 0, codec=native)
+        else:
+            for raw, chain, rf in tensors:
+                api.encode_tensor_ref_cuda(chain, rf[0], rf[1], raw, blob, 0)
         torch.cuda.synchronize()
     t0 = time.perf_counter()
     if ref is None:

@@ -25,6 +25,16 @@ struct RefSegDev {
   uint32_t pad;
 };
 
+// A slice of a Huffman segment packed by one workgroup: symbols
+// [sym0, sym0 + n) of segment seg.
+struct RefSliceDev {
+  uint64_t sym0;
+  uint64_t n;
+  uint32_t seg;
+  uint32_t pad[3];
+};
+constexpr uint64_t kSliceSyms = 1ull << 15;
+
 struct RefCopyOp {
   uint64_t src, dst, n;
   uint64_t rev_from;  // bytes from here on are copied from the source's end backward

@@ -14,14 +14,20 @@
 //   2. host: code tables per job (huffman_host.cpp: the reference tree,
 //      canonical codes and weights header; rANS: normalize_freqs and the
 //      EncSymbol reciprocal parameters of rans/compress.rs:35-122);
-//   3. Huffman: bits per segment (ref_huf_bits_kernel); rANS: each segment
-//      encoded by one lane into scratch (ref_rans_kernel; a segment's state
-//      chain is serial by construction, 64 segments run per wavefront);
+//   3. Huffman: bits per segment from the segment's histogram and the code
+//      lengths (the histograms are taken per split_four segment); rANS:
+//      each segment encoded by one lane into scratch (ref_rans_kernel; a
+//      segment's state chain is serial by construction, 64 segments run
+//      per wavefront);
 //   4. host: payload sizes, coded-or-raw decisions, output layout;
-//   5. Huffman segments packed in parallel (ref_huf_pack_kernel: every
-//      symbol's bit offset is a prefix sum of code lengths, so its final
-//      position in the backward stream is known), then headers, streams and
-//      raw fallbacks placed by one gather launch (ref_copy_kernel).
+//   5. Huffman segments packed in parallel: every symbol's bit offset is a
+//      prefix sum of code lengths, so each segment is cut into slices of
+//      kSliceSyms symbols, the bits of every slice summed
+//      (ref_huf_slice_bits_kernel) and scanned per segment
+//      (ref_huf_slice_scan_kernel), and every slice packed from its offset
+//      by its own workgroup (ref_huf_pack_kernel); then headers, streams
+//      and raw fallbacks placed by one gather launch of 64 KiB pieces
+//      (ref_copy_kernel).
 #include "ref_encode.h"
 
 #include <algorithm>
@@ -75,22 +81,61 @@ __global__ void __launch_bounds__(256) ref_hist_kernel(const RefJobDev* __restri
   if (s) atomicAdd(&hist[256u * blockIdx.y + t], s);
 }
 
-// Huffman: total code bits of each segment.
-__global__ void __launch_bounds__(256) ref_huf_bits_kernel(const RefSegDev* __restrict__ segs,
-                                                           const uint32_t* __restrict__ codes,
-                                                           unsigned long long* __restrict__ seg_bits) {
+// Huffman: total code bits of each slice.  The slice's bytes are read as the
+// aligned words that hold them, one word per thread per step.
+__global__ void __launch_bounds__(256) ref_huf_slice_bits_kernel(const RefSegDev* __restrict__ segs,
+                                                                 const RefSliceDev* __restrict__ slices,
+                                                                 const uint32_t* __restrict__ codes,
+                                                                 unsigned long long* __restrict__ slice_bits) {
   __shared__ uint8_t len[256];
   __shared__ unsigned long long part[4];
-  const RefSegDev S = segs[blockIdx.x];
+  const RefSliceDev L = slices[blockIdx.x];
+  const RefSegDev S = segs[L.seg];
   const uint32_t t = threadIdx.x;
   len[t] = (uint8_t)(codes[256u * S.table + t] >> 16);
   __syncthreads();
+  const uint64_t b0 = S.src + L.sym0, b1 = b0 + L.n, a0 = b0 & ~3ull;
   unsigned long long bits = 0;
-  for (uint64_t i = t; i < S.n; i += 256) bits += len[gbyte(S.src + i)];
+  for (uint64_t a = a0 + 4ull * t; a < b1; a += 1024) {
+    const uint32_t w = g_ld<uint32_t>(a);
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k)
+      if (a + k >= b0 && a + k < b1) bits += len[(w >> (8 * k)) & 0xFFu];
+  }
   for (int d = 32; d >= 1; d >>= 1) bits += __shfl_down(bits, d, 64);
   if ((t & 63u) == 0) part[t >> 6] = bits;
   __syncthreads();
-  if (t == 0) seg_bits[blockIdx.x] = part[0] + part[1] + part[2] + part[3];
+  if (t == 0) slice_bits[blockIdx.x] = part[0] + part[1] + part[2] + part[3];
+}
+
+// Exclusive scan of each segment's slice bits (workgroup g: the slices
+// [first[g], first[g + 1])), in place: each slice's starting bit.
+__global__ void __launch_bounds__(256) ref_huf_slice_scan_kernel(const uint32_t* __restrict__ first,
+                                                                 unsigned long long* __restrict__ slice_bits) {
+  __shared__ unsigned long long wsum[4];
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t s0 = first[blockIdx.x], s1 = first[blockIdx.x + 1];
+  unsigned long long carry = 0;
+  for (uint32_t b = s0; b < s1; b += 256) {
+    const uint32_t i = b + t;
+    const unsigned long long v = i < s1 ? slice_bits[i] : 0ull;
+    unsigned long long incl = v;
+#pragma unroll
+    for (uint32_t d = 1; d < 64; d <<= 1) {
+      const unsigned long long o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    unsigned long long before = 0, tot = 0;
+    for (uint32_t w = 0; w < 4; ++w) {
+      if (w < wave) before += wsum[w];
+      tot += wsum[w];
+    }
+    if (i < s1) slice_bits[i] = carry + before + incl - v;
+    carry += tot;
+    __syncthreads();
+  }
 }
 
 // Huffman: pack one segment's codes (bit-reversed canonical codes,
@@ -98,29 +143,50 @@ __global__ void __launch_bounds__(256) ref_huf_bits_kernel(const RefSegDev* __re
 // logical stream P (bit k = bit k % 8 of byte k / 8) is stored reversed
 // (S[m-1-i] = P[i]); in the segment's word-aligned scratch area of W words
 // whose last m bytes are S, logical word w is the byte-swapped word W-1-w.
-// The area must be zero; words shared by two threads are combined with OR.
+// One workgroup per slice (slice_off: the slice's first bit).  Each pass
+// covers 256 x kPackPerThread symbols: every thread reads its symbols as
+// the aligned words that hold them, a workgroup scan gives each thread its
+// bit offset, the pass's words are assembled in LDS (OR), and written out:
+// the pass's first and last word with a global OR (they may be shared with
+// the neighbouring pass or slice; the area starts zeroed), the others with
+// plain stores.
 constexpr uint32_t kPackPerThread = 8;
+constexpr uint32_t kPackWords = (256u * kPackPerThread * 11u + 31u) / 32u + 2u;
 __global__ void __launch_bounds__(256) ref_huf_pack_kernel(const RefSegDev* __restrict__ segs,
+                                                           const RefSliceDev* __restrict__ slices,
+                                                           const unsigned long long* __restrict__ slice_off,
                                                            const uint32_t* __restrict__ codes,
                                                            uint32_t* __restrict__ scratch) {
   __shared__ uint32_t code[256];
   __shared__ uint32_t wave_sum[4];
-  __shared__ unsigned long long s_base;
-  const RefSegDev S = segs[blockIdx.x];
+  __shared__ uint32_t asm_w[kPackWords];
+  const RefSliceDev L = slices[blockIdx.x];
+  const RefSegDev S = segs[L.seg];
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   code[t] = codes[256u * S.table + t];
-  if (t == 0) s_base = 0;
-  __syncthreads();
+  unsigned long long base = slice_off[blockIdx.x];
   uint32_t* area = scratch + S.scratch_word;
   const uint64_t W = S.words;
-  for (uint64_t pass = 0; pass < S.n; pass += 256ull * kPackPerThread) {
-    const uint64_t i0 = pass + (uint64_t)t * kPackPerThread;
+  const uint64_t src = S.src + L.sym0, end = src + L.n;
+  __syncthreads();
+  for (uint64_t pass = 0; pass < L.n; pass += 256ull * kPackPerThread) {
+    for (uint32_t k = t; k < kPackWords; k += 256) asm_w[k] = 0;
+    // this thread's symbols: bytes [a, a + 8) of the slice, from the three
+    // aligned words that hold them (a word is read only if it starts
+    // before the slice's end, so it holds one of the slice's bytes)
+    const uint64_t a = src + pass + (uint64_t)t * kPackPerThread;
+    const uint64_t aw = a & ~3ull;
+    const uint32_t sh = (uint32_t)(a & 3u);
+    uint32_t w[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) w[k] = aw + 4u * k < end ? g_ld<uint32_t>(aw + 4u * k) : 0u;
+    const uint32_t lo = __builtin_amdgcn_alignbyte(w[1], w[0], sh), hi = __builtin_amdgcn_alignbyte(w[2], w[1], sh);
     uint32_t sym_code[kPackPerThread];
     uint32_t bits = 0;
 #pragma unroll
     for (uint32_t k = 0; k < kPackPerThread; ++k) {
-      const uint64_t i = i0 + k;
-      sym_code[k] = i < S.n ? code[gbyte(S.src + i)] : 0u;
+      const uint32_t b = ((k < 4 ? lo : hi) >> (8 * (k & 3))) & 0xFFu;
+      sym_code[k] = a + k < end ? code[b] : 0u;
       bits += sym_code[k] >> 16;
     }
     // exclusive prefix of bits over the workgroup
@@ -133,30 +199,37 @@ __global__ void __launch_bounds__(256) ref_huf_pack_kernel(const RefSegDev* __re
     if (lane == 63) wave_sum[wave] = incl;
     __syncthreads();
     uint32_t before = 0, pass_bits = 0;
-    for (uint32_t w = 0; w < 4; ++w) {
-      if (w < wave) before += wave_sum[w];
-      pass_bits += wave_sum[w];
+    for (uint32_t v = 0; v < 4; ++v) {
+      if (v < wave) before += wave_sum[v];
+      pass_bits += wave_sum[v];
     }
-    const unsigned long long off = s_base + before + (incl - bits);
-    // pack: acc holds the bits from word (off >> 5) on
-    uint64_t w = off >> 5;
-    uint32_t fill = (uint32_t)(off & 31u);
+    // LDS word j holds the pass's logical word (base >> 5) + j
+    const uint32_t b0 = (uint32_t)(base & 31u);
+    uint32_t off = b0 + before + (incl - bits);
+    uint32_t j = off >> 5, fill = off & 31u;
     uint64_t acc = 0;
 #pragma unroll
     for (uint32_t k = 0; k < kPackPerThread; ++k) {
-      const uint32_t l = sym_code[k] >> 16;
       acc |= (uint64_t)(sym_code[k] & 0xFFFFu) << fill;
-      fill += l;
+      fill += sym_code[k] >> 16;
       if (fill >= 32) {
-        or_global(area + (W - 1 - w), __builtin_bswap32((uint32_t)acc));
+        atomicOr(&asm_w[j], (uint32_t)acc);
         acc >>= 32;
         fill -= 32;
-        ++w;
+        ++j;
       }
     }
-    if (fill) or_global(area + (W - 1 - w), __builtin_bswap32((uint32_t)acc));
+    if (fill) atomicOr(&asm_w[j], (uint32_t)acc);
     __syncthreads();
-    if (t == 0) s_base += pass_bits;
+    const uint32_t nw = (b0 + pass_bits + 31u) >> 5;
+    const uint64_t w0 = base >> 5;
+    for (uint32_t k = t; k < nw; k += 256) {
+      uint32_t* dst = area + (W - 1 - (w0 + k));
+      const uint32_t v = __builtin_bswap32(asm_w[k]);
+      if (k == 0 || k + 1 == nw) or_global(dst, v);
+      else g_st<uint32_t>(reinterpret_cast<uint64_t>(dst), v);
+    }
+    base += pass_bits;
     __syncthreads();
   }
 }
@@ -200,11 +273,24 @@ __global__ void __launch_bounds__(64) ref_rans_kernel(const RefSegDev* __restric
 // Byte copies of a batch of ranges: bytes [0, rev_from) forward, bytes
 // [rev_from, n) taken from the end of the source backward (the rANS renorm
 // bytes, emitted in the reverse of decoder order).
+// The forward part is copied in whole destination words: each is the
+// source's bytes at any alignment, taken from the aligned source words that
+// hold them (a source word is read only when it holds one of the bytes).
 __global__ void __launch_bounds__(256) ref_copy_kernel(const RefCopyOp* __restrict__ ops) {
   const RefCopyOp op = ops[blockIdx.x];
+  const uint32_t t = threadIdx.x;
   const uint64_t fwd = op.rev_from < op.n ? op.rev_from : op.n;
-  for (uint64_t i = threadIdx.x; i < fwd; i += 256) g_st<uint8_t>(op.dst + i, gbyte(op.src + i));
-  for (uint64_t i = fwd + threadIdx.x; i < op.n; i += 256) g_st<uint8_t>(op.dst + i, gbyte(op.src + op.n - 1 - (i - fwd)));
+  const uint64_t head = std::min<uint64_t>(fwd, (4u - (op.dst & 3u)) & 3u);
+  const uint64_t nw = (fwd - head) / 4;
+  for (uint64_t i = t; i < head; i += 256) g_st<uint8_t>(op.dst + i, gbyte(op.src + i));
+  for (uint64_t w = t; w < nw; w += 256) {
+    const uint64_t sa = op.src + head + 4 * w, a = sa & ~3ull;
+    const uint32_t sh = (uint32_t)(sa & 3u);
+    const uint32_t w0 = g_ld<uint32_t>(a), w1 = sh ? g_ld<uint32_t>(a + 4) : 0u;
+    g_st<uint32_t>(op.dst + head + 4 * w, __builtin_amdgcn_alignbyte(w1, w0, sh));
+  }
+  for (uint64_t i = head + 4 * nw + t; i < fwd; i += 256) g_st<uint8_t>(op.dst + i, gbyte(op.src + i));
+  for (uint64_t i = fwd + t; i < op.n; i += 256) g_st<uint8_t>(op.dst + i, gbyte(op.src + op.n - 1 - (i - fwd)));
 }
 
 // ---- host restatements of the reference's table construction ----
@@ -255,30 +341,43 @@ int64_t RefEncoder::plan(DevCtx& ctx, const std::vector<RefJob>& jobs, std::vect
   info_.assign(nj, JobInfo{});
   segs_.clear();
   if (nj == 0) return kOk;
-  // ---- 1. histograms ----
-  std::vector<RefJobDev> jd(nj);
+  // ---- 1. histograms, one per split_four segment (stream_frame.rs:11-62) ----
+  std::vector<RefJobDev> jd;
+  std::vector<uint32_t> sub0(nj, 0);
   uint64_t max_n = 0;
   for (uint32_t j = 0; j < nj; ++j) {
     if (jobs[j].codec != kCodecHuffman && jobs[j].codec != kCodecRans) return kUnsupported;
-    jd[j] = RefJobDev{jobs[j].src, jobs[j].n};
-    max_n = std::max(max_n, jobs[j].n);
+    sub0[j] = (uint32_t)jd.size();
+    if (jobs[j].n == 0) continue;
+    uint64_t st[4], sn[4];
+    split_four(jobs[j].n, st, sn);
+    for (int i = 0; i < 4; ++i) jd.push_back(RefJobDev{jobs[j].src + st[i], sn[i]});
+    max_n = std::max(max_n, sn[0]);
   }
-  PTWM_HIP_TRY(ctx.ref_jobs.ensure(nj * sizeof(RefJobDev)));
-  PTWM_HIP_TRY(ctx.ref_hist.ensure((size_t)nj * 256 * sizeof(uint32_t)));
-  PTWM_HIP_TRY(hipMemcpyAsync(ctx.ref_jobs.ptr, jd.data(), nj * sizeof(RefJobDev), hipMemcpyHostToDevice, s));
-  PTWM_HIP_TRY(hipMemsetAsync(ctx.ref_hist.ptr, 0, (size_t)nj * 256 * sizeof(uint32_t), s));
-  uint64_t hb = (max_n / 16 + 255) / 256;
-  hb = std::max<uint64_t>(1, std::min<uint64_t>(hb, 256));
-  for (uint32_t j0 = 0; j0 < nj; j0 += 65535) {
-    const uint32_t cnt = std::min<uint32_t>(65535, nj - j0);
-    hipLaunchKernelGGL(ref_hist_kernel, dim3((uint32_t)hb, cnt), dim3(256), 0, s,
-                       static_cast<const RefJobDev*>(ctx.ref_jobs.ptr) + j0,
-                       static_cast<uint32_t*>(ctx.ref_hist.ptr) + 256ull * j0);
-    PTWM_HIP_TRY(hipGetLastError());
+  const uint32_t nsub = (uint32_t)jd.size();
+  std::vector<uint32_t> seg_hist((size_t)nsub * 256);
+  if (nsub) {
+    PTWM_HIP_TRY(ctx.ref_jobs.ensure(nsub * sizeof(RefJobDev)));
+    PTWM_HIP_TRY(ctx.ref_hist.ensure((size_t)nsub * 256 * sizeof(uint32_t)));
+    PTWM_HIP_TRY(hipMemcpyAsync(ctx.ref_jobs.ptr, jd.data(), nsub * sizeof(RefJobDev), hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(hipMemsetAsync(ctx.ref_hist.ptr, 0, (size_t)nsub * 256 * sizeof(uint32_t), s));
+    uint64_t hb = (max_n / 16 + 255) / 256;
+    hb = std::max<uint64_t>(1, std::min<uint64_t>(hb, 256));
+    for (uint32_t j0 = 0; j0 < nsub; j0 += 65535) {
+      const uint32_t cnt = std::min<uint32_t>(65535, nsub - j0);
+      hipLaunchKernelGGL(ref_hist_kernel, dim3((uint32_t)hb, cnt), dim3(256), 0, s,
+                         static_cast<const RefJobDev*>(ctx.ref_jobs.ptr) + j0,
+                         static_cast<uint32_t*>(ctx.ref_hist.ptr) + 256ull * j0);
+      PTWM_HIP_TRY(hipGetLastError());
+    }
+    PTWM_HIP_TRY(hipMemcpyAsync(seg_hist.data(), ctx.ref_hist.ptr, seg_hist.size() * 4, hipMemcpyDeviceToHost, s));
+    PTWM_HIP_TRY(hipStreamSynchronize(s));
   }
-  std::vector<uint32_t> hist((size_t)nj * 256);
-  PTWM_HIP_TRY(hipMemcpyAsync(hist.data(), ctx.ref_hist.ptr, hist.size() * 4, hipMemcpyDeviceToHost, s));
-  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  std::vector<uint32_t> hist((size_t)nj * 256, 0);
+  for (uint32_t j = 0; j < nj; ++j)
+    if (jobs[j].n)
+      for (int i = 0; i < 4; ++i)
+        for (int b = 0; b < 256; ++b) hist[256ull * j + b] += seg_hist[256ull * (sub0[j] + i) + b];
   // ---- 2. tables; segments ----
   huf_codes_.assign((size_t)nj * 256, 0);
   rans_tab_.assign((size_t)nj * 256 * 4, 0);
@@ -336,13 +435,14 @@ int64_t RefEncoder::plan(DevCtx& ctx, const std::vector<RefJob>& jobs, std::vect
     PTWM_HIP_TRY(hipMemcpyAsync(ctx.ref_codes.ptr, huf_codes_.data(), huf_codes_.size() * 4, hipMemcpyHostToDevice, s));
     PTWM_HIP_TRY(
         hipMemcpyAsync(ctx.ref_rans_tab.ptr, rans_tab_.data(), rans_tab_.size() * 4, hipMemcpyHostToDevice, s));
-    // ---- 3. Huffman bits per segment; rANS segments encoded ----
-    hipLaunchKernelGGL(ref_huf_bits_kernel, dim3(ns), dim3(256), 0, s, static_cast<const RefSegDev*>(ctx.ref_segs.ptr),
-                       static_cast<const uint32_t*>(ctx.ref_codes.ptr),
-                       static_cast<unsigned long long*>(ctx.ref_seglen.ptr));
-    PTWM_HIP_TRY(hipGetLastError());
-    std::vector<unsigned long long> bits(ns);
-    PTWM_HIP_TRY(hipMemcpyAsync(bits.data(), ctx.ref_seglen.ptr, ns * 8, hipMemcpyDeviceToHost, s));
+    // ---- 3. Huffman bits per segment (its histogram x code lengths); rANS segments encoded ----
+    std::vector<unsigned long long> bits(ns, 0);
+    for (uint32_t g = 0; g < ns; ++g) {
+      const uint32_t j = segs_[g].table;
+      if (jobs[j].codec != kCodecHuffman) continue;
+      const uint32_t* h = &seg_hist[256ull * (sub0[j] + (g - info_[j].seg0))];
+      for (int b = 0; b < 256; ++b) bits[g] += (unsigned long long)h[b] * (huf_codes_[256ull * j + b] >> 16);
+    }
     // the rANS kernel gets the rANS segments only (a Huffman job's rANS
     // table row is empty)
     std::vector<RefSegDev> rsegs;
@@ -448,15 +548,36 @@ int64_t RefEncoder::write(DevCtx& ctx, const std::vector<uint64_t>& dst,
     PTWM_HIP_TRY(ctx.ref_pack.ensure(pack_words_ * 4));
     PTWM_HIP_TRY(hipMemsetAsync(ctx.ref_pack.ptr, 0, pack_words_ * 4, s));
     std::vector<RefSegDev> hs;
-    for (const RefSegDev& g : segs_)
-      if (jobs_[g.table].codec == kCodecHuffman && !info_[g.table].raw && g.n) hs.push_back(g);
+    std::vector<RefSliceDev> sl;
+    std::vector<uint32_t> first;
+    for (const RefSegDev& g : segs_) {
+      if (jobs_[g.table].codec != kCodecHuffman || info_[g.table].raw || !g.n) continue;
+      first.push_back((uint32_t)sl.size());
+      for (uint64_t a = 0; a < g.n; a += kSliceSyms)
+        sl.push_back(RefSliceDev{a, std::min<uint64_t>(kSliceSyms, g.n - a), (uint32_t)hs.size(), {0, 0, 0}});
+      hs.push_back(g);
+    }
+    first.push_back((uint32_t)sl.size());
     if (!hs.empty()) {
-      PTWM_HIP_TRY(ctx.ref_segs.ensure(hs.size() * sizeof(RefSegDev)));
-      PTWM_HIP_TRY(hipMemcpyAsync(ctx.ref_segs.ptr, hs.data(), hs.size() * sizeof(RefSegDev), hipMemcpyHostToDevice,
-                                  s));
-      hipLaunchKernelGGL(ref_huf_pack_kernel, dim3((uint32_t)hs.size()), dim3(256), 0, s,
-                         static_cast<const RefSegDev*>(ctx.ref_segs.ptr),
-                         static_cast<const uint32_t*>(ctx.ref_codes.ptr), static_cast<uint32_t*>(ctx.ref_pack.ptr));
+      if (sl.size() > 0x7FFFFFFFull) return kInternal;
+      const size_t b_seg = hs.size() * sizeof(RefSegDev), b_sl = sl.size() * sizeof(RefSliceDev);
+      PTWM_HIP_TRY(ctx.ref_segs.ensure(b_seg + b_sl + first.size() * 4));
+      PTWM_HIP_TRY(ctx.ref_seglen.ensure(sl.size() * sizeof(unsigned long long)));
+      uint8_t* d = static_cast<uint8_t*>(ctx.ref_segs.ptr);
+      PTWM_HIP_TRY(hipMemcpyAsync(d, hs.data(), b_seg, hipMemcpyHostToDevice, s));
+      PTWM_HIP_TRY(hipMemcpyAsync(d + b_seg, sl.data(), b_sl, hipMemcpyHostToDevice, s));
+      PTWM_HIP_TRY(hipMemcpyAsync(d + b_seg + b_sl, first.data(), first.size() * 4, hipMemcpyHostToDevice, s));
+      const RefSegDev* d_seg = reinterpret_cast<const RefSegDev*>(d);
+      const RefSliceDev* d_sl = reinterpret_cast<const RefSliceDev*>(d + b_seg);
+      const uint32_t* d_first = reinterpret_cast<const uint32_t*>(d + b_seg + b_sl);
+      unsigned long long* d_bits = static_cast<unsigned long long*>(ctx.ref_seglen.ptr);
+      const uint32_t* d_codes = static_cast<const uint32_t*>(ctx.ref_codes.ptr);
+      hipLaunchKernelGGL(ref_huf_slice_bits_kernel, dim3((uint32_t)sl.size()), dim3(256), 0, s, d_seg, d_sl, d_codes,
+                         d_bits);
+      hipLaunchKernelGGL(ref_huf_slice_scan_kernel, dim3((uint32_t)hs.size()), dim3(256), 0, s, d_first, d_bits);
+      hipLaunchKernelGGL(ref_huf_pack_kernel, dim3((uint32_t)sl.size()), dim3(256), 0, s, d_seg, d_sl,
+                         static_cast<const unsigned long long*>(d_bits), d_codes,
+                         static_cast<uint32_t*>(ctx.ref_pack.ptr));
       PTWM_HIP_TRY(hipGetLastError());
     }
   }
@@ -466,18 +587,19 @@ int64_t RefEncoder::write(DevCtx& ctx, const std::vector<uint64_t>& dst,
   for (size_t k = 0; k < literal.size(); ++k)
     if (!literal[k].second.empty())
       ops.push_back(RefCopyOp{hdr_dev + lit_off[k], literal[k].first, literal[k].second.size(), ~0ull});
-  for (const RefCopyOp& c : copies) {
-    // forward copies in pieces of at most 1 MiB, one workgroup each
-    for (uint64_t o = 0; o < c.n; o += (1ull << 20))
-      ops.push_back(RefCopyOp{c.src + o, c.dst + o, std::min<uint64_t>(1ull << 20, c.n - o), ~0ull});
-  }
+  // forward copies in pieces of at most kPiece bytes, one workgroup each
+  constexpr uint64_t kPiece = 64ull << 10;
+  const auto forward = [&](uint64_t src, uint64_t dst_addr, uint64_t n) {
+    for (uint64_t o = 0; o < n; o += kPiece)
+      ops.push_back(RefCopyOp{src + o, dst_addr + o, std::min<uint64_t>(kPiece, n - o), ~0ull});
+  };
+  for (const RefCopyOp& c : copies) forward(c.src, c.dst, c.n);
   for (uint32_t j = 0; j < nj; ++j) {
     const JobInfo& I = info_[j];
     const uint64_t hl = hdr_off[j + 1] - hdr_off[j];
     ops.push_back(RefCopyOp{hdr_dev + hdr_off[j], dst[j], hl, ~0ull});
     if (I.raw) {
-      for (uint64_t o = 0; o < jobs_[j].n; o += (1ull << 20))
-        ops.push_back(RefCopyOp{jobs_[j].src + o, dst[j] + 1 + o, std::min<uint64_t>(1ull << 20, jobs_[j].n - o), ~0ull});
+      forward(jobs_[j].src, dst[j] + 1, jobs_[j].n);
       continue;
     }
     uint64_t o = dst[j] + hl;
@@ -488,7 +610,7 @@ int64_t RefEncoder::write(DevCtx& ctx, const std::vector<uint64_t>& dst,
         if (jobs_[j].codec == kCodecHuffman) {
           // the stream is the last m bytes of the segment's word area
           const uint64_t area = reinterpret_cast<uint64_t>(ctx.ref_pack.ptr) + 4 * g.scratch_word;
-          ops.push_back(RefCopyOp{area + 4 * g.words - m, o, m, ~0ull});
+          forward(area + 4 * g.words - m, o, m);
         } else {
           const uint64_t area = reinterpret_cast<uint64_t>(ctx.ref_rans_scratch.ptr) + g.scratch_byte;
           ops.push_back(RefCopyOp{area, o, m, 4});
