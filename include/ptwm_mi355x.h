@@ -82,7 +82,8 @@ uint64_t ptwm_hardware_backend_v1_cuda_stream_handle(uint32_t device_ordinal);
  * decode plan (PTMD v1, layout in ptwm_amd/plan.py) describing one or more
  * tensors as the container stores them: chain, and per plane codec id,
  * payload offset/length inside the input buffer, decoded length, optional
- * CRC32 and chunk table.  Every tensor is restored (entropy decode + inverse
+ * CRC32, chunk table, inverse plane op (IntDelta, PredictorXor,
+ * MantissaZeroStrip) and codec state with row layout (Order1ScaleAC).  Every tensor is restored (entropy decode + inverse
  * chain) into the output buffer at its stated offset.  Returns the number of
  * restored bytes. */
 int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_version, const uint8_t *state_ptr,
