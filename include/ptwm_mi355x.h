@@ -242,6 +242,36 @@ int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t *plane
                                            uint64_t out_dev_ptr, size_t out_cap, uint8_t *plan_out, size_t plan_cap,
                                            size_t *plan_len_out, uint64_t *needed_out, uint32_t device_ordinal);
 
+/* Tensor-level encode into the reference's plane formats with plane ops
+ * (library addition): as ptwm_mi355x_encode_tensor_ref_cuda, and plane p is
+ * passed through plane_ops[p] before its codec, as the reference's split
+ * chains with one plane op do (python/ptwm/preprocessing/_chains.py:360-600,
+ * chain/dispatch.rs:96-122): 0 none, else op | param << 8 with op
+ * PTWM_MI355X_PLANE_OP_INT_DELTA (param: element width 1, 2, 4 or 8 bytes),
+ * PTWM_MI355X_PLANE_OP_PREDICTOR_XOR (width 1 or 2) or
+ * PTWM_MI355X_PLANE_OP_MANTISSA_ZERO_STRIP (param: k in 1..7; a plane with a
+ * nonzero low k bits is refused with -1, as the reference's forward fails).
+ * The plan carries the ops; the plane CRCs a caller adds cover the planes as
+ * coded.  chain_trial = 1 (plane_ops ignored, may be NULL; ieee16 and ieee32
+ * chains): the reference's chain trial (compressor.rs:504-640) among the
+ * production variants of that chain (_chains.py:1146-1185, the plane-codec
+ * ones): the plain split, IntDelta and PredictorXor on the exponent plane,
+ * MantissaZeroStrip k = 1..4 on the (low) mantissa plane, in that order;
+ * every variant's planes sized with plane_codecs (CODEC_SELECT: the
+ * reference's selection), the smallest total of plane payloads wins, the
+ * first on ties, and a variant whose op refuses its plane is skipped.
+ * ops_out (may be NULL) receives the chosen op per plane.  PredictorXor is
+ * one serial recurrence per plane on the device (slow on large planes). */
+#define PTWM_MI355X_PLANE_OP_INT_DELTA 1u
+#define PTWM_MI355X_PLANE_OP_PREDICTOR_XOR 2u
+#define PTWM_MI355X_PLANE_OP_MANTISSA_ZERO_STRIP 3u
+int64_t ptwm_mi355x_encode_tensor_ref_ops_cuda(uint32_t chain, const uint16_t *plane_codecs,
+                                               const uint16_t *plane_ops, uint32_t n_planes, uint32_t chain_trial,
+                                               uint32_t chunk_size, uint64_t in_dev_ptr, size_t in_len,
+                                               uint64_t out_dev_ptr, size_t out_cap, uint8_t *plan_out,
+                                               size_t plan_cap, size_t *plan_len_out, uint64_t *needed_out,
+                                               uint16_t *ops_out, uint32_t device_ordinal);
+
 /* CRC-32/ISO-HDLC of every plane of a device tensor: the tensor at in_dev is
  * split by `chain` (any alignment) and crc_out[p] receives crc32fast::hash of
  * plane p, the checksum the reference stores per plane record and verifies

@@ -462,6 +462,47 @@ def plane_op(op: int, param: int, data, inverse: bool) -> bytes:
     return fn(data, param, inverse)
 
 
+# ---- chain trial (compressor.rs:504-640) over the split chains' plane-op variants ----
+
+def split_chain_variants(chain: int):
+    """The production split-chain variants that stay within the plane codec
+    (python/ptwm/preprocessing/_chains.py:1146-1185 order): per variant the
+    (op, param) of every plane.  Exponent plane: 1 (bf16/fp16), 3 (fp32);
+    MantissaZeroStrip on plane 0."""
+    np_ = 2 if chain == CHAIN_IEEE16_SPLIT2 else 4
+    ex = 1 if chain == CHAIN_IEEE16_SPLIT2 else 3
+    none = [(PLANE_OP_NONE, 0)] * np_
+    out = [list(none)]
+    for op in (PLANE_OP_INT_DELTA, PLANE_OP_PREDICTOR_XOR):
+        v = list(none)
+        v[ex] = (op, 1)
+        out.append(v)
+    for k in range(1, 5):
+        v = list(none)
+        v[0] = (PLANE_OP_MANTISSA_ZERO_STRIP, k)
+        out.append(v)
+    return out
+
+
+def chain_trial(chain: int, data, menu):
+    """pass1_select_chain (compressor.rs:504-640): every variant forward and
+    every terminal trial-encoded over `menu` (select.rs:27-64); the first
+    variant with the smallest total payload wins; a variant whose forward
+    fails is skipped.  Returns (variant ops, [(codec, payload)] per plane)."""
+    planes = chain_forward(chain, data)
+    best = None
+    for ops in split_chain_variants(chain):
+        try:
+            terms = [plane_op(op, prm, pl, inverse=False) for (op, prm), pl in zip(ops, planes)]
+        except OracleError:
+            continue
+        enc = [select_encode(t, menu) for t in terms]
+        total = sum(len(e[1]) for e in enc)
+        if best is None or total < best[0]:
+            best = (total, ops, enc)
+    return best[1], best[2]
+
+
 # ---- Huffman internals ----
 
 def huf_lengths(freqs):

@@ -58,6 +58,10 @@ _SIGS = {
     "ptwm_mi355x_encode_tensor_ref_cuda": (
         C.c_int64, [C.c_uint32, C.POINTER(C.c_uint16), C.c_uint32, C.c_uint32, C.c_uint64, C.c_size_t, C.c_uint64,
                     C.c_size_t, _u8p, C.c_size_t, C.POINTER(C.c_size_t), C.POINTER(C.c_uint64), C.c_uint32]),
+    "ptwm_mi355x_encode_tensor_ref_ops_cuda": (
+        C.c_int64, [C.c_uint32, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), C.c_uint32, C.c_uint32, C.c_uint32,
+                    C.c_uint64, C.c_size_t, C.c_uint64, C.c_size_t, _u8p, C.c_size_t, C.POINTER(C.c_size_t),
+                    C.POINTER(C.c_uint64), C.POINTER(C.c_uint16), C.c_uint32]),
     "ptwm_mi355x_plane_crc32_cuda": (
         C.c_int64, [C.c_uint32, C.c_uint64, C.c_size_t, C.POINTER(C.c_uint32), C.c_uint32, C.c_uint32]),
     "ptwm_mi355x_xxh64_cuda": (C.c_int64, [C.c_uint64, C.c_size_t, C.POINTER(C.c_uint64), C.c_uint32]),

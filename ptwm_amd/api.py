@@ -237,6 +237,50 @@ def encode_tensor_ref_cuda(chain: int, plane_codecs, chunk_size: int, src, out,
     return rc, bytes(plan_buf[: plan_len.value])
 
 
+PLANE_OP_INT_DELTA = 1
+PLANE_OP_PREDICTOR_XOR = 2
+PLANE_OP_MANTISSA_ZERO_STRIP = 3
+
+
+def plane_op_spec(op: int, param: int) -> int:
+    """An encoder plane-op spec: op | param << 8 (0: none)."""
+    return 0 if op == 0 else op | param << 8
+
+
+def encode_tensor_ref_ops_cuda(chain: int, plane_codecs, plane_ops, chunk_size: int, src, out,
+                               device_ordinal: int = 0, chain_trial: bool = False) -> tuple[int, bytes, list[int]]:
+    """As :func:`encode_tensor_ref_cuda`, each plane first passed through its
+    op (``plane_ops[p]``: :func:`plane_op_spec`), or with ``chain_trial`` the
+    reference's trial among the production split-chain variants (library
+    addition).  Returns (bytes used in ``out``, PTMD plan, chosen op specs)."""
+    L = lib()
+    stream = int(L.ptwm_plane_codec_v1_cuda_stream_handle(device_ordinal))
+    ip, il = _dev_ptr_len(src, "src", device_ordinal, stream, False)
+    op, ol = _dev_ptr_len(out, "out", device_ordinal, stream, True, _both_torch(src, out))
+    n = len(plane_codecs)
+    codecs = (C.c_uint16 * n)(*plane_codecs)
+    ops = (C.c_uint16 * n)(*(plane_ops if plane_ops is not None else [0] * n))
+    ops_out = (C.c_uint16 * n)()
+    plan_len = C.c_size_t(0)
+    needed = C.c_uint64(0)
+    cap = 4096
+    while True:
+        plan_buf = (C.c_uint8 * cap)()
+        rc = L.ptwm_mi355x_encode_tensor_ref_ops_cuda(chain, codecs, ops, n, 1 if chain_trial else 0, chunk_size,
+                                                      ip, il, op, ol, plan_buf, cap, C.byref(plan_len),
+                                                      C.byref(needed), ops_out, device_ordinal)
+        if rc == -2 and plan_len.value > cap:
+            cap = plan_len.value
+            continue
+        break
+    if rc == -2:
+        err = NativeError(rc, f"encode_tensor_ref_ops_cuda: needs {needed.value} bytes")
+        err.needed = needed.value
+        raise err
+    check(rc, "encode_tensor_ref_ops_cuda")
+    return rc, bytes(plan_buf[: plan_len.value]), list(ops_out)
+
+
 def plane_crc32_cuda(chain: int, src, device_ordinal: int = 0) -> list[int]:
     """CRC-32 (crc32fast::hash) of every plane of the device tensor ``src``
     split by ``chain`` (library addition; the per-plane checksum of

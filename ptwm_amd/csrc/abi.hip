@@ -6,12 +6,14 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cstring>
 
 #include "../../include/ptwm_mi355x.h"
 #include "decode_sync.h"
 #include "ilv_host.h"
 #include "integrity.h"
+#include "plane_ops.h"
 #include "ref_encode.h"
 #include "runtime.h"
 
@@ -650,24 +652,75 @@ int64_t ptwm_mi355x_encode_tensors_cuda(uint32_t family, uint32_t n_tensors, con
   return (int64_t)out_used;
 }
 
-int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane_codecs, uint32_t n_codecs,
-                                           uint32_t chunk_size, uint64_t in_dev_ptr, size_t in_len,
-                                           uint64_t out_dev_ptr, size_t out_cap, uint8_t* plan_out, size_t plan_cap,
-                                           size_t* plan_len_out, uint64_t* needed_out, uint32_t device_ordinal) {
+namespace {
+
+// Plane op spec of the encoders: 0 none, else op | param << 8 (codes.h).
+constexpr uint32_t op_of(uint32_t spec) { return spec & 0xFFu; }
+constexpr uint32_t param_of(uint32_t spec) { return spec >> 8; }
+
+bool op_spec_ok(uint32_t chain, uint32_t spec) {
+  if (spec == 0) return true;
+  const uint32_t op = op_of(spec), param = param_of(spec);
+  if (chain != kChainIeee16Split2 && chain != kChainIeee32Split4 && chain != kChainPassthrough) return false;
+  if (op == kPlaneOpPredictorXor) return param == 1 || param == 2;
+  if (op == kPlaneOpIntDelta) return param == 1 || param == 2 || param == 4 || param == 8;
+  return op == kPlaneOpMantissaZeroStrip && param >= 1 && param <= 7;
+}
+
+// PTMD plane flag bits of an op spec (plan_parse.cpp)
+uint16_t op_flags(uint32_t spec) {
+  if (spec == 0) return 0;
+  const uint32_t op = op_of(spec), param = param_of(spec);
+  const uint32_t code = op == kPlaneOpMantissaZeroStrip ? param : (uint32_t)__builtin_ctz(param);
+  return (uint16_t)((op << 1) | (code << 3));
+}
+
+// Tensor-level encode into the reference's plane formats, plane p passed
+// through the op ops[p] first.  With `trial`, ops is ignored and the
+// reference's chain trial picks among the production split-chain variants
+// (_chains.py:1146-1185; compressor.rs:504-640: every candidate forward and
+// trial-encoded, the smallest total of plane payloads wins, the first on
+// ties, a candidate whose forward fails is skipped); ops_out gets the
+// chosen ops.
+int64_t encode_tensor_ref(uint32_t chain, const uint16_t* plane_codecs, const uint16_t* ops_in, uint32_t n_planes,
+                          bool trial, uint32_t chunk_size, uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                          size_t out_cap, uint8_t* plan_out, size_t plan_cap, size_t* plan_len_out,
+                          uint64_t* needed_out, uint16_t* ops_out, uint32_t device_ordinal) {
   const int np = chain_planes(chain);
-  if (np < 0 || !plan_out || !plan_len_out || !plane_codecs || n_codecs != (uint32_t)np) return kInvalidInput;
+  if (np < 0 || !plan_out || !plan_len_out || !plane_codecs || n_planes != (uint32_t)np) return kInvalidInput;
   uint32_t codecs[4] = {0, 0, 0, 0};
-  bool select = false;
   for (int p = 0; p < np; ++p) {
     codecs[p] = plane_codecs[p];
-    select |= codecs[p] == PTWM_MI355X_CODEC_SELECT;
     if (codecs[p] != kCodecIdentity && codecs[p] != kCodecHuffman && codecs[p] != kCodecRans &&
         codecs[p] != PTWM_MI355X_CODEC_SELECT)
       return kUnsupported;
   }
+  // the candidates: plane op specs per plane
+  std::vector<std::array<uint32_t, 4>> cand;
+  if (trial) {
+    if (chain != kChainIeee16Split2 && chain != kChainIeee32Split4) return kUnsupported;
+    const int ex = chain == kChainIeee16Split2 ? 1 : 3;  // the exponent plane (_chains.py:360-600)
+    cand.push_back({0, 0, 0, 0});
+    std::array<uint32_t, 4> c{0, 0, 0, 0};
+    c[ex] = kPlaneOpIntDelta | 1u << 8;
+    cand.push_back(c);
+    c[ex] = kPlaneOpPredictorXor | 1u << 8;
+    cand.push_back(c);
+    for (uint32_t k = 1; k <= 4; ++k) cand.push_back({kPlaneOpMantissaZeroStrip | k << 8, 0, 0, 0});
+  } else {
+    std::array<uint32_t, 4> c{0, 0, 0, 0};
+    for (int p = 0; p < np; ++p) {
+      c[p] = ops_in ? ops_in[p] : 0u;
+      if (!op_spec_ok(chain, c[p])) return kUnsupported;
+    }
+    cand.push_back(c);
+  }
   const uint64_t ratio = (uint64_t)chain_ratio(chain);
   if (in_len % ratio || (in_dev_ptr & 15u) || (out_dev_ptr & 255u)) return kInvalidInput;
   const uint64_t plane_len = in_len / ratio;
+  for (const auto& c : cand)
+    for (int p = 0; p < np; ++p)
+      if (c[p] && op_of(c[p]) != kPlaneOpMantissaZeroStrip && plane_len % param_of(c[p])) return kInvalidInput;
   // chunks: plane.chunks(chunk_size) (compressor.rs:316-381); 0 = unchunked
   const uint64_t cs = chunk_size ? chunk_size : (plane_len ? plane_len : 1);
   const uint64_t nch = chunk_size ? (plane_len == 0 ? 1 : (plane_len + cs - 1) / cs) : 1;
@@ -680,45 +733,131 @@ int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane
   DeviceScope ds(device_ordinal);
   if (!ds.ok) return kInvalidInput;
   DevCtx& ctx = *ds.ctx;
+  // the distinct (plane, op) planes of every candidate: the split planes,
+  // then one op output each
+  struct Var {
+    int plane;
+    uint32_t spec;
+    uint8_t* ptr;
+    bool refused;
+    uint64_t size;  // payload bytes of the plane with its codec (or the trial's choice)
+    uint32_t codec;
+  };
+  std::vector<Var> vars;
+  const auto var_of = [&](int p, uint32_t spec) {
+    for (size_t i = 0; i < vars.size(); ++i)
+      if (vars[i].plane == p && vars[i].spec == spec) return (int)i;
+    vars.push_back(Var{p, spec, nullptr, false, 0, 0});
+    return (int)vars.size() - 1;
+  };
+  for (int p = 0; p < np; ++p) var_of(p, 0);
+  for (const auto& c : cand)
+    for (int p = 0; p < np; ++p) var_of(p, c[p]);
   const uint64_t stride = (plane_len + 255) / 256 * 256;
-  PTWM_HIP_TRY(ctx.enc_split.ensure(stride * np + 256));
+  PTWM_HIP_TRY(ctx.enc_split.ensure(stride * vars.size() + 256));
+  for (size_t i = 0; i < vars.size(); ++i) vars[i].ptr = static_cast<uint8_t*>(ctx.enc_split.ptr) + stride * i;
   uint8_t* pl[4] = {};
-  for (int i = 0; i < np; ++i) pl[i] = static_cast<uint8_t*>(ctx.enc_split.ptr) + stride * i;
+  for (int i = 0; i < np; ++i) pl[i] = vars[i].ptr;  // the first np vars are the split planes
   if (plane_len && launch_split(chain, reinterpret_cast<const uint8_t*>(in_dev_ptr), plane_len, pl, ctx.stream) !=
                        hipSuccess)
     return kInvalidInput;
-  if (select) {
-    // trial encode of the whole plane (select.rs:27-64): Huffman, rANS and
-    // Identity sizes in menu order (dispatch.rs:13-49), smallest first wins;
-    // a chunked plane is then chunked with the winner (compressor.rs:316-381)
-    std::vector<RefJob> trial;
+  if (vars.size() > (size_t)np && plane_len) {
+    std::vector<PlaneOpJob> jobs;
+    for (size_t i = np; i < vars.size(); ++i)
+      jobs.push_back(PlaneOpJob{reinterpret_cast<uint64_t>(pl[vars[i].plane]), reinterpret_cast<uint64_t>(vars[i].ptr),
+                                plane_len, op_of(vars[i].spec), param_of(vars[i].spec), 0, 0});
+    std::vector<uint32_t> refused;
+    const int64_t rc = run_plane_ops(ctx, jobs, true, &refused);
+    if (rc != kOk) return rc;
+    for (size_t i = np; i < vars.size(); ++i) vars[i].refused = refused[i - np] != 0;
+  }
+  // sizes of every var the candidates need (trial) or the codecs' choice
+  // (select.rs:27-64: Huffman, rANS and Identity in menu order, smallest
+  // first wins)
+  std::vector<int> chosen_var(np, -1);
+  size_t best = 0;
+  if (cand.size() == 1) {
     for (int p = 0; p < np; ++p) {
-      if (codecs[p] != PTWM_MI355X_CODEC_SELECT) continue;
+      chosen_var[p] = var_of(p, cand[0][p]);
+      if (vars[chosen_var[p]].refused) return kInvalidInput;  // the forward op fails (mantissa_zero.rs)
+    }
+  }
+  const bool need_sizes = cand.size() > 1;
+  bool any_select = false;
+  for (int p = 0; p < np; ++p) any_select |= codecs[p] == PTWM_MI355X_CODEC_SELECT;
+  if (need_sizes || any_select) {
+    std::vector<RefJob> tj;
+    std::vector<std::pair<size_t, uint32_t>> tj_of;  // (var, codec)
+    for (size_t i = 0; i < vars.size(); ++i) {
+      const Var& V = vars[i];
+      if (V.refused || plane_len == 0) continue;
+      if (!need_sizes && chosen_var[V.plane] != (int)i) continue;
+      const uint32_t c = codecs[V.plane];
+      if (c == PTWM_MI355X_CODEC_SELECT || c == kCodecHuffman) {
+        tj.push_back(RefJob{reinterpret_cast<uint64_t>(V.ptr), plane_len, kCodecHuffman});
+        tj_of.emplace_back(i, kCodecHuffman);
+      }
+      if (c == PTWM_MI355X_CODEC_SELECT || c == kCodecRans) {
+        tj.push_back(RefJob{reinterpret_cast<uint64_t>(V.ptr), plane_len, kCodecRans});
+        tj_of.emplace_back(i, kCodecRans);
+      }
+    }
+    std::vector<uint64_t> tl;
+    if (!tj.empty()) {
+      RefEncoder t;
+      const int64_t rc = t.plan(ctx, tj, tl);
+      if (rc < 0) return rc;
+    }
+    for (size_t i = 0; i < vars.size(); ++i) {
+      Var& V = vars[i];
+      const uint32_t c = codecs[V.plane];
+      V.codec = c == PTWM_MI355X_CODEC_SELECT ? kCodecHuffman : c;
+      V.size = plane_len;  // Identity (and an empty plane: 0 bytes against a 1-byte tag)
       if (plane_len == 0) {
-        codecs[p] = kCodecIdentity;  // 0 bytes against a 1-byte raw tag
+        if (c == PTWM_MI355X_CODEC_SELECT) V.codec = kCodecIdentity;
         continue;
       }
-      trial.push_back(RefJob{reinterpret_cast<uint64_t>(pl[p]), plane_len, kCodecHuffman});
-      trial.push_back(RefJob{reinterpret_cast<uint64_t>(pl[p]), plane_len, kCodecRans});
-    }
-    if (!trial.empty()) {
-      RefEncoder t;
-      std::vector<uint64_t> tl;
-      const int64_t rc = t.plan(ctx, trial, tl);
-      if (rc < 0) return rc;
-      size_t j = 0;
-      for (int p = 0; p < np; ++p) {
-        if (codecs[p] != PTWM_MI355X_CODEC_SELECT) continue;
-        uint64_t best = tl[j];
-        codecs[p] = kCodecHuffman;
-        if (tl[j + 1] < best) {
-          best = tl[j + 1];
-          codecs[p] = kCodecRans;
+      bool first = true;
+      for (size_t k = 0; k < tj_of.size(); ++k) {
+        if (tj_of[k].first != i) continue;
+        if (first || tl[k] < V.size) {
+          V.size = tl[k];
+          V.codec = tj_of[k].second;
         }
-        if (plane_len < best) codecs[p] = kCodecIdentity;
-        j += 2;
+        first = false;
+      }
+      if (c == PTWM_MI355X_CODEC_SELECT && plane_len < V.size) {
+        V.size = plane_len;
+        V.codec = kCodecIdentity;
       }
     }
+    if (need_sizes) {
+      // compressor.rs:589-593: the first candidate with the smallest total
+      int bi = -1;
+      for (size_t k = 0; k < cand.size(); ++k) {
+        size_t total = 0;
+        bool ok = true;
+        for (int p = 0; p < np; ++p) {
+          const Var& V = vars[var_of(p, cand[k][p])];
+          ok &= !V.refused;
+          total += V.size;
+        }
+        if (ok && (bi < 0 || total < best)) {
+          bi = (int)k;
+          best = total;
+        }
+      }
+      if (bi < 0) return kInternal;  // the plain split never fails
+      for (int p = 0; p < np; ++p) chosen_var[p] = var_of(p, cand[bi][p]);
+    }
+    for (int p = 0; p < np; ++p)
+      if (codecs[p] == PTWM_MI355X_CODEC_SELECT) codecs[p] = vars[chosen_var[p]].codec;
+  }
+  uint32_t spec[4] = {0, 0, 0, 0};
+  for (int p = 0; p < np; ++p) {
+    pl[p] = vars[chosen_var[p]].ptr;
+    spec[p] = vars[chosen_var[p]].spec;
+    if (ops_out) ops_out[p] = (uint16_t)spec[p];
   }
   // one job per coded chunk; Identity payloads are the bytes themselves
   std::vector<RefJob> jobs;
@@ -783,7 +922,7 @@ int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane
   put(&magic, 4); put(&ver, 2); put(&flags, 2); put(&ntens, 4);
   put(&zero64, 8); put(&out_len, 8); put(&ch, 1); put(&npl, 1); put(&tflags, 2);
   for (int p = 0; p < np; ++p) {
-    const uint16_t codec = (uint16_t)codecs[p], pf = chunk_size ? 1 : 0;
+    const uint16_t codec = (uint16_t)codecs[p], pf = (uint16_t)((chunk_size ? 1 : 0) | op_flags(spec[p]));
     const uint32_t n_ch = chunk_size ? (uint32_t)nch : 0;
     put(&codec, 2); put(&pf, 2); put(&n_ch, 4);
     put(&poff[p], 8); put(&plen_total[p], 8); put(&plane_len, 8);
@@ -794,6 +933,28 @@ int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane
   }
   *plan_len_out = (size_t)(o - plan_out);
   return (int64_t)off;
+}
+
+}  // namespace
+
+int64_t ptwm_mi355x_encode_tensor_ref_cuda(uint32_t chain, const uint16_t* plane_codecs, uint32_t n_codecs,
+                                           uint32_t chunk_size, uint64_t in_dev_ptr, size_t in_len,
+                                           uint64_t out_dev_ptr, size_t out_cap, uint8_t* plan_out, size_t plan_cap,
+                                           size_t* plan_len_out, uint64_t* needed_out, uint32_t device_ordinal) {
+  return encode_tensor_ref(chain, plane_codecs, nullptr, n_codecs, false, chunk_size, in_dev_ptr, in_len, out_dev_ptr,
+                           out_cap, plan_out, plan_cap, plan_len_out, needed_out, nullptr, device_ordinal);
+}
+
+int64_t ptwm_mi355x_encode_tensor_ref_ops_cuda(uint32_t chain, const uint16_t* plane_codecs, const uint16_t* plane_ops,
+                                               uint32_t n_planes, uint32_t chain_trial, uint32_t chunk_size,
+                                               uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
+                                               size_t out_cap, uint8_t* plan_out, size_t plan_cap,
+                                               size_t* plan_len_out, uint64_t* needed_out, uint16_t* ops_out,
+                                               uint32_t device_ordinal) {
+  if (chain_trial > 1 || (!chain_trial && !plane_ops)) return kInvalidInput;
+  return encode_tensor_ref(chain, plane_codecs, plane_ops, n_planes, chain_trial != 0, chunk_size, in_dev_ptr, in_len,
+                           out_dev_ptr, out_cap, plan_out, plan_cap, plan_len_out, needed_out, ops_out,
+                           device_ordinal);
 }
 
 int64_t ptwm_mi355x_plane_crc32_cuda(uint32_t chain, uint64_t in_dev_ptr, size_t in_len, uint32_t* crc_out,

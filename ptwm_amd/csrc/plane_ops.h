@@ -26,8 +26,13 @@ static_assert(sizeof(PlaneOpJob) == 48, "PlaneOpJob layout");
 // widths 1 and 2, whose tables fit the LDS; the others always).
 bool plane_op_supported(uint32_t op, uint32_t param);
 
-// Enqueue every job on ctx.stream (no synchronisation).  Returns kOk,
-// kUnsupported for an op plane_op_supported refuses, or kInternal.
-int64_t run_plane_ops(DevCtx& ctx, std::vector<PlaneOpJob>& jobs);
+// Enqueue every job on ctx.stream: the inverse ops (decode), or with
+// `forward` the ops themselves (encode).  With `refused` (forward only) the
+// stream is synchronised and refused[j] is nonzero for a job whose plane the
+// op refuses (MantissaZeroStrip: a byte with nonzero low k bits), in the
+// caller's job order.  Reorders `jobs`.  Returns kOk, kUnsupported for an
+// op plane_op_supported refuses, or kInternal.
+int64_t run_plane_ops(DevCtx& ctx, std::vector<PlaneOpJob>& jobs, bool forward = false,
+                      std::vector<uint32_t>* refused = nullptr);
 
 }  // namespace ptwm

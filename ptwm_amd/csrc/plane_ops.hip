@@ -1,4 +1,5 @@
-// plane_ops.hip -- inverse plane ops on decoded terminal planes.
+// plane_ops.hip -- plane ops on terminal planes: their inverses for the
+// decode, the ops themselves for the encoder.
 //
 // The reference applies these ops to one terminal plane of a split chain
 // (python/ptwm/preprocessing/_chains.py:360-600: the exponent plane through
@@ -206,7 +207,7 @@ __global__ void __launch_bounds__(256) mzs_inverse(const PlaneOpJob* __restrict_
 // table[hash], value = residual ^ prediction, table[hash] = value,
 // hash = ((hash << 6) ^ value) & 0xFFFF), and the wavefront stores the
 // values.
-template <uint32_t W>
+template <uint32_t W, bool kForward = false>
 __global__ void __launch_bounds__(64) pxor_inverse(const PlaneOpJob* __restrict__ jobs,
                                                    const uint32_t* __restrict__ which) {
   extern __shared__ __align__(16) uint32_t lds[];
@@ -234,10 +235,11 @@ __global__ void __launch_bounds__(64) pxor_inverse(const PlaneOpJob* __restrict_
           uint32_t o4 = 0;
 #pragma unroll
           for (uint32_t k = 0; k < 4; ++k) {
-            const uint32_t v = ((x4 >> (8 * k)) & 0xFFu) ^ tab[h];
+            const uint32_t x = (x4 >> (8 * k)) & 0xFFu, r = x ^ tab[h];
+            const uint32_t v = kForward ? x : r;  // the value the table and hash follow
             tab[h] = (uint8_t)v;
             h = ((h << 6) ^ v) & 0xFFFFu;
-            o4 |= v << (8 * k);
+            o4 |= r << (8 * k);
           }
           outw[i / 4] = o4;
         }
@@ -248,10 +250,11 @@ __global__ void __launch_bounds__(64) pxor_inverse(const PlaneOpJob* __restrict_
           uint32_t o4 = 0;
 #pragma unroll
           for (uint32_t k = 0; k < 2; ++k) {
-            const uint32_t v = ((x4 >> (16 * k)) & 0xFFFFu) ^ tab[h];
+            const uint32_t x = (x4 >> (16 * k)) & 0xFFFFu, r = x ^ tab[h];
+            const uint32_t v = kForward ? x : r;
             tab[h] = (uint16_t)v;
             h = ((h << 6) ^ v) & 0xFFFFu;
-            o4 |= v << (16 * k);
+            o4 |= r << (16 * k);
           }
           outw[i / 4] = o4;
         }
@@ -264,6 +267,60 @@ __global__ void __launch_bounds__(64) pxor_inverse(const PlaneOpJob* __restrict_
       store16(J.dst, c + q, J.n, w);
     }
     __syncthreads();
+  }
+}
+
+// ---- forward ops (the encoder's direction) ----
+
+// IntDelta forward (int_delta.rs:38-46): out[0] = in[0], out[i] = in[i] -
+// in[i-1] at the element width; each thread also reads the element before
+// its 16 bytes.
+template <uint32_t W>
+__global__ void __launch_bounds__(256) idelta_forward(const PlaneOpJob* __restrict__ jobs, uint32_t n_jobs,
+                                                      uint64_t n_tiles) {
+  for (uint64_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+    const PlaneOpJob& J = jobs[find_job(jobs, n_jobs, t)];
+    const uint64_t o = (t - J.tile0) * kTile + 16ull * threadIdx.x;
+    if (o >= J.n) continue;
+    uint32_t w[4], v[4] = {0, 0, 0, 0};
+    load16(J.src, o, J.n, w);
+    uint64_t prev = 0;
+    if (o >= W) {
+      uint32_t pw[4];
+      load16(J.src, o - 16, J.n, pw);
+      prev = get_elem<W>(pw, 16 / W - 1);
+    }
+#pragma unroll
+    for (uint32_t e = 0; e < 16 / W; ++e) {
+      const uint64_t x = get_elem<W>(w, e);
+      set_elem<W>(v, e, o + e * W == 0 ? x : x - prev);
+      prev = x;
+    }
+    store16(J.dst, o, J.n, v);
+  }
+}
+
+// MantissaZeroStrip forward (mantissa_zero.rs forward): b >> k; a byte with
+// a nonzero low k bits refuses the plane (flag[job] = 1)
+__global__ void __launch_bounds__(256) mzs_forward(const PlaneOpJob* __restrict__ jobs, uint32_t n_jobs,
+                                                   uint64_t n_tiles, uint32_t* __restrict__ flag) {
+  for (uint64_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+    const uint32_t j = find_job(jobs, n_jobs, t);
+    const PlaneOpJob& J = jobs[j];
+    const uint64_t o = (t - J.tile0) * kTile + 16ull * threadIdx.x;
+    if (o >= J.n) continue;
+    const uint32_t k = J.param;
+    const uint32_t low = ((1u << k) - 1u) * 0x01010101u, keep = (0xFFu >> k) * 0x01010101u;
+    uint32_t w[4];
+    load16(J.src, o, J.n, w);  // bytes past the plane read as zero
+    uint32_t bad = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bad |= w[i] & low;
+      w[i] = (w[i] >> k) & keep;
+    }
+    if (bad) atomicOr(&flag[j], 1u);
+    store16(J.dst, o, J.n, w);
   }
 }
 
@@ -283,8 +340,15 @@ bool plane_op_supported(uint32_t op, uint32_t param) {
   }
 }
 
-int64_t run_plane_ops(DevCtx& ctx, std::vector<PlaneOpJob>& jobs) {
+int64_t run_plane_ops(DevCtx& ctx, std::vector<PlaneOpJob>& jobs, bool forward, std::vector<uint32_t>* refused) {
+  if (refused) refused->assign(jobs.size(), 0);
   if (jobs.empty()) return kOk;
+  // the jobs' caller order, for the refusal flags
+  std::vector<uint32_t> order(jobs.size());
+  for (uint32_t i = 0; i < jobs.size(); ++i) {
+    order[i] = i;
+    jobs[i].aux = i;  // reset below for IntDelta inverses
+  }
   for (const PlaneOpJob& J : jobs)
     if (J.op == kPlaneOpNone || !plane_op_supported(J.op, J.param) || (J.src & 15u) || (J.dst & 15u) ||
         J.n % (J.op == kPlaneOpMantissaZeroStrip ? 1 : J.param))
@@ -294,6 +358,7 @@ int64_t run_plane_ops(DevCtx& ctx, std::vector<PlaneOpJob>& jobs) {
   std::stable_sort(jobs.begin(), jobs.end(), [](const PlaneOpJob& a, const PlaneOpJob& b) {
     return a.op != b.op ? a.op < b.op : a.param < b.param;
   });
+  for (uint32_t i = 0; i < jobs.size(); ++i) order[i] = (uint32_t)jobs[i].aux;
   struct Group {
     uint32_t op, param, first, count;
     uint64_t tiles;
@@ -309,8 +374,8 @@ int64_t run_plane_ops(DevCtx& ctx, std::vector<PlaneOpJob>& jobs) {
     Group& G = groups.back();
     const uint64_t nt = (J.n + kTile - 1) / kTile;
     J.tile0 = G.tiles;
-    J.aux = J.op == kPlaneOpIntDelta ? sum_slots : 0;
-    if (J.op == kPlaneOpIntDelta) sum_slots += nt;
+    J.aux = J.op == kPlaneOpIntDelta && !forward ? sum_slots : 0;
+    if (J.op == kPlaneOpIntDelta && !forward) sum_slots += nt;
     G.tiles += nt;
     ++G.count;
   }
@@ -319,7 +384,9 @@ int64_t run_plane_ops(DevCtx& ctx, std::vector<PlaneOpJob>& jobs) {
   const size_t total = jb + jobs.size() * sizeof(uint32_t);
   PTWM_HIP_TRY(ctx.op_jobs.ensure(total));
   PTWM_HIP_TRY(ctx.h_op.ensure(total));
-  PTWM_HIP_TRY(ctx.op_sums.ensure(8 * (sum_slots ? sum_slots : 1)));
+  PTWM_HIP_TRY(ctx.op_sums.ensure(8 * std::max<uint64_t>(sum_slots, jobs.size()) + 8));
+  uint32_t* flags = static_cast<uint32_t*>(ctx.op_sums.ptr);  // forward strip refusals
+  if (forward) PTWM_HIP_TRY(hipMemsetAsync(flags, 0, 4 * jobs.size(), ctx.stream));
   uint8_t* h = static_cast<uint8_t*>(ctx.h_op.ptr);
   std::memcpy(h, jobs.data(), jb);
   uint32_t* hw = reinterpret_cast<uint32_t*>(h + jb);
@@ -332,7 +399,23 @@ int64_t run_plane_ops(DevCtx& ctx, std::vector<PlaneOpJob>& jobs) {
   for (const Group& G : groups) {
     const PlaneOpJob* gj = dj + G.first;
     if (G.tiles == 0 && G.op != kPlaneOpPredictorXor) continue;
-    if (G.op == kPlaneOpIntDelta) {
+    if (forward && G.op == kPlaneOpIntDelta) {
+#define PTWM_IDELTA_F(W)                                                                                  \
+  case W:                                                                                                 \
+    hipLaunchKernelGGL(idelta_forward<W>, dim3(grid_for(G.tiles)), dim3(256), 0, s, gj, G.count, G.tiles); \
+    break;
+      switch (G.param) {
+        PTWM_IDELTA_F(1)
+        PTWM_IDELTA_F(2)
+        PTWM_IDELTA_F(4)
+        PTWM_IDELTA_F(8)
+        default: return kUnsupported;
+      }
+#undef PTWM_IDELTA_F
+    } else if (forward && G.op == kPlaneOpMantissaZeroStrip) {
+      hipLaunchKernelGGL(mzs_forward, dim3(grid_for(G.tiles)), dim3(256), 0, s, gj, G.count, G.tiles,
+                         flags + G.first);
+    } else if (G.op == kPlaneOpIntDelta) {
 #define PTWM_IDELTA(W)                                                                                    \
   case W:                                                                                                 \
     hipLaunchKernelGGL(idelta_sums<W>, dim3(grid_for(G.tiles)), dim3(256), 0, s, gj, G.count, G.tiles, sums); \
@@ -351,7 +434,8 @@ int64_t run_plane_ops(DevCtx& ctx, std::vector<PlaneOpJob>& jobs) {
     } else if (G.op == kPlaneOpMantissaZeroStrip) {
       hipLaunchKernelGGL(mzs_inverse, dim3(grid_for(G.tiles)), dim3(256), 0, s, gj, G.count, G.tiles);
     } else if (G.op == kPlaneOpPredictorXor) {
-      const void* fn = G.param == 1 ? (const void*)pxor_inverse<1> : (const void*)pxor_inverse<2>;
+      const void* fn = forward ? (G.param == 1 ? (const void*)pxor_inverse<1, true> : (const void*)pxor_inverse<2, true>)
+                               : (G.param == 1 ? (const void*)pxor_inverse<1> : (const void*)pxor_inverse<2>);
       const size_t lds = pxor_lds_bytes(G.param);
       PTWM_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
       const uint32_t* which = dw + G.first;
@@ -359,6 +443,12 @@ int64_t run_plane_ops(DevCtx& ctx, std::vector<PlaneOpJob>& jobs) {
       PTWM_HIP_TRY(hipLaunchKernel(fn, dim3(G.count), dim3(64), args, lds, s));
     }
     PTWM_HIP_TRY(hipGetLastError());
+  }
+  if (refused) {
+    std::vector<uint32_t> f(jobs.size(), 0);
+    PTWM_HIP_TRY(hipMemcpyAsync(f.data(), flags, 4 * jobs.size(), hipMemcpyDeviceToHost, s));
+    PTWM_HIP_TRY(hipStreamSynchronize(s));
+    for (uint32_t i = 0; i < jobs.size(); ++i) (*refused)[order[i]] = f[i];
   }
   return kOk;
 }
