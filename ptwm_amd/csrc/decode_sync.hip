@@ -79,15 +79,30 @@ __device__ inline uint8_t gbyte(uint64_t a) {
 __device__ inline void stage_wave(const SyncStream& S, uint64_t L0, const uint16_t* __restrict__ tables,
                                   uint32_t* stage, uint16_t* tab) {
   const uint32_t lane = threadIdx.x;
-  const uint32_t tsize = 1u << S.max_bits;
-  const uint16_t* gt = tables + 2048ull * S.table;
-  for (uint32_t i = lane; i < tsize; i += kLanes) tab[i] = gt[i];
+  const uint32_t tsize = 1u << S.max_bits;  // >= 2
+  // the table as 32-bit words (each table starts 4 KiB-aligned)
+  const uint64_t gt = reinterpret_cast<uint64_t>(tables + 2048ull * S.table);
+  uint32_t* const t32 = reinterpret_cast<uint32_t*>(tab);
+  for (uint32_t i = lane; i < tsize / 2; i += kLanes) t32[i] = g_ld<uint32_t>(gt + 4ull * i);
+  // Logical bytes [b, b + 4) of a stage word are the physical bytes
+  // [m - 4 - b, m - 1 - b] reversed: one byte swap of the word at a =
+  // src + m - 4 - b, read as the aligned words that hold it (each holds a
+  // byte of the stream).  Words reaching past the stream's logical end are
+  // assembled bytewise (zero past the end).
   for (uint32_t q = lane; q < kStageWords; q += kLanes) {
+    const uint64_t b = L0 + 4ull * q;
     uint32_t v = 0;
+    if (b + 4 <= S.m) {
+      const uint64_t a = S.src + S.m - 4 - b, lo = a & ~3ull;
+      const uint32_t sh = (uint32_t)(a & 3u);
+      const uint32_t w0 = g_ld<uint32_t>(lo), w1 = sh ? g_ld<uint32_t>(lo + 4) : 0u;
+      v = __builtin_bswap32(__builtin_amdgcn_alignbyte(w1, w0, sh));
+    } else {
 #pragma unroll
-    for (uint32_t t = 0; t < 4; ++t) {
-      const uint64_t i = L0 + 4ull * q + t;
-      if (i < S.m) v |= (uint32_t)gbyte(S.src + S.m - 1 - i) << (8 * t);
+      for (uint32_t t = 0; t < 4; ++t) {
+        const uint64_t i = b + t;
+        if (i < S.m) v |= (uint32_t)gbyte(S.src + S.m - 1 - i) << (8 * t);
+      }
     }
     stage[q] = v;
   }
