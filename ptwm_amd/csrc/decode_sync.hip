@@ -12,7 +12,9 @@
 //            until no start changes (sync_pass_kernel);
 //   fix      the same across wavefronts, repeated until no wavefront's first
 //            start differs from the previous wavefront's last exit
-//            (sync_fix_kernel; the host loops on a flag);
+//            (sync_fix_kernel; passes are queued in batches, each pass
+//            skipping its work when the one before changed nothing, and the
+//            host reads the batch's flags once);
 //   scan     per stream, symbol counts -> output offsets (sync_scan_kernel);
 //   write    each lane decodes its subsequence again and writes the symbols
 //            (staged in LDS, stored coalesced), recording where symbol n-1
@@ -180,9 +182,12 @@ __global__ void __launch_bounds__(64) sync_fix_kernel(const SyncStream* __restri
                                                       const uint32_t* __restrict__ wave_job,
                                                       const uint32_t* __restrict__ job_wave0,
                                                       const uint16_t* __restrict__ tables, SyncArrays A,
+                                                      const uint32_t* __restrict__ prev_flag,
                                                       uint32_t* __restrict__ flag) {
   __shared__ uint16_t tab[2048];
   __shared__ uint32_t stage[kStageWords];
+  // the previous pass (queued before this one) changed nothing: settled
+  if (prev_flag && g_ld<uint32_t>(reinterpret_cast<uint64_t>(prev_flag)) == 0) return;
   const uint32_t d = wave_job[blockIdx.x];
   uint32_t w = blockIdx.x - job_wave0[d];
   const int s = locate(streams + 4ull * d, w);
@@ -429,11 +434,12 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   SyncArrays A{};
   uint32_t *d_wave_job = nullptr, *d_job_wave0 = nullptr, *d_flag = nullptr;
   const uint32_t nw = (uint32_t)wave_job.size();
+  constexpr uint32_t kFixBatch = 4;
   if (n_def) {
     PTWM_HIP_TRY(ctx.sync_streams.ensure(4ull * n_def * sizeof(SyncStream)));
     PTWM_HIP_TRY(ctx.sync_tables.ensure(2048ull * 2 * n_def));
     PTWM_HIP_TRY(ctx.sync_sub.ensure(subs * (8 + 8 + 4) + (uint64_t)nw * (8 + 4) + 64));
-    PTWM_HIP_TRY(ctx.sync_waves.ensure((wave_job.size() + job_wave0.size() + 1) * 4 + 64));
+    PTWM_HIP_TRY(ctx.sync_waves.ensure((wave_job.size() + job_wave0.size() + kFixBatch) * 4 + 64));
     streams = static_cast<SyncStream*>(ctx.sync_streams.ptr);
     tables = static_cast<uint16_t*>(ctx.sync_tables.ptr);
     uint8_t* sb = static_cast<uint8_t*>(ctx.sync_sub.ptr);
@@ -468,17 +474,16 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
     PTWM_HIP_TRY(ctx.h_small.ensure(64));
     volatile uint32_t* h_flag = static_cast<uint32_t*>(ctx.h_small.ptr);
     bool settled = false;
-    for (uint32_t pass = 0; pass < kMaxFixPasses; ++pass) {
-      PTWM_HIP_TRY(hipMemsetAsync(d_flag, 0, 4, s));
-      hipLaunchKernelGGL(sync_fix_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables, A,
-                         d_flag);
-      PTWM_HIP_TRY(hipGetLastError());
-      PTWM_HIP_TRY(hipMemcpyAsync(const_cast<uint32_t*>(h_flag), d_flag, 4, hipMemcpyDeviceToHost, s));
-      PTWM_HIP_TRY(hipStreamSynchronize(s));
-      if (*h_flag == 0) {
-        settled = true;
-        break;
+    for (uint32_t pass = 0; pass < kMaxFixPasses && !settled; pass += kFixBatch) {
+      PTWM_HIP_TRY(hipMemsetAsync(d_flag, 0, 4 * kFixBatch, s));
+      for (uint32_t k = 0; k < kFixBatch; ++k) {
+        hipLaunchKernelGGL(sync_fix_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables,
+                           A, k ? d_flag + k - 1 : nullptr, d_flag + k);
+        PTWM_HIP_TRY(hipGetLastError());
       }
+      PTWM_HIP_TRY(hipMemcpyAsync(const_cast<uint32_t*>(h_flag), d_flag, 4 * kFixBatch, hipMemcpyDeviceToHost, s));
+      PTWM_HIP_TRY(hipStreamSynchronize(s));
+      for (uint32_t k = 0; k < kFixBatch; ++k) settled |= h_flag[k] == 0;
     }
     if (settled) {
       hipLaunchKernelGGL(sync_wave_sum_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, A);
