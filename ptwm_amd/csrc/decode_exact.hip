@@ -29,6 +29,7 @@ namespace ptwm {
 namespace {
 
 constexpr int kHufMaxBits = 11;
+constexpr uint32_t kHdrStage = 160;  // staged Huffman header bytes: weights (<= 130) + jump table (16)
 constexpr uint32_t kRansProbBits = 11;
 constexpr uint32_t kRansScale = 1u << kRansProbBits;
 constexpr uint32_t kRansL = 1u << 23;
@@ -230,6 +231,7 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
   __shared__ uint16_t next_code[kHufMaxBits + 1];
   __shared__ uint16_t rev[256];
   __shared__ uint32_t table32[kRansScale];  // rANS: sym | freq << 8 | start << 20
+  __shared__ uint8_t hdr_stage[kHdrStage];   // Huffman: weights header and jump table
   uint16_t* table16 = reinterpret_cast<uint16_t*>(table32);  // Huffman: (len << 8) | sym
 
   const uint32_t lane = threadIdx.x;
@@ -266,7 +268,14 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
 
   if (h.kind == 1) {
     // ---- weights header (weights.rs:34-85) and tree (tree.rs:87-177) ----
+    // The header and jump table (at most 2 + 128 + 16 bytes) are staged in
+    // LDS by the wavefront first: lane 0 parses them from there instead of
+    // issuing its header loads to global memory one after another.
+    const uint8_t* const genc = enc;
+    for (uint32_t i = lane; i < kHdrStage; i += 64) hdr_stage[i] = i < enc_len ? g_ld<uint8_t>((uint64_t)(genc + i)) : 0;
+    __syncthreads();
     if (lane == 0) {
+      const uint8_t* enc = hdr_stage;
       uint32_t st = kStOk;
       uint64_t n = 0, hb = 0;
       if (enc_len == 0 || !(enc[0] & 0x80)) st = kStBadHeader;
