@@ -88,10 +88,39 @@ struct alignas(16) DecodeCtl {
   uint32_t pair[4];
   uint32_t packed[4];   // plane stored as packed nibbles (tag 2)
   uint32_t slot[4];     // LDS table slot of a coded plane
+  uint32_t hdr_avail[4];  // bytes of a coded plane's weights header in its head
+  uint64_t pbase[4], plen[4];  // the tensor's plane descriptors (IlvPlane)
+  uint32_t pcoded[4];
   uint32_t bad;
   uint32_t pad[3];
 };
 static_assert(sizeof(DecodeCtl) % 16 == 0, "DecodeCtl keeps the staging area 16-byte aligned");
+
+// Layout of a huff_ilv coded payload (tag 1): tag, n (4 bytes), the
+// weights header (0x80 | count, or 0x80 then count; then the 4-bit weights),
+// padding to 4 bytes, the block offset table (nb + 1 words), the blocks.
+// From the payload head `pay` (`avail` valid bytes) sets the table and data
+// offsets; false when the header's count bytes are invalid or the table
+// does not fit the payload's `len` bytes.
+__device__ __forceinline__ bool coded_layout(const uint8_t* pay, uint32_t avail, uint64_t len, uint32_t nb,
+                                             uint64_t& table, uint64_t& data) {
+  const uint32_t h0 = avail >= 6 ? pay[5] : 0u;
+  uint32_t hb = 0, nsym = 0;
+  if (h0 & 0x80u) {
+    if (h0 != 0x80u) {
+      hb = 1;
+      nsym = h0 & 0x7Fu;
+    } else if (avail >= 7) {
+      hb = 2;
+      nsym = pay[6] ? pay[6] : 256u;
+    }
+  }
+  uint64_t hd = 5 + hb + (nsym + 1) / 2;
+  hd += (4 - hd % 4) % 4;
+  table = hd;
+  data = hd + 4ull * (nb + 1);
+  return hb != 0 && data <= len;
+}
 
 // Build the tables of one plane from the weights header at hdr (LDS,
 // hdr_avail bytes valid), symbols transformed by `xf`: the pair table at
@@ -104,7 +133,7 @@ static_assert(sizeof(DecodeCtl) % 16 == 0, "DecodeCtl keeps the staging area 16-
 // values below lim[l], so a window's code length is 1 + the number of
 // limits it reaches and its symbol is sorted[base[len] + code].  Sets
 // bs.err (nonzero: invalid header), bs.pair and bs.hdr_len.
-__device__ void build_tables(uint16_t* tab, uint16_t* t64, bool pair_ok, uint32_t xf, BuildScratch& bs,
+__device__ __forceinline__ void build_tables(uint16_t* tab, uint16_t* t64, bool pair_ok, uint32_t xf, BuildScratch& bs,
                              const uint8_t* hdr, uint64_t hdr_avail) {
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
   // weights header (weights.rs): 0x80 | n, or 0x80, n (n = 128..256)
@@ -598,13 +627,14 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
 // tensors: all tensors of the call; tix[j]: the tensor of this launch's j-th
 // entry, whose 4-block tiles are tpre[j] .. tpre[j+1] - 1 (m entries,
 // n_tiles = tpre[m]).  Workgroup g takes tiles [g n_tiles / G, (g+1) n_tiles / G).
+// Four wavefronts per SIMD (four workgroups per CU, the LDS budget of the
+// one- and two-coded-plane chains) need at most 128 VGPRs per lane; the
+// four-plane IEEE-32 chain runs at two workgroups per CU (256 VGPRs).
 template <uint32_t kChain, bool kCrc>
-__global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __restrict__ tensors,
-                                                         const uint32_t* __restrict__ tix,
-                                                         const uint32_t* __restrict__ tpre, uint32_t m,
-                                                         uint32_t* __restrict__ status, uint32_t n_slots,
-                                                         uint32_t stage_words, const uint32_t* __restrict__ crc_tab,
-                                                         uint32_t* __restrict__ crc_part) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kChain == kChainIeee32Split4 ? 2 : 4)))
+ilv_decode_kernel(const IlvTensor* __restrict__ tensors, const uint32_t* __restrict__ tix,
+                  const uint32_t* __restrict__ tpre, uint32_t m, uint32_t* __restrict__ status, uint32_t n_slots,
+                  uint32_t stage_words, const uint32_t* __restrict__ crc_tab, uint32_t* __restrict__ crc_part) {
   constexpr uint32_t NP = ChainInfo<kChain>::np;
   constexpr uint32_t SLOT = chain_slot_bytes(kChain);
   // The kernel has no static LDS, so the dynamic area starts at LDS address
@@ -658,12 +688,121 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
     }
     for (uint32_t i = t; i < kIlvCrcWords; i += 256) crcT[i] = crc_tab[i < 1024 ? i : i - 1024 + kCrcTabS1024];
   }
+  // At a tensor's first tile each wavefront requests its block's offsets
+  // as soon as the payload heads are in LDS (while thread 0 parses them),
+  // then its lane counts, and touches every 128-byte line of the block
+  // before the tables are built (loads into one discarded register), so that
+  // the copy into LDS after the build reads from the L2 cache: the parse and
+  // the build hide the memory latency.
   for (uint32_t tile = tile0; tile < tile1; ++tile) {
     while (tile >= tpre[j + 1]) ++j;
     const uint32_t ti = tix[j];
     const IlvTensor& T = tensors[ti];
     const uint64_t n = T.n;
     const uint32_t nb = (uint32_t)((n + kIlvBlock - 1) / kIlvBlock);
+    const uint32_t bi = kIlvBlocksPerTile * (tile - tpre[j]) + wave;
+    // ---- block geometry of the wavefront's block (one wavefront per block) ----
+    BlockState<NP> st;
+    uint32_t lane_c[NP], tot[NP], first[NP];
+    uint32_t need = 4, need_skew = 0, uni_mask = 0;
+    bool ok = true, prepped = false, early = false;
+    uint32_t e_o0[NP], e_o1[NP], e_c[NP];  // offsets and count read before the build
+    uint32_t e_ready = 0;                  // planes whose e_o0 / e_o1 are requested
+    // block [o0, o1) of coded plane p; c = lane's word count (0 if rejected)
+    // offsets of an accepted stream are multiples of 4 (tab[0] == 0 and
+    // every block is 64 + 4 x words bytes long)
+    auto block_ok = [&](uint32_t p, uint32_t o0, uint32_t o1) -> bool {
+      return o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64 && (o0 & 3u) == 0 && (bi != 0 || o0 == 0) &&
+             (bi + 1 != nb || o1 == s_datalen[p]);
+    };
+    auto block_head = [&](uint32_t p, uint32_t& o0, uint32_t& o1, uint32_t& c) -> bool {
+      const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
+      o0 = gload_u32(tab + bi);
+      o1 = gload_u32(tab + bi + 1);
+      const bool bok = block_ok(p, o0, o1);
+      c = bok ? gload_u8(s_data[p] + o0 + lane) : 0u;
+      return bok;
+    };
+    // Loads issued here are consumed only after the build; every load is
+    // unconditional, with `safe` (the tensor descriptor) as the address of
+    // one that is not wanted, so no result is moved before it arrives.
+    const uint64_t safe = reinterpret_cast<uint64_t>(&T.n);
+    uint32_t e_touch[NP][2];
+    auto touch = [&]() {
+      early = true;
+#pragma unroll
+      for (uint32_t p = 0; p < NP; ++p) {
+        uint32_t o0 = 0, o1 = 0;
+        bool bok = false;
+        if (__builtin_amdgcn_readfirstlane(s_coded[p])) {
+          if ((e_ready >> p) & 1u) {
+            o0 = e_o0[p];
+            o1 = e_o1[p];
+            bok = block_ok(p, o0, o1);
+          } else {
+            uint32_t c;
+            bok = block_head(p, o0, o1, c);
+          }
+        }
+        // a rejected block reads as empty (prep then rejects it)
+        e_o0[p] = bok ? o0 : 0u;
+        e_o1[p] = bok ? o1 : 0u;
+        // the lane count, and the block's 128-byte lines (all inside the
+        // plane's data); blocks are at most 16 KiB + 64 bytes in practice,
+        // longer ones are read from memory after the build.  (Touching the
+        // raw planes' blocks as well was slower: the decode that reads them
+        // is bound by its VALU work, and the touches delay the staging.)
+        const uint64_t b = s_data[p] + o0;
+        const uint32_t len = bok ? o1 - o0 : 0u;
+        // (the word holding the lane's count byte: o0 is a multiple of 4)
+        e_c[p] = g_ld<uint32_t>(bok ? b + (lane & ~3u) : safe);
+        e_touch[p][0] = g_ld<uint32_t>(128 * lane < len ? b + 128 * lane : safe);
+        e_touch[p][1] = g_ld<uint32_t>(8192 + 128 * lane < len ? b + 8192 + 128 * lane : safe);
+      }
+    };
+    auto prep = [&]() {
+      prepped = true;
+      st.coded_mask = 0;
+      st.pair_mask = 0;
+      st.packed_mask = 0;
+#pragma unroll
+      for (uint32_t p = 0; p < NP; ++p) {
+        st.raw[p] = s_raw[p];
+        if (__builtin_amdgcn_readfirstlane(ctl.packed[p])) st.packed_mask |= 1u << p;
+        st.words[p] = nullptr;
+        st.nw[p] = 0;
+        st.q[p] = 0;
+        st.t64[p] = lds_addr(ctl.t64[p]);
+        st.lut[p] = luts + __builtin_amdgcn_readfirstlane(ctl.slot[p]) * SLOT;
+        lane_c[p] = tot[p] = first[p] = 0;
+        if (!__builtin_amdgcn_readfirstlane(s_coded[p])) continue;
+        st.coded_mask |= 1u << p;
+        uint32_t o0, o1, c;
+        bool bok;
+        if (early) {
+          o0 = e_o0[p];
+          o1 = e_o1[p];
+          bok = o1 - o0 >= 64;  // touch() leaves both 0 for a rejected block
+          c = bok ? (e_c[p] >> (8 * (lane & 3u))) & 0xFFu : 0u;
+        } else {
+          bok = block_head(p, o0, o1, c);
+        }
+        const uint8_t* blk = reinterpret_cast<const uint8_t*>(s_data[p]) + (bok ? o0 : 0);
+        const uint32_t incl = wave_incl_scan(c);
+        const uint32_t total = __shfl(incl, 63, 64);
+        if (!bok || 64u + 4u * total != o1 - o0) ok = false;
+        st.words[p] = reinterpret_cast<const uint32_t*>(blk + 64);
+        lane_c[p] = c;
+        tot[p] = total;
+        first[p] = incl - c;
+        need += (total + 3u) & ~3u;
+        const uint32_t c0 = __builtin_amdgcn_readfirstlane(c);
+        if (__ballot(c != c0) == 0 && c0 >= 4) {
+          uni_mask |= 1u << p;
+          need_skew += 128u;  // room for up to two skew words per lane
+        }
+      }
+    };
     if (ti != cur) {
       // ---- new tensor: parse its plane headers and build the LDS tables ----
       bad = wave_or_status(bad);
@@ -689,27 +828,58 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
         if (w == kIlvHeadWords) ctl.last[p] = v;
         else head[p][w] = v;
       }
+      if (t < NP) {
+        ctl.pbase[t] = T.planes[t].base;
+        ctl.plen[t] = T.planes[t].len;
+        ctl.pcoded[t] = T.planes[t].coded;
+      }
       __syncthreads();
+      // the block's offsets, requested while thread 0 parses the heads
+#pragma unroll
+      for (uint32_t p = 0; p < NP; ++p) {
+        const uint64_t len = ctl.plen[p];
+        const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
+        uint64_t tb = 0, dt = 0;
+        const bool v = bi < nb && ctl.pcoded[p] && len >= 5 && pay[0] == 1 &&
+                       coded_layout(pay, (uint32_t)(len < 4 * kIlvHeadWords ? len : 4 * kIlvHeadWords), len, nb, tb, dt);
+        // tb + 4 (bi + 2) <= dt <= len: inside the payload
+        const uint64_t a = ctl.pbase[p] + tb + 4ull * bi;
+        e_o0[p] = g_ld<uint32_t>(v ? a : safe);
+        e_o1[p] = g_ld<uint32_t>(v ? a + 4 : safe);
+        if (v) e_ready |= 1u << p;
+      }
       if (t == 0) {
         s_bad = 0;
         for (uint32_t p = 0; p < NP; ++p) {
-          const IlvPlane& P = T.planes[p];
-          s_raw[p] = P.base;
+          const uint64_t base = ctl.pbase[p], len = ctl.plen[p];
+          s_raw[p] = base;
           s_coded[p] = 0;
           ctl.packed[p] = 0;
-          if (!P.coded) continue;
+          if (!ctl.pcoded[p]) continue;
           // huff_ilv payload: tag 0 stores the plane after the tag byte, tag 2 packs it
           const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
-          if (P.len == 0) s_bad |= kIlvErrHeader;
+          if (len == 0) s_bad |= kIlvErrHeader;
           else if (pay[0] == 0) {
-            if (P.len != n + 1) s_bad |= kIlvErrHeader;
-            s_raw[p] = P.base + 1;
+            if (len != n + 1) s_bad |= kIlvErrHeader;
+            s_raw[p] = base + 1;
           } else if (pay[0] == 2) {
-            if (!packed_header_ok(pay, P.len, n, ctl.last[p])) s_bad |= kIlvErrHeader;
-            s_raw[p] = P.base + kPackedHeadBytes;
+            if (!packed_header_ok(pay, len, n, ctl.last[p])) s_bad |= kIlvErrHeader;
+            s_raw[p] = base + kPackedHeadBytes;
             ctl.packed[p] = 1;
-          } else if (pay[0] == 1 && P.len >= 5 && ld_u32le(pay + 1) == n) {
+          } else if (pay[0] == 1 && len >= 5 && ld_u32le(pay + 1) == n) {
             s_coded[p] = 1;
+            const uint32_t avail = (uint32_t)(len < 4 * kIlvHeadWords ? len : 4 * kIlvHeadWords);
+            ctl.hdr_avail[p] = avail - 5;
+            uint64_t tb, dt;
+            if (!coded_layout(pay, avail, len, nb, tb, dt)) {
+              s_bad |= kIlvErrHeader;
+            } else {
+              // tab[0] == 0 and tab[nb] == datalen are checked by the
+              // wavefronts of the first and last block
+              s_table[p] = base + tb;
+              s_data[p] = base + dt;
+              s_datalen[p] = len - dt;
+            }
           } else {
             s_bad |= kIlvErrHeader;
           }
@@ -729,86 +899,40 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
         }
       }
       __syncthreads();
-#pragma unroll
+      // (the build's barriers do not wait for global loads)
+      const bool touched = !s_bad && bi < nb;
+      if (touched) touch();
+#pragma unroll 1
       for (uint32_t p = 0; p < NP; ++p) {
         if (!s_coded[p]) continue;
-        const IlvPlane P = T.planes[p];
+        // no global loads here: they would wait for the touches (in order)
         uint16_t* tab16 = reinterpret_cast<uint16_t*>(smem + ctl.slot[p] * SLOT);
         const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
-        const uint64_t avail = P.len < 4 * kIlvHeadWords ? P.len : 4 * kIlvHeadWords;
         build_tables(tab16, ctl.t64[p], SLOT == kIlvPairLutBytes, ChainInfo<kChain>::xf[p], bs, pay + 5,
-                     avail >= 5 ? avail - 5 : 0);
+                     ctl.hdr_avail[p]);
         if (t == 0) {
           s_pair[p] = bs.pair;
           if (bs.err) s_bad |= kIlvErrHeader;
-          uint64_t head = 5 + bs.hdr_len;
-          head += (4 - head % 4) % 4;
-          const uint64_t data0 = head + 4ull * (nb + 1);
-          if (data0 > P.len) {
-            s_bad |= kIlvErrHeader;
-          } else {
-            // tab[0] == 0 and tab[nb] == datalen are checked by the
-            // wavefronts of the first and last block
-            s_table[p] = P.base + head;
-            s_data[p] = P.base + data0;
-            s_datalen[p] = P.len - data0;
-          }
         }
         __syncthreads();
+      }
+      if (touched) {  // the touches complete here
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) asm volatile("" ::"v"(e_touch[p][0]), "v"(e_touch[p][1]));
       }
       if (t == 0 && s_bad) atomicOr(&status[ti], s_bad);
     }
     if (s_bad) continue;  // uniform: the tensor is rejected
-    const uint32_t bi = kIlvBlocksPerTile * (tile - tpre[j]) + wave;
     if (bi >= nb) continue;
-    // ---- one wavefront per block ----
-    const uint64_t bstart = (uint64_t)bi * kIlvBlock;
-    BlockState<NP> st;
-    uint32_t lane_c[NP], tot[NP], first[NP];
-    uint32_t need = 4, need_skew = 0, uni_mask = 0;
-    bool ok = true;
-    st.coded_mask = 0;
-    st.pair_mask = 0;
-    st.packed_mask = 0;
-#pragma unroll
-    for (uint32_t p = 0; p < NP; ++p) {
-      st.raw[p] = s_raw[p];
-      if (__builtin_amdgcn_readfirstlane(ctl.packed[p])) st.packed_mask |= 1u << p;
-      st.words[p] = nullptr;
-      st.nw[p] = 0;
-      st.q[p] = 0;
-      st.t64[p] = lds_addr(ctl.t64[p]);
-      st.lut[p] = luts + __builtin_amdgcn_readfirstlane(ctl.slot[p]) * SLOT;
-      lane_c[p] = tot[p] = first[p] = 0;
-      if (!__builtin_amdgcn_readfirstlane(s_coded[p])) continue;
-      if (__builtin_amdgcn_readfirstlane(s_pair[p])) st.pair_mask |= 1u << p;
-      st.coded_mask |= 1u << p;
-      const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
-      const uint32_t o0 = gload_u32(tab + bi), o1 = gload_u32(tab + bi + 1);
-      // offsets of an accepted stream are multiples of 4 (tab[0] == 0 and
-      // every block is 64 + 4 x words bytes long)
-      const bool bok = o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64 && (o0 & 3u) == 0 &&
-                       (bi != 0 || o0 == 0) && (bi + 1 != nb || o1 == s_datalen[p]);
-      const uint8_t* blk = reinterpret_cast<const uint8_t*>(s_data[p]) + (bok ? o0 : 0);
-      const uint32_t c = bok ? gload_u8(reinterpret_cast<uint64_t>(blk) + lane) : 0u;
-      const uint32_t incl = wave_incl_scan(c);
-      const uint32_t total = __shfl(incl, 63, 64);
-      if (!bok || 64u + 4u * total != o1 - o0) ok = false;
-      st.words[p] = reinterpret_cast<const uint32_t*>(blk + 64);
-      lane_c[p] = c;
-      tot[p] = total;
-      first[p] = incl - c;
-      need += (total + 3u) & ~3u;
-      const uint32_t c0 = __builtin_amdgcn_readfirstlane(c);
-      if (__ballot(c != c0) == 0 && c0 >= 4) {
-        uni_mask |= 1u << p;
-        need_skew += 128u;  // room for up to two skew words per lane
-      }
-    }
+    if (!prepped) prep();
     if (!ok) {
       bad |= kIlvErrBlock;
       continue;
     }
+#pragma unroll
+    for (uint32_t p = 0; p < NP; ++p)
+      if ((st.coded_mask >> p) & 1u && __builtin_amdgcn_readfirstlane(s_pair[p])) st.pair_mask |= 1u << p;
+    const uint64_t bstart = (uint64_t)bi * kIlvBlock;
     // the fast path takes whole blocks of planes under 4 GiB whose raw
     // planes are aligned
     bool full = bstart + kIlvBlock <= n && n <= 0xFFFFFFFFull;
@@ -843,13 +967,13 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
         const uint32_t c0 = __builtin_amdgcn_readfirstlane(lane_c[p]);
         const bool uniform = (uni_mask >> p) & 1u;
         const uint32_t skew = uniform ? ((c0 & 1u) ? 2u : 1u) : 0u;
-        for (uint32_t i = 4 * lane; i < tot[p]; i += 256) {
+        // words i .. i + 3 (those below tot) to their staging positions
+        auto put = [&](uint32_t i, const uint32_t (&x)[4]) {
           if (!uniform) {
             if (i + 4 <= tot[p]) {
-              const u32x4a4 x = gload_u32x4(src + i);
-              *reinterpret_cast<u32x4*>(dst + i) = u32x4_make(x.x, x.y, x.z, x.w);
+              *reinterpret_cast<u32x4*>(dst + i) = u32x4_make(x[0], x[1], x[2], x[3]);
             } else {
-              for (uint32_t k = i; k < tot[p]; ++k) dst[k] = gload_u32(src + k);
+              for (uint32_t k = i; k < tot[p]; ++k) dst[k] = x[k - i];
             }
           } else {
             // lane of word i: i / c0 (float estimate, then exact correction);
@@ -858,22 +982,26 @@ __global__ void __launch_bounds__(256) ilv_decode_kernel(const IlvTensor* __rest
             if (j0 * c0 > i) --j0;
             if ((j0 + 1) * c0 <= i) ++j0;
             const uint32_t bnd = (j0 + 1) * c0;
-            uint32_t x[4] = {0, 0, 0, 0};
-            if (i + 4 <= tot[p]) {
-              const u32x4a4 v4 = gload_u32x4(src + i);
-              x[0] = v4.x;
-              x[1] = v4.y;
-              x[2] = v4.z;
-              x[3] = v4.w;
-            } else {
-              for (uint32_t k = i; k < tot[p]; ++k) x[k - i] = gload_u32(src + k);
-            }
 #pragma unroll
             for (uint32_t d = 0; d < 4; ++d) {
               const uint32_t w = i + d;
               if (w < tot[p]) dst[w + skew * (j0 + (w >= bnd ? 1u : 0u))] = x[d];
             }
           }
+        };
+        uint32_t i = 4 * lane;
+        for (; i < tot[p]; i += 256) {
+          uint32_t x[4] = {0, 0, 0, 0};
+          if (i + 4 <= tot[p]) {
+            const u32x4a4 v4 = gload_u32x4(src + i);
+            x[0] = v4.x;
+            x[1] = v4.y;
+            x[2] = v4.z;
+            x[3] = v4.w;
+          } else {
+            for (uint32_t k = i; k < tot[p]; ++k) x[k - i] = gload_u32(src + k);
+          }
+          put(i, x);
         }
         st.q[p] = lds_addr(dst + first[p] + skew * lane) * 8u - 1u;
         q0[p] = st.q[p];
