@@ -84,17 +84,32 @@ struct IlvPackJob {
   uint64_t n;
 };
 
+// A launch of at most kIlvInlineTensors tensors carries their descriptors
+// in its kernel arguments (no upload before it): tensor j of the launch is
+// t[j], its status word status[tix[j]], its tiles tpre[j] .. tpre[j+1] - 1.
+constexpr uint32_t kIlvInlineTensors = 4;
+struct IlvInline {
+  uint32_t m;  // 0: the descriptors are in device memory (the pointer arguments)
+  uint32_t tpre[kIlvInlineTensors + 1];
+  uint32_t tix[kIlvInlineTensors];
+  uint32_t pad[2];
+  IlvTensor t[kIlvInlineTensors];
+};
+
 // Fused decode of the tensors tix[0..m) (indexes into `tensors`, all of
 // chain `chain`); tensor tix[j] owns the 4-block tiles tpre[j] ..
-// tpre[j+1] - 1.  grid: persistent workgroups, each taking an equal range of
-// tiles.  n_slots: LDS table slots per workgroup (>= the coded planes of any
-// tensor); stage_words: LDS staging words per wavefront (multiple of 4);
-// blocks needing more are decoded from global memory.  crc_tab: the CRC
-// tables (crc_device.h layout) when some tensor has crc_first set, else
-// null; the kernel then also writes the CRC block partials to crc_part.
+// tpre[j+1] - 1 (or the same from `inl` when inl.m is nonzero).  grid:
+// persistent workgroups, each taking an equal range of tiles.  n_slots: LDS
+// table slots per workgroup (>= the coded planes of any tensor);
+// stage_words: LDS staging words per wavefront (multiple of 4); blocks
+// needing more are decoded from global memory.  status: one word per tensor
+// index, zero before the launch, in host-coherent memory (the kernel ORs
+// its error bits in at system scope).  crc_tab: the CRC tables
+// (crc_device.h layout) when some tensor has crc_first set, else null; the
+// kernel then also writes the CRC block partials to crc_part.
 hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uint32_t* tix, const uint32_t* tpre,
-                             uint32_t m, uint32_t grid, uint32_t* status, uint32_t n_slots, uint32_t stage_words,
-                             const uint32_t* crc_tab, uint32_t* crc_part, hipStream_t stream);
+                             uint32_t m, const IlvInline& inl, uint32_t grid, uint32_t* status, uint32_t n_slots,
+                             uint32_t stage_words, const uint32_t* crc_tab, uint32_t* crc_part, hipStream_t stream);
 size_t ilv_decode_lds_bytes(uint32_t chain, uint32_t n_slots, uint32_t stage_words, bool crc);
 hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage_words, bool crc, int* wg_per_cu);
 hipError_t launch_ilv_pack(const IlvPackJob* jobs, uint32_t n_jobs, uint64_t max_n, hipStream_t stream);

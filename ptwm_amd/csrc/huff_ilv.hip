@@ -42,6 +42,10 @@ namespace ptwm {
 
 namespace {
 
+// Constant address space: read-only global memory (and the kernel argument
+// segment); uniform loads through it become scalar loads.
+#define KConst __attribute__((address_space(4)))
+
 __device__ __forceinline__ uint32_t ld_u32le(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
@@ -632,9 +636,21 @@ __device__ __forceinline__ void decode_block(BlockState<ChainInfo<kChain>::np>& 
 // four-plane IEEE-32 chain runs at two workgroups per CU (256 VGPRs).
 template <uint32_t kChain, bool kCrc>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kChain == kChainIeee32Split4 ? 2 : 4)))
-ilv_decode_kernel(const IlvTensor* __restrict__ tensors, const uint32_t* __restrict__ tix,
-                  const uint32_t* __restrict__ tpre, uint32_t m, uint32_t* __restrict__ status, uint32_t n_slots,
-                  uint32_t stage_words, const uint32_t* __restrict__ crc_tab, uint32_t* __restrict__ crc_part) {
+ilv_decode_kernel(IlvInline inl_arg, const IlvTensor* __restrict__ tensors, const uint32_t* __restrict__ tix_mem,
+                  const uint32_t* __restrict__ tpre_mem, uint32_t m_mem, uint32_t* __restrict__ status,
+                  uint32_t n_slots, uint32_t stage_words, const uint32_t* __restrict__ crc_tab,
+                  uint32_t* __restrict__ crc_part) {
+  // Descriptors from the kernel arguments or from device memory, both read
+  // through constant-address-space pointers (uniform: scalar loads).  The
+  // inline ones are read in place (the first argument: offset 0 of the
+  // kernel argument segment); naming the by-value argument would copy it to
+  // per-lane scratch.
+  (void)inl_arg;
+  const KConst IlvInline& inl = *(const KConst IlvInline*)__builtin_amdgcn_kernarg_segment_ptr();
+  const bool inl_on = inl.m != 0;
+  const uint32_t m = inl_on ? inl.m : m_mem;
+  const KConst uint32_t* const tix = inl_on ? inl.tix : (const KConst uint32_t*)tix_mem;
+  const KConst uint32_t* const tpre = inl_on ? inl.tpre : (const KConst uint32_t*)tpre_mem;
   constexpr uint32_t NP = ChainInfo<kChain>::np;
   constexpr uint32_t SLOT = chain_slot_bytes(kChain);
   // The kernel has no static LDS, so the dynamic area starts at LDS address
@@ -662,7 +678,7 @@ ilv_decode_kernel(const IlvTensor* __restrict__ tensors, const uint32_t* __restr
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
   if (luts & (SLOT - 1)) {
     // not reachable with the layout above; refuse rather than mis-decode
-    if (t == 0 && blockIdx.x == 0) atomicOr(&status[tix[0]], kIlvErrHeader);
+    if (t == 0 && blockIdx.x == 0) status_or(&status[tix[0]], kIlvErrHeader);
     return;
   }
   const uint32_t n_tiles = tpre[m];
@@ -683,7 +699,7 @@ ilv_decode_kernel(const IlvTensor* __restrict__ tensors, const uint32_t* __restr
     // T0..T3 and the byte-sliced advance over 1 KiB
     uint32_t* const crcT = reinterpret_cast<uint32_t*>(lds);
     if (lds_addr(crcT) != 0) {  // not reachable: the kernel has no static LDS
-      if (t == 0 && blockIdx.x == 0) atomicOr(&status[tix[0]], kIlvErrHeader);
+      if (t == 0 && blockIdx.x == 0) status_or(&status[tix[0]], kIlvErrHeader);
       return;
     }
     for (uint32_t i = t; i < kIlvCrcWords; i += 256) crcT[i] = crc_tab[i < 1024 ? i : i - 1024 + kCrcTabS1024];
@@ -697,7 +713,7 @@ ilv_decode_kernel(const IlvTensor* __restrict__ tensors, const uint32_t* __restr
   for (uint32_t tile = tile0; tile < tile1; ++tile) {
     while (tile >= tpre[j + 1]) ++j;
     const uint32_t ti = tix[j];
-    const IlvTensor& T = tensors[ti];
+    const KConst IlvTensor& T = inl_on ? inl.t[j] : *(const KConst IlvTensor*)(tensors + ti);
     const uint64_t n = T.n;
     const uint32_t nb = (uint32_t)((n + kIlvBlock - 1) / kIlvBlock);
     const uint32_t bi = kIlvBlocksPerTile * (tile - tpre[j]) + wave;
@@ -806,7 +822,7 @@ ilv_decode_kernel(const IlvTensor* __restrict__ tensors, const uint32_t* __restr
     if (ti != cur) {
       // ---- new tensor: parse its plane headers and build the LDS tables ----
       bad = wave_or_status(bad);
-      if (bad && lane == 0) atomicOr(&status[cur], bad);
+      if (bad && lane == 0) status_or(&status[cur], bad);
       bad = 0;
       cur = ti;
       __syncthreads();  // every wavefront is done with the previous tables
@@ -920,7 +936,7 @@ ilv_decode_kernel(const IlvTensor* __restrict__ tensors, const uint32_t* __restr
 #pragma unroll
         for (uint32_t p = 0; p < NP; ++p) asm volatile("" ::"v"(e_touch[p][0]), "v"(e_touch[p][1]));
       }
-      if (t == 0 && s_bad) atomicOr(&status[ti], s_bad);
+      if (t == 0 && s_bad) status_or(&status[ti], s_bad);
     }
     if (s_bad) continue;  // uniform: the tensor is rejected
     if (bi >= nb) continue;
@@ -1057,7 +1073,7 @@ ilv_decode_kernel(const IlvTensor* __restrict__ tensors, const uint32_t* __restr
     }
   }
   bad = wave_or_status(bad);
-  if (bad && lane == 0) atomicOr(&status[cur], bad);
+  if (bad && lane == 0) status_or(&status[cur], bad);
 }
 
 // ---------------------------------------------------------------------------
@@ -1254,16 +1270,18 @@ hipError_t ilv_decode_occupancy(uint32_t chain, uint32_t n_slots, uint32_t stage
 }
 
 hipError_t launch_ilv_decode(uint32_t chain, const IlvTensor* tensors, const uint32_t* tix, const uint32_t* tpre,
-                             uint32_t m, uint32_t grid, uint32_t* status, uint32_t n_slots, uint32_t stage_words,
-                             const uint32_t* crc_tab, uint32_t* crc_part, hipStream_t stream) {
-  if (!grid || !m) return hipSuccess;
+                             uint32_t m, const IlvInline& inl_in, uint32_t grid, uint32_t* status, uint32_t n_slots,
+                             uint32_t stage_words, const uint32_t* crc_tab, uint32_t* crc_part, hipStream_t stream) {
+  if (!grid || !(inl_in.m ? inl_in.m : m)) return hipSuccess;
+  if (inl_in.m > kIlvInlineTensors) return hipErrorInvalidValue;
+  IlvInline inl = inl_in;
   if (stage_words % 4 != 0 || stage_words < 8) return hipErrorInvalidValue;
   const bool crc = crc_tab != nullptr;
   if (crc && (!crc_part || !ilv_crc_chain(chain))) return hipErrorInvalidValue;
   const size_t lds = ilv_decode_lds_bytes(chain, n_slots, stage_words, crc);
   const void* fn = ilv_decode_fn(chain, crc);
   if (!fn) return hipErrorInvalidValue;
-  void* args[] = {&tensors, &tix, &tpre, &m, &status, &n_slots, &stage_words, &crc_tab, &crc_part};
+  void* args[] = {&inl, &tensors, &tix, &tpre, &m, &status, &n_slots, &stage_words, &crc_tab, &crc_part};
   const hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, lds, stream);
   return e != hipSuccess ? e : hipGetLastError();
 }

@@ -304,6 +304,13 @@ __device__ __forceinline__ void store_group_full(uint64_t dst, uint32_t lane, co
   }
 }
 
+// Error bits into a tensor's status word.  The status words live in
+// host-coherent (pinned) memory that the host reads after the stream has
+// drained: system scope, a vector atomic.
+__device__ __forceinline__ void status_or(uint32_t* w, uint32_t v) {
+  __hip_atomic_fetch_or(w, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // OR of a status word (bits 0..7) over the wavefront's active lanes, so
 // that one lane reports it: per-lane atomics on one status word serialise.
 __device__ __forceinline__ uint32_t wave_or_status(uint32_t v) {

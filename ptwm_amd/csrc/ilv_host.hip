@@ -387,43 +387,63 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     idx.insert(idx.end(), tpre.begin(), tpre.end());
     idx.insert(idx.end(), tix.begin(), tix.end());
   }
-  // one upload: [tensor descriptors][launch index arrays][zeroed status words]
+  // Launches of at most kIlvInlineTensors huff_ilv tensors take their
+  // descriptors in the kernel arguments; the others read them from one
+  // upload: [tensor descriptors][launch index arrays].  The status words are
+  // host-coherent: zeroed here, ORed by the kernels, read after the stream
+  // has drained (no copy back).
+  PTWM_HIP_TRY(ctx.h_ilv_status.ensure(nt * sizeof(uint32_t)));
+  uint32_t* const hs = static_cast<uint32_t*>(ctx.h_ilv_status.ptr);
+  std::memset(hs, 0, nt * sizeof(uint32_t));
+  auto inline_ok = [](const Launch& L) { return L.family == kFamilyHuff && L.m <= kIlvInlineTensors; };
+  bool upload = false;
+  for (const Launch& L : launches) upload |= !inline_ok(L);
   const size_t off_idx = align_up(nt * sizeof(IlvTensor), 16);
-  const size_t off_status = align_up(off_idx + idx.size() * sizeof(uint32_t), 16);
-  const size_t args_bytes = off_status + nt * sizeof(uint32_t);
-  PTWM_HIP_TRY(ctx.ilv_args.ensure(args_bytes));
-  PTWM_HIP_TRY(ctx.h_ilv.ensure(args_bytes + nt * sizeof(uint32_t)));
-  uint8_t* h = static_cast<uint8_t*>(ctx.h_ilv.ptr);
-  std::memcpy(h, tensors.data(), nt * sizeof(IlvTensor));
-  std::memcpy(h + off_idx, idx.data(), idx.size() * sizeof(uint32_t));
-  std::memset(h + off_status, 0, nt * sizeof(uint32_t));
-  uint8_t* d = static_cast<uint8_t*>(ctx.ilv_args.ptr);
-  PTWM_HIP_TRY(hipMemcpyAsync(d, h, args_bytes, hipMemcpyHostToDevice, s));
+  const size_t args_bytes = off_idx + idx.size() * sizeof(uint32_t);
+  uint8_t* d = nullptr;
+  if (upload) {
+    PTWM_HIP_TRY(ctx.ilv_args.ensure(args_bytes));
+    PTWM_HIP_TRY(ctx.h_ilv.ensure(args_bytes));
+    uint8_t* h = static_cast<uint8_t*>(ctx.h_ilv.ptr);
+    std::memcpy(h, tensors.data(), nt * sizeof(IlvTensor));
+    std::memcpy(h + off_idx, idx.data(), idx.size() * sizeof(uint32_t));
+    d = static_cast<uint8_t*>(ctx.ilv_args.ptr);
+    PTWM_HIP_TRY(hipMemcpyAsync(d, h, args_bytes, hipMemcpyHostToDevice, s));
+  }
   if (ctx.profile) {
     PTWM_HIP_TRY(ctx.ensure_events());
     PTWM_HIP_TRY(hipEventRecord(ctx.ev[3], s));
   }
-  uint32_t* status_dev = reinterpret_cast<uint32_t*>(d + off_status);
   const uint32_t* crc_tab = nullptr;
   for (const Launch& L : launches)
     if (L.crc && !crc_tab)
       if (int64_t rc = crc_tables(ctx, &crc_tab); rc != kOk) return rc;
   for (const Launch& L : launches) {
+    const uint32_t* hidx = idx.data() + L.first;  // [m + 1 prefix][m tensor indexes]
+    if (inline_ok(L)) {
+      IlvInline inl{};
+      inl.m = L.m;
+      for (uint32_t j = 0; j <= L.m; ++j) inl.tpre[j] = hidx[j];
+      for (uint32_t j = 0; j < L.m; ++j) {
+        inl.tix[j] = hidx[L.m + 1 + j];
+        inl.t[j] = tensors[inl.tix[j]];
+      }
+      PTWM_HIP_TRY(launch_ilv_decode(L.chain, nullptr, nullptr, nullptr, 0, inl, L.grid, hs, L.slots,
+                                     L.stage_words, L.crc ? crc_tab : nullptr,
+                                     static_cast<uint32_t*>(ctx.crc_part.ptr), s));
+      continue;
+    }
     const uint32_t* base = reinterpret_cast<const uint32_t*>(d + off_idx) + L.first;
     const IlvTensor* td = reinterpret_cast<const IlvTensor*>(d);
     if (L.family == kFamilyHuff)
-      PTWM_HIP_TRY(launch_ilv_decode(L.chain, td, base + L.m + 1, base, L.m, L.grid, status_dev, L.slots,
+      PTWM_HIP_TRY(launch_ilv_decode(L.chain, td, base + L.m + 1, base, L.m, IlvInline{}, L.grid, hs, L.slots,
                                      L.stage_words, L.crc ? crc_tab : nullptr,
                                      static_cast<uint32_t*>(ctx.crc_part.ptr), s));
     else
-      PTWM_HIP_TRY(launch_rilv_decode(L.chain, td, base + L.m + 1, base, L.m, L.grid, status_dev, L.slots,
+      PTWM_HIP_TRY(launch_rilv_decode(L.chain, td, base + L.m + 1, base, L.m, L.grid, hs, L.slots,
                                       L.stage_words, s));
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], s));
-  // status read back into the host buffer's tail (the upload above is
-  // ordered before it on the same stream)
-  uint32_t* hs = reinterpret_cast<uint32_t*>(h + args_bytes);
-  PTWM_HIP_TRY(hipMemcpyAsync(hs, status_dev, nt * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   PTWM_HIP_TRY(hipStreamSynchronize(s));
   if (ctx.profile) {
     float ms = 0;

@@ -225,7 +225,7 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
     if (ti != cur) {
       // ---- new tensor: parse the plane headers, build the slot tables ----
       bad = wave_or_status(bad);
-      if (bad && lane == 0) atomicOr(&status[cur], bad);
+      if (bad && lane == 0) status_or(&status[cur], bad);
       bad = 0;
       cur = ti;
       __syncthreads();
@@ -327,7 +327,7 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
                                    ChainInfo<kChain>::xf[p]);
         __syncthreads();
       }
-      if (t == 0 && ctl.bad) atomicOr(&status[ti], ctl.bad);
+      if (t == 0 && ctl.bad) status_or(&status[ti], ctl.bad);
     }
     if (ctl.bad) continue;  // uniform: the tensor is rejected
     const uint32_t bi = kIlvBlocksPerTile * (tile - tpre[j]) + wave;
@@ -411,7 +411,7 @@ __global__ void __launch_bounds__(256) rilv_decode_kernel(const IlvTensor* __res
     }
   }
   bad = wave_or_status(bad);
-  if (bad && lane == 0) atomicOr(&status[cur], bad);
+  if (bad && lane == 0) status_or(&status[cur], bad);
 }
 
 // ---------------------------------------------------------------------------

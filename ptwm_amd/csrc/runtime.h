@@ -29,6 +29,7 @@ struct PinnedBuffer {
   void* ptr = nullptr;
   size_t cap = 0;
   bool borrowed = false;
+  unsigned flags = hipHostMallocDefault;  // hipHostMallocCoherent: kernels write it directly
   hipError_t ensure(size_t bytes);
   ~PinnedBuffer();
 };
@@ -47,6 +48,9 @@ constexpr uint64_t kNoAllocStubOff = kNoAllocCombOff + kNoAllocCombBytes, kNoAll
 constexpr uint64_t kNoAllocPartOff = kNoAllocStubOff + kNoAllocStubBytes;
 constexpr uint64_t kNoAllocPartBytes = kNoAllocScratchBytes - kNoAllocPartOff;
 constexpr uint64_t kNoAllocHostBytes = 1ull << 20;
+// host-coherent status words of the fused decode (one per tensor)
+constexpr uint64_t kNoAllocStatusBytes = 16ull << 10;
+static_assert(kNoAllocStatusBytes >= 4ull * 4096, "a status word for every tensor the allocation-free decode takes");
 // limits of a plan the allocation-free decode accepts
 constexpr uint32_t kNoAllocMaxTensors = 4096;
 constexpr uint64_t kNoAllocMaxCrcBlocks = kNoAllocPartBytes / 16;
@@ -88,6 +92,8 @@ struct DevCtx {
   DeviceBuffer ref_jobs, ref_hist, ref_segs, ref_seglen, ref_codes, ref_rans_tab, ref_rans_segs, ref_rans_scratch,
       ref_rans_len, ref_hdr, ref_pack, ref_ops;
   PinnedBuffer h_enc, h_ilv;
+  // fused-decode status words, written by the kernels (host-coherent)
+  PinnedBuffer h_ilv_status;
   // parallel Huffman decode of reference streams
   DeviceBuffer sync_streams, sync_tables, sync_sub, sync_waves, copy_args;
   // inverse plane ops (plane_ops.hip): job list and IntDelta tile sums
@@ -117,6 +123,7 @@ struct DevCtx {
   // in the scratch yet
   uint8_t* noalloc_dev = nullptr;
   std::unique_ptr<uint8_t[]> noalloc_host;
+  void* noalloc_status = nullptr;  // kNoAllocStatusBytes of host-coherent memory
   bool noalloc_tab_ready = false;
 };
 

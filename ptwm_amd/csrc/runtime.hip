@@ -45,7 +45,7 @@ hipError_t PinnedBuffer::ensure(size_t bytes) {
     cap = 0;
   }
   size_t want = bytes < 4096 ? 4096 : bytes;
-  hipError_t e = hipHostMalloc(&ptr, want, hipHostMallocDefault);
+  hipError_t e = hipHostMalloc(&ptr, want, flags);
   if (e == hipSuccess) cap = want;
   return e;
 }
@@ -89,11 +89,13 @@ DevCtx* get_ctx(uint32_t ord) {
     return nullptr;
   }
   ctx->stream = ctx->own_stream;
+  ctx->h_ilv_status.flags = hipHostMallocCoherent;
   // the allocation-free decode's scratch on this device (the device is
   // current): its address, or null, and the entry point then reports
   // MissingCapability
   void* sp = nullptr;
-  if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess && sp) {
+  if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess && sp &&
+      hipHostMalloc(&ctx->noalloc_status, kNoAllocStatusBytes, hipHostMallocCoherent) == hipSuccess) {
     ctx->noalloc_dev = static_cast<uint8_t*>(sp);
     ctx->noalloc_host.reset(new uint8_t[kNoAllocHostBytes]);
   } else {
@@ -129,8 +131,8 @@ namespace {
 struct Borrow {
   DeviceBuffer* dst[9];
   DeviceBuffer saved[9];
-  PinnedBuffer* hdst[3];
-  PinnedBuffer hsaved[3];
+  PinnedBuffer* hdst[4];
+  PinnedBuffer hsaved[4];
   bool tab_ready;
   DevCtx& ctx;
   explicit Borrow(DevCtx& c) : ctx(c) {
@@ -155,13 +157,14 @@ struct Borrow {
       v[i].b->borrowed = true;
     }
     uint8_t* h = c.noalloc_host.get();
-    PinnedBuffer* hb[3] = {&c.h_ilv, &c.h_jobs, &c.h_status};
-    const uint64_t hoff[3] = {0, kNoAllocHostBytes - 2048, kNoAllocHostBytes - 1024};
-    const uint64_t hlen[3] = {kNoAllocHostBytes - 2048, 1024, 1024};
-    for (int i = 0; i < 3; ++i) {
+    PinnedBuffer* hb[4] = {&c.h_ilv, &c.h_jobs, &c.h_status, &c.h_ilv_status};
+    uint8_t* const hbase[4] = {h, h, h, static_cast<uint8_t*>(c.noalloc_status)};
+    const uint64_t hoff[4] = {0, kNoAllocHostBytes - 2048, kNoAllocHostBytes - 1024, 0};
+    const uint64_t hlen[4] = {kNoAllocHostBytes - 2048, 1024, 1024, kNoAllocStatusBytes};
+    for (int i = 0; i < 4; ++i) {
       hdst[i] = hb[i];
       hsaved[i] = *hb[i];
-      hb[i]->ptr = h + hoff[i];
+      hb[i]->ptr = hbase[i] + hoff[i];
       hb[i]->cap = hlen[i];
       hb[i]->borrowed = true;
     }
@@ -172,7 +175,7 @@ struct Borrow {
     ctx.noalloc_tab_ready = ctx.crc_tab_ready;
     ctx.crc_tab_ready = tab_ready;
     for (int i = 0; i < 9; ++i) *dst[i] = saved[i];
-    for (int i = 0; i < 3; ++i) *hdst[i] = hsaved[i];
+    for (int i = 0; i < 4; ++i) *hdst[i] = hsaved[i];
   }
 };
 
