@@ -181,7 +181,7 @@ def build_workload(name: str, resident: bool = False, integrity: bool = False) -
     elif name == "mxfp4":
         specs = [((14336, 2048), "fp4"), ((14336, 128), "e8m0")]
         desc = "config 5: MXFP4 weights 14336x2048 (nibble split) + E8M0 scales 14336x128 (byte plane)"
-        kernel = "ilv_decode_kernel<5>, <6>"
+        kernel = "ilv_decode_kernel<0x156> (two-chain launch: nibble split 5 + passthrough 6)"
     # the configs in the reference's own plane formats (GPU-encoded, byte-identical
     # to the reference encoder), decoded by the exact route
     elif name == "c1_ref":
@@ -238,7 +238,7 @@ def kernel_label(wl, crc: bool) -> str:
     if k == EXACT_ROUTE or k.startswith("rilv"):
         return k
     fused = crc and any(t.chain in (1, 2, 6) for t in wl.plans)
-    k = re.sub(r"<(\d)>", lambda m: f"<{m.group(1)}, {'true' if fused else 'false'}>", k)
+    k = re.sub(r"<(\d|0x[0-9a-f]+)>", lambda m: f"<{m.group(1)}, {'true' if fused else 'false'}>", k)
     return k + (" + plane CRC-32 fused" if fused else "")
 
 

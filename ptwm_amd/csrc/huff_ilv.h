@@ -84,6 +84,19 @@ struct IlvPackJob {
   uint64_t n;
 };
 
+// Launch chain code of the two-chain decode kernel: tensors of chains `a`
+// and `b` (huff_ilv family, no fused CRC) in one launch, e.g. MXFP4 weights
+// (nibble split) with their E8M0 scales (passthrough).
+constexpr uint32_t ilv_chain_pair(uint32_t a, uint32_t b) { return 0x100u | a << 4 | b; }
+constexpr bool ilv_is_pair(uint32_t code) { return code >= 0x100u; }
+constexpr uint32_t ilv_pair_a(uint32_t code) { return (code >> 4) & 15u; }
+constexpr uint32_t ilv_pair_b(uint32_t code) { return code & 15u; }
+constexpr uint32_t kIlvPairNibblePass = ilv_chain_pair(5, 6);
+// whether a tensor of chain `chain` belongs to a launch of chain code `code`
+constexpr bool ilv_code_has(uint32_t code, uint32_t chain) {
+  return ilv_is_pair(code) ? (chain == ilv_pair_a(code) || chain == ilv_pair_b(code)) : chain == code;
+}
+
 // A launch of at most kIlvInlineTensors tensors carries their descriptors
 // in its kernel arguments (no upload before it): tensor j of the launch is
 // t[j], its status word status[tix[j]], its tiles tpre[j] .. tpre[j+1] - 1.

@@ -462,8 +462,18 @@ static_assert(sizeof(DecodeCtl) <= 3072, "LDS control block stays small");
 
 // LDS table slot size of a chain's coded planes (pair-mode capable or not).
 __host__ __device__ constexpr uint32_t chain_slot_bytes(uint32_t chain) {
-  return chain == kChainIeee16Split2 || chain == kChainIeee32Split4 ? kIlvLutBytes : kIlvPairLutBytes;
+  // a two-chain launch: the larger of its chains' slots
+  return ilv_is_pair(chain) ? (chain_slot_bytes(ilv_pair_a(chain)) > chain_slot_bytes(ilv_pair_b(chain))
+                                   ? chain_slot_bytes(ilv_pair_a(chain))
+                                   : chain_slot_bytes(ilv_pair_b(chain)))
+         : chain == kChainIeee16Split2 || chain == kChainIeee32Split4 ? kIlvLutBytes
+                                                                        : kIlvPairLutBytes;
 }
+
+template <uint32_t C>
+struct ChainTag {
+  static constexpr uint32_t value = C;
+};
 
 // Per-block state of one wavefront: for each plane, a raw-byte base or a
 // coded stream (staged: absolute LDS bit address; global: lane word pointer,
@@ -651,7 +661,6 @@ ilv_decode_kernel(IlvInline inl_arg, const IlvTensor* __restrict__ tensors, cons
   const uint32_t m = inl_on ? inl.m : m_mem;
   const KConst uint32_t* const tix = inl_on ? inl.tix : (const KConst uint32_t*)tix_mem;
   const KConst uint32_t* const tpre = inl_on ? inl.tpre : (const KConst uint32_t*)tpre_mem;
-  constexpr uint32_t NP = ChainInfo<kChain>::np;
   constexpr uint32_t SLOT = chain_slot_bytes(kChain);
   // The kernel has no static LDS, so the dynamic area starts at LDS address
   // 0 and every table sits on a SLOT boundary (entry address =
@@ -714,362 +723,374 @@ ilv_decode_kernel(IlvInline inl_arg, const IlvTensor* __restrict__ tensors, cons
     while (tile >= tpre[j + 1]) ++j;
     const uint32_t ti = tix[j];
     const KConst IlvTensor& T = inl_on ? inl.t[j] : *(const KConst IlvTensor*)(tensors + ti);
-    const uint64_t n = T.n;
-    const uint32_t nb = (uint32_t)((n + kIlvBlock - 1) / kIlvBlock);
-    const uint32_t bi = kIlvBlocksPerTile * (tile - tpre[j]) + wave;
-    // ---- block geometry of the wavefront's block (one wavefront per block) ----
-    BlockState<NP> st;
-    uint32_t lane_c[NP], tot[NP], first[NP];
-    uint32_t need = 4, need_skew = 0, uni_mask = 0;
-    bool ok = true, prepped = false, early = false;
-    uint32_t e_o0[NP], e_o1[NP], e_c[NP];  // offsets and count read before the build
-    uint32_t e_ready = 0;                  // planes whose e_o0 / e_o1 are requested
-    // block [o0, o1) of coded plane p; c = lane's word count (0 if rejected)
-    // offsets of an accepted stream are multiples of 4 (tab[0] == 0 and
-    // every block is 64 + 4 x words bytes long)
-    auto block_ok = [&](uint32_t p, uint32_t o0, uint32_t o1) -> bool {
-      return o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64 && (o0 & 3u) == 0 && (bi != 0 || o0 == 0) &&
-             (bi + 1 != nb || o1 == s_datalen[p]);
-    };
-    auto block_head = [&](uint32_t p, uint32_t& o0, uint32_t& o1, uint32_t& c) -> bool {
-      const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
-      o0 = gload_u32(tab + bi);
-      o1 = gload_u32(tab + bi + 1);
-      const bool bok = block_ok(p, o0, o1);
-      c = bok ? gload_u8(s_data[p] + o0 + lane) : 0u;
-      return bok;
-    };
-    // Loads issued here are consumed only after the build; every load is
-    // unconditional, with `safe` (the tensor descriptor) as the address of
-    // one that is not wanted, so no result is moved before it arrives.
-    const uint64_t safe = reinterpret_cast<uint64_t>(&T.n);
-    uint32_t e_touch[NP][2];
-    auto touch = [&]() {
-      early = true;
+    // the tile, decoded by the code of its tensor's chain (a two-chain
+    // launch holds both)
+    auto body = [&](auto tag) {
+      constexpr uint32_t C = decltype(tag)::value;
+      constexpr uint32_t NP = ChainInfo<C>::np;
+      const uint64_t n = T.n;
+      const uint32_t nb = (uint32_t)((n + kIlvBlock - 1) / kIlvBlock);
+      const uint32_t bi = kIlvBlocksPerTile * (tile - tpre[j]) + wave;
+      // ---- block geometry of the wavefront's block (one wavefront per block) ----
+      BlockState<NP> st;
+      uint32_t lane_c[NP], tot[NP], first[NP];
+      uint32_t need = 4, need_skew = 0, uni_mask = 0;
+      bool ok = true, prepped = false, early = false;
+      uint32_t e_o0[NP], e_o1[NP], e_c[NP];  // offsets and count read before the build
+      uint32_t e_ready = 0;                  // planes whose e_o0 / e_o1 are requested
+      // block [o0, o1) of coded plane p; c = lane's word count (0 if rejected)
+      // offsets of an accepted stream are multiples of 4 (tab[0] == 0 and
+      // every block is 64 + 4 x words bytes long)
+      auto block_ok = [&](uint32_t p, uint32_t o0, uint32_t o1) -> bool {
+        return o1 >= o0 && o1 <= s_datalen[p] && o1 - o0 >= 64 && (o0 & 3u) == 0 && (bi != 0 || o0 == 0) &&
+               (bi + 1 != nb || o1 == s_datalen[p]);
+      };
+      auto block_head = [&](uint32_t p, uint32_t& o0, uint32_t& o1, uint32_t& c) -> bool {
+        const uint32_t* tab = reinterpret_cast<const uint32_t*>(s_table[p]);
+        o0 = gload_u32(tab + bi);
+        o1 = gload_u32(tab + bi + 1);
+        const bool bok = block_ok(p, o0, o1);
+        c = bok ? gload_u8(s_data[p] + o0 + lane) : 0u;
+        return bok;
+      };
+      // Loads issued here are consumed only after the build; every load is
+      // unconditional, with `safe` (the tensor descriptor) as the address of
+      // one that is not wanted, so no result is moved before it arrives.
+      const uint64_t safe = reinterpret_cast<uint64_t>(&T.n);
+      uint32_t e_touch[NP][2];
+      auto touch = [&]() {
+        early = true;
 #pragma unroll
-      for (uint32_t p = 0; p < NP; ++p) {
-        uint32_t o0 = 0, o1 = 0;
-        bool bok = false;
-        if (__builtin_amdgcn_readfirstlane(s_coded[p])) {
-          if ((e_ready >> p) & 1u) {
+        for (uint32_t p = 0; p < NP; ++p) {
+          uint32_t o0 = 0, o1 = 0;
+          bool bok = false;
+          if (__builtin_amdgcn_readfirstlane(s_coded[p])) {
+            if ((e_ready >> p) & 1u) {
+              o0 = e_o0[p];
+              o1 = e_o1[p];
+              bok = block_ok(p, o0, o1);
+            } else {
+              uint32_t c;
+              bok = block_head(p, o0, o1, c);
+            }
+          }
+          // a rejected block reads as empty (prep then rejects it)
+          e_o0[p] = bok ? o0 : 0u;
+          e_o1[p] = bok ? o1 : 0u;
+          // the lane count, and the block's 128-byte lines (all inside the
+          // plane's data); blocks are at most 16 KiB + 64 bytes in practice,
+          // longer ones are read from memory after the build.  (Touching the
+          // raw planes' blocks as well was slower: the decode that reads them
+          // is bound by its VALU work, and the touches delay the staging.)
+          const uint64_t b = s_data[p] + o0;
+          const uint32_t len = bok ? o1 - o0 : 0u;
+          // (the word holding the lane's count byte: o0 is a multiple of 4)
+          e_c[p] = g_ld<uint32_t>(bok ? b + (lane & ~3u) : safe);
+          e_touch[p][0] = g_ld<uint32_t>(128 * lane < len ? b + 128 * lane : safe);
+          e_touch[p][1] = g_ld<uint32_t>(8192 + 128 * lane < len ? b + 8192 + 128 * lane : safe);
+        }
+      };
+      auto prep = [&]() {
+        prepped = true;
+        st.coded_mask = 0;
+        st.pair_mask = 0;
+        st.packed_mask = 0;
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+          st.raw[p] = s_raw[p];
+          if (__builtin_amdgcn_readfirstlane(ctl.packed[p])) st.packed_mask |= 1u << p;
+          st.words[p] = nullptr;
+          st.nw[p] = 0;
+          st.q[p] = 0;
+          st.t64[p] = lds_addr(ctl.t64[p]);
+          st.lut[p] = luts + __builtin_amdgcn_readfirstlane(ctl.slot[p]) * SLOT;
+          lane_c[p] = tot[p] = first[p] = 0;
+          if (!__builtin_amdgcn_readfirstlane(s_coded[p])) continue;
+          st.coded_mask |= 1u << p;
+          uint32_t o0, o1, c;
+          bool bok;
+          if (early) {
             o0 = e_o0[p];
             o1 = e_o1[p];
-            bok = block_ok(p, o0, o1);
+            bok = o1 - o0 >= 64;  // touch() leaves both 0 for a rejected block
+            c = bok ? (e_c[p] >> (8 * (lane & 3u))) & 0xFFu : 0u;
           } else {
-            uint32_t c;
             bok = block_head(p, o0, o1, c);
           }
-        }
-        // a rejected block reads as empty (prep then rejects it)
-        e_o0[p] = bok ? o0 : 0u;
-        e_o1[p] = bok ? o1 : 0u;
-        // the lane count, and the block's 128-byte lines (all inside the
-        // plane's data); blocks are at most 16 KiB + 64 bytes in practice,
-        // longer ones are read from memory after the build.  (Touching the
-        // raw planes' blocks as well was slower: the decode that reads them
-        // is bound by its VALU work, and the touches delay the staging.)
-        const uint64_t b = s_data[p] + o0;
-        const uint32_t len = bok ? o1 - o0 : 0u;
-        // (the word holding the lane's count byte: o0 is a multiple of 4)
-        e_c[p] = g_ld<uint32_t>(bok ? b + (lane & ~3u) : safe);
-        e_touch[p][0] = g_ld<uint32_t>(128 * lane < len ? b + 128 * lane : safe);
-        e_touch[p][1] = g_ld<uint32_t>(8192 + 128 * lane < len ? b + 8192 + 128 * lane : safe);
-      }
-    };
-    auto prep = [&]() {
-      prepped = true;
-      st.coded_mask = 0;
-      st.pair_mask = 0;
-      st.packed_mask = 0;
-#pragma unroll
-      for (uint32_t p = 0; p < NP; ++p) {
-        st.raw[p] = s_raw[p];
-        if (__builtin_amdgcn_readfirstlane(ctl.packed[p])) st.packed_mask |= 1u << p;
-        st.words[p] = nullptr;
-        st.nw[p] = 0;
-        st.q[p] = 0;
-        st.t64[p] = lds_addr(ctl.t64[p]);
-        st.lut[p] = luts + __builtin_amdgcn_readfirstlane(ctl.slot[p]) * SLOT;
-        lane_c[p] = tot[p] = first[p] = 0;
-        if (!__builtin_amdgcn_readfirstlane(s_coded[p])) continue;
-        st.coded_mask |= 1u << p;
-        uint32_t o0, o1, c;
-        bool bok;
-        if (early) {
-          o0 = e_o0[p];
-          o1 = e_o1[p];
-          bok = o1 - o0 >= 64;  // touch() leaves both 0 for a rejected block
-          c = bok ? (e_c[p] >> (8 * (lane & 3u))) & 0xFFu : 0u;
-        } else {
-          bok = block_head(p, o0, o1, c);
-        }
-        const uint8_t* blk = reinterpret_cast<const uint8_t*>(s_data[p]) + (bok ? o0 : 0);
-        const uint32_t incl = wave_incl_scan(c);
-        const uint32_t total = __shfl(incl, 63, 64);
-        if (!bok || 64u + 4u * total != o1 - o0) ok = false;
-        st.words[p] = reinterpret_cast<const uint32_t*>(blk + 64);
-        lane_c[p] = c;
-        tot[p] = total;
-        first[p] = incl - c;
-        need += (total + 3u) & ~3u;
-        const uint32_t c0 = __builtin_amdgcn_readfirstlane(c);
-        if (__ballot(c != c0) == 0 && c0 >= 4) {
-          uni_mask |= 1u << p;
-          need_skew += 128u;  // room for up to two skew words per lane
-        }
-      }
-    };
-    if (ti != cur) {
-      // ---- new tensor: parse its plane headers and build the LDS tables ----
-      bad = wave_or_status(bad);
-      if (bad && lane == 0) status_or(&status[cur], bad);
-      bad = 0;
-      cur = ti;
-      __syncthreads();  // every wavefront is done with the previous tables
-      // the payload heads (tag, n, weights header) and last bytes, loaded
-      // by all threads at once (coded payloads start 4-byte aligned)
-      for (uint32_t k = t; k < NP * (kIlvHeadWords + 1); k += 256) {
-        const uint32_t p = k / (kIlvHeadWords + 1), w = k % (kIlvHeadWords + 1);
-        const uint64_t base = T.planes[p].base, len = T.planes[p].len;
-        uint32_t v = 0;
-        if (T.planes[p].coded) {
-          if (w == kIlvHeadWords) {
-            if (len) v = gload_u8(base + len - 1);
-          } else if (4ull * w + 4 <= len) {
-            v = g_ld<uint32_t>(base + 4ull * w);
-          } else {
-            for (uint64_t b = 4ull * w; b < len && b < 4ull * w + 4; ++b) v |= gload_u8(base + b) << (8 * (b & 3));
+          const uint8_t* blk = reinterpret_cast<const uint8_t*>(s_data[p]) + (bok ? o0 : 0);
+          const uint32_t incl = wave_incl_scan(c);
+          const uint32_t total = __shfl(incl, 63, 64);
+          if (!bok || 64u + 4u * total != o1 - o0) ok = false;
+          st.words[p] = reinterpret_cast<const uint32_t*>(blk + 64);
+          lane_c[p] = c;
+          tot[p] = total;
+          first[p] = incl - c;
+          need += (total + 3u) & ~3u;
+          const uint32_t c0 = __builtin_amdgcn_readfirstlane(c);
+          if (__ballot(c != c0) == 0 && c0 >= 4) {
+            uni_mask |= 1u << p;
+            need_skew += 128u;  // room for up to two skew words per lane
           }
         }
-        if (w == kIlvHeadWords) ctl.last[p] = v;
-        else head[p][w] = v;
-      }
-      if (t < NP) {
-        ctl.pbase[t] = T.planes[t].base;
-        ctl.plen[t] = T.planes[t].len;
-        ctl.pcoded[t] = T.planes[t].coded;
-      }
-      __syncthreads();
-      // the block's offsets, requested while thread 0 parses the heads
-#pragma unroll
-      for (uint32_t p = 0; p < NP; ++p) {
-        const uint64_t len = ctl.plen[p];
-        const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
-        uint64_t tb = 0, dt = 0;
-        const bool v = bi < nb && ctl.pcoded[p] && len >= 5 && pay[0] == 1 &&
-                       coded_layout(pay, (uint32_t)(len < 4 * kIlvHeadWords ? len : 4 * kIlvHeadWords), len, nb, tb, dt);
-        // tb + 4 (bi + 2) <= dt <= len: inside the payload
-        const uint64_t a = ctl.pbase[p] + tb + 4ull * bi;
-        e_o0[p] = g_ld<uint32_t>(v ? a : safe);
-        e_o1[p] = g_ld<uint32_t>(v ? a + 4 : safe);
-        if (v) e_ready |= 1u << p;
-      }
-      if (t == 0) {
-        s_bad = 0;
-        for (uint32_t p = 0; p < NP; ++p) {
-          const uint64_t base = ctl.pbase[p], len = ctl.plen[p];
-          s_raw[p] = base;
-          s_coded[p] = 0;
-          ctl.packed[p] = 0;
-          if (!ctl.pcoded[p]) continue;
-          // huff_ilv payload: tag 0 stores the plane after the tag byte, tag 2 packs it
-          const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
-          if (len == 0) s_bad |= kIlvErrHeader;
-          else if (pay[0] == 0) {
-            if (len != n + 1) s_bad |= kIlvErrHeader;
-            s_raw[p] = base + 1;
-          } else if (pay[0] == 2) {
-            if (!packed_header_ok(pay, len, n, ctl.last[p])) s_bad |= kIlvErrHeader;
-            s_raw[p] = base + kPackedHeadBytes;
-            ctl.packed[p] = 1;
-          } else if (pay[0] == 1 && len >= 5 && ld_u32le(pay + 1) == n) {
-            s_coded[p] = 1;
-            const uint32_t avail = (uint32_t)(len < 4 * kIlvHeadWords ? len : 4 * kIlvHeadWords);
-            ctl.hdr_avail[p] = avail - 5;
-            uint64_t tb, dt;
-            if (!coded_layout(pay, avail, len, nb, tb, dt)) {
-              s_bad |= kIlvErrHeader;
+      };
+      if (ti != cur) {
+        // ---- new tensor: parse its plane headers and build the LDS tables ----
+        bad = wave_or_status(bad);
+        if (bad && lane == 0) status_or(&status[cur], bad);
+        bad = 0;
+        cur = ti;
+        __syncthreads();  // every wavefront is done with the previous tables
+        // the payload heads (tag, n, weights header) and last bytes, loaded
+        // by all threads at once (coded payloads start 4-byte aligned)
+        for (uint32_t k = t; k < NP * (kIlvHeadWords + 1); k += 256) {
+          const uint32_t p = k / (kIlvHeadWords + 1), w = k % (kIlvHeadWords + 1);
+          const uint64_t base = T.planes[p].base, len = T.planes[p].len;
+          uint32_t v = 0;
+          if (T.planes[p].coded) {
+            if (w == kIlvHeadWords) {
+              if (len) v = gload_u8(base + len - 1);
+            } else if (4ull * w + 4 <= len) {
+              v = g_ld<uint32_t>(base + 4ull * w);
             } else {
-              // tab[0] == 0 and tab[nb] == datalen are checked by the
-              // wavefronts of the first and last block
-              s_table[p] = base + tb;
-              s_data[p] = base + dt;
-              s_datalen[p] = len - dt;
+              for (uint64_t b = 4ull * w; b < len && b < 4ull * w + 4; ++b) v |= gload_u8(base + b) << (8 * (b & 3));
             }
-          } else {
-            s_bad |= kIlvErrHeader;
           }
+          if (w == kIlvHeadWords) ctl.last[p] = v;
+          else head[p][w] = v;
         }
-        // table slots of the coded planes, from the last plane down (the
-        // exponent plane of the IEEE chains takes slot 0)
-        uint32_t k = 0;
-        for (uint32_t p = NP; p-- > 0;) {
-          ctl.slot[p] = k;
-          if (!s_coded[p]) continue;
-          if (k < n_slots) {
-            ++k;
-          } else {  // no table for it in this launch: the tensor is decoded again
-            s_coded[p] = 0;
-            s_bad |= kIlvRetrySlots;
-          }
-        }
-      }
-      __syncthreads();
-      // (the build's barriers do not wait for global loads)
-      const bool touched = !s_bad && bi < nb;
-      if (touched) touch();
-#pragma unroll 1
-      for (uint32_t p = 0; p < NP; ++p) {
-        if (!s_coded[p]) continue;
-        // no global loads here: they would wait for the touches (in order)
-        uint16_t* tab16 = reinterpret_cast<uint16_t*>(smem + ctl.slot[p] * SLOT);
-        const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
-        build_tables(tab16, ctl.t64[p], SLOT == kIlvPairLutBytes, ChainInfo<kChain>::xf[p], bs, pay + 5,
-                     ctl.hdr_avail[p]);
-        if (t == 0) {
-          s_pair[p] = bs.pair;
-          if (bs.err) s_bad |= kIlvErrHeader;
+        if (t < NP) {
+          ctl.pbase[t] = T.planes[t].base;
+          ctl.plen[t] = T.planes[t].len;
+          ctl.pcoded[t] = T.planes[t].coded;
         }
         __syncthreads();
-      }
-      if (touched) {  // the touches complete here
-#pragma unroll
-        for (uint32_t p = 0; p < NP; ++p) asm volatile("" ::"v"(e_touch[p][0]), "v"(e_touch[p][1]));
-      }
-      if (t == 0 && s_bad) status_or(&status[ti], s_bad);
-    }
-    if (s_bad) continue;  // uniform: the tensor is rejected
-    if (bi >= nb) continue;
-    if (!prepped) prep();
-    if (!ok) {
-      bad |= kIlvErrBlock;
-      continue;
-    }
-#pragma unroll
-    for (uint32_t p = 0; p < NP; ++p)
-      if ((st.coded_mask >> p) & 1u && __builtin_amdgcn_readfirstlane(s_pair[p])) st.pair_mask |= 1u << p;
-    const uint64_t bstart = (uint64_t)bi * kIlvBlock;
-    // the fast path takes whole blocks of planes under 4 GiB whose raw
-    // planes are aligned
-    bool full = bstart + kIlvBlock <= n && n <= 0xFFFFFFFFull;
-#pragma unroll
-    for (uint32_t p = 0; p < NP; ++p) {
-      const bool packed = (st.packed_mask >> p) & 1u;
-      st.rbytes[p] = (st.coded_mask & (1u << p)) ? 0u : (uint32_t)(packed ? (n + 1) / 2 : n);
-      if (!(st.coded_mask & (1u << p)) && !raw_aligned(st.raw[p], packed)) full = false;
-    }
-    const uint64_t out = T.out;
-    uint32_t q0[NP];
-    const bool crc_on = kCrc && T.crc_first != kIlvNoCrc && bstart + kIlvBlock <= n;
-    uint32_t acc[NP];
-#pragma unroll
-    for (uint32_t p = 0; p < NP; ++p) acc[p] = 0;
-    // skew uniform planes only when the staging budget has room for it
-    if (need + need_skew > stage_words) uni_mask = 0;
-    if (need <= stage_words) {
-      // Coalesced copy of the block's lane streams into this wavefront's LDS
-      // region.  When every lane holds the same number of words c (a
-      // fixed-length code, e.g. a uniform nibble plane: 32 words per lane),
-      // lane j's stream goes to word (c + skew) j with c + skew odd; left
-      // contiguous, all 64 lanes' windows would fall into gcd(c, 64) banks.
-      __builtin_amdgcn_wave_barrier();
-      uint32_t base = 4;
-#pragma unroll
-      for (uint32_t p = 0; p < NP; ++p) {
-        q0[p] = 0;
-        if (!(st.coded_mask & (1u << p))) continue;
-        const uint32_t* src = st.words[p];
-        uint32_t* dst = sw + base;
-        const uint32_t c0 = __builtin_amdgcn_readfirstlane(lane_c[p]);
-        const bool uniform = (uni_mask >> p) & 1u;
-        const uint32_t skew = uniform ? ((c0 & 1u) ? 2u : 1u) : 0u;
-        // words i .. i + 3 (those below tot) to their staging positions
-        auto put = [&](uint32_t i, const uint32_t (&x)[4]) {
-          if (!uniform) {
-            if (i + 4 <= tot[p]) {
-              *reinterpret_cast<u32x4*>(dst + i) = u32x4_make(x[0], x[1], x[2], x[3]);
-            } else {
-              for (uint32_t k = i; k < tot[p]; ++k) dst[k] = x[k - i];
-            }
-          } else {
-            // lane of word i: i / c0 (float estimate, then exact correction);
-            // c0 >= 4, so the four words span at most two lanes
-            uint32_t j0 = (uint32_t)((float)i * __builtin_amdgcn_rcpf((float)c0));
-            if (j0 * c0 > i) --j0;
-            if ((j0 + 1) * c0 <= i) ++j0;
-            const uint32_t bnd = (j0 + 1) * c0;
-#pragma unroll
-            for (uint32_t d = 0; d < 4; ++d) {
-              const uint32_t w = i + d;
-              if (w < tot[p]) dst[w + skew * (j0 + (w >= bnd ? 1u : 0u))] = x[d];
-            }
-          }
-        };
-        uint32_t i = 4 * lane;
-        for (; i < tot[p]; i += 256) {
-          uint32_t x[4] = {0, 0, 0, 0};
-          if (i + 4 <= tot[p]) {
-            const u32x4a4 v4 = gload_u32x4(src + i);
-            x[0] = v4.x;
-            x[1] = v4.y;
-            x[2] = v4.z;
-            x[3] = v4.w;
-          } else {
-            for (uint32_t k = i; k < tot[p]; ++k) x[k - i] = gload_u32(src + k);
-          }
-          put(i, x);
-        }
-        st.q[p] = lds_addr(dst + first[p] + skew * lane) * 8u - 1u;
-        q0[p] = st.q[p];
-        base += (tot[p] + (uniform ? 128u : 0u) + 3u) & ~3u;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // the bf16 exponent-coded plane forms get a branch-free round body
-      const bool fix = kChain == kChainIeee16Split2 && st.coded_mask == 2u && st.pair_mask == 0u &&
-                       st.packed_mask == 0u;
-      if (full && crc_on) {
-        if (fix) decode_block<kChain, false, true, kCrc, 3>(st, luts, out, n, bstart, lane, acc);
-        else decode_block<kChain, false, true, kCrc>(st, luts, out, n, bstart, lane, acc);
-      } else if (full) {
-        if (fix) decode_block<kChain, false, true, false, 3>(st, luts, out, n, bstart, lane);
-        else decode_block<kChain, false, true, false>(st, luts, out, n, bstart, lane);
-      } else if (crc_on) {
-        decode_block<kChain, true, true, kCrc>(st, luts, out, n, bstart, lane, acc);
-      } else {
-        decode_block<kChain, true, true, false>(st, luts, out, n, bstart, lane);
-      }
-      __builtin_amdgcn_wave_barrier();
-    } else {
-#pragma unroll
-      for (uint32_t p = 0; p < NP; ++p) {
-        if (st.words[p]) st.words[p] += first[p];
-        st.nw[p] = lane_c[p];
-        q0[p] = 0;
-      }
-      if (crc_on) decode_block<kChain, true, false, kCrc>(st, luts, out, n, bstart, lane, acc);
-      else decode_block<kChain, true, false, false>(st, luts, out, n, bstart, lane);
-    }
-    if constexpr (kCrc) {
-      if (crc_on) {
-        // lane l's last piece ends 16 (63 - l) bytes before the block's end
-        const uint32_t K = crc_tab[kCrcTabK64 + lane];
+        // the block's offsets, requested while thread 0 parses the heads
 #pragma unroll
         for (uint32_t p = 0; p < NP; ++p) {
-          uint32_t a = gf2_mulmod_seq(acc[p], K);
+          const uint64_t len = ctl.plen[p];
+          const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
+          uint64_t tb = 0, dt = 0;
+          const bool v = bi < nb && ctl.pcoded[p] && len >= 5 && pay[0] == 1 &&
+                         coded_layout(pay, (uint32_t)(len < 4 * kIlvHeadWords ? len : 4 * kIlvHeadWords), len, nb, tb, dt);
+          // tb + 4 (bi + 2) <= dt <= len: inside the payload
+          const uint64_t a = ctl.pbase[p] + tb + 4ull * bi;
+          e_o0[p] = g_ld<uint32_t>(v ? a : safe);
+          e_o1[p] = g_ld<uint32_t>(v ? a + 4 : safe);
+          if (v) e_ready |= 1u << p;
+        }
+        if (t == 0) {
+          s_bad = 0;
+          for (uint32_t p = 0; p < NP; ++p) {
+            const uint64_t base = ctl.pbase[p], len = ctl.plen[p];
+            s_raw[p] = base;
+            s_coded[p] = 0;
+            ctl.packed[p] = 0;
+            if (!ctl.pcoded[p]) continue;
+            // huff_ilv payload: tag 0 stores the plane after the tag byte, tag 2 packs it
+            const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
+            if (len == 0) s_bad |= kIlvErrHeader;
+            else if (pay[0] == 0) {
+              if (len != n + 1) s_bad |= kIlvErrHeader;
+              s_raw[p] = base + 1;
+            } else if (pay[0] == 2) {
+              if (!packed_header_ok(pay, len, n, ctl.last[p])) s_bad |= kIlvErrHeader;
+              s_raw[p] = base + kPackedHeadBytes;
+              ctl.packed[p] = 1;
+            } else if (pay[0] == 1 && len >= 5 && ld_u32le(pay + 1) == n) {
+              s_coded[p] = 1;
+              const uint32_t avail = (uint32_t)(len < 4 * kIlvHeadWords ? len : 4 * kIlvHeadWords);
+              ctl.hdr_avail[p] = avail - 5;
+              uint64_t tb, dt;
+              if (!coded_layout(pay, avail, len, nb, tb, dt)) {
+                s_bad |= kIlvErrHeader;
+              } else {
+                // tab[0] == 0 and tab[nb] == datalen are checked by the
+                // wavefronts of the first and last block
+                s_table[p] = base + tb;
+                s_data[p] = base + dt;
+                s_datalen[p] = len - dt;
+              }
+            } else {
+              s_bad |= kIlvErrHeader;
+            }
+          }
+          // table slots of the coded planes, from the last plane down (the
+          // exponent plane of the IEEE chains takes slot 0)
+          uint32_t k = 0;
+          for (uint32_t p = NP; p-- > 0;) {
+            ctl.slot[p] = k;
+            if (!s_coded[p]) continue;
+            if (k < n_slots) {
+              ++k;
+            } else {  // no table for it in this launch: the tensor is decoded again
+              s_coded[p] = 0;
+              s_bad |= kIlvRetrySlots;
+            }
+          }
+        }
+        __syncthreads();
+        // (the build's barriers do not wait for global loads)
+        const bool touched = !s_bad && bi < nb;
+        if (touched) touch();
+#pragma unroll 1
+        for (uint32_t p = 0; p < NP; ++p) {
+          if (!s_coded[p]) continue;
+          // no global loads here: they would wait for the touches (in order)
+          uint16_t* tab16 = reinterpret_cast<uint16_t*>(smem + ctl.slot[p] * SLOT);
+          const uint8_t* pay = reinterpret_cast<const uint8_t*>(head[p]);
+          build_tables(tab16, ctl.t64[p], chain_slot_bytes(C) == kIlvPairLutBytes, ChainInfo<C>::xf[p], bs, pay + 5,
+                       ctl.hdr_avail[p]);
+          if (t == 0) {
+            s_pair[p] = bs.pair;
+            if (bs.err) s_bad |= kIlvErrHeader;
+          }
+          __syncthreads();
+        }
+        if (touched) {  // the touches complete here
 #pragma unroll
-          for (int d = 32; d >= 1; d >>= 1) a ^= __shfl_xor(a, d, 64);
-          if (lane == 0) g_st<uint32_t>(reinterpret_cast<uint64_t>(crc_part + 4ull * (T.crc_first + bi) + p), a);
+          for (uint32_t p = 0; p < NP; ++p) asm volatile("" ::"v"(e_touch[p][0]), "v"(e_touch[p][1]));
+        }
+        if (t == 0 && s_bad) status_or(&status[ti], s_bad);
+      }
+      if (s_bad) return;  // uniform: the tensor is rejected
+      if (bi >= nb) return;
+      if (!prepped) prep();
+      if (!ok) {
+        bad |= kIlvErrBlock;
+        return;
+      }
+#pragma unroll
+      for (uint32_t p = 0; p < NP; ++p)
+        if ((st.coded_mask >> p) & 1u && __builtin_amdgcn_readfirstlane(s_pair[p])) st.pair_mask |= 1u << p;
+      const uint64_t bstart = (uint64_t)bi * kIlvBlock;
+      // the fast path takes whole blocks of planes under 4 GiB whose raw
+      // planes are aligned
+      bool full = bstart + kIlvBlock <= n && n <= 0xFFFFFFFFull;
+#pragma unroll
+      for (uint32_t p = 0; p < NP; ++p) {
+        const bool packed = (st.packed_mask >> p) & 1u;
+        st.rbytes[p] = (st.coded_mask & (1u << p)) ? 0u : (uint32_t)(packed ? (n + 1) / 2 : n);
+        if (!(st.coded_mask & (1u << p)) && !raw_aligned(st.raw[p], packed)) full = false;
+      }
+      const uint64_t out = T.out;
+      uint32_t q0[NP];
+      const bool crc_on = kCrc && T.crc_first != kIlvNoCrc && bstart + kIlvBlock <= n;
+      uint32_t acc[NP];
+#pragma unroll
+      for (uint32_t p = 0; p < NP; ++p) acc[p] = 0;
+      // skew uniform planes only when the staging budget has room for it
+      if (need + need_skew > stage_words) uni_mask = 0;
+      if (need <= stage_words) {
+        // Coalesced copy of the block's lane streams into this wavefront's LDS
+        // region.  When every lane holds the same number of words c (a
+        // fixed-length code, e.g. a uniform nibble plane: 32 words per lane),
+        // lane j's stream goes to word (c + skew) j with c + skew odd; left
+        // contiguous, all 64 lanes' windows would fall into gcd(c, 64) banks.
+        __builtin_amdgcn_wave_barrier();
+        uint32_t base = 4;
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+          q0[p] = 0;
+          if (!(st.coded_mask & (1u << p))) continue;
+          const uint32_t* src = st.words[p];
+          uint32_t* dst = sw + base;
+          const uint32_t c0 = __builtin_amdgcn_readfirstlane(lane_c[p]);
+          const bool uniform = (uni_mask >> p) & 1u;
+          const uint32_t skew = uniform ? ((c0 & 1u) ? 2u : 1u) : 0u;
+          // words i .. i + 3 (those below tot) to their staging positions
+          auto put = [&](uint32_t i, const uint32_t (&x)[4]) {
+            if (!uniform) {
+              if (i + 4 <= tot[p]) {
+                *reinterpret_cast<u32x4*>(dst + i) = u32x4_make(x[0], x[1], x[2], x[3]);
+              } else {
+                for (uint32_t k = i; k < tot[p]; ++k) dst[k] = x[k - i];
+              }
+            } else {
+              // lane of word i: i / c0 (float estimate, then exact correction);
+              // c0 >= 4, so the four words span at most two lanes
+              uint32_t j0 = (uint32_t)((float)i * __builtin_amdgcn_rcpf((float)c0));
+              if (j0 * c0 > i) --j0;
+              if ((j0 + 1) * c0 <= i) ++j0;
+              const uint32_t bnd = (j0 + 1) * c0;
+#pragma unroll
+              for (uint32_t d = 0; d < 4; ++d) {
+                const uint32_t w = i + d;
+                if (w < tot[p]) dst[w + skew * (j0 + (w >= bnd ? 1u : 0u))] = x[d];
+              }
+            }
+          };
+          uint32_t i = 4 * lane;
+          for (; i < tot[p]; i += 256) {
+            uint32_t x[4] = {0, 0, 0, 0};
+            if (i + 4 <= tot[p]) {
+              const u32x4a4 v4 = gload_u32x4(src + i);
+              x[0] = v4.x;
+              x[1] = v4.y;
+              x[2] = v4.z;
+              x[3] = v4.w;
+            } else {
+              for (uint32_t k = i; k < tot[p]; ++k) x[k - i] = gload_u32(src + k);
+            }
+            put(i, x);
+          }
+          st.q[p] = lds_addr(dst + first[p] + skew * lane) * 8u - 1u;
+          q0[p] = st.q[p];
+          base += (tot[p] + (uniform ? 128u : 0u) + 3u) & ~3u;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // the bf16 exponent-coded plane forms get a branch-free round body
+        const bool fix = C == kChainIeee16Split2 && st.coded_mask == 2u && st.pair_mask == 0u &&
+                         st.packed_mask == 0u;
+        if (full && crc_on) {
+          if (fix) decode_block<C, false, true, kCrc, 3>(st, luts, out, n, bstart, lane, acc);
+          else decode_block<C, false, true, kCrc>(st, luts, out, n, bstart, lane, acc);
+        } else if (full) {
+          if (fix) decode_block<C, false, true, false, 3>(st, luts, out, n, bstart, lane);
+          else decode_block<C, false, true, false>(st, luts, out, n, bstart, lane);
+        } else if (crc_on) {
+          decode_block<C, true, true, kCrc>(st, luts, out, n, bstart, lane, acc);
+        } else {
+          decode_block<C, true, true, false>(st, luts, out, n, bstart, lane);
+        }
+        __builtin_amdgcn_wave_barrier();
+      } else {
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+          if (st.words[p]) st.words[p] += first[p];
+          st.nw[p] = lane_c[p];
+          q0[p] = 0;
+        }
+        if (crc_on) decode_block<C, true, false, kCrc>(st, luts, out, n, bstart, lane, acc);
+        else decode_block<C, true, false, false>(st, luts, out, n, bstart, lane);
+      }
+      if constexpr (kCrc) {
+        if (crc_on) {
+          // lane l's last piece ends 16 (63 - l) bytes before the block's end
+          const uint32_t K = crc_tab[kCrcTabK64 + lane];
+#pragma unroll
+          for (uint32_t p = 0; p < NP; ++p) {
+            uint32_t a = gf2_mulmod_seq(acc[p], K);
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) a ^= __shfl_xor(a, d, 64);
+            if (lane == 0) g_st<uint32_t>(reinterpret_cast<uint64_t>(crc_part + 4ull * (T.crc_first + bi) + p), a);
+          }
         }
       }
-    }
-    // acceptance: every lane's words hold exactly its codes
+      // acceptance: every lane's words hold exactly its codes
 #pragma unroll
-    for (uint32_t p = 0; p < NP; ++p) {
-      if (!(st.coded_mask & (1u << p))) continue;
-      const uint32_t used = st.q[p] - q0[p];
-      if ((used + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
+      for (uint32_t p = 0; p < NP; ++p) {
+        if (!(st.coded_mask & (1u << p))) continue;
+        const uint32_t used = st.q[p] - q0[p];
+        if ((used + 31u) / 32u != lane_c[p]) bad |= kIlvErrLane;
+      }
+    };
+    if constexpr (ilv_is_pair(kChain)) {
+      if (T.chain == ilv_pair_a(kChain)) body(ChainTag<ilv_pair_a(kChain)>{});
+      else body(ChainTag<ilv_pair_b(kChain)>{});
+    } else {
+      body(ChainTag<kChain>{});
     }
   }
   bad = wave_or_status(bad);
@@ -1258,6 +1279,7 @@ static const void* ilv_decode_fn(uint32_t chain, bool crc) {
     case kChainE5m2Nibble: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainE5m2Nibble, false>);
     case kChainNibbleSplit: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainNibbleSplit, false>);
     case kChainPassthrough: return reinterpret_cast<const void*>(&ilv_decode_kernel<kChainPassthrough, false>);
+    case kIlvPairNibblePass: return reinterpret_cast<const void*>(&ilv_decode_kernel<kIlvPairNibblePass, false>);
     default: return nullptr;
   }
 }

@@ -320,16 +320,41 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     bool crc;  // some tensor of the launch has fused CRC partials (huff_ilv family)
   };
   std::vector<Launch> launches;
+  // The launch chain codes of a family: one per chain present, except that
+  // huff_ilv nibble-split and passthrough tensors (MXFP4 weights and their
+  // scales) share one two-chain launch when none of them has fused CRC
+  // partials (the two-chain kernel has no CRC variant).
+  bool pair_ok = false;
+  {
+    bool has5 = false, has6 = false, crc56 = false;
+    for (const IlvTensor& T : tensors) {
+      if (T.family != kFamilyHuff || T.n == 0) continue;
+      has5 |= T.chain == kChainNibbleSplit;
+      has6 |= T.chain == kChainPassthrough;
+      crc56 |= (T.chain == kChainNibbleSplit || T.chain == kChainPassthrough) && T.crc_first != kIlvNoCrc;
+    }
+    pair_ok = has5 && has6 && !crc56;
+  }
+  auto launch_codes = [&](uint32_t fam) {
+    std::vector<uint32_t> codes{kChainIeee16Split2, kChainIeee32Split4, kChainE4m3Nibble, kChainE5m2Nibble};
+    if (fam == kFamilyHuff && pair_ok) {
+      codes.push_back(kIlvPairNibblePass);
+    } else {
+      codes.push_back(kChainNibbleSplit);
+      codes.push_back(kChainPassthrough);
+    }
+    return codes;
+  };
   std::vector<uint32_t> idx;  // per launch: [m + 1 prefix][m tensor indexes]
   for (uint32_t fam = kFamilyHuff; fam <= kFamilyRans; ++fam)
-  for (uint32_t chain = 1; chain <= 6; ++chain) {
+  for (uint32_t chain : launch_codes(fam)) {
     std::vector<uint32_t> tix, tpre{0};
     uint32_t slots = 0;
     uint64_t est = 0;
     bool crc = false;
     for (uint32_t ti = 0; ti < nt; ++ti) {
       const IlvTensor& T = tensors[ti];
-      if (T.family != fam || T.chain != chain || T.n == 0) continue;
+      if (T.family != fam || !ilv_code_has(chain, T.chain) || T.n == 0) continue;
       if (T.crc_first != kIlvNoCrc) {
         if (fam != kFamilyHuff) return kInternal;
         crc = true;
@@ -351,7 +376,7 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
         // huff_ilv nibble chains may carry fixed-length codes: room for the
         // kernel's per-lane skew of equal-length lane streams (two words per lane)
         const uint64_t skew =
-            fam == kFamilyRans || chain == kChainIeee16Split2 || chain == kChainIeee32Split4 ? 0 : 128;
+            fam == kFamilyRans || T.chain == kChainIeee16Split2 || T.chain == kChainIeee32Split4 ? 0 : 128;
         words += align_up(per_block + per_block / 50 + skew + 4, 4);
       }
       slots = std::max(slots, need_slots);
@@ -371,7 +396,7 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     if (stage < head_min) return kInternal;
     int per_cu = 0;
     const uint64_t occ_key =
-        (uint64_t)chain | ((uint64_t)slots << 8) | (stage << 16) | ((uint64_t)crc << 61) | ((uint64_t)fam << 62);
+        (uint64_t)chain | ((uint64_t)slots << 12) | (stage << 20) | ((uint64_t)crc << 61) | ((uint64_t)fam << 62);
     auto it = ctx.ilv_occupancy.find(occ_key);
     if (it != ctx.ilv_occupancy.end()) {
       per_cu = it->second;

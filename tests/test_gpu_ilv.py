@@ -226,6 +226,65 @@ def test_multi_tensor_plan_mixed_codecs():
     assert r[: len(a)] == a and r[out_off:] == b
 
 
+def mx_tensors(k, seed):
+    """k tensors alternating MXFP4 weight bytes (nibble split) and E8M0-like
+    scales (passthrough), of varied lengths."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(k):
+        if i % 2 == 0:
+            n = int(rng.integers(1, 300_000))
+            t = torch.from_numpy(rng.integers(0, 256, n).astype(np.uint8))
+            out.append((plan.CHAIN_NIBBLE_SPLIT, t))
+        else:
+            n = int(rng.integers(1, 40_000))
+            t = torch.from_numpy(np.clip(np.round(rng.normal(-6, 1.5, n)) + 127, 0, 255).astype(np.uint8))
+            out.append((plan.CHAIN_PASSTHROUGH, t))
+    return out
+
+
+@pytest.mark.parametrize("k", [2, 3, 7])
+def test_two_chain_launch_nibble_split_with_scales(k):
+    """Nibble-split and passthrough tensors in one call share one two-chain
+    launch (descriptors in the kernel arguments up to four tensors, uploaded
+    above); every tensor restores exactly, and a rejected payload in one of
+    them fails the call without disturbing the next one."""
+    items = mx_tensors(k, 40 + k)
+    note(f"two-chain launch, {k} tensors")
+    src = [(c, dev(t.numpy().tobytes())) for c, t in items]
+    total = sum(t.numel() for _, t in items)
+    out = torch.zeros(total * 2 + 65536 * k, dtype=torch.uint8, device="cuda:0")
+    used, st = api.encode_tensors_cuda(src, out, 0)
+    tp = plan.decode_plan(st)
+    assert {t.chain for t in tp} == {plan.CHAIN_NIBBLE_SPLIT, plan.CHAIN_PASSTHROUGH}
+    restored = torch.zeros(max(t.out_offset + t.out_len for t in tp), dtype=torch.uint8, device="cuda:0")
+    n = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, st,
+                                                  out[:used], restored, 0)
+    assert n == total
+    r = host(restored)
+    for t, (_, x) in zip(tp, items):
+        assert r[t.out_offset: t.out_offset + t.out_len] == x.numpy().tobytes()
+    # an invalid tag in the last tensor's first coded payload
+    bad = out[:used].clone()
+    hit = None
+    for t in reversed(tp):
+        for pl in t.planes:
+            if pl.codec == ids.CODEC_HUFF_ILV:
+                hit = pl.payload_offset
+                break
+        if hit is not None:
+            break
+    assert hit is not None
+    bad[hit] = 7
+    with pytest.raises(api.NativeError):
+        api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, st, bad,
+                                                  restored, 0)
+    restored.zero_()
+    n = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, st,
+                                                  out[:used], restored, 0)
+    assert n == total and host(restored) == r
+
+
 def test_stream_ordering_after_torch_producer():
     """The library stream waits for work queued on torch's current stream
     (the reference's __dlpack__(stream=...) contract): the payload is copied
