@@ -105,10 +105,11 @@ int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_versi
  * payloads (one codec per tensor, at least one coded plane, 4-byte aligned
  * in the input) or unchunked Identity planes, output 16-byte aligned, plane
  * CRC-32 only for the ieee16 / ieee32 / passthrough chains, no tensor XXH64.
- * All device scratch (descriptors, status words, CRC tables and block
- * partials) is one fixed array of PTWM_MI355X_NOALLOC_SCRATCH_BYTES per
- * device, held until the process ends; it calls no hipMalloc, hipFree or
- * hipHostMalloc.  Plans outside these limits (more than
+ * All device scratch (descriptors, CRC tables and block partials) is one
+ * fixed array of PTWM_MI355X_NOALLOC_SCRATCH_BYTES per device, and the
+ * per-tensor status words a fixed 16 KiB host-coherent pinned area
+ * allocated once with the device's context, both held until the process
+ * ends; the call itself calls no hipMalloc, hipFree or hipHostMalloc.  Plans outside these limits (more than
  * PTWM_MI355X_NOALLOC_MAX_TENSORS tensors, or more than
  * PTWM_MI355X_NOALLOC_MAX_CRC_BLOCKS CRC-checked 16384-byte plane blocks in
  * all) return -5 (Unsupported); -3 if the device's scratch could not be
