@@ -158,24 +158,33 @@ __global__ void __launch_bounds__(256) crc_range_kernel(const CrcRange* __restri
 }
 
 // Chains the ranges of one plane (blockIdx.x), applies init / final xor,
-// writes the plane's CRC.
+// writes the plane's CRC.  Multiplying by the whole-range shift s_full is
+// linear in the multiplicand, so it runs as four byte-sliced lookups into
+// tables of (v << 8k) * s_full built in LDS first.
 __global__ void __launch_bounds__(256) crc_combine_kernel(const CrcPlane* __restrict__ planes,
                                                           const uint32_t* __restrict__ part,
                                                           const uint32_t* __restrict__ gtab,
                                                           uint32_t* __restrict__ crc_out) {
   __shared__ uint32_t red[4];
+  __shared__ uint32_t mt[4][256];
   const CrcPlane B = planes[blockIdx.x];
   const uint32_t* X = gtab + kCrcTabX;
   const uint32_t t = threadIdx.x;
+  const uint32_t s_full = xpow8(B.range_len, X);
+  static_assert(kCrcThreads == 256, "one table entry per thread and slice");
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) mt[k][t] = gf2_mulmod(t << (8 * k), s_full);
+  __syncthreads();
   const uint32_t q = (B.n_ranges + kCrcThreads - 1) / kCrcThreads;
   const uint32_t r0 = std::min(B.n_ranges, t * q), r1 = std::min(B.n_ranges, r0 + q);
   uint32_t acc = 0;
   if (r0 < r1) {
     const uint64_t last_len = B.n - (uint64_t)(B.n_ranges - 1) * B.range_len;
-    const uint32_t s_full = xpow8(B.range_len, X);
     for (uint32_t r = r0; r < r1; ++r) {
-      const uint32_t s = r + 1 == B.n_ranges ? xpow8(last_len, X) : s_full;
-      acc = gf2_mulmod(acc, s) ^ part[4ull * (B.first_range + r) + B.plane];
+      const uint32_t x = r + 1 == B.n_ranges ? gf2_mulmod(acc, xpow8(last_len, X))
+                                             : mt[0][acc & 255u] ^ mt[1][(acc >> 8) & 255u] ^
+                                                   mt[2][(acc >> 16) & 255u] ^ mt[3][acc >> 24];
+      acc = x ^ part[4ull * (B.first_range + r) + B.plane];
     }
     const uint64_t end = r1 == B.n_ranges ? B.n : (uint64_t)r1 * B.range_len;
     acc = gf2_mulmod(acc, xpow8(B.n - end, X));
