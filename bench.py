@@ -122,6 +122,23 @@ def gen_tensor(kind, shape, seed):
 
 HUF, RANS = 1, 3   # reference codec wire ids (crates/ptwm-core/src/codec.rs:7-9)
 EXACT_ROUTE = "decode_exact (reference streams) + merge"
+REF_CHUNK = 256 << 10   # the reference's default compression_chunk (python/ptwm/_config.py:151)
+
+# Each config in the reference's own plane formats, by tensor kind: (codec per
+# plane, chunk size or 0).  The c*_ref workloads are these payloads (GPU-encoded,
+# byte-identical to the reference encoder) on the exact route, and every line's
+# CPU baseline decodes them on this host.
+REF_FORMATS = {
+    "c1": {"w": ([HUF, HUF], 0)},
+    "c2": {"fp32o": ([HUF, HUF, HUF, RANS], REF_CHUNK)},
+    "c3_huf": {"fp8": ([HUF, HUF], 0)},
+    "c3_rans": {"fp8": ([RANS, RANS], 0)},
+    "c4": {"w": ([HUF, HUF], REF_CHUNK), "n": ([HUF, HUF], REF_CHUNK)},
+    "c5": {"fp4": ([HUF, HUF], 0), "e8m0": ([HUF], 0)},
+}
+REF_LINES = ("c1_ref", "c2_ref", "c3_huf", "c3_rans", "c5_ref")
+CPU_FORMAT = {"llama8b": "c4", "bf16_1k": "c1", "c1_ref": "c1", "fp32_4k": "c2", "c2_ref": "c2", "fp8": "c3_huf",
+              "c3_huf": "c3_huf", "fp8@rans": "c3_rans", "c3_rans": "c3_rans", "mxfp4": "c5", "c5_ref": "c5"}
 
 
 MIN_DISTINCT_BYTES = 1 << 30   # rotate inputs of smaller workloads (the MALL holds 256 MB)
@@ -186,27 +203,27 @@ def build_workload(name: str, resident: bool = False, integrity: bool = False) -
     # to the reference encoder), decoded by the exact route
     elif name == "c1_ref":
         specs = [((1024, 1024), "w")]
-        ref = {"w": ([HUF, HUF], 0)}
+        ref = REF_FORMATS["c1"]
         desc = "config 1 in reference format: bf16 1024x1024, Huffman on each plane"
         kernel = exact
     elif name == "c2_ref":
         specs = [((4096, 4096), "fp32o")]
-        ref = {"fp32o": ([HUF, HUF, HUF, RANS], 262144)}
+        ref = REF_FORMATS["c2"]
         desc = "config 2 in reference format: fp32 4096x4096 + outliers, rANS exponent, Huffman mantissas, 256 KiB chunks"
         kernel = exact
     elif name == "c3_huf":
         specs = [((8192, 8192), "fp8")]
-        ref = {"fp8": ([HUF, HUF], 0)}
+        ref = REF_FORMATS["c3_huf"]
         desc = "config 3 in reference format: e4m3 8192x8192, Huffman on both nibble planes"
         kernel = exact
     elif name == "c3_rans":
         specs = [((8192, 8192), "fp8")]
-        ref = {"fp8": ([RANS, RANS], 0)}
+        ref = REF_FORMATS["c3_rans"]
         desc = "config 3 in reference format: e4m3 8192x8192, rANS on both nibble planes (unchunked)"
         kernel = exact
     elif name == "c5_ref":
         specs = [((14336, 2048), "fp4"), ((14336, 128), "e8m0")]
-        ref = {"fp4": ([HUF, HUF], 0), "e8m0": ([HUF], 0)}
+        ref = REF_FORMATS["c5"]
         desc = "config 5 in reference format: MXFP4 weights (Huffman nibble planes) + E8M0 scales (Huffman)"
         kernel = exact
     else:
@@ -271,6 +288,7 @@ def build_replica(desc, specs, CH, ref, native, integrity, rep) -> Workload:
     from ptwm_amd import api, plan
 
     wl = Workload(desc)
+    wl.kinds = [kind for _, kind in specs]
     if ref is not None:
         wl.codec = "reference Huffman / rANS plane payloads (exact route)"
     elif native == "rans_ilv":
@@ -432,7 +450,7 @@ def main():
     ap.add_argument("--workload", default="llama8b+crc",
                     help="<workload>[@rans][+crc][+hash]: the headline decode (default: config 4, plane "
                          "CRC-32 verified inside the timed region)")
-    ap.add_argument("--extra", default="fp8,mxfp4,c1_ref,c2_ref,c3_huf,c3_rans,c5_ref",
+    ap.add_argument("--extra", default="fp8,fp8@rans,mxfp4,bf16_1k,fp32_4k,c1_ref,c2_ref,c3_huf,c3_rans,c5_ref",
                     help="comma list of secondary workloads reported in config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--resident", action="store_true",
@@ -484,6 +502,12 @@ def main():
             m3, k3 = measure(wl, 3, 1, True, True)
             primary["hash_verified"] = secondary_line(wl, m3, k3, True, True)
             log(f"[bench] {base} with CRC-32 + XXH64: {m3:.3f} ms/step")
+    cpu = None
+    if not args.no_cpu_baseline and base in CPU_FORMAT:
+        # config 4: the tensors of layer 0 (a bounded sample of the same model)
+        sample = [i for i, t in enumerate(llama8b_shapes()) if ".layers.0." in t[0]] if base == "llama8b" else None
+        cpu = cpu_line(wl, base, sample, budget_s=3.0)
+        log(f"[bench] CPU restatement: {cpu['value']} GB/s at {cpu['cores']} threads, {cpu['value_1_thread']} at 1")
     for name in [x for x in args.extra.split(",") if x and x != args.workload]:
         del wl
         gc.collect()
@@ -492,6 +516,10 @@ def main():
         wl = build_workload(name, args.resident or slow)
         m2, k2 = measure(wl, 1 if slow else max(3, args.steps), 0 if slow else 1)
         extras[name] = secondary_line(wl, m2, k2)
+        if not args.no_cpu_baseline:
+            extras[name]["cpu_baseline"] = cpu_line(wl, name, budget_s=1.0)
+        log(f"[bench] {name}: {extras[name]['restored_gbs']} GB/s restored"
+            + (f", CPU {extras[name]['cpu_baseline']['value']} GB/s" if "cpu_baseline" in extras[name] else ""))
     primary["secondary"] = extras
     traffic_meas, traffic_src = measured_traffic(args.workload)
     ceil = hbm_ceilings()
@@ -518,10 +546,8 @@ def main():
         "roofline": {"bound": "hbm", "kernel": kernel_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel_ms": round(kms, 4),
                      "traffic": traffic_meas, "traffic_source": traffic_src, "ceilings": ceil},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
-    if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
 
 
@@ -554,65 +580,87 @@ def hbm_ceilings():
             "source": "torch copy_ / fill_ of 2 GiB on this device, same run"}
 
 
-def cpu_baseline():
-    """The oracle's C restatement of the reference CPU decode on a bounded
-    sample of config 4: bf16 N(0,0.02) tensors split into two planes, each
-    plane Huffman-coded in 256 KiB chunks (the reference's default
-    compression_chunk, _config.py:151) with its chunk frames; the whole set
-    decoded as the container does it (container.rs:1766-2050: tensors over
-    worker threads, each tensor's planes chunk by chunk, then the fused
-    inverse chain), timed on this host at `nproc` (at most 16) threads and at
-    one thread."""
-    import concurrent.futures as cf
-
-    import torch
-
-    import oracle as O
-
-    threads = min(16, os.cpu_count() or 1)
-    n_tensors = 2 * threads
-    g = torch.Generator().manual_seed(7)
-    raws = [(torch.randn(4096 * 4096, generator=g) * 0.02).to(torch.bfloat16).view(torch.uint8).numpy().tobytes()
-            for _ in range(n_tensors)]
-
-    def enc(w):
-        return (len(w), [O.encode_plane_chunked(O.CODEC_HUFFMAN, p, 256 << 10)
-                         for p in O.chain_forward(O.CHAIN_IEEE16_SPLIT2, w)])
-
-    with cf.ThreadPoolExecutor(threads) as ex:   # the oracle's C calls release the GIL
-        batch = O.TensorBatch(O.CODEC_HUFFMAN, O.CHAIN_IEEE16_SPLIT2, list(ex.map(enc, raws)))
-    comp = sum(len(pay) for _, planes in [enc(raws[0])] for pay, _ in planes)
-    batch.decode(threads)
-    assert all(batch.output(i) == raws[i] for i in range(n_tensors)), "CPU baseline round trip"
-
-    def rate(nthreads, seconds):
-        t0 = time.perf_counter()
-        reps = 0
-        while True:
-            batch.decode(nthreads)
-            reps += 1
-            if time.perf_counter() - t0 > seconds:
-                break
-        dt = time.perf_counter() - t0
-        return sum(len(w) for w in raws) * reps / dt / 1e9, reps
-
-    value, reps = rate(threads, 10.0)
-    one, reps1 = rate(1, 4.0)
-    model = "unknown"
+def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "value_1_thread": round(one, 3), "cpu_model": model, "nproc": os.cpu_count(),
-            "sample": f"{reps} passes over {n_tensors} x 32 MiB bf16 4096x4096 N(0,0.02) tensors at {threads} "
-                      f"threads ({reps1} passes at 1 thread), Huffman planes in 256 KiB chunks (ratio "
-                      f"{comp / len(raws[0]):.3f}); tensors over threads, chunks, fused inverse; oracle C "
-                      "restatement, no CRC / XXH64"}
+    return "unknown"
+
+
+def cpu_line(wl, name: str, sample=None, budget_s: float = 1.5):
+    """The oracle's C restatement of the reference CPU codec, timed on this
+    host, on this line's own input: replica 0's tensors (or the `sample` of
+    them), copied to host memory, in the config's reference plane format
+    (REF_FORMATS).  Encode (forward chain, then per plane Huffman or rANS,
+    chunk frames and table) and decode (chunks of every plane over the
+    threads as container.rs:1773,1996 run them, then the inverse chain),
+    each at min(16, nproc) threads and at one thread, passes repeated for
+    about `budget_s`.  For the c*_ref lines the CPU-encoded payloads are
+    checked equal to the GPU-encoded ones that line decodes, so both read
+    the same compressed bytes; every CPU decode is checked bit-exact."""
+    import oracle as O
+
+    fmt = REF_FORMATS[CPU_FORMAT[name]]
+    rep = wl.replicas[0]
+    idx = list(range(len(rep.tensors))) if sample is None else list(sample)
+    raws, items = [], []
+    for i in idx:
+        raw, chain, _ = rep.tensors[i]
+        codecs, chunk = fmt[rep.kinds[i]]
+        h = raw.cpu().numpy()
+        raws.append(h)
+        items.append((chain, h, [(c, chunk) for c in codecs]))
+    threads = min(16, os.cpu_count() or 1)
+    enc = O.PlaneBatchEncoder(items)
+    enc.encode(threads)
+    planes = enc.planes()
+    if name in REF_LINES:
+        blob = rep.blob.cpu().numpy()
+        k = 0
+        for i in idx:
+            for p in rep.plans[i].planes:
+                gpu = blob[p.payload_offset: p.payload_offset + p.payload_len].tobytes()
+                if planes[k][0] != gpu:
+                    raise SystemExit(f"{name}: GPU-encoded payload differs from the CPU restatement's (plane {k})")
+                k += 1
+    batch, k = [], 0
+    for (chain, h, pl) in items:
+        batch.append((chain, h.size, [(c, *planes[k + j]) for j, (c, _) in enumerate(pl)]))
+        k += len(pl)
+    dec = O.PlaneBatch(batch)
+    dec.decode(threads)
+    for n, h in enumerate(raws):
+        if dec.outs[n][: h.size].tobytes() != h.tobytes():
+            raise SystemExit(f"{name}: CPU restatement round trip differs")
+    nbytes = dec.restored
+    comp = sum(len(p) for p, _ in planes)
+
+    def rate(fn, nthreads):
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            fn(nthreads)
+            reps += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+        return nbytes * reps / (time.perf_counter() - t0) / 1e9, reps
+
+    dn, rn = rate(dec.decode, threads)
+    d1, r1 = rate(dec.decode, 1)
+    en, _ = rate(enc.encode, threads)
+    e1, _ = rate(enc.encode, 1)
+    fmt_txt = "; ".join(f"{kd}: {'/'.join('rANS' if c == RANS else 'Huffman' for c in cs)}"
+                        f"{f' in {ch >> 10} KiB chunks' if ch else ''}" for kd, (cs, ch) in fmt.items())
+    return {"value": round(dn, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "value_1_thread": round(d1, 3), "encode_gbs": round(en, 3), "encode_gbs_1_thread": round(e1, 3),
+            "nproc": os.cpu_count(), "cpu_model": cpu_model(),
+            "sample": f"{len(idx)} tensor(s), {nbytes / 2**20:.1f} MiB restored, ratio {comp / nbytes:.4f}, "
+                      f"reference format ({fmt_txt}); {rn} decode passes at {threads} threads, {r1} at 1; "
+                      "oracle C restatement, chunks over threads, no CRC-32 / XXH64"}
 
 
 if __name__ == "__main__":

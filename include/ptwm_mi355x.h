@@ -107,14 +107,20 @@ int64_t ptwm_hardware_backend_v1_dispatch_decode_cuda(uint8_t state_format_versi
  * CRC-32 only for the ieee16 / ieee32 / passthrough chains, no tensor XXH64.
  * All device scratch (descriptors, CRC tables and block partials) is one
  * fixed array of PTWM_MI355X_NOALLOC_SCRATCH_BYTES per device, and the
- * per-tensor status words a fixed 16 KiB host-coherent pinned area
- * allocated once with the device's context, both held until the process
- * ends; the call itself calls no hipMalloc, hipFree or hipHostMalloc.  Plans outside these limits (more than
- * PTWM_MI355X_NOALLOC_MAX_TENSORS tensors, or more than
+ * per-tensor status words a fixed 16 KiB host-coherent pinned area; both
+ * are set up by ptwm_mi355x_device_init (the device's context: its stream,
+ * the array's address, the status area), which the caller runs once per
+ * device beforehand, and are held until the process ends.  The call itself
+ * never creates the context, and calls no hipMalloc, hipFree, hipHostMalloc,
+ * stream or event creation (ptwm_mi355x_alloc_calls does not move across
+ * it).  Returns -3 (MissingCapability) when the device's context does not
+ * exist yet or its scratch could not be resolved.  Plans outside these
+ * limits (more than PTWM_MI355X_NOALLOC_MAX_TENSORS tensors, or more than
  * PTWM_MI355X_NOALLOC_MAX_CRC_BLOCKS CRC-checked 16384-byte plane blocks in
- * all) return -5 (Unsupported); -3 if the device's scratch could not be
- * resolved.  Calls on one device are serialised by the library; the array
- * keeps the last call's contents (every call rewrites what it reads). */
+ * all) return -5 (Unsupported).  Calls on one device are serialised by the
+ * library; the array keeps the last call's contents (every call rewrites
+ * what it reads), so calls that overlap on one device from outside the
+ * library (another process) would race. */
 #define PTWM_MI355X_NOALLOC_SCRATCH_BYTES (16u << 20)
 #define PTWM_MI355X_NOALLOC_MAX_TENSORS 4096u
 #define PTWM_MI355X_NOALLOC_MAX_CRC_BLOCKS 883456u
@@ -122,6 +128,20 @@ int64_t ptwm_mi355x_dispatch_decode_noalloc_cuda(uint8_t state_format_version, c
                                                  size_t state_len, const uint8_t *codec_id_ptr, size_t codec_id_len,
                                                  uint64_t in_dev_ptr, size_t in_len, uint64_t out_dev_ptr,
                                                  size_t out_len, uint32_t device_ordinal);
+
+/* Sets up the device's context (stream, pinned status words, the
+ * allocation-free decode's scratch address) if it does not exist yet; every
+ * other entry point does this on its first call on a device, the
+ * allocation-free decode does not.  0, -1 for an invalid ordinal, -3 when
+ * the allocation-free scratch could not be resolved.  No counterpart in the
+ * reference: for callers that cannot allocate later. */
+int64_t ptwm_mi355x_device_init(uint32_t device_ordinal);
+
+/* Process-wide count of the library's own hipMalloc / hipHostMalloc calls
+ * and stream / event creations (grow-only scratch, contexts, hashing
+ * workers).  No counterpart in the reference: lets a caller check that a
+ * call allocated nothing. */
+uint64_t ptwm_mi355x_alloc_calls(void);
 
 /* One tensor of a container, as ptwm_mi355x_container_plan lists it (in
  * record order, the order the reference's tools list and decode them). */

@@ -92,6 +92,10 @@ def lib():
         L.por_decode_plane_chunked_mt.argtypes = [C.c_int, vp, sz, vp, sz, vp, sz, C.c_int]
         L.por_decode_tensors_mt.restype = i64
         L.por_decode_tensors_mt.argtypes = [C.c_int, C.c_int, sz, vp, vp, vp, vp, vp, vp, C.c_int]
+        L.por_batch_decode_mt.restype = i64
+        L.por_batch_decode_mt.argtypes = [sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int]
+        L.por_batch_encode_mt.restype = i64
+        L.por_batch_encode_mt.argtypes = [sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int]
         L.por_huf_lengths_from_freqs.restype = C.c_int
         L.por_huf_lengths_from_freqs.argtypes = [vp, vp]
         L.por_huf_lengths_limited.restype = C.c_int
@@ -363,6 +367,103 @@ class TensorBatch:
 
     def output(self, i: int) -> bytes:
         return self.outs[i][: self.out_lens[i]].tobytes()
+
+
+def _arr(ctype, vals):
+    return (ctype * max(len(vals), 1))(*vals)
+
+
+class PlaneBatch:
+    """Tensors of any chain, each plane with its own codec, chunked or not,
+    decoded together by por_batch_decode_mt: chunks of every plane over the
+    threads (container.rs:1773,1996), then each tensor's inverse chain in
+    slices.  The per-config CPU baseline of the bench."""
+
+    def __init__(self, tensors):
+        """tensors: iterable of (chain, out_len, [(codec, payload, entries or None) per plane])."""
+        self._keep = []
+        chains, olens, outs, codecs, pays, plens, ents, nents, bufs = [], [], [], [], [], [], [], [], []
+        self.outs = []
+        for chain, out_len, planes in tensors:
+            pl = lib().por_chain_plane_len(chain, out_len)
+            assert pl >= 0 and len(planes) == lib().por_chain_nplanes(chain)
+            chains.append(chain)
+            olens.append(out_len)
+            o = np.zeros(max(out_len, 1), np.uint8)
+            self.outs.append(o)
+            outs.append(o.ctypes.data)
+            for codec, pay, ent in planes:
+                p = _buf(pay)
+                e = np.zeros((0, 2), np.uint32) if ent is None else np.ascontiguousarray(ent, dtype=np.uint32)
+                b = np.zeros(max(pl, 1), np.uint8)
+                self._keep += [p, e, b]
+                codecs.append(codec)
+                pays.append(p.ctypes.data)
+                plens.append(p.size)
+                ents.append(e.ctypes.data)
+                nents.append(e.shape[0])
+                bufs.append(b.ctypes.data)
+        self.out_lens = olens
+        self.n = len(olens)
+        self.restored = sum(olens)
+        self._args = (self.n, _arr(C.c_int, chains), _arr(C.c_size_t, olens), _arr(C.c_void_p, outs),
+                      _arr(C.c_int, codecs), _arr(C.c_void_p, pays), _arr(C.c_size_t, plens),
+                      _arr(C.c_void_p, ents), _arr(C.c_size_t, nents), _arr(C.c_void_p, bufs))
+
+    def decode(self, threads: int) -> None:
+        r = lib().por_batch_decode_mt(*self._args, threads)
+        if r < 0:
+            raise OracleError(r, "batch_decode_mt")
+
+    def output(self, i: int) -> bytes:
+        return self.outs[i][: self.out_lens[i]].tobytes()
+
+
+class PlaneBatchEncoder:
+    """The encode direction of PlaneBatch (por_batch_encode_mt): the forward
+    chain in slices, then every chunk of every plane over the threads."""
+
+    def __init__(self, tensors):
+        """tensors: iterable of (chain, raw bytes, [(codec, chunk_size or 0) per plane])."""
+        self._keep = []
+        chains, ilens, ins, codecs, csz, bufs, outs, ents = [], [], [], [], [], [], [], []
+        self._planes = []
+        for chain, raw, planes in tensors:
+            r = _buf(raw)
+            pl = lib().por_chain_plane_len(chain, r.size)
+            assert pl >= 0 and len(planes) == lib().por_chain_nplanes(chain)
+            self._keep.append(r)
+            chains.append(chain)
+            ilens.append(r.size)
+            ins.append(r.ctypes.data)
+            for codec, cs in planes:
+                nch = max(1, -(-pl // cs)) if cs else 1
+                cap = nch * (5 + lib().por_codec_encode_bound(cs)) if cs else lib().por_codec_encode_bound(pl)
+                b = np.zeros(max(pl, 1), np.uint8)
+                o = np.zeros(max(cap, 1), np.uint8)
+                e = np.zeros((nch, 2), np.uint32)
+                self._keep += [b, o, e]
+                self._planes.append((o, e, cs))
+                codecs.append(codec)
+                csz.append(cs)
+                bufs.append(b.ctypes.data)
+                outs.append(o.ctypes.data)
+                ents.append(e.ctypes.data)
+        self.restored = sum(ilens)
+        self._lens = (C.c_size_t * max(len(outs), 1))()
+        self._args = (len(chains), _arr(C.c_int, chains), _arr(C.c_size_t, ilens), _arr(C.c_void_p, ins),
+                      _arr(C.c_int, codecs), _arr(C.c_uint32, csz), _arr(C.c_void_p, bufs),
+                      _arr(C.c_void_p, outs), _arr(C.c_void_p, ents), self._lens)
+
+    def encode(self, threads: int) -> None:
+        r = lib().por_batch_encode_mt(*self._args, threads)
+        if r < 0:
+            raise OracleError(r, "batch_encode_mt")
+
+    def planes(self):
+        """[(payload bytes, entries or None)] in plane order, after encode()."""
+        return [(o[: self._lens[k]].tobytes(), e.copy() if cs else None)
+                for k, (o, e, cs) in enumerate(self._planes)]
 
 
 # ---- chains (transforms/fusion.rs) ----

@@ -10,6 +10,7 @@
  *
  * Parity pinning (what checks each part) is listed in tests/test_oracle_*.py.
  */
+#define _POSIX_C_SOURCE 200809L   /* pthread barriers under -std=c11 */
 #include "ptwm_oracle.h"
 
 #include <pthread.h>
@@ -1248,6 +1249,236 @@ int64_t por_decode_tensors_mt(int codec, int chain, size_t n_tensors, const uint
     for (int t = 0; t < threads; t++) pthread_join(th[t], NULL);
     free(th);
     return job.err;
+}
+
+/* ------------------------------------------------------------------------- */
+/* Per-config CPU baselines: a batch of tensors of any chain, each plane with */
+/* its own codec, chunked (chunk frames + table, compressor.rs:316-381) or    */
+/* not.  Decode: every chunk of every plane of every tensor is one unit on a  */
+/* shared queue over `threads` pthreads (container.rs:1773 runs tensors and   */
+/* :1996 their chunks on rayon workers), then each tensor's inverse chain in  */
+/* slices of 2^20 plane positions over the same workers (the reference runs   */
+/* a tensor's inverse on one worker: slicing only helps the CPU figure).      */
+/* Encode: the forward chain in slices, then one unit per chunk (written at a */
+/* fixed stride), then each plane's frames packed together with its table.   */
+/* ------------------------------------------------------------------------- */
+
+#define BATCH_SLICE ((size_t)1 << 20)
+
+typedef struct { size_t plane, chunk, dst, len; } batch_unit_t;
+typedef struct { size_t tensor, a, b; } batch_slice_t;
+
+typedef struct {
+    size_t n_units, n_slices, n_planes;
+    batch_unit_t *units; batch_slice_t *slices;
+    const int *chains; const size_t *plane_base;
+    /* decode */
+    const size_t *out_lens; uint8_t *const *outs;
+    const int *codecs; const uint8_t *const *payloads; const size_t *payload_lens;
+    const uint32_t *const *entries; const size_t *n_entries;
+    uint8_t *const *plane_bufs;
+    /* encode */
+    const uint8_t *const *ins; const uint32_t *chunk_sizes; uint8_t *const *enc_outs;
+    uint32_t *const *enc_entries; size_t *enc_lens; size_t *unit_len;
+    size_t next_unit, next_slice, next_plane;
+    pthread_barrier_t bar;
+    int64_t err;
+} batch_job_t;
+
+static void batch_fail(batch_job_t *j, int64_t r) { __atomic_store_n(&j->err, r, __ATOMIC_RELAXED); }
+
+static size_t batch_out_per_pos(int chain) {
+    return chain == POR_CHAIN_IEEE16_SPLIT2 ? 2 : chain == POR_CHAIN_IEEE32_SPLIT4 ? 4 : 1;
+}
+
+static void *batch_decode_worker(void *arg) {
+    batch_job_t *j = (batch_job_t *)arg;
+    for (;;) {
+        size_t u = __atomic_fetch_add(&j->next_unit, 1, __ATOMIC_RELAXED);
+        if (u >= j->n_units) break;
+        const batch_unit_t *U = &j->units[u];
+        size_t k = U->plane;
+        int64_t r;
+        if (j->n_entries[k] == 0) {
+            r = por_codec_decode(j->codecs[k], j->payloads[k], j->payload_lens[k], j->plane_bufs[k], U->dst);
+            if (r >= 0 && (size_t)r != U->dst) r = POR_EINVAL;
+        } else {
+            r = decode_one_chunk(j->codecs[k], j->payloads[k], j->payload_lens[k], j->entries[k], j->n_entries[k],
+                                 U->chunk, j->plane_bufs[k] + U->dst);
+        }
+        if (r < 0) batch_fail(j, r);
+    }
+    pthread_barrier_wait(&j->bar);
+    for (;;) {
+        size_t s = __atomic_fetch_add(&j->next_slice, 1, __ATOMIC_RELAXED);
+        if (s >= j->n_slices || __atomic_load_n(&j->err, __ATOMIC_RELAXED)) break;
+        const batch_slice_t *S = &j->slices[s];
+        int chain = j->chains[S->tensor];
+        size_t base = j->plane_base[S->tensor];
+        const uint8_t *pl[4] = {0, 0, 0, 0};
+        for (int p = 0; p < por_chain_nplanes(chain); p++) pl[p] = j->plane_bufs[base + p] + S->a;
+        int r = por_chain_inverse(chain, pl, S->b - S->a, j->outs[S->tensor] + S->a * batch_out_per_pos(chain));
+        if (r < 0) batch_fail(j, r);
+    }
+    return NULL;
+}
+
+/* Plans the units and slices shared by both directions; plane lengths from
+ * the tensor lengths.  Returns 0 or an error. */
+static int64_t batch_plan(batch_job_t *j, size_t n_tensors, const size_t *lens, int decode) {
+    size_t np_total = 0, n_units = 0, n_slices = 0;
+    size_t *base = (size_t *)malloc((n_tensors + 1) * sizeof(size_t));
+    if (!base) return POR_ESMALL;
+    for (size_t t = 0; t < n_tensors; t++) {
+        int np = por_chain_nplanes(j->chains[t]);
+        int64_t pl = por_chain_plane_len(j->chains[t], lens[t]);
+        if (np <= 0 || pl < 0) { free(base); return POR_EINVAL; }
+        base[t] = np_total;
+        for (int p = 0; p < np; p++) {
+            size_t k = np_total + (size_t)p;
+            if (decode) n_units += j->n_entries[k] ? j->n_entries[k] : 1;
+            else n_units += j->chunk_sizes[k] ? ((size_t)pl + j->chunk_sizes[k] - 1) / j->chunk_sizes[k] + !pl : 1;
+        }
+        np_total += (size_t)np;
+        n_slices += ((size_t)pl + BATCH_SLICE - 1) / BATCH_SLICE;
+    }
+    base[n_tensors] = np_total;
+    j->units = (batch_unit_t *)malloc((n_units + 1) * sizeof(batch_unit_t));
+    j->slices = (batch_slice_t *)malloc((n_slices + 1) * sizeof(batch_slice_t));
+    if (!j->units || !j->slices) { free(base); return POR_ESMALL; }
+    size_t u = 0, s = 0;
+    for (size_t t = 0; t < n_tensors; t++) {
+        size_t pl = (size_t)por_chain_plane_len(j->chains[t], lens[t]);
+        for (size_t k = base[t]; k < base[t + 1]; k++) {
+            if (decode && j->n_entries[k]) {
+                size_t dst = 0;
+                for (size_t i = 0; i < j->n_entries[k]; i++) {
+                    j->units[u++] = (batch_unit_t){k, i, dst, j->entries[k][2 * i + 1]};
+                    dst += j->entries[k][2 * i + 1];
+                }
+                if (dst != pl) { free(base); return POR_EINVAL; }
+            } else if (!decode && j->chunk_sizes[k]) {
+                size_t cs = j->chunk_sizes[k], nch = pl ? (pl + cs - 1) / cs : 1;
+                for (size_t i = 0; i < nch; i++)
+                    j->units[u++] = (batch_unit_t){k, i, i * cs, (i + 1) * cs < pl ? cs : pl - i * cs};
+            } else {
+                j->units[u++] = (batch_unit_t){k, (size_t)-1, pl, pl};
+            }
+        }
+        for (size_t a = 0; a < pl; a += BATCH_SLICE)
+            j->slices[s++] = (batch_slice_t){t, a, a + BATCH_SLICE < pl ? a + BATCH_SLICE : pl};
+    }
+    j->n_units = u;
+    j->n_slices = s;
+    j->n_planes = np_total;
+    j->plane_base = base;
+    return 0;
+}
+
+static void batch_free(batch_job_t *j) {
+    free(j->units);
+    free(j->slices);
+    free((void *)j->plane_base);
+}
+
+static int64_t batch_run(batch_job_t *j, int threads, void *(*fn)(void *)) {
+    if (threads < 1) threads = 1;
+    pthread_barrier_init(&j->bar, NULL, (unsigned)threads);
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
+    if (!th) return POR_ESMALL;
+    for (int t = 0; t < threads; t++) pthread_create(&th[t], NULL, fn, j);
+    for (int t = 0; t < threads; t++) pthread_join(th[t], NULL);
+    free(th);
+    pthread_barrier_destroy(&j->bar);
+    return j->err;
+}
+
+int64_t por_batch_decode_mt(size_t n_tensors, const int *chains, const size_t *out_lens, uint8_t *const *outs,
+                            const int *codecs, const uint8_t *const *payloads, const size_t *payload_lens,
+                            const uint32_t *const *entries, const size_t *n_entries, uint8_t *const *plane_bufs,
+                            int threads) {
+    batch_job_t j;
+    memset(&j, 0, sizeof j);
+    j.chains = chains; j.out_lens = out_lens; j.outs = outs; j.codecs = codecs; j.payloads = payloads;
+    j.payload_lens = payload_lens; j.entries = entries; j.n_entries = n_entries; j.plane_bufs = plane_bufs;
+    int64_t r = batch_plan(&j, n_tensors, out_lens, 1);
+    if (r == 0) r = batch_run(&j, threads, batch_decode_worker);
+    batch_free(&j);
+    return r;
+}
+
+static void *batch_encode_worker(void *arg) {
+    batch_job_t *j = (batch_job_t *)arg;
+    for (;;) {   /* forward chain, slice by slice, into the plane buffers */
+        size_t s = __atomic_fetch_add(&j->next_slice, 1, __ATOMIC_RELAXED);
+        if (s >= j->n_slices) break;
+        const batch_slice_t *S = &j->slices[s];
+        int chain = j->chains[S->tensor];
+        size_t base = j->plane_base[S->tensor];
+        uint8_t *pl[4] = {0, 0, 0, 0};
+        for (int p = 0; p < por_chain_nplanes(chain); p++) pl[p] = j->plane_bufs[base + p] + S->a;
+        size_t w = batch_out_per_pos(chain);
+        int r = por_chain_forward(chain, j->ins[S->tensor] + S->a * w, (S->b - S->a) * w, pl);
+        if (r < 0) batch_fail(j, r);
+    }
+    pthread_barrier_wait(&j->bar);
+    for (;;) {   /* one chunk (or unchunked plane) per unit, at its fixed stride */
+        size_t u = __atomic_fetch_add(&j->next_unit, 1, __ATOMIC_RELAXED);
+        if (u >= j->n_units || __atomic_load_n(&j->err, __ATOMIC_RELAXED)) break;
+        const batch_unit_t *U = &j->units[u];
+        size_t k = U->plane;
+        int64_t n;
+        if (U->chunk == (size_t)-1) {
+            n = por_codec_encode(j->codecs[k], j->plane_bufs[k], U->dst, j->enc_outs[k], por_codec_encode_bound(U->dst));
+        } else {
+            size_t cs = j->chunk_sizes[k], len = U->len;
+            uint8_t *o = j->enc_outs[k] + U->chunk * (5 + por_codec_encode_bound(cs));
+            o[0] = 0; st32(o + 1, 0);
+            n = por_codec_encode(j->codecs[k], j->plane_bufs[k] + U->dst, len, o + 5, por_codec_encode_bound(cs));
+            if (n >= 0) n += 5;
+        }
+        if (n < 0) batch_fail(j, n);
+        else j->unit_len[u] = (size_t)n;
+    }
+    pthread_barrier_wait(&j->bar);
+    for (;;) {   /* pack each chunked plane's frames and write its table */
+        size_t k = __atomic_fetch_add(&j->next_plane, 1, __ATOMIC_RELAXED);
+        if (k >= j->n_planes || __atomic_load_n(&j->err, __ATOMIC_RELAXED)) break;
+        size_t off = 0, i = 0;
+        for (size_t u = 0; u < j->n_units; u++) {
+            if (j->units[u].plane != k) continue;
+            if (j->units[u].chunk == (size_t)-1) { off = j->unit_len[u]; break; }
+            size_t stride = 5 + por_codec_encode_bound(j->chunk_sizes[k]);
+            memmove(j->enc_outs[k] + off, j->enc_outs[k] + i * stride, j->unit_len[u]);
+            j->enc_entries[k][2 * i] = (uint32_t)off;
+            j->enc_entries[k][2 * i + 1] = (uint32_t)j->units[u].len;
+            off += j->unit_len[u];
+            i++;
+        }
+        j->enc_lens[k] = off;
+    }
+    return NULL;
+}
+
+/* Encode batch: enc_outs[k] must hold n_chunks * (5 + bound(chunk)) bytes
+ * (one codec bound of the plane when unchunked), enc_entries[k] 2 u32 per
+ * chunk; enc_lens[k] receives the packed payload length. */
+int64_t por_batch_encode_mt(size_t n_tensors, const int *chains, const size_t *in_lens, const uint8_t *const *ins,
+                            const int *codecs, const uint32_t *chunk_sizes, uint8_t *const *plane_bufs,
+                            uint8_t *const *enc_outs, uint32_t *const *enc_entries, size_t *enc_lens, int threads) {
+    batch_job_t j;
+    memset(&j, 0, sizeof j);
+    j.chains = chains; j.ins = ins; j.codecs = codecs; j.chunk_sizes = chunk_sizes; j.plane_bufs = plane_bufs;
+    j.enc_outs = enc_outs; j.enc_entries = enc_entries; j.enc_lens = enc_lens;
+    int64_t r = batch_plan(&j, n_tensors, in_lens, 0);
+    if (r == 0) {
+        j.unit_len = (size_t *)calloc(j.n_units + 1, sizeof(size_t));
+        if (!j.unit_len) r = POR_ESMALL;
+    }
+    if (r == 0) r = batch_run(&j, threads, batch_encode_worker);
+    free(j.unit_len);
+    batch_free(&j);
+    return r;
 }
 
 /* ------------------------------------------------------------------------- */

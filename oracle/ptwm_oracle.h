@@ -177,6 +177,18 @@ int64_t por_decode_tensors_mt(int codec, int chain, size_t n_tensors, const uint
                               const size_t *payload_lens, const uint32_t *const *entries, const size_t *n_entries,
                               uint8_t *const *outs, const size_t *out_lens, int threads);
 
+/* per-config CPU baselines: tensors of any chain, a codec per plane, each
+ * plane chunked (n_entries > 0 / chunk_sizes > 0) or one payload; chunks of
+ * all planes over threads, then the inverse (forward) chain in slices.
+ * Planes are tensor-major (tensor t's planes follow tensor t-1's). */
+int64_t por_batch_decode_mt(size_t n_tensors, const int *chains, const size_t *out_lens, uint8_t *const *outs,
+                            const int *codecs, const uint8_t *const *payloads, const size_t *payload_lens,
+                            const uint32_t *const *entries, const size_t *n_entries, uint8_t *const *plane_bufs,
+                            int threads);
+int64_t por_batch_encode_mt(size_t n_tensors, const int *chains, const size_t *in_lens, const uint8_t *const *ins,
+                            const int *codecs, const uint32_t *chunk_sizes, uint8_t *const *plane_bufs,
+                            uint8_t *const *enc_outs, uint32_t *const *enc_entries, size_t *enc_lens, int threads);
+
 /* ---- huff_ilv: this build's GPU-native plane codec (no reference
  * counterpart; its wire format is specified by these two functions).  Code
  * lengths, canonical codes and the weights header are the reference

@@ -91,7 +91,9 @@ struct DeviceScope {
   std::unique_lock<std::mutex> lk;
   int prev = -1;
   bool ok = false;
-  explicit DeviceScope(uint32_t ord) : ctx(get_ctx(ord)) {
+  // create: make the device's context on first use (every entry point but
+  // the allocation-free decode, which only takes an existing one)
+  explicit DeviceScope(uint32_t ord, bool create = true) : ctx(create ? get_ctx(ord) : find_ctx(ord)) {
     if (!ctx) return;
     lk = std::unique_lock<std::mutex>(ctx->mu);
     ctx->stream = t_stream.set && t_stream.dev == ord ? reinterpret_cast<hipStream_t>(t_stream.stream) : ctx->own_stream;
@@ -366,7 +368,8 @@ int64_t ptwm_mi355x_dispatch_decode_noalloc_cuda(uint8_t state_format_version, c
   int64_t rc = accept_plan(state_ptr, state_len, codec_id_ptr, codec_id_len, in_dev_ptr, in_len, out_dev_ptr,
                            out_len, plan, &total);
   if (rc != kOk) return rc;
-  DeviceScope ds(device_ordinal);
+  DeviceScope ds(device_ordinal, false);
+  if (!ds.ctx) return kMissingCapability;  // ptwm_mi355x_device_init was not called for this device
   if (!ds.ok) return kInvalidInput;
   rc = execute_plan_noalloc(*ds.ctx, plan, in_dev_ptr, out_dev_ptr);
   return rc == kOk ? (int64_t)total : rc;
@@ -1028,11 +1031,20 @@ int64_t ptwm_mi355x_stream_wait(uint64_t producer_stream, uint32_t device_ordina
   DevCtx& ctx = *ds.ctx;
   hipStream_t prod = reinterpret_cast<hipStream_t>(producer_stream);
   if (prod == ctx.stream) return 0;
+  if (!ctx.order_ev) note_alloc();
   if (!ctx.order_ev) PTWM_HIP_TRY(hipEventCreateWithFlags(&ctx.order_ev, hipEventDisableTiming));
   PTWM_HIP_TRY(hipEventRecord(ctx.order_ev, prod));
   PTWM_HIP_TRY(hipStreamWaitEvent(ctx.stream, ctx.order_ev, 0));
   return 0;
 }
+
+int64_t ptwm_mi355x_device_init(uint32_t device_ordinal) {
+  DevCtx* c = get_ctx(device_ordinal);
+  if (!c) return kInvalidInput;
+  return c->noalloc_dev && c->noalloc_status ? 0 : kMissingCapability;
+}
+
+uint64_t ptwm_mi355x_alloc_calls(void) { return alloc_calls(); }
 
 int64_t ptwm_mi355x_set_profiling(uint32_t device_ordinal, uint32_t on) {
   DeviceScope ds(device_ordinal);

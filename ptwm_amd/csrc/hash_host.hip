@@ -26,12 +26,15 @@ namespace ptwm {
 hipError_t HashWorker::init() {
   if (stream) return hipSuccess;
   for (int i = 0; i < 2; ++i) {
+    note_alloc();
     hipError_t e = hipHostMalloc(&pinned[i], kHashChunk, hipHostMallocDefault);
     if (e != hipSuccess) return e;
+    note_alloc();
     e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
     if (e != hipSuccess) return e;
   }
   // default priority: mixing stream priorities is avoided on purpose
+  note_alloc();
   return hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
 }
 
@@ -95,6 +98,7 @@ int64_t xxh64_buffers(DevCtx& ctx, const std::vector<HashTask>& tasks, std::vect
   const uint32_t nw = (uint32_t)std::min<size_t>(want, tasks.size());
   if (ctx.hash_workers.size() < nw) ctx.hash_workers.resize(nw);
   for (uint32_t w = 0; w < nw; ++w) PTWM_HIP_TRY(ctx.hash_workers[w].init());
+  if (!ctx.hash_ready) note_alloc();
   if (!ctx.hash_ready) PTWM_HIP_TRY(hipEventCreateWithFlags(&ctx.hash_ready, hipEventDisableTiming));
   // everything queued on the call's stream (the restore) precedes the copies
   PTWM_HIP_TRY(hipEventRecord(ctx.hash_ready, ctx.stream));

@@ -21,6 +21,9 @@
 //   pieces by the whole wavefront.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
+#include <mutex>
+
 #include "decode_sync.h"
 
 namespace ptwm {
@@ -34,6 +37,14 @@ constexpr uint32_t kO1Stage = 4096;
 // LDS: [cum: 257 rows x 256 u16][row map: 256 u16][payload stage][symbol stage]
 constexpr size_t kO1CumBytes = 257ull * kO1Alpha * 2;
 constexpr size_t kO1Lds = kO1CumBytes + 2 * kO1Alpha + 2 * kO1Stage;
+
+// log2(4096 / p) for p = 1..4095, the bits per symbol of max_decodable_len
+// (:449-472), computed on the host with the C library's log2 (the one the
+// reference's f64::log2 calls on Linux) and copied here once per device, so
+// that the capacity bound's floating-point value, hence the accept / reject
+// decision at its edge, is the reference's bit for bit; the division and
+// floor after it are exactly rounded on both sides.
+__constant__ double o1_bits[kO1Total];
 
 __device__ __forceinline__ uint32_t ld8(const uint8_t* p) { return g_ld<uint8_t>(reinterpret_cast<uint64_t>(p)); }
 
@@ -165,7 +176,7 @@ __global__ void __launch_bounds__(64) o1sac_decode_kernel(const DecodeJob* __res
   const uint64_t rl = row_len_plan ? row_len_plan : (n ? n : 1);
   bool len_ok = n % rl == 0;
   if (len_ok && pmax < kO1Total) {
-    const double bits = log2((double)kO1Total / (double)pmax);
+    const double bits = o1_bits[pmax];
     const double budget = 8.0 * (double)(plen > 5 ? plen - 5 : 0);
     const double cap = floor(budget / bits) + 1.0;
     len_ok = cap >= 18446744073709551615.0 || (double)n <= cap;
@@ -227,7 +238,24 @@ __global__ void __launch_bounds__(64) o1sac_decode_kernel(const DecodeJob* __res
 
 hipError_t launch_o1sac_decode(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs, hipStream_t stream) {
   if (n_jobs == 0) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute((const void*)o1sac_decode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+  static std::mutex mu;
+  static bool bits_ready[64] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    if (!bits_ready[dev]) {
+      double bits[kO1Total];
+      bits[0] = 0.0;  // p_max >= 1 in a checked state
+      for (uint32_t p = 1; p < kO1Total; ++p) bits[p] = std::log2((double)kO1Total / (double)p);
+      e = hipMemcpyToSymbol(HIP_SYMBOL(o1_bits), bits, sizeof bits);
+      if (e != hipSuccess) return e;
+      bits_ready[dev] = true;
+    }
+  }
+  e = hipFuncSetAttribute((const void*)o1sac_decode_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)kO1Lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(o1sac_decode_kernel, dim3(n_jobs), dim3(64), kO1Lds, stream, jobs_dev, status_dev);

@@ -128,7 +128,17 @@ struct DevCtx {
 };
 
 // Returns nullptr if the ordinal is invalid or HIP initialisation fails.
+// Creates the device's context on its first call (a stream, pinned status
+// words, the allocation-free decode's scratch address).
 DevCtx* get_ctx(uint32_t device_ordinal);
+// The device's context if it exists, else nullptr; never creates one.
+DevCtx* find_ctx(uint32_t device_ordinal);
+
+// Process-wide count of the library's own hipMalloc / hipHostMalloc calls
+// and stream / event creations (ptwm_mi355x_alloc_calls); every such call
+// site counts itself with note_alloc().
+void note_alloc();
+uint64_t alloc_calls();
 
 
 // Decode every tensor of the plan from in_dev into out_dev (device

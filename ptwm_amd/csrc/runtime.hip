@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <array>
+#include <atomic>
 #include <cstring>
 #include <memory>
 
@@ -21,6 +22,12 @@
 
 namespace ptwm {
 
+namespace {
+std::atomic<uint64_t> g_alloc_calls{0};
+}
+void note_alloc() { g_alloc_calls.fetch_add(1, std::memory_order_relaxed); }
+uint64_t alloc_calls() { return g_alloc_calls.load(std::memory_order_relaxed); }
+
 hipError_t DeviceBuffer::ensure(size_t bytes) {
   if (bytes <= cap && ptr) return hipSuccess;
   if (borrowed) return hipErrorOutOfMemory;
@@ -30,6 +37,7 @@ hipError_t DeviceBuffer::ensure(size_t bytes) {
     cap = 0;
   }
   size_t want = bytes < 4096 ? 4096 : bytes;
+  note_alloc();
   hipError_t e = hipMalloc(&ptr, want);
   if (e == hipSuccess) cap = want;
   return e;
@@ -45,6 +53,7 @@ hipError_t PinnedBuffer::ensure(size_t bytes) {
     cap = 0;
   }
   size_t want = bytes < 4096 ? 4096 : bytes;
+  note_alloc();
   hipError_t e = hipHostMalloc(&ptr, want, flags);
   if (e == hipSuccess) cap = want;
   return e;
@@ -54,6 +63,7 @@ PinnedBuffer::~PinnedBuffer() {}
 hipError_t DevCtx::ensure_events() {
   for (auto& e : ev)
     if (!e) {
+      note_alloc();
       hipError_t r = hipEventCreate(&e);
       if (r != hipSuccess) return r;
     }
@@ -72,6 +82,12 @@ std::array<std::unique_ptr<DevCtx>, 64> g_ctx;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 }  // namespace
 
+DevCtx* find_ctx(uint32_t ord) {
+  if (ord >= g_ctx.size()) return nullptr;
+  std::lock_guard<std::mutex> lk(g_ctx_mu);
+  return g_ctx[ord].get();
+}
+
 DevCtx* get_ctx(uint32_t ord) {
   if (ord >= g_ctx.size()) return nullptr;
   std::lock_guard<std::mutex> lk(g_ctx_mu);
@@ -84,6 +100,7 @@ DevCtx* get_ctx(uint32_t ord) {
   auto ctx = std::make_unique<DevCtx>();
   ctx->dev = (int)ord;
   // default priority: mixing stream priorities is avoided on purpose
+  note_alloc();
   if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
     (void)hipSetDevice(prev);
     return nullptr;
@@ -94,6 +111,7 @@ DevCtx* get_ctx(uint32_t ord) {
   // current): its address, or null, and the entry point then reports
   // MissingCapability
   void* sp = nullptr;
+  note_alloc();
   if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess && sp &&
       hipHostMalloc(&ctx->noalloc_status, kNoAllocStatusBytes, hipHostMallocCoherent) == hipSuccess) {
     ctx->noalloc_dev = static_cast<uint8_t*>(sp);

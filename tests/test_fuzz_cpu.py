@@ -11,6 +11,7 @@ plan the reader writes always parses).
 import glob
 import os
 import shutil
+import struct
 import subprocess
 
 import pytest
@@ -37,8 +38,27 @@ def _seeds(d):
         open(os.path.join(d, "q%03d" % k), "wb").write(b"\x01" + plan)
         k += 1
     # regression: a legacy record whose name runs past the record's end
+    open(os.path.join(d, "r000"), "wb").write(b"\x00" + overlong_name_file())
+
+
+def overlong_name_file() -> bytes:
+    """legacy_v1_1_0.ptwm with its first record's name length (the u16 at
+    record offset 16, tensor_record.rs:265-420) set to the record's length,
+    so that the name runs past the record's end."""
     data = bytearray(open(os.path.join(HERE, "golden", "ptwm_files", "legacy_v1_1_0.ptwm"), "rb").read())
-    open(os.path.join(d, "r000"), "wb").write(b"\x00" + bytes(data))
+    _, ents, _ = api.container_plan(bytes(data))
+    e = ents[0]
+    assert struct.unpack_from("<H", data, e.record_offset + 16)[0] == len(e.name.encode())
+    struct.pack_into("<H", data, e.record_offset + 16, e.record_len)
+    return bytes(data)
+
+
+def test_overlong_legacy_name_is_rejected():
+    """The record is listed as invalid (-1, no name reported); the other
+    records still plan."""
+    _, ents, _ = api.container_plan(overlong_name_file())
+    assert ents[0].status == -1 and ents[0].plan_index == -1 and ents[0].name == ""
+    assert all(e.status == 0 for e in ents[1:])
 
 
 @pytest.mark.skipif(not os.path.exists(CLANG), reason="ROCm clang (libFuzzer) not installed")

@@ -149,3 +149,30 @@ def test_malformed_states_and_lengths_are_refused():
         with pytest.raises(Exception) as ei:
             dispatch(s, bl, out_len)
         assert getattr(ei.value, "rc", None) == -1, k
+
+
+def test_capacity_bound_edge_matches_the_oracle():
+    """A declared length exactly at max_decodable_len (order1_scale_ac.rs:
+    449-472) is decoded, one past it refused, on the device as by the oracle:
+    the bound's log2 comes from the host C library on both sides."""
+    import math
+
+    rng = np.random.default_rng(9)
+    st = make_state(rng, [1, 2, 3], skew=3.0)
+    pay = O.o1sac_encode(st, markov_plane(rng, 3000, 0), 0)
+    counts = np.frombuffer(st[32:], np.uint16)
+    cap = math.floor(8 * (len(pay) - 5) / math.log2(4096 / int(counts.max()))) + 1
+    note(f"o1sac capacity edge: pmax {int(counts.max())}, payload {len(pay)} B, cap {cap}")
+    blob = b"\x07" + st + b"\x01" + pay
+    soff, poff = 1, 2 + len(st)
+    for n, accepted in ((cap, True), (cap + 1, False)):
+        pp = P.PlanePlan(O.CODEC_O1SAC, poff, len(pay), n, None, None, state=(soff, len(st), 0, 1))
+        state = P.encode_plan([P.TensorPlan(P.CHAIN_PASSTHROUGH, 0, n, [pp])])
+        if accepted:
+            assert dispatch(state, blob, n) == O.o1sac_decode(st, pay, n, 0)
+        else:
+            with pytest.raises(O.OracleError):
+                O.o1sac_decode(st, pay, n, 0)
+            with pytest.raises(Exception) as ei:
+                dispatch(state, blob, n)
+            assert getattr(ei.value, "rc", None) == -1

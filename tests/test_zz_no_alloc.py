@@ -4,12 +4,16 @@
 
 Two calls in a row, the second with a smaller input, for both GPU-native
 codecs, with plane CRC-32 verification: restored bytes equal the regular
-entry point's and the inputs.  Plans outside the allocation-free route
-(tensor XXH64, reference-format planes) are refused with -5, a wrong CRC
-with -1, as the regular entry point does; the regular entry point still works
-after it.
+entry point's and the inputs, and the library's own allocation counter
+(ptwm_mi355x_alloc_calls) does not move across any allocation-free call.
+Plans outside the allocation-free route (tensor XXH64, reference-format
+planes) are refused with -5, a wrong CRC with -1, as the regular entry point
+does; the regular entry point still works after it.  In a fresh process the
+call returns -3 before ptwm_mi355x_device_init and decodes after it.
 """
 import ctypes as C
+import os
+import subprocess
 import sys
 
 import pytest
@@ -33,8 +37,11 @@ def plan_id() -> bytes:
 def noalloc(st: bytes, blob, out) -> int:
     torch.cuda.synchronize()
     pid = plan_id()
-    return lib().ptwm_mi355x_dispatch_decode_noalloc_cuda(
+    before = lib().ptwm_mi355x_alloc_calls()
+    rc = lib().ptwm_mi355x_dispatch_decode_noalloc_cuda(
         1, st, len(st), pid, 32, blob.data_ptr(), blob.numel(), out.data_ptr(), out.numel(), 0)
+    assert lib().ptwm_mi355x_alloc_calls() == before, "the allocation-free decode allocated"
+    return rc
 
 
 def regular(st: bytes, blob, out) -> int:
@@ -111,3 +118,56 @@ def test_noalloc_refuses_what_it_does_not_cover():
     assert regular(plan.encode_plan(plans), blob, out) == total
     for (_, r), t in zip(items, plans):
         assert torch.equal(out[t.out_offset: t.out_offset + t.out_len], r)
+
+
+FRESH = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import numpy as np
+import torch
+import oracle as O
+from ptwm_amd import ids, plan
+from ptwm_amd._native import lib
+
+L = lib()
+raw = (torch.randn(70001, generator=torch.Generator().manual_seed(5)) * 0.02).to(torch.bfloat16)
+raw = raw.view(torch.uint8).numpy().tobytes()
+planes = O.chain_forward(O.CHAIN_IEEE16_SPLIT2, raw)
+pays = [O.ilv_encode(p) for p in planes]
+off1 = (len(pays[0]) + 255) // 256 * 256
+blob = pays[0] + bytes(off1 - len(pays[0])) + pays[1]
+st = plan.encode_plan([plan.TensorPlan(plan.CHAIN_IEEE16_SPLIT2, 0, len(raw), [
+    plan.PlanePlan(ids.CODEC_HUFF_ILV, 0, len(pays[0]), len(planes[0])),
+    plan.PlanePlan(ids.CODEC_HUFF_ILV, off1, len(pays[1]), len(planes[1]))])])
+d_in = torch.from_numpy(np.frombuffer(blob, np.uint8).copy()).to("cuda:0")
+d_out = torch.zeros(len(raw), dtype=torch.uint8, device="cuda:0")
+pid = bytes.fromhex(ids.OWN_IDS[ids.DECODE_PLAN_LABEL])
+torch.cuda.synchronize()
+
+def call():
+    return L.ptwm_mi355x_dispatch_decode_noalloc_cuda(1, st, len(st), pid, 32, d_in.data_ptr(), d_in.numel(),
+                                                      d_out.data_ptr(), d_out.numel(), 0)
+
+n0 = L.ptwm_mi355x_alloc_calls()
+print("before init", call(), L.ptwm_mi355x_alloc_calls() - n0, flush=True)
+print("init", L.ptwm_mi355x_device_init(0), flush=True)
+n1 = L.ptwm_mi355x_alloc_calls()
+for k in range(2):
+    rc = call()
+    torch.cuda.synchronize()
+    print("call", k, rc, L.ptwm_mi355x_alloc_calls() - n1, d_out.cpu().numpy().tobytes() == raw, flush=True)
+"""
+
+
+def test_noalloc_needs_init_in_a_fresh_process():
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    note("noalloc fresh process: call before and after ptwm_mi355x_device_init")
+    r = subprocess.run([sys.executable, "-c", FRESH, root], capture_output=True, text=True, timeout=240)
+    note(r.stdout + r.stderr[-2000:])
+    assert r.returncode == 0
+    lines = [l.split() for l in r.stdout.splitlines()]
+    assert lines[0] == ["before", "init", "-3", "0"]   # no context: refused, nothing created
+    assert lines[1] == ["init", "0"]
+    n = 70001 * 2
+    assert lines[2] == ["call", "0", str(n), "0", "True"]
+    assert lines[3] == ["call", "1", str(n), "0", "True"]
