@@ -33,8 +33,17 @@ constexpr uint32_t kHdrStage = 160;  // staged Huffman header bytes: weights (<=
 constexpr uint32_t kRansProbBits = 11;
 constexpr uint32_t kRansScale = 1u << kRansProbBits;
 constexpr uint32_t kRansL = 1u << 23;
-constexpr uint32_t kRansStage = 1024;  // staged bytes per stream per round
-constexpr uint32_t kRansRound = 384;   // symbols per stream per round (<= 2 bytes each)
+// rANS stream bytes reach the four chains through one LDS ring per chain:
+// kRansRing bytes (a power of two) plus a copy of its first granule after
+// its end, so that the byte after the ring's last one is read at the next
+// address.  Each round the wavefront stages up to kRansStageGranules
+// 16-byte granules per chain (global loads issued before the round's decode
+// and written to the rings after it) and every chain decodes up to
+// kRansRound symbols from what is staged.
+constexpr uint32_t kRansRing = 2048;
+constexpr uint32_t kRansRingPad = 16;
+constexpr uint32_t kRansStageGranules = 32;   // 2 per lane: 512 bytes per chain per round
+constexpr uint32_t kRansRound = 256;          // <= 2 bytes per symbol: 512 bytes per chain
 
 __device__ inline uint32_t ld_u32le(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
@@ -220,6 +229,10 @@ __device__ void parse_job(const DecodeJob& job, SharedHeader& h) {
   h.enc_len = enc_len;
 }
 
+// kRans: the rANS jobs (their own launch: its table entries and stream rings
+// take three times the LDS of the other codecs), else every other job of
+// this kernel.
+template <bool kRans>
 __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __restrict__ jobs,
                                                           uint32_t* __restrict__ status,
                                                           SyncStream* __restrict__ sync_streams,
@@ -230,13 +243,18 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
   __shared__ uint16_t counts[kHufMaxBits + 1];
   __shared__ uint16_t next_code[kHufMaxBits + 1];
   __shared__ uint16_t rev[256];
-  __shared__ uint32_t table32[kRansScale];  // rANS: sym | freq << 8 | start << 20
+  // rANS: {freq | sym << 24, slot - start} per slot; tANS: one u32 per slot;
+  // Huffman: (len << 8) | sym per window
+  __shared__ __align__(16) uint32_t table_mem[(kRans ? 2 : 1) * kRansScale];
   __shared__ uint8_t hdr_stage[kHdrStage];   // Huffman: weights header and jump table
-  uint16_t* table16 = reinterpret_cast<uint16_t*>(table32);  // Huffman: (len << 8) | sym
+  uint2* table64 = reinterpret_cast<uint2*>(table_mem);
+  uint32_t* table32 = table_mem;
+  uint16_t* table16 = reinterpret_cast<uint16_t*>(table_mem);
 
   const uint32_t lane = threadIdx.x;
   const DecodeJob job = jobs[blockIdx.x];
   if (job.codec == kCodecZstd || job.codec == kCodecO1sac) return;  // zstd_decode_kernel's / o1sac_decode_kernel's job
+  if ((job.codec == kCodecRans) != kRans) return;                    // the other instantiation's job
   const uint8_t* src = reinterpret_cast<const uint8_t*>(job.src);
   uint8_t* dst = reinterpret_cast<uint8_t*>(job.dst);
 
@@ -266,6 +284,7 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
   const uint8_t* enc = src + h.enc_off;
   const uint64_t enc_len = h.enc_len;
 
+  if constexpr (!kRans) {
   if (h.kind == 1) {
     // ---- weights header (weights.rs:34-85) and tree (tree.rs:87-177) ----
     // The header and jump table (at most 2 + 128 + 16 bytes) are staged in
@@ -514,7 +533,9 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
     }
     return;
   }
-
+  if (lane == 0) status[blockIdx.x] = kStBadTag;  // not reached: parse_job gives rANS jobs kind 2
+  return;
+  } else {
   // ---- rANS (rans/decompress.rs) ----
   if (lane == 0) {
     uint32_t st = kStOk;
@@ -560,119 +581,165 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
     cum[256] = (uint16_t)run;
   }
   __syncthreads();
+  // slot i of symbol s: {freq | s << 24, i - start}, so that one 24-bit
+  // multiply-add, freq * (x >> 11) + (i - start), is the state update
   for (uint32_t s = lane; s < 256; s += 64) {
-    uint32_t f = rev[s], st = cum[s];
-    uint32_t entry = s | (f << 8) | (st << 20);
-    for (uint32_t j = 0; j < f; ++j) table32[st + j] = entry;
+    const uint32_t f = rev[s], st = cum[s];
+    for (uint32_t j = 0; j < f; ++j) table64[st + j] = make_uint2(f | (s << 24), j);
   }
-  __syncthreads();
-  // Four lanes run the four serial state chains.  The bytes each chain
-  // renormalises from are staged in LDS by the whole wavefront, a window per
-  // round; a lane that exhausts its window mid-renormalisation suspends and
-  // resumes after the next staging (every round makes progress).
-  __shared__ uint8_t rbuf[4][kRansStage];
-  __shared__ uint64_t rq[4];
-  __shared__ uint32_t rbusy;
+  // Four lanes run the four serial state chains (decompress.rs:80-111).
+  __shared__ __align__(16) uint8_t ring[4][kRansRing + kRansRingPad];
   uint64_t s4[4], e4[4];
   split_four(job.dst_len, s4, e4);
-  const uint8_t* st = enc + h.seg_src[lane & 3];
-  const uint32_t sl = (uint32_t)h.seg_len[lane & 3];  // jump-table lengths are u32
-  uint32_t k = (uint32_t)s4[lane & 3], q = 4;
-  const uint32_t end = (uint32_t)e4[lane & 3];
+  const uint32_t c = lane & 3;
+  const uint32_t sl = (uint32_t)h.seg_len[c];  // jump-table lengths are u32
+  uint32_t k = (uint32_t)s4[c];
+  const uint32_t end = (uint32_t)e4[c];
   const uint64_t out = reinterpret_cast<uint64_t>(dst);
-  uint32_t x = 0;
+  uint32_t x = 0, q = 4;  // state; next stream byte to read
   bool good = true, done = true, pending = false;
   if (lane < 4 && k != end) {
     if (sl < 4) good = false;
     else {
-      x = ld_u32le(st);
+      const uint8_t* st = enc + h.seg_src[c];
+      x = (uint32_t)g_ld<uint8_t>((uint64_t)st) | ((uint32_t)g_ld<uint8_t>((uint64_t)st + 1) << 8) |
+          ((uint32_t)g_ld<uint8_t>((uint64_t)st + 2) << 16) | ((uint32_t)g_ld<uint8_t>((uint64_t)st + 3) << 24);
       done = false;
     }
   }
+  // Staging, as every lane sees it: lane l loads granules (l & 15) and
+  // (l & 15) + 16 of the next ones of chain l >> 4 (of four; lanes 0-63).
+  // A granule is the 16-byte aligned global block g of the segment (its
+  // byte o is at absolute index o + (address & 15)); aligned blocks that
+  // hold a byte of the segment never cross a page, so reading the whole
+  // block is in bounds.  A granule goes to ring slot (16 g) mod kRansRing
+  // only once every byte that slot held has been consumed.
+  const uint32_t sc = lane >> 4, su = lane & 15;
+  const uint64_t sbase = reinterpret_cast<uint64_t>(enc + h.seg_src[sc]);
+  const uint32_t soff = (uint32_t)(sbase & 15u);
+  const uint64_t sgbase = sbase - soff;
+  const uint32_t s_end_g = (uint32_t)((h.seg_len[sc] + soff + 15) / 16);
+  uint32_t s_staged = 0;  // granules of chain sc staged so far (uniform per 16 lanes)
+  uint8_t* const my_ring = ring[c];
+  const uint32_t my_off = (uint32_t)((reinterpret_cast<uint64_t>(enc + h.seg_src[c])) & 15u);
+  __syncthreads();  // table and ring addresses in place
   for (;;) {
-    if (lane < 4) rq[lane] = done ? ~0ull : q;
-    if (lane == 0) rbusy = 0;
-    __syncthreads();
-    if (lane < 4 && !done) atomicOr(&rbusy, 1u);
-    for (uint32_t i = lane; i < 4 * kRansStage; i += 64) {
-      const uint32_t sj = i / kRansStage, o = i % kRansStage;
-      const uint64_t qb = rq[sj];
-      if (qb != ~0ull && qb + o < h.seg_len[sj]) rbuf[sj][o] = g_ld<uint8_t>((uint64_t)(enc + h.seg_src[sj] + qb + o));
-    }
-    __syncthreads();
-    if (rbusy == 0) break;
+    // this round's loads: chain sc's consumption point and done flag from lane sc
+    const uint32_t q_c = (uint32_t)__shfl(q, (int)sc, 64);
+    const bool done_c = __shfl((int)done, (int)sc, 64) != 0;
+    const uint32_t lim = (q_c + soff) / 16 + kRansRing / 16 - 1;  // first granule whose slot is not free
+    const uint32_t upto = done_c ? s_staged : min(min(lim, s_end_g), s_staged + kRansStageGranules);
+    const uint32_t g0 = s_staged + su, g1 = g0 + 16;
+    u32x4 v0 = u32x4_make(0, 0, 0, 0), v1 = v0;
+    if (g0 < upto) v0 = g_ld<u32x4>(sgbase + 16ull * g0);
+    if (g1 < upto) v1 = g_ld<u32x4>(sgbase + 16ull * g1);
+    // decode what is staged: stream bytes [.., avail) of this lane's chain
+    const uint32_t sg_mine = (uint32_t)__shfl((int)s_staged, (int)(16 * c), 64);
+    const bool any = __ballot(lane < 4 && !done) != 0;
     if (lane < 4 && !done) {
-      const uint32_t qb = q;
-      const uint32_t qlim = sl - qb < kRansStage ? sl : qb + kRansStage;  // staged bytes: [qb, qlim)
-      const uint8_t* buf = rbuf[lane];
-      for (uint32_t n = 0;;) {
+      const uint32_t avail = sg_mine ? min(16 * sg_mine - my_off, sl) : 0u;
+      uint32_t n = 0;
+      auto rb = [&](uint32_t o) -> uint32_t { return my_ring[(o + my_off) & (kRansRing - 1)]; };
+      for (;;) {
         if (pending) {  // careful renormalisation after a careful symbol (decompress.rs:104-107)
           bool suspend = false;
           while (x < kRansL) {
             if (q >= sl) { good = false; done = true; break; }
-            if (q >= qlim) { suspend = true; break; }
-            x = (x << 8) | buf[q - qb];
+            if (q >= avail) { suspend = true; break; }
+            x = (x << 8) | rb(q);
             ++q;
           }
           if (done || suspend) break;
           pending = false;
         }
-        // fast stretch: normalised state (x >= L, so at most two renormalising
-        // bytes per symbol) and two staged stream bytes in hand
-        // A normalised state decodes to at least x >> 11 >= 2^12, so two
-        // bytes always renormalise it: the state stays normalised through
-        // the stretch and m steps need no checks.
+        // Fast stretch: a normalised state (x >= L) decodes to at least
+        // x >> 11 >= 2^12, so at most two bytes renormalise it; with two
+        // staged bytes per step in hand the state stays normalised through
+        // the stretch and needs no checks.  One byte is taken when the
+        // decoded x1 < 2^23, a second when (x1 << 8 | b0) < 2^23, i.e.
+        // x1 < 2^15.
         if (x >= kRansL) {
-          uint32_t m = end - k < kRansRound - n ? end - k : kRansRound - n;
-          if (q + 2 <= qlim && (qlim - q) / 2 < m) m = (qlim - q) / 2;
-          if (q + 2 > qlim) m = 0;
-          auto step = [&]() {
-            const uint32_t idx = x & (kRansScale - 1);
-            const uint32_t e = table32[idx];
-            const uint32_t b0 = buf[q - qb], b1 = buf[q - qb + 1];
-            g_st<uint8_t>(out + k, (uint8_t)(e & 0xFF));
-            x = ((e >> 8) & 0xFFF) * (x >> kRansProbBits) + idx - (e >> 20);
-            // one byte when x < L = 2^23, a second when (x << 8 | b0) < L,
-            // i.e. x < 2^15: both tests on the decoded state
-            const bool n1 = x < kRansL, n2 = x < (kRansL >> 8);
-            const uint32_t x1 = (x << 8) | b0;
-            x = n2 ? (x1 << 8) | b1 : n1 ? x1 : x;
-            q += (uint32_t)n1 + (uint32_t)n2;
-            ++k;
-          };
+          uint32_t m = min(end - k, kRansRound - n);
+          m = min(m, (avail - min(q, avail)) / 2);
           n += m;
-          for (; m >= 2; m -= 2) {
-            step();
-            step();
+          // Straight-line step: the bytes renormalising x1 are its leading
+          // zero count rounded down to whole bytes (clz(x1) - 1 in 1..18 for
+          // x1 in [2^12, 2^31)), shifted in from the top of the next two
+          // stream bytes in one 64-bit shift.  qb is the ring read position
+          // in bits.
+          uint32_t qb = 8 * (q + my_off);
+          auto step = [&]() -> uint32_t {
+            const uint32_t idx = x & (kRansScale - 1);
+            const uint2 e = table64[idx];
+            uint16_t b01;
+            __builtin_memcpy(&b01, my_ring + __builtin_amdgcn_ubfe(qb, 3, 11), 2);
+            const uint32_t x1 = __umul24(e.x, x >> kRansProbBits) + e.y;
+            const uint32_t sh = ((uint32_t)__builtin_clz(x1) - 1u) & ~7u;
+            // [b0 b1 0 0] from the top byte down
+            const uint32_t w = __builtin_amdgcn_perm(0u, (uint32_t)b01, 0x00010C0Cu);
+            x = (uint32_t)(((((uint64_t)x1 << 32) | w) << sh) >> 32);
+            qb += sh;
+            return e.x;
+          };
+          // single steps up to a 4-byte aligned output address, then whole
+          // output words of four symbols, then single steps
+          for (; m && ((out + k) & 3u); --m, ++k) g_st<uint8_t>(out + k, (uint8_t)(step() >> 24));
+          for (; m >= 4; m -= 4, k += 4) {
+            // the symbols are the entries' top bytes: [a3 b3 d3 f3], low byte first
+            const uint32_t a = step(), b = step(), d = step(), f = step();
+            const uint32_t w = __builtin_amdgcn_perm(b, a, 0x0C0C0703u) | __builtin_amdgcn_perm(f, d, 0x07030C0Cu);
+            g_st<uint32_t>(out + k, w);
           }
-          if (m) step();
+          for (; m; --m, ++k) g_st<uint8_t>(out + k, (uint8_t)(step() >> 24));
+          q = qb / 8 - my_off;
         }
         // here pending is false: the last symbol's renormalisation is complete
         if (k == end) { done = true; break; }
         if (n >= kRansRound) break;
-        // one careful symbol (unnormalised start, or the stage's last bytes)
+        // one careful symbol (unnormalised start, or the staged bytes' end)
         const uint32_t idx = x & (kRansScale - 1);
-        const uint32_t e = table32[idx];
-        g_st<uint8_t>(out + k, (uint8_t)(e & 0xFF));
-        x = ((e >> 8) & 0xFFF) * (x >> kRansProbBits) + idx - (e >> 20);
+        const uint2 e = table64[idx];
+        g_st<uint8_t>(out + k, (uint8_t)(e.x >> 24));
+        x = __umul24(e.x, x >> kRansProbBits) + e.y;
         ++k;
         ++n;
         pending = true;
       }
     }
+    if (!any) break;
+    // this round's granules into the rings (after the decode: their slots
+    // held bytes consumed before the round began)
+    if (g0 < upto) {
+      *reinterpret_cast<u32x4*>(&ring[sc][(16 * g0) & (kRansRing - 1)]) = v0;
+      if (((16 * g0) & (kRansRing - 1)) == 0) *reinterpret_cast<u32x4*>(&ring[sc][kRansRing]) = v0;
+    }
+    if (g1 < upto) {
+      *reinterpret_cast<u32x4*>(&ring[sc][(16 * g1) & (kRansRing - 1)]) = v1;
+      if (((16 * g1) & (kRansRing - 1)) == 0) *reinterpret_cast<u32x4*>(&ring[sc][kRansRing]) = v1;
+    }
+    s_staged = max(s_staged, upto);
     __syncthreads();
   }
   if (lane < 4 && !good) atomicOr(&h.err, 1u);
   __syncthreads();
   if (lane == 0) status[blockIdx.x] = h.err ? kStBadStream : kStOk;
+  }
 }
 
 hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
                                SyncStream* sync_streams, uint16_t* sync_tables, uint64_t* copy_src,
                                hipStream_t stream) {
   if (n_jobs == 0) return hipSuccess;
-  hipLaunchKernelGGL(decode_exact_kernel, dim3(n_jobs), dim3(64), 0, stream, jobs_dev, status_dev, sync_streams,
+  hipLaunchKernelGGL(decode_exact_kernel<false>, dim3(n_jobs), dim3(64), 0, stream, jobs_dev, status_dev, sync_streams,
                      sync_tables, copy_src);
+  return hipGetLastError();
+}
+
+hipError_t launch_rans_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs, uint64_t* copy_src,
+                             hipStream_t stream) {
+  if (n_jobs == 0) return hipSuccess;
+  hipLaunchKernelGGL(decode_exact_kernel<true>, dim3(n_jobs), dim3(64), 0, stream, jobs_dev, status_dev, nullptr,
+                     nullptr, copy_src);
   return hipGetLastError();
 }
 

@@ -53,6 +53,10 @@ hipError_t launch_zstd_decode(const DecodeJob* jobs_dev, uint32_t* status_dev, u
 // per job, jobs of other codecs are left to the other kernels.  A job's
 // state: its chunk frame's, else pad[0..1] = state address, pad[2] = state
 // length | format version << 24; pad[3] = the plane's row length (0 Flat).
+// The reference rANS jobs of the list (decode_exact.hip; the other codecs'
+// jobs are launch_decode_exact's).
+hipError_t launch_rans_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs, uint64_t* copy_src,
+                             hipStream_t stream);
 hipError_t launch_o1sac_decode(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs, hipStream_t stream);
 
 }  // namespace ptwm

@@ -460,6 +460,9 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   bool any_zstd = false;
   for (size_t j = 0; j < n_jobs; ++j) any_zstd |= hj[j].codec == kCodecZstd;
   if (any_zstd) PTWM_HIP_TRY(launch_zstd_decode(d_jobs, status, (uint32_t)n_jobs, s));
+  bool any_rans = false;
+  for (size_t j = 0; j < n_jobs; ++j) any_rans |= hj[j].codec == kCodecRans;
+  if (any_rans) PTWM_HIP_TRY(launch_rans_exact(d_jobs, status, (uint32_t)n_jobs, d_copy_src, s));
   bool any_o1sac = false;
   for (size_t j = 0; j < n_jobs; ++j) any_o1sac |= hj[j].codec == kCodecO1sac;
   if (any_o1sac) PTWM_HIP_TRY(launch_o1sac_decode(d_jobs, status, (uint32_t)n_jobs, s));
