@@ -460,9 +460,19 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   bool any_zstd = false;
   for (size_t j = 0; j < n_jobs; ++j) any_zstd |= hj[j].codec == kCodecZstd;
   if (any_zstd) PTWM_HIP_TRY(launch_zstd_decode(d_jobs, status, (uint32_t)n_jobs, s));
+  // reference rANS payloads are a few long serial chains: they run on the
+  // side stream while this stream decodes everything else
   bool any_rans = false;
   for (size_t j = 0; j < n_jobs; ++j) any_rans |= hj[j].codec == kCodecRans;
-  if (any_rans) PTWM_HIP_TRY(launch_rans_exact(d_jobs, status, (uint32_t)n_jobs, d_copy_src, s));
+  if (any_rans) {
+    PTWM_HIP_TRY(ctx.ensure_side());
+    PTWM_HIP_TRY(hipEventRecord(ctx.side_fork, s));
+    PTWM_HIP_TRY(hipStreamWaitEvent(ctx.side_stream, ctx.side_fork, 0));
+    // (stored-bytes payloads of rANS jobs are copied by that kernel itself:
+    // raw_copy_kernel on this stream does not wait for the side stream)
+    PTWM_HIP_TRY(launch_rans_exact(d_jobs, status, (uint32_t)n_jobs, nullptr, ctx.side_stream));
+    PTWM_HIP_TRY(hipEventRecord(ctx.side_join, ctx.side_stream));
+  }
   bool any_o1sac = false;
   for (size_t j = 0; j < n_jobs; ++j) any_o1sac |= hj[j].codec == kCodecO1sac;
   if (any_o1sac) PTWM_HIP_TRY(launch_o1sac_decode(d_jobs, status, (uint32_t)n_jobs, s));
@@ -501,6 +511,7 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
       PTWM_HIP_TRY(hipGetLastError());
     }
   }
+  if (any_rans) PTWM_HIP_TRY(hipStreamWaitEvent(s, ctx.side_join, 0));
   uint32_t* hs = static_cast<uint32_t*>(ctx.h_status.ptr);
   PTWM_HIP_TRY(hipMemcpyAsync(hs, status, n_jobs * 4, hipMemcpyDeviceToHost, s));
   PTWM_HIP_TRY(hipStreamSynchronize(s));

@@ -237,32 +237,131 @@ __global__ void __launch_bounds__(256) ref_huf_pack_kernel(const RefSegDev* __re
 // rANS: one lane encodes one segment backward (encode_stream_into,
 // rans/compress.rs:140-185) into its scratch area: [x_final u32 LE][renorm
 // bytes in emission order]; seg_len = 4 + renorm bytes.  Table entries per
-// symbol: {rcp, bias, cmpl | freq << 12 | shift << 24, 0}.
-__global__ void __launch_bounds__(64) ref_rans_kernel(const RefSegDev* __restrict__ segs, uint32_t n_segs,
-                                                      const uint4* __restrict__ tables, uint8_t* __restrict__ scratch,
-                                                      unsigned long long* __restrict__ seg_len) {
-  const uint32_t s = blockIdx.x * 64u + threadIdx.x;
+// symbol: {rcp, bias, cmpl | shift << 24, freq << 20}.
+//
+// The state chain is serial by the format, so a step is kept short:
+// - the segment's symbols arrive as 16-byte aligned blocks, walked from the
+//   last to the first, each loaded four blocks ahead (a step takes exactly
+//   one symbol, so the schedule is fixed; aligned blocks that hold a byte of
+//   the segment never cross a page, so reading them whole is in bounds);
+// - the tables of the workgroup's jobs sit in LDS, and a block's sixteen
+//   entries, which depend on its symbols only, are read before its steps;
+// - x sheds its low byte while x >= freq << 20 (at most twice): both tests
+//   and both shifts run side by side, and the two low bytes of x go to the
+//   lane's LDS output buffer every step (a byte not shed is overwritten by
+//   the next step's); the buffer's whole words go to the scratch after each
+//   block as a fixed nine word stores.
+constexpr uint32_t kRansEncLanes = 64;                    // segments per workgroup
+constexpr uint32_t kRansEncJobs = kRansEncLanes / 4 + 1;  // job tables a workgroup can span
+constexpr uint32_t kRansEncOut = 48;                      // output buffer bytes per lane (3 + 32, words)
+constexpr uint64_t kRansEncSlack = 64;                    // scratch bytes past a segment's stream the flush may write
+
+__global__ void __launch_bounds__(kRansEncLanes) ref_rans_kernel(const RefSegDev* __restrict__ segs, uint32_t n_segs,
+                                                                 const uint4* __restrict__ tables,
+                                                                 uint8_t* __restrict__ scratch,
+                                                                 unsigned long long* __restrict__ seg_len) {
+  __shared__ uint4 tab[kRansEncJobs][257];  // + the identity entry
+  __shared__ __align__(16) uint8_t obuf[kRansEncLanes * kRansEncOut];
+  const uint32_t s0 = blockIdx.x * kRansEncLanes, lane = threadIdx.x;
+  const uint32_t s = s0 + lane;
+  const uint32_t last = min(n_segs, s0 + kRansEncLanes) - 1;
+  // A job's four segments are consecutive, so the workgroup's segments form
+  // runs of one job each (at most kRansEncJobs): run r's table goes to tab[r].
+  const uint32_t job = segs[min(s, last)].table;
+  const uint32_t prev_job = (uint32_t)__shfl_up((int)job, 1, 64);
+  const uint64_t starts = __ballot(lane == 0 || prev_job != job);
+  const uint32_t slot = (uint32_t)__popcll(starts & ((2ull << lane) - 1)) - 1;
+  uint64_t rest = starts;
+  for (uint32_t r = 0; rest; ++r) {
+    const uint32_t at = (uint32_t)__builtin_ctzll(rest);
+    rest &= rest - 1;
+    const uint32_t jr = (uint32_t)__builtin_amdgcn_readlane((int)job, at);
+    for (uint32_t i = lane; i < 256; i += kRansEncLanes) tab[r][i] = tables[256ull * jr + i];
+    // identity: rcp 0, bias 0, cmpl 0, no byte shed below 2^32 - 1
+    if (lane == 0) tab[r][256] = make_uint4(0u, 0u, 0u, 0xFFFFFFFFu);
+  }
+  __syncthreads();
   if (s >= n_segs) return;
   const RefSegDev S = segs[s];
-  const uint64_t tab = reinterpret_cast<uint64_t>(tables + 256u * S.table);
+  const uint4* const T = tab[slot];
   const uint64_t out = reinterpret_cast<uint64_t>(scratch + S.scratch_byte);
+  uint8_t* const ob = obuf + lane * kRansEncOut;
   uint32_t x = kRansL;
-  uint64_t nb = 4;
-  for (uint64_t k = S.n; k > 0; --k) {
-    const u32x4 e = g_ld<u32x4>(tab + 16ull * gbyte(S.src + k - 1));
-    const uint32_t freq = (e.z >> 12) & 0xFFFu;
-    if (freq == 0) {  // a symbol the table does not code: refuse (seg_len 0)
-      seg_len[s] = 0;
-      return;
+  uint64_t nb = 4;  // stream bytes stored after x_final
+  uint32_t E = 0;   // bytes in ob
+  if (S.n) {
+    const uint64_t first = S.src, end = S.src + S.n;  // symbols [first, end)
+    const uint64_t b_lo = first & ~15ull;
+    uint64_t blk = (end - 1) & ~15ull;  // block holding the last symbol
+    // one step (rans/compress.rs:150-167)
+    auto step = [&](const uint4 e) {
+      const bool n1 = x >= e.w, n2 = (x >> 8) >= e.w;
+      const uint32_t xs = n2 ? x >> 16 : n1 ? x >> 8 : x;
+      ob[E] = (uint8_t)x;  // byte stores: a 16-bit LDS store needs an even address
+      ob[E + 1] = (uint8_t)(x >> 8);
+      E += (uint32_t)n1 + (uint32_t)n2;
+      const uint32_t q = __umulhi(xs, e.x) >> (e.z >> 24);
+      x = xs + e.y + __umul24(q, e.z);
+    };
+    // One 16-symbol block, last symbol first.  In the segment's first and
+    // last blocks, positions outside the segment take the identity entry.
+    // Every symbol of the data has a nonzero frequency (the table is
+    // normalised from the same bytes' histogram).
+    auto block = [&](const u32x4 v, uint64_t at) {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      uint4 e[16];
+      if (at >= first && at + 16 <= end) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) e[i] = T[(w[i >> 2] >> (8 * (i & 3))) & 0xFFu];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const uint64_t a = at + (uint64_t)i;
+          e[i] = T[a >= first && a < end ? (w[i >> 2] >> (8 * (i & 3))) & 0xFFu : 256u];
+        }
+      }
+#pragma unroll
+      for (int i = 15; i >= 0; --i) step(e[i]);
+      // whole words of the buffer to the scratch (nine stores: at most 3 + 32
+      // bytes; words past the last whole one are rewritten by later flushes)
+      const uint32_t* o32 = reinterpret_cast<const uint32_t*>(ob);
+#pragma unroll
+      for (int k = 0; k < 9; ++k) g_st<uint32_t>(out + nb + 4 * k, o32[k]);
+      const uint32_t nd = E >> 2;
+      nb += 4 * nd;
+      *reinterpret_cast<uint32_t*>(ob) = o32[nd];
+      E &= 3;
+    };
+    // four blocks in flight, each slot refilled with the block four below
+    // it; every load is issued (below the segment's first block it reads
+    // that block again) so that the wait before a block's use counts the
+    // loads and stores issued after it
+    auto at_or_lo = [&](uint64_t a) { return a >= b_lo + 64 ? a - 64 : b_lo; };
+    u32x4 r0 = g_ld<u32x4>(blk);
+    u32x4 r1 = g_ld<u32x4>(blk >= b_lo + 16 ? blk - 16 : b_lo);
+    u32x4 r2 = g_ld<u32x4>(blk >= b_lo + 32 ? blk - 32 : b_lo);
+    u32x4 r3 = g_ld<u32x4>(blk >= b_lo + 48 ? blk - 48 : b_lo);
+    for (;;) {
+      block(r0, blk);
+      if (blk == b_lo) break;
+      r0 = g_ld<u32x4>(at_or_lo(blk));
+      blk -= 16;
+      block(r1, blk);
+      if (blk == b_lo) break;
+      r1 = g_ld<u32x4>(at_or_lo(blk));
+      blk -= 16;
+      block(r2, blk);
+      if (blk == b_lo) break;
+      r2 = g_ld<u32x4>(at_or_lo(blk));
+      blk -= 16;
+      block(r3, blk);
+      if (blk == b_lo) break;
+      r3 = g_ld<u32x4>(at_or_lo(blk));
+      blk -= 16;
     }
-    const uint32_t max_state = freq << 20;  // ((RANS_L >> PROB_BITS) << 8) * freq
-    while (x >= max_state) {
-      g_st<uint8_t>(out + nb++, (uint8_t)(x & 0xFFu));
-      x >>= 8;
-    }
-    const uint32_t q = __umulhi(x, e.x) >> (e.z >> 24);
-    x = x + e.y + q * (e.z & 0xFFFu);
   }
+  for (uint32_t k = 0; k < E; ++k) g_st<uint8_t>(out + nb + k, ob[k]);
+  nb += E;
   g_st<uint8_t>(out, (uint8_t)x);
   g_st<uint8_t>(out + 1, (uint8_t)(x >> 8));
   g_st<uint8_t>(out + 2, (uint8_t)(x >> 16));
@@ -295,7 +394,8 @@ __global__ void __launch_bounds__(256) ref_copy_kernel(const RefCopyOp* __restri
 
 // ---- host restatements of the reference's table construction ----
 
-// EncSymbol (rans/compress.rs:35-68) packed for ref_rans_kernel.
+// EncSymbol (rans/compress.rs:35-68) packed for ref_rans_kernel:
+// {rcp, bias, cmpl | shift << 24, freq << 20}.
 void rans_encsym(uint32_t start, uint32_t freq, uint32_t out[4]) {
   uint32_t rcp, bias, shift;
   if (freq < 2) {
@@ -311,8 +411,8 @@ void rans_encsym(uint32_t start, uint32_t freq, uint32_t out[4]) {
   }
   out[0] = rcp;
   out[1] = bias;
-  out[2] = (kRansScale - freq) | (freq << 12) | (shift << 24);
-  out[3] = 0;
+  out[2] = (kRansScale - freq) | (shift << 24);  // a 24-bit multiply reads the complement alone
+  out[3] = freq << 20;                            // x at or above it sheds a byte
 }
 
 void split_four(uint64_t len, uint64_t start[4], uint64_t n[4]) {
@@ -419,7 +519,7 @@ int64_t RefEncoder::plan(DevCtx& ctx, const std::vector<RefJob>& jobs, std::vect
       g.table = j;
       if (jobs[j].codec == kCodecRans) {
         g.scratch_byte = rans_scratch;
-        rans_scratch = align_up(rans_scratch + 4 + 2 * sn[i] + 16, 16);
+        rans_scratch = align_up(rans_scratch + 4 + 2 * sn[i] + kRansEncSlack, 16);
       }
       segs_.push_back(g);
     }
@@ -460,7 +560,7 @@ int64_t RefEncoder::plan(DevCtx& ctx, const std::vector<RefJob>& jobs, std::vect
       PTWM_HIP_TRY(ctx.ref_rans_len.ensure(nr * sizeof(unsigned long long)));
       PTWM_HIP_TRY(
           hipMemcpyAsync(ctx.ref_rans_segs.ptr, rsegs.data(), nr * sizeof(RefSegDev), hipMemcpyHostToDevice, s));
-      hipLaunchKernelGGL(ref_rans_kernel, dim3((nr + 63) / 64), dim3(64), 0, s,
+      hipLaunchKernelGGL(ref_rans_kernel, dim3((nr + kRansEncLanes - 1) / kRansEncLanes), dim3(kRansEncLanes), 0, s,
                          static_cast<const RefSegDev*>(ctx.ref_rans_segs.ptr), nr,
                          static_cast<const uint4*>(ctx.ref_rans_tab.ptr),
                          static_cast<uint8_t*>(ctx.ref_rans_scratch.ptr),

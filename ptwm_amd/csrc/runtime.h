@@ -115,6 +115,11 @@ struct DevCtx {
   bool profile = false;
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
   hipEvent_t order_ev = nullptr;  // producer-stream ordering (ptwm_mi355x_stream_wait)
+  // the exact route's reference rANS jobs run on a second stream, beside
+  // its Huffman kernels (forked from and joined back to `stream`)
+  hipStream_t side_stream = nullptr;
+  hipEvent_t side_fork = nullptr, side_join = nullptr;
+  hipError_t ensure_side();
   float last_ms[3] = {0, 0, 0};  // entropy decode, merge, whole call
   hipError_t ensure_events();
   // allocation-free decode: this device's copy of the fixed scratch array

@@ -70,6 +70,22 @@ hipError_t DevCtx::ensure_events() {
   return hipSuccess;
 }
 
+hipError_t DevCtx::ensure_side() {
+  if (!side_stream) {
+    note_alloc();
+    // default priority: mixing stream priorities is avoided on purpose
+    hipError_t e = hipStreamCreateWithFlags(&side_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return e;
+  }
+  for (hipEvent_t* ev : {&side_fork, &side_join})
+    if (!*ev) {
+      note_alloc();
+      hipError_t e = hipEventCreateWithFlags(ev, hipEventDisableTiming);
+      if (e != hipSuccess) return e;
+    }
+  return hipSuccess;
+}
+
 namespace {
 std::mutex g_ctx_mu;
 std::array<std::unique_ptr<DevCtx>, 64> g_ctx;
