@@ -183,6 +183,34 @@ int64_t ptwm_mi355x_container_plan(const uint8_t *file, size_t file_len, uint8_t
                                    size_t *n_tensors, uint64_t *out_len);
 
 /* ABI revision of this library (bumped on any incompatible change). */
+/* Re-serialise a compact container (\x89PTWC, ptwc.rs) or a compact frame
+ * (\x89PTWS, compact.rs) through this library's writer: the file is read
+ * into its sections and records with every field kept and written again
+ * (minimal varints, implicit spine edges, bound Sources, derived header,
+ * index and footer), which gives a file the reference wrote back byte for
+ * byte.  Returns the bytes written, -2 with *out_len set when out_cap is too
+ * small, -1 for a file that does not parse, -5 for another layout.  No
+ * counterpart in the reference: the writer half of container I/O
+ * (ptwc.rs:77-306, tensor_record_compact.rs, compact.rs) behind the ABI. */
+int64_t ptwm_mi355x_container_rewrite(const uint8_t *file, size_t file_len, uint8_t *out, size_t out_cap,
+                                      size_t *out_len);
+
+/* Write a new compact container (\x89PTWC) or, for one tensor with built-in
+ * codecs and no chunks, a compact frame (\x89PTWS), from encoded planes.
+ * `spec` ("PTWW" v1, layout in container_write.cpp) lists the tensors (name,
+ * dtype code, input format, decode-plan chain 1..6, shape, optional XXH64)
+ * and per plane its codec wire id, optional CRC-32 and chunk table, and its
+ * payload's range in `payloads` (host memory).  The chains are the
+ * reference's production graphs, shared through the registry with a bound
+ * Source; this library's codecs (0x7F01 huff_ilv, 0x7F02 rans_ilv) go into
+ * the Extension Table as third-party entries with their canonical ids
+ * (tensor_record_compact.rs:137-153).  Returns the file length, -2 with
+ * *out_len set when out_cap is too small, -1 for a bad spec, -5 for what the
+ * layout cannot store.  No counterpart in the reference's native ABI: the
+ * writer side of ptwc.rs / compact.rs for GPU-encoded planes. */
+int64_t ptwm_mi355x_container_write(const uint8_t *spec, size_t spec_len, const uint8_t *payloads,
+                                    size_t payloads_len, uint8_t *out, size_t out_cap, size_t *out_len);
+
 uint32_t ptwm_mi355x_abi_version(void);
 
 /* The canonical ids this library recognises: which = 0 own plane codec

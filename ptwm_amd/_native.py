@@ -76,6 +76,9 @@ _SIGS = {
         C.c_int64, [_u8p, C.c_size_t, _u8p, C.c_size_t, C.POINTER(C.c_size_t), C.c_void_p, C.c_size_t,
                     C.POINTER(C.c_size_t), C.POINTER(C.c_uint64)]),
     "ptwm_mi355x_device_init": (C.c_int64, [C.c_uint32]),
+    "ptwm_mi355x_container_rewrite": (C.c_int64, [_u8p, C.c_size_t, _u8p, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "ptwm_mi355x_container_write": (
+        C.c_int64, [_u8p, C.c_size_t, _u8p, C.c_size_t, _u8p, C.c_size_t, C.POINTER(C.c_size_t)]),
     "ptwm_mi355x_alloc_calls": (C.c_uint64, []),
     "ptwm_mi355x_set_profiling": (C.c_int64, [C.c_uint32, C.c_uint32]),
     "ptwm_mi355x_last_kernel_ms": (C.c_int64, [C.c_uint32, C.POINTER(C.c_float)]),

@@ -369,3 +369,76 @@ def container_plan(data) -> tuple[bytes, list[ContainerEntry], int]:
     check(rc, "container_plan")
     entries = [ContainerEntry(arr[i], buf) for i in range(n_t.value)]
     return bytes(plan[:plan_len.value]), entries, int(out_len.value)
+
+
+def container_rewrite(data) -> bytes:
+    """Read a compact container (\\x89PTWC) or frame (\\x89PTWS) into its
+    sections and records and write it again through the library's writer
+    (library addition: the writers of ptwc.rs, tensor_record_compact.rs,
+    chain/wire_compact.rs and compact.rs).  A file the reference wrote comes
+    back byte for byte."""
+    buf = bytes(data)
+    L = lib()
+    n = C.c_size_t(0)
+    rc = L.ptwm_mi355x_container_rewrite(buf, len(buf), None, 0, C.byref(n))
+    if rc != RC_BUFFER_TOO_SMALL and rc < 0:
+        check(rc, "container_rewrite")
+    out = (C.c_uint8 * max(n.value, 1))()
+    check(L.ptwm_mi355x_container_rewrite(buf, len(buf), out, n.value, C.byref(n)), "container_rewrite")
+    return bytes(out[:n.value])
+
+
+class WritePlane:
+    """One encoded plane for ``container_write``: codec wire id, payload bytes
+    (host), optional CRC-32 of the plane and chunk table [(offset, size)]."""
+
+    def __init__(self, codec: int, payload, crc32=None, chunks=None):
+        self.codec, self.payload, self.crc32, self.chunks = codec, bytes(payload), crc32, chunks
+
+
+class WriteTensor:
+    """One tensor for ``container_write``: name, public dtype code
+    (dtype.rs:79-103), decode-plan chain (plan.CHAIN_*), shape, planes in
+    the chain's plane order, optional XXH64 of the tensor's bytes."""
+
+    def __init__(self, name: str, dtype_code: int, chain: int, shape, planes, xxh64=None, input_format: int = 2):
+        self.name, self.dtype_code, self.chain, self.shape = name, dtype_code, chain, list(shape)
+        self.planes, self.xxh64, self.input_format = planes, xxh64, input_format
+
+
+def container_write(tensors, layout: str = "compact") -> bytes:
+    """Write the tensors and their encoded planes as a compact container
+    (\\x89PTWC) or, for one tensor, a compact frame (\\x89PTWS) through
+    ptwm_mi355x_container_write."""
+    import struct
+
+    spec = bytearray(struct.pack("<IHHI", 0x57575450, 1, 1 if layout == "compact" else 2, len(tensors)))
+    blob = bytearray()
+    for t in tensors:
+        nm = t.name.encode()
+        spec += struct.pack("<H", len(nm)) + nm
+        spec += struct.pack("<HBBB", t.dtype_code, t.input_format, t.chain, len(t.shape))
+        spec += b"".join(struct.pack("<Q", d) for d in t.shape)
+        spec += struct.pack("<B", 1 if t.xxh64 is not None else 0)
+        if t.xxh64 is not None:
+            spec += struct.pack("<Q", t.xxh64)
+        spec += struct.pack("<B", len(t.planes))
+        for p in t.planes:
+            fl = (1 if p.crc32 is not None else 0) | (2 if p.chunks is not None else 0)
+            spec += struct.pack("<HB", p.codec, fl)
+            if p.crc32 is not None:
+                spec += struct.pack("<I", p.crc32)
+            spec += struct.pack("<QQ", len(blob), len(p.payload))
+            blob += p.payload
+            if p.chunks is not None:
+                spec += struct.pack("<I", len(p.chunks)) + b"".join(struct.pack("<II", a, b) for a, b in p.chunks)
+    L = lib()
+    spec, blob = bytes(spec), bytes(blob)
+    n = C.c_size_t(0)
+    rc = L.ptwm_mi355x_container_write(spec, len(spec), blob, len(blob), None, 0, C.byref(n))
+    if rc != RC_BUFFER_TOO_SMALL and rc < 0:
+        check(rc, "container_write")
+    out = (C.c_uint8 * max(n.value, 1))()
+    check(L.ptwm_mi355x_container_write(spec, len(spec), blob, len(blob), out, n.value, C.byref(n)),
+          "container_write")
+    return bytes(out[:n.value])

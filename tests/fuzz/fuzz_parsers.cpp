@@ -6,6 +6,8 @@
 //                 against the file and the output size it reports
 //   first byte 1: parse_plan over the rest (PTMD state bytes), against
 //                 fixed input and output sizes
+//   first byte 2: ptwm_mi355x_container_rewrite over the rest (PTWC, PTWS);
+//                 what it writes must rewrite to itself and open in the reader
 // A crash, a sanitizer report or a violated invariant ends the run.
 #include <cstdint>
 #include <cstdio>
@@ -42,6 +44,21 @@ extern "C" int LLVMFuzzerTestOneInput(const uint8_t* data, size_t size) {
   } else if (data[0] == 1) {
     ptwm::Plan parsed;
     (void)ptwm::parse_plan(p, n, 1u << 20, 1u << 30, parsed);
+  } else if (data[0] == 2) {
+    size_t len = 0;
+    int64_t rc = ptwm_mi355x_container_rewrite(p, n, nullptr, 0, &len);
+    if (rc != -2) return 0;
+    std::vector<uint8_t> a(len ? len : 1), b(len ? len : 1);
+    if (ptwm_mi355x_container_rewrite(p, n, a.data(), len, &len) != (int64_t)len) std::abort();
+    size_t len2 = 0;
+    if (ptwm_mi355x_container_rewrite(a.data(), len, b.data(), b.size(), &len2) != (int64_t)len || len2 != len ||
+        a != b) {
+      std::fprintf(stderr, "a rewritten file does not rewrite to itself\n");
+      std::abort();
+    }
+    size_t plan_len = 0, n_t = 0;
+    uint64_t out_len = 0;
+    (void)ptwm_mi355x_container_plan(a.data(), len, nullptr, 0, &plan_len, nullptr, 0, &n_t, &out_len);
   }
   return 0;
 }

@@ -6,7 +6,8 @@ tests/fuzz/fuzz_parsers.cpp is a libFuzzer target over the container reader
 UndefinedBehaviorSanitizer by tests/fuzz/Makefile (no device code).  The
 seeds are the reference's golden files and the plans read from them; the
 run must end without a sanitizer report, a crash or a broken invariant (a
-plan the reader writes always parses).
+plan the reader writes always parses; a file the rewriter writes rewrites to
+itself).
 """
 import glob
 import os
@@ -28,12 +29,14 @@ def _seeds(d):
     for p in sorted(glob.glob(os.path.join(HERE, "golden", "ptwm_files", "*"))):
         data = open(p, "rb").read()
         open(os.path.join(d, "f%03d" % k), "wb").write(b"\x00" + data)
+        open(os.path.join(d, "g%03d" % k), "wb").write(b"\x02" + data)
         plan, _, _ = api.container_plan(data)
         open(os.path.join(d, "p%03d" % k), "wb").write(b"\x01" + plan)
         k += 1
     for p in sorted(glob.glob(os.path.join(HERE, "golden", "ptws_frames", "*.body"))):
         frame = b"\x89PTWS" + open(p, "rb").read()
         open(os.path.join(d, "s%03d" % k), "wb").write(b"\x00" + frame)
+        open(os.path.join(d, "w%03d" % k), "wb").write(b"\x02" + frame)
         plan, _, _ = api.container_plan(frame)  # plans with plane ops (the smooth frames)
         open(os.path.join(d, "q%03d" % k), "wb").write(b"\x01" + plan)
         k += 1
