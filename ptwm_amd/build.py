@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "libptwm_mi355x.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["transform.hip", "decode_exact.hip", "decode_sync.hip", "zstd_device.hip", "o1sac_device.hip", "huff_ilv.hip", "rans_ilv.hip", "ilv_host.hip", "rans_host.hip", "huffman_host.cpp", "runtime.hip", "plane_ops.hip",
-           "ref_encode.hip", "integrity.hip", "hash_host.hip", "xxh64_host.cpp", "container.cpp", "container_write.cpp", "plan_parse.cpp", "abi.hip"]
+           "ref_encode.hip", "integrity.hip", "hash_host.hip", "xxh64_host.cpp", "container.cpp", "container_write.cpp", "blake3_host.cpp", "plan_parse.cpp", "abi.hip"]
 
 CFLAGS = [
     "--offload-arch=gfx950",

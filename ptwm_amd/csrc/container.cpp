@@ -40,6 +40,7 @@
 #include <vector>
 
 #include "../../include/ptwm_mi355x.h"
+#include "blake3_host.h"
 #include "dtype_codes.h"
 #include "xxh64_host.h"
 
@@ -920,10 +921,15 @@ int64_t read_legacy(const uint8_t* f, size_t n, std::vector<TensorRec>& out, std
   const uint16_t flags = h.u16();
   if ((flags & 1u) != (ptwx ? 1u : 0u)) return kInvalid;
   const uint64_t et_off = h.u64(), et_len = h.u64();
-  h.take(32);  // BLAKE3 of the Extension Table (not checked here)
+  const uint8_t* et_hash = h.take(32);  // BLAKE3 of the Extension Table section
   const uint64_t ti_off = h.u64(), ti_len = h.u64(), sp_off = h.u64(), sp_len = h.u64();
   const auto in_file = [&](uint64_t o, uint64_t l) { return o <= n && l <= n - o; };
   if (!in_file(et_off, et_len) || !in_file(ti_off, ti_len) || !in_file(sp_off, sp_len)) return kInvalid;
+  if (et_len) {  // container.rs:1299: a table that does not match its hash is refused
+    uint8_t got[32];
+    blake3_hash(f + et_off, (size_t)et_len, got);
+    if (std::memcmp(got, et_hash, 32) != 0) return kInvalid;
+  }
   std::vector<EtEntry> et;
   {
     Rd r(f + et_off, (size_t)et_len);

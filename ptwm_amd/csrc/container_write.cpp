@@ -7,6 +7,12 @@
 //                                tensor_record_compact.rs:1-120 (records),
 //                                chain/wire_compact.rs:1-66 (CW2), prelude.rs
 //   frame             \x89PTWS   compact.rs:1-80 (one tensor)
+//   legacy container  \x89PTWM   container.rs:790-1060 (section order: header,
+//                     \x89PTWX   Extension Table, prelude, chain registry,
+//                                records, index, EOF), header.rs,
+//                                extension/table.rs:144-200, chain/wire.rs:36-130,
+//                                tensor_record.rs:106-240, plane_record.rs:52-110,
+//                                index.rs:18-30
 //
 // A File is what a container holds: for a compact container its Extension
 // Table entries, prelude entries, registry chains and tensor records; for a
@@ -28,7 +34,10 @@
 #include <string>
 #include <vector>
 
+#include <algorithm>
+
 #include "../../include/ptwm_mi355x.h"
+#include "blake3_host.h"
 #include "dtype_codes.h"
 #include "xxh64_host.h"
 
@@ -1031,6 +1040,410 @@ int64_t build_file(int layout, const std::vector<SpecTensor>& spec, const uint8_
   return 0;
 }
 
+// ---- the legacy container ------------------------------------------------------------
+
+struct LegacyChain {  // chain/wire.rs
+  std::vector<uint16_t> op;  // Extension Table index per node
+  std::vector<Bytes> params;
+  struct E {
+    uint8_t src = 0, src_out = 0, dst = 0, dst_in = 0;
+    bool has_role = false;
+    Bytes role;  // Role::write bytes
+    Bytes vendor;
+  };
+  struct T {
+    uint8_t node = 0, out = 0;
+    Bytes role;
+  };
+  std::vector<E> edges;
+  std::vector<T> terms;
+};
+
+struct LegacyPlane {  // plane_record.rs
+  uint8_t role = 0;
+  bool has_cti = true;  // PLANE_FLAG_CODEC_TABLE_IDX (always written by the current writer)
+  uint16_t codec_id = 0, cti = 0;
+  uint8_t state_source = 0, state_version = 0;
+  uint16_t state_info = 0;
+  bool has_crc = false;
+  uint32_t crc = 0;
+  bool chunked = false;
+  std::vector<std::pair<uint32_t, uint32_t>> chunks;
+  Bytes external;  // external state fields, as stored
+  uint8_t layout = 0;
+  uint32_t row_len = 0;
+  Bytes state, payload;
+};
+
+struct LegacyTensor {  // tensor_record.rs
+  uint16_t chain_ref = 0;
+  uint16_t dtype = 0;
+  uint8_t input_format = 0;
+  std::string name;
+  uint64_t orig = 0;
+  bool has_hash = false;
+  uint64_t hash = 0;
+  std::vector<Bytes> inline_et;  // inline chain: its table's entries
+  LegacyChain inline_chain;
+  bool has_deps = false;
+  uint16_t n_deps = 0;
+  Bytes deps;
+  bool has_meta = false;
+  Bytes meta;
+  std::vector<LegacyPlane> planes;
+};
+
+struct LegacyFile {
+  bool ptwx = false;
+  uint16_t flags = 0;
+  std::vector<Bytes> et;  // Extension Table entries, each in the legacy entry layout
+  std::vector<PreludeEntry> prelude;
+  std::vector<std::pair<uint16_t, LegacyChain>> registry;
+  std::vector<LegacyTensor> tensors;  // in file (append) order
+};
+
+const uint8_t kMagicPtwm[9] = {0x89, 'P', 'T', 'W', 'M', '\r', '\n', 0x1A, '\n'};
+const uint8_t kMagicPtwx[9] = {0x89, 'P', 'T', 'W', 'X', '\r', '\n', 0x1A, '\n'};
+constexpr size_t kLegacyHeader = 91;
+
+// one legacy Extension Table entry (extension/table.rs:202-260), kept as its bytes
+bool take_entry(In& r, Bytes& out) {
+  const size_t at = r.o;
+  r.take(32);
+  r.take((size_t)r.le(2));
+  r.le(2);
+  r.le(2);
+  r.u8();
+  r.u8();
+  const uint64_t cl = r.le(4);
+  if (cl > (1u << 20)) return r.ok = false;
+  r.take((size_t)cl);
+  r.u8();
+  r.take((size_t)r.le(2));
+  r.take((size_t)r.le(2));
+  r.le(8);
+  r.le(8);
+  if (!r.ok) return false;
+  out.assign(r.b + at, r.b + r.o);
+  return true;
+}
+bool read_legacy_table(In& r, std::vector<Bytes>& et) {
+  const uint64_t count = r.le(4);
+  if (!r.ok || count > 65536u || count > r.left() / 32) return r.ok = false;
+  et.assign((size_t)count, Bytes());
+  for (Bytes& e : et)
+    if (!take_entry(r, e)) return false;
+  return true;
+}
+void write_legacy_table(const std::vector<Bytes>& et, Bytes& o) {
+  put_le(o, et.size(), 4);
+  for (const Bytes& e : et) put_bytes(o, e);
+}
+
+bool read_legacy_chain(In& r, LegacyChain& c) {
+  c = LegacyChain{};
+  const uint32_t nn = r.u8(), ne = r.u8(), nt = r.u8();
+  const size_t nl = (size_t)r.le(2), el = (size_t)r.le(2), tl = (size_t)r.le(2);
+  In rn(r.take(nl), nl), re(r.take(el), el), rt(r.take(tl), tl);
+  if (!r.ok) return false;
+  for (uint32_t i = 0; i < nn; ++i) {
+    c.op.push_back((uint16_t)rn.le(2));
+    c.params.push_back(rn.bytes(rn.u8()));
+  }
+  for (uint32_t i = 0; i < ne; ++i) {
+    LegacyChain::E e;
+    e.src = re.u8();
+    e.src_out = re.u8();
+    e.dst = re.u8();
+    e.dst_in = re.u8();
+    e.has_role = re.u8() != 0;
+    if (e.has_role) {
+      const size_t at = re.o;
+      if (!take_role(re)) return false;
+      e.role.assign(re.b + at, re.b + re.o);
+    }
+    e.vendor = re.bytes((size_t)re.le(2));
+    c.edges.push_back(std::move(e));
+  }
+  for (uint32_t i = 0; i < nt; ++i) {
+    LegacyChain::T t;
+    t.node = rt.u8();
+    t.out = rt.u8();
+    const size_t at = rt.o;
+    if (!take_role(rt)) return false;
+    t.role.assign(rt.b + at, rt.b + rt.o);
+    c.terms.push_back(std::move(t));
+  }
+  return rn.done() && re.done() && rt.done();
+}
+void write_legacy_chain(const LegacyChain& c, Bytes& o) {  // chain/wire.rs:36-130
+  Bytes nb, eb, tb;
+  for (size_t i = 0; i < c.op.size(); ++i) {
+    put_le(nb, c.op[i], 2);
+    nb.push_back((uint8_t)c.params[i].size());
+    put_bytes(nb, c.params[i]);
+  }
+  for (const auto& e : c.edges) {
+    eb.insert(eb.end(), {e.src, e.src_out, e.dst, e.dst_in, (uint8_t)(e.has_role ? 1 : 0)});
+    put_bytes(eb, e.role);
+    put_le(eb, e.vendor.size(), 2);
+    put_bytes(eb, e.vendor);
+  }
+  for (const auto& t : c.terms) {
+    tb.push_back(t.node);
+    tb.push_back(t.out);
+    put_bytes(tb, t.role);
+  }
+  o.insert(o.end(), {(uint8_t)c.op.size(), (uint8_t)c.edges.size(), (uint8_t)c.terms.size()});
+  put_le(o, nb.size(), 2);
+  put_le(o, eb.size(), 2);
+  put_le(o, tb.size(), 2);
+  put_bytes(o, nb);
+  put_bytes(o, eb);
+  put_bytes(o, tb);
+}
+
+bool read_legacy_plane(In& r, LegacyPlane& p) {
+  p.role = r.u8();
+  const uint8_t fl = r.u8();
+  p.codec_id = (uint16_t)r.le(2);
+  p.has_cti = fl & 4u;
+  if (p.has_cti) p.cti = (uint16_t)r.le(2);
+  p.state_source = r.u8();
+  p.state_version = r.u8();
+  p.state_info = (uint16_t)r.le(2);
+  const size_t isl = (size_t)r.le(4);
+  const uint64_t pl = r.le(8);
+  if (!r.ok || (fl & ~7u)) return false;
+  p.has_crc = fl & 2u;
+  if (p.has_crc) p.crc = (uint32_t)r.le(4);
+  p.chunked = fl & 1u;
+  if (p.chunked) {
+    const uint64_t nc = r.le(4);
+    if (!r.ok || nc > r.left() / 8) return false;
+    p.chunks.resize((size_t)nc);
+    for (auto& c : p.chunks) {
+      c.first = (uint32_t)r.le(4);
+      c.second = (uint32_t)r.le(4);
+    }
+  }
+  if (p.state_source == 3) {
+    const size_t at = r.o;
+    r.u8();
+    const uint8_t rf = r.u8();
+    r.take((size_t)r.le(2));
+    r.u8();
+    if (rf & 1u) r.take(32);
+    if (!r.ok) return false;
+    p.external.assign(r.b + at, r.b + r.o);
+  }
+  p.layout = r.u8();
+  if (p.layout == 1) p.row_len = (uint32_t)r.le(4);
+  else if (p.layout != 0) return false;
+  p.state = r.bytes(isl);
+  if (!r.ok || pl > r.left()) return false;
+  p.payload = r.bytes((size_t)pl);
+  return r.ok;
+}
+void write_legacy_plane(const LegacyPlane& p, Bytes& o) {  // plane_record.rs:52-110
+  o.push_back(p.role);
+  o.push_back((uint8_t)((p.chunked ? 1 : 0) | (p.has_crc ? 2 : 0) | (p.has_cti ? 4 : 0)));
+  put_le(o, p.codec_id, 2);
+  if (p.has_cti) put_le(o, p.cti, 2);
+  o.push_back(p.state_source);
+  o.push_back(p.state_version);
+  put_le(o, p.state_info, 2);
+  put_le(o, p.state.size(), 4);
+  put_le(o, p.payload.size(), 8);
+  if (p.has_crc) put_le(o, p.crc, 4);
+  if (p.chunked) {
+    put_le(o, p.chunks.size(), 4);
+    for (const auto& c : p.chunks) {
+      put_le(o, c.first, 4);
+      put_le(o, c.second, 4);
+    }
+  }
+  put_bytes(o, p.external);
+  o.push_back(p.layout);
+  if (p.layout == 1) put_le(o, p.row_len, 4);
+  put_bytes(o, p.state);
+  put_bytes(o, p.payload);
+}
+
+bool read_legacy_record(const uint8_t* p, size_t n, LegacyTensor& t) {
+  In r(p, n);
+  t.chain_ref = (uint16_t)r.le(2);
+  t.dtype = (uint16_t)r.le(2);
+  t.input_format = r.u8();
+  const uint8_t np = r.u8();
+  const uint8_t fl = r.u8();
+  if (r.u8() != 0 || (fl & ~7u)) return false;  // reserved byte, known flags
+  t.orig = r.le(8);
+  const size_t nl = (size_t)r.le(2);
+  const uint8_t* nm = r.take(nl);
+  if (!r.ok) return false;
+  t.name.assign(reinterpret_cast<const char*>(nm), nl);
+  const uint8_t* pad = r.take((4 - nl % 4) % 4);
+  for (size_t i = 0; pad && i < (4 - nl % 4) % 4; ++i)
+    if (pad[i]) return false;
+  t.has_hash = fl & 4u;
+  if (t.has_hash) t.hash = r.le(8);
+  if (t.chain_ref & 0x8000u) {
+    if (!read_legacy_table(r, t.inline_et) || !read_legacy_chain(r, t.inline_chain)) return false;
+  }
+  t.has_deps = fl & 1u;
+  if (t.has_deps) {
+    t.n_deps = (uint16_t)r.le(2);
+    const size_t at = r.o;
+    for (uint32_t i = 0; i < t.n_deps && r.ok; ++i) {
+      r.u8();
+      const uint8_t rf = r.u8();
+      r.take((size_t)r.le(2));
+      if (rf & 1u) r.take(32);
+    }
+    if (!r.ok) return false;
+    t.deps.assign(p + at, p + r.o);
+  }
+  t.has_meta = fl & 2u;
+  if (t.has_meta) t.meta = r.bytes((size_t)r.le(4));
+  t.planes.resize(np);
+  for (LegacyPlane& q : t.planes)
+    if (!read_legacy_plane(r, q)) return false;
+  return r.done();
+}
+void write_legacy_record(const LegacyTensor& t, Bytes& o) {  // tensor_record.rs:119-240
+  put_le(o, t.chain_ref, 2);
+  put_le(o, t.dtype, 2);
+  o.push_back(t.input_format);
+  o.push_back((uint8_t)t.planes.size());
+  o.push_back((uint8_t)((t.has_deps ? 1 : 0) | (t.has_meta ? 2 : 0) | (t.has_hash ? 4 : 0)));
+  o.push_back(0);
+  put_le(o, t.orig, 8);
+  put_le(o, t.name.size(), 2);
+  o.insert(o.end(), t.name.begin(), t.name.end());
+  o.insert(o.end(), (4 - t.name.size() % 4) % 4, 0);
+  if (t.has_hash) put_le(o, t.hash, 8);
+  if (t.chain_ref & 0x8000u) {
+    write_legacy_table(t.inline_et, o);
+    write_legacy_chain(t.inline_chain, o);
+  }
+  if (t.has_deps) {
+    put_le(o, t.n_deps, 2);
+    put_bytes(o, t.deps);
+  }
+  if (t.has_meta) {
+    put_le(o, t.meta.size(), 4);
+    put_bytes(o, t.meta);
+  }
+  for (const LegacyPlane& q : t.planes) write_legacy_plane(q, o);
+}
+
+bool parse_legacy(const uint8_t* f, size_t n, LegacyFile& m) {
+  m = LegacyFile{};
+  if (n < kLegacyHeader + 8 || std::memcmp(f + n - 8, kEof, 8) != 0) return false;
+  m.ptwx = std::memcmp(f, kMagicPtwx, 9) == 0;
+  if (!m.ptwx && std::memcmp(f, kMagicPtwm, 9) != 0) return false;
+  In h(f, kLegacyHeader);
+  h.take(9);
+  m.flags = (uint16_t)h.le(2);
+  const uint64_t et_off = h.le(8), et_len = h.le(8);
+  h.take(32);
+  const uint64_t ti_off = h.le(8), ti_len = h.le(8), sp_off = h.le(8), sp_len = h.le(8);
+  // the writer's section order: the table right after the header, the
+  // prelude right after the table, then the records, the index and EOF
+  if (!h.ok || et_off != kLegacyHeader || et_len > n || sp_off != et_off + et_len || sp_len > n - sp_off ||
+      ti_off < sp_off + sp_len || ti_len > n || ti_off + ti_len + 8 != n)
+    return false;
+  {
+    In r(f + et_off, (size_t)et_len);
+    if (!read_legacy_table(r, m.et) || !r.done()) return false;
+  }
+  In sp(f + sp_off, (size_t)sp_len);
+  {
+    const size_t at = sp.o;
+    const uint64_t pc = sp.le(4);
+    if (!sp.ok || pc > sp.left() / 22) return false;
+    for (uint64_t i = 0; i < pc && sp.ok; ++i) {  // prelude.rs: fixed fields, name, pad, state
+      sp.take(16);
+      const size_t nl = (size_t)sp.le(2);
+      sp.take(nl + (4 - nl % 4) % 4);
+      sp.take((size_t)sp.le(4));
+    }
+    if (!sp.ok || !read_prelude(f + sp_off + at, sp.o - at, m.prelude)) return false;
+  }
+  const uint64_t nc = sp.le(2);
+  for (uint64_t i = 0; i < nc && sp.ok; ++i) {
+    const uint16_t id = (uint16_t)sp.le(2);
+    LegacyChain c;
+    if (!read_legacy_chain(sp, c)) return false;
+    m.registry.emplace_back(id, std::move(c));
+  }
+  if (!sp.done()) return false;
+  In ix(f + ti_off, (size_t)ti_len);
+  const uint64_t cnt = ix.le(8);
+  if (!ix.ok || cnt > ix.left() / 24) return false;
+  std::vector<std::pair<uint64_t, uint64_t>> recs((size_t)cnt);
+  for (auto& rc : recs) {
+    ix.le(8);
+    rc.first = ix.le(8);
+    rc.second = ix.le(8);
+  }
+  if (!ix.done()) return false;
+  std::sort(recs.begin(), recs.end());
+  uint64_t at = sp_off + sp_len;
+  for (const auto& rc : recs) {  // records back to back between the prelude and the index
+    if (rc.first != at || rc.second > ti_off - at) return false;
+    LegacyTensor t;
+    if (!read_legacy_record(f + rc.first, (size_t)rc.second, t)) return false;
+    m.tensors.push_back(std::move(t));
+    at += rc.second;
+  }
+  return at == ti_off;
+}
+
+void write_legacy(const LegacyFile& m, Bytes& out) {
+  Bytes et, sp, body, index;
+  write_legacy_table(m.et, et);
+  write_prelude(m.prelude, sp);
+  put_le(sp, m.registry.size(), 2);
+  for (const auto& rc : m.registry) {
+    put_le(sp, rc.first, 2);
+    write_legacy_chain(rc.second, sp);
+  }
+  const uint64_t body0 = kLegacyHeader + et.size() + sp.size();
+  std::vector<std::array<uint64_t, 3>> ent;  // (name hash, offset, length)
+  for (const LegacyTensor& t : m.tensors) {
+    const size_t at = body.size();
+    write_legacy_record(t, body);
+    Xxh64 x;
+    x.reset();
+    x.update(reinterpret_cast<const uint8_t*>(t.name.data()), t.name.size());
+    ent.push_back({x.digest(), body0 + at, body.size() - at});
+  }
+  std::stable_sort(ent.begin(), ent.end(), [](const auto& a, const auto& b) { return a[0] < b[0]; });
+  put_le(index, ent.size(), 8);
+  for (const auto& e : ent)
+    for (uint64_t v : e) put_le(index, v, 8);
+  // header (header.rs): magic, flags, table offset / length / BLAKE3, index
+  // offset / length, prelude offset / length (prelude and registry)
+  out.assign(m.ptwx ? kMagicPtwx : kMagicPtwm, (m.ptwx ? kMagicPtwx : kMagicPtwm) + 9);
+  put_le(out, m.flags, 2);
+  put_le(out, kLegacyHeader, 8);
+  put_le(out, et.size(), 8);
+  uint8_t hash[32] = {0};
+  if (!et.empty()) blake3_hash(et.data(), et.size(), hash);
+  put_bytes(out, hash, 32);
+  put_le(out, body0 + body.size(), 8);
+  put_le(out, index.size(), 8);
+  put_le(out, kLegacyHeader + et.size(), 8);
+  put_le(out, sp.size(), 8);
+  put_bytes(out, et);
+  put_bytes(out, sp);
+  put_bytes(out, body);
+  put_bytes(out, index);
+  put_bytes(out, kEof, 8);
+}
+
 }  // namespace cw
 
 // Re-serialise a compact container or frame through the writer: the file is
@@ -1045,6 +1458,12 @@ int64_t container_rewrite(const uint8_t* f, size_t n, std::vector<uint8_t>& out)
   if (n >= 5 && std::memcmp(f, cw::kMagicPtws, 5) == 0) {
     if (!cw::parse_ptws(f, n, m)) return -1;
     cw::write_ptws(m, out);
+    return 0;
+  }
+  if (n >= 9 && (std::memcmp(f, cw::kMagicPtwm, 9) == 0 || std::memcmp(f, cw::kMagicPtwx, 9) == 0)) {
+    cw::LegacyFile lm;
+    if (!cw::parse_legacy(f, n, lm)) return -1;
+    cw::write_legacy(lm, out);
     return 0;
   }
   return -5;

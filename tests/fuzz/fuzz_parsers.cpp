@@ -6,7 +6,8 @@
 //                 against the file and the output size it reports
 //   first byte 1: parse_plan over the rest (PTMD state bytes), against
 //                 fixed input and output sizes
-//   first byte 2: ptwm_mi355x_container_rewrite over the rest (PTWC, PTWS);
+//   first byte 2: ptwm_mi355x_container_rewrite over the rest (PTWC, PTWS,
+//                 PTWM / PTWX);
 //                 what it writes must rewrite to itself and open in the reader
 // A crash, a sanitizer report or a violated invariant ends the run.
 #include <cstdint>

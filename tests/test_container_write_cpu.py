@@ -1,11 +1,16 @@
 """The library's container writers on the CPU (no GPU).
 
-- Round trips: every compact container (\\x89PTWC) and compact frame
-  (\\x89PTWS) the reference wrote (tests/golden: the fuzz corpus files and
-  the 28 frames of its compact-frame tests) is read into its sections and
-  records and written again through the writer (ptwc.rs, extension/
-  compact_table.rs, tensor_record_compact.rs, chain/wire_compact.rs,
-  compact.rs), and comes back byte for byte.  The writer recomputes the
+- Round trips: every compact container (\\x89PTWC), compact frame
+  (\\x89PTWS) and legacy container (\\x89PTWM) the reference wrote
+  (tests/golden: the fuzz corpus files, the legacy files of its
+  compatibility tests and the 28 frames of its compact-frame tests) is read
+  into its sections and records and written again through the writer
+  (ptwc.rs, extension/compact_table.rs, tensor_record_compact.rs,
+  chain/wire_compact.rs, compact.rs; container.rs:790-1060, header.rs,
+  tensor_record.rs, plane_record.rs, chain/wire.rs, index.rs), and comes
+  back byte for byte.  The legacy header's Extension Table hash is BLAKE3
+  recomputed by the writer; the reader refuses a table that does not match
+  it (container.rs:1299).  The writer recomputes the
   header lengths and meta_xxh64, the registry, the index and the footer,
   and re-decides the implicit spine edges, bound Sources and the frame's
   stored orig_size, so a wrong rule shows as a byte difference.
@@ -33,6 +38,7 @@ import plan_oracle
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 COMPACT = sorted(glob.glob(os.path.join(HERE, "golden", "ptwm_files", "ptwc_*")))
+LEGACY = sorted(glob.glob(os.path.join(HERE, "golden", "ptwm_files", "legacy_*")))
 FRAMES = sorted(glob.glob(os.path.join(HERE, "golden", "ptws_frames", "*.body")))
 
 # public dtype codes (dtype.rs:79-103)
@@ -49,6 +55,35 @@ def test_compact_container_round_trip(path):
 def test_frame_round_trip(path):
     data = b"\x89PTWS" + open(path, "rb").read()
     assert api.container_rewrite(data) == data
+
+
+@pytest.mark.parametrize("path", LEGACY, ids=[os.path.basename(p) for p in LEGACY])
+def test_legacy_container_round_trip(path):
+    data = open(path, "rb").read()
+    assert api.container_rewrite(data) == data
+
+
+def test_legacy_header_hash_is_blake3_of_the_table():
+    assert LEGACY
+    for path in LEGACY:
+        data = open(path, "rb").read()
+        et_off, et_len = (int.from_bytes(data[k:k + 8], "little") for k in (11, 19))
+        assert et_off == 91 and et_len > 0
+        assert data[27:59] == O.blake3(data[et_off:et_off + et_len]), path
+
+
+def test_legacy_reader_refuses_a_table_that_misses_its_hash():
+    data = open(LEGACY[0], "rb").read()
+    api.container_plan(data)
+    for at in (91 + 4, 91 + 40):  # a byte of the table's first entry (canonical id, label)
+        bad = bytearray(data)
+        bad[at] ^= 0xFF
+        with pytest.raises(Exception):
+            api.container_plan(bytes(bad))
+    bad = bytearray(data)
+    bad[30] ^= 1  # the stored hash itself
+    with pytest.raises(Exception):
+        api.container_plan(bytes(bad))
 
 
 def test_rewrite_rejects_a_broken_file():
