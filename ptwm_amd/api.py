@@ -349,22 +349,35 @@ class ContainerEntry:
                 f"status={self.status}, out_offset={self.out_offset})")
 
 
+def _host_buf(data):
+    """(pointer argument, length, object to keep alive) of host bytes
+    (bytes, bytearray, memoryview or a numpy array), without a copy."""
+    if isinstance(data, bytes):
+        return data, len(data), data
+    import numpy as np
+
+    a = data.reshape(-1).view(np.uint8) if isinstance(data, np.ndarray) else np.frombuffer(data, np.uint8)
+    a = np.ascontiguousarray(a)
+    return C.c_void_p(int(a.ctypes.data) if a.size else None), int(a.size), a
+
+
 def container_plan(data) -> tuple[bytes, list[ContainerEntry], int]:
     """Read a .ptwm container (legacy or PTWC) or a PTWS frame held in host
-    memory (library addition: the reference-side plan construction of
-    container.rs:1590-1892 / compact.rs:407-480).  Returns the PTMD plan
-    whose payload offsets index ``data``, the tensors in record order, and
-    the output buffer length the plan restores into."""
-    buf = bytes(data)
+    memory (bytes or a numpy uint8 array; library addition: the
+    reference-side plan construction of container.rs:1590-1892 /
+    compact.rs:407-480).  Returns the PTMD plan whose payload offsets index
+    ``data``, the tensors in record order, and the output buffer length the
+    plan restores into."""
+    ptr, size, buf = _host_buf(data)
     L = lib()
     plan_len, n_t, out_len = C.c_size_t(0), C.c_size_t(0), C.c_uint64(0)
-    rc = L.ptwm_mi355x_container_plan(buf, len(buf), None, 0, C.byref(plan_len), None, 0, C.byref(n_t),
+    rc = L.ptwm_mi355x_container_plan(ptr, size, None, 0, C.byref(plan_len), None, 0, C.byref(n_t),
                                       C.byref(out_len))
     if rc != RC_BUFFER_TOO_SMALL and rc < 0:
         check(rc, "container_plan")
     plan = (C.c_uint8 * max(plan_len.value, 1))()
     arr = (_native.ContainerTensor * max(n_t.value, 1))()
-    rc = L.ptwm_mi355x_container_plan(buf, len(buf), plan, plan_len.value, C.byref(plan_len), arr, n_t.value,
+    rc = L.ptwm_mi355x_container_plan(ptr, size, plan, plan_len.value, C.byref(plan_len), arr, n_t.value,
                                       C.byref(n_t), C.byref(out_len))
     check(rc, "container_plan")
     entries = [ContainerEntry(arr[i], buf) for i in range(n_t.value)]
@@ -389,11 +402,14 @@ def container_rewrite(data) -> bytes:
 
 
 class WritePlane:
-    """One encoded plane for ``container_write``: codec wire id, payload bytes
-    (host), optional CRC-32 of the plane and chunk table [(offset, size)]."""
+    """One encoded plane for ``container_write``: codec wire id, payload
+    (host bytes, or an (offset, length) span of the ``payloads`` buffer
+    given to ``container_write``), optional CRC-32 of the plane and chunk
+    table [(offset, size)]."""
 
     def __init__(self, codec: int, payload, crc32=None, chunks=None):
-        self.codec, self.payload, self.crc32, self.chunks = codec, bytes(payload), crc32, chunks
+        self.codec, self.crc32, self.chunks = codec, crc32, chunks
+        self.payload = tuple(int(v) for v in payload) if isinstance(payload, tuple) else bytes(payload)
 
 
 class WriteTensor:
@@ -406,12 +422,19 @@ class WriteTensor:
         self.planes, self.xxh64, self.input_format = planes, xxh64, input_format
 
 
-def container_write(tensors, layout: str = "compact") -> bytes:
+def container_write(tensors, layout: str = "compact", payloads=None, as_array: bool = False):
     """Write the tensors and their encoded planes as a compact container
     (\\x89PTWC) or, for one tensor, a compact frame (\\x89PTWS) through
-    ptwm_mi355x_container_write."""
+    ptwm_mi355x_container_write.  With ``payloads`` (host bytes or a numpy
+    uint8 array) every plane's payload is an (offset, length) span of it,
+    and nothing is copied on the way in; ``as_array`` returns the file as a
+    numpy uint8 array instead of bytes."""
     import struct
 
+    import numpy as np
+
+    if layout not in ("compact", "frame"):
+        raise ValueError(f"container_write: unknown layout {layout!r}")
     spec = bytearray(struct.pack("<IHHI", 0x57575450, 1, 1 if layout == "compact" else 2, len(tensors)))
     blob = bytearray()
     for t in tensors:
@@ -428,17 +451,28 @@ def container_write(tensors, layout: str = "compact") -> bytes:
             spec += struct.pack("<HB", p.codec, fl)
             if p.crc32 is not None:
                 spec += struct.pack("<I", p.crc32)
-            spec += struct.pack("<QQ", len(blob), len(p.payload))
-            blob += p.payload
+            if isinstance(p.payload, tuple) != (payloads is not None):
+                raise ValueError("container_write: give every payload as a span of `payloads`, or none")
+            if payloads is not None:
+                spec += struct.pack("<QQ", *p.payload)
+            else:
+                spec += struct.pack("<QQ", len(blob), len(p.payload))
+                blob += p.payload
             if p.chunks is not None:
                 spec += struct.pack("<I", len(p.chunks)) + b"".join(struct.pack("<II", a, b) for a, b in p.chunks)
     L = lib()
-    spec, blob = bytes(spec), bytes(blob)
+    spec = bytes(spec)
+    bptr, blen, keep = _host_buf(payloads if payloads is not None else bytes(blob))
     n = C.c_size_t(0)
-    rc = L.ptwm_mi355x_container_write(spec, len(spec), blob, len(blob), None, 0, C.byref(n))
-    if rc != RC_BUFFER_TOO_SMALL and rc < 0:
-        check(rc, "container_write")
-    out = (C.c_uint8 * max(n.value, 1))()
-    check(L.ptwm_mi355x_container_write(spec, len(spec), blob, len(blob), out, n.value, C.byref(n)),
-          "container_write")
-    return bytes(out[:n.value])
+    cap = blen + 2 * len(spec) + 65536  # enough for the file: payloads plus overheads of the spec's size
+    while True:
+        out = np.empty(cap, np.uint8)
+        rc = L.ptwm_mi355x_container_write(spec, len(spec), bptr, blen, C.c_void_p(int(out.ctypes.data)), cap,
+                                           C.byref(n))
+        if rc == RC_BUFFER_TOO_SMALL and n.value > cap:
+            cap = n.value
+            continue
+        break
+    check(rc, "container_write")
+    del keep
+    return out[:n.value] if as_array else out[:n.value].tobytes()

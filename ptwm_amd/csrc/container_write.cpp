@@ -1495,6 +1495,7 @@ extern "C" int64_t ptwm_mi355x_container_write(const uint8_t* spec, size_t spec_
   const int64_t rc = build_file(layout, st, payloads, payloads_len, m);
   if (rc < 0) return rc;
   std::vector<uint8_t> o;
+  o.reserve(payloads_len + 2 * spec_len + 65536);  // the payloads plus record overheads of the spec's size
   if (layout == 1) write_ptwc(m, o);
   else write_ptws(m, o);
   *out_len = o.size();

@@ -18,7 +18,7 @@ def _o1sac_plane(data: bytes, p: P.PlanePlan, payload: bytes) -> bytes:
     """Order1ScaleAC: the plane's state (or each chunk frame's own, container.rs:2010-2049)."""
     off, ln, row_len, ver = p.state
     if p.chunks is None:
-        return O.o1sac_decode(data[off:off + ln], payload, p.plane_len, row_len, ver)
+        return O.o1sac_decode(bytes(data[off:off + ln]), payload, p.plane_len, row_len, ver)
     out = b""
     for k, (start, size) in enumerate(p.chunks):
         end = p.chunks[k + 1][0] if k + 1 < len(p.chunks) else len(payload)
@@ -31,7 +31,7 @@ def _o1sac_plane(data: bytes, p: P.PlanePlan, payload: bytes) -> bytes:
 def decode_tensor(data: bytes, t: P.TensorPlan) -> bytes:
     planes = []
     for p in t.planes:
-        payload = data[p.payload_offset:p.payload_offset + p.payload_len]
+        payload = bytes(data[p.payload_offset:p.payload_offset + p.payload_len])  # data: bytes or a uint8 array
         if p.codec == O.CODEC_O1SAC:
             plane = _o1sac_plane(data, p, payload)
         elif p.chunks is not None:

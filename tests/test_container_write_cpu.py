@@ -200,3 +200,31 @@ def test_write_refuses_what_the_layout_cannot_hold():
     dup = write_model(9, False, False)[0]
     with pytest.raises(Exception):
         api.container_write([dup[0], dup[0]])            # duplicate names
+
+
+def test_payload_spans_of_one_buffer_write_the_same_file():
+    """Payloads handed over as spans of one host buffer (how a GPU-encoded
+    model comes back from the device) write the same file, also as an array."""
+    items, raws = write_model(11, True, True)
+    want = api.container_write(items)
+    buf, spans = bytearray(b"\xee" * 13), []
+    for t in items:
+        for p in t.planes:
+            spans.append((len(buf), len(p.payload)))
+            buf += p.payload + b"\xee" * 7  # gaps the spans skip
+    k = 0
+    for t in items:
+        for i, p in enumerate(t.planes):
+            t.planes[i] = api.WritePlane(p.codec, spans[k], p.crc32, p.chunks)
+            k += 1
+    arr = np.frombuffer(bytes(buf), np.uint8)
+    got = api.container_write(items, payloads=arr, as_array=True)
+    assert isinstance(got, np.ndarray) and got.tobytes() == want
+    assert api.container_write(items, payloads=bytes(buf)) == want
+    open_and_decode(got.tobytes(), raws)
+    plan, ents, out_len = api.container_plan(got)  # the reader takes the array as it is
+    plan2, ents2, out_len2 = api.container_plan(want)
+    assert (plan, out_len) == (plan2, out_len2)
+    assert [e.name for e in ents] == [e.name for e in ents2] == [n for n, _ in raws]
+    with pytest.raises(ValueError):
+        api.container_write(items)  # spans without the buffer

@@ -6,11 +6,22 @@ decode verifies them (container.rs:2154-2159 plane CRC, :2185-2194 payload
 hash; emitted by default, python/ptwm/_config.py:177-179).
 
 - every restored tensor equals its input (torch.equal on the device);
-- a sample of tensors is checked against the CPU oracle: each plane payload
-  decoded by the format specification (por_ilv_decode) and merged by the
-  reference's fused inverse (fusion.rs), plane CRC-32 by the oracle's
-  crc32fast restatement, tensor XXH64 by the oracle's xxhash restatement;
-- a plan with one wrong CRC, or one wrong hash, is rejected (-1).
+- one tensor of every shape class (the 1 GiB embedding, attention q/o and
+  k/v, MLP gate/up and down, the norms) is checked against the CPU oracle:
+  each plane payload decoded by the format specification (por_ilv_decode)
+  and merged by the reference's fused inverse (fusion.rs), plane CRC-32 by
+  the oracle's crc32fast restatement, tensor XXH64 by the oracle's xxhash
+  restatement;
+- a plan with one wrong CRC, or one wrong hash, is rejected (-1);
+- the model as a file ("multi-tensor .ptwm container"):
+  the GPU-encoded payloads written by the library's container writer as a
+  compact container (\\x89PTWC, 290 records with shapes, plane CRC-32s and
+  XXH64s), re-opened by ptwm_mi355x_container_plan, restored in one call on
+  the GPU and the shape-class sample decoded from the file by the oracle;
+  the same model encoded on the GPU in the reference's own format (Huffman
+  planes in 256 KiB chunk frames, python/ptwm/_config.py:151), whose
+  payloads equal the oracle's restatement of the reference encoder on the
+  sample, written, re-opened and restored the same way.
 """
 import sys
 
@@ -20,6 +31,9 @@ import pytest
 import bench
 import oracle as O
 from ptwm_amd import api, ids, plan
+
+import file_writer
+import plan_oracle
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -75,9 +89,12 @@ def test_config4_full_model_one_call_crc_and_hash_verified(model):
     note("config 4: 290 tensors restored bit-exact with CRC-32 + XXH64 verified")
 
 
-SAMPLE = ["model.layers.0.self_attn.q_proj.weight", "model.layers.7.self_attn.k_proj.weight",
-          "model.layers.13.input_layernorm.weight", "model.layers.31.post_attention_layernorm.weight",
-          "model.layers.20.mlp.down_proj.weight"]
+# one tensor of every shape class of the model
+SAMPLE = ["model.embed_tokens.weight", "model.layers.0.self_attn.q_proj.weight",
+          "model.layers.7.self_attn.k_proj.weight", "model.layers.13.input_layernorm.weight",
+          "model.layers.31.post_attention_layernorm.weight", "model.layers.20.mlp.down_proj.weight",
+          "model.layers.26.mlp.up_proj.weight", "model.layers.5.self_attn.o_proj.weight"]
+DT_BF16 = 6  # dtype.rs:79-103
 
 
 def test_config4_sampled_tensors_match_oracle(model):
@@ -117,3 +134,93 @@ def test_config4_wrong_integrity_value_rejected(model, what):
     with pytest.raises(api.NativeError) as e:
         dispatch(plan.encode_plan(bad), blob, restored)
     assert e.value.rc == -1
+
+
+def test_sample_covers_every_shape_class():
+    classes = {(tuple(sh), k) for _, sh, k in bench.llama8b_shapes()}
+    by_name = {n: (tuple(sh), k) for n, sh, k in bench.llama8b_shapes()}
+    assert {by_name[n] for n in SAMPLE} == classes
+
+
+def host_np(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def to_device(a):
+    t = torch.empty(max(1, a.size), dtype=torch.uint8, device="cuda:0")
+    t[: a.size].copy_(torch.from_numpy(a))
+    return t[: a.size]
+
+
+def write_and_restore(names, items, entries, payloads, label):
+    """Write the model, re-open the file, restore it on the GPU in one call
+    with every CRC and hash checked; returns the file and its plan."""
+    data = api.container_write(file_writer.write_tensors(entries), payloads=payloads, as_array=True)
+    note(f"config 4 {label}: compact container written, {data.size} bytes")
+    assert data[:9].tobytes() == b"\x89PTWC\r\n\x1a\n"
+    plan_bytes, ents, out_len = api.container_plan(data)
+    assert [e.name for e in ents] == names
+    assert all(e.status == 0 and e.plan_index >= 0 and e.crc_checked and e.hash_checked for e in ents)
+    assert out_len >= R_TOTAL
+    src = to_device(data)
+    restored = torch.zeros(out_len, dtype=torch.uint8, device="cuda:0")
+    assert dispatch(plan_bytes, src, restored) == R_TOTAL
+    for e, (_, raw) in zip(ents, items):
+        assert torch.equal(restored[e.out_offset:e.out_offset + e.orig_size], raw), e.name
+    note(f"config 4 {label}: file re-opened, 290 tensors restored bit-exact, CRC-32 + XXH64 verified")
+    del src, restored
+    return data, plan_bytes, ents
+
+
+def oracle_sample_from_file(names, items, data, plan_bytes, ents, label):
+    tp = plan.decode_plan(plan_bytes)
+    for name in SAMPLE:
+        e = ents[names.index(name)]
+        got = plan_oracle.decode_tensor(data, tp[e.plan_index])  # checks the CRCs and the XXH64 too
+        assert got == host(items[names.index(name)][1]), name
+    note(f"config 4 {label}: shape-class sample decoded from the file by the oracle")
+
+
+def test_config4_as_a_file(model):
+    names, items, blob, plans = model
+    shapes = {n: list(sh) for n, sh, _ in bench.llama8b_shapes()}
+    payloads = host_np(blob)
+    entries = [(n, DT_BF16, shapes[n], t) for n, t in zip(names, plans)]
+    data, plan_bytes, ents = write_and_restore(names, items, entries, payloads, "huff_ilv")
+    del payloads
+    oracle_sample_from_file(names, items, data, plan_bytes, ents, "huff_ilv")
+
+
+def test_config4_reference_format_file(model):
+    names, items, _, plans = model
+    shapes = {n: list(sh) for n, sh, _ in bench.llama8b_shapes()}
+    codecs, chunk = bench.REF_FORMATS["c4"]["w"]
+    cap = R_TOTAL + 65536 * len(items) + (1 << 20)
+    blob = torch.empty(cap, dtype=torch.uint8, device="cuda:0")
+    off, entries = 0, []
+    for name, (chain, raw), p0 in zip(names, items, plans):
+        used, st = api.encode_tensor_ref_cuda(chain, codecs, chunk, raw, blob[off:], 0)
+        t = plan.decode_plan(st)[0]
+        for p, q in zip(t.planes, p0.planes):
+            p.payload_offset += off
+            p.crc32 = q.crc32  # the same planes as the huff_ilv encode's: CRC-32s by plane_crc32_cuda
+        t.xxh64 = p0.xxh64
+        entries.append((name, DT_BF16, shapes[name], t))
+        off = (off + used + 255) // 256 * 256
+    note(f"config 4 reference format: {off} bytes encoded on the GPU")
+    payloads = host_np(blob[:off])
+    del blob
+    # the GPU encoder's payloads are the reference encoder's (oracle restatement)
+    for name in SAMPLE:
+        i = names.index(name)
+        t = entries[i][3]
+        for p, pl in zip(t.planes, O.chain_forward(plan.CHAIN_IEEE16_SPLIT2, host(items[i][1]))):
+            pay, ent = O.encode_plane_chunked(codecs[0], pl, chunk)
+            assert p.codec == codecs[0] and p.crc32 == O.crc32(pl), name
+            assert payloads[p.payload_offset:p.payload_offset + p.payload_len].tobytes() == pay, name
+            assert [tuple(c) for c in p.chunks] == [tuple(int(v) for v in e) for e in ent], name
+    note("config 4 reference format: shape-class sample payloads == oracle encode")
+    data, plan_bytes, ents = write_and_restore(names, items, entries, payloads, "reference format")
+    del payloads
+    oracle_sample_from_file(names, items, data, plan_bytes, ents, "reference format")
