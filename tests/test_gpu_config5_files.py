@@ -52,7 +52,8 @@ def host(t) -> np.ndarray:
 def to_device(a: np.ndarray):
     t = torch.empty(max(1, a.size), dtype=torch.uint8, device="cuda:0")
     if a.size:
-        t[: a.size].copy_(torch.from_numpy(np.ascontiguousarray(a)))
+        a = np.ascontiguousarray(a)
+        t[: a.size].copy_(torch.from_numpy(a if a.flags.writeable else a.copy()))
     return t[: a.size]
 
 
