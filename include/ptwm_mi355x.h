@@ -143,6 +143,15 @@ int64_t ptwm_mi355x_device_init(uint32_t device_ordinal);
  * call allocated nothing. */
 uint64_t ptwm_mi355x_alloc_calls(void);
 
+/* Cumulative counts of this device's reference-format Huffman payloads on
+ * the exact route: out[0] accepted by the parallel decode, out[1] decoded
+ * again by the exact state machine (malformed, or declined by the parallel
+ * path's acceptance check), out[2] calls whose wavefront boundaries needed
+ * more fix passes than the queued ones.  Writes min(n, 3) values, returns 3.
+ * No counterpart in the reference: a caller (or a test) sees which path its
+ * payloads took. */
+int64_t ptwm_mi355x_decode_stats(uint32_t device_ordinal, uint64_t *out, size_t n);
+
 /* One tensor of a container, as ptwm_mi355x_container_plan lists it (in
  * record order, the order the reference's tools list and decode them). */
 typedef struct ptwm_mi355x_container_tensor {

@@ -80,6 +80,7 @@ _SIGS = {
     "ptwm_mi355x_container_write": (
         C.c_int64, [_u8p, C.c_size_t, _u8p, C.c_size_t, _u8p, C.c_size_t, C.POINTER(C.c_size_t)]),
     "ptwm_mi355x_alloc_calls": (C.c_uint64, []),
+    "ptwm_mi355x_decode_stats": (C.c_int64, [C.c_uint32, C.POINTER(C.c_uint64), C.c_size_t]),
     "ptwm_mi355x_set_profiling": (C.c_int64, [C.c_uint32, C.c_uint32]),
     "ptwm_mi355x_last_kernel_ms": (C.c_int64, [C.c_uint32, C.POINTER(C.c_float)]),
     "ptwm_mi355x_split_cuda": (

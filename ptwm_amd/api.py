@@ -293,6 +293,15 @@ def plane_crc32_cuda(chain: int, src, device_ordinal: int = 0) -> list[int]:
     return [int(out[i]) for i in range(n)]
 
 
+def decode_stats(device_ordinal: int = 0) -> dict:
+    """Cumulative path counts of the device's reference-format Huffman
+    payloads (library addition): accepted by the parallel decode, decoded
+    again by the exact state machine, calls that needed extra fix passes."""
+    out = (C.c_uint64 * 3)()
+    check(lib().ptwm_mi355x_decode_stats(device_ordinal, out, 3), "decode_stats")
+    return {"accepted": int(out[0]), "fallbacks": int(out[1]), "extra_rounds": int(out[2])}
+
+
 def xxh64_cuda(src, device_ordinal: int = 0) -> int:
     """XXH64 (seed 0) of the device bytes ``src`` (library addition; the
     tensor payload hash of container.rs:2185-2194)."""

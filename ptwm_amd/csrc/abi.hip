@@ -1046,6 +1046,15 @@ int64_t ptwm_mi355x_device_init(uint32_t device_ordinal) {
 
 uint64_t ptwm_mi355x_alloc_calls(void) { return alloc_calls(); }
 
+int64_t ptwm_mi355x_decode_stats(uint32_t device_ordinal, uint64_t* out, size_t n) {
+  if (n && !out) return kInvalidInput;
+  DeviceScope ds(device_ordinal);
+  if (!ds.ok) return kInvalidInput;
+  const uint64_t v[3] = {ds.ctx->sync_accepted, ds.ctx->sync_fallbacks, ds.ctx->sync_extra_rounds};
+  for (size_t i = 0; i < n && i < 3; ++i) out[i] = v[i];
+  return 3;
+}
+
 int64_t ptwm_mi355x_set_profiling(uint32_t device_ordinal, uint32_t on) {
   DeviceScope ds(device_ordinal);
   if (!ds.ok) return kInvalidInput;

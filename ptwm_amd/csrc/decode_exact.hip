@@ -239,10 +239,12 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
                                                           uint16_t* __restrict__ sync_tables,
                                                           uint64_t* __restrict__ copy_src) {
   __shared__ SharedHeader h;
-  __shared__ uint8_t lengths[256];
   __shared__ uint16_t counts[kHufMaxBits + 1];
   __shared__ uint16_t next_code[kHufMaxBits + 1];
   __shared__ uint16_t rev[256];
+  __shared__ uint16_t sym_base[kHufMaxBits + 1];   // Huffman: first index of each length in sorted_sym
+  __shared__ uint32_t code_end[kHufMaxBits + 1];   // Huffman: end of each length's left-aligned codes
+  __shared__ uint8_t sorted_sym[256];              // Huffman: symbols by (length, symbol)
   // rANS: {freq | sym << 24, slot - start} per slot; tANS: one u32 per slot;
   // Huffman: (len << 8) | sym per window
   __shared__ __align__(16) uint32_t table_mem[(kRans ? 2 : 1) * kRansScale];
@@ -288,64 +290,82 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
   if (h.kind == 1) {
     // ---- weights header (weights.rs:34-85) and tree (tree.rs:87-177) ----
     // The header and jump table (at most 2 + 128 + 16 bytes) are staged in
-    // LDS by the wavefront first: lane 0 parses them from there instead of
-    // issuing its header loads to global memory one after another.
+    // LDS by the wavefront first.  Every lane then reads the header fields
+    // (broadcast LDS reads) and the weights of symbols 4 lane .. 4 lane + 3;
+    // lengths, counts and each symbol's rank among the symbols of its
+    // length come from wave ballots, so the canonical code is built without
+    // a serial pass over the 256 symbols.
     const uint8_t* const genc = enc;
     for (uint32_t i = lane; i < kHdrStage; i += 64) hdr_stage[i] = i < enc_len ? g_ld<uint8_t>((uint64_t)(genc + i)) : 0;
     __syncthreads();
-    if (lane == 0) {
-      const uint8_t* enc = hdr_stage;
-      uint32_t st = kStOk;
-      uint64_t n = 0, hb = 0;
-      if (enc_len == 0 || !(enc[0] & 0x80)) st = kStBadHeader;
-      else if (enc[0] == 0x80) {
+    uint32_t st = kStOk;
+    uint32_t n = 0, hb = 0;
+    {
+      const uint8_t b0 = hdr_stage[0];
+      if (enc_len == 0 || !(b0 & 0x80)) st = kStBadHeader;
+      else if (b0 == 0x80) {
         if (enc_len < 2) st = kStBadHeader;
         else {
-          n = enc[1] ? enc[1] : 256;
+          n = hdr_stage[1] ? hdr_stage[1] : 256;
           hb = 2;
           if (n < 128) st = kStBadHeader;
         }
       } else {
-        n = enc[0] & 0x7F;
+        n = b0 & 0x7F;
         hb = 1;
         if (n == 0) st = kStBadHeader;
       }
       if (st == kStOk && enc_len < hb + (n + 1) / 2) st = kStBadHeader;
-      uint32_t maxb = 0, total = 0;
-      for (int i = 0; i <= kHufMaxBits; ++i) counts[i] = 0;
-      if (st == kStOk) {
-        for (uint64_t i = 0; i < 256; ++i) {
-          uint8_t w = 0;
-          if (i < n) {
-            uint8_t b = enc[hb + i / 2];
-            w = (i % 2 == 0) ? (b & 0x0F) : ((b >> 4) & 0x0F);
-          }
-          if (w > kHufMaxBits) { st = kStBadHeader; break; }
-          lengths[i] = w;
-          if (w) { counts[w]++; total++; if (w > maxb) maxb = w; }
+    }
+    uint32_t w[4] = {0, 0, 0, 0};
+    if (st == kStOk) {
+#pragma unroll
+      for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t i = 4 * lane + k;
+        if (i < n) {
+          const uint8_t b = hdr_stage[hb + i / 2];
+          w[k] = (i % 2 == 0) ? (b & 0x0Fu) : ((b >> 4) & 0x0Fu);
         }
       }
-      if (st == kStOk && total == 0) st = kStBadHeader;
-      if (maxb < 1) maxb = 1;
-      // canonical codes (tree.rs:119-141)
+    }
+    const bool over = w[0] > (uint32_t)kHufMaxBits || w[1] > (uint32_t)kHufMaxBits ||
+                      w[2] > (uint32_t)kHufMaxBits || w[3] > (uint32_t)kHufMaxBits;
+    if (__ballot(over) != 0) st = kStBadHeader;
+    uint32_t maxb = st == kStOk ? std::max(std::max(w[0], w[1]), std::max(w[2], w[3])) : 0u;
+    for (int o = 32; o >= 1; o >>= 1) maxb = std::max(maxb, (uint32_t)__shfl_xor((int)maxb, o, 64));
+    if (st == kStOk && maxb == 0) st = kStBadHeader;  // no symbol has a code
+    if (maxb < 1) maxb = 1;
+    // rank of each of the lane's symbols among the lower symbols of its length
+    uint32_t rank[4] = {0, 0, 0, 0};
+    if (st == kStOk) {
+      const uint64_t below = (1ull << lane) - 1ull;
+      for (uint32_t l = 1; l <= maxb; ++l) {
+        const uint64_t m0 = __ballot(w[0] == l), m1 = __ballot(w[1] == l), m2 = __ballot(w[2] == l),
+                       m3 = __ballot(w[3] == l);
+        const uint32_t r = __popcll(m0 & below) + __popcll(m1 & below) + __popcll(m2 & below) + __popcll(m3 & below);
+        const uint32_t e0 = w[0] == l, e1 = w[1] == l, e2 = w[2] == l;
+        if (w[0] == l) rank[0] = r;
+        if (w[1] == l) rank[1] = r + e0;
+        if (w[2] == l) rank[2] = r + e0 + e1;
+        if (w[3] == l) rank[3] = r + e0 + e1 + e2;
+        if (lane == 0) counts[l] = (uint16_t)(__popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3));
+      }
+    }
+    if (lane == 0) {
+      // canonical codes (tree.rs:119-141): the first code of each length,
+      // with the overflow checks the serial assignment makes; then, per
+      // length, the first index into the symbols sorted by (length,
+      // symbol) and the end of its left-aligned code range
       if (st == kStOk) {
-        uint32_t code = 0;
+        counts[0] = 0;
+        uint32_t code = 0, base = 0;
         for (uint32_t b = 1; b <= maxb; ++b) {
           code = ((code + counts[b - 1]) << 1) & 0xFFFF;
-          if (code > (1u << b)) { st = kStBadHeader; break; }
+          if (code > (1u << b) || (counts[b] && code + counts[b] - 1 >= (1u << b))) { st = kStBadHeader; break; }
           next_code[b] = (uint16_t)code;
-        }
-      }
-      if (st == kStOk) {
-        for (int s = 0; s < 256; ++s) {
-          uint32_t l = lengths[s];
-          if (!l) continue;
-          uint32_t c = next_code[l];
-          if (c >= (1u << l)) { st = kStBadHeader; break; }
-          next_code[l] = (uint16_t)(c + 1);
-          uint32_t rv = 0;
-          for (uint32_t k = 0; k < l; ++k) rv |= ((c >> k) & 1u) << (l - 1 - k);
-          rev[s] = (uint16_t)rv;
+          sym_base[b] = (uint16_t)base;
+          base += counts[b];
+          code_end[b] = (code + counts[b]) << (maxb - b);
         }
       }
       // jump table and segment streams (decompress.rs:14-48)
@@ -354,7 +374,7 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
       if (st == kStOk) {
         uint64_t tot = 0, so = pos + 16;
         for (int i = 0; i < 4; ++i) {
-          h.seg_len[i] = ld_u32le(enc + pos + 4 * i);
+          h.seg_len[i] = ld_u32le(hdr_stage + pos + 4 * i);
           h.seg_src[i] = so;
           so += h.seg_len[i];
           tot += h.seg_len[i];
@@ -369,18 +389,26 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
       if (lane == 0) status[blockIdx.x] = h.status;
       return;
     }
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k)
+      if (w[k]) sorted_sym[sym_base[w[k]] + rank[k]] = (uint8_t)(4 * lane + k);
+    __syncthreads();
+    // table: index i holds the next max_bits stream bits, first bit lowest;
+    // reversed, it is the left-aligned code value v, whose length is the
+    // first whose code range ends above v (the ranges rise with the length)
     const uint32_t max_bits = h.max_bits;
     const uint32_t tsize = 1u << max_bits;
     const uint16_t fallback = (uint16_t)(max_bits << 8);
-    for (uint32_t i = lane; i < tsize; i += 64) table16[i] = fallback;
-    __syncthreads();
-    // The Kraft check above guarantees a prefix code, so spreads never collide.
-    for (uint32_t s = lane; s < 256; s += 64) {
-      uint32_t l = lengths[s];
-      if (!l) continue;
-      uint16_t entry = (uint16_t)((l << 8) | s);
-      uint32_t spread = 1u << (max_bits - l);
-      for (uint32_t i = 0; i < spread; ++i) table16[rev[s] | (i << l)] = entry;
+    for (uint32_t i = lane; i < tsize; i += 64) {
+      const uint32_t v = __builtin_bitreverse32(i) >> (32 - max_bits);
+      uint16_t e = fallback;
+      if (v < code_end[max_bits]) {
+        uint32_t l = 1;
+        for (uint32_t b = 1; b < max_bits; ++b) l += v >= code_end[b];
+        const uint32_t c = v >> (max_bits - l);
+        e = (uint16_t)((l << 8) | sorted_sym[sym_base[l] + (c - next_code[l])]);
+      }
+      table16[i] = e;
     }
     __syncthreads();
 

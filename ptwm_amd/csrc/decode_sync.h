@@ -39,7 +39,11 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs);
 // Stored (tag 0 / Identity) payloads at least this long are copied by a
 // multi-workgroup kernel after the exact kernel has parsed them.
 constexpr uint64_t kCopyDeferMin = 4096;
-constexpr uint64_t kCopyChunk = 65536;
+// Output bytes per workgroup of that copy: small payloads in small pieces
+// (enough workgroups to fill the device), large ones in 64 KiB pieces.
+__host__ __device__ inline uint64_t copy_chunk(uint64_t len) { return len >= (8ull << 20) ? 65536ull : 8192ull; }
+// Fix passes queued after the first pass of the parallel Huffman decode.
+constexpr uint32_t kFixQueued = 4;
 
 // exact-path kernel launch (decode_exact.hip); copy_src (may be null): per
 // job, the source of a deferred stored-bytes copy (0: none)

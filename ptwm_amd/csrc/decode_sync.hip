@@ -12,9 +12,10 @@
 //            until no start changes (sync_pass_kernel);
 //   fix      the same across wavefronts, repeated until no wavefront's first
 //            start differs from the previous wavefront's last exit
-//            (sync_fix_kernel; passes are queued in batches, each pass
-//            skipping its work when the one before changed nothing, and the
-//            host reads the batch's flags once);
+//            (sync_fix_kernel; a fixed number of passes is queued, each pass
+//            skipping its work when the one before changed nothing; no host
+//            round trip: a payload still unsettled after them is caught by
+//            the wave-sum pass and reported, and the host queues more);
 //   scan     per stream, symbol counts -> output offsets (sync_scan_kernel);
 //   write    each lane decodes its subsequence again and writes the symbols
 //            (staged in LDS, stored coalesced), recording where symbol n-1
@@ -131,18 +132,100 @@ __device__ inline uint32_t run(const uint32_t* stage, const uint16_t* tab, uint3
   return p;
 }
 
-// Lanes restart from their left neighbour's exit until no start changes (at
-// most 63 rounds: each round fixes at least one more lane).
-__device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32_t mask, bool valid, uint32_t& st,
-                              uint32_t& ex, uint32_t& cnt, bool& changed) {
+// Codeword starts of a lane's path, one bit per bit of its subsequence:
+// word w of lane l at bm[w * kLanes + l] (consecutive lanes, consecutive banks).
+constexpr uint32_t kSubWords = kSyncSubBits / 32;
+
+// run() that also records the path's codeword starts (relative to base, the
+// lane's subsequence start) in the lane's bitmap.  A codeword is at most
+// kHufMaxBits < 32 bits, so consecutive starts never skip a bitmap word.
+__device__ inline uint32_t run_rec(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t base,
+                                   uint32_t p, uint32_t stop, uint32_t& cnt, uint32_t* bm) {
   const uint32_t lane = threadIdx.x;
+  uint32_t c = 0, wi = (p - base) >> 5, bits = 0;
+  for (uint32_t w = 0; w < wi; ++w) bm[w * kLanes + lane] = 0u;
+  while (p < stop) {
+    const uint32_t wi_p = p >> 5;
+    const uint32_t win = __builtin_amdgcn_alignbit(stage[wi_p + 1], stage[wi_p], p & 31u);
+    const uint32_t l = tab[win & mask] >> 8;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t q = k ? p + l : p;
+      if (k && q >= stop) break;
+      const uint32_t rel = q - base, w = rel >> 5;
+      if (w != wi) {
+        bm[wi * kLanes + lane] = bits;
+        wi = w;
+        bits = 0;
+      }
+      bits |= 1u << (rel & 31u);
+    }
+    p += l;
+    ++c;
+    if (p >= stop) break;
+    p += tab[(win >> l) & mask] >> 8;
+    ++c;
+  }
+  bm[wi * kLanes + lane] = bits;
+  for (uint32_t w = wi + 1; w < kSubWords; ++w) bm[w * kLanes + lane] = 0u;
+  cnt = c;
+  return p;
+}
+
+// Restart a lane whose bitmap holds its current path from a new start p:
+// decode until a position of the old path (its continuation, and so the
+// exit, is the old one: the count is the new prefix plus the old path's
+// starts from there), or, without meeting it, to the end.  Returns true and
+// updates ex / cnt.
+__device__ inline void run_join(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t base,
+                                uint32_t p, uint32_t stop, uint32_t& ex, uint32_t& cnt, const uint32_t* bm) {
+  const uint32_t lane = threadIdx.x;
+  uint32_t c = 0, wi = (p - base) >> 5, cur = bm[wi * kLanes + lane];
+  while (p < stop) {
+    const uint32_t rel = p - base, w = rel >> 5;
+    if (w != wi) {
+      wi = w;
+      cur = bm[wi * kLanes + lane];
+    }
+    if ((cur >> (rel & 31u)) & 1u) {
+      uint32_t rest = __popc(cur >> (rel & 31u));
+      for (uint32_t v = wi + 1; v < kSubWords; ++v) rest += __popc(bm[v * kLanes + lane]);
+      cnt = c + rest;
+      return;  // ex unchanged
+    }
+    const uint32_t win = __builtin_amdgcn_alignbit(stage[(p >> 5) + 1], stage[p >> 5], p & 31u);
+    p += tab[win & mask] >> 8;
+    ++c;
+  }
+  ex = p;
+  cnt = c;
+}
+
+// Lanes restart from their left neighbour's exit until no start changes (at
+// most 63 rounds: each round fixes at least one more lane).  With a bitmap
+// (bm non-null; bm_ok: it holds the lane's current path) a restart stops
+// where it joins the old path; a lane's later restarts run in full and
+// record again.
+__device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32_t mask, bool valid, uint32_t& st,
+                              uint32_t& ex, uint32_t& cnt, bool& changed, uint32_t* bm = nullptr,
+                              bool bm_ok = false) {
+  const uint32_t lane = threadIdx.x;
+  const uint32_t base = lane * kSyncSubBits, stop = base + kSyncSubBits;
   for (uint32_t round = 0; round < kLanes; ++round) {
     const uint32_t prev = (uint32_t)__shfl_up((int)ex, 1, 64);
     const bool ch = valid && lane > 0 && prev != st;
     if (__ballot(ch) == 0) break;
     if (ch) {
       st = prev;
-      ex = run(stage, tab, mask, st, (lane + 1) * kSyncSubBits, cnt);
+      if (bm && bm_ok) {
+        run_join(stage, tab, mask, base, st, stop, ex, cnt, bm);
+        bm_ok = false;  // the bitmap now also holds starts of the replaced prefix
+      } else if (bm) {
+        ex = run_rec(stage, tab, mask, base, st, stop, cnt, bm);
+        bm_ok = true;
+      } else {
+        ex = run(stage, tab, mask, st, stop, cnt);
+      }
       changed = true;
     }
   }
@@ -154,6 +237,7 @@ __global__ void __launch_bounds__(64) sync_pass_kernel(const SyncStream* __restr
                                                        const uint16_t* __restrict__ tables, SyncArrays A) {
   __shared__ uint16_t tab[2048];
   __shared__ uint32_t stage[kStageWords];
+  __shared__ uint32_t bm[kSubWords * kLanes];
   const uint32_t d = wave_job[blockIdx.x];
   uint32_t w = blockIdx.x - job_wave0[d];
   const int s = locate(streams + 4ull * d, w);
@@ -165,9 +249,9 @@ __global__ void __launch_bounds__(64) sync_pass_kernel(const SyncStream* __restr
   const uint32_t k = w * kLanes + lane;
   const bool valid = k < S.n_sub;
   uint32_t st = lane * kSyncSubBits, cnt = 0, ex = st;
-  if (valid) ex = run(stage, tab, mask, st, st + kSyncSubBits, cnt);
+  if (valid) ex = run_rec(stage, tab, mask, st, st, st + kSyncSubBits, cnt, bm);
   bool changed = false;
-  settle(stage, tab, mask, valid, st, ex, cnt, changed);
+  settle(stage, tab, mask, valid, st, ex, cnt, changed, bm, valid);
   if (valid) {
     const uint64_t g = (uint64_t)S.first_sub + k;
     A.start[g] = L0 * 8 + st;
@@ -223,7 +307,9 @@ __global__ void __launch_bounds__(64) sync_fix_kernel(const SyncStream* __restri
 }
 
 // Symbols per wavefront (sum of its 64 subsequence counts).
-__global__ void __launch_bounds__(64) sync_wave_sum_kernel(const SyncStream* __restrict__ streams,
+// A wavefront whose first start is not the previous wavefront's last exit
+// (the queued fix passes did not settle the stream) marks its stream.
+__global__ void __launch_bounds__(64) sync_wave_sum_kernel(SyncStream* __restrict__ streams,
                                                            const uint32_t* __restrict__ wave_job,
                                                            const uint32_t* __restrict__ job_wave0, SyncArrays A) {
   const uint32_t d = wave_job[blockIdx.x];
@@ -232,6 +318,10 @@ __global__ void __launch_bounds__(64) sync_wave_sum_kernel(const SyncStream* __r
   if (s < 0) return;
   const SyncStream S = streams[4ull * d + s];
   const uint32_t lane = threadIdx.x, k = w * kLanes + lane;
+  if (lane == 0 && w > 0) {
+    const uint64_t g0 = (uint64_t)S.first_sub + (uint64_t)w * kLanes;
+    if (A.exit[g0 - 1] != A.start[g0]) streams[4ull * d + s].pad = 1u;
+  }
   uint32_t c = k < S.n_sub ? A.count[(uint64_t)S.first_sub + k] : 0u;
   for (int o = 32; o >= 1; o >>= 1) c += (uint32_t)__shfl_xor((int)c, o, 64);
   if (lane == 0) A.wave_sum[blockIdx.x] = c;
@@ -327,7 +417,7 @@ __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__
 }
 
 // Stored bytes the exact kernel deferred (copy_src[j] != 0): one workgroup
-// per kCopyChunk of output.  Aligned dword stores; the source is realigned
+// per copy_chunk(len) of output.  Aligned dword stores; the source is realigned
 // with a funnel shift of two aligned words, used only where both words hold
 // source bytes.
 __global__ void __launch_bounds__(256) raw_copy_kernel(const DecodeJob* __restrict__ jobs,
@@ -338,8 +428,9 @@ __global__ void __launch_bounds__(256) raw_copy_kernel(const DecodeJob* __restri
   const uint64_t s = copy_src[j];
   if (s == 0) return;
   const DecodeJob J = jobs[j];
-  const uint64_t a = (uint64_t)(blockIdx.x - job_chunk0[j]) * kCopyChunk;
-  const uint64_t b = std::min<uint64_t>(J.dst_len, a + kCopyChunk);
+  const uint64_t cs = copy_chunk(J.dst_len);
+  const uint64_t a = (uint64_t)(blockIdx.x - job_chunk0[j]) * cs;
+  const uint64_t b = std::min<uint64_t>(J.dst_len, a + cs);
   if (a >= b) return;
   const uint32_t t = threadIdx.x;
   const uint64_t ba = J.dst + a, bb = J.dst + b;
@@ -367,9 +458,10 @@ __global__ void __launch_bounds__(64) sync_check_kernel(const SyncStream* __rest
   if (d >= n_def) return;
   const uint32_t job = streams[4ull * d].job;
   if (status[job] != kStDeferred) return;  // final already (the header was rejected)
-  bool ok = true;
+  bool ok = true, settled = true;
   for (int s = 0; s < 4; ++s) {
     const SyncStream S = streams[4ull * d + s];
+    settled = settled && S.pad == 0;
     if (S.n == 0) {
       ok = ok && S.m == 0;
       continue;
@@ -381,8 +473,39 @@ __global__ void __launch_bounds__(64) sync_check_kernel(const SyncStream* __rest
     const uint32_t used = (uint32_t)(S.T - 8 * (S.m - 1));  // bits of the last logical byte, 1..8
     if (used < 8 && (gbyte(S.src) >> used) != 0) ok = false;
   }
-  status[job] = ok ? kStOk : kStFallback;
+  status[job] = !settled ? kStUnsettled : ok ? kStOk : kStFallback;
 }
+
+}  // namespace
+
+namespace {
+
+#define PTWM_HIP_TRY_ERR(expr)          \
+  do {                                  \
+    const hipError_t _e = (expr);       \
+    if (_e != hipSuccess) return _e;    \
+  } while (0)
+
+__global__ void __launch_bounds__(256) clear_unsettled_kernel(SyncStream* __restrict__ streams, uint32_t n) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) streams[i].pad = 0u;
+}
+
+// Per-stream offsets, the write and the acceptance check (after the fix passes).
+hipError_t sync_finish(hipStream_t s, SyncStream* streams, const uint32_t* d_wave_job, const uint32_t* d_job_wave0,
+                       const uint16_t* tables, const SyncArrays& A, uint32_t nw, uint32_t n_def, uint32_t* status) {
+  hipLaunchKernelGGL(sync_wave_sum_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, A);
+  PTWM_HIP_TRY_ERR(hipGetLastError());
+  hipLaunchKernelGGL(sync_scan_kernel, dim3(4 * n_def), dim3(256), 0, s, streams, d_job_wave0, A);
+  PTWM_HIP_TRY_ERR(hipGetLastError());
+  hipLaunchKernelGGL(sync_write_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables, A);
+  PTWM_HIP_TRY_ERR(hipGetLastError());
+  hipLaunchKernelGGL(sync_check_kernel, dim3((n_def + kLanes - 1) / kLanes), dim3(kLanes), 0, s, streams, n_def,
+                     status);
+  return hipGetLastError();
+}
+
+size_t up16(size_t x) { return (x + 15) & ~size_t(15); }
 
 }  // namespace
 
@@ -391,7 +514,7 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   PTWM_HIP_TRY(ctx.status.ensure(n_jobs * sizeof(uint32_t) + 64));
   PTWM_HIP_TRY(ctx.h_status.ensure(n_jobs * sizeof(uint32_t) + 64));
   if (n_jobs == 0) return kOk;
-  // Payloads for the parallel path and their slots; output chunks for
+  // Payloads for the parallel path and their slots; output pieces for
   // deferred stored-bytes copies (any job may turn out to be stored).
   std::vector<uint32_t> wave_job, job_wave0, chunk_job, job_chunk0(n_jobs, 0);
   uint64_t subs = 0;
@@ -401,7 +524,8 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
     hj[j].sync_sub0 = 0;
     job_chunk0[j] = (uint32_t)chunk_job.size();
     if (hj[j].dst_len >= kCopyDeferMin) {
-      const uint64_t nc = (hj[j].dst_len + kCopyChunk - 1) / kCopyChunk;
+      const uint64_t cs = copy_chunk(hj[j].dst_len);
+      const uint64_t nc = (hj[j].dst_len + cs - 1) / cs;
       if (chunk_job.size() + nc > 0x7FFFFFFFull) return kInvalidInput;
       chunk_job.insert(chunk_job.end(), nc, (uint32_t)j);
     }
@@ -415,32 +539,42 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
     wave_job.insert(wave_job.end(), waves, n_def - 1);
     subs += u;
   }
-  PTWM_HIP_TRY(ctx.jobs.ensure(n_jobs * sizeof(DecodeJob) + 64));
-  PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, hj, n_jobs * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
-  const DecodeJob* d_jobs = static_cast<const DecodeJob*>(ctx.jobs.ptr);
-  // deferred copies: source per job, chunk -> job map, job -> first chunk
   const size_t nck = chunk_job.size();
-  PTWM_HIP_TRY(ctx.copy_args.ensure(n_jobs * 8 + (nck + n_jobs) * 4 + 64));
-  uint64_t* d_copy_src = static_cast<uint64_t*>(ctx.copy_args.ptr);
-  uint32_t* d_chunk_job = reinterpret_cast<uint32_t*>(d_copy_src + n_jobs);
-  uint32_t* d_job_chunk0 = d_chunk_job + nck;
-  PTWM_HIP_TRY(hipMemsetAsync(d_copy_src, 0, n_jobs * 8, s));
-  if (nck) {
-    PTWM_HIP_TRY(hipMemcpyAsync(d_chunk_job, chunk_job.data(), nck * 4, hipMemcpyHostToDevice, s));
-    PTWM_HIP_TRY(hipMemcpyAsync(d_job_chunk0, job_chunk0.data(), n_jobs * 4, hipMemcpyHostToDevice, s));
-  }
-  SyncStream* streams = nullptr;
+  const uint32_t nw = (uint32_t)wave_job.size();
+  // Every argument array in one upload from pinned memory:
+  //   jobs | copy sources (zero) | piece -> job | job -> first piece |
+  //   [stream records (zero) | wavefront -> payload | payload -> first
+  //    wavefront | fix-pass flags (zero)]
+  const size_t o_jobs = 0, o_src = up16(n_jobs * sizeof(DecodeJob)), o_cj = o_src + up16(n_jobs * 8),
+               o_jc = o_cj + up16(nck * 4), o_str = o_jc + up16(n_jobs * 4),
+               o_wj = o_str + up16(4ull * n_def * sizeof(SyncStream)), o_jw = o_wj + up16((size_t)nw * 4),
+               o_fl = o_jw + up16((size_t)n_def * 4), total = o_fl + up16(4 * kFixQueued);
+  PTWM_HIP_TRY(ctx.exact_args.ensure(total));
+  PTWM_HIP_TRY(ctx.h_exact_args.ensure(total));
+  uint8_t* hb = static_cast<uint8_t*>(ctx.h_exact_args.ptr);
+  uint8_t* db = static_cast<uint8_t*>(ctx.exact_args.ptr);
+  std::memcpy(hb + o_jobs, hj, n_jobs * sizeof(DecodeJob));
+  std::memset(hb + o_src, 0, o_cj - o_src);
+  if (nck) std::memcpy(hb + o_cj, chunk_job.data(), nck * 4);
+  std::memcpy(hb + o_jc, job_chunk0.data(), n_jobs * 4);
+  std::memset(hb + o_str, 0, o_wj - o_str);
+  if (nw) std::memcpy(hb + o_wj, wave_job.data(), (size_t)nw * 4);
+  if (n_def) std::memcpy(hb + o_jw, job_wave0.data(), (size_t)n_def * 4);
+  std::memset(hb + o_fl, 0, total - o_fl);
+  PTWM_HIP_TRY(hipMemcpyAsync(db, hb, total, hipMemcpyHostToDevice, s));
+  const DecodeJob* d_jobs = reinterpret_cast<const DecodeJob*>(db + o_jobs);
+  uint64_t* d_copy_src = reinterpret_cast<uint64_t*>(db + o_src);
+  const uint32_t* d_chunk_job = reinterpret_cast<const uint32_t*>(db + o_cj);
+  const uint32_t* d_job_chunk0 = reinterpret_cast<const uint32_t*>(db + o_jc);
+  SyncStream* streams = n_def ? reinterpret_cast<SyncStream*>(db + o_str) : nullptr;
+  const uint32_t* d_wave_job = reinterpret_cast<const uint32_t*>(db + o_wj);
+  const uint32_t* d_job_wave0 = reinterpret_cast<const uint32_t*>(db + o_jw);
+  uint32_t* d_flag = reinterpret_cast<uint32_t*>(db + o_fl);
   uint16_t* tables = nullptr;
   SyncArrays A{};
-  uint32_t *d_wave_job = nullptr, *d_job_wave0 = nullptr, *d_flag = nullptr;
-  const uint32_t nw = (uint32_t)wave_job.size();
-  constexpr uint32_t kFixBatch = 4;
   if (n_def) {
-    PTWM_HIP_TRY(ctx.sync_streams.ensure(4ull * n_def * sizeof(SyncStream)));
     PTWM_HIP_TRY(ctx.sync_tables.ensure(2048ull * 2 * n_def));
     PTWM_HIP_TRY(ctx.sync_sub.ensure(subs * (8 + 8 + 4) + (uint64_t)nw * (8 + 4) + 64));
-    PTWM_HIP_TRY(ctx.sync_waves.ensure((wave_job.size() + job_wave0.size() + kFixBatch) * 4 + 64));
-    streams = static_cast<SyncStream*>(ctx.sync_streams.ptr);
     tables = static_cast<uint16_t*>(ctx.sync_tables.ptr);
     uint8_t* sb = static_cast<uint8_t*>(ctx.sync_sub.ptr);
     A.start = reinterpret_cast<uint64_t*>(sb);
@@ -448,12 +582,6 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
     A.wave_prefix = A.exit + subs;
     A.count = reinterpret_cast<uint32_t*>(A.wave_prefix + nw);
     A.wave_sum = A.count + subs;
-    d_wave_job = static_cast<uint32_t*>(ctx.sync_waves.ptr);
-    d_job_wave0 = d_wave_job + wave_job.size();
-    d_flag = d_job_wave0 + job_wave0.size();
-    PTWM_HIP_TRY(hipMemsetAsync(streams, 0, 4ull * n_def * sizeof(SyncStream), s));
-    PTWM_HIP_TRY(hipMemcpyAsync(d_wave_job, wave_job.data(), wave_job.size() * 4, hipMemcpyHostToDevice, s));
-    PTWM_HIP_TRY(hipMemcpyAsync(d_job_wave0, job_wave0.data(), job_wave0.size() * 4, hipMemcpyHostToDevice, s));
   }
   uint32_t* status = static_cast<uint32_t*>(ctx.status.ptr);
   PTWM_HIP_TRY(launch_decode_exact(d_jobs, status, (uint32_t)n_jobs, streams, tables, d_copy_src, s));
@@ -484,42 +612,62 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   if (n_def) {
     hipLaunchKernelGGL(sync_pass_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables, A);
     PTWM_HIP_TRY(hipGetLastError());
-    PTWM_HIP_TRY(ctx.h_small.ensure(64));
-    volatile uint32_t* h_flag = static_cast<uint32_t*>(ctx.h_small.ptr);
-    bool settled = false;
-    for (uint32_t pass = 0; pass < kMaxFixPasses && !settled; pass += kFixBatch) {
-      PTWM_HIP_TRY(hipMemsetAsync(d_flag, 0, 4 * kFixBatch, s));
-      for (uint32_t k = 0; k < kFixBatch; ++k) {
-        hipLaunchKernelGGL(sync_fix_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables,
-                           A, k ? d_flag + k - 1 : nullptr, d_flag + k);
-        PTWM_HIP_TRY(hipGetLastError());
-      }
-      PTWM_HIP_TRY(hipMemcpyAsync(const_cast<uint32_t*>(h_flag), d_flag, 4 * kFixBatch, hipMemcpyDeviceToHost, s));
-      PTWM_HIP_TRY(hipStreamSynchronize(s));
-      for (uint32_t k = 0; k < kFixBatch; ++k) settled |= h_flag[k] == 0;
-    }
-    if (settled) {
-      hipLaunchKernelGGL(sync_wave_sum_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, A);
-      PTWM_HIP_TRY(hipGetLastError());
-      hipLaunchKernelGGL(sync_scan_kernel, dim3(4 * n_def), dim3(256), 0, s, streams, d_job_wave0, A);
-      PTWM_HIP_TRY(hipGetLastError());
-      hipLaunchKernelGGL(sync_write_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables,
-                         A);
-      PTWM_HIP_TRY(hipGetLastError());
-      hipLaunchKernelGGL(sync_check_kernel, dim3((n_def + kLanes - 1) / kLanes), dim3(kLanes), 0, s, streams, n_def,
-                         status);
+    for (uint32_t k = 0; k < kFixQueued; ++k) {
+      hipLaunchKernelGGL(sync_fix_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables, A,
+                         k ? d_flag + k - 1 : nullptr, d_flag + k);
       PTWM_HIP_TRY(hipGetLastError());
     }
+    PTWM_HIP_TRY(sync_finish(s, streams, d_wave_job, d_job_wave0, tables, A, nw, n_def, status));
   }
   if (any_rans) PTWM_HIP_TRY(hipStreamWaitEvent(s, ctx.side_join, 0));
   uint32_t* hs = static_cast<uint32_t*>(ctx.h_status.ptr);
   PTWM_HIP_TRY(hipMemcpyAsync(hs, status, n_jobs * 4, hipMemcpyDeviceToHost, s));
   PTWM_HIP_TRY(hipStreamSynchronize(s));
+  // payloads whose wavefront boundaries the queued passes did not settle:
+  // more fix passes until none changes (host-checked batches), then the
+  // offsets, the write and the check again
+  bool unsettled = false;
+  for (size_t j = 0; j < n_jobs; ++j) unsettled |= hs[j] == kStUnsettled;
+  if (unsettled) {
+    ++ctx.sync_extra_rounds;
+    constexpr uint32_t kBatch = 4;
+    PTWM_HIP_TRY(ctx.sync_waves.ensure(4 * kBatch + 64));
+    uint32_t* fl = static_cast<uint32_t*>(ctx.sync_waves.ptr);
+    PTWM_HIP_TRY(ctx.h_small.ensure(64));
+    volatile uint32_t* h_flag = static_cast<uint32_t*>(ctx.h_small.ptr);
+    bool settled = false;
+    for (uint32_t pass = 0; pass < kMaxFixPasses && !settled; pass += kBatch) {
+      PTWM_HIP_TRY(hipMemsetAsync(fl, 0, 4 * kBatch, s));
+      for (uint32_t k = 0; k < kBatch; ++k) {
+        hipLaunchKernelGGL(sync_fix_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables,
+                           A, k ? fl + k - 1 : nullptr, fl + k);
+        PTWM_HIP_TRY(hipGetLastError());
+      }
+      PTWM_HIP_TRY(hipMemcpyAsync(const_cast<uint32_t*>(h_flag), fl, 4 * kBatch, hipMemcpyDeviceToHost, s));
+      PTWM_HIP_TRY(hipStreamSynchronize(s));
+      for (uint32_t k = 0; k < kBatch; ++k) settled |= h_flag[k] == 0;
+    }
+    // the streams' unsettled marks are cleared; jobs already final keep
+    // their status (the write of a settled payload writes the same bytes)
+    std::vector<uint32_t> keep(hs, hs + n_jobs);
+    hipLaunchKernelGGL(clear_unsettled_kernel, dim3((4 * n_def + 255) / 256), dim3(256), 0, s, streams, 4 * n_def);
+    PTWM_HIP_TRY(hipGetLastError());
+    for (size_t j = 0; j < n_jobs; ++j)
+      if (keep[j] == kStUnsettled) keep[j] = kStDeferred;
+    PTWM_HIP_TRY(hipMemcpyAsync(status, keep.data(), n_jobs * 4, hipMemcpyHostToDevice, s));
+    PTWM_HIP_TRY(sync_finish(s, streams, d_wave_job, d_job_wave0, tables, A, nw, n_def, status));
+    PTWM_HIP_TRY(hipMemcpyAsync(hs, status, n_jobs * 4, hipMemcpyDeviceToHost, s));
+    PTWM_HIP_TRY(hipStreamSynchronize(s));
+    for (size_t j = 0; j < n_jobs; ++j)
+      if (keep[j] != kStDeferred) hs[j] = keep[j];
+  }
   // payloads the parallel path declined (or did not settle) go to the exact path
   std::vector<DecodeJob> again;
   std::vector<size_t> again_idx;
   for (size_t j = 0; j < n_jobs; ++j) {
-    if (hs[j] == kStFallback || hs[j] == kStDeferred) {
+    if (hj[j].sync_id && hs[j] == kStOk) ++ctx.sync_accepted;
+    if (hs[j] == kStFallback || hs[j] == kStDeferred || hs[j] == kStUnsettled) {
+      if (hj[j].sync_id) ++ctx.sync_fallbacks;
       DecodeJob J = hj[j];
       J.sync_id = 0;
       J.sync_sub0 = 0;
@@ -529,8 +677,10 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   }
   if (!again.empty()) {
     const size_t na = again.size();
+    PTWM_HIP_TRY(ctx.jobs.ensure(na * sizeof(DecodeJob) + 64));
     PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, again.data(), na * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
-    PTWM_HIP_TRY(launch_decode_exact(d_jobs, status, (uint32_t)na, nullptr, nullptr, nullptr, s));
+    PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr), status, (uint32_t)na, nullptr,
+                                     nullptr, nullptr, s));
     std::vector<uint32_t> st2(na);
     PTWM_HIP_TRY(hipMemcpyAsync(st2.data(), status, na * 4, hipMemcpyDeviceToHost, s));
     PTWM_HIP_TRY(hipStreamSynchronize(s));

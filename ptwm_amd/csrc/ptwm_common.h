@@ -48,6 +48,7 @@ enum DecodeStatus : uint32_t {
   kStBadStream = 5,      // bitstream inconsistent (reference decoder errors)
   kStDeferred = 6,       // header parsed, streams handed to the parallel Huffman path
   kStFallback = 7,       // parallel path declined the payload: decode it on the exact path
+  kStUnsettled = 8,      // parallel path: wavefront boundaries not settled by the queued fix passes
   kStNotRun = 0xFFFFFFFFu,
 };
 

@@ -95,7 +95,13 @@ struct DevCtx {
   // fused-decode status words, written by the kernels (host-coherent)
   PinnedBuffer h_ilv_status;
   // parallel Huffman decode of reference streams
-  DeviceBuffer sync_streams, sync_tables, sync_sub, sync_waves, copy_args;
+  DeviceBuffer sync_tables, sync_sub, sync_waves;
+  DeviceBuffer exact_args;  // the exact route's argument arrays, one upload per call
+  // reference Huffman payloads of the exact route, cumulative: accepted by
+  // the parallel path, decoded again by the exact state machine, and calls
+  // that needed fix passes beyond the queued ones
+  uint64_t sync_accepted = 0, sync_fallbacks = 0, sync_extra_rounds = 0;
+  PinnedBuffer h_exact_args;
   // inverse plane ops (plane_ops.hip): job list and IntDelta tile sums
   DeviceBuffer op_jobs, op_sums;
   PinnedBuffer h_op;

@@ -75,8 +75,12 @@ def planes():
 def test_parallel_huffman_decode_matches_reference(name, plane):
     payload = O.codec_encode(O.CODEC_HUFFMAN, plane)
     note(f"sync decode {name}: plane {len(plane)} payload {len(payload)} tag {payload[0]}")
+    before = api.decode_stats(0)
     got, n = gpu_decode(payload, len(plane))
     assert n == len(plane) and got == plane
+    after = api.decode_stats(0)
+    if payload[0] == 1 and len(payload) >= 16384:  # a coded payload on the parallel path: accepted there
+        assert after["accepted"] == before["accepted"] + 1 and after["fallbacks"] == before["fallbacks"], after
 
 
 def _streams_start(payload: bytes) -> int:
