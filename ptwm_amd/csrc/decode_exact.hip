@@ -415,7 +415,7 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
     if (job.sync_id) {
       // parallel path: publish the table and the four streams, stop here
       const uint32_t d = job.sync_id - 1;
-      for (uint32_t i = lane; i < tsize; i += 64) sync_tables[2048ull * d + i] = table16[i];
+      for (uint32_t i = lane; i < tsize; i += 64) sync_tables[(uint64_t)kSyncTableEntries * d + i] = table16[i];
       if (lane < 4) {
         uint64_t s4[4], e4[4];
         split_four(job.dst_len, s4, e4);

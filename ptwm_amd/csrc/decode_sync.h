@@ -47,6 +47,10 @@ constexpr uint32_t kFixQueued = 4;
 
 // exact-path kernel launch (decode_exact.hip); copy_src (may be null): per
 // job, the source of a deferred stored-bytes copy (0: none)
+// Decode tables of the parallel path: a slot of 2048 16-bit entries per
+// payload, (code length << 8) | symbol, indexed by the next max_bits stream
+// bits (first bit lowest).
+constexpr uint32_t kSyncTableEntries = 2048;
 hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
                                SyncStream* sync_streams, uint16_t* sync_tables, uint64_t* copy_src,
                                hipStream_t stream);

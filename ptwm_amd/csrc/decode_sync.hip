@@ -49,7 +49,7 @@ namespace {
 constexpr uint32_t kLanes = 64;
 constexpr uint32_t kSubBytes = kSyncSubBits / 8;
 constexpr uint32_t kWaveBits = kLanes * kSyncSubBits;
-constexpr uint32_t kStageWords = kWaveBits / 32 + 2;  // + the window overrun
+constexpr uint32_t kStageWords = kWaveBits / 32 + 3;  // + the window overrun and the cursor's look-ahead
 constexpr uint32_t kOutStage = 16384;                 // LDS output staging per wavefront
 constexpr uint32_t kMaxFixPasses = 256;
 static_assert(kSyncSubBits % 32 == 0 && (kSyncSubBits / 32) % 2 == 1, "subsequence size");
@@ -83,53 +83,96 @@ __device__ inline void stage_wave(const SyncStream& S, uint64_t L0, const uint16
                                   uint32_t* stage, uint16_t* tab) {
   const uint32_t lane = threadIdx.x;
   const uint32_t tsize = 1u << S.max_bits;  // >= 2
-  // the table as 32-bit words (each table starts 4 KiB-aligned)
-  const uint64_t gt = reinterpret_cast<uint64_t>(tables + 2048ull * S.table);
-  uint32_t* const t32 = reinterpret_cast<uint32_t*>(tab);
-  for (uint32_t i = lane; i < tsize / 2; i += kLanes) t32[i] = g_ld<uint32_t>(gt + 4ull * i);
+  // Every load is issued before the first LDS store, none of them under a
+  // condition, so the wavefront waits for memory once.  The table: the
+  // payload's whole slot (2048 entries, 4 KiB) in 16-byte loads.
+  constexpr uint32_t kTabIt = kSyncTableEntries / (8 * kLanes);
+  const uint64_t gt = reinterpret_cast<uint64_t>(tables + (uint64_t)kSyncTableEntries * S.table);
+  u32x4 t4[kTabIt];
+#pragma unroll
+  for (uint32_t it = 0; it < kTabIt; ++it) t4[it] = g_ld<u32x4>(gt + 16ull * (lane + kLanes * it));
   // Logical bytes [b, b + 4) of a stage word are the physical bytes
   // [m - 4 - b, m - 1 - b] reversed: one byte swap of the word at a =
-  // src + m - 4 - b, read as the aligned words that hold it (each holds a
-  // byte of the stream).  Words reaching past the stream's logical end are
-  // assembled bytewise (zero past the end).
-  for (uint32_t q = lane; q < kStageWords; q += kLanes) {
-    const uint64_t b = L0 + 4ull * q;
-    uint32_t v = 0;
-    if (b + 4 <= S.m) {
-      const uint64_t a = S.src + S.m - 4 - b, lo = a & ~3ull;
-      const uint32_t sh = (uint32_t)(a & 3u);
-      const uint32_t w0 = g_ld<uint32_t>(lo), w1 = sh ? g_ld<uint32_t>(lo + 4) : 0u;
-      v = __builtin_bswap32(__builtin_amdgcn_alignbyte(w1, w0, sh));
-    } else {
+  // src + m - 4 - b, read as the aligned words that hold it.  Bytes past the
+  // stream's logical end are masked to zero; the address of a word wholly
+  // past it is clamped to src - 8, which still lies in the payload (ahead
+  // of the streams sit the tag, the weights header and the jump table).
+  constexpr uint32_t kStIt = (kStageWords + kLanes - 1) / kLanes;
+  const uint64_t lo_min = (S.src - 8) & ~3ull;
+  uint32_t w0[kStIt], w1[kStIt];
 #pragma unroll
-      for (uint32_t t = 0; t < 4; ++t) {
-        const uint64_t i = b + t;
-        if (i < S.m) v |= (uint32_t)gbyte(S.src + S.m - 1 - i) << (8 * t);
-      }
-    }
-    stage[q] = v;
+  for (uint32_t it = 0; it < kStIt; ++it) {
+    const uint64_t b = L0 + 4ull * (lane + kLanes * it);
+    const uint64_t a = S.src + S.m - 4 - b;
+    const uint64_t lo = std::max<uint64_t>(a & ~3ull, lo_min);
+    w0[it] = g_ld<uint32_t>(lo);
+    w1[it] = g_ld<uint32_t>((a & 3u) ? lo + 4 : lo);
+  }
+  // (tsize >= 2: a table is stored as whole 32-bit words)
+  uint32_t* const t32 = reinterpret_cast<uint32_t*>(tab);
+#pragma unroll
+  for (uint32_t it = 0; it < kTabIt; ++it) {
+    const uint32_t i = 4 * (lane + kLanes * it);
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k)
+      if (2 * (i + k) < tsize) t32[i + k] = t4[it][k];
+  }
+#pragma unroll
+  for (uint32_t it = 0; it < kStIt; ++it) {
+    const uint32_t q = lane + kLanes * it;
+    const uint64_t b = L0 + 4ull * q;
+    const uint64_t a = S.src + S.m - 4 - b;
+    const uint64_t rem = b < S.m ? S.m - b : 0;
+    const uint32_t keep = rem >= 4 ? 0xFFFFFFFFu : (uint32_t)((1ull << (8 * rem)) - 1ull);
+    const uint32_t v = __builtin_bswap32(__builtin_amdgcn_alignbyte(w1[it], w0[it], (uint32_t)(a & 3u))) & keep;
+    if (q < kStageWords) stage[q] = v;
   }
   __syncthreads();
 }
 
+// A bit cursor over the staged span: the position and the three stage words
+// from the one holding it.  A step (two codewords) moves it by at most 22
+// bits, so it crosses at most one word boundary; the word loaded then is
+// needed only after the next crossing, so its LDS latency overlaps the table
+// lookups.
+struct Cursor {
+  uint32_t p, w0, w1, w2;
+};
+__device__ inline Cursor cur_open(const uint32_t* stage, uint32_t p) {
+  const uint32_t i = p >> 5;
+  return Cursor{p, stage[i], stage[i + 1], stage[i + 2]};
+}
+__device__ inline uint32_t cur_win(const Cursor& c) { return __builtin_amdgcn_alignbit(c.w1, c.w0, c.p & 31u); }
+__device__ inline void cur_adv(Cursor& c, const uint32_t* stage, uint32_t n) {
+  const uint32_t q = c.p + n;
+  if ((q >> 5) != (c.p >> 5)) {
+    c.w0 = c.w1;
+    c.w1 = c.w2;
+    c.w2 = stage[(q >> 5) + 2];
+  }
+  c.p = q;
+}
+
 // Decode from bit p (relative to the staged span) until p >= stop; returns
-// the exit bit, symbol count in `cnt`.  Every table entry consumes >= 1 bit.
+// the exit bit, symbol count in `cnt`.  Every codeword is >= 1 bit; two per
+// window (the second from the window's bits after the first: 32 - 11 >= 11).
 __device__ inline uint32_t run(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t p, uint32_t stop,
                                uint32_t& cnt) {
   uint32_t c = 0;
-  while (p < stop) {
-    const uint32_t wi = p >> 5;
-    const uint32_t win = __builtin_amdgcn_alignbit(stage[wi + 1], stage[wi], p & 31u);
-    const uint32_t e = tab[win & mask];
-    const uint32_t l = e >> 8;
-    p += l;
-    ++c;
-    if (p >= stop) break;
-    p += tab[(win >> l) & mask] >> 8;
-    ++c;
+  Cursor k = cur_open(stage, p);
+  while (k.p < stop) {
+    const uint32_t win = cur_win(k);
+    const uint32_t l1 = tab[win & mask] >> 8;
+    if (k.p + l1 >= stop) {
+      cur_adv(k, stage, l1);
+      ++c;
+      break;
+    }
+    cur_adv(k, stage, l1 + (tab[(win >> l1) & mask] >> 8));
+    c += 2;
   }
   cnt = c;
-  return p;
+  return k.p;
 }
 
 // Codeword starts of a lane's path, one bit per bit of its subsequence:
@@ -144,15 +187,15 @@ __device__ inline uint32_t run_rec(const uint32_t* stage, const uint16_t* tab, u
   const uint32_t lane = threadIdx.x;
   uint32_t c = 0, wi = (p - base) >> 5, bits = 0;
   for (uint32_t w = 0; w < wi; ++w) bm[w * kLanes + lane] = 0u;
-  while (p < stop) {
-    const uint32_t wi_p = p >> 5;
-    const uint32_t win = __builtin_amdgcn_alignbit(stage[wi_p + 1], stage[wi_p], p & 31u);
-    const uint32_t l = tab[win & mask] >> 8;
+  Cursor k = cur_open(stage, p);
+  while (k.p < stop) {
+    const uint32_t win = cur_win(k);
+    const uint32_t l1 = tab[win & mask] >> 8;
+    const bool two = k.p + l1 < stop;
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const uint32_t q = k ? p + l : p;
-      if (k && q >= stop) break;
-      const uint32_t rel = q - base, w = rel >> 5;
+    for (int j = 0; j < 2; ++j) {
+      if (j && !two) break;
+      const uint32_t rel = (j ? k.p + l1 : k.p) - base, w = rel >> 5;
       if (w != wi) {
         bm[wi * kLanes + lane] = bits;
         wi = w;
@@ -160,29 +203,26 @@ __device__ inline uint32_t run_rec(const uint32_t* stage, const uint16_t* tab, u
       }
       bits |= 1u << (rel & 31u);
     }
-    p += l;
-    ++c;
-    if (p >= stop) break;
-    p += tab[(win >> l) & mask] >> 8;
-    ++c;
+    cur_adv(k, stage, two ? l1 + (tab[(win >> l1) & mask] >> 8) : l1);
+    c += two ? 2u : 1u;
   }
   bm[wi * kLanes + lane] = bits;
   for (uint32_t w = wi + 1; w < kSubWords; ++w) bm[w * kLanes + lane] = 0u;
   cnt = c;
-  return p;
+  return k.p;
 }
 
 // Restart a lane whose bitmap holds its current path from a new start p:
 // decode until a position of the old path (its continuation, and so the
 // exit, is the old one: the count is the new prefix plus the old path's
-// starts from there), or, without meeting it, to the end.  Returns true and
-// updates ex / cnt.
+// starts from there), or, without meeting it, to the end; updates ex / cnt.
 __device__ inline void run_join(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t base,
                                 uint32_t p, uint32_t stop, uint32_t& ex, uint32_t& cnt, const uint32_t* bm) {
   const uint32_t lane = threadIdx.x;
   uint32_t c = 0, wi = (p - base) >> 5, cur = bm[wi * kLanes + lane];
-  while (p < stop) {
-    const uint32_t rel = p - base, w = rel >> 5;
+  Cursor k = cur_open(stage, p);
+  while (k.p < stop) {
+    const uint32_t rel = k.p - base, w = rel >> 5;
     if (w != wi) {
       wi = w;
       cur = bm[wi * kLanes + lane];
@@ -193,11 +233,10 @@ __device__ inline void run_join(const uint32_t* stage, const uint16_t* tab, uint
       cnt = c + rest;
       return;  // ex unchanged
     }
-    const uint32_t win = __builtin_amdgcn_alignbit(stage[(p >> 5) + 1], stage[p >> 5], p & 31u);
-    p += tab[win & mask] >> 8;
+    cur_adv(k, stage, tab[cur_win(k) & mask] >> 8);
     ++c;
   }
-  ex = p;
+  ex = k.p;
   cnt = c;
 }
 
@@ -235,7 +274,7 @@ __global__ void __launch_bounds__(64) sync_pass_kernel(const SyncStream* __restr
                                                        const uint32_t* __restrict__ wave_job,
                                                        const uint32_t* __restrict__ job_wave0,
                                                        const uint16_t* __restrict__ tables, SyncArrays A) {
-  __shared__ uint16_t tab[2048];
+  __shared__ uint16_t tab[kSyncTableEntries];
   __shared__ uint32_t stage[kStageWords];
   __shared__ uint32_t bm[kSubWords * kLanes];
   const uint32_t d = wave_job[blockIdx.x];
@@ -268,7 +307,7 @@ __global__ void __launch_bounds__(64) sync_fix_kernel(const SyncStream* __restri
                                                       const uint16_t* __restrict__ tables, SyncArrays A,
                                                       const uint32_t* __restrict__ prev_flag,
                                                       uint32_t* __restrict__ flag) {
-  __shared__ uint16_t tab[2048];
+  __shared__ uint16_t tab[kSyncTableEntries];
   __shared__ uint32_t stage[kStageWords];
   // the previous pass (queued before this one) changed nothing: settled
   if (prev_flag && g_ld<uint32_t>(reinterpret_cast<uint64_t>(prev_flag)) == 0) return;
@@ -363,7 +402,7 @@ __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__
                                                         const uint32_t* __restrict__ wave_job,
                                                         const uint32_t* __restrict__ job_wave0,
                                                         const uint16_t* __restrict__ tables, SyncArrays A) {
-  __shared__ uint16_t tab[2048];
+  __shared__ uint16_t tab[kSyncTableEntries];
   __shared__ uint32_t stage[kStageWords];
   __shared__ __attribute__((aligned(16))) uint8_t out[kOutStage + 16];
   const uint32_t d = wave_job[blockIdx.x];
@@ -392,17 +431,25 @@ __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__
   const uint64_t gA = S.dst + base, gB = S.dst + wave_end;
   const uint32_t skew = (uint32_t)(gA & 15u);
   if (valid && first < S.n) {
-    uint32_t p = (uint32_t)(A.start[g] - L0 * 8);
-    const uint64_t m = std::min<uint64_t>(cnt, S.n - first);
-    for (uint64_t i = 0; i < m; ++i) {
-      const uint32_t wi = p >> 5;
-      const uint32_t win = __builtin_amdgcn_alignbit(stage[wi + 1], stage[wi], p & 31u);
-      const uint32_t e = tab[win & mask];
-      p += e >> 8;
-      if (staged) out[skew + (first - base) + i] = (uint8_t)e;
-      else g_st<uint8_t>(S.dst + first + i, (uint8_t)e);
+    Cursor k = cur_open(stage, (uint32_t)(A.start[g] - L0 * 8));
+    const uint32_t m = (uint32_t)std::min<uint64_t>(cnt, S.n - first);
+    uint8_t* const o = out + skew + (first - base);
+    for (uint32_t i = 0; i < m;) {
+      const uint32_t win = cur_win(k);
+      const uint32_t e1 = tab[win & mask], l1 = e1 >> 8;
+      const bool two = i + 1 < m;
+      const uint32_t e2 = two ? tab[(win >> l1) & mask] : 0u;
+      if (staged) {
+        o[i] = (uint8_t)e1;
+        if (two) o[i + 1] = (uint8_t)e2;
+      } else {
+        g_st<uint8_t>(S.dst + first + i, (uint8_t)e1);
+        if (two) g_st<uint8_t>(S.dst + first + i + 1, (uint8_t)e2);
+      }
+      cur_adv(k, stage, l1 + (e2 >> 8));
+      i += two ? 2u : 1u;
     }
-    if (first + m == S.n) Sp->T = L0 * 8 + p;
+    if (first + m == S.n) Sp->T = L0 * 8 + k.p;
   }
   if (staged) {
     __syncthreads();
@@ -573,7 +620,7 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   uint16_t* tables = nullptr;
   SyncArrays A{};
   if (n_def) {
-    PTWM_HIP_TRY(ctx.sync_tables.ensure(2048ull * 2 * n_def));
+    PTWM_HIP_TRY(ctx.sync_tables.ensure(2ull * kSyncTableEntries * n_def));
     PTWM_HIP_TRY(ctx.sync_sub.ensure(subs * (8 + 8 + 4) + (uint64_t)nw * (8 + 4) + 64));
     tables = static_cast<uint16_t*>(ctx.sync_tables.ptr);
     uint8_t* sb = static_cast<uint8_t*>(ctx.sync_sub.ptr);
