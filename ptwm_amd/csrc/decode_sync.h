@@ -36,6 +36,34 @@ static_assert(sizeof(SyncStream) == 64, "SyncStream layout");
 // each job's final status.
 int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs);
 
+// The same in two phases, so that a caller can queue work that reads the
+// decoded planes (the merge) before it waits: decode_jobs_launch queues
+// every kernel and the copy of the statuses to ctx.h_status; after the
+// caller has synchronised the stream, decode_jobs_complete re-runs what the
+// parallel path did not settle or declined (launching and waiting as
+// needed) and reports in `rewritten` whether any job's output was written
+// again after the launch phase.  The device arguments of the launch live in
+// ExactRun until the next call on the device.
+struct SyncArrays {
+  uint64_t* start;        // per subsequence: first bit (stream-absolute)
+  uint64_t* exit;         // first codeword boundary at or past the subsequence end
+  uint32_t* count;        // symbols decoded from start to exit
+  uint32_t* wave_sum;     // per launched wavefront: symbols of its 64 subsequences
+  uint64_t* wave_prefix;  // per launched wavefront: symbols of the stream before it
+};
+struct ExactRun {
+  const DecodeJob* jobs = nullptr;
+  uint32_t* status = nullptr;
+  SyncStream* streams = nullptr;
+  uint16_t* tables = nullptr;
+  SyncArrays A{};
+  const uint32_t* wave_job = nullptr;
+  const uint32_t* job_wave0 = nullptr;
+  uint32_t nw = 0, n_def = 0;
+};
+int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& run);
+int64_t decode_jobs_complete(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& run, bool& rewritten);
+
 // Stored (tag 0 / Identity) payloads at least this long are copied by a
 // multi-workgroup kernel after the exact kernel has parsed them.
 constexpr uint64_t kCopyDeferMin = 4096;

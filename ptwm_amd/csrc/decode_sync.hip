@@ -54,14 +54,6 @@ constexpr uint32_t kOutStage = 16384;                 // LDS output staging per 
 constexpr uint32_t kMaxFixPasses = 256;
 static_assert(kSyncSubBits % 32 == 0 && (kSyncSubBits / 32) % 2 == 1, "subsequence size");
 
-struct SyncArrays {
-  uint64_t* start;        // per subsequence: first bit (stream-absolute)
-  uint64_t* exit;         // first codeword boundary at or past the subsequence end
-  uint32_t* count;        // symbols decoded from start to exit
-  uint32_t* wave_sum;     // per launched wavefront: symbols of its 64 subsequences
-  uint64_t* wave_prefix;  // per launched wavefront: symbols of the stream before it
-};
-
 // Which stream of deferred payload d, and which wavefront of it, wavefront
 // `w` of the payload's launch range covers; -1 when past the last.
 __device__ inline int locate(const SyncStream* S4, uint32_t& w) {
@@ -556,7 +548,7 @@ size_t up16(size_t x) { return (x + 15) & ~size_t(15); }
 
 }  // namespace
 
-int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
+int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& run) {
   hipStream_t s = ctx.stream;
   PTWM_HIP_TRY(ctx.status.ensure(n_jobs * sizeof(uint32_t) + 64));
   PTWM_HIP_TRY(ctx.h_status.ensure(n_jobs * sizeof(uint32_t) + 64));
@@ -667,9 +659,30 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
     PTWM_HIP_TRY(sync_finish(s, streams, d_wave_job, d_job_wave0, tables, A, nw, n_def, status));
   }
   if (any_rans) PTWM_HIP_TRY(hipStreamWaitEvent(s, ctx.side_join, 0));
+  PTWM_HIP_TRY(hipMemcpyAsync(ctx.h_status.ptr, status, n_jobs * 4, hipMemcpyDeviceToHost, s));
+  run.jobs = d_jobs;
+  run.status = status;
+  run.streams = streams;
+  run.tables = tables;
+  run.A = A;
+  run.wave_job = d_wave_job;
+  run.job_wave0 = d_job_wave0;
+  run.nw = nw;
+  run.n_def = n_def;
+  return kOk;
+}
+
+int64_t decode_jobs_complete(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& run, bool& rewritten) {
+  hipStream_t s = ctx.stream;
+  rewritten = false;
   uint32_t* hs = static_cast<uint32_t*>(ctx.h_status.ptr);
-  PTWM_HIP_TRY(hipMemcpyAsync(hs, status, n_jobs * 4, hipMemcpyDeviceToHost, s));
-  PTWM_HIP_TRY(hipStreamSynchronize(s));
+  uint32_t* status = run.status;
+  SyncStream* streams = run.streams;
+  const uint16_t* tables = run.tables;
+  const SyncArrays& A = run.A;
+  const uint32_t* d_wave_job = run.wave_job;
+  const uint32_t* d_job_wave0 = run.job_wave0;
+  const uint32_t nw = run.nw, n_def = run.n_def;
   // payloads whose wavefront boundaries the queued passes did not settle:
   // more fix passes until none changes (host-checked batches), then the
   // offsets, the write and the check again
@@ -677,6 +690,7 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
   for (size_t j = 0; j < n_jobs; ++j) unsettled |= hs[j] == kStUnsettled;
   if (unsettled) {
     ++ctx.sync_extra_rounds;
+    rewritten = true;
     constexpr uint32_t kBatch = 4;
     PTWM_HIP_TRY(ctx.sync_waves.ensure(4 * kBatch + 64));
     uint32_t* fl = static_cast<uint32_t*>(ctx.sync_waves.ptr);
@@ -723,6 +737,7 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
     }
   }
   if (!again.empty()) {
+    rewritten = true;
     const size_t na = again.size();
     PTWM_HIP_TRY(ctx.jobs.ensure(na * sizeof(DecodeJob) + 64));
     PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, again.data(), na * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
@@ -734,6 +749,15 @@ int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
     for (size_t i = 0; i < na; ++i) hs[again_idx[i]] = st2[i];
   }
   return kOk;
+}
+
+int64_t decode_jobs(DevCtx& ctx, DecodeJob* hj, size_t n_jobs) {
+  ExactRun run;
+  int64_t rc = decode_jobs_launch(ctx, hj, n_jobs, run);
+  if (rc != kOk || n_jobs == 0) return rc;
+  PTWM_HIP_TRY(hipStreamSynchronize(ctx.stream));
+  bool rewritten = false;
+  return decode_jobs_complete(ctx, hj, n_jobs, run, rewritten);
 }
 
 }  // namespace ptwm

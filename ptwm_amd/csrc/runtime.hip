@@ -586,14 +586,33 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     if (rc != kOk) return rc;
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[0], s));
-  if (n_jobs) {
-    // reference-format payloads: parallel Huffman path where it applies,
-    // exact path otherwise; final statuses in h_status
-    const int64_t rc = decode_jobs(ctx, hj, n_jobs);
+  // Reference-format payloads: parallel Huffman path where it applies, exact
+  // path otherwise.  Without plane ops the merges are queued right behind
+  // the decode and the statuses are read once, at the end; a job decoded
+  // again after that (not settled, or declined by the parallel path) has
+  // its tensor merged again.
+  bool any_op = false;
+  for (size_t t = 0; t < nt; ++t)
+    if (!fused[t])
+      for (const PlanPlane& P : plan.tensors[t].planes) any_op |= P.op != kPlaneOpNone;
+  ExactRun run;
+  const auto complete_jobs = [&](bool& rewritten) -> int64_t {
+    PTWM_HIP_TRY(hipStreamSynchronize(s));
+    const int64_t rc = decode_jobs_complete(ctx, hj, n_jobs, run, rewritten);
     if (rc != kOk) return rc;
     const uint32_t* st = static_cast<const uint32_t*>(ctx.h_status.ptr);
     for (size_t k = 0; k < n_jobs; ++k)
       if (st[k] != kStOk) return kInvalidInput;
+    return kOk;
+  };
+  if (n_jobs) {
+    int64_t rc = decode_jobs_launch(ctx, hj, n_jobs, run);
+    if (rc != kOk) return rc;
+    if (any_op) {
+      bool rewritten = false;
+      rc = complete_jobs(rewritten);
+      if (rc != kOk) return rc;
+    }
   }
   // inverse plane ops: decoded plane -> the plane the merge reads
   std::vector<std::vector<uint64_t>> merge_addr = plane_addr;
@@ -613,19 +632,35 @@ int64_t execute_plan(DevCtx& ctx, const Plan& plan, uint64_t in_dev, uint64_t ou
     if (rc != kOk) return rc;
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[1], s));
-  for (size_t t = 0; t < nt; ++t) {
-    if (fused[t]) continue;
-    const PlanTensor& T = plan.tensors[t];
-    const uint8_t* pp[4] = {nullptr, nullptr, nullptr, nullptr};
-    for (size_t p = 0; p < T.planes.size(); ++p) pp[p] = reinterpret_cast<const uint8_t*>(merge_addr[t][p]);
-    uint8_t* out = reinterpret_cast<uint8_t*>(out_dev + T.out_offset);
-    if (T.planes[0].plane_len == 0) continue;
-    if (merge_tmp[t] == kDirect) {
-      PTWM_HIP_TRY(launch_merge(T.chain, pp, T.planes[0].plane_len, out, s));
-    } else {
-      uint8_t* tmp = reinterpret_cast<uint8_t*>(scratch_base + merge_tmp[t]);
-      PTWM_HIP_TRY(launch_merge(T.chain, pp, T.planes[0].plane_len, tmp, s));
-      PTWM_HIP_TRY(hipMemcpyAsync(out, tmp, T.out_len, hipMemcpyDeviceToDevice, s));
+  const auto launch_merges = [&]() -> int64_t {
+    for (size_t t = 0; t < nt; ++t) {
+      if (fused[t]) continue;
+      const PlanTensor& T = plan.tensors[t];
+      const uint8_t* pp[4] = {nullptr, nullptr, nullptr, nullptr};
+      for (size_t p = 0; p < T.planes.size(); ++p) pp[p] = reinterpret_cast<const uint8_t*>(merge_addr[t][p]);
+      uint8_t* out = reinterpret_cast<uint8_t*>(out_dev + T.out_offset);
+      if (T.planes[0].plane_len == 0) continue;
+      if (merge_tmp[t] == kDirect) {
+        PTWM_HIP_TRY(launch_merge(T.chain, pp, T.planes[0].plane_len, out, s));
+      } else {
+        uint8_t* tmp = reinterpret_cast<uint8_t*>(scratch_base + merge_tmp[t]);
+        PTWM_HIP_TRY(launch_merge(T.chain, pp, T.planes[0].plane_len, tmp, s));
+        PTWM_HIP_TRY(hipMemcpyAsync(out, tmp, T.out_len, hipMemcpyDeviceToDevice, s));
+      }
+    }
+    return kOk;
+  };
+  {
+    int64_t rc = launch_merges();
+    if (rc != kOk) return rc;
+    if (n_jobs && !any_op) {
+      bool rewritten = false;
+      rc = complete_jobs(rewritten);
+      if (rc != kOk) return rc;
+      if (rewritten) {
+        rc = launch_merges();
+        if (rc != kOk) return rc;
+      }
     }
   }
   if (ctx.profile) PTWM_HIP_TRY(hipEventRecord(ctx.ev[2], s));
