@@ -808,6 +808,12 @@ struct Builder {
         for (size_t k = 0; k < p.chunks.size(); k += 2) tot += p.chunks[k + 1];
         if (tot != plane_len) return kInvalid;
         if (p.chunks.empty()) return kInvalid;
+        // container.rs:1998-2009: each chunk's frame runs from its offset to
+        // the next one's (the last to the payload's end), inside the payload
+        for (size_t k = 0; k < p.chunks.size(); k += 2) {
+          const uint64_t end = k + 2 < p.chunks.size() ? p.chunks[k + 2] : p.payload_len;
+          if (p.chunks[k] > end || end > p.payload_len) return kInvalid;
+        }
       }
     }
     if (any_crc && !all_crc) return kUnsup;  // the plan checks all of a tensor's planes or none

@@ -40,8 +40,11 @@ def _seeds(d):
         plan, _, _ = api.container_plan(frame)  # plans with plane ops (the smooth frames)
         open(os.path.join(d, "q%03d" % k), "wb").write(b"\x01" + plan)
         k += 1
-    # regression: a legacy record whose name runs past the record's end
+    # regressions: a legacy record whose name runs past the record's end;
+    # inputs the fuzzer found (tests/golden/fuzz_regress, with their mode byte)
     open(os.path.join(d, "r000"), "wb").write(b"\x00" + overlong_name_file())
+    for k, p in enumerate(sorted(glob.glob(os.path.join(HERE, "golden", "fuzz_regress", "*.bin")))):
+        shutil.copy(p, os.path.join(d, "x%03d" % k))
 
 
 def overlong_name_file() -> bytes:
@@ -62,6 +65,19 @@ def test_overlong_legacy_name_is_rejected():
     _, ents, _ = api.container_plan(overlong_name_file())
     assert ents[0].status == -1 and ents[0].plan_index == -1 and ents[0].name == ""
     assert all(e.status == 0 for e in ents[1:])
+
+
+def test_chunk_offset_past_the_payload_is_rejected():
+    """A legacy file the fuzzer derived from legacy_v1_1_0.ptwm: the chunk
+    table of the last tensor's first plane starts past the plane's payload.
+    The reference refuses the record at decode (container.rs:1998-2009);
+    the reader lists it invalid (-1, not planned) instead of writing a plan
+    whose chunk table leaves the payload, and the other records still plan."""
+    data = open(os.path.join(HERE, "golden", "fuzz_regress", "legacy_chunk_offset_past_payload.bin"), "rb").read()
+    assert data[0] == 0  # fuzz mode byte: the container reader
+    plan, ents, _ = api.container_plan(data[1:])
+    assert ents[-1].status == -1 and ents[-1].plan_index == -1
+    assert sum(e.plan_index >= 0 for e in ents) == 4
 
 
 @pytest.mark.skipif(not os.path.exists(CLANG), reason="ROCm clang (libFuzzer) not installed")
