@@ -89,6 +89,67 @@ const NamedId kCodecNames[] = {
     {"order1_arithmetic", 0x0017}, {"neural_predictor", 0x0018},
 };
 
+// Built-ins with an Extension Table entry but no wire id (extension/
+// builtins.rs BUILTIN_SPECS: the host-side chain builder and classifiers):
+// the only names a compact table stores under its named tag.
+const char* const kNamedOnly[] = {"production_chains", "classifier_heuristic", "classifier_hf_quant_config",
+                                  "classifier_ptwm_config", "classifier_explicit_flags"};
+// The built-in names: these five, the ops and the codecs above (all of
+// BUILTIN_SPECS, plus huffman_nibble, which has a wire id but no entry).
+constexpr const char* kBuiltinVersion = "1.1.0";  // CURRENT_BUILTIN_VERSION (the crate version)
+
+// CanonicalId::derive (extension/id.rs:21-30) with the built-ins' author key
+// (extension/mod.rs BUILTIN_PUBKEY, 32 bytes of 0xBB)
+void builtin_id(const std::string& name, const std::string& ver, uint8_t out[32]) {
+  std::vector<uint8_t> pre(32, 0xBB);
+  pre.push_back(0);
+  pre.insert(pre.end(), name.begin(), name.end());
+  pre.push_back(0);
+  pre.insert(pre.end(), ver.begin(), ver.end());
+  blake3_hash(pre.data(), pre.size(), out);
+}
+
+// The built-in an Extension Table entry names, as the reference dispatches
+// it (extension/builtins.rs:302-332 normalize_builtin_ids, then the registry
+// by id): an id of a built-in at the current version, or a built-in label
+// "io.ptwm.builtin.<name>@<version>" of another valid version whose id is
+// that version's derivation.  Returns the name, or empty.
+std::string builtin_of(const uint8_t* id, const uint8_t* label, size_t ll) {
+  struct CurrentIds {
+    std::vector<std::pair<std::string, std::array<uint8_t, 32>>> ids;
+    CurrentIds() {
+      std::vector<std::string> names;
+      for (const NamedId& n : kOpNames) names.push_back(n.name);
+      for (const NamedId& n : kCodecNames) names.push_back(n.name);
+      for (const char* n : kNamedOnly) names.push_back(n);
+      for (const std::string& n : names) {
+        std::array<uint8_t, 32> a;
+        builtin_id(n, kBuiltinVersion, a.data());
+        ids.emplace_back(n, a);
+      }
+    }
+  };
+  static const CurrentIds cur;
+  for (const auto& e : cur.ids)
+    if (std::memcmp(e.second.data(), id, 32) == 0) return e.first;
+  static const char kPrefix[] = "io.ptwm.builtin.";
+  const size_t pl = sizeof(kPrefix) - 1;
+  if (ll <= pl || std::memcmp(label, kPrefix, pl) != 0) return std::string();
+  const std::string rest(reinterpret_cast<const char*>(label) + pl, ll - pl);
+  const size_t at = rest.find('@');
+  if (at == std::string::npos) return std::string();
+  const std::string name = rest.substr(0, at), ver = rest.substr(at + 1);
+  // is_valid_builtin_version: non-empty, at most 64 bytes, no '@'
+  if (ver.empty() || ver.size() > 64 || ver.find('@') != std::string::npos || ver == kBuiltinVersion)
+    return std::string();
+  bool known = false;  // a name with an entry (BuiltinRegistry::by_name)
+  for (const auto& e : cur.ids) known |= e.first == name && name != "huffman_nibble";
+  if (!known) return std::string();
+  uint8_t want[32];
+  builtin_id(name, ver, want);
+  return std::memcmp(want, id, 32) == 0 ? name : std::string();
+}
+
 bool known_op(uint64_t id) {
   for (const NamedId& n : kOpNames)
     if (n.id == id) return true;
@@ -241,28 +302,58 @@ struct Chain {
 struct EtEntry {
   int kind = 0;  // 0 other, 1 built-in op, 2 plane codec
   uint16_t id = 0;
+  bool builtin = false;  // a built-in's entry (full-entry form only)
+  bool wasm = false;     // carries an embedded WASM range (full-entry form only)
 };
 
-// Role::write bytes (types/role.rs): parsed for their length.
-bool skip_role(Rd& r) {
+// Role::write bytes (types/role.rs:250-330): parsed for their length, with
+// the value checks of Role::read (ScaleFormat 0..=4, NibbleKind 0..=2, the
+// ValueFormat and ResidualFormat tags).  `coded`: whether the role has a
+// one-byte compact code (chain/wire_compact.rs:439-462 role_code).
+bool skip_role(Rd& r, bool* coded = nullptr) {
   const uint8_t t = r.u8();
+  bool c = false;
   switch (t) {
-    case 0x00: case 0x04: case 0x07: r.u8(); break;             // Scale / Nibble / GlobalScale
-    case 0x01: if (r.u8() == 1) r.u8(); break;                  // Value { Fp4E2m1 | IntN { bits } }
-    case 0x02: case 0x05: r.u8(); r.u8(); break;                // MantissaByte / IntegerByte
-    case 0x03: case 0x08: case 0x09: break;                     // ExponentByte / Raw / Index
-    case 0x06: if (r.u8() == 1) r.u16(); break;                 // Residual { Xor | dtype }
+    case 0x00: case 0x07: if (r.u8() > 4) r.ok = false; c = true; break;   // Scale / GlobalScale
+    case 0x04: if (r.u8() > 2) r.ok = false; c = true; break;              // Nibble
+    case 0x01: {                                                           // Value
+      const uint8_t f = r.u8();
+      if (f == 0) c = true;                                                // Fp4E2m1
+      else if (f == 1) { const uint8_t bits = r.u8(); c = bits >= 1 && bits <= 32; }  // IntN
+      else r.ok = false;
+      break;
+    }
+    case 0x02: case 0x05: {                                                // MantissaByte / IntegerByte
+      const uint8_t index = r.u8(), of = r.u8();
+      c = index < of && of >= 1 && of <= 8;
+      break;
+    }
+    case 0x03: case 0x08: case 0x09: c = true; break;                      // ExponentByte / Raw / Index
+    case 0x06: {                                                           // Residual
+      const uint8_t f = r.u8();
+      if (f == 0) c = true;                                                // Xor
+      else if (f == 1) r.u16();                                            // FloatDelta { dtype }
+      else r.ok = false;
+      break;
+    }
     case 0xFF: { r.u16(); const uint16_t l = r.u16(); r.take(l); break; }  // Vendor
     default: r.ok = false;
   }
+  if (coded) *coded = c;
   return r.ok;
 }
 
-// CW2 one-byte roles (chain/wire_compact.rs:52-66)
+// CW2 one-byte roles (chain/wire_compact.rs:485-535); an escaped role that
+// has a one-byte code is not canonical
 bool skip_compact_role(Rd& r) {
   const uint8_t b = r.u8();
   if (!r.ok) return false;
-  if (b == 0xFF) return skip_role(r);
+  if (b == 0xFF) {
+    bool coded = false;
+    if (!skip_role(r, &coded)) return false;
+    if (coded) r.ok = false;
+    return r.ok;
+  }
   if (b <= 0x04 || (b >= 0x08 && b <= 0x0C) || (b >= 0x10 && b <= 0x12) || (b >= 0x18 && b <= 0x1C)) return true;
   if (b >= 0x40 && b < 0xC0) {  // MantissaByte / IntegerByte: 8 (of - 1) + index, index < of
     const uint32_t k = b & 0x3F, of = k / 8 + 1, index = k % 8;
@@ -291,10 +382,10 @@ bool read_legacy_entry(Rd& r, EtEntry& e) {
   r.u8();  // attestation kind
   r.take(r.u16());
   r.take(r.u16());  // install hint
-  r.u64();
-  r.u64();  // embedded WASM offset / length
+  const uint64_t wasm_off = r.u64(), wasm_len = r.u64();  // embedded WASM offset / length
   if (!r.ok || !valid_utf8(label, ll)) return r.ok = false;
   e = EtEntry{};
+  e.wasm = wasm_off != 0 || wasm_len != 0;
   if (std::memcmp(id, kOwnHuffIlvId, 32) == 0) {
     e.kind = 2;
     e.id = kHuffIlv;
@@ -305,13 +396,9 @@ bool read_legacy_entry(Rd& r, EtEntry& e) {
     e.id = kRansIlv;
     return true;
   }
-  // io.ptwm.builtin.<name>@<version> (extension/mod.rs builtin labels)
-  static const char kPrefix[] = "io.ptwm.builtin.";
-  const size_t pl = sizeof(kPrefix) - 1;
-  if (ll <= pl || std::memcmp(label, kPrefix, pl) != 0) return true;
-  size_t at = pl;
-  while (at < ll && label[at] != '@') ++at;
-  const std::string name(reinterpret_cast<const char*>(label) + pl, at - pl);
+  const std::string name = builtin_of(id, label, ll);
+  if (name.empty()) return true;  // a third-party entry
+  e.builtin = true;
   for (const NamedId& n : kOpNames)
     if (name == n.name) {
       e.kind = 1;
@@ -353,13 +440,22 @@ bool read_compact_table(const uint8_t* p, size_t n, std::vector<EtEntry>& et) {
       et[i].kind = 2;
       et[i].id = (uint16_t)id;
     } else if (tag == 0x03) {
+      // extension/compact_table.rs:198-214: a built-in by name, allowed only
+      // for the built-ins without a wire id (those use their tags)
       const uint64_t l = r.var();
       if (l < 1 || l > 255) return false;
-      r.take((size_t)l);
+      const uint8_t* nm = r.take((size_t)l);
+      if (!r.ok) return false;
+      bool named_only = false;
+      for (const char* n : kNamedOnly) named_only |= std::strlen(n) == l && std::memcmp(n, nm, (size_t)l) == 0;
+      if (!named_only) return false;
     } else if (tag == 0x7F) {
+      // compact_table.rs:215-235: a third-party entry; a built-in's entry or
+      // one with embedded WASM is refused
       const size_t l = r.var_len();
       Rd sub(r.take(l), l);
       if (!r.ok || !read_legacy_entry(sub, et[i]) || !sub.done()) return false;
+      if (et[i].builtin || et[i].wasm) return false;
     } else {
       return false;
     }
@@ -441,6 +537,8 @@ bool read_cw2(Rd& r, bool op_is_wire, const std::vector<EtEntry>* et, const std:
     Edge e{(uint32_t)r.var_max(255), (uint32_t)r.var_max(255), (uint32_t)r.var_max(255), (uint32_t)r.var_max(255)};
     const uint8_t etag = r.u8();
     if (!r.ok || (etag & ~3u)) return false;
+    // the spine's next edge written out (no role, no vendor bytes) is not canonical
+    if (i == spine && etag == 0 && e.src == i && e.src_out == 0 && e.dst == i + 1 && e.dst_in == 0) return false;
     if ((etag & 1u) && !skip_compact_role(r)) return false;
     if (etag & 2u) {
       const uint64_t vl = r.var();
@@ -453,7 +551,12 @@ bool read_cw2(Rd& r, bool op_is_wire, const std::vector<EtEntry>* et, const std:
   for (uint64_t i = 0; i < nt; ++i) {
     const uint8_t ref = r.u8();
     Term t{(uint32_t)(ref >> 4), (uint32_t)(ref & 15u)};
-    if (ref == 0xFF) t = Term{r.u8(), r.u8()};
+    if (ref == 0xFF) {  // escaped (node, output): only when the byte cannot hold them
+      t = Term{r.u8(), r.u8()};
+      if (t.node <= 14 && t.out <= 15) return false;
+    } else if ((ref >> 4) == 15) {
+      return false;  // reserved
+    }
     if (!skip_compact_role(r)) return false;
     c.terms.push_back(t);
   }
@@ -704,7 +807,9 @@ struct PreludeEnt {
 };
 
 // parse_prelude (prelude.rs:65-150); base = file offset of r's start
-bool read_prelude(Rd& r, uint64_t base, std::vector<PreludeEnt>& out) {
+// canonical: the compact container's prelude, whose reserved field and name
+// padding must be zero (container.rs:1569-1580: one encoding per prelude)
+bool read_prelude(Rd& r, uint64_t base, std::vector<PreludeEnt>& out, bool canonical = false) {
   const uint32_t pc = r.u32();
   if (!r.ok || pc > r.left() / 22) return false;  // MIN_ENTRY_BYTES
   out.clear();
@@ -714,12 +819,17 @@ bool read_prelude(Rd& r, uint64_t base, std::vector<PreludeEnt>& out) {
     e.codec = r.u16();
     e.version = r.u8();
     e.mask = r.u8();
-    r.u16();  // reserved
+    const uint16_t reserved = r.u16();
     e.hash = r.u64();
     const uint16_t nl = r.u16();
     const uint8_t* name = r.take(nl);
     if (!r.ok || !known_codec(e.codec) || !valid_utf8(name, nl)) return false;
-    r.take((4 - nl % 4) % 4);
+    const uint8_t* pad = r.take((4 - nl % 4) % 4);
+    if (canonical && r.ok) {
+      if (reserved != 0) return false;
+      for (size_t k = 0; k < (4 - nl % 4) % 4u; ++k)
+        if (pad[k] != 0) return false;
+    }
     e.len = r.u32();
     e.off = base + r.o;
     r.take((size_t)e.len);
@@ -973,6 +1083,47 @@ int64_t read_legacy(const uint8_t* f, size_t n, std::vector<TensorRec>& out, std
 }
 
 // compact tensor record (tensor_record_compact.rs:497-815)
+// Whether metadata bytes are the canonical shape map that a compact record
+// stores as TF_SHAPE instead (metadata.rs:54-68 encode_shape_metadata: a
+// CBOR map of "shape" -> array of at most 64 unsigned ints and "dtype" ->
+// a UTF-8 text string, every head in its shortest form).
+bool is_shape_metadata(const uint8_t* p, size_t n) {
+  Rd r(p, n);
+  const auto head = [&](uint8_t major, uint64_t& v) {
+    const uint8_t b = r.u8();
+    if (!r.ok || (b >> 5) != major) return false;
+    const uint8_t ai = b & 31u;
+    if (ai < 24) {
+      v = ai;
+      return true;
+    }
+    if (ai > 27) return false;
+    const int bytes = 1 << (ai - 24);
+    v = 0;
+    for (int i = 0; i < bytes; ++i) v = (v << 8) | r.u8();
+    if (!r.ok) return false;
+    const uint64_t lo = ai == 24 ? 24 : (1ull << (4 << (ai - 24)));  // shortest form only
+    return v >= lo;
+  };
+  const auto tstr = [&](const char* want) {
+    uint64_t l = 0;
+    if (!head(3, l) || l != std::strlen(want)) return false;
+    const uint8_t* s = r.take((size_t)l);
+    return r.ok && std::memcmp(s, want, (size_t)l) == 0;
+  };
+  uint64_t v = 0;
+  if (!head(5, v) || v != 2 || !tstr("shape")) return false;
+  uint64_t nd = 0;
+  if (!head(4, nd) || nd > 64) return false;
+  for (uint64_t i = 0; i < nd; ++i)
+    if (!head(0, v)) return false;
+  if (!tstr("dtype")) return false;
+  uint64_t l = 0;
+  if (!head(3, l) || l > r.left()) return false;
+  const uint8_t* s = r.take((size_t)l);
+  return r.ok && valid_utf8(s, (size_t)l) && r.done();
+}
+
 void read_compact_record(const uint8_t* f, uint64_t off, uint64_t len, const std::vector<Chain>& reg,
                          const std::vector<EtEntry>& et, TensorRec& t) {
   Rd r(f + off, (size_t)len);
@@ -1007,7 +1158,11 @@ void read_compact_record(const uint8_t* f, uint64_t off, uint64_t len, const std
     }
     have_binding = bound_source_params(shape, t.dtype, binding);
   } else if (tf & 0x20u) {
-    r.take(r.var_len());
+    // tensor_record_compact.rs:563-572: raw metadata that TF_SHAPE stores
+    // is not canonical
+    const size_t ml = r.var_len();
+    const uint8_t* mp = r.take(ml);
+    if (r.ok && is_shape_metadata(mp, ml)) return fail();
   }
   if (!r.ok) return fail();
   if (tf & 0x01u) {
@@ -1023,6 +1178,14 @@ void read_compact_record(const uint8_t* f, uint64_t off, uint64_t len, const std
     Rd cr(r.take(cl), cl);
     if (!r.ok || !read_cw2(cr, false, &iet, have_binding ? &binding : nullptr, false, t.own_chain) || !cr.done())
       return fail();
+    // tensor_record_compact.rs:596-616: the inline table lists transforms
+    // only, in the order the chain first uses them
+    std::vector<uint16_t> first_use;
+    for (const Node& nd : t.own_chain.nodes)
+      if (std::find(first_use.begin(), first_use.end(), nd.op) == first_use.end()) first_use.push_back(nd.op);
+    if (first_use.size() != iet.size()) return fail();
+    for (size_t k = 0; k < iet.size(); ++k)
+      if (iet[k].kind != 1 || iet[k].id != first_use[k]) return fail();
     t.chain = &t.own_chain;
   } else {
     const Chain& rc = reg[(size_t)chain_id];
@@ -1137,7 +1300,7 @@ int64_t read_ptwc(const uint8_t* f, size_t n, std::vector<TensorRec>& out, std::
   if (!read_compact_table(f + hdr_end, (size_t)et_len, et)) return kInvalid;
   // the prelude fills its section exactly
   Rd pr(f + et_end, (size_t)pre_len);
-  if (pre_len && (!read_prelude(pr, et_end, prelude) || !pr.done())) return kInvalid;
+  if (pre_len && (!read_prelude(pr, et_end, prelude, true) || !pr.done())) return kInvalid;
   // registry (ptwc.rs:193-227)
   Rd rg(f + pre_end, (size_t)reg_len);
   const uint64_t nc = rg.var_max(0x8000);

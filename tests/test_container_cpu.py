@@ -16,6 +16,7 @@ import os
 import numpy as np
 import pytest
 
+import oracle as O
 from ptwm_amd import api, plan as P
 from ptwm_amd._native import NativeError
 
@@ -166,3 +167,173 @@ def test_plan_offsets_stay_inside_the_file():
             assert t.out_offset + t.out_len <= out_len
             for p in t.planes:
                 assert p.payload_offset + p.payload_len <= len(data)
+
+
+# ---- canonical forms and built-in ids ------------------------------------------------
+
+def _frame_passthrough():
+    """A one-tensor compact frame (bytes, passthrough chain, Identity plane)
+    and the offset of its CW2 chain, whose canonical bytes are
+    02 01 01 | 00 00 | 30 00 | 01 | 10 c7: two nodes (a bound Source, the
+    byte passthrough), one edge on the implicit spine, one terminal (node 1,
+    output 0, role Value { IntN { 8 } })."""
+    raw = bytes(range(256))
+    f = api.container_write([api.WriteTensor("x", 13, P.CHAIN_PASSTHROUGH, [256], [api.WritePlane(0, raw)])],
+                            layout="frame")
+    cw2 = bytes.fromhex("02010100003000" + "01" + "10c7")
+    at = f.find(cw2)
+    assert at > 0
+    return f, at, len(cw2)
+
+
+@pytest.mark.parametrize("what,chain", [
+    ("spine edge written out", "02010100003000" + "00" + "0000010000" + "10c7"),
+    ("terminal ref escaped needlessly", "02010100003000" + "01" + "ff0100c7"),
+    ("reserved terminal ref byte", "02010100003000" + "01" + "f0c7"),
+    ("role escaped needlessly", "02010100003000" + "01" + "10" + "ff010108"),
+    ("invalid escaped role", "02010100003000" + "01" + "10" + "ff0405"),
+])
+def test_non_canonical_chain_wire_is_refused(what, chain):
+    """chain/wire_compact.rs:339 (spine edge), :352 (terminal escape), the
+    reserved terminal bytes, :528 (role escape) and Role::read's value checks
+    (types/role.rs:283-291): the frame's chain is refused, so the frame is."""
+    f, at, n = _frame_passthrough()
+    api.container_plan(f)
+    bad = f[:at] + bytes.fromhex(chain) + f[at + n:]
+    with pytest.raises(Exception):
+        api.container_plan(bad)
+
+
+def test_escaped_role_without_a_code_is_read():
+    """A role with no one-byte code (Value { IntN { 40 } }) is written
+    escaped: the chain reads (the plane's role just has no decode plan)."""
+    f, at, n = _frame_passthrough()
+    ok = f[:at] + bytes.fromhex("02010100003000" + "01" + "10" + "ff010128") + f[at + n:]
+    _, ents, _ = api.container_plan(ok)
+    assert len(ents) == 1
+
+
+def _ptwc_split(d):
+    o = 11
+    lens = []
+    for _ in range(3):
+        v = sh = 0
+        while True:
+            c = d[o]
+            o += 1
+            v |= (c & 0x7F) << sh
+            sh += 7
+            if not c & 0x80:
+                break
+        lens.append(v)
+    hdr_end = o + 8
+    et = d[hdr_end:hdr_end + lens[0]]
+    pre = d[hdr_end + lens[0]:hdr_end + lens[0] + lens[1]]
+    reg = d[hdr_end + lens[0] + lens[1]:hdr_end + sum(lens)]
+    return d[:11], et, pre, reg, d[hdr_end + sum(lens):]
+
+
+def _var(v):
+    out = bytearray()
+    while True:
+        b = v & 0x7F
+        v >>= 7
+        out.append(b | (0x80 if v else 0))
+        if not v:
+            return bytes(out)
+
+
+def _ptwc_join(head11, et, pre, reg, rest):
+    """A compact container with new sections: the lengths and meta_xxh64
+    (over the header up to it and the three sections, ptwc.rs) recomputed;
+    records follow the registry, so the body is unchanged."""
+    pre_hdr = head11 + _var(len(et)) + _var(len(pre)) + _var(len(reg))
+    meta = O.xxh64(pre_hdr + et + pre + reg)
+    return pre_hdr + meta.to_bytes(8, "little") + et + pre + reg + rest
+
+
+def _with_entries(et, extra):
+    n = et[0]
+    assert n < 0x80
+    return bytes([n + len(extra)]) + et[1:] + b"".join(extra)
+
+
+def _builtin_id(name, version="1.1.0"):
+    return O.blake3(b"\xbb" * 32 + b"\x00" + name.encode() + b"\x00" + version.encode())
+
+
+def _full_entry(cid: bytes, label: str) -> bytes:
+    lb = label.encode()
+    e = cid + len(lb).to_bytes(2, "little") + lb + (2).to_bytes(2, "little") + (1).to_bytes(2, "little") + b"\x01\x02"
+    e += (0).to_bytes(4, "little") + b"\x01" + (0).to_bytes(2, "little") + (0).to_bytes(2, "little") + bytes(16)
+    return b"\x7f" + _var(len(e)) + e
+
+
+def test_compact_table_named_and_full_entries():
+    """extension/compact_table.rs:198-235: a built-in with a wire id stored by
+    name, or a full entry carrying a built-in's id (current or, with its
+    label, another version), is refused; the host-side built-ins by name and
+    a third-party full entry are read."""
+    d = open(os.path.join(FILES, "ptwc_trimmed"), "rb").read()
+    head, et, pre, reg, rest = _ptwc_split(d)
+    assert _ptwc_join(head, et, pre, reg, rest) == d  # the helpers rebuild the file
+    good = [b"\x03" + _var(20) + b"classifier_heuristic",
+            _full_entry(bytes(range(32)), "org.example.codec@1.0.0")]
+    for e in good:
+        _, ents, _ = api.container_plan(_ptwc_join(head, _with_entries(et, [e]), pre, reg, rest))
+        assert ents
+    bad = [b"\x03" + _var(7) + b"huffman",
+           b"\x03" + _var(5) + b"bogus",
+           _full_entry(_builtin_id("huffman"), "anything@1"),
+           _full_entry(_builtin_id("zstd", "1.0.0"), "io.ptwm.builtin.zstd@1.0.0")]
+    for e in bad:
+        with pytest.raises(Exception):
+            api.container_plan(_ptwc_join(head, _with_entries(et, [e]), pre, reg, rest))
+
+
+def test_compact_prelude_reserved_and_padding_must_be_zero():
+    """container.rs:1569-1580: the compact container's prelude is refused
+    unless it is the one encoding of its entries (reserved field and name
+    padding zero)."""
+    d = open(os.path.join(FILES, "ptwc_trimmed"), "rb").read()
+    head, et, pre, reg, rest = _ptwc_split(d)
+    assert pre == b"\x00" * 4
+    state = b"\x01\x02\x03"
+
+    def entry(reserved=0, pad=b"\x00"):
+        e = (7).to_bytes(2, "little") + (4).to_bytes(2, "little") + b"\x00\x01" + reserved.to_bytes(2, "little")
+        e += O.xxh64(state).to_bytes(8, "little") + (3).to_bytes(2, "little") + b"abc" + pad
+        return e + len(state).to_bytes(4, "little") + state
+
+    ok = (1).to_bytes(4, "little") + entry()
+    api.container_plan(_ptwc_join(head, et, ok, reg, rest))
+    for p in ((1).to_bytes(4, "little") + entry(reserved=1), (1).to_bytes(4, "little") + entry(pad=b"\x01")):
+        with pytest.raises(Exception):
+            api.container_plan(_ptwc_join(head, et, p, reg, rest))
+
+
+def test_legacy_builtin_entries_are_recognised_by_id():
+    """A legacy entry is a built-in only by its id (the current version's, or
+    its label's version derivation, extension/builtins.rs:302-332): with the
+    plane codecs' ids changed and their labels kept, no tensor plans (all
+    -5, codecs the device does not know) and the file still opens."""
+    d = bytearray(open(os.path.join(FILES, "legacy_v1_1_0.ptwm"), "rb").read())
+    et_off, et_len = (int.from_bytes(d[k:k + 8], "little") for k in (11, 19))
+    count = int.from_bytes(d[et_off:et_off + 4], "little")
+    o = et_off + 4
+    flipped = 0
+    for _ in range(count):  # flip a bit of every plane codec entry's canonical id
+        ll = int.from_bytes(d[o + 32:o + 34], "little")
+        if int.from_bytes(d[o + 34 + ll:o + 36 + ll], "little") == 2:  # Kind::PlaneCodec
+            d[o] ^= 1
+            flipped += 1
+        p = o + 34 + ll + 6
+        cl = int.from_bytes(d[p:p + 4], "little")
+        p += 4 + cl + 1
+        p += 2 + int.from_bytes(d[p:p + 2], "little")
+        p += 2 + int.from_bytes(d[p:p + 2], "little")
+        o = p + 16
+    assert o == et_off + et_len and flipped > 0
+    d[27:59] = O.blake3(bytes(d[et_off:et_off + et_len]))
+    _, ents, _ = api.container_plan(bytes(d))
+    assert ents and all(e.plan_index == -1 and e.status == -5 for e in ents), [e.status for e in ents]
