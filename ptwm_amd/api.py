@@ -75,19 +75,30 @@ def _dev_ptr_len(t, name: str, device_ordinal: int, stream: int, writable: bool,
         raise TypeError(f"{name}: expected a device tensor")
     if not t.is_contiguous():
         raise ValueError(f"{name}: tensor must be contiguous")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise ValueError(f"{name}: tensor is not on a GPU device")
-    if t.device.index != device_ordinal:
-        raise ValueError(f"{name}: tensor is on device {t.device.index}, call names device {device_ordinal}")
+    dev = t.get_device()
+    if dev != device_ordinal:
+        raise ValueError(f"{name}: tensor is on device {dev}, call names device {device_ordinal}")
     if not ordered:
         _order_after_producer(t, device_ordinal, stream)
-    return int(t.data_ptr()), int(t.numel() * t.element_size())
+    return int(t.data_ptr()), int(t.nbytes)
 
 
 def _resolve_own(selector: str, label: str) -> None:
     got = ids.resolve_codec_selector(selector)
-    if got.hex() != ids.OWN_IDS[label]:
+    if got != _own_id(label):
         raise LookupError(f"selector {selector!r} does not name this library's {label}")
+
+
+def _own_id(label: str) -> bytes:
+    c = _OWN_BYTES.get(label)
+    if c is None:
+        c = _OWN_BYTES[label] = bytes.fromhex(ids.OWN_IDS[label])
+    return c
+
+
+_OWN_BYTES: dict = {}
 
 
 def plane_codec_decode_cuda(selector: str, codec_id: str, state_bytes: bytes, src, dst,
@@ -141,7 +152,7 @@ def hardware_backend_dispatch_decode_cuda(canonical_id: str, codec_id: str, stat
     codec = ids.resolve_codec_selector(codec_id)
     ip, il = _dev_ptr_len(compressed, "compressed", device_ordinal, stream, False)
     op, ol = _dev_ptr_len(out, "out", device_ordinal, stream, True, _both_torch(compressed, out))
-    st = bytes(state_bytes)
+    st = state_bytes if isinstance(state_bytes, bytes) else bytes(state_bytes)
     rc = lib().ptwm_hardware_backend_v1_dispatch_decode_cuda(1, st if st else None, len(st), codec, 32, ip, il, op,
                                                              ol, device_ordinal)
     return check(rc, "hardware_backend_dispatch_decode_cuda")

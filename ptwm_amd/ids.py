@@ -6,7 +6,10 @@ extension/builtins.rs:18-27); the values below are those derivations, and
 tests recompute them.  This extension's own ids use the all-zero author key
 of the reference's in-tree bundles (extensions/*/manifest.toml).
 """
+
 from __future__ import annotations
+
+import functools
 
 BUILTIN_IDS = {
     ("identity", "1.1.0"): "fc2dea1265e3394c57c2df3b868b732ccaa1ee876bd4b1ce27d38f842c6112b5",
@@ -39,10 +42,12 @@ CODEC_RANS_ILV = 0x7F02
 CODEC_NAMES = {"identity": CODEC_IDENTITY, "huffman": CODEC_HUFFMAN, "rans": CODEC_RANS}
 
 
+@functools.lru_cache(maxsize=256)
 def resolve_codec_selector(selector: str) -> bytes:
     """Mirror of extension/resolve.rs:34-75 over the ids known here: a
     ``blake3:<hex>`` or bare 64-hex id, a built-in codec name, or one of
-    this extension's labels."""
+    this extension's labels.  (Results are cached: selectors are a handful
+    of constants, resolved on every device call.)"""
     s = selector.strip()
     hexpart = s[7:] if s.startswith("blake3:") else s
     if len(hexpart) == 64:
