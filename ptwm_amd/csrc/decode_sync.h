@@ -60,6 +60,7 @@ struct ExactRun {
   const uint32_t* wave_job = nullptr;
   const uint32_t* job_wave0 = nullptr;
   uint32_t nw = 0, n_def = 0;
+  uint32_t out_stage = 16384;  // LDS output staging of the write pass, bytes per wavefront
 };
 int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& run);
 int64_t decode_jobs_complete(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& run, bool& rewritten);

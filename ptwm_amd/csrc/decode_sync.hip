@@ -49,8 +49,12 @@ namespace {
 constexpr uint32_t kLanes = 64;
 constexpr uint32_t kSubBytes = kSyncSubBits / 8;
 constexpr uint32_t kWaveBits = kLanes * kSyncSubBits;
-constexpr uint32_t kStageWords = kWaveBits / 32 + 3;  // + the window overrun and the cursor's look-ahead
-constexpr uint32_t kOutStage = 16384;                 // LDS output staging per wavefront
+constexpr uint32_t kStageWords = kWaveBits / 32 + 5;  // + the window overrun and the bit buffer's look-ahead
+// LDS output staging per wavefront of the write pass: chosen per launch
+// from the payloads' expected symbols per wavefront, so that the LDS it
+// takes does not cap the occupancy lower than needed (a wavefront with more
+// output writes it straight to memory)
+constexpr uint32_t kOutStageMax = 16384;
 constexpr uint32_t kMaxFixPasses = 256;
 static_assert(kSyncSubBits % 32 == 0 && (kSyncSubBits / 32) % 2 == 1, "subsequence size");
 
@@ -122,27 +126,37 @@ __device__ inline void stage_wave(const SyncStream& S, uint64_t L0, const uint16
   __syncthreads();
 }
 
-// A bit cursor over the staged span: the position and the three stage words
-// from the one holding it.  A step (two codewords) moves it by at most 22
-// bits, so it crosses at most one word boundary; the word loaded then is
-// needed only after the next crossing, so its LDS latency overlaps the table
-// lookups.
+// A bit reader over the staged span: 64 bits from position p in a register
+// pair (at least 32 valid at the top of each step) and the stage word that
+// follows them, loaded at the previous refill.  A step takes at most 22 bits
+// (two codewords); a refill shifts that word in and loads the next one, so
+// the word a refill consumes has been in flight for at least one step (its
+// LDS latency overlaps the table lookups) and the load lands in the
+// register it is consumed from.
 struct Cursor {
-  uint32_t p, w0, w1, w2;
+  uint64_t buf;
+  uint32_t nb, nxt, nidx, p;
 };
 __device__ inline Cursor cur_open(const uint32_t* stage, uint32_t p) {
-  const uint32_t i = p >> 5;
-  return Cursor{p, stage[i], stage[i + 1], stage[i + 2]};
+  const uint32_t i = p >> 5, sh = p & 31u;
+  Cursor c;
+  c.buf = ((((uint64_t)stage[i + 1]) << 32) | stage[i]) >> sh;
+  c.nb = 64 - sh;
+  c.nxt = stage[i + 2];
+  c.nidx = i + 3;
+  c.p = p;
+  return c;
 }
-__device__ inline uint32_t cur_win(const Cursor& c) { return __builtin_amdgcn_alignbit(c.w1, c.w0, c.p & 31u); }
+__device__ inline uint32_t cur_win(const Cursor& c) { return (uint32_t)c.buf; }
 __device__ inline void cur_adv(Cursor& c, const uint32_t* stage, uint32_t n) {
-  const uint32_t q = c.p + n;
-  if ((q >> 5) != (c.p >> 5)) {
-    c.w0 = c.w1;
-    c.w1 = c.w2;
-    c.w2 = stage[(q >> 5) + 2];
+  c.buf >>= n;
+  c.nb -= n;
+  c.p += n;
+  if (c.nb < 32) {
+    c.buf |= (uint64_t)c.nxt << c.nb;
+    c.nb += 32;
+    c.nxt = stage[c.nidx++];
   }
-  c.p = q;
 }
 
 // Decode from bit p (relative to the staged span) until p >= stop; returns
@@ -155,13 +169,10 @@ __device__ inline uint32_t run(const uint32_t* stage, const uint16_t* tab, uint3
   while (k.p < stop) {
     const uint32_t win = cur_win(k);
     const uint32_t l1 = tab[win & mask] >> 8;
-    if (k.p + l1 >= stop) {
-      cur_adv(k, stage, l1);
-      ++c;
-      break;
-    }
-    cur_adv(k, stage, l1 + (tab[(win >> l1) & mask] >> 8));
-    c += 2;
+    const uint32_t l2 = tab[(win >> l1) & mask] >> 8;  // looked up whether or not it is taken
+    const bool two = k.p + l1 < stop;
+    cur_adv(k, stage, two ? l1 + l2 : l1);
+    c += two ? 2u : 1u;
   }
   cnt = c;
   return k.p;
@@ -181,13 +192,18 @@ __device__ inline uint32_t run_rec(const uint32_t* stage, const uint16_t* tab, u
   for (uint32_t w = 0; w < wi; ++w) bm[w * kLanes + lane] = 0u;
   Cursor k = cur_open(stage, p);
   while (k.p < stop) {
+    const uint32_t p0 = k.p;
     const uint32_t win = cur_win(k);
     const uint32_t l1 = tab[win & mask] >> 8;
-    const bool two = k.p + l1 < stop;
+    const uint32_t l2 = tab[(win >> l1) & mask] >> 8;  // looked up whether or not it is taken
+    const bool two = p0 + l1 < stop;
+    cur_adv(k, stage, two ? l1 + l2 : l1);
+    c += two ? 2u : 1u;
+    // record the starts after the step, so that no lookup waits for a bitmap store
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       if (j && !two) break;
-      const uint32_t rel = (j ? k.p + l1 : k.p) - base, w = rel >> 5;
+      const uint32_t rel = (j ? p0 + l1 : p0) - base, w = rel >> 5;
       if (w != wi) {
         bm[wi * kLanes + lane] = bits;
         wi = w;
@@ -195,8 +211,6 @@ __device__ inline uint32_t run_rec(const uint32_t* stage, const uint16_t* tab, u
       }
       bits |= 1u << (rel & 31u);
     }
-    cur_adv(k, stage, two ? l1 + (tab[(win >> l1) & mask] >> 8) : l1);
-    c += two ? 2u : 1u;
   }
   bm[wi * kLanes + lane] = bits;
   for (uint32_t w = wi + 1; w < kSubWords; ++w) bm[w * kLanes + lane] = 0u;
@@ -390,6 +404,7 @@ __global__ void __launch_bounds__(256) sync_scan_kernel(const SyncStream* __rest
 // Decode again from the settled starts and write symbols [0, n) of the
 // segment; the lane holding symbol n-1 records where it ends.  Symbols are
 // staged in LDS at their output address mod 16, so the store is dwordx4.
+template <uint32_t kOutStage>
 __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__ streams,
                                                         const uint32_t* __restrict__ wave_job,
                                                         const uint32_t* __restrict__ job_wave0,
@@ -425,21 +440,39 @@ __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__
   if (valid && first < S.n) {
     Cursor k = cur_open(stage, (uint32_t)(A.start[g] - L0 * 8));
     const uint32_t m = (uint32_t)std::min<uint64_t>(cnt, S.n - first);
-    uint8_t* const o = out + skew + (first - base);
-    for (uint32_t i = 0; i < m;) {
-      const uint32_t win = cur_win(k);
-      const uint32_t e1 = tab[win & mask], l1 = e1 >> 8;
-      const bool two = i + 1 < m;
-      const uint32_t e2 = two ? tab[(win >> l1) & mask] : 0u;
-      if (staged) {
+    // pairs of symbols with no branch inside the loop (the reader advanced
+    // before the stores, so no step waits for its own stores), the odd last
+    // symbol after it; staged or not is the same for the whole wavefront
+    uint32_t i = 0;
+    if (staged) {
+      uint8_t* const o = out + skew + (first - base);
+      for (; i + 2 <= m; i += 2) {
+        const uint32_t win = cur_win(k);
+        const uint32_t e1 = tab[win & mask], l1 = e1 >> 8;
+        const uint32_t e2 = tab[(win >> l1) & mask];
+        cur_adv(k, stage, l1 + (e2 >> 8));
         o[i] = (uint8_t)e1;
-        if (two) o[i + 1] = (uint8_t)e2;
-      } else {
-        g_st<uint8_t>(S.dst + first + i, (uint8_t)e1);
-        if (two) g_st<uint8_t>(S.dst + first + i + 1, (uint8_t)e2);
+        o[i + 1] = (uint8_t)e2;
       }
-      cur_adv(k, stage, l1 + (e2 >> 8));
-      i += two ? 2u : 1u;
+      if (i < m) {
+        const uint32_t e1 = tab[cur_win(k) & mask];
+        cur_adv(k, stage, e1 >> 8);
+        o[i] = (uint8_t)e1;
+      }
+    } else {
+      for (; i + 2 <= m; i += 2) {
+        const uint32_t win = cur_win(k);
+        const uint32_t e1 = tab[win & mask], l1 = e1 >> 8;
+        const uint32_t e2 = tab[(win >> l1) & mask];
+        cur_adv(k, stage, l1 + (e2 >> 8));
+        g_st<uint8_t>(S.dst + first + i, (uint8_t)e1);
+        g_st<uint8_t>(S.dst + first + i + 1, (uint8_t)e2);
+      }
+      if (i < m) {
+        const uint32_t e1 = tab[cur_win(k) & mask];
+        cur_adv(k, stage, e1 >> 8);
+        g_st<uint8_t>(S.dst + first + i, (uint8_t)e1);
+      }
     }
     if (first + m == S.n) Sp->T = L0 * 8 + k.p;
   }
@@ -532,12 +565,21 @@ __global__ void __launch_bounds__(256) clear_unsettled_kernel(SyncStream* __rest
 
 // Per-stream offsets, the write and the acceptance check (after the fix passes).
 hipError_t sync_finish(hipStream_t s, SyncStream* streams, const uint32_t* d_wave_job, const uint32_t* d_job_wave0,
-                       const uint16_t* tables, const SyncArrays& A, uint32_t nw, uint32_t n_def, uint32_t* status) {
+                       const uint16_t* tables, const SyncArrays& A, uint32_t nw, uint32_t n_def, uint32_t* status,
+                       uint32_t out_stage) {
   hipLaunchKernelGGL(sync_wave_sum_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, A);
   PTWM_HIP_TRY_ERR(hipGetLastError());
   hipLaunchKernelGGL(sync_scan_kernel, dim3(4 * n_def), dim3(256), 0, s, streams, d_job_wave0, A);
   PTWM_HIP_TRY_ERR(hipGetLastError());
-  hipLaunchKernelGGL(sync_write_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables, A);
+  if (out_stage <= 8192)
+    hipLaunchKernelGGL(sync_write_kernel<8192>, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables,
+                       A);
+  else if (out_stage <= 12288)
+    hipLaunchKernelGGL(sync_write_kernel<12288>, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0,
+                       tables, A);
+  else
+    hipLaunchKernelGGL(sync_write_kernel<kOutStageMax>, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job,
+                       d_job_wave0, tables, A);
   PTWM_HIP_TRY_ERR(hipGetLastError());
   hipLaunchKernelGGL(sync_check_kernel, dim3((n_def + kLanes - 1) / kLanes), dim3(kLanes), 0, s, streams, n_def,
                      status);
@@ -558,6 +600,7 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
   std::vector<uint32_t> wave_job, job_wave0, chunk_job, job_chunk0(n_jobs, 0);
   uint64_t subs = 0;
   uint32_t n_def = 0;
+  double out_per_wave = 0;  // expected symbols per wavefront, largest over the parallel-path payloads
   for (size_t j = 0; j < n_jobs; ++j) {
     hj[j].sync_id = 0;
     hj[j].sync_sub0 = 0;
@@ -574,6 +617,7 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
     if (subs + u > 0xFFFFFFFFull || wave_job.size() + waves > 0x7FFFFFFFull) continue;
     hj[j].sync_id = ++n_def;
     hj[j].sync_sub0 = (uint32_t)subs;
+    out_per_wave = std::max(out_per_wave, (double)kWaveBits * (double)hj[j].dst_len / (8.0 * (double)hj[j].src_len));
     job_wave0.push_back((uint32_t)wave_job.size());
     wave_job.insert(wave_job.end(), waves, n_def - 1);
     subs += u;
@@ -623,6 +667,7 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
     A.wave_sum = A.count + subs;
   }
   uint32_t* status = static_cast<uint32_t*>(ctx.status.ptr);
+  run.out_stage = (uint32_t)std::min<double>(kOutStageMax, 1.25 * out_per_wave + 64);
   PTWM_HIP_TRY(launch_decode_exact(d_jobs, status, (uint32_t)n_jobs, streams, tables, d_copy_src, s));
   bool any_zstd = false;
   for (size_t j = 0; j < n_jobs; ++j) any_zstd |= hj[j].codec == kCodecZstd;
@@ -656,7 +701,7 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
                          k ? d_flag + k - 1 : nullptr, d_flag + k);
       PTWM_HIP_TRY(hipGetLastError());
     }
-    PTWM_HIP_TRY(sync_finish(s, streams, d_wave_job, d_job_wave0, tables, A, nw, n_def, status));
+    PTWM_HIP_TRY(sync_finish(s, streams, d_wave_job, d_job_wave0, tables, A, nw, n_def, status, run.out_stage));
   }
   if (any_rans) PTWM_HIP_TRY(hipStreamWaitEvent(s, ctx.side_join, 0));
   PTWM_HIP_TRY(hipMemcpyAsync(ctx.h_status.ptr, status, n_jobs * 4, hipMemcpyDeviceToHost, s));
@@ -716,7 +761,7 @@ int64_t decode_jobs_complete(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun
     for (size_t j = 0; j < n_jobs; ++j)
       if (keep[j] == kStUnsettled) keep[j] = kStDeferred;
     PTWM_HIP_TRY(hipMemcpyAsync(status, keep.data(), n_jobs * 4, hipMemcpyHostToDevice, s));
-    PTWM_HIP_TRY(sync_finish(s, streams, d_wave_job, d_job_wave0, tables, A, nw, n_def, status));
+    PTWM_HIP_TRY(sync_finish(s, streams, d_wave_job, d_job_wave0, tables, A, nw, n_def, status, run.out_stage));
     PTWM_HIP_TRY(hipMemcpyAsync(hs, status, n_jobs * 4, hipMemcpyDeviceToHost, s));
     PTWM_HIP_TRY(hipStreamSynchronize(s));
     for (size_t j = 0; j < n_jobs; ++j)
