@@ -165,6 +165,7 @@ struct SharedHeader {
   uint32_t status;
   uint64_t copy_off;  // for kind 0
   uint32_t max_bits;
+  uint32_t fixed;     // Huffman: every used symbol's code is max_bits long
   uint32_t nw;        // number of weights
   uint64_t seg_src[4];
   uint64_t seg_len[4];
@@ -356,8 +357,12 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
       // with the overflow checks the serial assignment makes; then, per
       // length, the first index into the symbols sorted by (length,
       // symbol) and the end of its left-aligned code range
+      h.fixed = 0;
       if (st == kStOk) {
         counts[0] = 0;
+        uint32_t shorter = 0;
+        for (uint32_t b = 1; b < maxb; ++b) shorter += counts[b];
+        h.fixed = shorter == 0;
         uint32_t code = 0, base = 0;
         for (uint32_t b = 1; b <= maxb; ++b) {
           code = ((code + counts[b - 1]) << 1) & 0xFFFF;
@@ -430,7 +435,8 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
         S.job = blockIdx.x;
         S.first_sub = sub;
         S.n_sub = (uint32_t)((h.seg_len[lane] * 8 + kSyncSubBits - 1) / kSyncSubBits);
-        S.max_bits = max_bits;
+        S.max_bits = (uint16_t)max_bits;
+        S.fixed_len = h.fixed ? (uint16_t)max_bits : (uint16_t)0;
         S.table = d;
         S.pad = 0;
         sync_streams[4ull * d + lane] = S;

@@ -23,7 +23,8 @@ struct SyncStream {
   uint32_t job;        // index into the job / status arrays
   uint32_t first_sub;  // global slot of the stream's subsequence 0
   uint32_t n_sub;      // ceil(8 m / kSyncSubBits)
-  uint32_t max_bits;   // decode table width
+  uint16_t max_bits;   // decode table width
+  uint16_t fixed_len;  // every code max_bits long (a fixed-length code): max_bits, else 0
   uint32_t table;      // deferred payload slot (decode table index)
   uint32_t pad;
 };

@@ -289,6 +289,23 @@ __global__ void __launch_bounds__(64) sync_pass_kernel(const SyncStream* __restr
   if (s < 0) return;
   const SyncStream S = streams[4ull * d + s];
   const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
+  if (S.fixed_len) {
+    // a fixed-length code: codeword starts are the multiples of its length,
+    // so each lane's start, count and exit are arithmetic (and the wavefronts
+    // agree with their neighbours: nothing to settle)
+    const uint32_t lane = threadIdx.x, L = S.fixed_len, k = w * kLanes + lane;
+    if (k < S.n_sub) {
+      const uint64_t a0 = L0 * 8 + (uint64_t)lane * kSyncSubBits;
+      const uint64_t stop = a0 + kSyncSubBits;
+      const uint64_t st = (a0 + L - 1) / L * L;
+      const uint64_t n = st < stop ? (stop - st + L - 1) / L : 0;
+      const uint64_t g = (uint64_t)S.first_sub + k;
+      A.start[g] = st;
+      A.exit[g] = st + n * L;
+      A.count[g] = (uint32_t)n;
+    }
+    return;
+  }
   stage_wave(S, L0, tables, stage, tab);
   const uint32_t lane = threadIdx.x, mask = (1u << S.max_bits) - 1;
   const uint32_t k = w * kLanes + lane;
@@ -437,7 +454,28 @@ __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__
   const bool staged = wave_len <= kOutStage;
   const uint64_t gA = S.dst + base, gB = S.dst + wave_end;
   const uint32_t skew = (uint32_t)(gA & 15u);
-  if (valid && first < S.n) {
+  if (valid && first < S.n && S.fixed_len) {
+    // fixed-length code: symbol i starts at start + i L, so the lookups do
+    // not depend on each other
+    const uint32_t L = S.fixed_len, p0 = (uint32_t)(A.start[g] - L0 * 8);
+    const uint32_t m = (uint32_t)std::min<uint64_t>(cnt, S.n - first);
+    if (staged) {
+      uint8_t* const o = out + skew + (first - base);
+#pragma unroll 4
+      for (uint32_t i = 0; i < m; ++i) {
+        const uint32_t p = p0 + i * L, wi = p >> 5;
+        o[i] = (uint8_t)tab[__builtin_amdgcn_alignbit(stage[wi + 1], stage[wi], p & 31u) & mask];
+      }
+    } else {
+#pragma unroll 4
+      for (uint32_t i = 0; i < m; ++i) {
+        const uint32_t p = p0 + i * L, wi = p >> 5;
+        g_st<uint8_t>(S.dst + first + i,
+                      (uint8_t)tab[__builtin_amdgcn_alignbit(stage[wi + 1], stage[wi], p & 31u) & mask]);
+      }
+    }
+    if (first + m == S.n) Sp->T = L0 * 8 + p0 + m * L;
+  } else if (valid && first < S.n) {
     Cursor k = cur_open(stage, (uint32_t)(A.start[g] - L0 * 8));
     const uint32_t m = (uint32_t)std::min<uint64_t>(cnt, S.n - first);
     // pairs of symbols with no branch inside the loop (the reader advanced

@@ -89,10 +89,24 @@ def _streams_start(payload: bytes) -> int:
     return 5 + used + 16
 
 
-def test_parallel_huffman_malformed_matches_reference_outcome():
+def _fixed_length_code(payload: bytes) -> bool:
+    lengths = [w for w in O.huf_decode_weights(payload[5:])[0] if w]
+    return len(set(lengths)) == 1
+
+
+@pytest.mark.parametrize("kind", ["geometric", "uniform16"])
+def test_parallel_huffman_malformed_matches_reference_outcome(kind):
+    """Malformed payloads of a variable-length code, and of a fixed-length one
+    (16 near-equiprobable symbols: every code 4 bits, whose codeword starts
+    the parallel path computes instead of finding), decode or fail exactly as
+    the reference decoder."""
     rng = np.random.default_rng(99)
-    base = rng.geometric(0.25, 200_000).clip(0, 255).astype(np.uint8).tobytes()
+    if kind == "geometric":
+        base = rng.geometric(0.25, 200_000).clip(0, 255).astype(np.uint8).tobytes()
+    else:
+        base = rng.integers(0, 16, 200_000).astype(np.uint8).tobytes()
     payload = O.codec_encode(O.CODEC_HUFFMAN, base)
+    assert payload[0] == 1 and _fixed_length_code(payload) == (kind == "uniform16")
     s0 = _streams_start(payload)
     jump = struct.unpack_from("<4I", payload, s0 - 16)
     cases = []
