@@ -240,11 +240,7 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
                                                           uint16_t* __restrict__ sync_tables,
                                                           uint64_t* __restrict__ copy_src) {
   __shared__ SharedHeader h;
-  __shared__ uint16_t counts[kHufMaxBits + 1];
-  __shared__ uint16_t next_code[kHufMaxBits + 1];
   __shared__ uint16_t rev[256];
-  __shared__ uint16_t sym_base[kHufMaxBits + 1];   // Huffman: first index of each length in sorted_sym
-  __shared__ uint32_t code_end[kHufMaxBits + 1];   // Huffman: end of each length's left-aligned codes
   __shared__ uint8_t sorted_sym[256];              // Huffman: symbols by (length, symbol)
   // rANS: {freq | sym << 24, slot - start} per slot; tANS: one u32 per slot;
   // Huffman: (len << 8) | sym per window
@@ -332,15 +328,18 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
     const bool over = w[0] > (uint32_t)kHufMaxBits || w[1] > (uint32_t)kHufMaxBits ||
                       w[2] > (uint32_t)kHufMaxBits || w[3] > (uint32_t)kHufMaxBits;
     if (__ballot(over) != 0) st = kStBadHeader;
-    uint32_t maxb = st == kStOk ? std::max(std::max(w[0], w[1]), std::max(w[2], w[3])) : 0u;
-    for (int o = 32; o >= 1; o >>= 1) maxb = std::max(maxb, (uint32_t)__shfl_xor((int)maxb, o, 64));
-    if (st == kStOk && maxb == 0) st = kStBadHeader;  // no symbol has a code
-    if (maxb < 1) maxb = 1;
-    // rank of each of the lane's symbols among the lower symbols of its length
+    // Per length: the symbol count (wave-uniform) and the rank of each of
+    // the lane's symbols among the lower symbols of that length, from four
+    // ballots.  Everything derived from the counts below is wave-uniform and
+    // stays in scalar registers (constant indices in unrolled loops): no LDS
+    // round trips and no serial lane-0 pass.
+    uint32_t cnt[kHufMaxBits + 1];
     uint32_t rank[4] = {0, 0, 0, 0};
-    if (st == kStOk) {
+    cnt[0] = 0;
+    {
       const uint64_t below = (1ull << lane) - 1ull;
-      for (uint32_t l = 1; l <= maxb; ++l) {
+#pragma unroll
+      for (uint32_t l = 1; l <= (uint32_t)kHufMaxBits; ++l) {
         const uint64_t m0 = __ballot(w[0] == l), m1 = __ballot(w[1] == l), m2 = __ballot(w[2] == l),
                        m3 = __ballot(w[3] == l);
         const uint32_t r = __popcll(m0 & below) + __popcll(m1 & below) + __popcll(m2 & below) + __popcll(m3 & below);
@@ -349,30 +348,45 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
         if (w[1] == l) rank[1] = r + e0;
         if (w[2] == l) rank[2] = r + e0 + e1;
         if (w[3] == l) rank[3] = r + e0 + e1 + e2;
-        if (lane == 0) counts[l] = (uint16_t)(__popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3));
+        cnt[l] = __popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3);
       }
     }
-    if (lane == 0) {
-      // canonical codes (tree.rs:119-141): the first code of each length,
-      // with the overflow checks the serial assignment makes; then, per
-      // length, the first index into the symbols sorted by (length,
-      // symbol) and the end of its left-aligned code range
-      h.fixed = 0;
-      if (st == kStOk) {
-        counts[0] = 0;
-        uint32_t shorter = 0;
-        for (uint32_t b = 1; b < maxb; ++b) shorter += counts[b];
-        h.fixed = shorter == 0;
-        uint32_t code = 0, base = 0;
-        for (uint32_t b = 1; b <= maxb; ++b) {
-          code = ((code + counts[b - 1]) << 1) & 0xFFFF;
-          if (code > (1u << b) || (counts[b] && code + counts[b] - 1 >= (1u << b))) { st = kStBadHeader; break; }
-          next_code[b] = (uint16_t)code;
-          sym_base[b] = (uint16_t)base;
-          base += counts[b];
-          code_end[b] = (code + counts[b]) << (maxb - b);
+    uint32_t maxb = 0;
+#pragma unroll
+    for (uint32_t l = 1; l <= (uint32_t)kHufMaxBits; ++l)
+      if (cnt[l]) maxb = l;
+    if (st == kStOk && maxb == 0) st = kStBadHeader;  // no symbol has a code
+    if (maxb < 1) maxb = 1;
+    // canonical codes (tree.rs:119-141): the first code of each length, with
+    // the overflow checks the serial assignment makes; per length the offset
+    // from a code to its symbol's index in the symbols sorted by (length,
+    // symbol), and the end of its left-aligned code range (the ends rise
+    // with the length)
+    uint32_t sym_base[kHufMaxBits + 1], sym_off[kHufMaxBits + 1], code_end[kHufMaxBits + 1];
+    uint32_t end_max = 0, shorter = 0;
+    {
+      uint32_t code = 0, base = 0;
+      bool bad = false;
+#pragma unroll
+      for (uint32_t b = 1; b <= (uint32_t)kHufMaxBits; ++b) {
+        sym_base[b] = 0;
+        sym_off[b] = 0;
+        code_end[b] = 0;
+        if (b <= maxb) {
+          code = ((code + cnt[b - 1]) << 1) & 0xFFFF;
+          bad |= code > (1u << b) || (cnt[b] && code + cnt[b] - 1 >= (1u << b));
+          sym_base[b] = base;
+          sym_off[b] = base - code;
+          base += cnt[b];
+          code_end[b] = (code + cnt[b]) << (maxb - b);
+          if (b == maxb) end_max = code_end[b];
+          if (b < maxb) shorter += cnt[b];
         }
       }
+      if (st == kStOk && bad) st = kStBadHeader;
+    }
+    if (lane == 0) {
+      h.fixed = st == kStOk && shorter == 0;
       // jump table and segment streams (decompress.rs:14-48)
       uint64_t pos = hb + (n + 1) / 2;
       if (st == kStOk && enc_len - pos < 16) st = kStBadHeader;
@@ -389,29 +403,39 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
       h.status = st;
       h.max_bits = maxb;
     }
+    if (st == kStOk) {
+#pragma unroll
+      for (uint32_t k = 0; k < 4; ++k) {
+        uint32_t sb = 0;
+#pragma unroll
+        for (uint32_t b = 1; b <= (uint32_t)kHufMaxBits; ++b)
+          if (w[k] == b) sb = sym_base[b];
+        if (w[k]) sorted_sym[sb + rank[k]] = (uint8_t)(4 * lane + k);
+      }
+    }
     __syncthreads();
     if (h.status != kStOk) {
       if (lane == 0) status[blockIdx.x] = h.status;
       return;
     }
-#pragma unroll
-    for (uint32_t k = 0; k < 4; ++k)
-      if (w[k]) sorted_sym[sym_base[w[k]] + rank[k]] = (uint8_t)(4 * lane + k);
-    __syncthreads();
     // table: index i holds the next max_bits stream bits, first bit lowest;
     // reversed, it is the left-aligned code value v, whose length is the
-    // first whose code range ends above v (the ranges rise with the length)
-    const uint32_t max_bits = h.max_bits;
+    // first whose code range ends above v
+    const uint32_t max_bits = maxb;
     const uint32_t tsize = 1u << max_bits;
     const uint16_t fallback = (uint16_t)(max_bits << 8);
     for (uint32_t i = lane; i < tsize; i += 64) {
       const uint32_t v = __builtin_bitreverse32(i) >> (32 - max_bits);
       uint16_t e = fallback;
-      if (v < code_end[max_bits]) {
-        uint32_t l = 1;
-        for (uint32_t b = 1; b < max_bits; ++b) l += v >= code_end[b];
-        const uint32_t c = v >> (max_bits - l);
-        e = (uint16_t)((l << 8) | sorted_sym[sym_base[l] + (c - next_code[l])]);
+      if (v < end_max) {
+        uint32_t l = 1, off = sym_off[1];
+#pragma unroll
+        for (uint32_t b = 1; b < (uint32_t)kHufMaxBits; ++b)
+          if (b < max_bits && v >= code_end[b]) {
+            l = b + 1;
+            off = sym_off[b + 1];
+          }
+        e = (uint16_t)((l << 8) | sorted_sym[(v >> (max_bits - l)) + off]);
       }
       table16[i] = e;
     }
