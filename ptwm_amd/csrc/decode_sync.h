@@ -19,7 +19,7 @@ struct SyncStream {
   uint64_t m;          // stream bytes
   uint64_t dst;        // device address of the segment's first output byte
   uint64_t n;          // symbols of the segment (split_four of orig_len)
-  uint64_t T;          // bit position after symbol n-1 (write kernel); ~0 if not reached
+  uint64_t T;          // (unused)
   uint32_t job;        // index into the job / status arrays
   uint32_t first_sub;  // global slot of the stream's subsequence 0
   uint32_t n_sub;      // ceil(8 m / kSyncSubBits)
@@ -51,6 +51,10 @@ struct SyncArrays {
   uint32_t* count;        // symbols decoded from start to exit
   uint32_t* wave_sum;     // per launched wavefront: symbols of its 64 subsequences
   uint64_t* wave_prefix;  // per launched wavefront: symbols of the stream before it
+  uint32_t* verdict;      // per deferred payload: its streams' verdict bits
+  uint64_t* pub;          // per launched wavefront: look-back slot, (epoch << 8) | last exit past the span
+  uint64_t epoch;         // this launch's look-back tag
+  uint32_t look_back;     // 0: the first pass does not look back (a test mode)
 };
 struct ExactRun {
   const DecodeJob* jobs = nullptr;
@@ -72,8 +76,9 @@ constexpr uint64_t kCopyDeferMin = 4096;
 // Output bytes per workgroup of that copy: small payloads in small pieces
 // (enough workgroups to fill the device), large ones in 64 KiB pieces.
 __host__ __device__ inline uint64_t copy_chunk(uint64_t len) { return len >= (8ull << 20) ? 65536ull : 8192ull; }
-// Fix passes queued after the first pass of the parallel Huffman decode.
-constexpr uint32_t kFixQueued = 4;
+// Fix passes queued after the first pass of the parallel Huffman decode
+// (the first pass's look-back leaves them little to do).
+constexpr uint32_t kFixQueued = 1;
 
 // exact-path kernel launch (decode_exact.hip); copy_src (may be null): per
 // job, the source of a deferred stored-bytes copy (0: none)

@@ -9,20 +9,25 @@
 //   pass 1   each lane decodes from its subsequence's first bit up to the
 //            first codeword boundary at or past its end (its "exit"); lanes
 //            of a wavefront then restart from their left neighbour's exit
-//            until no start changes (sync_pass_kernel);
-//   fix      the same across wavefronts, repeated until no wavefront's first
-//            start differs from the previous wavefront's last exit
-//            (sync_fix_kernel; a fixed number of passes is queued, each pass
-//            skipping its work when the one before changed nothing; no host
-//            round trip: a payload still unsettled after them is caught by
-//            the wave-sum pass and reported, and the host queues more);
+//            until no start changes; the wavefront publishes its last exit,
+//            takes the previous wavefront's (look-back) and restarts its
+//            first lane there (sync_pass_kernel; its last workgroups copy
+//            stored payloads);
+//   fix      the same across wavefronts: a wavefront whose first start
+//            differs from the previous wavefront's last exit restarts there
+//            (sync_fix_kernel; kFixQueued passes are queued with no host
+//            round trip, each skipping its work when the one before changed
+//            nothing; a fix of the last of them that moves a wavefront's
+//            last exit marks the stream unsettled, and the host queues more
+//            passes, checking in between);
 //   scan     per stream, symbol counts -> output offsets (sync_scan_kernel);
 //   write    each lane decodes its subsequence again and writes the symbols
-//            (staged in LDS, stored coalesced), recording where symbol n-1
-//            ends (sync_write_kernel);
-//   check    the payload is accepted here only when, for all four streams,
-//            that end T satisfies ceil(T / 8) == stream bytes and the bits
-//            after T are zero (sync_check_kernel).
+//            (staged in LDS, stored coalesced) (sync_write_kernel);
+//   verdict  the payload is accepted here only when, for all four streams,
+//            the end T of symbol n-1 satisfies ceil(T / 8) == stream bytes
+//            and the bits after T are zero: the write pass's lane holding
+//            symbol n-1 judges its stream (the scan judges a stream without
+//            one), and the fourth verdict sets the payload's status.
 // Under that condition the reference reader (BitReader, decode_symbol,
 // decode_stream_tail) never lets its bit counter wrap and always indexes the
 // table with real stream bits, so it produces exactly the zero-padded
@@ -39,6 +44,7 @@
 #include "decode_sync.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -248,12 +254,11 @@ __device__ inline void run_join(const uint32_t* stage, const uint16_t* tab, uint
 
 // Lanes restart from their left neighbour's exit until no start changes (at
 // most 63 rounds: each round fixes at least one more lane).  With a bitmap
-// (bm non-null; bm_ok: it holds the lane's current path) a restart stops
-// where it joins the old path; a lane's later restarts run in full and
-// record again.
+// (bm non-null; bm_ok: it holds the lane's current path, updated here) a
+// restart stops where it joins the old path; a lane's later restarts run in
+// full and record again.
 __device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32_t mask, bool valid, uint32_t& st,
-                              uint32_t& ex, uint32_t& cnt, bool& changed, uint32_t* bm = nullptr,
-                              bool bm_ok = false) {
+                              uint32_t& ex, uint32_t& cnt, bool& changed, uint32_t* bm, bool& bm_ok) {
   const uint32_t lane = threadIdx.x;
   const uint32_t base = lane * kSyncSubBits, stop = base + kSyncSubBits;
   for (uint32_t round = 0; round < kLanes; ++round) {
@@ -275,74 +280,177 @@ __device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32
     }
   }
 }
+__device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32_t mask, bool valid, uint32_t& st,
+                              uint32_t& ex, uint32_t& cnt, bool& changed) {
+  bool no_bm = false;
+  settle(stage, tab, mask, valid, st, ex, cnt, changed, nullptr, no_bm);
+}
 
+// Stored bytes the exact kernel deferred (copy_src[j] != 0): output bytes
+// [a, b) of job J, by nt threads.  Aligned dword stores; the source is
+// realigned with a funnel shift of two aligned words, used only where both
+// words hold source bytes.
+__device__ inline void copy_range(const DecodeJob& J, uint64_t s, uint64_t a, uint64_t b, uint32_t t, uint32_t nt) {
+  const uint64_t ba = J.dst + a, bb = J.dst + b;
+  const uint64_t lo = std::min<uint64_t>((ba + 3) & ~3ull, bb);
+  const uint64_t hi = std::max<uint64_t>(bb & ~3ull, lo);
+  for (uint64_t x = ba + t; x < lo; x += nt) g_st<uint8_t>(x, g_ld<uint8_t>(s + (x - J.dst)));
+  for (uint64_t x = hi + t; x < bb; x += nt) g_st<uint8_t>(x, g_ld<uint8_t>(s + (x - J.dst)));
+#pragma unroll 4
+  for (uint64_t x = lo + 4ull * t; x < hi; x += 4ull * nt) {
+    const uint64_t o = x - J.dst;
+    if (o + 5 <= J.dst_len) {
+      const uint64_t S = s + o;
+      const uint64_t sa = S & ~3ull;
+      g_st<uint32_t>(x, __builtin_amdgcn_alignbyte(g_ld<uint32_t>(sa + 4), g_ld<uint32_t>(sa), (uint32_t)(S & 3u)));
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) g_st<uint8_t>(x + k, g_ld<uint8_t>(s + o + k));
+    }
+  }
+}
+
+// Deferred stored-bytes copies as workgroups of `parts` pieces per
+// copy_chunk(len) of output: piece i of the launch's copy range.
+struct CopyArgs {
+  const DecodeJob* jobs;
+  const uint64_t* copy_src;
+  const uint32_t* chunk_job;
+  const uint32_t* job_chunk0;
+};
+__device__ inline void copy_piece(const CopyArgs& C, uint32_t i, uint32_t parts, uint32_t t, uint32_t nt) {
+  const uint32_t c = i / parts, q = i % parts;
+  const uint32_t j = C.chunk_job[c];
+  const uint64_t s = C.copy_src[j];
+  if (s == 0) return;
+  const DecodeJob J = C.jobs[j];
+  const uint64_t cs = copy_chunk(J.dst_len), ps = cs / parts;
+  const uint64_t a = (uint64_t)(c - C.job_chunk0[j]) * cs + q * ps;
+  const uint64_t b = std::min<uint64_t>(J.dst_len, a + ps);
+  if (a < b) copy_range(J, s, a, b, t, nt);
+}
+
+__global__ void __launch_bounds__(256) raw_copy_kernel(CopyArgs C) { copy_piece(C, blockIdx.x, 1, threadIdx.x, 256); }
+
+__device__ inline uint32_t wave_total(uint32_t c) {
+  for (int o = 32; o >= 1; o >>= 1) c += (uint32_t)__shfl_xor((int)c, o, 64);
+  return c;
+}
+
+// The previous wavefront of the stream publishes where its last lane's path
+// leaves its span: pub[wavefront] = (epoch << 8) | (exit - span end), the
+// overrun of a codeword (< kHufMaxBits bits).  A reader waits for it at most
+// kLookBackTicks of the 100 MHz clock; without it the fix pass does the work.
+constexpr uint64_t kLookBackTicks = 2000;
+__device__ inline bool look_back(const uint64_t* pub, uint32_t wave, uint64_t epoch, uint32_t& rel) {
+  const uint64_t t_end = __builtin_amdgcn_s_memrealtime() + kLookBackTicks;
+  for (;;) {
+    const uint64_t v = __hip_atomic_load(pub + wave, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    const uint64_t u = ((uint64_t)hi << 32) | lo;
+    if ((u >> 8) == epoch) {
+      rel = (uint32_t)(u & 0xFFu);
+      return true;
+    }
+    if (__builtin_amdgcn_s_memrealtime() > t_end) return false;
+    __builtin_amdgcn_s_sleep(4);
+  }
+}
+
+// First pass.  Each lane decodes its subsequence, recording its codeword
+// starts; the lanes settle; the wavefront publishes its last exit, takes
+// the previous wavefront's (look-back), restarts its first lane there (a
+// join on the recorded path) and settles again.  Workgroups past the
+// wavefronts copy deferred stored bytes (four per copy piece).
 __global__ void __launch_bounds__(64) sync_pass_kernel(const SyncStream* __restrict__ streams,
                                                        const uint32_t* __restrict__ wave_job,
                                                        const uint32_t* __restrict__ job_wave0,
-                                                       const uint16_t* __restrict__ tables, SyncArrays A) {
+                                                       const uint16_t* __restrict__ tables, SyncArrays A,
+                                                       uint32_t nw, CopyArgs C) {
   __shared__ uint16_t tab[kSyncTableEntries];
   __shared__ uint32_t stage[kStageWords];
   __shared__ uint32_t bm[kSubWords * kLanes];
+  if (blockIdx.x >= nw) {
+    copy_piece(C, blockIdx.x - nw, 4, threadIdx.x, kLanes);
+    return;
+  }
   const uint32_t d = wave_job[blockIdx.x];
   uint32_t w = blockIdx.x - job_wave0[d];
   const int s = locate(streams + 4ull * d, w);
   if (s < 0) return;
   const SyncStream S = streams[4ull * d + s];
   const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
+  const uint32_t lane = threadIdx.x, k = w * kLanes + lane;
+  const bool valid = k < S.n_sub;
+  const uint64_t g = (uint64_t)S.first_sub + k;
   if (S.fixed_len) {
     // a fixed-length code: codeword starts are the multiples of its length,
     // so each lane's start, count and exit are arithmetic (and the wavefronts
     // agree with their neighbours: nothing to settle)
-    const uint32_t lane = threadIdx.x, L = S.fixed_len, k = w * kLanes + lane;
-    if (k < S.n_sub) {
+    const uint32_t L = S.fixed_len;
+    uint32_t n = 0;
+    if (valid) {
       const uint64_t a0 = L0 * 8 + (uint64_t)lane * kSyncSubBits;
       const uint64_t stop = a0 + kSyncSubBits;
       const uint64_t st = (a0 + L - 1) / L * L;
-      const uint64_t n = st < stop ? (stop - st + L - 1) / L : 0;
-      const uint64_t g = (uint64_t)S.first_sub + k;
+      n = st < stop ? (uint32_t)((stop - st + L - 1) / L) : 0u;
       A.start[g] = st;
-      A.exit[g] = st + n * L;
-      A.count[g] = (uint32_t)n;
+      A.exit[g] = st + (uint64_t)n * L;
+      A.count[g] = n;
     }
+    const uint32_t tot = wave_total(n);
+    if (lane == 0) A.wave_sum[blockIdx.x] = tot;
     return;
   }
   stage_wave(S, L0, tables, stage, tab);
-  const uint32_t lane = threadIdx.x, mask = (1u << S.max_bits) - 1;
-  const uint32_t k = w * kLanes + lane;
-  const bool valid = k < S.n_sub;
+  const uint32_t mask = (1u << S.max_bits) - 1;
   uint32_t st = lane * kSyncSubBits, cnt = 0, ex = st;
   if (valid) ex = run_rec(stage, tab, mask, st, st, st + kSyncSubBits, cnt, bm);
-  bool changed = false;
-  settle(stage, tab, mask, valid, st, ex, cnt, changed, bm, valid);
+  bool changed = false, bm_ok = valid;
+  settle(stage, tab, mask, valid, st, ex, cnt, changed, bm, bm_ok);
+  if (lane == kLanes - 1 && valid && k + 1 < S.n_sub)
+    __hip_atomic_store(A.pub + blockIdx.x, (A.epoch << 8) | (uint64_t)(ex - kWaveBits), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t rel = 0;
+  if (w > 0 && A.look_back && look_back(A.pub, blockIdx.x - 1, A.epoch, rel) && rel != 0 && rel < kSyncSubBits) {
+    // the true first start lies rel bits into the span: lane 0 joins its
+    // recorded path from there (it never restarted, so the bitmap is its
+    // path), and a changed exit propagates as in the first settle
+    if (lane == 0) {
+      st = rel;
+      run_join(stage, tab, mask, 0, st, kSyncSubBits, ex, cnt, bm);
+      bm_ok = false;
+    }
+    settle(stage, tab, mask, valid, st, ex, cnt, changed, bm, bm_ok);
+  }
   if (valid) {
-    const uint64_t g = (uint64_t)S.first_sub + k;
     A.start[g] = L0 * 8 + st;
     A.exit[g] = L0 * 8 + ex;
     A.count[g] = cnt;
   }
+  const uint32_t tot = wave_total(valid ? cnt : 0u);
+  if (lane == 0) A.wave_sum[blockIdx.x] = tot;
 }
 
-// One fix pass: a wavefront whose first start differs from the previous
-// wavefront's last exit restarts from it and settles again.
-__global__ void __launch_bounds__(64) sync_fix_kernel(const SyncStream* __restrict__ streams,
-                                                      const uint32_t* __restrict__ wave_job,
-                                                      const uint32_t* __restrict__ job_wave0,
-                                                      const uint16_t* __restrict__ tables, SyncArrays A,
-                                                      const uint32_t* __restrict__ prev_flag,
-                                                      uint32_t* __restrict__ flag) {
-  __shared__ uint16_t tab[kSyncTableEntries];
-  __shared__ uint32_t stage[kStageWords];
-  // the previous pass (queued before this one) changed nothing: settled
-  if (prev_flag && g_ld<uint32_t>(reinterpret_cast<uint64_t>(prev_flag)) == 0) return;
-  const uint32_t d = wave_job[blockIdx.x];
-  uint32_t w = blockIdx.x - job_wave0[d];
+// Fix passes: a wavefront whose first start differs from the previous
+// wavefront's last exit restarts from it and settles again.  A workgroup
+// checks 64 wavefronts at once (a lane each) and fixes those that need it.
+// With mark 1 (the last pass queued without a host check), a fix that moves
+// a wavefront's last exit marks the stream unsettled: the next wavefront
+// may have been checked against the old exit.  With mark 2 any fix does (a
+// test mode that drives the host's extra passes).
+__device__ inline void fix_wave(SyncStream* __restrict__ streams, const uint32_t* __restrict__ wave_job,
+                                const uint32_t* __restrict__ job_wave0, const uint16_t* __restrict__ tables,
+                                const SyncArrays& A, uint32_t wl, uint32_t mark, uint32_t* tab32, uint32_t* stage) {
+  uint16_t* const tab = reinterpret_cast<uint16_t*>(tab32);
+  const uint32_t d = wave_job[wl];
+  uint32_t w = wl - job_wave0[d];
   const int s = locate(streams + 4ull * d, w);
-  if (s < 0 || w == 0) return;
   const SyncStream S = streams[4ull * d + s];
   const uint64_t g0 = (uint64_t)S.first_sub + (uint64_t)w * kLanes;
   const uint64_t prev_exit = A.exit[g0 - 1];
-  if (prev_exit == A.start[g0]) return;
   const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
+  __syncthreads();  // the previous wavefront's reads of the staged span are done
   stage_wave(S, L0, tables, stage, tab);
   const uint32_t lane = threadIdx.x, mask = (1u << S.max_bits) - 1;
   const uint32_t k = w * kLanes + lane;
@@ -353,6 +461,7 @@ __global__ void __launch_bounds__(64) sync_fix_kernel(const SyncStream* __restri
     ex = (uint32_t)(A.exit[g0 + lane] - L0 * 8);
     cnt = A.count[g0 + lane];
   }
+  const uint32_t ex_before = ex;
   bool changed = false;
   if (lane == 0) {  // prev_exit lies in [L0 * 8, L0 * 8 + 11): a codeword overruns by < 11 bits
     st = (uint32_t)std::min<uint64_t>(prev_exit - L0 * 8, kSyncSubBits);
@@ -365,34 +474,73 @@ __global__ void __launch_bounds__(64) sync_fix_kernel(const SyncStream* __restri
     A.exit[g0 + lane] = L0 * 8 + ex;
     A.count[g0 + lane] = cnt;
   }
-  if (lane == 0) *flag = 1u;
+  const uint32_t tot = wave_total(valid ? cnt : 0u);
+  if (lane == 0) A.wave_sum[wl] = tot;
+  if (mark && lane == kLanes - 1 && ((valid && k + 1 < S.n_sub && ex != ex_before) || mark == 2))
+    streams[4ull * d + s].pad = 1u;
 }
 
-// Symbols per wavefront (sum of its 64 subsequence counts).
-// A wavefront whose first start is not the previous wavefront's last exit
-// (the queued fix passes did not settle the stream) marks its stream.
-__global__ void __launch_bounds__(64) sync_wave_sum_kernel(SyncStream* __restrict__ streams,
-                                                           const uint32_t* __restrict__ wave_job,
-                                                           const uint32_t* __restrict__ job_wave0, SyncArrays A) {
-  const uint32_t d = wave_job[blockIdx.x];
-  uint32_t w = blockIdx.x - job_wave0[d];
-  const int s = locate(streams + 4ull * d, w);
-  if (s < 0) return;
-  const SyncStream S = streams[4ull * d + s];
-  const uint32_t lane = threadIdx.x, k = w * kLanes + lane;
-  if (lane == 0 && w > 0) {
-    const uint64_t g0 = (uint64_t)S.first_sub + (uint64_t)w * kLanes;
-    if (A.exit[g0 - 1] != A.start[g0]) streams[4ull * d + s].pad = 1u;
+__global__ void __launch_bounds__(64) sync_fix_kernel(SyncStream* __restrict__ streams,
+                                                      const uint32_t* __restrict__ wave_job,
+                                                      const uint32_t* __restrict__ job_wave0,
+                                                      const uint16_t* __restrict__ tables, SyncArrays A, uint32_t nw,
+                                                      const uint32_t* __restrict__ prev_flag,
+                                                      uint32_t* __restrict__ flag, uint32_t mark) {
+  __shared__ uint32_t tab32[kSyncTableEntries / 2];
+  __shared__ uint32_t stage[kStageWords];
+  // the previous pass (queued before this one) changed nothing: settled
+  if (prev_flag && g_ld<uint32_t>(reinterpret_cast<uint64_t>(prev_flag)) == 0) return;
+  const uint32_t lane = threadIdx.x;
+  bool any = false;
+  for (uint32_t c = blockIdx.x * kLanes; c < nw; c += gridDim.x * kLanes) {
+    const uint32_t wl = c + lane;
+    bool need = false;
+    if (wl < nw) {
+      const uint32_t d = wave_job[wl];
+      uint32_t w = wl - job_wave0[d];
+      const int s = locate(streams + 4ull * d, w);
+      if (s >= 0 && w > 0) {
+        const uint64_t g0 = (uint64_t)streams[4ull * d + s].first_sub + (uint64_t)w * kLanes;
+        need = A.exit[g0 - 1] != A.start[g0];
+      }
+    }
+    uint64_t m = __ballot(need);
+    any |= m != 0;
+    while (m) {
+      const uint32_t i = (uint32_t)__builtin_ctzll(m);
+      m &= m - 1;
+      fix_wave(streams, wave_job, job_wave0, tables, A, c + i, mark, tab32, stage);
+    }
   }
-  uint32_t c = k < S.n_sub ? A.count[(uint64_t)S.first_sub + k] : 0u;
-  for (int o = 32; o >= 1; o >>= 1) c += (uint32_t)__shfl_xor((int)c, o, 64);
-  if (lane == 0) A.wave_sum[blockIdx.x] = c;
+  if (any && lane == 0) *flag = 1u;
+}
+
+// A stream's verdict under the exactness condition, reported once per
+// stream into its payload's word (bit s: reported, 4 + s: failed, 8 + s:
+// unsettled); the report that completes the four sets the payload's status,
+// unless the exact kernel gave it a final one (a rejected header: the
+// stream records keep the host's zeros, max_bits 0).
+__device__ inline void report_stream(const SyncStream& S, uint32_t s, uint32_t* verdict, uint32_t d, bool ok,
+                                     uint32_t* status) {
+  const uint32_t mine = (1u << s) | (ok ? 0u : 1u << (4 + s)) | (S.pad ? 1u << (8 + s) : 0u);
+  const uint32_t all = atomicOr(verdict + d, mine) | mine;
+  if ((all & 0xFu) != 0xFu || ((all ^ mine) & 0xFu) == 0xFu) return;
+  if (S.max_bits == 0) return;
+  status[S.job] = (all & 0xF00u) ? kStUnsettled : (all & 0xF0u) ? kStFallback : kStOk;
+}
+
+// The condition for a stream whose symbol n-1 ends at bit T.
+__device__ inline bool stream_exact(const SyncStream& S, uint64_t T) {
+  if (T > 8 * S.m || T <= 8 * (S.m - 1)) return false;
+  const uint32_t used = (uint32_t)(T - 8 * (S.m - 1));  // bits of the last logical byte, 1..8
+  return used == 8 || (gbyte(S.src) >> used) == 0;
 }
 
 // Exclusive scan of the wavefront sums of one stream (blockIdx.x = 4 d + s);
 // its wavefronts are consecutive in the launch, after those of streams < s.
 __global__ void __launch_bounds__(256) sync_scan_kernel(const SyncStream* __restrict__ streams,
-                                                        const uint32_t* __restrict__ job_wave0, SyncArrays A) {
+                                                        const uint32_t* __restrict__ job_wave0, SyncArrays A,
+                                                        uint32_t* __restrict__ status) {
   __shared__ uint64_t part[256];
   const uint32_t d = blockIdx.x / 4, s = blockIdx.x % 4;
   uint32_t w0 = job_wave0[d];
@@ -416,16 +564,22 @@ __global__ void __launch_bounds__(256) sync_scan_kernel(const SyncStream* __rest
     A.wave_prefix[w0 + k] = acc;
     acc += A.wave_sum[w0 + k];
   }
+  // a stream with no symbol n-1 (none expected, or too few decoded) is
+  // judged here; every other stream by the write pass's wavefront holding it
+  const SyncStream& S = streams[blockIdx.x];
+  if (t == 0 && (S.n == 0 || part[255] < S.n))
+    report_stream(S, s, A.verdict, d, S.n == 0 && S.m == 0, status);
 }
 
 // Decode again from the settled starts and write symbols [0, n) of the
 // segment; the lane holding symbol n-1 records where it ends.  Symbols are
 // staged in LDS at their output address mod 16, so the store is dwordx4.
 template <uint32_t kOutStage>
-__global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__ streams,
+__global__ void __launch_bounds__(64) sync_write_kernel(const SyncStream* __restrict__ streams,
                                                         const uint32_t* __restrict__ wave_job,
                                                         const uint32_t* __restrict__ job_wave0,
-                                                        const uint16_t* __restrict__ tables, SyncArrays A) {
+                                                        const uint16_t* __restrict__ tables, SyncArrays A,
+                                                        uint32_t* __restrict__ status) {
   __shared__ uint16_t tab[kSyncTableEntries];
   __shared__ uint32_t stage[kStageWords];
   __shared__ __attribute__((aligned(16))) uint8_t out[kOutStage + 16];
@@ -433,8 +587,7 @@ __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__
   uint32_t w = blockIdx.x - job_wave0[d];
   const int s = locate(streams + 4ull * d, w);
   if (s < 0) return;
-  SyncStream* Sp = streams + 4ull * d + s;
-  const SyncStream S = *Sp;
+  const SyncStream S = streams[4ull * d + s];
   const uint64_t base = A.wave_prefix[blockIdx.x];
   if (base >= S.n) return;  // the whole wavefront decodes padding
   const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
@@ -474,7 +627,7 @@ __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__
                       (uint8_t)tab[__builtin_amdgcn_alignbit(stage[wi + 1], stage[wi], p & 31u) & mask]);
       }
     }
-    if (first + m == S.n) Sp->T = L0 * 8 + p0 + m * L;
+    if (first + m == S.n) report_stream(S, (uint32_t)s, A.verdict, d, stream_exact(S, L0 * 8 + p0 + m * L), status);
   } else if (valid && first < S.n) {
     Cursor k = cur_open(stage, (uint32_t)(A.start[g] - L0 * 8));
     const uint32_t m = (uint32_t)std::min<uint64_t>(cnt, S.n - first);
@@ -512,7 +665,7 @@ __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__
         g_st<uint8_t>(S.dst + first + i, (uint8_t)e1);
       }
     }
-    if (first + m == S.n) Sp->T = L0 * 8 + k.p;
+    if (first + m == S.n) report_stream(S, (uint32_t)s, A.verdict, d, stream_exact(S, L0 * 8 + k.p), status);
   }
   if (staged) {
     __syncthreads();
@@ -526,66 +679,6 @@ __global__ void __launch_bounds__(64) sync_write_kernel(SyncStream* __restrict__
   }
 }
 
-// Stored bytes the exact kernel deferred (copy_src[j] != 0): one workgroup
-// per copy_chunk(len) of output.  Aligned dword stores; the source is realigned
-// with a funnel shift of two aligned words, used only where both words hold
-// source bytes.
-__global__ void __launch_bounds__(256) raw_copy_kernel(const DecodeJob* __restrict__ jobs,
-                                                       const uint64_t* __restrict__ copy_src,
-                                                       const uint32_t* __restrict__ chunk_job,
-                                                       const uint32_t* __restrict__ job_chunk0) {
-  const uint32_t j = chunk_job[blockIdx.x];
-  const uint64_t s = copy_src[j];
-  if (s == 0) return;
-  const DecodeJob J = jobs[j];
-  const uint64_t cs = copy_chunk(J.dst_len);
-  const uint64_t a = (uint64_t)(blockIdx.x - job_chunk0[j]) * cs;
-  const uint64_t b = std::min<uint64_t>(J.dst_len, a + cs);
-  if (a >= b) return;
-  const uint32_t t = threadIdx.x;
-  const uint64_t ba = J.dst + a, bb = J.dst + b;
-  const uint64_t lo = std::min<uint64_t>((ba + 3) & ~3ull, bb);
-  const uint64_t hi = std::max<uint64_t>(bb & ~3ull, lo);
-  for (uint64_t x = ba + t; x < lo; x += 256) g_st<uint8_t>(x, g_ld<uint8_t>(s + (x - J.dst)));
-  for (uint64_t x = hi + t; x < bb; x += 256) g_st<uint8_t>(x, g_ld<uint8_t>(s + (x - J.dst)));
-  for (uint64_t x = lo + 4ull * t; x < hi; x += 1024) {
-    const uint64_t o = x - J.dst;
-    if (o + 5 <= J.dst_len) {
-      const uint64_t S = s + o;
-      const uint64_t sa = S & ~3ull;
-      g_st<uint32_t>(x, __builtin_amdgcn_alignbyte(g_ld<uint32_t>(sa + 4), g_ld<uint32_t>(sa), (uint32_t)(S & 3u)));
-    } else {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) g_st<uint8_t>(x + k, g_ld<uint8_t>(s + o + k));
-    }
-  }
-}
-
-// Accept a deferred payload only under the exactness condition above.
-__global__ void __launch_bounds__(64) sync_check_kernel(const SyncStream* __restrict__ streams, uint32_t n_def,
-                                                        uint32_t* __restrict__ status) {
-  const uint32_t d = blockIdx.x * kLanes + threadIdx.x;
-  if (d >= n_def) return;
-  const uint32_t job = streams[4ull * d].job;
-  if (status[job] != kStDeferred) return;  // final already (the header was rejected)
-  bool ok = true, settled = true;
-  for (int s = 0; s < 4; ++s) {
-    const SyncStream S = streams[4ull * d + s];
-    settled = settled && S.pad == 0;
-    if (S.n == 0) {
-      ok = ok && S.m == 0;
-      continue;
-    }
-    if (S.T == ~0ull || S.T > 8 * S.m || S.T <= 8 * (S.m - 1)) {
-      ok = false;
-      continue;
-    }
-    const uint32_t used = (uint32_t)(S.T - 8 * (S.m - 1));  // bits of the last logical byte, 1..8
-    if (used < 8 && (gbyte(S.src) >> used) != 0) ok = false;
-  }
-  status[job] = !settled ? kStUnsettled : ok ? kStOk : kStFallback;
-}
-
 }  // namespace
 
 namespace {
@@ -596,33 +689,36 @@ namespace {
     if (_e != hipSuccess) return _e;    \
   } while (0)
 
-__global__ void __launch_bounds__(256) clear_unsettled_kernel(SyncStream* __restrict__ streams, uint32_t n) {
+// Before the offsets and the write are run again: the streams' unsettled
+// marks and the payloads' verdict words cleared.
+__global__ void __launch_bounds__(256) clear_unsettled_kernel(SyncStream* __restrict__ streams, uint32_t* verdict,
+                                                              uint32_t n_def) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-  if (i < n) streams[i].pad = 0u;
+  if (i < 4 * n_def) streams[i].pad = 0u;
+  if (i < n_def) verdict[i] = 0u;
 }
 
-// Per-stream offsets, the write and the acceptance check (after the fix passes).
+// Per-stream offsets and the write; the streams' verdicts set the deferred
+// payloads' statuses (after the fix passes).
 hipError_t sync_finish(hipStream_t s, SyncStream* streams, const uint32_t* d_wave_job, const uint32_t* d_job_wave0,
                        const uint16_t* tables, const SyncArrays& A, uint32_t nw, uint32_t n_def, uint32_t* status,
                        uint32_t out_stage) {
-  hipLaunchKernelGGL(sync_wave_sum_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, A);
-  PTWM_HIP_TRY_ERR(hipGetLastError());
-  hipLaunchKernelGGL(sync_scan_kernel, dim3(4 * n_def), dim3(256), 0, s, streams, d_job_wave0, A);
+  hipLaunchKernelGGL(sync_scan_kernel, dim3(4 * n_def), dim3(256), 0, s, streams, d_job_wave0, A, status);
   PTWM_HIP_TRY_ERR(hipGetLastError());
   if (out_stage <= 8192)
     hipLaunchKernelGGL(sync_write_kernel<8192>, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables,
-                       A);
+                       A, status);
   else if (out_stage <= 12288)
     hipLaunchKernelGGL(sync_write_kernel<12288>, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0,
-                       tables, A);
+                       tables, A, status);
   else
     hipLaunchKernelGGL(sync_write_kernel<kOutStageMax>, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job,
-                       d_job_wave0, tables, A);
-  PTWM_HIP_TRY_ERR(hipGetLastError());
-  hipLaunchKernelGGL(sync_check_kernel, dim3((n_def + kLanes - 1) / kLanes), dim3(kLanes), 0, s, streams, n_def,
-                     status);
+                       d_job_wave0, tables, A, status);
   return hipGetLastError();
 }
+
+// Fix-pass grid: a lane per wavefront to check, a workgroup per 64.
+uint32_t fix_grid(uint32_t nw) { return std::min<uint32_t>((nw + kLanes - 1) / kLanes, 2048u); }
 
 size_t up16(size_t x) { return (x + 15) & ~size_t(15); }
 
@@ -630,7 +726,9 @@ size_t up16(size_t x) { return (x + 15) & ~size_t(15); }
 
 int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& run) {
   hipStream_t s = ctx.stream;
-  PTWM_HIP_TRY(ctx.status.ensure(n_jobs * sizeof(uint32_t) + 64));
+  // the kernels write the statuses to host-coherent memory (no copy back);
+  // the second half takes the exact path's second run
+  PTWM_HIP_TRY(ctx.h_job_status.ensure(2 * n_jobs * sizeof(uint32_t) + 64));
   PTWM_HIP_TRY(ctx.h_status.ensure(n_jobs * sizeof(uint32_t) + 64));
   if (n_jobs == 0) return kOk;
   // Payloads for the parallel path and their slots; output pieces for
@@ -664,12 +762,14 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
   const uint32_t nw = (uint32_t)wave_job.size();
   // Every argument array in one upload from pinned memory:
   //   jobs | copy sources (zero) | piece -> job | job -> first piece |
-  //   [stream records (zero) | wavefront -> payload | payload -> first
-  //    wavefront | fix-pass flags (zero)]
+  //   [stream records (zero but their job) | wavefront -> payload |
+  //    payload -> first wavefront | payload verdicts (zero) | fix-pass
+  //    flags (zero)]
   const size_t o_jobs = 0, o_src = up16(n_jobs * sizeof(DecodeJob)), o_cj = o_src + up16(n_jobs * 8),
                o_jc = o_cj + up16(nck * 4), o_str = o_jc + up16(n_jobs * 4),
                o_wj = o_str + up16(4ull * n_def * sizeof(SyncStream)), o_jw = o_wj + up16((size_t)nw * 4),
-               o_fl = o_jw + up16((size_t)n_def * 4), total = o_fl + up16(4 * kFixQueued);
+               o_vd = o_jw + up16((size_t)n_def * 4), o_fl = o_vd + up16((size_t)n_def * 4),
+               total = o_fl + up16(4 * kFixQueued);
   PTWM_HIP_TRY(ctx.exact_args.ensure(total));
   PTWM_HIP_TRY(ctx.h_exact_args.ensure(total));
   uint8_t* hb = static_cast<uint8_t*>(ctx.h_exact_args.ptr);
@@ -679,9 +779,15 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
   if (nck) std::memcpy(hb + o_cj, chunk_job.data(), nck * 4);
   std::memcpy(hb + o_jc, job_chunk0.data(), n_jobs * 4);
   std::memset(hb + o_str, 0, o_wj - o_str);
+  // a payload whose header the exact kernel rejects keeps these records:
+  // its verdict then leaves the status the exact kernel set
+  SyncStream* hrec = reinterpret_cast<SyncStream*>(hb + o_str);
+  for (size_t j = 0; j < n_jobs; ++j)
+    if (hj[j].sync_id)
+      for (int q = 0; q < 4; ++q) hrec[4ull * (hj[j].sync_id - 1) + q].job = (uint32_t)j;
   if (nw) std::memcpy(hb + o_wj, wave_job.data(), (size_t)nw * 4);
   if (n_def) std::memcpy(hb + o_jw, job_wave0.data(), (size_t)n_def * 4);
-  std::memset(hb + o_fl, 0, total - o_fl);
+  std::memset(hb + o_vd, 0, total - o_vd);
   PTWM_HIP_TRY(hipMemcpyAsync(db, hb, total, hipMemcpyHostToDevice, s));
   const DecodeJob* d_jobs = reinterpret_cast<const DecodeJob*>(db + o_jobs);
   uint64_t* d_copy_src = reinterpret_cast<uint64_t*>(db + o_src);
@@ -693,6 +799,9 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
   uint32_t* d_flag = reinterpret_cast<uint32_t*>(db + o_fl);
   uint16_t* tables = nullptr;
   SyncArrays A{};
+  // test mode: no look-back, and the queued fix pass marks every stream it
+  // touches unsettled, so that the host's extra passes run
+  const bool force_unsettled = std::getenv("PTWM_SYNC_FORCE_UNSETTLED") != nullptr;
   if (n_def) {
     PTWM_HIP_TRY(ctx.sync_tables.ensure(2ull * kSyncTableEntries * n_def));
     PTWM_HIP_TRY(ctx.sync_sub.ensure(subs * (8 + 8 + 4) + (uint64_t)nw * (8 + 4) + 64));
@@ -703,8 +812,17 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
     A.wave_prefix = A.exit + subs;
     A.count = reinterpret_cast<uint32_t*>(A.wave_prefix + nw);
     A.wave_sum = A.count + subs;
+    A.verdict = reinterpret_cast<uint32_t*>(db + o_vd);
+    // look-back slots: stale values carry an older epoch; fresh memory is
+    // cleared once
+    const void* old_pub = ctx.sync_pub.ptr;
+    PTWM_HIP_TRY(ctx.sync_pub.ensure((size_t)nw * 8));
+    if (ctx.sync_pub.ptr != old_pub) PTWM_HIP_TRY(hipMemsetAsync(ctx.sync_pub.ptr, 0, ctx.sync_pub.cap, s));
+    A.pub = static_cast<uint64_t*>(ctx.sync_pub.ptr);
+    A.epoch = ++ctx.sync_epoch;
+    A.look_back = force_unsettled ? 0u : 1u;
   }
-  uint32_t* status = static_cast<uint32_t*>(ctx.status.ptr);
+  uint32_t* status = static_cast<uint32_t*>(ctx.h_job_status.ptr);
   run.out_stage = (uint32_t)std::min<double>(kOutStageMax, 1.25 * out_per_wave + 64);
   PTWM_HIP_TRY(launch_decode_exact(d_jobs, status, (uint32_t)n_jobs, streams, tables, d_copy_src, s));
   bool any_zstd = false;
@@ -726,23 +844,27 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
   bool any_o1sac = false;
   for (size_t j = 0; j < n_jobs; ++j) any_o1sac |= hj[j].codec == kCodecO1sac;
   if (any_o1sac) PTWM_HIP_TRY(launch_o1sac_decode(d_jobs, status, (uint32_t)n_jobs, s));
-  if (nck) {
-    hipLaunchKernelGGL(raw_copy_kernel, dim3((uint32_t)nck), dim3(256), 0, s, d_jobs, d_copy_src, d_chunk_job,
-                       d_job_chunk0);
+  const CopyArgs C{d_jobs, d_copy_src, d_chunk_job, d_job_chunk0};
+  const uint32_t queued = kFixQueued;
+  if (nck && !n_def) {
+    hipLaunchKernelGGL(raw_copy_kernel, dim3((uint32_t)nck), dim3(256), 0, s, C);
     PTWM_HIP_TRY(hipGetLastError());
   }
   if (n_def) {
-    hipLaunchKernelGGL(sync_pass_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables, A);
+    // the deferred copies ride along as the first pass's last workgroups
+    if ((uint64_t)nw + 4ull * nck > 0xFFFFFFFFull) return kInvalidInput;
+    hipLaunchKernelGGL(sync_pass_kernel, dim3(nw + 4 * (uint32_t)nck), dim3(kLanes), 0, s, streams, d_wave_job,
+                       d_job_wave0, tables, A, nw, C);
     PTWM_HIP_TRY(hipGetLastError());
-    for (uint32_t k = 0; k < kFixQueued; ++k) {
-      hipLaunchKernelGGL(sync_fix_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables, A,
-                         k ? d_flag + k - 1 : nullptr, d_flag + k);
+    for (uint32_t k = 0; k < queued; ++k) {
+      hipLaunchKernelGGL(sync_fix_kernel, dim3(fix_grid(nw)), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0,
+                         tables, A, nw, k ? d_flag + k - 1 : nullptr, d_flag + k,
+                         k + 1 < queued ? 0u : force_unsettled ? 2u : 1u);
       PTWM_HIP_TRY(hipGetLastError());
     }
     PTWM_HIP_TRY(sync_finish(s, streams, d_wave_job, d_job_wave0, tables, A, nw, n_def, status, run.out_stage));
   }
   if (any_rans) PTWM_HIP_TRY(hipStreamWaitEvent(s, ctx.side_join, 0));
-  PTWM_HIP_TRY(hipMemcpyAsync(ctx.h_status.ptr, status, n_jobs * 4, hipMemcpyDeviceToHost, s));
   run.jobs = d_jobs;
   run.status = status;
   run.streams = streams;
@@ -758,8 +880,8 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
 int64_t decode_jobs_complete(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& run, bool& rewritten) {
   hipStream_t s = ctx.stream;
   rewritten = false;
-  uint32_t* hs = static_cast<uint32_t*>(ctx.h_status.ptr);
-  uint32_t* status = run.status;
+  uint32_t* const status = run.status;
+  volatile uint32_t* const hs = status;  // host-coherent: read after the stream is synchronised
   SyncStream* streams = run.streams;
   const uint16_t* tables = run.tables;
   const SyncArrays& A = run.A;
@@ -783,27 +905,35 @@ int64_t decode_jobs_complete(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun
     for (uint32_t pass = 0; pass < kMaxFixPasses && !settled; pass += kBatch) {
       PTWM_HIP_TRY(hipMemsetAsync(fl, 0, 4 * kBatch, s));
       for (uint32_t k = 0; k < kBatch; ++k) {
-        hipLaunchKernelGGL(sync_fix_kernel, dim3(nw), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0, tables,
-                           A, k ? fl + k - 1 : nullptr, fl + k);
+        hipLaunchKernelGGL(sync_fix_kernel, dim3(fix_grid(nw)), dim3(kLanes), 0, s, streams, d_wave_job, d_job_wave0,
+                           tables, A, nw, k ? fl + k - 1 : nullptr, fl + k, 0u);
         PTWM_HIP_TRY(hipGetLastError());
       }
       PTWM_HIP_TRY(hipMemcpyAsync(const_cast<uint32_t*>(h_flag), fl, 4 * kBatch, hipMemcpyDeviceToHost, s));
       PTWM_HIP_TRY(hipStreamSynchronize(s));
       for (uint32_t k = 0; k < kBatch; ++k) settled |= h_flag[k] == 0;
     }
-    // the streams' unsettled marks are cleared; jobs already final keep
-    // their status (the write of a settled payload writes the same bytes)
-    std::vector<uint32_t> keep(hs, hs + n_jobs);
-    hipLaunchKernelGGL(clear_unsettled_kernel, dim3((4 * n_def + 255) / 256), dim3(256), 0, s, streams, 4 * n_def);
-    PTWM_HIP_TRY(hipGetLastError());
-    for (size_t j = 0; j < n_jobs; ++j)
-      if (keep[j] == kStUnsettled) keep[j] = kStDeferred;
-    PTWM_HIP_TRY(hipMemcpyAsync(status, keep.data(), n_jobs * 4, hipMemcpyHostToDevice, s));
-    PTWM_HIP_TRY(sync_finish(s, streams, d_wave_job, d_job_wave0, tables, A, nw, n_def, status, run.out_stage));
-    PTWM_HIP_TRY(hipMemcpyAsync(hs, status, n_jobs * 4, hipMemcpyDeviceToHost, s));
-    PTWM_HIP_TRY(hipStreamSynchronize(s));
-    for (size_t j = 0; j < n_jobs; ++j)
-      if (keep[j] != kStDeferred) hs[j] = keep[j];
+    if (!settled) {
+      // still moving after kMaxFixPasses: the exact path decodes them
+      for (size_t j = 0; j < n_jobs; ++j)
+        if (hs[j] == kStUnsettled) hs[j] = kStFallback;
+    } else {
+      // the streams' unsettled marks and the verdicts are cleared; jobs
+      // already final keep their status (the write of a settled payload
+      // writes the same bytes)
+      std::vector<uint32_t> keep(n_jobs);
+      for (size_t j = 0; j < n_jobs; ++j) keep[j] = hs[j];
+      hipLaunchKernelGGL(clear_unsettled_kernel, dim3((4 * n_def + 255) / 256), dim3(256), 0, s, streams, A.verdict,
+                         n_def);
+      PTWM_HIP_TRY(hipGetLastError());
+      for (size_t j = 0; j < n_jobs; ++j)
+        if (keep[j] == kStUnsettled) keep[j] = kStDeferred;
+      for (size_t j = 0; j < n_jobs; ++j) hs[j] = keep[j];
+      PTWM_HIP_TRY(sync_finish(s, streams, d_wave_job, d_job_wave0, tables, A, nw, n_def, status, run.out_stage));
+      PTWM_HIP_TRY(hipStreamSynchronize(s));
+      for (size_t j = 0; j < n_jobs; ++j)
+        if (keep[j] != kStDeferred) hs[j] = keep[j];
+    }
   }
   // payloads the parallel path declined (or did not settle) go to the exact path
   std::vector<DecodeJob> again;
@@ -824,13 +954,13 @@ int64_t decode_jobs_complete(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun
     const size_t na = again.size();
     PTWM_HIP_TRY(ctx.jobs.ensure(na * sizeof(DecodeJob) + 64));
     PTWM_HIP_TRY(hipMemcpyAsync(ctx.jobs.ptr, again.data(), na * sizeof(DecodeJob), hipMemcpyHostToDevice, s));
-    PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr), status, (uint32_t)na, nullptr,
-                                     nullptr, nullptr, s));
-    std::vector<uint32_t> st2(na);
-    PTWM_HIP_TRY(hipMemcpyAsync(st2.data(), status, na * 4, hipMemcpyDeviceToHost, s));
+    PTWM_HIP_TRY(launch_decode_exact(static_cast<const DecodeJob*>(ctx.jobs.ptr), status + n_jobs, (uint32_t)na,
+                                     nullptr, nullptr, nullptr, s));
     PTWM_HIP_TRY(hipStreamSynchronize(s));
-    for (size_t i = 0; i < na; ++i) hs[again_idx[i]] = st2[i];
+    for (size_t i = 0; i < na; ++i) hs[again_idx[i]] = hs[n_jobs + i];
   }
+  uint32_t* const out = static_cast<uint32_t*>(ctx.h_status.ptr);
+  for (size_t j = 0; j < n_jobs; ++j) out[j] = hs[j];
   return kOk;
 }
 

@@ -95,7 +95,9 @@ struct DevCtx {
   // fused-decode status words, written by the kernels (host-coherent)
   PinnedBuffer h_ilv_status;
   // parallel Huffman decode of reference streams
-  DeviceBuffer sync_tables, sync_sub, sync_waves;
+  DeviceBuffer sync_tables, sync_sub, sync_waves, sync_pub;
+  PinnedBuffer h_job_status;  // the exact route's status words, written by the kernels (host-coherent)
+  uint64_t sync_epoch = 0;  // look-back tag of the parallel Huffman decode's first pass, one per launch
   DeviceBuffer exact_args;  // the exact route's argument arrays, one upload per call
   // reference Huffman payloads of the exact route, cumulative: accepted by
   // the parallel path, decoded again by the exact state machine, and calls

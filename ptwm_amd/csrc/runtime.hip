@@ -123,6 +123,7 @@ DevCtx* get_ctx(uint32_t ord) {
   }
   ctx->stream = ctx->own_stream;
   ctx->h_ilv_status.flags = hipHostMallocCoherent;
+  ctx->h_job_status.flags = hipHostMallocCoherent;
   // the allocation-free decode's scratch on this device (the device is
   // current): its address, or null, and the entry point then reports
   // MissingCapability

@@ -138,6 +138,31 @@ def test_parallel_huffman_malformed_matches_reference_outcome(kind):
             assert got == want, name
 
 
+def test_unsettled_streams_take_the_host_fix_passes(monkeypatch):
+    """A stream the queued fix passes leave unsettled gets more passes from
+    the host, then its offsets, write and verdict again.  The library's test
+    mode (PTWM_SYNC_FORCE_UNSETTLED) drops the first pass's look-back and
+    marks every stream its queued fix pass touches, so this path runs."""
+    rng = np.random.default_rng(5)
+    plane = rng.geometric(0.3, 300_000).clip(0, 255).astype(np.uint8).tobytes()
+    payload = O.codec_encode(O.CODEC_HUFFMAN, plane)
+    bad = bytearray(payload)
+    bad[len(bad) // 2] ^= 0x10
+    bad = bytes(bad)
+    monkeypatch.setenv("PTWM_SYNC_FORCE_UNSETTLED", "1")
+    note("sync forced-unsettled: valid payload")
+    before = api.decode_stats(0)
+    got, n = gpu_decode(payload, len(plane))
+    after = api.decode_stats(0)
+    assert n == len(plane) and got == plane
+    assert after["extra_rounds"] == before["extra_rounds"] + 1, after
+    assert after["accepted"] == before["accepted"] + 1, after
+    note("sync forced-unsettled: one bit flipped")
+    want = oracle_decode(bad, len(plane))
+    got, _ = gpu_decode(bad, len(plane))
+    assert (got is None) == (want is None) and (want is None or got == want)
+
+
 @pytest.mark.parametrize("n", [4095, 4096, 4097, 65536, 65539, (1 << 20) + 1, 3 * (1 << 20) + 7])
 def test_stored_payload_copy(n):
     """Stored (tag 0) payloads of 4 KiB and more are copied by the
