@@ -448,17 +448,19 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
       if (lane < 4) {
         uint64_t s4[4], e4[4];
         split_four(job.dst_len, s4, e4);
+        const uint32_t sb = job.pad[3];  // subsequence bits, chosen by the host
         uint32_t sub = job.sync_sub0;
-        for (int i = 0; i < (int)lane; ++i) sub += (uint32_t)((h.seg_len[i] * 8 + kSyncSubBits - 1) / kSyncSubBits);
+        for (int i = 0; i < (int)lane; ++i) sub += (uint32_t)((h.seg_len[i] * 8 + sb - 1) / sb);
         SyncStream S;
         S.src = job.src + h.enc_off + h.seg_src[lane];
         S.m = h.seg_len[lane];
         S.dst = job.dst + s4[lane];
         S.n = e4[lane] - s4[lane];
-        S.T = ~0ull;
+        S.sub_bits = sb;
+        S.reserved = 0;
         S.job = blockIdx.x;
         S.first_sub = sub;
-        S.n_sub = (uint32_t)((h.seg_len[lane] * 8 + kSyncSubBits - 1) / kSyncSubBits);
+        S.n_sub = (uint32_t)((h.seg_len[lane] * 8 + sb - 1) / sb);
         S.max_bits = (uint16_t)max_bits;
         S.fixed_len = h.fixed ? (uint16_t)max_bits : (uint16_t)0;
         S.table = d;

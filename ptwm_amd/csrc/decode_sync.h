@@ -7,8 +7,9 @@ namespace ptwm {
 
 // Bits per subsequence: one lane decodes one subsequence of a stream.  A
 // multiple of 32 with an odd word count, so lanes of a wavefront start in
-// different LDS banks.
-constexpr uint32_t kSyncSubBits = 480;
+// different LDS banks: 480 unless a launch has too few wavefronts to fill
+// the device, then down to 96 (chosen per payload by the host).
+constexpr uint32_t kSyncSubBitsMax = 480, kSyncSubBitsMin = 96;
 // Payloads (Huffman, tag 1) at least this long take the parallel path.
 constexpr uint64_t kSyncMinBytes = 16384;
 
@@ -19,10 +20,11 @@ struct SyncStream {
   uint64_t m;          // stream bytes
   uint64_t dst;        // device address of the segment's first output byte
   uint64_t n;          // symbols of the segment (split_four of orig_len)
-  uint64_t T;          // (unused)
+  uint32_t sub_bits;   // bits per subsequence
+  uint32_t reserved;
   uint32_t job;        // index into the job / status arrays
   uint32_t first_sub;  // global slot of the stream's subsequence 0
-  uint32_t n_sub;      // ceil(8 m / kSyncSubBits)
+  uint32_t n_sub;      // ceil(8 m / sub_bits)
   uint16_t max_bits;   // decode table width
   uint16_t fixed_len;  // every code max_bits long (a fixed-length code): max_bits, else 0
   uint32_t table;      // deferred payload slot (decode table index)

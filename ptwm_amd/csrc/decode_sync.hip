@@ -5,7 +5,8 @@
 // serially by the reference (decompress.rs:8-211).  Prefix codes
 // resynchronise: a decoder started at an arbitrary bit soon lands on a true
 // codeword boundary.  So every stream is cut into subsequences of
-// kSyncSubBits bits, one lane each:
+// sub_bits bits (480, fewer for launches too small to fill the device), one
+// lane each:
 //   pass 1   each lane decodes from its subsequence's first bit up to the
 //            first codeword boundary at or past its end (its "exit"); lanes
 //            of a wavefront then restart from their left neighbour's exit
@@ -53,16 +54,15 @@ namespace ptwm {
 namespace {
 
 constexpr uint32_t kLanes = 64;
-constexpr uint32_t kSubBytes = kSyncSubBits / 8;
-constexpr uint32_t kWaveBits = kLanes * kSyncSubBits;
-constexpr uint32_t kStageWords = kWaveBits / 32 + 5;  // + the window overrun and the bit buffer's look-ahead
+// the largest wavefront span, + the window overrun and the bit buffer's look-ahead
+constexpr uint32_t kStageWords = kLanes * kSyncSubBitsMax / 32 + 5;
 // LDS output staging per wavefront of the write pass: chosen per launch
 // from the payloads' expected symbols per wavefront, so that the LDS it
 // takes does not cap the occupancy lower than needed (a wavefront with more
 // output writes it straight to memory)
 constexpr uint32_t kOutStageMax = 16384;
 constexpr uint32_t kMaxFixPasses = 256;
-static_assert(kSyncSubBits % 32 == 0 && (kSyncSubBits / 32) % 2 == 1, "subsequence size");
+static_assert(kSyncSubBitsMax % 64 == 32 && kSyncSubBitsMin % 64 == 32, "subsequence sizes: odd word counts");
 
 // Which stream of deferred payload d, and which wavefront of it, wavefront
 // `w` of the payload's launch range covers; -1 when past the last.
@@ -79,8 +79,9 @@ __device__ inline uint8_t gbyte(uint64_t a) {
   return *(const __attribute__((address_space(1))) uint8_t*)(uintptr_t)a;
 }
 
-// Stage logical bytes [L0, L0 + 4 * kStageWords) of the stream in LDS
-// (logical order, zero past the stream's end) and its decode table.
+// Stage logical bytes [L0, L0 + 4 (2 sub_bits + 5)) of the stream in LDS
+// (a wavefront's span and the look-ahead; logical order, zero past the
+// stream's end) and its decode table.
 __device__ inline void stage_wave(const SyncStream& S, uint64_t L0, const uint16_t* __restrict__ tables,
                                   uint32_t* stage, uint16_t* tab) {
   const uint32_t lane = threadIdx.x;
@@ -100,6 +101,9 @@ __device__ inline void stage_wave(const SyncStream& S, uint64_t L0, const uint16
   // past it is clamped to src - 8, which still lies in the payload (ahead
   // of the streams sit the tag, the weights header and the jump table).
   constexpr uint32_t kStIt = (kStageWords + kLanes - 1) / kLanes;
+  // (words past the span are loaded too, at in-bounds addresses, and not
+  // stored: a load under a condition would make the stores wait for each)
+  const uint32_t n_words = 2 * S.sub_bits + 5;
   const uint64_t lo_min = (S.src - 8) & ~3ull;
   uint32_t w0[kStIt], w1[kStIt];
 #pragma unroll
@@ -127,7 +131,7 @@ __device__ inline void stage_wave(const SyncStream& S, uint64_t L0, const uint16
     const uint64_t rem = b < S.m ? S.m - b : 0;
     const uint32_t keep = rem >= 4 ? 0xFFFFFFFFu : (uint32_t)((1ull << (8 * rem)) - 1ull);
     const uint32_t v = __builtin_bswap32(__builtin_amdgcn_alignbyte(w1[it], w0[it], (uint32_t)(a & 3u))) & keep;
-    if (q < kStageWords) stage[q] = v;
+    if (q < n_words) stage[q] = v;
   }
   __syncthreads();
 }
@@ -186,14 +190,14 @@ __device__ inline uint32_t run(const uint32_t* stage, const uint16_t* tab, uint3
 
 // Codeword starts of a lane's path, one bit per bit of its subsequence:
 // word w of lane l at bm[w * kLanes + l] (consecutive lanes, consecutive banks).
-constexpr uint32_t kSubWords = kSyncSubBits / 32;
+constexpr uint32_t kSubWordsMax = kSyncSubBitsMax / 32;
 
 // run() that also records the path's codeword starts (relative to base, the
 // lane's subsequence start) in the lane's bitmap.  A codeword is at most
 // kHufMaxBits < 32 bits, so consecutive starts never skip a bitmap word.
 __device__ inline uint32_t run_rec(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t base,
                                    uint32_t p, uint32_t stop, uint32_t& cnt, uint32_t* bm) {
-  const uint32_t lane = threadIdx.x;
+  const uint32_t lane = threadIdx.x, sw = (stop - base) >> 5;
   uint32_t c = 0, wi = (p - base) >> 5, bits = 0;
   for (uint32_t w = 0; w < wi; ++w) bm[w * kLanes + lane] = 0u;
   Cursor k = cur_open(stage, p);
@@ -219,7 +223,7 @@ __device__ inline uint32_t run_rec(const uint32_t* stage, const uint16_t* tab, u
     }
   }
   bm[wi * kLanes + lane] = bits;
-  for (uint32_t w = wi + 1; w < kSubWords; ++w) bm[w * kLanes + lane] = 0u;
+  for (uint32_t w = wi + 1; w < sw; ++w) bm[w * kLanes + lane] = 0u;
   cnt = c;
   return k.p;
 }
@@ -230,7 +234,7 @@ __device__ inline uint32_t run_rec(const uint32_t* stage, const uint16_t* tab, u
 // starts from there), or, without meeting it, to the end; updates ex / cnt.
 __device__ inline void run_join(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t base,
                                 uint32_t p, uint32_t stop, uint32_t& ex, uint32_t& cnt, const uint32_t* bm) {
-  const uint32_t lane = threadIdx.x;
+  const uint32_t lane = threadIdx.x, sw = (stop - base) >> 5;
   uint32_t c = 0, wi = (p - base) >> 5, cur = bm[wi * kLanes + lane];
   Cursor k = cur_open(stage, p);
   while (k.p < stop) {
@@ -241,7 +245,7 @@ __device__ inline void run_join(const uint32_t* stage, const uint16_t* tab, uint
     }
     if ((cur >> (rel & 31u)) & 1u) {
       uint32_t rest = __popc(cur >> (rel & 31u));
-      for (uint32_t v = wi + 1; v < kSubWords; ++v) rest += __popc(bm[v * kLanes + lane]);
+      for (uint32_t v = wi + 1; v < sw; ++v) rest += __popc(bm[v * kLanes + lane]);
       cnt = c + rest;
       return;  // ex unchanged
     }
@@ -257,10 +261,10 @@ __device__ inline void run_join(const uint32_t* stage, const uint16_t* tab, uint
 // (bm non-null; bm_ok: it holds the lane's current path, updated here) a
 // restart stops where it joins the old path; a lane's later restarts run in
 // full and record again.
-__device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32_t mask, bool valid, uint32_t& st,
-                              uint32_t& ex, uint32_t& cnt, bool& changed, uint32_t* bm, bool& bm_ok) {
+__device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t sb, bool valid,
+                              uint32_t& st, uint32_t& ex, uint32_t& cnt, bool& changed, uint32_t* bm, bool& bm_ok) {
   const uint32_t lane = threadIdx.x;
-  const uint32_t base = lane * kSyncSubBits, stop = base + kSyncSubBits;
+  const uint32_t base = lane * sb, stop = base + sb;
   for (uint32_t round = 0; round < kLanes; ++round) {
     const uint32_t prev = (uint32_t)__shfl_up((int)ex, 1, 64);
     const bool ch = valid && lane > 0 && prev != st;
@@ -280,10 +284,10 @@ __device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32
     }
   }
 }
-__device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32_t mask, bool valid, uint32_t& st,
-                              uint32_t& ex, uint32_t& cnt, bool& changed) {
+__device__ inline void settle(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t sb, bool valid,
+                              uint32_t& st, uint32_t& ex, uint32_t& cnt, bool& changed) {
   bool no_bm = false;
-  settle(stage, tab, mask, valid, st, ex, cnt, changed, nullptr, no_bm);
+  settle(stage, tab, mask, sb, valid, st, ex, cnt, changed, nullptr, no_bm);
 }
 
 // Stored bytes the exact kernel deferred (copy_src[j] != 0): output bytes
@@ -369,7 +373,7 @@ __global__ void __launch_bounds__(64) sync_pass_kernel(const SyncStream* __restr
                                                        uint32_t nw, CopyArgs C) {
   __shared__ uint16_t tab[kSyncTableEntries];
   __shared__ uint32_t stage[kStageWords];
-  __shared__ uint32_t bm[kSubWords * kLanes];
+  __shared__ uint32_t bm[kSubWordsMax * kLanes];
   if (blockIdx.x >= nw) {
     copy_piece(C, blockIdx.x - nw, 4, threadIdx.x, kLanes);
     return;
@@ -379,7 +383,8 @@ __global__ void __launch_bounds__(64) sync_pass_kernel(const SyncStream* __restr
   const int s = locate(streams + 4ull * d, w);
   if (s < 0) return;
   const SyncStream S = streams[4ull * d + s];
-  const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
+  const uint32_t sb = S.sub_bits;
+  const uint64_t L0 = (uint64_t)w * kLanes * (sb / 8);
   const uint32_t lane = threadIdx.x, k = w * kLanes + lane;
   const bool valid = k < S.n_sub;
   const uint64_t g = (uint64_t)S.first_sub + k;
@@ -390,8 +395,8 @@ __global__ void __launch_bounds__(64) sync_pass_kernel(const SyncStream* __restr
     const uint32_t L = S.fixed_len;
     uint32_t n = 0;
     if (valid) {
-      const uint64_t a0 = L0 * 8 + (uint64_t)lane * kSyncSubBits;
-      const uint64_t stop = a0 + kSyncSubBits;
+      const uint64_t a0 = L0 * 8 + (uint64_t)lane * sb;
+      const uint64_t stop = a0 + sb;
       const uint64_t st = (a0 + L - 1) / L * L;
       n = st < stop ? (uint32_t)((stop - st + L - 1) / L) : 0u;
       A.start[g] = st;
@@ -404,24 +409,24 @@ __global__ void __launch_bounds__(64) sync_pass_kernel(const SyncStream* __restr
   }
   stage_wave(S, L0, tables, stage, tab);
   const uint32_t mask = (1u << S.max_bits) - 1;
-  uint32_t st = lane * kSyncSubBits, cnt = 0, ex = st;
-  if (valid) ex = run_rec(stage, tab, mask, st, st, st + kSyncSubBits, cnt, bm);
+  uint32_t st = lane * sb, cnt = 0, ex = st;
+  if (valid) ex = run_rec(stage, tab, mask, st, st, st + sb, cnt, bm);
   bool changed = false, bm_ok = valid;
-  settle(stage, tab, mask, valid, st, ex, cnt, changed, bm, bm_ok);
+  settle(stage, tab, mask, sb, valid, st, ex, cnt, changed, bm, bm_ok);
   if (lane == kLanes - 1 && valid && k + 1 < S.n_sub)
-    __hip_atomic_store(A.pub + blockIdx.x, (A.epoch << 8) | (uint64_t)(ex - kWaveBits), __ATOMIC_RELAXED,
+    __hip_atomic_store(A.pub + blockIdx.x, (A.epoch << 8) | (uint64_t)(ex - kLanes * sb), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   uint32_t rel = 0;
-  if (w > 0 && A.look_back && look_back(A.pub, blockIdx.x - 1, A.epoch, rel) && rel != 0 && rel < kSyncSubBits) {
+  if (w > 0 && A.look_back && look_back(A.pub, blockIdx.x - 1, A.epoch, rel) && rel != 0 && rel < sb) {
     // the true first start lies rel bits into the span: lane 0 joins its
     // recorded path from there (it never restarted, so the bitmap is its
     // path), and a changed exit propagates as in the first settle
     if (lane == 0) {
       st = rel;
-      run_join(stage, tab, mask, 0, st, kSyncSubBits, ex, cnt, bm);
+      run_join(stage, tab, mask, 0, st, sb, ex, cnt, bm);
       bm_ok = false;
     }
-    settle(stage, tab, mask, valid, st, ex, cnt, changed, bm, bm_ok);
+    settle(stage, tab, mask, sb, valid, st, ex, cnt, changed, bm, bm_ok);
   }
   if (valid) {
     A.start[g] = L0 * 8 + st;
@@ -449,7 +454,8 @@ __device__ inline void fix_wave(SyncStream* __restrict__ streams, const uint32_t
   const SyncStream S = streams[4ull * d + s];
   const uint64_t g0 = (uint64_t)S.first_sub + (uint64_t)w * kLanes;
   const uint64_t prev_exit = A.exit[g0 - 1];
-  const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
+  const uint32_t sb = S.sub_bits;
+  const uint64_t L0 = (uint64_t)w * kLanes * (sb / 8);
   __syncthreads();  // the previous wavefront's reads of the staged span are done
   stage_wave(S, L0, tables, stage, tab);
   const uint32_t lane = threadIdx.x, mask = (1u << S.max_bits) - 1;
@@ -464,11 +470,11 @@ __device__ inline void fix_wave(SyncStream* __restrict__ streams, const uint32_t
   const uint32_t ex_before = ex;
   bool changed = false;
   if (lane == 0) {  // prev_exit lies in [L0 * 8, L0 * 8 + 11): a codeword overruns by < 11 bits
-    st = (uint32_t)std::min<uint64_t>(prev_exit - L0 * 8, kSyncSubBits);
-    ex = run(stage, tab, mask, st, kSyncSubBits, cnt);
+    st = (uint32_t)std::min<uint64_t>(prev_exit - L0 * 8, sb);
+    ex = run(stage, tab, mask, st, sb, cnt);
     changed = true;
   }
-  settle(stage, tab, mask, valid, st, ex, cnt, changed);
+  settle(stage, tab, mask, sb, valid, st, ex, cnt, changed);
   if (valid && changed) {
     A.start[g0 + lane] = L0 * 8 + st;
     A.exit[g0 + lane] = L0 * 8 + ex;
@@ -590,7 +596,7 @@ __global__ void __launch_bounds__(64) sync_write_kernel(const SyncStream* __rest
   const SyncStream S = streams[4ull * d + s];
   const uint64_t base = A.wave_prefix[blockIdx.x];
   if (base >= S.n) return;  // the whole wavefront decodes padding
-  const uint64_t L0 = (uint64_t)w * kLanes * kSubBytes;
+  const uint64_t L0 = (uint64_t)w * kLanes * (S.sub_bits / 8);
   stage_wave(S, L0, tables, stage, tab);
   const uint32_t lane = threadIdx.x, mask = (1u << S.max_bits) - 1;
   const uint64_t g = (uint64_t)S.first_sub + (uint64_t)w * kLanes + lane;
@@ -737,6 +743,16 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
   uint64_t subs = 0;
   uint32_t n_def = 0;
   double out_per_wave = 0;  // expected symbols per wavefront, largest over the parallel-path payloads
+  // Subsequence size: kSyncSubBitsMax, or, when the launch's wavefronts at
+  // that size would not fill the device, smaller in proportion (towards
+  // kFillWaves wavefronts), but long enough for about kMinLaneSymbols
+  // symbols per lane at the payload's mean code length (a lane that starts
+  // off a codeword boundary needs a few codewords to resynchronise).
+  constexpr double kFillWaves = 2048, kMinLaneSymbols = 24;
+  double bits_all = 0;
+  for (size_t j = 0; j < n_jobs; ++j)
+    if (hj[j].codec == kCodecHuffman && hj[j].src_len >= kSyncMinBytes) bits_all += 8.0 * (double)hj[j].src_len;
+  const double scale = std::min(1.0, bits_all / (kLanes * (double)kSyncSubBitsMax) / kFillWaves);
   for (size_t j = 0; j < n_jobs; ++j) {
     hj[j].sync_id = 0;
     hj[j].sync_sub0 = 0;
@@ -748,12 +764,17 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
       chunk_job.insert(chunk_job.end(), nc, (uint32_t)j);
     }
     if (hj[j].codec != kCodecHuffman || hj[j].src_len < kSyncMinBytes) continue;
-    const uint64_t u = (hj[j].src_len * 8 + kSyncSubBits - 1) / kSyncSubBits + 4;
+    const double mean_bits = hj[j].dst_len ? 8.0 * (double)hj[j].src_len / (double)hj[j].dst_len : 8.0;
+    const double want = std::max(scale * kSyncSubBitsMax, kMinLaneSymbols * mean_bits);
+    uint32_t sb = kSyncSubBitsMin;
+    while (sb < kSyncSubBitsMax && sb < want) sb += 64;
+    const uint64_t u = (hj[j].src_len * 8 + sb - 1) / sb + 4;
     const uint64_t waves = (u + kLanes - 1) / kLanes + 4;
     if (subs + u > 0xFFFFFFFFull || wave_job.size() + waves > 0x7FFFFFFFull) continue;
     hj[j].sync_id = ++n_def;
     hj[j].sync_sub0 = (uint32_t)subs;
-    out_per_wave = std::max(out_per_wave, (double)kWaveBits * (double)hj[j].dst_len / (8.0 * (double)hj[j].src_len));
+    hj[j].pad[3] = sb;
+    out_per_wave = std::max(out_per_wave, (double)kLanes * sb * (double)hj[j].dst_len / (8.0 * (double)hj[j].src_len));
     job_wave0.push_back((uint32_t)wave_job.size());
     wave_job.insert(wave_job.end(), waves, n_def - 1);
     subs += u;

@@ -64,7 +64,7 @@ struct DecodeJob {
   uint32_t framed;    // 1: src starts with a chunk frame header
   uint32_t sync_id;   // 0, or 1 + slot of a Huffman payload whose streams go to the parallel path
   uint32_t sync_sub0; // first subsequence slot of that payload
-  uint32_t pad[4];
+  uint32_t pad[4];     // Order1ScaleAC: its state (o1sac_device.hip); parallel-path Huffman: pad[3] = subsequence bits
 };
 static_assert(sizeof(DecodeJob) == 64, "DecodeJob layout");
 
