@@ -358,28 +358,24 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
     if (st == kStOk && maxb == 0) st = kStBadHeader;  // no symbol has a code
     if (maxb < 1) maxb = 1;
     // canonical codes (tree.rs:119-141): the first code of each length, with
-    // the overflow checks the serial assignment makes; per length the offset
-    // from a code to its symbol's index in the symbols sorted by (length,
-    // symbol), and the end of its left-aligned code range (the ends rise
-    // with the length)
-    uint32_t sym_base[kHufMaxBits + 1], sym_off[kHufMaxBits + 1], code_end[kHufMaxBits + 1];
-    uint32_t end_max = 0, shorter = 0;
+    // the overflow checks the serial assignment makes; per length the index
+    // of its first symbol in the symbols sorted by (length, symbol), and the
+    // end of its left-aligned code range
+    uint32_t sym_base[kHufMaxBits + 1], code_end[kHufMaxBits + 1];
+    uint32_t shorter = 0;
     {
       uint32_t code = 0, base = 0;
       bool bad = false;
 #pragma unroll
       for (uint32_t b = 1; b <= (uint32_t)kHufMaxBits; ++b) {
         sym_base[b] = 0;
-        sym_off[b] = 0;
         code_end[b] = 0;
         if (b <= maxb) {
           code = ((code + cnt[b - 1]) << 1) & 0xFFFF;
           bad |= code > (1u << b) || (cnt[b] && code + cnt[b] - 1 >= (1u << b));
           sym_base[b] = base;
-          sym_off[b] = base - code;
           base += cnt[b];
           code_end[b] = (code + cnt[b]) << (maxb - b);
-          if (b == maxb) end_max = code_end[b];
           if (b < maxb) shorter += cnt[b];
         }
       }
@@ -419,26 +415,26 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
       return;
     }
     // table: index i holds the next max_bits stream bits, first bit lowest;
-    // reversed, it is the left-aligned code value v, whose length is the
-    // first whose code range ends above v
+    // reversed, it is the left-aligned code value v.  The codes of length l
+    // take v in [code_end[l - 1], code_end[l]), each symbol 2^(max_bits - l)
+    // consecutive values in symbol order; the values past the last range
+    // (an incomplete code) hold the fallback entry.  Filled length by
+    // length, a value per lane.
     const uint32_t max_bits = maxb;
     const uint32_t tsize = 1u << max_bits;
     const uint16_t fallback = (uint16_t)(max_bits << 8);
-    for (uint32_t i = lane; i < tsize; i += 64) {
-      const uint32_t v = __builtin_bitreverse32(i) >> (32 - max_bits);
-      uint16_t e = fallback;
-      if (v < end_max) {
-        uint32_t l = 1, off = sym_off[1];
+    uint32_t vstart = 0;
 #pragma unroll
-        for (uint32_t b = 1; b < (uint32_t)kHufMaxBits; ++b)
-          if (b < max_bits && v >= code_end[b]) {
-            l = b + 1;
-            off = sym_off[b + 1];
-          }
-        e = (uint16_t)((l << 8) | sorted_sym[(v >> (max_bits - l)) + off]);
+    for (uint32_t l = 1; l <= (uint32_t)kHufMaxBits; ++l) {
+      if (l <= max_bits) {
+        const uint32_t vend = code_end[l], sh = max_bits - l, sb = sym_base[l];
+        for (uint32_t v = vstart + lane; v < vend; v += 64)
+          table16[__builtin_bitreverse32(v) >> (32 - max_bits)] =
+              (uint16_t)((l << 8) | sorted_sym[sb + ((v - vstart) >> sh)]);
+        vstart = vend;
       }
-      table16[i] = e;
     }
+    for (uint32_t v = vstart + lane; v < tsize; v += 64) table16[__builtin_bitreverse32(v) >> (32 - max_bits)] = fallback;
     __syncthreads();
 
     if (job.sync_id) {
