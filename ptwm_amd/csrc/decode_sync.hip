@@ -748,7 +748,7 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
   // kFillWaves wavefronts), but long enough for about kMinLaneSymbols
   // symbols per lane at the payload's mean code length (a lane that starts
   // off a codeword boundary needs a few codewords to resynchronise).
-  constexpr double kFillWaves = 2048, kMinLaneSymbols = 24;
+  constexpr double kFillWaves = 2048, kMinLaneSymbols = 24, kWaveSymbols = 6400;
   double bits_all = 0;
   for (size_t j = 0; j < n_jobs; ++j)
     if (hj[j].codec == kCodecHuffman && hj[j].src_len >= kSyncMinBytes) bits_all += 8.0 * (double)hj[j].src_len;
@@ -768,6 +768,9 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
     const double want = std::max(scale * kSyncSubBitsMax, kMinLaneSymbols * mean_bits);
     uint32_t sb = kSyncSubBitsMin;
     while (sb < kSyncSubBitsMax && sb < want) sb += 64;
+    // at most about kWaveSymbols symbols per wavefront, so that the write
+    // pass's LDS output staging stays small
+    while (sb > kSyncSubBitsMin && kLanes * (double)sb > kWaveSymbols * mean_bits) sb -= 64;
     const uint64_t u = (hj[j].src_len * 8 + sb - 1) / sb + 4;
     const uint64_t waves = (u + kLanes - 1) / kLanes + 4;
     if (subs + u > 0xFFFFFFFFull || wave_job.size() + waves > 0x7FFFFFFFull) continue;
