@@ -577,6 +577,42 @@ __global__ void __launch_bounds__(256) sync_scan_kernel(const SyncStream* __rest
     report_stream(S, s, A.verdict, d, S.n == 0 && S.m == 0, status);
 }
 
+// Symbols [0, m) of a lane of a fixed-length code (length L, K L <= 32)
+// from bit p0: K independent lookups per window of the bit reader, into the
+// LDS output staging (o) or straight to memory (gd).
+template <uint32_t K, bool kStaged>
+__device__ inline void write_fixed(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t L, uint32_t p0,
+                                   uint32_t m, uint8_t* o, uint64_t gd) {
+  Cursor k = cur_open(stage, p0);
+  uint32_t i = 0;
+  for (; i + K <= m; i += K) {
+    const uint32_t win = cur_win(k);
+    uint32_t e[K];
+#pragma unroll
+    for (uint32_t j = 0; j < K; ++j) e[j] = tab[(win >> (j * L)) & mask];
+    cur_adv(k, stage, K * L);
+#pragma unroll
+    for (uint32_t j = 0; j < K; ++j) {
+      if constexpr (kStaged) o[i + j] = (uint8_t)e[j];
+      else g_st<uint8_t>(gd + i + j, (uint8_t)e[j]);
+    }
+  }
+  for (; i < m; ++i) {
+    const uint32_t e = tab[cur_win(k) & mask];
+    cur_adv(k, stage, L);
+    if constexpr (kStaged) o[i] = (uint8_t)e;
+    else g_st<uint8_t>(gd + i, (uint8_t)e);
+  }
+}
+template <bool kStaged>
+__device__ inline void write_fixed_any(const uint32_t* stage, const uint16_t* tab, uint32_t mask, uint32_t L,
+                                       uint32_t p0, uint32_t m, uint8_t* o, uint64_t gd) {
+  if (L <= 4) write_fixed<8, kStaged>(stage, tab, mask, L, p0, m, o, gd);
+  else if (L <= 8) write_fixed<4, kStaged>(stage, tab, mask, L, p0, m, o, gd);
+  else if (L <= 10) write_fixed<3, kStaged>(stage, tab, mask, L, p0, m, o, gd);
+  else write_fixed<2, kStaged>(stage, tab, mask, L, p0, m, o, gd);
+}
+
 // Decode again from the settled starts and write symbols [0, n) of the
 // segment; the lane holding symbol n-1 records where it ends.  Symbols are
 // staged in LDS at their output address mod 16, so the store is dwordx4.
@@ -618,21 +654,10 @@ __global__ void __launch_bounds__(64) sync_write_kernel(const SyncStream* __rest
     // not depend on each other
     const uint32_t L = S.fixed_len, p0 = (uint32_t)(A.start[g] - L0 * 8);
     const uint32_t m = (uint32_t)std::min<uint64_t>(cnt, S.n - first);
-    if (staged) {
-      uint8_t* const o = out + skew + (first - base);
-#pragma unroll 4
-      for (uint32_t i = 0; i < m; ++i) {
-        const uint32_t p = p0 + i * L, wi = p >> 5;
-        o[i] = (uint8_t)tab[__builtin_amdgcn_alignbit(stage[wi + 1], stage[wi], p & 31u) & mask];
-      }
-    } else {
-#pragma unroll 4
-      for (uint32_t i = 0; i < m; ++i) {
-        const uint32_t p = p0 + i * L, wi = p >> 5;
-        g_st<uint8_t>(S.dst + first + i,
-                      (uint8_t)tab[__builtin_amdgcn_alignbit(stage[wi + 1], stage[wi], p & 31u) & mask]);
-      }
-    }
+    uint8_t* const o = out + skew + (first - base);
+    const uint64_t gd = S.dst + first;
+    if (staged) write_fixed_any<true>(stage, tab, mask, L, p0, m, o, gd);
+    else write_fixed_any<false>(stage, tab, mask, L, p0, m, o, gd);
     if (first + m == S.n) report_stream(S, (uint32_t)s, A.verdict, d, stream_exact(S, L0 * 8 + p0 + m * L), status);
   } else if (valid && first < S.n) {
     Cursor k = cur_open(stage, (uint32_t)(A.start[g] - L0 * 8));
