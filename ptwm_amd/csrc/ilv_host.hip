@@ -346,13 +346,30 @@ int64_t ilv_decode_tensors(DevCtx& ctx, const std::vector<IlvTensor>& tensors_in
     return codes;
   };
   std::vector<uint32_t> idx;  // per launch: [m + 1 prefix][m tensor indexes]
+  // Within a launch, the tensors whose tiles build decode tables come first:
+  // the workgroups of the last tiles start a few microseconds late and set
+  // up under the others' streaming traffic, so the tiles with the longest
+  // setup (table builds and staging) go to the first workgroups (MXFP4: the
+  // coded E8M0 scales ahead of the packed weights).
+  std::vector<uint32_t> order;
+  order.reserve(nt);
+  for (int pass = 0; pass < 2; ++pass)
+    for (uint32_t ti = 0; ti < nt; ++ti) {
+      const IlvTensor& T = tensors[ti];
+      bool tables = false;
+      for (uint32_t p = 0; p < T.n_planes; ++p) {
+        const IlvPlane& P = T.planes[p];
+        tables |= P.coded && P.len != T.n + 1 && P.len != kPackedHeadBytes + (T.n + 1) / 2;
+      }
+      if (tables == (pass == 0)) order.push_back(ti);
+    }
   for (uint32_t fam = kFamilyHuff; fam <= kFamilyRans; ++fam)
   for (uint32_t chain : launch_codes(fam)) {
     std::vector<uint32_t> tix, tpre{0};
     uint32_t slots = 0;
     uint64_t est = 0;
     bool crc = false;
-    for (uint32_t ti = 0; ti < nt; ++ti) {
+    for (const uint32_t ti : order) {
       const IlvTensor& T = tensors[ti];
       if (T.family != fam || !ilv_code_has(chain, T.chain) || T.n == 0) continue;
       if (T.crc_first != kIlvNoCrc) {
