@@ -163,6 +163,63 @@ def test_unsettled_streams_take_the_host_fix_passes(monkeypatch):
     assert (got is None) == (want is None) and (want is None or got == want)
 
 
+def _random_plane(rng, n):
+    kind = int(rng.integers(0, 6))
+    if kind == 0:
+        return rng.geometric(float(rng.choice([0.05, 0.2, 0.5, 0.8])), n).clip(0, 255).astype(np.uint8)
+    if kind == 1:  # uniform over k symbols (16: a fixed-length code; 256: stored)
+        return rng.integers(0, int(rng.choice([2, 3, 16, 64, 256])), n).astype(np.uint8)
+    if kind == 2:  # Zipf-like
+        return (rng.zipf(float(rng.choice([1.3, 2.0])), n) % 256).astype(np.uint8)
+    if kind == 3:  # two clusters
+        return np.where(rng.random(n) < 0.7, rng.integers(100, 104, n), rng.integers(0, 256, n)).astype(np.uint8)
+    if kind == 4:  # runs
+        return np.repeat(rng.integers(0, 8, n // 64 + 1), 64)[:n].astype(np.uint8)
+    return (rng.normal(128, float(rng.choice([1.0, 6.0, 30.0])), n).clip(0, 255)).astype(np.uint8)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_parallel_huffman_batches_match_reference(seed):
+    """Several reference Huffman payloads of varied sizes and symbol
+    distributions in one launch (passthrough tensors of one plan): their
+    subsequence sizes, fixed- and variable-length codes and stored payloads
+    mix in the passes; every tensor restores the oracle decoder's bytes.  In
+    half the batches one payload has a stream bit flipped, and the call then
+    fails exactly when the oracle decoder rejects that payload."""
+    from ptwm_amd import plan as P
+    rng = np.random.default_rng(1000 + seed)
+    k = int(rng.integers(2, 7))
+    planes = [_random_plane(rng, int(rng.integers(20_000, 2_500_000))).tobytes() for _ in range(k)]
+    payloads = [O.codec_encode(O.CODEC_HUFFMAN, pl) for pl in planes]
+    bad = int(rng.integers(0, k)) if seed % 2 else -1
+    if bad >= 0 and payloads[bad][0] == 1:
+        b = bytearray(payloads[bad])
+        i = int(rng.integers(_streams_start(payloads[bad]), len(b)))
+        b[i] ^= 1 << int(rng.integers(0, 8))
+        payloads[bad] = bytes(b)
+    blob, tensors, off_out = b"", [], 0
+    for pl, pay in zip(planes, payloads):
+        tensors.append(P.TensorPlan(P.CHAIN_PASSTHROUGH, off_out, len(pl),
+                                    [P.PlanePlan(O.CODEC_HUFFMAN, len(blob), len(pay), len(pl))]))
+        blob += pay + bytes(-len(pay) % 16)
+        off_out += (len(pl) + 255) // 256 * 256
+    want = [oracle_decode(pay, len(pl)) for pl, pay in zip(planes, payloads)]
+    note(f"sync batch {seed}: {k} payloads, sizes {[len(p) for p in planes]}, tags {[p[0] for p in payloads]}, "
+         f"corrupted {bad}, oracle rejects {[w is None for w in want]}")
+    out = torch.zeros(off_out + 16, dtype=torch.uint8, device="cuda:0")
+    try:
+        n = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL,
+                                                      P.encode_plan(tensors), dev(blob), out[:off_out], 0)
+        torch.cuda.synchronize()
+    except Exception:  # noqa: BLE001
+        n = None
+    assert (n is None) == any(w is None for w in want)
+    if n is not None:
+        got = out.cpu().numpy().tobytes()
+        for t, w in zip(tensors, want):
+            assert got[t.out_offset:t.out_offset + t.out_len] == w
+
+
 @pytest.mark.parametrize("n", [4095, 4096, 4097, 65536, 65539, (1 << 20) + 1, 3 * (1 << 20) + 7])
 def test_stored_payload_copy(n):
     """Stored (tag 0) payloads of 4 KiB and more are copied by the
