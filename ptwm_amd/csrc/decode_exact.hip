@@ -269,7 +269,7 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
   if (h.kind == 0) {  // stored bytes
     const uint8_t* s = src + h.copy_off;
     if (copy_src && job.dst_len >= kCopyDeferMin) {
-      // large: copied by raw_copy_kernel, one workgroup per 64 KiB
+      // large: copied by the parallel path's first pass or raw_copy_kernel, in pieces
       if (lane == 0) {
         copy_src[blockIdx.x] = reinterpret_cast<uint64_t>(s);
         status[blockIdx.x] = kStOk;
