@@ -44,6 +44,25 @@ constexpr uint32_t kRansRing = 2048;
 constexpr uint32_t kRansRingPad = 16;
 constexpr uint32_t kRansStageGranules = 32;   // 2 per lane: 512 bytes per chain per round
 constexpr uint32_t kRansRound = 256;          // <= 2 bytes per symbol: 512 bytes per chain
+constexpr uint32_t kTansStageWords = 1024;    // tANS stream words staged at a time (4 KiB)
+
+// inclusive sum over the wavefront: within each row of 16 lanes by row
+// shifts, then each row's predecessors' totals through the row broadcasts
+// of lanes 15 and 31
+__device__ __forceinline__ uint32_t wave_incl_sum_u32(uint32_t v) {
+  uint32_t x = v;
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
+  return x;
+}
+__device__ __forceinline__ uint32_t wave_excl_sum_u32(uint32_t v) { return wave_incl_sum_u32(v) - v; }
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  return __builtin_amdgcn_readlane(wave_incl_sum_u32(v), 63);
+}
 
 __device__ inline uint32_t ld_u32le(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
@@ -497,98 +516,7 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
     return;
   }
 
-  if (h.kind == 5) {
-    // ---- tANS (entropy/tans/mod.rs:372-455): one serial state chain ----
-    // Header: table_log 11, nsym in 2..=256, (sym u8, freq u16) pairs with no
-    // repeat and no zero summing to L = 2048, total_bits u64 <= 8 x stream.
-    __shared__ uint16_t tcum[256];
-    if (lane == 0) {
-      uint32_t st = kStOk, nsym = 0, sum = 0;
-      if (enc_len < 3 || enc[0] != 11) {
-        st = kStBadHeader;
-      } else {
-        nsym = (uint32_t)enc[1] | ((uint32_t)enc[2] << 8);
-        if (nsym < 2 || nsym > 256 || 3 + 3 * (uint64_t)nsym + 8 > enc_len) st = kStBadHeader;
-      }
-      for (int s = 0; s < 256; ++s) rev[s] = 0;  // reuse: normalized frequency per symbol
-      for (uint32_t i = 0; st == kStOk && i < nsym; ++i) {
-        const uint8_t* e = enc + 3 + 3 * i;
-        const uint32_t s = e[0], f = (uint32_t)e[1] | ((uint32_t)e[2] << 8);
-        if (rev[s] != 0 || f == 0) st = kStBadHeader;
-        rev[s] = (uint16_t)f;
-        sum += f;
-      }
-      if (st == kStOk && sum != 2048) st = kStBadHeader;
-      const uint64_t bs_off = 3 + 3 * (uint64_t)nsym + 8;
-      if (st == kStOk) {
-        uint64_t tb = 0;
-        for (int k = 7; k >= 0; --k) tb = (tb << 8) | enc[bs_off - 8 + (uint64_t)k];
-        if (tb > (enc_len - bs_off) * 8) st = kStBadHeader;
-        h.seg_src[0] = bs_off;
-        h.seg_len[0] = tb;  // total bits of the stream
-      }
-      uint32_t run = 0;
-      for (int s = 0; s < 256; ++s) {
-        tcum[s] = (uint16_t)run;
-        run += rev[s];
-      }
-      h.status = st;
-    }
-    __syncthreads();
-    if (h.status != kStOk) {
-      if (lane == 0) status[blockIdx.x] = h.status;
-      return;
-    }
-    // spread (mod.rs:199-211): the k-th placement, in symbol order, lands on
-    // slot k (L/2 + L/8 + 3) mod L; the step is odd, so every slot once
-    for (uint32_t s = lane; s < 256; s += 64)
-      for (uint32_t k = tcum[s], e = tcum[s] + rev[s]; k < e; ++k) table32[(k * 1283u) & 2047u] = s;
-    __syncthreads();
-    if (lane == 0) {
-      // build_decode (mod.rs:346-368): slots in order; the occurrence x of
-      // the slot's symbol runs from norm[s] to 2 norm[s] - 1
-      for (uint32_t u = 0; u < 2048; ++u) {
-        const uint32_t s = table32[u] & 255u;
-        const uint32_t x = rev[s]++;
-        const uint32_t nb = 11u - (31u - (uint32_t)__builtin_clz(x));
-        table32[u] = s | (nb << 8) | (((x << nb) - 2048u) << 16);
-      }
-      // LIFO reader (mod.rs:102-150): pops the nb bits below `pos`; a 64-bit
-      // window of the stream at bit wb serves several pops per reload
-      const uint8_t* bs = enc + h.seg_src[0];
-      const uint64_t bl = enc_len - h.seg_src[0];
-      uint64_t pos = h.seg_len[0], wb = ~0ull, w = 0;
-      bool good = true;
-      auto pop = [&](uint32_t nb) -> uint32_t {
-        if (nb == 0) return 0;
-        if (pos < nb) {
-          good = false;
-          return 0;
-        }
-        const uint64_t start = pos - nb;
-        if (wb == ~0ull || start < wb) {
-          wb = start > 40 ? (start - 40) & ~7ull : 0;
-          w = 0;
-          for (uint64_t k = 0; k < 8; ++k)
-            if ((wb >> 3) + k < bl) w |= (uint64_t)g_ld<uint8_t>((uint64_t)(bs + (wb >> 3) + k)) << (8 * k);
-        }
-        pos = start;
-        return (uint32_t)(w >> (start - wb)) & ((1u << nb) - 1u);
-      };
-      uint32_t state = pop(11);
-      if (state >= 2048u) good = false;
-      for (uint64_t i = 0; good && i < job.dst_len; ++i) {
-        const uint32_t e = table32[state];
-        g_st<uint8_t>((uint64_t)(dst + i), (uint8_t)e);
-        state = (e >> 16) + pop((e >> 8) & 15u);
-        if (state >= 2048u) good = false;
-      }
-      // fully consumed and back at the start state (mod.rs:444-453)
-      if (good && (pos != 0 || state != 0)) good = false;
-      status[blockIdx.x] = good ? kStOk : kStBadStream;
-    }
-    return;
-  }
+  if (h.kind == 5) return;  // tans_decode_kernel's job
   if (lane == 0) status[blockIdx.x] = kStBadTag;  // not reached: parse_job gives rANS jobs kind 2
   return;
   } else {
@@ -782,12 +710,235 @@ __global__ void __launch_bounds__(64) decode_exact_kernel(const DecodeJob* __res
   }
 }
 
+// tANS payloads: one serial state chain each.  The job is parsed as
+// decode_exact_kernel parses it; that kernel reports every other outcome of
+// a tANS job (refusals, stored payloads, empty planes), this one the chains.
+__global__ void __launch_bounds__(64) tans_decode_kernel(const DecodeJob* __restrict__ jobs,
+                                                         uint32_t* __restrict__ status) {
+  __shared__ SharedHeader h;
+  __shared__ uint16_t rev[256];
+  __shared__ uint8_t sorted_sym[256];
+  __shared__ __align__(16) uint32_t table32[2048];
+  const uint32_t lane = threadIdx.x;
+  const DecodeJob job = jobs[blockIdx.x];
+  if (job.codec != kCodecTans) return;
+  if (lane == 0) parse_job(job, h);
+  __syncthreads();
+  if (h.status != kStOk || h.kind != 5) return;
+  uint8_t* dst = reinterpret_cast<uint8_t*>(job.dst);
+  const uint8_t* enc = reinterpret_cast<const uint8_t*>(job.src) + h.enc_off;
+  const uint64_t enc_len = h.enc_len;
+  // ---- tANS (entropy/tans/mod.rs:372-455): one serial state chain ----
+  // Header: table_log 11, nsym in 2..=256, (sym u8, freq u16) pairs with no
+  // repeat and no zero summing to L = 2048, total_bits u64 <= 8 x stream.
+  // The wavefront parses it (four entries per lane; a repeat shows as a
+  // symbol whose owner slot names another entry), builds the decode table
+  // slot-parallel, then runs the state chain with wave-uniform state.
+  __shared__ uint16_t tcum[256];
+  __shared__ __align__(16) uint32_t tstage[kTansStageWords];
+  uint8_t* const owner = sorted_sym;  // reuse: the entry that names a symbol
+  for (uint32_t s = lane; s < 256; s += 64) rev[s] = 0;  // reuse: normalized frequency per symbol
+  uint32_t nsym = 0;
+  bool hok = enc_len >= 3 && g_ld<uint8_t>((uint64_t)enc) == 11;
+  if (hok) {
+    nsym = g_ld<uint8_t>((uint64_t)(enc + 1)) | ((uint32_t)g_ld<uint8_t>((uint64_t)(enc + 2)) << 8);
+    hok = nsym >= 2 && nsym <= 256 && 3 + 3 * (uint64_t)nsym + 8 <= enc_len;
+  }
+  uint32_t es[4], ef[4];
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t i = lane + 64 * k;
+    es[k] = 0;
+    ef[k] = 0;
+    if (hok && i < nsym) {
+      const uint8_t* e = enc + 3 + 3 * i;
+      es[k] = g_ld<uint8_t>((uint64_t)e);
+      ef[k] = g_ld<uint8_t>((uint64_t)(e + 1)) | ((uint32_t)g_ld<uint8_t>((uint64_t)(e + 2)) << 8);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k)
+    if (hok && lane + 64 * k < nsym) owner[es[k]] = (uint8_t)(lane + 64 * k);
+  __syncthreads();
+  bool bad = false;
+  uint32_t sum = 0;
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    if (hok && lane + 64 * k < nsym) {
+      bad |= owner[es[k]] != (uint8_t)(lane + 64 * k) || ef[k] == 0;  // a repeat, or a zero
+      sum += ef[k];
+      rev[es[k]] = (uint16_t)ef[k];
+    }
+  }
+  uint64_t tb = 0;
+  const uint64_t bs_off = 3 + 3 * (uint64_t)nsym + 8;
+  if (hok) {
+#pragma unroll
+    for (int k = 7; k >= 0; --k) tb = (tb << 8) | g_ld<uint8_t>((uint64_t)(enc + bs_off - 8 + (uint64_t)k));
+  }
+  hok = hok && __ballot(bad) == 0 && wave_sum_u32(sum) == 2048 && tb <= (enc_len - bs_off) * 8;
+  if (!hok) {
+    if (lane == 0) status[blockIdx.x] = kStBadHeader;
+    return;
+  }
+  __syncthreads();
+  {
+    uint32_t c[4], t = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) t += (c[k] = rev[4 * lane + k]);
+    uint32_t run = wave_excl_sum_u32(t);
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+      tcum[4 * lane + k] = (uint16_t)run;
+      run += c[k];
+    }
+  }
+  __syncthreads();
+  // spread (mod.rs:199-211): the k-th placement, in symbol order, lands on
+  // slot k (L/2 + L/8 + 3) mod L; the step is odd, so every slot once
+  for (uint32_t s = lane; s < 256; s += 64)
+    for (uint32_t k = tcum[s], e = tcum[s] + rev[s]; k < e; ++k) table32[(k * 1283u) & 2047u] = s;
+  __syncthreads();
+  // build_decode (mod.rs:346-368): slots in order; the occurrence x of the
+  // slot's symbol runs from norm[s] to 2 norm[s] - 1.  64 slots a round:
+  // a slot's x is its symbol's count so far plus the lanes below it with
+  // the same symbol (eight ballots find them); the group's last lane
+  // advances the count.
+  for (uint32_t u0 = 0; u0 < 2048; u0 += 64) {
+    const uint32_t u = u0 + lane;
+    const uint32_t sy = table32[u] & 255u;
+    uint64_t same = ~0ull;
+#pragma unroll
+    for (uint32_t bit = 0; bit < 8; ++bit) {
+      const uint64_t bl = __ballot((sy >> bit) & 1u);
+      same &= ((sy >> bit) & 1u) ? bl : ~bl;
+    }
+    const uint64_t below = same & ((1ull << lane) - 1ull);
+    const uint32_t x = rev[sy] + (uint32_t)__popcll(below);
+    __builtin_amdgcn_wave_barrier();
+    if ((same >> lane) == 1ull) rev[sy] = (uint16_t)(x + 1);
+    const uint32_t nb = 11u - (31u - (uint32_t)__builtin_clz(x));
+    table32[u] = sy | (nb << 8) | (((x << nb) - 2048u) << 16);
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  // LIFO reader (mod.rs:102-150): pops the nb bits below `pos` (bit i of
+  // the stream is bit i & 7 of byte i >> 3).  The stream is staged in LDS
+  // as 32-bit words, kTansStageWords at a time from its end down; a 64-bit
+  // register window holds bits [32 wi, 32 wi + 64) and takes the next
+  // lower word (read one refill earlier) when fewer than 32 bits lie below
+  // pos.  The decode table sits in registers: entry u in register u / 64
+  // of lane u % 64, read by a register-indexed move and a lane read.
+  const uint8_t* bs = enc + bs_off;
+  const uint64_t bl = enc_len - bs_off;
+  const int64_t top = tb ? (int64_t)((tb - 1) >> 5) : -1;  // word holding bit tb - 1
+  int64_t stage_lo = top >= 0 ? top / kTansStageWords * kTansStageWords : 0;  // first word staged
+  auto stage = [&]() {  // words stage_lo.. ; bytes past the stream read as zero
+    __syncthreads();
+    if (bl == 0) {
+      for (uint32_t j = lane; j < kTansStageWords; j += 64) tstage[j] = 0;
+    } else {
+#pragma unroll 4
+      for (uint32_t j = lane; j < kTansStageWords; j += 64) {
+        const uint64_t b0 = 4ull * ((uint64_t)stage_lo + j);
+        uint32_t v = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+          const uint32_t x = g_ld<uint8_t>((uint64_t)(bs + (b0 + q < bl ? b0 + q : bl - 1)));
+          v |= (b0 + q < bl ? x : 0u) << (8 * q);
+        }
+        tstage[j] = v;
+      }
+    }
+    __syncthreads();
+  };
+  // word w of the stream as read from the stage (0 below the stream); the
+  // value is a vector register, made wave-uniform where it is used
+  auto word = [&](int64_t w) -> uint32_t {
+    if (w < 0) return 0u;
+    if (w < stage_lo) {
+      stage_lo -= kTansStageWords;
+      stage();
+    }
+    return tstage[w - stage_lo];
+  };
+  stage();
+  uint32_t tab[32];
+#pragma unroll
+  for (uint32_t r = 0; r < 32; ++r) tab[r] = table32[64 * r + lane];
+  // the window starts at bit 32 wi (wi < 0: bits below the stream, zero);
+  // rel = pos - 32 wi.  pos only decreases, so a pop below the stream's
+  // start (pos < nb) leaves pos negative at the end: the chain runs on
+  // through zero bits and the final check refuses it.
+  int64_t wi = top - 1;
+  const uint32_t w_top = __builtin_amdgcn_readfirstlane(word(top));
+  uint64_t win = ((uint64_t)w_top << 32) | (uint32_t)__builtin_amdgcn_readfirstlane(word(top - 1));
+  uint32_t next = word(top - 2);
+  uint32_t rel = (uint32_t)(tb - 32 * (uint64_t)(top - 1));  // tb - 32 wi, in [33, 64] (tb > 0)
+  auto refill = [&]() {
+    win = (win << 32) | (uint32_t)__builtin_amdgcn_readfirstlane(next);
+    rel += 32;
+    --wi;
+    next = word(wi - 1);
+  };
+  uint32_t state = 0;
+  if (tb >= 11) {
+    rel -= 11;
+    state = (uint32_t)(win >> rel) & 2047u;
+    if (rel < 32) refill();
+  }
+  // one step: the symbol of `state`, then its nb bits
+  auto step = [&]() -> uint32_t {
+    const uint32_t e = __builtin_amdgcn_readlane(tab[__builtin_amdgcn_readfirstlane(state >> 6)], state & 63u);
+    const uint32_t nb = (e >> 8) & 15u;
+    rel -= nb;  // rel >= 32 before the pop, nb <= 11
+    state = (e >> 16) + ((uint32_t)(win >> rel) & ((1u << nb) - 1u));
+    if (rel < 32) refill();
+    return e & 255u;
+  };
+  uint8_t* const out = dst;
+  const uint64_t n = tb >= 11 ? job.dst_len : 0;
+  for (uint64_t i = 0; i < n; i += 256) {
+    // 256 symbols a round, four to a lane's word
+    const uint32_t m = n - i < 256 ? (uint32_t)(n - i) : 256u;
+    uint32_t outv = 0, j = 0;
+    for (; j + 4 <= m; j += 4) {
+      uint32_t pk = step();
+      pk |= step() << 8;
+      pk |= step() << 16;
+      pk |= step() << 24;
+      outv = lane == (j >> 2) ? pk : outv;
+    }
+    if (j < m) {
+      uint32_t pk = 0;
+      for (uint32_t t = 0; j + t < m; ++t) pk |= step() << (8 * t);
+      outv = lane == (j >> 2) ? pk : outv;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q)
+      if (4 * lane + q < m) g_st<uint8_t>((uint64_t)(out + i + 4 * lane + q), (uint8_t)(outv >> (8 * q)));
+  }
+  const int64_t pos = tb >= 11 ? 32 * wi + (int64_t)rel : -1;
+  bool good = true;
+  // fully consumed and back at the start state (mod.rs:444-453)
+  if (good && (pos != 0 || state != 0)) good = false;
+  if (lane == 0) status[blockIdx.x] = good ? kStOk : kStBadStream;
+  return;
+}
+
 hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
                                SyncStream* sync_streams, uint16_t* sync_tables, uint64_t* copy_src,
                                hipStream_t stream) {
   if (n_jobs == 0) return hipSuccess;
   hipLaunchKernelGGL(decode_exact_kernel<false>, dim3(n_jobs), dim3(64), 0, stream, jobs_dev, status_dev, sync_streams,
                      sync_tables, copy_src);
+  return hipGetLastError();
+}
+
+hipError_t launch_tans_decode(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs, hipStream_t stream) {
+  if (n_jobs == 0) return hipSuccess;
+  hipLaunchKernelGGL(tans_decode_kernel, dim3(n_jobs), dim3(64), 0, stream, jobs_dev, status_dev);
   return hipGetLastError();
 }
 

@@ -91,6 +91,9 @@ constexpr uint32_t kSyncTableEntries = 2048;
 hipError_t launch_decode_exact(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs,
                                SyncStream* sync_streams, uint16_t* sync_tables, uint64_t* copy_src,
                                hipStream_t stream);
+// tANS chains of the jobs with codec tANS (launch_decode_exact parses them
+// too and reports their refusals, stored payloads and empty planes).
+hipError_t launch_tans_decode(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs, hipStream_t stream);
 // Zstd payloads of the job list (zstd_device.hip): one workgroup per job,
 // jobs of other codecs are left to the exact kernel
 hipError_t launch_zstd_decode(const DecodeJob* jobs_dev, uint32_t* status_dev, uint32_t n_jobs, hipStream_t stream);

@@ -874,9 +874,13 @@ int64_t decode_jobs_launch(DevCtx& ctx, DecodeJob* hj, size_t n_jobs, ExactRun& 
   uint32_t* status = static_cast<uint32_t*>(ctx.h_job_status.ptr);
   run.out_stage = (uint32_t)std::min<double>(kOutStageMax, 1.25 * out_per_wave + 64);
   PTWM_HIP_TRY(launch_decode_exact(d_jobs, status, (uint32_t)n_jobs, streams, tables, d_copy_src, s));
-  bool any_zstd = false;
-  for (size_t j = 0; j < n_jobs; ++j) any_zstd |= hj[j].codec == kCodecZstd;
+  bool any_zstd = false, any_tans = false;
+  for (size_t j = 0; j < n_jobs; ++j) {
+    any_zstd |= hj[j].codec == kCodecZstd;
+    any_tans |= hj[j].codec == kCodecTans;
+  }
   if (any_zstd) PTWM_HIP_TRY(launch_zstd_decode(d_jobs, status, (uint32_t)n_jobs, s));
+  if (any_tans) PTWM_HIP_TRY(launch_tans_decode(d_jobs, status, (uint32_t)n_jobs, s));
   // reference rANS payloads are a few long serial chains: they run on the
   // side stream while this stream decodes everything else
   bool any_rans = false;

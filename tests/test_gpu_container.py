@@ -134,6 +134,47 @@ def test_tans_payloads_decode_bit_exact(name, plane):
     assert np.array_equal(got[tensors[1].out_offset:tensors[1].out_offset + n], plane)
 
 
+def _tans_top_word(payload):
+    """Index of the stream word holding the last coded bit (the decoder
+    stages the stream in pieces of 1024 words from the end down)."""
+    enc = payload[5:]
+    nsym = enc[1] | (enc[2] << 8)
+    off = 3 + 3 * nsym + 8
+    tb = int.from_bytes(enc[off - 8:off], "little")
+    return (tb - 1) >> 5
+
+
+@pytest.mark.parametrize("edge", [0, 1, 2])
+def test_tans_streams_whose_last_words_straddle_a_stage_piece(edge):
+    """The decoder reads the top word, the one below and the next one before
+    the first symbol: streams whose top word is the first, second or third
+    of a 1024-word piece restage on one of those reads."""
+    rng = np.random.default_rng(40 + edge)
+    base = np.clip(rng.normal(120, 20, 200_000), 0, 255).astype(np.uint8)
+    # h bits per symbol on average: aim at the piece edge, then walk outwards
+    n0 = 150_000
+    h = 32 * _tans_top_word(O.codec_encode(O.CODEC_TANS, base[:n0])) / n0
+    aim = int((32 * (1024 * 29 + edge) + 16) / h)
+    found = None
+    for d in range(400):
+        for n in (aim + d, aim - d):
+            pay = O.codec_encode(O.CODEC_TANS, base[:n])
+            top = _tans_top_word(pay)
+            if top % 1024 == edge:
+                found = n
+                break
+        if found:
+            break
+    assert found, "no prefix length puts the top word at the piece edge"
+    n = found
+    note(f"tans stage edge {edge}: n={n} top word {top}")
+    plane = base[:n]
+    t = P.TensorPlan(P.CHAIN_PASSTHROUGH, 0, n, [P.PlanePlan(O.CODEC_TANS, 0, len(pay), n)])
+    out = torch.zeros(n, dtype=torch.uint8, device="cuda:0")
+    assert dispatch(P.encode_plan([t]), dev_bytes(pay), out) == n
+    assert np.array_equal(out.cpu().numpy(), plane)
+
+
 def test_tans_planes_of_a_bf16_tensor():
     w = (torch.randn(1000, 1500, generator=torch.Generator().manual_seed(2)) * 0.02).to(torch.bfloat16)
     data = w.view(torch.uint8).reshape(-1).numpy().tobytes()
