@@ -26,6 +26,10 @@ namespace ptwm {
 namespace {
 
 constexpr uint32_t kZBlockMax = 128u * 1024u;
+constexpr uint32_t kZBatch = 256;               // sequences decoded per batch
+constexpr uint32_t kZRing = 64u * 1024u;        // LDS history ring (bytes)
+constexpr uint32_t kZLitStage = 16u * 1024u;    // literal bytes of a batch staged in LDS
+constexpr uint32_t kZSeqStage = 1024;            // sequence stream words staged per batch
 constexpr uint32_t kZHufMax = 12;
 
 // code tables of RFC 8878 3.1.1.3.2.1 and default distributions 3.1.1.3.2.2
@@ -49,53 +53,144 @@ __device__ __forceinline__ uint32_t hibit(uint32_t x) { return 31u - (uint32_t)_
 
 // Backward bit reader (RFC 8878 4.1 / 4.2.2): `pos` = real bits not yet read;
 // reading nb bits takes stream bits [pos - nb, pos) as a little-endian
-// integer (zeros below bit 0) and lowers pos, which may go negative.  A
-// 64-bit window of the stream starting at bit wb serves the reads.
+// integer (zeros below bit 0) and lowers pos, which may go negative.
+// The stream is read as aligned 32-bit words (a word holding a stream byte
+// never crosses a page); bit positions count from the first aligned word
+// (stream bit 0 is bit 8 a, a = the stream's address mod 4).  A 64-bit
+// window holds bits [32 wi, 32 wi + 64) with rel = pos + 8 a - 32 wi in
+// [32, 64] between reads; when a read leaves fewer than 32 bits in it, the
+// next lower word, loaded one refill earlier, is shifted in.  Bits below
+// the stream (before its first byte, or below word 0) read as zero.
 struct ZBits {
-  const uint8_t* p;
-  uint64_t n;
-  int64_t pos;
-  int64_t wb;
+  uint64_t base;   // the stream's address rounded down to 4
+  uint32_t lead;   // 8 a: bits of word 0 before the stream
+  uint32_t rel;
+  int64_t wi;
   uint64_t w;
+  uint32_t nx;     // word wi - 1 as loaded (word 0 when wi - 1 < 0)
+  int32_t sw;      // sequence reader: wi's index in the LDS stage
 };
+
+__device__ __forceinline__ uint32_t zb_load(const ZBits& b, int64_t k) {
+  return g_ld<uint32_t>(b.base + 4ull * (uint64_t)(k < 0 ? 0 : k));
+}
+// word k as the window takes it: zero below the stream
+__device__ __forceinline__ uint32_t zb_take(const ZBits& b, int64_t k, uint32_t v) {
+  if ((int32_t)((uint64_t)k >> 32) < 0) return 0u;  // k < 0
+  return k == 0 ? v & ~((1u << b.lead) - 1u) : v;  // lead < 32
+}
 
 __device__ bool zb_init(ZBits& b, const uint8_t* p, uint64_t n) {
   if (n == 0) return false;
   const uint32_t last = zld8(p + n - 1);
   if (!last) return false;
-  b.p = p;
-  b.n = n;
-  b.pos = (int64_t)(n * 8) - (int64_t)(8 - hibit(last));
-  b.wb = -1;
-  b.w = 0;
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  b.base = a & ~3ull;
+  b.lead = 8u * (uint32_t)(a & 3u);
+  const int64_t pa = (int64_t)(n * 8) - (int64_t)(8 - hibit(last)) + b.lead;  // >= lead >= 0
+  const int64_t top = (pa - 1) >> 5;  // word holding bit pa - 1 (-1 when pa == 0)
+  b.wi = top - 1;
+  b.w = ((uint64_t)zb_take(b, top, zb_load(b, top)) << 32) | zb_take(b, top - 1, zb_load(b, top - 1));
+  b.nx = zb_load(b, top - 2);
+  b.rel = (uint32_t)(pa - 32 * b.wi);  // in [33, 64]
   return true;
 }
 
-// nb <= 25
-__device__ uint32_t zb_peek(ZBits& b, uint32_t nb) {
-  if (nb == 0 || b.pos <= 0) return 0;
-  const int64_t start = b.pos - (int64_t)nb, lo = start < 0 ? 0 : start;
-  if (b.wb < 0 || lo < b.wb || b.pos > b.wb + 64) {
-    b.wb = lo > 32 ? (lo - 32) & ~7ll : 0;
-    uint64_t w = 0;
-    const uint64_t byte0 = (uint64_t)b.wb >> 3;
-    for (uint32_t k = 0; k < 8; ++k)
-      if (byte0 + k < b.n) w |= (uint64_t)zld8(b.p + byte0 + k) << (8 * k);
-    b.w = w;
-  }
-  const uint32_t width = (uint32_t)(b.pos - lo);
-  const uint64_t v = (b.w >> (lo - b.wb)) & ((1ull << width) - 1);
-  return (uint32_t)(v << (lo - start));
+__device__ __forceinline__ int64_t zb_pos(const ZBits& b) { return 32 * b.wi + (int64_t)b.rel - (int64_t)b.lead; }
+
+// nb <= 32
+__device__ __forceinline__ uint32_t zb_peek(const ZBits& b, uint32_t nb) {
+  return nb == 0 ? 0u : (uint32_t)((b.w >> (b.rel - nb)) & ((1ull << nb) - 1ull));
 }
 
-__device__ uint32_t zb_read(ZBits& b, uint32_t nb) {
-  if (nb > 24) {  // offset extra bits (up to 31): the high part first
-    const uint32_t hi = zb_read(b, nb - 16);
-    return (hi << 16) | zb_read(b, 16);
+__device__ __forceinline__ void zb_skip(ZBits& b, uint32_t nb) {
+  b.rel -= nb;
+  if (b.rel < 32) {
+    b.w = (b.w << 32) | zb_take(b, b.wi - 1, b.nx);
+    b.rel += 32;
+    --b.wi;
+    b.nx = zb_load(b, b.wi - 1);
   }
+}
+
+__device__ __forceinline__ uint32_t zb_read(ZBits& b, uint32_t nb) {
   const uint32_t v = zb_peek(b, nb);
-  b.pos -= nb;
+  zb_skip(b, nb);
   return v;
+}
+
+// The sequence stream's reader takes its words from an LDS stage instead:
+// before each batch the wavefront stages the kZSeqStage words below the
+// window (a batch reads at most kZBatch x 90 bits), and a refill reads the
+// next lower word from there; the word read at one refill is made
+// wave-uniform at the next, so the LDS read is not waited for in between.
+__device__ __forceinline__ void zs_skip(ZBits& b, uint32_t nb, const uint32_t* stage) {
+  b.rel -= nb;
+  if (b.rel < 32) {
+    b.w = (b.w << 32) | zb_take(b, b.wi - 1, (uint32_t)__builtin_amdgcn_readfirstlane(b.nx));
+    b.rel += 32;
+    --b.wi;
+    --b.sw;
+    b.nx = b.sw >= 1 ? stage[b.sw - 1] : 0u;
+  }
+}
+__device__ __forceinline__ uint32_t zs_read(ZBits& b, uint32_t nb, const uint32_t* stage) {
+  const uint32_t v = zb_peek(b, nb);
+  zs_skip(b, nb, stage);
+  return v;
+}
+
+// a 64-bit value read from LDS, made wave-uniform
+__device__ __forceinline__ uint64_t zu64(uint64_t v) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
+         (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+}
+
+// an output byte, to the plane and to the history ring
+__device__ __forceinline__ void z_put(uint8_t* dst, uint8_t* ring, uint64_t pos, uint32_t b) {
+  g_st<uint8_t>((uint64_t)(dst + pos), (uint8_t)b);
+  ring[pos & (kZRing - 1)] = (uint8_t)b;
+}
+
+// A match (3.1.1.4) of ml bytes at output position o from off bytes back,
+// by the wavefront, 64 bytes an instruction.  Offsets up to the ring's
+// size read the LDS ring (the wavefront's LDS accesses complete in order,
+// so a chunk sees every earlier chunk); an offset below 64 repeats the last
+// off bytes (byte j of the match is byte j mod off of them).  Longer
+// offsets read the plane: a chunk whose sources reach bytes stored since
+// the last fence fences first; the caller may pass the match's first bytes
+// already loaded (pre, pn).
+__device__ __forceinline__ void z_match(uint8_t* dst, uint8_t* ring, uint64_t o, uint32_t off, uint32_t ml,
+                                        uint32_t lane, uint64_t& fence_o, const uint8_t* pre, uint32_t pn) {
+  if (ml == 0) return;
+  if (off < 64) {
+    uint32_t ph = lane % off;  // (c + lane) mod off for chunk start c
+    const uint32_t step = 64u % off;
+    for (uint32_t c0 = 0; c0 < ml; c0 += 64) {
+      const uint32_t b = ring[(o - off + ph) & (kZRing - 1)];
+      if (c0 + lane < ml) z_put(dst, ring, o + c0 + lane, b);
+      ph += step;
+      if (ph >= off) ph -= off;
+    }
+  } else if (off <= kZRing) {
+    for (uint32_t c0 = 0; c0 < ml; c0 += 64) {
+      const uint64_t pos = o + c0 + lane;
+      const uint32_t b = ring[(pos - off) & (kZRing - 1)];
+      if (c0 + lane < ml) z_put(dst, ring, pos, b);
+    }
+  } else {
+    // the first pn bytes (pn <= 8) were loaded with the batch's other far
+    // sources before it ran
+    for (uint32_t c0 = 0; c0 < ml; c0 += 64) {
+      if (c0 + 64 > pn && ml > pn && o + c0 - off + 64 > fence_o) {
+        __threadfence_block();
+        fence_o = o + c0;
+      }
+      const uint64_t pos = o + c0 + lane;
+      const uint32_t b = c0 + lane < pn ? (uint32_t)pre[lane] : c0 + lane < ml ? zld8(dst + pos - off) : 0u;
+      if (c0 + lane < ml) z_put(dst, ring, pos, b);
+    }
+  }
 }
 
 // forward bit reader over global bytes (FSE table descriptions, 4.1.1)
@@ -212,6 +307,14 @@ struct ZCtl {
   uint32_t huf_bits;
   uint32_t ns;                // Huffman symbols (with the implied last one)
   uint32_t al[3];             // accuracy logs of the LL, OF, ML tables
+  uint64_t nseq;              // sequences of the current block
+  uint32_t batch, seq_ok;     // sequences in the current batch; no error so far
+  uint64_t batch_lits;        // literal bytes the batch copies
+  int64_t seq_wi;             // the sequence reader's window word
+  uint64_t seq_base;          // the sequence stream's aligned address
+  uint64_t seq_w;             // the reader's window, offset and next word
+  uint32_t seq_rel, seq_nx, seq_lead;
+  uint32_t seq_state[3];      // LL, OF, ML states
 };
 
 // XXH64 with seed 0 (the frame checksum), serial on one lane
@@ -292,14 +395,14 @@ __device__ int64_t z_huf_weights(const uint8_t* p, uint64_t n, uint8_t* w, uint3
       if (nw > 253) return -1;
       w[nw++] = (uint8_t)ftab[s1];
       s1 = (ftab[s1] >> 16) + zb_read(r, (ftab[s1] >> 8) & 255u);
-      if (r.pos < 0) {
+      if (zb_pos(r) < 0) {
         w[nw++] = (uint8_t)ftab[s2];
         break;
       }
       if (nw > 253) return -1;
       w[nw++] = (uint8_t)ftab[s2];
       s2 = (ftab[s2] >> 16) + zb_read(r, (ftab[s2] >> 8) & 255u);
-      if (r.pos < 0) {
+      if (zb_pos(r) < 0) {
         w[nw++] = (uint8_t)ftab[s1];
         break;
       }
@@ -335,10 +438,21 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
   __shared__ uint32_t ftab[64];             // the weights' FSE table
   __shared__ int16_t norm[256];
   __shared__ uint16_t next[256];
+  __shared__ uint32_t sq_ll[kZBatch], sq_ml[kZBatch], sq_off[kZBatch];  // a batch of decoded sequences
+  __shared__ uint64_t sq_src[kZBatch];                                  // their match sources
+  __shared__ uint8_t sq_pre[8 * kZBatch];                               // first source bytes of far matches
+  __shared__ uint8_t ring[kZRing];                                      // the last kZRing output bytes
+  __shared__ uint32_t ll_code[36], ml_code[53];                         // baseline | extra bits << 24
+  __shared__ uint32_t ll_x[512], ml_x[512];                             // the code of each LL / ML state's symbol
+  __shared__ uint8_t lit_stage[kZLitStage];                             // literals of the current batch
+  __shared__ uint32_t seq_stage[kZSeqStage];                            // sequence stream words below the window
+  uint64_t fence_o = 0;  // output bytes below this were stored before the last fence
 
   const DecodeJob job = jobs[blockIdx.x];
   if (job.codec != kCodecZstd) return;
   const uint32_t lane = threadIdx.x;
+  if (lane < 36) ll_code[lane] = kLLBase[lane] | ((uint32_t)kLLBits[lane] << 24);
+  if (lane < 53) ml_code[lane] = kMLBase[lane] | ((uint32_t)kMLBits[lane] << 24);
   const uint8_t* src = reinterpret_cast<const uint8_t*>(job.src);
   uint8_t* dst = reinterpret_cast<uint8_t*>(job.dst);
   const uint64_t cap = job.dst_len;
@@ -573,11 +687,10 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
     const uint32_t act = c.action;
     if (act == kZDone || act == kZError) break;
     if (act == kZRaw) {
-      for (uint64_t k = lane; k < c.blk_len; k += 64)
-        g_st<uint8_t>((uint64_t)(dst + c.o + k), (uint8_t)zld8(src + c.blk_off + k));
+      for (uint64_t k = lane; k < c.blk_len; k += 64) z_put(dst, ring, c.o + k, zld8(src + c.blk_off + k));
     } else if (act == kZRle) {
-      const uint8_t v = (uint8_t)zld8(src + c.blk_off);
-      for (uint64_t k = lane; k < c.blk_len; k += 64) g_st<uint8_t>((uint64_t)(dst + c.o + k), v);
+      const uint32_t v = zld8(src + c.blk_off);
+      for (uint64_t k = lane; k < c.blk_len; k += 64) z_put(dst, ring, c.o + k, v);
     } else {
       // ---- Huffman literals into the output's last `regen` bytes ----
       if (c.huf_new) {
@@ -590,6 +703,19 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
         }
       }
       __syncthreads();
+      if (c.n_streams) {
+        // Huffman-coded literals: the streams' cache lines touched by the
+        // wavefront first (one round of loads), so each lane's word loads,
+        // issued a refill ahead, find them in the L2 rather than in HBM.
+        // (seg_off / seg_len describe the current block only when it has
+        // Huffman streams.)
+        const uint64_t a0 = (uint64_t)(src + c.seg_off[0]) & ~63ull;
+        const uint64_t a1 = (uint64_t)(src + c.seg_off[c.n_streams - 1] + c.seg_len[c.n_streams - 1]);
+        uint32_t sink = 0;
+        for (uint64_t a = a0 + 64ull * lane; a < a1; a += 64ull * 64)
+          sink += g_ld<uint32_t>(a);
+        if (sink == 0xFFFFFFFFu && c.n_streams > 4) c.err = sink;  // never true: keeps the loads
+      }
       if (lane < c.n_streams) {
         const uint64_t lit0 = cap - c.regen;
         uint64_t out = lit0;
@@ -600,12 +726,17 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
         for (uint32_t k = 0; good && k < c.seg_cnt[lane]; ++k) {
           const uint32_t e = huf[zb_peek(r, mb)];
           g_st<uint8_t>((uint64_t)(dst + out + k), (uint8_t)e);
-          r.pos -= e >> 8;
+          zb_skip(r, e >> 8);
         }
-        if (!good || r.pos != 0) atomicOr(&c.err, 1u);  // each stream consumed exactly
+        if (!good || zb_pos(r) != 0) atomicOr(&c.err, 1u);  // each stream consumed exactly
       }
       __syncthreads();
-      // ---- sequences: tables, the state chain and execution on lane 0 ----
+      // ---- sequences (3.1.1.3.2): lane 0 parses the section header and
+      // tables, then decodes the sequences kZBatch at a time into LDS; the
+      // wavefront executes each batch (literal copies and matches 64 bytes
+      // per instruction, history through the LDS ring) ----
+      ZBits r;                          // lane 0's reader and FSE states
+      uint32_t sl = 0, so = 0, sm = 0;
       if (lane == 0) {
         bool ok = c.err == 0;
         const uint8_t* p = src + c.seq_off;
@@ -628,12 +759,6 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
             }
           }
         }
-        uint64_t o = c.o, lpos = 0;
-        const uint64_t regen = c.regen, lit0 = cap - regen;
-        const uint32_t lt = c.lit_type;
-        auto lit = [&](uint64_t k) -> uint8_t {
-          return lt == 0 ? (uint8_t)zld8(src + c.lit_src + k) : lt == 1 ? (uint8_t)c.lit_src : (uint8_t)zld8(dst + lit0 + k);
-        };
         if (ok && nseq > 0) {
           ok = n - q >= 1;
           const uint32_t modes = ok ? zld8(p + q) : 0;
@@ -677,84 +802,229 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
               ok = *x.have != 0;
             }
           }
-          ZBits r;
           ok = ok && zb_init(r, p + q, n - q);
-          uint32_t sl = 0, so = 0, sm = 0;
           if (ok) {
             sl = zb_read(r, c.al[0]);
             so = zb_read(r, c.al[1]);
             sm = zb_read(r, c.al[2]);
           }
-          for (uint64_t s = 0; ok && s < nseq; ++s) {
-            const uint32_t le = ll_t[sl], oe = of_t[so], me = ml_t[sm];
+        } else if (ok) {
+          ok = q == n;  // no sequences: nothing follows the count
+          nseq = 0;
+        }
+        c.nseq = ok ? nseq : 0;
+        c.seq_ok = ok;
+        c.seq_wi = r.wi;
+        c.seq_base = r.base;
+        c.seq_lead = r.lead;
+        c.seq_rel = r.rel;
+        c.seq_w = r.w;
+        c.seq_nx = r.nx;
+        c.seq_state[0] = sl;
+        c.seq_state[1] = so;
+        c.seq_state[2] = sm;
+      }
+      __syncthreads();
+      // each LL / ML state's code (baseline | extra bits << 24), so a step
+      // reads its state's entry and code together (symbols past the code
+      // tables are refused by the step before it uses the code)
+      if (c.seq_ok && c.nseq) {
+        for (uint32_t u = lane; u < (1u << c.al[0]); u += 64) {
+          const uint32_t sy = ll_t[u] & 255u;
+          ll_x[u] = sy < 36 ? ll_code[sy] : 0u;
+        }
+        for (uint32_t u = lane; u < (1u << c.al[2]); u += 64) {
+          const uint32_t sy = ml_t[u] & 255u;
+          ml_x[u] = sy < 53 ? ml_code[sy] : 0u;
+        }
+      }
+      __syncthreads();
+      // every lane runs the sequence chain with wave-uniform values from here
+      ZBits q;
+      q.base = zu64(c.seq_base);
+      q.lead = __builtin_amdgcn_readfirstlane(c.seq_lead);
+      q.rel = __builtin_amdgcn_readfirstlane(c.seq_rel);
+      q.wi = (int64_t)zu64((uint64_t)c.seq_wi);
+      q.w = zu64(c.seq_w);
+      q.nx = __builtin_amdgcn_readfirstlane(c.seq_nx);
+      uint32_t ql = __builtin_amdgcn_readfirstlane(c.seq_state[0]), qo = __builtin_amdgcn_readfirstlane(c.seq_state[1]),
+               qm = __builtin_amdgcn_readfirstlane(c.seq_state[2]);
+      const uint64_t regen = __builtin_amdgcn_readfirstlane(c.regen), lit0 = cap - regen, nseq = zu64(c.nseq);
+      const uint32_t lt = __builtin_amdgcn_readfirstlane(c.lit_type);
+      const uint64_t lit_src = zu64(c.lit_src), frame_start = zu64(c.frame_start);
+      auto lit = [&](uint64_t k) -> uint32_t {
+        return lt == 0 ? zld8(src + lit_src + k) : lt == 1 ? (uint32_t)(uint8_t)lit_src : zld8(dst + lit0 + k);
+      };
+      bool ok = c.seq_ok;
+      uint64_t o = zu64(c.o), lpos = 0, done = 0;
+      while (ok && done < nseq) {
+        // the words a batch may read: [wi - kZSeqStage, wi)
+        const int64_t stage_lo = c.seq_wi - (int64_t)kZSeqStage;
+        for (uint32_t j = lane; j < kZSeqStage; j += 64) {
+          const int64_t k = stage_lo + j;
+          seq_stage[j] = g_ld<uint32_t>(c.seq_base + 4ull * (uint64_t)(k < 0 ? 0 : k));
+        }
+        __syncthreads();
+        q.sw = (int32_t)kZSeqStage;  // q.wi - stage_lo
+        {
+          // every lane decodes the batch (the same values in every lane);
+          // validation as the serial execution checks it, on copies of the
+          // output and literal positions
+          uint64_t oo = o, lp = lpos;
+          uint32_t k = 0;
+          bool good = true;
+          uint32_t rep0 = __builtin_amdgcn_readfirstlane(c.rep[0]), rep1 = __builtin_amdgcn_readfirstlane(c.rep[1]),
+                   rep2 = __builtin_amdgcn_readfirstlane(c.rep[2]);
+          for (; k < kZBatch && done + k < nseq; ++k) {
+            const uint32_t le = __builtin_amdgcn_readfirstlane(ll_t[ql]), oe = __builtin_amdgcn_readfirstlane(of_t[qo]),
+                           me = __builtin_amdgcn_readfirstlane(ml_t[qm]);
+            const uint32_t llx = ll_x[ql], mlx = ml_x[qm];
             const uint32_t ofc = oe & 255u, mlc = me & 255u, llc = le & 255u;
             if (ofc > 31 || mlc > 52 || llc > 35) {
-              ok = false;
+              good = false;
               break;
             }
-            const uint32_t ofv = (1u << ofc) + zb_read(r, ofc);
-            const uint32_t ml = kMLBase[mlc] + zb_read(r, kMLBits[mlc]);
-            const uint32_t ll = kLLBase[llc] + zb_read(r, kLLBits[llc]);
+            const uint32_t mli = __builtin_amdgcn_readfirstlane(mlx), lli = __builtin_amdgcn_readfirstlane(llx);
+            const uint32_t ofv = (1u << ofc) + zs_read(q, ofc, seq_stage);
+            const uint32_t ml = (mli & 0xFFFFFFu) + zs_read(q, mli >> 24, seq_stage);
+            const uint32_t ll = (lli & 0xFFFFFFu) + zs_read(q, lli >> 24, seq_stage);
             uint32_t off;
             if (ofv > 3) {  // 3.1.1.5 repeat offsets
               off = ofv - 3;
-              c.rep[2] = c.rep[1];
-              c.rep[1] = c.rep[0];
-              c.rep[0] = off;
+              rep2 = rep1;
+              rep1 = rep0;
+              rep0 = off;
             } else {
               const uint32_t idx = ofv + (ll == 0 ? 1u : 0u);
               if (idx == 1) {
-                off = c.rep[0];
+                off = rep0;
               } else if (idx == 2) {
-                off = c.rep[1];
-                c.rep[1] = c.rep[0];
-                c.rep[0] = off;
+                off = rep1;
+                rep1 = rep0;
+                rep0 = off;
               } else if (idx == 3) {
-                off = c.rep[2];
-                c.rep[2] = c.rep[1];
-                c.rep[1] = c.rep[0];
-                c.rep[0] = off;
+                off = rep2;
+                rep2 = rep1;
+                rep1 = rep0;
+                rep0 = off;
               } else {
-                off = c.rep[0] - 1;
+                off = rep0 - 1;
                 if (off == 0) {
-                  ok = false;
+                  good = false;
                   break;
                 }
-                c.rep[2] = c.rep[1];
-                c.rep[1] = c.rep[0];
-                c.rep[0] = off;
+                rep2 = rep1;
+                rep1 = rep0;
+                rep0 = off;
               }
             }
-            if (s + 1 < nseq) {
-              sl = (le >> 16) + zb_read(r, (le >> 8) & 255u);
-              sm = (me >> 16) + zb_read(r, (me >> 8) & 255u);
-              so = (oe >> 16) + zb_read(r, (oe >> 8) & 255u);
+            if (done + k + 1 < nseq) {
+              ql = (le >> 16) + zs_read(q, (le >> 8) & 255u, seq_stage);
+              qm = (me >> 16) + zs_read(q, (me >> 8) & 255u, seq_stage);
+              qo = (oe >> 16) + zs_read(q, (oe >> 8) & 255u, seq_stage);
             }
             // execute (3.1.1.4): the writes stay below the unread literals
-            if (ll > regen - lpos || o + ll + (regen - lpos - ll) > cap) {
-              ok = false;
+            if (ll > regen - lp || oo + ll + (regen - lp - ll) > cap) {
+              good = false;
               break;
             }
-            for (uint32_t k = 0; k < ll; ++k) g_st<uint8_t>((uint64_t)(dst + o + k), lit(lpos + k));
-            o += ll;
-            lpos += ll;
-            if (off > o - c.frame_start || ml > cap - o - (regen - lpos)) {
-              ok = false;
+            oo += ll;
+            lp += ll;
+            if (off > oo - frame_start || ml > cap - oo - (regen - lp)) {
+              good = false;
               break;
             }
-            for (uint32_t k = 0; k < ml; ++k)
-              g_st<uint8_t>((uint64_t)(dst + o + k), g_ld<uint8_t>((uint64_t)(dst + o + k - off)));
-            o += ml;
+            if (lane == 0) {
+              sq_ll[k] = ll;
+              sq_ml[k] = ml;
+              sq_off[k] = off;
+              sq_src[k] = oo - off;
+            }
+            oo += ml;
           }
-          ok = ok && r.pos == 0;
-        } else if (ok) {
-          ok = q == n;  // no sequences: nothing follows the count
+          __syncthreads();  // every lane has read c before lane 0 updates it
+          if (lane == 0) {
+            c.rep[0] = rep0;
+            c.rep[1] = rep1;
+            c.rep[2] = rep2;
+            c.seq_wi = q.wi;
+            c.batch = k;
+            c.batch_lits = lp - lpos;
+            c.seq_ok = good;
+          }
         }
-        if (ok) {
-          for (uint64_t k = lpos; k < regen; ++k) g_st<uint8_t>((uint64_t)(dst + o + (k - lpos)), lit(k));
-          o += regen - lpos;
-          ok = o - c.o <= c.bmax;
+        __syncthreads();
+        const uint32_t bn = c.batch;
+        // the batch's literals (their first kZLitStage bytes) staged in LDS
+        // with all their loads issued together
+        const uint64_t lit_base = lpos;
+        const uint64_t staged = c.batch_lits < kZLitStage ? c.batch_lits : kZLitStage;
+        for (uint64_t j0 = 0; j0 < staged; j0 += 16 * 64) {
+          uint32_t v[16];
+#pragma unroll
+          for (uint32_t t = 0; t < 16; ++t) {
+            const uint64_t j = j0 + 64 * t + lane;
+            v[t] = j < staged ? lit(lit_base + j) : 0u;
+          }
+#pragma unroll
+          for (uint32_t t = 0; t < 16; ++t) {
+            const uint64_t j = j0 + 64 * t + lane;
+            if (j < staged) lit_stage[j] = (uint8_t)v[t];
+          }
         }
+        auto blit = [&](uint64_t k) -> uint32_t {  // literal k of the block
+          return k - lit_base < staged ? (uint32_t)lit_stage[k - lit_base] : lit(k);
+        };
+        // the first 8 source bytes of every match reaching past the ring,
+        // where they were stored before this batch: eight matches per
+        // instruction, all loads issued before the first is used
+        const uint64_t ob = o;
+        if (o > fence_o) {
+          __threadfence_block();
+          fence_o = o;
+        }
+        {
+          uint32_t v[kZBatch / 8];
+#pragma unroll
+          for (uint32_t t = 0; t < kZBatch / 8; ++t) {
+            const uint32_t k = 8 * t + lane / 8, j = lane & 7u;
+            bool take = false;
+            uint64_t a = 0;
+            if (k < bn) {
+              a = sq_src[k] + j;
+              take = sq_off[k] > kZRing && j < sq_ml[k] && a < ob;
+            }
+            v[t] = take ? zld8(dst + a) : 0u;
+          }
+#pragma unroll
+          for (uint32_t t = 0; t < kZBatch / 8; ++t) sq_pre[8 * (8 * t) + lane] = (uint8_t)v[t];
+        }
+        for (uint32_t k = 0; k < bn; ++k) {
+          const uint32_t ll = sq_ll[k], ml = sq_ml[k], off = sq_off[k];
+          for (uint32_t j = lane; j < ll; j += 64) z_put(dst, ring, o + j, blit(lpos + j));
+          o += ll;
+          lpos += ll;
+          // prefetched leading bytes: those below ob, at most 8
+          const uint64_t src0 = o - off;
+          const uint64_t below = ob > src0 ? ob - src0 : 0;
+          const uint32_t pn = off > kZRing ? (uint32_t)(below < 8 ? below : 8) : 0u;
+          z_match(dst, ring, o, off, ml, lane, fence_o, sq_pre + 8 * k, pn < ml ? pn : ml);
+          o += ml;
+        }
+        done += bn;
+        ok = c.seq_ok;
+        __syncthreads();  // lane 0 refills the batch arrays next
+      }
+      if (lane == 0 && ok && nseq) c.seq_ok = zb_pos(q) == 0;
+      __syncthreads();
+      ok = ok && c.seq_ok;
+      if (ok) {
+        for (uint64_t k = lane; k < regen - lpos; k += 64) z_put(dst, ring, o + k, lit(lpos + k));
+        o += regen - lpos;
+        ok = o - c.o <= c.bmax;
+      }
+      __syncthreads();  // every lane has read c.o
+      if (lane == 0) {
         c.o = o;
         if (!ok) c.action = kZError;
       }
