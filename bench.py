@@ -442,6 +442,116 @@ def secondary_line(wl, ms, kms, crc=False, hsh=False):
             "description": wl.name}
 
 
+
+def zstd_line(steps, with_cpu=True):
+    """Zstd plane payloads at scale (codec 0x0004, zstd_device.hip): the bytes
+    of a bf16 16384 x 32768 N(0, 0.02) tensor (1 GiB) as one passthrough
+    plane in 256 KiB chunk frames ([version][state length 0][frame], as
+    compressor.rs:316-381 writes chunked planes), each frame written by the
+    image's libzstd at level 3 (the reference's Zstd codec calls libzstd at
+    level 3, codecs/zstd.rs).  Every chunk is one wavefront's serial frame
+    decode; the restored bytes are checked against the tensor after the
+    timed steps.  CPU baseline: the oracle's RFC 8878 restatement decoding a
+    sample of the same frames over 16 threads (and at one), with libzstd's
+    own ZSTD_decompress on the same frames reported beside it."""
+    import ctypes as C
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    import torch
+
+    from ptwm_amd import api, ids, plan
+
+    z = C.CDLL("libzstd.so.1")
+    z.ZSTD_compressBound.argtypes = [C.c_size_t]
+    z.ZSTD_compressBound.restype = C.c_size_t
+    z.ZSTD_compress.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_int]
+    z.ZSTD_compress.restype = C.c_size_t
+    z.ZSTD_decompress.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t]
+    z.ZSTD_decompress.restype = C.c_size_t
+    z.ZSTD_isError.argtypes = [C.c_size_t]
+    z.ZSTD_isError.restype = C.c_uint
+    g = torch.Generator(device="cuda:0").manual_seed(90)
+    t = (torch.randn(16384, 32768, generator=g, device="cuda:0") * 0.02).to(torch.bfloat16)
+    dev_raw = t.view(torch.uint8).reshape(-1)
+    raw = dev_raw.cpu().numpy()
+    n, CH = raw.size, 256 << 10
+    t0 = time.perf_counter()
+    frames = []
+    for a in range(0, n, CH):
+        part = np.ascontiguousarray(raw[a:a + CH])
+        cap = z.ZSTD_compressBound(part.size)
+        buf = np.empty(cap, np.uint8)
+        r = z.ZSTD_compress(buf.ctypes.data, cap, part.ctypes.data, part.size, 3)
+        if z.ZSTD_isError(r):
+            raise SystemExit("libzstd compress failed")
+        frames.append(buf[:r].tobytes())
+    enc_s = time.perf_counter() - t0
+    body, ents = bytearray(), []
+    for k, f in enumerate(frames):
+        ents.append((len(body), min(CH, n - k * CH)))
+        body += b"\x00\x00\x00\x00\x00" + f
+    pp = plan.PlanePlan(ids.CODEC_ZSTD, 0, len(body), n, ents)
+    state = plan.encode_plan([plan.TensorPlan(plan.CHAIN_PASSTHROUGH, 0, n, [pp])])
+    src = torch.from_numpy(np.frombuffer(bytes(body), np.uint8).copy()).to("cuda:0")
+    out = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+
+    def step():
+        return api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, state,
+                                                         src, out, 0)
+
+    step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    if not torch.equal(out, dev_raw):
+        raise SystemExit("zstd: restored bytes differ from the tensor")
+    line = {"restored_gbs": round(n / (ms * 1e-3) / 1e9, 2), "ms_per_step": round(ms, 3),
+            "kernel": "zstd_decode_kernel (one wavefront per 256 KiB chunk frame)",
+            "ratio": round(len(body) / n, 4), "frames": len(frames),
+            "encode": f"libzstd level 3 on the host, {n / enc_s / 1e9:.2f} GB/s (input to the bench, not measured)",
+            "description": "bf16 16384x32768 N(0,0.02) bytes (1 GiB) as one passthrough plane, 256 KiB Zstd chunk frames"}
+    if with_cpu:
+        import oracle as O
+
+        sample = list(range(0, len(frames), max(1, len(frames) // 32)))[:32]
+        sizes = [ents[k][1] for k in sample]
+        nbytes = sum(sizes)
+        for k in sample[:4]:  # the restatement decodes the same frames bit-exactly
+            if O.zstd_decompress(frames[k], sizes[sample.index(k)]) != raw[k * CH:k * CH + sizes[sample.index(k)]].tobytes():
+                raise SystemExit("zstd: CPU restatement differs")
+        outs = [np.empty(sz, np.uint8) for sz in sizes]
+        srcs = [np.frombuffer(frames[k], np.uint8) for k in sample]
+
+        def port(i):
+            O.zstd_decompress(frames[sample[i]], sizes[i])
+
+        def libz(i):
+            r = z.ZSTD_decompress(outs[i].ctypes.data, sizes[i], srcs[i].ctypes.data, srcs[i].size)
+            if z.ZSTD_isError(r):
+                raise SystemExit("libzstd decompress failed")
+
+        def rate(fn, nthreads, budget=1.0):
+            with ThreadPoolExecutor(nthreads) as ex:
+                t0, reps = time.perf_counter(), 0
+                while True:
+                    list(ex.map(fn, range(len(sample))))
+                    reps += 1
+                    if time.perf_counter() - t0 > budget:
+                        break
+                return round(nbytes * reps / (time.perf_counter() - t0) / 1e9, 3)
+
+        threads = min(16, os.cpu_count() or 1)
+        line["cpu_baseline"] = {"value": rate(port, threads), "unit": "GB/s", "cores": threads, "kind": "port",
+                                "value_1_thread": rate(port, 1),
+                                "libzstd_gbs": rate(libz, threads), "libzstd_gbs_1_thread": rate(libz, 1),
+                                "sample": f"{len(sample)} of the {len(frames)} frames ({nbytes / 2**20:.0f} MiB), "
+                                          "oracle/zstd_oracle.c; libzstd ZSTD_decompress on the same frames"}
+    return line
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -450,7 +560,7 @@ def main():
     ap.add_argument("--workload", default="llama8b+crc",
                     help="<workload>[@rans][+crc][+hash]: the headline decode (default: config 4, plane "
                          "CRC-32 verified inside the timed region)")
-    ap.add_argument("--extra", default="fp8,fp8@rans,mxfp4,bf16_1k,fp32_4k,c1_ref,c2_ref,c3_huf,c3_rans,c5_ref",
+    ap.add_argument("--extra", default="fp8,fp8@rans,mxfp4,bf16_1k,fp32_4k,c1_ref,c2_ref,c3_huf,c3_rans,c5_ref,zstd",
                     help="comma list of secondary workloads reported in config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--resident", action="store_true",
@@ -512,6 +622,13 @@ def main():
         del wl
         gc.collect()
         torch.cuda.empty_cache()
+        if name == "zstd":
+            wl = None
+            extras[name] = zstd_line(max(3, args.steps // 2), not args.no_cpu_baseline)
+            log(f"[bench] zstd: {extras[name]['restored_gbs']} GB/s restored"
+                + (f", CPU {extras[name]['cpu_baseline']['value']} GB/s (libzstd "
+                   f"{extras[name]['cpu_baseline']['libzstd_gbs']})" if "cpu_baseline" in extras[name] else ""))
+            continue
         slow = name == "c3_rans"   # four serial rANS chains per 64 MiB plane: seconds per step
         wl = build_workload(name, args.resident or slow)
         m2, k2 = measure(wl, 1 if slow else max(3, args.steps), 0 if slow else 1)

@@ -27,8 +27,9 @@ namespace {
 
 constexpr uint32_t kZBlockMax = 128u * 1024u;
 constexpr uint32_t kZBatch = 256;               // sequences decoded per batch
-constexpr uint32_t kZRing = 64u * 1024u;        // LDS history ring (bytes)
-constexpr uint32_t kZLitStage = 16u * 1024u;    // literal bytes of a batch staged in LDS
+// LDS: about 51 KB a workgroup, so three payloads decode on a CU at once
+constexpr uint32_t kZRing = 16u * 1024u;        // LDS history ring (bytes)
+constexpr uint32_t kZLitStage = 4u * 1024u;     // literal bytes of a batch staged in LDS
 constexpr uint32_t kZSeqStage = 1024;            // sequence stream words staged per batch
 constexpr uint32_t kZHufMax = 12;
 

@@ -37,6 +37,7 @@ OWN_IDS = {
 CODEC_IDENTITY = 0x0000
 CODEC_HUFFMAN = 0x0001
 CODEC_RANS = 0x0003
+CODEC_ZSTD = 0x0004
 CODEC_HUFF_ILV = 0x7F01            # this library's GPU-native codecs
 CODEC_RANS_ILV = 0x7F02
 CODEC_NAMES = {"identity": CODEC_IDENTITY, "huffman": CODEC_HUFFMAN, "rans": CODEC_RANS}
