@@ -1341,6 +1341,24 @@ int64_t read_ptwc(const uint8_t* f, size_t n, std::vector<TensorRec>& out, std::
   return kOk;
 }
 
+// The row layout a frame's planes decode with (compact.rs:479-505: the
+// terminal descriptor's layout, chain/runtime.rs:359-438).  The Source emits
+// Rows { last dimension } (Flat for a scalar; transforms/source.rs:145-176),
+// BytePassthrough keeps its input's layout, and the bit reorders and the
+// byte and nibble splits emit Flat planes that the plane ops keep.  So a
+// plane of a Source-only or Source -> BytePassthrough chain has rows of the
+// last dimension and every other plane this reader plans is Flat (0).
+uint32_t terminal_row_len(const Chain& c) {
+  if (c.nodes.empty() || c.nodes[0].op != kOpSource) return 0;
+  for (size_t i = 1; i < c.nodes.size(); ++i)
+    if (c.nodes[i].op != kOpBytePassthrough) return 0;
+  const std::vector<uint8_t>& sp = c.nodes[0].params;
+  if (sp.empty() || sp[0] == 0 || sp.size() < 1 + 4 * (size_t)sp[0]) return 0;
+  uint32_t last;
+  std::memcpy(&last, sp.data() + 1 + 4 * ((size_t)sp[0] - 1), 4);
+  return last;  // 0: PlaneLayout::rows(0) is None, Flat
+}
+
 // PTWS frame (compact.rs:321-550): one tensor
 int64_t read_ptws(const uint8_t* f, size_t n, std::vector<TensorRec>& out) {
   out.resize(1);
@@ -1426,15 +1444,21 @@ int64_t read_ptws(const uint8_t* f, size_t n, std::vector<TensorRec>& out) {
   // planes in terminal order: head, [state], payload_len, [crc], payload
   const size_t np = t.own_chain.terms.size();
   t.planes.resize(np);
+  const uint32_t row_len = terminal_row_len(t.own_chain);
   for (size_t i = 0; i < np; ++i) {
     PlaneRec& p = t.planes[i];
     const uint64_t head = r.var();
     if (!r.ok || (head >> 2) > 0xFFFF || !known_codec(head >> 2) || (head & 3u) == 3) return kInvalid;
     p.et_kind = 2;
     p.codec = (uint16_t)(head >> 2);
-    if ((head & 3u) == 1) {
+    p.row_len = row_len;
+    if ((head & 3u) == 1) {  // inline state: version, length-prefixed bytes
       const uint8_t v = r.u8();
       const size_t sl = r.var_len();
+      p.state_source = 1;
+      p.state_version = v;
+      p.inl_off = r.o;
+      p.inl_len = sl;
       r.take(sl);
       if (v == 0 && sl == 0) return kInvalid;
     }

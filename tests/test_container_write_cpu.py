@@ -228,3 +228,52 @@ def test_payload_spans_of_one_buffer_write_the_same_file():
     assert [e.name for e in ents] == [e.name for e in ents2] == [n for n, _ in raws]
     with pytest.raises(ValueError):
         api.container_write(items)  # spans without the buffer
+
+
+def _leb(v: int) -> bytes:
+    out = bytearray()
+    while v >= 0x80:
+        out.append((v & 0x7F) | 0x80)
+        v >>= 7
+    out.append(v)
+    return bytes(out)
+
+
+def o1sac_frame(rows: int, row_len: int, seed: int = 4):
+    """A compact frame holding an E8M0-like scale tensor [rows, row_len] as
+    one Order1ScaleAC plane with its state inline (compact.rs:479-505: head
+    (codec << 2 | 1), version, state, payload).  Written through the
+    library's frame writer with an Identity plane, whose tail is then
+    replaced.  Returns (frame, plane, state)."""
+    from test_oracle_o1sac import make_state
+
+    rng = np.random.default_rng(seed)
+    plane = np.clip(np.round(rng.normal(-6, 1.5, rows * row_len)) + 127, 0, 255).astype(np.uint8).tobytes()
+    st = make_state(rng, sorted(set(plane)), skew=2.0)
+    ident = O.codec_encode(O.CODEC_IDENTITY, plane)
+    base = api.container_write([api.WriteTensor("s", DT_U8, P.CHAIN_PASSTHROUGH, [rows, row_len],
+                                                [api.WritePlane(O.CODEC_IDENTITY, ident)])], layout="frame")
+    tail = b"\x00" + _leb(len(ident)) + ident          # head 0 (Identity, no state), length, payload
+    assert base.endswith(tail)
+    pay = O.o1sac_encode(st, plane, row_len)
+    frame = base[:-len(tail)] + _leb((O.CODEC_O1SAC << 2) | 1) + b"\x01" + _leb(len(st)) + st + _leb(len(pay)) + pay
+    return frame, plane, st
+
+
+@pytest.mark.parametrize("rows,row_len", [(64, 128), (7, 33), (1, 500)])
+def test_frame_order1scaleac_plane_plans_with_its_state_and_rows(rows, row_len):
+    """A frame's Order1ScaleAC plane decodes with its inline state and the
+    rows of the Source's last dimension (transforms/source.rs:145-176), as
+    the reference's decode_body passes legacy_plane_layout(descriptor.layout)
+    to the codec (compact.rs:479-505)."""
+    frame, plane, st = o1sac_frame(rows, row_len)
+    plan, ents, out_len = api.container_plan(frame)
+    assert ents[0].status == 0 and ents[0].plan_index == 0
+    t = P.decode_plan(plan)[0]
+    assert [p.codec for p in t.planes] == [O.CODEC_O1SAC]
+    off, ln, rl, ver = t.planes[0].state
+    assert (frame[off:off + ln], rl, ver) == (st, row_len, 1)
+    assert plan_oracle.decode_plan(frame, plan, out_len)[:len(plane)] == plane
+    # a flat layout would code the plane as one row: the row length matters
+    if rows > 1:
+        assert O.o1sac_encode(st, plane, 0) != O.o1sac_encode(st, plane, row_len)

@@ -176,3 +176,21 @@ def test_capacity_bound_edge_matches_the_oracle():
             with pytest.raises(Exception) as ei:
                 dispatch(state, blob, n)
             assert getattr(ei.value, "rc", None) == -1
+
+
+@pytest.mark.parametrize("rows,row_len", [(64, 128), (7, 33)])
+def test_order1scaleac_plane_of_a_compact_frame(rows, row_len):
+    """A compact frame's Order1ScaleAC plane (inline state, rows of the
+    Source's last dimension) restores on the device from the reader's plan."""
+    from test_container_write_cpu import o1sac_frame
+
+    note(f"o1sac frame {rows}x{row_len}")
+    frame, plane, _ = o1sac_frame(rows, row_len)
+    plan_b, ents, out_len = api.container_plan(frame)
+    assert ents[0].status == 0
+    out = torch.full((out_len,), 0xA5, dtype=torch.uint8, device="cuda:0")
+    n = api.hardware_backend_dispatch_decode_cuda(ids.HARDWARE_BACKEND_LABEL, ids.DECODE_PLAN_LABEL, plan_b,
+                                                  dev_bytes(frame), out, 0)
+    torch.cuda.synchronize()
+    assert n == len(plane)
+    assert out[:len(plane)].cpu().numpy().tobytes() == plane
