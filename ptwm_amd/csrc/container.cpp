@@ -889,10 +889,13 @@ struct Builder {
       if (p.et_kind != 2) return p.et_kind == 1 ? kInvalid : kUnsup;
       if (p.state_source == 3) return kInvalid;  // container.rs:2104-2108
       if (!device_codec(p.codec)) return kUnsup;
-      if (p.codec == kO1sac && !p.chunked) {
-        // container.rs:2051-2100: the plane's state, inline or from the
-        // prelude (same version, role covered by applies_to_mask, bytes
-        // matching the stored xxh64); chunked planes carry theirs per frame
+      if (!p.chunked) {
+        // container.rs:2051-2100: an unchunked plane's state, inline or from
+        // the prelude (same version, role covered by applies_to_mask, bytes
+        // matching the stored xxh64: checked whatever the codec).  Only
+        // Order1ScaleAC reads it; the other codecs here ignore theirs
+        // (codecs/zstd.rs:65-106 and the like).  Chunked planes carry their
+        // state per frame and the record's is not read (:1975-2044).
         if (p.state_source == 1) {
           st[pi] = {p.inl_off, p.inl_len, p.state_version};
         } else if (p.state_source == 2) {
@@ -906,10 +909,9 @@ struct Builder {
           if (p.role >= 1 && p.role <= 8 && !(e->mask & (1u << (p.role - 1)))) return kInvalid;
           if (xxh64_once(file + e->off, (size_t)e->len) != e->hash) return kInvalid;
           st[pi] = {e->off, e->len, e->version};
-        }  // state_source 0: no state; the decode refuses it
+        }  // state_source 0: no state (Order1ScaleAC's decode refuses it)
+        if (p.codec != kO1sac) st[pi] = {0, 0, 0};
         if (st[pi][1] > 0xFFFFFFFFull) return kInvalid;
-      } else if (p.state_source == 2) {
-        return kUnsup;  // shared state of another codec
       }
       all_crc &= p.has_crc;
       any_crc |= p.has_crc;

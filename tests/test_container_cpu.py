@@ -337,3 +337,82 @@ def test_legacy_builtin_entries_are_recognised_by_id():
     d[27:59] = O.blake3(bytes(d[et_off:et_off + et_len]))
     _, ents, _ = api.container_plan(bytes(d))
     assert ents and all(e.plan_index == -1 and e.status == -5 for e in ents), [e.status for e in ents]
+
+
+def _legacy_plane_state_at(data: bytes, payload_off: int, payload_len: int, rows: bool = False) -> int:
+    """File offset of a legacy plane record's state_source byte, found back
+    from its payload (plane_record.rs:110-272: role, flags, codec, table
+    index, state_source, state_version, state_info u16, inline length u32,
+    payload_len u64, CRC u32, layout u8 [row_len u32], payload) for an
+    unchunked plane with a CRC and no inline state."""
+    import struct
+
+    o = payload_off - 1 - (4 if rows else 0) - 4 - 8
+    if struct.unpack_from("<Q", data, o)[0] != payload_len or struct.unpack_from("<I", data, o - 4)[0] != 0:
+        return None  # another record shape (rows layout, inline state)
+    return o - 8
+
+
+def _prelude_mask_at(data: bytes, state_off: int) -> int:
+    """File offset of the applies_to_mask byte of the prelude entry whose state starts at state_off
+    (prelude.rs write_prelude: id, codec, version, mask, reserved, xxh64,
+    name_len, name, pad to 4, state_len, state)."""
+    import struct
+
+    for n in range(64):
+        pad = (4 - n % 4) % 4
+        e = state_off - 4 - pad - n - 18
+        if e >= 0 and struct.unpack_from("<H", data, e + 16)[0] == n and \
+                struct.unpack_from("<H", data, e + 2)[0] == O.CODEC_O1SAC:
+            return e + 5
+    raise AssertionError("prelude entry not found")
+
+
+def test_shared_state_of_a_stateless_codec_is_checked_then_ignored():
+    """container.rs:2051-2100 resolves an unchunked plane's shared state
+    whatever its codec (entry present, same version, role covered by
+    applies_to_mask, stored xxh64); a codec without state then ignores it
+    (codecs/zstd.rs:65-106 and the like).  Planes of legacy_v1_1_0.ptwm
+    patched to name the file's Order1ScaleAC prelude entry plan and decode
+    as before when the checks pass, and are refused (-1) when they fail."""
+    name = "legacy_v1_1_0.ptwm"
+    data = open(os.path.join(FILES, name), "rb").read()
+    plan, ents, out_len = api.container_plan(data)
+    ts = P.decode_plan(plan)
+    want = plan_oracle.decode_plan(data, plan, out_len)
+    scale = [(e, ts[e.plan_index]) for e in ents if e.name.endswith(".scale")][0][1].planes[0]
+    s_off, _, _, s_ver = scale.state
+    o1 = _legacy_plane_state_at(data, scale.payload_offset, scale.payload_len, rows=True)
+    assert o1 is not None and data[o1] == 2  # the scale plane names its prelude entry
+    sid = data[o1 + 2] | (data[o1 + 3] << 8)
+    mask_at = _prelude_mask_at(data, s_off)
+    cases, accepted = 0, 0
+    for e in ents:
+        t = ts[e.plan_index]
+        for p in t.planes:
+            if p.codec == O.CODEC_O1SAC or p.chunks:
+                continue
+            at = _legacy_plane_state_at(data, p.payload_offset, p.payload_len)
+            if at is None:
+                continue
+            role = data[at - 6]
+            for mask, ver, ident in ((data[mask_at], s_ver, sid), (0xFF, s_ver, sid), (0xFF, s_ver + 1, sid),
+                                     (0xFF, s_ver, sid + 7)):
+                ok = ver == s_ver and ident == sid and (not 1 <= role <= 8 or bool(mask >> (role - 1) & 1))
+                b = bytearray(data)
+                b[mask_at] = mask  # the entry's stored xxh64 covers its state bytes only
+                b[at] = 2
+                b[at + 1] = ver
+                b[at + 2:at + 4] = ident.to_bytes(2, "little")
+                plan2, ents2, out2 = api.container_plan(bytes(b))
+                e2 = [x for x in ents2 if x.name == e.name][0]
+                if ok:
+                    assert e2.status == 0, (e.name, role)
+                    got = plan_oracle.decode_plan(bytes(b), plan2, out2)
+                    assert got[e2.out_offset:e2.out_offset + e2.orig_size] == \
+                        want[e.out_offset:e.out_offset + e.orig_size]
+                    accepted += 1
+                else:
+                    assert e2.status == -1, (e.name, role, ver, ident)
+                cases += 1
+    assert cases >= 12 and accepted >= 3
