@@ -876,11 +876,24 @@ __global__ void __launch_bounds__(64) tans_decode_kernel(const DecodeJob* __rest
   uint64_t win = ((uint64_t)w_top << 32) | (uint32_t)__builtin_amdgcn_readfirstlane(word(top - 1));
   uint32_t next = word(top - 2);
   uint32_t rel = (uint32_t)(tb - 32 * (uint64_t)(top - 1));  // tb - 32 wi, in [33, 64] (tb > 0)
+  // stage index of word wi - 1 (negative below the stage), so that a
+  // refill compares 32-bit indices and restages only when it leaves the piece
+  int32_t si = (int32_t)(wi - 1 - stage_lo);
   auto refill = [&]() {
     win = (win << 32) | (uint32_t)__builtin_amdgcn_readfirstlane(next);
     rel += 32;
     --wi;
-    next = word(wi - 1);
+    --si;
+    if (si >= 0) {
+      next = tstage[si];
+    } else if (stage_lo > 0) {  // word wi - 1 = stage_lo - 1: the piece below
+      stage_lo -= kTansStageWords;
+      stage();
+      si += (int32_t)kTansStageWords;
+      next = tstage[si];
+    } else {
+      next = 0u;  // below the stream
+    }
   };
   uint32_t state = 0;
   if (tb >= 11) {
