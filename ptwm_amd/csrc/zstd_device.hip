@@ -135,11 +135,14 @@ __device__ __forceinline__ void zs_skip(ZBits& b, uint32_t nb, const uint32_t* s
     b.nx = b.sw >= 1 ? stage[b.sw - 1] : 0u;
   }
 }
-__device__ __forceinline__ uint32_t zs_read(ZBits& b, uint32_t nb, const uint32_t* stage) {
+// nb bits with no refill (the caller keeps rel >= nb)
+__device__ __forceinline__ uint32_t zs_take(ZBits& b, uint32_t nb) {
   const uint32_t v = zb_peek(b, nb);
-  zs_skip(b, nb, stage);
+  b.rel -= nb;
   return v;
 }
+// refill once if fewer than 32 bits remain (one refill restores >= 32)
+__device__ __forceinline__ void zs_fill(ZBits& b, const uint32_t* stage) { zs_skip(b, 0, stage); }
 
 // a 64-bit value read from LDS, made wave-uniform
 __device__ __forceinline__ uint64_t zu64(uint64_t v) {
@@ -871,8 +874,14 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
           // every lane decodes the batch (the same values in every lane);
           // validation as the serial execution checks it, on copies of the
           // output and literal positions
-          uint64_t oo = o, lp = lpos;
-          uint32_t k = 0;
+          // 32-bit positions inside the batch: pb output bytes and lq
+          // literals so far (a batch produces under 2^26 bytes); room =
+          // cap - o (clamped: the checks below never reach 2^32), lrem =
+          // regen - lpos, fs = o - frame_start
+          const uint64_t room64 = cap - o, fs = o - frame_start;
+          const uint32_t room = room64 > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)room64;
+          const uint32_t lrem = (uint32_t)(regen - lpos);
+          uint32_t pb = 0, lq = 0, k = 0;
           bool good = true;
           uint32_t rep0 = __builtin_amdgcn_readfirstlane(c.rep[0]), rep1 = __builtin_amdgcn_readfirstlane(c.rep[1]),
                    rep2 = __builtin_amdgcn_readfirstlane(c.rep[2]);
@@ -886,9 +895,14 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
               break;
             }
             const uint32_t mli = __builtin_amdgcn_readfirstlane(mlx), lli = __builtin_amdgcn_readfirstlane(llx);
-            const uint32_t ofv = (1u << ofc) + zs_read(q, ofc, seq_stage);
-            const uint32_t ml = (mli & 0xFFFFFFu) + zs_read(q, mli >> 24, seq_stage);
-            const uint32_t ll = (lli & 0xFFFFFFu) + zs_read(q, lli >> 24, seq_stage);
+            // the window holds >= 32 bits between refills: the offset's
+            // extra bits (<= 31), then ML + LL extra bits (<= 16 + 16), then
+            // the three state updates (<= 9 + 9 + 8), a refill check after each
+            const uint32_t ofv = (1u << ofc) + zs_take(q, ofc);
+            zs_fill(q, seq_stage);
+            const uint32_t ml = (mli & 0xFFFFFFu) + zs_take(q, mli >> 24);
+            const uint32_t ll = (lli & 0xFFFFFFu) + zs_take(q, lli >> 24);
+            zs_fill(q, seq_stage);
             uint32_t off;
             if (ofv > 3) {  // 3.1.1.5 repeat offsets
               off = ofv - 3;
@@ -896,42 +910,35 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
               rep1 = rep0;
               rep0 = off;
             } else {
-              const uint32_t idx = ofv + (ll == 0 ? 1u : 0u);
+              const uint32_t idx = ofv + (ll == 0 ? 1u : 0u);  // 1..4
               if (idx == 1) {
                 off = rep0;
-              } else if (idx == 2) {
-                off = rep1;
-                rep1 = rep0;
-                rep0 = off;
-              } else if (idx == 3) {
-                off = rep2;
-                rep2 = rep1;
-                rep1 = rep0;
-                rep0 = off;
               } else {
-                off = rep0 - 1;
-                if (off == 0) {
+                off = idx == 2 ? rep1 : idx == 3 ? rep2 : rep0 - 1;
+                if (off == 0) {  // idx 4 of rep0 == 1
                   good = false;
                   break;
                 }
-                rep2 = rep1;
+                if (idx != 2) rep2 = rep1;
                 rep1 = rep0;
                 rep0 = off;
               }
             }
             if (done + k + 1 < nseq) {
-              ql = (le >> 16) + zs_read(q, (le >> 8) & 255u, seq_stage);
-              qm = (me >> 16) + zs_read(q, (me >> 8) & 255u, seq_stage);
-              qo = (oe >> 16) + zs_read(q, (oe >> 8) & 255u, seq_stage);
+              ql = (le >> 16) + zs_take(q, (le >> 8) & 255u);
+              qm = (me >> 16) + zs_take(q, (me >> 8) & 255u);
+              qo = (oe >> 16) + zs_take(q, (oe >> 8) & 255u);
+              zs_fill(q, seq_stage);
             }
             // execute (3.1.1.4): the writes stay below the unread literals
-            if (ll > regen - lp || oo + ll + (regen - lp - ll) > cap) {
+            // (pb + (lrem - lq) <= room, so the subtraction below stays >= 0)
+            if (ll > lrem - lq || pb + (lrem - lq) > room) {
               good = false;
               break;
             }
-            oo += ll;
-            lp += ll;
-            if (off > oo - frame_start || ml > cap - oo - (regen - lp)) {
+            pb += ll;
+            lq += ll;
+            if ((uint64_t)off > fs + pb || ml > room - pb - (lrem - lq)) {
               good = false;
               break;
             }
@@ -939,10 +946,11 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
               sq_ll[k] = ll;
               sq_ml[k] = ml;
               sq_off[k] = off;
-              sq_src[k] = oo - off;
+              sq_src[k] = o + pb - off;
             }
-            oo += ml;
+            pb += ml;
           }
+          const uint64_t lp = lpos + lq;
           __syncthreads();  // every lane has read c before lane 0 updates it
           if (lane == 0) {
             c.rep[0] = rep0;
