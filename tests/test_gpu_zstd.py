@@ -123,3 +123,20 @@ def test_corruptions_rejected_where_the_oracle_rejects():
     with pytest.raises(Exception) as ei:
         dispatch(one(f, len(data) + 1), f, len(data) + 1)
     assert getattr(ei.value, "rc", None) == -1
+
+
+@pytest.mark.parametrize("period", [8 * 1024 + 3, 40 * 1024 + 1, 200 * 1024 + 7])
+def test_matches_beyond_the_history_ring(period):
+    """Random bytes repeated with a period past the decoder's 8 KiB LDS
+    history ring: every match reads the plane itself, often bytes the same
+    sequence batch stored (the decoder fences before reading bytes stored
+    since its last fence), and with the 200 KiB period across blocks."""
+    rng = np.random.default_rng(period)
+    unit = rng.integers(0, 256, period, dtype=np.uint8).tobytes()
+    data = (unit * (3 + (600 * 1024) // period))[:600 * 1024 + 11]
+    for level in (1, 9):
+        note(f"zstd repeat period {period} level {level}")
+        f = ZF.compress(data, level, window_log=20)
+        assert O.zstd_decompress(f, len(data)) == data
+        n, got = dispatch(one(f, len(data)), f, len(data))
+        assert n == len(data) and got == data
