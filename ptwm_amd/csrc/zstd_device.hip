@@ -27,7 +27,7 @@ namespace {
 
 constexpr uint32_t kZBlockMax = 128u * 1024u;
 constexpr uint32_t kZBatch = 128;               // sequences decoded per batch
-// LDS: about 30 KB a workgroup, so five payloads decode on a CU at once
+// LDS: about 26 KB a workgroup, so six payloads decode on a CU at once
 constexpr uint32_t kZRing = 4u * 1024u;         // LDS history ring (bytes)
 constexpr uint32_t kZLitStage = 1u * 1024u;     // literal bytes of a batch staged in LDS
 constexpr uint32_t kZSeqStage = 384;             // sequence stream words staged per batch
@@ -446,8 +446,6 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
   __shared__ uint64_t sq_src[kZBatch];                                  // their match sources
   __shared__ uint8_t sq_pre[8 * kZBatch];                               // first source bytes of far matches
   __shared__ uint8_t ring[kZRing];                                      // the last kZRing output bytes
-  __shared__ uint32_t ll_code[36], ml_code[53];                         // baseline | extra bits << 24
-  __shared__ uint32_t ll_x[512], ml_x[512];                             // the code of each LL / ML state's symbol
   __shared__ uint8_t lit_stage[kZLitStage];                             // literals of the current batch
   __shared__ uint32_t seq_stage[kZSeqStage];                            // sequence stream words below the window
   uint64_t fence_o = 0;  // output bytes below this were stored before the last fence
@@ -455,8 +453,10 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
   const DecodeJob job = jobs[blockIdx.x];
   if (job.codec != kCodecZstd) return;
   const uint32_t lane = threadIdx.x;
-  if (lane < 36) ll_code[lane] = kLLBase[lane] | ((uint32_t)kLLBits[lane] << 24);
-  if (lane < 53) ml_code[lane] = kMLBase[lane] | ((uint32_t)kMLBits[lane] << 24);
+  // the LL and ML codes (baseline | extra bits << 24), code c in lane c of a
+  // register: a sequence step reads its codes with one lane read each
+  const uint32_t ll_code = lane < 36 ? kLLBase[lane] | ((uint32_t)kLLBits[lane] << 24) : 0u;
+  const uint32_t ml_code = lane < 53 ? kMLBase[lane] | ((uint32_t)kMLBits[lane] << 24) : 0u;
   const uint8_t* src = reinterpret_cast<const uint8_t*>(job.src);
   uint8_t* dst = reinterpret_cast<uint8_t*>(job.dst);
   const uint64_t cap = job.dst_len;
@@ -829,20 +829,6 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
         c.seq_state[2] = sm;
       }
       __syncthreads();
-      // each LL / ML state's code (baseline | extra bits << 24), so a step
-      // reads its state's entry and code together (symbols past the code
-      // tables are refused by the step before it uses the code)
-      if (c.seq_ok && c.nseq) {
-        for (uint32_t u = lane; u < (1u << c.al[0]); u += 64) {
-          const uint32_t sy = ll_t[u] & 255u;
-          ll_x[u] = sy < 36 ? ll_code[sy] : 0u;
-        }
-        for (uint32_t u = lane; u < (1u << c.al[2]); u += 64) {
-          const uint32_t sy = ml_t[u] & 255u;
-          ml_x[u] = sy < 53 ? ml_code[sy] : 0u;
-        }
-      }
-      __syncthreads();
       // every lane runs the sequence chain with wave-uniform values from here
       ZBits q;
       q.base = zu64(c.seq_base);
@@ -888,13 +874,12 @@ __global__ void __launch_bounds__(64) zstd_decode_kernel(const DecodeJob* __rest
           for (; k < kZBatch && done + k < nseq; ++k) {
             const uint32_t le = __builtin_amdgcn_readfirstlane(ll_t[ql]), oe = __builtin_amdgcn_readfirstlane(of_t[qo]),
                            me = __builtin_amdgcn_readfirstlane(ml_t[qm]);
-            const uint32_t llx = ll_x[ql], mlx = ml_x[qm];
             const uint32_t ofc = oe & 255u, mlc = me & 255u, llc = le & 255u;
             if (ofc > 31 || mlc > 52 || llc > 35) {
               good = false;
               break;
             }
-            const uint32_t mli = __builtin_amdgcn_readfirstlane(mlx), lli = __builtin_amdgcn_readfirstlane(llx);
+            const uint32_t mli = __builtin_amdgcn_readlane(ml_code, mlc), lli = __builtin_amdgcn_readlane(ll_code, llc);
             // the window holds >= 32 bits between refills: the offset's
             // extra bits (<= 31), then ML + LL extra bits (<= 16 + 16), then
             // the three state updates (<= 9 + 9 + 8), a refill check after each
