@@ -26,11 +26,11 @@ namespace ptwm {
 namespace {
 
 constexpr uint32_t kZBlockMax = 128u * 1024u;
-constexpr uint32_t kZBatch = 128;               // sequences decoded per batch
-// LDS: about 26 KB a workgroup, so six payloads decode on a CU at once
-constexpr uint32_t kZRing = 4u * 1024u;         // LDS history ring (bytes)
+constexpr uint32_t kZBatch = 96;                // sequences decoded per batch
+// LDS: about 23 KB a workgroup, so seven payloads decode on a CU at once
+constexpr uint32_t kZRing = 2u * 1024u;         // LDS history ring (bytes)
 constexpr uint32_t kZLitStage = 1u * 1024u;     // literal bytes of a batch staged in LDS
-constexpr uint32_t kZSeqStage = 384;             // sequence stream words staged per batch
+constexpr uint32_t kZSeqStage = 288;             // sequence stream words staged per batch
 constexpr uint32_t kZHufMax = 12;
 
 // code tables of RFC 8878 3.1.1.3.2.1 and default distributions 3.1.1.3.2.2
